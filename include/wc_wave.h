@@ -1,0 +1,203 @@
+/*
+ * wc_wave.h — C ABI of the MI355X (gfx950) wave executor.
+ *
+ * The reference's wave executor is a Rust crate (engine/src/gpu/) whose
+ * callers hold a `GpuClient` and submit `PackedJob`s. This ABI is what that
+ * crate's FFI would bind instead: plain pointers and sizes, the job in its
+ * WCJ8 bytes (docs/TREE.md; engine/src/serialize.rs:1052-1129), results as
+ * pointer+length views. Every call returns 0 on success or a negative code;
+ * wc_last_error() then names the failure (the reference returns
+ * Result<_, String> at the same points).
+ */
+#ifndef WC_WAVE_H
+#define WC_WAVE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WC_OK 0
+#define WC_ERR_INVALID -1   /* malformed input (bytes, shapes, arguments) */
+#define WC_ERR_DEVICE -2    /* HIP runtime failure */
+#define WC_ERR_GONE -3      /* the service has shut down */
+#define WC_ERR_UNSUPPORTED -4
+
+/* Leaf-net arithmetic. PRECISE reproduces the CPU net's float32 loop order
+ * exactly (the reference's oracle mode, engine/src/gpu/device.rs:375-402);
+ * F16/BF16 run the MFMA GEMM chain with f32 accumulation (the reference's
+ * fast mode, CUBLAS_COMPUTE_32F_FAST_16F). */
+#define WC_PRECISE 0
+#define WC_F16 1
+#define WC_BF16 2
+
+/* Thread-local text of the last failure on this thread. */
+const char* wc_last_error(void);
+
+/* Network description: the flat `set_weights(dims, w, b, ln)` bank
+ * (engine/src/gpu/client.rs:257-272). dims[0] names the family:
+ *   [101, in, hidden, layers, heads, pool]                      MLP
+ *   [102, in, width, pub_layers, priv_in, priv_layers, pool]    two-tower
+ * w: MLP = W_1 [in x hidden] row-major, W_2..W_L [hidden x hidden],
+ *    W_head [heads x hidden]; b = b_1..b_L [hidden], b_head [heads]. */
+typedef struct wc_net_desc {
+    const uint32_t* dims;
+    uint32_t ndims;
+    const float* w;
+    size_t nw;
+    const float* b;
+    size_t nb;
+    const float* ln; /* unused by the synthetic families; pass NULL, 0 */
+    size_t nln;
+} wc_net_desc;
+
+/* Float counts a family expects for w and b. */
+int wc_net_sizes(const uint32_t* dims, uint32_t ndims, size_t* nw, size_t* nb);
+
+/* ------------------------------------------------------------ service API
+ * Replaces service::spawn / GpuClient / SolveHandle
+ * (engine/src/gpu/service.rs:55-82, client.rs:196-313). */
+
+typedef struct wc_service wc_service;
+typedef struct wc_ticket wc_ticket;
+typedef struct wc_result wc_result;
+
+typedef struct wc_service_opts {
+    uint32_t lanes;        /* executor lanes (streams) per device; reference WARCHEST_WAVE_LANES, default 2 */
+    uint32_t wave_jobs;    /* max jobs per wave; reference WARCHEST_WAVE_JOBS, default 64 */
+    uint32_t wave_rows;    /* max network rows per wave; reference WARCHEST_WAVE_ROWS, default 49152 */
+    uint32_t window_us;    /* bucket-fill window; reference WARCHEST_WAVE_US, default 800 */
+} wc_service_opts;
+
+/* service::spawn(device, dims, w, b, ln, precise): blocks until every lane is
+ * ready; fails if any lane fails (service.rs:55-82,144-162). opts may be NULL. */
+int wc_service_create(int device, const wc_net_desc* net, int precision, const wc_service_opts* opts,
+                      wc_service** out);
+/* Drop of the last GpuClient: shuts the dispatcher down and joins (client.rs:293-300). */
+void wc_service_destroy(wc_service* svc);
+/* GpuClient::set_weights: returns the new monotone version; queued waves keep theirs. */
+uint64_t wc_set_weights(wc_service* svc, const wc_net_desc* net);
+/* GpuClient::queued_work: monotone cost estimate of queued and running work. */
+uint64_t wc_queued_work(wc_service* svc);
+/* GpuClient::submit_tagged: copies the job bytes; the ticket is completed when the wave finishes. */
+int wc_submit(wc_service* svc, const uint8_t* job, size_t len, uint64_t tag, wc_ticket** out);
+/* SolveHandle::wait: blocks; *out owns the result (wc_result_free). Frees the ticket. */
+int wc_wait(wc_ticket* t, wc_result** out);
+/* 1 when wc_wait would not block, 0 otherwise. */
+int wc_poll(const wc_ticket* t);
+
+/* SolveResult views (client.rs:113-122). All indices are solve-local. */
+uint64_t wc_result_tag(const wc_result* r);
+uint64_t wc_result_weight_version(const wc_result* r);
+/* Final average strategy, one float per legal cell (soff-aligned). */
+const float* wc_result_strategy(const wc_result* r, size_t* n);
+/* Root values: nroots x (n0 + n1) floats, player 0's configs first. */
+const float* wc_result_root_values(const wc_result* r, uint32_t* nroots, uint32_t* n0, uint32_t* n1);
+/* Carried beliefs, f16 bits: slots x snapshot_configs, laid out by the job's snap_coff. */
+const uint16_t* wc_result_carries(const wc_result* r, uint32_t* slots, uint32_t* snapshot_configs);
+void wc_result_free(wc_result* r);
+
+/* ------------------------------------------------------ executor (lane) API
+ * Replaces Executor::{new, publish, launch, collect, solve}, Wave::pack and
+ * Harvest::unpack (engine/src/gpu/device.rs:515-831, wave.rs:127-221): one
+ * device, one stream, one wave at a time. */
+
+typedef struct wc_executor wc_executor;
+typedef struct wc_wave wc_wave;
+
+int wc_executor_create(int device, int precision, wc_executor** out);
+void wc_executor_destroy(wc_executor* ex);
+/* Executor::publish: an immutable weight bank; returns its version (> 0) or 0 on failure. */
+uint64_t wc_executor_publish(wc_executor* ex, const wc_net_desc* net);
+/* Wave::pack: concatenate compatible jobs into one wave-global index space. */
+int wc_wave_pack(const uint8_t* const* jobs, const size_t* lens, uint32_t njobs, wc_wave** out);
+void wc_wave_free(wc_wave* w);
+
+/* Counts of a packed wave, for admission, benchmarks and the roofline. */
+typedef struct wc_wave_stats {
+    uint32_t jobs, nodes, decision_nodes, chance_nodes, leaves, rows, terminals;
+    uint32_t levels, iters, nroots_max, carry_slots;
+    uint64_t cells, reach_slots, reach_len, vals_len, rev_nnz, rvd_nnz, draw_nnz, snapshot_configs;
+    uint64_t table_bytes, arena_bytes;
+    uint64_t cfr_bytes_per_iter[2]; /* algorithmic HBM bytes of one CFR iteration, traverser 0 / 1 */
+    uint64_t mlp_flops_per_query;
+} wc_wave_stats;
+int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* out);
+
+/* Executor::launch + collect (+ Harvest::unpack): runs the whole schedule,
+ * blocks, and returns one result per job in submission order
+ * (results[k] owned by the caller). */
+int wc_solve_wave(wc_executor* ex, wc_wave* w, uint64_t version, wc_result** results);
+
+/* Benchmark helper: upload once, then run the full schedule `reps` times on
+ * the device (inputs resident in HBM), returning the mean device time per
+ * wave in milliseconds, measured with HIP events on the executor's stream.
+ * kernel_ms (optional, 5 doubles) receives one profiled schedule's device
+ * time per launch class: [0] CFR sweeps, [1] leaf MLP, [2] leaf input,
+ * [3] everything else, and [4] the mean duration of one CFR-sweep launch. */
+int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t reps, double* wave_ms,
+                 double* kernel_ms);
+
+/* Leaf-net inference alone (the value-net GEMM chain): x is rows x in f32 on
+ * the host; out receives rows x heads f32 (head rows 0..heads-1). */
+int wc_mlp_forward(wc_executor* ex, uint64_t version, uint32_t rows, const float* x, float* out);
+/* Benchmark helper for the chain alone: x resident on the device, `reps` launches,
+ * mean milliseconds per chain from HIP events on the executor's stream. */
+int wc_time_mlp(wc_executor* ex, uint64_t version, uint32_t rows, const float* x, uint32_t reps,
+                double* chain_ms, double* layer_ms);
+
+/* ------------------------------------------------- job contract utilities */
+
+/* Decode and re-encode a WCJ8 job (byte-identical round trip), writing up to
+ * cap bytes into out and the full length into *len. */
+int wc_job_roundtrip(const uint8_t* job, size_t len, uint8_t* out, size_t cap, size_t* out_len);
+/* Structural validation of one job (indices in range, CSRs monotone,
+ * parents before children). */
+int wc_job_validate(const uint8_t* job, size_t len);
+
+/* Synthetic workloads (seeded). Trees grow breadth-first to a node budget,
+ * decision nodes carry config-dependent legal cells grouped into public
+ * observations, chance nodes carry per-config outcome rows, and every table
+ * is packed the way engine/src/serialize.rs:689-956 packs a real solver. */
+typedef struct wc_synth_spec {
+    uint64_t seed;
+    uint32_t trees;
+    uint32_t nodes_lo, nodes_hi;
+    uint32_t exact_decisions, exact_leaves;
+    uint32_t act_lo, act_hi;
+    float collapse;
+    uint32_t chance;
+    uint32_t draw_lo, draw_hi;
+    uint32_t info_fixed;
+    float info_median, info_p99;
+    uint32_t info_cap;
+    float legal_p, shift_p, notrans_p, terminal_p;
+    uint32_t dirichlet;
+    uint32_t nroots;
+    float whale_frac;
+    uint32_t whale_nodes, whale_info;
+    uint32_t depth, iters, snapshots;
+    float alpha, beta, gamma, predict;
+    const uint32_t* net_dims;
+    uint32_t n_net_dims;
+} wc_synth_spec;
+
+typedef struct wc_jobset wc_jobset;
+void wc_synth_spec_default(wc_synth_spec* spec);
+int wc_synth(const wc_synth_spec* spec, wc_jobset** out);
+uint32_t wc_jobset_count(const wc_jobset* s);
+const uint8_t* wc_jobset_job(const wc_jobset* s, uint32_t k, size_t* len);
+void wc_jobset_free(wc_jobset* s);
+/* Kaiming-normal weights and U[-0.1, 0.1] biases for a family (sizes from wc_net_sizes). */
+int wc_synth_weights(const uint32_t* dims, uint32_t ndims, uint64_t seed, float* w, size_t nw, float* b,
+                     size_t nb);
+/* rows x width features, U[0,1) with 30% of dims in one-hot blocks of width 8. */
+int wc_synth_features(uint32_t rows, uint32_t width, uint64_t seed, float* x);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WC_WAVE_H */

@@ -1,0 +1,165 @@
+"""ctypes loader for the oracle (test infrastructure; see oracle.c's header).
+
+Only tests, the smoke check and the benchmark's CPU-baseline leg import this.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+
+NET_EMPTY, NET_F32, NET_F16, NET_BF16 = 0, 1, 2, 3
+
+_lib = None
+
+
+class Shape(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in (
+        "nodes", "ncells", "rows", "nterm", "ncfg", "reach_len", "nroots", "root_n0", "root_n1",
+        "snapshot_configs", "carry_slots", "iters", "nlevels", "decision_nodes", "chance_nodes",
+        "leaves")]
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        L = C.CDLL(LIB)
+        u8p, f32p, u32p = C.POINTER(C.c_uint8), C.POINTER(C.c_float), C.POINTER(C.c_uint32)
+        L.oracle_last_error.restype = C.c_char_p
+        L.oracle_job_shape.argtypes = [u8p, C.c_size_t, C.POINTER(Shape)]
+        L.oracle_solve.argtypes = [u8p, C.c_size_t, C.c_int, u32p, C.c_uint32, f32p, C.c_size_t, f32p,
+                                   C.c_size_t, f32p, f32p, f32p, f32p]
+        L.oracle_mlp.argtypes = [C.c_uint32, f32p, C.c_uint32, u32p, C.c_int, u32p, C.c_uint32, f32p,
+                                 C.c_size_t, f32p, C.c_size_t, f32p, f32p]
+        L.oracle_solve_batch.argtypes = [C.c_uint32, C.POINTER(u8p), C.POINTER(C.c_size_t), C.c_uint32,
+                                         C.c_int, u32p, C.c_uint32, f32p, C.c_size_t, f32p, C.c_size_t,
+                                         C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
+        L.oracle_solve_batch.restype = C.c_double
+        L.oracle_mlp_batch.argtypes = [C.c_uint32, f32p, C.c_uint32, u32p, C.c_uint32, C.c_int, u32p,
+                                       C.c_uint32, f32p, C.c_size_t, f32p, C.c_size_t, f32p]
+        L.oracle_mlp_batch.restype = C.c_double
+        L.oracle_factor.argtypes = [C.c_float, C.c_float]
+        L.oracle_factor.restype = C.c_float
+        L.oracle_round_f16.argtypes = [C.c_float]
+        L.oracle_round_f16.restype = C.c_float
+        L.oracle_round_bf16.argtypes = [C.c_float]
+        L.oracle_round_bf16.restype = C.c_float
+        _lib = L
+    return _lib
+
+
+def _p(a, ctype):
+    return a.ctypes.data_as(C.POINTER(ctype))
+
+
+def _err():
+    return lib().oracle_last_error().decode(errors="replace")
+
+
+def shape(job: bytes) -> Shape:
+    s = Shape()
+    buf = (C.c_uint8 * len(job)).from_buffer_copy(job)
+    if lib().oracle_job_shape(buf, len(job), C.byref(s)) != 0:
+        raise ValueError(_err())
+    return s
+
+
+def _net_args(net, mode):
+    if net is None or mode == NET_EMPTY:
+        z = np.zeros(1, np.float32)
+        d = np.zeros(1, np.uint32)
+        return d, 0, z, 0, z, 0
+    d = np.ascontiguousarray(net.dims, np.uint32)
+    w = np.ascontiguousarray(net.w, np.float32)
+    b = np.ascontiguousarray(net.b, np.float32)
+    return d, len(d), w, w.size, b, b.size
+
+
+def solve(job: bytes, net=None, mode=NET_F32, conv=False):
+    """Solve one job on the CPU: returns dict(strategy, roots [nroots, n0+n1], carries
+    [slots, snapshot_configs], conv (nash, zero_sum) or None)."""
+    s = shape(job)
+    strategy = np.zeros(max(s.ncells, 1), np.float32)
+    roots = np.zeros(max(s.nroots * (s.root_n0 + s.root_n1), 1), np.float32)
+    carries = np.zeros(max(s.carry_slots * s.snapshot_configs, 1), np.float32)
+    cv = np.zeros(2, np.float32)
+    d, nd, w, nw, b, nb = _net_args(net, mode)
+    buf = (C.c_uint8 * len(job)).from_buffer_copy(job)
+    rc = lib().oracle_solve(buf, len(job), mode, _p(d, C.c_uint32), nd, _p(w, C.c_float), nw,
+                            _p(b, C.c_float), nb, _p(strategy, C.c_float), _p(roots, C.c_float),
+                            _p(carries, C.c_float), _p(cv, C.c_float) if conv else None)
+    if rc != 0:
+        raise ValueError(_err())
+    return {
+        "strategy": strategy[: s.ncells],
+        "roots": roots[: s.nroots * (s.root_n0 + s.root_n1)].reshape(s.nroots, s.root_n0 + s.root_n1),
+        "carries": carries[: s.carry_slots * s.snapshot_configs].reshape(s.carry_slots, s.snapshot_configs),
+        "conv": (float(cv[0]), float(cv[1])) if conv else None,
+        "shape": s,
+    }
+
+
+def mlp(x: np.ndarray, keys: np.ndarray, net, mode=NET_F32, want_h=False):
+    x = np.ascontiguousarray(x, np.float32)
+    keys = np.ascontiguousarray(keys, np.uint32)
+    rows, nk = keys.shape
+    out = np.zeros((rows, nk), np.float32)
+    hidden = net.dims[2]
+    h = np.zeros((rows, hidden), np.float32) if want_h else None
+    d, nd, w, nw, b, nb = _net_args(net, mode)
+    rc = lib().oracle_mlp(rows, _p(x, C.c_float), nk, _p(keys, C.c_uint32), mode, _p(d, C.c_uint32), nd,
+                          _p(w, C.c_float), nw, _p(b, C.c_float), nb, _p(out, C.c_float),
+                          _p(h, C.c_float) if want_h else None)
+    if rc != 0:
+        raise ValueError(_err())
+    return (out, h) if want_h else out
+
+
+def solve_batch(jobs, net, mode=NET_F32, threads=1):
+    """Time `jobs` solved one per thread on `threads` threads: (seconds, node_iters, leaf_queries)."""
+    bufs = [(C.c_uint8 * len(j)).from_buffer_copy(j) for j in jobs]
+    u8p = C.POINTER(C.c_uint8)
+    ptrs = (u8p * len(jobs))(*[C.cast(b, u8p) for b in bufs])
+    lens = (C.c_size_t * len(jobs))(*[len(j) for j in jobs])
+    d, nd, w, nw, b, nb = _net_args(net, mode)
+    ni, lq = C.c_uint64(), C.c_uint64()
+    sec = lib().oracle_solve_batch(len(jobs), ptrs, lens, threads, mode, _p(d, C.c_uint32), nd,
+                                   _p(w, C.c_float), nw, _p(b, C.c_float), nb, C.byref(ni), C.byref(lq))
+    if sec < 0:
+        raise ValueError(_err())
+    return sec, ni.value, lq.value
+
+
+def mlp_batch(x, heads, net, mode=NET_F32, threads=1):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros((x.shape[0], heads), np.float32)
+    d, nd, w, nw, b, nb = _net_args(net, mode)
+    sec = lib().oracle_mlp_batch(x.shape[0], _p(x, C.c_float), heads, None, threads, mode,
+                                 _p(d, C.c_uint32), nd, _p(w, C.c_float), nw, _p(b, C.c_float), nb,
+                                 _p(out, C.c_float))
+    if sec < 0:
+        raise ValueError(_err())
+    return sec, out
+
+
+def factor(t, p):
+    return lib().oracle_factor(t, p)
+
+
+def round_f16(x):
+    return lib().oracle_round_f16(x)
+
+
+def round_bf16(x):
+    return lib().oracle_round_bf16(x)

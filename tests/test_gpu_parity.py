@@ -1,0 +1,187 @@
+"""GPU parity: the HIP wave executor against the CPU oracle, through the C ABI.
+
+Float32 (WC_PRECISE) runs must be bit-identical to the oracle: every
+reduction on the device runs in the CPU solver's order without contraction.
+The f16/bf16 MFMA path is compared with the oracle's reduced-precision mode
+(same operand rounding, wide accumulation) tightly, and with the float32 CPU
+net at the 2e-3 relative root-value tolerance.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+import warchest_wave as ww
+import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+_EX = {}
+
+
+def executor(precision):
+    if precision not in _EX:
+        _EX[precision] = ww.Executor(0, precision)
+    return _EX[precision]
+
+
+def gpu_solve(jobs, net, precision):
+    ex = executor(precision)
+    v = ex.publish(net)
+    wave = ww.Wave(jobs)
+    out = ex.solve(wave, v)
+    wave.close()
+    return out
+
+
+def f16_carries(o):
+    return o["carries"].astype(np.float16)
+
+
+def assert_bit_exact(g, o, tag):
+    np.testing.assert_array_equal(g.strategy, o["strategy"], err_msg=f"{tag}: strategy")
+    np.testing.assert_array_equal(g.root_values, o["roots"], err_msg=f"{tag}: root values")
+    if o["carries"].size:
+        np.testing.assert_array_equal(g.carries, f16_carries(o), err_msg=f"{tag}: carries")
+
+
+def test_c1_float32_bit_exact():
+    say("case c1 float32: 1 tree, 16 iterations")
+    jobs = W.jobs("c1")
+    net = W.net_for("c1")
+    [g] = gpu_solve(jobs, net, ww.WC_PRECISE)
+    o = O.solve(jobs[0], net, O.NET_F32)
+    assert_bit_exact(g, o, "c1")
+
+
+def test_zero_network_is_uniform():
+    say("case zero network: c1 tree, all weights and biases zero")
+    jobs = W.jobs("c1")
+    net = W.net_for("c1")
+    zero = ww.Net(net.dims, np.zeros_like(net.w), np.zeros_like(net.b))
+    [g] = gpu_solve(jobs, zero, ww.WC_PRECISE)
+    o = O.solve(jobs[0], zero, O.NET_F32)
+    assert_bit_exact(g, o, "zero")
+    assert np.all(g.root_values == 0.0)
+
+
+def small_wave(**kw):
+    spec = dict(trees=8, nodes_lo=30, nodes_hi=90, chance=1, terminal_p=0.15, notrans_p=0.05, nroots=3,
+                iters=8, info_median=6.0, info_p99=40.0, info_cap=40, seed=11)
+    spec.update(kw)
+    return W.jobs("c4", **spec)
+
+
+def test_small_wave_float32_bit_exact():
+    jobs = small_wave()
+    net = W.net_for("c4")
+    say(f"case small wave float32: {len(jobs)} trees with chance, terminals, 3 carried roots")
+    got = gpu_solve(jobs, net, ww.WC_PRECISE)
+    for k, (j, g) in enumerate(zip(jobs, got)):
+        o = O.solve(j, net, O.NET_F32)
+        assert_bit_exact(g, o, f"tree {k}")
+
+
+def test_wave_composition_is_invariant():
+    jobs = small_wave(trees=6, seed=21)
+    net = W.net_for("c4")
+    say("case composition: tree 2 alone vs inside a 6-tree wave")
+    alone = gpu_solve([jobs[2]], net, ww.WC_PRECISE)[0]
+    inside = gpu_solve(jobs, net, ww.WC_PRECISE)[2]
+    np.testing.assert_array_equal(alone.strategy, inside.strategy)
+    np.testing.assert_array_equal(alone.root_values, inside.root_values)
+    np.testing.assert_array_equal(alone.carries, inside.carries)
+
+
+def test_repeat_is_deterministic():
+    jobs = small_wave(trees=4, seed=31)
+    net = W.net_for("c4")
+    say("case determinism: the same wave twice, f16")
+    a = gpu_solve(jobs, net, ww.WC_F16)
+    b = gpu_solve(jobs, net, ww.WC_F16)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x.strategy, y.strategy)
+        np.testing.assert_array_equal(x.root_values, y.root_values)
+
+
+def test_mlp_f16_matches_reduced_precision_oracle():
+    net = W.net_for("c2")
+    x = W.c2_inputs(rows=2048)
+    say("case mlp f16: 2048 queries, 512 -> 3x384 -> 64")
+    ex = executor(ww.WC_F16)
+    v = ex.publish(net)
+    got = ex.mlp(v, x, heads=64)
+    keys = np.tile(np.arange(64, dtype=np.uint32), (x.shape[0], 1))
+    emu = O.mlp(x, keys, net, O.NET_F16)
+    ref = O.mlp(x, keys, net, O.NET_F32)
+    scale = np.abs(ref).max()
+    # f32 accumulation order differs from the oracle's wide sum; operands are identical.
+    np.testing.assert_allclose(got, emu, rtol=2e-3, atol=2e-3 * scale)
+    assert np.abs(got - ref).max() <= 2e-2 * scale
+
+
+def test_mlp_bf16_matches_reduced_precision_oracle():
+    net = W.net_for("c2")
+    x = W.c2_inputs(rows=1024, seed=9)
+    say("case mlp bf16: 1024 queries")
+    ex = executor(ww.WC_BF16)
+    v = ex.publish(net)
+    got = ex.mlp(v, x, heads=64)
+    keys = np.tile(np.arange(64, dtype=np.uint32), (x.shape[0], 1))
+    emu = O.mlp(x, keys, net, O.NET_BF16)
+    scale = np.abs(emu).max()
+    np.testing.assert_allclose(got, emu, rtol=1e-2, atol=1e-2 * scale)
+
+
+def test_mlp_float32_bit_exact():
+    net = W.net_for("c2")
+    x = W.c2_inputs(rows=256, seed=5)
+    say("case mlp float32: 256 queries")
+    ex = executor(ww.WC_PRECISE)
+    v = ex.publish(net)
+    got = ex.mlp(v, x, heads=64)
+    keys = np.tile(np.arange(64, dtype=np.uint32), (x.shape[0], 1))
+    ref = O.mlp(x, keys, net, O.NET_F32)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_c3_f16_within_tolerance():
+    jobs = W.jobs("c3", trees=16)
+    net = W.net_for("c3")
+    say(f"case c3 f16: {len(jobs)} trees, 64 iterations")
+    got = gpu_solve(jobs, net, ww.WC_F16)
+    worst_rel = 0.0
+    for k, (j, g) in enumerate(zip(jobs, got)):
+        emu = O.solve(j, net, O.NET_F16)
+        ref = O.solve(j, net, O.NET_F32)
+        # Against the same operand rounding: only accumulation order differs.
+        np.testing.assert_allclose(g.root_values, emu["roots"], rtol=1e-3, atol=1e-4, err_msg=f"tree {k} vs f16 oracle")
+        # Against the float32 CPU net: 2e-3 relative on root values, scaled by the root's magnitude.
+        scale = np.abs(ref["roots"]).max() + 1e-12
+        rel = np.abs(g.root_values - ref["roots"]).max() / scale
+        worst_rel = max(worst_rel, rel)
+        assert rel <= 2e-3, f"tree {k}: root values {rel:.2e} relative to the float32 net"
+    say(f"c3 f16 worst root-value error vs float32 net: {worst_rel:.2e} (relative to max |root value|)")
+
+
+def test_service_submit_wait():
+    jobs = small_wave(trees=5, seed=41)
+    net = W.net_for("c4")
+    say("case service: 5 jobs through submit/wait, 1 lane")
+    ref = gpu_solve(jobs, net, ww.WC_PRECISE)
+    with ww.spawn(0, net, ww.WC_PRECISE, lanes=1, wave_jobs=8, window_us=2000) as client:
+        handles = [client.submit(j, tag=100 + k) for k, j in enumerate(jobs)]
+        assert client.queued_work() >= 0
+        got = [h.wait() for h in handles]
+    for k, (g, r) in enumerate(zip(got, ref)):
+        assert g.tag == 100 + k
+        assert g.weight_version == 1
+        np.testing.assert_array_equal(g.strategy, r.strategy)
+        np.testing.assert_array_equal(g.root_values, r.root_values)

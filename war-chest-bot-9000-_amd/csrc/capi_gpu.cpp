@@ -1,0 +1,304 @@
+// Device-facing entry points of the C ABI: executor, wave, service, results.
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <string>
+
+#include "../../include/wc_wave.h"
+#include "common.h"
+#include "executor.h"
+#include "service.h"
+#include "wave.h"
+
+using namespace wc;
+
+struct wc_executor {
+    std::unique_ptr<Executor> ex;
+};
+struct wc_wave {
+    WaveHost host;
+};
+struct wc_result {
+    Result r;
+};
+struct wc_service {
+    std::unique_ptr<Service> svc;
+};
+struct wc_ticket {
+    std::shared_ptr<Ticket> t;
+};
+
+namespace {
+
+bool read_net(const wc_net_desc* net, NetCopy* out, std::string* err) {
+    if (!net || !net->dims || net->ndims == 0 || (!net->w && net->nw) || (!net->b && net->nb)) {
+        *err = "network description is incomplete";
+        return false;
+    }
+    out->dims.assign(net->dims, net->dims + net->ndims);
+    if (!out->ns.parse(out->dims, err)) return false;
+    out->w.assign(net->w, net->w + net->nw);
+    out->b.assign(net->b, net->b + net->nb);
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wc_executor_create(int device, int precision, wc_executor** out) {
+    if (!out) return fail(WC_ERR_INVALID, "wc_executor_create: null output");
+    try {
+        auto* e = new wc_executor;
+        e->ex.reset(new Executor(device, precision));
+        if (!e->ex->ok()) {
+            std::string m = e->ex->error();
+            delete e;
+            return fail(WC_ERR_DEVICE, m);
+        }
+        *out = e;
+    } catch (const std::exception& e) {
+        return fail(WC_ERR_DEVICE, e.what());
+    }
+    return WC_OK;
+}
+
+void wc_executor_destroy(wc_executor* ex) { delete ex; }
+
+uint64_t wc_executor_publish(wc_executor* ex, const wc_net_desc* net) {
+    if (!ex) {
+        fail(WC_ERR_INVALID, "wc_executor_publish: null executor");
+        return 0;
+    }
+    NetCopy n;
+    std::string err;
+    if (!read_net(net, &n, &err)) {
+        fail(WC_ERR_INVALID, err);
+        return 0;
+    }
+    uint64_t v = ex->ex->publish(n.ns, n.dims, n.w.data(), n.w.size(), n.b.data(), n.b.size(), &err);
+    if (!v) fail(WC_ERR_INVALID, err);
+    return v;
+}
+
+int wc_wave_pack(const uint8_t* const* jobs, const size_t* lens, uint32_t njobs, wc_wave** out) {
+    if (!jobs || !lens || !out || njobs == 0) return fail(WC_ERR_INVALID, "wc_wave_pack: empty wave");
+    std::vector<Job> parsed(njobs);
+    std::string err;
+    for (uint32_t k = 0; k < njobs; k++)
+        if (!jobs[k] || !from_bytes(jobs[k], lens[k], &parsed[k], &err))
+            return fail(WC_ERR_INVALID, "job " + std::to_string(k) + ": " + err);
+    auto* w = new wc_wave;
+    if (!pack_wave(std::move(parsed), &w->host, &err)) {
+        delete w;
+        return fail(WC_ERR_INVALID, err);
+    }
+    *out = w;
+    return WC_OK;
+}
+
+void wc_wave_free(wc_wave* w) { delete w; }
+
+int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
+    if (!w || !s) return fail(WC_ERR_INVALID, "wc_wave_stats_get: null argument");
+    const WaveHost& h = w->host;
+    std::memset(s, 0, sizeof *s);
+    s->jobs = (uint32_t)h.jobs.size();
+    s->nodes = h.nodes();
+    for (uint32_t i = 0; i < h.nodes(); i++) {
+        uint32_t kind = h.node_meta[i] & 3u;
+        if (kind == 0) s->decision_nodes++;
+        if (kind == 1) s->chance_nodes++;
+        if (kind == 2) s->leaves++;
+    }
+    s->rows = h.rows();
+    s->terminals = (uint32_t)h.term_node.size();
+    s->levels = h.max_levels;
+    s->iters = h.meta.iters;
+    s->nroots_max = h.nroots_max;
+    s->carry_slots = h.carry_slots;
+    s->cells = h.ncells;
+    s->reach_slots = h.reach_task[0].size() + h.reach_task[1].size();
+    s->reach_len = h.reach_len;
+    s->vals_len = h.vals_len;
+    s->rev_nnz = h.rev_src.size();
+    s->rvd_nnz = h.rvd_src.size();
+    s->draw_nnz = h.draw_to.size();
+    s->snapshot_configs = h.snapshot_configs;
+    size_t tb = 0;
+    tb += 4 * (h.node_meta.size() + h.node_nc.size() + h.child_start.size() + h.child.size() + h.legal_row_of.size() +
+               h.legal_off.size() + h.legal_value.size() + h.draw_off.size() + h.draw_row_off.size() +
+               h.draw_row_start.size() + h.draw_to.size() + h.draw_p.size() + h.reach_base.size() +
+               h.vals_base.size() + h.parent.size() + h.rev_row_of.size() + h.rev_start.size() + h.rev_src.size() +
+               h.rev_cell.size() + h.rvd_row_of.size() + h.rvd_start.size() + h.rvd_src.size() + h.rvd_p.size() +
+               h.row_node.size() + h.row_cfg_off.size() + h.row_cfg.size() + h.cfg_key.size() + h.cfg_emb.size());
+    tb += h.pub_raw.size();
+    for (int p = 0; p < 2; p++)
+        tb += 8 * (h.back_task[p].size() + h.reach_task[p].size() + h.decision[p].size()) +
+              4 * (h.back_lvl[p].size() + h.reach_lvl[p].size());
+    s->table_bytes = tb;
+    s->arena_bytes = 4 * (4ull * h.ncells + 2ull * h.reach_len + h.vals_len + 2ull * h.rows() * (h.net.pool + 1) +
+                          h.root_values_len) +
+                     2ull * h.carry_slots * h.snapshot_configs;
+    s->cfr_bytes_per_iter[0] = cfr_bytes_per_iter(h, 0);
+    s->cfr_bytes_per_iter[1] = cfr_bytes_per_iter(h, 1);
+    const NetShape& ns = h.net;
+    s->mlp_flops_per_query = 2ull * (uint64_t(ns.in) * ns.hidden + uint64_t(ns.layers - 1) * ns.hidden * ns.hidden +
+                                     uint64_t(ns.hidden) * ns.heads);
+    return WC_OK;
+}
+
+int wc_solve_wave(wc_executor* ex, wc_wave* w, uint64_t version, wc_result** results) {
+    if (!ex || !w || !results) return fail(WC_ERR_INVALID, "wc_solve_wave: null argument");
+    std::vector<Result> out;
+    std::string err;
+    if (!ex->ex->solve(w->host, version, &out, &err)) return fail(WC_ERR_DEVICE, err);
+    for (size_t k = 0; k < out.size(); k++) {
+        results[k] = new wc_result;
+        results[k]->r = std::move(out[k]);
+    }
+    return WC_OK;
+}
+
+int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t reps, double* wave_ms, double* kernel_ms) {
+    if (!ex || !w || !wave_ms) return fail(WC_ERR_INVALID, "wc_time_wave: null argument");
+    ScheduleTimes prof;
+    std::string err;
+    if (!ex->ex->time_wave(w->host, version, reps, wave_ms, kernel_ms ? &prof : nullptr, &err))
+        return fail(WC_ERR_DEVICE, err);
+    if (kernel_ms) {
+        kernel_ms[0] = prof.cfr;
+        kernel_ms[1] = prof.mlp;
+        kernel_ms[2] = prof.leaf_input;
+        kernel_ms[3] = prof.other;
+        kernel_ms[4] = prof.cfr_launch_mean;
+    }
+    return WC_OK;
+}
+
+int wc_mlp_forward(wc_executor* ex, uint64_t version, uint32_t rows, const float* x, float* out) {
+    if (!ex || !x || !out) return fail(WC_ERR_INVALID, "wc_mlp_forward: null argument");
+    std::string err;
+    if (!ex->ex->mlp_forward(version, rows, x, out, &err)) return fail(WC_ERR_DEVICE, err);
+    return WC_OK;
+}
+
+int wc_time_mlp(wc_executor* ex, uint64_t version, uint32_t rows, const float* x, uint32_t reps, double* chain_ms,
+                double* layer_ms) {
+    if (!ex || !x || !chain_ms) return fail(WC_ERR_INVALID, "wc_time_mlp: null argument");
+    std::string err;
+    std::vector<double> layers;
+    if (!ex->ex->time_mlp(version, rows, x, reps, chain_ms, layer_ms ? &layers : nullptr, &err))
+        return fail(WC_ERR_DEVICE, err);
+    if (layer_ms)
+        for (size_t k = 0; k < layers.size() && k < 8; k++) layer_ms[k] = layers[k];
+    return WC_OK;
+}
+
+// ------------------------------------------------------------------ service
+
+int wc_service_create(int device, const wc_net_desc* net, int precision, const wc_service_opts* opts,
+                      wc_service** out) {
+    if (!out) return fail(WC_ERR_INVALID, "wc_service_create: null output");
+    NetCopy n;
+    std::string err;
+    if (!read_net(net, &n, &err)) return fail(WC_ERR_INVALID, err);
+    ServiceOpts o;
+    if (opts) {
+        if (opts->lanes) o.lanes = opts->lanes;
+        if (opts->wave_jobs) o.wave_jobs = opts->wave_jobs;
+        if (opts->wave_rows) o.wave_rows = opts->wave_rows;
+        o.window_us = opts->window_us;
+    }
+    try {
+        auto* s = new wc_service;
+        s->svc.reset(new Service(device, precision, o));
+        if (!s->svc->start(n, &err)) {
+            delete s;
+            return fail(WC_ERR_DEVICE, err);
+        }
+        *out = s;
+    } catch (const std::exception& e) {
+        return fail(WC_ERR_DEVICE, e.what());
+    }
+    return WC_OK;
+}
+
+void wc_service_destroy(wc_service* svc) { delete svc; }
+
+uint64_t wc_set_weights(wc_service* svc, const wc_net_desc* net) {
+    if (!svc) {
+        fail(WC_ERR_INVALID, "wc_set_weights: null service");
+        return 0;
+    }
+    NetCopy n;
+    std::string err;
+    if (!read_net(net, &n, &err)) {
+        fail(WC_ERR_INVALID, err);
+        return 0;
+    }
+    uint64_t v = svc->svc->set_weights(std::move(n), &err);
+    if (!v) fail(WC_ERR_GONE, err);
+    return v;
+}
+
+uint64_t wc_queued_work(wc_service* svc) { return svc ? svc->svc->queued_work() : 0; }
+
+int wc_submit(wc_service* svc, const uint8_t* job, size_t len, uint64_t tag, wc_ticket** out) {
+    if (!svc || !job || !out) return fail(WC_ERR_INVALID, "wc_submit: null argument");
+    std::shared_ptr<Ticket> t;
+    std::string err;
+    if (!svc->svc->submit(job, len, tag, &t, &err))
+        return fail(err == "GPU wave executor is gone" ? WC_ERR_GONE : WC_ERR_INVALID, err);
+    *out = new wc_ticket{t};
+    return WC_OK;
+}
+
+int wc_wait(wc_ticket* t, wc_result** out) {
+    if (!t || !out) return fail(WC_ERR_INVALID, "wc_wait: null argument");
+    std::shared_ptr<Ticket> tk = t->t;
+    delete t;
+    std::unique_lock<std::mutex> lk(tk->mu);
+    tk->cv.wait(lk, [&] { return tk->done; });
+    if (tk->rc != 0) return fail(tk->rc, tk->err);
+    *out = new wc_result;
+    (*out)->r = std::move(tk->result);
+    return WC_OK;
+}
+
+int wc_poll(const wc_ticket* t) {
+    if (!t) return 0;
+    std::lock_guard<std::mutex> lk(t->t->mu);
+    return t->t->done ? 1 : 0;
+}
+
+uint64_t wc_result_tag(const wc_result* r) { return r ? r->r.tag : 0; }
+uint64_t wc_result_weight_version(const wc_result* r) { return r ? r->r.weight_version : 0; }
+
+const float* wc_result_strategy(const wc_result* r, size_t* n) {
+    if (!r) {
+        if (n) *n = 0;
+        return nullptr;
+    }
+    if (n) *n = r->r.strategy.size();
+    return r->r.strategy.data();
+}
+
+const float* wc_result_root_values(const wc_result* r, uint32_t* nroots, uint32_t* n0, uint32_t* n1) {
+    if (!r) return nullptr;
+    if (nroots) *nroots = r->r.nroots;
+    if (n0) *n0 = r->r.n0;
+    if (n1) *n1 = r->r.n1;
+    return r->r.root_values.data();
+}
+
+const uint16_t* wc_result_carries(const wc_result* r, uint32_t* slots, uint32_t* snapshot_configs) {
+    if (!r) return nullptr;
+    if (slots) *slots = r->r.slots;
+    if (snapshot_configs) *snapshot_configs = r->r.snapshot_configs;
+    return r->r.carries.data();
+}
+
+void wc_result_free(wc_result* r) { delete r; }
+
+}  // extern "C"

@@ -1,0 +1,658 @@
+// Executor: weight banks, wave upload and the CFR schedule on one HIP stream.
+// The schedule follows engine/src/gpu/device.rs:641-718 (initialise, the
+// iteration loop with snapshots, Phase 2 per carried root).
+#include "executor.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "../../include/wc_wave.h"
+
+namespace wc {
+
+namespace {
+
+#define HIP_TRY(expr)                                                       \
+    do {                                                                    \
+        hipError_t e_ = (expr);                                             \
+        if (e_ != hipSuccess) {                                             \
+            if (err) *err = std::string(#expr ": ") + hipGetErrorString(e_); \
+            return false;                                                   \
+        }                                                                   \
+    } while (0)
+
+// `t^p / (t^p + 1)` with the infinities evaluated (engine/src/search.rs:185-193).
+float cfr_factor(float t, float p) {
+    if (std::isinf(p)) return p > 0.0f ? 1.0f : 0.0f;
+    float x = std::pow(t, p);
+    return x / (x + 1.0f);
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct Blob {
+    std::vector<uint8_t>& b;
+    explicit Blob(std::vector<uint8_t>& buf) : b(buf) { b.clear(); }
+    template <class T>
+    size_t put(const std::vector<T>& v) {
+        size_t at = align256(b.size());
+        b.resize(at + std::max<size_t>(v.size() * sizeof(T), 4), 0);
+        if (!v.empty()) std::memcpy(b.data() + at, v.data(), v.size() * sizeof(T));
+        return at;
+    }
+};
+
+}  // namespace
+
+Executor::Executor(int device, int precision) : device_(device), precision_(precision) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+        err_ = "no HIP device";
+        return;
+    }
+    if (device < 0 || device >= n) {
+        err_ = "device index out of range";
+        return;
+    }
+    if (precision < WC_PRECISE || precision > WC_BF16) {
+        err_ = "unknown precision";
+        return;
+    }
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking) != hipSuccess) {
+        err_ = "cannot create the executor stream";
+        return;
+    }
+    ok_ = true;
+}
+
+Executor::~Executor() {
+    if (!ok_) return;
+    hipSetDevice(device_);
+    hipStreamSynchronize(stream_);
+    for (auto& kv : banks_) hipFree(kv.second.mem);
+    hipFree(table_);
+    hipFree(arena_);
+    hipFree(mlp_);
+    hipStreamDestroy(stream_);
+}
+
+bool Executor::ensure(void** p, size_t* cap, size_t need, std::string* err) {
+    if (need <= *cap && *p) return true;
+    if (*p) {
+        HIP_TRY(hipStreamSynchronize(stream_));
+        HIP_TRY(hipFree(*p));
+        *p = nullptr;
+    }
+    size_t sz = 1;
+    while (sz < need) sz <<= 1;  // power-of-two reservation, as the reference's arena
+    HIP_TRY(hipMalloc(p, sz));
+    *cap = sz;
+    return true;
+}
+
+uint64_t Executor::publish(const NetShape& ns, const std::vector<uint32_t>& dims, const float* w, size_t nw,
+                           const float* b, size_t nb, std::string* err) {
+    if (ns.kind != MODEL_MLP) {
+        *err = "this executor builds the MLP leaf network only";
+        return 0;
+    }
+    if (ns.layers == 0 || ns.layers > 15) {
+        *err = "MLP depth out of range";
+        return 0;
+    }
+    size_t need_w = size_t(ns.in) * ns.hidden + size_t(ns.layers - 1) * ns.hidden * ns.hidden +
+                    size_t(ns.heads) * ns.hidden;
+    size_t need_b = size_t(ns.layers) * ns.hidden + ns.heads;
+    if (nw != need_w || nb != need_b) {
+        *err = "weight bank sizes disagree with dims";
+        return 0;
+    }
+    if (precision_ != WC_PRECISE && (ns.in % 32 || ns.hidden % 32)) {
+        *err = "the MFMA path needs input and hidden widths that are multiples of 32";
+        return 0;
+    }
+    if (hipSetDevice(device_) != hipSuccess) {
+        *err = "hipSetDevice failed";
+        return 0;
+    }
+    NetBank bank;
+    bank.ns = ns;
+    bank.precision = precision_;
+    const size_t esz = precision_ == WC_PRECISE ? 4 : 2;
+    // Layout: matrices (as stored for the arithmetic), then f32 biases.
+    std::vector<size_t> moff;
+    size_t at = 0;
+    std::vector<std::pair<size_t, size_t>> mats;  // (rows, cols) of each source matrix in w
+    mats.push_back({ns.in, ns.hidden});
+    for (uint32_t l = 1; l < ns.layers; l++) mats.push_back({ns.hidden, ns.hidden});
+    mats.push_back({ns.heads, ns.hidden});
+    for (auto& m : mats) {
+        moff.push_back(at);
+        at = align256(at + m.first * m.second * esz);
+    }
+    size_t boff = at;
+    at = align256(at + nb * 4);
+    // Staging for f32 -> 16-bit conversion on the device.
+    size_t stage = precision_ == WC_PRECISE ? 0 : at;
+    size_t total = at + (precision_ == WC_PRECISE ? 0 : nw * 4);
+    void* mem = nullptr;
+    if (hipMalloc(&mem, total) != hipSuccess) {
+        *err = "hipMalloc of the weight bank failed";
+        return 0;
+    }
+    char* base = (char*)mem;
+    bool okc = hipMemcpyAsync(base + boff, b, nb * 4, hipMemcpyHostToDevice, stream_) == hipSuccess;
+    if (precision_ == WC_PRECISE) {
+        size_t src = 0;
+        for (size_t k = 0; k < mats.size(); k++) {
+            size_t n = mats[k].first * mats[k].second;
+            okc = okc && hipMemcpyAsync(base + moff[k], w + src, n * 4, hipMemcpyHostToDevice, stream_) == hipSuccess;
+            src += n;
+        }
+    } else {
+        okc = okc && hipMemcpyAsync(base + stage, w, nw * 4, hipMemcpyHostToDevice, stream_) == hipSuccess;
+        size_t src = 0;
+        for (size_t k = 0; k < mats.size(); k++) {
+            size_t n = mats[k].first * mats[k].second;
+            // Trunk matrices [K x N] are stored transposed ([N x K], K-contiguous);
+            // the head is already one K-contiguous row per output.
+            bool transpose = k + 1 < mats.size();
+            launch_to16(precision_, (const float*)(base + stage) + src, base + moff[k], (uint32_t)mats[k].first,
+                        (uint32_t)mats[k].second, transpose, stream_);
+            src += n;
+        }
+    }
+    okc = okc && hipStreamSynchronize(stream_) == hipSuccess && hipGetLastError() == hipSuccess;
+    if (!okc) {
+        hipFree(mem);
+        *err = "weight upload failed";
+        return 0;
+    }
+    bank.mem = mem;
+    for (uint32_t l = 0; l < ns.layers; l++) {
+        bank.W[l] = base + moff[l];
+        bank.B[l] = (const float*)(base + boff) + size_t(l) * ns.hidden;
+    }
+    bank.Whead = base + moff[ns.layers];
+    bank.bhead = (const float*)(base + boff) + size_t(ns.layers) * ns.hidden;
+    bank.version = next_version_++;
+    (void)dims;
+    banks_[bank.version] = bank;
+    return bank.version;
+}
+
+void Executor::retain_from(uint64_t oldest) {
+    hipSetDevice(device_);
+    for (auto it = banks_.begin(); it != banks_.end();) {
+        if (it->first < oldest) {
+            hipStreamSynchronize(stream_);
+            hipFree(it->second.mem);
+            it = banks_.erase(it);
+        } else {
+            ++it;
+        }
+    }
+}
+
+bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) {
+    const NetShape& ns = bank.ns;
+    if (w.net.kind != ns.kind || w.net.in != ns.in || w.net.hidden != ns.hidden || w.net.pool != ns.pool ||
+        w.net.heads != ns.heads || w.net.layers != ns.layers) {
+        *err = "wave network shape disagrees with the weight bank";
+        return false;
+    }
+    HIP_TRY(hipSetDevice(device_));
+    Blob blob(host_blob_);
+    struct Off {
+        size_t node_meta, nc, child_start, child, legal_row_of, legal_off, legal_value, draw_off, draw_row_off,
+            draw_row_start, draw_to, draw_p, reach_base, vals_base, parent, rev_row_of, rev_start, rev_src, rev_cell,
+            rvd_row_of, rvd_start, rvd_src, rvd_p, row_node, row_cfg_off, row_cfg, cfg_key, cfg_emb, pub_raw,
+            term_node, term_util, roots, carried, exit_node, exit_coff, trees, bt0, bt1, rt0, rt1, d0, d1, bl0, bl1,
+            rl0, rl1;
+    } o;
+    o.node_meta = blob.put(w.node_meta);
+    o.nc = blob.put(w.node_nc);
+    o.child_start = blob.put(w.child_start);
+    o.child = blob.put(w.child);
+    o.legal_row_of = blob.put(w.legal_row_of);
+    o.legal_off = blob.put(w.legal_off);
+    o.legal_value = blob.put(w.legal_value);
+    o.draw_off = blob.put(w.draw_off);
+    o.draw_row_off = blob.put(w.draw_row_off);
+    o.draw_row_start = blob.put(w.draw_row_start);
+    o.draw_to = blob.put(w.draw_to);
+    o.draw_p = blob.put(w.draw_p);
+    o.reach_base = blob.put(w.reach_base);
+    o.vals_base = blob.put(w.vals_base);
+    o.parent = blob.put(w.parent);
+    o.rev_row_of = blob.put(w.rev_row_of);
+    o.rev_start = blob.put(w.rev_start);
+    o.rev_src = blob.put(w.rev_src);
+    o.rev_cell = blob.put(w.rev_cell);
+    o.rvd_row_of = blob.put(w.rvd_row_of);
+    o.rvd_start = blob.put(w.rvd_start);
+    o.rvd_src = blob.put(w.rvd_src);
+    o.rvd_p = blob.put(w.rvd_p);
+    o.row_node = blob.put(w.row_node);
+    o.row_cfg_off = blob.put(w.row_cfg_off);
+    o.row_cfg = blob.put(w.row_cfg);
+    o.cfg_key = blob.put(w.cfg_key);
+    o.cfg_emb = blob.put(w.cfg_emb);
+    o.pub_raw = blob.put(w.pub_raw);
+    o.term_node = blob.put(w.term_node);
+    o.term_util = blob.put(w.term_util);
+    o.roots = blob.put(w.roots);
+    o.carried = blob.put(w.carried);
+    o.exit_node = blob.put(w.exit_node);
+    o.exit_coff = blob.put(w.exit_coff);
+    o.trees = blob.put(w.trees);
+    o.bt0 = blob.put(w.back_task[0]);
+    o.bt1 = blob.put(w.back_task[1]);
+    o.rt0 = blob.put(w.reach_task[0]);
+    o.rt1 = blob.put(w.reach_task[1]);
+    o.d0 = blob.put(w.decision[0]);
+    o.d1 = blob.put(w.decision[1]);
+    o.bl0 = blob.put(w.back_lvl[0]);
+    o.bl1 = blob.put(w.back_lvl[1]);
+    o.rl0 = blob.put(w.reach_lvl[0]);
+    o.rl1 = blob.put(w.reach_lvl[1]);
+    if (!ensure(&table_, &table_cap_, host_blob_.size(), err)) return false;
+    HIP_TRY(hipMemcpyAsync(table_, host_blob_.data(), host_blob_.size(), hipMemcpyHostToDevice, stream_));
+
+    // Mutable arena.
+    const size_t cells = std::max<uint32_t>(w.ncells, 1), rl = std::max<uint32_t>(w.reach_len, 1),
+                 vl = std::max<uint32_t>(w.vals_len, 1), rows = w.rows();
+    size_t at = 0;
+    auto take = [&](size_t bytes) {
+        size_t a = align256(at);
+        at = a + std::max<size_t>(bytes, 4);
+        return a;
+    };
+    size_t a_regret = take(cells * 4), a_cur = take(cells * 4), a_sum = take(cells * 4), a_snap = take(cells * 4);
+    size_t a_reach = take(rl * 4), a_sreach = take(rl * 4), a_vals = take(vl * 4);
+    size_t a_pooled = take(rows * 2 * ns.pool * 4), a_mass = take(rows * 2 * 4);
+    size_t a_roots = take(size_t(w.root_values_len) * 4);
+    size_t a_carry = take(size_t(w.carry_slots) * w.snapshot_configs * 2);
+    if (!ensure(&arena_, &arena_cap_, at, err)) return false;
+    // Leaf-network activations.
+    const size_t esz = precision_ == WC_PRECISE ? 4 : 2;
+    size_t mt = 0;
+    auto mtake = [&](size_t bytes) {
+        size_t a = align256(mt);
+        mt = a + std::max<size_t>(bytes, 4);
+        return a;
+    };
+    size_t m_x = mtake(rows * ns.in * esz), m_h0 = mtake(rows * ns.hidden * esz), m_h1 = mtake(rows * ns.hidden * esz),
+           m_out = mtake(rows * ns.heads * 4);
+    if (!ensure(&mlp_, &mlp_cap_, mt, err)) return false;
+
+    char* T = (char*)table_;
+    char* A = (char*)arena_;
+    char* M = (char*)mlp_;
+    WaveDev& d = dev_;
+    d = WaveDev{};
+    d.node_meta = (const uint32_t*)(T + o.node_meta);
+    d.nc = (const uint32_t*)(T + o.nc);
+    d.child_start = (const uint32_t*)(T + o.child_start);
+    d.child = (const uint32_t*)(T + o.child);
+    d.legal_row_of = (const uint32_t*)(T + o.legal_row_of);
+    d.legal_off = (const uint32_t*)(T + o.legal_off);
+    d.legal_value = (const uint32_t*)(T + o.legal_value);
+    d.draw_off = (const uint32_t*)(T + o.draw_off);
+    d.draw_row_off = (const uint32_t*)(T + o.draw_row_off);
+    d.draw_row_start = (const uint32_t*)(T + o.draw_row_start);
+    d.draw_to = (const uint32_t*)(T + o.draw_to);
+    d.draw_p = (const float*)(T + o.draw_p);
+    d.reach_base = (const uint32_t*)(T + o.reach_base);
+    d.vals_base = (const uint32_t*)(T + o.vals_base);
+    d.parent = (const uint32_t*)(T + o.parent);
+    d.rev_row_of = (const uint32_t*)(T + o.rev_row_of);
+    d.rev_start = (const uint32_t*)(T + o.rev_start);
+    d.rev_src = (const uint32_t*)(T + o.rev_src);
+    d.rev_cell = (const uint32_t*)(T + o.rev_cell);
+    d.rvd_row_of = (const uint32_t*)(T + o.rvd_row_of);
+    d.rvd_start = (const uint32_t*)(T + o.rvd_start);
+    d.rvd_src = (const uint32_t*)(T + o.rvd_src);
+    d.rvd_p = (const float*)(T + o.rvd_p);
+    d.row_node = (const uint32_t*)(T + o.row_node);
+    d.row_cfg_off = (const uint32_t*)(T + o.row_cfg_off);
+    d.row_cfg = (const uint32_t*)(T + o.row_cfg);
+    d.cfg_key = (const uint32_t*)(T + o.cfg_key);
+    d.cfg_emb = (const float*)(T + o.cfg_emb);
+    d.pub_raw = (const uint8_t*)(T + o.pub_raw);
+    d.term_node = (const uint32_t*)(T + o.term_node);
+    d.term_util = (const float*)(T + o.term_util);
+    d.roots = (const float*)(T + o.roots);
+    d.carried = (const float*)(T + o.carried);
+    d.exit_node = (const uint32_t*)(T + o.exit_node);
+    d.exit_coff = (const uint32_t*)(T + o.exit_coff);
+    d.trees = (const TreeDev*)(T + o.trees);
+    d.back_task0 = (const Task*)(T + o.bt0);
+    d.back_task1 = (const Task*)(T + o.bt1);
+    d.reach_task0 = (const Task*)(T + o.rt0);
+    d.reach_task1 = (const Task*)(T + o.rt1);
+    d.decision0 = (const Task*)(T + o.d0);
+    d.decision1 = (const Task*)(T + o.d1);
+    d.back_lvl0 = (const uint32_t*)(T + o.bl0);
+    d.back_lvl1 = (const uint32_t*)(T + o.bl1);
+    d.reach_lvl0 = (const uint32_t*)(T + o.rl0);
+    d.reach_lvl1 = (const uint32_t*)(T + o.rl1);
+    d.regret = (float*)(A + a_regret);
+    d.cur = (float*)(A + a_cur);
+    d.sum = (float*)(A + a_sum);
+    d.snap = (float*)(A + a_snap);
+    d.reach = (float*)(A + a_reach);
+    d.snap_reach = (float*)(A + a_sreach);
+    d.vals = (float*)(A + a_vals);
+    d.pooled = (float*)(A + a_pooled);
+    d.mass = (float*)(A + a_mass);
+    d.root_values = (float*)(A + a_roots);
+    d.carry = (uint16_t*)(A + a_carry);
+    d.ntrees = (uint32_t)w.trees.size();
+    d.rows = w.rows();
+    d.pool = ns.pool;
+    d.in = ns.in;
+    d.row_bytes = ns.row_bytes;
+    d.snapshot_configs = w.snapshot_configs;
+    d.nexit = (uint32_t)w.exit_node.size();
+    d.ncells = w.ncells;
+    d.ndec0 = (uint32_t)w.decision[0].size();
+    d.ndec1 = (uint32_t)w.decision[1].size();
+    X_ = M + m_x;
+    H_[0] = M + m_h0;
+    H_[1] = M + m_h1;
+    head_out_ = (float*)(M + m_out);
+    rows_ = w.rows();
+    HIP_TRY(hipStreamSynchronize(stream_));
+    return true;
+}
+
+void Executor::run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::vector<hipEvent_t>* marks) {
+    const NetShape& ns = bank.ns;
+    auto mark = [&]() {
+        if (marks) {
+            hipEvent_t e;
+            hipEventCreate(&e);
+            hipEventRecord(e, stream_);
+            marks->push_back(e);
+        }
+    };
+    const void* in = x;
+    uint32_t k = ns.in;
+    for (uint32_t l = 0; l < ns.layers; l++) {
+        void* out = H_[l & 1];
+        if (precision_ == WC_PRECISE)
+            launch_dense_exact((const float*)in, k, (const float*)bank.W[l], bank.B[l], ns.hidden, (float*)out, rows,
+                               stream_);
+        else
+            launch_gemm16(precision_, in, k, bank.W[l], bank.B[l], ns.hidden, out, rows, true, true, stream_);
+        mark();
+        in = out;
+        k = ns.hidden;
+    }
+    if (precision_ == WC_PRECISE)
+        launch_head_exact((const float*)in, ns.hidden, (const float*)bank.Whead, bank.bhead, ns.heads, head_out_,
+                          rows, stream_);
+    else
+        launch_gemm16(precision_, in, ns.hidden, bank.Whead, bank.bhead, ns.heads, head_out_, rows, false, false,
+                      stream_);
+    mark();
+}
+
+void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTimes* prof) {
+    const WaveDev& d = dev_;
+    hipStream_t s = stream_;
+    const Meta& m = w.meta;
+    // Per-class attribution: an event after every launch group, binned by class.
+    std::vector<std::pair<hipEvent_t, int>> ev;
+    enum { C_CFR = 0, C_MLP = 1, C_LEAF = 2, C_OTHER = 3 };
+    hipEvent_t start = nullptr;
+    auto mark = [&](int cls) {
+        if (!prof) return;
+        hipEvent_t e;
+        hipEventCreate(&e);
+        hipEventRecord(e, s);
+        ev.push_back({e, cls});
+    };
+    if (prof) {
+        hipEventCreate(&start);
+        hipEventRecord(start, s);
+    }
+    auto mlp = [&](int q) {
+        launch_build_x(d, q, precision_, X_, s);
+        mark(C_LEAF);
+        run_mlp(bank, d.rows, X_, nullptr);
+        mark(C_MLP);
+    };
+
+    launch_zero(d.regret, w.ncells, s);
+    launch_init_strategy(d, s);
+    launch_seed_reach(d, d.reach, -1, s);
+    launch_reach_both(d, d.reach, d.cur, s);
+    launch_seed_sum(d, s);
+    if (w.carry_slots) launch_gather_carry(d, d.reach, 0, s);
+    launch_pool(d, -1, s);
+    mark(C_OTHER);
+    if (m.iters == 0) launch_normalize(d, 0, 0, s);
+    for (uint32_t t = 0; t < m.iters; t++) {
+        const int p = (int)(t & 1);
+        mlp(p);
+        const float mm = (float)(t / 2 + 1);
+        const float da = cfr_factor(mm, m.cfr.alpha), db = cfr_factor(mm, m.cfr.beta);
+        const float ds = std::pow(mm / (mm + 1.0f), m.cfr.gamma);
+        launch_cfr(d, head_out_, bank.ns.heads, p, MODE_REGRET, da, db, ds, m.cfr.predict, s);
+        mark(C_CFR);
+        launch_pool(d, p, s);
+        mark(C_LEAF);
+        const uint32_t done = t + 1;
+        auto it = std::find(m.snap_iters.begin(), m.snap_iters.end(), done);
+        if (it != m.snap_iters.end() && (m.snapshots || done == m.iters)) {
+            size_t si = size_t(it - m.snap_iters.begin());
+            launch_normalize(d, 1, done >= 2 ? 1 : 0, s);
+            if (m.snapshots && si + 1 < m.snap_iters.size()) {
+                launch_seed_reach(d, d.snap_reach, -1, s);
+                launch_reach_both(d, d.snap_reach, d.snap, s);
+                launch_gather_carry(d, d.snap_reach, (int)si, s);
+            }
+            mark(C_OTHER);
+        }
+    }
+    // Phase 2: root values under the final average for every carried root.
+    for (uint32_t root = 0; root < w.nroots_max; root++) {
+        launch_seed_reach(d, d.reach, (int)root, s);
+        launch_reach_both(d, d.reach, d.snap, s);
+        mark(C_OTHER);
+        launch_pool(d, -1, s);
+        mark(C_LEAF);
+        for (int p = 0; p < 2; p++) {
+            mlp(p);
+            launch_cfr(d, head_out_, bank.ns.heads, p, MODE_VALUE, 0.0f, 0.0f, 0.0f, 0.0f, s);
+            launch_collect_root(d, (int)root, p, s);
+            mark(C_OTHER);
+        }
+    }
+    if (prof) {
+        hipStreamSynchronize(s);
+        *prof = ScheduleTimes{};
+        hipEvent_t prev = start;
+        double regret_cfr = 0;
+        uint32_t regret_n = 0;
+        for (auto& e : ev) {
+            float ms = 0.0f;
+            hipEventElapsedTime(&ms, prev, e.first);
+            switch (e.second) {
+                case C_CFR:
+                    prof->cfr += ms;
+                    regret_cfr += ms;
+                    regret_n++;
+                    break;
+                case C_MLP: prof->mlp += ms; break;
+                case C_LEAF: prof->leaf_input += ms; break;
+                default: prof->other += ms;
+            }
+            prev = e.first;
+        }
+        float tot = 0.0f;
+        if (!ev.empty()) hipEventElapsedTime(&tot, start, ev.back().first);
+        prof->total = tot;
+        prof->cfr_launches = regret_n;
+        prof->cfr_launch_mean = regret_n ? regret_cfr / regret_n : 0.0;
+        for (auto& e : ev) hipEventDestroy(e.first);
+        hipEventDestroy(start);
+    }
+}
+
+bool Executor::solve(const WaveHost& w, uint64_t version, std::vector<Result>* out, std::string* err) {
+    auto it = banks_.find(version);
+    if (it == banks_.end()) {
+        *err = "GPU weight version " + std::to_string(version) + " is unavailable";
+        return false;
+    }
+    if (!upload(w, it->second, err)) return false;
+    run_schedule(w, it->second, nullptr);
+    HIP_TRY(hipGetLastError());
+    // Collect (Harvest::unpack): per-job slices back to solve-local indices.
+    std::vector<float> strat(w.ncells), roots(w.root_values_len);
+    std::vector<uint16_t> carry(size_t(w.carry_slots) * w.snapshot_configs);
+    if (w.ncells) HIP_TRY(hipMemcpyAsync(strat.data(), dev_.snap, strat.size() * 4, hipMemcpyDeviceToHost, stream_));
+    if (!roots.empty())
+        HIP_TRY(hipMemcpyAsync(roots.data(), dev_.root_values, roots.size() * 4, hipMemcpyDeviceToHost, stream_));
+    if (!carry.empty())
+        HIP_TRY(hipMemcpyAsync(carry.data(), dev_.carry, carry.size() * 2, hipMemcpyDeviceToHost, stream_));
+    HIP_TRY(hipStreamSynchronize(stream_));
+    out->clear();
+    uint32_t cell0 = 0, cfg0 = 0;
+    for (size_t k = 0; k < w.jobs.size(); k++) {
+        const Job& j = w.jobs[k];
+        const TreeDev& t = w.trees[k];
+        Result r;
+        r.weight_version = version;
+        r.strategy.assign(strat.begin() + cell0, strat.begin() + cell0 + j.t.ncells);
+        r.nroots = t.nroots;
+        r.n0 = t.n0;
+        r.n1 = t.n1;
+        r.root_values.assign(roots.begin() + t.root_value0, roots.begin() + t.root_value0 + t.nroots * (t.n0 + t.n1));
+        r.slots = w.carry_slots;
+        r.snapshot_configs = j.t.snapshot_configs();
+        r.carries.resize(size_t(r.slots) * r.snapshot_configs);
+        for (uint32_t sl = 0; sl < r.slots; sl++)
+            std::memcpy(r.carries.data() + size_t(sl) * r.snapshot_configs,
+                        carry.data() + size_t(sl) * w.snapshot_configs + cfg0, size_t(r.snapshot_configs) * 2);
+        cell0 += j.t.ncells;
+        cfg0 += r.snapshot_configs;
+        out->push_back(std::move(r));
+    }
+    return true;
+}
+
+bool Executor::time_wave(const WaveHost& w, uint64_t version, uint32_t reps, double* wave_ms, ScheduleTimes* prof,
+                         std::string* err) {
+    auto it = banks_.find(version);
+    if (it == banks_.end()) {
+        *err = "GPU weight version " + std::to_string(version) + " is unavailable";
+        return false;
+    }
+    if (!upload(w, it->second, err)) return false;
+    run_schedule(w, it->second, nullptr);  // warm
+    HIP_TRY(hipStreamSynchronize(stream_));
+    HIP_TRY(hipGetLastError());
+    hipEvent_t a, b;
+    HIP_TRY(hipEventCreate(&a));
+    HIP_TRY(hipEventCreate(&b));
+    HIP_TRY(hipEventRecord(a, stream_));
+    for (uint32_t r = 0; r < reps; r++) run_schedule(w, it->second, nullptr);
+    HIP_TRY(hipEventRecord(b, stream_));
+    HIP_TRY(hipEventSynchronize(b));
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, a, b));
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    *wave_ms = reps ? ms / reps : 0.0;
+    if (prof) run_schedule(w, it->second, prof);
+    HIP_TRY(hipGetLastError());
+    return true;
+}
+
+bool Executor::mlp_forward(uint64_t version, uint32_t rows, const float* x, float* out, std::string* err) {
+    auto it = banks_.find(version);
+    if (it == banks_.end()) {
+        *err = "GPU weight version unavailable";
+        return false;
+    }
+    const NetShape& ns = it->second.ns;
+    HIP_TRY(hipSetDevice(device_));
+    const size_t esz = precision_ == WC_PRECISE ? 4 : 2;
+    size_t mt = 0;
+    auto mtake = [&](size_t bytes) {
+        size_t a = align256(mt);
+        mt = a + std::max<size_t>(bytes, 4);
+        return a;
+    };
+    size_t m_x = mtake(size_t(rows) * ns.in * esz), m_h0 = mtake(size_t(rows) * ns.hidden * esz),
+           m_h1 = mtake(size_t(rows) * ns.hidden * esz), m_out = mtake(size_t(rows) * ns.heads * 4),
+           m_stage = mtake(size_t(rows) * ns.in * 4);
+    if (!ensure(&mlp_, &mlp_cap_, mt, err)) return false;
+    char* M = (char*)mlp_;
+    X_ = M + m_x;
+    H_[0] = M + m_h0;
+    H_[1] = M + m_h1;
+    head_out_ = (float*)(M + m_out);
+    if (precision_ == WC_PRECISE) {
+        HIP_TRY(hipMemcpyAsync(X_, x, size_t(rows) * ns.in * 4, hipMemcpyHostToDevice, stream_));
+    } else {
+        HIP_TRY(hipMemcpyAsync(M + m_stage, x, size_t(rows) * ns.in * 4, hipMemcpyHostToDevice, stream_));
+        launch_to16(precision_, (const float*)(M + m_stage), X_, rows, ns.in, false, stream_);
+    }
+    run_mlp(it->second, rows, X_, nullptr);
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipMemcpyAsync(out, head_out_, size_t(rows) * ns.heads * 4, hipMemcpyDeviceToHost, stream_));
+    HIP_TRY(hipStreamSynchronize(stream_));
+    rows_ = 0;  // the wave buffers were repurposed; a later wave re-uploads
+    return true;
+}
+
+bool Executor::time_mlp(uint64_t version, uint32_t rows, const float* x, uint32_t reps, double* chain_ms,
+                        std::vector<double>* layer_ms, std::string* err) {
+    auto it = banks_.find(version);
+    if (it == banks_.end()) {
+        *err = "GPU weight version unavailable";
+        return false;
+    }
+    std::vector<float> tmp(size_t(rows) * it->second.ns.heads);
+    if (!mlp_forward(version, rows, x, tmp.data(), err)) return false;  // uploads x, warms
+    hipEvent_t a, b;
+    HIP_TRY(hipEventCreate(&a));
+    HIP_TRY(hipEventCreate(&b));
+    HIP_TRY(hipEventRecord(a, stream_));
+    for (uint32_t r = 0; r < reps; r++) run_mlp(it->second, rows, X_, nullptr);
+    HIP_TRY(hipEventRecord(b, stream_));
+    HIP_TRY(hipEventSynchronize(b));
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, a, b));
+    *chain_ms = reps ? ms / reps : 0.0;
+    if (layer_ms) {
+        std::vector<hipEvent_t> marks;
+        hipEvent_t s0;
+        HIP_TRY(hipEventCreate(&s0));
+        HIP_TRY(hipEventRecord(s0, stream_));
+        run_mlp(it->second, rows, X_, &marks);
+        HIP_TRY(hipStreamSynchronize(stream_));
+        layer_ms->clear();
+        hipEvent_t prev = s0;
+        for (auto e : marks) {
+            float lm = 0.0f;
+            hipEventElapsedTime(&lm, prev, e);
+            layer_ms->push_back(lm);
+            prev = e;
+        }
+        for (auto e : marks) hipEventDestroy(e);
+        hipEventDestroy(s0);
+    }
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    HIP_TRY(hipGetLastError());
+    return true;
+}
+
+}  // namespace wc

@@ -1,0 +1,102 @@
+// One device, one stream: weight banks, wave upload, the CFR schedule, results.
+// Counterpart of the reference's `Executor` (engine/src/gpu/device.rs:515-831).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "job.h"
+#include "kernels.h"
+#include "wave.h"
+
+namespace wc {
+
+struct NetBank {
+    uint64_t version = 0;
+    NetShape ns;
+    int precision = 0;
+    void* mem = nullptr;  // one device allocation holding every matrix and bias
+    const void* W[16] = {};
+    const float* B[16] = {};
+    const void* Whead = nullptr;
+    const float* bhead = nullptr;
+};
+
+struct Result {
+    uint64_t tag = 0;
+    uint64_t weight_version = 0;
+    std::vector<float> strategy;
+    uint32_t nroots = 0, n0 = 0, n1 = 0;
+    std::vector<float> root_values;
+    uint32_t slots = 0, snapshot_configs = 0;
+    std::vector<uint16_t> carries;
+};
+
+// Per-launch-class device times of one schedule (milliseconds), from HIP events.
+struct ScheduleTimes {
+    double total = 0, cfr = 0, mlp = 0, leaf_input = 0, other = 0;
+    double cfr_launch_mean = 0;  // mean duration of one CFR-sweep launch
+    uint32_t cfr_launches = 0;
+};
+
+class Executor {
+  public:
+    Executor(int device, int precision);
+    ~Executor();
+    bool ok() const { return ok_; }
+    const std::string& error() const { return err_; }
+    int device() const { return device_; }
+    int precision() const { return precision_; }
+    hipStream_t stream() const { return stream_; }
+
+    // Publish an immutable weight bank; returns its version (0 on failure).
+    uint64_t publish(const NetShape& ns, const std::vector<uint32_t>& dims, const float* w, size_t nw,
+                     const float* b, size_t nb, std::string* err);
+    void retain_from(uint64_t oldest);
+    bool has_version(uint64_t v) const { return banks_.count(v) != 0; }
+
+    // Upload, run the whole schedule, collect one result per job.
+    bool solve(const WaveHost& w, uint64_t version, std::vector<Result>* out, std::string* err);
+    // Upload once, run `reps` schedules; mean wave time, and per-class times of
+    // one extra profiled schedule.
+    bool time_wave(const WaveHost& w, uint64_t version, uint32_t reps, double* wave_ms, ScheduleTimes* prof,
+                   std::string* err);
+    // The leaf GEMM chain alone on rows x in host inputs.
+    bool mlp_forward(uint64_t version, uint32_t rows, const float* x, float* out, std::string* err);
+    bool time_mlp(uint64_t version, uint32_t rows, const float* x, uint32_t reps, double* chain_ms,
+                  std::vector<double>* layer_ms, std::string* err);
+
+  private:
+    bool upload(const WaveHost& w, const NetBank& bank, std::string* err);
+    void run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTimes* prof);
+    void run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::vector<hipEvent_t>* marks);
+    bool ensure(void** p, size_t* cap, size_t need, std::string* err);
+
+    int device_ = 0, precision_ = 0;
+    bool ok_ = false;
+    std::string err_;
+    hipStream_t stream_ = nullptr;
+    std::map<uint64_t, NetBank> banks_;
+    uint64_t next_version_ = 1;
+
+    // Device buffers of the current wave (grow-only).
+    void* table_ = nullptr;
+    size_t table_cap_ = 0;
+    void* arena_ = nullptr;
+    size_t arena_cap_ = 0;
+    void* mlp_ = nullptr;  // query inputs, hidden activations, head outputs
+    size_t mlp_cap_ = 0;
+    std::vector<uint8_t> host_blob_;
+    WaveDev dev_{};
+    void* X_ = nullptr;
+    void* H_[2] = {};
+    float* head_out_ = nullptr;
+    uint32_t rows_ = 0;
+};
+
+}  // namespace wc

@@ -1,0 +1,75 @@
+// Device-side view of a packed wave: table and arena pointers passed to every
+// kernel by value.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "wave.h"
+
+namespace wc {
+
+enum : int { MODE_REGRET = 0, MODE_VALUE = 1 };
+
+struct WaveDev {
+    // immutable tables
+    const uint32_t *node_meta, *nc, *child_start, *child;
+    const uint32_t *legal_row_of, *legal_off, *legal_value;
+    const uint32_t *draw_off, *draw_row_off, *draw_row_start, *draw_to;
+    const float* draw_p;
+    const uint32_t *reach_base, *vals_base, *parent;
+    const uint32_t *rev_row_of, *rev_start, *rev_src, *rev_cell;
+    const uint32_t *rvd_row_of, *rvd_start, *rvd_src;
+    const float* rvd_p;
+    const uint32_t *row_node, *row_cfg_off, *row_cfg, *cfg_key;
+    const float* cfg_emb;
+    const uint8_t* pub_raw;
+    const uint32_t* term_node;
+    const float* term_util;
+    const float *roots, *carried;
+    const uint32_t *exit_node, *exit_coff;
+    const TreeDev* trees;
+    const Task *back_task0, *back_task1, *reach_task0, *reach_task1, *decision0, *decision1;
+    const uint32_t *back_lvl0, *back_lvl1, *reach_lvl0, *reach_lvl1;
+    // mutable arena
+    float *regret, *cur, *sum, *snap;
+    float *reach, *snap_reach, *vals;
+    float *pooled, *mass, *root_values;
+    uint16_t* carry;
+    // sizes
+    uint32_t ntrees, rows, pool, in, row_bytes, snapshot_configs, nexit, ncells;
+    uint32_t ndec0, ndec1;
+};
+
+// Launchers (kernels.hip). All take the executor's stream.
+void launch_zero(float* p, size_t n, hipStream_t s);
+void launch_init_strategy(const WaveDev& w, hipStream_t s);
+void launch_seed_reach(const WaveDev& w, float* reach, int root_index, hipStream_t s);
+void launch_reach_both(const WaveDev& w, float* reach, const float* strat, hipStream_t s);
+void launch_seed_sum(const WaveDev& w, hipStream_t s);
+void launch_pool(const WaveDev& w, int player /* -1 = both */, hipStream_t s);
+void launch_build_x(const WaveDev& w, int traverser, int precision, void* x, hipStream_t s);
+void launch_cfr(const WaveDev& w, const float* head_out, uint32_t heads, int traverser, int mode, float da,
+                float db, float ds, float predict, hipStream_t s);
+void launch_normalize(const WaveDev& w, int touched0, int touched1, hipStream_t s);
+void launch_gather_carry(const WaveDev& w, const float* reach, int slot, hipStream_t s);
+void launch_collect_root(const WaveDev& w, int root, int player, hipStream_t s);
+
+// Leaf MLP.
+// Exact float32 dense ReLU layer in the CPU loop order: Y = relu(X W + b), W [K x N] row-major.
+void launch_dense_exact(const float* X, uint32_t K, const float* W, const float* b, uint32_t N, float* Y,
+                        uint32_t rows, hipStream_t s);
+// Exact float32 head: out[r, k] = b[k] + sum_j Wh[k, j] H[r, j], Wh [heads x hidden].
+void launch_head_exact(const float* H, uint32_t hidden, const float* Wh, const float* bh, uint32_t heads,
+                       float* out, uint32_t rows, hipStream_t s);
+// MFMA GEMM: Y[M, N] = act(X[M, K] Wt[N, K]^T + b); 16-bit operands, f32 accumulate.
+// precision WC_F16 / WC_BF16; relu selects the activation; out16 selects a 16-bit
+// (next-layer operand) or f32 output.
+void launch_gemm16(int precision, const void* X, uint32_t K, const void* Wt, const float* b, uint32_t N,
+                   void* Y, uint32_t M, bool relu, bool out16, hipStream_t s);
+// Convert f32 -> 16-bit operands (row-major copy, or transposing [K x N] -> [N x K]).
+void launch_to16(int precision, const float* src, void* dst, uint32_t rows, uint32_t cols, bool transpose,
+                 hipStream_t s);
+
+}  // namespace wc

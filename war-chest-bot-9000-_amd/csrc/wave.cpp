@@ -1,0 +1,447 @@
+// Host wave packing (counterpart of engine/src/gpu/wave.rs:132-644).
+#include "wave.h"
+
+#include <algorithm>
+#include <cstring>
+
+namespace wc {
+
+namespace {
+
+bool same_meta(const Meta& a, const Meta& b) {
+    auto bits = [](float x) {
+        uint32_t u;
+        std::memcpy(&u, &x, 4);
+        return u;
+    };
+    return a.depth == b.depth && a.iters == b.iters && a.snapshots == b.snapshots &&
+           bits(a.cfr.alpha) == bits(b.cfr.alpha) && bits(a.cfr.beta) == bits(b.cfr.beta) &&
+           bits(a.cfr.gamma) == bits(b.cfr.gamma) && bits(a.cfr.predict) == bits(b.cfr.predict) &&
+           a.snap_iters == b.snap_iters && a.net_dims == b.net_dims;
+}
+
+// Per-player value slots: the two players share one span (values are built for
+// one traverser at a time); across a chance edge the non-drawing player's
+// vector is its sole child's and aliases it (engine/src/serialize.rs:447-480).
+bool value_layout(const Tables& t, std::vector<uint32_t> base[2], uint32_t* len, std::string* err) {
+    uint32_t lengths[2] = {0, 0};
+    for (int p = 0; p < 2; p++) {
+        base[p].assign(t.nodes, 0);
+        std::vector<uint8_t> ready(t.nodes, 0);
+        uint32_t at = 0;
+        for (size_t k = t.bfs_order.size(); k-- > 0;) {
+            uint32_t node = t.bfs_order[k];
+            if (t.node_kind[node] == 1 && t.node_player[node] != p) {
+                uint32_t lo = t.node_child_start[node], hi = t.node_child_start[node + 1];
+                if (hi != lo + 1) {
+                    *err = "chance node without exactly one child";
+                    return false;
+                }
+                uint32_t child = t.node_child[lo];
+                if (!ready[child]) {
+                    *err = "value layout: child not ready (bfs order)";
+                    return false;
+                }
+                base[p][node] = base[p][child];
+            } else {
+                base[p][node] = at;
+                at += t.nc(node, p);
+            }
+            ready[node] = 1;
+        }
+        lengths[p] = at;
+    }
+    *len = std::max(lengths[0], lengths[1]);
+    return true;
+}
+
+template <class T>
+void append_shift(std::vector<T>& dst, const std::vector<T>& src, size_t skip, T add, bool keep_none) {
+    for (size_t k = skip; k < src.size(); k++) {
+        T x = src[k];
+        dst.push_back(keep_none && x == (T)NONE ? x : (T)(x + add));
+    }
+}
+
+}  // namespace
+
+bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err) {
+    if (jobs.empty()) {
+        *err = "cannot pack an empty wave";
+        return false;
+    }
+    WaveHost w;
+    w.meta = jobs[0].meta;
+    for (size_t k = 1; k < jobs.size(); k++)
+        if (!same_meta(jobs[0].meta, jobs[k].meta)) {
+            *err = "wave mixes different CFR schedules";
+            return false;
+        }
+    if (!w.net.parse(w.meta.net_dims, err)) return false;
+    if (w.net.kind == MODEL_V5) {
+        *err = "the v5 leaf network is not built by this executor";
+        return false;
+    }
+    for (auto& j : jobs)
+        if (!validate(j, err)) return false;
+    for (uint32_t x : w.meta.snap_iters)
+        if (x > w.meta.iters) {
+            *err = "snap_iters beyond iters";
+            return false;
+        }
+
+    w.legal_off.push_back(0);
+    w.child_start.clear();
+    w.rev_start.push_back(0);
+    w.rvd_start.push_back(0);
+    w.row_cfg_off.push_back(0);
+    w.exit_coff.push_back(0);
+    for (int p = 0; p < 2; p++) {
+        w.back_lvl[p].clear();
+        w.reach_lvl[p].clear();
+    }
+    uint32_t cfg_total = 0;
+
+    for (const Job& job : jobs) {
+        const Tables& t = job.t;
+        const uint32_t N = t.nodes;
+        const uint32_t node0 = w.nodes();
+        const uint32_t child0 = (uint32_t)w.child.size();
+        const uint32_t legal_row0 = (uint32_t)w.legal_off.size() - 1;
+        const uint32_t cell0 = w.ncells;
+        const uint32_t draw0 = (uint32_t)w.draw_to.size();
+        const uint32_t draw_row0 = (uint32_t)w.draw_row_start.size();
+        const uint32_t reach0 = w.reach_len;
+        const uint32_t vals0 = w.vals_len;
+        const uint32_t rev_row0 = (uint32_t)w.rev_start.size() - 1;
+        const uint32_t rev0 = (uint32_t)w.rev_src.size();
+        const uint32_t rvd_row0 = (uint32_t)w.rvd_start.size() - 1;
+        const uint32_t rvd0 = (uint32_t)w.rvd_src.size();
+        const uint32_t row0 = w.rows();
+        const uint32_t member0 = (uint32_t)w.row_cfg.size();
+        const uint32_t cfg0 = cfg_total;
+        const uint32_t exit0 = (uint32_t)w.exit_node.size();
+        const uint32_t exit_cfg0 = w.snapshot_configs;
+
+        TreeDev td{};
+        td.node0 = node0;
+        td.nodes = N;
+        for (uint32_t i = 0; i < N; i++) {
+            w.node_meta.push_back(uint32_t(t.node_kind[i]) | uint32_t(t.node_player[i]) << 2);
+            w.node_nc.push_back(t.nc(i, 0));
+            w.node_nc.push_back(t.nc(i, 1));
+            w.child_start.push_back(child0 + t.node_child_start[i]);
+            w.legal_row_of.push_back(t.legal_row_of[i] == NONE ? NONE : legal_row0 + t.legal_row_of[i]);
+            w.draw_off.push_back(draw0 + t.draw_off[i]);
+            w.draw_row_off.push_back(draw_row0 + t.draw_row_off[i]);
+            w.parent.push_back(t.node_parent[i] == NONE ? NONE : node0 + t.node_parent[i]);
+            w.rev_row_of.push_back(t.rev_row_of[i] == NONE ? NONE : rev_row0 + t.rev_row_of[i]);
+            w.rvd_row_of.push_back(t.rvd_row_of[i] == NONE ? NONE : rvd_row0 + t.rvd_row_of[i]);
+        }
+        for (uint32_t c : t.node_child) w.child.push_back(node0 + c);
+        append_shift<uint32_t>(w.legal_off, t.legal_off, 1, cell0, false);
+        w.draw_row_start.insert(w.draw_row_start.end(), t.draw_row_start.begin(), t.draw_row_start.end());
+        w.draw_to.insert(w.draw_to.end(), t.draw_to.begin(), t.draw_to.end());
+        w.draw_p.insert(w.draw_p.end(), t.draw_p.begin(), t.draw_p.end());
+
+        // Reach slots in BFS order; a player who did not act at the parent
+        // keeps the parent's vector (engine/src/gpu/wave.rs:358-374).
+        w.reach_base.resize(2 * size_t(node0 + N), 0);
+        uint32_t reach_at = reach0;
+        for (uint32_t local : t.bfs_order) {
+            uint32_t node = node0 + local;
+            for (int p = 0; p < 2; p++) {
+                if (local == 0 || t.node_player[t.node_parent[local]] == p) {
+                    w.reach_base[2 * node + p] = reach_at;
+                    reach_at += t.nc(local, p);
+                } else {
+                    w.reach_base[2 * node + p] = w.reach_base[2 * (node0 + t.node_parent[local]) + p];
+                }
+            }
+        }
+        w.reach_len = reach_at;
+
+        std::vector<uint32_t> vb[2];
+        uint32_t vlen = 0;
+        if (!value_layout(t, vb, &vlen, err)) return false;
+        w.vals_base.resize(2 * size_t(node0 + N), 0);
+        for (uint32_t i = 0; i < N; i++)
+            for (int p = 0; p < 2; p++) w.vals_base[2 * (node0 + i) + p] = vals0 + vb[p][i];
+        w.vals_len = vals0 + vlen;
+
+        // Direct value index of each legal cell's successor (wave.rs:393-411).
+        w.legal_value.resize(cell0 + t.ncells, NONE);
+        for (uint32_t i = 0; i < N; i++) {
+            if (t.node_kind[i] != 0) continue;
+            int p = t.node_player[i];
+            uint32_t rowa = t.legal_row_of[i];
+            for (uint32_t c = 0; c < t.nc(i, p); c++)
+                for (uint32_t g = t.legal_off[rowa + c]; g < t.legal_off[rowa + c + 1]; g++)
+                    if (t.legal_trans[g] != NONE)
+                        w.legal_value[cell0 + g] = w.vals_base[2 * (node0 + t.legal_child[g]) + p] + t.legal_trans[g];
+        }
+        w.ncells += t.ncells;
+
+        append_shift<uint32_t>(w.rev_start, t.rev_start, 1, rev0, false);
+        w.rev_src.insert(w.rev_src.end(), t.rev_src.begin(), t.rev_src.end());
+        append_shift<uint32_t>(w.rev_cell, t.rev_cell, 0, cell0, false);
+        append_shift<uint32_t>(w.rvd_start, t.rvd_start, 1, rvd0, false);
+        w.rvd_src.insert(w.rvd_src.end(), t.rvd_src.begin(), t.rvd_src.end());
+        w.rvd_p.insert(w.rvd_p.end(), t.rvd_p.begin(), t.rvd_p.end());
+
+        // Network rows and interned configs.
+        for (uint32_t r : t.leaf_rows) w.row_node.push_back(node0 + r);
+        append_shift<uint32_t>(w.row_cfg_off, t.leaf_coff, 1, member0, false);
+        append_shift<uint32_t>(w.row_cfg, t.leaf_cidx, 0, cfg0, false);
+        for (uint32_t c = 0; c < t.ncfg; c++) {
+            const float* phi = &t.cphi[size_t(c) * w.net.cfeat];
+            float key = phi[0];
+            if (!(key >= 0.0f) || key != (float)(uint32_t)key || (w.net.heads && (uint32_t)key >= w.net.heads)) {
+                *err = "config head index out of range";
+                return false;
+            }
+            w.cfg_key.push_back((uint32_t)key);
+            w.cfg_emb.insert(w.cfg_emb.end(), phi + 1, phi + 1 + w.net.pool);
+        }
+        cfg_total += t.ncfg;
+        w.pub_raw.insert(w.pub_raw.end(), t.leaf_raw.begin(), t.leaf_raw.end());
+        td.row0 = row0;
+        td.rows = t.rows;
+        td.term0 = (uint32_t)w.term_node.size();
+        td.nterm = (uint32_t)t.term_leaves.size();
+        for (size_t k = 0; k < t.term_leaves.size(); k++) {
+            w.term_node.push_back(node0 + t.term_leaves[k]);
+            w.term_util.push_back(t.terminal_utility[k]);
+        }
+        td.reach0 = reach0;
+        td.reach_len = reach_at - reach0;
+        td.root0 = (uint32_t)w.roots.size();
+        td.n0 = t.nc(0, 0);
+        td.n1 = t.nc(0, 1);
+        w.roots.insert(w.roots.end(), job.root[0].begin(), job.root[0].end());
+        w.roots.insert(w.roots.end(), job.root[1].begin(), job.root[1].end());
+        td.carried0 = (uint32_t)w.carried.size();
+        td.nroots = job.nroots();
+        for (uint32_t r = 0; r < job.nroots(); r++) {
+            w.carried.insert(w.carried.end(), job.carried[0][r].begin(), job.carried[0][r].end());
+            w.carried.insert(w.carried.end(), job.carried[1][r].begin(), job.carried[1][r].end());
+        }
+        td.root_value0 = w.root_values_len;
+        w.root_values_len += job.nroots() * (td.n0 + td.n1);
+        w.nroots_max = std::max(w.nroots_max, job.nroots());
+        td.exit0 = exit0;
+        td.nexit = (uint32_t)(t.leaf_rows.size() + t.term_leaves.size());
+        for (uint32_t r : t.leaf_rows) w.exit_node.push_back(node0 + r);
+        for (uint32_t r : t.term_leaves) w.exit_node.push_back(node0 + r);
+        append_shift<uint32_t>(w.exit_coff, t.snap_coff, 1, exit_cfg0, false);
+        w.snapshot_configs += t.snapshot_configs();
+
+        // Level schedules of this tree.
+        const uint32_t L = t.nlevels();
+        td.nlevels = L;
+        td.lvl0 = w.lvl_len;
+        w.lvl_len += L + 1;
+        w.max_levels = std::max(w.max_levels, L);
+        for (int p = 0; p < 2; p++) {
+            for (uint32_t l = 0; l < L; l++) {
+                w.back_lvl[p].push_back((uint32_t)w.back_task[p].size());
+                w.reach_lvl[p].push_back((uint32_t)w.reach_task[p].size());
+                for (uint32_t k = t.level_start[l]; k < t.level_start[l + 1]; k++) {
+                    uint32_t local = t.bfs_order[k], node = node0 + local;
+                    uint8_t kind = t.node_kind[local];
+                    if (kind != 2 && !(kind == 1 && t.node_player[local] != p))
+                        for (uint32_t c = 0; c < t.nc(local, p); c++) w.back_task[p].push_back({node, c});
+                    if (local != 0 && t.node_player[t.node_parent[local]] == p)
+                        for (uint32_t c = 0; c < t.nc(local, p); c++) w.reach_task[p].push_back({node, c});
+                }
+            }
+            w.back_lvl[p].push_back((uint32_t)w.back_task[p].size());
+            w.reach_lvl[p].push_back((uint32_t)w.reach_task[p].size());
+            td.dec0[p] = (uint32_t)w.decision[p].size();
+            for (uint32_t i = 0; i < N; i++)
+                if (t.node_kind[i] == 0 && t.node_player[i] == p)
+                    for (uint32_t c = 0; c < t.nc(i, p); c++) w.decision[p].push_back({node0 + i, c});
+            td.dec1[p] = (uint32_t)w.decision[p].size();
+        }
+        w.trees.push_back(td);
+    }
+    w.child_start.push_back((uint32_t)w.child.size());
+    w.carry_slots = (w.meta.snapshots && w.meta.snap_iters.size() > 1) ? (uint32_t)w.meta.snap_iters.size() - 1 : 0;
+    w.jobs = std::move(jobs);
+    if (!validate_deep(w, err)) return false;
+    *out = std::move(w);
+    return true;
+}
+
+// Every index a kernel dereferences, checked against the buffer it indexes.
+// The device code relies on these bounds and performs no checks of its own.
+bool validate_deep(const WaveHost& w, std::string* err) {
+    auto fail = [&](const char* m) {
+        *err = std::string("wave bounds: ") + m;
+        return false;
+    };
+    const uint64_t N = w.nodes();
+    if (w.node_nc.size() != 2 * N || w.child_start.size() != N + 1 || w.legal_row_of.size() != N ||
+        w.draw_off.size() != N || w.draw_row_off.size() != N || w.reach_base.size() != 2 * N ||
+        w.vals_base.size() != 2 * N || w.parent.size() != N || w.rev_row_of.size() != N || w.rvd_row_of.size() != N)
+        return fail("node arrays disagree");
+    if (w.legal_value.size() != w.ncells || w.legal_off.empty() || w.legal_off.back() != w.ncells)
+        return fail("cell arrays disagree");
+    for (uint64_t i = 0; i < N; i++) {
+        uint32_t kind = w.node_meta[i] & 3u, actor = w.node_meta[i] >> 2;
+        if (kind > 2 || actor > 1) return fail("node_meta");
+        for (int p = 0; p < 2; p++) {
+            uint64_t n = w.nc((uint32_t)i, p);
+            if (uint64_t(w.reach_base[2 * i + p]) + n > w.reach_len) return fail("reach slot");
+            if (uint64_t(w.vals_base[2 * i + p]) + n > w.vals_len) return fail("value slot");
+        }
+        if (w.child_start[i + 1] < w.child_start[i] || w.child_start[i + 1] > w.child.size()) return fail("child CSR");
+        for (uint32_t x = w.child_start[i]; x < w.child_start[i + 1]; x++)
+            if (w.child[x] >= N || w.parent[w.child[x]] != i) return fail("child index");
+        if (kind == 0) {
+            uint64_t r0 = w.legal_row_of[i], nc = w.nc((uint32_t)i, actor);
+            if (r0 == NONE || r0 + nc + 1 > w.legal_off.size()) return fail("legal rows");
+            for (uint64_t r = r0; r < r0 + nc; r++)
+                if (w.legal_off[r + 1] < w.legal_off[r] || w.legal_off[r + 1] > w.ncells) return fail("legal_off");
+            if (w.child_start[i + 1] == w.child_start[i]) return fail("decision node without children");
+        } else if (kind == 1) {
+            if (w.child_start[i + 1] != w.child_start[i] + 1) return fail("chance child");
+            uint32_t ch = w.child[w.child_start[i]];
+            uint64_t rb = w.draw_row_off[i], nc = w.nc((uint32_t)i, actor);
+            if (rb + nc + 1 > w.draw_row_start.size()) return fail("draw rows");
+            for (uint64_t c = 0; c < nc; c++) {
+                uint64_t lo = w.draw_row_start[rb + c], hi = w.draw_row_start[rb + c + 1];
+                if (hi < lo || uint64_t(w.draw_off[i]) + hi > w.draw_to.size()) return fail("draw entries");
+                for (uint64_t x = lo; x < hi; x++)
+                    if (w.draw_to[w.draw_off[i] + x] >= w.nc(ch, actor)) return fail("draw_to");
+            }
+        }
+        uint32_t par = w.parent[i];
+        if (par != NONE) {
+            if (par >= N) return fail("parent");
+            int p = (int)(w.node_meta[par] >> 2);
+            uint64_t nc = w.nc((uint32_t)i, p);
+            if (w.rev_row_of[i] != NONE) {
+                uint64_t r0 = w.rev_row_of[i];
+                if (r0 + nc + 1 > w.rev_start.size()) return fail("rev rows");
+                for (uint64_t c = 0; c < nc; c++)
+                    for (uint64_t x = w.rev_start[r0 + c]; x < w.rev_start[r0 + c + 1]; x++)
+                        if (x >= w.rev_src.size() || w.rev_src[x] >= w.nc(par, p) || w.rev_cell[x] >= w.ncells)
+                            return fail("rev entry");
+            } else if (w.rvd_row_of[i] != NONE) {
+                uint64_t r0 = w.rvd_row_of[i];
+                if (r0 + nc + 1 > w.rvd_start.size()) return fail("rvd rows");
+                for (uint64_t c = 0; c < nc; c++)
+                    for (uint64_t x = w.rvd_start[r0 + c]; x < w.rvd_start[r0 + c + 1]; x++)
+                        if (x >= w.rvd_src.size() || w.rvd_src[x] >= w.nc(par, p)) return fail("rvd entry");
+            } else {
+                return fail("node without gather rows");
+            }
+        }
+    }
+    for (uint32_t v : w.legal_value)
+        if (v != NONE && v >= w.vals_len) return fail("legal_value");
+    const uint64_t rows = w.rows();
+    if (w.row_cfg_off.size() != 2 * rows + 1 || w.row_cfg_off.back() != w.row_cfg.size()) return fail("row_cfg_off");
+    const uint64_t ncfg = w.cfg_key.size();
+    if (w.cfg_emb.size() != ncfg * w.net.pool || w.pub_raw.size() != rows * w.net.row_bytes) return fail("row payload");
+    for (uint64_t r = 0; r < rows; r++) {
+        uint32_t node = w.row_node[r];
+        if (node >= N || (w.node_meta[node] & 3u) != 2) return fail("row_node");
+        for (int p = 0; p < 2; p++)
+            if (w.row_cfg_off[2 * r + p + 1] - w.row_cfg_off[2 * r + p] != w.nc(node, p)) return fail("row configs");
+    }
+    for (uint32_t c : w.row_cfg)
+        if (c >= ncfg) return fail("row_cfg");
+    for (uint32_t k : w.cfg_key)
+        if (k >= w.net.heads) return fail("cfg_key");
+    for (uint32_t t : w.term_node)
+        if (t >= N || (w.node_meta[t] & 3u) != 2) return fail("term_node");
+    const uint64_t nexit = w.exit_node.size();
+    if (w.exit_coff.size() != 2 * nexit + 1 || w.exit_coff.back() != w.snapshot_configs) return fail("exit_coff");
+    for (uint64_t e = 0; e < nexit; e++)
+        for (int p = 0; p < 2; p++)
+            if (w.exit_node[e] >= N || w.exit_coff[2 * e + p + 1] - w.exit_coff[2 * e + p] != w.nc(w.exit_node[e], p))
+                return fail("exit configs");
+    for (int p = 0; p < 2; p++) {
+        for (const Task& q : w.back_task[p])
+            if (q.node >= N || q.config >= w.nc(q.node, p)) return fail("back task");
+        for (const Task& q : w.reach_task[p])
+            if (q.node >= N || q.config >= w.nc(q.node, p) || w.parent[q.node] == NONE) return fail("reach task");
+        for (const Task& q : w.decision[p])
+            if (q.node >= N || q.config >= w.nc(q.node, p) || (w.node_meta[q.node] & 3u) != 0) return fail("decision task");
+        if (w.back_lvl[p].size() != w.lvl_len || w.reach_lvl[p].size() != w.lvl_len) return fail("level arrays");
+    }
+    for (const TreeDev& t : w.trees) {
+        if (uint64_t(t.node0) + t.nodes > N || uint64_t(t.lvl0) + t.nlevels + 1 > w.lvl_len) return fail("tree range");
+        for (int p = 0; p < 2; p++) {
+            const auto& bl = w.back_lvl[p];
+            const auto& rl = w.reach_lvl[p];
+            for (uint32_t l = 0; l < t.nlevels; l++) {
+                if (bl[t.lvl0 + l + 1] < bl[t.lvl0 + l] || bl[t.lvl0 + l + 1] > w.back_task[p].size())
+                    return fail("back levels");
+                if (rl[t.lvl0 + l + 1] < rl[t.lvl0 + l] || rl[t.lvl0 + l + 1] > w.reach_task[p].size())
+                    return fail("reach levels");
+            }
+            if (t.dec0[p] > t.dec1[p] || t.dec1[p] > w.decision[p].size()) return fail("decision range");
+        }
+        if (uint64_t(t.row0) + t.rows > rows || uint64_t(t.term0) + t.nterm > w.term_node.size()) return fail("leaf range");
+        if (uint64_t(t.reach0) + t.reach_len > w.reach_len) return fail("reach range");
+        if (t.n0 != w.nc(t.node0, 0) || t.n1 != w.nc(t.node0, 1)) return fail("root support");
+        const uint64_t nr = uint64_t(t.n0) + t.n1;
+        if (t.root0 + nr > w.roots.size() || t.carried0 + t.nroots * nr > w.carried.size() ||
+            t.root_value0 + t.nroots * nr > w.root_values_len)
+            return fail("root ranges");
+        if (uint64_t(t.exit0) + t.nexit > nexit) return fail("exit range");
+    }
+    return true;
+}
+
+// Algorithmic HBM bytes of one CFR iteration (readout, backprop with the
+// regret/DCFR update, reach gather, average accumulation) for traverser p:
+//   44 C_p  legal cells of p: successor index 4, child value 4, cur read 4 +
+//           write 4, regret read+write 8, sum read+write 8, accumulate: cur 4 +
+//           sum read+write 8
+//   16 G_p  gather entries into p's reach: source 4, cell or probability 4,
+//           parent reach 4, strategy 4
+//    4 S_p  p's reach slots written
+//   12 R_p  p's decision rows: row offsets 8, reach read by the accumulation 4
+//    4 O_p  child-value reads at opponent decision nodes
+//   12 H_p  draw entries at p's chance nodes: successor 4, probability 4, value 4
+//    8 L_p  leaf value slots of p: net output read 4, value write 4
+//    4 L_o  opponent reach read for the leaf reach mass
+uint64_t cfr_bytes_per_iter(const WaveHost& w, int p) {
+    uint64_t C = 0, G = 0, S = 0, R = 0, O = 0, H = 0, Lp = 0, Lo = 0;
+    const uint32_t N = w.nodes();
+    for (uint32_t i = 0; i < N; i++) {
+        uint32_t kind = w.node_meta[i] & 3u, actor = w.node_meta[i] >> 2;
+        uint32_t ncp = w.nc(i, p);
+        if (kind == 0 && actor == (uint32_t)p) {
+            R += ncp;
+            uint32_t r0 = w.legal_row_of[i];
+            C += w.legal_off[r0 + ncp] - w.legal_off[r0];
+        } else if (kind == 0) {
+            O += uint64_t(ncp) * (w.child_start[i + 1] - w.child_start[i]);
+        } else if (kind == 1 && actor == (uint32_t)p) {
+            uint32_t rb = w.draw_row_off[i];
+            H += w.draw_row_start[rb + ncp] - w.draw_row_start[rb];
+        } else if (kind == 2) {
+            Lp += ncp;
+            Lo += w.nc(i, 1 - p);
+        }
+        uint32_t par = w.parent[i];
+        if (par != NONE && (w.node_meta[par] >> 2) == (uint32_t)p) {
+            S += ncp;
+            if (w.rev_row_of[i] != NONE) {
+                uint32_t r0 = w.rev_row_of[i];
+                G += w.rev_start[r0 + ncp] - w.rev_start[r0];
+            } else {
+                uint32_t r0 = w.rvd_row_of[i];
+                G += w.rvd_start[r0 + ncp] - w.rvd_start[r0];
+            }
+        }
+    }
+    return 44 * C + 16 * G + 4 * S + 12 * R + 4 * O + 12 * H + 8 * Lp + 4 * Lo;
+}
+
+}  // namespace wc

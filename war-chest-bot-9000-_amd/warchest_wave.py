@@ -1,0 +1,461 @@
+"""Python host binding of the MI355X wave executor's C ABI (include/wc_wave.h).
+
+The names mirror the reference client surface (engine/src/gpu/client.rs,
+service.rs): `spawn` returns a `GpuClient` with `submit`, `submit_tagged`,
+`set_weights`, `queued_work`; `SolveHandle.wait()` returns a `SolveResult`.
+Lower-level `Executor` / `Wave` objects mirror `Executor` and `Wave::pack`
+(engine/src/gpu/device.rs:515-831, wave.rs:127-221) for tests and benchmarks.
+
+Nothing here computes: every call goes through the native library, and loading
+fails loudly when it is missing (build it with `python build.py`).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libwcwave.so")
+
+WC_PRECISE, WC_F16, WC_BF16 = 0, 1, 2
+MODEL_MLP, MODEL_TWO_TOWER = 101, 102
+
+_lib = None
+
+
+class WaveError(RuntimeError):
+    pass
+
+
+def lib():
+    """Load the native library (once). Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise WaveError(f"native library missing: {LIB_PATH} (run build.py)")
+    L = C.CDLL(LIB_PATH)
+    _declare(L)
+    _lib = L
+    return L
+
+
+class NetDesc(C.Structure):
+    _fields_ = [
+        ("dims", C.POINTER(C.c_uint32)), ("ndims", C.c_uint32),
+        ("w", C.POINTER(C.c_float)), ("nw", C.c_size_t),
+        ("b", C.POINTER(C.c_float)), ("nb", C.c_size_t),
+        ("ln", C.POINTER(C.c_float)), ("nln", C.c_size_t),
+    ]
+
+
+class ServiceOpts(C.Structure):
+    _fields_ = [("lanes", C.c_uint32), ("wave_jobs", C.c_uint32),
+                ("wave_rows", C.c_uint32), ("window_us", C.c_uint32)]
+
+
+class SynthSpecC(C.Structure):
+    _fields_ = [
+        ("seed", C.c_uint64), ("trees", C.c_uint32),
+        ("nodes_lo", C.c_uint32), ("nodes_hi", C.c_uint32),
+        ("exact_decisions", C.c_uint32), ("exact_leaves", C.c_uint32),
+        ("act_lo", C.c_uint32), ("act_hi", C.c_uint32),
+        ("collapse", C.c_float), ("chance", C.c_uint32),
+        ("draw_lo", C.c_uint32), ("draw_hi", C.c_uint32),
+        ("info_fixed", C.c_uint32), ("info_median", C.c_float), ("info_p99", C.c_float),
+        ("info_cap", C.c_uint32),
+        ("legal_p", C.c_float), ("shift_p", C.c_float), ("notrans_p", C.c_float),
+        ("terminal_p", C.c_float),
+        ("dirichlet", C.c_uint32), ("nroots", C.c_uint32),
+        ("whale_frac", C.c_float), ("whale_nodes", C.c_uint32), ("whale_info", C.c_uint32),
+        ("depth", C.c_uint32), ("iters", C.c_uint32), ("snapshots", C.c_uint32),
+        ("alpha", C.c_float), ("beta", C.c_float), ("gamma", C.c_float), ("predict", C.c_float),
+        ("net_dims", C.POINTER(C.c_uint32)), ("n_net_dims", C.c_uint32),
+    ]
+
+
+class WaveStats(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in (
+        "jobs", "nodes", "decision_nodes", "chance_nodes", "leaves", "rows", "terminals",
+        "levels", "iters", "nroots_max", "carry_slots")] + [(n, C.c_uint64) for n in (
+        "cells", "reach_slots", "reach_len", "vals_len", "rev_nnz", "rvd_nnz", "draw_nnz",
+        "snapshot_configs", "table_bytes", "arena_bytes")] + [
+        ("cfr_bytes_per_iter", C.c_uint64 * 2), ("mlp_flops_per_query", C.c_uint64)]
+
+    def as_dict(self):
+        out = {}
+        for name, _ in self._fields_:
+            v = getattr(self, name)
+            out[name] = list(v) if name == "cfr_bytes_per_iter" else int(v)
+        return out
+
+
+# Symbols every build must export (checked by the CPU test suite).
+EXPORTS = [
+    "wc_last_error", "wc_net_sizes",
+    "wc_service_create", "wc_service_destroy", "wc_set_weights", "wc_queued_work",
+    "wc_submit", "wc_wait", "wc_poll",
+    "wc_result_tag", "wc_result_weight_version", "wc_result_strategy", "wc_result_root_values",
+    "wc_result_carries", "wc_result_free",
+    "wc_executor_create", "wc_executor_destroy", "wc_executor_publish",
+    "wc_wave_pack", "wc_wave_free", "wc_wave_stats_get", "wc_solve_wave", "wc_time_wave",
+    "wc_mlp_forward", "wc_time_mlp",
+    "wc_job_roundtrip", "wc_job_validate",
+    "wc_synth_spec_default", "wc_synth", "wc_jobset_count", "wc_jobset_job", "wc_jobset_free",
+    "wc_synth_weights", "wc_synth_features",
+]
+
+_u8p = C.POINTER(C.c_uint8)
+_f32p = C.POINTER(C.c_float)
+_u32p = C.POINTER(C.c_uint32)
+_u16p = C.POINTER(C.c_uint16)
+
+
+def _declare(L):
+    L.wc_last_error.restype = C.c_char_p
+    L.wc_net_sizes.argtypes = [_u32p, C.c_uint32, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+    L.wc_service_create.argtypes = [C.c_int, C.POINTER(NetDesc), C.c_int, C.POINTER(ServiceOpts),
+                                    C.POINTER(C.c_void_p)]
+    L.wc_service_destroy.argtypes = [C.c_void_p]
+    L.wc_service_destroy.restype = None
+    L.wc_set_weights.argtypes = [C.c_void_p, C.POINTER(NetDesc)]
+    L.wc_set_weights.restype = C.c_uint64
+    L.wc_queued_work.argtypes = [C.c_void_p]
+    L.wc_queued_work.restype = C.c_uint64
+    L.wc_submit.argtypes = [C.c_void_p, _u8p, C.c_size_t, C.c_uint64, C.POINTER(C.c_void_p)]
+    L.wc_wait.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+    L.wc_poll.argtypes = [C.c_void_p]
+    L.wc_result_tag.argtypes = [C.c_void_p]
+    L.wc_result_tag.restype = C.c_uint64
+    L.wc_result_weight_version.argtypes = [C.c_void_p]
+    L.wc_result_weight_version.restype = C.c_uint64
+    L.wc_result_strategy.argtypes = [C.c_void_p, C.POINTER(C.c_size_t)]
+    L.wc_result_strategy.restype = _f32p
+    L.wc_result_root_values.argtypes = [C.c_void_p, _u32p, _u32p, _u32p]
+    L.wc_result_root_values.restype = _f32p
+    L.wc_result_carries.argtypes = [C.c_void_p, _u32p, _u32p]
+    L.wc_result_carries.restype = _u16p
+    L.wc_result_free.argtypes = [C.c_void_p]
+    L.wc_result_free.restype = None
+    L.wc_executor_create.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_void_p)]
+    L.wc_executor_destroy.argtypes = [C.c_void_p]
+    L.wc_executor_destroy.restype = None
+    L.wc_executor_publish.argtypes = [C.c_void_p, C.POINTER(NetDesc)]
+    L.wc_executor_publish.restype = C.c_uint64
+    L.wc_wave_pack.argtypes = [C.POINTER(_u8p), C.POINTER(C.c_size_t), C.c_uint32, C.POINTER(C.c_void_p)]
+    L.wc_wave_free.argtypes = [C.c_void_p]
+    L.wc_wave_free.restype = None
+    L.wc_wave_stats_get.argtypes = [C.c_void_p, C.POINTER(WaveStats)]
+    L.wc_solve_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p)]
+    L.wc_time_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint32,
+                               C.POINTER(C.c_double), C.POINTER(C.c_double)]
+    L.wc_mlp_forward.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, _f32p, _f32p]
+    L.wc_time_mlp.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, _f32p, C.c_uint32,
+                              C.POINTER(C.c_double), C.POINTER(C.c_double)]
+    L.wc_job_roundtrip.argtypes = [_u8p, C.c_size_t, _u8p, C.c_size_t, C.POINTER(C.c_size_t)]
+    L.wc_job_validate.argtypes = [_u8p, C.c_size_t]
+    L.wc_synth_spec_default.argtypes = [C.POINTER(SynthSpecC)]
+    L.wc_synth_spec_default.restype = None
+    L.wc_synth.argtypes = [C.POINTER(SynthSpecC), C.POINTER(C.c_void_p)]
+    L.wc_jobset_count.argtypes = [C.c_void_p]
+    L.wc_jobset_count.restype = C.c_uint32
+    L.wc_jobset_job.argtypes = [C.c_void_p, C.c_uint32, C.POINTER(C.c_size_t)]
+    L.wc_jobset_job.restype = _u8p
+    L.wc_jobset_free.argtypes = [C.c_void_p]
+    L.wc_jobset_free.restype = None
+    L.wc_synth_weights.argtypes = [_u32p, C.c_uint32, C.c_uint64, _f32p, C.c_size_t, _f32p, C.c_size_t]
+    L.wc_synth_features.argtypes = [C.c_uint32, C.c_uint32, C.c_uint64, _f32p]
+
+
+def _check(rc):
+    if rc != 0:
+        raise WaveError(lib().wc_last_error().decode(errors="replace") or f"error {rc}")
+
+
+def _bytes_ptr(b: bytes):
+    buf = (C.c_uint8 * len(b)).from_buffer_copy(b)
+    return buf, C.cast(buf, _u8p)
+
+
+def _arr(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    ctype = {np.float32: C.c_float, np.uint32: C.c_uint32}[dtype]
+    return a, a.ctypes.data_as(C.POINTER(ctype))
+
+
+# ------------------------------------------------------------------ networks
+
+def mlp_dims(inputs=512, hidden=384, layers=3, heads=22, pool=64):
+    return [MODEL_MLP, inputs, hidden, layers, heads, pool]
+
+
+def two_tower_dims(inputs=512, width=512, pub_layers=2, priv_in=96, priv_layers=2, pool=64):
+    return [MODEL_TWO_TOWER, inputs, width, pub_layers, priv_in, priv_layers, pool]
+
+
+def net_sizes(dims):
+    d, dp = _arr(dims, np.uint32)
+    nw, nb = C.c_size_t(), C.c_size_t()
+    _check(lib().wc_net_sizes(dp, len(d), C.byref(nw), C.byref(nb)))
+    return nw.value, nb.value
+
+
+@dataclass
+class Net:
+    dims: list
+    w: np.ndarray
+    b: np.ndarray
+
+    def desc(self):
+        """A NetDesc whose pointers stay valid while this object lives."""
+        self._d, dp = _arr(self.dims, np.uint32)
+        self._w, wp = _arr(self.w, np.float32)
+        self._b, bp = _arr(self.b, np.float32)
+        return NetDesc(dp, len(self._d), wp, self._w.size, bp, self._b.size, None, 0)
+
+
+def synth_weights(dims, seed=1):
+    nw, nb = net_sizes(dims)
+    w = np.zeros(nw, np.float32)
+    b = np.zeros(nb, np.float32)
+    d, dp = _arr(dims, np.uint32)
+    _check(lib().wc_synth_weights(dp, len(d), seed, w.ctypes.data_as(_f32p), nw, b.ctypes.data_as(_f32p), nb))
+    return Net(list(dims), w, b)
+
+
+def synth_features(rows, width, seed=7):
+    x = np.zeros((rows, width), np.float32)
+    _check(lib().wc_synth_features(rows, width, seed, x.ctypes.data_as(_f32p)))
+    return x
+
+
+# ------------------------------------------------------------------ workloads
+
+def default_spec(**kw):
+    s = SynthSpecC()
+    lib().wc_synth_spec_default(C.byref(s))
+    for k, v in kw.items():
+        if k == "net_dims":
+            continue
+        if not hasattr(s, k):
+            raise KeyError(k)
+        setattr(s, k, v)
+    return s
+
+
+def synth_jobs(net_dims, **kw) -> list:
+    """Seeded synthetic jobs as WCJ8 bytes, one per tree."""
+    s = default_spec(**kw)
+    d, dp = _arr(net_dims, np.uint32)
+    s.net_dims = dp
+    s.n_net_dims = len(d)
+    h = C.c_void_p()
+    _check(lib().wc_synth(C.byref(s), C.byref(h)))
+    try:
+        out = []
+        for k in range(lib().wc_jobset_count(h)):
+            n = C.c_size_t()
+            p = lib().wc_jobset_job(h, k, C.byref(n))
+            out.append(C.string_at(p, n.value))
+        return out
+    finally:
+        lib().wc_jobset_free(h)
+
+
+def job_roundtrip(b: bytes) -> bytes:
+    buf, p = _bytes_ptr(b)
+    n = C.c_size_t()
+    _check(lib().wc_job_roundtrip(p, len(b), None, 0, C.byref(n)))
+    out = (C.c_uint8 * n.value)()
+    _check(lib().wc_job_roundtrip(p, len(b), out, n.value, C.byref(n)))
+    return bytes(out)
+
+
+def job_validate(b: bytes):
+    buf, p = _bytes_ptr(b)
+    _check(lib().wc_job_validate(p, len(b)))
+
+
+# ------------------------------------------------------------------ results
+
+@dataclass
+class SolveResult:
+    """`SolveResult` (engine/src/gpu/client.rs:113-122), copied out of the native result."""
+    tag: int
+    weight_version: int
+    strategy: np.ndarray
+    root_values: np.ndarray  # [nroots, n0 + n1]
+    root_n: tuple
+    carries: np.ndarray      # [slots, snapshot_configs] float16
+
+    @staticmethod
+    def take(ptr) -> "SolveResult":
+        L = lib()
+        n = C.c_size_t()
+        sp = L.wc_result_strategy(ptr, C.byref(n))
+        strategy = np.ctypeslib.as_array(sp, (n.value,)).copy() if n.value else np.zeros(0, np.float32)
+        nr, n0, n1 = C.c_uint32(), C.c_uint32(), C.c_uint32()
+        rp = L.wc_result_root_values(ptr, C.byref(nr), C.byref(n0), C.byref(n1))
+        k = nr.value * (n0.value + n1.value)
+        roots = (np.ctypeslib.as_array(rp, (k,)).copy() if k else np.zeros(0, np.float32)).reshape(
+            nr.value, n0.value + n1.value)
+        slots, cfgs = C.c_uint32(), C.c_uint32()
+        cp = L.wc_result_carries(ptr, C.byref(slots), C.byref(cfgs))
+        k = slots.value * cfgs.value
+        carries = (np.ctypeslib.as_array(cp, (k,)).copy() if k else np.zeros(0, np.uint16)).view(
+            np.float16).reshape(slots.value, cfgs.value)
+        r = SolveResult(int(L.wc_result_tag(ptr)), int(L.wc_result_weight_version(ptr)), strategy, roots,
+                        (n0.value, n1.value), carries)
+        L.wc_result_free(ptr)
+        return r
+
+
+# ------------------------------------------------------------------ executor
+
+class Wave:
+    """`Wave::pack` over WCJ8 jobs."""
+
+    def __init__(self, jobs: Sequence[bytes]):
+        L = lib()
+        self._bufs = [(C.c_uint8 * len(j)).from_buffer_copy(j) for j in jobs]
+        ptrs = (_u8p * len(jobs))(*[C.cast(b, _u8p) for b in self._bufs])
+        lens = (C.c_size_t * len(jobs))(*[len(j) for j in jobs])
+        h = C.c_void_p()
+        _check(L.wc_wave_pack(ptrs, lens, len(jobs), C.byref(h)))
+        self.h = h
+        self.njobs = len(jobs)
+
+    def stats(self) -> dict:
+        s = WaveStats()
+        _check(lib().wc_wave_stats_get(self.h, C.byref(s)))
+        return s.as_dict()
+
+    def close(self):
+        if self.h:
+            lib().wc_wave_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Executor:
+    """One device, one stream: `Executor::{new, publish, solve}`."""
+
+    def __init__(self, device=0, precision=WC_PRECISE):
+        h = C.c_void_p()
+        _check(lib().wc_executor_create(device, precision, C.byref(h)))
+        self.h = h
+
+    def publish(self, net: Net) -> int:
+        d = net.desc()
+        v = lib().wc_executor_publish(self.h, C.byref(d))
+        if v == 0:
+            _check(-1)
+        return int(v)
+
+    def solve(self, wave: Wave, version: int) -> list:
+        res = (C.c_void_p * wave.njobs)()
+        _check(lib().wc_solve_wave(self.h, wave.h, version, res))
+        return [SolveResult.take(res[k]) for k in range(wave.njobs)]
+
+    def time_wave(self, wave: Wave, version: int, reps: int):
+        ms = C.c_double()
+        parts = (C.c_double * 5)()
+        _check(lib().wc_time_wave(self.h, wave.h, version, reps, C.byref(ms), parts))
+        return ms.value, list(parts)
+
+    def mlp(self, version: int, x: np.ndarray, heads: int) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros((x.shape[0], heads), np.float32)
+        _check(lib().wc_mlp_forward(self.h, version, x.shape[0], x.ctypes.data_as(_f32p),
+                                    out.ctypes.data_as(_f32p)))
+        return out
+
+    def time_mlp(self, version: int, x: np.ndarray, reps: int):
+        x = np.ascontiguousarray(x, np.float32)
+        ms = C.c_double()
+        layers = (C.c_double * 8)()
+        _check(lib().wc_time_mlp(self.h, version, x.shape[0], x.ctypes.data_as(_f32p), reps,
+                                 C.byref(ms), layers))
+        return ms.value, list(layers)
+
+    def close(self):
+        if self.h:
+            lib().wc_executor_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------ service
+
+class SolveHandle:
+    def __init__(self, ticket):
+        self._t = ticket
+
+    def ready(self) -> bool:
+        return bool(lib().wc_poll(self._t))
+
+    def wait(self) -> SolveResult:
+        out = C.c_void_p()
+        t, self._t = self._t, None
+        if t is None:
+            raise WaveError("handle already waited on")
+        _check(lib().wc_wait(t, C.byref(out)))
+        return SolveResult.take(out)
+
+
+class GpuClient:
+    """`GpuClient` (engine/src/gpu/client.rs:196-313) over the native service."""
+
+    def __init__(self, handle):
+        self.h = handle
+
+    def submit(self, job: bytes, tag: int = 0) -> SolveHandle:
+        buf, p = _bytes_ptr(job)
+        t = C.c_void_p()
+        _check(lib().wc_submit(self.h, p, len(job), tag, C.byref(t)))
+        return SolveHandle(t)
+
+    def set_weights(self, net: Net) -> int:
+        d = net.desc()
+        v = lib().wc_set_weights(self.h, C.byref(d))
+        if v == 0:
+            _check(-1)
+        return int(v)
+
+    def queued_work(self) -> int:
+        return int(lib().wc_queued_work(self.h))
+
+    def close(self):
+        if self.h:
+            lib().wc_service_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+
+def spawn(device: int, net: Net, precision=WC_PRECISE, lanes=2, wave_jobs=64, wave_rows=49152,
+          window_us=800) -> GpuClient:
+    """`service::spawn` (engine/src/gpu/service.rs:55-82)."""
+    d = net.desc()
+    opts = ServiceOpts(lanes, wave_jobs, wave_rows, window_us)
+    h = C.c_void_p()
+    _check(lib().wc_service_create(device, C.byref(d), precision, C.byref(opts), C.byref(h)))
+    return GpuClient(h)
