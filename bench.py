@@ -1,0 +1,156 @@
+"""Throughput of the MI355X wave executor on one GPU.
+
+One step = one wave solved end to end on the device: 256 seeded depth-2 DCFR
+subgames (200..800 public nodes, chance nodes with 2..6 outcomes, lognormal
+infostates with median 22 and p99 567), 64 DCFR(1.5, 0, 2) iterations with an
+f16 512 -> 3x384 -> 567 value-net call per iteration, then Phase 2 (root
+values under the final average strategy). Tables, weights and state are
+resident in HBM before the timed region; device time comes from HIP events
+on the executor's stream.
+
+Printed as one JSON line: CFR node-iterations/s (`value`), leaf queries/s,
+the roofline of the dominant kernel, the value-net GEMM chain alone on
+65,536 queries (512 -> 3x384 -> 64) against the MFMA roofline, and the CPU
+oracle timed on a bounded sample of the same wave on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "war-chest-bot-9000-_amd"), os.path.join(ROOT, "oracle")]
+
+HBM_PEAK_GBS = 8000.0     # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16/bf16
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", default="c4", choices=["c3", "c4"])
+    ap.add_argument("--cpu-trees", type=int, default=0, help="trees in the CPU-baseline sample (0 = 2 per thread)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-mlp", action="store_true", help="skip the GEMM-chain-alone leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the wave executor shards whole trees across devices with no exchange, "
+              f"and this build runs on a single MI355X (got --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    import warchest_wave as ww
+    import workloads as W
+
+    t0 = time.time()
+    jobs = W.jobs(args.workload)
+    net = W.net_for(args.workload)
+    log(f"[bench] generated {len(jobs)} subgames in {time.time() - t0:.1f}s")
+    wave = ww.Wave(jobs)
+    st = wave.stats()
+    log(f"[bench] wave: {st['nodes']} nodes, {st['cells']} cells, {st['rows']} leaf rows, {st['levels']} levels")
+
+    ex = ww.Executor(0, ww.WC_F16)
+    ver = ex.publish(net)
+    wave_ms, parts = ex.time_wave(wave, ver, reps=args.steps, warmup=args.warmup)
+    log(f"[bench] {args.steps} timed waves: {wave_ms:.3f} ms/wave; per class {parts}")
+
+    iters = st["iters"]
+    node_iters = st["nodes"] * iters
+    queries = st["rows"] * (iters + 2 * st["nroots_max"])
+    value = node_iters / (wave_ms * 1e-3)
+    cfr_ms, mlp_ms, leaf_ms, other_ms, cfr_launch_ms = parts
+    bytes_per_launch = 0.5 * (st["cfr_bytes_per_iter"][0] + st["cfr_bytes_per_iter"][1])
+    cfr_gbs = bytes_per_launch / (cfr_launch_ms * 1e-3) / 1e9
+    mlp_flops_wave = st["rows"] * st["mlp_flops_per_query"] * (iters + 2 * st["nroots_max"])
+    mlp_tflops_in_wave = mlp_flops_wave / (mlp_ms * 1e-3) / 1e12 if mlp_ms > 0 else 0.0
+
+    out = {
+        "metric": "CFR node-iters/sec + value-net leaf queries/sec on 1 MI355X; % HBM/MFMA peak",
+        "value": round(value, 1),
+        "unit": "node-iters/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wave_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 CFR state, f16 leaf-net operands (f32 accumulate)",
+        "data": "synthetic (seeded subgames and Kaiming-normal random-init value net)",
+        "config": {
+            "workload": f"wave of {st['jobs']} depth-2 DCFR subgames, {iters} iterations, 512->3x384->567 f16 "
+                        f"value net ({args.workload})",
+            "trees": st["jobs"], "nodes": st["nodes"], "legal_cells": st["cells"], "leaf_rows": st["rows"],
+            "iters": iters, "parallelism": "1 GPU, one workgroup per subgame",
+        },
+        "leaf_queries_per_s": round(queries / (wave_ms * 1e-3), 1),
+        "ms_by_class": {"cfr": round(cfr_ms, 4), "mlp": round(mlp_ms, 4), "leaf_input": round(leaf_ms, 4),
+                        "other": round(other_ms, 4)},
+        "roofline": {"bound": "hbm", "kernel": "k_cfr (one DCFR iteration)", "achieved": round(cfr_gbs, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(cfr_gbs / HBM_PEAK_GBS, 5),
+                     "traffic": None, "bytes_per_launch": int(bytes_per_launch),
+                     "launch_ms": round(cfr_launch_ms, 5)},
+        "roofline_mlp_in_wave": {"bound": "mfma", "achieved": round(mlp_tflops_in_wave, 2),
+                                 "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(mlp_tflops_in_wave / MFMA_F16_PEAK_TFLOPS, 5)},
+    }
+
+    if not args.no_mlp:
+        mnet = W.net_for("c2")
+        x = W.c2_inputs()
+        mex = ww.Executor(0, ww.WC_F16)
+        mv = mex.publish(mnet)
+        chain_ms, layer_ms = mex.time_mlp(mv, x, reps=20)
+        flops = x.shape[0] * 2 * (512 * 384 + 2 * 384 * 384 + 384 * 64)
+        tf = flops / (chain_ms * 1e-3) / 1e12
+        out["mlp_alone"] = {"workload": "65,536 queries, 512->384->384->384->64, f16 operands, f32 accumulate",
+                            "queries_per_s": round(x.shape[0] / (chain_ms * 1e-3), 1),
+                            "ms": round(chain_ms, 5), "layer_ms": [round(v, 5) for v in layer_ms[:4]],
+                            "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 5)}
+        mex.close()
+        log(f"[bench] GEMM chain alone: {chain_ms:.4f} ms, {tf:.1f} TFLOP/s")
+
+    if not args.no_cpu:
+        import oracle as O
+
+        threads = max(1, min(16, os.cpu_count() or 1))
+        n = args.cpu_trees or min(len(jobs), 2 * threads)
+        sample = jobs[:n]
+        log(f"[bench] CPU oracle: {n} trees on {threads} threads ...")
+        sec, ni, lq = O.solve_batch(sample, net, O.NET_F32, threads=threads)
+        out["cpu_baseline"] = {"value": round(ni / sec, 1), "unit": "node-iters/s", "cores": threads,
+                               "kind": "port", "leaf_queries_per_s": round(lq / sec, 1),
+                               "sample": f"first {n} of the {len(jobs)} subgames, all {iters} iterations + Phase 2, "
+                                         f"one subgame per thread, f32 net, {sec:.1f} s wall",
+                               "cpu": cpu_model()}
+        log(f"[bench] CPU oracle: {sec:.1f}s, {ni / sec:.0f} node-iters/s")
+
+    ex.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -131,13 +131,14 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* out);
  * (results[k] owned by the caller). */
 int wc_solve_wave(wc_executor* ex, wc_wave* w, uint64_t version, wc_result** results);
 
-/* Benchmark helper: upload once, then run the full schedule `reps` times on
- * the device (inputs resident in HBM), returning the mean device time per
- * wave in milliseconds, measured with HIP events on the executor's stream.
- * kernel_ms (optional, 5 doubles) receives one profiled schedule's device
- * time per launch class: [0] CFR sweeps, [1] leaf MLP, [2] leaf input,
- * [3] everything else, and [4] the mean duration of one CFR-sweep launch. */
-int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t reps, double* wave_ms,
+/* Benchmark helper: upload once, run the full schedule `warmup` times
+ * untimed, then `reps` times timed (inputs resident in HBM), returning the
+ * mean device time per wave in milliseconds, measured with HIP events on the
+ * executor's stream. kernel_ms (optional, 5 doubles) receives one profiled
+ * schedule's device time per launch class: [0] CFR sweeps, [1] leaf MLP,
+ * [2] leaf input, [3] everything else, and [4] the mean duration of one
+ * CFR-sweep launch. */
+int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup, uint32_t reps, double* wave_ms,
                  double* kernel_ms);
 
 /* Leaf-net inference alone (the value-net GEMM chain): x is rows x in f32 on

@@ -1,0 +1,84 @@
+"""CPU checks of the C ABI: the library loads, exports what the header declares,
+and its host-only entry points (job codec, validation, synthesis, packing) work
+without a GPU."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import warchest_wave as ww
+import workloads as W
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "wc_wave.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    L = ww.lib()
+    syms = header_symbols()
+    assert len(syms) >= 30
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+    assert set(syms) == set(ww.EXPORTS)
+
+
+def test_job_roundtrip_is_byte_identical():
+    for name in ("c1", "c3"):
+        for j in W.jobs(name, trees=3) if name == "c3" else W.jobs(name):
+            assert ww.job_roundtrip(j) == j
+            ww.job_validate(j)
+
+
+def test_truncated_and_corrupt_jobs_are_rejected():
+    j = W.jobs("c1")[0]
+    for cut in (0, 3, 8, len(j) // 2, len(j) - 1):
+        with pytest.raises(ww.WaveError):
+            ww.job_validate(j[:cut])
+    bad = bytearray(j)
+    bad[0] ^= 0xFF  # magic
+    with pytest.raises(ww.WaveError, match="magic"):
+        ww.job_validate(bytes(bad))
+    with pytest.raises(ww.WaveError):
+        ww.job_validate(j + b"\0")
+
+
+def test_wave_pack_rejects_mixed_schedules():
+    a = W.jobs("c1")[0]
+    b = W.jobs("c1", iters=8)[0]
+    with pytest.raises(ww.WaveError, match="schedule"):
+        ww.Wave([a, b])
+
+
+def test_wave_counts_add_up():
+    jobs = W.jobs("c3", trees=5)
+    st = ww.Wave(jobs).stats()
+    parts = [ww.Wave([j]).stats() for j in jobs]
+    for k in ("nodes", "cells", "rows", "rev_nnz", "reach_len", "vals_len", "snapshot_configs"):
+        assert st[k] == sum(p[k] for p in parts), k
+    assert st["jobs"] == 5
+    assert st["cfr_bytes_per_iter"][0] == sum(p["cfr_bytes_per_iter"][0] for p in parts)
+
+
+def test_synthesis_is_seeded_and_prefix_stable():
+    a = W.jobs("c3", trees=4)
+    b = W.jobs("c3", trees=6)
+    assert a == b[:4]
+    assert W.jobs("c3", trees=2, seed=99) != a[:2]
+
+
+def test_weights_and_features_are_seeded():
+    n1 = W.net_for("c2")
+    n2 = W.net_for("c2")
+    np.testing.assert_array_equal(n1.w, n2.w)
+    x = W.c2_inputs(rows=64)
+    assert x.shape == (64, 512)
+    assert x.min() >= 0.0 and x.max() <= 1.0
+    # Kaiming-normal: first-layer std ~ sqrt(2 / 512)
+    w1 = n1.w[: 512 * 384]
+    assert abs(w1.std() - np.sqrt(2 / 512)) < 0.003

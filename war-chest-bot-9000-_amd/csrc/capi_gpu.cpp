@@ -160,11 +160,12 @@ int wc_solve_wave(wc_executor* ex, wc_wave* w, uint64_t version, wc_result** res
     return WC_OK;
 }
 
-int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t reps, double* wave_ms, double* kernel_ms) {
+int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup, uint32_t reps, double* wave_ms,
+                 double* kernel_ms) {
     if (!ex || !w || !wave_ms) return fail(WC_ERR_INVALID, "wc_time_wave: null argument");
     ScheduleTimes prof;
     std::string err;
-    if (!ex->ex->time_wave(w->host, version, reps, wave_ms, kernel_ms ? &prof : nullptr, &err))
+    if (!ex->ex->time_wave(w->host, version, warmup, reps, wave_ms, kernel_ms ? &prof : nullptr, &err))
         return fail(WC_ERR_DEVICE, err);
     if (kernel_ms) {
         kernel_ms[0] = prof.cfr;

@@ -546,15 +546,15 @@ bool Executor::solve(const WaveHost& w, uint64_t version, std::vector<Result>* o
     return true;
 }
 
-bool Executor::time_wave(const WaveHost& w, uint64_t version, uint32_t reps, double* wave_ms, ScheduleTimes* prof,
-                         std::string* err) {
+bool Executor::time_wave(const WaveHost& w, uint64_t version, uint32_t warmup, uint32_t reps, double* wave_ms,
+                         ScheduleTimes* prof, std::string* err) {
     auto it = banks_.find(version);
     if (it == banks_.end()) {
         *err = "GPU weight version " + std::to_string(version) + " is unavailable";
         return false;
     }
     if (!upload(w, it->second, err)) return false;
-    run_schedule(w, it->second, nullptr);  // warm
+    for (uint32_t r = 0; r < warmup; r++) run_schedule(w, it->second, nullptr);
     HIP_TRY(hipStreamSynchronize(stream_));
     HIP_TRY(hipGetLastError());
     hipEvent_t a, b;

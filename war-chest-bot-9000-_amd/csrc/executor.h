@@ -62,10 +62,10 @@ class Executor {
 
     // Upload, run the whole schedule, collect one result per job.
     bool solve(const WaveHost& w, uint64_t version, std::vector<Result>* out, std::string* err);
-    // Upload once, run `reps` schedules; mean wave time, and per-class times of
-    // one extra profiled schedule.
-    bool time_wave(const WaveHost& w, uint64_t version, uint32_t reps, double* wave_ms, ScheduleTimes* prof,
-                   std::string* err);
+    // Upload once, run `warmup` untimed schedules, then `reps` timed ones; mean
+    // wave time, and per-class times of one extra profiled schedule.
+    bool time_wave(const WaveHost& w, uint64_t version, uint32_t warmup, uint32_t reps, double* wave_ms,
+                   ScheduleTimes* prof, std::string* err);
     // The leaf GEMM chain alone on rows x in host inputs.
     bool mlp_forward(uint64_t version, uint32_t rows, const float* x, float* out, std::string* err);
     bool time_mlp(uint64_t version, uint32_t rows, const float* x, uint32_t reps, double* chain_ms,

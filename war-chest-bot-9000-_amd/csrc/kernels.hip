@@ -297,8 +297,10 @@ __device__ __forceinline__ void backprop_task(const WaveDev& w, int p, Task q, i
 // One CFR iteration (or one fixed-strategy value pass) for traverser p, one
 // workgroup per tree: leaf values, bottom-up values with the regret update,
 // top-down reach under the new strategy, average accumulation.
-__global__ __launch_bounds__(BLOCK) void k_cfr(WaveDev w, const float* head_out, uint32_t heads, int p, int mode,
-                                             float da, float db, float ds, float predict) {
+template <int MODE>
+__global__ __launch_bounds__(BLOCK) void k_cfr(WaveDev w, const float* head_out, uint32_t heads, int p, float da,
+                                             float db, float ds, float predict) {
+    constexpr int mode = MODE;
     const TreeDev t = w.trees[blockIdx.x];
     const int opp = 1 - p;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
@@ -350,8 +352,12 @@ __global__ __launch_bounds__(BLOCK) void k_cfr(WaveDev w, const float* head_out,
 
 void launch_cfr(const WaveDev& w, const float* head_out, uint32_t heads, int traverser, int mode, float da,
                 float db, float ds, float predict, hipStream_t s) {
-    hipLaunchKernelGGL(k_cfr, dim3(w.ntrees), dim3(BLOCK), 0, s, w, head_out, heads, traverser, mode, da, db, ds,
-                       predict);
+    if (mode == MODE_VALUE)
+        hipLaunchKernelGGL(k_cfr<MODE_VALUE>, dim3(w.ntrees), dim3(BLOCK), 0, s, w, head_out, heads, traverser, da,
+                           db, ds, predict);
+    else
+        hipLaunchKernelGGL(k_cfr<MODE_REGRET>, dim3(w.ntrees), dim3(BLOCK), 0, s, w, head_out, heads, traverser, da,
+                           db, ds, predict);
 }
 
 // Average strategy: sum / row sum, uniform when the sum is not positive, the

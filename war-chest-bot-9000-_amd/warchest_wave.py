@@ -151,7 +151,7 @@ def _declare(L):
     L.wc_wave_free.restype = None
     L.wc_wave_stats_get.argtypes = [C.c_void_p, C.POINTER(WaveStats)]
     L.wc_solve_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p)]
-    L.wc_time_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint32,
+    L.wc_time_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32,
                                C.POINTER(C.c_double), C.POINTER(C.c_double)]
     L.wc_mlp_forward.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, _f32p, _f32p]
     L.wc_time_mlp.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, _f32p, C.c_uint32,
@@ -366,10 +366,12 @@ class Executor:
         _check(lib().wc_solve_wave(self.h, wave.h, version, res))
         return [SolveResult.take(res[k]) for k in range(wave.njobs)]
 
-    def time_wave(self, wave: Wave, version: int, reps: int):
+    def time_wave(self, wave: Wave, version: int, reps: int, warmup: int = 1):
+        """Mean device ms per wave over `reps` timed schedules after `warmup` untimed
+        ones, and one profiled schedule's [cfr, mlp, leaf input, other, mean cfr launch] ms."""
         ms = C.c_double()
         parts = (C.c_double * 5)()
-        _check(lib().wc_time_wave(self.h, wave.h, version, reps, C.byref(ms), parts))
+        _check(lib().wc_time_wave(self.h, wave.h, version, warmup, reps, C.byref(ms), parts))
         return ms.value, list(parts)
 
     def mlp(self, version: int, x: np.ndarray, heads: int) -> np.ndarray:
