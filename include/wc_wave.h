@@ -126,6 +126,13 @@ typedef struct wc_wave_stats {
 } wc_wave_stats;
 int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* out);
 
+/* Read-only view of one packed uint32 index array of a wave, by name, for tests
+ * and tooling: "row_node", "reach_base", "vals_base", "exit_node", "exit_coff",
+ * "legal_value", "child_start", "child", "legal_off". Returns NULL (and sets
+ * wc_last_error) for an unknown name; *n receives the element count. The view
+ * lives as long as the wave. */
+const uint32_t* wc_wave_array(const wc_wave* w, const char* name, size_t* n);
+
 /* Executor::launch + collect (+ Harvest::unpack): runs the whole schedule,
  * blocks, and returns one result per job in submission order
  * (results[k] owned by the caller). */

@@ -148,6 +148,32 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
     return WC_OK;
 }
 
+const uint32_t* wc_wave_array(const wc_wave* w, const char* name, size_t* n) {
+    if (n) *n = 0;
+    if (!w || !name) {
+        fail(WC_ERR_INVALID, "wc_wave_array: null argument");
+        return nullptr;
+    }
+    const WaveHost& h = w->host;
+    const std::vector<uint32_t>* v = nullptr;
+    const std::string k = name;
+    if (k == "row_node") v = &h.row_node;
+    else if (k == "reach_base") v = &h.reach_base;
+    else if (k == "vals_base") v = &h.vals_base;
+    else if (k == "exit_node") v = &h.exit_node;
+    else if (k == "exit_coff") v = &h.exit_coff;
+    else if (k == "legal_value") v = &h.legal_value;
+    else if (k == "child_start") v = &h.child_start;
+    else if (k == "child") v = &h.child;
+    else if (k == "legal_off") v = &h.legal_off;
+    if (!v) {
+        fail(WC_ERR_INVALID, "wc_wave_array: unknown array " + k);
+        return nullptr;
+    }
+    if (n) *n = v->size();
+    return v->data();
+}
+
 int wc_solve_wave(wc_executor* ex, wc_wave* w, uint64_t version, wc_result** results) {
     if (!ex || !w || !results) return fail(WC_ERR_INVALID, "wc_solve_wave: null argument");
     std::vector<Result> out;

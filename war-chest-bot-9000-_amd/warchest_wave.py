@@ -102,7 +102,7 @@ EXPORTS = [
     "wc_result_tag", "wc_result_weight_version", "wc_result_strategy", "wc_result_root_values",
     "wc_result_carries", "wc_result_free",
     "wc_executor_create", "wc_executor_destroy", "wc_executor_publish",
-    "wc_wave_pack", "wc_wave_free", "wc_wave_stats_get", "wc_solve_wave", "wc_time_wave",
+    "wc_wave_pack", "wc_wave_free", "wc_wave_stats_get", "wc_wave_array", "wc_solve_wave", "wc_time_wave",
     "wc_mlp_forward", "wc_time_mlp",
     "wc_job_roundtrip", "wc_job_validate",
     "wc_synth_spec_default", "wc_synth", "wc_jobset_count", "wc_jobset_job", "wc_jobset_free",
@@ -150,6 +150,8 @@ def _declare(L):
     L.wc_wave_free.argtypes = [C.c_void_p]
     L.wc_wave_free.restype = None
     L.wc_wave_stats_get.argtypes = [C.c_void_p, C.POINTER(WaveStats)]
+    L.wc_wave_array.argtypes = [C.c_void_p, C.c_char_p, C.POINTER(C.c_size_t)]
+    L.wc_wave_array.restype = _u32p
     L.wc_solve_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p)]
     L.wc_time_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32,
                                C.POINTER(C.c_double), C.POINTER(C.c_double)]
@@ -333,6 +335,14 @@ class Wave:
         s = WaveStats()
         _check(lib().wc_wave_stats_get(self.h, C.byref(s)))
         return s.as_dict()
+
+    def array(self, name: str) -> np.ndarray:
+        """A copy of one packed index array (wc_wave_array)."""
+        n = C.c_size_t()
+        p = lib().wc_wave_array(self.h, name.encode(), C.byref(n))
+        if not p:
+            _check(-1)
+        return np.ctypeslib.as_array(p, (n.value,)).copy() if n.value else np.zeros(0, np.uint32)
 
     def close(self):
         if self.h:
