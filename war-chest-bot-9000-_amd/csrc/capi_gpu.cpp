@@ -1,4 +1,5 @@
 // Device-facing entry points of the C ABI: executor, wave, service, results.
+#include <cstdlib>
 #include <cstring>
 #include <exception>
 #include <memory>
@@ -88,8 +89,15 @@ int wc_wave_pack(const uint8_t* const* jobs, const size_t* lens, uint32_t njobs,
     for (uint32_t k = 0; k < njobs; k++)
         if (!jobs[k] || !from_bytes(jobs[k], lens[k], &parsed[k], &err))
             return fail(WC_ERR_INVALID, "job " + std::to_string(k) + ": " + err);
+    // WC_UNIT_SLOTS tunes the subtree-unit budget (value slots per unit).
+    uint32_t slots = UNIT_SLOTS;
+    if (const char* env = std::getenv("WC_UNIT_SLOTS")) {
+        long v = std::strtol(env, nullptr, 10);
+        if (v < 64 || v > (1L << 24)) return fail(WC_ERR_INVALID, "WC_UNIT_SLOTS out of range [64, 2^24]");
+        slots = (uint32_t)v;
+    }
     auto* w = new wc_wave;
-    if (!pack_wave(std::move(parsed), &w->host, &err)) {
+    if (!pack_wave(std::move(parsed), &w->host, &err, slots)) {
         delete w;
         return fail(WC_ERR_INVALID, err);
     }
@@ -114,6 +122,8 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
     s->rows = h.rows();
     s->terminals = (uint32_t)h.term_node.size();
     s->levels = h.max_levels;
+    s->units = (uint32_t)h.units.size();
+    s->subtree_units = h.nsub;
     s->iters = h.meta.iters;
     s->nroots_max = h.nroots_max;
     s->carry_slots = h.carry_slots;
@@ -136,12 +146,16 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
     for (int p = 0; p < 2; p++)
         tb += 8 * (h.back_task[p].size() + h.reach_task[p].size() + h.decision[p].size()) +
               4 * (h.back_lvl[p].size() + h.reach_lvl[p].size());
+    tb += sizeof(UnitDev) * h.units.size() + 4 * (h.unit_row.size() + h.unit_term.size());
     s->table_bytes = tb;
     s->arena_bytes = 4 * (4ull * h.ncells + 2ull * h.reach_len + h.vals_len + 2ull * h.rows() * (h.net.pool + 1) +
                           h.root_values_len) +
                      2ull * h.carry_slots * h.snapshot_configs;
-    s->cfr_bytes_per_iter[0] = cfr_bytes_per_iter(h, 0);
-    s->cfr_bytes_per_iter[1] = cfr_bytes_per_iter(h, 1);
+    for (int p = 0; p < 2; p++) {
+        CfrBytes cb = cfr_bytes_per_iter(h, p);
+        s->cfr_bytes_per_iter[p] = cb.total();
+        for (int k = 0; k < 3; k++) s->cfr_bytes_by_kernel[p][k] = cb.part[k];
+    }
     const NetShape& ns = h.net;
     s->mlp_flops_per_query = 2ull * (uint64_t(ns.in) * ns.hidden + uint64_t(ns.layers - 1) * ns.hidden * ns.hidden +
                                      uint64_t(ns.hidden) * ns.heads);
@@ -199,6 +213,9 @@ int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup,
         kernel_ms[2] = prof.leaf_input;
         kernel_ms[3] = prof.other;
         kernel_ms[4] = prof.cfr_launch_mean;
+        kernel_ms[5] = prof.back_mean;
+        kernel_ms[6] = prof.top_mean;
+        kernel_ms[7] = prof.reach_mean;
     }
     return WC_OK;
 }

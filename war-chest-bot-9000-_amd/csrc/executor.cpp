@@ -208,8 +208,8 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         size_t node_meta, nc, child_start, child, legal_row_of, legal_off, legal_value, draw_off, draw_row_off,
             draw_row_start, draw_to, draw_p, reach_base, vals_base, parent, rev_row_of, rev_start, rev_src, rev_cell,
             rvd_row_of, rvd_start, rvd_src, rvd_p, row_node, row_cfg_off, row_cfg, cfg_key, cfg_emb, pub_raw,
-            term_node, term_util, roots, carried, exit_node, exit_coff, trees, bt0, bt1, rt0, rt1, d0, d1, bl0, bl1,
-            rl0, rl1;
+            term_node, term_util, roots, carried, exit_node, exit_coff, trees, units, bt[2], rt[2], dc[2], bl[2],
+            rl[2], unit_row, unit_term;
     } o;
     o.node_meta = blob.put(w.node_meta);
     o.nc = blob.put(w.node_nc);
@@ -247,16 +247,16 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     o.exit_node = blob.put(w.exit_node);
     o.exit_coff = blob.put(w.exit_coff);
     o.trees = blob.put(w.trees);
-    o.bt0 = blob.put(w.back_task[0]);
-    o.bt1 = blob.put(w.back_task[1]);
-    o.rt0 = blob.put(w.reach_task[0]);
-    o.rt1 = blob.put(w.reach_task[1]);
-    o.d0 = blob.put(w.decision[0]);
-    o.d1 = blob.put(w.decision[1]);
-    o.bl0 = blob.put(w.back_lvl[0]);
-    o.bl1 = blob.put(w.back_lvl[1]);
-    o.rl0 = blob.put(w.reach_lvl[0]);
-    o.rl1 = blob.put(w.reach_lvl[1]);
+    o.units = blob.put(w.units);
+    for (int p = 0; p < 2; p++) {
+        o.bt[p] = blob.put(w.back_task[p]);
+        o.rt[p] = blob.put(w.reach_task[p]);
+        o.dc[p] = blob.put(w.decision[p]);
+        o.bl[p] = blob.put(w.back_lvl[p]);
+        o.rl[p] = blob.put(w.reach_lvl[p]);
+    }
+    o.unit_row = blob.put(w.unit_row);
+    o.unit_term = blob.put(w.unit_term);
     if (!ensure(&table_, &table_cap_, host_blob_.size(), err)) return false;
     HIP_TRY(hipMemcpyAsync(table_, host_blob_.data(), host_blob_.size(), hipMemcpyHostToDevice, stream_));
 
@@ -271,7 +271,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     };
     size_t a_regret = take(cells * 4), a_cur = take(cells * 4), a_sum = take(cells * 4), a_snap = take(cells * 4);
     size_t a_reach = take(rl * 4), a_sreach = take(rl * 4), a_vals = take(vl * 4);
-    size_t a_pooled = take(rows * 2 * ns.pool * 4), a_mass = take(rows * 2 * 4);
+    size_t a_mass = take(rows * 2 * 4);
     size_t a_roots = take(size_t(w.root_values_len) * 4);
     size_t a_carry = take(size_t(w.carry_slots) * w.snapshot_configs * 2);
     if (!ensure(&arena_, &arena_cap_, at, err)) return false;
@@ -283,8 +283,8 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         mt = a + std::max<size_t>(bytes, 4);
         return a;
     };
-    size_t m_x = mtake(rows * ns.in * esz), m_h0 = mtake(rows * ns.hidden * esz), m_h1 = mtake(rows * ns.hidden * esz),
-           m_out = mtake(rows * ns.heads * 4);
+    size_t m_x = mtake(rows * ns.in * esz), m_x1 = mtake(rows * ns.in * esz), m_h0 = mtake(rows * ns.hidden * esz),
+           m_h1 = mtake(rows * ns.hidden * esz), m_out = mtake(rows * ns.heads * 4);
     if (!ensure(&mlp_, &mlp_cap_, mt, err)) return false;
 
     char* T = (char*)table_;
@@ -328,16 +328,19 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     d.exit_node = (const uint32_t*)(T + o.exit_node);
     d.exit_coff = (const uint32_t*)(T + o.exit_coff);
     d.trees = (const TreeDev*)(T + o.trees);
-    d.back_task0 = (const Task*)(T + o.bt0);
-    d.back_task1 = (const Task*)(T + o.bt1);
-    d.reach_task0 = (const Task*)(T + o.rt0);
-    d.reach_task1 = (const Task*)(T + o.rt1);
-    d.decision0 = (const Task*)(T + o.d0);
-    d.decision1 = (const Task*)(T + o.d1);
-    d.back_lvl0 = (const uint32_t*)(T + o.bl0);
-    d.back_lvl1 = (const uint32_t*)(T + o.bl1);
-    d.reach_lvl0 = (const uint32_t*)(T + o.rl0);
-    d.reach_lvl1 = (const uint32_t*)(T + o.rl1);
+    d.units = (const UnitDev*)(T + o.units);
+    for (int p = 0; p < 2; p++) {
+        d.back_task[p] = (const Task*)(T + o.bt[p]);
+        d.reach_task[p] = (const Task*)(T + o.rt[p]);
+        d.decision[p] = (const Task*)(T + o.dc[p]);
+        d.back_lvl[p] = (const uint32_t*)(T + o.bl[p]);
+        d.reach_lvl[p] = (const uint32_t*)(T + o.rl[p]);
+        d.ndec[p] = (uint32_t)w.decision[p].size();
+    }
+    d.unit_row = (const uint32_t*)(T + o.unit_row);
+    d.unit_term = (const uint32_t*)(T + o.unit_term);
+    d.nunits = (uint32_t)w.units.size();
+    d.nsub = w.nsub;
     d.regret = (float*)(A + a_regret);
     d.cur = (float*)(A + a_cur);
     d.sum = (float*)(A + a_sum);
@@ -345,7 +348,6 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     d.reach = (float*)(A + a_reach);
     d.snap_reach = (float*)(A + a_sreach);
     d.vals = (float*)(A + a_vals);
-    d.pooled = (float*)(A + a_pooled);
     d.mass = (float*)(A + a_mass);
     d.root_values = (float*)(A + a_roots);
     d.carry = (uint16_t*)(A + a_carry);
@@ -357,13 +359,15 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     d.snapshot_configs = w.snapshot_configs;
     d.nexit = (uint32_t)w.exit_node.size();
     d.ncells = w.ncells;
-    d.ndec0 = (uint32_t)w.decision[0].size();
-    d.ndec1 = (uint32_t)w.decision[1].size();
     X_ = M + m_x;
+    Xq_[0] = M + m_x;
+    Xq_[1] = M + m_x1;
     H_[0] = M + m_h0;
     H_[1] = M + m_h1;
     head_out_ = (float*)(M + m_out);
     rows_ = w.rows();
+    launch_query_static(d, precision_, Xq_[0], Xq_[1], stream_);
+    HIP_TRY(hipGetLastError());
     HIP_TRY(hipStreamSynchronize(stream_));
     return true;
 }
@@ -404,9 +408,10 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     const WaveDev& d = dev_;
     hipStream_t s = stream_;
     const Meta& m = w.meta;
+    const uint32_t nsub = w.nsub, ntop = (uint32_t)w.units.size() - w.nsub;
     // Per-class attribution: an event after every launch group, binned by class.
+    enum { C_BACK = 0, C_TOP = 1, C_REACH = 2, C_MLP = 3, C_LEAF = 4, C_OTHER = 5 };
     std::vector<std::pair<hipEvent_t, int>> ev;
-    enum { C_CFR = 0, C_MLP = 1, C_LEAF = 2, C_OTHER = 3 };
     hipEvent_t start = nullptr;
     auto mark = [&](int cls) {
         if (!prof) return;
@@ -420,19 +425,22 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         hipEventRecord(start, s);
     }
     auto mlp = [&](int q) {
-        launch_build_x(d, q, precision_, X_, s);
-        mark(C_LEAF);
-        run_mlp(bank, d.rows, X_, nullptr);
+        run_mlp(bank, d.rows, Xq_[q], nullptr);
         mark(C_MLP);
+    };
+    // Both players' reach under a fixed strategy: tops first, then their subtrees.
+    auto reach_both = [&](float* reach, const float* strat) {
+        launch_reach(d, nsub, ntop, reach, strat, -1, false, s);
+        launch_reach(d, 0, nsub, reach, strat, -1, false, s);
     };
 
     launch_zero(d.regret, w.ncells, s);
     launch_init_strategy(d, s);
     launch_seed_reach(d, d.reach, -1, s);
-    launch_reach_both(d, d.reach, d.cur, s);
+    reach_both(d.reach, d.cur);
     launch_seed_sum(d, s);
     if (w.carry_slots) launch_gather_carry(d, d.reach, 0, s);
-    launch_pool(d, -1, s);
+    launch_pool(d, -1, precision_, Xq_[0], Xq_[1], s);
     mark(C_OTHER);
     if (m.iters == 0) launch_normalize(d, 0, 0, s);
     for (uint32_t t = 0; t < m.iters; t++) {
@@ -441,9 +449,13 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         const float mm = (float)(t / 2 + 1);
         const float da = cfr_factor(mm, m.cfr.alpha), db = cfr_factor(mm, m.cfr.beta);
         const float ds = std::pow(mm / (mm + 1.0f), m.cfr.gamma);
-        launch_cfr(d, head_out_, bank.ns.heads, p, MODE_REGRET, da, db, ds, m.cfr.predict, s);
-        mark(C_CFR);
-        launch_pool(d, p, s);
+        launch_sweep(d, false, 0, nsub, head_out_, bank.ns.heads, p, MODE_REGRET, da, db, ds, m.cfr.predict, s);
+        mark(C_BACK);
+        launch_sweep(d, true, nsub, ntop, head_out_, bank.ns.heads, p, MODE_REGRET, da, db, ds, m.cfr.predict, s);
+        mark(C_TOP);
+        launch_reach(d, 0, nsub, d.reach, d.cur, p, true, s);
+        mark(C_REACH);
+        launch_pool(d, p, precision_, Xq_[0], Xq_[1], s);
         mark(C_LEAF);
         const uint32_t done = t + 1;
         auto it = std::find(m.snap_iters.begin(), m.snap_iters.end(), done);
@@ -452,7 +464,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
             launch_normalize(d, 1, done >= 2 ? 1 : 0, s);
             if (m.snapshots && si + 1 < m.snap_iters.size()) {
                 launch_seed_reach(d, d.snap_reach, -1, s);
-                launch_reach_both(d, d.snap_reach, d.snap, s);
+                reach_both(d.snap_reach, d.snap);
                 launch_gather_carry(d, d.snap_reach, (int)si, s);
             }
             mark(C_OTHER);
@@ -461,13 +473,14 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     // Phase 2: root values under the final average for every carried root.
     for (uint32_t root = 0; root < w.nroots_max; root++) {
         launch_seed_reach(d, d.reach, (int)root, s);
-        launch_reach_both(d, d.reach, d.snap, s);
+        reach_both(d.reach, d.snap);
         mark(C_OTHER);
-        launch_pool(d, -1, s);
+        launch_pool(d, -1, precision_, Xq_[0], Xq_[1], s);
         mark(C_LEAF);
         for (int p = 0; p < 2; p++) {
             mlp(p);
-            launch_cfr(d, head_out_, bank.ns.heads, p, MODE_VALUE, 0.0f, 0.0f, 0.0f, 0.0f, s);
+            launch_sweep(d, false, 0, nsub, head_out_, bank.ns.heads, p, MODE_VALUE, 0.0f, 0.0f, 0.0f, 0.0f, s);
+            launch_sweep(d, true, nsub, ntop, head_out_, bank.ns.heads, p, MODE_VALUE, 0.0f, 0.0f, 0.0f, 0.0f, s);
             launch_collect_root(d, (int)root, p, s);
             mark(C_OTHER);
         }
@@ -476,28 +489,27 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         hipStreamSynchronize(s);
         *prof = ScheduleTimes{};
         hipEvent_t prev = start;
-        double regret_cfr = 0;
-        uint32_t regret_n = 0;
+        double cls_ms[6] = {0, 0, 0, 0, 0, 0};
+        uint32_t cls_n[6] = {0, 0, 0, 0, 0, 0};
         for (auto& e : ev) {
             float ms = 0.0f;
             hipEventElapsedTime(&ms, prev, e.first);
-            switch (e.second) {
-                case C_CFR:
-                    prof->cfr += ms;
-                    regret_cfr += ms;
-                    regret_n++;
-                    break;
-                case C_MLP: prof->mlp += ms; break;
-                case C_LEAF: prof->leaf_input += ms; break;
-                default: prof->other += ms;
-            }
+            cls_ms[e.second] += ms;
+            cls_n[e.second]++;
             prev = e.first;
         }
         float tot = 0.0f;
         if (!ev.empty()) hipEventElapsedTime(&tot, start, ev.back().first);
         prof->total = tot;
-        prof->cfr_launches = regret_n;
-        prof->cfr_launch_mean = regret_n ? regret_cfr / regret_n : 0.0;
+        prof->cfr = cls_ms[C_BACK] + cls_ms[C_TOP] + cls_ms[C_REACH];
+        prof->mlp = cls_ms[C_MLP];
+        prof->leaf_input = cls_ms[C_LEAF];
+        prof->other = cls_ms[C_OTHER];
+        prof->back_mean = cls_n[C_BACK] ? cls_ms[C_BACK] / cls_n[C_BACK] : 0.0;
+        prof->top_mean = cls_n[C_TOP] ? cls_ms[C_TOP] / cls_n[C_TOP] : 0.0;
+        prof->reach_mean = cls_n[C_REACH] ? cls_ms[C_REACH] / cls_n[C_REACH] : 0.0;
+        prof->cfr_launches = cls_n[C_BACK];
+        prof->cfr_launch_mean = cls_n[C_BACK] ? prof->cfr / cls_n[C_BACK] : 0.0;
         for (auto& e : ev) hipEventDestroy(e.first);
         hipEventDestroy(start);
     }

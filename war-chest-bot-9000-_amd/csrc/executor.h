@@ -40,7 +40,8 @@ struct Result {
 // Per-launch-class device times of one schedule (milliseconds), from HIP events.
 struct ScheduleTimes {
     double total = 0, cfr = 0, mlp = 0, leaf_input = 0, other = 0;
-    double cfr_launch_mean = 0;  // mean duration of one CFR-sweep launch
+    double back_mean = 0, top_mean = 0, reach_mean = 0;  // mean duration of one launch of each CFR kernel
+    double cfr_launch_mean = 0;  // mean device time of one CFR iteration (the three kernels)
     uint32_t cfr_launches = 0;
 };
 
@@ -94,6 +95,7 @@ class Executor {
     std::vector<uint8_t> host_blob_;
     WaveDev dev_{};
     void* X_ = nullptr;
+    void* Xq_[2] = {};  // the wave's query inputs, one per traverser
     void* H_[2] = {};
     float* head_out_ = nullptr;
     uint32_t rows_ = 0;

@@ -479,6 +479,16 @@ bool validate(const Job& job, std::string* err) {
         if (x >= N || seen[x]) return fail("bfs_order not a permutation");
         seen[x] = 1;
     }
+    // Levels are depths: the root alone at level 0, every child one level below its parent.
+    if (t.level_start.size() < 2 || t.level_start[0] != 0 || t.level_start[1] != 1 || t.bfs_order[0] != 0)
+        return fail("level 0 must hold the root alone");
+    std::vector<uint32_t> level(N, 0);
+    for (size_t l = 0; l + 1 < t.level_start.size(); l++) {
+        if (t.level_start[l + 1] < t.level_start[l] || t.level_start[l + 1] > N) return fail("level_start not monotone");
+        for (uint32_t k = t.level_start[l]; k < t.level_start[l + 1]; k++) level[t.bfs_order[k]] = (uint32_t)l;
+    }
+    for (uint32_t i = 1; i < N; i++)
+        if (level[i] != level[t.node_parent[i]] + 1) return fail("levels disagree with parents");
     return true;
 }
 

@@ -30,28 +30,39 @@ struct WaveDev {
     const float *roots, *carried;
     const uint32_t *exit_node, *exit_coff;
     const TreeDev* trees;
-    const Task *back_task0, *back_task1, *reach_task0, *reach_task1, *decision0, *decision1;
-    const uint32_t *back_lvl0, *back_lvl1, *reach_lvl0, *reach_lvl1;
+    const UnitDev* units;
+    const Task *back_task[2], *reach_task[2], *decision[2];
+    const uint32_t *back_lvl[2], *reach_lvl[2];
+    const uint32_t *unit_row, *unit_term;
     // mutable arena
     float *regret, *cur, *sum, *snap;
     float *reach, *snap_reach, *vals;
-    float *pooled, *mass, *root_values;
+    float *mass, *root_values;
     uint16_t* carry;
     // sizes
-    uint32_t ntrees, rows, pool, in, row_bytes, snapshot_configs, nexit, ncells;
-    uint32_t ndec0, ndec1;
+    uint32_t ntrees, nunits, nsub, rows, pool, in, row_bytes, snapshot_configs, nexit, ncells;
+    uint32_t ndec[2];
 };
 
 // Launchers (kernels.hip). All take the executor's stream.
 void launch_zero(float* p, size_t n, hipStream_t s);
 void launch_init_strategy(const WaveDev& w, hipStream_t s);
 void launch_seed_reach(const WaveDev& w, float* reach, int root_index, hipStream_t s);
-void launch_reach_both(const WaveDev& w, float* reach, const float* strat, hipStream_t s);
+// Top-down reach of units [unit0, unit0 + n) under `strat`, for one player or
+// both (player < 0); with `accumulate`, then sum += reach * cur over the
+// player's decision rows of each unit.
+void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
+                  bool accumulate, hipStream_t s);
 void launch_seed_sum(const WaveDev& w, hipStream_t s);
-void launch_pool(const WaveDev& w, int player /* -1 = both */, hipStream_t s);
-void launch_build_x(const WaveDev& w, int traverser, int precision, void* x, hipStream_t s);
-void launch_cfr(const WaveDev& w, const float* head_out, uint32_t heads, int traverser, int mode, float da,
-                float db, float ds, float predict, hipStream_t s);
+// Leaf reach masses and pooled beliefs of one player (-1 = both), written into
+// the query inputs x0 (traverser 0) and x1 (traverser 1) in the operand precision.
+void launch_pool(const WaveDev& w, int player, int precision, void* x0, void* x1, hipStream_t s);
+// Seat and public features of both query inputs (once per upload).
+void launch_query_static(const WaveDev& w, int precision, void* x0, void* x1, hipStream_t s);
+// Leaf values and the bottom-up sweep of units [unit0, unit0 + n) for the
+// traverser; for top units in regret mode, then their reach and accumulation.
+void launch_sweep(const WaveDev& w, bool top, uint32_t unit0, uint32_t n, const float* head_out, uint32_t heads,
+                  int traverser, int mode, float da, float db, float ds, float predict, hipStream_t s);
 void launch_normalize(const WaveDev& w, int touched0, int touched1, hipStream_t s);
 void launch_gather_carry(const WaveDev& w, const float* reach, int slot, hipStream_t s);
 void launch_collect_root(const WaveDev& w, int root, int player, hipStream_t s);

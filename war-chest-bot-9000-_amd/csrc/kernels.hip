@@ -18,6 +18,8 @@ namespace wc {
 #define SMOOTHF 1e-30f   // belief normalisation floor (engine/src/rebel.rs:359)
 
 constexpr int BLOCK = 256;
+// Top units hold the widest levels of the largest trees: they get the largest workgroup.
+constexpr int TOP_BLOCK = 1024;
 
 static inline unsigned grid_for(size_t n, int block = BLOCK) { return (unsigned)((n + block - 1) / block); }
 
@@ -37,12 +39,12 @@ void launch_zero(float* p, size_t n, hipStream_t s) {
 }
 
 __device__ __forceinline__ const Task& decision_task(const WaveDev& w, uint32_t i, int* p) {
-    if (i < w.ndec0) {
+    if (i < w.ndec[0]) {
         *p = 0;
-        return w.decision0[i];
+        return w.decision[0][i];
     }
     *p = 1;
-    return w.decision1[i - w.ndec0];
+    return w.decision[1][i - w.ndec[0]];
 }
 
 // ------------------------------------------------------------- CFR state
@@ -50,7 +52,7 @@ __device__ __forceinline__ const Task& decision_task(const WaveDev& w, uint32_t 
 // cur = 1/len over each acting row (engine/src/search.rs:826-836).
 __global__ void k_init_strategy(WaveDev w) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= w.ndec0 + w.ndec1) return;
+    if (i >= w.ndec[0] + w.ndec[1]) return;
     int p;
     Task q = decision_task(w, i, &p);
     uint32_t row = w.legal_row_of[q.node] + q.config;
@@ -60,7 +62,7 @@ __global__ void k_init_strategy(WaveDev w) {
 }
 
 void launch_init_strategy(const WaveDev& w, hipStream_t s) {
-    uint32_t n = w.ndec0 + w.ndec1;
+    uint32_t n = w.ndec[0] + w.ndec[1];
     if (n) hipLaunchKernelGGL(k_init_strategy, dim3(grid_for(n)), dim3(BLOCK), 0, s, w);
 }
 
@@ -82,6 +84,11 @@ void launch_seed_reach(const WaveDev& w, float* reach, int root_index, hipStream
     hipLaunchKernelGGL(k_seed_reach, dim3(w.ntrees), dim3(BLOCK), 0, s, w, reach, root_index);
 }
 
+// Rows of up to ROW_BATCH elements are handled with their loads issued as one
+// batch (indices, then the values they name) and the reduction taken after,
+// in element order; longer rows fall back to the element loop.
+constexpr uint32_t ROW_BATCH = 16;
+
 // One child config's reach: the reverse gather in stored order (the CPU's
 // scatter order, engine/src/serialize.rs:714-723).
 __device__ __forceinline__ void reach_task(const WaveDev& w, float* reach, const float* strat, int p, Task q) {
@@ -91,42 +98,125 @@ __device__ __forceinline__ void reach_task(const WaveDev& w, float* reach, const
     uint32_t rr = w.rev_row_of[node];
     if (rr != 0xffffffffu) {
         uint32_t row = rr + c;
-        for (uint32_t x = w.rev_start[row]; x < w.rev_start[row + 1]; x++)
-            v += reach[base + w.rev_src[x]] * strat[w.rev_cell[x]];
+        uint32_t lo = w.rev_start[row], n = w.rev_start[row + 1] - lo;
+        if (n <= ROW_BATCH) {
+            uint32_t src[ROW_BATCH], cell[ROW_BATCH];
+            float a[ROW_BATCH], b[ROW_BATCH];
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) {
+                    src[k] = w.rev_src[lo + k];
+                    cell[k] = w.rev_cell[lo + k];
+                }
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) {
+                    a[k] = reach[base + src[k]];
+                    b[k] = strat[cell[k]];
+                }
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) v += a[k] * b[k];
+        } else {
+            for (uint32_t x = lo; x < lo + n; x++) v += reach[base + w.rev_src[x]] * strat[w.rev_cell[x]];
+        }
     } else {
         uint32_t row = w.rvd_row_of[node] + c;
-        for (uint32_t x = w.rvd_start[row]; x < w.rvd_start[row + 1]; x++)
-            v += reach[base + w.rvd_src[x]] * w.rvd_p[x];
+        uint32_t lo = w.rvd_start[row], n = w.rvd_start[row + 1] - lo;
+        if (n <= ROW_BATCH) {
+            uint32_t src[ROW_BATCH];
+            float a[ROW_BATCH], pr[ROW_BATCH];
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) {
+                    src[k] = w.rvd_src[lo + k];
+                    pr[k] = w.rvd_p[lo + k];
+                }
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) a[k] = reach[base + src[k]];
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) v += a[k] * pr[k];
+        } else {
+            for (uint32_t x = lo; x < lo + n; x++) v += reach[base + w.rvd_src[x]] * w.rvd_p[x];
+        }
     }
     reach[w.reach_base[2 * node + p] + c] = v;
 }
 
-// Both players' reach under one fixed strategy, one workgroup per tree, top-down
-// levels separated by block barriers.
-__global__ __launch_bounds__(BLOCK) void k_reach_both(WaveDev w, float* reach, const float* strat) {
-    const TreeDev t = w.trees[blockIdx.x];
-    for (uint32_t l = 1; l < t.nlevels; l++) {
-        uint32_t b0 = w.reach_lvl0[t.lvl0 + l], e0 = w.reach_lvl0[t.lvl0 + l + 1];
-        uint32_t b1 = w.reach_lvl1[t.lvl0 + l], e1 = w.reach_lvl1[t.lvl0 + l + 1];
-        uint32_t n0 = e0 - b0, n = n0 + (e1 - b1);
-        for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
-            if (k < n0)
-                reach_task(w, reach, strat, 0, w.reach_task0[b0 + k]);
-            else
-                reach_task(w, reach, strat, 1, w.reach_task1[b1 + k - n0]);
+// Average-strategy accumulation over one unit's decision rows of player p
+// (engine/src/search.rs:1818-1835).
+__device__ __forceinline__ void accumulate_unit(const WaveDev& w, const UnitDev& u, int p) {
+    const Task* dec = w.decision[p];
+    for (uint32_t k = u.dec0[p] + threadIdx.x; k < u.dec1[p]; k += blockDim.x) {
+        Task q = dec[k];
+        uint32_t row = w.legal_row_of[q.node] + q.config;
+        float r = w.reach[w.reach_base[2 * q.node + p] + q.config];
+        uint32_t lo = w.legal_off[row], n = w.legal_off[row + 1] - lo;
+        if (n <= ROW_BATCH) {
+            float cu[ROW_BATCH], sm[ROW_BATCH];
+#pragma unroll
+            for (uint32_t j = 0; j < ROW_BATCH; j++)
+                if (j < n) {
+                    cu[j] = w.cur[lo + j];
+                    sm[j] = w.sum[lo + j];
+                }
+#pragma unroll
+            for (uint32_t j = 0; j < ROW_BATCH; j++)
+                if (j < n) w.sum[lo + j] = sm[j] + r * cu[j];
+        } else {
+            for (uint32_t g = lo; g < lo + n; g++) w.sum[g] += r * w.cur[g];
+        }
+    }
+}
+
+// Top-down reach of one unit, level by level under block barriers: player p
+// alone, or both players (p < 0) whose task lists of a level are independent.
+__device__ __forceinline__ void reach_unit(const WaveDev& w, const UnitDev& u, float* reach, const float* strat,
+                                           int p) {
+    for (uint32_t l = 0; l < u.nlevels; l++) {
+        if (p < 0) {
+            uint32_t b0 = w.reach_lvl[0][u.lvl0 + l], e0 = w.reach_lvl[0][u.lvl0 + l + 1];
+            uint32_t b1 = w.reach_lvl[1][u.lvl0 + l], e1 = w.reach_lvl[1][u.lvl0 + l + 1];
+            uint32_t n0 = e0 - b0, n = n0 + (e1 - b1);
+            for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
+                if (k < n0)
+                    reach_task(w, reach, strat, 0, w.reach_task[0][b0 + k]);
+                else
+                    reach_task(w, reach, strat, 1, w.reach_task[1][b1 + k - n0]);
+            }
+        } else {
+            uint32_t b = w.reach_lvl[p][u.lvl0 + l], e = w.reach_lvl[p][u.lvl0 + l + 1];
+            for (uint32_t k = b + threadIdx.x; k < e; k += blockDim.x) reach_task(w, reach, strat, p, w.reach_task[p][k]);
         }
         __syncthreads();
     }
 }
 
-void launch_reach_both(const WaveDev& w, float* reach, const float* strat, hipStream_t s) {
-    hipLaunchKernelGGL(k_reach_both, dim3(w.ntrees), dim3(BLOCK), 0, s, w, reach, strat);
+template <int NT>
+__global__ __launch_bounds__(NT) void k_reach(WaveDev w, uint32_t unit0, float* reach, const float* strat,
+                                            int player, int accumulate) {
+    const UnitDev u = w.units[unit0 + blockIdx.x];
+    reach_unit(w, u, reach, strat, player);
+    if (accumulate) accumulate_unit(w, u, player);
+}
+
+void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
+                  bool accumulate, hipStream_t s) {
+    if (!n) return;
+    if (unit0 >= w.nsub)
+        hipLaunchKernelGGL(k_reach<TOP_BLOCK>, dim3(n), dim3(TOP_BLOCK), 0, s, w, unit0, reach, strat, player,
+                           accumulate ? 1 : 0);
+    else
+        hipLaunchKernelGGL(k_reach<BLOCK>, dim3(n), dim3(BLOCK), 0, s, w, unit0, reach, strat, player,
+                           accumulate ? 1 : 0);
 }
 
 // sum = reach * cur: one reach-weighted uniform strategy (engine/src/search.rs:854-870).
 __global__ void k_seed_sum(WaveDev w) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= w.ndec0 + w.ndec1) return;
+    if (i >= w.ndec[0] + w.ndec[1]) return;
     int p;
     Task q = decision_task(w, i, &p);
     uint32_t row = w.legal_row_of[q.node] + q.config;
@@ -135,58 +225,11 @@ __global__ void k_seed_sum(WaveDev w) {
 }
 
 void launch_seed_sum(const WaveDev& w, hipStream_t s) {
-    uint32_t n = w.ndec0 + w.ndec1;
+    uint32_t n = w.ndec[0] + w.ndec[1];
     if (n) hipLaunchKernelGGL(k_seed_sum, dim3(grid_for(n)), dim3(BLOCK), 0, s, w);
 }
 
 // --------------------------------------------------------------- leaf input
-
-// One wavefront per (network row, player): the leaf's reach mass, and the
-// pooled belief sum_c beta(c) e(c) with beta the normalised reach
-// (normalize_weights, engine/src/rebel.rs:1054-1068; accumulate, net.rs:161-170).
-// Every lane forms the mass in config order; lane k owns pooled[k].
-__global__ __launch_bounds__(BLOCK) void k_pool(WaveDev w, int player) {
-    uint32_t task = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    uint32_t lane = threadIdx.x & 63;
-    uint32_t row, p;
-    if (player < 0) {
-        row = task >> 1;
-        p = task & 1;
-    } else {
-        row = task;
-        p = (uint32_t)player;
-    }
-    if (row >= w.rows) return;
-    uint32_t node = w.row_node[row];
-    uint32_t n = w.nc[2 * node + p];
-    const float* r = w.reach + w.reach_base[2 * node + p];
-    float tot = 0.0f;
-    for (uint32_t c = 0; c < n; c++) tot += r[c];
-    float scale, flat;
-    if (tot > SMOOTHF) {
-        scale = 1.0f / tot;
-        flat = 0.0f;
-    } else {
-        scale = 0.0f;
-        flat = 1.0f / (float)(n > 0 ? n : 1);
-    }
-    uint32_t q = 2 * row + p;
-    if (lane == 0) w.mass[q] = tot;
-    const uint32_t* cfgs = w.row_cfg + w.row_cfg_off[q];
-    for (uint32_t k = lane; k < w.pool; k += 64) {
-        float acc = 0.0f;
-        for (uint32_t c = 0; c < n; c++) {
-            float wc = r[c] * scale + flat;
-            acc += wc * w.cfg_emb[(size_t)cfgs[c] * w.pool + k];
-        }
-        w.pooled[(size_t)q * w.pool + k] = acc;
-    }
-}
-
-void launch_pool(const WaveDev& w, int player, hipStream_t s) {
-    size_t waves = (size_t)w.rows * (player < 0 ? 2 : 1);
-    if (waves) hipLaunchKernelGGL(k_pool, dim3(grid_for(waves * 64)), dim3(BLOCK), 0, s, w, player);
-}
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rn(float x) {
     uint32_t u = __float_as_uint(x);
@@ -200,47 +243,147 @@ __device__ __forceinline__ uint16_t f32_to_f16_rn(float x) {
     return __builtin_bit_cast(uint16_t, h);
 }
 
-// Query rows for traverser q: [pooled_q | pooled_{1-q} | seat | public / 255].
 template <int PREC>
-__global__ void k_build_x(WaveDev w, int q, void* xout) {
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    size_t total = (size_t)w.rows * w.in;
-    if (i >= total) return;
-    uint32_t row = (uint32_t)(i / w.in), k = (uint32_t)(i % w.in);
-    uint32_t pool = w.pool;
-    float v;
-    if (k < pool)
-        v = w.pooled[(size_t)(2 * row + q) * pool + k];
-    else if (k < 2 * pool)
-        v = w.pooled[(size_t)(2 * row + 1 - q) * pool + (k - pool)];
-    else if (k == 2 * pool)
-        v = q ? 1.0f : -1.0f;
-    else
-        v = (float)w.pub_raw[(size_t)row * w.row_bytes + (k - 2 * pool - 1)] / 255.0f;
+__device__ __forceinline__ void store_operand(void* base, size_t i, float v) {
     if (PREC == WC_PRECISE)
-        ((float*)xout)[i] = v;
+        ((float*)base)[i] = v;
     else if (PREC == WC_F16)
-        ((uint16_t*)xout)[i] = f32_to_f16_rn(v);
+        ((uint16_t*)base)[i] = f32_to_f16_rn(v);
     else
-        ((uint16_t*)xout)[i] = f32_to_bf16_rn(v);
+        ((uint16_t*)base)[i] = f32_to_bf16_rn(v);
 }
 
-void launch_build_x(const WaveDev& w, int traverser, int precision, void* x, hipStream_t s) {
-    size_t n = (size_t)w.rows * w.in;
+__device__ __forceinline__ float lane_value(float v, uint32_t j) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)j));
+}
+__device__ __forceinline__ uint32_t lane_value(uint32_t v, uint32_t j) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)j);
+}
+
+// One wavefront per (network row, player): the leaf's reach mass, and the
+// pooled belief sum_c beta(c) e(c) with beta the normalised reach
+// (normalize_weights, engine/src/rebel.rs:1054-1068; accumulate,
+// net.rs:161-170). Lanes load 64 configs at a time; both reductions then run
+// in config order with every lane holding the running value, so the result is
+// the CPU's sequential sum. The pooled block goes straight into the two query
+// inputs that carry it: [pooled_q | pooled_{1-q} | seat | public] for
+// traverser q.
+template <int PREC>
+__global__ __launch_bounds__(BLOCK) void k_pool(WaveDev w, int player, void* x0, void* x1) {
+    const uint32_t task = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const uint32_t lane = threadIdx.x & 63;
+    uint32_t row, p;
+    if (player < 0) {
+        row = task >> 1;
+        p = task & 1;
+    } else {
+        row = task;
+        p = (uint32_t)player;
+    }
+    if (row >= w.rows) return;  // wave-uniform
+    const uint32_t node = w.row_node[row];
+    const uint32_t n = w.nc[2 * node + p];
+    const float* r = w.reach + w.reach_base[2 * node + p];
+    const uint32_t* cfgs = w.row_cfg + w.row_cfg_off[2 * row + p];
+    float tot = 0.0f;
+    for (uint32_t c0 = 0; c0 < n; c0 += 64) {
+        float v = c0 + lane < n ? r[c0 + lane] : 0.0f;
+        uint32_t m = n - c0 < 64 ? n - c0 : 64;
+        for (uint32_t j = 0; j < m; j++) tot += lane_value(v, j);
+    }
+    float scale, flat;
+    if (tot > SMOOTHF) {
+        scale = 1.0f / tot;
+        flat = 0.0f;
+    } else {
+        scale = 0.0f;
+        flat = 1.0f / (float)(n > 0 ? n : 1);
+    }
+    if (lane == 0) w.mass[2 * row + p] = tot;
+    const uint32_t pool = w.pool, in = w.in;
+    void* own = p ? x1 : x0;    // pooled_p is the first block of traverser p's query
+    void* other = p ? x0 : x1;  // and the second block of the other traverser's
+    for (uint32_t k0 = 0; k0 < pool; k0 += 64) {
+        const uint32_t k = k0 + lane;
+        const bool live = k < pool;
+        float acc = 0.0f;
+        for (uint32_t c0 = 0; c0 < n; c0 += 64) {
+            uint32_t cf = c0 + lane < n ? cfgs[c0 + lane] : 0u;
+            float beta = c0 + lane < n ? r[c0 + lane] * scale + flat : 0.0f;
+            uint32_t m = n - c0 < 64 ? n - c0 : 64;
+            uint32_t j = 0;
+            for (; j + 8 <= m; j += 8) {
+                float e[8], b[8];
+#pragma unroll
+                for (uint32_t t = 0; t < 8; t++) {
+                    uint32_t cj = lane_value(cf, j + t);
+                    b[t] = lane_value(beta, j + t);
+                    e[t] = live ? w.cfg_emb[(size_t)cj * pool + k] : 0.0f;
+                }
+#pragma unroll
+                for (uint32_t t = 0; t < 8; t++) acc += b[t] * e[t];
+            }
+            for (; j < m; j++) {
+                uint32_t cj = lane_value(cf, j);
+                float e = live ? w.cfg_emb[(size_t)cj * pool + k] : 0.0f;
+                acc += lane_value(beta, j) * e;
+            }
+        }
+        if (live) {
+            store_operand<PREC>(own, (size_t)row * in + k, acc);
+            store_operand<PREC>(other, (size_t)row * in + pool + k, acc);
+        }
+    }
+}
+
+void launch_pool(const WaveDev& w, int player, int precision, void* x0, void* x1, hipStream_t s) {
+    size_t waves = (size_t)w.rows * (player < 0 ? 2 : 1);
+    if (!waves) return;
+    dim3 g(grid_for(waves * 64));
+    if (precision == WC_PRECISE)
+        hipLaunchKernelGGL(k_pool<WC_PRECISE>, g, dim3(BLOCK), 0, s, w, player, x0, x1);
+    else if (precision == WC_F16)
+        hipLaunchKernelGGL(k_pool<WC_F16>, g, dim3(BLOCK), 0, s, w, player, x0, x1);
+    else
+        hipLaunchKernelGGL(k_pool<WC_BF16>, g, dim3(BLOCK), 0, s, w, player, x0, x1);
+}
+
+// The fixed part of both traversers' query inputs: the seat (-1 for player 0,
+// +1 for player 1) and the row's public features / 255.
+template <int PREC>
+__global__ void k_query_static(WaveDev w, void* x0, void* x1) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t width = w.in - 2 * w.pool;
+    if (i >= (size_t)w.rows * width) return;
+    uint32_t row = (uint32_t)(i / width), k = (uint32_t)(i % width);
+    size_t at = (size_t)row * w.in + 2 * w.pool + k;
+    if (k == 0) {
+        store_operand<PREC>(x0, at, -1.0f);
+        store_operand<PREC>(x1, at, 1.0f);
+    } else {
+        float v = (float)w.pub_raw[(size_t)row * w.row_bytes + (k - 1)] / 255.0f;
+        store_operand<PREC>(x0, at, v);
+        store_operand<PREC>(x1, at, v);
+    }
+}
+
+void launch_query_static(const WaveDev& w, int precision, void* x0, void* x1, hipStream_t s) {
+    size_t n = (size_t)w.rows * (w.in - 2 * w.pool);
     if (!n) return;
     if (precision == WC_PRECISE)
-        hipLaunchKernelGGL(k_build_x<WC_PRECISE>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, traverser, x);
+        hipLaunchKernelGGL(k_query_static<WC_PRECISE>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, x0, x1);
     else if (precision == WC_F16)
-        hipLaunchKernelGGL(k_build_x<WC_F16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, traverser, x);
+        hipLaunchKernelGGL(k_query_static<WC_F16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, x0, x1);
     else
-        hipLaunchKernelGGL(k_build_x<WC_BF16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, traverser, x);
+        hipLaunchKernelGGL(k_query_static<WC_BF16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, x0, x1);
 }
 
 // ------------------------------------------------------------- the sweep
 
 // One backprop task for traverser p (engine/src/search.rs:1672-1803).
-__device__ __forceinline__ void backprop_task(const WaveDev& w, int p, Task q, int mode, float da, float db,
-                                              float ds, float predict, const float* strat) {
+template <int MODE>
+__device__ __forceinline__ void backprop_task(const WaveDev& w, int p, Task q, float da, float db, float ds,
+                                              float predict, const float* strat) {
     uint32_t node = q.node, c = q.config;
     uint32_t meta = w.node_meta[node];
     uint32_t kind = meta & 3u, actor = meta >> 2;
@@ -252,28 +395,105 @@ __device__ __forceinline__ void backprop_task(const WaveDev& w, int p, Task q, i
         uint32_t lo = w.draw_row_start[rb + c], hi = w.draw_row_start[rb + c + 1];
         uint32_t cb = w.vals_base[2 * child + p];
         float v = 0.0f;
-        for (uint32_t x = lo; x < hi; x++) v += w.draw_p[d0 + x] * vals[cb + w.draw_to[d0 + x]];
+        uint32_t n = hi - lo;
+        if (n <= ROW_BATCH) {
+            uint32_t to[ROW_BATCH];
+            float pr[ROW_BATCH], cv[ROW_BATCH];
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) {
+                    to[k] = w.draw_to[d0 + lo + k];
+                    pr[k] = w.draw_p[d0 + lo + k];
+                }
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) cv[k] = vals[cb + to[k]];
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) v += pr[k] * cv[k];
+        } else {
+            for (uint32_t x = lo; x < hi; x++) v += w.draw_p[d0 + x] * vals[cb + w.draw_to[d0 + x]];
+        }
         vals[vb + c] = v;
         return;
     }
     if (actor != (uint32_t)p) {  // opponent decision: sum the children in child order
+        uint32_t lo = w.child_start[node], n = w.child_start[node + 1] - lo;
         float v = 0.0f;
-        for (uint32_t x = w.child_start[node]; x < w.child_start[node + 1]; x++)
-            v += vals[w.vals_base[2 * w.child[x] + p] + c];
+        if (n <= ROW_BATCH) {
+            uint32_t ch[ROW_BATCH], cb[ROW_BATCH];
+            float cv[ROW_BATCH];
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) ch[k] = w.child[lo + k];
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) cb[k] = w.vals_base[2 * ch[k] + p];
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) cv[k] = vals[cb[k] + c];
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < n) v += cv[k];
+        } else {
+            for (uint32_t x = lo; x < lo + n; x++) v += vals[w.vals_base[2 * w.child[x] + p] + c];
+        }
         vals[vb + c] = v;
         return;
     }
     uint32_t row = w.legal_row_of[node] + c;
     uint32_t lo = w.legal_off[row], hi = w.legal_off[row + 1];
-    const float* st = mode == MODE_VALUE ? strat : w.cur;
+    const float* st = MODE == MODE_VALUE ? strat : w.cur;
+    const uint32_t n = hi - lo;
+    if (n <= ROW_BATCH) {
+        uint32_t lv[ROW_BATCH];
+        float sv[ROW_BATCH], qv[ROW_BATCH], old[ROW_BATCH], sm[ROW_BATCH];
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < n) {
+                lv[k] = w.legal_value[lo + k];
+                sv[k] = st[lo + k];
+                if (MODE == MODE_REGRET) {
+                    old[k] = w.regret[lo + k];
+                    sm[k] = w.sum[lo + k];
+                }
+            }
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < n) qv[k] = lv[k] != 0xffffffffu ? vals[lv[k]] : 0.0f;
+        float base = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < n && lv[k] != 0xffffffffu) base += qv[k] * sv[k];
+        vals[vb + c] = base;
+        if (MODE == MODE_VALUE) return;
+        // Fused regret matching with DCFR discounting (search.rs:1742-1779).
+        float total = 0.0f, v[ROW_BATCH];
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < n) {
+                float delta = 0.0f;
+                if (lv[k] != 0xffffffffu) delta += qv[k];
+                delta -= base;
+                float r = old[k] * (old[k] > 0.0f ? da : db) + delta;
+                w.regret[lo + k] = r;
+                v[k] = fmaxf(r + predict * delta, EPSF);
+                total += v[k];
+                w.sum[lo + k] = sm[k] * ds;
+            }
+        float inv = total > 0.0f ? 1.0f / total : 1.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < n) w.cur[lo + k] = total > 0.0f ? v[k] * inv : v[k];
+        return;
+    }
     float base = 0.0f;
     for (uint32_t g = lo; g < hi; g++) {
         uint32_t lv = w.legal_value[g];
         if (lv != 0xffffffffu) base += vals[lv] * st[g];
     }
     vals[vb + c] = base;
-    if (mode == MODE_VALUE) return;
-    // Fused regret matching with DCFR discounting (search.rs:1742-1779).
+    if (MODE == MODE_VALUE) return;
     float total = 0.0f;
     for (uint32_t g = lo; g < hi; g++) {
         uint32_t lv = w.legal_value[g];
@@ -294,18 +514,24 @@ __device__ __forceinline__ void backprop_task(const WaveDev& w, int p, Task q, i
     }
 }
 
-// One CFR iteration (or one fixed-strategy value pass) for traverser p, one
-// workgroup per tree: leaf values, bottom-up values with the regret update,
-// top-down reach under the new strategy, average accumulation.
-template <int MODE>
-__global__ __launch_bounds__(BLOCK) void k_cfr(WaveDev w, const float* head_out, uint32_t heads, int p, float da,
-                                             float db, float ds, float predict) {
+// Leaf values and the bottom-up value sweep of one unit for traverser p, one
+// workgroup per unit: leaf values first (net value x opponent reach mass,
+// engine/src/search.rs:1587-1636), then levels from the deepest up, with the
+// fused regret/DCFR update at the traverser's rows. A top unit in regret mode
+// then pushes the traverser's reach down its levels under the new strategy
+// and accumulates the average strategy; subtree units do that in k_reach,
+// after every top unit has finished.
+template <int MODE, bool TOP>
+__global__ __launch_bounds__(TOP ? TOP_BLOCK : BLOCK) void k_sweep(WaveDev w, uint32_t unit0, const float* head_out,
+                                                                uint32_t heads, int p, float da, float db, float ds,
+                                                                float predict) {
     constexpr int mode = MODE;
-    const TreeDev t = w.trees[blockIdx.x];
+    const UnitDev u = w.units[unit0 + blockIdx.x];
     const int opp = 1 - p;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-    // Leaf values: net value x opponent reach mass (search.rs:1587-1636).
-    for (uint32_t r = t.row0 + wave; r < t.row0 + t.rows; r += nwaves) {
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nwaves = blockDim.x >> 6;
+    for (uint32_t k = u.row0 + wave; k < u.row1; k += nwaves) {
+        uint32_t r = w.unit_row[k];
         uint32_t node = w.row_node[r];
         uint32_t n = w.nc[2 * node + p];
         float m = w.mass[2 * r + opp];
@@ -314,50 +540,49 @@ __global__ __launch_bounds__(BLOCK) void k_cfr(WaveDev w, const float* head_out,
         const float* h = head_out + (size_t)r * heads;
         for (uint32_t c = lane; c < n; c += 64) out[c] = h[w.cfg_key[cfgs[c]]] * m;
     }
-    for (uint32_t k = t.term0 + threadIdx.x; k < t.term0 + t.nterm; k += blockDim.x) {
+    for (uint32_t x = u.term0 + threadIdx.x; x < u.term1; x += blockDim.x) {
+        uint32_t k = w.unit_term[x];
         uint32_t node = w.term_node[k];
         const float* ro = w.reach + w.reach_base[2 * node + opp];
         float m = 0.0f;
         for (uint32_t c = 0; c < w.nc[2 * node + opp]; c++) m += ro[c];
-        float u = (w.node_meta[node] >> 2) == (uint32_t)p ? w.term_util[k] : -w.term_util[k];
+        float uu = (w.node_meta[node] >> 2) == (uint32_t)p ? w.term_util[k] : -w.term_util[k];
         float* out = w.vals + w.vals_base[2 * node + p];
-        for (uint32_t c = 0; c < w.nc[2 * node + p]; c++) out[c] = u * m;
+        for (uint32_t c = 0; c < w.nc[2 * node + p]; c++) out[c] = uu * m;
     }
     __syncthreads();
-    const Task* back = p ? w.back_task1 : w.back_task0;
-    const uint32_t* blvl = p ? w.back_lvl1 : w.back_lvl0;
-    for (uint32_t l = t.nlevels; l-- > 0;) {
-        uint32_t b = blvl[t.lvl0 + l], e = blvl[t.lvl0 + l + 1];
+    const Task* back = w.back_task[p];
+    const uint32_t* blvl = w.back_lvl[p];
+    for (uint32_t l = u.nlevels; l-- > 0;) {
+        uint32_t b = blvl[u.lvl0 + l], e = blvl[u.lvl0 + l + 1];
         for (uint32_t k = b + threadIdx.x; k < e; k += blockDim.x)
-            backprop_task(w, p, back[k], mode, da, db, ds, predict, w.snap);
+            backprop_task<MODE>(w, p, back[k], da, db, ds, predict, w.snap);
         __syncthreads();
     }
-    if (mode == MODE_VALUE) return;
-    const Task* rt = p ? w.reach_task1 : w.reach_task0;
-    const uint32_t* rlvl = p ? w.reach_lvl1 : w.reach_lvl0;
-    for (uint32_t l = 1; l < t.nlevels; l++) {
-        uint32_t b = rlvl[t.lvl0 + l], e = rlvl[t.lvl0 + l + 1];
-        for (uint32_t k = b + threadIdx.x; k < e; k += blockDim.x) reach_task(w, w.reach, w.cur, p, rt[k]);
-        __syncthreads();
-    }
-    // Average-strategy accumulation over p's decision rows (search.rs:1818-1835).
-    const Task* dec = p ? w.decision1 : w.decision0;
-    for (uint32_t k = t.dec0[p] + threadIdx.x; k < t.dec1[p]; k += blockDim.x) {
-        Task q = dec[k];
-        uint32_t row = w.legal_row_of[q.node] + q.config;
-        float r = w.reach[w.reach_base[2 * q.node + p] + q.config];
-        for (uint32_t g = w.legal_off[row]; g < w.legal_off[row + 1]; g++) w.sum[g] += r * w.cur[g];
+    if (TOP && mode == MODE_REGRET) {
+        reach_unit(w, u, w.reach, w.cur, p);
+        accumulate_unit(w, u, p);
     }
 }
 
-void launch_cfr(const WaveDev& w, const float* head_out, uint32_t heads, int traverser, int mode, float da,
-                float db, float ds, float predict, hipStream_t s) {
-    if (mode == MODE_VALUE)
-        hipLaunchKernelGGL(k_cfr<MODE_VALUE>, dim3(w.ntrees), dim3(BLOCK), 0, s, w, head_out, heads, traverser, da,
-                           db, ds, predict);
-    else
-        hipLaunchKernelGGL(k_cfr<MODE_REGRET>, dim3(w.ntrees), dim3(BLOCK), 0, s, w, head_out, heads, traverser, da,
-                           db, ds, predict);
+void launch_sweep(const WaveDev& w, bool top, uint32_t unit0, uint32_t n, const float* head_out, uint32_t heads,
+                  int traverser, int mode, float da, float db, float ds, float predict, hipStream_t s) {
+    if (!n) return;
+#define WC_SWEEP(M, T)                                                                                        \
+    hipLaunchKernelGGL((k_sweep<M, T>), dim3(n), dim3(T ? TOP_BLOCK : BLOCK), 0, s, w, unit0, head_out, heads, \
+                       traverser, da, db, ds, predict)
+    if (mode == MODE_VALUE) {
+        if (top)
+            WC_SWEEP(MODE_VALUE, true);
+        else
+            WC_SWEEP(MODE_VALUE, false);
+    } else {
+        if (top)
+            WC_SWEEP(MODE_REGRET, true);
+        else
+            WC_SWEEP(MODE_REGRET, false);
+    }
+#undef WC_SWEEP
 }
 
 // Average strategy: sum / row sum, uniform when the sum is not positive, the
@@ -365,7 +590,7 @@ void launch_cfr(const WaveDev& w, const float* head_out, uint32_t heads, int tra
 // (engine/src/search.rs:899-938).
 __global__ void k_normalize(WaveDev w, int touched0, int touched1) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= w.ndec0 + w.ndec1) return;
+    if (i >= w.ndec[0] + w.ndec[1]) return;
     int p;
     Task q = decision_task(w, i, &p);
     uint32_t row = w.legal_row_of[q.node] + q.config;
@@ -381,7 +606,7 @@ __global__ void k_normalize(WaveDev w, int touched0, int touched1) {
 }
 
 void launch_normalize(const WaveDev& w, int touched0, int touched1, hipStream_t s) {
-    uint32_t n = w.ndec0 + w.ndec1;
+    uint32_t n = w.ndec[0] + w.ndec[1];
     if (n) hipLaunchKernelGGL(k_normalize, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, touched0, touched1);
 }
 

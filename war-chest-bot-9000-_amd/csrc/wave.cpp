@@ -20,17 +20,33 @@ bool same_meta(const Meta& a, const Meta& b) {
            a.snap_iters == b.snap_iters && a.net_dims == b.net_dims;
 }
 
+// DFS preorder of one tree, children in child order.
+std::vector<uint32_t> preorder(const Tables& t) {
+    std::vector<uint32_t> pre, stack{0};
+    pre.reserve(t.nodes);
+    while (!stack.empty()) {
+        uint32_t i = stack.back();
+        stack.pop_back();
+        pre.push_back(i);
+        for (uint32_t k = t.node_child_start[i + 1]; k-- > t.node_child_start[i];) stack.push_back(t.node_child[k]);
+    }
+    return pre;
+}
+
 // Per-player value slots: the two players share one span (values are built for
 // one traverser at a time); across a chance edge the non-drawing player's
 // vector is its sole child's and aliases it (engine/src/serialize.rs:447-480).
-bool value_layout(const Tables& t, std::vector<uint32_t> base[2], uint32_t* len, std::string* err) {
+// Slots are allocated in reverse preorder, so a subtree (a preorder range) owns
+// one contiguous run of slots.
+bool value_layout(const Tables& t, const std::vector<uint32_t>& pre, std::vector<uint32_t> base[2], uint32_t* len,
+                  std::string* err) {
     uint32_t lengths[2] = {0, 0};
     for (int p = 0; p < 2; p++) {
         base[p].assign(t.nodes, 0);
         std::vector<uint8_t> ready(t.nodes, 0);
         uint32_t at = 0;
-        for (size_t k = t.bfs_order.size(); k-- > 0;) {
-            uint32_t node = t.bfs_order[k];
+        for (size_t k = pre.size(); k-- > 0;) {
+            uint32_t node = pre[k];
             if (t.node_kind[node] == 1 && t.node_player[node] != p) {
                 uint32_t lo = t.node_child_start[node], hi = t.node_child_start[node + 1];
                 if (hi != lo + 1) {
@@ -39,7 +55,7 @@ bool value_layout(const Tables& t, std::vector<uint32_t> base[2], uint32_t* len,
                 }
                 uint32_t child = t.node_child[lo];
                 if (!ready[child]) {
-                    *err = "value layout: child not ready (bfs order)";
+                    *err = "value layout: child not ready";
                     return false;
                 }
                 base[p][node] = base[p][child];
@@ -65,7 +81,7 @@ void append_shift(std::vector<T>& dst, const std::vector<T>& src, size_t skip, T
 
 }  // namespace
 
-bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err) {
+bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_t unit_slots) {
     if (jobs.empty()) {
         *err = "cannot pack an empty wave";
         return false;
@@ -96,11 +112,12 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err) {
     w.rvd_start.push_back(0);
     w.row_cfg_off.push_back(0);
     w.exit_coff.push_back(0);
-    for (int p = 0; p < 2; p++) {
-        w.back_lvl[p].clear();
-        w.reach_lvl[p].clear();
+    if (unit_slots == 0) {
+        *err = "unit budget must be positive";
+        return false;
     }
     uint32_t cfg_total = 0;
+    std::vector<UnitDev> sub_units, top_units;
 
     for (const Job& job : jobs) {
         const Tables& t = job.t;
@@ -126,6 +143,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err) {
         TreeDev td{};
         td.node0 = node0;
         td.nodes = N;
+        const uint32_t row_base = row0, term_base = (uint32_t)w.term_node.size();
         for (uint32_t i = 0; i < N; i++) {
             w.node_meta.push_back(uint32_t(t.node_kind[i]) | uint32_t(t.node_player[i]) << 2);
             w.node_nc.push_back(t.nc(i, 0));
@@ -161,9 +179,14 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err) {
         }
         w.reach_len = reach_at;
 
+        const std::vector<uint32_t> pre = preorder(t);
+        if (pre.size() != N) {
+            *err = "tree is not connected from its root";
+            return false;
+        }
         std::vector<uint32_t> vb[2];
         uint32_t vlen = 0;
-        if (!value_layout(t, vb, &vlen, err)) return false;
+        if (!value_layout(t, pre, vb, &vlen, err)) return false;
         w.vals_base.resize(2 * size_t(node0 + N), 0);
         for (uint32_t i = 0; i < N; i++)
             for (int p = 0; p < 2; p++) w.vals_base[2 * (node0 + i) + p] = vals0 + vb[p][i];
@@ -205,10 +228,6 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err) {
         }
         cfg_total += t.ncfg;
         w.pub_raw.insert(w.pub_raw.end(), t.leaf_raw.begin(), t.leaf_raw.end());
-        td.row0 = row0;
-        td.rows = t.rows;
-        td.term0 = (uint32_t)w.term_node.size();
-        td.nterm = (uint32_t)t.term_leaves.size();
         for (size_t k = 0; k < t.term_leaves.size(); k++) {
             w.term_node.push_back(node0 + t.term_leaves[k]);
             w.term_util.push_back(t.terminal_utility[k]);
@@ -236,36 +255,113 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err) {
         append_shift<uint32_t>(w.exit_coff, t.snap_coff, 1, exit_cfg0, false);
         w.snapshot_configs += t.snapshot_configs();
 
-        // Level schedules of this tree.
-        const uint32_t L = t.nlevels();
-        td.nlevels = L;
-        td.lvl0 = w.lvl_len;
-        w.lvl_len += L + 1;
-        w.max_levels = std::max(w.max_levels, L);
-        for (int p = 0; p < 2; p++) {
-            for (uint32_t l = 0; l < L; l++) {
+        // Sweep units of this tree.
+        w.node_top.resize(node0 + N, 0);
+        std::vector<uint32_t> depth(N, 0);
+        for (uint32_t l = 0; l < t.nlevels(); l++)
+            for (uint32_t k = t.level_start[l]; k < t.level_start[l + 1]; k++) depth[t.bfs_order[k]] = l;
+        std::vector<uint64_t> sub(N, 0);
+        for (size_t k = pre.size(); k-- > 0;) {
+            uint32_t i = pre[k];
+            sub[i] += std::max<uint32_t>(std::max(t.nc(i, 0), t.nc(i, 1)), 1);
+            if (t.node_parent[i] != NONE) sub[t.node_parent[i]] += sub[i];
+        }
+        std::vector<uint32_t> pos(N);
+        for (uint32_t k = 0; k < N; k++) pos[pre[k]] = k;
+        std::vector<uint32_t> row_of(N, NONE), term_of(N, NONE);
+        for (uint32_t r = 0; r < t.rows; r++) row_of[t.leaf_rows[r]] = r;
+        for (uint32_t k = 0; k < t.term_leaves.size(); k++) term_of[t.term_leaves[k]] = k;
+        const uint32_t tree_index = (uint32_t)w.trees.size();
+        // Emit one unit over `nodes` (in preorder) with unit-local levels depth - d0.
+        auto emit = [&](const std::vector<uint32_t>& nodes, uint32_t d0, bool top) {
+            UnitDev u{};
+            u.tree = tree_index;
+            u.top = top ? 1u : 0u;
+            uint32_t L = 0;
+            for (uint32_t i : nodes) L = std::max(L, depth[i] - d0 + 1);
+            u.nlevels = L;
+            u.lvl0 = w.lvl_len;
+            w.lvl_len += L + 1;
+            w.max_levels = std::max(w.max_levels, L);
+            std::vector<std::vector<uint32_t>> by_level(L);
+            for (uint32_t i : nodes) by_level[depth[i] - d0].push_back(i);
+            uint64_t slots = 0;
+            for (uint32_t i : nodes) slots += std::max(t.nc(i, 0), t.nc(i, 1));
+            u.slots = (uint32_t)std::min<uint64_t>(slots, 0xffffffffu);
+            for (int p = 0; p < 2; p++) {
+                for (uint32_t l = 0; l < L; l++) {
+                    w.back_lvl[p].push_back((uint32_t)w.back_task[p].size());
+                    w.reach_lvl[p].push_back((uint32_t)w.reach_task[p].size());
+                    for (uint32_t local : by_level[l]) {
+                        uint32_t node = node0 + local;
+                        uint8_t kind = t.node_kind[local];
+                        if (kind != 2 && !(kind == 1 && t.node_player[local] != p))
+                            for (uint32_t c = 0; c < t.nc(local, p); c++) w.back_task[p].push_back({node, c});
+                        if (local != 0 && t.node_player[t.node_parent[local]] == p)
+                            for (uint32_t c = 0; c < t.nc(local, p); c++) w.reach_task[p].push_back({node, c});
+                    }
+                }
                 w.back_lvl[p].push_back((uint32_t)w.back_task[p].size());
                 w.reach_lvl[p].push_back((uint32_t)w.reach_task[p].size());
-                for (uint32_t k = t.level_start[l]; k < t.level_start[l + 1]; k++) {
-                    uint32_t local = t.bfs_order[k], node = node0 + local;
-                    uint8_t kind = t.node_kind[local];
-                    if (kind != 2 && !(kind == 1 && t.node_player[local] != p))
-                        for (uint32_t c = 0; c < t.nc(local, p); c++) w.back_task[p].push_back({node, c});
-                    if (local != 0 && t.node_player[t.node_parent[local]] == p)
-                        for (uint32_t c = 0; c < t.nc(local, p); c++) w.reach_task[p].push_back({node, c});
-                }
+                u.dec0[p] = (uint32_t)w.decision[p].size();
+                for (uint32_t local : nodes)
+                    if (t.node_kind[local] == 0 && t.node_player[local] == p)
+                        for (uint32_t c = 0; c < t.nc(local, p); c++) w.decision[p].push_back({node0 + local, c});
+                u.dec1[p] = (uint32_t)w.decision[p].size();
             }
-            w.back_lvl[p].push_back((uint32_t)w.back_task[p].size());
-            w.reach_lvl[p].push_back((uint32_t)w.reach_task[p].size());
-            td.dec0[p] = (uint32_t)w.decision[p].size();
-            for (uint32_t i = 0; i < N; i++)
-                if (t.node_kind[i] == 0 && t.node_player[i] == p)
-                    for (uint32_t c = 0; c < t.nc(i, p); c++) w.decision[p].push_back({node0 + i, c});
-            td.dec1[p] = (uint32_t)w.decision[p].size();
+            if (top)
+                for (uint32_t local : nodes) w.node_top[node0 + local] = 1;
+            u.row0 = (uint32_t)w.unit_row.size();
+            for (uint32_t local : nodes)
+                if (row_of[local] != NONE) w.unit_row.push_back(row_base + row_of[local]);
+            u.row1 = (uint32_t)w.unit_row.size();
+            u.term0 = (uint32_t)w.unit_term.size();
+            for (uint32_t local : nodes)
+                if (term_of[local] != NONE) w.unit_term.push_back(term_base + term_of[local]);
+            u.term1 = (uint32_t)w.unit_term.size();
+            (top ? top_units : sub_units).push_back(u);
+        };
+        // The nodes of the subtree rooted at r, in preorder.
+        auto subtree = [&](uint32_t r, std::vector<uint32_t>* out) {
+            uint32_t k = pos[r];
+            uint32_t end = k + 1;
+            while (end < N && depth[pre[end]] > depth[r]) end++;
+            out->insert(out->end(), pre.begin() + k, pre.begin() + end);
+        };
+        if (sub[0] <= unit_slots) {
+            emit(pre, 0, false);
+        } else {
+            std::vector<uint32_t> top;
+            for (uint32_t i : pre)
+                if (sub[i] > unit_slots) top.push_back(i);
+            // Runs of fitting sibling subtrees below each top node, in child order.
+            for (uint32_t i : top) {
+                std::vector<uint32_t> run;
+                uint64_t run_slots = 0;
+                for (uint32_t k = t.node_child_start[i]; k < t.node_child_start[i + 1]; k++) {
+                    uint32_t c = t.node_child[k];
+                    if (sub[c] > unit_slots) continue;
+                    if (!run.empty() && run_slots + sub[c] > unit_slots) {
+                        emit(run, depth[i] + 1, false);
+                        run.clear();
+                        run_slots = 0;
+                    }
+                    subtree(c, &run);
+                    run_slots += sub[c];
+                }
+                if (!run.empty()) emit(run, depth[i] + 1, false);
+            }
+            emit(top, 0, true);
         }
         w.trees.push_back(td);
     }
     w.child_start.push_back((uint32_t)w.child.size());
+    // Subtree units largest first (the device takes them in launch order), then the tops.
+    std::stable_sort(sub_units.begin(), sub_units.end(),
+                     [](const UnitDev& a, const UnitDev& b) { return a.slots > b.slots; });
+    w.nsub = (uint32_t)sub_units.size();
+    w.units = std::move(sub_units);
+    w.units.insert(w.units.end(), top_units.begin(), top_units.end());
     w.carry_slots = (w.meta.snapshots && w.meta.snap_iters.size() > 1) ? (uint32_t)w.meta.snap_iters.size() - 1 : 0;
     w.jobs = std::move(jobs);
     if (!validate_deep(w, err)) return false;
@@ -372,20 +468,30 @@ bool validate_deep(const WaveHost& w, std::string* err) {
             if (q.node >= N || q.config >= w.nc(q.node, p) || (w.node_meta[q.node] & 3u) != 0) return fail("decision task");
         if (w.back_lvl[p].size() != w.lvl_len || w.reach_lvl[p].size() != w.lvl_len) return fail("level arrays");
     }
-    for (const TreeDev& t : w.trees) {
-        if (uint64_t(t.node0) + t.nodes > N || uint64_t(t.lvl0) + t.nlevels + 1 > w.lvl_len) return fail("tree range");
+    if (w.unit_row.size() != rows || w.unit_term.size() != w.term_node.size()) return fail("unit leaf lists");
+    for (uint32_t r : w.unit_row)
+        if (r >= rows) return fail("unit_row");
+    for (uint32_t k : w.unit_term)
+        if (k >= w.term_node.size()) return fail("unit_term");
+    if (w.nsub > w.units.size()) return fail("unit counts");
+    for (const UnitDev& u : w.units) {
+        if (uint64_t(u.lvl0) + u.nlevels + 1 > w.lvl_len || u.tree >= w.trees.size()) return fail("unit range");
         for (int p = 0; p < 2; p++) {
             const auto& bl = w.back_lvl[p];
             const auto& rl = w.reach_lvl[p];
-            for (uint32_t l = 0; l < t.nlevels; l++) {
-                if (bl[t.lvl0 + l + 1] < bl[t.lvl0 + l] || bl[t.lvl0 + l + 1] > w.back_task[p].size())
+            for (uint32_t l = 0; l < u.nlevels; l++) {
+                if (bl[u.lvl0 + l + 1] < bl[u.lvl0 + l] || bl[u.lvl0 + l + 1] > w.back_task[p].size())
                     return fail("back levels");
-                if (rl[t.lvl0 + l + 1] < rl[t.lvl0 + l] || rl[t.lvl0 + l + 1] > w.reach_task[p].size())
+                if (rl[u.lvl0 + l + 1] < rl[u.lvl0 + l] || rl[u.lvl0 + l + 1] > w.reach_task[p].size())
                     return fail("reach levels");
             }
-            if (t.dec0[p] > t.dec1[p] || t.dec1[p] > w.decision[p].size()) return fail("decision range");
+            if (u.dec0[p] > u.dec1[p] || u.dec1[p] > w.decision[p].size()) return fail("decision range");
         }
-        if (uint64_t(t.row0) + t.rows > rows || uint64_t(t.term0) + t.nterm > w.term_node.size()) return fail("leaf range");
+        if (u.row0 > u.row1 || u.row1 > w.unit_row.size() || u.term0 > u.term1 || u.term1 > w.unit_term.size())
+            return fail("unit leaf range");
+    }
+    for (const TreeDev& t : w.trees) {
+        if (uint64_t(t.node0) + t.nodes > N) return fail("tree range");
         if (uint64_t(t.reach0) + t.reach_len > w.reach_len) return fail("reach range");
         if (t.n0 != w.nc(t.node0, 0) || t.n1 != w.nc(t.node0, 1)) return fail("root support");
         const uint64_t nr = uint64_t(t.n0) + t.n1;
@@ -400,48 +506,56 @@ bool validate_deep(const WaveHost& w, std::string* err) {
 // Algorithmic HBM bytes of one CFR iteration (readout, backprop with the
 // regret/DCFR update, reach gather, average accumulation) for traverser p:
 //   44 C_p  legal cells of p: successor index 4, child value 4, cur read 4 +
-//           write 4, regret read+write 8, sum read+write 8, accumulate: cur 4 +
-//           sum read+write 8
+//           write 4, regret read+write 8, sum read+write 8 (value sweep: 32);
+//           accumulate: cur 4 + sum read+write 8 (reach sweep: 12)
 //   16 G_p  gather entries into p's reach: source 4, cell or probability 4,
 //           parent reach 4, strategy 4
 //    4 S_p  p's reach slots written
-//   12 R_p  p's decision rows: row offsets 8, reach read by the accumulation 4
+//   12 R_p  p's decision rows: row offsets 8 (value sweep), reach read by the
+//           accumulation 4 (reach sweep)
 //    4 O_p  child-value reads at opponent decision nodes
 //   12 H_p  draw entries at p's chance nodes: successor 4, probability 4, value 4
 //    8 L_p  leaf value slots of p: net output read 4, value write 4
 //    4 L_o  opponent reach read for the leaf reach mass
-uint64_t cfr_bytes_per_iter(const WaveHost& w, int p) {
-    uint64_t C = 0, G = 0, S = 0, R = 0, O = 0, H = 0, Lp = 0, Lo = 0;
+// A node's value-sweep bytes go to the kernel that sweeps its unit's values
+// (subtree sweep or top sweep), its reach bytes to the kernel that gathers its
+// reach (subtree reach or top sweep).
+CfrBytes cfr_bytes_per_iter(const WaveHost& w, int p) {
+    CfrBytes out;
     const uint32_t N = w.nodes();
     for (uint32_t i = 0; i < N; i++) {
         uint32_t kind = w.node_meta[i] & 3u, actor = w.node_meta[i] >> 2;
         uint32_t ncp = w.nc(i, p);
+        const bool top = !w.node_top.empty() && w.node_top[i];
+        uint64_t& back = out.part[top ? 1 : 0];
+        uint64_t& reach = out.part[top ? 1 : 2];
         if (kind == 0 && actor == (uint32_t)p) {
-            R += ncp;
             uint32_t r0 = w.legal_row_of[i];
-            C += w.legal_off[r0 + ncp] - w.legal_off[r0];
+            uint64_t C = w.legal_off[r0 + ncp] - w.legal_off[r0];
+            back += 32 * C + 8 * uint64_t(ncp);
+            reach += 12 * C + 4 * uint64_t(ncp);
         } else if (kind == 0) {
-            O += uint64_t(ncp) * (w.child_start[i + 1] - w.child_start[i]);
+            back += 4 * uint64_t(ncp) * (w.child_start[i + 1] - w.child_start[i]);
         } else if (kind == 1 && actor == (uint32_t)p) {
             uint32_t rb = w.draw_row_off[i];
-            H += w.draw_row_start[rb + ncp] - w.draw_row_start[rb];
+            back += 12 * uint64_t(w.draw_row_start[rb + ncp] - w.draw_row_start[rb]);
         } else if (kind == 2) {
-            Lp += ncp;
-            Lo += w.nc(i, 1 - p);
+            back += 8 * uint64_t(ncp) + 4 * uint64_t(w.nc(i, 1 - p));
         }
         uint32_t par = w.parent[i];
         if (par != NONE && (w.node_meta[par] >> 2) == (uint32_t)p) {
-            S += ncp;
+            uint64_t G;
             if (w.rev_row_of[i] != NONE) {
                 uint32_t r0 = w.rev_row_of[i];
-                G += w.rev_start[r0 + ncp] - w.rev_start[r0];
+                G = w.rev_start[r0 + ncp] - w.rev_start[r0];
             } else {
                 uint32_t r0 = w.rvd_row_of[i];
-                G += w.rvd_start[r0 + ncp] - w.rvd_start[r0];
+                G = w.rvd_start[r0 + ncp] - w.rvd_start[r0];
             }
+            reach += 4 * uint64_t(ncp) + 16 * G;
         }
     }
-    return 44 * C + 16 * G + 4 * S + 12 * R + 4 * O + 12 * H + 8 * Lp + 4 * Lo;
+    return out;
 }
 
 }  // namespace wc

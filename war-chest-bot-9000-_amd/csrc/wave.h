@@ -1,12 +1,17 @@
 // Host packing of one immutable wave: jobs concatenated into one wave-global
 // index space, offsets patched, value/reach aliasing laid out, and the
-// per-tree level schedules the device sweeps walk.
+// unit schedules the device sweeps walk.
 //
 // Counterpart of the reference's `Wave::pack` (engine/src/gpu/wave.rs:132-644)
 // and `device_value_layout` (engine/src/serialize.rs:447-480). The reach and
-// value aliasing follow the reference exactly; the schedules differ: instead
-// of wave-wide level task lists walked under grid-wide barriers, every tree
-// keeps its own level lists so one workgroup can sweep it with block barriers.
+// value aliasing follow the reference; the schedules differ. Instead of
+// wave-wide level task lists walked under grid-wide barriers, each tree is cut
+// into units that one workgroup sweeps with block barriers: runs of sibling
+// subtrees that fit a slot budget (swept independently, largest first, so big
+// and small trees balance across the CUs) and, for trees that do not fit, the
+// top region above them (swept after its subtrees for values, before them for
+// reach). Value slots are allocated in reverse DFS preorder, so every unit's
+// slots form one contiguous window.
 #pragma once
 
 #include <cstdint>
@@ -21,19 +26,35 @@ struct Task {
     uint32_t node, config;
 };
 
-// Per-tree record the device kernels read (one workgroup per tree).
+// Per-tree record: root beliefs, carried roots, outputs.
 struct TreeDev {
-    uint32_t node0, nodes, nlevels, lvl0;  // lvl0: base of this tree's (nlevels + 1) level boundaries
-    uint32_t dec0[2], dec1[2];             // decision-row task ranges per player
-    uint32_t row0, rows, term0, nterm;     // network rows and terminal leaves
-    uint32_t reach0, reach_len;            // reach span (zeroed by seed)
-    uint32_t root0, n0, n1;                // root beliefs at roots[root0 ..], n0 + n1 floats
-    uint32_t carried0, nroots;             // carried roots at carried[carried0 + k * (n0 + n1)]
-    uint32_t root_value0;                  // output offset of this tree's root values
+    uint32_t node0, nodes;        // wave-global node range
+    uint32_t reach0, reach_len;   // reach span (zeroed by seed)
+    uint32_t root0, n0, n1;       // root beliefs at roots[root0 ..], n0 + n1 floats
+    uint32_t carried0, nroots;    // carried roots at carried[carried0 + k * (n0 + n1)]
+    uint32_t root_value0;         // output offset of this tree's root values
     uint32_t exit0, nexit;
-    uint32_t pad[2];
 };
-static_assert(sizeof(TreeDev) == 24 * 4, "TreeDev is 96 bytes");
+static_assert(sizeof(TreeDev) == 12 * 4, "TreeDev is 48 bytes");
+
+// One sweep unit, processed by one workgroup. A subtree unit is a run of
+// sibling subtrees whose value slots fit the unit budget; a top unit is the
+// part of one tree above its subtree units (the nodes whose own subtree does
+// not fit). Levels are unit-local depths; task and row lists live in the
+// wave's flattened arrays at the offsets given here.
+struct UnitDev {
+    uint32_t nlevels, lvl0;     // level boundaries at back_lvl / reach_lvl [lvl0, lvl0 + nlevels]
+    uint32_t dec0[2], dec1[2];  // decision rows of each player: decision[p][dec0 .. dec1)
+    uint32_t row0, row1;        // network leaf rows: unit_row[row0 .. row1)
+    uint32_t term0, term1;      // terminal leaves: unit_term[term0 .. term1)
+    uint32_t slots;             // value slots (max over players, before aliasing)
+    uint32_t tree, top;         // owning tree; 1 for a top unit
+    uint32_t pad[3];
+};
+static_assert(sizeof(UnitDev) == 16 * 4, "UnitDev is 64 bytes");
+
+// Default unit budget in value slots (floats of one player's value vector).
+constexpr uint32_t UNIT_SLOTS = 8192;
 
 struct WaveHost {
     Meta meta;
@@ -68,9 +89,15 @@ struct WaveHost {
     std::vector<uint32_t> exit_node, exit_coff;
     uint32_t snapshot_configs = 0;
 
-    // Schedules. Level boundaries: tree t, level l -> [lvl[lvl0 + l], lvl[lvl0 + l + 1]).
+    // Sweep units: [0, nsub) subtree units in descending size, then one top
+    // unit per tree that does not fit a single unit. Lists are unit-major;
+    // level l of unit u spans [lvl[u.lvl0 + l], lvl[u.lvl0 + l + 1]).
+    std::vector<UnitDev> units;
+    uint32_t nsub = 0;
     std::vector<Task> back_task[2], reach_task[2], decision[2];
     std::vector<uint32_t> back_lvl[2], reach_lvl[2];
+    std::vector<uint32_t> unit_row, unit_term;
+    std::vector<uint8_t> node_top;  // 1 for a node of a top unit
     uint32_t lvl_len = 0;
 
     uint32_t max_levels = 0, nroots_max = 0, carry_slots = 0;
@@ -81,14 +108,21 @@ struct WaveHost {
 };
 
 // Pack parsed jobs into one wave. Fails (with a message) on incompatible
-// schedules, malformed tables or unsupported networks.
-bool pack_wave(std::vector<Job>&& jobs, WaveHost* w, std::string* err);
+// schedules, malformed tables or unsupported networks. `unit_slots` bounds the
+// value slots of one subtree unit.
+bool pack_wave(std::vector<Job>&& jobs, WaveHost* w, std::string* err, uint32_t unit_slots = UNIT_SLOTS);
 
 // Bounds of every index the kernels dereference (run by pack_wave).
 bool validate_deep(const WaveHost& w, std::string* err);
 
 // Algorithmic HBM bytes of one CFR iteration for traverser p (the counting
-// rule is written next to the implementation).
-uint64_t cfr_bytes_per_iter(const WaveHost& w, int p);
+// rule is written next to the implementation), split by the kernel that moves
+// them: [0] the subtree value sweep, [1] the top sweep (values, reach and
+// accumulation of the top units), [2] the subtree reach and accumulation.
+struct CfrBytes {
+    uint64_t part[3] = {0, 0, 0};
+    uint64_t total() const { return part[0] + part[1] + part[2]; }
+};
+CfrBytes cfr_bytes_per_iter(const WaveHost& w, int p);
 
 }  // namespace wc

@@ -81,16 +81,22 @@ class SynthSpecC(C.Structure):
 class WaveStats(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in (
         "jobs", "nodes", "decision_nodes", "chance_nodes", "leaves", "rows", "terminals",
-        "levels", "iters", "nroots_max", "carry_slots")] + [(n, C.c_uint64) for n in (
+        "levels", "iters", "nroots_max", "carry_slots", "units", "subtree_units")] + [(n, C.c_uint64) for n in (
         "cells", "reach_slots", "reach_len", "vals_len", "rev_nnz", "rvd_nnz", "draw_nnz",
         "snapshot_configs", "table_bytes", "arena_bytes")] + [
-        ("cfr_bytes_per_iter", C.c_uint64 * 2), ("mlp_flops_per_query", C.c_uint64)]
+        ("cfr_bytes_per_iter", C.c_uint64 * 2), ("cfr_bytes_by_kernel", (C.c_uint64 * 3) * 2),
+        ("mlp_flops_per_query", C.c_uint64)]
 
     def as_dict(self):
         out = {}
         for name, _ in self._fields_:
             v = getattr(self, name)
-            out[name] = list(v) if name == "cfr_bytes_per_iter" else int(v)
+            if name == "cfr_bytes_per_iter":
+                out[name] = list(v)
+            elif name == "cfr_bytes_by_kernel":
+                out[name] = [list(r) for r in v]
+            else:
+                out[name] = int(v)
         return out
 
 
@@ -378,9 +384,10 @@ class Executor:
 
     def time_wave(self, wave: Wave, version: int, reps: int, warmup: int = 1):
         """Mean device ms per wave over `reps` timed schedules after `warmup` untimed
-        ones, and one profiled schedule's [cfr, mlp, leaf input, other, mean cfr launch] ms."""
+        ones, and one profiled schedule's [cfr, mlp, leaf input, other, mean CFR iteration,
+        mean subtree sweep, mean top sweep, mean subtree reach] ms."""
         ms = C.c_double()
-        parts = (C.c_double * 5)()
+        parts = (C.c_double * 8)()
         _check(lib().wc_time_wave(self.h, wave.h, version, warmup, reps, C.byref(ms), parts))
         return ms.value, list(parts)
 
