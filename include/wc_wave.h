@@ -119,11 +119,11 @@ void wc_wave_free(wc_wave* w);
 typedef struct wc_wave_stats {
     uint32_t jobs, nodes, decision_nodes, chance_nodes, leaves, rows, terminals;
     uint32_t levels, iters, nroots_max, carry_slots;
-    uint32_t units, subtree_units; /* sweep units: all, and the subtree ones (the rest are tree tops) */
+    uint32_t units, top_levels;    /* subtree units, and the depths of the top regions swept per launch */
     uint64_t cells, reach_slots, reach_len, vals_len, rev_nnz, rvd_nnz, draw_nnz, snapshot_configs;
     uint64_t table_bytes, arena_bytes;
     uint64_t cfr_bytes_per_iter[2]; /* algorithmic HBM bytes of one CFR iteration, traverser 0 / 1 */
-    /* the same bytes by kernel, [traverser][kernel]: subtree value sweep, top sweep, subtree reach sweep */
+    /* the same bytes by kernel, [traverser][kernel]: subtree value sweep, top-region launches, subtree reach sweep */
     uint64_t cfr_bytes_by_kernel[2][3];
     uint64_t mlp_flops_per_query;
 } wc_wave_stats;
@@ -147,9 +147,9 @@ int wc_solve_wave(wc_executor* ex, wc_wave* w, uint64_t version, wc_result** res
  * executor's stream. kernel_ms (optional, 8 doubles) receives one profiled
  * schedule's device time per launch class: [0] CFR sweeps, [1] leaf MLP,
  * [2] leaf input, [3] everything else; [4] the mean device time of one CFR
- * iteration (its three sweep kernels), and the mean duration of one launch of
- * [5] the subtree value sweep, [6] the top-region sweep, [7] the subtree reach
- * sweep. */
+ * iteration (all its sweep kernels), and the mean device time per iteration of
+ * [5] the subtree value sweep, [6] the top-region launches (values and reach,
+ * one launch per depth each), [7] the subtree reach sweep. */
 int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup, uint32_t reps, double* wave_ms,
                  double* kernel_ms);
 

@@ -89,6 +89,42 @@ def test_small_wave_float32_bit_exact():
         assert_bit_exact(g, o, f"tree {k}")
 
 
+def solve_with_budget(jobs, net, precision, slots):
+    """Pack with a given subtree-unit budget (WC_UNIT_SLOTS), so that the top-region
+    path (nodes whose subtree does not fit one unit) carries most of the tree."""
+    import os
+    old = os.environ.get("WC_UNIT_SLOTS")
+    os.environ["WC_UNIT_SLOTS"] = str(slots)
+    try:
+        return gpu_solve(jobs, net, precision)
+    finally:
+        if old is None:
+            del os.environ["WC_UNIT_SLOTS"]
+        else:
+            os.environ["WC_UNIT_SLOTS"] = old
+
+
+def test_top_regions_float32_bit_exact():
+    jobs = small_wave(seed=13)
+    net = W.net_for("c4")
+    say(f"case top regions float32: {len(jobs)} trees packed with a 64-slot unit budget")
+    got = solve_with_budget(jobs, net, ww.WC_PRECISE, 64)
+    for k, (j, g) in enumerate(zip(jobs, got)):
+        assert_bit_exact(g, O.solve(j, net, O.NET_F32), f"tree {k}")
+
+
+def test_unit_budget_is_invisible():
+    jobs = small_wave(trees=5, seed=17, nodes_lo=60, nodes_hi=120)
+    net = W.net_for("c4")
+    say("case unit budgets: the same wave under budgets 64, 300 and 8192")
+    runs = [solve_with_budget(jobs, net, ww.WC_PRECISE, b) for b in (64, 300, 8192)]
+    for other in runs[1:]:
+        for x, y in zip(runs[0], other):
+            np.testing.assert_array_equal(x.strategy, y.strategy)
+            np.testing.assert_array_equal(x.root_values, y.root_values)
+            np.testing.assert_array_equal(x.carries, y.carries)
+
+
 def test_wave_composition_is_invariant():
     jobs = small_wave(trees=6, seed=21)
     net = W.net_for("c4")

@@ -123,7 +123,7 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
     s->terminals = (uint32_t)h.term_node.size();
     s->levels = h.max_levels;
     s->units = (uint32_t)h.units.size();
-    s->subtree_units = h.nsub;
+    s->top_levels = h.top_levels;
     s->iters = h.meta.iters;
     s->nroots_max = h.nroots_max;
     s->carry_slots = h.carry_slots;
@@ -147,6 +147,7 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
         tb += 8 * (h.back_task[p].size() + h.reach_task[p].size() + h.decision[p].size()) +
               4 * (h.back_lvl[p].size() + h.reach_lvl[p].size());
     tb += sizeof(UnitDev) * h.units.size() + 4 * (h.unit_row.size() + h.unit_term.size());
+    for (int p = 0; p < 2; p++) tb += 8 * (h.top_back[p].size() + h.top_reach[p].size());
     s->table_bytes = tb;
     s->arena_bytes = 4 * (4ull * h.ncells + 2ull * h.reach_len + h.vals_len + 2ull * h.rows() * (h.net.pool + 1) +
                           h.root_values_len) +

@@ -209,7 +209,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
             draw_row_start, draw_to, draw_p, reach_base, vals_base, parent, rev_row_of, rev_start, rev_src, rev_cell,
             rvd_row_of, rvd_start, rvd_src, rvd_p, row_node, row_cfg_off, row_cfg, cfg_key, cfg_emb, pub_raw,
             term_node, term_util, roots, carried, exit_node, exit_coff, trees, units, bt[2], rt[2], dc[2], bl[2],
-            rl[2], unit_row, unit_term;
+            rl[2], unit_row, unit_term, tb[2], tr[2];
     } o;
     o.node_meta = blob.put(w.node_meta);
     o.nc = blob.put(w.node_nc);
@@ -257,6 +257,10 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     }
     o.unit_row = blob.put(w.unit_row);
     o.unit_term = blob.put(w.unit_term);
+    for (int p = 0; p < 2; p++) {
+        o.tb[p] = blob.put(w.top_back[p]);
+        o.tr[p] = blob.put(w.top_reach[p]);
+    }
     if (!ensure(&table_, &table_cap_, host_blob_.size(), err)) return false;
     HIP_TRY(hipMemcpyAsync(table_, host_blob_.data(), host_blob_.size(), hipMemcpyHostToDevice, stream_));
 
@@ -339,6 +343,12 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     }
     d.unit_row = (const uint32_t*)(T + o.unit_row);
     d.unit_term = (const uint32_t*)(T + o.unit_term);
+    for (int p = 0; p < 2; p++) {
+        top_back_dev_[p] = (const Task*)(T + o.tb[p]);
+        top_reach_dev_[p] = (const Task*)(T + o.tr[p]);
+        d.top_dec[p] = d.decision[p] + w.top_dec0[p];
+        d.ntop_dec[p] = (uint32_t)w.decision[p].size() - w.top_dec0[p];
+    }
     d.nunits = (uint32_t)w.units.size();
     d.nsub = w.nsub;
     d.regret = (float*)(A + a_regret);
@@ -408,7 +418,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     const WaveDev& d = dev_;
     hipStream_t s = stream_;
     const Meta& m = w.meta;
-    const uint32_t nsub = w.nsub, ntop = (uint32_t)w.units.size() - w.nsub;
+    const uint32_t nsub = w.nsub;
     // Per-class attribution: an event after every launch group, binned by class.
     enum { C_BACK = 0, C_TOP = 1, C_REACH = 2, C_MLP = 3, C_LEAF = 4, C_OTHER = 5 };
     std::vector<std::pair<hipEvent_t, int>> ev;
@@ -428,9 +438,23 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         run_mlp(bank, d.rows, Xq_[q], nullptr);
         mark(C_MLP);
     };
+    // Top regions, one depth per launch: values bottom-up, reach top-down.
+    auto top_back = [&](int p, int mode, float da, float db, float ds, float pr) {
+        for (uint32_t l = w.top_levels; l-- > 0;) {
+            uint32_t b = w.top_back_lvl[p][l], e = w.top_back_lvl[p][l + 1];
+            launch_back_rows(d, top_back_dev_[p] + b, e - b, p, mode, da, db, ds, pr, s);
+        }
+    };
+    auto top_reach = [&](int p, float* reach, const float* strat) {  // p < 0: both players
+        for (uint32_t l = 1; l < w.top_levels; l++) {
+            uint32_t b0 = w.top_reach_lvl[0][l], n0 = p == 1 ? 0 : w.top_reach_lvl[0][l + 1] - b0;
+            uint32_t b1 = w.top_reach_lvl[1][l], n1 = p == 0 ? 0 : w.top_reach_lvl[1][l + 1] - b1;
+            launch_reach_rows(d, top_reach_dev_[0] + b0, n0, top_reach_dev_[1] + b1, n1, reach, strat, s);
+        }
+    };
     // Both players' reach under a fixed strategy: tops first, then their subtrees.
     auto reach_both = [&](float* reach, const float* strat) {
-        launch_reach(d, nsub, ntop, reach, strat, -1, false, s);
+        top_reach(-1, reach, strat);
         launch_reach(d, 0, nsub, reach, strat, -1, false, s);
     };
 
@@ -449,9 +473,10 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         const float mm = (float)(t / 2 + 1);
         const float da = cfr_factor(mm, m.cfr.alpha), db = cfr_factor(mm, m.cfr.beta);
         const float ds = std::pow(mm / (mm + 1.0f), m.cfr.gamma);
-        launch_sweep(d, false, 0, nsub, head_out_, bank.ns.heads, p, MODE_REGRET, da, db, ds, m.cfr.predict, s);
+        launch_sweep(d, 0, nsub, head_out_, bank.ns.heads, p, MODE_REGRET, da, db, ds, m.cfr.predict, s);
         mark(C_BACK);
-        launch_sweep(d, true, nsub, ntop, head_out_, bank.ns.heads, p, MODE_REGRET, da, db, ds, m.cfr.predict, s);
+        top_back(p, MODE_REGRET, da, db, ds, m.cfr.predict);
+        top_reach(p, d.reach, d.cur);
         mark(C_TOP);
         launch_reach(d, 0, nsub, d.reach, d.cur, p, true, s);
         mark(C_REACH);
@@ -479,8 +504,8 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         mark(C_LEAF);
         for (int p = 0; p < 2; p++) {
             mlp(p);
-            launch_sweep(d, false, 0, nsub, head_out_, bank.ns.heads, p, MODE_VALUE, 0.0f, 0.0f, 0.0f, 0.0f, s);
-            launch_sweep(d, true, nsub, ntop, head_out_, bank.ns.heads, p, MODE_VALUE, 0.0f, 0.0f, 0.0f, 0.0f, s);
+            launch_sweep(d, 0, nsub, head_out_, bank.ns.heads, p, MODE_VALUE, 0.0f, 0.0f, 0.0f, 0.0f, s);
+            top_back(p, MODE_VALUE, 0.0f, 0.0f, 0.0f, 0.0f);
             launch_collect_root(d, (int)root, p, s);
             mark(C_OTHER);
         }

@@ -96,6 +96,8 @@ class Executor {
     WaveDev dev_{};
     void* X_ = nullptr;
     void* Xq_[2] = {};  // the wave's query inputs, one per traverser
+    const Task* top_back_dev_[2] = {};   // top-region rows by depth (device copies)
+    const Task* top_reach_dev_[2] = {};
     void* H_[2] = {};
     float* head_out_ = nullptr;
     uint32_t rows_ = 0;

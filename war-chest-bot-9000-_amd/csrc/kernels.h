@@ -34,6 +34,7 @@ struct WaveDev {
     const Task *back_task[2], *reach_task[2], *decision[2];
     const uint32_t *back_lvl[2], *reach_lvl[2];
     const uint32_t *unit_row, *unit_term;
+    const Task* top_dec[2];
     // mutable arena
     float *regret, *cur, *sum, *snap;
     float *reach, *snap_reach, *vals;
@@ -41,28 +42,33 @@ struct WaveDev {
     uint16_t* carry;
     // sizes
     uint32_t ntrees, nunits, nsub, rows, pool, in, row_bytes, snapshot_configs, nexit, ncells;
-    uint32_t ndec[2];
+    uint32_t ndec[2], ntop_dec[2];
 };
 
 // Launchers (kernels.hip). All take the executor's stream.
 void launch_zero(float* p, size_t n, hipStream_t s);
 void launch_init_strategy(const WaveDev& w, hipStream_t s);
 void launch_seed_reach(const WaveDev& w, float* reach, int root_index, hipStream_t s);
-// Top-down reach of units [unit0, unit0 + n) under `strat`, for one player or
-// both (player < 0); with `accumulate`, then sum += reach * cur over the
-// player's decision rows of each unit.
+// Top-down reach of subtree units [unit0, unit0 + n) under `strat`, for one
+// player or both (player < 0); with `accumulate`, then sum += reach * cur over
+// the player's decision rows of each unit and of the top regions.
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
                   bool accumulate, hipStream_t s);
+// Top-region reach at one depth (rows of player 0 and of player 1).
+void launch_reach_rows(const WaveDev& w, const Task* r0, uint32_t n0, const Task* r1, uint32_t n1, float* reach,
+                       const float* strat, hipStream_t s);
 void launch_seed_sum(const WaveDev& w, hipStream_t s);
 // Leaf reach masses and pooled beliefs of one player (-1 = both), written into
 // the query inputs x0 (traverser 0) and x1 (traverser 1) in the operand precision.
 void launch_pool(const WaveDev& w, int player, int precision, void* x0, void* x1, hipStream_t s);
 // Seat and public features of both query inputs (once per upload).
 void launch_query_static(const WaveDev& w, int precision, void* x0, void* x1, hipStream_t s);
-// Leaf values and the bottom-up sweep of units [unit0, unit0 + n) for the
-// traverser; for top units in regret mode, then their reach and accumulation.
-void launch_sweep(const WaveDev& w, bool top, uint32_t unit0, uint32_t n, const float* head_out, uint32_t heads,
-                  int traverser, int mode, float da, float db, float ds, float predict, hipStream_t s);
+// Leaf values and the bottom-up sweep of subtree units [unit0, unit0 + n) for the traverser.
+void launch_sweep(const WaveDev& w, uint32_t unit0, uint32_t n, const float* head_out, uint32_t heads, int traverser,
+                  int mode, float da, float db, float ds, float predict, hipStream_t s);
+// Top-region values at one depth for the traverser.
+void launch_back_rows(const WaveDev& w, const Task* rows, uint32_t n, int traverser, int mode, float da, float db,
+                      float ds, float predict, hipStream_t s);
 void launch_normalize(const WaveDev& w, int touched0, int touched1, hipStream_t s);
 void launch_gather_carry(const WaveDev& w, const float* reach, int slot, hipStream_t s);
 void launch_collect_root(const WaveDev& w, int root, int player, hipStream_t s);

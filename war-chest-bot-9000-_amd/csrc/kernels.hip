@@ -18,8 +18,6 @@ namespace wc {
 #define SMOOTHF 1e-30f   // belief normalisation floor (engine/src/rebel.rs:359)
 
 constexpr int BLOCK = 256;
-// Top units hold the widest levels of the largest trees: they get the largest workgroup.
-constexpr int TOP_BLOCK = 1024;
 
 static inline unsigned grid_for(size_t n, int block = BLOCK) { return (unsigned)((n + block - 1) / block); }
 
@@ -194,9 +192,20 @@ __device__ __forceinline__ void reach_unit(const WaveDev& w, const UnitDev& u, f
     }
 }
 
-template <int NT>
-__global__ __launch_bounds__(NT) void k_reach(WaveDev w, uint32_t unit0, float* reach, const float* strat,
-                                            int player, int accumulate) {
+// Subtree units' reach; with `accumulate`, each unit then accumulates its own
+// decision rows, and the blocks past the units accumulate the top regions'
+// decision rows, one row per thread (their reach is final by then).
+__global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, uint32_t nunits, float* reach,
+                                               const float* strat, int player, int accumulate) {
+    if (blockIdx.x >= nunits) {
+        const uint32_t k = (blockIdx.x - nunits) * blockDim.x + threadIdx.x;
+        if (k >= w.ntop_dec[player]) return;
+        Task q = w.top_dec[player][k];
+        uint32_t row = w.legal_row_of[q.node] + q.config;
+        float r = w.reach[w.reach_base[2 * q.node + player] + q.config];
+        for (uint32_t g = w.legal_off[row]; g < w.legal_off[row + 1]; g++) w.sum[g] += r * w.cur[g];
+        return;
+    }
     const UnitDev u = w.units[unit0 + blockIdx.x];
     reach_unit(w, u, reach, strat, player);
     if (accumulate) accumulate_unit(w, u, player);
@@ -204,13 +213,26 @@ __global__ __launch_bounds__(NT) void k_reach(WaveDev w, uint32_t unit0, float* 
 
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
                   bool accumulate, hipStream_t s) {
-    if (!n) return;
-    if (unit0 >= w.nsub)
-        hipLaunchKernelGGL(k_reach<TOP_BLOCK>, dim3(n), dim3(TOP_BLOCK), 0, s, w, unit0, reach, strat, player,
+    uint32_t extra = accumulate ? grid_for(w.ntop_dec[player]) : 0;
+    if (n + extra)
+        hipLaunchKernelGGL(k_reach, dim3(n + extra), dim3(BLOCK), 0, s, w, unit0, n, reach, strat, player,
                            accumulate ? 1 : 0);
-    else
-        hipLaunchKernelGGL(k_reach<BLOCK>, dim3(n), dim3(BLOCK), 0, s, w, unit0, reach, strat, player,
-                           accumulate ? 1 : 0);
+}
+
+// Top-region reach at one depth, all trees together: one row per thread.
+__global__ __launch_bounds__(BLOCK) void k_reach_rows(WaveDev w, const Task* r0, uint32_t n0, const Task* r1,
+                                                    uint32_t n1, float* reach, const float* strat) {
+    uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k < n0)
+        reach_task(w, reach, strat, 0, r0[k]);
+    else if (k < n0 + n1)
+        reach_task(w, reach, strat, 1, r1[k - n0]);
+}
+
+void launch_reach_rows(const WaveDev& w, const Task* r0, uint32_t n0, const Task* r1, uint32_t n1, float* reach,
+                       const float* strat, hipStream_t s) {
+    if (n0 + n1)
+        hipLaunchKernelGGL(k_reach_rows, dim3(grid_for(n0 + n1)), dim3(BLOCK), 0, s, w, r0, n0, r1, n1, reach, strat);
 }
 
 // sum = reach * cur: one reach-weighted uniform strategy (engine/src/search.rs:854-870).
@@ -514,18 +536,13 @@ __device__ __forceinline__ void backprop_task(const WaveDev& w, int p, Task q, f
     }
 }
 
-// Leaf values and the bottom-up value sweep of one unit for traverser p, one
-// workgroup per unit: leaf values first (net value x opponent reach mass,
-// engine/src/search.rs:1587-1636), then levels from the deepest up, with the
-// fused regret/DCFR update at the traverser's rows. A top unit in regret mode
-// then pushes the traverser's reach down its levels under the new strategy
-// and accumulates the average strategy; subtree units do that in k_reach,
-// after every top unit has finished.
-template <int MODE, bool TOP>
-__global__ __launch_bounds__(TOP ? TOP_BLOCK : BLOCK) void k_sweep(WaveDev w, uint32_t unit0, const float* head_out,
-                                                                uint32_t heads, int p, float da, float db, float ds,
-                                                                float predict) {
-    constexpr int mode = MODE;
+// Leaf values and the bottom-up value sweep of one subtree unit for traverser
+// p, one workgroup per unit: leaf values first (net value x opponent reach
+// mass, engine/src/search.rs:1587-1636), then levels from the deepest up, with
+// the fused regret/DCFR update at the traverser's rows.
+template <int MODE>
+__global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, const float* head_out, uint32_t heads,
+                                               int p, float da, float db, float ds, float predict) {
     const UnitDev u = w.units[unit0 + blockIdx.x];
     const int opp = 1 - p;
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -559,30 +576,36 @@ __global__ __launch_bounds__(TOP ? TOP_BLOCK : BLOCK) void k_sweep(WaveDev w, ui
             backprop_task<MODE>(w, p, back[k], da, db, ds, predict, w.snap);
         __syncthreads();
     }
-    if (TOP && mode == MODE_REGRET) {
-        reach_unit(w, u, w.reach, w.cur, p);
-        accumulate_unit(w, u, p);
-    }
 }
 
-void launch_sweep(const WaveDev& w, bool top, uint32_t unit0, uint32_t n, const float* head_out, uint32_t heads,
-                  int traverser, int mode, float da, float db, float ds, float predict, hipStream_t s) {
+void launch_sweep(const WaveDev& w, uint32_t unit0, uint32_t n, const float* head_out, uint32_t heads, int traverser,
+                  int mode, float da, float db, float ds, float predict, hipStream_t s) {
     if (!n) return;
-#define WC_SWEEP(M, T)                                                                                        \
-    hipLaunchKernelGGL((k_sweep<M, T>), dim3(n), dim3(T ? TOP_BLOCK : BLOCK), 0, s, w, unit0, head_out, heads, \
-                       traverser, da, db, ds, predict)
-    if (mode == MODE_VALUE) {
-        if (top)
-            WC_SWEEP(MODE_VALUE, true);
-        else
-            WC_SWEEP(MODE_VALUE, false);
-    } else {
-        if (top)
-            WC_SWEEP(MODE_REGRET, true);
-        else
-            WC_SWEEP(MODE_REGRET, false);
-    }
-#undef WC_SWEEP
+    if (mode == MODE_VALUE)
+        hipLaunchKernelGGL(k_sweep<MODE_VALUE>, dim3(n), dim3(BLOCK), 0, s, w, unit0, head_out, heads, traverser, da,
+                           db, ds, predict);
+    else
+        hipLaunchKernelGGL(k_sweep<MODE_REGRET>, dim3(n), dim3(BLOCK), 0, s, w, unit0, head_out, heads, traverser,
+                           da, db, ds, predict);
+}
+
+// Top-region values at one depth, all trees together: one row per thread.
+template <int MODE>
+__global__ __launch_bounds__(BLOCK) void k_back_rows(WaveDev w, const Task* rows, uint32_t n, int p, float da,
+                                                   float db, float ds, float predict) {
+    uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k < n) backprop_task<MODE>(w, p, rows[k], da, db, ds, predict, w.snap);
+}
+
+void launch_back_rows(const WaveDev& w, const Task* rows, uint32_t n, int traverser, int mode, float da, float db,
+                      float ds, float predict, hipStream_t s) {
+    if (!n) return;
+    if (mode == MODE_VALUE)
+        hipLaunchKernelGGL(k_back_rows<MODE_VALUE>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, rows, n, traverser, da,
+                           db, ds, predict);
+    else
+        hipLaunchKernelGGL(k_back_rows<MODE_REGRET>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, rows, n, traverser, da,
+                           db, ds, predict);
 }
 
 // Average strategy: sum / row sum, uniform when the sum is not positive, the

@@ -116,8 +116,15 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
         *err = "unit budget must be positive";
         return false;
     }
+    // Every leaf must fit a unit (tops carry no leaves): the budget is at least
+    // the widest node of the wave.
+    for (const Job& job : jobs)
+        for (uint32_t i = 0; i < job.t.nodes; i++)
+            unit_slots = std::max(unit_slots, std::max(job.t.nc(i, 0), job.t.nc(i, 1)));
     uint32_t cfg_total = 0;
-    std::vector<UnitDev> sub_units, top_units;
+    std::vector<UnitDev> sub_units;
+    std::vector<std::vector<Task>> top_back[2], top_reach[2];
+    std::vector<Task> top_dec[2];
 
     for (const Job& job : jobs) {
         const Tables& t = job.t;
@@ -273,10 +280,9 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
         for (uint32_t k = 0; k < t.term_leaves.size(); k++) term_of[t.term_leaves[k]] = k;
         const uint32_t tree_index = (uint32_t)w.trees.size();
         // Emit one unit over `nodes` (in preorder) with unit-local levels depth - d0.
-        auto emit = [&](const std::vector<uint32_t>& nodes, uint32_t d0, bool top) {
+        auto emit = [&](const std::vector<uint32_t>& nodes, uint32_t d0) {
             UnitDev u{};
             u.tree = tree_index;
-            u.top = top ? 1u : 0u;
             uint32_t L = 0;
             for (uint32_t i : nodes) L = std::max(L, depth[i] - d0 + 1);
             u.nlevels = L;
@@ -309,8 +315,6 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
                         for (uint32_t c = 0; c < t.nc(local, p); c++) w.decision[p].push_back({node0 + local, c});
                 u.dec1[p] = (uint32_t)w.decision[p].size();
             }
-            if (top)
-                for (uint32_t local : nodes) w.node_top[node0 + local] = 1;
             u.row0 = (uint32_t)w.unit_row.size();
             for (uint32_t local : nodes)
                 if (row_of[local] != NONE) w.unit_row.push_back(row_base + row_of[local]);
@@ -319,7 +323,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             for (uint32_t local : nodes)
                 if (term_of[local] != NONE) w.unit_term.push_back(term_base + term_of[local]);
             u.term1 = (uint32_t)w.unit_term.size();
-            (top ? top_units : sub_units).push_back(u);
+            sub_units.push_back(u);
         };
         // The nodes of the subtree rooted at r, in preorder.
         auto subtree = [&](uint32_t r, std::vector<uint32_t>* out) {
@@ -329,7 +333,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             out->insert(out->end(), pre.begin() + k, pre.begin() + end);
         };
         if (sub[0] <= unit_slots) {
-            emit(pre, 0, false);
+            emit(pre, 0);
         } else {
             std::vector<uint32_t> top;
             for (uint32_t i : pre)
@@ -342,26 +346,59 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
                     uint32_t c = t.node_child[k];
                     if (sub[c] > unit_slots) continue;
                     if (!run.empty() && run_slots + sub[c] > unit_slots) {
-                        emit(run, depth[i] + 1, false);
+                        emit(run, depth[i] + 1);
                         run.clear();
                         run_slots = 0;
                     }
                     subtree(c, &run);
                     run_slots += sub[c];
                 }
-                if (!run.empty()) emit(run, depth[i] + 1, false);
+                if (!run.empty()) emit(run, depth[i] + 1);
             }
-            emit(top, 0, true);
+            // The top region joins every other tree's at its depth.
+            for (uint32_t local : top) {
+                uint32_t node = node0 + local, d = depth[local];
+                w.node_top[node] = 1;
+                for (int p = 0; p < 2; p++) {
+                    if (top_back[p].size() <= d) {
+                        top_back[p].resize(d + 1);
+                        top_reach[p].resize(d + 1);
+                    }
+                    uint8_t kind = t.node_kind[local];
+                    if (kind != 2 && !(kind == 1 && t.node_player[local] != p))
+                        for (uint32_t c = 0; c < t.nc(local, p); c++) top_back[p][d].push_back({node, c});
+                    if (local != 0 && t.node_player[t.node_parent[local]] == p)
+                        for (uint32_t c = 0; c < t.nc(local, p); c++) top_reach[p][d].push_back({node, c});
+                    if (kind == 0 && t.node_player[local] == p)
+                        for (uint32_t c = 0; c < t.nc(local, p); c++) top_dec[p].push_back({node, c});
+                }
+            }
         }
         w.trees.push_back(td);
     }
     w.child_start.push_back((uint32_t)w.child.size());
-    // Subtree units largest first (the device takes them in launch order), then the tops.
+    // Subtree units largest first: the device takes them in launch order.
     std::stable_sort(sub_units.begin(), sub_units.end(),
                      [](const UnitDev& a, const UnitDev& b) { return a.slots > b.slots; });
     w.nsub = (uint32_t)sub_units.size();
     w.units = std::move(sub_units);
-    w.units.insert(w.units.end(), top_units.begin(), top_units.end());
+    w.top_levels = (uint32_t)std::max(top_back[0].size(), top_back[1].size());
+    for (int p = 0; p < 2; p++) {
+        top_back[p].resize(w.top_levels);
+        top_reach[p].resize(w.top_levels);
+        for (uint32_t l = 0; l < w.top_levels; l++) {
+            w.top_back_lvl[p].push_back((uint32_t)w.top_back[p].size());
+            w.top_reach_lvl[p].push_back((uint32_t)w.top_reach[p].size());
+            w.top_back[p].insert(w.top_back[p].end(), top_back[p][l].begin(), top_back[p][l].end());
+            w.top_reach[p].insert(w.top_reach[p].end(), top_reach[p][l].begin(), top_reach[p][l].end());
+        }
+        w.top_back_lvl[p].push_back((uint32_t)w.top_back[p].size());
+        w.top_reach_lvl[p].push_back((uint32_t)w.top_reach[p].size());
+        // Top decision rows follow every unit's rows, so whole-list kernels
+        // (uniform start, seeded sums, the average) cover them too.
+        w.top_dec0[p] = (uint32_t)w.decision[p].size();
+        w.decision[p].insert(w.decision[p].end(), top_dec[p].begin(), top_dec[p].end());
+    }
     w.carry_slots = (w.meta.snapshots && w.meta.snap_iters.size() > 1) ? (uint32_t)w.meta.snap_iters.size() - 1 : 0;
     w.jobs = std::move(jobs);
     if (!validate_deep(w, err)) return false;
@@ -490,6 +527,23 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         if (u.row0 > u.row1 || u.row1 > w.unit_row.size() || u.term0 > u.term1 || u.term1 > w.unit_term.size())
             return fail("unit leaf range");
     }
+    for (int p = 0; p < 2; p++) {
+        if (w.top_back_lvl[p].size() != w.top_levels + 1 || w.top_reach_lvl[p].size() != w.top_levels + 1)
+            return fail("top levels");
+        for (uint32_t l = 0; l < w.top_levels; l++)
+            if (w.top_back_lvl[p][l + 1] < w.top_back_lvl[p][l] || w.top_reach_lvl[p][l + 1] < w.top_reach_lvl[p][l])
+                return fail("top level order");
+        if (w.top_back_lvl[p][w.top_levels] != w.top_back[p].size() ||
+            w.top_reach_lvl[p][w.top_levels] != w.top_reach[p].size())
+            return fail("top level bounds");
+        for (const Task& q : w.top_back[p])
+            if (q.node >= N || q.config >= w.nc(q.node, p)) return fail("top back task");
+        for (const Task& q : w.top_reach[p])
+            if (q.node >= N || q.config >= w.nc(q.node, p) || w.parent[q.node] == NONE) return fail("top reach task");
+        if (w.top_dec0[p] > w.decision[p].size()) return fail("top decision rows");
+        for (const UnitDev& u : w.units)
+            if (u.dec1[p] > w.top_dec0[p]) return fail("unit decision rows overlap the top rows");
+    }
     for (const TreeDev& t : w.trees) {
         if (uint64_t(t.node0) + t.nodes > N) return fail("tree range");
         if (uint64_t(t.reach0) + t.reach_len > w.reach_len) return fail("reach range");
@@ -533,7 +587,7 @@ CfrBytes cfr_bytes_per_iter(const WaveHost& w, int p) {
             uint32_t r0 = w.legal_row_of[i];
             uint64_t C = w.legal_off[r0 + ncp] - w.legal_off[r0];
             back += 32 * C + 8 * uint64_t(ncp);
-            reach += 12 * C + 4 * uint64_t(ncp);
+            out.part[2] += 12 * C + 4 * uint64_t(ncp);  // every accumulation runs in the subtree reach launch
         } else if (kind == 0) {
             back += 4 * uint64_t(ncp) * (w.child_start[i + 1] - w.child_start[i]);
         } else if (kind == 1 && actor == (uint32_t)p) {

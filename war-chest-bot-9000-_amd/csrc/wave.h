@@ -7,11 +7,12 @@
 // value aliasing follow the reference; the schedules differ. Instead of
 // wave-wide level task lists walked under grid-wide barriers, each tree is cut
 // into units that one workgroup sweeps with block barriers: runs of sibling
-// subtrees that fit a slot budget (swept independently, largest first, so big
-// and small trees balance across the CUs) and, for trees that do not fit, the
-// top region above them (swept after its subtrees for values, before them for
-// reach). Value slots are allocated in reverse DFS preorder, so every unit's
-// slots form one contiguous window.
+// subtrees that fit a slot budget, swept independently and largest first so
+// big and small trees balance across the CUs. The nodes above them (the top
+// region of a tree that does not fit one unit) are swept one depth per launch
+// across all trees: after the units for values, before them for reach. Value
+// slots are allocated in reverse DFS preorder, so every unit's slots form one
+// contiguous window.
 #pragma once
 
 #include <cstdint>
@@ -37,19 +38,17 @@ struct TreeDev {
 };
 static_assert(sizeof(TreeDev) == 12 * 4, "TreeDev is 48 bytes");
 
-// One sweep unit, processed by one workgroup. A subtree unit is a run of
-// sibling subtrees whose value slots fit the unit budget; a top unit is the
-// part of one tree above its subtree units (the nodes whose own subtree does
-// not fit). Levels are unit-local depths; task and row lists live in the
-// wave's flattened arrays at the offsets given here.
+// One subtree unit, swept by one workgroup: a run of sibling subtrees whose
+// value slots fit the unit budget. Levels are unit-local depths; task and row
+// lists live in the wave's flattened arrays at the offsets given here.
 struct UnitDev {
     uint32_t nlevels, lvl0;     // level boundaries at back_lvl / reach_lvl [lvl0, lvl0 + nlevels]
     uint32_t dec0[2], dec1[2];  // decision rows of each player: decision[p][dec0 .. dec1)
     uint32_t row0, row1;        // network leaf rows: unit_row[row0 .. row1)
     uint32_t term0, term1;      // terminal leaves: unit_term[term0 .. term1)
     uint32_t slots;             // value slots (max over players, before aliasing)
-    uint32_t tree, top;         // owning tree; 1 for a top unit
-    uint32_t pad[3];
+    uint32_t tree;              // owning tree
+    uint32_t pad[4];
 };
 static_assert(sizeof(UnitDev) == 16 * 4, "UnitDev is 64 bytes");
 
@@ -89,16 +88,22 @@ struct WaveHost {
     std::vector<uint32_t> exit_node, exit_coff;
     uint32_t snapshot_configs = 0;
 
-    // Sweep units: [0, nsub) subtree units in descending size, then one top
-    // unit per tree that does not fit a single unit. Lists are unit-major;
-    // level l of unit u spans [lvl[u.lvl0 + l], lvl[u.lvl0 + l + 1]).
+    // Subtree units in descending size; lists are unit-major and level l of
+    // unit u spans [lvl[u.lvl0 + l], lvl[u.lvl0 + l + 1]).
     std::vector<UnitDev> units;
     uint32_t nsub = 0;
     std::vector<Task> back_task[2], reach_task[2], decision[2];
     std::vector<uint32_t> back_lvl[2], reach_lvl[2];
     std::vector<uint32_t> unit_row, unit_term;
-    std::vector<uint8_t> node_top;  // 1 for a node of a top unit
     uint32_t lvl_len = 0;
+    // Top regions (the nodes whose subtree does not fit a unit), all trees
+    // together by depth: level l spans [top_*_lvl[p][l], top_*_lvl[p][l + 1]).
+    // Their decision rows close each decision list: decision[p][top_dec0[p] ..).
+    std::vector<Task> top_back[2], top_reach[2];
+    uint32_t top_dec0[2] = {0, 0};
+    std::vector<uint32_t> top_back_lvl[2], top_reach_lvl[2];
+    uint32_t top_levels = 0;
+    std::vector<uint8_t> node_top;  // 1 for a node of a top region
 
     uint32_t max_levels = 0, nroots_max = 0, carry_slots = 0;
 
@@ -117,8 +122,8 @@ bool validate_deep(const WaveHost& w, std::string* err);
 
 // Algorithmic HBM bytes of one CFR iteration for traverser p (the counting
 // rule is written next to the implementation), split by the kernel that moves
-// them: [0] the subtree value sweep, [1] the top sweep (values, reach and
-// accumulation of the top units), [2] the subtree reach and accumulation.
+// them: [0] the subtree value sweep, [1] the top-region launches, [2] the
+// subtree reach and accumulation.
 struct CfrBytes {
     uint64_t part[3] = {0, 0, 0};
     uint64_t total() const { return part[0] + part[1] + part[2]; }
