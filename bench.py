@@ -48,7 +48,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--workload", default="c4", choices=["c3", "c4"])
+    ap.add_argument("--workload", default="wave256", choices=["wave64", "wave256"])
     ap.add_argument("--cpu-trees", type=int, default=0, help="trees in the CPU-baseline sample (0 = 2 per thread)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-mlp", action="store_true", help="skip the GEMM-chain-alone leg")
@@ -133,8 +133,8 @@ def main():
     }
 
     if not args.no_mlp:
-        mnet = W.net_for("c2")
-        x = W.c2_inputs()
+        mnet = W.net_for("mlp65k")
+        x = W.mlp65k_inputs()
         mex = ww.Executor(0, ww.WC_F16)
         mv = mex.publish(mnet)
         chain_ms, layer_ms = mex.time_mlp(mv, x, reps=20)

@@ -77,7 +77,9 @@ int wc_service_create(int device, const wc_net_desc* net, int precision, const w
                       wc_service** out);
 /* Drop of the last GpuClient: shuts the dispatcher down and joins (client.rs:293-300). */
 void wc_service_destroy(wc_service* svc);
-/* GpuClient::set_weights: returns the new monotone version; queued waves keep theirs. */
+/* GpuClient::set_weights: returns the new monotone version (1, 2, ...; the bank given to
+ * wc_service_create is version 0), or 0 on failure. Jobs already submitted keep the
+ * version that was current when they were submitted (engine/src/gpu/service.rs:233). */
 uint64_t wc_set_weights(wc_service* svc, const wc_net_desc* net);
 /* GpuClient::queued_work: monotone cost estimate of queued and running work. */
 uint64_t wc_queued_work(wc_service* svc);

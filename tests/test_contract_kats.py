@@ -91,7 +91,7 @@ def test_opponent_chance_values_alias_the_child():
 
 
 def test_cpp_codec_agrees_with_python_codec():
-    for name, kw in (("c1", {}), ("c3", {"trees": 3}), ("c4", {"trees": 2, "nodes_lo": 60, "nodes_hi": 90,
+    for name, kw in (("tree48", {}), ("wave64", {"trees": 3}), ("wave256", {"trees": 2, "nodes_lo": 60, "nodes_hi": 90,
                                                                 "terminal_p": 0.2, "nroots": 3})):
         for b in W.jobs(name, **kw):
             d = wcj8.decode(b)
@@ -101,7 +101,7 @@ def test_cpp_codec_agrees_with_python_codec():
 
 @pytest.mark.parametrize("field", ["legal_trans", "rev_src", "draw_to", "leaf_cidx"])
 def test_out_of_range_indices_are_rejected(field):
-    [b] = W.jobs("c4", trees=1, nodes_lo=40, nodes_hi=60, seed=5)
+    [b] = W.jobs("wave256", trees=1, nodes_lo=40, nodes_hi=60, seed=5)
     d = wcj8.decode(b)
     arr = np.array(d[field], np.uint32)
     assert arr.size

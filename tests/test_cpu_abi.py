@@ -29,14 +29,14 @@ def test_every_declared_symbol_is_exported():
 
 
 def test_job_roundtrip_is_byte_identical():
-    for name in ("c1", "c3"):
-        for j in W.jobs(name, trees=3) if name == "c3" else W.jobs(name):
+    for name in ("tree48", "wave64"):
+        for j in W.jobs(name, trees=3) if name == "wave64" else W.jobs(name):
             assert ww.job_roundtrip(j) == j
             ww.job_validate(j)
 
 
 def test_truncated_and_corrupt_jobs_are_rejected():
-    j = W.jobs("c1")[0]
+    j = W.jobs("tree48")[0]
     for cut in (0, 3, 8, len(j) // 2, len(j) - 1):
         with pytest.raises(ww.WaveError):
             ww.job_validate(j[:cut])
@@ -49,14 +49,14 @@ def test_truncated_and_corrupt_jobs_are_rejected():
 
 
 def test_wave_pack_rejects_mixed_schedules():
-    a = W.jobs("c1")[0]
-    b = W.jobs("c1", iters=8)[0]
+    a = W.jobs("tree48")[0]
+    b = W.jobs("tree48", iters=8)[0]
     with pytest.raises(ww.WaveError, match="schedule"):
         ww.Wave([a, b])
 
 
 def test_wave_counts_add_up():
-    jobs = W.jobs("c3", trees=5)
+    jobs = W.jobs("wave64", trees=5)
     st = ww.Wave(jobs).stats()
     parts = [ww.Wave([j]).stats() for j in jobs]
     for k in ("nodes", "cells", "rows", "rev_nnz", "reach_len", "vals_len", "snapshot_configs"):
@@ -66,17 +66,17 @@ def test_wave_counts_add_up():
 
 
 def test_synthesis_is_seeded_and_prefix_stable():
-    a = W.jobs("c3", trees=4)
-    b = W.jobs("c3", trees=6)
+    a = W.jobs("wave64", trees=4)
+    b = W.jobs("wave64", trees=6)
     assert a == b[:4]
-    assert W.jobs("c3", trees=2, seed=99) != a[:2]
+    assert W.jobs("wave64", trees=2, seed=99) != a[:2]
 
 
 def test_weights_and_features_are_seeded():
-    n1 = W.net_for("c2")
-    n2 = W.net_for("c2")
+    n1 = W.net_for("mlp65k")
+    n2 = W.net_for("mlp65k")
     np.testing.assert_array_equal(n1.w, n2.w)
-    x = W.c2_inputs(rows=64)
+    x = W.mlp65k_inputs(rows=64)
     assert x.shape == (64, 512)
     assert x.min() >= 0.0 and x.max() <= 1.0
     # Kaiming-normal: first-layer std ~ sqrt(2 / 512)

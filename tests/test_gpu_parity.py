@@ -52,19 +52,19 @@ def assert_bit_exact(g, o, tag):
         np.testing.assert_array_equal(g.carries, f16_carries(o), err_msg=f"{tag}: carries")
 
 
-def test_c1_float32_bit_exact():
-    say("case c1 float32: 1 tree, 16 iterations")
-    jobs = W.jobs("c1")
-    net = W.net_for("c1")
+def test_tree48_float32_bit_exact():
+    say("case tree48 float32: 1 tree, 16 iterations")
+    jobs = W.jobs("tree48")
+    net = W.net_for("tree48")
     [g] = gpu_solve(jobs, net, ww.WC_PRECISE)
     o = O.solve(jobs[0], net, O.NET_F32)
-    assert_bit_exact(g, o, "c1")
+    assert_bit_exact(g, o, "tree48")
 
 
 def test_zero_network_is_uniform():
-    say("case zero network: c1 tree, all weights and biases zero")
-    jobs = W.jobs("c1")
-    net = W.net_for("c1")
+    say("case zero network: tree48, all weights and biases zero")
+    jobs = W.jobs("tree48")
+    net = W.net_for("tree48")
     zero = ww.Net(net.dims, np.zeros_like(net.w), np.zeros_like(net.b))
     [g] = gpu_solve(jobs, zero, ww.WC_PRECISE)
     o = O.solve(jobs[0], zero, O.NET_F32)
@@ -76,12 +76,12 @@ def small_wave(**kw):
     spec = dict(trees=8, nodes_lo=30, nodes_hi=90, chance=1, terminal_p=0.15, notrans_p=0.05, nroots=3,
                 iters=8, info_median=6.0, info_p99=40.0, info_cap=40, seed=11)
     spec.update(kw)
-    return W.jobs("c4", **spec)
+    return W.jobs("wave256", **spec)
 
 
 def test_small_wave_float32_bit_exact():
     jobs = small_wave()
-    net = W.net_for("c4")
+    net = W.net_for("wave256")
     say(f"case small wave float32: {len(jobs)} trees with chance, terminals, 3 carried roots")
     got = gpu_solve(jobs, net, ww.WC_PRECISE)
     for k, (j, g) in enumerate(zip(jobs, got)):
@@ -106,7 +106,7 @@ def solve_with_budget(jobs, net, precision, slots):
 
 def test_top_regions_float32_bit_exact():
     jobs = small_wave(seed=13)
-    net = W.net_for("c4")
+    net = W.net_for("wave256")
     say(f"case top regions float32: {len(jobs)} trees packed with a 64-slot unit budget")
     got = solve_with_budget(jobs, net, ww.WC_PRECISE, 64)
     for k, (j, g) in enumerate(zip(jobs, got)):
@@ -115,7 +115,7 @@ def test_top_regions_float32_bit_exact():
 
 def test_unit_budget_is_invisible():
     jobs = small_wave(trees=5, seed=17, nodes_lo=60, nodes_hi=120)
-    net = W.net_for("c4")
+    net = W.net_for("wave256")
     say("case unit budgets: the same wave under budgets 64, 300 and 8192")
     runs = [solve_with_budget(jobs, net, ww.WC_PRECISE, b) for b in (64, 300, 8192)]
     for other in runs[1:]:
@@ -127,7 +127,7 @@ def test_unit_budget_is_invisible():
 
 def test_wave_composition_is_invariant():
     jobs = small_wave(trees=6, seed=21)
-    net = W.net_for("c4")
+    net = W.net_for("wave256")
     say("case composition: tree 2 alone vs inside a 6-tree wave")
     alone = gpu_solve([jobs[2]], net, ww.WC_PRECISE)[0]
     inside = gpu_solve(jobs, net, ww.WC_PRECISE)[2]
@@ -138,7 +138,7 @@ def test_wave_composition_is_invariant():
 
 def test_repeat_is_deterministic():
     jobs = small_wave(trees=4, seed=31)
-    net = W.net_for("c4")
+    net = W.net_for("wave256")
     say("case determinism: the same wave twice, f16")
     a = gpu_solve(jobs, net, ww.WC_F16)
     b = gpu_solve(jobs, net, ww.WC_F16)
@@ -148,8 +148,8 @@ def test_repeat_is_deterministic():
 
 
 def test_mlp_f16_matches_reduced_precision_oracle():
-    net = W.net_for("c2")
-    x = W.c2_inputs(rows=2048)
+    net = W.net_for("mlp65k")
+    x = W.mlp65k_inputs(rows=2048)
     say("case mlp f16: 2048 queries, 512 -> 3x384 -> 64")
     ex = executor(ww.WC_F16)
     v = ex.publish(net)
@@ -164,8 +164,8 @@ def test_mlp_f16_matches_reduced_precision_oracle():
 
 
 def test_mlp_bf16_matches_reduced_precision_oracle():
-    net = W.net_for("c2")
-    x = W.c2_inputs(rows=1024, seed=9)
+    net = W.net_for("mlp65k")
+    x = W.mlp65k_inputs(rows=1024, seed=9)
     say("case mlp bf16: 1024 queries")
     ex = executor(ww.WC_BF16)
     v = ex.publish(net)
@@ -177,8 +177,8 @@ def test_mlp_bf16_matches_reduced_precision_oracle():
 
 
 def test_mlp_float32_bit_exact():
-    net = W.net_for("c2")
-    x = W.c2_inputs(rows=256, seed=5)
+    net = W.net_for("mlp65k")
+    x = W.mlp65k_inputs(rows=256, seed=5)
     say("case mlp float32: 256 queries")
     ex = executor(ww.WC_PRECISE)
     v = ex.publish(net)
@@ -197,7 +197,7 @@ def ref_cmp_ratio(got, want, atol, rtol):
     return float((np.abs(got - want) / tol).max()) if got.size else 0.0
 
 
-def test_c3_f16_fast_mode_tracks_exact_math():
+def test_wave64_f16_fast_mode_tracks_exact_math():
     """Plain f16 operands against the float32 CPU net, 64 DCFR iterations.
 
     The reference bounds its own f16 tensor-core head against exact math by the
@@ -208,9 +208,9 @@ def test_c3_f16_fast_mode_tracks_exact_math():
     1e-2 after 64 iterations, in the CPU emulation of f16 operands as much as
     on the device. Root values are therefore bounded here at 2e-2 of the tree's
     largest root value; the compensated-f16 mode carries the 2e-3 bound."""
-    jobs = W.jobs("c3", trees=12)
-    net = W.net_for("c3")
-    say(f"case c3 f16: {len(jobs)} trees, 64 iterations")
+    jobs = W.jobs("wave64", trees=12)
+    net = W.net_for("wave64")
+    say(f"case wave64 f16: {len(jobs)} trees, 64 iterations")
     got = gpu_solve(jobs, net, ww.WC_F16)
     for k, (j, g) in enumerate(zip(jobs, got)):
         ref = O.solve(j, net, O.NET_F32)
@@ -225,7 +225,7 @@ def test_c3_f16_fast_mode_tracks_exact_math():
 
 def test_service_submit_wait():
     jobs = small_wave(trees=5, seed=41)
-    net = W.net_for("c4")
+    net = W.net_for("wave256")
     say("case service: 5 jobs through submit/wait, 1 lane")
     ref = gpu_solve(jobs, net, ww.WC_PRECISE)
     with ww.spawn(0, net, ww.WC_PRECISE, lanes=1, wave_jobs=8, window_us=2000) as client:
@@ -234,6 +234,23 @@ def test_service_submit_wait():
         got = [h.wait() for h in handles]
     for k, (g, r) in enumerate(zip(got, ref)):
         assert g.tag == 100 + k
-        assert g.weight_version == 1
+        assert g.weight_version == 0
+        np.testing.assert_array_equal(g.strategy, r.strategy)
+        np.testing.assert_array_equal(g.root_values, r.root_values)
+
+
+def test_service_weight_versions_follow_submission():
+    jobs = small_wave(trees=4, seed=43)
+    net, net2 = W.net_for("wave256"), W.net_for("wave256", seed=2)
+    say("case service weights: 2 jobs, set_weights, 2 more jobs")
+    with ww.spawn(0, net, ww.WC_PRECISE, lanes=1, wave_jobs=8, window_us=2000) as client:
+        first = [client.submit(j, tag=k) for k, j in enumerate(jobs[:2])]
+        assert client.set_weights(net2) == 1
+        second = [client.submit(j, tag=10 + k) for k, j in enumerate(jobs[2:])]
+        got1 = [h.wait() for h in first]
+        got2 = [h.wait() for h in second]
+    assert [g.weight_version for g in got1] == [0, 0]
+    assert [g.weight_version for g in got2] == [1, 1]
+    for g, r in zip(got1 + got2, gpu_solve(jobs[:2], net, ww.WC_PRECISE) + gpu_solve(jobs[2:], net2, ww.WC_PRECISE)):
         np.testing.assert_array_equal(g.strategy, r.strategy)
         np.testing.assert_array_equal(g.root_values, r.root_values)

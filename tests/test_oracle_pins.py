@@ -35,7 +35,7 @@ VARIANTS = {  # engine/src/search.rs:141-179
 
 def tiny_terminal_tree(seed, variant="dcfr", iters=500, notrans=0.0, chance=1):
     a, b, g, p = VARIANTS[variant]
-    [j] = W.jobs("c4", trees=1, seed=seed, nodes_lo=8, nodes_hi=24, act_lo=2, act_hi=4, chance=chance, draw_lo=2,
+    [j] = W.jobs("wave256", trees=1, seed=seed, nodes_lo=8, nodes_hi=24, act_lo=2, act_hi=4, chance=chance, draw_lo=2,
                  draw_hi=3, info_fixed=3, terminal_p=1.0, notrans_p=notrans, collapse=0.3, iters=iters, dirichlet=1,
                  nroots=1, alpha=a, beta=b, gamma=g, predict=float(p))
     return j
@@ -176,7 +176,7 @@ def gathered_reach(d, cur):
 
 
 def test_reverse_gathers_replay_the_forward_scatter():
-    jobs = W.jobs("c4", trees=3, seed=17, nodes_lo=40, nodes_hi=90, chance=1, notrans_p=0.05, collapse=0.5,
+    jobs = W.jobs("wave256", trees=3, seed=17, nodes_lo=40, nodes_hi=90, chance=1, notrans_p=0.05, collapse=0.5,
                   info_median=6.0, info_p99=30.0, info_cap=30, terminal_p=0.1, iters=4)
     for job in jobs:
         d = wcj8.decode(job)
@@ -200,7 +200,7 @@ def test_reverse_gathers_replay_the_forward_scatter():
 
 def test_belief_fallback_is_uniform():
     """normalize_weights: a reach vector summing to <= 1e-30 becomes uniform 1/n."""
-    [job] = W.jobs("c4", trees=1, seed=23, nodes_lo=30, nodes_hi=50, chance=1, info_fixed=5, iters=2,
+    [job] = W.jobs("wave256", trees=1, seed=23, nodes_lo=30, nodes_hi=50, chance=1, info_fixed=5, iters=2,
                    terminal_p=0.2)
     d = wcj8.decode(job)
     d["root"][1] = np.zeros_like(d["root"][1])
@@ -226,7 +226,7 @@ def test_dcfr_factors():
 
 @pytest.mark.parametrize("iters", [1, 2, 8, 16, 64, 100])
 def test_snapshot_iterations_are_log_spaced_plus_final(iters):
-    [job] = W.jobs("c1", iters=iters)
+    [job] = W.jobs("tree48", iters=iters)
     got = list(wcj8.decode(job)["snap_iters"])
     want = [t for t in range(iters + 1) if t == 0 or (t & (t - 1)) == 0 or t == iters]
     assert got == want
@@ -261,10 +261,10 @@ def test_bf16_rounding_is_nearest_even():
 # ------------------------------------------------------------------------ net
 
 def test_mlp_matches_float64_numpy():
-    net = W.net_for("c2")
+    net = W.net_for("mlp65k")
     dims = net.dims
     inp, hid, layers, heads = dims[1], dims[2], dims[3], dims[4]
-    x = W.c2_inputs(rows=96, seed=12)
+    x = W.mlp65k_inputs(rows=96, seed=12)
     w = net.w.astype(np.float64)
     b = net.b.astype(np.float64)
     h = x.astype(np.float64)
@@ -286,8 +286,8 @@ def test_mlp_matches_float64_numpy():
 
 
 def test_zero_network_keeps_every_value_zero():
-    [job] = W.jobs("c1")
-    net = W.net_for("c1")
+    [job] = W.jobs("tree48")
+    net = W.net_for("tree48")
     zero = type(net)(net.dims, np.zeros_like(net.w), np.zeros_like(net.b))
     o = O.solve(job, zero, O.NET_F32)
     assert np.all(o["roots"] == 0.0)
@@ -369,8 +369,8 @@ def numpy_value_under(d, net, root):
 def test_value_under_matches_float64_restatement():
     """Pins belief_blocks, the query input, readout and the Value backprop:
     a zero-iteration solve is value_under under the uniform strategy."""
-    net = W.net_for("c4")
-    jobs = W.jobs("c4", trees=2, seed=29, nodes_lo=30, nodes_hi=60, chance=1, terminal_p=0.2, notrans_p=0.05,
+    net = W.net_for("wave256")
+    jobs = W.jobs("wave256", trees=2, seed=29, nodes_lo=30, nodes_hi=60, chance=1, terminal_p=0.2, notrans_p=0.05,
                   info_median=5.0, info_p99=20.0, info_cap=20, iters=0, nroots=2)
     for job in jobs:
         d = wcj8.decode(job)

@@ -30,7 +30,7 @@ Service::~Service() { shutdown(); }
 bool Service::start(const NetCopy& net, std::string* err) {
     auto first = std::make_shared<NetCopy>(net);
     first->version = next_version_++;
-    nets_[first->version] = first;
+    current_ = first;
     for (uint32_t l = 0; l < opts_.lanes; l++) lanes_.emplace_back(&Service::lane_main, this, l);
     std::unique_lock<std::mutex> lk(ready_mu_);
     ready_cv_.wait(lk, [&] { return ready_ + failed_ == opts_.lanes; });
@@ -51,10 +51,9 @@ uint64_t Service::set_weights(NetCopy net, std::string* err) {
     }
     auto copy = std::make_shared<NetCopy>(std::move(net));
     copy->version = next_version_++;
-    nets_[copy->version] = copy;
-    // Host copies of the two newest versions are retained; waves already formed
-    // hold their own reference to the bank they run under.
-    while (nets_.size() > 2) nets_.erase(nets_.begin());
+    // Jobs already queued keep the version they were submitted under
+    // (engine/src/gpu/service.rs:233); each holds its own reference to it.
+    current_ = copy;
     return copy->version;
 }
 
@@ -76,6 +75,7 @@ bool Service::submit(const uint8_t* bytes, size_t len, uint64_t tag, std::shared
             *err = "GPU wave executor is gone";
             return false;
         }
+        p.net = current_;
         queued_.fetch_add(t->cost, std::memory_order_relaxed);
         queue_.push_back(std::move(p));
     }
@@ -94,14 +94,17 @@ bool Service::take_wave(std::vector<Pending>* wave) {
     auto deadline = std::chrono::steady_clock::now() + std::chrono::microseconds(opts_.window_us);
     size_t rows = 0;
     const Meta head = queue_.front().job.meta;
-    auto compatible = [&](const Meta& m) {
-        return m.iters == head.iters && m.snapshots == head.snapshots && m.snap_iters == head.snap_iters &&
-               m.net_dims == head.net_dims && m.depth == head.depth &&
+    const uint64_t head_version = queue_.front().net->version;
+    // One wave runs one schedule under one weight version (service.rs:626).
+    auto compatible = [&](const Pending& q) {
+        const Meta& m = q.job.meta;
+        return q.net->version == head_version && m.iters == head.iters && m.snapshots == head.snapshots &&
+               m.snap_iters == head.snap_iters && m.net_dims == head.net_dims && m.depth == head.depth &&
                std::memcmp(&m.cfr, &head.cfr, sizeof(Cfr)) == 0;
     };
     for (;;) {
         for (auto it = queue_.begin(); it != queue_.end() && wave->size() < opts_.wave_jobs;) {
-            if (compatible(it->job.meta) && (wave->empty() || rows + it->rows <= opts_.wave_rows)) {
+            if (compatible(*it) && (wave->empty() || rows + it->rows <= opts_.wave_rows)) {
                 rows += it->rows;
                 wave->push_back(std::move(*it));
                 it = queue_.erase(it);
@@ -112,7 +115,7 @@ bool Service::take_wave(std::vector<Pending>* wave) {
         if (wave->size() >= opts_.wave_jobs || stop_) break;
         if (cv_.wait_until(lk, deadline) == std::cv_status::timeout) {
             for (auto it = queue_.begin(); it != queue_.end() && wave->size() < opts_.wave_jobs;) {
-                if (compatible(it->job.meta) && rows + it->rows <= opts_.wave_rows) {
+                if (compatible(*it) && rows + it->rows <= opts_.wave_rows) {
                     rows += it->rows;
                     wave->push_back(std::move(*it));
                     it = queue_.erase(it);
@@ -137,7 +140,7 @@ void Service::lane_main(uint32_t lane) {
         std::shared_ptr<const NetCopy> net;
         {
             std::lock_guard<std::mutex> lk(mu_);
-            if (!nets_.empty()) net = nets_.rbegin()->second;
+            net = current_;
         }
         if (ok && net) {
             uint64_t v = ex->publish(net->ns, net->dims, net->w.data(), net->w.size(), net->b.data(), net->b.size(), &err);
@@ -158,11 +161,7 @@ void Service::lane_main(uint32_t lane) {
         std::vector<Pending> wave;
         if (!take_wave(&wave)) break;
         if (wave.empty()) continue;
-        std::shared_ptr<const NetCopy> net;
-        {
-            std::lock_guard<std::mutex> lk(mu_);
-            net = nets_.rbegin()->second;
-        }
+        std::shared_ptr<const NetCopy> net = wave.front().net;
         std::string err;
         bool ok = true;
         uint64_t exv = 0;
@@ -172,8 +171,9 @@ void Service::lane_main(uint32_t lane) {
             ok = exv != 0;
             if (ok) {
                 bank_of[net->version] = exv;
-                // keep the two newest banks on this lane
-                while (bank_of.size() > 2) {
+                // keep the three newest banks on this lane; an older version
+                // still queued is published again when its wave comes
+                while (bank_of.size() > 3) {
                     ex->retain_from(std::next(bank_of.begin())->second);
                     bank_of.erase(bank_of.begin());
                 }

@@ -49,7 +49,7 @@ class Service {
   public:
     Service(int device, int precision, const ServiceOpts& opts);
     ~Service();
-    // Starts the lanes and publishes `net` as version 1; blocks until every lane is ready.
+    // Starts the lanes and publishes `net` as version 0; blocks until every lane is ready.
     bool start(const NetCopy& net, std::string* err);
     uint64_t set_weights(NetCopy net, std::string* err);
     uint64_t queued_work() const { return queued_.load(std::memory_order_relaxed); }
@@ -61,6 +61,7 @@ class Service {
         std::shared_ptr<Ticket> ticket;
         Job job;
         size_t rows = 0;
+        std::shared_ptr<const NetCopy> net;  // the weights current when the job was submitted
     };
     void lane_main(uint32_t lane);
     bool take_wave(std::vector<Pending>* wave);
@@ -73,8 +74,8 @@ class Service {
     std::deque<Pending> queue_;
     bool stop_ = false;
     std::atomic<uint64_t> queued_{0};
-    std::map<uint64_t, std::shared_ptr<const NetCopy>> nets_;
-    uint64_t next_version_ = 1;
+    std::shared_ptr<const NetCopy> current_;  // newest published weights
+    uint64_t next_version_ = 0;
     // lane start-up handshake
     std::mutex ready_mu_;
     std::condition_variable ready_cv_;
