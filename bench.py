@@ -94,8 +94,10 @@ def main():
     dominant = max(("k_sweep<regret>", "k_reach"), key=lambda n: by_kernel[n]["launch_ms"])
     bytes_per_iter = 0.5 * (st["cfr_bytes_per_iter"][0] + st["cfr_bytes_per_iter"][1])
     iter_gbs = bytes_per_iter / (iter_ms * 1e-3) / 1e9
-    mlp_flops_wave = st["rows"] * st["mlp_flops_per_query"] * (iters + 2 * st["nroots_max"])
+    passes = iters + 2 * st["nroots_max"]  # leaf-net passes per wave
+    mlp_flops_wave = st["mlp_flops_algorithmic"] * passes
     mlp_tflops_in_wave = mlp_flops_wave / (mlp_ms * 1e-3) / 1e12 if mlp_ms > 0 else 0.0
+    mlp_exec_tflops = st["mlp_flops_executed"] * passes / (mlp_ms * 1e-3) / 1e12 if mlp_ms > 0 else 0.0
     d = by_kernel[dominant]
 
     out = {
@@ -129,7 +131,10 @@ def main():
                                    "bytes_per_iter": int(bytes_per_iter), "iter_ms": round(iter_ms, 5)},
         "roofline_mlp_in_wave": {"bound": "mfma", "achieved": round(mlp_tflops_in_wave, 2),
                                  "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                 "frac": round(mlp_tflops_in_wave / MFMA_F16_PEAK_TFLOPS, 5)},
+                                 "frac": round(mlp_tflops_in_wave / MFMA_F16_PEAK_TFLOPS, 5),
+                                 "flops_per_pass": st["mlp_flops_algorithmic"],
+                                 "executed_tflops": round(mlp_exec_tflops, 2),
+                                 "note": "algorithmic = trunk + one head row per traverser config"},
     }
 
     if not args.no_mlp:

@@ -127,7 +127,10 @@ typedef struct wc_wave_stats {
     uint64_t cfr_bytes_per_iter[2]; /* algorithmic HBM bytes of one CFR iteration, traverser 0 / 1 */
     /* the same bytes by kernel, [traverser][kernel]: subtree value sweep, top-region launches, subtree reach sweep */
     uint64_t cfr_bytes_by_kernel[2][3];
-    uint64_t mlp_flops_per_query;
+    uint64_t mlp_flops_per_query;   /* trunk + every head row */
+    /* one leaf-net pass over all network rows: FLOP the head-width-trimmed GEMMs
+     * execute, and the algorithmic FLOP (trunk + the traverser's configs' head rows) */
+    uint64_t mlp_flops_executed, mlp_flops_algorithmic;
 } wc_wave_stats;
 int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* out);
 

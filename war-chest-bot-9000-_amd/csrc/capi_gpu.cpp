@@ -1,4 +1,5 @@
 // Device-facing entry points of the C ABI: executor, wave, service, results.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <exception>
@@ -160,6 +161,18 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
     const NetShape& ns = h.net;
     s->mlp_flops_per_query = 2ull * (uint64_t(ns.in) * ns.hidden + uint64_t(ns.layers - 1) * ns.hidden * ns.hidden +
                                      uint64_t(ns.hidden) * ns.heads);
+    // Executed per wave query: the trunk, plus the head columns of its 128-row tile
+    // rounded up to whole 128-column tiles; algorithmic: the trunk plus one head row
+    // per config of the traverser (averaged over the two traversers).
+    uint64_t head_exec = 0, head_alg = 0;
+    for (uint32_t r = 0; r < h.rows(); r++) {
+        uint64_t tn = h.head_tile_n[r / 128];
+        head_exec += std::min<uint64_t>((tn + 127) / 128 * 128, ns.heads);
+        head_alg += h.row_cfg_off[2 * r + 2] - h.row_cfg_off[2 * r];
+    }
+    const uint64_t trunk = 2ull * (uint64_t(ns.in) * ns.hidden + uint64_t(ns.layers - 1) * ns.hidden * ns.hidden);
+    s->mlp_flops_executed = h.rows() * trunk + 2ull * ns.hidden * head_exec;
+    s->mlp_flops_algorithmic = h.rows() * trunk + ns.hidden * head_alg;
     return WC_OK;
 }
 

@@ -120,17 +120,26 @@ uint64_t Executor::publish(const NetShape& ns, const std::vector<uint32_t>& dims
     bank.ns = ns;
     bank.precision = precision_;
     const size_t esz = precision_ == WC_PRECISE ? 4 : 2;
-    // Layout: matrices (as stored for the arithmetic), then f32 biases.
+    // Layout: matrices (as stored for the arithmetic), then f32 biases. The
+    // exact net keeps the source layout; the MFMA net stores each matrix as the
+    // GEMM's B operand, fragment-major with gemm_rows(N) zero-padded rows.
     std::vector<size_t> moff;
     size_t at = 0;
     std::vector<std::pair<size_t, size_t>> mats;  // (rows, cols) of each source matrix in w
     mats.push_back({ns.in, ns.hidden});
     for (uint32_t l = 1; l < ns.layers; l++) mats.push_back({ns.hidden, ns.hidden});
     mats.push_back({ns.heads, ns.hidden});
-    for (auto& m : mats) {
+    auto stored_bytes = [&](size_t k) {
+        if (precision_ == WC_PRECISE) return mats[k].first * mats[k].second * esz;
+        bool head = k + 1 == mats.size();
+        size_t n = head ? mats[k].first : mats[k].second, kdim = head ? mats[k].second : mats[k].first;
+        return size_t(gemm_rows((uint32_t)n)) * kdim * esz;
+    };
+    for (size_t k = 0; k < mats.size(); k++) {
         moff.push_back(at);
-        at = align256(at + m.first * m.second * esz);
+        at = align256(at + stored_bytes(k));
     }
+    const size_t mats_end = at;
     size_t boff = at;
     at = align256(at + nb * 4);
     // Staging for f32 -> 16-bit conversion on the device.
@@ -151,15 +160,17 @@ uint64_t Executor::publish(const NetShape& ns, const std::vector<uint32_t>& dims
             src += n;
         }
     } else {
+        okc = okc && hipMemsetAsync(base, 0, mats_end, stream_) == hipSuccess;  // row padding
         okc = okc && hipMemcpyAsync(base + stage, w, nw * 4, hipMemcpyHostToDevice, stream_) == hipSuccess;
         size_t src = 0;
         for (size_t k = 0; k < mats.size(); k++) {
             size_t n = mats[k].first * mats[k].second;
-            // Trunk matrices [K x N] are stored transposed ([N x K], K-contiguous);
-            // the head is already one K-contiguous row per output.
-            bool transpose = k + 1 < mats.size();
-            launch_to16(precision_, (const float*)(base + stage) + src, base + moff[k], (uint32_t)mats[k].first,
-                        (uint32_t)mats[k].second, transpose, stream_);
+            // Trunk matrices are [K x N] (B row n = source column n); the head is
+            // [N x K] (one K-contiguous row per output).
+            bool head = k + 1 == mats.size();
+            uint32_t rows = (uint32_t)(head ? mats[k].first : mats[k].second);
+            uint32_t kdim = (uint32_t)(head ? mats[k].second : mats[k].first);
+            launch_to16(precision_, (const float*)(base + stage) + src, base + moff[k], rows, kdim, !head, stream_);
             src += n;
         }
     }
@@ -209,7 +220,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
             draw_row_start, draw_to, draw_p, reach_base, vals_base, parent, rev_row_of, rev_start, rev_src, rev_cell,
             rvd_row_of, rvd_start, rvd_src, rvd_p, row_node, row_cfg_off, row_cfg, cfg_key, cfg_emb, pub_raw,
             term_node, term_util, roots, carried, exit_node, exit_coff, trees, units, bt[2], rt[2], dc[2], bl[2],
-            rl[2], unit_row, unit_term, tb[2], tr[2];
+            rl[2], unit_row, unit_term, tb[2], tr[2], head_tile_n;
     } o;
     o.node_meta = blob.put(w.node_meta);
     o.nc = blob.put(w.node_nc);
@@ -257,6 +268,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     }
     o.unit_row = blob.put(w.unit_row);
     o.unit_term = blob.put(w.unit_term);
+    o.head_tile_n = blob.put(w.head_tile_n);
     for (int p = 0; p < 2; p++) {
         o.tb[p] = blob.put(w.top_back[p]);
         o.tr[p] = blob.put(w.top_reach[p]);
@@ -287,8 +299,9 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         mt = a + std::max<size_t>(bytes, 4);
         return a;
     };
-    size_t m_x = mtake(rows * ns.in * esz), m_x1 = mtake(rows * ns.in * esz), m_h0 = mtake(rows * ns.hidden * esz),
-           m_h1 = mtake(rows * ns.hidden * esz), m_out = mtake(rows * ns.heads * 4);
+    const size_t prow = precision_ == WC_PRECISE ? rows : gemm_rows((uint32_t)rows);  // GEMM operands: padded rows
+    size_t m_x = mtake(prow * ns.in * esz), m_x1 = mtake(prow * ns.in * esz), m_h0 = mtake(prow * ns.hidden * esz),
+           m_h1 = mtake(prow * ns.hidden * esz), m_out = mtake(rows * ns.heads * 4);
     if (!ensure(&mlp_, &mlp_cap_, mt, err)) return false;
 
     char* T = (char*)table_;
@@ -343,6 +356,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     }
     d.unit_row = (const uint32_t*)(T + o.unit_row);
     d.unit_term = (const uint32_t*)(T + o.unit_term);
+    head_tile_n_ = (const uint32_t*)(T + o.head_tile_n);
     for (int p = 0; p < 2; p++) {
         top_back_dev_[p] = (const Task*)(T + o.tb[p]);
         top_reach_dev_[p] = (const Task*)(T + o.tr[p]);
@@ -382,7 +396,8 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     return true;
 }
 
-void Executor::run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::vector<hipEvent_t>* marks) {
+void Executor::run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::vector<hipEvent_t>* marks,
+                       const uint32_t* head_tile_n) {
     const NetShape& ns = bank.ns;
     auto mark = [&]() {
         if (marks) {
@@ -410,7 +425,7 @@ void Executor::run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::v
                           rows, stream_);
     else
         launch_gemm16(precision_, in, ns.hidden, bank.Whead, bank.bhead, ns.heads, head_out_, rows, false, false,
-                      stream_);
+                      stream_, head_tile_n);
     mark();
 }
 
@@ -435,7 +450,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         hipEventRecord(start, s);
     }
     auto mlp = [&](int q) {
-        run_mlp(bank, d.rows, Xq_[q], nullptr);
+        run_mlp(bank, d.rows, Xq_[q], nullptr, head_tile_n_);
         mark(C_MLP);
     };
     // Top regions, one depth per launch: values bottom-up, reach top-down.
@@ -626,9 +641,9 @@ bool Executor::mlp_forward(uint64_t version, uint32_t rows, const float* x, floa
         mt = a + std::max<size_t>(bytes, 4);
         return a;
     };
-    size_t m_x = mtake(size_t(rows) * ns.in * esz), m_h0 = mtake(size_t(rows) * ns.hidden * esz),
-           m_h1 = mtake(size_t(rows) * ns.hidden * esz), m_out = mtake(size_t(rows) * ns.heads * 4),
-           m_stage = mtake(size_t(rows) * ns.in * 4);
+    const size_t prow = precision_ == WC_PRECISE ? rows : gemm_rows(rows);  // GEMM operands: padded rows
+    size_t m_x = mtake(prow * ns.in * esz), m_h0 = mtake(prow * ns.hidden * esz), m_h1 = mtake(prow * ns.hidden * esz),
+           m_out = mtake(size_t(rows) * ns.heads * 4), m_stage = mtake(size_t(rows) * ns.in * 4);
     if (!ensure(&mlp_, &mlp_cap_, mt, err)) return false;
     char* M = (char*)mlp_;
     X_ = M + m_x;

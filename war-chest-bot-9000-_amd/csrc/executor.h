@@ -75,7 +75,8 @@ class Executor {
   private:
     bool upload(const WaveHost& w, const NetBank& bank, std::string* err);
     void run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTimes* prof);
-    void run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::vector<hipEvent_t>* marks);
+    void run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::vector<hipEvent_t>* marks,
+                 const uint32_t* head_tile_n = nullptr);
     bool ensure(void** p, size_t* cap, size_t need, std::string* err);
 
     int device_ = 0, precision_ = 0;
@@ -97,6 +98,7 @@ class Executor {
     void* X_ = nullptr;
     void* Xq_[2] = {};  // the wave's query inputs, one per traverser
     const Task* top_back_dev_[2] = {};   // top-region rows by depth (device copies)
+    const uint32_t* head_tile_n_ = nullptr;  // head width per 128-row tile (device copy)
     const Task* top_reach_dev_[2] = {};
     void* H_[2] = {};
     float* head_out_ = nullptr;

@@ -12,6 +12,17 @@ namespace wc {
 
 enum : int { MODE_REGRET = 0, MODE_VALUE = 1 };
 
+// Fragment-major layout of a 16-bit GEMM operand with K columns: every
+// (16-row block, 32-column step) is one contiguous 1 KB block holding the 64
+// lanes' 16-byte MFMA fragments in lane order (lane l: row l % 16, columns
+// 8 (l / 16) .. + 7 of the step), so one fragment load is one coalesced read.
+// Rows are padded to a multiple of GEMM_ROWS; K must be a multiple of 32.
+constexpr uint32_t GEMM_ROWS = 128;
+__host__ __device__ inline size_t frag_off(uint32_t row, uint32_t k, uint32_t K) {
+    return ((size_t)((row >> 4) * (K >> 5) + (k >> 5)) * 64 + (row & 15) + ((k & 31) >> 3) * 16) * 8 + (k & 7);
+}
+inline uint32_t gemm_rows(uint32_t rows) { return (rows + GEMM_ROWS - 1) / GEMM_ROWS * GEMM_ROWS; }
+
 struct WaveDev {
     // immutable tables
     const uint32_t *node_meta, *nc, *child_start, *child;
@@ -80,13 +91,17 @@ void launch_dense_exact(const float* X, uint32_t K, const float* W, const float*
 // Exact float32 head: out[r, k] = b[k] + sum_j Wh[k, j] H[r, j], Wh [heads x hidden].
 void launch_head_exact(const float* H, uint32_t hidden, const float* Wh, const float* bh, uint32_t heads,
                        float* out, uint32_t rows, hipStream_t s);
-// MFMA GEMM: Y[M, N] = act(X[M, K] Wt[N, K]^T + b); 16-bit operands, f32 accumulate.
-// precision WC_F16 / WC_BF16; relu selects the activation; out16 selects a 16-bit
-// (next-layer operand) or f32 output.
+// MFMA GEMM: Y[M, N] = act(X[M, K] Wt[N, K]^T + b); 16-bit fragment-major
+// operands (X with gemm_rows(M) rows, Wt with gemm_rows(N) rows), f32
+// accumulate. precision WC_F16 / WC_BF16; relu selects the activation; out16
+// selects a 16-bit fragment-major output with K = N (the next layer's operand,
+// N % 32 == 0) or a row-major f32 output. tile_n (optional, one entry per
+// 128-row tile) bounds the columns each row tile needs; the rest are not computed.
 void launch_gemm16(int precision, const void* X, uint32_t K, const void* Wt, const float* b, uint32_t N,
-                   void* Y, uint32_t M, bool relu, bool out16, hipStream_t s);
-// Convert f32 -> 16-bit operands (row-major copy, or transposing [K x N] -> [N x K]).
-void launch_to16(int precision, const float* src, void* dst, uint32_t rows, uint32_t cols, bool transpose,
+                   void* Y, uint32_t M, bool relu, bool out16, hipStream_t s, const uint32_t* tile_n = nullptr);
+// Convert f32 -> a 16-bit fragment-major operand of `rows` rows and K columns;
+// element (r, k) is src[k * rows + r] when `transposed`, else src[r * K + k].
+void launch_to16(int precision, const float* src, void* dst, uint32_t rows, uint32_t K, bool transposed,
                  hipStream_t s);
 
 }  // namespace wc

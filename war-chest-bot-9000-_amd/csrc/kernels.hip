@@ -275,6 +275,12 @@ __device__ __forceinline__ void store_operand(void* base, size_t i, float v) {
         ((uint16_t*)base)[i] = f32_to_bf16_rn(v);
 }
 
+// Query inputs are row-major float32 for the exact net, fragment-major 16-bit for MFMA.
+template <int PREC>
+__device__ __forceinline__ size_t operand_at(uint32_t row, uint32_t k, uint32_t K) {
+    return PREC == WC_PRECISE ? (size_t)row * K + k : frag_off(row, k, K);
+}
+
 __device__ __forceinline__ float lane_value(float v, uint32_t j) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)j));
 }
@@ -352,8 +358,8 @@ __global__ __launch_bounds__(BLOCK) void k_pool(WaveDev w, int player, void* x0,
             }
         }
         if (live) {
-            store_operand<PREC>(own, (size_t)row * in + k, acc);
-            store_operand<PREC>(other, (size_t)row * in + pool + k, acc);
+            store_operand<PREC>(own, operand_at<PREC>(row, k, in), acc);
+            store_operand<PREC>(other, operand_at<PREC>(row, pool + k, in), acc);
         }
     }
 }
@@ -378,7 +384,7 @@ __global__ void k_query_static(WaveDev w, void* x0, void* x1) {
     const uint32_t width = w.in - 2 * w.pool;
     if (i >= (size_t)w.rows * width) return;
     uint32_t row = (uint32_t)(i / width), k = (uint32_t)(i % width);
-    size_t at = (size_t)row * w.in + 2 * w.pool + k;
+    size_t at = operand_at<PREC>(row, 2 * w.pool + k, w.in);
     if (k == 0) {
         store_operand<PREC>(x0, at, -1.0f);
         store_operand<PREC>(x1, at, 1.0f);
@@ -726,75 +732,91 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
 template <int PREC>
-__global__ void k_to16(const float* src, uint16_t* dst, uint32_t rows, uint32_t cols, int transpose) {
+__global__ void k_to16(const float* src, uint16_t* dst, uint32_t rows, uint32_t K, int transposed) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)rows * cols) return;
-    uint32_t r = (uint32_t)(i / cols), c = (uint32_t)(i % cols);
-    float v = src[i];
-    uint16_t h = PREC == WC_F16 ? f32_to_f16_rn(v) : f32_to_bf16_rn(v);
-    if (transpose)
-        dst[(size_t)c * rows + r] = h;
-    else
-        dst[i] = h;
+    if (i >= (size_t)rows * K) return;
+    uint32_t r = (uint32_t)(i / K), k = (uint32_t)(i % K);
+    float v = transposed ? src[(size_t)k * rows + r] : src[i];
+    dst[frag_off(r, k, K)] = PREC == WC_F16 ? f32_to_f16_rn(v) : f32_to_bf16_rn(v);
 }
 
-void launch_to16(int precision, const float* src, void* dst, uint32_t rows, uint32_t cols, bool transpose,
+void launch_to16(int precision, const float* src, void* dst, uint32_t rows, uint32_t K, bool transposed,
                  hipStream_t s) {
-    size_t n = (size_t)rows * cols;
+    size_t n = (size_t)rows * K;
     if (!n) return;
     if (precision == WC_F16)
-        hipLaunchKernelGGL(k_to16<WC_F16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, src, (uint16_t*)dst, rows, cols,
-                           (int)transpose);
+        hipLaunchKernelGGL(k_to16<WC_F16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, src, (uint16_t*)dst, rows, K,
+                           (int)transposed);
     else
-        hipLaunchKernelGGL(k_to16<WC_BF16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, src, (uint16_t*)dst, rows, cols,
-                           (int)transpose);
+        hipLaunchKernelGGL(k_to16<WC_BF16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, src, (uint16_t*)dst, rows, K,
+                           (int)transposed);
 }
 
-// 16x16x32 MFMA tile GEMM, 128 x 128 output per workgroup (4 wavefronts in a
-// 2 x 2 grid, 64 x 64 each = 4 x 4 MFMA tiles). Both operands are K-contiguous
-// (X row-major [M, K], Wt [N, K]), so each lane's 8-element fragment is one
-// 16-byte load. Lane l holds A[l % 16][8 (l / 16) ..] and B[..][l % 16]; the
-// 4 accumulators of lane l are D[4 (l / 16) + v][l % 16].
+// 16x16x32 MFMA step over a 64 x 64 wave tile: acc[a][b] += A(a) B(b)^T.
+template <int PREC>
+__device__ __forceinline__ void mfma_step(float4v (&acc)[4][4], const uint4 (&af)[4], const uint4 (&bf)[4]) {
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            if (PREC == WC_F16)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, af[a]),
+                                                                   __builtin_bit_cast(half8, bf[b]), acc[a][b], 0, 0,
+                                                                   0);
+            else
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[a]),
+                                                                    __builtin_bit_cast(bf16x8, bf[b]), acc[a][b], 0,
+                                                                    0, 0);
+        }
+}
+
+// Fragment-major MFMA GEMM. A 128 x 128 output tile per workgroup, 64 x 64 per
+// wavefront (4 x 4 16x16x32 tiles). Both operands are fragment-major, so each
+// of a step's 8 fragment loads is one contiguous 1 KB read. Two fragment sets
+// ping-pong: while one step's 16 MFMAs run, the next step's loads are in
+// flight (the loop is unrolled by two so the compiler waits only for the set
+// it is about to use). The epilogue adds the bias, applies ReLU and stores
+// either the next layer's 16-bit fragment-major operand or row-major f32.
 template <int PREC, bool RELU, bool OUT16>
-__global__ __launch_bounds__(256) void k_gemm16(const uint16_t* __restrict__ X, uint32_t K,
-                                                const uint16_t* __restrict__ Wt, const float* __restrict__ bias,
-                                                uint32_t N, void* __restrict__ Y, uint32_t M) {
+__global__ __launch_bounds__(256) void k_gemm(const uint16_t* __restrict__ X, uint32_t K,
+                                              const uint16_t* __restrict__ Wt, const float* __restrict__ bias,
+                                              uint32_t N, void* __restrict__ Y, uint32_t M,
+                                              const uint32_t* __restrict__ tile_n) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t m0 = blockIdx.x * 128 + (wave & 1) * 64;
-    const uint32_t n0 = blockIdx.y * 128 + (wave >> 1) * 64;
-    const uint32_t li = lane & 15, kb = lane >> 4;
+    if (tile_n && blockIdx.y * GEMM_ROWS >= tile_n[blockIdx.x]) return;  // block-uniform
+    const uint32_t m0 = blockIdx.x * GEMM_ROWS + (wave & 1) * 64;
+    const uint32_t n0 = blockIdx.y * GEMM_ROWS + (wave >> 1) * 64;
+    const uint32_t ks = K >> 5;  // 32-wide k steps
     float4v acc[4][4];
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[a][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-    const uint4 zero = make_uint4(0, 0, 0, 0);
-    for (uint32_t k0 = 0; k0 < K; k0 += 32) {
-        uint4 af[4], bfr[4];
+    // Fragment (block, step) lives at ((block * ks + step) * 64 + lane) * 8.
+    const uint16_t* ap = X + ((size_t)(m0 >> 4) * ks * 64 + lane) * 8;
+    const uint16_t* bp = Wt + ((size_t)(n0 >> 4) * ks * 64 + lane) * 8;
+    const size_t blk = (size_t)ks * 64 * 8;  // halves between consecutive 16-row blocks
+    uint4 af[4], bf[4], an[4], bn[4];
+    auto load = [&](uint4 (&fa)[4], uint4 (&fb)[4], uint32_t step) {
 #pragma unroll
-        for (int a = 0; a < 4; a++) {
-            uint32_t row = m0 + a * 16 + li;
-            af[a] = row < M ? *(const uint4*)(X + (size_t)row * K + k0 + kb * 8) : zero;
-        }
+        for (int a = 0; a < 4; a++) fa[a] = *(const uint4*)(ap + a * blk + (size_t)step * 512);
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            uint32_t col = n0 + b * 16 + li;
-            bfr[b] = col < N ? *(const uint4*)(Wt + (size_t)col * K + k0 + kb * 8) : zero;
-        }
-#pragma unroll
-        for (int a = 0; a < 4; a++)
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                if (PREC == WC_F16)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, af[a]),
-                                                                       __builtin_bit_cast(half8, bfr[b]), acc[a][b],
-                                                                       0, 0, 0);
-                else
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[a]),
-                                                                        __builtin_bit_cast(bf16x8, bfr[b]),
-                                                                        acc[a][b], 0, 0, 0);
-            }
+        for (int b = 0; b < 4; b++) fb[b] = *(const uint4*)(bp + b * blk + (size_t)step * 512);
+    };
+    load(af, bf, 0);
+    uint32_t st = 0;
+    for (; st + 2 <= ks; st += 2) {
+        load(an, bn, st + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_step<PREC>(acc, af, bf);
+        __builtin_amdgcn_sched_barrier(0);
+        load(af, bf, st + 2 < ks ? st + 2 : st + 1);  // past the end: re-read a valid step, unused
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_step<PREC>(acc, an, bn);
+        __builtin_amdgcn_sched_barrier(0);
     }
+    if (st < ks) mfma_step<PREC>(acc, af, bf);  // odd step count: af holds the last step
+    const uint32_t li = lane & 15, kb = lane >> 4;
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
@@ -809,7 +831,7 @@ __global__ __launch_bounds__(256) void k_gemm16(const uint16_t* __restrict__ X, 
                 float y = acc[a][b][v] + bv;
                 if (RELU) y = y > 0.0f ? y : 0.0f;
                 if (OUT16)
-                    ((uint16_t*)Y)[(size_t)row * N + col] = PREC == WC_F16 ? f32_to_f16_rn(y) : f32_to_bf16_rn(y);
+                    ((uint16_t*)Y)[frag_off(row, col, N)] = PREC == WC_F16 ? f32_to_f16_rn(y) : f32_to_bf16_rn(y);
                 else
                     ((float*)Y)[(size_t)row * N + col] = y;
             }
@@ -817,12 +839,12 @@ __global__ __launch_bounds__(256) void k_gemm16(const uint16_t* __restrict__ X, 
 }
 
 void launch_gemm16(int precision, const void* X, uint32_t K, const void* Wt, const float* b, uint32_t N, void* Y,
-                   uint32_t M, bool relu, bool out16, hipStream_t s) {
+                   uint32_t M, bool relu, bool out16, hipStream_t s, const uint32_t* tile_n) {
     if (M == 0 || N == 0) return;
-    dim3 grid((M + 127) / 128, (N + 127) / 128);
+    dim3 grid(gemm_rows(M) / GEMM_ROWS, gemm_rows(N) / GEMM_ROWS);
     const uint16_t* x = (const uint16_t*)X;
     const uint16_t* wt = (const uint16_t*)Wt;
-#define WC_GEMM(P, R, O) hipLaunchKernelGGL((k_gemm16<P, R, O>), grid, dim3(256), 0, s, x, K, wt, b, N, Y, M)
+#define WC_GEMM(P, R, O) hipLaunchKernelGGL((k_gemm<P, R, O>), grid, dim3(256), 0, s, x, K, wt, b, N, Y, M, tile_n)
     if (precision == WC_F16) {
         if (relu && out16)
             WC_GEMM(WC_F16, true, true);

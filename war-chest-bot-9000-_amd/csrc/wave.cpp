@@ -377,6 +377,14 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
         w.trees.push_back(td);
     }
     w.child_start.push_back((uint32_t)w.child.size());
+    // Head width per 128-row tile of the network rows.
+    const uint32_t nrows = w.rows();
+    w.head_tile_n.assign((nrows + 127) / 128, 0);
+    for (uint32_t r = 0; r < nrows; r++)
+        for (uint32_t x = w.row_cfg_off[2 * r]; x < w.row_cfg_off[2 * r + 2]; x++) {
+            uint32_t& n = w.head_tile_n[r / 128];
+            n = std::max(n, w.cfg_key[w.row_cfg[x]] + 1);
+        }
     // Subtree units largest first: the device takes them in launch order.
     std::stable_sort(sub_units.begin(), sub_units.end(),
                      [](const UnitDev& a, const UnitDev& b) { return a.slots > b.slots; });

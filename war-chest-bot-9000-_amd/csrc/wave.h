@@ -81,6 +81,9 @@ struct WaveHost {
     std::vector<uint32_t> cfg_key;  // head row of each interned config
     std::vector<float> cfg_emb;     // [ncfg, pool]
     std::vector<uint8_t> pub_raw;   // [rows, row_bytes]
+    // Head columns each 128-row tile of the network rows needs: 1 + the largest
+    // head key among the tile's configs (the head GEMM skips the rest).
+    std::vector<uint32_t> head_tile_n;
     std::vector<uint32_t> term_node;
     std::vector<float> term_util;
     std::vector<float> roots, carried;
