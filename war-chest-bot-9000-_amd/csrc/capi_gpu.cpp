@@ -145,10 +145,10 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
                h.row_node.size() + h.row_cfg_off.size() + h.row_cfg.size() + h.cfg_key.size() + h.cfg_emb.size());
     tb += h.pub_raw.size();
     for (int p = 0; p < 2; p++)
-        tb += 8 * (h.back_task[p].size() + h.reach_task[p].size() + h.decision[p].size()) +
-              4 * (h.back_lvl[p].size() + h.reach_lvl[p].size());
+        tb += 16 * (h.back_rec[p].size() + h.reach_rec[p].size() + h.acc_rec[p].size() + h.top_back_rec[p].size() +
+                    h.top_reach_rec[p].size()) +
+              4 * (h.back_lvl[p].size() + h.reach_lvl[p].size() + h.child_vb[p].size());
     tb += sizeof(UnitDev) * h.units.size() + 4 * (h.unit_row.size() + h.unit_term.size());
-    for (int p = 0; p < 2; p++) tb += 8 * (h.top_back[p].size() + h.top_reach[p].size());
     s->table_bytes = tb;
     s->arena_bytes = 4 * (4ull * h.ncells + 2ull * h.reach_len + h.vals_len + 2ull * h.rows() * (h.net.pool + 1) +
                           h.root_values_len) +

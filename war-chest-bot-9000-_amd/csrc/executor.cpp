@@ -220,7 +220,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
             draw_row_start, draw_to, draw_p, reach_base, vals_base, parent, rev_row_of, rev_start, rev_src, rev_cell,
             rvd_row_of, rvd_start, rvd_src, rvd_p, row_node, row_cfg_off, row_cfg, cfg_key, cfg_emb, pub_raw,
             term_node, term_util, roots, carried, exit_node, exit_coff, trees, units, bt[2], rt[2], dc[2], bl[2],
-            rl[2], unit_row, unit_term, tb[2], tr[2], head_tile_n;
+            rl[2], cv[2], unit_row, unit_term, tb[2], tr[2], head_tile_n;
     } o;
     o.node_meta = blob.put(w.node_meta);
     o.nc = blob.put(w.node_nc);
@@ -260,9 +260,10 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     o.trees = blob.put(w.trees);
     o.units = blob.put(w.units);
     for (int p = 0; p < 2; p++) {
-        o.bt[p] = blob.put(w.back_task[p]);
-        o.rt[p] = blob.put(w.reach_task[p]);
-        o.dc[p] = blob.put(w.decision[p]);
+        o.bt[p] = blob.put(w.back_rec[p]);
+        o.rt[p] = blob.put(w.reach_rec[p]);
+        o.dc[p] = blob.put(w.acc_rec[p]);
+        o.cv[p] = blob.put(w.child_vb[p]);
         o.bl[p] = blob.put(w.back_lvl[p]);
         o.rl[p] = blob.put(w.reach_lvl[p]);
     }
@@ -270,8 +271,8 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     o.unit_term = blob.put(w.unit_term);
     o.head_tile_n = blob.put(w.head_tile_n);
     for (int p = 0; p < 2; p++) {
-        o.tb[p] = blob.put(w.top_back[p]);
-        o.tr[p] = blob.put(w.top_reach[p]);
+        o.tb[p] = blob.put(w.top_back_rec[p]);
+        o.tr[p] = blob.put(w.top_reach_rec[p]);
     }
     if (!ensure(&table_, &table_cap_, host_blob_.size(), err)) return false;
     HIP_TRY(hipMemcpyAsync(table_, host_blob_.data(), host_blob_.size(), hipMemcpyHostToDevice, stream_));
@@ -347,9 +348,10 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     d.trees = (const TreeDev*)(T + o.trees);
     d.units = (const UnitDev*)(T + o.units);
     for (int p = 0; p < 2; p++) {
-        d.back_task[p] = (const Task*)(T + o.bt[p]);
-        d.reach_task[p] = (const Task*)(T + o.rt[p]);
-        d.decision[p] = (const Task*)(T + o.dc[p]);
+        d.back_rec[p] = (const BackRec*)(T + o.bt[p]);
+        d.reach_rec[p] = (const ReachRec*)(T + o.rt[p]);
+        d.acc_rec[p] = (const AccRec*)(T + o.dc[p]);
+        d.child_vb[p] = (const uint32_t*)(T + o.cv[p]);
         d.back_lvl[p] = (const uint32_t*)(T + o.bl[p]);
         d.reach_lvl[p] = (const uint32_t*)(T + o.rl[p]);
         d.ndec[p] = (uint32_t)w.decision[p].size();
@@ -358,9 +360,9 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     d.unit_term = (const uint32_t*)(T + o.unit_term);
     head_tile_n_ = (const uint32_t*)(T + o.head_tile_n);
     for (int p = 0; p < 2; p++) {
-        top_back_dev_[p] = (const Task*)(T + o.tb[p]);
-        top_reach_dev_[p] = (const Task*)(T + o.tr[p]);
-        d.top_dec[p] = d.decision[p] + w.top_dec0[p];
+        top_back_dev_[p] = (const BackRec*)(T + o.tb[p]);
+        top_reach_dev_[p] = (const ReachRec*)(T + o.tr[p]);
+        d.top_acc[p] = d.acc_rec[p] + w.top_dec0[p];
         d.ntop_dec[p] = (uint32_t)w.decision[p].size() - w.top_dec0[p];
     }
     d.nunits = (uint32_t)w.units.size();

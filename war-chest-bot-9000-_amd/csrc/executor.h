@@ -97,9 +97,9 @@ class Executor {
     WaveDev dev_{};
     void* X_ = nullptr;
     void* Xq_[2] = {};  // the wave's query inputs, one per traverser
-    const Task* top_back_dev_[2] = {};   // top-region rows by depth (device copies)
+    const BackRec* top_back_dev_[2] = {};    // top-region rows by depth (device copies)
+    const ReachRec* top_reach_dev_[2] = {};
     const uint32_t* head_tile_n_ = nullptr;  // head width per 128-row tile (device copy)
-    const Task* top_reach_dev_[2] = {};
     void* H_[2] = {};
     float* head_out_ = nullptr;
     uint32_t rows_ = 0;

@@ -42,10 +42,13 @@ struct WaveDev {
     const uint32_t *exit_node, *exit_coff;
     const TreeDev* trees;
     const UnitDev* units;
-    const Task *back_task[2], *reach_task[2], *decision[2];
+    const BackRec* back_rec[2];
+    const ReachRec* reach_rec[2];
+    const AccRec* acc_rec[2];  // every decision row; the top regions' rows close each list
+    const uint32_t* child_vb[2];
     const uint32_t *back_lvl[2], *reach_lvl[2];
     const uint32_t *unit_row, *unit_term;
-    const Task* top_dec[2];
+    const AccRec* top_acc[2];
     // mutable arena
     float *regret, *cur, *sum, *snap;
     float *reach, *snap_reach, *vals;
@@ -66,8 +69,8 @@ void launch_seed_reach(const WaveDev& w, float* reach, int root_index, hipStream
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
                   bool accumulate, hipStream_t s);
 // Top-region reach at one depth (rows of player 0 and of player 1).
-void launch_reach_rows(const WaveDev& w, const Task* r0, uint32_t n0, const Task* r1, uint32_t n1, float* reach,
-                       const float* strat, hipStream_t s);
+void launch_reach_rows(const WaveDev& w, const ReachRec* r0, uint32_t n0, const ReachRec* r1, uint32_t n1,
+                       float* reach, const float* strat, hipStream_t s);
 void launch_seed_sum(const WaveDev& w, hipStream_t s);
 // Leaf reach masses and pooled beliefs of one player (-1 = both), written into
 // the query inputs x0 (traverser 0) and x1 (traverser 1) in the operand precision.
@@ -78,8 +81,8 @@ void launch_query_static(const WaveDev& w, int precision, void* x0, void* x1, hi
 void launch_sweep(const WaveDev& w, uint32_t unit0, uint32_t n, const float* head_out, uint32_t heads, int traverser,
                   int mode, float da, float db, float ds, float predict, hipStream_t s);
 // Top-region values at one depth for the traverser.
-void launch_back_rows(const WaveDev& w, const Task* rows, uint32_t n, int traverser, int mode, float da, float db,
-                      float ds, float predict, hipStream_t s);
+void launch_back_rows(const WaveDev& w, const BackRec* rows, uint32_t n, int traverser, int mode, float da,
+                      float db, float ds, float predict, hipStream_t s);
 void launch_normalize(const WaveDev& w, int touched0, int touched1, hipStream_t s);
 void launch_gather_carry(const WaveDev& w, const float* reach, int slot, hipStream_t s);
 void launch_collect_root(const WaveDev& w, int root, int player, hipStream_t s);

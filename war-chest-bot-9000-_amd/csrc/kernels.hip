@@ -36,13 +36,13 @@ void launch_zero(float* p, size_t n, hipStream_t s) {
     hipLaunchKernelGGL(k_zero, dim3(g), dim3(BLOCK), 0, s, p, n);
 }
 
-__device__ __forceinline__ const Task& decision_task(const WaveDev& w, uint32_t i, int* p) {
+__device__ __forceinline__ const AccRec& decision_row(const WaveDev& w, uint32_t i, int* p) {
     if (i < w.ndec[0]) {
         *p = 0;
-        return w.decision[0][i];
+        return w.acc_rec[0][i];
     }
     *p = 1;
-    return w.decision[1][i - w.ndec[0]];
+    return w.acc_rec[1][i - w.ndec[0]];
 }
 
 // ------------------------------------------------------------- CFR state
@@ -52,11 +52,9 @@ __global__ void k_init_strategy(WaveDev w) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= w.ndec[0] + w.ndec[1]) return;
     int p;
-    Task q = decision_task(w, i, &p);
-    uint32_t row = w.legal_row_of[q.node] + q.config;
-    uint32_t lo = w.legal_off[row], hi = w.legal_off[row + 1];
-    float u = 1.0f / (float)(hi - lo);
-    for (uint32_t g = lo; g < hi; g++) w.cur[g] = u;
+    AccRec q = decision_row(w, i, &p);
+    float u = 1.0f / (float)q.n;
+    for (uint32_t g = q.lo; g < q.lo + q.n; g++) w.cur[g] = u;
 }
 
 void launch_init_strategy(const WaveDev& w, hipStream_t s) {
@@ -89,14 +87,10 @@ constexpr uint32_t ROW_BATCH = 16;
 
 // One child config's reach: the reverse gather in stored order (the CPU's
 // scatter order, engine/src/serialize.rs:714-723).
-__device__ __forceinline__ void reach_task(const WaveDev& w, float* reach, const float* strat, int p, Task q) {
-    uint32_t node = q.node, c = q.config;
-    uint32_t base = w.reach_base[2 * w.parent[node] + p];
+__device__ __forceinline__ void reach_row(const WaveDev& w, float* reach, const float* strat, ReachRec q) {
+    const uint32_t lo = q.start, n = q.kn & REC_N, base = q.pbase;
     float v = 0.0f;
-    uint32_t rr = w.rev_row_of[node];
-    if (rr != 0xffffffffu) {
-        uint32_t row = rr + c;
-        uint32_t lo = w.rev_start[row], n = w.rev_start[row + 1] - lo;
+    if ((q.kn >> 31) == REACH_REV) {
         if (n <= ROW_BATCH) {
             uint32_t src[ROW_BATCH], cell[ROW_BATCH];
             float a[ROW_BATCH], b[ROW_BATCH];
@@ -119,8 +113,6 @@ __device__ __forceinline__ void reach_task(const WaveDev& w, float* reach, const
             for (uint32_t x = lo; x < lo + n; x++) v += reach[base + w.rev_src[x]] * strat[w.rev_cell[x]];
         }
     } else {
-        uint32_t row = w.rvd_row_of[node] + c;
-        uint32_t lo = w.rvd_start[row], n = w.rvd_start[row + 1] - lo;
         if (n <= ROW_BATCH) {
             uint32_t src[ROW_BATCH];
             float a[ROW_BATCH], pr[ROW_BATCH];
@@ -140,33 +132,32 @@ __device__ __forceinline__ void reach_task(const WaveDev& w, float* reach, const
             for (uint32_t x = lo; x < lo + n; x++) v += reach[base + w.rvd_src[x]] * w.rvd_p[x];
         }
     }
-    reach[w.reach_base[2 * node + p] + c] = v;
+    reach[q.out] = v;
 }
 
-// Average-strategy accumulation over one unit's decision rows of player p
-// (engine/src/search.rs:1818-1835).
-__device__ __forceinline__ void accumulate_unit(const WaveDev& w, const UnitDev& u, int p) {
-    const Task* dec = w.decision[p];
-    for (uint32_t k = u.dec0[p] + threadIdx.x; k < u.dec1[p]; k += blockDim.x) {
-        Task q = dec[k];
-        uint32_t row = w.legal_row_of[q.node] + q.config;
-        float r = w.reach[w.reach_base[2 * q.node + p] + q.config];
-        uint32_t lo = w.legal_off[row], n = w.legal_off[row + 1] - lo;
-        if (n <= ROW_BATCH) {
-            float cu[ROW_BATCH], sm[ROW_BATCH];
+// sum += reach * cur over one decision row (engine/src/search.rs:1818-1835).
+__device__ __forceinline__ void accumulate_row(const WaveDev& w, AccRec q) {
+    const float r = w.reach[q.ridx];
+    const uint32_t lo = q.lo, n = q.n;
+    if (n <= ROW_BATCH) {
+        float cu[ROW_BATCH], sm[ROW_BATCH];
 #pragma unroll
-            for (uint32_t j = 0; j < ROW_BATCH; j++)
-                if (j < n) {
-                    cu[j] = w.cur[lo + j];
-                    sm[j] = w.sum[lo + j];
-                }
+        for (uint32_t j = 0; j < ROW_BATCH; j++)
+            if (j < n) {
+                cu[j] = w.cur[lo + j];
+                sm[j] = w.sum[lo + j];
+            }
 #pragma unroll
-            for (uint32_t j = 0; j < ROW_BATCH; j++)
-                if (j < n) w.sum[lo + j] = sm[j] + r * cu[j];
-        } else {
-            for (uint32_t g = lo; g < lo + n; g++) w.sum[g] += r * w.cur[g];
-        }
+        for (uint32_t j = 0; j < ROW_BATCH; j++)
+            if (j < n) w.sum[lo + j] = sm[j] + r * cu[j];
+    } else {
+        for (uint32_t g = lo; g < lo + n; g++) w.sum[g] += r * w.cur[g];
     }
+}
+
+// Average-strategy accumulation over one unit's decision rows of player p.
+__device__ __forceinline__ void accumulate_unit(const WaveDev& w, const UnitDev& u, int p) {
+    for (uint32_t k = u.dec0[p] + threadIdx.x; k < u.dec1[p]; k += blockDim.x) accumulate_row(w, w.acc_rec[p][k]);
 }
 
 // Top-down reach of one unit, level by level under block barriers: player p
@@ -180,13 +171,13 @@ __device__ __forceinline__ void reach_unit(const WaveDev& w, const UnitDev& u, f
             uint32_t n0 = e0 - b0, n = n0 + (e1 - b1);
             for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
                 if (k < n0)
-                    reach_task(w, reach, strat, 0, w.reach_task[0][b0 + k]);
+                    reach_row(w, reach, strat, w.reach_rec[0][b0 + k]);
                 else
-                    reach_task(w, reach, strat, 1, w.reach_task[1][b1 + k - n0]);
+                    reach_row(w, reach, strat, w.reach_rec[1][b1 + k - n0]);
             }
         } else {
             uint32_t b = w.reach_lvl[p][u.lvl0 + l], e = w.reach_lvl[p][u.lvl0 + l + 1];
-            for (uint32_t k = b + threadIdx.x; k < e; k += blockDim.x) reach_task(w, reach, strat, p, w.reach_task[p][k]);
+            for (uint32_t k = b + threadIdx.x; k < e; k += blockDim.x) reach_row(w, reach, strat, w.reach_rec[p][k]);
         }
         __syncthreads();
     }
@@ -199,11 +190,7 @@ __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, uint
                                                const float* strat, int player, int accumulate) {
     if (blockIdx.x >= nunits) {
         const uint32_t k = (blockIdx.x - nunits) * blockDim.x + threadIdx.x;
-        if (k >= w.ntop_dec[player]) return;
-        Task q = w.top_dec[player][k];
-        uint32_t row = w.legal_row_of[q.node] + q.config;
-        float r = w.reach[w.reach_base[2 * q.node + player] + q.config];
-        for (uint32_t g = w.legal_off[row]; g < w.legal_off[row + 1]; g++) w.sum[g] += r * w.cur[g];
+        if (k < w.ntop_dec[player]) accumulate_row(w, w.top_acc[player][k]);
         return;
     }
     const UnitDev u = w.units[unit0 + blockIdx.x];
@@ -220,17 +207,18 @@ void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, co
 }
 
 // Top-region reach at one depth, all trees together: one row per thread.
-__global__ __launch_bounds__(BLOCK) void k_reach_rows(WaveDev w, const Task* r0, uint32_t n0, const Task* r1,
-                                                    uint32_t n1, float* reach, const float* strat) {
+__global__ __launch_bounds__(BLOCK) void k_reach_rows(WaveDev w, const ReachRec* r0, uint32_t n0,
+                                                    const ReachRec* r1, uint32_t n1, float* reach,
+                                                    const float* strat) {
     uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
     if (k < n0)
-        reach_task(w, reach, strat, 0, r0[k]);
+        reach_row(w, reach, strat, r0[k]);
     else if (k < n0 + n1)
-        reach_task(w, reach, strat, 1, r1[k - n0]);
+        reach_row(w, reach, strat, r1[k - n0]);
 }
 
-void launch_reach_rows(const WaveDev& w, const Task* r0, uint32_t n0, const Task* r1, uint32_t n1, float* reach,
-                       const float* strat, hipStream_t s) {
+void launch_reach_rows(const WaveDev& w, const ReachRec* r0, uint32_t n0, const ReachRec* r1, uint32_t n1,
+                       float* reach, const float* strat, hipStream_t s) {
     if (n0 + n1)
         hipLaunchKernelGGL(k_reach_rows, dim3(grid_for(n0 + n1)), dim3(BLOCK), 0, s, w, r0, n0, r1, n1, reach, strat);
 }
@@ -240,10 +228,9 @@ __global__ void k_seed_sum(WaveDev w) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= w.ndec[0] + w.ndec[1]) return;
     int p;
-    Task q = decision_task(w, i, &p);
-    uint32_t row = w.legal_row_of[q.node] + q.config;
-    float r = w.reach[w.reach_base[2 * q.node + p] + q.config];
-    for (uint32_t g = w.legal_off[row]; g < w.legal_off[row + 1]; g++) w.sum[g] = r * w.cur[g];
+    AccRec q = decision_row(w, i, &p);
+    float r = w.reach[q.ridx];
+    for (uint32_t g = q.lo; g < q.lo + q.n; g++) w.sum[g] = r * w.cur[g];
 }
 
 void launch_seed_sum(const WaveDev& w, hipStream_t s) {
@@ -408,30 +395,23 @@ void launch_query_static(const WaveDev& w, int precision, void* x0, void* x1, hi
 
 // ------------------------------------------------------------- the sweep
 
-// One backprop task for traverser p (engine/src/search.rs:1672-1803).
+// One value row of traverser p (engine/src/search.rs:1672-1803).
 template <int MODE>
-__device__ __forceinline__ void backprop_task(const WaveDev& w, int p, Task q, float da, float db, float ds,
-                                              float predict, const float* strat) {
-    uint32_t node = q.node, c = q.config;
-    uint32_t meta = w.node_meta[node];
-    uint32_t kind = meta & 3u, actor = meta >> 2;
+__device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q, float da, float db, float ds,
+                                             float predict, const float* strat) {
     float* vals = w.vals;
-    uint32_t vb = w.vals_base[2 * node + p];
-    if (kind == 1) {  // the traverser draws: push values through the outcome row
-        uint32_t child = w.child[w.child_start[node]];
-        uint32_t d0 = w.draw_off[node], rb = w.draw_row_off[node];
-        uint32_t lo = w.draw_row_start[rb + c], hi = w.draw_row_start[rb + c + 1];
-        uint32_t cb = w.vals_base[2 * child + p];
+    const uint32_t kind = q.kn >> 30, n = q.kn & REC_N, lo = q.start;
+    if (kind == BACK_DRAW) {  // the traverser draws: push values through the outcome row
+        const uint32_t cb = q.arg;
         float v = 0.0f;
-        uint32_t n = hi - lo;
         if (n <= ROW_BATCH) {
             uint32_t to[ROW_BATCH];
             float pr[ROW_BATCH], cv[ROW_BATCH];
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
                 if (k < n) {
-                    to[k] = w.draw_to[d0 + lo + k];
-                    pr[k] = w.draw_p[d0 + lo + k];
+                    to[k] = w.draw_to[lo + k];
+                    pr[k] = w.draw_p[lo + k];
                 }
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
@@ -440,23 +420,21 @@ __device__ __forceinline__ void backprop_task(const WaveDev& w, int p, Task q, f
             for (uint32_t k = 0; k < ROW_BATCH; k++)
                 if (k < n) v += pr[k] * cv[k];
         } else {
-            for (uint32_t x = lo; x < hi; x++) v += w.draw_p[d0 + x] * vals[cb + w.draw_to[d0 + x]];
+            for (uint32_t x = lo; x < lo + n; x++) v += w.draw_p[x] * vals[cb + w.draw_to[x]];
         }
-        vals[vb + c] = v;
+        vals[q.out] = v;
         return;
     }
-    if (actor != (uint32_t)p) {  // opponent decision: sum the children in child order
-        uint32_t lo = w.child_start[node], n = w.child_start[node + 1] - lo;
+    if (kind == BACK_OPP) {  // opponent decision: sum the children in child order
+        const uint32_t c = q.arg;
+        const uint32_t* cvb = w.child_vb[p] + lo;
         float v = 0.0f;
         if (n <= ROW_BATCH) {
-            uint32_t ch[ROW_BATCH], cb[ROW_BATCH];
+            uint32_t cb[ROW_BATCH];
             float cv[ROW_BATCH];
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) ch[k] = w.child[lo + k];
-#pragma unroll
-            for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) cb[k] = w.vals_base[2 * ch[k] + p];
+                if (k < n) cb[k] = cvb[k];
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
                 if (k < n) cv[k] = vals[cb[k] + c];
@@ -464,15 +442,12 @@ __device__ __forceinline__ void backprop_task(const WaveDev& w, int p, Task q, f
             for (uint32_t k = 0; k < ROW_BATCH; k++)
                 if (k < n) v += cv[k];
         } else {
-            for (uint32_t x = lo; x < lo + n; x++) v += vals[w.vals_base[2 * w.child[x] + p] + c];
+            for (uint32_t x = 0; x < n; x++) v += vals[cvb[x] + c];
         }
-        vals[vb + c] = v;
+        vals[q.out] = v;
         return;
     }
-    uint32_t row = w.legal_row_of[node] + c;
-    uint32_t lo = w.legal_off[row], hi = w.legal_off[row + 1];
     const float* st = MODE == MODE_VALUE ? strat : w.cur;
-    const uint32_t n = hi - lo;
     if (n <= ROW_BATCH) {
         uint32_t lv[ROW_BATCH];
         float sv[ROW_BATCH], qv[ROW_BATCH], old[ROW_BATCH], sm[ROW_BATCH];
@@ -493,7 +468,7 @@ __device__ __forceinline__ void backprop_task(const WaveDev& w, int p, Task q, f
 #pragma unroll
         for (uint32_t k = 0; k < ROW_BATCH; k++)
             if (k < n && lv[k] != 0xffffffffu) base += qv[k] * sv[k];
-        vals[vb + c] = base;
+        vals[q.out] = base;
         if (MODE == MODE_VALUE) return;
         // Fused regret matching with DCFR discounting (search.rs:1742-1779).
         float total = 0.0f, v[ROW_BATCH];
@@ -515,12 +490,13 @@ __device__ __forceinline__ void backprop_task(const WaveDev& w, int p, Task q, f
             if (k < n) w.cur[lo + k] = total > 0.0f ? v[k] * inv : v[k];
         return;
     }
+    const uint32_t hi = lo + n;
     float base = 0.0f;
     for (uint32_t g = lo; g < hi; g++) {
         uint32_t lv = w.legal_value[g];
         if (lv != 0xffffffffu) base += vals[lv] * st[g];
     }
-    vals[vb + c] = base;
+    vals[q.out] = base;
     if (MODE == MODE_VALUE) return;
     float total = 0.0f;
     for (uint32_t g = lo; g < hi; g++) {
@@ -574,12 +550,12 @@ __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, cons
         for (uint32_t c = 0; c < w.nc[2 * node + p]; c++) out[c] = uu * m;
     }
     __syncthreads();
-    const Task* back = w.back_task[p];
+    const BackRec* back = w.back_rec[p];
     const uint32_t* blvl = w.back_lvl[p];
     for (uint32_t l = u.nlevels; l-- > 0;) {
         uint32_t b = blvl[u.lvl0 + l], e = blvl[u.lvl0 + l + 1];
         for (uint32_t k = b + threadIdx.x; k < e; k += blockDim.x)
-            backprop_task<MODE>(w, p, back[k], da, db, ds, predict, w.snap);
+            backprop_row<MODE>(w, p, back[k], da, db, ds, predict, w.snap);
         __syncthreads();
     }
 }
@@ -597,14 +573,14 @@ void launch_sweep(const WaveDev& w, uint32_t unit0, uint32_t n, const float* hea
 
 // Top-region values at one depth, all trees together: one row per thread.
 template <int MODE>
-__global__ __launch_bounds__(BLOCK) void k_back_rows(WaveDev w, const Task* rows, uint32_t n, int p, float da,
+__global__ __launch_bounds__(BLOCK) void k_back_rows(WaveDev w, const BackRec* rows, uint32_t n, int p, float da,
                                                    float db, float ds, float predict) {
     uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-    if (k < n) backprop_task<MODE>(w, p, rows[k], da, db, ds, predict, w.snap);
+    if (k < n) backprop_row<MODE>(w, p, rows[k], da, db, ds, predict, w.snap);
 }
 
-void launch_back_rows(const WaveDev& w, const Task* rows, uint32_t n, int traverser, int mode, float da, float db,
-                      float ds, float predict, hipStream_t s) {
+void launch_back_rows(const WaveDev& w, const BackRec* rows, uint32_t n, int traverser, int mode, float da,
+                      float db, float ds, float predict, hipStream_t s) {
     if (!n) return;
     if (mode == MODE_VALUE)
         hipLaunchKernelGGL(k_back_rows<MODE_VALUE>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, rows, n, traverser, da,
@@ -621,9 +597,8 @@ __global__ void k_normalize(WaveDev w, int touched0, int touched1) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= w.ndec[0] + w.ndec[1]) return;
     int p;
-    Task q = decision_task(w, i, &p);
-    uint32_t row = w.legal_row_of[q.node] + q.config;
-    uint32_t lo = w.legal_off[row], hi = w.legal_off[row + 1];
+    AccRec q = decision_row(w, i, &p);
+    uint32_t lo = q.lo, hi = q.lo + q.n;
     if (!(p ? touched1 : touched0)) {
         for (uint32_t g = lo; g < hi; g++) w.snap[g] = w.cur[g];
         return;

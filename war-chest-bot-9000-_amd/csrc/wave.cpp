@@ -79,6 +79,67 @@ void append_shift(std::vector<T>& dst, const std::vector<T>& src, size_t skip, T
     }
 }
 
+// Row records from the task lists (see BackRec / ReachRec / AccRec).
+void build_records(WaveHost* wp) {
+    WaveHost& w = *wp;
+    for (int p = 0; p < 2; p++) {
+        std::vector<uint32_t> cvb_at(w.nodes(), NONE);
+        auto back = [&](const Task& q) {
+            const uint32_t node = q.node, c = q.config;
+            const uint32_t kind = w.node_meta[node] & 3u, actor = w.node_meta[node] >> 2;
+            BackRec r{};
+            r.out = w.vals_base[2 * node + p] + c;
+            if (kind == 1) {
+                uint32_t child = w.child[w.child_start[node]];
+                uint32_t d0 = w.draw_off[node], rb = w.draw_row_off[node];
+                uint32_t lo = w.draw_row_start[rb + c], hi = w.draw_row_start[rb + c + 1];
+                r.arg = w.vals_base[2 * child + p];
+                r.start = d0 + lo;
+                r.kn = BACK_DRAW << 30 | (hi - lo);
+            } else if (actor != (uint32_t)p) {
+                if (cvb_at[node] == NONE) {
+                    cvb_at[node] = (uint32_t)w.child_vb[p].size();
+                    for (uint32_t x = w.child_start[node]; x < w.child_start[node + 1]; x++)
+                        w.child_vb[p].push_back(w.vals_base[2 * w.child[x] + p]);
+                }
+                r.arg = c;
+                r.start = cvb_at[node];
+                r.kn = BACK_OPP << 30 | (w.child_start[node + 1] - w.child_start[node]);
+            } else {
+                uint32_t row = w.legal_row_of[node] + c;
+                r.start = w.legal_off[row];
+                r.kn = BACK_OWN << 30 | (w.legal_off[row + 1] - w.legal_off[row]);
+            }
+            return r;
+        };
+        auto reach = [&](const Task& q) {
+            const uint32_t node = q.node, c = q.config;
+            ReachRec r{};
+            r.out = w.reach_base[2 * node + p] + c;
+            r.pbase = w.reach_base[2 * w.parent[node] + p];
+            if (w.rev_row_of[node] != NONE) {
+                uint32_t row = w.rev_row_of[node] + c;
+                r.start = w.rev_start[row];
+                r.kn = REACH_REV << 31 | (w.rev_start[row + 1] - w.rev_start[row]);
+            } else {
+                uint32_t row = w.rvd_row_of[node] + c;
+                r.start = w.rvd_start[row];
+                r.kn = REACH_RVD << 31 | (w.rvd_start[row + 1] - w.rvd_start[row]);
+            }
+            return r;
+        };
+        for (const Task& q : w.back_task[p]) w.back_rec[p].push_back(back(q));
+        for (const Task& q : w.top_back[p]) w.top_back_rec[p].push_back(back(q));
+        for (const Task& q : w.reach_task[p]) w.reach_rec[p].push_back(reach(q));
+        for (const Task& q : w.top_reach[p]) w.top_reach_rec[p].push_back(reach(q));
+        for (const Task& q : w.decision[p]) {
+            uint32_t row = w.legal_row_of[q.node] + q.config;
+            w.acc_rec[p].push_back({w.reach_base[2 * q.node + p] + q.config, w.legal_off[row],
+                                    w.legal_off[row + 1] - w.legal_off[row], 0});
+        }
+    }
+}
+
 }  // namespace
 
 bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_t unit_slots) {
@@ -408,6 +469,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
         w.decision[p].insert(w.decision[p].end(), top_dec[p].begin(), top_dec[p].end());
     }
     w.carry_slots = (w.meta.snapshots && w.meta.snap_iters.size() > 1) ? (uint32_t)w.meta.snap_iters.size() - 1 : 0;
+    build_records(&w);
     w.jobs = std::move(jobs);
     if (!validate_deep(w, err)) return false;
     *out = std::move(w);
@@ -551,6 +613,57 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         if (w.top_dec0[p] > w.decision[p].size()) return fail("top decision rows");
         for (const UnitDev& u : w.units)
             if (u.dec1[p] > w.top_dec0[p]) return fail("unit decision rows overlap the top rows");
+    }
+    // Row records: every slot and element they name.
+    for (int p = 0; p < 2; p++) {
+        auto back_ok = [&](const BackRec& r) {
+            const uint64_t n = r.kn & REC_N, kind = r.kn >> 30;
+            if (r.out >= w.vals_len) return false;
+            if (kind == BACK_OWN) {
+                if (uint64_t(r.start) + n > w.ncells) return false;
+                for (uint64_t g = r.start; g < r.start + n; g++)
+                    if (w.legal_value[g] != NONE && w.legal_value[g] >= w.vals_len) return false;
+            } else if (kind == BACK_DRAW) {
+                if (uint64_t(r.start) + n > w.draw_to.size()) return false;
+                for (uint64_t x = r.start; x < r.start + n; x++)
+                    if (uint64_t(r.arg) + w.draw_to[x] >= w.vals_len) return false;
+            } else if (kind == BACK_OPP) {
+                if (uint64_t(r.start) + n > w.child_vb[p].size()) return false;
+                for (uint64_t x = r.start; x < r.start + n; x++)
+                    if (uint64_t(w.child_vb[p][x]) + r.arg >= w.vals_len) return false;
+            } else {
+                return false;
+            }
+            return true;
+        };
+        auto reach_ok = [&](const ReachRec& r) {
+            const uint64_t n = r.kn & REC_N;
+            if (r.out >= w.reach_len) return false;
+            if ((r.kn >> 31) == REACH_REV) {
+                if (uint64_t(r.start) + n > w.rev_src.size()) return false;
+                for (uint64_t x = r.start; x < r.start + n; x++)
+                    if (uint64_t(r.pbase) + w.rev_src[x] >= w.reach_len || w.rev_cell[x] >= w.ncells) return false;
+            } else {
+                if (uint64_t(r.start) + n > w.rvd_src.size()) return false;
+                for (uint64_t x = r.start; x < r.start + n; x++)
+                    if (uint64_t(r.pbase) + w.rvd_src[x] >= w.reach_len) return false;
+            }
+            return true;
+        };
+        if (w.back_rec[p].size() != w.back_task[p].size() || w.top_back_rec[p].size() != w.top_back[p].size() ||
+            w.reach_rec[p].size() != w.reach_task[p].size() || w.top_reach_rec[p].size() != w.top_reach[p].size() ||
+            w.acc_rec[p].size() != w.decision[p].size())
+            return fail("record counts");
+        for (const BackRec& r : w.back_rec[p])
+            if (!back_ok(r)) return fail("back record");
+        for (const BackRec& r : w.top_back_rec[p])
+            if (!back_ok(r)) return fail("top back record");
+        for (const ReachRec& r : w.reach_rec[p])
+            if (!reach_ok(r)) return fail("reach record");
+        for (const ReachRec& r : w.top_reach_rec[p])
+            if (!reach_ok(r)) return fail("top reach record");
+        for (const AccRec& r : w.acc_rec[p])
+            if (r.ridx >= w.reach_len || uint64_t(r.lo) + r.n > w.ncells) return fail("accumulation record");
     }
     for (const TreeDev& t : w.trees) {
         if (uint64_t(t.node0) + t.nodes > N) return fail("tree range");

@@ -27,6 +27,30 @@ struct Task {
     uint32_t node, config;
 };
 
+// Row records the device sweeps read: everything a row needs is one load away
+// (its output slot, its element range and what the elements index), so a
+// level costs one record read, one element read and one gather.
+enum : uint32_t { BACK_OWN = 0, BACK_DRAW = 1, BACK_OPP = 2 };
+enum : uint32_t { REACH_REV = 0, REACH_RVD = 1 };
+constexpr uint32_t REC_N = 0x3fffffffu;  // element count bits of `kn`
+
+// One value row of the traverser: out = its value slot; kn = kind << 30 | n.
+//   BACK_OWN  cells [start, start + n) of the traverser's decision row (arg unused)
+//   BACK_DRAW draw entries [start, start + n) (wave-global), values at arg + draw_to
+//   BACK_OPP  child value bases child_vb[p][start .. start + n), plus arg = the config
+struct BackRec {
+    uint32_t out, arg, start, kn;
+};
+// One reach row: out = its reach slot; pbase = the parent's reach slot of the
+// same player; kn = kind << 31 | n over rev or rvd entries [start, start + n).
+struct ReachRec {
+    uint32_t out, pbase, start, kn;
+};
+// One decision row: its reach slot and its cells [lo, lo + n).
+struct AccRec {
+    uint32_t ridx, lo, n, pad;
+};
+
 // Per-tree record: root beliefs, carried roots, outputs.
 struct TreeDev {
     uint32_t node0, nodes;        // wave-global node range
@@ -109,6 +133,12 @@ struct WaveHost {
     std::vector<uint8_t> node_top;  // 1 for a node of a top region
 
     uint32_t max_levels = 0, nroots_max = 0, carry_slots = 0;
+
+    // Device row records, index-aligned with the task lists above.
+    std::vector<BackRec> back_rec[2], top_back_rec[2];
+    std::vector<ReachRec> reach_rec[2], top_reach_rec[2];
+    std::vector<AccRec> acc_rec[2];
+    std::vector<uint32_t> child_vb[2];  // child value bases of the opponent rows
 
     uint32_t nodes() const { return (uint32_t)node_meta.size(); }
     uint32_t rows() const { return (uint32_t)row_node.size(); }
