@@ -146,7 +146,7 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
     tb += h.pub_raw.size();
     for (int p = 0; p < 2; p++)
         tb += 16 * (h.back_rec[p].size() + h.reach_rec[p].size() + h.acc_rec[p].size() + h.top_back_rec[p].size() +
-                    h.top_reach_rec[p].size()) +
+                    h.top_reach_rec[p].size() + h.leaf_rec[p].size()) +
               4 * (h.back_lvl[p].size() + h.reach_lvl[p].size() + h.child_vb[p].size());
     tb += sizeof(UnitDev) * h.units.size() + 4 * (h.unit_row.size() + h.unit_term.size());
     s->table_bytes = tb;

@@ -18,6 +18,8 @@ namespace wc {
 #define SMOOTHF 1e-30f   // belief normalisation floor (engine/src/rebel.rs:359)
 
 constexpr int BLOCK = 256;
+// The subtree sweep stages a unit's values in LDS when the widest window fits this.
+constexpr size_t SWEEP_LDS_MAX = 64 * 1024;
 
 static inline unsigned grid_for(size_t n, int block = BLOCK) { return (unsigned)((n + block - 1) / block); }
 
@@ -80,10 +82,10 @@ void launch_seed_reach(const WaveDev& w, float* reach, int root_index, hipStream
     hipLaunchKernelGGL(k_seed_reach, dim3(w.ntrees), dim3(BLOCK), 0, s, w, reach, root_index);
 }
 
-// Rows of up to ROW_BATCH elements are handled with their loads issued as one
-// batch (indices, then the values they name) and the reduction taken after,
-// in element order; longer rows fall back to the element loop.
-constexpr uint32_t ROW_BATCH = 16;
+// Row elements are handled ROW_BATCH at a time: a batch's loads are issued
+// together (indices, then the values they name) and its part of the reduction
+// is taken after, in element order, so every sum keeps the CPU's order.
+constexpr uint32_t ROW_BATCH = 8;
 
 // One child config's reach: the reverse gather in stored order (the CPU's
 // scatter order, engine/src/serialize.rs:714-723).
@@ -91,45 +93,43 @@ __device__ __forceinline__ void reach_row(const WaveDev& w, float* reach, const 
     const uint32_t lo = q.start, n = q.kn & REC_N, base = q.pbase;
     float v = 0.0f;
     if ((q.kn >> 31) == REACH_REV) {
-        if (n <= ROW_BATCH) {
+        for (uint32_t c0 = 0; c0 < n; c0 += ROW_BATCH) {
+            const uint32_t m = n - c0 < ROW_BATCH ? n - c0 : ROW_BATCH;
             uint32_t src[ROW_BATCH], cell[ROW_BATCH];
             float a[ROW_BATCH], b[ROW_BATCH];
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) {
-                    src[k] = w.rev_src[lo + k];
-                    cell[k] = w.rev_cell[lo + k];
+                if (k < m) {
+                    src[k] = w.rev_src[lo + c0 + k];
+                    cell[k] = w.rev_cell[lo + c0 + k];
                 }
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) {
+                if (k < m) {
                     a[k] = reach[base + src[k]];
                     b[k] = strat[cell[k]];
                 }
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) v += a[k] * b[k];
-        } else {
-            for (uint32_t x = lo; x < lo + n; x++) v += reach[base + w.rev_src[x]] * strat[w.rev_cell[x]];
+                if (k < m) v += a[k] * b[k];
         }
     } else {
-        if (n <= ROW_BATCH) {
+        for (uint32_t c0 = 0; c0 < n; c0 += ROW_BATCH) {
+            const uint32_t m = n - c0 < ROW_BATCH ? n - c0 : ROW_BATCH;
             uint32_t src[ROW_BATCH];
             float a[ROW_BATCH], pr[ROW_BATCH];
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) {
-                    src[k] = w.rvd_src[lo + k];
-                    pr[k] = w.rvd_p[lo + k];
+                if (k < m) {
+                    src[k] = w.rvd_src[lo + c0 + k];
+                    pr[k] = w.rvd_p[lo + c0 + k];
                 }
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) a[k] = reach[base + src[k]];
+                if (k < m) a[k] = reach[base + src[k]];
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) v += a[k] * pr[k];
-        } else {
-            for (uint32_t x = lo; x < lo + n; x++) v += reach[base + w.rvd_src[x]] * w.rvd_p[x];
+                if (k < m) v += a[k] * pr[k];
         }
     }
     reach[q.out] = v;
@@ -139,19 +139,18 @@ __device__ __forceinline__ void reach_row(const WaveDev& w, float* reach, const 
 __device__ __forceinline__ void accumulate_row(const WaveDev& w, AccRec q) {
     const float r = w.reach[q.ridx];
     const uint32_t lo = q.lo, n = q.n;
-    if (n <= ROW_BATCH) {
+    for (uint32_t c0 = 0; c0 < n; c0 += ROW_BATCH) {
+        const uint32_t m = n - c0 < ROW_BATCH ? n - c0 : ROW_BATCH;
         float cu[ROW_BATCH], sm[ROW_BATCH];
 #pragma unroll
         for (uint32_t j = 0; j < ROW_BATCH; j++)
-            if (j < n) {
-                cu[j] = w.cur[lo + j];
-                sm[j] = w.sum[lo + j];
+            if (j < m) {
+                cu[j] = w.cur[lo + c0 + j];
+                sm[j] = w.sum[lo + c0 + j];
             }
 #pragma unroll
         for (uint32_t j = 0; j < ROW_BATCH; j++)
-            if (j < n) w.sum[lo + j] = sm[j] + r * cu[j];
-    } else {
-        for (uint32_t g = lo; g < lo + n; g++) w.sum[g] += r * w.cur[g];
+            if (j < m) w.sum[lo + c0 + j] = sm[j] + r * cu[j];
     }
 }
 
@@ -396,65 +395,74 @@ void launch_query_static(const WaveDev& w, int precision, void* x0, void* x1, hi
 // ------------------------------------------------------------- the sweep
 
 // One value row of traverser p (engine/src/search.rs:1672-1803).
-template <int MODE>
+// Values come from the unit's LDS window when LDSV (slot i at lv[i - vw]),
+// else from HBM; results go to both.
+template <int MODE, bool LDSV>
 __device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q, float da, float db, float ds,
-                                             float predict, const float* strat) {
+                                             float predict, const float* strat, float* lv, uint32_t vw) {
     float* vals = w.vals;
+    auto get = [&](uint32_t i) { return LDSV ? lv[i - vw] : vals[i]; };
+    auto put = [&](uint32_t i, float v) {
+        vals[i] = v;
+        if (LDSV) lv[i - vw] = v;
+    };
     const uint32_t kind = q.kn >> 30, n = q.kn & REC_N, lo = q.start;
     if (kind == BACK_DRAW) {  // the traverser draws: push values through the outcome row
         const uint32_t cb = q.arg;
         float v = 0.0f;
-        if (n <= ROW_BATCH) {
+        for (uint32_t c0 = 0; c0 < n; c0 += ROW_BATCH) {
+            const uint32_t m = n - c0 < ROW_BATCH ? n - c0 : ROW_BATCH;
             uint32_t to[ROW_BATCH];
             float pr[ROW_BATCH], cv[ROW_BATCH];
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) {
-                    to[k] = w.draw_to[lo + k];
-                    pr[k] = w.draw_p[lo + k];
+                if (k < m) {
+                    to[k] = w.draw_to[lo + c0 + k];
+                    pr[k] = w.draw_p[lo + c0 + k];
                 }
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) cv[k] = vals[cb + to[k]];
+                if (k < m) cv[k] = get(cb + to[k]);
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) v += pr[k] * cv[k];
-        } else {
-            for (uint32_t x = lo; x < lo + n; x++) v += w.draw_p[x] * vals[cb + w.draw_to[x]];
+                if (k < m) v += pr[k] * cv[k];
         }
-        vals[q.out] = v;
+        put(q.out, v);
         return;
     }
     if (kind == BACK_OPP) {  // opponent decision: sum the children in child order
         const uint32_t c = q.arg;
         const uint32_t* cvb = w.child_vb[p] + lo;
         float v = 0.0f;
-        if (n <= ROW_BATCH) {
+        for (uint32_t c0 = 0; c0 < n; c0 += ROW_BATCH) {
+            const uint32_t m = n - c0 < ROW_BATCH ? n - c0 : ROW_BATCH;
             uint32_t cb[ROW_BATCH];
             float cv[ROW_BATCH];
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) cb[k] = cvb[k];
+                if (k < m) cb[k] = cvb[c0 + k];
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) cv[k] = vals[cb[k] + c];
+                if (k < m) cv[k] = get(cb[k] + c);
 #pragma unroll
             for (uint32_t k = 0; k < ROW_BATCH; k++)
-                if (k < n) v += cv[k];
-        } else {
-            for (uint32_t x = 0; x < n; x++) v += vals[cvb[x] + c];
+                if (k < m) v += cv[k];
         }
-        vals[q.out] = v;
+        put(q.out, v);
         return;
     }
+    // The traverser's own row: base = sum of child value x strategy in action
+    // order, then the fused regret matching with DCFR discounting
+    // (search.rs:1742-1779): r = old (old > 0 ? da : db) + delta, cur = max(r +
+    // predict delta, EPS), normalised by a reciprocal multiply, sum *= ds.
     const float* st = MODE == MODE_VALUE ? strat : w.cur;
-    if (n <= ROW_BATCH) {
-        uint32_t lv[ROW_BATCH];
+    if (n <= ROW_BATCH) {  // one batch: everything stays in registers
+        uint32_t lvi[ROW_BATCH];
         float sv[ROW_BATCH], qv[ROW_BATCH], old[ROW_BATCH], sm[ROW_BATCH];
 #pragma unroll
         for (uint32_t k = 0; k < ROW_BATCH; k++)
             if (k < n) {
-                lv[k] = w.legal_value[lo + k];
+                lvi[k] = w.legal_value[lo + k];
                 sv[k] = st[lo + k];
                 if (MODE == MODE_REGRET) {
                     old[k] = w.regret[lo + k];
@@ -463,20 +471,19 @@ __device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q,
             }
 #pragma unroll
         for (uint32_t k = 0; k < ROW_BATCH; k++)
-            if (k < n) qv[k] = lv[k] != 0xffffffffu ? vals[lv[k]] : 0.0f;
+            if (k < n) qv[k] = lvi[k] != 0xffffffffu ? get(lvi[k]) : 0.0f;
         float base = 0.0f;
 #pragma unroll
         for (uint32_t k = 0; k < ROW_BATCH; k++)
-            if (k < n && lv[k] != 0xffffffffu) base += qv[k] * sv[k];
-        vals[q.out] = base;
+            if (k < n && lvi[k] != 0xffffffffu) base += qv[k] * sv[k];
+        put(q.out, base);
         if (MODE == MODE_VALUE) return;
-        // Fused regret matching with DCFR discounting (search.rs:1742-1779).
         float total = 0.0f, v[ROW_BATCH];
 #pragma unroll
         for (uint32_t k = 0; k < ROW_BATCH; k++)
             if (k < n) {
                 float delta = 0.0f;
-                if (lv[k] != 0xffffffffu) delta += qv[k];
+                if (lvi[k] != 0xffffffffu) delta += qv[k];
                 delta -= base;
                 float r = old[k] * (old[k] > 0.0f ? da : db) + delta;
                 w.regret[lo + k] = r;
@@ -490,31 +497,69 @@ __device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q,
             if (k < n) w.cur[lo + k] = total > 0.0f ? v[k] * inv : v[k];
         return;
     }
-    const uint32_t hi = lo + n;
+    // Longer rows: the same arithmetic in three batched passes (base; update,
+    // with cur holding the unnormalised value; normalisation).
     float base = 0.0f;
-    for (uint32_t g = lo; g < hi; g++) {
-        uint32_t lv = w.legal_value[g];
-        if (lv != 0xffffffffu) base += vals[lv] * st[g];
+    for (uint32_t c0 = 0; c0 < n; c0 += ROW_BATCH) {
+        const uint32_t m = n - c0 < ROW_BATCH ? n - c0 : ROW_BATCH;
+        uint32_t lvi[ROW_BATCH];
+        float sv[ROW_BATCH], qv[ROW_BATCH];
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < m) {
+                lvi[k] = w.legal_value[lo + c0 + k];
+                sv[k] = st[lo + c0 + k];
+            }
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < m) qv[k] = lvi[k] != 0xffffffffu ? get(lvi[k]) : 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < m && lvi[k] != 0xffffffffu) base += qv[k] * sv[k];
     }
-    vals[q.out] = base;
+    put(q.out, base);
     if (MODE == MODE_VALUE) return;
     float total = 0.0f;
-    for (uint32_t g = lo; g < hi; g++) {
-        uint32_t lv = w.legal_value[g];
-        float delta = 0.0f;
-        if (lv != 0xffffffffu) delta += vals[lv];
-        delta -= base;
-        float old = w.regret[g];
-        float r = old * (old > 0.0f ? da : db) + delta;
-        w.regret[g] = r;
-        float v = fmaxf(r + predict * delta, EPSF);
-        w.cur[g] = v;
-        total += v;
-        w.sum[g] *= ds;
+    for (uint32_t c0 = 0; c0 < n; c0 += ROW_BATCH) {
+        const uint32_t m = n - c0 < ROW_BATCH ? n - c0 : ROW_BATCH;
+        uint32_t lvi[ROW_BATCH];
+        float qv[ROW_BATCH], old[ROW_BATCH], sm[ROW_BATCH];
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < m) {
+                lvi[k] = w.legal_value[lo + c0 + k];
+                old[k] = w.regret[lo + c0 + k];
+                sm[k] = w.sum[lo + c0 + k];
+            }
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < m) qv[k] = lvi[k] != 0xffffffffu ? get(lvi[k]) : 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < m) {
+                float delta = 0.0f;
+                if (lvi[k] != 0xffffffffu) delta += qv[k];
+                delta -= base;
+                float r = old[k] * (old[k] > 0.0f ? da : db) + delta;
+                w.regret[lo + c0 + k] = r;
+                float v = fmaxf(r + predict * delta, EPSF);
+                w.cur[lo + c0 + k] = v;
+                total += v;
+                w.sum[lo + c0 + k] = sm[k] * ds;
+            }
     }
     if (total > 0.0f) {
-        float inv = 1.0f / total;
-        for (uint32_t g = lo; g < hi; g++) w.cur[g] *= inv;
+        const float inv = 1.0f / total;
+        for (uint32_t c0 = 0; c0 < n; c0 += ROW_BATCH) {
+            const uint32_t m = n - c0 < ROW_BATCH ? n - c0 : ROW_BATCH;
+            float cu[ROW_BATCH];
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < m) cu[k] = w.cur[lo + c0 + k];
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < m) w.cur[lo + c0 + k] = cu[k] * inv;
+        }
     }
 }
 
@@ -522,22 +567,19 @@ __device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q,
 // p, one workgroup per unit: leaf values first (net value x opponent reach
 // mass, engine/src/search.rs:1587-1636), then levels from the deepest up, with
 // the fused regret/DCFR update at the traverser's rows.
-template <int MODE>
+template <int MODE, bool LDSV>
 __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, const float* head_out, uint32_t heads,
                                                int p, float da, float db, float ds, float predict) {
+    extern __shared__ float lds_vals[];  // the unit's value window of player p (when LDSV)
     const UnitDev u = w.units[unit0 + blockIdx.x];
     const int opp = 1 - p;
-    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t nwaves = blockDim.x >> 6;
-    for (uint32_t k = u.row0 + wave; k < u.row1; k += nwaves) {
-        uint32_t r = w.unit_row[k];
-        uint32_t node = w.row_node[r];
-        uint32_t n = w.nc[2 * node + p];
-        float m = w.mass[2 * r + opp];
-        const uint32_t* cfgs = w.row_cfg + w.row_cfg_off[2 * r + p];
-        float* out = w.vals + w.vals_base[2 * node + p];
-        const float* h = head_out + (size_t)r * heads;
-        for (uint32_t c = lane; c < n; c += 64) out[c] = h[w.cfg_key[cfgs[c]]] * m;
+    const uint32_t vw = u.vwin[p];
+    // Network leaves: one value slot per thread.
+    for (uint32_t k = u.leaf0[p] + threadIdx.x; k < u.leaf1[p]; k += blockDim.x) {
+        const LeafRec q = w.leaf_rec[p][k];
+        const float v = head_out[q.head] * w.mass[q.mass];
+        w.vals[q.out] = v;
+        if (LDSV) lds_vals[q.out - vw] = v;
     }
     for (uint32_t x = u.term0 + threadIdx.x; x < u.term1; x += blockDim.x) {
         uint32_t k = w.unit_term[x];
@@ -546,8 +588,11 @@ __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, cons
         float m = 0.0f;
         for (uint32_t c = 0; c < w.nc[2 * node + opp]; c++) m += ro[c];
         float uu = (w.node_meta[node] >> 2) == (uint32_t)p ? w.term_util[k] : -w.term_util[k];
-        float* out = w.vals + w.vals_base[2 * node + p];
-        for (uint32_t c = 0; c < w.nc[2 * node + p]; c++) out[c] = uu * m;
+        const uint32_t ob = w.vals_base[2 * node + p];
+        for (uint32_t c = 0; c < w.nc[2 * node + p]; c++) {
+            w.vals[ob + c] = uu * m;
+            if (LDSV) lds_vals[ob + c - vw] = uu * m;
+        }
     }
     __syncthreads();
     const BackRec* back = w.back_rec[p];
@@ -555,7 +600,7 @@ __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, cons
     for (uint32_t l = u.nlevels; l-- > 0;) {
         uint32_t b = blvl[u.lvl0 + l], e = blvl[u.lvl0 + l + 1];
         for (uint32_t k = b + threadIdx.x; k < e; k += blockDim.x)
-            backprop_row<MODE>(w, p, back[k], da, db, ds, predict, w.snap);
+            backprop_row<MODE, LDSV>(w, p, back[k], da, db, ds, predict, w.snap, lds_vals, vw);
         __syncthreads();
     }
 }
@@ -563,12 +608,23 @@ __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, cons
 void launch_sweep(const WaveDev& w, uint32_t unit0, uint32_t n, const float* head_out, uint32_t heads, int traverser,
                   int mode, float da, float db, float ds, float predict, hipStream_t s) {
     if (!n) return;
-    if (mode == MODE_VALUE)
-        hipLaunchKernelGGL(k_sweep<MODE_VALUE>, dim3(n), dim3(BLOCK), 0, s, w, unit0, head_out, heads, traverser, da,
-                           db, ds, predict);
-    else
-        hipLaunchKernelGGL(k_sweep<MODE_REGRET>, dim3(n), dim3(BLOCK), 0, s, w, unit0, head_out, heads, traverser,
-                           da, db, ds, predict);
+    const size_t lds = (size_t)w.max_vwin * sizeof(float);
+    const bool staged = lds <= SWEEP_LDS_MAX;
+#define WC_SWEEP(M, L)                                                                                          \
+    hipLaunchKernelGGL((k_sweep<M, L>), dim3(n), dim3(BLOCK), L ? lds : 0, s, w, unit0, head_out, heads, traverser, \
+                       da, db, ds, predict)
+    if (mode == MODE_VALUE) {
+        if (staged)
+            WC_SWEEP(MODE_VALUE, true);
+        else
+            WC_SWEEP(MODE_VALUE, false);
+    } else {
+        if (staged)
+            WC_SWEEP(MODE_REGRET, true);
+        else
+            WC_SWEEP(MODE_REGRET, false);
+    }
+#undef WC_SWEEP
 }
 
 // Top-region values at one depth, all trees together: one row per thread.
@@ -576,7 +632,7 @@ template <int MODE>
 __global__ __launch_bounds__(BLOCK) void k_back_rows(WaveDev w, const BackRec* rows, uint32_t n, int p, float da,
                                                    float db, float ds, float predict) {
     uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-    if (k < n) backprop_row<MODE>(w, p, rows[k], da, db, ds, predict, w.snap);
+    if (k < n) backprop_row<MODE, false>(w, p, rows[k], da, db, ds, predict, w.snap, nullptr, 0);
 }
 
 void launch_back_rows(const WaveDev& w, const BackRec* rows, uint32_t n, int traverser, int mode, float da,

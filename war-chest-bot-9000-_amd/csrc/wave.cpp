@@ -132,6 +132,19 @@ void build_records(WaveHost* wp) {
         for (const Task& q : w.top_back[p]) w.top_back_rec[p].push_back(back(q));
         for (const Task& q : w.reach_task[p]) w.reach_rec[p].push_back(reach(q));
         for (const Task& q : w.top_reach[p]) w.top_reach_rec[p].push_back(reach(q));
+        // Network-leaf slots, unit by unit (the value sweep writes them first).
+        const uint32_t heads = w.net.heads;
+        for (UnitDev& u : w.units) {
+            u.leaf0[p] = (uint32_t)w.leaf_rec[p].size();
+            for (uint32_t k = u.row0; k < u.row1; k++) {
+                const uint32_t r = w.unit_row[k], node = w.row_node[r];
+                const uint32_t* cfgs = &w.row_cfg[w.row_cfg_off[2 * r + p]];
+                for (uint32_t c = 0; c < w.nc(node, p); c++)
+                    w.leaf_rec[p].push_back({w.vals_base[2 * node + p] + c, r * heads + w.cfg_key[cfgs[c]],
+                                             2 * r + (1 - p), 0});
+            }
+            u.leaf1[p] = (uint32_t)w.leaf_rec[p].size();
+        }
         for (const Task& q : w.decision[p]) {
             uint32_t row = w.legal_row_of[q.node] + q.config;
             w.acc_rec[p].push_back({w.reach_base[2 * q.node + p] + q.config, w.legal_off[row],
@@ -355,6 +368,19 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             uint64_t slots = 0;
             for (uint32_t i : nodes) slots += std::max(t.nc(i, 0), t.nc(i, 1));
             u.slots = (uint32_t)std::min<uint64_t>(slots, 0xffffffffu);
+            // Value window of each player: the unit owns a contiguous run of slots.
+            for (int p = 0; p < 2; p++) {
+                uint32_t lo = NONE, hi = 0;
+                for (uint32_t i : nodes) {
+                    if (t.nc(i, p) == 0) continue;
+                    uint32_t b = w.vals_base[2 * (node0 + i) + p];
+                    lo = std::min(lo, b);
+                    hi = std::max(hi, b + t.nc(i, p));
+                }
+                u.vwin[p] = lo == NONE ? 0 : lo;
+                u.vwin_n[p] = lo == NONE ? 0 : hi - lo;
+                w.max_vwin = std::max(w.max_vwin, u.vwin_n[p]);
+            }
             for (int p = 0; p < 2; p++) {
                 for (uint32_t l = 0; l < L; l++) {
                     w.back_lvl[p].push_back((uint32_t)w.back_task[p].size());
@@ -469,6 +495,10 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
         w.decision[p].insert(w.decision[p].end(), top_dec[p].begin(), top_dec[p].end());
     }
     w.carry_slots = (w.meta.snapshots && w.meta.snap_iters.size() > 1) ? (uint32_t)w.meta.snap_iters.size() - 1 : 0;
+    if (uint64_t(w.rows()) * w.net.heads >= (1ull << 32)) {
+        *err = "wave too large: network rows x heads exceeds 2^32";
+        return false;
+    }
     build_records(&w);
     w.jobs = std::move(jobs);
     if (!validate_deep(w, err)) return false;
@@ -665,6 +695,43 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         for (const AccRec& r : w.acc_rec[p])
             if (r.ridx >= w.reach_len || uint64_t(r.lo) + r.n > w.ncells) return fail("accumulation record");
     }
+    for (int p = 0; p < 2; p++)
+        for (const LeafRec& r : w.leaf_rec[p])
+            if (r.out >= w.vals_len || uint64_t(r.head) >= uint64_t(rows) * w.net.heads || r.mass >= 2 * rows)
+                return fail("leaf record");
+    // The subtree sweep keeps each unit's values in LDS: every slot a unit
+    // writes (its leaves, its rows) and reads (its rows' children) must lie
+    // inside the unit's window.
+    for (const UnitDev& u : w.units)
+        for (int p = 0; p < 2; p++) {
+            const uint64_t lo = u.vwin[p], hi = lo + u.vwin_n[p];
+            auto in = [&](uint64_t i) { return i >= lo && i < hi; };
+            if (u.leaf0[p] > u.leaf1[p] || u.leaf1[p] > w.leaf_rec[p].size()) return fail("unit leaf range");
+            for (uint32_t k = u.leaf0[p]; k < u.leaf1[p]; k++)
+                if (!in(w.leaf_rec[p][k].out)) return fail("unit leaf outside its value window");
+            for (uint32_t k = u.term0; k < u.term1; k++) {
+                uint32_t node = w.term_node[w.unit_term[k]];
+                if (w.nc(node, p) && (!in(w.vals_base[2 * node + p]) || !in(w.vals_base[2 * node + p] + w.nc(node, p) - 1)))
+                    return fail("unit terminal outside its value window");
+            }
+            for (uint32_t x = w.back_lvl[p][u.lvl0]; x < w.back_lvl[p][u.lvl0 + u.nlevels]; x++) {
+                const BackRec& r = w.back_rec[p][x];
+                const uint32_t n = r.kn & REC_N, kind = r.kn >> 30;
+                if (!in(r.out)) return fail("unit row outside its value window");
+                for (uint32_t k = 0; k < n; k++) {
+                    uint64_t i;
+                    if (kind == BACK_OWN) {
+                        if (w.legal_value[r.start + k] == NONE) continue;
+                        i = w.legal_value[r.start + k];
+                    } else if (kind == BACK_DRAW) {
+                        i = uint64_t(r.arg) + w.draw_to[r.start + k];
+                    } else {
+                        i = uint64_t(w.child_vb[p][r.start + k]) + r.arg;
+                    }
+                    if (!in(i)) return fail("unit row reads outside its value window");
+                }
+            }
+        }
     for (const TreeDev& t : w.trees) {
         if (uint64_t(t.node0) + t.nodes > N) return fail("tree range");
         if (uint64_t(t.reach0) + t.reach_len > w.reach_len) return fail("reach range");

@@ -72,12 +72,19 @@ struct UnitDev {
     uint32_t term0, term1;      // terminal leaves: unit_term[term0 .. term1)
     uint32_t slots;             // value slots (max over players, before aliasing)
     uint32_t tree;              // owning tree
-    uint32_t pad[4];
+    uint32_t vwin[2], vwin_n[2];  // the unit's value slots of each player: [vwin, vwin + vwin_n)
+    uint32_t leaf0[2], leaf1[2];  // network-leaf value slots of each player: leaf_rec[p][leaf0 .. leaf1)
 };
-static_assert(sizeof(UnitDev) == 16 * 4, "UnitDev is 64 bytes");
+static_assert(sizeof(UnitDev) == 20 * 4, "UnitDev is 80 bytes");
+
+// One network-leaf value slot of the traverser: vals[out] = head_out[head] * mass[mass]
+// (the net's value of the slot's config times the opponent's reach mass).
+struct LeafRec {
+    uint32_t out, head, mass, pad;
+};
 
 // Default unit budget in value slots (floats of one player's value vector).
-constexpr uint32_t UNIT_SLOTS = 8192;
+constexpr uint32_t UNIT_SLOTS = 4096;
 
 struct WaveHost {
     Meta meta;
@@ -133,11 +140,13 @@ struct WaveHost {
     std::vector<uint8_t> node_top;  // 1 for a node of a top region
 
     uint32_t max_levels = 0, nroots_max = 0, carry_slots = 0;
+    uint32_t max_vwin = 0;  // the widest unit value window (floats): the sweep's LDS size
 
     // Device row records, index-aligned with the task lists above.
     std::vector<BackRec> back_rec[2], top_back_rec[2];
     std::vector<ReachRec> reach_rec[2], top_reach_rec[2];
     std::vector<AccRec> acc_rec[2];
+    std::vector<LeafRec> leaf_rec[2];  // unit-major network-leaf slots
     std::vector<uint32_t> child_vb[2];  // child value bases of the opponent rows
 
     uint32_t nodes() const { return (uint32_t)node_meta.size(); }
