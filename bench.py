@@ -52,6 +52,8 @@ def main():
     ap.add_argument("--cpu-trees", type=int, default=0, help="trees in the CPU-baseline sample (0 = 2 per thread)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-mlp", action="store_true", help="skip the GEMM-chain-alone leg")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="after the run, copy MIB MiB device to device 3 times (calibrates HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the wave executor shards whole trees across devices with no exchange, "
@@ -169,6 +171,22 @@ def main():
         log(f"[bench] CPU oracle: {sec:.1f}s, {ni / sec:.0f} node-iters/s")
 
     ex.close()
+    if args.copy_probe:
+        # A plain device-to-device copy through the HIP runtime's blit kernel:
+        # the reference point that scales the HBM byte counters.
+        import ctypes
+
+        hip = ctypes.CDLL("libamdhip64.so")
+        n = args.copy_probe << 20
+        src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+        assert hip.hipMalloc(ctypes.byref(src), ctypes.c_size_t(n)) == 0
+        assert hip.hipMalloc(ctypes.byref(dst), ctypes.c_size_t(n)) == 0
+        for _ in range(3):
+            assert hip.hipMemcpy(dst, src, ctypes.c_size_t(n), 3) == 0  # hipMemcpyDeviceToDevice
+        assert hip.hipDeviceSynchronize() == 0
+        hip.hipFree(src)
+        hip.hipFree(dst)
+        log(f"[bench] copy probe: 3 x {n} bytes read and written")
     print(json.dumps(out), flush=True)
 
 

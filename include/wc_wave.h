@@ -122,6 +122,7 @@ typedef struct wc_wave_stats {
     uint32_t jobs, nodes, decision_nodes, chance_nodes, leaves, rows, terminals;
     uint32_t levels, iters, nroots_max, carry_slots;
     uint32_t units, top_levels;    /* subtree units, and the depths of the top regions swept per launch */
+    uint32_t max_window;           /* value slots of the widest unit window (the sweep stages it in LDS) */
     uint64_t cells, reach_slots, reach_len, vals_len, rev_nnz, rvd_nnz, draw_nnz, snapshot_configs;
     uint64_t table_bytes, arena_bytes;
     uint64_t cfr_bytes_per_iter[2]; /* algorithmic HBM bytes of one CFR iteration, traverser 0 / 1 */

@@ -65,6 +65,17 @@ def test_wave_counts_add_up():
     assert st["cfr_bytes_per_iter"][0] == sum(p["cfr_bytes_per_iter"][0] for p in parts)
 
 
+@pytest.mark.parametrize("budget", [256, 1024, None])
+def test_unit_windows_fit_the_budget(budget, monkeypatch):
+    # A unit is a run of sibling subtrees; its value slots form one window no
+    # wider than the slot budget, so the sweep can stage every unit in LDS.
+    if budget is not None:
+        monkeypatch.setenv("WC_UNIT_SLOTS", str(budget))
+    st = ww.Wave(W.jobs("wave256", trees=12)).stats()
+    assert st["units"] > 12 and st["top_levels"] > 0
+    assert 0 < st["max_window"] <= (budget or 4096)
+
+
 def test_synthesis_is_seeded_and_prefix_stable():
     a = W.jobs("wave64", trees=4)
     b = W.jobs("wave64", trees=6)

@@ -176,6 +176,27 @@ def test_mlp_bf16_matches_reduced_precision_oracle():
     np.testing.assert_allclose(got, emu, rtol=1e-2, atol=1e-2 * scale)
 
 
+@pytest.mark.parametrize("inputs,hidden,layers,heads,rows", [
+    (512, 384, 3, 567, 1000),  # the wave net: two head passes, a partial last row tile
+    (256, 128, 2, 40, 300),    # a narrow trunk: one 16-feature block per wavefront
+    (512, 96, 2, 70, 260),     # fewer feature blocks than wavefronts
+    (640, 416, 2, 70, 260),    # wider than the fused kernel takes: the layer-by-layer GEMMs
+])
+def test_mlp_f16_shapes(inputs, hidden, layers, heads, rows):
+    dims = ww.mlp_dims(inputs=inputs, hidden=hidden, layers=layers, heads=heads, pool=64)
+    net = ww.synth_weights(dims, seed=3)
+    x = ww.synth_features(rows, inputs, seed=11)
+    say(f"case mlp f16 shape: {rows} queries, {inputs} -> {layers}x{hidden} -> {heads}")
+    ex = executor(ww.WC_F16)
+    v = ex.publish(net)
+    got = ex.mlp(v, x, heads=heads)
+    keys = np.tile(np.arange(heads, dtype=np.uint32), (rows, 1))
+    emu = O.mlp(x, keys, net, O.NET_F16)
+    scale = np.abs(emu).max()
+    assert scale > 0
+    np.testing.assert_allclose(got, emu, rtol=2e-3, atol=2e-3 * scale)
+
+
 def test_mlp_float32_bit_exact():
     net = W.net_for("mlp65k")
     x = W.mlp65k_inputs(rows=256, seed=5)

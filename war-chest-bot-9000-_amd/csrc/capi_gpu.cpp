@@ -125,6 +125,7 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
     s->levels = h.max_levels;
     s->units = (uint32_t)h.units.size();
     s->top_levels = h.top_levels;
+    s->max_window = h.max_vwin;
     s->iters = h.meta.iters;
     s->nroots_max = h.nroots_max;
     s->carry_slots = h.carry_slots;

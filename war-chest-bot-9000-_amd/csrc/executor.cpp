@@ -412,6 +412,22 @@ void Executor::run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::v
             marks->push_back(e);
         }
     };
+    if (precision_ != WC_PRECISE && chain_fits(ns.in, ns.hidden, ns.layers)) {
+        ChainNet net{};
+        for (uint32_t l = 0; l < ns.layers; l++) {
+            net.w[l] = (const uint16_t*)bank.W[l];
+            net.b[l] = bank.B[l];
+        }
+        net.w[ns.layers] = (const uint16_t*)bank.Whead;
+        net.b[ns.layers] = bank.bhead;
+        net.in = ns.in;
+        net.hidden = ns.hidden;
+        net.layers = ns.layers;
+        net.heads = ns.heads;
+        launch_chain(precision_, net, x, rows, head_out_, head_tile_n, stream_);
+        mark();
+        return;
+    }
     const void* in = x;
     uint32_t k = ns.in;
     for (uint32_t l = 0; l < ns.layers; l++) {

@@ -104,6 +104,23 @@ void launch_head_exact(const float* H, uint32_t hidden, const float* Wh, const f
 // 128-row tile) bounds the columns each row tile needs; the rest are not computed.
 void launch_gemm16(int precision, const void* X, uint32_t K, const void* Wt, const float* b, uint32_t N,
                    void* Y, uint32_t M, bool relu, bool out16, hipStream_t s, const uint32_t* tile_n = nullptr);
+// Whole-network MLP in one launch (16-bit operands, f32 accumulate): one
+// 128-row tile per workgroup with the activations resident in LDS; writes
+// out[r, k] (row-major f32, `heads` columns) for r < rows and the columns
+// tile_n allows (all heads when tile_n is null). X is the fragment-major input
+// with gemm_rows(rows) rows; w/b hold the trunk layers and then the head, as
+// launch_gemm16 takes them. Applies when chain_fits(in, hidden, layers).
+constexpr uint32_t CHAIN_MAX_LAYERS = 8, CHAIN_MAX_WIDTH = 512;
+// Eight wavefronts per tile, each owning up to CHAIN_NB 16-feature blocks of a layer.
+constexpr uint32_t CHAIN_WAVES = 8, CHAIN_NB = 3;
+struct ChainNet {
+    const uint16_t* w[CHAIN_MAX_LAYERS + 1];
+    const float* b[CHAIN_MAX_LAYERS + 1];
+    uint32_t in, hidden, layers, heads;
+};
+bool chain_fits(uint32_t in, uint32_t hidden, uint32_t layers);
+void launch_chain(int precision, const ChainNet& net, const void* X, uint32_t rows, float* out,
+                  const uint32_t* tile_n, hipStream_t s);
 // Convert f32 -> a 16-bit fragment-major operand of `rows` rows and K columns;
 // element (r, k) is src[k * rows + r] when `transposed`, else src[r * K + k].
 void launch_to16(int precision, const float* src, void* dst, uint32_t rows, uint32_t K, bool transposed,

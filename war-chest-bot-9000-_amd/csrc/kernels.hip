@@ -898,4 +898,190 @@ void launch_gemm16(int precision, const void* X, uint32_t K, const void* Wt, con
 #undef WC_GEMM
 }
 
+
+// ------------------------------------------------------- fused leaf network
+//
+// One launch runs the whole MLP over a 128-row tile per workgroup: the tile's
+// input operand is staged into LDS once, every trunk layer reads its input
+// from LDS and writes its bias + ReLU output back over it (fragment-major,
+// 16-bit: the next layer's operand), and the head writes row-major f32. Only
+// the tile's input, the weights (shared by every tile, L2-resident) and the
+// head outputs touch HBM.
+//
+// Products are computed transposed, D = W X^T: the weight fragment is the
+// MFMA's A operand and the activation fragment its B operand, so lane l holds
+// four consecutive output features 4 (l / 16) .. + 3 of one row l % 16 --
+// one 8-byte LDS store per 16x16 tile in the next layer's fragment layout.
+// Every output is the same f32 sum over the same 32-wide k steps, in the same
+// order, as the layer-by-layer k_gemm.
+
+constexpr uint32_t CHAIN_LDS_HALVES = GEMM_ROWS * CHAIN_MAX_WIDTH;
+
+bool chain_fits(uint32_t in, uint32_t hidden, uint32_t layers) {
+    return in % 32 == 0 && in <= CHAIN_MAX_WIDTH && hidden % 32 == 0 &&
+           hidden <= CHAIN_WAVES * CHAIN_NB * 16 && layers >= 1 && layers <= CHAIN_MAX_LAYERS;
+}
+
+template <int PREC>
+__device__ __forceinline__ float4v mfma16(const uint4& a, const uint4& b, const float4v& c) {
+    if (PREC == WC_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c,
+                                                      0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+}
+
+// acc[a][b] (b < NB) = sum over ks steps of W(block b) X(rows 16a..)^T. xs: the
+// LDS operand at this lane's fragment slot (fragment (a, s) at xs + (a ks + s)
+// 512); wp: the wavefront's first weight block at this lane's slot (block b at
+// wp + b wstride). Two fragment sets ping-pong so one step's loads overlap the
+// previous step's MFMAs.
+template <int PREC, int NB>
+__device__ __forceinline__ void chain_kloop(float4v (&acc)[8][CHAIN_NB], const uint16_t* xs, uint32_t ks,
+                                            const uint16_t* __restrict__ wp, size_t wstride) {
+#pragma unroll
+    for (int a = 0; a < 8; a++)
+#pragma unroll
+        for (int b = 0; b < NB; b++) acc[a][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    uint4 x0[8], w0[NB], x1[8], w1[NB];
+    auto load = [&](uint4 (&fx)[8], uint4 (&fw)[NB], uint32_t s) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) fw[b] = *(const uint4*)(wp + b * wstride + (size_t)s * 512);
+#pragma unroll
+        for (int a = 0; a < 8; a++) fx[a] = *(const uint4*)(xs + ((size_t)a * ks + s) * 512);
+    };
+    auto step = [&](const uint4 (&fx)[8], const uint4 (&fw)[NB]) {
+#pragma unroll
+        for (int a = 0; a < 8; a++)
+#pragma unroll
+            for (int b = 0; b < NB; b++) acc[a][b] = mfma16<PREC>(fw[b], fx[a], acc[a][b]);
+    };
+    load(x0, w0, 0);
+    uint32_t s = 0;
+    for (; s + 2 <= ks; s += 2) {
+        load(x1, w1, s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        step(x0, w0);
+        __builtin_amdgcn_sched_barrier(0);
+        load(x0, w0, s + 2 < ks ? s + 2 : s + 1);  // past the end: re-read a valid step, unused
+        __builtin_amdgcn_sched_barrier(0);
+        step(x1, w1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (s < ks) step(x0, w0);  // odd step count: x0/w0 hold the last step
+}
+
+// The wavefront's share of one layer: 16-feature blocks blk0, blk0 + CHAIN_WAVES,
+// ... (nb of them, 0..CHAIN_NB) of all 128 rows.
+template <int PREC>
+__device__ __forceinline__ void chain_blocks(float4v (&acc)[8][CHAIN_NB], uint32_t nb, const uint16_t* lds,
+                                             uint32_t ks, const uint16_t* __restrict__ W, uint32_t blk0,
+                                             uint32_t lane) {
+    const uint16_t* xs = lds + lane * 8;
+    const uint16_t* wp = W + ((size_t)blk0 * ks * 64 + lane) * 8;
+    const size_t wstride = (size_t)CHAIN_WAVES * ks * 512;
+    static_assert(CHAIN_NB == 3, "dispatch below covers 1..3 blocks");
+    if (nb == 1)
+        chain_kloop<PREC, 1>(acc, xs, ks, wp, wstride);
+    else if (nb == 2)
+        chain_kloop<PREC, 2>(acc, xs, ks, wp, wstride);
+    else if (nb == 3)
+        chain_kloop<PREC, 3>(acc, xs, ks, wp, wstride);
+}
+
+__device__ __forceinline__ uint32_t pack16(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
+
+template <int PREC>
+__global__ __launch_bounds__(CHAIN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_chain(
+    ChainNet net, const uint16_t* __restrict__ X, uint32_t rows, float* __restrict__ out,
+    const uint32_t* __restrict__ tile_n) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[CHAIN_LDS_HALVES];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tile = blockIdx.x;
+    const uint32_t q = lane >> 4, r = lane & 15;
+    {  // the tile's input operand is one contiguous run of 128 x in halves
+        const uint4* src = (const uint4*)(X + (size_t)tile * GEMM_ROWS * net.in);
+        uint4* dst = (uint4*)lds;
+        const uint32_t n = GEMM_ROWS * net.in / 8;
+#pragma unroll 4
+        for (uint32_t i = threadIdx.x; i < n; i += CHAIN_WAVES * 64) dst[i] = src[i];
+    }
+    __syncthreads();
+    float4v acc[8][CHAIN_NB];
+    const uint32_t hblk = net.hidden >> 4, ksn = net.hidden >> 5;
+    const uint32_t nb = hblk > wave ? (hblk - wave + CHAIN_WAVES - 1) / CHAIN_WAVES : 0;
+    uint32_t K = net.in;
+    for (uint32_t l = 0; l < net.layers; l++) {
+        chain_blocks<PREC>(acc, nb, lds, K >> 5, net.w[l], wave, lane);
+        __syncthreads();  // the layer input is dead from here on
+        // bias + ReLU, stored over the input as the next operand (K = hidden)
+        const float* bias = net.b[l];
+#pragma unroll
+        for (int b = 0; b < CHAIN_NB; b++) {
+            if ((uint32_t)b >= nb) break;
+            const uint32_t n = (wave + CHAIN_WAVES * b) * 16 + 4 * q;
+            const float b0 = bias[n], b1 = bias[n + 1], b2 = bias[n + 2], b3 = bias[n + 3];
+            const size_t col = (size_t)(n >> 5) * 64 + r + ((n & 31) >> 3) * 16;
+#pragma unroll
+            for (int a = 0; a < 8; a++) {
+                float y0 = acc[a][b][0] + b0, y1 = acc[a][b][1] + b1, y2 = acc[a][b][2] + b2,
+                      y3 = acc[a][b][3] + b3;
+                y0 = y0 > 0.0f ? y0 : 0.0f;
+                y1 = y1 > 0.0f ? y1 : 0.0f;
+                y2 = y2 > 0.0f ? y2 : 0.0f;
+                y3 = y3 > 0.0f ? y3 : 0.0f;
+                uint2 v;
+                if (PREC == WC_F16) {
+                    v.x = pack16(f32_to_f16_rn(y0), f32_to_f16_rn(y1));
+                    v.y = pack16(f32_to_f16_rn(y2), f32_to_f16_rn(y3));
+                } else {
+                    v.x = pack16(f32_to_bf16_rn(y0), f32_to_bf16_rn(y1));
+                    v.y = pack16(f32_to_bf16_rn(y2), f32_to_bf16_rn(y3));
+                }
+                *(uint2*)(lds + (((size_t)a * ksn * 64 + col) * 8 + (n & 7))) = v;
+            }
+        }
+        __syncthreads();
+        K = net.hidden;
+    }
+    // Head: the tile's 16-column blocks go round-robin to the wavefronts,
+    // CHAIN_WAVES * CHAIN_NB per pass; row-major f32 out.
+    const uint32_t cols = tile_n ? min(tile_n[tile], net.heads) : net.heads;
+    const uint32_t nt = (cols + 15) >> 4, row0 = tile * GEMM_ROWS;
+    const uint16_t* wh = net.w[net.layers];
+    const float* bh = net.b[net.layers];
+    for (uint32_t c0 = 0; c0 < nt; c0 += CHAIN_WAVES * CHAIN_NB) {
+        const uint32_t end = min(nt, c0 + CHAIN_WAVES * CHAIN_NB);
+        const uint32_t hb = end > c0 + wave ? (end - c0 - wave + CHAIN_WAVES - 1) / CHAIN_WAVES : 0;
+        chain_blocks<PREC>(acc, hb, lds, ksn, wh, c0 + wave, lane);
+#pragma unroll
+        for (int b = 0; b < CHAIN_NB; b++) {
+            if ((uint32_t)b >= hb) break;
+            const uint32_t n = (c0 + wave + CHAIN_WAVES * b) * 16 + 4 * q;
+            float bv[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) bv[v] = n + v < net.heads ? bh[n + v] : 0.0f;
+#pragma unroll
+            for (int a = 0; a < 8; a++) {
+                const uint32_t m = row0 + a * 16 + r;
+                if (m >= rows) continue;
+                float* o = out + (size_t)m * net.heads + n;
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    if (n + v < net.heads) o[v] = acc[a][b][v] + bv[v];
+            }
+        }
+    }
+}
+
+void launch_chain(int precision, const ChainNet& net, const void* X, uint32_t rows, float* out,
+                  const uint32_t* tile_n, hipStream_t s) {
+    if (rows == 0) return;
+    dim3 grid(gemm_rows(rows) / GEMM_ROWS), block(CHAIN_WAVES * 64);
+    if (precision == WC_F16)
+        hipLaunchKernelGGL(k_chain<WC_F16>, grid, block, 0, s, net, (const uint16_t*)X, rows, out, tile_n);
+    else
+        hipLaunchKernelGGL(k_chain<WC_BF16>, grid, block, 0, s, net, (const uint16_t*)X, rows, out, tile_n);
+}
+
 }  // namespace wc

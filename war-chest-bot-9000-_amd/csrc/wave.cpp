@@ -426,17 +426,20 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             for (uint32_t i : pre)
                 if (sub[i] > unit_slots) top.push_back(i);
             // Runs of fitting sibling subtrees below each top node, in child order.
+            // A top child ends the run: its subtree's value slots lie between
+            // its siblings', and a unit's window must stay contiguous.
             for (uint32_t i : top) {
                 std::vector<uint32_t> run;
                 uint64_t run_slots = 0;
                 for (uint32_t k = t.node_child_start[i]; k < t.node_child_start[i + 1]; k++) {
                     uint32_t c = t.node_child[k];
-                    if (sub[c] > unit_slots) continue;
-                    if (!run.empty() && run_slots + sub[c] > unit_slots) {
+                    const bool fits = sub[c] <= unit_slots;
+                    if (!run.empty() && (!fits || run_slots + sub[c] > unit_slots)) {
                         emit(run, depth[i] + 1);
                         run.clear();
                         run_slots = 0;
                     }
+                    if (!fits) continue;
                     subtree(c, &run);
                     run_slots += sub[c];
                 }

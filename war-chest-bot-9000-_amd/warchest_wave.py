@@ -81,7 +81,7 @@ class SynthSpecC(C.Structure):
 class WaveStats(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in (
         "jobs", "nodes", "decision_nodes", "chance_nodes", "leaves", "rows", "terminals",
-        "levels", "iters", "nroots_max", "carry_slots", "units", "top_levels")] + [(n, C.c_uint64) for n in (
+        "levels", "iters", "nroots_max", "carry_slots", "units", "top_levels", "max_window")] + [(n, C.c_uint64) for n in (
         "cells", "reach_slots", "reach_len", "vals_len", "rev_nnz", "rvd_nnz", "draw_nnz",
         "snapshot_configs", "table_bytes", "arena_bytes")] + [
         ("cfr_bytes_per_iter", C.c_uint64 * 2), ("cfr_bytes_by_kernel", (C.c_uint64 * 3) * 2),
