@@ -220,7 +220,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
             draw_row_start, draw_to, draw_p, reach_base, vals_base, parent, rev_row_of, rev_start, rev_src, rev_cell,
             rvd_row_of, rvd_start, rvd_src, rvd_p, row_node, row_cfg_off, row_cfg, cfg_key, cfg_emb, pub_raw,
             term_node, term_util, roots, carried, exit_node, exit_coff, trees, units, bt[2], rt[2], dc[2], bl[2],
-            rl[2], cv[2], lr[2], unit_row, unit_term, tb[2], tr[2], head_tile_n;
+            rl[2], cv[2], lr[2], pg[2], unit_row, unit_term, tb[2], tr[2], head_tile_n;
     } o;
     o.node_meta = blob.put(w.node_meta);
     o.nc = blob.put(w.node_nc);
@@ -265,6 +265,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         o.dc[p] = blob.put(w.acc_rec[p]);
         o.cv[p] = blob.put(w.child_vb[p]);
         o.lr[p] = blob.put(w.leaf_rec[p]);
+        o.pg[p] = blob.put(w.pool_grp[p]);
         o.bl[p] = blob.put(w.back_lvl[p]);
         o.rl[p] = blob.put(w.reach_lvl[p]);
     }
@@ -354,6 +355,8 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         d.acc_rec[p] = (const AccRec*)(T + o.dc[p]);
         d.child_vb[p] = (const uint32_t*)(T + o.cv[p]);
         d.leaf_rec[p] = (const LeafRec*)(T + o.lr[p]);
+        d.pool_grp[p] = (const PoolGroup*)(T + o.pg[p]);
+        d.npool[p] = (uint32_t)w.pool_grp[p].size();
         d.back_lvl[p] = (const uint32_t*)(T + o.bl[p]);
         d.reach_lvl[p] = (const uint32_t*)(T + o.rl[p]);
         d.ndec[p] = (uint32_t)w.decision[p].size();

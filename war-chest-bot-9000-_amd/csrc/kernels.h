@@ -46,6 +46,7 @@ struct WaveDev {
     const ReachRec* reach_rec[2];
     const AccRec* acc_rec[2];  // every decision row; the top regions' rows close each list
     const LeafRec* leaf_rec[2];
+    const PoolGroup* pool_grp[2];
     const uint32_t* child_vb[2];
     const uint32_t *back_lvl[2], *reach_lvl[2];
     const uint32_t *unit_row, *unit_term;
@@ -59,6 +60,7 @@ struct WaveDev {
     uint32_t ntrees, nunits, nsub, rows, pool, in, row_bytes, snapshot_configs, nexit, ncells;
     uint32_t max_vwin;  // widest unit value window (floats)
     uint32_t ndec[2], ntop_dec[2];
+    uint32_t npool[2];  // pool groups of each player
 };
 
 // Launchers (kernels.hip). All take the executor's stream.

@@ -14,6 +14,11 @@
 
 namespace wc {
 
+// MFMA operand and accumulator vectors.
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
 #define EPSF 1e-6f       // regret-matching floor (engine/src/search.rs:1658)
 #define SMOOTHF 1e-30f   // belief normalisation floor (engine/src/rebel.rs:359)
 
@@ -274,16 +279,15 @@ __device__ __forceinline__ uint32_t lane_value(uint32_t v, uint32_t j) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)j);
 }
 
-// One wavefront per (network row, player): the leaf's reach mass, and the
-// pooled belief sum_c beta(c) e(c) with beta the normalised reach
-// (normalize_weights, engine/src/rebel.rs:1054-1068; accumulate,
+// Float32 net: one wavefront per (network row, player). The leaf's reach
+// mass, and the pooled belief sum_c beta(c) e(c) with beta the normalised
+// reach (normalize_weights, engine/src/rebel.rs:1054-1068; accumulate,
 // net.rs:161-170). Lanes load 64 configs at a time; both reductions then run
 // in config order with every lane holding the running value, so the result is
 // the CPU's sequential sum. The pooled block goes straight into the two query
 // inputs that carry it: [pooled_q | pooled_{1-q} | seat | public] for
 // traverser q.
-template <int PREC>
-__global__ __launch_bounds__(BLOCK) void k_pool(WaveDev w, int player, void* x0, void* x1) {
+__global__ __launch_bounds__(BLOCK) void k_pool_exact(WaveDev w, int player, float* x0, float* x1) {
     const uint32_t task = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const uint32_t lane = threadIdx.x & 63;
     uint32_t row, p;
@@ -315,8 +319,8 @@ __global__ __launch_bounds__(BLOCK) void k_pool(WaveDev w, int player, void* x0,
     }
     if (lane == 0) w.mass[2 * row + p] = tot;
     const uint32_t pool = w.pool, in = w.in;
-    void* own = p ? x1 : x0;    // pooled_p is the first block of traverser p's query
-    void* other = p ? x0 : x1;  // and the second block of the other traverser's
+    float* own = p ? x1 : x0;    // pooled_p is the first block of traverser p's query
+    float* other = p ? x0 : x1;  // and the second block of the other traverser's
     for (uint32_t k0 = 0; k0 < pool; k0 += 64) {
         const uint32_t k = k0 + lane;
         const bool live = k < pool;
@@ -344,22 +348,130 @@ __global__ __launch_bounds__(BLOCK) void k_pool(WaveDev w, int player, void* x0,
             }
         }
         if (live) {
-            store_operand<PREC>(own, operand_at<PREC>(row, k, in), acc);
-            store_operand<PREC>(other, operand_at<PREC>(row, pool + k, in), acc);
+            own[(size_t)row * in + k] = acc;
+            other[(size_t)row * in + pool + k] = acc;
+        }
+    }
+}
+
+// 16-bit nets: one wavefront per pool group (up to POOL_GROUP rows of one
+// player whose configs are the same list), on the f32 MFMA. With A the
+// group's reach rows (row 15: ones) and B the configs' embeddings, four
+// 16x16x4 products per 4 configs accumulate U[r][k] = sum_c reach_r(c) e_c(k)
+// and, in row 15, S[k] = sum_c e_c(k); each row's mass is summed on the VALU
+// from the same reach values. Then pooled = U / mass, or S / n where
+// the mass is below the smoothing floor (the uniform weights of
+// normalize_weights). Each config's embedding is read once for the group.
+// Products are exact f32; only the summation order differs from the CPU's,
+// far below the 16-bit rounding of the stored query input.
+template <int PREC>
+__global__ __launch_bounds__(BLOCK) void k_pool_mfma(WaveDev w, int player, uint16_t* x0, uint16_t* x1) {
+    uint32_t g = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const uint32_t lane = threadIdx.x & 63;
+    uint32_t p = player < 0 ? 0u : (uint32_t)player;
+    if (player < 0 && g >= w.npool[0]) {
+        g -= w.npool[0];
+        p = 1;
+    }
+    if (g >= w.npool[p]) return;  // wave-uniform
+    const PoolGroup* grp = w.pool_grp[p] + g;
+    const uint32_t n = grp->n, G = grp->nrows;
+    const uint32_t i = lane & 15, q = lane >> 4;  // A row / B column, and config within a 4-step
+    const float* ra = w.reach + w.reach_base[2 * w.row_node[grp->row[i < G ? i : 0]] + p];
+    const float aconst = i == 15 ? 1.0f : 0.0f;  // rows G..14 are zero, row 15 sums the embeddings
+    const uint32_t* cfgs = w.row_cfg + grp->cfg;
+    const uint32_t pool = w.pool, in = w.in;
+    uint16_t* own = p ? x1 : x0;
+    uint16_t* other = p ? x0 : x1;
+    float tot[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // mass of rows 4q .. 4q + 3
+    for (uint32_t k0 = 0; k0 < pool; k0 += 64) {
+        float4v acc[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[t] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        bool kl[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) kl[t] = k0 + 16 * t + i < pool;
+        float tpart = 0.0f;  // this lane's share of row i's mass: configs 4 s + q
+        // 64 configs per chunk: one coalesced load of their indices, the reach
+        // gathers of all 16 steps in flight together, each step's index handed
+        // to its lanes by a shuffle, then 8 steps' embeddings at a time. Steps
+        // past the end of the list are skipped.
+        for (uint32_t c0 = 0; c0 < n; c0 += 64) {
+            const uint32_t cfl = c0 + lane < n ? cfgs[c0 + lane] : 0xffffffffu;
+            float a[16];
+#pragma unroll
+            for (int s = 0; s < 16; s++) {
+                const uint32_t c = c0 + 4 * s + q;
+                a[s] = c < n ? (i < G ? ra[c] : aconst) : 0.0f;
+            }
+#pragma unroll
+            for (int s = 0; s < 16; s++) tpart += a[s];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                if (c0 + 32 * h >= n) break;  // wave-uniform
+                uint32_t cf[8];
+                float b[8][4];
+#pragma unroll
+                for (int s = 0; s < 8; s++) cf[s] = (uint32_t)__shfl((int)cfl, 4 * (8 * h + s) + (int)q, 64);
+#pragma unroll
+                for (int s = 0; s < 8; s++) {
+                    const bool live = cf[s] != 0xffffffffu;
+                    const float* e = w.cfg_emb + (size_t)(live ? cf[s] : 0u) * pool + k0 + i;
+#pragma unroll
+                    for (int t = 0; t < 4; t++) b[s][t] = live && kl[t] ? e[16 * t] : 0.0f;
+                }
+#pragma unroll
+                for (int s = 0; s < 8; s++) {
+                    if (c0 + 4 * (8 * h + s) >= n) break;  // wave-uniform
+#pragma unroll
+                    for (int t = 0; t < 4; t++)
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[8 * h + s], b[s][t], acc[t], 0, 0, 0);
+                }
+            }
+        }
+        if (k0 == 0) {
+            // Row i's mass: lanes i, i + 16, i + 32, i + 48 hold its partial sums.
+            float ti = tpart + __shfl_xor(tpart, 16, 64);
+            ti += __shfl_xor(ti, 32, 64);
+#pragma unroll
+            for (int v = 0; v < 4; v++) tot[v] = __shfl(ti, (int)(4 * q + v), 64);
+            if (q == 0 && i < G) w.mass[2 * grp->row[i] + p] = ti;
+        }
+        const float inv_n = 1.0f / (float)(n > 0 ? n : 1);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float S = __shfl(acc[t][3], (int)(48 + i), 64);  // row 15 of this column
+            const uint32_t k = k0 + 16 * t + i;
+            if (!kl[t]) continue;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const uint32_t rr = 4 * q + v;
+                if (rr >= G) continue;
+                const float y = tot[v] > SMOOTHF ? acc[t][v] * (1.0f / tot[v]) : S * inv_n;
+                const uint32_t row = grp->row[rr];
+                const uint16_t h = PREC == WC_F16 ? f32_to_f16_rn(y) : f32_to_bf16_rn(y);
+                own[frag_off(row, k, in)] = h;
+                other[frag_off(row, pool + k, in)] = h;
+            }
         }
     }
 }
 
 void launch_pool(const WaveDev& w, int player, int precision, void* x0, void* x1, hipStream_t s) {
-    size_t waves = (size_t)w.rows * (player < 0 ? 2 : 1);
+    if (precision == WC_PRECISE) {
+        size_t waves = (size_t)w.rows * (player < 0 ? 2 : 1);
+        if (!waves) return;
+        hipLaunchKernelGGL(k_pool_exact, dim3(grid_for(waves * 64)), dim3(BLOCK), 0, s, w, player, (float*)x0,
+                           (float*)x1);
+        return;
+    }
+    size_t waves = player < 0 ? (size_t)w.npool[0] + w.npool[1] : w.npool[player];
     if (!waves) return;
     dim3 g(grid_for(waves * 64));
-    if (precision == WC_PRECISE)
-        hipLaunchKernelGGL(k_pool<WC_PRECISE>, g, dim3(BLOCK), 0, s, w, player, x0, x1);
-    else if (precision == WC_F16)
-        hipLaunchKernelGGL(k_pool<WC_F16>, g, dim3(BLOCK), 0, s, w, player, x0, x1);
+    if (precision == WC_F16)
+        hipLaunchKernelGGL(k_pool_mfma<WC_F16>, g, dim3(BLOCK), 0, s, w, player, (uint16_t*)x0, (uint16_t*)x1);
     else
-        hipLaunchKernelGGL(k_pool<WC_BF16>, g, dim3(BLOCK), 0, s, w, player, x0, x1);
+        hipLaunchKernelGGL(k_pool_mfma<WC_BF16>, g, dim3(BLOCK), 0, s, w, player, (uint16_t*)x0, (uint16_t*)x1);
 }
 
 // The fixed part of both traversers' query inputs: the seat (-1 for player 0,
@@ -758,9 +870,6 @@ void launch_head_exact(const float* H, uint32_t hidden, const float* Wh, const f
 
 // ------------------------------------------------------- leaf MLP (MFMA)
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float float4v __attribute__((ext_vector_type(4)));
 
 template <int PREC>
 __global__ void k_to16(const float* src, uint16_t* dst, uint32_t rows, uint32_t K, int transposed) {

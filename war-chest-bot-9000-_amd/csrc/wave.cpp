@@ -1,6 +1,9 @@
 // Host wave packing (counterpart of engine/src/gpu/wave.rs:132-644).
 #include "wave.h"
 
+#include <string>
+#include <unordered_map>
+
 #include <algorithm>
 #include <cstring>
 
@@ -475,6 +478,32 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             uint32_t& n = w.head_tile_n[r / 128];
             n = std::max(n, w.cfg_key[w.row_cfg[x]] + 1);
         }
+    // Pool groups: rows with the same config list (same tree, same
+    // infostates in the same order), at most POOL_GROUP per group, in row
+    // order within a list; longest lists launch first.
+    for (int p = 0; p < 2; p++) {
+        std::unordered_map<std::string, uint32_t> key_of;
+        std::vector<std::vector<uint32_t>> lists;
+        for (uint32_t r = 0; r < nrows; r++) {
+            const uint32_t a = w.row_cfg_off[2 * r + p], b = w.row_cfg_off[2 * r + p + 1];
+            std::string key((const char*)(w.row_cfg.data() + a), size_t(b - a) * sizeof(uint32_t));
+            auto it = key_of.emplace(std::move(key), (uint32_t)lists.size()).first;
+            if (it->second == lists.size()) lists.emplace_back();
+            lists[it->second].push_back(r);
+        }
+        auto& out = w.pool_grp[p];
+        out.clear();
+        for (const auto& rows_of : lists)
+            for (size_t k = 0; k < rows_of.size(); k += POOL_GROUP) {
+                PoolGroup g{};
+                g.cfg = w.row_cfg_off[2 * rows_of[0] + p];
+                g.n = w.row_cfg_off[2 * rows_of[0] + p + 1] - g.cfg;
+                g.nrows = (uint32_t)std::min<size_t>(POOL_GROUP, rows_of.size() - k);
+                for (uint32_t i = 0; i < g.nrows; i++) g.row[i] = rows_of[k + i];
+                out.push_back(g);
+            }
+        std::stable_sort(out.begin(), out.end(), [](const PoolGroup& a, const PoolGroup& b) { return a.n > b.n; });
+    }
     // Subtree units largest first: the device takes them in launch order.
     std::stable_sort(sub_units.begin(), sub_units.end(),
                      [](const UnitDev& a, const UnitDev& b) { return a.slots > b.slots; });
@@ -589,6 +618,24 @@ bool validate_deep(const WaveHost& w, std::string* err) {
     }
     for (uint32_t c : w.row_cfg)
         if (c >= ncfg) return fail("row_cfg");
+    for (int p = 0; p < 2; p++) {  // every row in exactly one group, with the group's list
+        std::vector<uint8_t> seen(rows, 0);
+        for (const PoolGroup& g : w.pool_grp[p]) {
+            if (g.nrows == 0 || g.nrows > POOL_GROUP || (uint64_t)g.cfg + g.n > w.row_cfg.size())
+                return fail("pool group");
+            for (uint32_t i = 0; i < g.nrows; i++) {
+                const uint32_t r = g.row[i];
+                if (r >= rows || seen[r]) return fail("pool group row");
+                seen[r] = 1;
+                const uint32_t a = w.row_cfg_off[2 * r + p];
+                if (w.row_cfg_off[2 * r + p + 1] - a != g.n ||
+                    !std::equal(w.row_cfg.begin() + a, w.row_cfg.begin() + a + g.n, w.row_cfg.begin() + g.cfg))
+                    return fail("pool group list");
+            }
+        }
+        for (uint8_t v : seen)
+            if (!v) return fail("pool group cover");
+    }
     for (uint32_t k : w.cfg_key)
         if (k >= w.net.heads) return fail("cfg_key");
     for (uint32_t t : w.term_node)

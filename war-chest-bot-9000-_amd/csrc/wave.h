@@ -83,6 +83,16 @@ struct LeafRec {
     uint32_t out, head, mass, pad;
 };
 
+// Network rows whose configs for one player are the same list, pooled by one
+// wavefront of the 16-bit nets: every config's embedding is read once for all
+// of them (the f32 MFMA's 16 rows: up to 15 network rows and a ones row).
+constexpr uint32_t POOL_GROUP = 15;
+struct PoolGroup {
+    uint32_t cfg, n, nrows;  // the shared list row_cfg[cfg .. cfg + n), rows row[0 .. nrows)
+    uint32_t row[POOL_GROUP];
+};
+static_assert(sizeof(PoolGroup) == 18 * 4, "PoolGroup is 72 bytes");
+
 // Default unit budget in value slots (floats of one player's value vector).
 constexpr uint32_t UNIT_SLOTS = 4096;
 
@@ -147,6 +157,7 @@ struct WaveHost {
     std::vector<ReachRec> reach_rec[2], top_reach_rec[2];
     std::vector<AccRec> acc_rec[2];
     std::vector<LeafRec> leaf_rec[2];  // unit-major network-leaf slots
+    std::vector<PoolGroup> pool_grp[2];  // network rows grouped by config list, longest lists first
     std::vector<uint32_t> child_vb[2];  // child value bases of the opponent rows
 
     uint32_t nodes() const { return (uint32_t)node_meta.size(); }
