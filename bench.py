@@ -32,6 +32,21 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def measured_traffic(workload, kernel):
+    """HBM bytes per dispatch of `kernel` from the committed rocprofv3 counter
+    summary of this workload (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", f"{workload}_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) == 5 and cells[0] == f"`{kernel}`":
+                    return int(cells[4])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -101,6 +116,9 @@ def main():
     mlp_tflops_in_wave = mlp_flops_wave / (mlp_ms * 1e-3) / 1e12 if mlp_ms > 0 else 0.0
     mlp_exec_tflops = st["mlp_flops_executed"] * passes / (mlp_ms * 1e-3) / 1e12 if mlp_ms > 0 else 0.0
     d = by_kernel[dominant]
+    trace_name = {"k_sweep<regret>": "wc::k_sweep<0, %s>" % ("true" if st["max_window"] * 4 <= 65536 else "false"),
+                  "k_reach": "wc::k_reach"}[dominant]
+    traffic = measured_traffic(args.workload, trace_name)
 
     out = {
         "metric": "CFR node-iters/sec + value-net leaf queries/sec on 1 MI355X; % HBM/MFMA peak",
@@ -126,8 +144,9 @@ def main():
         "ms_by_class": {"cfr": round(cfr_ms, 4), "mlp": round(mlp_ms, 4), "leaf_input": round(leaf_ms, 4),
                         "other": round(other_ms, 4)},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": d["achieved_gbs"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": d["frac"], "traffic": None, "bytes_per_launch": d["bytes_per_launch"],
-                     "launch_ms": d["launch_ms"]},
+                     "unit": "GB/s", "frac": d["frac"], "traffic": traffic, "bytes_per_launch": d["bytes_per_launch"],
+                     "launch_ms": d["launch_ms"],
+                     "traffic_source": f"profiles/{args.workload}_hbm_traffic.md ({trace_name})" if traffic else None},
         "roofline_cfr_iteration": {"bound": "hbm", "kernels": by_kernel, "achieved": round(iter_gbs, 2),
                                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(iter_gbs / HBM_PEAK_GBS, 5),
                                    "bytes_per_iter": int(bytes_per_iter), "iter_ms": round(iter_ms, 5)},
