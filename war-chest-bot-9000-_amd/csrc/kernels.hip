@@ -90,7 +90,10 @@ void launch_seed_reach(const WaveDev& w, float* reach, int root_index, hipStream
 // Row elements are handled ROW_BATCH at a time: a batch's loads are issued
 // together (indices, then the values they name) and its part of the reduction
 // is taken after, in element order, so every sum keeps the CPU's order.
-constexpr uint32_t ROW_BATCH = 8;
+constexpr uint32_t ROW_BATCH = 16;   // value rows: decision rows up to 16 actions in one pass
+constexpr uint32_t REACH_BATCH = 8;  // reach gathers and average accumulation
+// Network-leaf slots in flight per thread in the sweep's leaf phase.
+constexpr uint32_t LEAF_BATCH = 4;
 
 // One child config's reach: the reverse gather in stored order (the CPU's
 // scatter order, engine/src/serialize.rs:714-723).
@@ -98,42 +101,42 @@ __device__ __forceinline__ void reach_row(const WaveDev& w, float* reach, const 
     const uint32_t lo = q.start, n = q.kn & REC_N, base = q.pbase;
     float v = 0.0f;
     if ((q.kn >> 31) == REACH_REV) {
-        for (uint32_t c0 = 0; c0 < n; c0 += ROW_BATCH) {
-            const uint32_t m = n - c0 < ROW_BATCH ? n - c0 : ROW_BATCH;
-            uint32_t src[ROW_BATCH], cell[ROW_BATCH];
-            float a[ROW_BATCH], b[ROW_BATCH];
+        for (uint32_t c0 = 0; c0 < n; c0 += REACH_BATCH) {
+            const uint32_t m = n - c0 < REACH_BATCH ? n - c0 : REACH_BATCH;
+            uint32_t src[REACH_BATCH], cell[REACH_BATCH];
+            float a[REACH_BATCH], b[REACH_BATCH];
 #pragma unroll
-            for (uint32_t k = 0; k < ROW_BATCH; k++)
+            for (uint32_t k = 0; k < REACH_BATCH; k++)
                 if (k < m) {
                     src[k] = w.rev_src[lo + c0 + k];
                     cell[k] = w.rev_cell[lo + c0 + k];
                 }
 #pragma unroll
-            for (uint32_t k = 0; k < ROW_BATCH; k++)
+            for (uint32_t k = 0; k < REACH_BATCH; k++)
                 if (k < m) {
                     a[k] = reach[base + src[k]];
                     b[k] = strat[cell[k]];
                 }
 #pragma unroll
-            for (uint32_t k = 0; k < ROW_BATCH; k++)
+            for (uint32_t k = 0; k < REACH_BATCH; k++)
                 if (k < m) v += a[k] * b[k];
         }
     } else {
-        for (uint32_t c0 = 0; c0 < n; c0 += ROW_BATCH) {
-            const uint32_t m = n - c0 < ROW_BATCH ? n - c0 : ROW_BATCH;
-            uint32_t src[ROW_BATCH];
-            float a[ROW_BATCH], pr[ROW_BATCH];
+        for (uint32_t c0 = 0; c0 < n; c0 += REACH_BATCH) {
+            const uint32_t m = n - c0 < REACH_BATCH ? n - c0 : REACH_BATCH;
+            uint32_t src[REACH_BATCH];
+            float a[REACH_BATCH], pr[REACH_BATCH];
 #pragma unroll
-            for (uint32_t k = 0; k < ROW_BATCH; k++)
+            for (uint32_t k = 0; k < REACH_BATCH; k++)
                 if (k < m) {
                     src[k] = w.rvd_src[lo + c0 + k];
                     pr[k] = w.rvd_p[lo + c0 + k];
                 }
 #pragma unroll
-            for (uint32_t k = 0; k < ROW_BATCH; k++)
+            for (uint32_t k = 0; k < REACH_BATCH; k++)
                 if (k < m) a[k] = reach[base + src[k]];
 #pragma unroll
-            for (uint32_t k = 0; k < ROW_BATCH; k++)
+            for (uint32_t k = 0; k < REACH_BATCH; k++)
                 if (k < m) v += a[k] * pr[k];
         }
     }
@@ -144,17 +147,17 @@ __device__ __forceinline__ void reach_row(const WaveDev& w, float* reach, const 
 __device__ __forceinline__ void accumulate_row(const WaveDev& w, AccRec q) {
     const float r = w.reach[q.ridx];
     const uint32_t lo = q.lo, n = q.n;
-    for (uint32_t c0 = 0; c0 < n; c0 += ROW_BATCH) {
-        const uint32_t m = n - c0 < ROW_BATCH ? n - c0 : ROW_BATCH;
-        float cu[ROW_BATCH], sm[ROW_BATCH];
+    for (uint32_t c0 = 0; c0 < n; c0 += REACH_BATCH) {
+        const uint32_t m = n - c0 < REACH_BATCH ? n - c0 : REACH_BATCH;
+        float cu[REACH_BATCH], sm[REACH_BATCH];
 #pragma unroll
-        for (uint32_t j = 0; j < ROW_BATCH; j++)
+        for (uint32_t j = 0; j < REACH_BATCH; j++)
             if (j < m) {
                 cu[j] = w.cur[lo + c0 + j];
                 sm[j] = w.sum[lo + c0 + j];
             }
 #pragma unroll
-        for (uint32_t j = 0; j < ROW_BATCH; j++)
+        for (uint32_t j = 0; j < REACH_BATCH; j++)
             if (j < m) w.sum[lo + c0 + j] = sm[j] + r * cu[j];
     }
 }
@@ -513,9 +516,12 @@ template <int MODE, bool LDSV>
 __device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q, float da, float db, float ds,
                                              float predict, const float* strat, float* lv, uint32_t vw) {
     float* vals = w.vals;
+    // A staged unit keeps its values in LDS; only values read outside the
+    // unit (REC_EXPORT) also go to HBM.
+    const bool to_hbm = !LDSV || (q.kn & REC_EXPORT);
     auto get = [&](uint32_t i) { return LDSV ? lv[i - vw] : vals[i]; };
     auto put = [&](uint32_t i, float v) {
-        vals[i] = v;
+        if (to_hbm) vals[i] = v;
         if (LDSV) lv[i - vw] = v;
     };
     const uint32_t kind = q.kn >> 30, n = q.kn & REC_N, lo = q.start;
@@ -686,15 +692,33 @@ __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, cons
     const UnitDev u = w.units[unit0 + blockIdx.x];
     const int opp = 1 - p;
     const uint32_t vw = u.vwin[p];
-    // Network leaves: one value slot per thread.
-    for (uint32_t k = u.leaf0[p] + threadIdx.x; k < u.leaf1[p]; k += blockDim.x) {
-        const LeafRec q = w.leaf_rec[p][k];
-        const float v = head_out[q.head] * w.mass[q.mass];
-        w.vals[q.out] = v;
-        if (LDSV) lds_vals[q.out - vw] = v;
+    // Network leaves: one value slot per thread, LEAF_BATCH slots per thread
+    // in flight (their records, then the values they name).
+    for (uint32_t k0 = u.leaf0[p]; k0 < u.leaf1[p]; k0 += LEAF_BATCH * BLOCK) {
+        LeafRec q[LEAF_BATCH];
+        float h[LEAF_BATCH], m[LEAF_BATCH];
+#pragma unroll
+        for (uint32_t j = 0; j < LEAF_BATCH; j++) {
+            const uint32_t k = k0 + j * BLOCK + threadIdx.x;
+            if (k < u.leaf1[p]) q[j] = w.leaf_rec[p][k];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < LEAF_BATCH; j++)
+            if (k0 + j * BLOCK + threadIdx.x < u.leaf1[p]) {
+                h[j] = head_out[q[j].head];
+                m[j] = w.mass[q[j].mass];
+            }
+#pragma unroll
+        for (uint32_t j = 0; j < LEAF_BATCH; j++)
+            if (k0 + j * BLOCK + threadIdx.x < u.leaf1[p]) {
+                const float v = h[j] * m[j];
+                if (!LDSV || q[j].exported) w.vals[q[j].out] = v;
+                if (LDSV) lds_vals[q[j].out - vw] = v;
+            }
     }
     for (uint32_t x = u.term0 + threadIdx.x; x < u.term1; x += blockDim.x) {
-        uint32_t k = w.unit_term[x];
+        const uint32_t te = w.unit_term[x], k = te & TERM_INDEX;
+        const bool to_hbm = !LDSV || (te & term_export(p));
         uint32_t node = w.term_node[k];
         const float* ro = w.reach + w.reach_base[2 * node + opp];
         float m = 0.0f;
@@ -702,16 +726,30 @@ __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, cons
         float uu = (w.node_meta[node] >> 2) == (uint32_t)p ? w.term_util[k] : -w.term_util[k];
         const uint32_t ob = w.vals_base[2 * node + p];
         for (uint32_t c = 0; c < w.nc[2 * node + p]; c++) {
-            w.vals[ob + c] = uu * m;
+            if (to_hbm) w.vals[ob + c] = uu * m;
             if (LDSV) lds_vals[ob + c - vw] = uu * m;
         }
     }
     __syncthreads();
+    // Levels from the deepest up. The next level's bounds and each thread's
+    // first record of it are fetched while the current level runs.
     const BackRec* back = w.back_rec[p];
-    const uint32_t* blvl = w.back_lvl[p];
-    for (uint32_t l = u.nlevels; l-- > 0;) {
-        uint32_t b = blvl[u.lvl0 + l], e = blvl[u.lvl0 + l + 1];
-        for (uint32_t k = b + threadIdx.x; k < e; k += blockDim.x)
+    const uint32_t* blvl = w.back_lvl[p] + u.lvl0;
+    uint32_t l = u.nlevels;
+    uint32_t e = l ? blvl[l] : 0, b = l ? blvl[l - 1] : 0;
+    BackRec nxt{};
+    if (l && b + threadIdx.x < e) nxt = back[b + threadIdx.x];
+    while (l-- > 0) {
+        const uint32_t lb = b, le = e;
+        const BackRec first = nxt;
+        if (l) {
+            e = lb;
+            b = blvl[l - 1];
+            if (b + threadIdx.x < e) nxt = back[b + threadIdx.x];
+        }
+        uint32_t k = lb + threadIdx.x;
+        if (k < le) backprop_row<MODE, LDSV>(w, p, first, da, db, ds, predict, w.snap, lds_vals, vw);
+        for (k += blockDim.x; k < le; k += blockDim.x)
             backprop_row<MODE, LDSV>(w, p, back[k], da, db, ds, predict, w.snap, lds_vals, vw);
         __syncthreads();
     }
@@ -1044,8 +1082,10 @@ __device__ __forceinline__ float4v mfma16(const uint4& a, const uint4& b, const 
 // acc[a][b] (b < NB) = sum over ks steps of W(block b) X(rows 16a..)^T. xs: the
 // LDS operand at this lane's fragment slot (fragment (a, s) at xs + (a ks + s)
 // 512); wp: the wavefront's first weight block at this lane's slot (block b at
-// wp + b wstride). Two fragment sets ping-pong so one step's loads overlap the
-// previous step's MFMAs.
+// wp + b wstride). Weight fragments (from L2) are fetched two steps ahead
+// through a ring of four sets, activation fragments (from LDS) one step ahead
+// through two; the loop is unrolled by four so every set keeps a fixed role.
+// Loads past the last step re-read the last step (in bounds, unused).
 template <int PREC, int NB>
 __device__ __forceinline__ void chain_kloop(float4v (&acc)[8][CHAIN_NB], const uint16_t* xs, uint32_t ks,
                                             const uint16_t* __restrict__ wp, size_t wstride) {
@@ -1053,10 +1093,14 @@ __device__ __forceinline__ void chain_kloop(float4v (&acc)[8][CHAIN_NB], const u
     for (int a = 0; a < 8; a++)
 #pragma unroll
         for (int b = 0; b < NB; b++) acc[a][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-    uint4 x0[8], w0[NB], x1[8], w1[NB];
-    auto load = [&](uint4 (&fx)[8], uint4 (&fw)[NB], uint32_t s) {
+    uint4 xa[8], xb[8], w0[NB], w1[NB], w2[NB], w3[NB];
+    auto ldw = [&](uint4 (&fw)[NB], uint32_t s) {
+        s = s < ks ? s : ks - 1;
 #pragma unroll
         for (int b = 0; b < NB; b++) fw[b] = *(const uint4*)(wp + b * wstride + (size_t)s * 512);
+    };
+    auto ldx = [&](uint4 (&fx)[8], uint32_t s) {
+        s = s < ks ? s : ks - 1;
 #pragma unroll
         for (int a = 0; a < 8; a++) fx[a] = *(const uint4*)(xs + ((size_t)a * ks + s) * 512);
     };
@@ -1066,19 +1110,37 @@ __device__ __forceinline__ void chain_kloop(float4v (&acc)[8][CHAIN_NB], const u
 #pragma unroll
             for (int b = 0; b < NB; b++) acc[a][b] = mfma16<PREC>(fw[b], fx[a], acc[a][b]);
     };
-    load(x0, w0, 0);
+    ldw(w0, 0);
+    ldw(w1, 1);
+    ldx(xa, 0);
     uint32_t s = 0;
-    for (; s + 2 <= ks; s += 2) {
-        load(x1, w1, s + 1);
+    for (; s + 4 <= ks; s += 4) {
+        ldw(w2, s + 2);
+        ldx(xb, s + 1);
         __builtin_amdgcn_sched_barrier(0);
-        step(x0, w0);
+        step(xa, w0);
         __builtin_amdgcn_sched_barrier(0);
-        load(x0, w0, s + 2 < ks ? s + 2 : s + 1);  // past the end: re-read a valid step, unused
+        ldw(w3, s + 3);
+        ldx(xa, s + 2);
         __builtin_amdgcn_sched_barrier(0);
-        step(x1, w1);
+        step(xb, w1);
+        __builtin_amdgcn_sched_barrier(0);
+        ldw(w0, s + 4);
+        ldx(xb, s + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        step(xa, w2);
+        __builtin_amdgcn_sched_barrier(0);
+        ldw(w1, s + 5);
+        ldx(xa, s + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        step(xb, w3);
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (s < ks) step(x0, w0);  // odd step count: x0/w0 hold the last step
+    for (; s < ks; s++) {  // K not a multiple of 128: the last steps one at a time
+        ldw(w0, s);
+        ldx(xa, s);
+        step(xa, w0);
+    }
 }
 
 // The wavefront's share of one layer: 16-feature blocks blk0, blk0 + CHAIN_WAVES,

@@ -148,6 +148,33 @@ void build_records(WaveHost* wp) {
             }
             u.leaf1[p] = (uint32_t)w.leaf_rec[p].size();
         }
+        // Exported slots: the values read outside their unit, by the top
+        // regions' rows or as a tree's root values. Only these leave an
+        // LDS-staged unit sweep for HBM.
+        std::vector<uint8_t> ex(w.vals_len, 0);
+        for (const BackRec& r : w.top_back_rec[p]) {
+            const uint32_t n = r.kn & REC_N, kind = r.kn >> 30;
+            for (uint32_t k = 0; k < n; k++) {
+                uint32_t slot;
+                if (kind == BACK_OWN)
+                    slot = w.legal_value[r.start + k];
+                else if (kind == BACK_DRAW)
+                    slot = r.arg + w.draw_to[r.start + k];
+                else
+                    slot = w.child_vb[p][r.start + k] + r.arg;
+                if (slot < w.vals_len) ex[slot] = 1;
+            }
+        }
+        for (const TreeDev& t : w.trees)
+            for (uint32_t c = 0; c < w.nc(t.node0, p); c++) ex[w.vals_base[2 * t.node0 + p] + c] = 1;
+        for (BackRec& r : w.back_rec[p])
+            if (ex[r.out]) r.kn |= REC_EXPORT;
+        for (LeafRec& r : w.leaf_rec[p]) r.exported = ex[r.out];
+        for (uint32_t& te : w.unit_term) {
+            const uint32_t node = w.term_node[te & TERM_INDEX];
+            for (uint32_t c = 0; c < w.nc(node, p); c++)
+                if (ex[w.vals_base[2 * node + p] + c]) te |= term_export(p);
+        }
         for (const Task& q : w.decision[p]) {
             uint32_t row = w.legal_row_of[q.node] + q.config;
             w.acc_rec[p].push_back({w.reach_base[2 * q.node + p] + q.config, w.legal_off[row],
@@ -531,6 +558,12 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
         *err = "wave too large: network rows x heads exceeds 2^32";
         return false;
     }
+    // Row records keep element counts in REC_N bits and terminal indices in TERM_INDEX bits.
+    if (w.ncells > REC_N || w.draw_to.size() > REC_N || w.child.size() > REC_N || w.rev_src.size() > REC_N ||
+        w.rvd_src.size() > REC_N || w.term_node.size() > TERM_INDEX) {
+        *err = "wave too large for the row records";
+        return false;
+    }
     build_records(&w);
     w.jobs = std::move(jobs);
     if (!validate_deep(w, err)) return false;
@@ -658,8 +691,8 @@ bool validate_deep(const WaveHost& w, std::string* err) {
     if (w.unit_row.size() != rows || w.unit_term.size() != w.term_node.size()) return fail("unit leaf lists");
     for (uint32_t r : w.unit_row)
         if (r >= rows) return fail("unit_row");
-    for (uint32_t k : w.unit_term)
-        if (k >= w.term_node.size()) return fail("unit_term");
+    for (uint32_t te : w.unit_term)
+        if ((te & TERM_INDEX) >= w.term_node.size()) return fail("unit_term");
     if (w.nsub > w.units.size()) return fail("unit counts");
     for (const UnitDev& u : w.units) {
         if (uint64_t(u.lvl0) + u.nlevels + 1 > w.lvl_len || u.tree >= w.trees.size()) return fail("unit range");
@@ -760,7 +793,7 @@ bool validate_deep(const WaveHost& w, std::string* err) {
             for (uint32_t k = u.leaf0[p]; k < u.leaf1[p]; k++)
                 if (!in(w.leaf_rec[p][k].out)) return fail("unit leaf outside its value window");
             for (uint32_t k = u.term0; k < u.term1; k++) {
-                uint32_t node = w.term_node[w.unit_term[k]];
+                uint32_t node = w.term_node[w.unit_term[k] & TERM_INDEX];
                 if (w.nc(node, p) && (!in(w.vals_base[2 * node + p]) || !in(w.vals_base[2 * node + p] + w.nc(node, p) - 1)))
                     return fail("unit terminal outside its value window");
             }

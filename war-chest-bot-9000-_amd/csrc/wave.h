@@ -32,9 +32,15 @@ struct Task {
 // level costs one record read, one element read and one gather.
 enum : uint32_t { BACK_OWN = 0, BACK_DRAW = 1, BACK_OPP = 2 };
 enum : uint32_t { REACH_REV = 0, REACH_RVD = 1 };
-constexpr uint32_t REC_N = 0x3fffffffu;  // element count bits of `kn`
+constexpr uint32_t REC_N = 0x1fffffffu;       // element count bits of `kn`
+constexpr uint32_t REC_EXPORT = 1u << 29;     // BackRec: the row's value is read outside its unit
+// unit_term entries: the terminal index, plus one bit per player whose values
+// at that terminal are read outside the unit.
+constexpr uint32_t TERM_INDEX = 0x3fffffffu;
+constexpr uint32_t term_export(int p) { return 1u << (31 - p); }
 
-// One value row of the traverser: out = its value slot; kn = kind << 30 | n.
+// One value row of the traverser: out = its value slot; kn = kind << 30 |
+// REC_EXPORT (when set) | n.
 //   BACK_OWN  cells [start, start + n) of the traverser's decision row (arg unused)
 //   BACK_DRAW draw entries [start, start + n) (wave-global), values at arg + draw_to
 //   BACK_OPP  child value bases child_vb[p][start .. start + n), plus arg = the config
@@ -78,9 +84,10 @@ struct UnitDev {
 static_assert(sizeof(UnitDev) == 20 * 4, "UnitDev is 80 bytes");
 
 // One network-leaf value slot of the traverser: vals[out] = head_out[head] * mass[mass]
-// (the net's value of the slot's config times the opponent's reach mass).
+// (the net's value of the slot's config times the opponent's reach mass);
+// exported = 1 when the slot is read outside its unit.
 struct LeafRec {
-    uint32_t out, head, mass, pad;
+    uint32_t out, head, mass, exported;
 };
 
 // Network rows whose configs for one player are the same list, pooled by one
