@@ -190,6 +190,31 @@ __device__ __forceinline__ void reach_unit(const WaveDev& w, const UnitDev& u, f
     }
 }
 
+// One player's top-down reach of one unit, the next level's bounds and each
+// thread's first record of it fetched while the current level runs.
+__device__ __forceinline__ void reach_unit_one(const WaveDev& w, const UnitDev& u, float* reach, const float* strat,
+                                               int p) {
+    const ReachRec* rec = w.reach_rec[p];
+    const uint32_t* lvl = w.reach_lvl[p] + u.lvl0;
+    const uint32_t L = u.nlevels;
+    uint32_t b = L ? lvl[0] : 0, e = L ? lvl[1] : 0;
+    ReachRec nxt{};
+    if (L && b + threadIdx.x < e) nxt = rec[b + threadIdx.x];
+    for (uint32_t l = 0; l < L; l++) {
+        const uint32_t lb = b, le = e;
+        const ReachRec first = nxt;
+        if (l + 1 < L) {
+            b = le;
+            e = lvl[l + 2];
+            if (b + threadIdx.x < e) nxt = rec[b + threadIdx.x];
+        }
+        uint32_t k = lb + threadIdx.x;
+        if (k < le) reach_row(w, reach, strat, first);
+        for (k += blockDim.x; k < le; k += blockDim.x) reach_row(w, reach, strat, rec[k]);
+        __syncthreads();
+    }
+}
+
 // Subtree units' reach; with `accumulate`, each unit then accumulates its own
 // decision rows, and the blocks past the units accumulate the top regions'
 // decision rows, one row per thread (their reach is final by then).
@@ -201,7 +226,10 @@ __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, uint
         return;
     }
     const UnitDev u = w.units[unit0 + blockIdx.x];
-    reach_unit(w, u, reach, strat, player);
+    if (player < 0)
+        reach_unit(w, u, reach, strat, player);
+    else
+        reach_unit_one(w, u, reach, strat, player);
     if (accumulate) accumulate_unit(w, u, player);
 }
 
@@ -821,16 +849,22 @@ void launch_normalize(const WaveDev& w, int touched0, int touched1, hipStream_t 
 }
 
 // Normalised beliefs at every exit, f16 (the carry store, engine/src/gpu/client.rs:20-111).
+// One wavefront per (exit, player): lanes load 64 configs at a time and the
+// mass is summed in config order from the lanes' values.
 __global__ __launch_bounds__(BLOCK) void k_gather_carry(WaveDev w, const float* reach, int slot) {
-    uint32_t task = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    uint32_t lane = threadIdx.x & 63;
-    uint32_t e = task >> 1, p = task & 1;
-    if (e >= w.nexit) return;
-    uint32_t node = w.exit_node[e];
-    uint32_t n = w.nc[2 * node + p];
+    const uint32_t task = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t e = task >> 1, p = task & 1;
+    if (e >= w.nexit) return;  // wave-uniform
+    const uint32_t node = w.exit_node[e];
+    const uint32_t n = w.nc[2 * node + p];
     const float* r = reach + w.reach_base[2 * node + p];
     float tot = 0.0f;
-    for (uint32_t c = 0; c < n; c++) tot += r[c];
+    for (uint32_t c0 = 0; c0 < n; c0 += 64) {
+        const float v = c0 + lane < n ? r[c0 + lane] : 0.0f;
+        const uint32_t m = n - c0 < 64 ? n - c0 : 64;
+        for (uint32_t j = 0; j < m; j++) tot += lane_value(v, j);
+    }
     float scale, flat;
     if (tot > SMOOTHF) {
         scale = 1.0f / tot;
