@@ -76,13 +76,15 @@ def test_unit_windows_fit_the_budget(budget, monkeypatch):
     assert 0 < st["max_window"] <= (budget or 4096)
 
 
+@pytest.mark.parametrize("family", ["wave256", "wave512w"])
 @pytest.mark.parametrize("budget", [64, 300, 8192])
-def test_parity_waves_pack_and_validate(budget, monkeypatch):
-    # The GPU parity suite's waves (chance nodes, terminals, 3 carried roots)
-    # at its unit budgets: packing runs the full host-side validation.
+def test_parity_waves_pack_and_validate(budget, family, monkeypatch):
+    # The GPU parity suite's waves (chance nodes, terminals, 3 carried roots;
+    # MLP and two-tower nets) at its unit budgets: packing runs the full
+    # host-side validation.
     monkeypatch.setenv("WC_UNIT_SLOTS", str(budget))
-    jobs = W.jobs("wave256", trees=8, nodes_lo=30, nodes_hi=90, chance=1, terminal_p=0.15, notrans_p=0.05,
-                  nroots=3, iters=8, info_median=6.0, info_p99=40.0, info_cap=40, seed=13)
+    jobs = W.jobs(family, trees=8, nodes_lo=30, nodes_hi=90, chance=1, terminal_p=0.15, notrans_p=0.05,
+                  nroots=3, iters=8, info_median=6.0, info_p99=40.0, info_cap=40, seed=13, whale_frac=0.0)
     st = ww.Wave(jobs).stats()
     assert st["terminals"] > 0 and st["chance_nodes"] > 0
     if budget == 64:

@@ -244,6 +244,42 @@ def test_wave64_f16_fast_mode_tracks_exact_math():
         say(f"tree {k}: mean strategy error {mean_s:.2e}, root error {rel:.2e} of max |root|")
 
 
+def test_two_tower_float32_bit_exact():
+    """The two-tower leaf net (public tower over the query, private tower over
+    each infostate's features, readout of their product) in float32: strategy,
+    root values and carries bit-identical to the oracle."""
+    jobs = W.jobs("wave512w", trees=6, nodes_lo=30, nodes_hi=90, chance=1, terminal_p=0.15, notrans_p=0.05, nroots=2,
+                  iters=8, info_median=6.0, info_p99=40.0, info_cap=40, seed=31, whale_frac=0.0)
+    net = W.net_for("wave512w")
+    say(f"case two-tower float32: {len(jobs)} trees, 512 -> 2x512 public, 96 -> 2x512 private")
+    got = gpu_solve(jobs, net, ww.WC_PRECISE)
+    for k, (j, g) in enumerate(zip(jobs, got)):
+        assert_bit_exact(g, O.solve(j, net, O.NET_F32), f"tree {k}")
+
+
+def test_two_tower_bf16_tracks_reduced_precision_oracle():
+    """bf16 operands, f32 accumulation, against the oracle's bf16 emulation
+    (same operand rounding, wide accumulation), with whale trees (100
+    infostates) among ordinary ones. 64 iterations, as the reference bounds its
+    reduced-precision head (engine/src/gpu/tests.rs:392-446): over a few
+    iterations one regret near zero changing sign under 8-bit mantissas moves a
+    strategy entry by ~0.5."""
+    jobs = W.jobs("wave512w", trees=4, nodes_lo=40, nodes_hi=80, chance=1, iters=64, info_median=10.0,
+                  info_p99=120.0, info_cap=120, seed=37, whale_frac=0.5, whale_nodes=150, whale_info=100)
+    net = W.net_for("wave512w")
+    say(f"case two-tower bf16: {len(jobs)} trees, half of them whales")
+    got = gpu_solve(jobs, net, ww.WC_BF16)
+    for k, (j, g) in enumerate(zip(jobs, got)):
+        ref = O.solve(j, net, O.NET_BF16)
+        mean_s = float(np.abs(g.strategy - ref["strategy"]).mean())
+        assert mean_s <= 5e-3, f"tree {k}: mean strategy error {mean_s:.2e}"
+        assert ref_cmp_ratio(g.strategy, ref["strategy"], 0.4, 0.1) <= 1.0, f"tree {k}: strategy guard"
+        scale = np.abs(ref["roots"]).max()
+        rel = np.abs(g.root_values - ref["roots"]).max() / scale
+        assert rel <= 2e-2, f"tree {k}: root values {rel:.2e} of the largest root value"
+        say(f"tree {k}: mean strategy error {mean_s:.2e}, root error {rel:.2e} of max |root|")
+
+
 def test_service_submit_wait():
     jobs = small_wave(trees=5, seed=41)
     net = W.net_for("wave256")

@@ -300,15 +300,29 @@ def numpy_value_under(d, net, root):
     propagate, pooled beliefs (search.rs:1501-1547), the MLP per traverser,
     leaf readout (search.rs:1587-1636) and the Value backprop (search.rs:1654-1803)."""
     dims = [int(x) for x in net.dims]
-    inp, hid, layers, heads, pool = dims[1:6]
-    cfeat = 1 + pool
     w, b = net.w.astype(np.float64), net.b.astype(np.float64)
-    mats, at, k = [], 0, inp
-    for _ in range(layers):
-        mats.append(w[at:at + k * hid].reshape(k, hid))
-        at += k * hid
-        k = hid
-    Wh = w[at:at + heads * hid].reshape(heads, hid)
+
+    def tower(at, k, layers, hid):
+        mats = []
+        for _ in range(layers):
+            mats.append(w[at:at + k * hid].reshape(k, hid))
+            at += k * hid
+            k = hid
+        return mats, at
+
+    if dims[0] == 101:  # MLP: [101, in, hidden, layers, heads, pool]
+        inp, hid, layers, heads, pool = dims[1:6]
+        cfeat = 1 + pool
+        mats, at = tower(0, inp, layers, hid)
+        Wh = w[at:at + heads * hid].reshape(heads, hid)
+    else:  # two-tower: [102, in, width, pub_layers, priv_in, priv_layers, pool]
+        inp, hid, layers, priv_in, priv_layers, pool = dims[1:7]
+        cfeat = 1 + pool + priv_in
+        mats, at = tower(0, inp, layers, hid)
+        pmats, at = tower(at, priv_in, priv_layers, hid)
+        wread = w[at:at + hid]
+        pb = b[layers * hid:(layers + priv_layers) * hid]
+        bread = b[(layers + priv_layers) * hid]
     cur = uniform_cur(d)
     dd = dict(d, root=[np.asarray(root[0]), np.asarray(root[1])])
     reach = forward_reach(dd, cur)
@@ -320,7 +334,7 @@ def numpy_value_under(d, net, root):
             wv = reach[leaf][p]
             beta = wv / wv.sum() if wv.sum() > 1e-30 else np.full(len(wv), 1.0 / max(len(wv), 1))
             cid = d["leaf_cidx"][d["leaf_coff"][2 * r + p]:d["leaf_coff"][2 * r + p + 1]]
-            pooled[(r, p)] = beta @ cphi[cid, 1:] if len(cid) else np.zeros(pool)
+            pooled[(r, p)] = beta @ cphi[cid, 1:1 + pool] if len(cid) else np.zeros(pool)
     out = []
     for p in (0, 1):
         vals = {}
@@ -333,8 +347,16 @@ def numpy_value_under(d, net, root):
             for l in range(layers):
                 h = np.maximum(h @ mats[l] + b[l * hid:(l + 1) * hid], 0.0)
             cid = d["leaf_cidx"][d["leaf_coff"][2 * r + p]:d["leaf_coff"][2 * r + p + 1]]
-            keys = cphi[cid, 0].astype(int)
-            v = Wh[keys] @ h + b[layers * hid + keys]
+            if dims[0] == 101:
+                keys = cphi[cid, 0].astype(int)
+                v = Wh[keys] @ h + b[layers * hid + keys]
+            else:  # <w_read * private_tower(features(c)), public_tower(query)> + b_read
+                v = np.zeros(len(cid))
+                for x, c in enumerate(cid):
+                    f = cphi[c, 1 + pool:]
+                    for l in range(priv_layers):
+                        f = np.maximum(f @ pmats[l] + pb[l * hid:(l + 1) * hid], 0.0)
+                    v[x] = (wread * f) @ h + bread
             vals[int(leaf)] = v * reach[leaf][1 - p].sum()
         for i in range(d["nodes"] - 1, -1, -1):
             kind, me = int(d["node_kind"][i]), int(d["node_player"][i])
@@ -366,12 +388,14 @@ def numpy_value_under(d, net, root):
     return np.concatenate(out)
 
 
-def test_value_under_matches_float64_restatement():
-    """Pins belief_blocks, the query input, readout and the Value backprop:
-    a zero-iteration solve is value_under under the uniform strategy."""
-    net = W.net_for("wave256")
-    jobs = W.jobs("wave256", trees=2, seed=29, nodes_lo=30, nodes_hi=60, chance=1, terminal_p=0.2, notrans_p=0.05,
-                  info_median=5.0, info_p99=20.0, info_cap=20, iters=0, nroots=2)
+@pytest.mark.parametrize("family", ["wave256", "wave512w"])
+def test_value_under_matches_float64_restatement(family):
+    """Pins belief_blocks, the query input, readout and the Value backprop, for
+    the MLP and for the two-tower net: a zero-iteration solve is value_under
+    under the uniform strategy."""
+    net = W.net_for(family)
+    jobs = W.jobs(family, trees=2, seed=29, nodes_lo=30, nodes_hi=60, chance=1, terminal_p=0.2, notrans_p=0.05,
+                  info_median=5.0, info_p99=20.0, info_cap=20, iters=0, nroots=2, whale_frac=0.0)
     for job in jobs:
         d = wcj8.decode(job)
         o = O.solve(job, net, O.NET_F32)

@@ -93,23 +93,42 @@ bool Executor::ensure(void** p, size_t* cap, size_t need, std::string* err) {
 
 uint64_t Executor::publish(const NetShape& ns, const std::vector<uint32_t>& dims, const float* w, size_t nw,
                            const float* b, size_t nb, std::string* err) {
-    if (ns.kind != MODEL_MLP) {
-        *err = "this executor builds the MLP leaf network only";
+    const bool tower = ns.kind == MODEL_TWO_TOWER;
+    if (ns.kind != MODEL_MLP && !tower) {
+        *err = "this executor builds the MLP and two-tower leaf networks only";
         return 0;
     }
-    if (ns.layers == 0 || ns.layers > 15) {
-        *err = "MLP depth out of range";
+    if (ns.layers == 0 || ns.layers > 15 || (tower && (ns.priv_layers == 0 || ns.priv_layers > 15))) {
+        *err = "network depth out of range";
         return 0;
     }
-    size_t need_w = size_t(ns.in) * ns.hidden + size_t(ns.layers - 1) * ns.hidden * ns.hidden +
-                    size_t(ns.heads) * ns.hidden;
-    size_t need_b = size_t(ns.layers) * ns.hidden + ns.heads;
+    // Source matrices in `w` order, (K, N) each: the MLP's trunk then head
+    // ([heads x hidden], one row per output); the two-tower's public then
+    // private tower, then the readout weight vector.
+    struct Mat {
+        size_t k, n;
+        bool head;
+    };
+    std::vector<Mat> mats;
+    mats.push_back({ns.in, ns.hidden, false});
+    for (uint32_t l = 1; l < ns.layers; l++) mats.push_back({ns.hidden, ns.hidden, false});
+    if (tower) {
+        mats.push_back({ns.priv_in, ns.hidden, false});
+        for (uint32_t l = 1; l < ns.priv_layers; l++) mats.push_back({ns.hidden, ns.hidden, false});
+    } else {
+        mats.push_back({ns.hidden, ns.heads, true});
+    }
+    size_t need_w = tower ? ns.hidden : 0;
+    for (const Mat& m : mats) need_w += m.k * m.n;
+    const size_t need_b = tower ? size_t(ns.layers + ns.priv_layers) * ns.hidden + 1
+                                : size_t(ns.layers) * ns.hidden + ns.heads;
     if (nw != need_w || nb != need_b) {
         *err = "weight bank sizes disagree with dims";
         return 0;
     }
-    if (precision_ != WC_PRECISE && (ns.in % 32 || ns.hidden % 32)) {
-        *err = "the MFMA path needs input and hidden widths that are multiples of 32";
+    if (precision_ != WC_PRECISE && (ns.in % 32 || ns.hidden % 32 || (tower && (ns.priv_in % 32 || ns.hidden > 512)))) {
+        *err = tower ? "the MFMA path needs input, private-input and width multiples of 32 (width at most 512)"
+                     : "the MFMA path needs input and hidden widths that are multiples of 32";
         return 0;
     }
     if (hipSetDevice(device_) != hipSuccess) {
@@ -120,31 +139,28 @@ uint64_t Executor::publish(const NetShape& ns, const std::vector<uint32_t>& dims
     bank.ns = ns;
     bank.precision = precision_;
     const size_t esz = precision_ == WC_PRECISE ? 4 : 2;
-    // Layout: matrices (as stored for the arithmetic), then f32 biases. The
-    // exact net keeps the source layout; the MFMA net stores each matrix as the
-    // GEMM's B operand, fragment-major with gemm_rows(N) zero-padded rows.
+    // Layout: matrices (as stored for the arithmetic), then f32 biases, then
+    // the two-tower readout weight. The exact net keeps the source layout; the
+    // MFMA net stores each matrix as the GEMM's B operand (one row per output,
+    // K-contiguous), fragment-major with gemm_rows(N) zero-padded rows.
     std::vector<size_t> moff;
     size_t at = 0;
-    std::vector<std::pair<size_t, size_t>> mats;  // (rows, cols) of each source matrix in w
-    mats.push_back({ns.in, ns.hidden});
-    for (uint32_t l = 1; l < ns.layers; l++) mats.push_back({ns.hidden, ns.hidden});
-    mats.push_back({ns.heads, ns.hidden});
-    auto stored_bytes = [&](size_t k) {
-        if (precision_ == WC_PRECISE) return mats[k].first * mats[k].second * esz;
-        bool head = k + 1 == mats.size();
-        size_t n = head ? mats[k].first : mats[k].second, kdim = head ? mats[k].second : mats[k].first;
-        return size_t(gemm_rows((uint32_t)n)) * kdim * esz;
+    auto stored_bytes = [&](const Mat& m) {
+        if (precision_ == WC_PRECISE) return m.k * m.n * esz;
+        return size_t(gemm_rows((uint32_t)m.n)) * m.k * esz;
     };
-    for (size_t k = 0; k < mats.size(); k++) {
+    for (const Mat& m : mats) {
         moff.push_back(at);
-        at = align256(at + stored_bytes(k));
+        at = align256(at + stored_bytes(m));
     }
     const size_t mats_end = at;
-    size_t boff = at;
+    const size_t boff = at;
     at = align256(at + nb * 4);
+    const size_t roff = at;  // readout weight (two-tower), f32
+    if (tower) at = align256(at + size_t(ns.hidden) * 4);
     // Staging for f32 -> 16-bit conversion on the device.
-    size_t stage = precision_ == WC_PRECISE ? 0 : at;
-    size_t total = at + (precision_ == WC_PRECISE ? 0 : nw * 4);
+    const size_t stage = precision_ == WC_PRECISE ? 0 : at;
+    const size_t total = at + (precision_ == WC_PRECISE ? 0 : nw * 4);
     void* mem = nullptr;
     if (hipMalloc(&mem, total) != hipSuccess) {
         *err = "hipMalloc of the weight bank failed";
@@ -152,28 +168,28 @@ uint64_t Executor::publish(const NetShape& ns, const std::vector<uint32_t>& dims
     }
     char* base = (char*)mem;
     bool okc = hipMemcpyAsync(base + boff, b, nb * 4, hipMemcpyHostToDevice, stream_) == hipSuccess;
+    size_t src = 0;
     if (precision_ == WC_PRECISE) {
-        size_t src = 0;
         for (size_t k = 0; k < mats.size(); k++) {
-            size_t n = mats[k].first * mats[k].second;
+            const size_t n = mats[k].k * mats[k].n;
             okc = okc && hipMemcpyAsync(base + moff[k], w + src, n * 4, hipMemcpyHostToDevice, stream_) == hipSuccess;
             src += n;
         }
     } else {
         okc = okc && hipMemsetAsync(base, 0, mats_end, stream_) == hipSuccess;  // row padding
         okc = okc && hipMemcpyAsync(base + stage, w, nw * 4, hipMemcpyHostToDevice, stream_) == hipSuccess;
-        size_t src = 0;
         for (size_t k = 0; k < mats.size(); k++) {
-            size_t n = mats[k].first * mats[k].second;
-            // Trunk matrices are [K x N] (B row n = source column n); the head is
-            // [N x K] (one K-contiguous row per output).
-            bool head = k + 1 == mats.size();
-            uint32_t rows = (uint32_t)(head ? mats[k].first : mats[k].second);
-            uint32_t kdim = (uint32_t)(head ? mats[k].second : mats[k].first);
-            launch_to16(precision_, (const float*)(base + stage) + src, base + moff[k], rows, kdim, !head, stream_);
+            const size_t n = mats[k].k * mats[k].n;
+            // Trunk and tower matrices are [K x N] (B row n = source column n);
+            // the MLP head is [N x K] (one K-contiguous row per output).
+            launch_to16(precision_, (const float*)(base + stage) + src, base + moff[k], (uint32_t)mats[k].n,
+                        (uint32_t)mats[k].k, !mats[k].head, stream_);
             src += n;
         }
     }
+    if (tower)
+        okc = okc && hipMemcpyAsync(base + roff, w + src, size_t(ns.hidden) * 4, hipMemcpyHostToDevice, stream_) ==
+                         hipSuccess;
     okc = okc && hipStreamSynchronize(stream_) == hipSuccess && hipGetLastError() == hipSuccess;
     if (!okc) {
         hipFree(mem);
@@ -185,8 +201,17 @@ uint64_t Executor::publish(const NetShape& ns, const std::vector<uint32_t>& dims
         bank.W[l] = base + moff[l];
         bank.B[l] = (const float*)(base + boff) + size_t(l) * ns.hidden;
     }
-    bank.Whead = base + moff[ns.layers];
-    bank.bhead = (const float*)(base + boff) + size_t(ns.layers) * ns.hidden;
+    if (tower) {
+        for (uint32_t l = 0; l < ns.priv_layers; l++) {
+            bank.PW[l] = base + moff[ns.layers + l];
+            bank.PB[l] = (const float*)(base + boff) + size_t(ns.layers + l) * ns.hidden;
+        }
+        bank.wread = (const float*)(base + roff);
+        bank.bread = b[size_t(ns.layers + ns.priv_layers) * ns.hidden];
+    } else {
+        bank.Whead = base + moff[ns.layers];
+        bank.bhead = (const float*)(base + boff) + size_t(ns.layers) * ns.hidden;
+    }
     bank.version = next_version_++;
     (void)dims;
     banks_[bank.version] = bank;
@@ -209,7 +234,8 @@ void Executor::retain_from(uint64_t oldest) {
 bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) {
     const NetShape& ns = bank.ns;
     if (w.net.kind != ns.kind || w.net.in != ns.in || w.net.hidden != ns.hidden || w.net.pool != ns.pool ||
-        w.net.heads != ns.heads || w.net.layers != ns.layers) {
+        w.net.heads != ns.heads || w.net.layers != ns.layers || w.net.priv_in != ns.priv_in ||
+        w.net.priv_layers != ns.priv_layers) {
         *err = "wave network shape disagrees with the weight bank";
         return false;
     }
@@ -220,7 +246,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
             draw_row_start, draw_to, draw_p, reach_base, vals_base, parent, rev_row_of, rev_start, rev_src, rev_cell,
             rvd_row_of, rvd_start, rvd_src, rvd_p, row_node, row_cfg_off, row_cfg, cfg_key, cfg_emb, pub_raw,
             term_node, term_util, roots, carried, exit_node, exit_coff, trees, units, bt[2], rt[2], dc[2], bl[2],
-            rl[2], cv[2], lr[2], pg[2], unit_row, unit_term, tb[2], tr[2], head_tile_n;
+            rl[2], cv[2], lr[2], pg[2], cfg_priv, unit_row, unit_term, tb[2], tr[2], head_tile_n;
     } o;
     o.node_meta = blob.put(w.node_meta);
     o.nc = blob.put(w.node_nc);
@@ -250,6 +276,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     o.row_cfg = blob.put(w.row_cfg);
     o.cfg_key = blob.put(w.cfg_key);
     o.cfg_emb = blob.put(w.cfg_emb);
+    o.cfg_priv = blob.put(w.cfg_priv);
     o.pub_raw = blob.put(w.pub_raw);
     o.term_node = blob.put(w.term_node);
     o.term_util = blob.put(w.term_util);
@@ -303,8 +330,18 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         return a;
     };
     const size_t prow = precision_ == WC_PRECISE ? rows : gemm_rows((uint32_t)rows);  // GEMM operands: padded rows
+    const bool tower = ns.kind == MODEL_TWO_TOWER;
+    const size_t ncfg = w.cfg_key.size(), pcfg = precision_ == WC_PRECISE ? ncfg : gemm_rows((uint32_t)ncfg);
     size_t m_x = mtake(prow * ns.in * esz), m_x1 = mtake(prow * ns.in * esz), m_h0 = mtake(prow * ns.hidden * esz),
-           m_h1 = mtake(prow * ns.hidden * esz), m_out = mtake(rows * ns.heads * 4);
+           m_h1 = mtake(prow * ns.hidden * esz),
+           m_out = mtake(tower ? w.row_cfg.size() * 4 : rows * ns.heads * 4);
+    size_t m_px = 0, m_p0 = 0, m_p1 = 0, m_f = 0;
+    if (tower) {
+        m_px = mtake(precision_ == WC_PRECISE ? 0 : pcfg * ns.priv_in * esz);
+        m_p0 = mtake(pcfg * ns.hidden * esz);
+        m_p1 = mtake(pcfg * ns.hidden * esz);
+        m_f = mtake(ncfg * ns.hidden * esz);
+    }
     if (!ensure(&mlp_, &mlp_cap_, mt, err)) return false;
 
     char* T = (char*)table_;
@@ -357,6 +394,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         d.leaf_rec[p] = (const LeafRec*)(T + o.lr[p]);
         d.pool_grp[p] = (const PoolGroup*)(T + o.pg[p]);
         d.npool[p] = (uint32_t)w.pool_grp[p].size();
+        d.nleaf[p] = (uint32_t)w.leaf_rec[p].size();
         d.back_lvl[p] = (const uint32_t*)(T + o.bl[p]);
         d.reach_lvl[p] = (const uint32_t*)(T + o.rl[p]);
         d.ndec[p] = (uint32_t)w.decision[p].size();
@@ -397,6 +435,12 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     H_[0] = M + m_h0;
     H_[1] = M + m_h1;
     head_out_ = (float*)(M + m_out);
+    cfg_priv_ = (const float*)(T + o.cfg_priv);
+    PX_ = tower ? M + m_px : nullptr;
+    P_[0] = tower ? M + m_p0 : nullptr;
+    P_[1] = tower ? M + m_p1 : nullptr;
+    F_ = tower ? M + m_f : nullptr;
+    ncfg_ = tower ? (uint32_t)ncfg : 0;
     rows_ = w.rows();
     launch_query_static(d, precision_, Xq_[0], Xq_[1], stream_);
     HIP_TRY(hipGetLastError());
@@ -453,6 +497,45 @@ void Executor::run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::v
     mark();
 }
 
+void Executor::run_tower_private(const NetBank& bank) {
+    const NetShape& ns = bank.ns;
+    if (!ncfg_) return;
+    const void* in = cfg_priv_;
+    uint32_t k = ns.priv_in;
+    if (precision_ != WC_PRECISE) {
+        launch_to16(precision_, cfg_priv_, PX_, ncfg_, ns.priv_in, false, stream_);
+        in = PX_;
+    }
+    for (uint32_t l = 0; l < ns.priv_layers; l++) {
+        void* out = P_[l & 1];
+        if (precision_ == WC_PRECISE)
+            launch_dense_exact((const float*)in, k, (const float*)bank.PW[l], bank.PB[l], ns.hidden, (float*)out,
+                               ncfg_, stream_);
+        else
+            launch_gemm16(precision_, in, k, bank.PW[l], bank.PB[l], ns.hidden, out, ncfg_, true, true, stream_);
+        in = out;
+        k = ns.hidden;
+    }
+    launch_tower_f(precision_, in, ns.hidden, ncfg_, bank.wread, F_, stream_);
+}
+
+void Executor::run_tower(const NetBank& bank, uint32_t rows, int traverser) {
+    const NetShape& ns = bank.ns;
+    const void* in = Xq_[traverser];
+    uint32_t k = ns.in;
+    for (uint32_t l = 0; l < ns.layers; l++) {
+        void* out = H_[l & 1];
+        if (precision_ == WC_PRECISE)
+            launch_dense_exact((const float*)in, k, (const float*)bank.W[l], bank.B[l], ns.hidden, (float*)out, rows,
+                               stream_);
+        else
+            launch_gemm16(precision_, in, k, bank.W[l], bank.B[l], ns.hidden, out, rows, true, true, stream_);
+        in = out;
+        k = ns.hidden;
+    }
+    launch_tower_head(dev_, traverser, precision_, in, ns.hidden, F_, bank.bread, head_out_, stream_);
+}
+
 void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTimes* prof) {
     const WaveDev& d = dev_;
     hipStream_t s = stream_;
@@ -473,8 +556,12 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         hipEventCreate(&start);
         hipEventRecord(start, s);
     }
+    const bool tower = bank.ns.kind == MODEL_TWO_TOWER;
     auto mlp = [&](int q) {
-        run_mlp(bank, d.rows, Xq_[q], nullptr, head_tile_n_);
+        if (tower)
+            run_tower(bank, d.rows, q);
+        else
+            run_mlp(bank, d.rows, Xq_[q], nullptr, head_tile_n_);
         mark(C_MLP);
     };
     // Top regions, one depth per launch: values bottom-up, reach top-down.
@@ -497,6 +584,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         launch_reach(d, 0, nsub, reach, strat, -1, false, s);
     };
 
+    if (tower) run_tower_private(bank);  // F for this wave's configs under this bank
     launch_zero(d.regret, w.ncells, s);
     launch_init_strategy(d, s);
     launch_seed_reach(d, d.reach, -1, s);
@@ -657,6 +745,10 @@ bool Executor::mlp_forward(uint64_t version, uint32_t rows, const float* x, floa
         return false;
     }
     const NetShape& ns = it->second.ns;
+    if (ns.kind != MODEL_MLP) {
+        *err = "leaf-network inference alone takes the MLP; the two-tower net runs inside a wave";
+        return false;
+    }
     HIP_TRY(hipSetDevice(device_));
     const size_t esz = precision_ == WC_PRECISE ? 4 : 2;
     size_t mt = 0;

@@ -25,6 +25,12 @@ struct NetBank {
     const float* B[16] = {};
     const void* Whead = nullptr;
     const float* bhead = nullptr;
+    // Two-tower net: W/B hold the public tower; the private tower, the readout
+    // weight (f32) and the readout bias.
+    const void* PW[16] = {};
+    const float* PB[16] = {};
+    const float* wread = nullptr;
+    float bread = 0.0f;
 };
 
 struct Result {
@@ -75,6 +81,9 @@ class Executor {
   private:
     bool upload(const WaveHost& w, const NetBank& bank, std::string* err);
     void run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTimes* prof);
+    // Two-tower net: F for the uploaded wave's configs, then one traverser's public tower and readout.
+    void run_tower_private(const NetBank& bank);
+    void run_tower(const NetBank& bank, uint32_t rows, int traverser);
     void run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::vector<hipEvent_t>* marks,
                  const uint32_t* head_tile_n = nullptr);
     bool ensure(void** p, size_t* cap, size_t need, std::string* err);
@@ -101,7 +110,13 @@ class Executor {
     const ReachRec* top_reach_dev_[2] = {};
     const uint32_t* head_tile_n_ = nullptr;  // head width per 128-row tile (device copy)
     void* H_[2] = {};
-    float* head_out_ = nullptr;
+    float* head_out_ = nullptr;  // MLP head outputs, or the two-tower readout per (row, config)
+    // Two-tower net: private-tower input, layer outputs and F (one row per interned config).
+    const float* cfg_priv_ = nullptr;
+    void* PX_ = nullptr;
+    void* P_[2] = {};
+    void* F_ = nullptr;
+    uint32_t ncfg_ = 0;
     uint32_t rows_ = 0;
 };
 

@@ -61,6 +61,7 @@ struct WaveDev {
     uint32_t max_vwin;  // widest unit value window (floats)
     uint32_t ndec[2], ntop_dec[2];
     uint32_t npool[2];  // pool groups of each player
+    uint32_t nleaf[2];  // network-leaf slots of each player (leaf_rec entries)
 };
 
 // Launchers (kernels.hip). All take the executor's stream.
@@ -123,6 +124,14 @@ struct ChainNet {
 bool chain_fits(uint32_t in, uint32_t hidden, uint32_t layers);
 void launch_chain(int precision, const ChainNet& net, const void* X, uint32_t rows, float* out,
                   const uint32_t* tile_n, hipStream_t s);
+// Two-tower net: F = private-tower output (ncfg rows, fragment-major 16-bit or
+// row-major f32) times the readout weight, row-major; then the readout of
+// player p's leaf slots, tv[row_cfg position] = <F[config], H[row]> + bread,
+// from the public-tower output H (fragment-major 16-bit or row-major f32).
+void launch_tower_f(int precision, const void* Hp, uint32_t width, uint32_t ncfg, const float* wread, void* F,
+                    hipStream_t s);
+void launch_tower_head(const WaveDev& w, int player, int precision, const void* H, uint32_t width, const void* F,
+                       float bread, float* tv, hipStream_t s);
 // Convert f32 -> a 16-bit fragment-major operand of `rows` rows and K columns;
 // element (r, k) is src[k * rows + r] when `transposed`, else src[r * K + k].
 void launch_to16(int precision, const float* src, void* dst, uint32_t rows, uint32_t K, bool transposed,

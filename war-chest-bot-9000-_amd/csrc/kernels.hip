@@ -982,6 +982,17 @@ __device__ __forceinline__ void mfma_step(float4v (&acc)[4][4], const uint4 (&af
         }
 }
 
+// One 16x16x32 MFMA: acc += A(a) B(b)^T.
+template <int PREC>
+__device__ __forceinline__ float4v mfma_step16(const uint4& a, const uint4& b, const float4v& acc) {
+    if (PREC == WC_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), acc,
+                                                      0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       acc, 0, 0, 0);
+}
+
 // Fragment-major MFMA GEMM. A 128 x 128 output tile per workgroup, 64 x 64 per
 // wavefront (4 x 4 16x16x32 tiles). Both operands are fragment-major, so each
 // of a step's 8 fragment loads is one contiguous 1 KB read. Two fragment sets
@@ -1079,6 +1090,124 @@ void launch_gemm16(int precision, const void* X, uint32_t K, const void* Wt, con
 #undef WC_GEMM
 }
 
+
+// ------------------------------------------------------------ two-tower net
+//
+// The two-tower leaf value of row r and infostate c is <f(c), h(r)> + b_read
+// with h the public tower's output for the row's query and f(c) the private
+// tower's output for the infostate's features times the readout weight
+// (elementwise). f is formed once per wave and weight bank.
+
+// F[c][k] = Hp[c][k] * wread[k]; the 16-bit nets round the product to the
+// operand type (Hp fragment-major with K = width, F row-major), float32 keeps it.
+template <int PREC>
+__global__ void k_tower_f(const void* __restrict__ Hp, uint32_t width, uint32_t ncfg, const float* __restrict__ wread,
+                          void* __restrict__ F) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)ncfg * width) return;
+    const uint32_t c = (uint32_t)(i / width), k = (uint32_t)(i % width);
+    if (PREC == WC_PRECISE) {
+        ((float*)F)[i] = ((const float*)Hp)[i] * wread[k];
+        return;
+    }
+    const uint16_t hv = ((const uint16_t*)Hp)[frag_off(c, k, width)];
+    float h;
+    if (PREC == WC_F16)
+        h = (float)__builtin_bit_cast(_Float16, hv);
+    else
+        h = __uint_as_float((uint32_t)hv << 16);
+    const float f = h * wread[k];
+    ((uint16_t*)F)[i] = PREC == WC_F16 ? f32_to_f16_rn(f) : f32_to_bf16_rn(f);
+}
+
+void launch_tower_f(int precision, const void* Hp, uint32_t width, uint32_t ncfg, const float* wread, void* F,
+                    hipStream_t s) {
+    const size_t n = (size_t)ncfg * width;
+    if (!n) return;
+    if (precision == WC_PRECISE)
+        hipLaunchKernelGGL(k_tower_f<WC_PRECISE>, dim3(grid_for(n)), dim3(BLOCK), 0, s, Hp, width, ncfg, wread, F);
+    else if (precision == WC_F16)
+        hipLaunchKernelGGL(k_tower_f<WC_F16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, Hp, width, ncfg, wread, F);
+    else
+        hipLaunchKernelGGL(k_tower_f<WC_BF16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, Hp, width, ncfg, wread, F);
+}
+
+// Float32 readout: one thread per network-leaf slot of player p, the sum from
+// b_read in k order as the CPU net forms it. tv is indexed by the slot's
+// position in row_cfg.
+__global__ __launch_bounds__(BLOCK) void k_tower_head_exact(WaveDev w, int p, const float* __restrict__ H,
+                                                          uint32_t width, const float* __restrict__ F, float bread,
+                                                          float* __restrict__ tv) {
+    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= w.nleaf[p]) return;
+    const LeafRec q = w.leaf_rec[p][k];
+    const uint32_t r = q.mass >> 1;  // the mass slot is 2 r + opponent
+    const float* h = H + (size_t)r * width;
+    const float* f = F + (size_t)w.row_cfg[q.head] * width;
+    float acc = bread;
+    for (uint32_t j = 0; j < width; j++) acc += f[j] * h[j];
+    tv[q.head] = acc;
+}
+
+// 16-bit readout on MFMA: one wavefront per pool group of player p (rows
+// sharing a config list). A = the group's rows of H (fragments gathered from
+// the fragment-major public-tower output, lanes past the group repeat its
+// first row), B = 16 configs' F rows at a time; D[row][config] + b_read goes to
+// tv[row_cfg_off[2 row + p] + config position].
+constexpr uint32_t TOWER_MAX_KS = 16;  // width <= 512
+template <int PREC>
+__global__ __launch_bounds__(BLOCK) void k_tower_head(WaveDev w, int p, const uint16_t* __restrict__ H,
+                                                    uint32_t width, const uint16_t* __restrict__ F, float bread,
+                                                    float* __restrict__ tv) {
+    const uint32_t g = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    if (g >= w.npool[p]) return;  // wave-uniform
+    const uint32_t lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    const PoolGroup* grp = w.pool_grp[p] + g;
+    const uint32_t n = grp->n, G = grp->nrows, ks = width >> 5;
+    const uint32_t arow = grp->row[i < G ? i : 0];
+    uint4 a[TOWER_MAX_KS];
+#pragma unroll
+    for (uint32_t s = 0; s < TOWER_MAX_KS; s++)
+        if (s < ks) a[s] = *(const uint4*)(H + frag_off(arow, 32 * s + 8 * q, width));
+    const uint32_t* cfgs = w.row_cfg + grp->cfg;
+    uint32_t orow[4];
+#pragma unroll
+    for (uint32_t v = 0; v < 4; v++) orow[v] = 4 * q + v < G ? w.row_cfg_off[2 * grp->row[4 * q + v] + p] : 0u;
+    for (uint32_t c0 = 0; c0 < n; c0 += 16) {
+        const uint32_t c = c0 + i;
+        const uint16_t* fb = F + (size_t)cfgs[c < n ? c : n - 1] * width + 8 * q;
+        uint4 b[TOWER_MAX_KS];
+#pragma unroll
+        for (uint32_t s = 0; s < TOWER_MAX_KS; s++)
+            if (s < ks) b[s] = *(const uint4*)(fb + 32 * s);
+        float4v acc = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t s = 0; s < TOWER_MAX_KS; s++)
+            if (s < ks) acc = mfma_step16<PREC>(a[s], b[s], acc);
+        if (c < n)
+#pragma unroll
+            for (uint32_t v = 0; v < 4; v++)
+                if (4 * q + v < G) tv[orow[v] + c] = acc[v] + bread;
+    }
+}
+
+void launch_tower_head(const WaveDev& w, int player, int precision, const void* H, uint32_t width, const void* F,
+                       float bread, float* tv, hipStream_t s) {
+    if (precision == WC_PRECISE) {
+        if (w.nleaf[player])
+            hipLaunchKernelGGL(k_tower_head_exact, dim3(grid_for(w.nleaf[player])), dim3(BLOCK), 0, s, w, player,
+                               (const float*)H, width, (const float*)F, bread, tv);
+        return;
+    }
+    if (!w.npool[player]) return;
+    dim3 g(grid_for((size_t)w.npool[player] * 64));
+    if (precision == WC_F16)
+        hipLaunchKernelGGL(k_tower_head<WC_F16>, g, dim3(BLOCK), 0, s, w, player, (const uint16_t*)H, width,
+                           (const uint16_t*)F, bread, tv);
+    else
+        hipLaunchKernelGGL(k_tower_head<WC_BF16>, g, dim3(BLOCK), 0, s, w, player, (const uint16_t*)H, width,
+                           (const uint16_t*)F, bread, tv);
+}
 
 // ------------------------------------------------------- fused leaf network
 //

@@ -137,13 +137,15 @@ void build_records(WaveHost* wp) {
         for (const Task& q : w.top_reach[p]) w.top_reach_rec[p].push_back(reach(q));
         // Network-leaf slots, unit by unit (the value sweep writes them first).
         const uint32_t heads = w.net.heads;
+        const bool tower = w.net.kind == MODEL_TWO_TOWER;
         for (UnitDev& u : w.units) {
             u.leaf0[p] = (uint32_t)w.leaf_rec[p].size();
             for (uint32_t k = u.row0; k < u.row1; k++) {
                 const uint32_t r = w.unit_row[k], node = w.row_node[r];
                 const uint32_t* cfgs = &w.row_cfg[w.row_cfg_off[2 * r + p]];
                 for (uint32_t c = 0; c < w.nc(node, p); c++)
-                    w.leaf_rec[p].push_back({w.vals_base[2 * node + p] + c, r * heads + w.cfg_key[cfgs[c]],
+                    w.leaf_rec[p].push_back({w.vals_base[2 * node + p] + c,
+                                             tower ? w.row_cfg_off[2 * r + p] + c : r * heads + w.cfg_key[cfgs[c]],
                                              2 * r + (1 - p), 0});
             }
             u.leaf1[p] = (uint32_t)w.leaf_rec[p].size();
@@ -336,6 +338,8 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             }
             w.cfg_key.push_back((uint32_t)key);
             w.cfg_emb.insert(w.cfg_emb.end(), phi + 1, phi + 1 + w.net.pool);
+            if (w.net.kind == MODEL_TWO_TOWER)
+                w.cfg_priv.insert(w.cfg_priv.end(), phi + 1 + w.net.pool, phi + 1 + w.net.pool + w.net.priv_in);
         }
         cfg_total += t.ncfg;
         w.pub_raw.insert(w.pub_raw.end(), t.leaf_raw.begin(), t.leaf_raw.end());
@@ -669,8 +673,10 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         for (uint8_t v : seen)
             if (!v) return fail("pool group cover");
     }
-    for (uint32_t k : w.cfg_key)
-        if (k >= w.net.heads) return fail("cfg_key");
+    if (w.net.kind == MODEL_MLP)
+        for (uint32_t k : w.cfg_key)
+            if (k >= w.net.heads) return fail("cfg_key");
+    if (w.cfg_priv.size() != (w.net.kind == MODEL_TWO_TOWER ? ncfg * w.net.priv_in : 0)) return fail("cfg_priv");
     for (uint32_t t : w.term_node)
         if (t >= N || (w.node_meta[t] & 3u) != 2) return fail("term_node");
     const uint64_t nexit = w.exit_node.size();
@@ -778,9 +784,14 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         for (const AccRec& r : w.acc_rec[p])
             if (r.ridx >= w.reach_len || uint64_t(r.lo) + r.n > w.ncells) return fail("accumulation record");
     }
+    const uint64_t heads_end =
+        w.net.kind == MODEL_TWO_TOWER ? uint64_t(w.row_cfg.size()) : uint64_t(rows) * w.net.heads;
     for (int p = 0; p < 2; p++)
         for (const LeafRec& r : w.leaf_rec[p])
-            if (r.out >= w.vals_len || uint64_t(r.head) >= uint64_t(rows) * w.net.heads || r.mass >= 2 * rows)
+            if (r.out >= w.vals_len || uint64_t(r.head) >= heads_end || r.mass >= 2 * rows ||
+                (w.net.kind == MODEL_TWO_TOWER &&
+                 (r.mass != 2 * (r.mass >> 1) + uint32_t(1 - p) || r.head < w.row_cfg_off[r.mass - (1 - p) + p] ||
+                  r.head >= w.row_cfg_off[r.mass - (1 - p) + p + 1])))
                 return fail("leaf record");
     // The subtree sweep keeps each unit's values in LDS: every slot a unit
     // writes (its leaves, its rows) and reads (its rows' children) must lie

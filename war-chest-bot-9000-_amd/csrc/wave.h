@@ -85,7 +85,10 @@ static_assert(sizeof(UnitDev) == 20 * 4, "UnitDev is 80 bytes");
 
 // One network-leaf value slot of the traverser: vals[out] = head_out[head] * mass[mass]
 // (the net's value of the slot's config times the opponent's reach mass);
-// exported = 1 when the slot is read outside its unit.
+// exported = 1 when the slot is read outside its unit. head is row * heads +
+// the config's head row for the MLP; for the two-tower net, whose readout
+// gives one value per (row, config), it is the config's position in
+// row_cfg (row_cfg_off[2 row + p] + c).
 struct LeafRec {
     uint32_t out, head, mass, exported;
 };
@@ -128,6 +131,7 @@ struct WaveHost {
     std::vector<uint32_t> row_node, row_cfg_off, row_cfg;
     std::vector<uint32_t> cfg_key;  // head row of each interned config
     std::vector<float> cfg_emb;     // [ncfg, pool]
+    std::vector<float> cfg_priv;    // [ncfg, priv_in] private-tower features (two-tower net)
     std::vector<uint8_t> pub_raw;   // [rows, row_bytes]
     // Head columns each 128-row tile of the network rows needs: 1 + the largest
     // head key among the tile's configs (the head GEMM skips the rest).
