@@ -63,7 +63,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--workload", default="wave256", choices=["wave64", "wave256"])
+    ap.add_argument("--workload", default="wave256", choices=["wave64", "wave256", "wave512w"],
+                    help="wave256: 256 depth-2 subgames, f16 MLP (the headline); wave512w: 512 subgames with 10%% "
+                         "whales, 128 iterations, bf16 two-tower net")
     ap.add_argument("--cpu-trees", type=int, default=0, help="trees in the CPU-baseline sample (0 = 2 per thread)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-mlp", action="store_true", help="skip the GEMM-chain-alone leg")
@@ -88,7 +90,8 @@ def main():
     st = wave.stats()
     log(f"[bench] wave: {st['nodes']} nodes, {st['cells']} cells, {st['rows']} leaf rows, {st['levels']} levels")
 
-    ex = ww.Executor(0, ww.WC_F16)
+    tower = args.workload == "wave512w"
+    ex = ww.Executor(0, ww.WC_BF16 if tower else ww.WC_F16)
     ver = ex.publish(net)
     wave_ms, parts = ex.time_wave(wave, ver, reps=args.steps, warmup=args.warmup)
     log(f"[bench] {args.steps} timed waves: {wave_ms:.3f} ms/wave; per class {parts}")
@@ -131,11 +134,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 CFR state, f16 leaf-net operands (f32 accumulate)",
+        "dtype": "f32 CFR state, %s leaf-net operands (f32 accumulate)" % ("bf16" if tower else "f16"),
         "data": "synthetic (seeded subgames and Kaiming-normal random-init value net)",
         "config": {
-            "workload": f"wave of {st['jobs']} depth-2 DCFR subgames, {iters} iterations, 512->3x384->567 f16 "
-                        f"value net ({args.workload})",
+            "workload": (f"wave of {st['jobs']} depth-2 DCFR subgames (10% whales: 2,000 nodes, 567 infostates), "
+                         f"{iters} iterations, bf16 two-tower value net 512->2x512 public, 96->2x512 private "
+                         f"({args.workload})") if tower else
+                        (f"wave of {st['jobs']} depth-2 DCFR subgames, {iters} iterations, 512->3x384->567 f16 "
+                         f"value net ({args.workload})"),
             "trees": st["jobs"], "nodes": st["nodes"], "legal_cells": st["cells"], "leaf_rows": st["rows"],
             "iters": iters, "sweep_units": st["units"], "top_levels": st["top_levels"],
             "parallelism": "1 GPU; subgames cut into subtree units, one workgroup per unit",
@@ -155,7 +161,8 @@ def main():
                                  "frac": round(mlp_tflops_in_wave / MFMA_F16_PEAK_TFLOPS, 5),
                                  "flops_per_pass": st["mlp_flops_algorithmic"],
                                  "executed_tflops": round(mlp_exec_tflops, 2),
-                                 "note": "algorithmic = trunk + one head row per traverser config"},
+                                 "note": "public tower + one readout per (row, config) of the traverser" if tower
+                                 else "algorithmic = trunk + one head row per traverser config"},
     }
 
     if not args.no_mlp:

@@ -160,6 +160,17 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
         for (int k = 0; k < 3; k++) s->cfr_bytes_by_kernel[p][k] = cb.part[k];
     }
     const NetShape& ns = h.net;
+    if (ns.kind == MODEL_TWO_TOWER) {
+        // Per pass: the public tower over every row, plus one width-long
+        // readout per (row, config) of the traverser (averaged over both).
+        const uint64_t tower = 2ull * (uint64_t(ns.in) * ns.hidden + uint64_t(ns.layers - 1) * ns.hidden * ns.hidden);
+        s->mlp_flops_per_query = tower + 2ull * ns.hidden;
+        const uint64_t slots = h.row_cfg.size();
+        const uint64_t tiles = h.tower_unit[0].size() + h.tower_unit[1].size();  // 64 x 64 readout tiles
+        s->mlp_flops_algorithmic = h.rows() * tower + ns.hidden * slots;
+        s->mlp_flops_executed = h.rows() * tower + tiles * TOWER_TILE * TOWER_TILE * ns.hidden;
+        return WC_OK;
+    }
     s->mlp_flops_per_query = 2ull * (uint64_t(ns.in) * ns.hidden + uint64_t(ns.layers - 1) * ns.hidden * ns.hidden +
                                      uint64_t(ns.hidden) * ns.heads);
     // Executed per wave query: the trunk, plus the head columns of its 128-row tile

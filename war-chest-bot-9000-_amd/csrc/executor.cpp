@@ -246,7 +246,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
             draw_row_start, draw_to, draw_p, reach_base, vals_base, parent, rev_row_of, rev_start, rev_src, rev_cell,
             rvd_row_of, rvd_start, rvd_src, rvd_p, row_node, row_cfg_off, row_cfg, cfg_key, cfg_emb, pub_raw,
             term_node, term_util, roots, carried, exit_node, exit_coff, trees, units, bt[2], rt[2], dc[2], bl[2],
-            rl[2], cv[2], lr[2], pg[2], cfg_priv, unit_row, unit_term, tb[2], tr[2], head_tile_n;
+            rl[2], cv[2], lr[2], pg[2], twb[2], twu[2], cfg_priv, unit_row, unit_term, tb[2], tr[2], head_tile_n;
     } o;
     o.node_meta = blob.put(w.node_meta);
     o.nc = blob.put(w.node_nc);
@@ -293,6 +293,8 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         o.cv[p] = blob.put(w.child_vb[p]);
         o.lr[p] = blob.put(w.leaf_rec[p]);
         o.pg[p] = blob.put(w.pool_grp[p]);
+        o.twb[p] = blob.put(w.tower_blk[p]);
+        o.twu[p] = blob.put(w.tower_unit[p]);
         o.bl[p] = blob.put(w.back_lvl[p]);
         o.rl[p] = blob.put(w.reach_lvl[p]);
     }
@@ -334,7 +336,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     const size_t ncfg = w.cfg_key.size(), pcfg = precision_ == WC_PRECISE ? ncfg : gemm_rows((uint32_t)ncfg);
     size_t m_x = mtake(prow * ns.in * esz), m_x1 = mtake(prow * ns.in * esz), m_h0 = mtake(prow * ns.hidden * esz),
            m_h1 = mtake(prow * ns.hidden * esz),
-           m_out = mtake(tower ? w.row_cfg.size() * 4 : rows * ns.heads * 4);
+           m_out = mtake(tower ? w.tower_len * 4 : rows * ns.heads * 4);
     size_t m_px = 0, m_p0 = 0, m_p1 = 0, m_f = 0;
     if (tower) {
         m_px = mtake(precision_ == WC_PRECISE ? 0 : pcfg * ns.priv_in * esz);
@@ -395,6 +397,10 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         d.pool_grp[p] = (const PoolGroup*)(T + o.pg[p]);
         d.npool[p] = (uint32_t)w.pool_grp[p].size();
         d.nleaf[p] = (uint32_t)w.leaf_rec[p].size();
+        d.tower_blk[p] = (const TowerBlock*)(T + o.twb[p]);
+        d.tower_unit[p] = (const TowerUnit*)(T + o.twu[p]);
+        d.ntower_blk[p] = (uint32_t)w.tower_blk[p].size();
+        d.ntower_unit[p] = (uint32_t)w.tower_unit[p].size();
         d.back_lvl[p] = (const uint32_t*)(T + o.bl[p]);
         d.reach_lvl[p] = (const uint32_t*)(T + o.rl[p]);
         d.ndec[p] = (uint32_t)w.decision[p].size();

@@ -62,6 +62,9 @@ struct WaveDev {
     uint32_t ndec[2], ntop_dec[2];
     uint32_t npool[2];  // pool groups of each player
     uint32_t nleaf[2];  // network-leaf slots of each player (leaf_rec entries)
+    const TowerBlock* tower_blk[2];  // two-tower readout blocks and tiles of each player
+    const TowerUnit* tower_unit[2];
+    uint32_t ntower_blk[2], ntower_unit[2];
 };
 
 // Launchers (kernels.hip). All take the executor's stream.
@@ -125,9 +128,9 @@ bool chain_fits(uint32_t in, uint32_t hidden, uint32_t layers);
 void launch_chain(int precision, const ChainNet& net, const void* X, uint32_t rows, float* out,
                   const uint32_t* tile_n, hipStream_t s);
 // Two-tower net: F = private-tower output (ncfg rows, fragment-major 16-bit or
-// row-major f32) times the readout weight, row-major; then the readout of
-// player p's leaf slots, tv[row_cfg position] = <F[config], H[row]> + bread,
-// from the public-tower output H (fragment-major 16-bit or row-major f32).
+// row-major f32) times the readout weight, row-major; then player p's readout
+// blocks, tv[entry (row, config)] = <F[config], H[row]> + bread, from the
+// public-tower output H (fragment-major 16-bit or row-major f32).
 void launch_tower_f(int precision, const void* Hp, uint32_t width, uint32_t ncfg, const float* wread, void* F,
                     hipStream_t s);
 void launch_tower_head(const WaveDev& w, int player, int precision, const void* H, uint32_t width, const void* F,

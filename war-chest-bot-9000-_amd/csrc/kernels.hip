@@ -1132,80 +1132,111 @@ void launch_tower_f(int precision, const void* Hp, uint32_t width, uint32_t ncfg
         hipLaunchKernelGGL(k_tower_f<WC_BF16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, Hp, width, ncfg, wread, F);
 }
 
-// Float32 readout: one thread per network-leaf slot of player p, the sum from
-// b_read in k order as the CPU net forms it. tv is indexed by the slot's
-// position in row_cfg.
-__global__ __launch_bounds__(BLOCK) void k_tower_head_exact(WaveDev w, int p, const float* __restrict__ H,
-                                                          uint32_t width, const float* __restrict__ F, float bread,
-                                                          float* __restrict__ tv) {
-    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-    if (k >= w.nleaf[p]) return;
-    const LeafRec q = w.leaf_rec[p][k];
-    const uint32_t r = q.mass >> 1;  // the mass slot is 2 r + opponent
-    const float* h = H + (size_t)r * width;
-    const float* f = F + (size_t)w.row_cfg[q.head] * width;
-    float acc = bread;
-    for (uint32_t j = 0; j < width; j++) acc += f[j] * h[j];
-    tv[q.head] = acc;
+// Float32 readout: one workgroup per readout block of player p, one thread
+// per (row, config) entry, the sum from b_read in k order as the CPU net forms
+// it (engine/src/net.rs:844-853 pattern: bias, then += f[k] h[k]).
+__global__ __launch_bounds__(BLOCK) void k_tower_dense_exact(WaveDev w, int p, const float* __restrict__ H,
+                                                           uint32_t width, const float* __restrict__ F, float bread,
+                                                           float* __restrict__ tv) {
+    const TowerBlock b = w.tower_blk[p][blockIdx.x];
+    const uint32_t nc = b.chi - b.clo, n = (b.r1 - b.r0) * nc;
+    for (uint32_t x = threadIdx.x; x < n; x += blockDim.x) {
+        const uint32_t r = b.r0 + x / nc, c = b.clo + x % nc;
+        const float* h = H + (size_t)r * width;
+        const float* f = F + (size_t)c * width;
+        float acc = bread;
+        for (uint32_t j = 0; j < width; j++) acc += f[j] * h[j];
+        tv[b.dbase + x] = acc;
+    }
 }
 
-// 16-bit readout on MFMA: one wavefront per pool group of player p (rows
-// sharing a config list). A = the group's rows of H (fragments gathered from
-// the fragment-major public-tower output, lanes past the group repeat its
-// first row), B = 16 configs' F rows at a time; D[row][config] + b_read goes to
-// tv[row_cfg_off[2 row + p] + config position].
-constexpr uint32_t TOWER_MAX_KS = 16;  // width <= 512
+// 16-bit readout on MFMA: one wavefront per 64 x 64 tile of a readout block,
+// 4 x 4 16x16x32 tiles over the width. A = 16-row blocks of the public-tower
+// output H (whole fragments: tile rows are 16-aligned; blocks past the tree's
+// last row re-read its last block), B = 16 configs' F rows per tile (configs
+// past the block re-read its last config). Entries outside the block are not
+// stored.
 template <int PREC>
-__global__ __launch_bounds__(BLOCK) void k_tower_head(WaveDev w, int p, const uint16_t* __restrict__ H,
-                                                    uint32_t width, const uint16_t* __restrict__ F, float bread,
-                                                    float* __restrict__ tv) {
-    const uint32_t g = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-    if (g >= w.npool[p]) return;  // wave-uniform
+__global__ __launch_bounds__(BLOCK) void k_tower_dense(WaveDev w, int p, const uint16_t* __restrict__ H,
+                                                     uint32_t width, const uint16_t* __restrict__ F, float bread,
+                                                     float* __restrict__ tv) {
+    const uint32_t k = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    if (k >= w.ntower_unit[p]) return;  // wave-uniform
     const uint32_t lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
-    const PoolGroup* grp = w.pool_grp[p] + g;
-    const uint32_t n = grp->n, G = grp->nrows, ks = width >> 5;
-    const uint32_t arow = grp->row[i < G ? i : 0];
-    uint4 a[TOWER_MAX_KS];
+    const TowerUnit u = w.tower_unit[p][k];
+    const TowerBlock b = w.tower_blk[p][u.block];
+    const uint32_t ks = width >> 5, last_blk = (b.r1 - 1) & ~15u;
+    const uint16_t* ap[4];
+    const uint16_t* bp[4];
 #pragma unroll
-    for (uint32_t s = 0; s < TOWER_MAX_KS; s++)
-        if (s < ks) a[s] = *(const uint4*)(H + frag_off(arow, 32 * s + 8 * q, width));
-    const uint32_t* cfgs = w.row_cfg + grp->cfg;
-    uint32_t orow[4];
+    for (int t = 0; t < 4; t++) {
+        const uint32_t rb = min(u.row + 16 * t, last_blk);
+        ap[t] = H + ((size_t)(rb >> 4) * ks * 64 + lane) * 8;  // fragment (block, step) at + step * 512
+        const uint32_t c = min(u.cfg + 16 * t + i, b.chi - 1);
+        bp[t] = F + (size_t)c * width + 8 * q;  // this lane's 8 columns of step s at + 32 s
+    }
+    float4v acc[4][4];
 #pragma unroll
-    for (uint32_t v = 0; v < 4; v++) orow[v] = 4 * q + v < G ? w.row_cfg_off[2 * grp->row[4 * q + v] + p] : 0u;
-    for (uint32_t c0 = 0; c0 < n; c0 += 16) {
-        const uint32_t c = c0 + i;
-        const uint16_t* fb = F + (size_t)cfgs[c < n ? c : n - 1] * width + 8 * q;
-        uint4 b[TOWER_MAX_KS];
+    for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (uint32_t s = 0; s < TOWER_MAX_KS; s++)
-            if (s < ks) b[s] = *(const uint4*)(fb + 32 * s);
-        float4v acc = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < 4; c++) acc[a][c] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    uint4 fa[4], fb[4], na[4], nb[4];
+    auto load = [&](uint4 (&xa)[4], uint4 (&xb)[4], uint32_t s) {
 #pragma unroll
-        for (uint32_t s = 0; s < TOWER_MAX_KS; s++)
-            if (s < ks) acc = mfma_step16<PREC>(a[s], b[s], acc);
-        if (c < n)
+        for (int t = 0; t < 4; t++) {
+            xa[t] = *(const uint4*)(ap[t] + (size_t)s * 512);
+            xb[t] = *(const uint4*)(bp[t] + 32 * s);
+        }
+    };
+    auto step = [&](const uint4 (&xa)[4], const uint4 (&xb)[4]) {
 #pragma unroll
-            for (uint32_t v = 0; v < 4; v++)
-                if (4 * q + v < G) tv[orow[v] + c] = acc[v] + bread;
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[a][c] = mfma_step16<PREC>(xa[a], xb[c], acc[a][c]);
+    };
+    load(fa, fb, 0);
+    uint32_t s = 0;
+    for (; s + 2 <= ks; s += 2) {
+        load(na, nb, s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        step(fa, fb);
+        __builtin_amdgcn_sched_barrier(0);
+        load(fa, fb, s + 2 < ks ? s + 2 : s + 1);  // past the end: re-read a valid step, unused
+        __builtin_amdgcn_sched_barrier(0);
+        step(na, nb);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (s < ks) step(fa, fb);
+    const uint32_t nc = b.chi - b.clo;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t cfg = u.cfg + 16 * c + i;
+        if (cfg >= b.chi) continue;
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const uint32_t r = u.row + 16 * a + 4 * q + v;
+                if (r >= b.r0 && r < b.r1) tv[b.dbase + (r - b.r0) * nc + (cfg - b.clo)] = acc[a][c][v] + bread;
+            }
     }
 }
 
 void launch_tower_head(const WaveDev& w, int player, int precision, const void* H, uint32_t width, const void* F,
                        float bread, float* tv, hipStream_t s) {
     if (precision == WC_PRECISE) {
-        if (w.nleaf[player])
-            hipLaunchKernelGGL(k_tower_head_exact, dim3(grid_for(w.nleaf[player])), dim3(BLOCK), 0, s, w, player,
+        if (w.ntower_blk[player])
+            hipLaunchKernelGGL(k_tower_dense_exact, dim3(w.ntower_blk[player]), dim3(BLOCK), 0, s, w, player,
                                (const float*)H, width, (const float*)F, bread, tv);
         return;
     }
-    if (!w.npool[player]) return;
-    dim3 g(grid_for((size_t)w.npool[player] * 64));
+    if (!w.ntower_unit[player]) return;
+    dim3 g(grid_for((size_t)w.ntower_unit[player] * 64));
     if (precision == WC_F16)
-        hipLaunchKernelGGL(k_tower_head<WC_F16>, g, dim3(BLOCK), 0, s, w, player, (const uint16_t*)H, width,
+        hipLaunchKernelGGL(k_tower_dense<WC_F16>, g, dim3(BLOCK), 0, s, w, player, (const uint16_t*)H, width,
                            (const uint16_t*)F, bread, tv);
     else
-        hipLaunchKernelGGL(k_tower_head<WC_BF16>, g, dim3(BLOCK), 0, s, w, player, (const uint16_t*)H, width,
+        hipLaunchKernelGGL(k_tower_dense<WC_BF16>, g, dim3(BLOCK), 0, s, w, player, (const uint16_t*)H, width,
                            (const uint16_t*)F, bread, tv);
 }
 

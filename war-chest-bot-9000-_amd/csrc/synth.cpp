@@ -7,10 +7,14 @@
 #include "synth.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <deque>
+#include <exception>
 #include <map>
+#include <mutex>
 #include <stdexcept>
+#include <thread>
 
 namespace wc {
 
@@ -549,14 +553,33 @@ std::vector<Job> synth_jobs(const SynthSpec& spec) {
     std::string err;
     if (!ns.parse(spec.net_dims, &err)) throw std::runtime_error(err);
     if (ns.kind == MODEL_V5) throw std::runtime_error("synthetic jobs need a synthetic value-net tag");
+    // Tree k's stream is the k-th draw of the master stream, so the trees are
+    // independent and built on several host threads.
     Rng master(spec.seed);
-    std::vector<Job> jobs;
-    jobs.reserve(spec.trees);
-    for (uint32_t k = 0; k < spec.trees; k++) {
-        Rng r(master.next());
-        bool whale = spec.whale_frac > 0.0f && r.unit() < spec.whale_frac;
-        jobs.push_back(build_job(r, spec, ns, whale));
-    }
+    std::vector<uint64_t> seeds(spec.trees);
+    for (uint32_t k = 0; k < spec.trees; k++) seeds[k] = master.next();
+    std::vector<Job> jobs(spec.trees);
+    std::atomic<uint32_t> next{0};
+    std::exception_ptr failure;
+    std::mutex failure_mu;
+    auto work = [&]() {
+        for (uint32_t k; (k = next.fetch_add(1)) < spec.trees;) {
+            try {
+                Rng r(seeds[k]);
+                bool whale = spec.whale_frac > 0.0f && r.unit() < spec.whale_frac;
+                jobs[k] = build_job(r, spec, ns, whale);
+            } catch (...) {
+                std::lock_guard<std::mutex> g(failure_mu);
+                if (!failure) failure = std::current_exception();
+            }
+        }
+    };
+    const uint32_t threads = std::max(1u, std::min({std::thread::hardware_concurrency(), 16u, spec.trees}));
+    std::vector<std::thread> pool;
+    for (uint32_t t = 1; t < threads; t++) pool.emplace_back(work);
+    work();
+    for (auto& t : pool) t.join();
+    if (failure) std::rethrow_exception(failure);
     return jobs;
 }
 

@@ -138,6 +138,16 @@ void build_records(WaveHost* wp) {
         // Network-leaf slots, unit by unit (the value sweep writes them first).
         const uint32_t heads = w.net.heads;
         const bool tower = w.net.kind == MODEL_TWO_TOWER;
+        std::vector<uint32_t> row_blk;  // two-tower: each row's readout block for p
+        if (tower) {
+            row_blk.assign(w.rows(), NONE);
+            for (uint32_t bi = 0; bi < w.tower_blk[p].size(); bi++)
+                for (uint32_t r = w.tower_blk[p][bi].r0; r < w.tower_blk[p][bi].r1; r++) row_blk[r] = bi;
+        }
+        auto tower_entry = [&](uint32_t r, uint32_t cfg) {
+            const TowerBlock& b = w.tower_blk[p][row_blk[r]];
+            return b.dbase + (r - b.r0) * (b.chi - b.clo) + (cfg - b.clo);
+        };
         for (UnitDev& u : w.units) {
             u.leaf0[p] = (uint32_t)w.leaf_rec[p].size();
             for (uint32_t k = u.row0; k < u.row1; k++) {
@@ -145,7 +155,7 @@ void build_records(WaveHost* wp) {
                 const uint32_t* cfgs = &w.row_cfg[w.row_cfg_off[2 * r + p]];
                 for (uint32_t c = 0; c < w.nc(node, p); c++)
                     w.leaf_rec[p].push_back({w.vals_base[2 * node + p] + c,
-                                             tower ? w.row_cfg_off[2 * r + p] + c : r * heads + w.cfg_key[cfgs[c]],
+                                             tower ? tower_entry(r, cfgs[c]) : r * heads + w.cfg_key[cfgs[c]],
                                              2 * r + (1 - p), 0});
             }
             u.leaf1[p] = (uint32_t)w.leaf_rec[p].size();
@@ -231,6 +241,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     std::vector<UnitDev> sub_units;
     std::vector<std::vector<Task>> top_back[2], top_reach[2];
     std::vector<Task> top_dec[2];
+    std::vector<uint32_t> job_rows;  // first network row of each job
 
     for (const Job& job : jobs) {
         const Tables& t = job.t;
@@ -326,6 +337,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
         w.rvd_p.insert(w.rvd_p.end(), t.rvd_p.begin(), t.rvd_p.end());
 
         // Network rows and interned configs.
+        job_rows.push_back((uint32_t)w.row_node.size());
         for (uint32_t r : t.leaf_rows) w.row_node.push_back(node0 + r);
         append_shift<uint32_t>(w.row_cfg_off, t.leaf_coff, 1, member0, false);
         append_shift<uint32_t>(w.row_cfg, t.leaf_cidx, 0, cfg0, false);
@@ -534,6 +546,36 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
                 out.push_back(g);
             }
         std::stable_sort(out.begin(), out.end(), [](const PoolGroup& a, const PoolGroup& b) { return a.n > b.n; });
+    }
+    // Two-tower readout blocks: per tree and player, its rows times the
+    // config range its rows name.
+    if (w.net.kind == MODEL_TWO_TOWER) {
+        job_rows.push_back(nrows);
+        w.tower_len = 0;
+        for (int p = 0; p < 2; p++) {
+            for (size_t t = 0; t + 1 < job_rows.size(); t++) {
+                TowerBlock b{};
+                b.r0 = job_rows[t];
+                b.r1 = job_rows[t + 1];
+                b.clo = NONE;
+                for (uint32_t r = b.r0; r < b.r1; r++)
+                    for (uint32_t x = w.row_cfg_off[2 * r + p]; x < w.row_cfg_off[2 * r + p + 1]; x++) {
+                        b.clo = std::min(b.clo, w.row_cfg[x]);
+                        b.chi = std::max(b.chi, w.row_cfg[x] + 1);
+                    }
+                if (b.clo == NONE) continue;  // no configs named by this player's rows
+                b.dbase = (uint32_t)w.tower_len;
+                w.tower_len += uint64_t(b.r1 - b.r0) * (b.chi - b.clo);
+                const uint32_t bi = (uint32_t)w.tower_blk[p].size();
+                for (uint32_t r = b.r0 / 16 * 16; r < b.r1; r += TOWER_TILE)
+                    for (uint32_t c = b.clo; c < b.chi; c += TOWER_TILE) w.tower_unit[p].push_back({bi, r, c, 0});
+                w.tower_blk[p].push_back(b);
+            }
+        }
+        if (w.tower_len >= (1ull << 32)) {
+            *err = "wave too large for the two-tower readout";
+            return false;
+        }
     }
     // Subtree units largest first: the device takes them in launch order.
     std::stable_sort(sub_units.begin(), sub_units.end(),
@@ -784,15 +826,30 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         for (const AccRec& r : w.acc_rec[p])
             if (r.ridx >= w.reach_len || uint64_t(r.lo) + r.n > w.ncells) return fail("accumulation record");
     }
-    const uint64_t heads_end =
-        w.net.kind == MODEL_TWO_TOWER ? uint64_t(w.row_cfg.size()) : uint64_t(rows) * w.net.heads;
+    const uint64_t heads_end = w.net.kind == MODEL_TWO_TOWER ? w.tower_len : uint64_t(rows) * w.net.heads;
     for (int p = 0; p < 2; p++)
         for (const LeafRec& r : w.leaf_rec[p])
-            if (r.out >= w.vals_len || uint64_t(r.head) >= heads_end || r.mass >= 2 * rows ||
-                (w.net.kind == MODEL_TWO_TOWER &&
-                 (r.mass != 2 * (r.mass >> 1) + uint32_t(1 - p) || r.head < w.row_cfg_off[r.mass - (1 - p) + p] ||
-                  r.head >= w.row_cfg_off[r.mass - (1 - p) + p + 1])))
+            if (r.out >= w.vals_len || uint64_t(r.head) >= heads_end || r.mass >= 2 * rows)
                 return fail("leaf record");
+    if (w.net.kind == MODEL_TWO_TOWER)
+        for (int p = 0; p < 2; p++) {
+            // Blocks lie inside the rows, configs and values; every row of a
+            // block names only configs of the block; every unit tiles a block.
+            for (const TowerBlock& b : w.tower_blk[p]) {
+                if (b.r0 >= b.r1 || b.r1 > rows || b.clo >= b.chi || b.chi > ncfg ||
+                    uint64_t(b.dbase) + uint64_t(b.r1 - b.r0) * (b.chi - b.clo) > w.tower_len)
+                    return fail("tower block");
+                for (uint32_t r = b.r0; r < b.r1; r++)
+                    for (uint32_t x = w.row_cfg_off[2 * r + p]; x < w.row_cfg_off[2 * r + p + 1]; x++)
+                        if (w.row_cfg[x] < b.clo || w.row_cfg[x] >= b.chi) return fail("tower block configs");
+            }
+            for (const TowerUnit& u : w.tower_unit[p]) {
+                if (u.block >= w.tower_blk[p].size()) return fail("tower unit");
+                const TowerBlock& b = w.tower_blk[p][u.block];
+                if (u.row % 16 || u.row + 16 <= b.r0 || u.row >= b.r1 || u.cfg < b.clo || u.cfg >= b.chi)
+                    return fail("tower unit");
+            }
+        }
     // The subtree sweep keeps each unit's values in LDS: every slot a unit
     // writes (its leaves, its rows) and reads (its rows' children) must lie
     // inside the unit's window.

@@ -87,11 +87,25 @@ static_assert(sizeof(UnitDev) == 20 * 4, "UnitDev is 80 bytes");
 // (the net's value of the slot's config times the opponent's reach mass);
 // exported = 1 when the slot is read outside its unit. head is row * heads +
 // the config's head row for the MLP; for the two-tower net, whose readout
-// gives one value per (row, config), it is the config's position in
-// row_cfg (row_cfg_off[2 row + p] + c).
+// gives one value per (row, config), it is the (row, config) entry of the
+// tree's readout block for the player (TowerBlock).
 struct LeafRec {
     uint32_t out, head, mass, exported;
 };
+
+// Two-tower readout, block-diagonal by tree: per (tree, player), the tree's
+// network rows [r0, r1) times the configs [clo, chi) the player's rows name,
+// computed densely into tower values at dbase + (row - r0) (chi - clo) +
+// (config - clo). A unit is one 64 x 64 tile of a block: rows from `row`
+// (16-aligned, so whole fragment blocks; rows outside the block are not
+// stored), configs from `cfg`.
+struct TowerBlock {
+    uint32_t r0, r1, clo, chi, dbase, pad[3];
+};
+struct TowerUnit {
+    uint32_t block, row, cfg, pad;
+};
+constexpr uint32_t TOWER_TILE = 64;
 
 // Network rows whose configs for one player are the same list, pooled by one
 // wavefront of the 16-bit nets: every config's embedding is read once for all
@@ -169,6 +183,10 @@ struct WaveHost {
     std::vector<AccRec> acc_rec[2];
     std::vector<LeafRec> leaf_rec[2];  // unit-major network-leaf slots
     std::vector<PoolGroup> pool_grp[2];  // network rows grouped by config list, longest lists first
+    // Two-tower readout blocks and their tiles, per player; tower_len floats of values.
+    std::vector<TowerBlock> tower_blk[2];
+    std::vector<TowerUnit> tower_unit[2];
+    uint64_t tower_len = 0;
     std::vector<uint32_t> child_vb[2];  // child value bases of the opponent rows
 
     uint32_t nodes() const { return (uint32_t)node_meta.size(); }
