@@ -571,10 +571,10 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         mark(C_MLP);
     };
     // Top regions, one depth per launch: values bottom-up, reach top-down.
-    auto top_back = [&](int p, int mode, float da, float db, float ds, float pr) {
+    auto top_back = [&](int p, int mode, float da, float db, float pr) {
         for (uint32_t l = w.top_levels; l-- > 0;) {
             uint32_t b = w.top_back_lvl[p][l], e = w.top_back_lvl[p][l + 1];
-            launch_back_rows(d, top_back_dev_[p] + b, e - b, p, mode, da, db, ds, pr, s);
+            launch_back_rows(d, top_back_dev_[p] + b, e - b, p, mode, da, db, pr, s);
         }
     };
     auto top_reach = [&](int p, float* reach, const float* strat) {  // p < 0: both players
@@ -587,7 +587,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     // Both players' reach under a fixed strategy: tops first, then their subtrees.
     auto reach_both = [&](float* reach, const float* strat) {
         top_reach(-1, reach, strat);
-        launch_reach(d, 0, nsub, reach, strat, -1, false, s);
+        launch_reach(d, 0, nsub, reach, strat, -1, false, 1.0f, s);
     };
 
     if (tower) run_tower_private(bank);  // F for this wave's configs under this bank
@@ -606,12 +606,12 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         const float mm = (float)(t / 2 + 1);
         const float da = cfr_factor(mm, m.cfr.alpha), db = cfr_factor(mm, m.cfr.beta);
         const float ds = std::pow(mm / (mm + 1.0f), m.cfr.gamma);
-        launch_sweep(d, 0, nsub, head_out_, bank.ns.heads, p, MODE_REGRET, da, db, ds, m.cfr.predict, s);
+        launch_sweep(d, 0, nsub, head_out_, bank.ns.heads, p, MODE_REGRET, da, db, m.cfr.predict, s);
         mark(C_BACK);
-        top_back(p, MODE_REGRET, da, db, ds, m.cfr.predict);
+        top_back(p, MODE_REGRET, da, db, m.cfr.predict);
         top_reach(p, d.reach, d.cur);
         mark(C_TOP);
-        launch_reach(d, 0, nsub, d.reach, d.cur, p, true, s);
+        launch_reach(d, 0, nsub, d.reach, d.cur, p, true, ds, s);
         mark(C_REACH);
         launch_pool(d, p, precision_, Xq_[0], Xq_[1], s);
         mark(C_LEAF);
@@ -637,8 +637,8 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         mark(C_LEAF);
         for (int p = 0; p < 2; p++) {
             mlp(p);
-            launch_sweep(d, 0, nsub, head_out_, bank.ns.heads, p, MODE_VALUE, 0.0f, 0.0f, 0.0f, 0.0f, s);
-            top_back(p, MODE_VALUE, 0.0f, 0.0f, 0.0f, 0.0f);
+            launch_sweep(d, 0, nsub, head_out_, bank.ns.heads, p, MODE_VALUE, 0.0f, 0.0f, 0.0f, s);
+            top_back(p, MODE_VALUE, 0.0f, 0.0f, 0.0f);
             launch_collect_root(d, (int)root, p, s);
             mark(C_OTHER);
         }

@@ -72,10 +72,10 @@ void launch_zero(float* p, size_t n, hipStream_t s);
 void launch_init_strategy(const WaveDev& w, hipStream_t s);
 void launch_seed_reach(const WaveDev& w, float* reach, int root_index, hipStream_t s);
 // Top-down reach of subtree units [unit0, unit0 + n) under `strat`, for one
-// player or both (player < 0); with `accumulate`, then sum += reach * cur over
-// the player's decision rows of each unit and of the top regions.
+// player or both (player < 0); with `accumulate`, then sum = sum * ds + reach *
+// cur over the player's decision rows of each unit and of the top regions.
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
-                  bool accumulate, hipStream_t s);
+                  bool accumulate, float ds, hipStream_t s);
 // Top-region reach at one depth (rows of player 0 and of player 1).
 void launch_reach_rows(const WaveDev& w, const ReachRec* r0, uint32_t n0, const ReachRec* r1, uint32_t n1,
                        float* reach, const float* strat, hipStream_t s);
@@ -87,10 +87,10 @@ void launch_pool(const WaveDev& w, int player, int precision, void* x0, void* x1
 void launch_query_static(const WaveDev& w, int precision, void* x0, void* x1, hipStream_t s);
 // Leaf values and the bottom-up sweep of subtree units [unit0, unit0 + n) for the traverser.
 void launch_sweep(const WaveDev& w, uint32_t unit0, uint32_t n, const float* head_out, uint32_t heads, int traverser,
-                  int mode, float da, float db, float ds, float predict, hipStream_t s);
+                  int mode, float da, float db, float predict, hipStream_t s);
 // Top-region values at one depth for the traverser.
 void launch_back_rows(const WaveDev& w, const BackRec* rows, uint32_t n, int traverser, int mode, float da,
-                      float db, float ds, float predict, hipStream_t s);
+                      float db, float predict, hipStream_t s);
 void launch_normalize(const WaveDev& w, int touched0, int touched1, hipStream_t s);
 void launch_gather_carry(const WaveDev& w, const float* reach, int slot, hipStream_t s);
 void launch_collect_root(const WaveDev& w, int root, int player, hipStream_t s);

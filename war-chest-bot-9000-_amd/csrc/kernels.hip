@@ -90,7 +90,7 @@ void launch_seed_reach(const WaveDev& w, float* reach, int root_index, hipStream
 // Row elements are handled ROW_BATCH at a time: a batch's loads are issued
 // together (indices, then the values they name) and its part of the reduction
 // is taken after, in element order, so every sum keeps the CPU's order.
-constexpr uint32_t ROW_BATCH = 16;   // value rows: decision rows up to 16 actions in one pass
+constexpr uint32_t ROW_BATCH = 12;   // value rows: decision rows up to 12 actions in one pass
 constexpr uint32_t REACH_BATCH = 8;  // reach gathers and average accumulation
 // Network-leaf slots in flight per thread in the sweep's leaf phase.
 constexpr uint32_t LEAF_BATCH = 4;
@@ -143,8 +143,11 @@ __device__ __forceinline__ void reach_row(const WaveDev& w, float* reach, const 
     reach[q.out] = v;
 }
 
-// sum += reach * cur over one decision row (engine/src/search.rs:1818-1835).
-__device__ __forceinline__ void accumulate_row(const WaveDev& w, AccRec q) {
+// sum = sum * ds + reach * cur over one decision row: the DCFR discount of the
+// traverser's average-strategy sum (search.rs:1770-1779, applied at the
+// backprop) and this iteration's accumulation (engine/src/search.rs:1818-1835),
+// the same two rounded steps in the same order, taken in one pass.
+__device__ __forceinline__ void accumulate_row(const WaveDev& w, AccRec q, float ds) {
     const float r = w.reach[q.ridx];
     const uint32_t lo = q.lo, n = q.n;
     for (uint32_t c0 = 0; c0 < n; c0 += REACH_BATCH) {
@@ -158,13 +161,14 @@ __device__ __forceinline__ void accumulate_row(const WaveDev& w, AccRec q) {
             }
 #pragma unroll
         for (uint32_t j = 0; j < REACH_BATCH; j++)
-            if (j < m) w.sum[lo + c0 + j] = sm[j] + r * cu[j];
+            if (j < m) w.sum[lo + c0 + j] = sm[j] * ds + r * cu[j];
     }
 }
 
 // Average-strategy accumulation over one unit's decision rows of player p.
-__device__ __forceinline__ void accumulate_unit(const WaveDev& w, const UnitDev& u, int p) {
-    for (uint32_t k = u.dec0[p] + threadIdx.x; k < u.dec1[p]; k += blockDim.x) accumulate_row(w, w.acc_rec[p][k]);
+__device__ __forceinline__ void accumulate_unit(const WaveDev& w, const UnitDev& u, int p, float ds) {
+    for (uint32_t k = u.dec0[p] + threadIdx.x; k < u.dec1[p]; k += blockDim.x)
+        accumulate_row(w, w.acc_rec[p][k], ds);
 }
 
 // Top-down reach of one unit, level by level under block barriers: player p
@@ -219,10 +223,10 @@ __device__ __forceinline__ void reach_unit_one(const WaveDev& w, const UnitDev& 
 // decision rows, and the blocks past the units accumulate the top regions'
 // decision rows, one row per thread (their reach is final by then).
 __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, uint32_t nunits, float* reach,
-                                               const float* strat, int player, int accumulate) {
+                                               const float* strat, int player, int accumulate, float ds) {
     if (blockIdx.x >= nunits) {
         const uint32_t k = (blockIdx.x - nunits) * blockDim.x + threadIdx.x;
-        if (k < w.ntop_dec[player]) accumulate_row(w, w.top_acc[player][k]);
+        if (k < w.ntop_dec[player]) accumulate_row(w, w.top_acc[player][k], ds);
         return;
     }
     const UnitDev u = w.units[unit0 + blockIdx.x];
@@ -230,15 +234,15 @@ __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, uint
         reach_unit(w, u, reach, strat, player);
     else
         reach_unit_one(w, u, reach, strat, player);
-    if (accumulate) accumulate_unit(w, u, player);
+    if (accumulate) accumulate_unit(w, u, player, ds);
 }
 
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
-                  bool accumulate, hipStream_t s) {
+                  bool accumulate, float ds, hipStream_t s) {
     uint32_t extra = accumulate ? grid_for(w.ntop_dec[player]) : 0;
     if (n + extra)
         hipLaunchKernelGGL(k_reach, dim3(n + extra), dim3(BLOCK), 0, s, w, unit0, n, reach, strat, player,
-                           accumulate ? 1 : 0);
+                           accumulate ? 1 : 0, ds);
 }
 
 // Top-region reach at one depth, all trees together: one row per thread.
@@ -541,8 +545,8 @@ void launch_query_static(const WaveDev& w, int precision, void* x0, void* x1, hi
 // Values come from the unit's LDS window when LDSV (slot i at lv[i - vw]),
 // else from HBM; results go to both.
 template <int MODE, bool LDSV>
-__device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q, float da, float db, float ds,
-                                             float predict, const float* strat, float* lv, uint32_t vw) {
+__device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q, float da, float db, float predict,
+                                             const float* strat, float* lv, uint32_t vw) {
     float* vals = w.vals;
     // A staged unit keeps its values in LDS; only values read outside the
     // unit (REC_EXPORT) also go to HBM.
@@ -600,20 +604,18 @@ __device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q,
     // The traverser's own row: base = sum of child value x strategy in action
     // order, then the fused regret matching with DCFR discounting
     // (search.rs:1742-1779): r = old (old > 0 ? da : db) + delta, cur = max(r +
-    // predict delta, EPS), normalised by a reciprocal multiply, sum *= ds.
+    // predict delta, EPS), normalised by a reciprocal multiply. The sum's
+    // discount (sum *= ds) is taken with the accumulation in the reach sweep.
     const float* st = MODE == MODE_VALUE ? strat : w.cur;
     if (n <= ROW_BATCH) {  // one batch: everything stays in registers
         uint32_t lvi[ROW_BATCH];
-        float sv[ROW_BATCH], qv[ROW_BATCH], old[ROW_BATCH], sm[ROW_BATCH];
+        float sv[ROW_BATCH], qv[ROW_BATCH], old[ROW_BATCH];
 #pragma unroll
         for (uint32_t k = 0; k < ROW_BATCH; k++)
             if (k < n) {
                 lvi[k] = w.legal_value[lo + k];
                 sv[k] = st[lo + k];
-                if (MODE == MODE_REGRET) {
-                    old[k] = w.regret[lo + k];
-                    sm[k] = w.sum[lo + k];
-                }
+                if (MODE == MODE_REGRET) old[k] = w.regret[lo + k];
             }
 #pragma unroll
         for (uint32_t k = 0; k < ROW_BATCH; k++)
@@ -635,7 +637,6 @@ __device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q,
                 w.regret[lo + k] = r;
                 v[k] = fmaxf(r + predict * delta, EPSF);
                 total += v[k];
-                w.sum[lo + k] = sm[k] * ds;
             }
         float inv = total > 0.0f ? 1.0f / total : 1.0f;
 #pragma unroll
@@ -669,13 +670,12 @@ __device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q,
     for (uint32_t c0 = 0; c0 < n; c0 += ROW_BATCH) {
         const uint32_t m = n - c0 < ROW_BATCH ? n - c0 : ROW_BATCH;
         uint32_t lvi[ROW_BATCH];
-        float qv[ROW_BATCH], old[ROW_BATCH], sm[ROW_BATCH];
+        float qv[ROW_BATCH], old[ROW_BATCH];
 #pragma unroll
         for (uint32_t k = 0; k < ROW_BATCH; k++)
             if (k < m) {
                 lvi[k] = w.legal_value[lo + c0 + k];
                 old[k] = w.regret[lo + c0 + k];
-                sm[k] = w.sum[lo + c0 + k];
             }
 #pragma unroll
         for (uint32_t k = 0; k < ROW_BATCH; k++)
@@ -691,7 +691,6 @@ __device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q,
                 float v = fmaxf(r + predict * delta, EPSF);
                 w.cur[lo + c0 + k] = v;
                 total += v;
-                w.sum[lo + c0 + k] = sm[k] * ds;
             }
     }
     if (total > 0.0f) {
@@ -715,7 +714,7 @@ __device__ __forceinline__ void backprop_row(const WaveDev& w, int p, BackRec q,
 // the fused regret/DCFR update at the traverser's rows.
 template <int MODE, bool LDSV>
 __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, const float* head_out, uint32_t heads,
-                                               int p, float da, float db, float ds, float predict) {
+                                               int p, float da, float db, float predict) {
     extern __shared__ float lds_vals[];  // the unit's value window of player p (when LDSV)
     const UnitDev u = w.units[unit0 + blockIdx.x];
     const int opp = 1 - p;
@@ -776,21 +775,21 @@ __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, cons
             if (b + threadIdx.x < e) nxt = back[b + threadIdx.x];
         }
         uint32_t k = lb + threadIdx.x;
-        if (k < le) backprop_row<MODE, LDSV>(w, p, first, da, db, ds, predict, w.snap, lds_vals, vw);
+        if (k < le) backprop_row<MODE, LDSV>(w, p, first, da, db, predict, w.snap, lds_vals, vw);
         for (k += blockDim.x; k < le; k += blockDim.x)
-            backprop_row<MODE, LDSV>(w, p, back[k], da, db, ds, predict, w.snap, lds_vals, vw);
+            backprop_row<MODE, LDSV>(w, p, back[k], da, db, predict, w.snap, lds_vals, vw);
         __syncthreads();
     }
 }
 
 void launch_sweep(const WaveDev& w, uint32_t unit0, uint32_t n, const float* head_out, uint32_t heads, int traverser,
-                  int mode, float da, float db, float ds, float predict, hipStream_t s) {
+                  int mode, float da, float db, float predict, hipStream_t s) {
     if (!n) return;
     const size_t lds = (size_t)w.max_vwin * sizeof(float);
     const bool staged = lds <= SWEEP_LDS_MAX;
 #define WC_SWEEP(M, L)                                                                                          \
     hipLaunchKernelGGL((k_sweep<M, L>), dim3(n), dim3(BLOCK), L ? lds : 0, s, w, unit0, head_out, heads, traverser, \
-                       da, db, ds, predict)
+                       da, db, predict)
     if (mode == MODE_VALUE) {
         if (staged)
             WC_SWEEP(MODE_VALUE, true);
@@ -808,20 +807,20 @@ void launch_sweep(const WaveDev& w, uint32_t unit0, uint32_t n, const float* hea
 // Top-region values at one depth, all trees together: one row per thread.
 template <int MODE>
 __global__ __launch_bounds__(BLOCK) void k_back_rows(WaveDev w, const BackRec* rows, uint32_t n, int p, float da,
-                                                   float db, float ds, float predict) {
+                                                   float db, float predict) {
     uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-    if (k < n) backprop_row<MODE, false>(w, p, rows[k], da, db, ds, predict, w.snap, nullptr, 0);
+    if (k < n) backprop_row<MODE, false>(w, p, rows[k], da, db, predict, w.snap, nullptr, 0);
 }
 
 void launch_back_rows(const WaveDev& w, const BackRec* rows, uint32_t n, int traverser, int mode, float da,
-                      float db, float ds, float predict, hipStream_t s) {
+                      float db, float predict, hipStream_t s) {
     if (!n) return;
     if (mode == MODE_VALUE)
         hipLaunchKernelGGL(k_back_rows<MODE_VALUE>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, rows, n, traverser, da,
-                           db, ds, predict);
+                           db, predict);
     else
         hipLaunchKernelGGL(k_back_rows<MODE_REGRET>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, rows, n, traverser, da,
-                           db, ds, predict);
+                           db, predict);
 }
 
 // Average strategy: sum / row sum, uniform when the sum is not positive, the
