@@ -110,18 +110,36 @@ def main():
         gbs = nbytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
         by_kernel[name] = {"launch_ms": round(ms, 5), "bytes_per_launch": int(nbytes), "achieved_gbs": round(gbs, 2),
                            "frac": round(gbs / HBM_PEAK_GBS, 5)}
-    # The roofline names one kernel: the single-launch CFR kernel with the longest launch.
-    dominant = max(("k_sweep<regret>", "k_reach"), key=lambda n: by_kernel[n]["launch_ms"])
     bytes_per_iter = 0.5 * (st["cfr_bytes_per_iter"][0] + st["cfr_bytes_per_iter"][1])
     iter_gbs = bytes_per_iter / (iter_ms * 1e-3) / 1e9
     passes = iters + 2 * st["nroots_max"]  # leaf-net passes per wave
     mlp_flops_wave = st["mlp_flops_algorithmic"] * passes
     mlp_tflops_in_wave = mlp_flops_wave / (mlp_ms * 1e-3) / 1e12 if mlp_ms > 0 else 0.0
     mlp_exec_tflops = st["mlp_flops_executed"] * passes / (mlp_ms * 1e-3) / 1e12 if mlp_ms > 0 else 0.0
-    d = by_kernel[dominant]
-    trace_name = {"k_sweep<regret>": "wc::k_sweep<0, %s>" % ("true" if st["max_window"] * 4 <= 65536 else "false"),
-                  "k_reach": "wc::k_reach"}[dominant]
-    traffic = measured_traffic(args.workload, trace_name)
+    # The roofline names one kernel: the one with the most device time per wave
+    # among the subtree sweep, the subtree reach and the value net.
+    net_name = "two-tower net (k_gemm layers + k_tower_dense)" if tower else "k_chain"
+    per_wave = {"k_sweep<regret>": back_ms * iters, "k_reach": reach_ms * iters, net_name: mlp_ms}
+    dominant = max(per_wave, key=per_wave.get)
+    if dominant == net_name:
+        launch_ms = mlp_ms / passes
+        flops = st["mlp_flops_algorithmic"]
+        tf = flops / (launch_ms * 1e-3) / 1e12
+        trace_name = "wc::k_chain<1>"
+        roofline = {"bound": "mfma", "kernel": dominant, "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 5), "flops_per_launch": flops,
+                    "launch_ms": round(launch_ms, 5)}
+    else:
+        d = by_kernel[dominant]
+        trace_name = {"k_sweep<regret>": "wc::k_sweep<0, %s>" % ("true" if st["max_window"] * 4 <= 65536 else "false"),
+                      "k_reach": "wc::k_reach"}[dominant]
+        roofline = {"bound": "hbm", "kernel": dominant, "achieved": d["achieved_gbs"], "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": d["frac"], "bytes_per_launch": d["bytes_per_launch"],
+                    "launch_ms": d["launch_ms"]}
+    traffic = measured_traffic(args.workload, trace_name) if not tower else None
+    roofline["traffic"] = traffic
+    roofline["traffic_source"] = f"profiles/{args.workload}_hbm_traffic.md ({trace_name})" if traffic else None
+    roofline["ms_per_wave"] = round(per_wave[dominant], 4)
 
     out = {
         "metric": "CFR node-iters/sec + value-net leaf queries/sec on 1 MI355X; % HBM/MFMA peak",
@@ -149,10 +167,7 @@ def main():
         "leaf_queries_per_s": round(queries / (wave_ms * 1e-3), 1),
         "ms_by_class": {"cfr": round(cfr_ms, 4), "mlp": round(mlp_ms, 4), "leaf_input": round(leaf_ms, 4),
                         "other": round(other_ms, 4)},
-        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": d["achieved_gbs"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": d["frac"], "traffic": traffic, "bytes_per_launch": d["bytes_per_launch"],
-                     "launch_ms": d["launch_ms"],
-                     "traffic_source": f"profiles/{args.workload}_hbm_traffic.md ({trace_name})" if traffic else None},
+        "roofline": roofline,
         "roofline_cfr_iteration": {"bound": "hbm", "kernels": by_kernel, "achieved": round(iter_gbs, 2),
                                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(iter_gbs / HBM_PEAK_GBS, 5),
                                    "bytes_per_iter": int(bytes_per_iter), "iter_ms": round(iter_ms, 5)},
