@@ -28,10 +28,15 @@ extern "C" {
 /* Leaf-net arithmetic. PRECISE reproduces the CPU net's float32 loop order
  * exactly (the reference's oracle mode, engine/src/gpu/device.rs:375-402);
  * F16/BF16 run the MFMA GEMM chain with f32 accumulation (the reference's
- * fast mode, CUBLAS_COMPUTE_32F_FAST_16F). */
+ * fast mode, CUBLAS_COMPUTE_32F_FAST_16F). F16X (no counterpart in the
+ * reference) is compensated f16: every operand is held as an f16 pair
+ * hi + lo and every product as three f16 MFMAs (hi hi + hi lo + lo hi) with
+ * f32 accumulation, near float32 accuracy on the f16 matrix cores; MLP only,
+ * layer by layer. */
 #define WC_PRECISE 0
 #define WC_F16 1
 #define WC_BF16 2
+#define WC_F16X 3
 
 /* Thread-local text of the last failure on this thread. */
 const char* wc_last_error(void);

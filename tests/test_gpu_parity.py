@@ -228,7 +228,7 @@ def test_wave64_f16_fast_mode_tracks_exact_math():
     activations alone (2^-12 relative) moves some trees' root values by up to
     1e-2 after 64 iterations, in the CPU emulation of f16 operands as much as
     on the device. Root values are therefore bounded here at 2e-2 of the tree's
-    largest root value; the compensated-f16 mode carries the 2e-3 bound."""
+    largest root value; compensated f16 (WC_F16X) holds the 2e-3 bound below."""
     jobs = W.jobs("wave64", trees=12)
     net = W.net_for("wave64")
     say(f"case wave64 f16: {len(jobs)} trees, 64 iterations")
@@ -277,6 +277,39 @@ def test_two_tower_bf16_tracks_reduced_precision_oracle():
         scale = np.abs(ref["roots"]).max()
         rel = np.abs(g.root_values - ref["roots"]).max() / scale
         assert rel <= 2e-2, f"tree {k}: root values {rel:.2e} of the largest root value"
+        say(f"tree {k}: mean strategy error {mean_s:.2e}, root error {rel:.2e} of max |root|")
+
+
+def test_mlp_compensated_f16_tracks_float32():
+    """Compensated f16 (hi + lo operand pairs, three MFMAs per product) against
+    the float32 CPU net."""
+    net = W.net_for("mlp65k")
+    x = W.mlp65k_inputs(rows=1024, seed=13)
+    say("case mlp compensated f16: 1024 queries")
+    ex = executor(ww.WC_F16X)
+    v = ex.publish(net)
+    got = ex.mlp(v, x, heads=64)
+    keys = np.tile(np.arange(64, dtype=np.uint32), (x.shape[0], 1))
+    ref = O.mlp(x, keys, net, O.NET_F32)
+    scale = np.abs(ref).max()
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5 * scale)
+
+
+def test_wave64_compensated_f16_meets_the_2e3_bound():
+    """The wave the plain-f16 test uses, in compensated f16: root values within
+    2e-3 of the tree's largest root value of the float32 CPU solver, the bound
+    the plain f16 operands cannot hold on these ill-conditioned subgames."""
+    jobs = W.jobs("wave64", trees=12)
+    net = W.net_for("wave64")
+    say(f"case wave64 compensated f16: {len(jobs)} trees, 64 iterations")
+    got = gpu_solve(jobs, net, ww.WC_F16X)
+    for k, (j, g) in enumerate(zip(jobs, got)):
+        ref = O.solve(j, net, O.NET_F32)
+        mean_s = float(np.abs(g.strategy - ref["strategy"]).mean())
+        assert mean_s <= 1e-4, f"tree {k}: mean strategy error {mean_s:.2e}"
+        scale = np.abs(ref["roots"]).max()
+        rel = np.abs(g.root_values - ref["roots"]).max() / scale
+        assert rel <= 2e-3, f"tree {k}: root values {rel:.2e} of the largest root value"
         say(f"tree {k}: mean strategy error {mean_s:.2e}, root error {rel:.2e} of max |root|")
 
 

@@ -55,7 +55,7 @@ Executor::Executor(int device, int precision) : device_(device), precision_(prec
         err_ = "device index out of range";
         return;
     }
-    if (precision < WC_PRECISE || precision > WC_BF16) {
+    if (precision < WC_PRECISE || precision > WC_F16X) {
         err_ = "unknown precision";
         return;
     }
@@ -126,6 +126,10 @@ uint64_t Executor::publish(const NetShape& ns, const std::vector<uint32_t>& dims
         *err = "weight bank sizes disagree with dims";
         return 0;
     }
+    if (tower && precision_ == WC_F16X) {
+        *err = "compensated f16 takes the MLP leaf network only";
+        return 0;
+    }
     if (precision_ != WC_PRECISE && (ns.in % 32 || ns.hidden % 32 || (tower && (ns.priv_in % 32 || ns.hidden > 512)))) {
         *err = tower ? "the MFMA path needs input, private-input and width multiples of 32 (width at most 512)"
                      : "the MFMA path needs input and hidden widths that are multiples of 32";
@@ -138,7 +142,9 @@ uint64_t Executor::publish(const NetShape& ns, const std::vector<uint32_t>& dims
     NetBank bank;
     bank.ns = ns;
     bank.precision = precision_;
-    const size_t esz = precision_ == WC_PRECISE ? 4 : 2;
+    // Bytes per stored matrix element: float32, one 16-bit value, or the
+    // compensated pair (hi and lo planes).
+    const size_t esz = precision_ == WC_PRECISE ? 4 : precision_ == WC_F16X ? 4 : 2;
     // Layout: matrices (as stored for the arithmetic), then f32 biases, then
     // the two-tower readout weight. The exact net keeps the source layout; the
     // MFMA net stores each matrix as the GEMM's B operand (one row per output,
@@ -323,8 +329,8 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     size_t a_roots = take(size_t(w.root_values_len) * 4);
     size_t a_carry = take(size_t(w.carry_slots) * w.snapshot_configs * 2);
     if (!ensure(&arena_, &arena_cap_, at, err)) return false;
-    // Leaf-network activations.
-    const size_t esz = precision_ == WC_PRECISE ? 4 : 2;
+    // Leaf-network activations (compensated f16: hi and lo planes, 4 bytes per element).
+    const size_t esz = precision_ == WC_PRECISE || precision_ == WC_F16X ? 4 : 2;
     size_t mt = 0;
     auto mtake = [&](size_t bytes) {
         size_t a = align256(mt);
@@ -433,6 +439,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     d.in = ns.in;
     d.row_bytes = ns.row_bytes;
     d.snapshot_configs = w.snapshot_configs;
+    d.xplane = uint64_t(prow) * ns.in;
     d.nexit = (uint32_t)w.exit_node.size();
     d.ncells = w.ncells;
     X_ = M + m_x;
@@ -465,7 +472,7 @@ void Executor::run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::v
             marks->push_back(e);
         }
     };
-    if (precision_ != WC_PRECISE && chain_fits(ns.in, ns.hidden, ns.layers)) {
+    if ((precision_ == WC_F16 || precision_ == WC_BF16) && chain_fits(ns.in, ns.hidden, ns.layers)) {
         ChainNet net{};
         for (uint32_t l = 0; l < ns.layers; l++) {
             net.w[l] = (const uint16_t*)bank.W[l];
@@ -756,7 +763,7 @@ bool Executor::mlp_forward(uint64_t version, uint32_t rows, const float* x, floa
         return false;
     }
     HIP_TRY(hipSetDevice(device_));
-    const size_t esz = precision_ == WC_PRECISE ? 4 : 2;
+    const size_t esz = precision_ == WC_PRECISE || precision_ == WC_F16X ? 4 : 2;
     size_t mt = 0;
     auto mtake = [&](size_t bytes) {
         size_t a = align256(mt);

@@ -65,6 +65,7 @@ struct WaveDev {
     const TowerBlock* tower_blk[2];  // two-tower readout blocks and tiles of each player
     const TowerUnit* tower_unit[2];
     uint32_t ntower_blk[2], ntower_unit[2];
+    uint64_t xplane;  // compensated f16: elements between a query input's hi and lo planes
 };
 
 // Launchers (kernels.hip). All take the executor's stream.

@@ -291,14 +291,21 @@ __device__ __forceinline__ uint16_t f32_to_f16_rn(float x) {
     return __builtin_bit_cast(uint16_t, h);
 }
 
+// One query-input element. Compensated f16 keeps two planes `plane` elements
+// apart: hi = f16(v) and lo = f16(v - hi).
 template <int PREC>
-__device__ __forceinline__ void store_operand(void* base, size_t i, float v) {
-    if (PREC == WC_PRECISE)
+__device__ __forceinline__ void store_operand(void* base, size_t i, float v, size_t plane) {
+    if (PREC == WC_PRECISE) {
         ((float*)base)[i] = v;
-    else if (PREC == WC_F16)
+    } else if (PREC == WC_F16) {
         ((uint16_t*)base)[i] = f32_to_f16_rn(v);
-    else
+    } else if (PREC == WC_BF16) {
         ((uint16_t*)base)[i] = f32_to_bf16_rn(v);
+    } else {
+        const uint16_t hi = f32_to_f16_rn(v);
+        ((uint16_t*)base)[i] = hi;
+        ((uint16_t*)base)[i + plane] = f32_to_f16_rn(v - (float)__builtin_bit_cast(_Float16, hi));
+    }
 }
 
 // Query inputs are row-major float32 for the exact net, fragment-major 16-bit for MFMA.
@@ -484,9 +491,8 @@ __global__ __launch_bounds__(BLOCK) void k_pool_mfma(WaveDev w, int player, uint
                 if (rr >= G) continue;
                 const float y = tot[v] > SMOOTHF ? acc[t][v] * (1.0f / tot[v]) : S * inv_n;
                 const uint32_t row = grp->row[rr];
-                const uint16_t h = PREC == WC_F16 ? f32_to_f16_rn(y) : f32_to_bf16_rn(y);
-                own[frag_off(row, k, in)] = h;
-                other[frag_off(row, pool + k, in)] = h;
+                store_operand<PREC>(own, frag_off(row, k, in), y, w.xplane);
+                store_operand<PREC>(other, frag_off(row, pool + k, in), y, w.xplane);
             }
         }
     }
@@ -505,8 +511,10 @@ void launch_pool(const WaveDev& w, int player, int precision, void* x0, void* x1
     dim3 g(grid_for(waves * 64));
     if (precision == WC_F16)
         hipLaunchKernelGGL(k_pool_mfma<WC_F16>, g, dim3(BLOCK), 0, s, w, player, (uint16_t*)x0, (uint16_t*)x1);
-    else
+    else if (precision == WC_BF16)
         hipLaunchKernelGGL(k_pool_mfma<WC_BF16>, g, dim3(BLOCK), 0, s, w, player, (uint16_t*)x0, (uint16_t*)x1);
+    else
+        hipLaunchKernelGGL(k_pool_mfma<WC_F16X>, g, dim3(BLOCK), 0, s, w, player, (uint16_t*)x0, (uint16_t*)x1);
 }
 
 // The fixed part of both traversers' query inputs: the seat (-1 for player 0,
@@ -519,12 +527,12 @@ __global__ void k_query_static(WaveDev w, void* x0, void* x1) {
     uint32_t row = (uint32_t)(i / width), k = (uint32_t)(i % width);
     size_t at = operand_at<PREC>(row, 2 * w.pool + k, w.in);
     if (k == 0) {
-        store_operand<PREC>(x0, at, -1.0f);
-        store_operand<PREC>(x1, at, 1.0f);
+        store_operand<PREC>(x0, at, -1.0f, w.xplane);
+        store_operand<PREC>(x1, at, 1.0f, w.xplane);
     } else {
         float v = (float)w.pub_raw[(size_t)row * w.row_bytes + (k - 1)] / 255.0f;
-        store_operand<PREC>(x0, at, v);
-        store_operand<PREC>(x1, at, v);
+        store_operand<PREC>(x0, at, v, w.xplane);
+        store_operand<PREC>(x1, at, v, w.xplane);
     }
 }
 
@@ -535,8 +543,10 @@ void launch_query_static(const WaveDev& w, int precision, void* x0, void* x1, hi
         hipLaunchKernelGGL(k_query_static<WC_PRECISE>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, x0, x1);
     else if (precision == WC_F16)
         hipLaunchKernelGGL(k_query_static<WC_F16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, x0, x1);
-    else
+    else if (precision == WC_BF16)
         hipLaunchKernelGGL(k_query_static<WC_BF16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, x0, x1);
+    else
+        hipLaunchKernelGGL(k_query_static<WC_F16X>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, x0, x1);
 }
 
 // ------------------------------------------------------------- the sweep
@@ -943,24 +953,29 @@ void launch_head_exact(const float* H, uint32_t hidden, const float* Wh, const f
 
 
 template <int PREC>
-__global__ void k_to16(const float* src, uint16_t* dst, uint32_t rows, uint32_t K, int transposed) {
+__global__ void k_to16(const float* src, uint16_t* dst, uint32_t rows, uint32_t K, int transposed, size_t plane) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (size_t)rows * K) return;
     uint32_t r = (uint32_t)(i / K), k = (uint32_t)(i % K);
     float v = transposed ? src[(size_t)k * rows + r] : src[i];
-    dst[frag_off(r, k, K)] = PREC == WC_F16 ? f32_to_f16_rn(v) : f32_to_bf16_rn(v);
+    store_operand<PREC>(dst, frag_off(r, k, K), v, plane);
 }
 
 void launch_to16(int precision, const float* src, void* dst, uint32_t rows, uint32_t K, bool transposed,
                  hipStream_t s) {
     size_t n = (size_t)rows * K;
     if (!n) return;
+    const size_t plane = (size_t)gemm_rows(rows) * K;  // compensated f16: the lo plane follows the hi plane
+#define WC_TO16(P)                                                                                              \
+    hipLaunchKernelGGL(k_to16<P>, dim3(grid_for(n)), dim3(BLOCK), 0, s, src, (uint16_t*)dst, rows, K, (int)transposed, \
+                       plane)
     if (precision == WC_F16)
-        hipLaunchKernelGGL(k_to16<WC_F16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, src, (uint16_t*)dst, rows, K,
-                           (int)transposed);
+        WC_TO16(WC_F16);
+    else if (precision == WC_BF16)
+        WC_TO16(WC_BF16);
     else
-        hipLaunchKernelGGL(k_to16<WC_BF16>, dim3(grid_for(n)), dim3(BLOCK), 0, s, src, (uint16_t*)dst, rows, K,
-                           (int)transposed);
+        WC_TO16(WC_F16X);
+#undef WC_TO16
 }
 
 // 16x16x32 MFMA step over a 64 x 64 wave tile: acc[a][b] += A(a) B(b)^T.
@@ -1060,10 +1075,93 @@ __global__ __launch_bounds__(256) void k_gemm(const uint16_t* __restrict__ X, ui
         }
 }
 
+// Compensated f16 GEMM: each operand is an f16 pair hi + lo in two planes
+// (xplane / wplane elements apart), each product is taken as lo hi + hi lo +
+// hi hi (f32 accumulation), the output likewise split when 16-bit. Tiles as
+// k_gemm, without its load pipelining: this is the accuracy mode.
+template <bool RELU, bool OUT16>
+__global__ __launch_bounds__(256) void k_gemm_x(const uint16_t* __restrict__ X, uint32_t K,
+                                                const uint16_t* __restrict__ Wt, const float* __restrict__ bias,
+                                                uint32_t N, void* __restrict__ Y, uint32_t M,
+                                                const uint32_t* __restrict__ tile_n, size_t xplane, size_t wplane,
+                                                size_t yplane) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (tile_n && blockIdx.y * GEMM_ROWS >= tile_n[blockIdx.x]) return;  // block-uniform
+    const uint32_t m0 = blockIdx.x * GEMM_ROWS + (wave & 1) * 64;
+    const uint32_t n0 = blockIdx.y * GEMM_ROWS + (wave >> 1) * 64;
+    const uint32_t ks = K >> 5;
+    float4v acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint16_t* ap = X + ((size_t)(m0 >> 4) * ks * 64 + lane) * 8;
+    const uint16_t* bp = Wt + ((size_t)(n0 >> 4) * ks * 64 + lane) * 8;
+    const size_t blk = (size_t)ks * 64 * 8;
+    for (uint32_t st = 0; st < ks; st++) {
+        uint4 ah[4], al[4], bh[4], bl[4];
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            ah[a] = *(const uint4*)(ap + a * blk + (size_t)st * 512);
+            al[a] = *(const uint4*)(ap + xplane + a * blk + (size_t)st * 512);
+        }
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            bh[b] = *(const uint4*)(bp + b * blk + (size_t)st * 512);
+            bl[b] = *(const uint4*)(bp + wplane + b * blk + (size_t)st * 512);
+        }
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                acc[a][b] = mfma_step16<WC_F16>(al[a], bh[b], acc[a][b]);
+                acc[a][b] = mfma_step16<WC_F16>(ah[a], bl[b], acc[a][b]);
+                acc[a][b] = mfma_step16<WC_F16>(ah[a], bh[b], acc[a][b]);
+            }
+    }
+    const uint32_t li = lane & 15, kb = lane >> 4;
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            uint32_t col = n0 + b * 16 + li;
+            if (col >= N) continue;
+            float bv = bias[col];
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                uint32_t row = m0 + a * 16 + kb * 4 + v;
+                if (row >= M) continue;
+                float y = acc[a][b][v] + bv;
+                if (RELU) y = y > 0.0f ? y : 0.0f;
+                if (OUT16)
+                    store_operand<WC_F16X>(Y, frag_off(row, col, N), y, yplane);
+                else
+                    ((float*)Y)[(size_t)row * N + col] = y;
+            }
+        }
+}
+
 void launch_gemm16(int precision, const void* X, uint32_t K, const void* Wt, const float* b, uint32_t N, void* Y,
                    uint32_t M, bool relu, bool out16, hipStream_t s, const uint32_t* tile_n) {
     if (M == 0 || N == 0) return;
     dim3 grid(gemm_rows(M) / GEMM_ROWS, gemm_rows(N) / GEMM_ROWS);
+    if (precision == WC_F16X) {
+        const size_t xp = (size_t)gemm_rows(M) * K, wp = (size_t)gemm_rows(N) * K, yp = (size_t)gemm_rows(M) * N;
+        const uint16_t* x = (const uint16_t*)X;
+        const uint16_t* wt = (const uint16_t*)Wt;
+#define WC_GEMMX(R, O) \
+    hipLaunchKernelGGL((k_gemm_x<R, O>), grid, dim3(256), 0, s, x, K, wt, b, N, Y, M, tile_n, xp, wp, yp)
+        if (relu && out16)
+            WC_GEMMX(true, true);
+        else if (relu)
+            WC_GEMMX(true, false);
+        else if (out16)
+            WC_GEMMX(false, true);
+        else
+            WC_GEMMX(false, false);
+#undef WC_GEMMX
+        return;
+    }
     const uint16_t* x = (const uint16_t*)X;
     const uint16_t* wt = (const uint16_t*)Wt;
 #define WC_GEMM(P, R, O) hipLaunchKernelGGL((k_gemm<P, R, O>), grid, dim3(256), 0, s, x, K, wt, b, N, Y, M, tile_n)

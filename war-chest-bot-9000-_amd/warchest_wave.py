@@ -21,7 +21,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libwcwave.so")
 
-WC_PRECISE, WC_F16, WC_BF16 = 0, 1, 2
+WC_PRECISE, WC_F16, WC_BF16, WC_F16X = 0, 1, 2, 3
 MODEL_MLP, MODEL_TWO_TOWER = 101, 102
 
 _lib = None
