@@ -181,6 +181,11 @@ def test_mlp_bf16_matches_reduced_precision_oracle():
     (256, 128, 2, 40, 300),    # a narrow trunk: one 16-feature block per wavefront
     (512, 96, 2, 70, 260),     # fewer feature blocks than wavefronts
     (640, 416, 2, 70, 260),    # wider than the fused kernel takes: the layer-by-layer GEMMs
+    # Enough rows for full 128-row passes and short last passes on every CU;
+    # the head split four ways by rows (4 column blocks), two ways (10), none (36).
+    (512, 384, 3, 64, 40000),
+    (512, 384, 3, 150, 36000),
+    (512, 384, 3, 567, 33001),
 ])
 def test_mlp_f16_shapes(inputs, hidden, layers, heads, rows):
     dims = ww.mlp_dims(inputs=inputs, hidden=hidden, layers=layers, heads=heads, pool=64)
@@ -190,6 +195,9 @@ def test_mlp_f16_shapes(inputs, hidden, layers, heads, rows):
     ex = executor(ww.WC_F16)
     v = ex.publish(net)
     got = ex.mlp(v, x, heads=heads)
+    if rows > 2000:  # rows are independent: the oracle checks a spread subset (and the last row)
+        pick = np.unique(np.concatenate([np.arange(0, rows, 29), [rows - 1]]))
+        x, got, rows = x[pick], got[pick], len(pick)
     keys = np.tile(np.arange(heads, dtype=np.uint32), (rows, 1))
     emu = O.mlp(x, keys, net, O.NET_F16)
     scale = np.abs(emu).max()

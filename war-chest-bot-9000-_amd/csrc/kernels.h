@@ -112,7 +112,8 @@ void launch_head_exact(const float* H, uint32_t hidden, const float* Wh, const f
 void launch_gemm16(int precision, const void* X, uint32_t K, const void* Wt, const float* b, uint32_t N,
                    void* Y, uint32_t M, bool relu, bool out16, hipStream_t s, const uint32_t* tile_n = nullptr);
 // Whole-network MLP in one launch (16-bit operands, f32 accumulate): one
-// 128-row tile per workgroup with the activations resident in LDS; writes
+// workgroup per CU, each taking an even share of the 16-row blocks in passes
+// of up to 128 rows with the activations resident in LDS; writes
 // out[r, k] (row-major f32, `heads` columns) for r < rows and the columns
 // tile_n allows (all heads when tile_n is null). X is the fragment-major input
 // with gemm_rows(rows) rows; w/b hold the trunk layers and then the head, as

@@ -10,6 +10,9 @@
 
 #include <hip/hip_fp16.h>
 
+#include <algorithm>
+#include <atomic>
+
 #include "../../include/wc_wave.h"
 
 namespace wc {
@@ -1370,34 +1373,35 @@ __device__ __forceinline__ float4v mfma16(const uint4& a, const uint4& b, const 
                                                        c, 0, 0, 0);
 }
 
-// acc[a][b] (b < NB) = sum over ks steps of W(block b) X(rows 16a..)^T. xs: the
-// LDS operand at this lane's fragment slot (fragment (a, s) at xs + (a ks + s)
-// 512); wp: the wavefront's first weight block at this lane's slot (block b at
-// wp + b wstride). Weight fragments (from L2) are fetched two steps ahead
-// through a ring of four sets, activation fragments (from LDS) one step ahead
-// through two; the loop is unrolled by four so every set keeps a fixed role.
-// Loads past the last step re-read the last step (in bounds, unused).
-template <int PREC, int NB>
+// acc[a][b] (a < RB, b < NB) = sum over ks steps of W(block b) X(rows 16a..)^T.
+// xs: the LDS operand at this lane's fragment slot (fragment (a, s) at xs + (a
+// ks + s) 512); wp: the wavefront's first weight block at this lane's slot
+// (block b at wp + b wstride). Weight fragments (from L2) are fetched two
+// steps ahead through a ring of four sets, activation fragments (from LDS) one
+// step ahead through two; the loop is unrolled by four so every set keeps a
+// fixed role. Loads past the last step re-read the last step (in bounds,
+// unused).
+template <int PREC, int NB, int RB>
 __device__ __forceinline__ void chain_kloop(float4v (&acc)[8][CHAIN_NB], const uint16_t* xs, uint32_t ks,
                                             const uint16_t* __restrict__ wp, size_t wstride) {
 #pragma unroll
-    for (int a = 0; a < 8; a++)
+    for (int a = 0; a < RB; a++)
 #pragma unroll
         for (int b = 0; b < NB; b++) acc[a][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-    uint4 xa[8], xb[8], w0[NB], w1[NB], w2[NB], w3[NB];
+    uint4 xa[RB], xb[RB], w0[NB], w1[NB], w2[NB], w3[NB];
     auto ldw = [&](uint4 (&fw)[NB], uint32_t s) {
         s = s < ks ? s : ks - 1;
 #pragma unroll
         for (int b = 0; b < NB; b++) fw[b] = *(const uint4*)(wp + b * wstride + (size_t)s * 512);
     };
-    auto ldx = [&](uint4 (&fx)[8], uint32_t s) {
+    auto ldx = [&](uint4 (&fx)[RB], uint32_t s) {
         s = s < ks ? s : ks - 1;
 #pragma unroll
-        for (int a = 0; a < 8; a++) fx[a] = *(const uint4*)(xs + ((size_t)a * ks + s) * 512);
+        for (int a = 0; a < RB; a++) fx[a] = *(const uint4*)(xs + ((size_t)a * ks + s) * 512);
     };
-    auto step = [&](const uint4 (&fx)[8], const uint4 (&fw)[NB]) {
+    auto step = [&](const uint4 (&fx)[RB], const uint4 (&fw)[NB]) {
 #pragma unroll
-        for (int a = 0; a < 8; a++)
+        for (int a = 0; a < RB; a++)
 #pragma unroll
             for (int b = 0; b < NB; b++) acc[a][b] = mfma16<PREC>(fw[b], fx[a], acc[a][b]);
     };
@@ -1434,47 +1438,95 @@ __device__ __forceinline__ void chain_kloop(float4v (&acc)[8][CHAIN_NB], const u
     }
 }
 
-// The wavefront's share of one layer: 16-feature blocks blk0, blk0 + CHAIN_WAVES,
-// ... (nb of them, 0..CHAIN_NB) of all 128 rows.
-template <int PREC>
+// The wavefront's share of one layer: 16-feature blocks blk0, blk0 + bstep,
+// ... (nb of them, 0..CHAIN_NB) of RB row blocks from the LDS operand at lds.
+template <int PREC, int RB>
 __device__ __forceinline__ void chain_blocks(float4v (&acc)[8][CHAIN_NB], uint32_t nb, const uint16_t* lds,
                                              uint32_t ks, const uint16_t* __restrict__ W, uint32_t blk0,
-                                             uint32_t lane) {
+                                             uint32_t bstep, uint32_t lane) {
     const uint16_t* xs = lds + lane * 8;
     const uint16_t* wp = W + ((size_t)blk0 * ks * 64 + lane) * 8;
-    const size_t wstride = (size_t)CHAIN_WAVES * ks * 512;
+    const size_t wstride = (size_t)bstep * ks * 512;
     static_assert(CHAIN_NB == 3, "dispatch below covers 1..3 blocks");
     if (nb == 1)
-        chain_kloop<PREC, 1>(acc, xs, ks, wp, wstride);
+        chain_kloop<PREC, 1, RB>(acc, xs, ks, wp, wstride);
     else if (nb == 2)
-        chain_kloop<PREC, 2>(acc, xs, ks, wp, wstride);
+        chain_kloop<PREC, 2, RB>(acc, xs, ks, wp, wstride);
     else if (nb == 3)
-        chain_kloop<PREC, 3>(acc, xs, ks, wp, wstride);
+        chain_kloop<PREC, 3, RB>(acc, xs, ks, wp, wstride);
 }
 
 __device__ __forceinline__ uint32_t pack16(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
 
-template <int PREC>
-__global__ __launch_bounds__(CHAIN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_chain(
-    ChainNet net, const uint16_t* __restrict__ X, uint32_t rows, float* __restrict__ out,
-    const uint32_t* __restrict__ tile_n) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[CHAIN_LDS_HALVES];
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tile = blockIdx.x;
+// The head over the pass's RB row blocks (LDS operand, K = hidden): rg row
+// groups of RBW blocks each (RBW = ceil(RB / rg); a group's blocks past RB are
+// computed from in-bounds LDS and not stored) by 8 / rg column groups; the
+// wavefront's column blocks are c, c + 8 / rg, ... in steps of CHAIN_NB of
+// them. Row-major f32 out.
+template <int PREC, int RB, int RBW>
+__device__ __forceinline__ void chain_head(const ChainNet& net, uint32_t rows, float* __restrict__ out,
+                                           uint32_t rb0, uint32_t nt, uint32_t rg, const uint16_t* lds,
+                                           uint32_t lane, uint32_t wave) {
+    const uint32_t q = lane >> 4, r = lane & 15, ksn = net.hidden >> 5;
+    const uint32_t cg = CHAIN_WAVES / rg, g = wave / cg, c = wave % cg, a0 = g * RBW;
+    const uint16_t* wh = net.w[net.layers];
+    const float* bh = net.b[net.layers];
+    const uint16_t* xs = lds + (size_t)a0 * ksn * 512;
+    float4v acc[8][CHAIN_NB];
+    for (uint32_t c0 = 0; c0 < nt; c0 += cg * CHAIN_NB) {
+        const uint32_t end = min(nt, c0 + cg * CHAIN_NB);
+        const uint32_t hb = end > c0 + c ? (end - c0 - c + cg - 1) / cg : 0;
+        chain_blocks<PREC, RBW>(acc, hb, xs, ksn, wh, c0 + c, cg, lane);
+#pragma unroll
+        for (int b = 0; b < CHAIN_NB; b++) {
+            if ((uint32_t)b >= hb) break;
+            const uint32_t n = (c0 + c + cg * b) * 16 + 4 * q;
+            float bv[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) bv[v] = n + v < net.heads ? bh[n + v] : 0.0f;
+            // The row indices are recomputed per column step from an opaque
+            // copy of the lane's row: kept live across the loop, they spill.
+            uint32_t rr = r;
+            asm volatile("" : "+v"(rr));
+#pragma unroll
+            for (int a = 0; a < RBW; a++) {
+                if (a0 + a >= RB) break;
+                const uint32_t m = (rb0 + a0 + a) * 16 + rr;
+                if (m >= rows) continue;
+                float* o = out + (size_t)m * net.heads + n;
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    if (n + v < net.heads) o[v] = acc[a][b][v] + bv[v];
+            }
+        }
+    }
+}
+
+// One pass of the whole network over RB consecutive 16-row blocks from row
+// block rb0 (RB <= 8): stage their input operand in LDS, run the trunk layers
+// in place, write the head.
+template <int PREC, int RB>
+__device__ __forceinline__ void chain_pass(const ChainNet& net, const uint16_t* __restrict__ X, uint32_t rows,
+                                           float* __restrict__ out, const uint32_t* __restrict__ tile_n,
+                                           uint32_t rb0, uint16_t* lds, uint32_t lane, uint32_t wave) {
     const uint32_t q = lane >> 4, r = lane & 15;
-    {  // the tile's input operand is one contiguous run of 128 x in halves
-        const uint4* src = (const uint4*)(X + (size_t)tile * GEMM_ROWS * net.in);
+    const uint32_t hblk = net.hidden >> 4, ksn = net.hidden >> 5;
+    const uint32_t nb = hblk > wave ? (hblk - wave + CHAIN_WAVES - 1) / CHAIN_WAVES : 0;
+    uint32_t cols = net.heads;  // head columns the pass's 128-row tiles need
+    if (tile_n) cols = min(max(tile_n[rb0 / 8], tile_n[(rb0 + RB - 1) / 8]), net.heads);
+    const uint32_t nt = (cols + 15) >> 4;
+    {  // a run of row blocks is one contiguous run of RB 16 x in halves
+        const uint4* src = (const uint4*)(X + (size_t)rb0 * 16 * net.in);
         uint4* dst = (uint4*)lds;
-        const uint32_t n = GEMM_ROWS * net.in / 8;
+        const uint32_t n = RB * 16 * net.in / 8;
 #pragma unroll 4
         for (uint32_t i = threadIdx.x; i < n; i += CHAIN_WAVES * 64) dst[i] = src[i];
     }
     __syncthreads();
     float4v acc[8][CHAIN_NB];
-    const uint32_t hblk = net.hidden >> 4, ksn = net.hidden >> 5;
-    const uint32_t nb = hblk > wave ? (hblk - wave + CHAIN_WAVES - 1) / CHAIN_WAVES : 0;
     uint32_t K = net.in;
     for (uint32_t l = 0; l < net.layers; l++) {
-        chain_blocks<PREC>(acc, nb, lds, K >> 5, net.w[l], wave, lane);
+        chain_blocks<PREC, RB>(acc, nb, lds, K >> 5, net.w[l], wave, CHAIN_WAVES, lane);
         __syncthreads();  // the layer input is dead from here on
         // bias + ReLU, stored over the input as the next operand (K = hidden)
         const float* bias = net.b[l];
@@ -1485,7 +1537,7 @@ __global__ __launch_bounds__(CHAIN_WAVES * 64) __attribute__((amdgpu_waves_per_e
             const float b0 = bias[n], b1 = bias[n + 1], b2 = bias[n + 2], b3 = bias[n + 3];
             const size_t col = (size_t)(n >> 5) * 64 + r + ((n & 31) >> 3) * 16;
 #pragma unroll
-            for (int a = 0; a < 8; a++) {
+            for (int a = 0; a < RB; a++) {
                 float y0 = acc[a][b][0] + b0, y1 = acc[a][b][1] + b1, y2 = acc[a][b][2] + b2,
                       y3 = acc[a][b][3] + b3;
                 y0 = y0 > 0.0f ? y0 : 0.0f;
@@ -1506,44 +1558,71 @@ __global__ __launch_bounds__(CHAIN_WAVES * 64) __attribute__((amdgpu_waves_per_e
         __syncthreads();
         K = net.hidden;
     }
-    // Head: the tile's 16-column blocks go round-robin to the wavefronts,
-    // CHAIN_WAVES * CHAIN_NB per pass; row-major f32 out.
-    const uint32_t cols = tile_n ? min(tile_n[tile], net.heads) : net.heads;
-    const uint32_t nt = (cols + 15) >> 4, row0 = tile * GEMM_ROWS;
-    const uint16_t* wh = net.w[net.layers];
-    const float* bh = net.b[net.layers];
-    for (uint32_t c0 = 0; c0 < nt; c0 += CHAIN_WAVES * CHAIN_NB) {
-        const uint32_t end = min(nt, c0 + CHAIN_WAVES * CHAIN_NB);
-        const uint32_t hb = end > c0 + wave ? (end - c0 - wave + CHAIN_WAVES - 1) / CHAIN_WAVES : 0;
-        chain_blocks<PREC>(acc, hb, lds, ksn, wh, c0 + wave, lane);
-#pragma unroll
-        for (int b = 0; b < CHAIN_NB; b++) {
-            if ((uint32_t)b >= hb) break;
-            const uint32_t n = (c0 + wave + CHAIN_WAVES * b) * 16 + 4 * q;
-            float bv[4];
-#pragma unroll
-            for (int v = 0; v < 4; v++) bv[v] = n + v < net.heads ? bh[n + v] : 0.0f;
-#pragma unroll
-            for (int a = 0; a < 8; a++) {
-                const uint32_t m = row0 + a * 16 + r;
-                if (m >= rows) continue;
-                float* o = out + (size_t)m * net.heads + n;
-#pragma unroll
-                for (int v = 0; v < 4; v++)
-                    if (n + v < net.heads) o[v] = acc[a][b][v] + bv[v];
-            }
-        }
+    // Head: the columns the pass's 128-row tiles need (tile_n), nt 16-column
+    // blocks. Few blocks go to groups of wavefronts that split the rows (rg
+    // row groups of RB / rg blocks, 8 / rg blocks per column step), so that
+    // every wavefront has work and reads fewer operand fragments per product.
+    if (nt <= 6 && RB >= 4)
+        chain_head<PREC, RB, (RB + 3) / 4>(net, rows, out, rb0, nt, 4, lds, lane, wave);
+    else if (nt <= 12 && RB >= 2)
+        chain_head<PREC, RB, (RB + 1) / 2>(net, rows, out, rb0, nt, 2, lds, lane, wave);
+    else
+        chain_head<PREC, RB, RB>(net, rows, out, rb0, nt, 1, lds, lane, wave);
+}
+
+// Rows are dealt to `shares` shares of 16-row blocks, as evenly as whole
+// blocks allow (one share per CU), and each share is taken in passes of up to
+// eight blocks, one pass per workgroup: workgroup i runs pass i / shares of
+// share i % shares. Every CU's first pass is a full 128 rows and the last
+// passes are about equally short, where whole 128-row tiles would leave part of
+// the device idle for the last round.
+template <int PREC>
+__global__ __launch_bounds__(CHAIN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_chain(
+    ChainNet net, const uint16_t* __restrict__ X, uint32_t rows, float* __restrict__ out,
+    const uint32_t* __restrict__ tile_n, uint32_t shares) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[CHAIN_LDS_HALVES];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t nrb = (rows + 15) >> 4, share = blockIdx.x % shares, pass = blockIdx.x / shares;
+    const uint32_t b1 = (uint32_t)((uint64_t)(share + 1) * nrb / shares);
+    const uint32_t rb = (uint32_t)((uint64_t)share * nrb / shares) + 8 * pass;
+    if (rb >= b1) return;  // workgroup-uniform
+    switch (min(8u, b1 - rb)) {
+        case 8: chain_pass<PREC, 8>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
+        case 7: chain_pass<PREC, 7>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
+        case 6: chain_pass<PREC, 6>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
+        case 5: chain_pass<PREC, 5>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
+        case 4: chain_pass<PREC, 4>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
+        case 3: chain_pass<PREC, 3>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
+        case 2: chain_pass<PREC, 2>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
+        default: chain_pass<PREC, 1>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
     }
+}
+
+// Compute units of the current device (cached per device).
+static uint32_t device_cus() {
+    static std::atomic<uint32_t> cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    uint32_t c = cus[dev].load(std::memory_order_relaxed);
+    if (!c) {
+        int n = 0;
+        c = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? (uint32_t)n
+                                                                                                       : 256;
+        cus[dev].store(c, std::memory_order_relaxed);
+    }
+    return c;
 }
 
 void launch_chain(int precision, const ChainNet& net, const void* X, uint32_t rows, float* out,
                   const uint32_t* tile_n, hipStream_t s) {
     if (rows == 0) return;
-    dim3 grid(gemm_rows(rows) / GEMM_ROWS), block(CHAIN_WAVES * 64);
+    const uint32_t nrb = (rows + 15) / 16, shares = std::min(nrb, device_cus());
+    const uint32_t passes = ((nrb + shares - 1) / shares + 7) / 8;  // passes of the largest share
+    dim3 grid(shares * passes), block(CHAIN_WAVES * 64);
     if (precision == WC_F16)
-        hipLaunchKernelGGL(k_chain<WC_F16>, grid, block, 0, s, net, (const uint16_t*)X, rows, out, tile_n);
+        hipLaunchKernelGGL(k_chain<WC_F16>, grid, block, 0, s, net, (const uint16_t*)X, rows, out, tile_n, shares);
     else
-        hipLaunchKernelGGL(k_chain<WC_BF16>, grid, block, 0, s, net, (const uint16_t*)X, rows, out, tile_n);
+        hipLaunchKernelGGL(k_chain<WC_BF16>, grid, block, 0, s, net, (const uint16_t*)X, rows, out, tile_n, shares);
 }
 
 }  // namespace wc
