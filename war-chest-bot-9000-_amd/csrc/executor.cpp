@@ -63,6 +63,9 @@ Executor::Executor(int device, int precision) : device_(device), precision_(prec
         err_ = "cannot create the executor stream";
         return;
     }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+        cus_ = (uint32_t)cus;
     ok_ = true;
 }
 
@@ -252,7 +255,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
             draw_row_start, draw_to, draw_p, reach_base, vals_base, parent, rev_row_of, rev_start, rev_src, rev_cell,
             rvd_row_of, rvd_start, rvd_src, rvd_p, row_node, row_cfg_off, row_cfg, cfg_key, cfg_emb, pub_raw,
             term_node, term_util, roots, carried, exit_node, exit_coff, trees, units, bt[2], rt[2], dc[2], bl[2],
-            rl[2], cv[2], lr[2], pg[2], twb[2], twu[2], cfg_priv, unit_row, unit_term, tb[2], tr[2], head_tile_n;
+            rl[2], cv[2], lr[2], pg[2], twb[2], twu[2], cfg_priv, unit_row, unit_term, tb[2], tr[2], head_tile_n, cp[2];
     } o;
     o.node_meta = blob.put(w.node_meta);
     o.nc = blob.put(w.node_nc);
@@ -307,6 +310,14 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     o.unit_row = blob.put(w.unit_row);
     o.unit_term = blob.put(w.unit_term);
     o.head_tile_n = blob.put(w.head_tile_n);
+    std::vector<ChainPass> plan[2];
+    for (int p = 0; p < 2; p++) {
+        plan[p] = plan_chain(w.head_rb_n[p].data(), (uint32_t)w.head_rb_n[p].size(), w.net.heads, cus_);
+        if (!check_chain_plan(plan[p], w.head_rb_n[p].data(), (uint32_t)w.head_rb_n[p].size(), w.net.heads, err))
+            return false;
+        o.cp[p] = blob.put(plan[p]);
+        chain_npass_[p] = (uint32_t)plan[p].size();
+    }
     for (int p = 0; p < 2; p++) {
         o.tb[p] = blob.put(w.top_back_rec[p]);
         o.tr[p] = blob.put(w.top_reach_rec[p]);
@@ -414,6 +425,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     d.unit_row = (const uint32_t*)(T + o.unit_row);
     d.unit_term = (const uint32_t*)(T + o.unit_term);
     head_tile_n_ = (const uint32_t*)(T + o.head_tile_n);
+    for (int p = 0; p < 2; p++) chain_plan_[p] = (const ChainPass*)(T + o.cp[p]);
     for (int p = 0; p < 2; p++) {
         top_back_dev_[p] = (const BackRec*)(T + o.tb[p]);
         top_reach_dev_[p] = (const ReachRec*)(T + o.tr[p]);
@@ -462,7 +474,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
 }
 
 void Executor::run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::vector<hipEvent_t>* marks,
-                       const uint32_t* head_tile_n) {
+                       const uint32_t* head_tile_n, const ChainPass* plan, uint32_t npass) {
     const NetShape& ns = bank.ns;
     auto mark = [&]() {
         if (marks) {
@@ -484,7 +496,7 @@ void Executor::run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::v
         net.hidden = ns.hidden;
         net.layers = ns.layers;
         net.heads = ns.heads;
-        launch_chain(precision_, net, x, rows, head_out_, head_tile_n, stream_);
+        launch_chain(precision_, net, x, rows, head_out_, plan, npass, stream_);
         mark();
         return;
     }
@@ -574,7 +586,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         if (tower)
             run_tower(bank, d.rows, q);
         else
-            run_mlp(bank, d.rows, Xq_[q], nullptr, head_tile_n_);
+            run_mlp(bank, d.rows, Xq_[q], nullptr, head_tile_n_, chain_plan_[q], chain_npass_[q]);
         mark(C_MLP);
     };
     // Top regions, one depth per launch: values bottom-up, reach top-down.
@@ -771,21 +783,29 @@ bool Executor::mlp_forward(uint64_t version, uint32_t rows, const float* x, floa
         return a;
     };
     const size_t prow = precision_ == WC_PRECISE ? rows : gemm_rows(rows);  // GEMM operands: padded rows
+    const std::vector<ChainPass> plan = plan_chain(nullptr, (rows + 15) / 16, ns.heads, cus_);
+    if (!check_chain_plan(plan, nullptr, (rows + 15) / 16, ns.heads, err)) return false;
     size_t m_x = mtake(prow * ns.in * esz), m_h0 = mtake(prow * ns.hidden * esz), m_h1 = mtake(prow * ns.hidden * esz),
-           m_out = mtake(size_t(rows) * ns.heads * 4), m_stage = mtake(size_t(rows) * ns.in * 4);
+           m_out = mtake(size_t(rows) * ns.heads * 4), m_stage = mtake(size_t(rows) * ns.in * 4),
+           m_plan = mtake(plan.size() * sizeof(ChainPass));
     if (!ensure(&mlp_, &mlp_cap_, mt, err)) return false;
     char* M = (char*)mlp_;
     X_ = M + m_x;
     H_[0] = M + m_h0;
     H_[1] = M + m_h1;
     head_out_ = (float*)(M + m_out);
+    mlp_plan_ = (const ChainPass*)(M + m_plan);
+    mlp_npass_ = (uint32_t)plan.size();
+    if (!plan.empty())
+        HIP_TRY(hipMemcpyAsync(M + m_plan, plan.data(), plan.size() * sizeof(ChainPass), hipMemcpyHostToDevice,
+                               stream_));
     if (precision_ == WC_PRECISE) {
         HIP_TRY(hipMemcpyAsync(X_, x, size_t(rows) * ns.in * 4, hipMemcpyHostToDevice, stream_));
     } else {
         HIP_TRY(hipMemcpyAsync(M + m_stage, x, size_t(rows) * ns.in * 4, hipMemcpyHostToDevice, stream_));
         launch_to16(precision_, (const float*)(M + m_stage), X_, rows, ns.in, false, stream_);
     }
-    run_mlp(it->second, rows, X_, nullptr);
+    run_mlp(it->second, rows, X_, nullptr, nullptr, mlp_plan_, mlp_npass_);
     HIP_TRY(hipGetLastError());
     HIP_TRY(hipMemcpyAsync(out, head_out_, size_t(rows) * ns.heads * 4, hipMemcpyDeviceToHost, stream_));
     HIP_TRY(hipStreamSynchronize(stream_));
@@ -806,7 +826,7 @@ bool Executor::time_mlp(uint64_t version, uint32_t rows, const float* x, uint32_
     HIP_TRY(hipEventCreate(&a));
     HIP_TRY(hipEventCreate(&b));
     HIP_TRY(hipEventRecord(a, stream_));
-    for (uint32_t r = 0; r < reps; r++) run_mlp(it->second, rows, X_, nullptr);
+    for (uint32_t r = 0; r < reps; r++) run_mlp(it->second, rows, X_, nullptr, nullptr, mlp_plan_, mlp_npass_);
     HIP_TRY(hipEventRecord(b, stream_));
     HIP_TRY(hipEventSynchronize(b));
     float ms = 0.0f;
@@ -817,7 +837,7 @@ bool Executor::time_mlp(uint64_t version, uint32_t rows, const float* x, uint32_
         hipEvent_t s0;
         HIP_TRY(hipEventCreate(&s0));
         HIP_TRY(hipEventRecord(s0, stream_));
-        run_mlp(it->second, rows, X_, &marks);
+        run_mlp(it->second, rows, X_, &marks, nullptr, mlp_plan_, mlp_npass_);
         HIP_TRY(hipStreamSynchronize(stream_));
         layer_ms->clear();
         hipEvent_t prev = s0;

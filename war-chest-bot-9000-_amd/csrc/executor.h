@@ -84,11 +84,15 @@ class Executor {
     // Two-tower net: F for the uploaded wave's configs, then one traverser's public tower and readout.
     void run_tower_private(const NetBank& bank);
     void run_tower(const NetBank& bank, uint32_t rows, int traverser);
+    // The MLP over `rows` query rows: the fused kernel over `plan` (npass
+    // passes, device copy) where it applies, else layer by layer (head width
+    // per 128-row tile: head_tile_n).
     void run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::vector<hipEvent_t>* marks,
-                 const uint32_t* head_tile_n = nullptr);
+                 const uint32_t* head_tile_n, const ChainPass* plan, uint32_t npass);
     bool ensure(void** p, size_t* cap, size_t need, std::string* err);
 
     int device_ = 0, precision_ = 0;
+    uint32_t cus_ = 1;  // compute units of the device (fused value net plans)
     bool ok_ = false;
     std::string err_;
     hipStream_t stream_ = nullptr;
@@ -109,6 +113,10 @@ class Executor {
     const BackRec* top_back_dev_[2] = {};    // top-region rows by depth (device copies)
     const ReachRec* top_reach_dev_[2] = {};
     const uint32_t* head_tile_n_ = nullptr;  // head width per 128-row tile (device copy)
+    const ChainPass* chain_plan_[2] = {};    // fused value net passes per traverser (device copies)
+    uint32_t chain_npass_[2] = {0, 0};
+    const ChainPass* mlp_plan_ = nullptr;    // the same for mlp_forward's rows
+    uint32_t mlp_npass_ = 0;
     void* H_[2] = {};
     float* head_out_ = nullptr;  // MLP head outputs, or the two-tower readout per (row, config)
     // Two-tower net: private-tower input, layer outputs and F (one row per interned config).

@@ -112,12 +112,12 @@ void launch_head_exact(const float* H, uint32_t hidden, const float* Wh, const f
 void launch_gemm16(int precision, const void* X, uint32_t K, const void* Wt, const float* b, uint32_t N,
                    void* Y, uint32_t M, bool relu, bool out16, hipStream_t s, const uint32_t* tile_n = nullptr);
 // Whole-network MLP in one launch (16-bit operands, f32 accumulate): one
-// workgroup per CU, each taking an even share of the 16-row blocks in passes
-// of up to 128 rows with the activations resident in LDS; writes
-// out[r, k] (row-major f32, `heads` columns) for r < rows and the columns
-// tile_n allows (all heads when tile_n is null). X is the fragment-major input
-// with gemm_rows(rows) rows; w/b hold the trunk layers and then the head, as
-// launch_gemm16 takes them. Applies when chain_fits(in, hidden, layers).
+// workgroup per pass of a plan (plan_chain), each running its up to 128 rows
+// through every layer with the activations resident in LDS; writes out[r, k]
+// (row-major f32, `heads` columns) for r < rows and the columns k < the pass's
+// cols. X is the fragment-major input with gemm_rows(rows) rows; w/b hold the
+// trunk layers and then the head, as launch_gemm16 takes them. Applies when
+// chain_fits(in, hidden, layers).
 constexpr uint32_t CHAIN_MAX_LAYERS = 8, CHAIN_MAX_WIDTH = 512;
 // Eight wavefronts per tile, each owning up to CHAIN_NB 16-feature blocks of a layer.
 constexpr uint32_t CHAIN_WAVES = 8, CHAIN_NB = 3;
@@ -128,7 +128,7 @@ struct ChainNet {
 };
 bool chain_fits(uint32_t in, uint32_t hidden, uint32_t layers);
 void launch_chain(int precision, const ChainNet& net, const void* X, uint32_t rows, float* out,
-                  const uint32_t* tile_n, hipStream_t s);
+                  const ChainPass* plan, uint32_t npass, hipStream_t s);
 // Two-tower net: F = private-tower output (ncfg rows, fragment-major 16-bit or
 // row-major f32) times the readout weight, row-major; then player p's readout
 // blocks, tv[entry (row, config)] = <F[config], H[row]> + bread, from the

@@ -11,7 +11,6 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
-#include <atomic>
 
 #include "../../include/wc_wave.h"
 
@@ -1465,8 +1464,8 @@ __device__ __forceinline__ uint32_t pack16(uint16_t lo, uint16_t hi) { return (u
 // them. Row-major f32 out.
 template <int PREC, int RB, int RBW>
 __device__ __forceinline__ void chain_head(const ChainNet& net, uint32_t rows, float* __restrict__ out,
-                                           uint32_t rb0, uint32_t nt, uint32_t rg, const uint16_t* lds,
-                                           uint32_t lane, uint32_t wave) {
+                                           const ChainPass* __restrict__ ps, uint32_t nt, uint32_t rg,
+                                           const uint16_t* lds, uint32_t lane, uint32_t wave) {
     const uint32_t q = lane >> 4, r = lane & 15, ksn = net.hidden >> 5;
     const uint32_t cg = CHAIN_WAVES / rg, g = wave / cg, c = wave % cg, a0 = g * RBW;
     const uint16_t* wh = net.w[net.layers];
@@ -1491,7 +1490,7 @@ __device__ __forceinline__ void chain_head(const ChainNet& net, uint32_t rows, f
 #pragma unroll
             for (int a = 0; a < RBW; a++) {
                 if (a0 + a >= RB) break;
-                const uint32_t m = (rb0 + a0 + a) * 16 + rr;
+                const uint32_t m = ps->rb[a0 + a] * 16 + rr;
                 if (m >= rows) continue;
                 float* o = out + (size_t)m * net.heads + n;
 #pragma unroll
@@ -1502,25 +1501,24 @@ __device__ __forceinline__ void chain_head(const ChainNet& net, uint32_t rows, f
     }
 }
 
-// One pass of the whole network over RB consecutive 16-row blocks from row
-// block rb0 (RB <= 8): stage their input operand in LDS, run the trunk layers
-// in place, write the head.
+// One pass of the whole network over the pass's RB 16-row blocks (RB <= 8):
+// stage their input operand in LDS, run the trunk layers in place, write the
+// head.
 template <int PREC, int RB>
 __device__ __forceinline__ void chain_pass(const ChainNet& net, const uint16_t* __restrict__ X, uint32_t rows,
-                                           float* __restrict__ out, const uint32_t* __restrict__ tile_n,
-                                           uint32_t rb0, uint16_t* lds, uint32_t lane, uint32_t wave) {
+                                           float* __restrict__ out, const ChainPass* __restrict__ ps,
+                                           uint16_t* lds, uint32_t lane, uint32_t wave) {
     const uint32_t q = lane >> 4, r = lane & 15;
     const uint32_t hblk = net.hidden >> 4, ksn = net.hidden >> 5;
     const uint32_t nb = hblk > wave ? (hblk - wave + CHAIN_WAVES - 1) / CHAIN_WAVES : 0;
-    uint32_t cols = net.heads;  // head columns the pass's 128-row tiles need
-    if (tile_n) cols = min(max(tile_n[rb0 / 8], tile_n[(rb0 + RB - 1) / 8]), net.heads);
-    const uint32_t nt = (cols + 15) >> 4;
-    {  // a run of row blocks is one contiguous run of RB 16 x in halves
-        const uint4* src = (const uint4*)(X + (size_t)rb0 * 16 * net.in);
-        uint4* dst = (uint4*)lds;
-        const uint32_t n = RB * 16 * net.in / 8;
-#pragma unroll 4
-        for (uint32_t i = threadIdx.x; i < n; i += CHAIN_WAVES * 64) dst[i] = src[i];
+    const uint32_t nt = (min(ps->cols, net.heads) + 15) >> 4;  // head column blocks the pass needs
+    // Each row block is one contiguous run of 16 x in halves, in LDS in pass order.
+    const uint32_t per = 2 * net.in;  // uint4 per row block
+#pragma unroll
+    for (int a = 0; a < RB; a++) {
+        const uint4* src = (const uint4*)(X + (size_t)ps->rb[a] * 16 * net.in);
+        uint4* dst = (uint4*)lds + a * per;
+        for (uint32_t i = threadIdx.x; i < per; i += CHAIN_WAVES * 64) dst[i] = src[i];
     }
     __syncthreads();
     float4v acc[8][CHAIN_NB];
@@ -1558,71 +1556,47 @@ __device__ __forceinline__ void chain_pass(const ChainNet& net, const uint16_t* 
         __syncthreads();
         K = net.hidden;
     }
-    // Head: the columns the pass's 128-row tiles need (tile_n), nt 16-column
-    // blocks. Few blocks go to groups of wavefronts that split the rows (rg
+    // Head: the columns the pass's rows need, nt 16-column blocks. Few blocks go to groups of wavefronts that split the rows (rg
     // row groups of RB / rg blocks, 8 / rg blocks per column step), so that
     // every wavefront has work and reads fewer operand fragments per product.
     if (nt <= 6 && RB >= 4)
-        chain_head<PREC, RB, (RB + 3) / 4>(net, rows, out, rb0, nt, 4, lds, lane, wave);
+        chain_head<PREC, RB, (RB + 3) / 4>(net, rows, out, ps, nt, 4, lds, lane, wave);
     else if (nt <= 12 && RB >= 2)
-        chain_head<PREC, RB, (RB + 1) / 2>(net, rows, out, rb0, nt, 2, lds, lane, wave);
+        chain_head<PREC, RB, (RB + 1) / 2>(net, rows, out, ps, nt, 2, lds, lane, wave);
     else
-        chain_head<PREC, RB, RB>(net, rows, out, rb0, nt, 1, lds, lane, wave);
+        chain_head<PREC, RB, RB>(net, rows, out, ps, nt, 1, lds, lane, wave);
 }
 
-// Rows are dealt to `shares` shares of 16-row blocks, as evenly as whole
-// blocks allow (one share per CU), and each share is taken in passes of up to
-// eight blocks, one pass per workgroup: workgroup i runs pass i / shares of
-// share i % shares. Every CU's first pass is a full 128 rows and the last
-// passes are about equally short, where whole 128-row tiles would leave part of
-// the device idle for the last round.
+// One workgroup per pass of the plan (plan_chain orders the passes so that
+// the costly ones start first).
 template <int PREC>
-__global__ __launch_bounds__(CHAIN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_chain(
+__global__ __launch_bounds__(CHAIN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(CHAIN_WAVES / 4, CHAIN_WAVES / 4))) void k_chain(
     ChainNet net, const uint16_t* __restrict__ X, uint32_t rows, float* __restrict__ out,
-    const uint32_t* __restrict__ tile_n, uint32_t shares) {
+    const ChainPass* __restrict__ plan) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[CHAIN_LDS_HALVES];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t nrb = (rows + 15) >> 4, share = blockIdx.x % shares, pass = blockIdx.x / shares;
-    const uint32_t b1 = (uint32_t)((uint64_t)(share + 1) * nrb / shares);
-    const uint32_t rb = (uint32_t)((uint64_t)share * nrb / shares) + 8 * pass;
-    if (rb >= b1) return;  // workgroup-uniform
-    switch (min(8u, b1 - rb)) {
-        case 8: chain_pass<PREC, 8>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
-        case 7: chain_pass<PREC, 7>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
-        case 6: chain_pass<PREC, 6>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
-        case 5: chain_pass<PREC, 5>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
-        case 4: chain_pass<PREC, 4>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
-        case 3: chain_pass<PREC, 3>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
-        case 2: chain_pass<PREC, 2>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
-        default: chain_pass<PREC, 1>(net, X, rows, out, tile_n, rb, lds, lane, wave); break;
+    const ChainPass* ps = plan + blockIdx.x;
+    switch (min(CHAIN_PASS_BLOCKS, ps->n)) {
+        case 8: chain_pass<PREC, 8>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 7: chain_pass<PREC, 7>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 6: chain_pass<PREC, 6>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 5: chain_pass<PREC, 5>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 4: chain_pass<PREC, 4>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 3: chain_pass<PREC, 3>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 2: chain_pass<PREC, 2>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 1: chain_pass<PREC, 1>(net, X, rows, out, ps, lds, lane, wave); break;
+        default: break;
     }
-}
-
-// Compute units of the current device (cached per device).
-static uint32_t device_cus() {
-    static std::atomic<uint32_t> cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    uint32_t c = cus[dev].load(std::memory_order_relaxed);
-    if (!c) {
-        int n = 0;
-        c = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? (uint32_t)n
-                                                                                                       : 256;
-        cus[dev].store(c, std::memory_order_relaxed);
-    }
-    return c;
 }
 
 void launch_chain(int precision, const ChainNet& net, const void* X, uint32_t rows, float* out,
-                  const uint32_t* tile_n, hipStream_t s) {
-    if (rows == 0) return;
-    const uint32_t nrb = (rows + 15) / 16, shares = std::min(nrb, device_cus());
-    const uint32_t passes = ((nrb + shares - 1) / shares + 7) / 8;  // passes of the largest share
-    dim3 grid(shares * passes), block(CHAIN_WAVES * 64);
+                  const ChainPass* plan, uint32_t npass, hipStream_t s) {
+    if (rows == 0 || npass == 0) return;
+    dim3 grid(npass), block(CHAIN_WAVES * 64);
     if (precision == WC_F16)
-        hipLaunchKernelGGL(k_chain<WC_F16>, grid, block, 0, s, net, (const uint16_t*)X, rows, out, tile_n, shares);
+        hipLaunchKernelGGL(k_chain<WC_F16>, grid, block, 0, s, net, (const uint16_t*)X, rows, out, plan);
     else
-        hipLaunchKernelGGL(k_chain<WC_BF16>, grid, block, 0, s, net, (const uint16_t*)X, rows, out, tile_n, shares);
+        hipLaunchKernelGGL(k_chain<WC_BF16>, grid, block, 0, s, net, (const uint16_t*)X, rows, out, plan);
 }
 
 }  // namespace wc

@@ -521,6 +521,14 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             uint32_t& n = w.head_tile_n[r / 128];
             n = std::max(n, w.cfg_key[w.row_cfg[x]] + 1);
         }
+    for (int p = 0; p < 2; p++) {
+        w.head_rb_n[p].assign((nrows + 15) / 16, 0);
+        for (uint32_t r = 0; r < nrows; r++)
+            for (uint32_t x = w.row_cfg_off[2 * r + p]; x < w.row_cfg_off[2 * r + p + 1]; x++) {
+                uint32_t& n = w.head_rb_n[p][r / 16];
+                n = std::max(n, w.cfg_key[w.row_cfg[x]] + 1);
+            }
+    }
     // Pool groups: rows with the same config list (same tree, same
     // infostates in the same order), at most POOL_GROUP per group, in row
     // order within a list; longest lists launch first.
@@ -894,6 +902,100 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         if (uint64_t(t.exit0) + t.nexit > nexit) return fail("exit range");
     }
     return true;
+}
+
+bool check_chain_plan(const std::vector<ChainPass>& plan, const uint32_t* cols, uint32_t nrb, uint32_t heads,
+                      std::string* err) {
+    auto fail = [&](const char* m) {
+        *err = m;
+        return false;
+    };
+    std::vector<uint8_t> seen(nrb, 0);
+    for (const ChainPass& ps : plan) {
+        if (ps.n < 1 || ps.n > CHAIN_PASS_BLOCKS) return fail("value net plan: pass size");
+        for (uint32_t j = 0; j < ps.n; j++) {
+            const uint32_t rb = ps.rb[j];
+            if (rb >= nrb || seen[rb]) return fail("value net plan: row block repeated or out of range");
+            seen[rb] = 1;
+            if (ps.cols < (cols ? cols[rb] : heads)) return fail("value net plan: head columns");
+        }
+    }
+    for (uint32_t rb = 0; rb < nrb; rb++)
+        if (!seen[rb]) return fail("value net plan: row block missing");
+    return true;
+}
+
+std::vector<ChainPass> plan_chain(const uint32_t* cols, uint32_t nrb, uint32_t heads, uint32_t cus) {
+    std::vector<ChainPass> out;
+    if (!nrb) return out;
+    cus = std::max(cus, 1u);
+    auto width = [&](uint32_t rb) { return cols ? cols[rb] : heads; };
+    std::vector<uint32_t> order(nrb);
+    for (uint32_t i = 0; i < nrb; i++) order[i] = i;
+    std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return width(a) > width(b); });
+    // Cost in units of one 16-row block's trunk: a pass costs about three of
+    // them on top of its blocks, and each 16 head columns of a block about 0.024
+    // (measured on the 512 -> 3 x 384 net).
+    const double pass_cost = 3.0, col_cost = 0.024;
+    std::vector<double> c(nrb);
+    double total = 0.0, cmax = 0.0;
+    for (uint32_t i = 0; i < nrb; i++) {
+        c[i] = 1.0 + col_cost * ((width(order[i]) + 15) / 16);
+        total += c[i];
+        cmax = std::max(cmax, c[i]);
+    }
+    // Shares of consecutive blocks under a cost bound t; returns their ends.
+    auto deal = [&](double t, std::vector<uint32_t>* ends) {
+        uint32_t shares = 0, i = 0;
+        while (i < nrb) {
+            uint32_t n = 0;
+            double sum = 0.0;
+            while (i < nrb) {
+                const double with = pass_cost * ((n + CHAIN_PASS_BLOCKS) / CHAIN_PASS_BLOCKS) + sum + c[i];
+                if (n > 0 && with > t) break;
+                sum += c[i];
+                n++;
+                i++;
+            }
+            shares++;
+            if (ends) ends->push_back(i);
+        }
+        return shares;
+    };
+    double lo = pass_cost + cmax, hi = pass_cost * ((nrb + CHAIN_PASS_BLOCKS - 1) / CHAIN_PASS_BLOCKS) + total;
+    for (int it = 0; it < 48 && hi - lo > 1e-6 * hi; it++) {  // the least bound that fits the CUs
+        const double mid = 0.5 * (lo + hi);
+        if (deal(mid, nullptr) <= cus)
+            hi = mid;
+        else
+            lo = mid;
+    }
+    std::vector<uint32_t> ends;
+    deal(hi, &ends);
+    std::vector<uint32_t> starts(ends.size());
+    for (size_t k = 0; k < ends.size(); k++) starts[k] = k ? ends[k - 1] : 0;
+    for (uint32_t round = 0;; round++) {
+        bool any = false;
+        for (size_t k = 0; k < ends.size(); k++) {
+            const uint32_t b = starts[k] + round * CHAIN_PASS_BLOCKS;
+            if (b >= ends[k]) continue;
+            any = true;
+            ChainPass ps{};
+            ps.n = std::min(CHAIN_PASS_BLOCKS, ends[k] - b);
+            for (uint32_t j = 0; j < ps.n; j++) {
+                ps.rb[j] = order[b + j];
+                ps.cols = std::max(ps.cols, width(order[b + j]));
+            }
+            out.push_back(ps);
+        }
+        if (!any) break;
+    }
+    // Longest first: CUs that take the next pass as they free up then end
+    // close together (the shares set the pass sizes).
+    auto cost = [&](const ChainPass& ps) { return pass_cost + ps.n * (1.0 + col_cost * ((ps.cols + 15) / 16)); };
+    std::stable_sort(out.begin(), out.end(),
+                     [&](const ChainPass& a, const ChainPass& b) { return cost(a) > cost(b); });
+    return out;
 }
 
 // Algorithmic HBM bytes of one CFR iteration (readout, backprop with the

@@ -117,6 +117,34 @@ struct PoolGroup {
 };
 static_assert(sizeof(PoolGroup) == 18 * 4, "PoolGroup is 72 bytes");
 
+// One pass of the fused value net: up to CHAIN_PASS_BLOCKS 16-row blocks of the
+// network rows (any blocks, in any order; rb[0 .. n)) and the head columns
+// they need (cols).
+constexpr uint32_t CHAIN_PASS_BLOCKS = 8;
+struct ChainPass {
+    uint32_t rb[CHAIN_PASS_BLOCKS];
+    uint32_t n, cols, pad[2];
+};
+static_assert(sizeof(ChainPass) == 12 * 4, "ChainPass is 48 bytes");
+
+// Passes of the fused value net over nrb row blocks whose head widths are
+// cols[rb] (cols null: every block needs `heads`), for a device of `cus`
+// compute units that each run one pass at a time. Blocks are taken widest
+// head first; consecutive blocks of that order are dealt to at most `cus`
+// shares of about equal estimated cost (a per-pass overhead, a per-block
+// trunk cost and a per-block head cost that grows with the width), each share
+// is cut into passes of up to CHAIN_PASS_BLOCKS blocks, and the passes are
+// listed by estimated cost, longest first: run in list order on CUs that take
+// the next pass as they free up (longest-processing-time-first list
+// scheduling), the last passes end at about the same time. Every block is in
+// exactly one pass.
+std::vector<ChainPass> plan_chain(const uint32_t* cols, uint32_t nrb, uint32_t heads, uint32_t cus);
+// What the fused kernel assumes of a plan: every block below nrb in exactly
+// one pass, 1..CHAIN_PASS_BLOCKS blocks per pass, and each pass's cols at
+// least every one of its blocks' widths.
+bool check_chain_plan(const std::vector<ChainPass>& plan, const uint32_t* cols, uint32_t nrb, uint32_t heads,
+                      std::string* err);
+
 // Default unit budget in value slots (floats of one player's value vector).
 constexpr uint32_t UNIT_SLOTS = 4096;
 
@@ -150,6 +178,8 @@ struct WaveHost {
     // Head columns each 128-row tile of the network rows needs: 1 + the largest
     // head key among the tile's configs (the head GEMM skips the rest).
     std::vector<uint32_t> head_tile_n;
+    // The same per 16-row block and player: the keys of that player's configs.
+    std::vector<uint32_t> head_rb_n[2];
     std::vector<uint32_t> term_node;
     std::vector<float> term_util;
     std::vector<float> roots, carried;
