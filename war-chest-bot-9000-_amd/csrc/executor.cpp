@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <thread>
 
 #include "../../include/wc_wave.h"
 
@@ -31,15 +32,38 @@ float cfr_factor(float t, float p) {
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// The table blob: arrays at 256-byte aligned offsets, laid out first, then
+// copied into pinned staging memory on several host threads (the upload is one
+// asynchronous copy from there). The sources must outlive copy_to.
 struct Blob {
-    std::vector<uint8_t>& b;
-    explicit Blob(std::vector<uint8_t>& buf) : b(buf) { b.clear(); }
+    struct Piece {
+        const uint8_t* src;
+        size_t bytes, at;
+    };
+    std::vector<Piece> pieces;
+    size_t size = 0;
     template <class T>
     size_t put(const std::vector<T>& v) {
-        size_t at = align256(b.size());
-        b.resize(at + std::max<size_t>(v.size() * sizeof(T), 4), 0);
-        if (!v.empty()) std::memcpy(b.data() + at, v.data(), v.size() * sizeof(T));
+        const size_t at = align256(size), bytes = v.size() * sizeof(T);
+        if (bytes) pieces.push_back({(const uint8_t*)v.data(), bytes, at});
+        size = at + std::max<size_t>(bytes, 4);
         return at;
+    }
+    void copy_to(uint8_t* dst) const {
+        constexpr size_t CHUNK = size_t(8) << 20;
+        std::vector<Piece> parts;  // pieces cut into chunks of at most CHUNK bytes
+        for (const Piece& pc : pieces)
+            for (size_t o = 0; o < pc.bytes; o += CHUNK)
+                parts.push_back({pc.src + o, std::min(CHUNK, pc.bytes - o), pc.at + o});
+        const size_t nt = std::min<size_t>(std::max(1u, std::min(8u, std::thread::hardware_concurrency())),
+                                           parts.size());
+        auto work = [&](size_t t) {
+            for (size_t k = t; k < parts.size(); k += nt) std::memcpy(dst + parts[k].at, parts[k].src, parts[k].bytes);
+        };
+        std::vector<std::thread> th;
+        for (size_t t = 1; t < nt; t++) th.emplace_back(work, t);
+        if (nt) work(0);
+        for (auto& x : th) x.join();
     }
 };
 
@@ -77,6 +101,8 @@ Executor::~Executor() {
     hipFree(table_);
     hipFree(arena_);
     hipFree(mlp_);
+    if (pin_) hipHostFree(pin_);
+    if (res_pin_) hipHostFree(res_pin_);
     hipStreamDestroy(stream_);
 }
 
@@ -90,6 +116,25 @@ bool Executor::ensure(void** p, size_t* cap, size_t need, std::string* err) {
     size_t sz = 1;
     while (sz < need) sz <<= 1;  // power-of-two reservation, as the reference's arena
     HIP_TRY(hipMalloc(p, sz));
+    *cap = sz;
+    return true;
+}
+
+// Grow-only pinned host staging (a power-of-two reservation, like the device
+// buffers); the stream is drained before a buffer is replaced.
+bool Executor::ensure_pinned(uint8_t** p, size_t* cap, size_t need, std::string* err) {
+    if (need <= *cap && *p) return true;
+    if (*p) {
+        HIP_TRY(hipStreamSynchronize(stream_));
+        HIP_TRY(hipHostFree(*p));
+        *p = nullptr;
+        *cap = 0;
+    }
+    size_t sz = 1;
+    while (sz < need) sz <<= 1;
+    void* q = nullptr;
+    HIP_TRY(hipHostMalloc(&q, sz, hipHostMallocDefault));
+    *p = (uint8_t*)q;
     *cap = sz;
     return true;
 }
@@ -249,41 +294,27 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         return false;
     }
     HIP_TRY(hipSetDevice(device_));
-    Blob blob(host_blob_);
+    Blob blob;
     struct Off {
-        size_t node_meta, nc, child_start, child, legal_row_of, legal_off, legal_value, draw_off, draw_row_off,
-            draw_row_start, draw_to, draw_p, reach_base, vals_base, parent, rev_row_of, rev_start, rev_src, rev_cell,
-            rvd_row_of, rvd_start, rvd_src, rvd_p, row_node, row_cfg_off, row_cfg, cfg_key, cfg_emb, pub_raw,
-            term_node, term_util, roots, carried, exit_node, exit_coff, trees, units, bt[2], rt[2], dc[2], bl[2],
-            rl[2], cv[2], lr[2], pg[2], twb[2], twu[2], cfg_priv, unit_row, unit_term, tb[2], tr[2], head_tile_n, cp[2];
+        size_t node_meta, nc, legal_value, draw_to, draw_p, reach_base, vals_base, rev_src, rev_cell, rvd_src, rvd_p,
+            row_node, row_cfg_off, row_cfg, cfg_emb, pub_raw, term_node, term_util, roots, carried, exit_node,
+            exit_coff, trees, units, bt[2], rt[2], dc[2], bl[2], rl[2], cv[2], lr[2], pg[2], twb[2], twu[2], cfg_priv,
+            unit_term, tb[2], tr[2], head_tile_n, cp[2];
     } o;
     o.node_meta = blob.put(w.node_meta);
     o.nc = blob.put(w.node_nc);
-    o.child_start = blob.put(w.child_start);
-    o.child = blob.put(w.child);
-    o.legal_row_of = blob.put(w.legal_row_of);
-    o.legal_off = blob.put(w.legal_off);
     o.legal_value = blob.put(w.legal_value);
-    o.draw_off = blob.put(w.draw_off);
-    o.draw_row_off = blob.put(w.draw_row_off);
-    o.draw_row_start = blob.put(w.draw_row_start);
     o.draw_to = blob.put(w.draw_to);
     o.draw_p = blob.put(w.draw_p);
     o.reach_base = blob.put(w.reach_base);
     o.vals_base = blob.put(w.vals_base);
-    o.parent = blob.put(w.parent);
-    o.rev_row_of = blob.put(w.rev_row_of);
-    o.rev_start = blob.put(w.rev_start);
     o.rev_src = blob.put(w.rev_src);
     o.rev_cell = blob.put(w.rev_cell);
-    o.rvd_row_of = blob.put(w.rvd_row_of);
-    o.rvd_start = blob.put(w.rvd_start);
     o.rvd_src = blob.put(w.rvd_src);
     o.rvd_p = blob.put(w.rvd_p);
     o.row_node = blob.put(w.row_node);
     o.row_cfg_off = blob.put(w.row_cfg_off);
     o.row_cfg = blob.put(w.row_cfg);
-    o.cfg_key = blob.put(w.cfg_key);
     o.cfg_emb = blob.put(w.cfg_emb);
     o.cfg_priv = blob.put(w.cfg_priv);
     o.pub_raw = blob.put(w.pub_raw);
@@ -307,7 +338,6 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         o.bl[p] = blob.put(w.back_lvl[p]);
         o.rl[p] = blob.put(w.reach_lvl[p]);
     }
-    o.unit_row = blob.put(w.unit_row);
     o.unit_term = blob.put(w.unit_term);
     o.head_tile_n = blob.put(w.head_tile_n);
     std::vector<ChainPass> plan[2];
@@ -322,8 +352,10 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         o.tb[p] = blob.put(w.top_back_rec[p]);
         o.tr[p] = blob.put(w.top_reach_rec[p]);
     }
-    if (!ensure(&table_, &table_cap_, host_blob_.size(), err)) return false;
-    HIP_TRY(hipMemcpyAsync(table_, host_blob_.data(), host_blob_.size(), hipMemcpyHostToDevice, stream_));
+    if (!ensure(&table_, &table_cap_, blob.size, err)) return false;
+    if (!ensure_pinned(&pin_, &pin_cap_, blob.size, err)) return false;
+    blob.copy_to(pin_);
+    HIP_TRY(hipMemcpyAsync(table_, pin_, blob.size, hipMemcpyHostToDevice, stream_));
 
     // Mutable arena.
     const size_t cells = std::max<uint32_t>(w.ncells, 1), rl = std::max<uint32_t>(w.reach_len, 1),
@@ -370,31 +402,18 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     d = WaveDev{};
     d.node_meta = (const uint32_t*)(T + o.node_meta);
     d.nc = (const uint32_t*)(T + o.nc);
-    d.child_start = (const uint32_t*)(T + o.child_start);
-    d.child = (const uint32_t*)(T + o.child);
-    d.legal_row_of = (const uint32_t*)(T + o.legal_row_of);
-    d.legal_off = (const uint32_t*)(T + o.legal_off);
     d.legal_value = (const uint32_t*)(T + o.legal_value);
-    d.draw_off = (const uint32_t*)(T + o.draw_off);
-    d.draw_row_off = (const uint32_t*)(T + o.draw_row_off);
-    d.draw_row_start = (const uint32_t*)(T + o.draw_row_start);
     d.draw_to = (const uint32_t*)(T + o.draw_to);
     d.draw_p = (const float*)(T + o.draw_p);
     d.reach_base = (const uint32_t*)(T + o.reach_base);
     d.vals_base = (const uint32_t*)(T + o.vals_base);
-    d.parent = (const uint32_t*)(T + o.parent);
-    d.rev_row_of = (const uint32_t*)(T + o.rev_row_of);
-    d.rev_start = (const uint32_t*)(T + o.rev_start);
     d.rev_src = (const uint32_t*)(T + o.rev_src);
     d.rev_cell = (const uint32_t*)(T + o.rev_cell);
-    d.rvd_row_of = (const uint32_t*)(T + o.rvd_row_of);
-    d.rvd_start = (const uint32_t*)(T + o.rvd_start);
     d.rvd_src = (const uint32_t*)(T + o.rvd_src);
     d.rvd_p = (const float*)(T + o.rvd_p);
     d.row_node = (const uint32_t*)(T + o.row_node);
     d.row_cfg_off = (const uint32_t*)(T + o.row_cfg_off);
     d.row_cfg = (const uint32_t*)(T + o.row_cfg);
-    d.cfg_key = (const uint32_t*)(T + o.cfg_key);
     d.cfg_emb = (const float*)(T + o.cfg_emb);
     d.pub_raw = (const uint8_t*)(T + o.pub_raw);
     d.term_node = (const uint32_t*)(T + o.term_node);
@@ -422,7 +441,6 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         d.reach_lvl[p] = (const uint32_t*)(T + o.rl[p]);
         d.ndec[p] = (uint32_t)w.decision[p].size();
     }
-    d.unit_row = (const uint32_t*)(T + o.unit_row);
     d.unit_term = (const uint32_t*)(T + o.unit_term);
     head_tile_n_ = (const uint32_t*)(T + o.head_tile_n);
     for (int p = 0; p < 2; p++) chain_plan_[p] = (const ChainPass*)(T + o.cp[p]);
@@ -701,14 +719,17 @@ bool Executor::solve(const WaveHost& w, uint64_t version, std::vector<Result>* o
     if (!upload(w, it->second, err)) return false;
     run_schedule(w, it->second, nullptr);
     HIP_TRY(hipGetLastError());
-    // Collect (Harvest::unpack): per-job slices back to solve-local indices.
-    std::vector<float> strat(w.ncells), roots(w.root_values_len);
-    std::vector<uint16_t> carry(size_t(w.carry_slots) * w.snapshot_configs);
-    if (w.ncells) HIP_TRY(hipMemcpyAsync(strat.data(), dev_.snap, strat.size() * 4, hipMemcpyDeviceToHost, stream_));
-    if (!roots.empty())
-        HIP_TRY(hipMemcpyAsync(roots.data(), dev_.root_values, roots.size() * 4, hipMemcpyDeviceToHost, stream_));
-    if (!carry.empty())
-        HIP_TRY(hipMemcpyAsync(carry.data(), dev_.carry, carry.size() * 2, hipMemcpyDeviceToHost, stream_));
+    // Collect (Harvest::unpack): the outputs into pinned memory, then per-job
+    // slices back to solve-local indices.
+    const size_t ns_ = w.ncells, nr = w.root_values_len, nc = size_t(w.carry_slots) * w.snapshot_configs;
+    const size_t o_roots = align256(ns_ * 4), o_carry = o_roots + align256(nr * 4);
+    if (!ensure_pinned(&res_pin_, &res_pin_cap_, o_carry + nc * 2 + 4, err)) return false;
+    const float* strat = (const float*)res_pin_;
+    const float* roots = (const float*)(res_pin_ + o_roots);
+    const uint16_t* carry = (const uint16_t*)(res_pin_ + o_carry);
+    if (ns_) HIP_TRY(hipMemcpyAsync(res_pin_, dev_.snap, ns_ * 4, hipMemcpyDeviceToHost, stream_));
+    if (nr) HIP_TRY(hipMemcpyAsync(res_pin_ + o_roots, dev_.root_values, nr * 4, hipMemcpyDeviceToHost, stream_));
+    if (nc) HIP_TRY(hipMemcpyAsync(res_pin_ + o_carry, dev_.carry, nc * 2, hipMemcpyDeviceToHost, stream_));
     HIP_TRY(hipStreamSynchronize(stream_));
     out->clear();
     uint32_t cell0 = 0, cfg0 = 0;
@@ -717,17 +738,17 @@ bool Executor::solve(const WaveHost& w, uint64_t version, std::vector<Result>* o
         const TreeDev& t = w.trees[k];
         Result r;
         r.weight_version = version;
-        r.strategy.assign(strat.begin() + cell0, strat.begin() + cell0 + j.t.ncells);
+        r.strategy.assign(strat + cell0, strat + cell0 + j.t.ncells);
         r.nroots = t.nroots;
         r.n0 = t.n0;
         r.n1 = t.n1;
-        r.root_values.assign(roots.begin() + t.root_value0, roots.begin() + t.root_value0 + t.nroots * (t.n0 + t.n1));
+        r.root_values.assign(roots + t.root_value0, roots + t.root_value0 + t.nroots * (t.n0 + t.n1));
         r.slots = w.carry_slots;
         r.snapshot_configs = j.t.snapshot_configs();
         r.carries.resize(size_t(r.slots) * r.snapshot_configs);
         for (uint32_t sl = 0; sl < r.slots; sl++)
             std::memcpy(r.carries.data() + size_t(sl) * r.snapshot_configs,
-                        carry.data() + size_t(sl) * w.snapshot_configs + cfg0, size_t(r.snapshot_configs) * 2);
+                        carry + size_t(sl) * w.snapshot_configs + cfg0, size_t(r.snapshot_configs) * 2);
         cell0 += j.t.ncells;
         cfg0 += r.snapshot_configs;
         out->push_back(std::move(r));

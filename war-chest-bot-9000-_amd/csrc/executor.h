@@ -90,6 +90,7 @@ class Executor {
     void run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::vector<hipEvent_t>* marks,
                  const uint32_t* head_tile_n, const ChainPass* plan, uint32_t npass);
     bool ensure(void** p, size_t* cap, size_t need, std::string* err);
+    bool ensure_pinned(uint8_t** p, size_t* cap, size_t need, std::string* err);
 
     int device_ = 0, precision_ = 0;
     uint32_t cus_ = 1;  // compute units of the device (fused value net plans)
@@ -106,7 +107,10 @@ class Executor {
     size_t arena_cap_ = 0;
     void* mlp_ = nullptr;  // query inputs, hidden activations, head outputs
     size_t mlp_cap_ = 0;
-    std::vector<uint8_t> host_blob_;
+    uint8_t* pin_ = nullptr;  // pinned staging of the table blob (grow-only)
+    size_t pin_cap_ = 0;
+    uint8_t* res_pin_ = nullptr;  // pinned landing of the collected outputs (grow-only)
+    size_t res_pin_cap_ = 0;
     WaveDev dev_{};
     void* X_ = nullptr;
     void* Xq_[2] = {};  // the wave's query inputs, one per traverser

@@ -24,16 +24,14 @@ __host__ __device__ inline size_t frag_off(uint32_t row, uint32_t k, uint32_t K)
 inline uint32_t gemm_rows(uint32_t rows) { return (rows + GEMM_ROWS - 1) / GEMM_ROWS * GEMM_ROWS; }
 
 struct WaveDev {
-    // immutable tables
-    const uint32_t *node_meta, *nc, *child_start, *child;
-    const uint32_t *legal_row_of, *legal_off, *legal_value;
-    const uint32_t *draw_off, *draw_row_off, *draw_row_start, *draw_to;
+    // immutable tables (the ones the kernels read; row records carry the
+    // offsets into the element arrays)
+    const uint32_t *node_meta, *nc, *legal_value, *draw_to;
     const float* draw_p;
-    const uint32_t *reach_base, *vals_base, *parent;
-    const uint32_t *rev_row_of, *rev_start, *rev_src, *rev_cell;
-    const uint32_t *rvd_row_of, *rvd_start, *rvd_src;
+    const uint32_t *reach_base, *vals_base;
+    const uint32_t *rev_src, *rev_cell, *rvd_src;
     const float* rvd_p;
-    const uint32_t *row_node, *row_cfg_off, *row_cfg, *cfg_key;
+    const uint32_t *row_node, *row_cfg_off, *row_cfg;
     const float* cfg_emb;
     const uint8_t* pub_raw;
     const uint32_t* term_node;
@@ -49,7 +47,7 @@ struct WaveDev {
     const PoolGroup* pool_grp[2];
     const uint32_t* child_vb[2];
     const uint32_t *back_lvl[2], *reach_lvl[2];
-    const uint32_t *unit_row, *unit_term;
+    const uint32_t* unit_term;
     const AccRec* top_acc[2];
     // mutable arena
     float *regret, *cur, *sum, *snap;
