@@ -48,6 +48,17 @@ def test_truncated_and_corrupt_jobs_are_rejected():
         ww.job_validate(j + b"\0")
 
 
+def test_wave_pack_names_the_first_bad_job():
+    # Jobs parse on several threads; the error still names the first bad one.
+    jobs = W.jobs("wave64", trees=5)
+    bad = bytearray(jobs[1])
+    bad[0] ^= 0xFF  # magic
+    jobs[1] = bytes(bad)
+    jobs[3] = jobs[3][: len(jobs[3]) // 2]
+    with pytest.raises(ww.WaveError, match="job 1: .*magic"):
+        ww.Wave(jobs)
+
+
 def test_wave_pack_rejects_mixed_schedules():
     a = W.jobs("tree48")[0]
     b = W.jobs("tree48", iters=8)[0]

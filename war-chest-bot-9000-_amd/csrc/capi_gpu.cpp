@@ -8,6 +8,7 @@
 
 #include "../../include/wc_wave.h"
 #include "common.h"
+#include "par.h"
 #include "executor.h"
 #include "service.h"
 #include "wave.h"
@@ -86,10 +87,19 @@ uint64_t wc_executor_publish(wc_executor* ex, const wc_net_desc* net) {
 int wc_wave_pack(const uint8_t* const* jobs, const size_t* lens, uint32_t njobs, wc_wave** out) {
     if (!jobs || !lens || !out || njobs == 0) return fail(WC_ERR_INVALID, "wc_wave_pack: empty wave");
     std::vector<Job> parsed(njobs);
-    std::string err;
+    std::vector<std::string> errs(njobs);
+    std::vector<uint8_t> bad(njobs, 0);
+    parallel_for(njobs, [&](size_t k) {  // jobs parse independently
+        if (!jobs[k]) {
+            errs[k] = "null job";
+            bad[k] = 1;
+        } else if (!from_bytes(jobs[k], lens[k], &parsed[k], &errs[k])) {
+            bad[k] = 1;
+        }
+    });
     for (uint32_t k = 0; k < njobs; k++)
-        if (!jobs[k] || !from_bytes(jobs[k], lens[k], &parsed[k], &err))
-            return fail(WC_ERR_INVALID, "job " + std::to_string(k) + ": " + err);
+        if (bad[k]) return fail(WC_ERR_INVALID, "job " + std::to_string(k) + ": " + errs[k]);
+    std::string err;
     // WC_UNIT_SLOTS tunes the subtree-unit budget (value slots per unit).
     uint32_t slots = UNIT_SLOTS;
     if (const char* env = std::getenv("WC_UNIT_SLOTS")) {

@@ -189,7 +189,7 @@ void Service::lane_main(uint32_t lane) {
             jobs.push_back(std::move(p.job));
         }
         WaveHost wh;
-        if (ok) ok = pack_wave(std::move(jobs), &wh, &err);
+        if (ok) ok = pack_wave(std::move(jobs), &wh, &err, UNIT_SLOTS, true);  // validated at submit
         if (ok) ok = ex->solve(wh, exv, &results, &err);
         for (size_t k = 0; k < tickets.size(); k++) {
             auto& t = tickets[k];

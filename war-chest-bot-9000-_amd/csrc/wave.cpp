@@ -1,11 +1,12 @@
 // Host wave packing (counterpart of engine/src/gpu/wave.rs:132-644).
 #include "wave.h"
 
+#include <algorithm>
+#include <cstring>
 #include <string>
 #include <unordered_map>
 
-#include <algorithm>
-#include <cstring>
+#include "par.h"
 
 namespace wc {
 
@@ -85,7 +86,12 @@ void append_shift(std::vector<T>& dst, const std::vector<T>& src, size_t skip, T
 // Row records from the task lists (see BackRec / ReachRec / AccRec).
 void build_records(WaveHost* wp) {
     WaveHost& w = *wp;
-    for (int p = 0; p < 2; p++) {
+    // The two players' records are independent (each thread writes only its
+    // player's lists and fields); the export bits of shared terminal entries
+    // are gathered per player and merged after.
+    std::vector<uint8_t> term_ex[2];
+    parallel_for(2, [&](size_t pi) {
+        const int p = (int)pi;
         std::vector<uint32_t> cvb_at(w.nodes(), NONE);
         auto back = [&](const Task& q) {
             const uint32_t node = q.node, c = q.config;
@@ -131,6 +137,10 @@ void build_records(WaveHost* wp) {
             }
             return r;
         };
+        w.back_rec[p].reserve(w.back_task[p].size());
+        w.top_back_rec[p].reserve(w.top_back[p].size());
+        w.reach_rec[p].reserve(w.reach_task[p].size());
+        w.top_reach_rec[p].reserve(w.top_reach[p].size());
         for (const Task& q : w.back_task[p]) w.back_rec[p].push_back(back(q));
         for (const Task& q : w.top_back[p]) w.top_back_rec[p].push_back(back(q));
         for (const Task& q : w.reach_task[p]) w.reach_rec[p].push_back(reach(q));
@@ -182,22 +192,27 @@ void build_records(WaveHost* wp) {
         for (BackRec& r : w.back_rec[p])
             if (ex[r.out]) r.kn |= REC_EXPORT;
         for (LeafRec& r : w.leaf_rec[p]) r.exported = ex[r.out];
-        for (uint32_t& te : w.unit_term) {
-            const uint32_t node = w.term_node[te & TERM_INDEX];
+        term_ex[p].assign(w.unit_term.size(), 0);
+        for (size_t k = 0; k < w.unit_term.size(); k++) {
+            const uint32_t node = w.term_node[w.unit_term[k] & TERM_INDEX];
             for (uint32_t c = 0; c < w.nc(node, p); c++)
-                if (ex[w.vals_base[2 * node + p] + c]) te |= term_export(p);
+                if (ex[w.vals_base[2 * node + p] + c]) term_ex[p][k] = 1;
         }
+        w.acc_rec[p].reserve(w.decision[p].size());
         for (const Task& q : w.decision[p]) {
             uint32_t row = w.legal_row_of[q.node] + q.config;
             w.acc_rec[p].push_back({w.reach_base[2 * q.node + p] + q.config, w.legal_off[row],
                                     w.legal_off[row + 1] - w.legal_off[row], 0});
         }
-    }
+    });
+    for (size_t k = 0; k < w.unit_term.size(); k++)
+        for (int p = 0; p < 2; p++)
+            if (term_ex[p][k]) w.unit_term[k] |= term_export(p);
 }
 
 }  // namespace
 
-bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_t unit_slots) {
+bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_t unit_slots, bool validated) {
     if (jobs.empty()) {
         *err = "cannot pack an empty wave";
         return false;
@@ -214,8 +229,16 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
         *err = "the v5 leaf network is not built by this executor";
         return false;
     }
-    for (auto& j : jobs)
-        if (!validate(j, err)) return false;
+    if (!validated) {  // jobs validate independently; the first failure in job order is reported
+        std::vector<std::string> errs(jobs.size());
+        std::vector<uint8_t> bad(jobs.size(), 0);
+        parallel_for(jobs.size(), [&](size_t k) { bad[k] = !validate(jobs[k], &errs[k]); });
+        for (size_t k = 0; k < jobs.size(); k++)
+            if (bad[k]) {
+                *err = errs[k];
+                return false;
+            }
+    }
     for (uint32_t x : w.meta.snap_iters)
         if (x > w.meta.iters) {
             *err = "snap_iters beyond iters";
@@ -632,6 +655,22 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         *err = std::string("wave bounds: ") + m;
         return false;
     };
+    // The first failure of check(i) over [0, n) in index order (nullptr: none),
+    // checked in chunks on several host threads.
+    auto first_fail = [&](uint64_t n, auto check) -> const char* {
+        const uint64_t chunk = 4096, nch = (n + chunk - 1) / chunk;
+        std::vector<const char*> e(nch, nullptr);
+        parallel_for(nch, [&](size_t c) {
+            for (uint64_t i = c * chunk; i < std::min<uint64_t>(n, (c + 1) * chunk); i++)
+                if (const char* m = check(i)) {
+                    e[c] = m;
+                    return;
+                }
+        });
+        for (const char* m : e)
+            if (m) return m;
+        return nullptr;
+    };
     const uint64_t N = w.nodes();
     if (w.node_nc.size() != 2 * N || w.child_start.size() != N + 1 || w.legal_row_of.size() != N ||
         w.draw_off.size() != N || w.draw_row_off.size() != N || w.reach_base.size() != 2 * N ||
@@ -639,58 +678,60 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         return fail("node arrays disagree");
     if (w.legal_value.size() != w.ncells || w.legal_off.empty() || w.legal_off.back() != w.ncells)
         return fail("cell arrays disagree");
-    for (uint64_t i = 0; i < N; i++) {
+    auto node_check = [&](uint64_t i) -> const char* {
         uint32_t kind = w.node_meta[i] & 3u, actor = w.node_meta[i] >> 2;
-        if (kind > 2 || actor > 1) return fail("node_meta");
+        if (kind > 2 || actor > 1) return "node_meta";
         for (int p = 0; p < 2; p++) {
             uint64_t n = w.nc((uint32_t)i, p);
-            if (uint64_t(w.reach_base[2 * i + p]) + n > w.reach_len) return fail("reach slot");
-            if (uint64_t(w.vals_base[2 * i + p]) + n > w.vals_len) return fail("value slot");
+            if (uint64_t(w.reach_base[2 * i + p]) + n > w.reach_len) return "reach slot";
+            if (uint64_t(w.vals_base[2 * i + p]) + n > w.vals_len) return "value slot";
         }
-        if (w.child_start[i + 1] < w.child_start[i] || w.child_start[i + 1] > w.child.size()) return fail("child CSR");
+        if (w.child_start[i + 1] < w.child_start[i] || w.child_start[i + 1] > w.child.size()) return "child CSR";
         for (uint32_t x = w.child_start[i]; x < w.child_start[i + 1]; x++)
-            if (w.child[x] >= N || w.parent[w.child[x]] != i) return fail("child index");
+            if (w.child[x] >= N || w.parent[w.child[x]] != i) return "child index";
         if (kind == 0) {
             uint64_t r0 = w.legal_row_of[i], nc = w.nc((uint32_t)i, actor);
-            if (r0 == NONE || r0 + nc + 1 > w.legal_off.size()) return fail("legal rows");
+            if (r0 == NONE || r0 + nc + 1 > w.legal_off.size()) return "legal rows";
             for (uint64_t r = r0; r < r0 + nc; r++)
-                if (w.legal_off[r + 1] < w.legal_off[r] || w.legal_off[r + 1] > w.ncells) return fail("legal_off");
-            if (w.child_start[i + 1] == w.child_start[i]) return fail("decision node without children");
+                if (w.legal_off[r + 1] < w.legal_off[r] || w.legal_off[r + 1] > w.ncells) return "legal_off";
+            if (w.child_start[i + 1] == w.child_start[i]) return "decision node without children";
         } else if (kind == 1) {
-            if (w.child_start[i + 1] != w.child_start[i] + 1) return fail("chance child");
+            if (w.child_start[i + 1] != w.child_start[i] + 1) return "chance child";
             uint32_t ch = w.child[w.child_start[i]];
             uint64_t rb = w.draw_row_off[i], nc = w.nc((uint32_t)i, actor);
-            if (rb + nc + 1 > w.draw_row_start.size()) return fail("draw rows");
+            if (rb + nc + 1 > w.draw_row_start.size()) return "draw rows";
             for (uint64_t c = 0; c < nc; c++) {
                 uint64_t lo = w.draw_row_start[rb + c], hi = w.draw_row_start[rb + c + 1];
-                if (hi < lo || uint64_t(w.draw_off[i]) + hi > w.draw_to.size()) return fail("draw entries");
+                if (hi < lo || uint64_t(w.draw_off[i]) + hi > w.draw_to.size()) return "draw entries";
                 for (uint64_t x = lo; x < hi; x++)
-                    if (w.draw_to[w.draw_off[i] + x] >= w.nc(ch, actor)) return fail("draw_to");
+                    if (w.draw_to[w.draw_off[i] + x] >= w.nc(ch, actor)) return "draw_to";
             }
         }
         uint32_t par = w.parent[i];
         if (par != NONE) {
-            if (par >= N) return fail("parent");
+            if (par >= N) return "parent";
             int p = (int)(w.node_meta[par] >> 2);
             uint64_t nc = w.nc((uint32_t)i, p);
             if (w.rev_row_of[i] != NONE) {
                 uint64_t r0 = w.rev_row_of[i];
-                if (r0 + nc + 1 > w.rev_start.size()) return fail("rev rows");
+                if (r0 + nc + 1 > w.rev_start.size()) return "rev rows";
                 for (uint64_t c = 0; c < nc; c++)
                     for (uint64_t x = w.rev_start[r0 + c]; x < w.rev_start[r0 + c + 1]; x++)
                         if (x >= w.rev_src.size() || w.rev_src[x] >= w.nc(par, p) || w.rev_cell[x] >= w.ncells)
-                            return fail("rev entry");
+                            return "rev entry";
             } else if (w.rvd_row_of[i] != NONE) {
                 uint64_t r0 = w.rvd_row_of[i];
-                if (r0 + nc + 1 > w.rvd_start.size()) return fail("rvd rows");
+                if (r0 + nc + 1 > w.rvd_start.size()) return "rvd rows";
                 for (uint64_t c = 0; c < nc; c++)
                     for (uint64_t x = w.rvd_start[r0 + c]; x < w.rvd_start[r0 + c + 1]; x++)
-                        if (x >= w.rvd_src.size() || w.rvd_src[x] >= w.nc(par, p)) return fail("rvd entry");
+                        if (x >= w.rvd_src.size() || w.rvd_src[x] >= w.nc(par, p)) return "rvd entry";
             } else {
-                return fail("node without gather rows");
+                return "node without gather rows";
             }
         }
-    }
+            return nullptr;
+    };
+    if (const char* m = first_fail(N, node_check)) return fail(m);
     for (uint32_t v : w.legal_value)
         if (v != NONE && v >= w.vals_len) return fail("legal_value");
     const uint64_t rows = w.rows();
@@ -823,12 +864,12 @@ bool validate_deep(const WaveHost& w, std::string* err) {
             w.reach_rec[p].size() != w.reach_task[p].size() || w.top_reach_rec[p].size() != w.top_reach[p].size() ||
             w.acc_rec[p].size() != w.decision[p].size())
             return fail("record counts");
-        for (const BackRec& r : w.back_rec[p])
-            if (!back_ok(r)) return fail("back record");
+        if (first_fail(w.back_rec[p].size(), [&](uint64_t k) { return back_ok(w.back_rec[p][k]) ? nullptr : "x"; }))
+            return fail("back record");
         for (const BackRec& r : w.top_back_rec[p])
             if (!back_ok(r)) return fail("top back record");
-        for (const ReachRec& r : w.reach_rec[p])
-            if (!reach_ok(r)) return fail("reach record");
+        if (first_fail(w.reach_rec[p].size(), [&](uint64_t k) { return reach_ok(w.reach_rec[p][k]) ? nullptr : "x"; }))
+            return fail("reach record");
         for (const ReachRec& r : w.top_reach_rec[p])
             if (!reach_ok(r)) return fail("top reach record");
         for (const AccRec& r : w.acc_rec[p])
@@ -861,22 +902,23 @@ bool validate_deep(const WaveHost& w, std::string* err) {
     // The subtree sweep keeps each unit's values in LDS: every slot a unit
     // writes (its leaves, its rows) and reads (its rows' children) must lie
     // inside the unit's window.
-    for (const UnitDev& u : w.units)
+    auto unit_check = [&](uint64_t ui) -> const char* {
+        const UnitDev& u = w.units[ui];
         for (int p = 0; p < 2; p++) {
             const uint64_t lo = u.vwin[p], hi = lo + u.vwin_n[p];
             auto in = [&](uint64_t i) { return i >= lo && i < hi; };
-            if (u.leaf0[p] > u.leaf1[p] || u.leaf1[p] > w.leaf_rec[p].size()) return fail("unit leaf range");
+            if (u.leaf0[p] > u.leaf1[p] || u.leaf1[p] > w.leaf_rec[p].size()) return "unit leaf range";
             for (uint32_t k = u.leaf0[p]; k < u.leaf1[p]; k++)
-                if (!in(w.leaf_rec[p][k].out)) return fail("unit leaf outside its value window");
+                if (!in(w.leaf_rec[p][k].out)) return "unit leaf outside its value window";
             for (uint32_t k = u.term0; k < u.term1; k++) {
                 uint32_t node = w.term_node[w.unit_term[k] & TERM_INDEX];
                 if (w.nc(node, p) && (!in(w.vals_base[2 * node + p]) || !in(w.vals_base[2 * node + p] + w.nc(node, p) - 1)))
-                    return fail("unit terminal outside its value window");
+                    return "unit terminal outside its value window";
             }
             for (uint32_t x = w.back_lvl[p][u.lvl0]; x < w.back_lvl[p][u.lvl0 + u.nlevels]; x++) {
                 const BackRec& r = w.back_rec[p][x];
                 const uint32_t n = r.kn & REC_N, kind = r.kn >> 30;
-                if (!in(r.out)) return fail("unit row outside its value window");
+                if (!in(r.out)) return "unit row outside its value window";
                 for (uint32_t k = 0; k < n; k++) {
                     uint64_t i;
                     if (kind == BACK_OWN) {
@@ -887,10 +929,13 @@ bool validate_deep(const WaveHost& w, std::string* err) {
                     } else {
                         i = uint64_t(w.child_vb[p][r.start + k]) + r.arg;
                     }
-                    if (!in(i)) return fail("unit row reads outside its value window");
+                    if (!in(i)) return "unit row reads outside its value window";
                 }
             }
         }
+        return nullptr;
+    };
+    if (const char* m = first_fail(w.units.size(), unit_check)) return fail(m);
     for (const TreeDev& t : w.trees) {
         if (uint64_t(t.node0) + t.nodes > N) return fail("tree range");
         if (uint64_t(t.reach0) + t.reach_len > w.reach_len) return fail("reach range");

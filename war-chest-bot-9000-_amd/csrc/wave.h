@@ -227,7 +227,10 @@ struct WaveHost {
 // Pack parsed jobs into one wave. Fails (with a message) on incompatible
 // schedules, malformed tables or unsupported networks. `unit_slots` bounds the
 // value slots of one subtree unit.
-bool pack_wave(std::vector<Job>&& jobs, WaveHost* w, std::string* err, uint32_t unit_slots = UNIT_SLOTS);
+// `validated`: every job already passed validate() (the service checks each
+// job when it is submitted), so the per-job checks are not repeated.
+bool pack_wave(std::vector<Job>&& jobs, WaveHost* w, std::string* err, uint32_t unit_slots = UNIT_SLOTS,
+               bool validated = false);
 
 // Bounds of every index the kernels dereference (run by pack_wave).
 bool validate_deep(const WaveHost& w, std::string* err);
