@@ -69,6 +69,10 @@ def main():
     ap.add_argument("--cpu-trees", type=int, default=0, help="trees in the CPU-baseline sample (0 = 2 per thread)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-mlp", action="store_true", help="skip the GEMM-chain-alone leg")
+    ap.add_argument("--no-host", action="store_true", help="skip the host-path (PCIe-inclusive) leg")
+    ap.add_argument("--service", type=int, default=0, metavar="WAVES",
+                    help="also stream WAVES copies of the wave's subgames through the service (wc_submit / wc_wait) "
+                         "and report the end-to-end rate")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="after the run, copy MIB MiB device to device 3 times (calibrates HBM counters)")
     args = ap.parse_args()
@@ -195,6 +199,51 @@ def main():
                             "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 5)}
         mex.close()
         log(f"[bench] GEMM chain alone: {chain_ms:.4f} ms, {tf:.1f} TFLOP/s")
+
+    if not args.no_host:
+        # The boundary takes host buffers: the same wave through wc_solve_wave
+        # (pinned upload of the packed tables, the schedule, collection and the
+        # per-job unpack), and the packing itself. Reported beside `value`, never as it.
+        t = time.time()
+        ww.Wave(jobs).close()
+        pack_s = time.time() - t
+        ex.solve(wave, ver)  # sizes the pinned staging
+        reps = 3
+        t = time.time()
+        for _ in range(reps):
+            ex.solve(wave, ver)
+        solve_ms = (time.time() - t) / reps * 1e3
+        out["host_path"] = {
+            "solve_ms_per_wave": round(solve_ms, 3),
+            "solve_node_iters_per_s": round(node_iters / (solve_ms * 1e-3), 1),
+            "pack_ms_per_wave": round(pack_s * 1e3, 1),
+            "table_bytes": st["table_bytes"],
+            "note": "wc_solve_wave on a packed wave: pinned H2D of the tables, the schedule, D2H and unpack; "
+                    "pack = parse + validate + wc_wave_pack on the host",
+        }
+        log(f"[bench] host path: solve {solve_ms:.1f} ms per wave, pack {pack_s * 1e3:.0f} ms")
+    if args.service:
+        from concurrent.futures import ThreadPoolExecutor
+
+        lanes, subs = 8, 8
+        cl = ww.spawn(0, net, ww.WC_BF16 if tower else ww.WC_F16, lanes=lanes, wave_jobs=len(jobs),
+                      wave_rows=1 << 30, window_us=100000)
+        for h in [cl.submit(j, tag=i) for i, j in enumerate(jobs)]:  # warm-up wave
+            h.wait()
+        allj = [(i, j) for _ in range(args.service) for i, j in enumerate(jobs)]
+        t = time.time()
+        with ThreadPoolExecutor(subs) as pool:  # wc_submit parses each job: several submitting threads
+            hs = list(pool.map(lambda ij: cl.submit(ij[1], tag=ij[0]), allj))
+        for h in hs:
+            h.wait()
+        dt = time.time() - t
+        cl.close()
+        out["service"] = {"waves": args.service, "lanes": lanes, "submit_threads": subs,
+                          "ms_per_wave": round(dt / args.service * 1e3, 2),
+                          "node_iters_per_s": round(args.service * node_iters / dt, 1),
+                          "note": "end to end: WCJ8 bytes submitted, results waited on; parse at submit, pack on "
+                                  "the lanes, pinned transfers, lanes overlap on their own streams"}
+        log(f"[bench] service: {dt / args.service * 1e3:.1f} ms per wave end to end")
 
     if not args.no_cpu:
         import oracle as O

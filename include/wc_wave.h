@@ -129,7 +129,7 @@ typedef struct wc_wave_stats {
     uint32_t units, top_levels;    /* subtree units, and the depths of the top regions swept per launch */
     uint32_t max_window;           /* value slots of the widest unit window (the sweep stages it in LDS) */
     uint64_t cells, reach_slots, reach_len, vals_len, rev_nnz, rvd_nnz, draw_nnz, snapshot_configs;
-    uint64_t table_bytes, arena_bytes;
+    uint64_t table_bytes, arena_bytes; /* device bytes: the uploaded immutable tables; the solve state */
     uint64_t cfr_bytes_per_iter[2]; /* algorithmic HBM bytes of one CFR iteration, traverser 0 / 1 */
     /* the same bytes by kernel, [traverser][kernel]: subtree value sweep, top-region launches, subtree reach sweep */
     uint64_t cfr_bytes_by_kernel[2][3];

@@ -147,19 +147,19 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
     s->rvd_nnz = h.rvd_src.size();
     s->draw_nnz = h.draw_to.size();
     s->snapshot_configs = h.snapshot_configs;
-    size_t tb = 0;
-    tb += 4 * (h.node_meta.size() + h.node_nc.size() + h.child_start.size() + h.child.size() + h.legal_row_of.size() +
-               h.legal_off.size() + h.legal_value.size() + h.draw_off.size() + h.draw_row_off.size() +
-               h.draw_row_start.size() + h.draw_to.size() + h.draw_p.size() + h.reach_base.size() +
-               h.vals_base.size() + h.parent.size() + h.rev_row_of.size() + h.rev_start.size() + h.rev_src.size() +
-               h.rev_cell.size() + h.rvd_row_of.size() + h.rvd_start.size() + h.rvd_src.size() + h.rvd_p.size() +
-               h.row_node.size() + h.row_cfg_off.size() + h.row_cfg.size() + h.cfg_key.size() + h.cfg_emb.size());
-    tb += h.pub_raw.size();
+    // The immutable tables the executor uploads (without alignment padding).
+    auto bytes = [](const auto& v) { return uint64_t(v.size()) * sizeof(v[0]); };
+    uint64_t tb = bytes(h.node_meta) + bytes(h.node_nc) + bytes(h.legal_value) + bytes(h.draw_to) + bytes(h.draw_p) +
+                  bytes(h.reach_base) + bytes(h.vals_base) + bytes(h.rev_src) + bytes(h.rev_cell) + bytes(h.rvd_src) +
+                  bytes(h.rvd_p) + bytes(h.row_node) + bytes(h.row_cfg_off) + bytes(h.row_cfg) + bytes(h.cfg_emb) +
+                  bytes(h.cfg_priv) + bytes(h.pub_raw) + bytes(h.term_node) + bytes(h.term_util) + bytes(h.roots) +
+                  bytes(h.carried) + bytes(h.exit_node) + bytes(h.exit_coff) + bytes(h.trees) + bytes(h.units) +
+                  bytes(h.unit_term) + bytes(h.head_tile_n);
     for (int p = 0; p < 2; p++)
-        tb += 16 * (h.back_rec[p].size() + h.reach_rec[p].size() + h.acc_rec[p].size() + h.top_back_rec[p].size() +
-                    h.top_reach_rec[p].size() + h.leaf_rec[p].size()) +
-              4 * (h.back_lvl[p].size() + h.reach_lvl[p].size() + h.child_vb[p].size());
-    tb += sizeof(UnitDev) * h.units.size() + 4 * (h.unit_row.size() + h.unit_term.size());
+        tb += bytes(h.back_rec[p]) + bytes(h.reach_rec[p]) + bytes(h.acc_rec[p]) + bytes(h.top_back_rec[p]) +
+              bytes(h.top_reach_rec[p]) + bytes(h.leaf_rec[p]) + bytes(h.back_lvl[p]) + bytes(h.reach_lvl[p]) +
+              bytes(h.child_vb[p]) + bytes(h.pool_grp[p]) + bytes(h.tower_blk[p]) + bytes(h.tower_unit[p]) +
+              bytes(h.top_back_lvl[p]) + bytes(h.top_reach_lvl[p]);
     s->table_bytes = tb;
     s->arena_bytes = 4 * (4ull * h.ncells + 2ull * h.reach_len + h.vals_len + 2ull * h.rows() * (h.net.pool + 1) +
                           h.root_values_len) +
