@@ -337,6 +337,23 @@ def test_service_submit_wait():
         np.testing.assert_array_equal(g.root_values, r.root_values)
 
 
+def test_service_lane_reuses_its_wave_buffers():
+    # One lane packs every wave into the same host lists: a wave of 4 jobs,
+    # then smaller ones, each checked against a fresh solve.
+    jobs = small_wave(trees=7, seed=47)
+    net = W.net_for("wave256")
+    say("case service lane reuse: waves of 4, 2 and 1 jobs through 1 lane")
+    ref = gpu_solve(jobs, net, ww.WC_PRECISE)
+    got = []
+    with ww.spawn(0, net, ww.WC_PRECISE, lanes=1, wave_jobs=4, window_us=2000) as client:
+        for chunk in (jobs[:4], jobs[4:6], jobs[6:]):
+            handles = [client.submit(j, tag=k) for k, j in enumerate(chunk)]
+            got += [h.wait() for h in handles]
+    for g, r in zip(got, ref):
+        np.testing.assert_array_equal(g.strategy, r.strategy)
+        np.testing.assert_array_equal(g.root_values, r.root_values)
+
+
 def test_service_weight_versions_follow_submission():
     jobs = small_wave(trees=4, seed=43)
     net, net2 = W.net_for("wave256"), W.net_for("wave256", seed=2)

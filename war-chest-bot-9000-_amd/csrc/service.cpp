@@ -157,6 +157,7 @@ void Service::lane_main(uint32_t lane) {
         ready_cv_.notify_all();
         if (!ok) return;
     }
+    WaveHost wh;  // reused wave to wave: its lists keep their buffers
     for (;;) {
         std::vector<Pending> wave;
         if (!take_wave(&wave)) break;
@@ -188,7 +189,6 @@ void Service::lane_main(uint32_t lane) {
             tickets.push_back(p.ticket);
             jobs.push_back(std::move(p.job));
         }
-        WaveHost wh;
         if (ok) ok = pack_wave(std::move(jobs), &wh, &err, UNIT_SLOTS, true);  // validated at submit
         if (ok) ok = ex->solve(wh, exv, &results, &err);
         for (size_t k = 0; k < tickets.size(); k++) {

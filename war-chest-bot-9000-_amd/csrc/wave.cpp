@@ -212,12 +212,69 @@ void build_records(WaveHost* wp) {
 
 }  // namespace
 
+constexpr size_t WAVE_HOST_BYTES = 2208;  // sizeof(WaveHost) on x86-64 (libstdc++)
+static_assert(sizeof(WaveHost) == WAVE_HOST_BYTES, "a WaveHost member was added or changed: update reset()");
+void WaveHost::reset() {
+    const WaveHost blank;
+    auto keep = [](auto& v) { v.clear(); };
+    meta = blank.meta;
+    net = blank.net;
+    for (auto* v : {&node_meta, &node_nc, &child_start, &child, &legal_row_of, &legal_off, &legal_value, &draw_off,
+                    &draw_row_off, &draw_row_start, &draw_to, &reach_base, &vals_base, &parent, &rev_row_of,
+                    &rev_start, &rev_src, &rev_cell, &rvd_row_of, &rvd_start, &rvd_src, &row_node, &row_cfg_off,
+                    &row_cfg, &cfg_key, &head_tile_n, &term_node, &exit_node, &exit_coff, &unit_row, &unit_term})
+        keep(*v);
+    for (auto* v : {&draw_p, &rvd_p, &cfg_emb, &cfg_priv, &term_util, &roots, &carried}) keep(*v);
+    keep(jobs);
+    keep(trees);
+    keep(pub_raw);
+    keep(units);
+    keep(node_top);
+    for (int p = 0; p < 2; p++) {
+        keep(head_rb_n[p]);
+        keep(back_task[p]);
+        keep(reach_task[p]);
+        keep(decision[p]);
+        keep(back_lvl[p]);
+        keep(reach_lvl[p]);
+        keep(top_back[p]);
+        keep(top_reach[p]);
+        keep(top_back_lvl[p]);
+        keep(top_reach_lvl[p]);
+        keep(back_rec[p]);
+        keep(top_back_rec[p]);
+        keep(reach_rec[p]);
+        keep(top_reach_rec[p]);
+        keep(acc_rec[p]);
+        keep(leaf_rec[p]);
+        keep(pool_grp[p]);
+        keep(tower_blk[p]);
+        keep(tower_unit[p]);
+        keep(child_vb[p]);
+        top_dec0[p] = blank.top_dec0[p];
+    }
+    reach_len = blank.reach_len;
+    vals_len = blank.vals_len;
+    ncells = blank.ncells;
+    root_values_len = blank.root_values_len;
+    snapshot_configs = blank.snapshot_configs;
+    nsub = blank.nsub;
+    lvl_len = blank.lvl_len;
+    top_levels = blank.top_levels;
+    max_levels = blank.max_levels;
+    nroots_max = blank.nroots_max;
+    carry_slots = blank.carry_slots;
+    max_vwin = blank.max_vwin;
+    tower_len = blank.tower_len;
+}
+
 bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_t unit_slots, bool validated) {
     if (jobs.empty()) {
         *err = "cannot pack an empty wave";
         return false;
     }
-    WaveHost w;
+    WaveHost& w = *out;  // packed in place: a reused WaveHost keeps its buffers
+    w.reset();
     w.meta = jobs[0].meta;
     for (size_t k = 1; k < jobs.size(); k++)
         if (!same_meta(jobs[0].meta, jobs[k].meta)) {
@@ -644,7 +701,6 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     build_records(&w);
     w.jobs = std::move(jobs);
     if (!validate_deep(w, err)) return false;
-    *out = std::move(w);
     return true;
 }
 

@@ -221,6 +221,12 @@ struct WaveHost {
 
     uint32_t nodes() const { return (uint32_t)node_meta.size(); }
     uint32_t rows() const { return (uint32_t)row_node.size(); }
+    // Empty every list, keeping its buffer, and zero every count: packing the
+    // next wave into the same WaveHost then neither allocates nor faults in
+    // fresh pages for lists that have grown before. (A member added to this
+    // struct must be added to reset(): the size check next to it fails until
+    // it is.)
+    void reset();
     uint32_t nc(uint32_t node, int p) const { return node_nc[2 * node + p]; }
 };
 
