@@ -630,7 +630,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     if (tower) run_tower_private(bank);  // F for this wave's configs under this bank
     launch_zero(d.regret, w.ncells, s);
     launch_init_strategy(d, s);
-    launch_seed_reach(d, d.reach, -1, s);
+    launch_seed_reach(d, d.reach, w.reach_len, -1, s);
     reach_both(d.reach, d.cur);
     launch_seed_sum(d, s);
     if (w.carry_slots) launch_gather_carry(d, d.reach, 0, s);
@@ -658,7 +658,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
             size_t si = size_t(it - m.snap_iters.begin());
             launch_normalize(d, 1, done >= 2 ? 1 : 0, s);
             if (m.snapshots && si + 1 < m.snap_iters.size()) {
-                launch_seed_reach(d, d.snap_reach, -1, s);
+                launch_seed_reach(d, d.snap_reach, w.reach_len, -1, s);
                 reach_both(d.snap_reach, d.snap);
                 launch_gather_carry(d, d.snap_reach, (int)si, s);
             }
@@ -667,7 +667,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     }
     // Phase 2: root values under the final average for every carried root.
     for (uint32_t root = 0; root < w.nroots_max; root++) {
-        launch_seed_reach(d, d.reach, (int)root, s);
+        launch_seed_reach(d, d.reach, w.reach_len, (int)root, s);
         reach_both(d.reach, d.snap);
         mark(C_OTHER);
         launch_pool(d, -1, precision_, Xq_[0], Xq_[1], s);

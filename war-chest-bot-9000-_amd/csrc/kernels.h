@@ -69,7 +69,9 @@ struct WaveDev {
 // Launchers (kernels.hip). All take the executor's stream.
 void launch_zero(float* p, size_t n, hipStream_t s);
 void launch_init_strategy(const WaveDev& w, hipStream_t s);
-void launch_seed_reach(const WaveDev& w, float* reach, int root_index, hipStream_t s);
+// Zero `reach` (reach_len floats), then write every tree's root beliefs
+// (root_index < 0) or its carried root `root_index`.
+void launch_seed_reach(const WaveDev& w, float* reach, size_t reach_len, int root_index, hipStream_t s);
 // Top-down reach of subtree units [unit0, unit0 + n) under `strat`, for one
 // player or both (player < 0); with `accumulate`, then sum = sum * ds + reach *
 // cur over the player's decision rows of each unit and of the top regions.

@@ -72,10 +72,9 @@ void launch_init_strategy(const WaveDev& w, hipStream_t s) {
 }
 
 // Zero one tree's reach span and write its root (or carried root k) beliefs.
+// Root beliefs into the zeroed reach (launch_seed_reach clears it first).
 __global__ void k_seed_reach(WaveDev w, float* reach, int root_index) {
     const TreeDev t = w.trees[blockIdx.x];
-    for (uint32_t i = threadIdx.x; i < t.reach_len; i += blockDim.x) reach[t.reach0 + i] = 0.0f;
-    __syncthreads();
     if (root_index >= (int)t.nroots) return;
     const float* src = root_index < 0 ? w.roots + t.root0 : w.carried + t.carried0 + (size_t)root_index * (t.n0 + t.n1);
     for (uint32_t i = threadIdx.x; i < t.n0 + t.n1; i += blockDim.x) {
@@ -85,7 +84,8 @@ __global__ void k_seed_reach(WaveDev w, float* reach, int root_index) {
     }
 }
 
-void launch_seed_reach(const WaveDev& w, float* reach, int root_index, hipStream_t s) {
+void launch_seed_reach(const WaveDev& w, float* reach, size_t reach_len, int root_index, hipStream_t s) {
+    launch_zero(reach, reach_len, s);  // every tree's reach span: the trees tile [0, reach_len)
     hipLaunchKernelGGL(k_seed_reach, dim3(w.ntrees), dim3(BLOCK), 0, s, w, reach, root_index);
 }
 
