@@ -131,8 +131,9 @@ typedef struct wc_wave_stats {
     uint64_t cells, reach_slots, reach_len, vals_len, rev_nnz, rvd_nnz, draw_nnz, snapshot_configs;
     uint64_t table_bytes, arena_bytes; /* device bytes: the uploaded immutable tables; the solve state */
     uint64_t cfr_bytes_per_iter[2]; /* algorithmic HBM bytes of one CFR iteration, traverser 0 / 1 */
-    /* the same bytes by kernel, [traverser][kernel]: subtree value sweep, top-region launches, subtree reach sweep */
-    uint64_t cfr_bytes_by_kernel[2][3];
+    /* the same bytes by launch, [traverser][k]: subtree value sweep, top-region launches, subtree reach sweep,
+     * average-strategy accumulation (run in the leaf-input launch) */
+    uint64_t cfr_bytes_by_kernel[2][4];
     uint64_t mlp_flops_per_query;   /* trunk + every head row */
     /* one leaf-net pass over all network rows: FLOP the head-width-trimmed GEMMs
      * execute, and the algorithmic FLOP (trunk + the traverser's configs' head rows) */

@@ -167,7 +167,7 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
     for (int p = 0; p < 2; p++) {
         CfrBytes cb = cfr_bytes_per_iter(h, p);
         s->cfr_bytes_per_iter[p] = cb.total();
-        for (int k = 0; k < 3; k++) s->cfr_bytes_by_kernel[p][k] = cb.part[k];
+        for (int k = 0; k < 4; k++) s->cfr_bytes_by_kernel[p][k] = cb.part[k];
     }
     const NetShape& ns = h.net;
     if (ns.kind == MODEL_TWO_TOWER) {

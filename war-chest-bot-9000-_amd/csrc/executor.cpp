@@ -447,8 +447,6 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     for (int p = 0; p < 2; p++) {
         top_back_dev_[p] = (const BackRec*)(T + o.tb[p]);
         top_reach_dev_[p] = (const ReachRec*)(T + o.tr[p]);
-        d.top_acc[p] = d.acc_rec[p] + w.top_dec0[p];
-        d.ntop_dec[p] = (uint32_t)w.decision[p].size() - w.top_dec0[p];
     }
     d.nunits = (uint32_t)w.units.size();
     d.max_vwin = w.max_vwin;
@@ -624,7 +622,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     // Both players' reach under a fixed strategy: tops first, then their subtrees.
     auto reach_both = [&](float* reach, const float* strat) {
         top_reach(-1, reach, strat);
-        launch_reach(d, 0, nsub, reach, strat, -1, false, 1.0f, s);
+        launch_reach(d, 0, nsub, reach, strat, -1, s);
     };
 
     if (tower) run_tower_private(bank);  // F for this wave's configs under this bank
@@ -648,9 +646,9 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         top_back(p, MODE_REGRET, da, db, m.cfr.predict);
         top_reach(p, d.reach, d.cur);
         mark(C_TOP);
-        launch_reach(d, 0, nsub, d.reach, d.cur, p, true, ds, s);
+        launch_reach(d, 0, nsub, d.reach, d.cur, p, s);
         mark(C_REACH);
-        launch_pool(d, p, precision_, Xq_[0], Xq_[1], s);
+        launch_pool(d, p, precision_, Xq_[0], Xq_[1], s, p, ds);  // with p's average accumulation
         mark(C_LEAF);
         const uint32_t done = t + 1;
         auto it = std::find(m.snap_iters.begin(), m.snap_iters.end(), done);

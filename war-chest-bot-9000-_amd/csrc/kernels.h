@@ -48,7 +48,6 @@ struct WaveDev {
     const uint32_t* child_vb[2];
     const uint32_t *back_lvl[2], *reach_lvl[2];
     const uint32_t* unit_term;
-    const AccRec* top_acc[2];
     // mutable arena
     float *regret, *cur, *sum, *snap;
     float *reach, *snap_reach, *vals;
@@ -57,7 +56,7 @@ struct WaveDev {
     // sizes
     uint32_t ntrees, nunits, nsub, rows, pool, in, row_bytes, snapshot_configs, nexit, ncells;
     uint32_t max_vwin;  // widest unit value window (floats)
-    uint32_t ndec[2], ntop_dec[2];
+    uint32_t ndec[2];
     uint32_t npool[2];  // pool groups of each player
     uint32_t nleaf[2];  // network-leaf slots of each player (leaf_rec entries)
     const TowerBlock* tower_blk[2];  // two-tower readout blocks and tiles of each player
@@ -73,17 +72,22 @@ void launch_init_strategy(const WaveDev& w, hipStream_t s);
 // (root_index < 0) or its carried root `root_index`.
 void launch_seed_reach(const WaveDev& w, float* reach, size_t reach_len, int root_index, hipStream_t s);
 // Top-down reach of subtree units [unit0, unit0 + n) under `strat`, for one
-// player or both (player < 0); with `accumulate`, then sum = sum * ds + reach *
-// cur over the player's decision rows of each unit and of the top regions.
+// player or both (player < 0).
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
-                  bool accumulate, float ds, hipStream_t s);
+                  hipStream_t s);
 // Top-region reach at one depth (rows of player 0 and of player 1).
 void launch_reach_rows(const WaveDev& w, const ReachRec* r0, uint32_t n0, const ReachRec* r1, uint32_t n1,
                        float* reach, const float* strat, hipStream_t s);
 void launch_seed_sum(const WaveDev& w, hipStream_t s);
 // Leaf reach masses and pooled beliefs of one player (-1 = both), written into
 // the query inputs x0 (traverser 0) and x1 (traverser 1) in the operand precision.
-void launch_pool(const WaveDev& w, int player, int precision, void* x0, void* x1, hipStream_t s);
+// With acc >= 0, the same launch also takes player acc's average-strategy
+// accumulation, sum = sum * ds + reach * cur over all its decision rows (the
+// discount and this iteration's addition, search.rs:1770-1779,1818-1835), in
+// workgroups of their own: it reads only the final reach and cur, as the
+// leaf input does.
+void launch_pool(const WaveDev& w, int player, int precision, void* x0, void* x1, hipStream_t s, int acc = -1,
+                 float ds = 1.0f);
 // Seat and public features of both query inputs (once per upload).
 void launch_query_static(const WaveDev& w, int precision, void* x0, void* x1, hipStream_t s);
 // Leaf values and the bottom-up sweep of subtree units [unit0, unit0 + n) for the traverser.

@@ -167,12 +167,6 @@ __device__ __forceinline__ void accumulate_row(const WaveDev& w, AccRec q, float
     }
 }
 
-// Average-strategy accumulation over one unit's decision rows of player p.
-__device__ __forceinline__ void accumulate_unit(const WaveDev& w, const UnitDev& u, int p, float ds) {
-    for (uint32_t k = u.dec0[p] + threadIdx.x; k < u.dec1[p]; k += blockDim.x)
-        accumulate_row(w, w.acc_rec[p][k], ds);
-}
-
 // Top-down reach of one unit, level by level under block barriers: player p
 // alone, or both players (p < 0) whose task lists of a level are independent.
 __device__ __forceinline__ void reach_unit(const WaveDev& w, const UnitDev& u, float* reach, const float* strat,
@@ -221,30 +215,30 @@ __device__ __forceinline__ void reach_unit_one(const WaveDev& w, const UnitDev& 
     }
 }
 
-// Subtree units' reach; with `accumulate`, each unit then accumulates its own
-// decision rows, and the blocks past the units accumulate the top regions'
-// decision rows, one row per thread (their reach is final by then).
-__global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, uint32_t nunits, float* reach,
-                                               const float* strat, int player, int accumulate, float ds) {
-    if (blockIdx.x >= nunits) {
-        const uint32_t k = (blockIdx.x - nunits) * blockDim.x + threadIdx.x;
-        if (k < w.ntop_dec[player]) accumulate_row(w, w.top_acc[player][k], ds);
-        return;
-    }
+// Subtree units' reach, one unit per workgroup.
+__global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, float* reach, const float* strat,
+                                               int player) {
     const UnitDev u = w.units[unit0 + blockIdx.x];
     if (player < 0)
         reach_unit(w, u, reach, strat, player);
     else
         reach_unit_one(w, u, reach, strat, player);
-    if (accumulate) accumulate_unit(w, u, player, ds);
 }
 
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
-                  bool accumulate, float ds, hipStream_t s) {
-    uint32_t extra = accumulate ? grid_for(w.ntop_dec[player]) : 0;
-    if (n + extra)
-        hipLaunchKernelGGL(k_reach, dim3(n + extra), dim3(BLOCK), 0, s, w, unit0, n, reach, strat, player,
-                           accumulate ? 1 : 0, ds);
+                  hipStream_t s) {
+    if (n) hipLaunchKernelGGL(k_reach, dim3(n), dim3(BLOCK), 0, s, w, unit0, reach, strat, player);
+}
+
+// The average-strategy accumulation of player `acc` over all its decision rows
+// (units' and top regions'), one row per thread, in the workgroups of a launch
+// past its first `first` (the leaf-input kernels run it beside their own work:
+// both only read the final reach).
+__device__ __forceinline__ bool accumulate_blocks(const WaveDev& w, int acc, float ds, uint32_t first) {
+    if (acc < 0 || blockIdx.x < first) return false;
+    const uint32_t k = (blockIdx.x - first) * blockDim.x + threadIdx.x;
+    if (k < w.ndec[acc]) accumulate_row(w, w.acc_rec[acc][k], ds);
+    return true;
 }
 
 // Top-region reach at one depth, all trees together: one row per thread.
@@ -331,7 +325,9 @@ __device__ __forceinline__ uint32_t lane_value(uint32_t v, uint32_t j) {
 // the CPU's sequential sum. The pooled block goes straight into the two query
 // inputs that carry it: [pooled_q | pooled_{1-q} | seat | public] for
 // traverser q.
-__global__ __launch_bounds__(BLOCK) void k_pool_exact(WaveDev w, int player, float* x0, float* x1) {
+__global__ __launch_bounds__(BLOCK) void k_pool_exact(WaveDev w, int player, float* x0, float* x1, int acc,
+                                                    float ds, uint32_t pool_blocks) {
+    if (accumulate_blocks(w, acc, ds, pool_blocks)) return;
     const uint32_t task = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const uint32_t lane = threadIdx.x & 63;
     uint32_t row, p;
@@ -409,7 +405,9 @@ __global__ __launch_bounds__(BLOCK) void k_pool_exact(WaveDev w, int player, flo
 // Products are exact f32; only the summation order differs from the CPU's,
 // far below the 16-bit rounding of the stored query input.
 template <int PREC>
-__global__ __launch_bounds__(BLOCK) void k_pool_mfma(WaveDev w, int player, uint16_t* x0, uint16_t* x1) {
+__global__ __launch_bounds__(BLOCK) void k_pool_mfma(WaveDev w, int player, uint16_t* x0, uint16_t* x1, int acc,
+                                                   float ds, uint32_t pool_blocks) {
+    if (accumulate_blocks(w, acc, ds, pool_blocks)) return;
     uint32_t g = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const uint32_t lane = threadIdx.x & 63;
     uint32_t p = player < 0 ? 0u : (uint32_t)player;
@@ -500,23 +498,30 @@ __global__ __launch_bounds__(BLOCK) void k_pool_mfma(WaveDev w, int player, uint
     }
 }
 
-void launch_pool(const WaveDev& w, int player, int precision, void* x0, void* x1, hipStream_t s) {
+void launch_pool(const WaveDev& w, int player, int precision, void* x0, void* x1, hipStream_t s, int acc,
+                 float ds) {
+    const uint32_t accb = acc >= 0 ? grid_for(w.ndec[acc]) : 0;
     if (precision == WC_PRECISE) {
         size_t waves = (size_t)w.rows * (player < 0 ? 2 : 1);
-        if (!waves) return;
-        hipLaunchKernelGGL(k_pool_exact, dim3(grid_for(waves * 64)), dim3(BLOCK), 0, s, w, player, (float*)x0,
-                           (float*)x1);
+        const uint32_t pb = grid_for(waves * 64);
+        if (pb + accb)
+            hipLaunchKernelGGL(k_pool_exact, dim3(pb + accb), dim3(BLOCK), 0, s, w, player, (float*)x0, (float*)x1,
+                               acc, ds, pb);
         return;
     }
     size_t waves = player < 0 ? (size_t)w.npool[0] + w.npool[1] : w.npool[player];
-    if (!waves) return;
-    dim3 g(grid_for(waves * 64));
+    const uint32_t pb = grid_for(waves * 64);
+    if (!(pb + accb)) return;
+    dim3 g(pb + accb);
     if (precision == WC_F16)
-        hipLaunchKernelGGL(k_pool_mfma<WC_F16>, g, dim3(BLOCK), 0, s, w, player, (uint16_t*)x0, (uint16_t*)x1);
+        hipLaunchKernelGGL(k_pool_mfma<WC_F16>, g, dim3(BLOCK), 0, s, w, player, (uint16_t*)x0, (uint16_t*)x1, acc,
+                           ds, pb);
     else if (precision == WC_BF16)
-        hipLaunchKernelGGL(k_pool_mfma<WC_BF16>, g, dim3(BLOCK), 0, s, w, player, (uint16_t*)x0, (uint16_t*)x1);
+        hipLaunchKernelGGL(k_pool_mfma<WC_BF16>, g, dim3(BLOCK), 0, s, w, player, (uint16_t*)x0, (uint16_t*)x1, acc,
+                           ds, pb);
     else
-        hipLaunchKernelGGL(k_pool_mfma<WC_F16X>, g, dim3(BLOCK), 0, s, w, player, (uint16_t*)x0, (uint16_t*)x1);
+        hipLaunchKernelGGL(k_pool_mfma<WC_F16X>, g, dim3(BLOCK), 0, s, w, player, (uint16_t*)x0, (uint16_t*)x1, acc,
+                           ds, pb);
 }
 
 // The fixed part of both traversers' query inputs: the seat (-1 for player 0,

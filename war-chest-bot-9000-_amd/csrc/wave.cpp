@@ -1103,19 +1103,20 @@ std::vector<ChainPass> plan_chain(const uint32_t* cols, uint32_t nrb, uint32_t h
 // regret/DCFR update, reach gather, average accumulation) for traverser p:
 //   44 C_p  legal cells of p: successor index 4, child value 4, cur read 4 +
 //           write 4, regret read+write 8, sum read+write 8 (value sweep: 32);
-//           accumulate: cur 4 + sum read+write 8 (reach sweep: 12)
+//           accumulate: cur 4 + sum read+write 8 (accumulation: 12)
 //   16 G_p  gather entries into p's reach: source 4, cell or probability 4,
 //           parent reach 4, strategy 4
 //    4 S_p  p's reach slots written
 //   12 R_p  p's decision rows: row offsets 8 (value sweep), reach read by the
-//           accumulation 4 (reach sweep)
+//           accumulation 4 (accumulation)
 //    4 O_p  child-value reads at opponent decision nodes
 //   12 H_p  draw entries at p's chance nodes: successor 4, probability 4, value 4
 //    8 L_p  leaf value slots of p: net output read 4, value write 4
 //    4 L_o  opponent reach read for the leaf reach mass
 // A node's value-sweep bytes go to the kernel that sweeps its unit's values
 // (subtree sweep or top sweep), its reach bytes to the kernel that gathers its
-// reach (subtree reach or top sweep).
+// reach (subtree reach or top sweep), its accumulation bytes to the leaf-input
+// launch that runs every accumulation.
 CfrBytes cfr_bytes_per_iter(const WaveHost& w, int p) {
     CfrBytes out;
     const uint32_t N = w.nodes();
@@ -1129,7 +1130,7 @@ CfrBytes cfr_bytes_per_iter(const WaveHost& w, int p) {
             uint32_t r0 = w.legal_row_of[i];
             uint64_t C = w.legal_off[r0 + ncp] - w.legal_off[r0];
             back += 32 * C + 8 * uint64_t(ncp);
-            out.part[2] += 12 * C + 4 * uint64_t(ncp);  // every accumulation runs in the subtree reach launch
+            out.part[3] += 12 * C + 4 * uint64_t(ncp);  // every accumulation runs in the leaf-input launch
         } else if (kind == 0) {
             back += 4 * uint64_t(ncp) * (w.child_start[i + 1] - w.child_start[i]);
         } else if (kind == 1 && actor == (uint32_t)p) {

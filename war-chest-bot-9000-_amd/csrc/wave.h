@@ -242,12 +242,13 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* w, std::string* err, uint32_t 
 bool validate_deep(const WaveHost& w, std::string* err);
 
 // Algorithmic HBM bytes of one CFR iteration for traverser p (the counting
-// rule is written next to the implementation), split by the kernel that moves
+// rule is written next to the implementation), split by the launch that moves
 // them: [0] the subtree value sweep, [1] the top-region launches, [2] the
-// subtree reach and accumulation.
+// subtree reach, [3] the average-strategy accumulation (run in the leaf-input
+// launch).
 struct CfrBytes {
-    uint64_t part[3] = {0, 0, 0};
-    uint64_t total() const { return part[0] + part[1] + part[2]; }
+    uint64_t part[4] = {0, 0, 0, 0};
+    uint64_t total() const { return part[0] + part[1] + part[2] + part[3]; }
 };
 CfrBytes cfr_bytes_per_iter(const WaveHost& w, int p);
 

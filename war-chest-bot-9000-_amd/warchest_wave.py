@@ -84,7 +84,7 @@ class WaveStats(C.Structure):
         "levels", "iters", "nroots_max", "carry_slots", "units", "top_levels", "max_window")] + [(n, C.c_uint64) for n in (
         "cells", "reach_slots", "reach_len", "vals_len", "rev_nnz", "rvd_nnz", "draw_nnz",
         "snapshot_configs", "table_bytes", "arena_bytes")] + [
-        ("cfr_bytes_per_iter", C.c_uint64 * 2), ("cfr_bytes_by_kernel", (C.c_uint64 * 3) * 2),
+        ("cfr_bytes_per_iter", C.c_uint64 * 2), ("cfr_bytes_by_kernel", (C.c_uint64 * 4) * 2),
         ("mlp_flops_per_query", C.c_uint64), ("mlp_flops_executed", C.c_uint64),
         ("mlp_flops_algorithmic", C.c_uint64)]
 
