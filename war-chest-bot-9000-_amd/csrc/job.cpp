@@ -91,14 +91,25 @@ struct W {
         u32((uint32_t)v.size());
         b.insert(b.end(), v.begin(), v.end());
     }
-    void u32s(const std::vector<uint32_t>& v) {
+    // Arrays of 32-bit words, little-endian: one block copy on a little-endian
+    // host, word by word elsewhere.
+    template <class T>
+    void words(const std::vector<T>& v) {
+        static_assert(sizeof(T) == 4, "32-bit words");
         u32((uint32_t)v.size());
-        for (uint32_t x : v) u32(x);
+#if defined(__BYTE_ORDER__) && __BYTE_ORDER__ == __ORDER_LITTLE_ENDIAN__
+        const uint8_t* p = (const uint8_t*)v.data();
+        b.insert(b.end(), p, p + v.size() * 4);
+#else
+        for (const T& x : v) {
+            uint32_t u;
+            std::memcpy(&u, &x, 4);
+            u32(u);
+        }
+#endif
     }
-    void f32s(const std::vector<float>& v) {
-        u32((uint32_t)v.size());
-        for (float x : v) f32(x);
-    }
+    void u32s(const std::vector<uint32_t>& v) { words(v); }
+    void f32s(const std::vector<float>& v) { words(v); }
 };
 
 struct R {
@@ -138,18 +149,26 @@ struct R {
         v.assign(b + at, b + at + k);
         at += k;
     }
-    void u32s(std::vector<uint32_t>& v, const char* what) {
+    // Arrays of little-endian 32-bit words: one block copy on a little-endian
+    // host, word by word elsewhere.
+    template <class T>
+    void words(std::vector<T>& v, const char* what) {
+        static_assert(sizeof(T) == 4, "32-bit words");
         uint32_t k = u32(what);
         if (!take(size_t(k) * 4, what)) return;
         v.resize(k);
-        for (uint32_t i = 0; i < k; i++) v[i] = u32(what);
+#if defined(__BYTE_ORDER__) && __BYTE_ORDER__ == __ORDER_LITTLE_ENDIAN__
+        if (k) std::memcpy(v.data(), b + at, size_t(k) * 4);
+        at += size_t(k) * 4;
+#else
+        for (uint32_t i = 0; i < k; i++) {
+            uint32_t u = u32(what);
+            std::memcpy(&v[i], &u, 4);
+        }
+#endif
     }
-    void f32s(std::vector<float>& v, const char* what) {
-        uint32_t k = u32(what);
-        if (!take(size_t(k) * 4, what)) return;
-        v.resize(k);
-        for (uint32_t i = 0; i < k; i++) v[i] = f32(what);
-    }
+    void u32s(std::vector<uint32_t>& v, const char* what) { words(v, what); }
+    void f32s(std::vector<float>& v, const char* what) { words(v, what); }
 };
 
 bool check(size_t got, size_t want, const char* what, std::string* err) {

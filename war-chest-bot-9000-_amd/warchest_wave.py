@@ -185,7 +185,12 @@ def _check(rc):
         raise WaveError(lib().wc_last_error().decode(errors="replace") or f"error {rc}")
 
 
-def _bytes_ptr(b: bytes):
+def _bytes_ptr(b):
+    """A uint8 pointer to the bytes of `b` and the object that keeps them alive.
+    An immutable `bytes` is passed in place (the library copies what it keeps
+    during the call); other buffers are copied first."""
+    if isinstance(b, bytes):
+        return b, C.cast(C.c_char_p(b), _u8p)
     buf = (C.c_uint8 * len(b)).from_buffer_copy(b)
     return buf, C.cast(buf, _u8p)
 
@@ -330,8 +335,8 @@ class Wave:
 
     def __init__(self, jobs: Sequence[bytes]):
         L = lib()
-        self._bufs = [(C.c_uint8 * len(j)).from_buffer_copy(j) for j in jobs]
-        ptrs = (_u8p * len(jobs))(*[C.cast(b, _u8p) for b in self._bufs])
+        held = [_bytes_ptr(j) for j in jobs]  # the library parses the jobs during the call
+        ptrs = (_u8p * len(jobs))(*[p for _, p in held])
         lens = (C.c_size_t * len(jobs))(*[len(j) for j in jobs])
         h = C.c_void_p()
         _check(L.wc_wave_pack(ptrs, lens, len(jobs), C.byref(h)))
