@@ -1346,12 +1346,13 @@ void launch_tower_head(const WaveDev& w, int player, int precision, const void* 
 
 // ------------------------------------------------------- fused leaf network
 //
-// One launch runs the whole MLP over a 128-row tile per workgroup: the tile's
-// input operand is staged into LDS once, every trunk layer reads its input
-// from LDS and writes its bias + ReLU output back over it (fragment-major,
-// 16-bit: the next layer's operand), and the head writes row-major f32. Only
-// the tile's input, the weights (shared by every tile, L2-resident) and the
-// head outputs touch HBM.
+// One launch runs the whole MLP, one pass of up to eight 16-row blocks per
+// workgroup (the passes come from plan_chain): the pass's input operand is
+// staged into LDS once, every trunk layer reads its input from LDS and writes
+// its bias + ReLU output back over it (fragment-major, 16-bit: the next
+// layer's operand), and the head writes row-major f32. Only the pass's input,
+// the weights (shared by every pass, L2-resident) and the head outputs touch
+// HBM.
 //
 // Products are computed transposed, D = W X^T: the weight fragment is the
 // MFMA's A operand and the activation fragment its B operand, so lane l holds
