@@ -317,6 +317,63 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     for (const Job& job : jobs)
         for (uint32_t i = 0; i < job.t.nodes; i++)
             unit_slots = std::max(unit_slots, std::max(job.t.nc(i, 0), job.t.nc(i, 1)));
+    {  // every list's final size (or a bound on it) first: the loop below appends without regrowing
+        size_t nodes = 0, kids = 0, cells = 0, lrows = 0, draws = 0, drows = 0, revs = 0, rrows = 0, rvds = 0,
+               vrows = 0, rows = 0, members = 0, cfgs = 0, pub = 0, terms = 0, slots[2] = {0, 0};
+        for (const Job& j : jobs) {
+            const Tables& t = j.t;
+            nodes += t.nodes;
+            kids += t.node_child.size();
+            cells += t.ncells;
+            lrows += t.legal_off.size();
+            draws += t.draw_to.size();
+            drows += t.draw_row_start.size();
+            revs += t.rev_src.size();
+            rrows += t.rev_start.size();
+            rvds += t.rvd_src.size();
+            vrows += t.rvd_start.size();
+            rows += t.rows;
+            members += t.leaf_cidx.size();
+            cfgs += t.ncfg;
+            pub += t.leaf_raw.size();
+            terms += t.term_leaves.size();
+            for (uint32_t i = 0; i < t.nodes; i++)
+                for (int p = 0; p < 2; p++) slots[p] += t.nc(i, p);
+        }
+        for (auto* v : {&w.node_meta, &w.child_start, &w.legal_row_of, &w.draw_off, &w.draw_row_off, &w.parent,
+                        &w.rev_row_of, &w.rvd_row_of})
+            v->reserve(nodes + 1);
+        w.node_nc.reserve(2 * nodes);
+        w.reach_base.reserve(2 * nodes);
+        w.vals_base.reserve(2 * nodes);
+        w.child.reserve(kids);
+        w.legal_off.reserve(lrows + 1);
+        w.legal_value.reserve(cells);
+        w.draw_to.reserve(draws);
+        w.draw_p.reserve(draws);
+        w.draw_row_start.reserve(drows);
+        w.rev_src.reserve(revs);
+        w.rev_cell.reserve(revs);
+        w.rev_start.reserve(rrows + 1);
+        w.rvd_src.reserve(rvds);
+        w.rvd_p.reserve(rvds);
+        w.rvd_start.reserve(vrows + 1);
+        w.row_node.reserve(rows);
+        w.row_cfg_off.reserve(2 * rows + 1);
+        w.row_cfg.reserve(members);
+        w.cfg_key.reserve(cfgs);
+        w.cfg_emb.reserve(cfgs * w.net.pool);
+        w.pub_raw.reserve(pub);
+        w.term_node.reserve(terms);
+        w.term_util.reserve(terms);
+        w.exit_node.reserve(rows + terms);
+        w.exit_coff.reserve(2 * (rows + terms) + 1);
+        for (int p = 0; p < 2; p++) {  // every (node, config) of p is at most one task of each kind
+            w.back_task[p].reserve(slots[p]);
+            w.reach_task[p].reserve(slots[p]);
+            w.decision[p].reserve(slots[p]);
+        }
+    }
     uint32_t cfg_total = 0;
     std::vector<UnitDev> sub_units;
     std::vector<std::vector<Task>> top_back[2], top_reach[2];
