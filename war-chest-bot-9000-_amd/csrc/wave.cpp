@@ -1102,16 +1102,27 @@ std::vector<ChainPass> plan_chain(const uint32_t* cols, uint32_t nrb, uint32_t h
         total += c[i];
         cmax = std::max(cmax, c[i]);
     }
+    // A pass also closes before its cost would exceed that of a full pass of
+    // narrow (64-column) blocks, so passes of wide-head blocks hold fewer rows
+    // and the longest passes, which start first, stay short.
+    const double cap = (pass_cost + CHAIN_PASS_BLOCKS * (1.0 + col_cost * 4)) * (1.0 + 1e-9);
+    auto closes = [&](uint32_t pn, double pc, uint32_t i) {
+        return pn == CHAIN_PASS_BLOCKS || (pn > 0 && pass_cost + pc + c[i] > cap);
+    };
     // Shares of consecutive blocks under a cost bound t; returns their ends.
     auto deal = [&](double t, std::vector<uint32_t>* ends) {
         uint32_t shares = 0, i = 0;
         while (i < nrb) {
-            uint32_t n = 0;
-            double sum = 0.0;
+            double sum = 0.0, pc = 0.0;
+            uint32_t n = 0, pn = 0;
             while (i < nrb) {
-                const double with = pass_cost * ((n + CHAIN_PASS_BLOCKS) / CHAIN_PASS_BLOCKS) + sum + c[i];
+                const bool fresh = pn == 0 || closes(pn, pc, i);
+                const double with = sum + (fresh ? pass_cost : 0.0) + c[i];
                 if (n > 0 && with > t) break;
-                sum += c[i];
+                if (fresh) pn = 0, pc = 0.0;
+                sum = with;
+                pc += c[i];
+                pn++;
                 n++;
                 i++;
             }
@@ -1120,7 +1131,7 @@ std::vector<ChainPass> plan_chain(const uint32_t* cols, uint32_t nrb, uint32_t h
         }
         return shares;
     };
-    double lo = pass_cost + cmax, hi = pass_cost * ((nrb + CHAIN_PASS_BLOCKS - 1) / CHAIN_PASS_BLOCKS) + total;
+    double lo = pass_cost + cmax, hi = pass_cost * nrb + total;
     for (int it = 0; it < 48 && hi - lo > 1e-6 * hi; it++) {  // the least bound that fits the CUs
         const double mid = 0.5 * (lo + hi);
         if (deal(mid, nullptr) <= cus)
@@ -1130,23 +1141,20 @@ std::vector<ChainPass> plan_chain(const uint32_t* cols, uint32_t nrb, uint32_t h
     }
     std::vector<uint32_t> ends;
     deal(hi, &ends);
-    std::vector<uint32_t> starts(ends.size());
-    for (size_t k = 0; k < ends.size(); k++) starts[k] = k ? ends[k - 1] : 0;
-    for (uint32_t round = 0;; round++) {
-        bool any = false;
-        for (size_t k = 0; k < ends.size(); k++) {
-            const uint32_t b = starts[k] + round * CHAIN_PASS_BLOCKS;
-            if (b >= ends[k]) continue;
-            any = true;
-            ChainPass ps{};
-            ps.n = std::min(CHAIN_PASS_BLOCKS, ends[k] - b);
-            for (uint32_t j = 0; j < ps.n; j++) {
-                ps.rb[j] = order[b + j];
-                ps.cols = std::max(ps.cols, width(order[b + j]));
+    for (size_t k = 0; k < ends.size(); k++) {  // each share cut into passes by the same rule
+        ChainPass ps{};
+        double pc = 0.0;
+        for (uint32_t i = k ? ends[k - 1] : 0; i < ends[k]; i++) {
+            if (closes(ps.n, pc, i)) {
+                out.push_back(ps);
+                ps = ChainPass{};
+                pc = 0.0;
             }
-            out.push_back(ps);
+            ps.rb[ps.n++] = order[i];
+            ps.cols = std::max(ps.cols, width(order[i]));
+            pc += c[i];
         }
-        if (!any) break;
+        if (ps.n) out.push_back(ps);
     }
     // Longest first: CUs that take the next pass as they free up then end
     // close together (the shares set the pass sizes).

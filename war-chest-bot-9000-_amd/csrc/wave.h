@@ -133,7 +133,8 @@ static_assert(sizeof(ChainPass) == 12 * 4, "ChainPass is 48 bytes");
 // head first; consecutive blocks of that order are dealt to at most `cus`
 // shares of about equal estimated cost (a per-pass overhead, a per-block
 // trunk cost and a per-block head cost that grows with the width), each share
-// is cut into passes of up to CHAIN_PASS_BLOCKS blocks, and the passes are
+// is cut into passes of up to CHAIN_PASS_BLOCKS blocks and at most the cost of
+// a full pass of 64-column blocks (wide-head passes hold fewer), and the passes are
 // listed by estimated cost, longest first: run in list order on CUs that take
 // the next pass as they free up (longest-processing-time-first list
 // scheduling), the last passes end at about the same time. Every block is in
