@@ -1092,9 +1092,13 @@ std::vector<ChainPass> plan_chain(const uint32_t* cols, uint32_t nrb, uint32_t h
     for (uint32_t i = 0; i < nrb; i++) order[i] = i;
     std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return width(a) > width(b); });
     // Cost in units of one 16-row block's trunk: a pass costs about three of
-    // them on top of its blocks, and each 16 head columns of a block about 0.024
-    // (measured on the 512 -> 3 x 384 net).
-    const double pass_cost = 3.0, col_cost = 0.024;
+    // them on top of its blocks (measured on the 512 -> 3 x 384 net). Each 16
+    // head columns of a block are weighted 0.07, about three times their
+    // measured share of a pass (0.024): the extra weight keeps the passes of
+    // wide-head blocks, which finish last otherwise, short. Value net time per
+    // wave of 256 subgames with 567 heads, by weight: 0.016 5.44 ms, 0.024
+    // 5.20 ms, 0.07 4.90 ms, 0.15 5.25 ms.
+    const double pass_cost = 3.0, col_cost = 0.07;
     std::vector<double> c(nrb);
     double total = 0.0, cmax = 0.0;
     for (uint32_t i = 0; i < nrb; i++) {
