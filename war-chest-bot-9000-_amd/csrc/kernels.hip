@@ -735,26 +735,29 @@ __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, cons
     extern __shared__ float lds_vals[];  // the unit's value window of player p (when LDSV)
     const UnitDev u = w.units[unit0 + blockIdx.x];
     const int opp = 1 - p;
-    const uint32_t vw = u.vwin[p];
+    // The player's fields by select, not by index: indexing the record's
+    // arrays with the run-time p would place the record in scratch memory.
+    const uint32_t vw = p ? u.vwin[1] : u.vwin[0];
+    const uint32_t leaf0 = p ? u.leaf0[1] : u.leaf0[0], leaf1 = p ? u.leaf1[1] : u.leaf1[0];
     // Network leaves: one value slot per thread, LEAF_BATCH slots per thread
     // in flight (their records, then the values they name).
-    for (uint32_t k0 = u.leaf0[p]; k0 < u.leaf1[p]; k0 += LEAF_BATCH * BLOCK) {
+    for (uint32_t k0 = leaf0; k0 < leaf1; k0 += LEAF_BATCH * BLOCK) {
         LeafRec q[LEAF_BATCH];
         float h[LEAF_BATCH], m[LEAF_BATCH];
 #pragma unroll
         for (uint32_t j = 0; j < LEAF_BATCH; j++) {
             const uint32_t k = k0 + j * BLOCK + threadIdx.x;
-            if (k < u.leaf1[p]) q[j] = w.leaf_rec[p][k];
+            if (k < leaf1) q[j] = w.leaf_rec[p][k];
         }
 #pragma unroll
         for (uint32_t j = 0; j < LEAF_BATCH; j++)
-            if (k0 + j * BLOCK + threadIdx.x < u.leaf1[p]) {
+            if (k0 + j * BLOCK + threadIdx.x < leaf1) {
                 h[j] = head_out[q[j].head];
                 m[j] = w.mass[q[j].mass];
             }
 #pragma unroll
         for (uint32_t j = 0; j < LEAF_BATCH; j++)
-            if (k0 + j * BLOCK + threadIdx.x < u.leaf1[p]) {
+            if (k0 + j * BLOCK + threadIdx.x < leaf1) {
                 const float v = h[j] * m[j];
                 if (!LDSV || q[j].exported) w.vals[q[j].out] = v;
                 if (LDSV) lds_vals[q[j].out - vw] = v;
