@@ -148,6 +148,16 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* out);
  * lives as long as the wave. */
 const uint32_t* wc_wave_array(const wc_wave* w, const char* name, size_t* n);
 
+/* The fused value net's pass plan, for tests and tooling (no counterpart in
+ * the reference, whose head GEMMs take fixed tiles: device.rs:1218-1305): for
+ * nrb 16-row blocks whose head widths are cols[rb] (cols NULL: every block
+ * needs `heads`) on a device of `cus` compute units, the passes in launch
+ * order as rows of 10 uint32: block count n, head columns, then the n block
+ * indices (the rest 0). Writes at most cap rows to out; *npass receives the
+ * number of passes. */
+int wc_value_net_plan(const uint32_t* cols, uint32_t nrb, uint32_t heads, uint32_t cus, uint32_t* out, size_t cap,
+                      size_t* npass);
+
 /* Executor::launch + collect (+ Harvest::unpack): runs the whole schedule,
  * blocks, and returns one result per job in submission order
  * (results[k] owned by the caller). */

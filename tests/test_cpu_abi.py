@@ -119,3 +119,40 @@ def test_weights_and_features_are_seeded():
     # Kaiming-normal: first-layer std ~ sqrt(2 / 512)
     w1 = n1.w[: 512 * 384]
     assert abs(w1.std() - np.sqrt(2 / 512)) < 0.003
+
+
+def test_value_net_plan_covers_every_block_once():
+    # 65,536 queries with 64 heads on 256 CUs: 4,096 blocks of one width, so
+    # every pass is a full eight-block pass, two per CU.
+    plan = ww.value_net_plan(4096, 256, heads=64)
+    assert len(plan) == 512
+    assert all(c == 64 and len(b) == 8 for c, b in plan)
+    assert sorted(x for _, b in plan for x in b) == list(range(4096))
+
+
+def test_value_net_plan_keeps_wide_passes_short():
+    # A wave's spread of head widths: most blocks need a few 16-column steps,
+    # some all 567 columns. Widest blocks come first, each pass's width covers
+    # its blocks, and passes of 567-column blocks hold fewer blocks than
+    # passes of 64-column blocks (their estimated cost is capped).
+    rng = np.random.default_rng(5)
+    cols = rng.choice([16, 32, 64, 128, 256, 567], size=3086, p=[0.3, 0.25, 0.2, 0.12, 0.08, 0.05])
+    cols = cols.astype(np.uint32)
+    plan = ww.value_net_plan(cols, 256, heads=567)
+    seen = sorted(x for _, b in plan for x in b)
+    assert seen == list(range(len(cols)))
+    for c, b in plan:
+        assert 1 <= len(b) <= 8
+        assert c == max(int(cols[x]) for x in b)
+    wide = [len(b) for c, b in plan if c == 567]
+    narrow = [len(b) for c, b in plan if c == 64]
+    assert wide and narrow and max(wide) < max(narrow) == 8
+    assert plan[0][0] == 567  # the longest passes start first
+    assert len(plan) >= 256  # at least one pass per CU
+
+
+def test_value_net_plan_rejects_null_output():
+    n = ww.C.c_size_t(7)
+    assert ww.lib().wc_value_net_plan(None, 4, 64, 256, None, 4, ww.C.byref(n)) == -1  # WC_ERR_INVALID
+    assert n.value == 0
+    assert ww.lib().wc_value_net_plan(None, 4, 64, 256, None, 0, None) == -1  # WC_ERR_INVALID

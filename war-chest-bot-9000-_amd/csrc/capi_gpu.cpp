@@ -224,6 +224,28 @@ const uint32_t* wc_wave_array(const wc_wave* w, const char* name, size_t* n) {
     return v->data();
 }
 
+static_assert(CHAIN_PASS_BLOCKS == 8, "wc_value_net_plan rows are 2 + 8 words");
+int wc_value_net_plan(const uint32_t* cols, uint32_t nrb, uint32_t heads, uint32_t cus, uint32_t* out, size_t cap,
+                      size_t* npass) {
+    if (npass) *npass = 0;
+    if (!npass || (cap && !out)) return fail(WC_ERR_INVALID, "wc_value_net_plan: null argument");
+    try {
+        const std::vector<ChainPass> plan = plan_chain(cols, nrb, heads, cus);
+        std::string err;
+        if (!check_chain_plan(plan, cols, nrb, heads, &err)) return fail(WC_ERR_INVALID, err);
+        *npass = plan.size();
+        for (size_t i = 0; i < plan.size() && i < cap; i++) {
+            uint32_t* row = out + i * (2 + CHAIN_PASS_BLOCKS);
+            row[0] = plan[i].n;
+            row[1] = plan[i].cols;
+            for (uint32_t j = 0; j < CHAIN_PASS_BLOCKS; j++) row[2 + j] = j < plan[i].n ? plan[i].rb[j] : 0;
+        }
+        return WC_OK;
+    } catch (const std::exception& e) {
+        return fail(WC_ERR_INVALID, e.what());
+    }
+}
+
 int wc_solve_wave(wc_executor* ex, wc_wave* w, uint64_t version, wc_result** results) {
     if (!ex || !w || !results) return fail(WC_ERR_INVALID, "wc_solve_wave: null argument");
     std::vector<Result> out;

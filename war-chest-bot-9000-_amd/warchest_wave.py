@@ -109,7 +109,8 @@ EXPORTS = [
     "wc_result_tag", "wc_result_weight_version", "wc_result_strategy", "wc_result_root_values",
     "wc_result_carries", "wc_result_free",
     "wc_executor_create", "wc_executor_destroy", "wc_executor_publish",
-    "wc_wave_pack", "wc_wave_free", "wc_wave_stats_get", "wc_wave_array", "wc_solve_wave", "wc_time_wave",
+    "wc_wave_pack", "wc_wave_free", "wc_wave_stats_get", "wc_wave_array", "wc_value_net_plan", "wc_solve_wave",
+    "wc_time_wave",
     "wc_mlp_forward", "wc_time_mlp",
     "wc_job_roundtrip", "wc_job_validate",
     "wc_synth_spec_default", "wc_synth", "wc_jobset_count", "wc_jobset_job", "wc_jobset_free",
@@ -159,6 +160,8 @@ def _declare(L):
     L.wc_wave_stats_get.argtypes = [C.c_void_p, C.POINTER(WaveStats)]
     L.wc_wave_array.argtypes = [C.c_void_p, C.c_char_p, C.POINTER(C.c_size_t)]
     L.wc_wave_array.restype = _u32p
+    L.wc_value_net_plan.argtypes = [C.POINTER(C.c_uint32), C.c_uint32, C.c_uint32, C.c_uint32,
+                                    C.POINTER(C.c_uint32), C.c_size_t, C.POINTER(C.c_size_t)]
     L.wc_solve_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p)]
     L.wc_time_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32,
                                C.POINTER(C.c_double), C.POINTER(C.c_double)]
@@ -202,6 +205,25 @@ def _arr(a, dtype):
 
 
 # ------------------------------------------------------------------ networks
+
+def value_net_plan(cols, cus, heads=None):
+    """The fused value net's passes (wc_value_net_plan) for 16-row blocks of
+    head widths `cols` (or, with cols an int, that many blocks of width
+    `heads`) on `cus` compute units: a list of (head columns, [blocks]) in
+    launch order."""
+    if isinstance(cols, int):
+        nrb, cp = cols, None
+    else:
+        a = np.ascontiguousarray(cols, dtype=np.uint32)
+        nrb, cp = len(a), a.ctypes.data_as(C.POINTER(C.c_uint32))
+        heads = int(a.max()) if heads is None and nrb else (heads or 0)
+    n = C.c_size_t(0)
+    _check(lib().wc_value_net_plan(cp, nrb, heads, cus, None, 0, C.byref(n)))
+    out = np.zeros((max(n.value, 1), 10), dtype=np.uint32)
+    _check(lib().wc_value_net_plan(cp, nrb, heads, cus, out.ctypes.data_as(C.POINTER(C.c_uint32)), n.value,
+                                   C.byref(n)))
+    return [(int(r[1]), [int(b) for b in r[2:2 + r[0]]]) for r in out[:n.value]]
+
 
 def mlp_dims(inputs=512, hidden=384, layers=3, heads=22, pool=64):
     return [MODEL_MLP, inputs, hidden, layers, heads, pool]
