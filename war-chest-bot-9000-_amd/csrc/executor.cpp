@@ -386,6 +386,11 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     size_t m_x = mtake(prow * ns.in * esz), m_x1 = mtake(prow * ns.in * esz), m_h0 = mtake(prow * ns.hidden * esz),
            m_h1 = mtake(prow * ns.hidden * esz),
            m_out = mtake(tower ? w.tower_len * 4 : rows * ns.heads * 4);
+    // The fused net's first-layer product over the fixed query columns, when
+    // the pooled columns are whole 32-column k steps ahead of them.
+    const bool split = !tower && (precision_ == WC_F16 || precision_ == WC_BF16) &&
+                       chain_fits(ns.in, ns.hidden, ns.layers) && ns.in > 2 * ns.pool && (2 * ns.pool) % 32 == 0;
+    size_t m_s0 = split ? mtake(prow * ns.hidden * 4) : 0, m_s1 = split ? mtake(prow * ns.hidden * 4) : 0;
     size_t m_px = 0, m_p0 = 0, m_p1 = 0, m_f = 0;
     if (tower) {
         m_px = mtake(precision_ == WC_PRECISE ? 0 : pcfg * ns.priv_in * esz);
@@ -475,6 +480,8 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     Xq_[1] = M + m_x1;
     H_[0] = M + m_h0;
     H_[1] = M + m_h1;
+    S_[0] = split ? (float*)(M + m_s0) : nullptr;
+    S_[1] = split ? (float*)(M + m_s1) : nullptr;
     head_out_ = (float*)(M + m_out);
     cfg_priv_ = (const float*)(T + o.cfg_priv);
     PX_ = tower ? M + m_px : nullptr;
@@ -489,8 +496,25 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     return true;
 }
 
+// The fused kernel's view of a 16-bit MLP bank.
+static ChainNet chain_net(const NetBank& bank) {
+    const NetShape& ns = bank.ns;
+    ChainNet net{};
+    for (uint32_t l = 0; l < ns.layers; l++) {
+        net.w[l] = (const uint16_t*)bank.W[l];
+        net.b[l] = bank.B[l];
+    }
+    net.w[ns.layers] = (const uint16_t*)bank.Whead;
+    net.b[ns.layers] = bank.bhead;
+    net.in = ns.in;
+    net.hidden = ns.hidden;
+    net.layers = ns.layers;
+    net.heads = ns.heads;
+    return net;
+}
+
 void Executor::run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::vector<hipEvent_t>* marks,
-                       const uint32_t* head_tile_n, const ChainPass* plan, uint32_t npass) {
+                       const uint32_t* head_tile_n, const ChainPass* plan, uint32_t npass, const float* part) {
     const NetShape& ns = bank.ns;
     auto mark = [&]() {
         if (marks) {
@@ -501,17 +525,11 @@ void Executor::run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::v
         }
     };
     if ((precision_ == WC_F16 || precision_ == WC_BF16) && chain_fits(ns.in, ns.hidden, ns.layers)) {
-        ChainNet net{};
-        for (uint32_t l = 0; l < ns.layers; l++) {
-            net.w[l] = (const uint16_t*)bank.W[l];
-            net.b[l] = bank.B[l];
+        ChainNet net = chain_net(bank);
+        if (part) {
+            net.part = part;
+            net.dsteps = 2 * ns.pool / 32;
         }
-        net.w[ns.layers] = (const uint16_t*)bank.Whead;
-        net.b[ns.layers] = bank.bhead;
-        net.in = ns.in;
-        net.hidden = ns.hidden;
-        net.layers = ns.layers;
-        net.heads = ns.heads;
         launch_chain(precision_, net, x, rows, head_out_, plan, npass, stream_);
         mark();
         return;
@@ -602,7 +620,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         if (tower)
             run_tower(bank, d.rows, q);
         else
-            run_mlp(bank, d.rows, Xq_[q], nullptr, head_tile_n_, chain_plan_[q], chain_npass_[q]);
+            run_mlp(bank, d.rows, Xq_[q], nullptr, head_tile_n_, chain_plan_[q], chain_npass_[q], S_[q]);
         mark(C_MLP);
     };
     // Top regions, one depth per launch: values bottom-up, reach top-down.
@@ -626,6 +644,13 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     };
 
     if (tower) run_tower_private(bank);  // F for this wave's configs under this bank
+    if (S_[0]) {  // the first layer over the fixed query columns, under this bank
+        ChainNet net = chain_net(bank);
+        net.dsteps = 2 * bank.ns.pool / 32;  // the pooled columns come first; the rest are fixed
+        for (int q = 0; q < 2; q++)
+            launch_chain_static(precision_, net, Xq_[q], S_[q], chain_plan_[q], chain_npass_[q], s);
+        mark(C_MLP);
+    }
     launch_zero(d.regret, w.ncells, s);
     launch_init_strategy(d, s);
     launch_seed_reach(d, d.reach, w.reach_len, -1, s);
@@ -812,6 +837,7 @@ bool Executor::mlp_forward(uint64_t version, uint32_t rows, const float* x, floa
     X_ = M + m_x;
     H_[0] = M + m_h0;
     H_[1] = M + m_h1;
+    S_[0] = S_[1] = nullptr;  // this layout holds no partial products
     head_out_ = (float*)(M + m_out);
     mlp_plan_ = (const ChainPass*)(M + m_plan);
     mlp_npass_ = (uint32_t)plan.size();

@@ -87,8 +87,10 @@ class Executor {
     // The MLP over `rows` query rows: the fused kernel over `plan` (npass
     // passes, device copy) where it applies, else layer by layer (head width
     // per 128-row tile: head_tile_n).
+    // part: the first layer's precomputed product over the query inputs'
+    // fixed columns (S_), or null.
     void run_mlp(const NetBank& bank, uint32_t rows, const void* x, std::vector<hipEvent_t>* marks,
-                 const uint32_t* head_tile_n, const ChainPass* plan, uint32_t npass);
+                 const uint32_t* head_tile_n, const ChainPass* plan, uint32_t npass, const float* part = nullptr);
     bool ensure(void** p, size_t* cap, size_t need, std::string* err);
     bool ensure_pinned(uint8_t** p, size_t* cap, size_t need, std::string* err);
 
@@ -122,6 +124,10 @@ class Executor {
     const ChainPass* mlp_plan_ = nullptr;    // the same for mlp_forward's rows
     uint32_t mlp_npass_ = 0;
     void* H_[2] = {};
+    // The fused value net's first-layer product over each traverser's fixed
+    // query columns (seat, public features), f32 accumulator tiles; computed
+    // at the start of each schedule (null where the fused net does not run).
+    float* S_[2] = {};
     float* head_out_ = nullptr;  // MLP head outputs, or the two-tower readout per (row, config)
     // Two-tower net: private-tower input, layer outputs and F (one row per interned config).
     const float* cfg_priv_ = nullptr;

@@ -129,10 +129,23 @@ struct ChainNet {
     const uint16_t* w[CHAIN_MAX_LAYERS + 1];
     const float* b[CHAIN_MAX_LAYERS + 1];
     uint32_t in, hidden, layers, heads;
+    // With part set, the first layer takes only its first dsteps 32-column
+    // k steps from X and starts from part, the product of the remaining
+    // columns computed beforehand by launch_chain_static (f32, one 16 x 16
+    // tile of 1 KB per (row block, feature block), in the MFMA accumulator's
+    // lane order).
+    const float* part = nullptr;
+    uint32_t dsteps = 0;
 };
 bool chain_fits(uint32_t in, uint32_t hidden, uint32_t layers);
 void launch_chain(int precision, const ChainNet& net, const void* X, uint32_t rows, float* out,
                   const ChainPass* plan, uint32_t npass, hipStream_t s);
+// The first layer's product over X's columns from k step net.dsteps on (the
+// columns that stay fixed while a wave is solved: seat and public features),
+// without bias, into part (the layout ChainNet::part describes), for every
+// row block of the plan.
+void launch_chain_static(int precision, const ChainNet& net, const void* X, float* part, const ChainPass* plan,
+                         uint32_t npass, hipStream_t s);
 // Two-tower net: F = private-tower output (ncfg rows, fragment-major 16-bit or
 // row-major f32) times the readout weight, row-major; then player p's readout
 // blocks, tv[entry (row, config)] = <F[config], H[row]> + bread, from the

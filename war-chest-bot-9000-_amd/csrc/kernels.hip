@@ -1389,13 +1389,15 @@ __device__ __forceinline__ float4v mfma16(const uint4& a, const uint4& b, const 
 // step ahead through two; the loop is unrolled by four so every set keeps a
 // fixed role. Loads past the last step re-read the last step (in bounds,
 // unused).
-template <int PREC, int NB, int RB>
+template <int PREC, int NB, int RB, bool ZERO = true>
 __device__ __forceinline__ void chain_kloop(float4v (&acc)[8][CHAIN_NB], const uint16_t* xs, uint32_t ks,
                                             const uint16_t* __restrict__ wp, size_t wstride) {
+    if (ZERO) {  // else acc arrives holding the product's starting value
 #pragma unroll
-    for (int a = 0; a < RB; a++)
+        for (int a = 0; a < RB; a++)
 #pragma unroll
-        for (int b = 0; b < NB; b++) acc[a][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int b = 0; b < NB; b++) acc[a][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    }
     uint4 xa[RB], xb[RB], w0[NB], w1[NB], w2[NB], w3[NB];
     auto ldw = [&](uint4 (&fw)[NB], uint32_t s) {
         s = s < ks ? s : ks - 1;
@@ -1447,21 +1449,30 @@ __device__ __forceinline__ void chain_kloop(float4v (&acc)[8][CHAIN_NB], const u
 }
 
 // The wavefront's share of one layer: 16-feature blocks blk0, blk0 + bstep,
-// ... (nb of them, 0..CHAIN_NB) of RB row blocks from the LDS operand at lds.
-template <int PREC, int RB>
+// ... (nb of them, 0..CHAIN_NB) of RB row blocks from the LDS operand at lds,
+// which holds ks k steps per row block: weight steps w0 .. w0 + ks of
+// matrices with kw steps (all of them when ks == kw).
+template <int PREC, int RB, bool ZERO = true>
 __device__ __forceinline__ void chain_blocks(float4v (&acc)[8][CHAIN_NB], uint32_t nb, const uint16_t* lds,
                                              uint32_t ks, const uint16_t* __restrict__ W, uint32_t blk0,
-                                             uint32_t bstep, uint32_t lane) {
+                                             uint32_t bstep, uint32_t lane, uint32_t kw = 0, uint32_t w0 = 0) {
+    if (!kw) kw = ks;
     const uint16_t* xs = lds + lane * 8;
-    const uint16_t* wp = W + ((size_t)blk0 * ks * 64 + lane) * 8;
-    const size_t wstride = (size_t)bstep * ks * 512;
+    const uint16_t* wp = W + ((size_t)blk0 * kw * 64 + lane) * 8 + (size_t)w0 * 512;
+    const size_t wstride = (size_t)bstep * kw * 512;
     static_assert(CHAIN_NB == 3, "dispatch below covers 1..3 blocks");
     if (nb == 1)
-        chain_kloop<PREC, 1, RB>(acc, xs, ks, wp, wstride);
+        chain_kloop<PREC, 1, RB, ZERO>(acc, xs, ks, wp, wstride);
     else if (nb == 2)
-        chain_kloop<PREC, 2, RB>(acc, xs, ks, wp, wstride);
+        chain_kloop<PREC, 2, RB, ZERO>(acc, xs, ks, wp, wstride);
     else if (nb == 3)
-        chain_kloop<PREC, 3, RB>(acc, xs, ks, wp, wstride);
+        chain_kloop<PREC, 3, RB, ZERO>(acc, xs, ks, wp, wstride);
+}
+
+// One (row block, feature block) tile of a first-layer partial product: the
+// lane's four accumulator values.
+__device__ __forceinline__ size_t part_tile(uint32_t rb, uint32_t fb, uint32_t hblk, uint32_t lane) {
+    return ((size_t)rb * hblk + fb) * 256 + lane * 4;
 }
 
 __device__ __forceinline__ uint32_t pack16(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
@@ -1513,7 +1524,10 @@ __device__ __forceinline__ void chain_head(const ChainNet& net, uint32_t rows, f
 // One pass of the whole network over the pass's RB 16-row blocks (RB <= 8):
 // stage their input operand in LDS, run the trunk layers in place, write the
 // head.
-template <int PREC, int RB>
+// Modes: the whole net; the whole net with the first layer started from a
+// precomputed partial product; the partial product alone.
+constexpr int CHAIN_FULL = 0, CHAIN_PART = 1, CHAIN_STATIC = 2;
+template <int PREC, int RB, int MODE>
 __device__ __forceinline__ void chain_pass(const ChainNet& net, const uint16_t* __restrict__ X, uint32_t rows,
                                            float* __restrict__ out, const ChainPass* __restrict__ ps,
                                            uint16_t* lds, uint32_t lane, uint32_t wave) {
@@ -1521,19 +1535,52 @@ __device__ __forceinline__ void chain_pass(const ChainNet& net, const uint16_t* 
     const uint32_t hblk = net.hidden >> 4, ksn = net.hidden >> 5;
     const uint32_t nb = hblk > wave ? (hblk - wave + CHAIN_WAVES - 1) / CHAIN_WAVES : 0;
     const uint32_t nt = (min(ps->cols, net.heads) + 15) >> 4;  // head column blocks the pass needs
-    // Each row block is one contiguous run of 16 x in halves, in LDS in pass order.
-    const uint32_t per = 2 * net.in;  // uint4 per row block
+    // The first layer's k steps [s0, s0 + sn) of each row block (a contiguous
+    // run of 1 KB steps in X), packed in LDS in pass order: all of them, the
+    // first dsteps (partial start) or the rest (the static product).
+    const uint32_t ks0 = net.in >> 5;
+    constexpr bool part = MODE == CHAIN_PART;
+    const uint32_t s0 = MODE == CHAIN_STATIC ? net.dsteps : 0;
+    const uint32_t sn = MODE == CHAIN_STATIC ? ks0 - net.dsteps : part ? net.dsteps : ks0;
+    const uint32_t per = sn * 64;  // uint4 per row block
 #pragma unroll
     for (int a = 0; a < RB; a++) {
-        const uint4* src = (const uint4*)(X + (size_t)ps->rb[a] * 16 * net.in);
+        const uint4* src = (const uint4*)(X + ((size_t)ps->rb[a] * ks0 + s0) * 512);
         uint4* dst = (uint4*)lds + a * per;
         for (uint32_t i = threadIdx.x; i < per; i += CHAIN_WAVES * 64) dst[i] = src[i];
     }
-    __syncthreads();
     float4v acc[8][CHAIN_NB];
+    if constexpr (part) {  // the first layer starts from the precomputed product of its other columns
+#pragma unroll
+        for (int a = 0; a < RB; a++)
+#pragma unroll
+            for (int b = 0; b < CHAIN_NB; b++)
+                if ((uint32_t)b < nb)
+                    acc[a][b] = *(const float4v*)(net.part + part_tile(ps->rb[a], wave + CHAIN_WAVES * b, hblk, lane));
+    }
+    __syncthreads();
+    if constexpr (MODE == CHAIN_STATIC) {
+        chain_blocks<PREC, RB>(acc, nb, lds, sn, net.w[0], wave, CHAIN_WAVES, lane, ks0, s0);
+#pragma unroll
+        for (int a = 0; a < RB; a++)
+#pragma unroll
+            for (int b = 0; b < CHAIN_NB; b++)
+                if ((uint32_t)b < nb)
+                    *(float4v*)(out + part_tile(ps->rb[a], wave + CHAIN_WAVES * b, hblk, lane)) = acc[a][b];
+        return;
+    }
     uint32_t K = net.in;
     for (uint32_t l = 0; l < net.layers; l++) {
-        chain_blocks<PREC, RB>(acc, nb, lds, K >> 5, net.w[l], wave, CHAIN_WAVES, lane);
+        if constexpr (part) {  // the later layers start from zero
+            if (l > 0)
+#pragma unroll
+                for (int a = 0; a < RB; a++)
+#pragma unroll
+                    for (int b = 0; b < CHAIN_NB; b++) acc[a][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        // (sn = ks0 without the partial start: the same call for every layer)
+        chain_blocks<PREC, RB, !part>(acc, nb, lds, l ? K >> 5 : sn, net.w[l], wave, CHAIN_WAVES, lane,
+                                      l ? 0 : ks0, 0);
         __syncthreads();  // the layer input is dead from here on
         // bias + ReLU, stored over the input as the next operand (K = hidden)
         const float* bias = net.b[l];
@@ -1578,7 +1625,7 @@ __device__ __forceinline__ void chain_pass(const ChainNet& net, const uint16_t* 
 
 // One workgroup per pass of the plan (plan_chain orders the passes so that
 // the costly ones start first).
-template <int PREC>
+template <int PREC, int MODE>
 __global__ __launch_bounds__(CHAIN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(CHAIN_WAVES / 4, CHAIN_WAVES / 4))) void k_chain(
     ChainNet net, const uint16_t* __restrict__ X, uint32_t rows, float* __restrict__ out,
     const ChainPass* __restrict__ plan) {
@@ -1586,14 +1633,14 @@ __global__ __launch_bounds__(CHAIN_WAVES * 64) __attribute__((amdgpu_waves_per_e
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const ChainPass* ps = plan + blockIdx.x;
     switch (min(CHAIN_PASS_BLOCKS, ps->n)) {
-        case 8: chain_pass<PREC, 8>(net, X, rows, out, ps, lds, lane, wave); break;
-        case 7: chain_pass<PREC, 7>(net, X, rows, out, ps, lds, lane, wave); break;
-        case 6: chain_pass<PREC, 6>(net, X, rows, out, ps, lds, lane, wave); break;
-        case 5: chain_pass<PREC, 5>(net, X, rows, out, ps, lds, lane, wave); break;
-        case 4: chain_pass<PREC, 4>(net, X, rows, out, ps, lds, lane, wave); break;
-        case 3: chain_pass<PREC, 3>(net, X, rows, out, ps, lds, lane, wave); break;
-        case 2: chain_pass<PREC, 2>(net, X, rows, out, ps, lds, lane, wave); break;
-        case 1: chain_pass<PREC, 1>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 8: chain_pass<PREC, 8, MODE>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 7: chain_pass<PREC, 7, MODE>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 6: chain_pass<PREC, 6, MODE>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 5: chain_pass<PREC, 5, MODE>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 4: chain_pass<PREC, 4, MODE>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 3: chain_pass<PREC, 3, MODE>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 2: chain_pass<PREC, 2, MODE>(net, X, rows, out, ps, lds, lane, wave); break;
+        case 1: chain_pass<PREC, 1, MODE>(net, X, rows, out, ps, lds, lane, wave); break;
         default: break;
     }
 }
@@ -1602,10 +1649,30 @@ void launch_chain(int precision, const ChainNet& net, const void* X, uint32_t ro
                   const ChainPass* plan, uint32_t npass, hipStream_t s) {
     if (rows == 0 || npass == 0) return;
     dim3 grid(npass), block(CHAIN_WAVES * 64);
+    const uint16_t* x = (const uint16_t*)X;
+    if (precision == WC_F16) {
+        if (net.part)
+            hipLaunchKernelGGL((k_chain<WC_F16, CHAIN_PART>), grid, block, 0, s, net, x, rows, out, plan);
+        else
+            hipLaunchKernelGGL((k_chain<WC_F16, CHAIN_FULL>), grid, block, 0, s, net, x, rows, out, plan);
+    } else {
+        if (net.part)
+            hipLaunchKernelGGL((k_chain<WC_BF16, CHAIN_PART>), grid, block, 0, s, net, x, rows, out, plan);
+        else
+            hipLaunchKernelGGL((k_chain<WC_BF16, CHAIN_FULL>), grid, block, 0, s, net, x, rows, out, plan);
+    }
+}
+
+void launch_chain_static(int precision, const ChainNet& net, const void* X, float* part, const ChainPass* plan,
+                         uint32_t npass, hipStream_t s) {
+    if (npass == 0) return;
+    dim3 grid(npass), block(CHAIN_WAVES * 64);
     if (precision == WC_F16)
-        hipLaunchKernelGGL(k_chain<WC_F16>, grid, block, 0, s, net, (const uint16_t*)X, rows, out, plan);
+        hipLaunchKernelGGL((k_chain<WC_F16, CHAIN_STATIC>), grid, block, 0, s, net, (const uint16_t*)X, 0u, part,
+                           plan);
     else
-        hipLaunchKernelGGL(k_chain<WC_BF16>, grid, block, 0, s, net, (const uint16_t*)X, rows, out, plan);
+        hipLaunchKernelGGL((k_chain<WC_BF16, CHAIN_STATIC>), grid, block, 0, s, net, (const uint16_t*)X, 0u, part,
+                           plan);
 }
 
 }  // namespace wc
