@@ -144,7 +144,7 @@ def main():
         launch_ms = mlp_ms / passes
         flops = mlp_flops_wave / passes  # mean per launch, the fixed-column product included once per traverser
         tf = flops / (launch_ms * 1e-3) / 1e12
-        trace_name = "wc::k_chain<1>"
+        trace_name = "wc::k_chain<1, 1>" if fixed else "wc::k_chain<1, 0>"
         roofline = {"bound": "mfma", "kernel": dominant, "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 5), "flops_per_launch": round(flops),
                     "launch_ms": round(launch_ms, 5)}
