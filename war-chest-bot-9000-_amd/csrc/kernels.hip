@@ -1362,7 +1362,9 @@ void launch_tower_head(const WaveDev& w, int player, int precision, const void* 
 // four consecutive output features 4 (l / 16) .. + 3 of one row l % 16 --
 // one 8-byte LDS store per 16x16 tile in the next layer's fragment layout.
 // Every output is the same f32 sum over the same 32-wide k steps, in the same
-// order, as the layer-by-layer k_gemm.
+// order, as the layer-by-layer k_gemm, except in the partial-start mode, whose
+// first layer adds the pooled columns' steps to the precomputed sum over the
+// fixed columns (the same products, summed in another order).
 
 constexpr uint32_t CHAIN_LDS_HALVES = GEMM_ROWS * CHAIN_MAX_WIDTH;
 
