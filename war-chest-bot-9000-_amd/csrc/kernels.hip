@@ -252,10 +252,17 @@ __global__ __launch_bounds__(BLOCK) void k_reach_rows(WaveDev w, const ReachRec*
         reach_row(w, reach, strat, r1[k - n0]);
 }
 
+// A top depth holds 10k-50k rows, one per thread: one-wavefront workgroups
+// spread them over four times as many CUs as 256-thread ones, so each CU's
+// memory pipeline serves fewer of the rows' dependent loads (0.33 ms per wave
+// of 256 subgames over 1,120 launches).
+constexpr int TOP_BLOCK = 64;
+
 void launch_reach_rows(const WaveDev& w, const ReachRec* r0, uint32_t n0, const ReachRec* r1, uint32_t n1,
                        float* reach, const float* strat, hipStream_t s) {
     if (n0 + n1)
-        hipLaunchKernelGGL(k_reach_rows, dim3(grid_for(n0 + n1)), dim3(BLOCK), 0, s, w, r0, n0, r1, n1, reach, strat);
+        hipLaunchKernelGGL(k_reach_rows, dim3(grid_for(n0 + n1, TOP_BLOCK)), dim3(TOP_BLOCK), 0, s, w, r0, n0, r1, n1,
+                           reach, strat);
 }
 
 // sum = reach * cur: one reach-weighted uniform strategy (engine/src/search.rs:854-870).
@@ -836,11 +843,11 @@ void launch_back_rows(const WaveDev& w, const BackRec* rows, uint32_t n, int tra
                       float db, float predict, hipStream_t s) {
     if (!n) return;
     if (mode == MODE_VALUE)
-        hipLaunchKernelGGL(k_back_rows<MODE_VALUE>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, rows, n, traverser, da,
-                           db, predict);
+        hipLaunchKernelGGL(k_back_rows<MODE_VALUE>, dim3(grid_for(n, TOP_BLOCK)), dim3(TOP_BLOCK), 0, s, w, rows, n,
+                           traverser, da, db, predict);
     else
-        hipLaunchKernelGGL(k_back_rows<MODE_REGRET>, dim3(grid_for(n)), dim3(BLOCK), 0, s, w, rows, n, traverser, da,
-                           db, predict);
+        hipLaunchKernelGGL(k_back_rows<MODE_REGRET>, dim3(grid_for(n, TOP_BLOCK)), dim3(TOP_BLOCK), 0, s, w, rows, n,
+                           traverser, da, db, predict);
 }
 
 // Average strategy: sum / row sum, uniform when the sum is not positive, the
