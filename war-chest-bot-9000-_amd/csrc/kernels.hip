@@ -905,7 +905,9 @@ __global__ __launch_bounds__(BLOCK) void k_gather_carry(WaveDev w, const float* 
 
 void launch_gather_carry(const WaveDev& w, const float* reach, int slot, hipStream_t s) {
     size_t waves = (size_t)w.nexit * 2;
-    if (waves) hipLaunchKernelGGL(k_gather_carry, dim3(grid_for(waves * 64)), dim3(BLOCK), 0, s, w, reach, slot);
+    // one wavefront per (exit, player), one per workgroup: a wavefront that
+    // finishes frees its slot at once
+    if (waves) hipLaunchKernelGGL(k_gather_carry, dim3((uint32_t)waves), dim3(64), 0, s, w, reach, slot);
 }
 
 __global__ void k_collect_root(WaveDev w, int root, int p) {
