@@ -129,7 +129,7 @@ def main():
     if not tower:  # the executor splits when the fused kernel takes the net (chain_fits) and the
         _, n_in, hidden, layers, _, pool = dims  # pooled columns are whole 32-column steps
         fused = n_in % 32 == 0 and n_in <= 512 and hidden % 32 == 0 and hidden <= 384 and 1 <= layers <= 8
-        if fused and n_in > 2 * pool and (2 * pool) % 32 == 0:
+        if fused and 0 < 2 * pool < n_in and (2 * pool) % 32 == 0:
             fixed = st["rows"] * 2 * (n_in - 2 * pool) * hidden
     pass_flops = st["mlp_flops_algorithmic"] - fixed
     mlp_flops_wave = pass_flops * passes + 2 * fixed

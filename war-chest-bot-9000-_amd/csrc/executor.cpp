@@ -389,7 +389,8 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     // The fused net's first-layer product over the fixed query columns, when
     // the pooled columns are whole 32-column k steps ahead of them.
     const bool split = !tower && (precision_ == WC_F16 || precision_ == WC_BF16) &&
-                       chain_fits(ns.in, ns.hidden, ns.layers) && ns.in > 2 * ns.pool && (2 * ns.pool) % 32 == 0;
+                       chain_fits(ns.in, ns.hidden, ns.layers) && ns.pool > 0 && ns.in > 2 * ns.pool &&
+                       (2 * ns.pool) % 32 == 0;
     size_t m_s0 = split ? mtake(prow * ns.hidden * 4) : 0, m_s1 = split ? mtake(prow * ns.hidden * 4) : 0;
     size_t m_px = 0, m_p0 = 0, m_p1 = 0, m_f = 0;
     if (tower) {
