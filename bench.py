@@ -47,15 +47,45 @@ def measured_traffic(workload, kernel):
     return None
 
 
-def cpu_model():
+def host_cpu():
+    """The host's CPU model and core counts, from lscpu."""
+    import subprocess
+
+    info = {}
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in txt.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return "unknown"
+    model = info.get("Model name", "unknown")
+    sockets = info.get("Socket(s)", "?")
+    cores = info.get("Core(s) per socket", "?")
+    tpc = info.get("Thread(s) per core", "?")
+    return f"{model}; {sockets} socket(s) x {cores} cores x {tpc} threads = {os.cpu_count()} logical CPUs"
+
+
+def cpu_share():
+    """Threads for the CPU baseline: the CPUs this process may run on, bounded by
+    the cgroup's CPU quota and by the share the environment states
+    (OMP_NUM_THREADS), and a description of where the number came from."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    why = [f"{n} CPUs in the affinity mask"]
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            q = max(1, int(int(quota) // int(period)))
+            why.append(f"cgroup quota {q} CPUs")
+            n = min(n, q)
+    except (OSError, ValueError):
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        why.append(f"OMP_NUM_THREADS={omp}")
+        n = min(n, int(omp))
+    return max(1, n), ", ".join(why)
 
 
 def main():
@@ -73,6 +103,8 @@ def main():
     ap.add_argument("--service", type=int, default=0, metavar="WAVES",
                     help="also stream WAVES copies of the wave's subgames through the service (wc_submit / wc_wait) "
                          "and report the end-to-end rate")
+    ap.add_argument("--graph-compare", action="store_true",
+                    help="also time the schedule captured into one HIP graph and replayed")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="after the run, copy MIB MiB device to device 3 times (calibrates HBM counters)")
     args = ap.parse_args()
@@ -104,7 +136,7 @@ def main():
     node_iters = st["nodes"] * iters
     queries = st["rows"] * (iters + 2 * st["nroots_max"])
     value = node_iters / (wave_ms * 1e-3)
-    cfr_ms, mlp_ms, leaf_ms, other_ms, iter_ms, back_ms, top_ms, reach_ms = parts
+    cfr_ms, mlp_ms, leaf_ms, other_ms, iter_ms, back_ms, top_ms, reach_ms, _ = parts
     # Algorithmic bytes of one launch of each CFR kernel, averaged over the two traversers.
     kernels = {"k_sweep<regret>": (0, back_ms), "top-region launches (k_back_rows, k_reach_rows)": (1, top_ms),
                "k_reach": (2, reach_ms)}
@@ -203,6 +235,36 @@ def main():
                                  else "algorithmic = trunk + one head row per traverser config"},
     }
 
+    # The leaf-input launches: per iteration the traverser's pooling (its rows'
+    # pooled beliefs into both query inputs) with the traverser's average-strategy
+    # accumulation beside it, and in Phase 2 both players' pooling per carried root.
+    lib_bytes = st["leaf_input_bytes"]
+    acc = [bk[0][3], bk[1][3]]
+    leaf_launches = iters + st["nroots_max"]
+    leaf_total = sum(lib_bytes[t & 1] + acc[t & 1] for t in range(iters)) + \
+        st["nroots_max"] * (lib_bytes[0] + lib_bytes[1])
+    leaf_gbs = leaf_total / (leaf_ms * 1e-3) / 1e9 if leaf_ms > 0 else 0.0
+    out["roofline_leaf_input"] = {
+        "bound": "hbm", "kernel": "k_pool_mfma<1>" if not tower else "k_pool_mfma<2>",
+        "achieved": round(leaf_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(leaf_gbs / HBM_PEAK_GBS, 5),
+        "bytes_per_launch": int(leaf_total / leaf_launches), "launch_ms": round(leaf_ms / leaf_launches, 5),
+        "note": "pooling: each row's reach and outputs, each distinct config list and embedding once; plus the "
+                "traverser's average-strategy accumulation (12 B per cell + 4 B per row) in the same launch"}
+
+    if args.graph_compare:
+        # The same schedule captured once into a HIP graph and replayed.
+        os.environ["WC_GRAPH"] = "1"
+        gex = ww.Executor(0, ww.WC_BF16 if tower else ww.WC_F16)
+        del os.environ["WC_GRAPH"]
+        gv = gex.publish(net)
+        g_ms, g_parts = gex.time_wave(wave, gv, reps=args.steps, warmup=args.warmup)
+        gex.close()
+        out["graph"] = {"ms_per_wave": round(g_ms, 4), "eager_ms_per_wave": round(wave_ms, 4),
+                        "build_ms": round(g_parts[8], 2),
+                        "note": "the whole schedule (one wave) captured into one hipGraph, instantiated once, replayed"}
+        log(f"[bench] graph replay: {g_ms:.3f} ms/wave (eager {wave_ms:.3f}); capture + instantiate "
+            f"{g_parts[8]:.1f} ms on the host")
+
     if not args.no_mlp:
         mnet = W.net_for("mlp65k")
         x = W.mlp65k_inputs()
@@ -267,16 +329,17 @@ def main():
     if not args.no_cpu:
         import oracle as O
 
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads, share = cpu_share()
         n = args.cpu_trees or min(len(jobs), 2 * threads)
         sample = jobs[:n]
-        log(f"[bench] CPU oracle: {n} trees on {threads} threads ...")
+        host = host_cpu()
+        log(f"[bench] CPU oracle: {n} trees on {threads} threads ({share}; host: {host}) ...")
         sec, ni, lq = O.solve_batch(sample, net, O.NET_F32, threads=threads)
         out["cpu_baseline"] = {"value": round(ni / sec, 1), "unit": "node-iters/s", "cores": threads,
                                "kind": "port", "leaf_queries_per_s": round(lq / sec, 1),
                                "sample": f"first {n} of the {len(jobs)} subgames, all {iters} iterations + Phase 2, "
-                                         f"one subgame per thread, f32 net, {sec:.1f} s wall",
-                               "cpu": cpu_model()}
+                                         f"one subgame per thread at a time, f32 net, {sec:.1f} s wall",
+                               "cpu": host, "cpu_share": share}
         log(f"[bench] CPU oracle: {sec:.1f}s, {ni / sec:.0f} node-iters/s")
 
     ex.close()

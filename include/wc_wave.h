@@ -74,6 +74,11 @@ typedef struct wc_service_opts {
     uint32_t wave_jobs;    /* max jobs per wave; reference WARCHEST_WAVE_JOBS, default 64 */
     uint32_t wave_rows;    /* max network rows per wave; reference WARCHEST_WAVE_ROWS, default 49152 */
     uint32_t window_us;    /* bucket-fill window; reference WARCHEST_WAVE_US, default 800 */
+    uint32_t whale_lanes;  /* lanes that take exclusive-route jobs; reference WARCHEST_WAVE_WHALE_LANES,
+                              default (0) 1, clamped to 1..lanes (service.rs:100) */
+    uint32_t class_shift;  /* coarsens the cost classes; reference WARCHEST_WAVE_CLASS_SHIFT, 0..2 (service.rs:993) */
+    uint64_t route_unit;   /* bytes per route-threshold unit: exclusive >= 4, card-exclusive >= 6 units of
+                              reservation (serialize.rs:174-201); 0 = 1 GiB, the reference's thresholds */
 } wc_service_opts;
 
 /* service::spawn(device, dims, w, b, ln, precise): blocks until every lane is
@@ -94,6 +99,24 @@ int wc_submit(wc_service* svc, const uint8_t* job, size_t len, uint64_t tag, wc_
 int wc_wait(wc_ticket* t, wc_result** out);
 /* 1 when wc_wait would not block, 0 otherwise. */
 int wc_poll(const wc_ticket* t);
+/* Drop a ticket without waiting for its result (the reference drops the
+ * SolveHandle's receiver; the solve still runs and its result is discarded). */
+void wc_ticket_free(wc_ticket* t);
+/* Waves launched and guarded routes taken by the service so far (tooling). */
+int wc_service_stats(wc_service* svc, uint64_t* waves, uint64_t* guarded_routes);
+
+/* PackedJob::work and the service's view of one job (serialize.rs:159-201,394-431;
+ * client.rs:282-291; service.rs:967-991), for admission, routing and tests:
+ * the work vector as an executor of `precision` would run the job, its queued-work
+ * cost and its cost class (route thresholds in units of route_unit bytes; 0 = 1 GiB). */
+typedef struct wc_work_vector {
+    uint64_t network_rows, legal_cells, reach_slots, reverse_nonzeros;
+    uint64_t table_bytes, mutable_bytes, carried_output_bytes, levels;
+    uint64_t reserved_bytes;
+    uint32_t exclusive_route, arena_guard_route, card_exclusive_route; /* 0 / 1 */
+} wc_work_vector;
+int wc_job_work(const uint8_t* job, size_t len, int precision, uint64_t route_unit, uint32_t class_shift,
+                wc_work_vector* out, uint64_t* cost, uint32_t* cost_class);
 
 /* SolveResult views (client.rs:113-122). All indices are solve-local. */
 uint64_t wc_result_tag(const wc_result* r);
@@ -104,6 +127,9 @@ const float* wc_result_strategy(const wc_result* r, size_t* n);
 const float* wc_result_root_values(const wc_result* r, uint32_t* nroots, uint32_t* n0, uint32_t* n1);
 /* Carried beliefs, f16 bits: slots x snapshot_configs, laid out by the job's snap_coff. */
 const uint16_t* wc_result_carries(const wc_result* r, uint32_t* slots, uint32_t* snapshot_configs);
+/* SolveResult::{oversize_route, card_exclusive_route} (client.rs:120-121): the
+ * routes the service took for the job (exclusive one-job wave; whole-device drain). */
+int wc_result_routes(const wc_result* r, int* oversize_route, int* card_exclusive_route);
 void wc_result_free(wc_result* r);
 
 /* ------------------------------------------------------ executor (lane) API
@@ -138,6 +164,9 @@ typedef struct wc_wave_stats {
     /* one leaf-net pass over all network rows: FLOP the head-width-trimmed GEMMs
      * execute, and the algorithmic FLOP (trunk + the traverser's configs' head rows) */
     uint64_t mlp_flops_executed, mlp_flops_algorithmic;
+    /* one leaf-input pooling of player p's network rows, 16-bit query inputs:
+     * each row's reach and outputs, each distinct config list and embedding once */
+    uint64_t leaf_input_bytes[2];
 } wc_wave_stats;
 int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* out);
 
@@ -163,15 +192,39 @@ int wc_value_net_plan(const uint32_t* cols, uint32_t nrb, uint32_t heads, uint32
  * (results[k] owned by the caller). */
 int wc_solve_wave(wc_executor* ex, wc_wave* w, uint64_t version, wc_result** results);
 
+/* Executor::launch (device.rs:596-757): queue the wave's upload, its whole
+ * schedule and the result copies on the executor's stream and return at once.
+ * The wave may be freed or repacked as soon as this returns. At most two waves
+ * may be launched on one executor and not yet collected. */
+typedef struct wc_inflight wc_inflight;
+int wc_launch(wc_executor* ex, wc_wave* w, uint64_t version, wc_inflight** out);
+/* 1 when wc_collect would not block, 0 otherwise. */
+int wc_inflight_ready(const wc_executor* ex, const wc_inflight* f);
+/* Executor::collect + Harvest::unpack (device.rs:759-831): wait, then one result
+ * per job of the launched wave (results[k] owned by the caller). Frees f. */
+int wc_collect(wc_executor* ex, wc_inflight* f, wc_result** results);
+
+/* Tooling (no counterpart in the reference): the leaf net's values at the
+ * initial reach (uniform strategy, root beliefs) for one traverser, computed
+ * by the wave's own leaf-input and value-net kernels. values: for each network
+ * row in wave order, the value of each of the row's configs of the traverser,
+ * in the row's config order (*count receives the total; nothing is written
+ * when it exceeds cap); mass (rows x 2, may be NULL): the rows' reach masses. */
+int wc_wave_leaf_probe(wc_executor* ex, wc_wave* w, uint64_t version, int traverser, float* values, size_t cap,
+                       size_t* count, float* mass);
+
 /* Benchmark helper: upload once, run the full schedule `warmup` times
  * untimed, then `reps` times timed (inputs resident in HBM), returning the
  * mean device time per wave in milliseconds, measured with HIP events on the
- * executor's stream. kernel_ms (optional, 8 doubles) receives one profiled
+ * executor's stream. kernel_ms (optional, 9 doubles) receives one profiled
  * schedule's device time per launch class: [0] CFR sweeps, [1] leaf MLP,
  * [2] leaf input, [3] everything else; [4] the mean device time of one CFR
  * iteration (all its sweep kernels), and the mean device time per iteration of
  * [5] the subtree value sweep, [6] the top-region launches (values and reach,
- * one launch per depth each), [7] the subtree reach sweep. */
+ * one launch per depth each), [7] the subtree reach sweep; [8] the host time
+ * to capture and instantiate the schedule as one HIP graph (0 when the
+ * executor runs without graphs: the environment variable WC_GRAPH=1 at
+ * executor creation turns them on). */
 int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup, uint32_t reps, double* wave_ms,
                  double* kernel_ms);
 

@@ -37,7 +37,14 @@
 #define SMOOTH 1e-30f  /* rebel.rs:359 */
 
 enum { MODEL_V5 = 5, MODEL_MLP = 101, MODEL_TWO_TOWER = 102 };
-enum { NET_EMPTY = 0, NET_F32 = 1, NET_F16 = 2, NET_BF16 = 3 };
+/* Leaf-net arithmetic models. F32 is the CPU net's float32 loop, bit for
+ * bit. The others model a device: operands rounded on entry (and every
+ * activation that feeds a layer), exact products, and either a wide (double)
+ * sum or, for F16A, a float32 sum in ascending k order -- two equally faithful
+ * f16 realizations that differ only in how the f32-level sum is rounded.
+ * F16X holds each operand as the f16 pair hi + lo (about 22 significant bits:
+ * the compensated mode), F32W keeps float32 operands with a wide sum. */
+enum { NET_EMPTY = 0, NET_F32 = 1, NET_F16 = 2, NET_BF16 = 3, NET_F16A = 4, NET_F16X = 5, NET_F32W = 6 };
 enum { BACK_REGRET = 0, BACK_VALUE = 1, BACK_BR = 2 };
 
 static __thread char g_err[256];
@@ -385,7 +392,7 @@ float oracle_round_bf16(float x) { return round_bf16(x); }
 /* ------------------------------------------------------------------ net */
 
 typedef struct {
-    int mode; /* NET_EMPTY / NET_F32 / NET_F16 / NET_BF16 */
+    int mode; /* NET_EMPTY / NET_F32 / NET_F16 / NET_BF16 / NET_F16A / NET_F16X / NET_F32W */
     uint32_t kind, in, hidden, layers, heads, pool, priv_in, priv_layers;
     /* MLP: W[0] in x hidden, W[1..layers-1] hidden x hidden, Whead heads x hidden */
     const float* w;
@@ -403,10 +410,17 @@ typedef struct {
 } Net;
 
 static float q_op(const Net* n, float x) {
-    if (n->mode == NET_F16) return round_f16(x);
+    if (n->mode == NET_F16 || n->mode == NET_F16A) return round_f16(x);
     if (n->mode == NET_BF16) return round_bf16(x);
+    if (n->mode == NET_F16X) {
+        float hi = round_f16(x);
+        return hi + round_f16(x - hi);
+    }
     return x;
 }
+
+/* The model sums in double (every reduced-precision model but F16A, and F32W). */
+static int wide_sum(const Net* n) { return n->mode != NET_F32 && n->mode != NET_F16A; }
 
 static int net_init(Net* n, int mode, const uint32_t* dims, uint32_t ndims, const float* w, size_t nw,
                     const float* b, size_t nb) {
@@ -458,7 +472,7 @@ static int net_init(Net* n, int mode, const uint32_t* dims, uint32_t ndims, cons
     n->w = w;
     n->b = b;
     const float* ww = w;
-    if (mode == NET_F16 || mode == NET_BF16) {
+    if (mode == NET_F16 || mode == NET_BF16 || mode == NET_F16A || mode == NET_F16X) {
         n->wq = (float*)malloc(nw * sizeof(float));
         for (size_t k = 0; k < nw; k++) n->wq[k] = q_op(n, w[k]);
         ww = n->wq;
@@ -516,7 +530,7 @@ static void net_free(Net* n) {
  * rounded on entry, products are exact, the sum is taken in double. */
 static void dense_relu(const Net* n, const float* x, uint32_t k, const float* W, const float* bias,
                        uint32_t m, float* y) {
-    if (n->mode == NET_F32) {
+    if (!wide_sum(n)) {
         for (uint32_t j = 0; j < m; j++) y[j] = 0.0f;
         for (uint32_t p = 0; p < k; p++) {
             float a = x[p];
@@ -570,6 +584,11 @@ static float head_value(const Net* n, const float* h, uint32_t key) {
         float v = n->bhead[key];
         for (uint32_t j = 0; j < n->hidden; j++) v += row[j] * h[j];
         return v;
+    }
+    if (n->mode == NET_F16A) { /* the product's f32 sum, then the bias, as a GEMM epilogue adds it */
+        float v = 0.0f;
+        for (uint32_t j = 0; j < n->hidden; j++) v += row[j] * h[j];
+        return v + n->bhead[key];
     }
     double v = 0.0;
     for (uint32_t j = 0; j < n->hidden; j++) v += (double)row[j] * (double)h[j];
@@ -736,6 +755,27 @@ static void pbs_head(Solver* s, int traverser) {
     }
 }
 
+/* The net's value of network row r's c-th config of player p, from the trunk
+ * output of the last pbs_head (engine/src/net.rs:844-853 for the MLP head). */
+static float net_value(const Solver* s, uint32_t r, int p, uint32_t c) {
+    const Job* j = s->j;
+    const Net* n = s->net;
+    const uint32_t* cidx = j->leaf_cidx.v + j->leaf_coff.v[2 * r + (uint32_t)p];
+    const float* h = s->h + (size_t)r * n->hidden;
+    const float* phi = j->cphi.v + (size_t)cidx[c] * j->cfeat;
+    if (n->kind == MODEL_MLP) return head_value(n, h, (uint32_t)phi[0]);
+    /* two-tower: <f(c), h> + bias with f(c) = private tower output x readout weight */
+    const float* f = s->fcfg + (size_t)cidx[c] * n->hidden;
+    if (!wide_sum(n)) {
+        float acc = n->bread;
+        for (uint32_t k = 0; k < n->hidden; k++) acc += f[k] * h[k];
+        return acc;
+    }
+    double acc = 0.0;
+    for (uint32_t k = 0; k < n->hidden; k++) acc += (double)f[k] * (double)h[k];
+    return (float)acc + n->bread;
+}
+
 /* Leaf counterfactual values for player p (engine/src/search.rs:1587-1636). */
 static void readout(Solver* s, int p) {
     const Job* j = s->j;
@@ -761,26 +801,7 @@ static void readout(Solver* s, int p) {
             for (uint32_t c = 0; c < nn; c++) v[c] = 0.0f;
             continue;
         }
-        const uint32_t* cidx = j->leaf_cidx.v + j->leaf_coff.v[2 * r + (uint32_t)p];
-        const float* h = s->h + (size_t)r * n->hidden;
-        for (uint32_t c = 0; c < nn; c++) {
-            const float* phi = j->cphi.v + (size_t)cidx[c] * j->cfeat;
-            if (n->kind == MODEL_MLP) {
-                v[c] = head_value(n, h, (uint32_t)phi[0]);
-            } else {
-                /* two-tower: <f(c), h> + bias with f(c) = private tower output x readout weight */
-                const float* f = s->fcfg + (size_t)cidx[c] * n->hidden;
-                if (n->mode == NET_F32) {
-                    float acc = n->bread;
-                    for (uint32_t k = 0; k < n->hidden; k++) acc += f[k] * h[k];
-                    v[c] = acc;
-                } else {
-                    double acc = 0.0;
-                    for (uint32_t k = 0; k < n->hidden; k++) acc += (double)f[k] * (double)h[k];
-                    v[c] = (float)acc + n->bread;
-                }
-            }
-        }
+        for (uint32_t c = 0; c < nn; c++) v[c] = net_value(s, r, p, c);
         for (uint32_t c = 0; c < nn; c++) v[c] *= opp_reach;
     }
 }
@@ -1241,6 +1262,56 @@ int oracle_solve(const uint8_t* b, size_t n, int net_mode, const uint32_t* dims,
     if (roots) value_under(&s, roots);
     if (carries && j.snapshots) carried_beliefs(&s, carries);
     if (conv) nash_conv(&s, &conv[0], &conv[1]);
+    rc = 0;
+out:
+    solver_free(&s);
+    net_free(&net);
+    job_free(&j);
+    return rc;
+}
+
+/* The leaf net's values at the initial reach (Solver::new: uniform strategy,
+ * the root beliefs) for traverser p: for each network row in order, the net's
+ * value of each of the row's configs of player p, in the row's config order
+ * (values: the sum over rows of nc_p floats, *count receives it; nothing is
+ * written when it exceeds cap), and every row's reach masses of both players
+ * (mass: rows x 2, config-order sums). */
+int oracle_leaf_probe(const uint8_t* b, size_t n, int net_mode, const uint32_t* dims, uint32_t ndims,
+                      const float* w, size_t nw, const float* bias, size_t nb, int traverser, float* values,
+                      size_t cap, size_t* count, float* mass) {
+    Job j;
+    Net net;
+    Solver s;
+    int rc = -1;
+    memset(&s, 0, sizeof s);
+    memset(&net, 0, sizeof net);
+    if (!parse_job(b, n, &j)) goto out;
+    if (!net_init(&net, net_mode, dims, ndims, w, nw, bias, nb)) goto out;
+    if (net_mode == NET_EMPTY || traverser < 0 || traverser > 1) {
+        snprintf(g_err, sizeof g_err, "leaf probe needs a network and a traverser 0 or 1");
+        goto out;
+    }
+    if (!solver_init(&s, &j, &net)) goto out;
+    leaf_beliefs_both(&s);
+    pbs_head(&s, traverser);
+    size_t k = 0;
+    for (uint32_t r = 0; r < j.rows; r++) k += S_nc(&s, j.leaf_rows.v[r], traverser);
+    *count = k;
+    if (k > cap) {
+        rc = 0;
+        goto out;
+    }
+    k = 0;
+    for (uint32_t r = 0; r < j.rows; r++) {
+        uint32_t i = j.leaf_rows.v[r];
+        for (uint32_t c = 0; c < S_nc(&s, i, traverser); c++) values[k++] = net_value(&s, r, traverser, c);
+        for (int p = 0; p < 2; p++) {
+            const float* ro = reach_of(&s, i, p);
+            float tot = 0.0f;
+            for (uint32_t c = 0; c < S_nc(&s, i, p); c++) tot += ro[c];
+            if (mass) mass[2 * r + (uint32_t)p] = tot;
+        }
+    }
     rc = 0;
 out:
     solver_free(&s);

@@ -14,6 +14,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "liboracle.so")
 
 NET_EMPTY, NET_F32, NET_F16, NET_BF16 = 0, 1, 2, 3
+# Further arithmetic models of the leaf net (oracle.c): f16 operands with a
+# float32 sum in ascending k order; compensated f16 operand pairs (hi + lo);
+# float32 operands with a wide sum.
+NET_F16A, NET_F16X, NET_F32W = 4, 5, 6
 
 _lib = None
 
@@ -49,6 +53,8 @@ def lib():
         L.oracle_mlp_batch.argtypes = [C.c_uint32, f32p, C.c_uint32, u32p, C.c_uint32, C.c_int, u32p,
                                        C.c_uint32, f32p, C.c_size_t, f32p, C.c_size_t, f32p]
         L.oracle_mlp_batch.restype = C.c_double
+        L.oracle_leaf_probe.argtypes = [u8p, C.c_size_t, C.c_int, u32p, C.c_uint32, f32p, C.c_size_t, f32p,
+                                        C.c_size_t, C.c_int, f32p, C.c_size_t, C.POINTER(C.c_size_t), f32p]
         L.oracle_factor.argtypes = [C.c_float, C.c_float]
         L.oracle_factor.restype = C.c_float
         L.oracle_round_f16.argtypes = [C.c_float]
@@ -108,6 +114,28 @@ def solve(job: bytes, net=None, mode=NET_F32, conv=False):
         "conv": (float(cv[0]), float(cv[1])) if conv else None,
         "shape": s,
     }
+
+
+def leaf_probe(job: bytes, net, mode, traverser):
+    """The leaf net's values at the initial reach for `traverser` (oracle_leaf_probe):
+    (values: each network row's configs of the traverser in row order, concatenated;
+    mass: [rows, 2] reach masses)."""
+    s = shape(job)
+    d, nd, w, nw, b, nb = _net_args(net, mode)
+    buf = (C.c_uint8 * len(job)).from_buffer_copy(job)
+    count = C.c_size_t()
+    mass = np.zeros((max(s.rows, 1), 2), np.float32)
+    rc = lib().oracle_leaf_probe(buf, len(job), mode, _p(d, C.c_uint32), nd, _p(w, C.c_float), nw,
+                                 _p(b, C.c_float), nb, traverser, None, 0, C.byref(count), None)
+    if rc != 0:
+        raise ValueError(_err())
+    vals = np.zeros(max(count.value, 1), np.float32)
+    rc = lib().oracle_leaf_probe(buf, len(job), mode, _p(d, C.c_uint32), nd, _p(w, C.c_float), nw,
+                                 _p(b, C.c_float), nb, traverser, _p(vals, C.c_float), vals.size, C.byref(count),
+                                 _p(mass, C.c_float))
+    if rc != 0:
+        raise ValueError(_err())
+    return vals[: count.value], mass[: s.rows]
 
 
 def mlp(x: np.ndarray, keys: np.ndarray, net, mode=NET_F32, want_h=False):

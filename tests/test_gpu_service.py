@@ -1,0 +1,182 @@
+"""The service and the executor's launch/collect split on the GPU, through the C ABI.
+
+- queued_work (engine/src/gpu/client.rs:274-291) is the sum of the queued
+  jobs' job_cost while they wait, and drains to zero;
+- several lanes and several submitting threads return every job's result
+  bit-identical to a solve of that job alone (the reference's lanes,
+  engine/src/gpu/service.rs:546-742);
+- wc_launch / wc_collect (engine/src/gpu/device.rs:596-831): two waves in
+  flight on one executor, the packed wave freed while its wave runs;
+- cost classes and guarded routes (service.rs:452-532,967-991): exclusive
+  jobs run in one-job waves, guarded jobs after every lane has drained and
+  trimmed, and the results carry their route flags (client.rs:119-121).
+"""
+import sys
+import threading
+
+import numpy as np
+import pytest
+
+import warchest_wave as ww
+import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def small_jobs(trees, seed, **kw):
+    spec = dict(trees=trees, nodes_lo=30, nodes_hi=90, chance=1, terminal_p=0.15, notrans_p=0.05, nroots=2, iters=8,
+                info_median=6.0, info_p99=40.0, info_cap=40, seed=seed)
+    spec.update(kw)
+    return W.jobs("wave256", **spec)
+
+
+_EX = []
+
+
+def alone(jobs, net):
+    """Each job solved in a wave of its own (float32)."""
+    if not _EX:
+        _EX.append(ww.Executor(0, ww.WC_PRECISE))
+    ex = _EX[0]
+    v = ex.publish(net)
+    out = []
+    for j in jobs:
+        w = ww.Wave([j])
+        out.append(ex.solve(w, v)[0])
+        w.close()
+    return out
+
+
+def same(g, r, tag):
+    np.testing.assert_array_equal(g.strategy, r.strategy, err_msg=tag)
+    np.testing.assert_array_equal(g.root_values, r.root_values, err_msg=tag)
+    np.testing.assert_array_equal(g.carries, r.carries, err_msg=tag)
+
+
+def test_queued_work_is_the_sum_of_job_costs_and_drains():
+    jobs = small_jobs(6, 51)
+    net = W.net_for("wave256")
+    costs = [ww.job_work(j, ww.WC_PRECISE)["cost"] for j in jobs]
+    say(f"case queued work: 6 jobs, costs {costs}")
+    # A 3-second bucket window: the lane holds the wave open while every job
+    # is submitted, so nothing is answered before the check.
+    with ww.spawn(0, net, ww.WC_PRECISE, lanes=1, wave_jobs=64, window_us=3_000_000) as client:
+        handles = [client.submit(j, tag=k) for k, j in enumerate(jobs)]
+        assert client.queued_work() == sum(costs)
+        got = [h.wait() for h in handles]
+        assert client.queued_work() == 0
+    for k, (g, r) in enumerate(zip(got, alone(jobs, net))):
+        same(g, r, f"job {k}")
+
+
+def test_lanes_and_submitting_threads():
+    jobs = small_jobs(20, 53)
+    net = W.net_for("wave256")
+    ref = alone(jobs, net)
+    say("case lanes: 3 lanes, 4 submitting threads, 20 jobs, waves of at most 3")
+    results = {}
+    errors = []
+    with ww.spawn(0, net, ww.WC_PRECISE, lanes=3, wave_jobs=3, window_us=500) as client:
+        def submitter(t):
+            try:
+                mine = list(range(t, len(jobs), 4))
+                handles = [(k, client.submit(jobs[k], tag=1000 + k)) for k in mine]
+                for k, h in handles:
+                    results[k] = h.wait()
+            except Exception as e:  # reported after the join
+                errors.append(e)
+
+        threads = [threading.Thread(target=submitter, args=(t,)) for t in range(4)]
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join()
+        stats = client.stats()
+        assert client.queued_work() == 0
+    assert not errors, errors
+    say(f"{stats['waves']} waves")
+    assert stats["waves"] >= 7
+    for k in range(len(jobs)):
+        assert results[k].tag == 1000 + k
+        same(results[k], ref[k], f"job {k}")
+
+
+def test_launch_collect_two_waves_in_flight():
+    jobs = small_jobs(7, 57)
+    net = W.net_for("wave256")
+    ref = alone(jobs, net)
+    say("case launch/collect: waves of 4 and 3 jobs in flight together on one executor")
+    ex = ww.Executor(0, ww.WC_PRECISE)
+    v = ex.publish(net)
+    a, b = ww.Wave(jobs[:4]), ww.Wave(jobs[4:])
+    fa = ex.launch(a, v)
+    a.close()  # the packed wave may go as soon as launch returns
+    fb = ex.launch(b, v)
+    c = ww.Wave(jobs[:1])
+    with pytest.raises(ww.WaveError):
+        ex.launch(c, v)  # a third wave before a collect
+    got = fa.collect() + fb.collect()
+    assert fb.ready() is False  # collected
+    fc = ex.launch(c, v)
+    got_c = fc.collect()
+    b.close()
+    c.close()
+    ex.close()
+    for k, (g, r) in enumerate(zip(got, ref)):
+        same(g, r, f"job {k}")
+    same(got_c[0], ref[0], "relaunch")
+
+
+def test_cost_classes_and_guarded_routes():
+    """With the route unit lowered so that the larger of these jobs need one-job
+    waves, arena guards or the whole device (the reference's 4 / 6 GiB
+    thresholds scaled down), results stay bit-exact and carry their routes."""
+    jobs = small_jobs(6, 59) + small_jobs(4, 61, nodes_lo=150, nodes_hi=260, info_median=12.0, info_p99=80.0,
+                                          info_cap=80)
+    net = W.net_for("wave256")
+    ref = alone(jobs, net)
+    work = [ww.job_work(j, ww.WC_PRECISE) for j in jobs]
+    reserved = sorted(w["reserved_bytes"] for w in work)
+    chosen = None
+    for unit in sorted({max(r // 6, 1) for r in reserved} | {max(r // 4, 1) for r in reserved}):
+        ws = [ww.job_work(j, ww.WC_PRECISE, route_unit=unit) for j in jobs]
+        ex = sum(w["exclusive_route"] for w in ws)
+        card = sum(w["card_exclusive_route"] for w in ws)
+        guard = sum(w["arena_guard_route"] for w in ws)
+        if 1 <= card and 1 <= guard + card and ex < len(jobs) - 2:
+            chosen, work = unit, ws
+            break
+    assert chosen, "no route unit splits these jobs into ordinary, exclusive and card-exclusive"
+    guarded = sum(1 for w in work if w["arena_guard_route"] or w["card_exclusive_route"])
+    say(f"case routes: unit {chosen} bytes; exclusive {[w['exclusive_route'] for w in work]}, "
+        f"card {[w['card_exclusive_route'] for w in work]}, guard {[w['arena_guard_route'] for w in work]}")
+    with ww.spawn(0, net, ww.WC_PRECISE, lanes=2, wave_jobs=8, window_us=1000, route_unit=chosen) as client:
+        handles = [client.submit(j, tag=k) for k, j in enumerate(jobs)]
+        got = [h.wait() for h in handles]
+        stats = client.stats()
+        assert client.queued_work() == 0
+    assert stats["guarded_routes"] == guarded
+    exclusive = sum(w["exclusive_route"] for w in work)
+    assert stats["waves"] >= exclusive + 1
+    for k, (g, r, w) in enumerate(zip(got, ref, work)):
+        same(g, r, f"job {k}")
+        assert g.oversize_route == bool(w["exclusive_route"])
+        assert g.card_exclusive_route == bool(w["card_exclusive_route"])
+
+
+def test_dropped_handle_frees_its_ticket():
+    jobs = small_jobs(3, 63)
+    net = W.net_for("wave256")
+    say("case dropped handle: a job submitted and never waited on")
+    with ww.spawn(0, net, ww.WC_PRECISE, lanes=1, wave_jobs=1, window_us=0) as client:
+        h = client.submit(jobs[0], tag=1)
+        del h
+        rest = [client.submit(j, tag=2 + k) for k, j in enumerate(jobs[1:])]
+        got = [h.wait() for h in rest]
+    for g, r in zip(got, alone(jobs[1:], net)):
+        same(g, r, "after a dropped handle")

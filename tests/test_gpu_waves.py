@@ -1,0 +1,237 @@
+"""GPU parity at the workloads' own shapes, through the C ABI.
+
+- The leaf net inside a wave (wc_wave_leaf_probe): the values the device's
+  leaf-input and value-net kernels produce at the initial reach, per network
+  row and config, against the oracle's leaf probe. One network evaluation is a
+  well-conditioned quantity, so the reduced-precision device is held to the
+  oracle's model of its own operand rounding tightly, on every row of the
+  waves, including the first layer's fixed-column split and the per-block
+  head widths of the 256-subgame wave.
+- The 256-subgame wave's subgames at their full shape (200..800 nodes,
+  lognormal infostates up to 567, 64 iterations, the 567-head net): float32
+  bit-exact, f16 within the f16 envelope.
+- The heavy-tail wave's whales (2,000 nodes, 567 infostates per player,
+  128 iterations, the two-tower net): float32 bit-exact; bf16 within the
+  spread that bf16 rounding itself produces (tests/test_conditioning.py).
+"""
+import os
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+
+import oracle as O
+import warchest_wave as ww
+import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def pmap(fn, items):
+    with ThreadPoolExecutor(THREADS) as pool:
+        return list(pool.map(fn, items))
+
+
+_EX = {}
+
+
+def executor(precision):
+    if precision not in _EX:
+        _EX[precision] = ww.Executor(0, precision)
+    return _EX[precision]
+
+
+def oracle_probe(jobs, net, mode, p):
+    """The oracle's leaf values and masses for every job, concatenated in wave order."""
+    out = pmap(lambda j: O.leaf_probe(j, net, mode, p), jobs)
+    return np.concatenate([v for v, _ in out]), np.concatenate([m for _, m in out])
+
+
+def device_probe(ex, jobs, net, p):
+    v = ex.publish(net)
+    wave = ww.Wave(jobs)
+    try:
+        return ex.leaf_probe(wave, v, p)
+    finally:
+        wave.close()
+
+
+def assert_tracks(got, want, rtol_scale, tag):
+    """|got - want| <= rtol_scale * max |want| (the MLP tests' criterion), and the
+    median error far below it."""
+    assert got.shape == want.shape, tag
+    scale = float(np.abs(want).max())
+    err = np.abs(got.astype(np.float64) - want)
+    say(f"{tag}: {got.size} values, max error {err.max() / scale:.2e}, median {np.median(err) / scale:.2e} "
+        f"of the largest |value|")
+    assert err.max() <= rtol_scale * scale, tag
+    assert np.median(err) <= 0.05 * rtol_scale * scale, tag
+
+
+def test_leaf_probe_float32_bit_exact():
+    jobs = W.jobs("wave64")
+    net = W.net_for("wave64")
+    ex = executor(ww.WC_PRECISE)
+    for p in (0, 1):
+        say(f"case leaf probe float32: wave64, all {len(jobs)} subgames, traverser {p}")
+        got, mass = device_probe(ex, jobs, net, p)
+        want, want_mass = oracle_probe(jobs, net, O.NET_F32, p)
+        np.testing.assert_array_equal(got, want)
+        np.testing.assert_array_equal(mass, want_mass)
+
+
+@pytest.mark.parametrize("precision,mode,tol", [(ww.WC_F16, O.NET_F16, 2e-3), (ww.WC_BF16, O.NET_BF16, 1e-2)])
+def test_leaf_probe_wave64_tracks_the_operand_model(precision, mode, tol):
+    """Every row of the 64-subgame wave: the grouped MFMA pooling, the fused
+    net's passes, the leaf records."""
+    jobs = W.jobs("wave64")
+    net = W.net_for("wave64")
+    ex = executor(precision)
+    for p in (0, 1):
+        say(f"case leaf probe {'f16' if precision == ww.WC_F16 else 'bf16'}: wave64, traverser {p}")
+        got, mass = device_probe(ex, jobs, net, p)
+        want, want_mass = oracle_probe(jobs, net, mode, p)
+        assert_tracks(got, want, tol, f"wave64 traverser {p}")
+        # masses: the same float32 reach, summed in another order
+        np.testing.assert_allclose(mass, want_mass, rtol=2e-6, atol=1e-30)
+
+
+def test_leaf_probe_wave256_fixed_column_split():
+    """The whole 256-subgame wave (49,371 rows, 567 heads, per-block head widths):
+    the fused net with the first layer's fixed-column product precomputed (the
+    schedule's default) against the f16 operand model, and against the same
+    net run without the split (WC_CHAIN_SPLIT=0), which sums the first layer
+    in another order only."""
+    jobs = W.jobs("wave256")
+    net = W.net_for("wave256")
+    split = ww.Executor(0, ww.WC_F16)
+    os.environ["WC_CHAIN_SPLIT"] = "0"
+    try:
+        whole = ww.Executor(0, ww.WC_F16)
+    finally:
+        del os.environ["WC_CHAIN_SPLIT"]
+    try:
+        for p in (0, 1):
+            say(f"case leaf probe f16: wave256, all {len(jobs)} subgames, traverser {p}, split and unsplit")
+            a, _ = device_probe(split, jobs, net, p)
+            b, _ = device_probe(whole, jobs, net, p)
+            want, _ = oracle_probe(jobs, net, O.NET_F16, p)
+            assert_tracks(a, want, 2e-3, f"wave256 split, traverser {p}")
+            assert_tracks(b, want, 2e-3, f"wave256 unsplit, traverser {p}")
+            # the two orders agree except where a first-layer sum rounds to a
+            # neighbouring f16 activation
+            assert_tracks(a, b.astype(np.float64), 2e-3, f"wave256 split vs unsplit, traverser {p}")
+            same = np.mean(np.abs(a - b) <= 1e-6 * np.abs(b).max())
+            say(f"split and unsplit agree to 1e-6 on {same:.1%} of the values")
+            assert same >= 0.5
+    finally:
+        split.close()
+        whole.close()
+
+
+def full_wave256(trees=16):
+    return W.jobs("wave256")[:trees]
+
+
+def test_wave256_full_shape_float32_bit_exact():
+    jobs = full_wave256()
+    net = W.net_for("wave256")
+    say(f"case wave256 full shape float32: {len(jobs)} subgames of 200..800 nodes, 64 iterations, 567 heads")
+    ex = executor(ww.WC_PRECISE)
+    v = ex.publish(net)
+    wave = ww.Wave(jobs)
+    got = ex.solve(wave, v)
+    wave.close()
+    refs = pmap(lambda j: O.solve(j, net, O.NET_F32), jobs)
+    for k, (g, o) in enumerate(zip(got, refs)):
+        np.testing.assert_array_equal(g.strategy, o["strategy"], err_msg=f"tree {k}: strategy")
+        np.testing.assert_array_equal(g.root_values, o["roots"], err_msg=f"tree {k}: root values")
+        np.testing.assert_array_equal(g.carries, o["carries"].astype(np.float16), err_msg=f"tree {k}: carries")
+
+
+def test_wave256_full_shape_f16_within_the_f16_envelope():
+    """f16, the 16 full-shape subgames, judged by the envelope of the two f16
+    emulations (tests/envelope.py)."""
+    import envelope
+    jobs = full_wave256()
+    net = W.net_for("wave256")
+    say(f"case wave256 full shape f16: {len(jobs)} subgames, against float32 and two f16 emulations")
+    ex = executor(ww.WC_F16)
+    v = ex.publish(net)
+    wave = ww.Wave(jobs)
+    got = ex.solve(wave, v)
+    wave.close()
+    work = [(j, m) for m in (O.NET_F32, O.NET_F16, O.NET_F16A) for j in jobs]
+    out = pmap(lambda a: O.solve(a[0], net, a[1]), work)
+    n = len(jobs)
+    f32, e16, e16a = out[:n], out[n:2 * n], out[2 * n:]
+    dev, emu, ms = [], [], []
+    for k, g in enumerate(got):
+        scale = np.abs(f32[k]["roots"]).max()
+        dev.append(np.abs(g.root_values - f32[k]["roots"]).max() / scale)
+        emu.append(max(np.abs(e16[k]["roots"] - f32[k]["roots"]).max(),
+                       np.abs(e16a[k]["roots"] - f32[k]["roots"]).max()) / scale)
+        ms.append(float(np.abs(g.strategy - f32[k]["strategy"]).mean()))
+    envelope.check(dev, emu, ms, 5e-3, say, "wave256 f16", frac=0.8)
+
+
+def whale_wave():
+    """Two whales (2,000 nodes, 567 infostates per player) and two ordinary
+    subgames of the heavy-tail wave, at its shape: 128 iterations."""
+    jobs = W.jobs("wave512w", trees=40)
+    whales = [j for j in jobs if O.shape(j).nodes >= 1500][:2]
+    others = [j for j in jobs if O.shape(j).nodes < 1500][:2]
+    assert len(whales) == 2 and len(others) == 2
+    return whales + others
+
+
+@pytest.mark.timeout(400)
+def test_wave512w_whales_float32_bit_exact_and_bf16_near_float32():
+    jobs = whale_wave()
+    net = W.net_for("wave512w")
+    shapes = [(O.shape(j).nodes, O.shape(j).root_n0, O.shape(j).iters) for j in jobs]
+    say(f"case wave512w whales: (nodes, root infostates, iterations) = {shapes}, two-tower net")
+    v32 = executor(ww.WC_PRECISE).publish(net)
+    wave = ww.Wave(jobs)
+    exact = executor(ww.WC_PRECISE).solve(wave, v32)
+    vb = executor(ww.WC_BF16).publish(net)
+    fast = executor(ww.WC_BF16).solve(wave, vb)
+    wave.close()
+    say("device solves done; oracle float32 solves (about a minute per whale) ...")
+    refs = pmap(lambda j: O.solve(j, net, O.NET_F32), jobs)
+    for k, (g, b, o) in enumerate(zip(exact, fast, refs)):
+        np.testing.assert_array_equal(g.strategy, o["strategy"], err_msg=f"tree {k}: strategy")
+        np.testing.assert_array_equal(g.root_values, o["roots"], err_msg=f"tree {k}: root values")
+        mean_s = float(np.abs(b.strategy - o["strategy"]).mean())
+        tol = 0.4 + 0.1 * np.maximum(np.abs(b.strategy), np.abs(o["strategy"]))
+        ratio = float((np.abs(b.strategy - o["strategy"]) / tol).max())
+        rel = np.abs(b.root_values - o["roots"]).max() / np.abs(o["roots"]).max()
+        say(f"tree {k}: float32 bit-exact; bf16 mean strategy error {mean_s:.2e}, pointwise guard ratio "
+            f"{ratio:.2f}, root error {rel:.2e} of the largest root value")
+        # bf16 keeps 8 significant bits: over the 64-subgame wave its emulation's
+        # mean strategy error reaches 1.4e-2 and its root error 0.25 (median 6e-3);
+        # a near-tie between two actions can flip one strategy entry (the
+        # pointwise guard), which is reported, not bounded.
+        assert mean_s <= 1.5e-2, f"tree {k}"
+        assert rel <= 5e-2, f"tree {k}"
+
+
+def test_wave512w_whale_leaf_probe_bf16():
+    """The two-tower net's values on the whales (1,000+ interned configs, the
+    block-diagonal readout) against the bf16 operand model."""
+    jobs = whale_wave()
+    net = W.net_for("wave512w")
+    ex = executor(ww.WC_BF16)
+    for p in (0, 1):
+        say(f"case leaf probe bf16 two-tower: whales, traverser {p}")
+        got, _ = device_probe(ex, jobs, net, p)
+        want, _ = oracle_probe(jobs, net, O.NET_BF16, p)
+        assert_tracks(got, want, 1e-2, f"whales traverser {p}")

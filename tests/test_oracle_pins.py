@@ -295,10 +295,10 @@ def test_zero_network_keeps_every_value_zero():
     np.testing.assert_allclose(o["strategy"], uniform_cur(d), rtol=2e-6)
 
 
-def numpy_value_under(d, net, root):
-    """value_under (search.rs:1851-1871) in float64 under the uniform strategy:
-    propagate, pooled beliefs (search.rs:1501-1547), the MLP per traverser,
-    leaf readout (search.rs:1587-1636) and the Value backprop (search.rs:1654-1803)."""
+def numpy_leaf_net(d, net, reach):
+    """The leaf net in float64 at a given reach: pooled beliefs (search.rs:1501-1547),
+    the query input, the MLP or two-tower net. Returns values(r, p): the net's
+    value of each of network row r's configs of traverser p."""
     dims = [int(x) for x in net.dims]
     w, b = net.w.astype(np.float64), net.b.astype(np.float64)
 
@@ -323,9 +323,6 @@ def numpy_value_under(d, net, root):
         wread = w[at:at + hid]
         pb = b[layers * hid:(layers + priv_layers) * hid]
         bread = b[(layers + priv_layers) * hid]
-    cur = uniform_cur(d)
-    dd = dict(d, root=[np.asarray(root[0]), np.asarray(root[1])])
-    reach = forward_reach(dd, cur)
     cphi = d["cphi"].astype(np.float64).reshape(-1, cfeat)
     rb = len(d["leaf_raw"]) // max(d["rows"], 1)
     pooled = {}
@@ -335,6 +332,35 @@ def numpy_value_under(d, net, root):
             beta = wv / wv.sum() if wv.sum() > 1e-30 else np.full(len(wv), 1.0 / max(len(wv), 1))
             cid = d["leaf_cidx"][d["leaf_coff"][2 * r + p]:d["leaf_coff"][2 * r + p + 1]]
             pooled[(r, p)] = beta @ cphi[cid, 1:1 + pool] if len(cid) else np.zeros(pool)
+
+    def values(r, p):
+        raw = d["leaf_raw"][r * rb:(r + 1) * rb].astype(np.float64) / 255.0
+        h = np.concatenate([pooled[(r, p)], pooled[(r, 1 - p)], [1.0 if p else -1.0], raw])
+        for l in range(layers):
+            h = np.maximum(h @ mats[l] + b[l * hid:(l + 1) * hid], 0.0)
+        cid = d["leaf_cidx"][d["leaf_coff"][2 * r + p]:d["leaf_coff"][2 * r + p + 1]]
+        if dims[0] == 101:
+            keys = cphi[cid, 0].astype(int)
+            return Wh[keys] @ h + b[layers * hid + keys]
+        v = np.zeros(len(cid))  # <w_read * private_tower(features(c)), public_tower(query)> + b_read
+        for x, c in enumerate(cid):
+            f = cphi[c, 1 + pool:]
+            for l in range(priv_layers):
+                f = np.maximum(f @ pmats[l] + pb[l * hid:(l + 1) * hid], 0.0)
+            v[x] = (wread * f) @ h + bread
+        return v
+
+    return values
+
+
+def numpy_value_under(d, net, root):
+    """value_under (search.rs:1851-1871) in float64 under the uniform strategy:
+    propagate, the leaf net, leaf readout (search.rs:1587-1636) and the Value
+    backprop (search.rs:1654-1803)."""
+    cur = uniform_cur(d)
+    dd = dict(d, root=[np.asarray(root[0]), np.asarray(root[1])])
+    reach = forward_reach(dd, cur)
+    leaf_net = numpy_leaf_net(d, net, reach)
     out = []
     for p in (0, 1):
         vals = {}
@@ -342,22 +368,7 @@ def numpy_value_under(d, net, root):
             u = d["terminal_utility"][k] if d["node_player"][leaf] == p else -d["terminal_utility"][k]
             vals[int(leaf)] = np.full(nc_of(d, leaf, p), float(u) * reach[leaf][1 - p].sum())
         for r, leaf in enumerate(d["leaf_rows"]):
-            raw = d["leaf_raw"][r * rb:(r + 1) * rb].astype(np.float64) / 255.0
-            h = np.concatenate([pooled[(r, p)], pooled[(r, 1 - p)], [1.0 if p else -1.0], raw])
-            for l in range(layers):
-                h = np.maximum(h @ mats[l] + b[l * hid:(l + 1) * hid], 0.0)
-            cid = d["leaf_cidx"][d["leaf_coff"][2 * r + p]:d["leaf_coff"][2 * r + p + 1]]
-            if dims[0] == 101:
-                keys = cphi[cid, 0].astype(int)
-                v = Wh[keys] @ h + b[layers * hid + keys]
-            else:  # <w_read * private_tower(features(c)), public_tower(query)> + b_read
-                v = np.zeros(len(cid))
-                for x, c in enumerate(cid):
-                    f = cphi[c, 1 + pool:]
-                    for l in range(priv_layers):
-                        f = np.maximum(f @ pmats[l] + pb[l * hid:(l + 1) * hid], 0.0)
-                    v[x] = (wread * f) @ h + bread
-            vals[int(leaf)] = v * reach[leaf][1 - p].sum()
+            vals[int(leaf)] = leaf_net(r, p) * reach[leaf][1 - p].sum()
         for i in range(d["nodes"] - 1, -1, -1):
             kind, me = int(d["node_kind"][i]), int(d["node_player"][i])
             if kind == 2:
@@ -403,3 +414,84 @@ def test_value_under_matches_float64_restatement(family):
             want = numpy_value_under(d, net, (c0, c1))
             got = o["roots"][r].astype(np.float64)
             assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max() + 1e-7, r
+
+
+@pytest.mark.parametrize("family", ["wave256", "wave512w"])
+def test_leaf_probe_matches_float64_restatement(family):
+    """Pins oracle_leaf_probe (the leaf net's values and the reach masses at the
+    initial reach, the reference for the device's own leaf probe) against the
+    float64 restatement, for both traversers."""
+    net = W.net_for(family)
+    jobs = W.jobs(family, trees=2, seed=23, nodes_lo=30, nodes_hi=70, chance=1, terminal_p=0.15, notrans_p=0.05,
+                  info_median=6.0, info_p99=30.0, info_cap=30, iters=4, nroots=1, whale_frac=0.0)
+    for job in jobs:
+        d = wcj8.decode(job)
+        reach = forward_reach(d, uniform_cur(d))
+        leaf_net = numpy_leaf_net(d, net, reach)
+        for p in (0, 1):
+            want = np.concatenate([leaf_net(r, p) for r in range(d["rows"])])
+            got, mass = O.leaf_probe(job, net, O.NET_F32, p)
+            assert got.shape == want.shape
+            assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max() + 1e-7
+            for mode in (O.NET_F32W, O.NET_F16X):  # near-float32 models stay near float32
+                other, _ = O.leaf_probe(job, net, mode, p)
+                assert np.abs(other - want).max() <= 1e-4 * np.abs(want).max()
+        want_mass = np.array([[reach[leaf][q].sum() for q in (0, 1)] for leaf in d["leaf_rows"]])
+        np.testing.assert_allclose(mass, want_mass, rtol=1e-6, atol=1e-30)
+
+
+def f16_round(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def test_reduced_precision_models_match_numpy():
+    """The MLP's arithmetic models (oracle.c): F16A is f16-rounded operands and
+    activations with a float32 sum in ascending k (zero inputs skipped), the
+    bias added after the sum; F16 / F32W / F16X sum wide (float64) over f16,
+    float32 and hi + lo pair operands."""
+    dims = [101, 64, 32, 2, 10, 8]
+    import warchest_wave as ww
+    net = ww.synth_weights(dims, seed=5)
+    x = ww.synth_features(40, 64, seed=6)
+    keys = np.tile(np.arange(10, dtype=np.uint32), (40, 1))
+    inp, hid, layers, heads = 64, 32, 2, 10
+    w, b = net.w, net.b
+
+    def mats(q):
+        out, at, k = [], 0, inp
+        for _ in range(layers):
+            out.append(q(w[at:at + k * hid]).reshape(k, hid))
+            at += k * hid
+            k = hid
+        return out, q(w[at:at + heads * hid]).reshape(heads, hid)
+
+    # F16A: float32 products and sums, one k at a time
+    M, Wh = mats(f16_round)
+    h = f16_round(x)
+    for l in range(layers):
+        acc = np.zeros((h.shape[0], hid), np.float32)
+        for k in range(h.shape[1]):
+            acc = np.where(h[:, k:k + 1] != 0, acc + h[:, k:k + 1] * M[l][k][None, :], acc).astype(np.float32)
+        h = f16_round(np.maximum(acc + b[l * hid:(l + 1) * hid], 0))
+    acc = np.zeros((h.shape[0], heads), np.float32)
+    for k in range(hid):
+        acc = (acc + h[:, k:k + 1] * Wh[:, k][None, :]).astype(np.float32)
+    want = (acc + b[layers * hid:layers * hid + heads]).astype(np.float32)
+    np.testing.assert_array_equal(O.mlp(x, keys, net, O.NET_F16A), want)
+
+    def wide(q):
+        M, Wh = mats(q)
+        h = q(x).astype(np.float64)
+        for l in range(layers):
+            pre = (h @ M[l].astype(np.float64)).astype(np.float32) + b[l * hid:(l + 1) * hid]
+            h = q(np.maximum(pre, 0)).astype(np.float64)
+        return (h @ Wh.astype(np.float64).T).astype(np.float32) + b[layers * hid:layers * hid + heads]
+
+    def pair(a):
+        hi = f16_round(a)
+        return hi + f16_round(np.asarray(a, np.float32) - hi)
+
+    for mode, q in ((O.NET_F16, f16_round), (O.NET_F32W, lambda a: np.asarray(a, np.float32)), (O.NET_F16X, pair)):
+        got = O.mlp(x, keys, net, mode)
+        ref = wide(q)
+        assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max(), mode

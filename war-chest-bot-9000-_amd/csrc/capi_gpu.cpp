@@ -30,8 +30,40 @@ struct wc_service {
 struct wc_ticket {
     std::shared_ptr<Ticket> t;
 };
+struct wc_inflight {
+    InFlight f;
+};
 
 namespace {
+
+// Runs an entry point's body, turning a C++ exception (std::bad_alloc from a
+// result or job buffer, above all) into a status instead of letting it cross
+// the C boundary.
+template <class F>
+int shielded(const char* what, F&& body) {
+    try {
+        return body();
+    } catch (const std::bad_alloc&) {
+        return fail(WC_ERR_DEVICE, std::string(what) + ": out of host memory");
+    } catch (const std::exception& e) {
+        return fail(WC_ERR_DEVICE, std::string(what) + ": " + e.what());
+    } catch (...) {
+        return fail(WC_ERR_DEVICE, std::string(what) + ": unknown exception");
+    }
+}
+
+void hand_out(std::vector<Result>& out, wc_result** results) {
+    size_t k = 0;
+    try {
+        for (; k < out.size(); k++) {
+            results[k] = new wc_result;
+            results[k]->r = std::move(out[k]);
+        }
+    } catch (...) {
+        for (size_t j = 0; j < k; j++) delete results[j];
+        throw;
+    }
+}
 
 bool read_net(const wc_net_desc* net, NetCopy* out, std::string* err) {
     if (!net || !net->dims || net->ndims == 0 || (!net->w && net->nw) || (!net->b && net->nb)) {
@@ -73,19 +105,20 @@ uint64_t wc_executor_publish(wc_executor* ex, const wc_net_desc* net) {
         fail(WC_ERR_INVALID, "wc_executor_publish: null executor");
         return 0;
     }
-    NetCopy n;
-    std::string err;
-    if (!read_net(net, &n, &err)) {
-        fail(WC_ERR_INVALID, err);
-        return 0;
-    }
-    uint64_t v = ex->ex->publish(n.ns, n.dims, n.w.data(), n.w.size(), n.b.data(), n.b.size(), &err);
-    if (!v) fail(WC_ERR_INVALID, err);
+    uint64_t v = 0;
+    shielded("wc_executor_publish", [&] {
+        NetCopy n;
+        std::string err;
+        if (!read_net(net, &n, &err)) return fail(WC_ERR_INVALID, err);
+        v = ex->ex->publish(n.ns, n.dims, n.w.data(), n.w.size(), n.b.data(), n.b.size(), &err);
+        return v ? WC_OK : fail(WC_ERR_INVALID, err);
+    });
     return v;
 }
 
 int wc_wave_pack(const uint8_t* const* jobs, const size_t* lens, uint32_t njobs, wc_wave** out) {
     if (!jobs || !lens || !out || njobs == 0) return fail(WC_ERR_INVALID, "wc_wave_pack: empty wave");
+    return shielded("wc_wave_pack", [&] {
     std::vector<Job> parsed(njobs);
     std::vector<std::string> errs(njobs);
     std::vector<uint8_t> bad(njobs, 0);
@@ -107,13 +140,11 @@ int wc_wave_pack(const uint8_t* const* jobs, const size_t* lens, uint32_t njobs,
         if (v < 64 || v > (1L << 24)) return fail(WC_ERR_INVALID, "WC_UNIT_SLOTS out of range [64, 2^24]");
         slots = (uint32_t)v;
     }
-    auto* w = new wc_wave;
-    if (!pack_wave(std::move(parsed), &w->host, &err, slots)) {
-        delete w;
-        return fail(WC_ERR_INVALID, err);
-    }
-    *out = w;
+    std::unique_ptr<wc_wave> w(new wc_wave);
+    if (!pack_wave(std::move(parsed), &w->host, &err, slots)) return fail(WC_ERR_INVALID, err);
+    *out = w.release();
     return WC_OK;
+    });
 }
 
 void wc_wave_free(wc_wave* w) { delete w; }
@@ -168,6 +199,7 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
         CfrBytes cb = cfr_bytes_per_iter(h, p);
         s->cfr_bytes_per_iter[p] = cb.total();
         for (int k = 0; k < 4; k++) s->cfr_bytes_by_kernel[p][k] = cb.part[k];
+        s->leaf_input_bytes[p] = leaf_input_bytes(h, p, 2);
     }
     const NetShape& ns = h.net;
     if (ns.kind == MODEL_TWO_TOWER) {
@@ -248,14 +280,52 @@ int wc_value_net_plan(const uint32_t* cols, uint32_t nrb, uint32_t heads, uint32
 
 int wc_solve_wave(wc_executor* ex, wc_wave* w, uint64_t version, wc_result** results) {
     if (!ex || !w || !results) return fail(WC_ERR_INVALID, "wc_solve_wave: null argument");
-    std::vector<Result> out;
-    std::string err;
-    if (!ex->ex->solve(w->host, version, &out, &err)) return fail(WC_ERR_DEVICE, err);
-    for (size_t k = 0; k < out.size(); k++) {
-        results[k] = new wc_result;
-        results[k]->r = std::move(out[k]);
-    }
-    return WC_OK;
+    return shielded("wc_solve_wave", [&] {
+        std::vector<Result> out;
+        std::string err;
+        if (!ex->ex->solve(w->host, version, &out, &err)) return fail(WC_ERR_DEVICE, err);
+        hand_out(out, results);
+        return WC_OK;
+    });
+}
+
+int wc_launch(wc_executor* ex, wc_wave* w, uint64_t version, wc_inflight** out) {
+    if (!ex || !w || !out) return fail(WC_ERR_INVALID, "wc_launch: null argument");
+    return shielded("wc_launch", [&] {
+        std::unique_ptr<wc_inflight> f(new wc_inflight);
+        std::string err;
+        if (!ex->ex->launch(w->host, version, &f->f, &err)) return fail(WC_ERR_DEVICE, err);
+        *out = f.release();
+        return WC_OK;
+    });
+}
+
+int wc_inflight_ready(const wc_executor* ex, const wc_inflight* f) { return ex && f && ex->ex->ready(f->f) ? 1 : 0; }
+
+int wc_collect(wc_executor* ex, wc_inflight* f, wc_result** results) {
+    if (!ex || !f || !results) return fail(WC_ERR_INVALID, "wc_collect: null argument");
+    std::unique_ptr<wc_inflight> own(f);
+    return shielded("wc_collect", [&] {
+        std::vector<Result> out;
+        std::string err;
+        if (!ex->ex->collect(&own->f, &out, &err)) return fail(WC_ERR_DEVICE, err);
+        hand_out(out, results);
+        return WC_OK;
+    });
+}
+
+int wc_wave_leaf_probe(wc_executor* ex, wc_wave* w, uint64_t version, int traverser, float* values, size_t cap,
+                       size_t* count, float* mass) {
+    if (!ex || !w || !count || (cap && !values)) return fail(WC_ERR_INVALID, "wc_wave_leaf_probe: null argument");
+    return shielded("wc_wave_leaf_probe", [&] {
+        std::vector<float> v, m;
+        std::string err;
+        if (!ex->ex->leaf_probe(w->host, version, traverser, &v, &m, &err)) return fail(WC_ERR_DEVICE, err);
+        *count = v.size();
+        if (v.size() <= cap) std::copy(v.begin(), v.end(), values);
+        if (mass) std::copy(m.begin(), m.end(), mass);
+        return WC_OK;
+    });
 }
 
 int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup, uint32_t reps, double* wave_ms,
@@ -263,8 +333,12 @@ int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup,
     if (!ex || !w || !wave_ms) return fail(WC_ERR_INVALID, "wc_time_wave: null argument");
     ScheduleTimes prof;
     std::string err;
-    if (!ex->ex->time_wave(w->host, version, warmup, reps, wave_ms, kernel_ms ? &prof : nullptr, &err))
-        return fail(WC_ERR_DEVICE, err);
+    const int rc = shielded("wc_time_wave", [&] {
+        return ex->ex->time_wave(w->host, version, warmup, reps, wave_ms, kernel_ms ? &prof : nullptr, &err)
+                   ? WC_OK
+                   : fail(WC_ERR_DEVICE, err);
+    });
+    if (rc != WC_OK) return rc;
     if (kernel_ms) {
         kernel_ms[0] = prof.cfr;
         kernel_ms[1] = prof.mlp;
@@ -274,15 +348,17 @@ int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup,
         kernel_ms[5] = prof.back_mean;
         kernel_ms[6] = prof.top_mean;
         kernel_ms[7] = prof.reach_mean;
+        kernel_ms[8] = prof.graph_build_ms;
     }
     return WC_OK;
 }
 
 int wc_mlp_forward(wc_executor* ex, uint64_t version, uint32_t rows, const float* x, float* out) {
     if (!ex || !x || !out) return fail(WC_ERR_INVALID, "wc_mlp_forward: null argument");
-    std::string err;
-    if (!ex->ex->mlp_forward(version, rows, x, out, &err)) return fail(WC_ERR_DEVICE, err);
-    return WC_OK;
+    return shielded("wc_mlp_forward", [&] {
+        std::string err;
+        return ex->ex->mlp_forward(version, rows, x, out, &err) ? WC_OK : fail(WC_ERR_DEVICE, err);
+    });
 }
 
 int wc_time_mlp(wc_executor* ex, uint64_t version, uint32_t rows, const float* x, uint32_t reps, double* chain_ms,
@@ -290,8 +366,12 @@ int wc_time_mlp(wc_executor* ex, uint64_t version, uint32_t rows, const float* x
     if (!ex || !x || !chain_ms) return fail(WC_ERR_INVALID, "wc_time_mlp: null argument");
     std::string err;
     std::vector<double> layers;
-    if (!ex->ex->time_mlp(version, rows, x, reps, chain_ms, layer_ms ? &layers : nullptr, &err))
-        return fail(WC_ERR_DEVICE, err);
+    const int rc = shielded("wc_time_mlp", [&] {
+        return ex->ex->time_mlp(version, rows, x, reps, chain_ms, layer_ms ? &layers : nullptr, &err)
+                   ? WC_OK
+                   : fail(WC_ERR_DEVICE, err);
+    });
+    if (rc != WC_OK) return rc;
     if (layer_ms)
         for (size_t k = 0; k < layers.size() && k < 8; k++) layer_ms[k] = layers[k];
     return WC_OK;
@@ -311,6 +391,9 @@ int wc_service_create(int device, const wc_net_desc* net, int precision, const w
         if (opts->wave_jobs) o.wave_jobs = opts->wave_jobs;
         if (opts->wave_rows) o.wave_rows = opts->wave_rows;
         o.window_us = opts->window_us;
+        if (opts->whale_lanes) o.whale_lanes = opts->whale_lanes;
+        o.class_shift = opts->class_shift;
+        if (opts->route_unit) o.route_unit = opts->route_unit;
     }
     try {
         auto* s = new wc_service;
@@ -333,14 +416,14 @@ uint64_t wc_set_weights(wc_service* svc, const wc_net_desc* net) {
         fail(WC_ERR_INVALID, "wc_set_weights: null service");
         return 0;
     }
-    NetCopy n;
-    std::string err;
-    if (!read_net(net, &n, &err)) {
-        fail(WC_ERR_INVALID, err);
-        return 0;
-    }
-    uint64_t v = svc->svc->set_weights(std::move(n), &err);
-    if (!v) fail(WC_ERR_GONE, err);
+    uint64_t v = 0;
+    shielded("wc_set_weights", [&] {
+        NetCopy n;
+        std::string err;
+        if (!read_net(net, &n, &err)) return fail(WC_ERR_INVALID, err);
+        v = svc->svc->set_weights(std::move(n), &err);
+        return v ? WC_OK : fail(WC_ERR_GONE, err);
+    });
     return v;
 }
 
@@ -348,30 +431,73 @@ uint64_t wc_queued_work(wc_service* svc) { return svc ? svc->svc->queued_work() 
 
 int wc_submit(wc_service* svc, const uint8_t* job, size_t len, uint64_t tag, wc_ticket** out) {
     if (!svc || !job || !out) return fail(WC_ERR_INVALID, "wc_submit: null argument");
-    std::shared_ptr<Ticket> t;
-    std::string err;
-    if (!svc->svc->submit(job, len, tag, &t, &err))
-        return fail(err == "GPU wave executor is gone" ? WC_ERR_GONE : WC_ERR_INVALID, err);
-    *out = new wc_ticket{t};
-    return WC_OK;
+    return shielded("wc_submit", [&] {
+        std::shared_ptr<Ticket> t;
+        std::string err;
+        if (!svc->svc->submit(job, len, tag, &t, &err))
+            return fail(err == "GPU wave executor is gone" ? WC_ERR_GONE : WC_ERR_INVALID, err);
+        *out = new wc_ticket{t};
+        return WC_OK;
+    });
 }
 
 int wc_wait(wc_ticket* t, wc_result** out) {
     if (!t || !out) return fail(WC_ERR_INVALID, "wc_wait: null argument");
     std::shared_ptr<Ticket> tk = t->t;
     delete t;
-    std::unique_lock<std::mutex> lk(tk->mu);
-    tk->cv.wait(lk, [&] { return tk->done; });
-    if (tk->rc != 0) return fail(tk->rc, tk->err);
-    *out = new wc_result;
-    (*out)->r = std::move(tk->result);
-    return WC_OK;
+    return shielded("wc_wait", [&] {
+        std::unique_lock<std::mutex> lk(tk->mu);
+        tk->cv.wait(lk, [&] { return tk->done; });
+        if (tk->rc != 0) return fail(tk->rc, tk->err);
+        std::unique_ptr<wc_result> r(new wc_result);
+        r->r = std::move(tk->result);
+        *out = r.release();
+        return WC_OK;
+    });
 }
 
 int wc_poll(const wc_ticket* t) {
     if (!t) return 0;
     std::lock_guard<std::mutex> lk(t->t->mu);
     return t->t->done ? 1 : 0;
+}
+
+void wc_ticket_free(wc_ticket* t) { delete t; }
+
+int wc_service_stats(wc_service* svc, uint64_t* waves, uint64_t* guarded_routes) {
+    if (!svc) return fail(WC_ERR_INVALID, "wc_service_stats: null service");
+    if (waves) *waves = svc->svc->waves();
+    if (guarded_routes) *guarded_routes = svc->svc->guarded_routes();
+    return WC_OK;
+}
+
+int wc_job_work(const uint8_t* job, size_t len, int precision, uint64_t route_unit, uint32_t class_shift,
+                wc_work_vector* out, uint64_t* cost, uint32_t* cls) {
+    if (!job || !out) return fail(WC_ERR_INVALID, "wc_job_work: null argument");
+    if (precision < WC_PRECISE || precision > WC_F16X) return fail(WC_ERR_INVALID, "wc_job_work: unknown precision");
+    return shielded("wc_job_work", [&] {
+        Job j;
+        std::string err;
+        if (!from_bytes(job, len, &j, &err)) return fail(WC_ERR_INVALID, err);
+        const uint64_t unit = route_unit ? route_unit : WorkVector::ROUTE_UNIT;
+        const WorkVector w = work_vector(j, precision);
+        std::memset(out, 0, sizeof *out);
+        out->network_rows = w.network_rows;
+        out->legal_cells = w.legal_cells;
+        out->reach_slots = w.reach_slots;
+        out->reverse_nonzeros = w.reverse_nonzeros;
+        out->table_bytes = w.table_bytes;
+        out->mutable_bytes = w.mutable_bytes;
+        out->carried_output_bytes = w.carried_output_bytes;
+        out->levels = w.levels;
+        out->reserved_bytes = w.reserved_bytes();
+        out->exclusive_route = w.requires_exclusive_route(unit);
+        out->arena_guard_route = w.requires_arena_guard_route(unit);
+        out->card_exclusive_route = w.requires_card_exclusive_route(unit);
+        if (cost) *cost = job_cost(w, j.meta.iters);
+        if (cls) *cls = cost_class(w, class_shift, unit);
+        return WC_OK;
+    });
 }
 
 uint64_t wc_result_tag(const wc_result* r) { return r ? r->r.tag : 0; }
@@ -399,6 +525,13 @@ const uint16_t* wc_result_carries(const wc_result* r, uint32_t* slots, uint32_t*
     if (slots) *slots = r->r.slots;
     if (snapshot_configs) *snapshot_configs = r->r.snapshot_configs;
     return r->r.carries.data();
+}
+
+int wc_result_routes(const wc_result* r, int* oversize_route, int* card_exclusive_route) {
+    if (!r) return fail(WC_ERR_INVALID, "wc_result_routes: null result");
+    if (oversize_route) *oversize_route = r->r.oversize_route ? 1 : 0;
+    if (card_exclusive_route) *card_exclusive_route = r->r.card_exclusive_route ? 1 : 0;
+    return WC_OK;
 }
 
 void wc_result_free(wc_result* r) { delete r; }

@@ -4,9 +4,12 @@
 #include "executor.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <thread>
+#include <unordered_map>
 
 #include "../../include/wc_wave.h"
 
@@ -90,19 +93,32 @@ Executor::Executor(int device, int precision) : device_(device), precision_(prec
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
         cus_ = (uint32_t)cus;
+    for (Slot& sl : slots_)
+        if (hipEventCreateWithFlags(&sl.uploaded, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&sl.done, hipEventDisableTiming) != hipSuccess) {
+            err_ = "cannot create the executor's events";
+            return;
+        }
+    if (const char* env = std::getenv("WC_CHAIN_SPLIT")) split_ = std::strcmp(env, "0") != 0;
+    if (const char* env = std::getenv("WC_GRAPH")) graph_ = std::strcmp(env, "1") == 0;
     ok_ = true;
 }
 
 Executor::~Executor() {
-    if (!ok_) return;
+    if (!stream_) return;
     hipSetDevice(device_);
     hipStreamSynchronize(stream_);
     for (auto& kv : banks_) hipFree(kv.second.mem);
     hipFree(table_);
     hipFree(arena_);
     hipFree(mlp_);
-    if (pin_) hipHostFree(pin_);
-    if (res_pin_) hipHostFree(res_pin_);
+    for (Slot& sl : slots_) {
+        if (sl.pin) hipHostFree(sl.pin);
+        if (sl.res) hipHostFree(sl.res);
+        if (sl.uploaded) hipEventDestroy(sl.uploaded);
+        if (sl.done) hipEventDestroy(sl.done);
+        if (sl.exec) hipGraphExecDestroy(sl.exec);
+    }
     hipStreamDestroy(stream_);
 }
 
@@ -285,7 +301,7 @@ void Executor::retain_from(uint64_t oldest) {
     }
 }
 
-bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) {
+bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std::string* err) {
     const NetShape& ns = bank.ns;
     if (w.net.kind != ns.kind || w.net.in != ns.in || w.net.hidden != ns.hidden || w.net.pool != ns.pool ||
         w.net.heads != ns.heads || w.net.layers != ns.layers || w.net.priv_in != ns.priv_in ||
@@ -353,9 +369,13 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
         o.tr[p] = blob.put(w.top_reach_rec[p]);
     }
     if (!ensure(&table_, &table_cap_, blob.size, err)) return false;
-    if (!ensure_pinned(&pin_, &pin_cap_, blob.size, err)) return false;
-    blob.copy_to(pin_);
-    HIP_TRY(hipMemcpyAsync(table_, pin_, blob.size, hipMemcpyHostToDevice, stream_));
+    Slot& sl = slots_[slot];
+    if (sl.recorded) HIP_TRY(hipEventSynchronize(sl.uploaded));  // the slot's last upload has left its staging
+    if (!ensure_pinned(&sl.pin, &sl.pin_cap, blob.size, err)) return false;
+    blob.copy_to(sl.pin);
+    HIP_TRY(hipMemcpyAsync(table_, sl.pin, blob.size, hipMemcpyHostToDevice, stream_));
+    HIP_TRY(hipEventRecord(sl.uploaded, stream_));
+    sl.recorded = true;
 
     // Mutable arena.
     const size_t cells = std::max<uint32_t>(w.ncells, 1), rl = std::max<uint32_t>(w.reach_len, 1),
@@ -388,7 +408,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
            m_out = mtake(tower ? w.tower_len * 4 : rows * ns.heads * 4);
     // The fused net's first-layer product over the fixed query columns, when
     // the pooled columns are whole 32-column k steps ahead of them.
-    const bool split = !tower && (precision_ == WC_F16 || precision_ == WC_BF16) &&
+    const bool split = split_ && !tower && (precision_ == WC_F16 || precision_ == WC_BF16) &&
                        chain_fits(ns.in, ns.hidden, ns.layers) && ns.pool > 0 && ns.in > 2 * ns.pool &&
                        (2 * ns.pool) % 32 == 0;
     size_t m_s0 = split ? mtake(prow * ns.hidden * 4) : 0, m_s1 = split ? mtake(prow * ns.hidden * 4) : 0;
@@ -493,7 +513,6 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, std::string* err) 
     rows_ = w.rows();
     launch_query_static(d, precision_, Xq_[0], Xq_[1], stream_);
     HIP_TRY(hipGetLastError());
-    HIP_TRY(hipStreamSynchronize(stream_));
     return true;
 }
 
@@ -596,6 +615,69 @@ void Executor::run_tower(const NetBank& bank, uint32_t rows, int traverser) {
     launch_tower_head(dev_, traverser, precision_, in, ns.hidden, F_, bank.bread, head_out_, stream_);
 }
 
+const NetBank* Executor::bank_of(uint64_t version, std::string* err) const {
+    auto it = banks_.find(version);
+    if (it == banks_.end()) {
+        *err = "GPU weight version " + std::to_string(version) + " is unavailable";
+        return nullptr;
+    }
+    return &it->second;
+}
+
+void Executor::leaf_net(const NetBank& bank, int q) {
+    if (bank.ns.kind == MODEL_TWO_TOWER)
+        run_tower(bank, dev_.rows, q);
+    else
+        run_mlp(bank, dev_.rows, Xq_[q], nullptr, head_tile_n_, chain_plan_[q], chain_npass_[q], S_[q]);
+}
+
+// Top regions, one depth per launch: values bottom-up.
+void Executor::top_back(const WaveHost& w, int p, int mode, float da, float db, float pr) {
+    for (uint32_t l = w.top_levels; l-- > 0;) {
+        uint32_t b = w.top_back_lvl[p][l], e = w.top_back_lvl[p][l + 1];
+        launch_back_rows(dev_, top_back_dev_[p] + b, e - b, p, mode, da, db, pr, stream_);
+    }
+}
+
+// Top regions' reach, one depth per launch, top-down; p < 0: both players.
+void Executor::top_reach(const WaveHost& w, int p, float* reach, const float* strat) {
+    for (uint32_t l = 1; l < w.top_levels; l++) {
+        uint32_t b0 = w.top_reach_lvl[0][l], n0 = p == 1 ? 0 : w.top_reach_lvl[0][l + 1] - b0;
+        uint32_t b1 = w.top_reach_lvl[1][l], n1 = p == 0 ? 0 : w.top_reach_lvl[1][l + 1] - b1;
+        launch_reach_rows(dev_, top_reach_dev_[0] + b0, n0, top_reach_dev_[1] + b1, n1, reach, strat, stream_);
+    }
+}
+
+// Both players' reach under a fixed strategy: tops first, then their subtrees.
+void Executor::reach_both(const WaveHost& w, float* reach, const float* strat) {
+    top_reach(w, -1, reach, strat);
+    launch_reach(dev_, 0, w.nsub, reach, strat, -1, stream_);
+}
+
+// The first layer's product over each traverser's fixed query columns, under
+// this bank (when the fused net runs with the split).
+void Executor::static_products(const NetBank& bank) {
+    if (!S_[0]) return;
+    ChainNet net = chain_net(bank);
+    net.dsteps = 2 * bank.ns.pool / 32;  // the pooled columns come first; the rest are fixed
+    for (int q = 0; q < 2; q++) launch_chain_static(precision_, net, Xq_[q], S_[q], chain_plan_[q], chain_npass_[q], stream_);
+}
+
+// Solver::new on the device (engine/src/search.rs:826-888): uniform strategy,
+// zero regret, reach from the root beliefs, the seeded average sums, the first
+// carries, and both players' leaf inputs.
+void Executor::init_state(const WaveHost& w) {
+    const WaveDev& d = dev_;
+    hipStream_t s = stream_;
+    launch_zero(d.regret, w.ncells, s);
+    launch_init_strategy(d, s);
+    launch_seed_reach(d, d.reach, w.reach_len, -1, s);
+    reach_both(w, d.reach, d.cur);
+    launch_seed_sum(d, s);
+    if (w.carry_slots) launch_gather_carry(d, d.reach, 0, s);
+    launch_pool(d, -1, precision_, Xq_[0], Xq_[1], s);
+}
+
 void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTimes* prof) {
     const WaveDev& d = dev_;
     hipStream_t s = stream_;
@@ -617,60 +699,25 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         hipEventRecord(start, s);
     }
     const bool tower = bank.ns.kind == MODEL_TWO_TOWER;
-    auto mlp = [&](int q) {
-        if (tower)
-            run_tower(bank, d.rows, q);
-        else
-            run_mlp(bank, d.rows, Xq_[q], nullptr, head_tile_n_, chain_plan_[q], chain_npass_[q], S_[q]);
-        mark(C_MLP);
-    };
-    // Top regions, one depth per launch: values bottom-up, reach top-down.
-    auto top_back = [&](int p, int mode, float da, float db, float pr) {
-        for (uint32_t l = w.top_levels; l-- > 0;) {
-            uint32_t b = w.top_back_lvl[p][l], e = w.top_back_lvl[p][l + 1];
-            launch_back_rows(d, top_back_dev_[p] + b, e - b, p, mode, da, db, pr, s);
-        }
-    };
-    auto top_reach = [&](int p, float* reach, const float* strat) {  // p < 0: both players
-        for (uint32_t l = 1; l < w.top_levels; l++) {
-            uint32_t b0 = w.top_reach_lvl[0][l], n0 = p == 1 ? 0 : w.top_reach_lvl[0][l + 1] - b0;
-            uint32_t b1 = w.top_reach_lvl[1][l], n1 = p == 0 ? 0 : w.top_reach_lvl[1][l + 1] - b1;
-            launch_reach_rows(d, top_reach_dev_[0] + b0, n0, top_reach_dev_[1] + b1, n1, reach, strat, s);
-        }
-    };
-    // Both players' reach under a fixed strategy: tops first, then their subtrees.
-    auto reach_both = [&](float* reach, const float* strat) {
-        top_reach(-1, reach, strat);
-        launch_reach(d, 0, nsub, reach, strat, -1, s);
-    };
-
     if (tower) run_tower_private(bank);  // F for this wave's configs under this bank
-    if (S_[0]) {  // the first layer over the fixed query columns, under this bank
-        ChainNet net = chain_net(bank);
-        net.dsteps = 2 * bank.ns.pool / 32;  // the pooled columns come first; the rest are fixed
-        for (int q = 0; q < 2; q++)
-            launch_chain_static(precision_, net, Xq_[q], S_[q], chain_plan_[q], chain_npass_[q], s);
+    if (S_[0]) {
+        static_products(bank);
         mark(C_MLP);
     }
-    launch_zero(d.regret, w.ncells, s);
-    launch_init_strategy(d, s);
-    launch_seed_reach(d, d.reach, w.reach_len, -1, s);
-    reach_both(d.reach, d.cur);
-    launch_seed_sum(d, s);
-    if (w.carry_slots) launch_gather_carry(d, d.reach, 0, s);
-    launch_pool(d, -1, precision_, Xq_[0], Xq_[1], s);
+    init_state(w);
     mark(C_OTHER);
     if (m.iters == 0) launch_normalize(d, 0, 0, s);
     for (uint32_t t = 0; t < m.iters; t++) {
         const int p = (int)(t & 1);
-        mlp(p);
+        leaf_net(bank, p);
+        mark(C_MLP);
         const float mm = (float)(t / 2 + 1);
         const float da = cfr_factor(mm, m.cfr.alpha), db = cfr_factor(mm, m.cfr.beta);
         const float ds = std::pow(mm / (mm + 1.0f), m.cfr.gamma);
         launch_sweep(d, 0, nsub, head_out_, bank.ns.heads, p, MODE_REGRET, da, db, m.cfr.predict, s);
         mark(C_BACK);
-        top_back(p, MODE_REGRET, da, db, m.cfr.predict);
-        top_reach(p, d.reach, d.cur);
+        top_back(w, p, MODE_REGRET, da, db, m.cfr.predict);
+        top_reach(w, p, d.reach, d.cur);
         mark(C_TOP);
         launch_reach(d, 0, nsub, d.reach, d.cur, p, s);
         mark(C_REACH);
@@ -683,7 +730,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
             launch_normalize(d, 1, done >= 2 ? 1 : 0, s);
             if (m.snapshots && si + 1 < m.snap_iters.size()) {
                 launch_seed_reach(d, d.snap_reach, w.reach_len, -1, s);
-                reach_both(d.snap_reach, d.snap);
+                reach_both(w, d.snap_reach, d.snap);
                 launch_gather_carry(d, d.snap_reach, (int)si, s);
             }
             mark(C_OTHER);
@@ -692,14 +739,14 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     // Phase 2: root values under the final average for every carried root.
     for (uint32_t root = 0; root < w.nroots_max; root++) {
         launch_seed_reach(d, d.reach, w.reach_len, (int)root, s);
-        reach_both(d.reach, d.snap);
+        reach_both(w, d.reach, d.snap);
         mark(C_OTHER);
         launch_pool(d, -1, precision_, Xq_[0], Xq_[1], s);
         mark(C_LEAF);
         for (int p = 0; p < 2; p++) {
-            mlp(p);
+            leaf_net(bank, p);
             launch_sweep(d, 0, nsub, head_out_, bank.ns.heads, p, MODE_VALUE, 0.0f, 0.0f, 0.0f, s);
-            top_back(p, MODE_VALUE, 0.0f, 0.0f, 0.0f);
+            top_back(w, p, MODE_VALUE, 0.0f, 0.0f, 0.0f);
             launch_collect_root(d, (int)root, p, s);
             mark(C_OTHER);
         }
@@ -734,48 +781,201 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     }
 }
 
-bool Executor::solve(const WaveHost& w, uint64_t version, std::vector<Result>* out, std::string* err) {
-    auto it = banks_.find(version);
-    if (it == banks_.end()) {
-        *err = "GPU weight version " + std::to_string(version) + " is unavailable";
+bool Executor::capture(const WaveHost& w, const NetBank& bank, hipGraphExec_t* exec, double* build_ms,
+                       std::string* err) {
+    const auto t0 = std::chrono::steady_clock::now();
+    HIP_TRY(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    run_schedule(w, bank, nullptr);
+    hipGraph_t g = nullptr;
+    HIP_TRY(hipStreamEndCapture(stream_, &g));
+    const hipError_t e = hipGraphInstantiate(exec, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        *err = std::string("hipGraphInstantiate: ") + hipGetErrorString(e);
         return false;
     }
-    if (!upload(w, it->second, err)) return false;
-    run_schedule(w, it->second, nullptr);
+    if (build_ms)
+        *build_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    return true;
+}
+
+bool Executor::launch(const WaveHost& w, uint64_t version, InFlight* f, std::string* err) {
+    const NetBank* bank = bank_of(version, err);
+    if (!bank) return false;
+    if (f->live) {
+        *err = "this in-flight record holds a wave that was not collected";
+        return false;
+    }
+    // The lowest free slot: a caller that collects each wave before launching
+    // the next keeps reusing one slot's pinned buffers.
+    uint32_t k = MAX_IN_FLIGHT;
+    for (uint32_t i = 0; i < MAX_IN_FLIGHT; i++)
+        if (!slots_[i].busy) {
+            k = i;
+            break;
+        }
+    if (k == MAX_IN_FLIGHT) {
+        *err = "the executor already has " + std::to_string(MAX_IN_FLIGHT) + " waves in flight; collect one first";
+        return false;
+    }
+    Slot& sl = slots_[k];
+    if (!upload(w, *bank, k, err)) return false;
+    if (sl.exec) {
+        HIP_TRY(hipGraphExecDestroy(sl.exec));
+        sl.exec = nullptr;
+    }
+    if (graph_) {
+        if (!capture(w, *bank, &sl.exec, nullptr, err)) return false;
+        HIP_TRY(hipGraphLaunch(sl.exec, stream_));
+    } else {
+        run_schedule(w, *bank, nullptr);
+    }
     HIP_TRY(hipGetLastError());
-    // Collect (Harvest::unpack): the outputs into pinned memory, then per-job
-    // slices back to solve-local indices.
+    // The outputs go into the slot's pinned landing, in the stream after the schedule.
     const size_t ns_ = w.ncells, nr = w.root_values_len, nc = size_t(w.carry_slots) * w.snapshot_configs;
     const size_t o_roots = align256(ns_ * 4), o_carry = o_roots + align256(nr * 4);
-    if (!ensure_pinned(&res_pin_, &res_pin_cap_, o_carry + nc * 2 + 4, err)) return false;
-    const float* strat = (const float*)res_pin_;
-    const float* roots = (const float*)(res_pin_ + o_roots);
-    const uint16_t* carry = (const uint16_t*)(res_pin_ + o_carry);
-    if (ns_) HIP_TRY(hipMemcpyAsync(res_pin_, dev_.snap, ns_ * 4, hipMemcpyDeviceToHost, stream_));
-    if (nr) HIP_TRY(hipMemcpyAsync(res_pin_ + o_roots, dev_.root_values, nr * 4, hipMemcpyDeviceToHost, stream_));
-    if (nc) HIP_TRY(hipMemcpyAsync(res_pin_ + o_carry, dev_.carry, nc * 2, hipMemcpyDeviceToHost, stream_));
+    if (!ensure_pinned(&sl.res, &sl.res_cap, o_carry + nc * 2 + 4, err)) return false;
+    if (ns_) HIP_TRY(hipMemcpyAsync(sl.res, dev_.snap, ns_ * 4, hipMemcpyDeviceToHost, stream_));
+    if (nr) HIP_TRY(hipMemcpyAsync(sl.res + o_roots, dev_.root_values, nr * 4, hipMemcpyDeviceToHost, stream_));
+    if (nc) HIP_TRY(hipMemcpyAsync(sl.res + o_carry, dev_.carry, nc * 2, hipMemcpyDeviceToHost, stream_));
+    HIP_TRY(hipEventRecord(sl.done, stream_));
+    f->slot = k;
+    f->version = version;
+    f->ncells = ns_;
+    f->nroots = nr;
+    f->carry_slots = w.carry_slots;
+    f->snapshot_configs = w.snapshot_configs;
+    f->o_roots = o_roots;
+    f->o_carry = o_carry;
+    f->jobs.resize(w.jobs.size());
+    for (size_t j = 0; j < w.jobs.size(); j++) {
+        const TreeDev& t = w.trees[j];
+        JobSlice& js = f->jobs[j];
+        js.ncells = w.jobs[j].t.ncells;
+        js.nroots = t.nroots;
+        js.n0 = t.n0;
+        js.n1 = t.n1;
+        js.root_value0 = t.root_value0;
+        js.snapshot_configs = w.jobs[j].t.snapshot_configs();
+    }
+    sl.busy = true;
+    in_flight_++;
+    f->live = true;
+    return true;
+}
+
+bool Executor::trim(std::string* err) {
+    if (in_flight_) {
+        *err = "cannot trim with waves in flight";
+        return false;
+    }
+    HIP_TRY(hipSetDevice(device_));
     HIP_TRY(hipStreamSynchronize(stream_));
+    HIP_TRY(hipFree(table_));
+    HIP_TRY(hipFree(arena_));
+    HIP_TRY(hipFree(mlp_));
+    table_ = arena_ = mlp_ = nullptr;
+    table_cap_ = arena_cap_ = mlp_cap_ = 0;
+    for (Slot& sl : slots_) {
+        if (sl.pin) HIP_TRY(hipHostFree(sl.pin));
+        if (sl.res) HIP_TRY(hipHostFree(sl.res));
+        sl.pin = sl.res = nullptr;
+        sl.pin_cap = sl.res_cap = 0;
+    }
+    rows_ = 0;
+    return true;
+}
+
+bool Executor::ready(const InFlight& f) const {
+    return f.live && hipEventQuery(slots_[f.slot].done) == hipSuccess;
+}
+
+// Collect (Harvest::unpack, engine/src/gpu/device.rs:759-831): wait for the
+// wave, then split its outputs back into per-job, solve-local results.
+bool Executor::collect(InFlight* f, std::vector<Result>* out, std::string* err) {
+    if (!f->live) {
+        *err = "nothing in flight to collect";
+        return false;
+    }
+    Slot& sl = slots_[f->slot];
+    f->live = false;
+    sl.busy = false;
+    in_flight_--;
+    HIP_TRY(hipSetDevice(device_));
+    HIP_TRY(hipEventSynchronize(sl.done));
+    HIP_TRY(hipGetLastError());
+    const float* strat = (const float*)sl.res;
+    const float* roots = (const float*)(sl.res + f->o_roots);
+    const uint16_t* carry = (const uint16_t*)(sl.res + f->o_carry);
     out->clear();
     uint32_t cell0 = 0, cfg0 = 0;
-    for (size_t k = 0; k < w.jobs.size(); k++) {
-        const Job& j = w.jobs[k];
-        const TreeDev& t = w.trees[k];
+    for (const JobSlice& j : f->jobs) {
         Result r;
-        r.weight_version = version;
-        r.strategy.assign(strat + cell0, strat + cell0 + j.t.ncells);
-        r.nroots = t.nroots;
-        r.n0 = t.n0;
-        r.n1 = t.n1;
-        r.root_values.assign(roots + t.root_value0, roots + t.root_value0 + t.nroots * (t.n0 + t.n1));
-        r.slots = w.carry_slots;
-        r.snapshot_configs = j.t.snapshot_configs();
+        r.weight_version = f->version;
+        r.strategy.assign(strat + cell0, strat + cell0 + j.ncells);
+        r.nroots = j.nroots;
+        r.n0 = j.n0;
+        r.n1 = j.n1;
+        r.root_values.assign(roots + j.root_value0, roots + j.root_value0 + j.nroots * (j.n0 + j.n1));
+        r.slots = (uint32_t)f->carry_slots;
+        r.snapshot_configs = j.snapshot_configs;
         r.carries.resize(size_t(r.slots) * r.snapshot_configs);
-        for (uint32_t sl = 0; sl < r.slots; sl++)
-            std::memcpy(r.carries.data() + size_t(sl) * r.snapshot_configs,
-                        carry + size_t(sl) * w.snapshot_configs + cfg0, size_t(r.snapshot_configs) * 2);
-        cell0 += j.t.ncells;
+        for (uint32_t s = 0; s < r.slots; s++)
+            std::memcpy(r.carries.data() + size_t(s) * r.snapshot_configs,
+                        carry + size_t(s) * f->snapshot_configs + cfg0, size_t(r.snapshot_configs) * 2);
+        cell0 += j.ncells;
         cfg0 += r.snapshot_configs;
         out->push_back(std::move(r));
+    }
+    return true;
+}
+
+bool Executor::solve(const WaveHost& w, uint64_t version, std::vector<Result>* out, std::string* err) {
+    InFlight f;
+    if (!launch(w, version, &f, err)) return false;
+    return collect(&f, out, err);
+}
+
+bool Executor::leaf_probe(const WaveHost& w, uint64_t version, int traverser, std::vector<float>* values,
+                          std::vector<float>* mass, std::string* err) {
+    const NetBank* bank = bank_of(version, err);
+    if (!bank) return false;
+    if (traverser < 0 || traverser > 1) {
+        *err = "the traverser must be 0 or 1";
+        return false;
+    }
+    if (in_flight_) {
+        *err = "collect the launched waves before probing";
+        return false;
+    }
+    if (!upload(w, *bank, 0, err)) return false;
+    if (bank->ns.kind == MODEL_TWO_TOWER) run_tower_private(*bank);
+    static_products(*bank);
+    init_state(w);
+    leaf_net(*bank, traverser);
+    HIP_TRY(hipGetLastError());
+    const size_t nout = bank->ns.kind == MODEL_TWO_TOWER ? w.tower_len : size_t(w.rows()) * bank->ns.heads;
+    std::vector<float> head(nout);
+    mass->assign(size_t(w.rows()) * 2, 0.0f);
+    if (nout) HIP_TRY(hipMemcpyAsync(head.data(), head_out_, nout * 4, hipMemcpyDeviceToHost, stream_));
+    if (w.rows()) HIP_TRY(hipMemcpyAsync(mass->data(), dev_.mass, mass->size() * 4, hipMemcpyDeviceToHost, stream_));
+    HIP_TRY(hipStreamSynchronize(stream_));
+    // Each network-leaf value slot's net value, by the records the sweep reads.
+    const int p = traverser;
+    std::unordered_map<uint32_t, uint32_t> head_of;
+    head_of.reserve(w.leaf_rec[p].size());
+    for (const LeafRec& q : w.leaf_rec[p]) head_of[q.out] = q.head;
+    values->clear();
+    for (uint32_t r = 0; r < w.rows(); r++) {
+        const uint32_t node = w.row_node[r], base = w.vals_base[2 * node + p];
+        for (uint32_t c = 0; c < w.nc(node, p); c++) {
+            auto it = head_of.find(base + c);
+            if (it == head_of.end() || it->second >= nout) {
+                *err = "network row " + std::to_string(r) + " has a value slot without a leaf record";
+                return false;
+            }
+            values->push_back(head[it->second]);
+        }
     }
     return true;
 }
@@ -787,23 +987,42 @@ bool Executor::time_wave(const WaveHost& w, uint64_t version, uint32_t warmup, u
         *err = "GPU weight version " + std::to_string(version) + " is unavailable";
         return false;
     }
-    if (!upload(w, it->second, err)) return false;
-    for (uint32_t r = 0; r < warmup; r++) run_schedule(w, it->second, nullptr);
+    if (in_flight_) {
+        *err = "collect the launched waves before timing";
+        return false;
+    }
+    if (!upload(w, it->second, 0, err)) return false;
+    hipGraphExec_t exec = nullptr;
+    double build_ms = 0.0;
+    if (graph_) {
+        HIP_TRY(hipStreamSynchronize(stream_));
+        if (!capture(w, it->second, &exec, &build_ms, err)) return false;
+    }
+    auto once = [&]() -> hipError_t {
+        if (exec) return hipGraphLaunch(exec, stream_);
+        run_schedule(w, it->second, nullptr);
+        return hipSuccess;
+    };
+    for (uint32_t r = 0; r < warmup; r++) HIP_TRY(once());
     HIP_TRY(hipStreamSynchronize(stream_));
     HIP_TRY(hipGetLastError());
     hipEvent_t a, b;
     HIP_TRY(hipEventCreate(&a));
     HIP_TRY(hipEventCreate(&b));
     HIP_TRY(hipEventRecord(a, stream_));
-    for (uint32_t r = 0; r < reps; r++) run_schedule(w, it->second, nullptr);
+    for (uint32_t r = 0; r < reps; r++) HIP_TRY(once());
     HIP_TRY(hipEventRecord(b, stream_));
     HIP_TRY(hipEventSynchronize(b));
     float ms = 0.0f;
     HIP_TRY(hipEventElapsedTime(&ms, a, b));
     hipEventDestroy(a);
     hipEventDestroy(b);
+    if (exec) HIP_TRY(hipGraphExecDestroy(exec));
     *wave_ms = reps ? ms / reps : 0.0;
-    if (prof) run_schedule(w, it->second, prof);
+    if (prof) {
+        run_schedule(w, it->second, prof);
+        prof->graph_build_ms = build_ms;
+    }
     HIP_TRY(hipGetLastError());
     return true;
 }

@@ -36,6 +36,7 @@ struct NetBank {
 struct Result {
     uint64_t tag = 0;
     uint64_t weight_version = 0;
+    bool oversize_route = false, card_exclusive_route = false;  // set by the service (client.rs:119-121)
     std::vector<float> strategy;
     uint32_t nroots = 0, n0 = 0, n1 = 0;
     std::vector<float> root_values;
@@ -49,6 +50,25 @@ struct ScheduleTimes {
     double back_mean = 0, top_mean = 0, reach_mean = 0;  // mean duration of one launch of each CFR kernel
     double cfr_launch_mean = 0;  // mean device time of one CFR iteration (the three kernels)
     uint32_t cfr_launches = 0;
+    double graph_build_ms = 0;   // host time to capture and instantiate the schedule's graph (0: not captured)
+};
+
+// Per-job facts the unpack of a collected wave needs, copied at launch so the
+// packed wave can be reused (repacked) while the wave runs.
+struct JobSlice {
+    uint32_t ncells = 0, nroots = 0, n0 = 0, n1 = 0, root_value0 = 0, snapshot_configs = 0;
+};
+
+// One launched wave (the reference's `InFlight`, engine/src/gpu/device.rs:596-757):
+// the schedule and the result copies are queued on the executor's stream; collect
+// waits for them and splits the results per job.
+struct InFlight {
+    uint32_t slot = 0;
+    uint64_t version = 0;
+    std::vector<JobSlice> jobs;
+    size_t ncells = 0, nroots = 0, carry_slots = 0, snapshot_configs = 0;
+    size_t o_roots = 0, o_carry = 0;
+    bool live = false;
 };
 
 class Executor {
@@ -69,6 +89,26 @@ class Executor {
 
     // Upload, run the whole schedule, collect one result per job.
     bool solve(const WaveHost& w, uint64_t version, std::vector<Result>* out, std::string* err);
+    // The same in two halves: launch queues the upload, the schedule and the
+    // result copies and returns; collect waits and unpacks. At most
+    // MAX_IN_FLIGHT waves may be launched and not yet collected; the packed
+    // wave may be reused as soon as launch returns.
+    static constexpr uint32_t MAX_IN_FLIGHT = 2;
+    bool launch(const WaveHost& w, uint64_t version, InFlight* out, std::string* err);
+    bool collect(InFlight* f, std::vector<Result>* out, std::string* err);
+    bool ready(const InFlight& f) const;
+    uint32_t in_flight() const { return in_flight_; }
+    // Executor::trim (engine/src/gpu/device.rs:574): release the grow-only device
+    // buffers and pinned staging of past waves (the weight banks stay), so a
+    // guarded wave on another lane finds the memory free. Fails while waves
+    // are in flight.
+    bool trim(std::string* err);
+    // The leaf net's values at the initial reach (uniform strategy, root
+    // beliefs) for one traverser, computed by the wave's own kernels: for each
+    // network row in order, the value of each of the row's configs of the
+    // traverser (row config order), and the reach masses [rows x 2].
+    bool leaf_probe(const WaveHost& w, uint64_t version, int traverser, std::vector<float>* values,
+                    std::vector<float>* mass, std::string* err);
     // Upload once, run `warmup` untimed schedules, then `reps` timed ones; mean
     // wave time, and per-class times of one extra profiled schedule.
     bool time_wave(const WaveHost& w, uint64_t version, uint32_t warmup, uint32_t reps, double* wave_ms,
@@ -79,8 +119,24 @@ class Executor {
                   std::vector<double>* layer_ms, std::string* err);
 
   private:
-    bool upload(const WaveHost& w, const NetBank& bank, std::string* err);
+    // Copies the wave's tables into the pinned staging of `slot` and queues
+    // their upload; sets up the device views of the wave.
+    bool upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std::string* err);
     void run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTimes* prof);
+    // Pieces of the schedule: the first layer's fixed-column products, the
+    // initial CFR state (strategy, reach, sums, carries, leaf inputs), both
+    // players' reach under a strategy, the top regions' value and reach
+    // launches, one traverser's leaf net.
+    void static_products(const NetBank& bank);
+    void init_state(const WaveHost& w);
+    void reach_both(const WaveHost& w, float* reach, const float* strat);
+    void top_back(const WaveHost& w, int p, int mode, float da, float db, float pr);
+    void top_reach(const WaveHost& w, int p, float* reach, const float* strat);
+    void leaf_net(const NetBank& bank, int q);
+    const NetBank* bank_of(uint64_t version, std::string* err) const;
+    // The schedule captured into one HIP graph (kernels only: the schedule
+    // issues no memset or copy) and instantiated; *build_ms gets the host time.
+    bool capture(const WaveHost& w, const NetBank& bank, hipGraphExec_t* exec, double* build_ms, std::string* err);
     // Two-tower net: F for the uploaded wave's configs, then one traverser's public tower and readout.
     void run_tower_private(const NetBank& bank);
     void run_tower(const NetBank& bank, uint32_t rows, int traverser);
@@ -109,10 +165,21 @@ class Executor {
     size_t arena_cap_ = 0;
     void* mlp_ = nullptr;  // query inputs, hidden activations, head outputs
     size_t mlp_cap_ = 0;
-    uint8_t* pin_ = nullptr;  // pinned staging of the table blob (grow-only)
-    size_t pin_cap_ = 0;
-    uint8_t* res_pin_ = nullptr;  // pinned landing of the collected outputs (grow-only)
-    size_t res_pin_cap_ = 0;
+    // Per launch slot: pinned staging of the table blob and pinned landing of
+    // the collected outputs (grow-only), and events marking the end of the
+    // slot's upload and of its wave.
+    struct Slot {
+        uint8_t* pin = nullptr;
+        size_t pin_cap = 0;
+        uint8_t* res = nullptr;
+        size_t res_cap = 0;
+        hipEvent_t uploaded = nullptr, done = nullptr;
+        bool recorded = false;  // `uploaded` has been recorded at least once
+        bool busy = false;      // launched, not yet collected
+        hipGraphExec_t exec = nullptr;  // the launched wave's captured schedule
+    };
+    Slot slots_[MAX_IN_FLIGHT];
+    uint32_t in_flight_ = 0;
     WaveDev dev_{};
     void* X_ = nullptr;
     void* Xq_[2] = {};  // the wave's query inputs, one per traverser
@@ -136,6 +203,8 @@ class Executor {
     void* F_ = nullptr;
     uint32_t ncfg_ = 0;
     uint32_t rows_ = 0;
+    bool split_ = true;  // WC_CHAIN_SPLIT=0 turns the first layer's fixed-column product off
+    bool graph_ = false; // WC_GRAPH=1: each wave's schedule runs as one captured HIP graph
 };
 
 }  // namespace wc

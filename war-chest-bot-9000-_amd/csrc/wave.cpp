@@ -1224,4 +1224,25 @@ CfrBytes cfr_bytes_per_iter(const WaveHost& w, int p) {
     return out;
 }
 
+uint64_t leaf_input_bytes(const WaveHost& w, int p, uint32_t elem) {
+    // Per network row: its reach over player p's configs (4 each) and its
+    // outputs (the pooled block into both query inputs, and the mass); per
+    // distinct config list, its config indices once (4 each); per distinct
+    // config, its embedding once.
+    const uint32_t pool = w.net.pool;
+    uint64_t bytes = 0;
+    std::vector<uint8_t> seen(w.cfg_key.size(), 0);
+    for (uint32_t r = 0; r < w.rows(); r++) {
+        const uint32_t lo = w.row_cfg_off[2 * r + p], hi = w.row_cfg_off[2 * r + p + 1];
+        bytes += 4 * uint64_t(hi - lo) + 2 * uint64_t(pool) * elem + 4;
+        for (uint32_t k = lo; k < hi; k++)
+            if (w.row_cfg[k] < seen.size() && !seen[w.row_cfg[k]]) {
+                seen[w.row_cfg[k]] = 1;
+                bytes += 4 * uint64_t(pool);
+            }
+    }
+    for (const PoolGroup& g : w.pool_grp[p]) bytes += 4 * uint64_t(g.n);
+    return bytes;
+}
+
 }  // namespace wc

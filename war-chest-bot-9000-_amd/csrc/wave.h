@@ -253,4 +253,11 @@ struct CfrBytes {
 };
 CfrBytes cfr_bytes_per_iter(const WaveHost& w, int p);
 
+// Algorithmic HBM bytes of one leaf-input pooling of player p's network rows
+// (the pooled-belief half of a leaf-input launch): every row's reach over its
+// configs and its outputs (two pooled blocks of `elem`-byte operands and the
+// mass), every distinct config list's indices and every distinct config's
+// embedding once.
+uint64_t leaf_input_bytes(const WaveHost& w, int p, uint32_t elem);
+
 }  // namespace wc

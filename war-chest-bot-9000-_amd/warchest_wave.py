@@ -55,7 +55,15 @@ class NetDesc(C.Structure):
 
 class ServiceOpts(C.Structure):
     _fields_ = [("lanes", C.c_uint32), ("wave_jobs", C.c_uint32),
-                ("wave_rows", C.c_uint32), ("window_us", C.c_uint32)]
+                ("wave_rows", C.c_uint32), ("window_us", C.c_uint32),
+                ("whale_lanes", C.c_uint32), ("class_shift", C.c_uint32), ("route_unit", C.c_uint64)]
+
+
+class WorkVectorC(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "network_rows", "legal_cells", "reach_slots", "reverse_nonzeros", "table_bytes", "mutable_bytes",
+        "carried_output_bytes", "levels", "reserved_bytes")] + [
+        (n, C.c_uint32) for n in ("exclusive_route", "arena_guard_route", "card_exclusive_route")]
 
 
 class SynthSpecC(C.Structure):
@@ -86,13 +94,13 @@ class WaveStats(C.Structure):
         "snapshot_configs", "table_bytes", "arena_bytes")] + [
         ("cfr_bytes_per_iter", C.c_uint64 * 2), ("cfr_bytes_by_kernel", (C.c_uint64 * 4) * 2),
         ("mlp_flops_per_query", C.c_uint64), ("mlp_flops_executed", C.c_uint64),
-        ("mlp_flops_algorithmic", C.c_uint64)]
+        ("mlp_flops_algorithmic", C.c_uint64), ("leaf_input_bytes", C.c_uint64 * 2)]
 
     def as_dict(self):
         out = {}
         for name, _ in self._fields_:
             v = getattr(self, name)
-            if name == "cfr_bytes_per_iter":
+            if name in ("cfr_bytes_per_iter", "leaf_input_bytes"):
                 out[name] = list(v)
             elif name == "cfr_bytes_by_kernel":
                 out[name] = [list(r) for r in v]
@@ -105,11 +113,12 @@ class WaveStats(C.Structure):
 EXPORTS = [
     "wc_last_error", "wc_net_sizes",
     "wc_service_create", "wc_service_destroy", "wc_set_weights", "wc_queued_work",
-    "wc_submit", "wc_wait", "wc_poll",
+    "wc_submit", "wc_wait", "wc_poll", "wc_ticket_free", "wc_service_stats", "wc_job_work",
     "wc_result_tag", "wc_result_weight_version", "wc_result_strategy", "wc_result_root_values",
-    "wc_result_carries", "wc_result_free",
+    "wc_result_carries", "wc_result_routes", "wc_result_free",
     "wc_executor_create", "wc_executor_destroy", "wc_executor_publish",
     "wc_wave_pack", "wc_wave_free", "wc_wave_stats_get", "wc_wave_array", "wc_value_net_plan", "wc_solve_wave",
+    "wc_launch", "wc_inflight_ready", "wc_collect", "wc_wave_leaf_probe",
     "wc_time_wave",
     "wc_mlp_forward", "wc_time_mlp",
     "wc_job_roundtrip", "wc_job_validate",
@@ -137,6 +146,17 @@ def _declare(L):
     L.wc_submit.argtypes = [C.c_void_p, _u8p, C.c_size_t, C.c_uint64, C.POINTER(C.c_void_p)]
     L.wc_wait.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
     L.wc_poll.argtypes = [C.c_void_p]
+    L.wc_ticket_free.argtypes = [C.c_void_p]
+    L.wc_ticket_free.restype = None
+    L.wc_service_stats.argtypes = [C.c_void_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
+    L.wc_job_work.argtypes = [_u8p, C.c_size_t, C.c_int, C.c_uint64, C.c_uint32, C.POINTER(WorkVectorC),
+                              C.POINTER(C.c_uint64), C.POINTER(C.c_uint32)]
+    L.wc_result_routes.argtypes = [C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_int)]
+    L.wc_launch.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p)]
+    L.wc_inflight_ready.argtypes = [C.c_void_p, C.c_void_p]
+    L.wc_collect.argtypes = [C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)]
+    L.wc_wave_leaf_probe.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_int, _f32p, C.c_size_t,
+                                     C.POINTER(C.c_size_t), _f32p]
     L.wc_result_tag.argtypes = [C.c_void_p]
     L.wc_result_tag.restype = C.c_uint64
     L.wc_result_weight_version.argtypes = [C.c_void_p]
@@ -316,6 +336,20 @@ def job_validate(b: bytes):
     _check(lib().wc_job_validate(p, len(b)))
 
 
+def job_work(b: bytes, precision=WC_PRECISE, route_unit=0, class_shift=0) -> dict:
+    """`PackedJob::work`, `job_cost` and `cost_class` of one job (wc_job_work): the work
+    vector's fields, `reserved_bytes`, the three route predicates, `cost` and `cost_class`."""
+    buf, p = _bytes_ptr(b)
+    w = WorkVectorC()
+    cost, cls = C.c_uint64(), C.c_uint32()
+    _check(lib().wc_job_work(p, len(b), precision, route_unit, class_shift, C.byref(w), C.byref(cost),
+                             C.byref(cls)))
+    out = {name: int(getattr(w, name)) for name, _ in w._fields_}
+    out["cost"] = int(cost.value)
+    out["cost_class"] = int(cls.value)
+    return out
+
+
 # ------------------------------------------------------------------ results
 
 @dataclass
@@ -327,6 +361,8 @@ class SolveResult:
     root_values: np.ndarray  # [nroots, n0 + n1]
     root_n: tuple
     carries: np.ndarray      # [slots, snapshot_configs] float16
+    oversize_route: bool = False
+    card_exclusive_route: bool = False
 
     @staticmethod
     def take(ptr) -> "SolveResult":
@@ -344,8 +380,10 @@ class SolveResult:
         k = slots.value * cfgs.value
         carries = (np.ctypeslib.as_array(cp, (k,)).copy() if k else np.zeros(0, np.uint16)).view(
             np.float16).reshape(slots.value, cfgs.value)
+        ov, card = C.c_int(), C.c_int()
+        _check(L.wc_result_routes(ptr, C.byref(ov), C.byref(card)))
         r = SolveResult(int(L.wc_result_tag(ptr)), int(L.wc_result_weight_version(ptr)), strategy, roots,
-                        (n0.value, n1.value), carries)
+                        (n0.value, n1.value), carries, bool(ov.value), bool(card.value))
         L.wc_result_free(ptr)
         return r
 
@@ -410,12 +448,31 @@ class Executor:
         _check(lib().wc_solve_wave(self.h, wave.h, version, res))
         return [SolveResult.take(res[k]) for k in range(wave.njobs)]
 
+    def launch(self, wave: Wave, version: int) -> "InFlight":
+        """`Executor::launch`: queue the wave and return at once; `collect` the record later."""
+        f = C.c_void_p()
+        _check(lib().wc_launch(self.h, wave.h, version, C.byref(f)))
+        return InFlight(self, f, wave.njobs)
+
+    def leaf_probe(self, wave: Wave, version: int, traverser: int):
+        """The leaf net's values at the initial reach for `traverser`, from the wave's own
+        kernels (wc_wave_leaf_probe): (values in row order, each row's configs of the
+        traverser; mass [rows, 2])."""
+        rows = wave.stats()["rows"]
+        n = C.c_size_t()
+        mass = np.zeros((max(rows, 1), 2), np.float32)
+        _check(lib().wc_wave_leaf_probe(self.h, wave.h, version, traverser, None, 0, C.byref(n), None))
+        vals = np.zeros(max(n.value, 1), np.float32)
+        _check(lib().wc_wave_leaf_probe(self.h, wave.h, version, traverser, vals.ctypes.data_as(_f32p), vals.size,
+                                        C.byref(n), mass.ctypes.data_as(_f32p)))
+        return vals[: n.value], mass[:rows]
+
     def time_wave(self, wave: Wave, version: int, reps: int, warmup: int = 1):
         """Mean device ms per wave over `reps` timed schedules after `warmup` untimed
         ones, and one profiled schedule's [cfr, mlp, leaf input, other, mean CFR iteration,
-        mean subtree sweep, mean top sweep, mean subtree reach] ms."""
+        mean subtree sweep, mean top sweep, mean subtree reach, graph build (host)] ms."""
         ms = C.c_double()
-        parts = (C.c_double * 8)()
+        parts = (C.c_double * 9)()
         _check(lib().wc_time_wave(self.h, wave.h, version, warmup, reps, C.byref(ms), parts))
         return ms.value, list(parts)
 
@@ -446,6 +503,24 @@ class Executor:
             pass
 
 
+class InFlight:
+    """A launched wave (`InFlight`, engine/src/gpu/device.rs:596-757)."""
+
+    def __init__(self, ex: Executor, handle, njobs: int):
+        self.ex, self.h, self.njobs = ex, handle, njobs
+
+    def ready(self) -> bool:
+        return bool(self.h) and bool(lib().wc_inflight_ready(self.ex.h, self.h))
+
+    def collect(self) -> list:
+        if not self.h:
+            raise WaveError("already collected")
+        res = (C.c_void_p * self.njobs)()
+        h, self.h = self.h, None
+        _check(lib().wc_collect(self.ex.h, h, res))
+        return [SolveResult.take(res[k]) for k in range(self.njobs)]
+
+
 # ------------------------------------------------------------------ service
 
 class SolveHandle:
@@ -462,6 +537,15 @@ class SolveHandle:
             raise WaveError("handle already waited on")
         _check(lib().wc_wait(t, C.byref(out)))
         return SolveResult.take(out)
+
+    def __del__(self):
+        # a handle dropped without wait frees its ticket (the solve's result is discarded)
+        t, self._t = getattr(self, "_t", None), None
+        if t is not None:
+            try:
+                lib().wc_ticket_free(t)
+            except Exception:
+                pass
 
 
 class GpuClient:
@@ -486,6 +570,12 @@ class GpuClient:
     def queued_work(self) -> int:
         return int(lib().wc_queued_work(self.h))
 
+    def stats(self) -> dict:
+        """Waves launched and guarded routes taken so far."""
+        w, g = C.c_uint64(), C.c_uint64()
+        _check(lib().wc_service_stats(self.h, C.byref(w), C.byref(g)))
+        return {"waves": int(w.value), "guarded_routes": int(g.value)}
+
     def close(self):
         if self.h:
             lib().wc_service_destroy(self.h)
@@ -499,10 +589,10 @@ class GpuClient:
 
 
 def spawn(device: int, net: Net, precision=WC_PRECISE, lanes=2, wave_jobs=64, wave_rows=49152,
-          window_us=800) -> GpuClient:
+          window_us=800, whale_lanes=1, class_shift=0, route_unit=0) -> GpuClient:
     """`service::spawn` (engine/src/gpu/service.rs:55-82)."""
     d = net.desc()
-    opts = ServiceOpts(lanes, wave_jobs, wave_rows, window_us)
+    opts = ServiceOpts(lanes, wave_jobs, wave_rows, window_us, whale_lanes, class_shift, route_unit)
     h = C.c_void_p()
     _check(lib().wc_service_create(device, C.byref(d), precision, C.byref(opts), C.byref(h)))
     return GpuClient(h)
