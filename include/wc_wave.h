@@ -231,6 +231,20 @@ int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup,
 /* Leaf-net inference alone (the value-net GEMM chain): x is rows x in f32 on
  * the host; out receives rows x heads f32 (head rows 0..heads-1). */
 int wc_mlp_forward(wc_executor* ex, uint64_t version, uint32_t rows, const float* x, float* out);
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). wc_mlp_forward on device-resident buffers -- x: rows x in
+ * f32, out: rows x heads f32 -- with every intermediate (the 16-bit input
+ * operand, hidden activations, the pass plan) in one fixed device array of
+ * WC_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; the call
+ * makes no device allocation. stream NULL: queued on the executor's stream
+ * and the call waits for the result; otherwise queued on that hipStream_t and
+ * the call returns at once. Calls that overlap on one GPU share the array and
+ * race. Fails (WC_ERR_INVALID) when the rows need more than the array holds
+ * (about 32k rows of a 512-input 16-bit net, 8k of the float32 net). */
+#define WC_NOALLOC_SCRATCH_BYTES (32u << 20)
+int wc_mlp_forward_noalloc(wc_executor* ex, uint64_t version, uint32_t rows, const float* x, float* out,
+                           void* stream);
 /* Benchmark helper for the chain alone: x resident on the device, `reps` launches,
  * mean milliseconds per chain from HIP events on the executor's stream. */
 int wc_time_mlp(wc_executor* ex, uint64_t version, uint32_t rows, const float* x, uint32_t reps,

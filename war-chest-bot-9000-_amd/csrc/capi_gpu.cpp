@@ -361,6 +361,20 @@ int wc_mlp_forward(wc_executor* ex, uint64_t version, uint32_t rows, const float
     });
 }
 
+int wc_mlp_forward_noalloc(wc_executor* ex, uint64_t version, uint32_t rows, const float* x, float* out,
+                           void* stream) {
+    if (!ex || (rows && (!x || !out))) return fail(WC_ERR_INVALID, "wc_mlp_forward_noalloc: null argument");
+    return shielded("wc_mlp_forward_noalloc", [&] {
+        std::string err;
+        if (ex->ex->mlp_forward_noalloc(version, rows, x, out, (hipStream_t)stream, &err)) return WC_OK;
+        return fail(err.find("scratch") != std::string::npos || err.find("version") != std::string::npos ||
+                            err.find("takes the MLP") != std::string::npos
+                        ? WC_ERR_INVALID
+                        : WC_ERR_DEVICE,
+                    err);
+    });
+}
+
 int wc_time_mlp(wc_executor* ex, uint64_t version, uint32_t rows, const float* x, uint32_t reps, double* chain_ms,
                 double* layer_ms) {
     if (!ex || !x || !chain_ms) return fail(WC_ERR_INVALID, "wc_time_mlp: null argument");

@@ -99,6 +99,7 @@ Executor::Executor(int device, int precision) : device_(device), precision_(prec
             err_ = "cannot create the executor's events";
             return;
         }
+    if (!noalloc_scratch(device, &scratch_, &scratch_err_)) scratch_ = nullptr;
     if (const char* env = std::getenv("WC_CHAIN_SPLIT")) split_ = std::strcmp(env, "0") != 0;
     if (const char* env = std::getenv("WC_GRAPH")) graph_ = std::strcmp(env, "1") == 0;
     ok_ = true;
@@ -516,8 +517,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
     return true;
 }
 
-// The fused kernel's view of a 16-bit MLP bank.
-static ChainNet chain_net(const NetBank& bank) {
+ChainNet chain_net(const NetBank& bank) {
     const NetShape& ns = bank.ns;
     ChainNet net{};
     for (uint32_t l = 0; l < ns.layers; l++) {

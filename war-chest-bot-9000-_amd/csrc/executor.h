@@ -71,6 +71,12 @@ struct InFlight {
     bool live = false;
 };
 
+// The fused kernel's view of a 16-bit MLP bank.
+ChainNet chain_net(const NetBank& bank);
+// The allocation-free entry point's scratch array on `device` (current): its
+// device address, looked up once per device (noalloc.hip).
+bool noalloc_scratch(int device, void** out, std::string* err);
+
 class Executor {
   public:
     Executor(int device, int precision);
@@ -115,6 +121,11 @@ class Executor {
                    ScheduleTimes* prof, std::string* err);
     // The leaf GEMM chain alone on rows x in host inputs.
     bool mlp_forward(uint64_t version, uint32_t rows, const float* x, float* out, std::string* err);
+    // The same on device-resident x and out, every intermediate in the fixed
+    // scratch array (no allocation); queued on `stream` (null: the executor's
+    // stream, and waits).
+    bool mlp_forward_noalloc(uint64_t version, uint32_t rows, const float* x, float* out, hipStream_t stream,
+                             std::string* err);
     bool time_mlp(uint64_t version, uint32_t rows, const float* x, uint32_t reps, double* chain_ms,
                   std::vector<double>* layer_ms, std::string* err);
 
@@ -203,6 +214,8 @@ class Executor {
     void* F_ = nullptr;
     uint32_t ncfg_ = 0;
     uint32_t rows_ = 0;
+    void* scratch_ = nullptr;  // the allocation-free scratch on this device
+    std::string scratch_err_;
     bool split_ = true;  // WC_CHAIN_SPLIT=0 turns the first layer's fixed-column product off
     bool graph_ = false; // WC_GRAPH=1: each wave's schedule runs as one captured HIP graph
 };

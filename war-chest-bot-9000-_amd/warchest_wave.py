@@ -120,7 +120,7 @@ EXPORTS = [
     "wc_wave_pack", "wc_wave_free", "wc_wave_stats_get", "wc_wave_array", "wc_value_net_plan", "wc_solve_wave",
     "wc_launch", "wc_inflight_ready", "wc_collect", "wc_wave_leaf_probe",
     "wc_time_wave",
-    "wc_mlp_forward", "wc_time_mlp",
+    "wc_mlp_forward", "wc_mlp_forward_noalloc", "wc_time_mlp",
     "wc_job_roundtrip", "wc_job_validate",
     "wc_synth_spec_default", "wc_synth", "wc_jobset_count", "wc_jobset_job", "wc_jobset_free",
     "wc_synth_weights", "wc_synth_features",
@@ -186,6 +186,7 @@ def _declare(L):
     L.wc_time_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32,
                                C.POINTER(C.c_double), C.POINTER(C.c_double)]
     L.wc_mlp_forward.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, _f32p, _f32p]
+    L.wc_mlp_forward_noalloc.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p]
     L.wc_time_mlp.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, _f32p, C.c_uint32,
                               C.POINTER(C.c_double), C.POINTER(C.c_double)]
     L.wc_job_roundtrip.argtypes = [_u8p, C.c_size_t, _u8p, C.c_size_t, C.POINTER(C.c_size_t)]
@@ -482,6 +483,12 @@ class Executor:
         _check(lib().wc_mlp_forward(self.h, version, x.shape[0], x.ctypes.data_as(_f32p),
                                     out.ctypes.data_as(_f32p)))
         return out
+
+    def mlp_noalloc(self, version: int, rows: int, x_dev: int, out_dev: int, stream: int = 0):
+        """wc_mlp_forward_noalloc on device buffers (addresses as ints): x_dev rows x in f32,
+        out_dev rows x heads f32. stream 0 waits on the executor's stream."""
+        _check(lib().wc_mlp_forward_noalloc(self.h, version, rows, C.c_void_p(x_dev), C.c_void_p(out_dev),
+                                            C.c_void_p(stream) if stream else None))
 
     def time_mlp(self, version: int, x: np.ndarray, reps: int):
         x = np.ascontiguousarray(x, np.float32)
