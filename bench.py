@@ -349,6 +349,13 @@ def main():
         import ctypes
 
         hip = ctypes.CDLL("libamdhip64.so")
+        # every call's signature declared: no argument goes through ctypes' default int conversion
+        hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+        hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        hip.hipFree.argtypes = [ctypes.c_void_p]
+        hip.hipDeviceSynchronize.argtypes = []
+        for f in (hip.hipMalloc, hip.hipMemcpy, hip.hipFree, hip.hipDeviceSynchronize):
+            f.restype = ctypes.c_int
         n = args.copy_probe << 20
         src, dst = ctypes.c_void_p(), ctypes.c_void_p()
         assert hip.hipMalloc(ctypes.byref(src), ctypes.c_size_t(n)) == 0
