@@ -43,10 +43,13 @@ const char* wc_last_error(void);
 
 /* Network description: the flat `set_weights(dims, w, b, ln)` bank
  * (engine/src/gpu/client.rs:257-272). dims[0] names the family:
+ *   [5]                                                         the reference's v5 network
  *   [101, in, hidden, layers, heads, pool]                      MLP
  *   [102, in, width, pub_layers, priv_in, priv_layers, pool]    two-tower
  * w: MLP = W_1 [in x hidden] row-major, W_2..W_L [hidden x hidden],
- *    W_head [heads x hidden]; b = b_1..b_L [hidden], b_head [heads]. */
+ *    W_head [heads x hidden]; b = b_1..b_L [hidden], b_head [heads].
+ * v5: w, b and ln in the blob order of NetLayout::new (engine/src/net.rs:272-316),
+ *    ln = the (gain, shift) pair of every LayerNorm in application order. */
 typedef struct wc_net_desc {
     const uint32_t* dims;
     uint32_t ndims;
@@ -54,12 +57,14 @@ typedef struct wc_net_desc {
     size_t nw;
     const float* b;
     size_t nb;
-    const float* ln; /* unused by the synthetic families; pass NULL, 0 */
+    const float* ln; /* v5 only; the synthetic families take NULL, 0 */
     size_t nln;
 } wc_net_desc;
 
-/* Float counts a family expects for w and b. */
+/* Float counts a family expects for w and b (net.rs:272-316 for v5). */
 int wc_net_sizes(const uint32_t* dims, uint32_t ndims, size_t* nw, size_t* nb);
+/* Float count a family expects for ln (0 for the synthetic families). */
+int wc_net_norms(const uint32_t* dims, uint32_t ndims, size_t* nln);
 
 /* ------------------------------------------------------------ service API
  * Replaces service::spawn / GpuClient / SolveHandle
@@ -295,6 +300,8 @@ void wc_jobset_free(wc_jobset* s);
 /* Kaiming-normal weights and U[-0.1, 0.1] biases for a family (sizes from wc_net_sizes). */
 int wc_synth_weights(const uint32_t* dims, uint32_t ndims, uint64_t seed, float* w, size_t nw, float* b,
                      size_t nb);
+/* LayerNorm pairs for a family (v5: gains 1 + N(0, 0.01), shifts N(0, 0.01)). */
+int wc_synth_norms(const uint32_t* dims, uint32_t ndims, uint64_t seed, float* ln, size_t nln);
 /* rows x width features, U[0,1) with 30% of dims in one-hot blocks of width 8. */
 int wc_synth_features(uint32_t rows, uint32_t width, uint64_t seed, float* x);
 

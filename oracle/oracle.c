@@ -19,6 +19,8 @@
  *   belief_blocks        pinned: numpy float64 restatement
  *   mlp_trunk/values     pinned: numpy float64 restatement
  *   value_under          pinned: brute force
+ *   v5 network (v5.c)    pinned: torch float64 restatement of each piece, board
+ *                        geometry invariants, special cases (tests/test_v5_pins.py)
  *   carried_beliefs      pinned: brute force (normalised reach under snapshots)
  *
  * Build: see oracle/Makefile (gcc -O2 -ffp-contract=off: the reference's Rust
@@ -32,6 +34,8 @@
 #include <string.h>
 #include <time.h>
 
+#include "v5.h"
+
 #define NONE 0xffffffffu
 #define EPS 1e-6f      /* search.rs:1658 */
 #define SMOOTH 1e-30f  /* rebel.rs:359 */
@@ -43,8 +47,9 @@ enum { MODEL_V5 = 5, MODEL_MLP = 101, MODEL_TWO_TOWER = 102 };
  * sum or, for F16A, a float32 sum in ascending k order -- two equally faithful
  * f16 realizations that differ only in how the f32-level sum is rounded.
  * F16X holds each operand as the f16 pair hi + lo (about 22 significant bits:
- * the compensated mode), F32W keeps float32 operands with a wide sum. */
-enum { NET_EMPTY = 0, NET_F32 = 1, NET_F16 = 2, NET_BF16 = 3, NET_F16A = 4, NET_F16X = 5, NET_F32W = 6 };
+ * the compensated mode), F32W keeps float32 operands with a wide sum, BF16A
+ * (v5 network only) is F16A with bfloat16 operands. */
+enum { NET_EMPTY = 0, NET_F32 = 1, NET_F16 = 2, NET_BF16 = 3, NET_F16A = 4, NET_F16X = 5, NET_F32W = 6, NET_BF16A = 7 };
 enum { BACK_REGRET = 0, BACK_VALUE = 1, BACK_BR = 2 };
 
 static __thread char g_err[256];
@@ -282,15 +287,21 @@ static int parse_job(const uint8_t* b, size_t n, Job* j) {
         j->priv_layers = j->net_dims.v[5];
         j->pool = j->net_dims.v[6];
         j->cfeat = 1 + j->pool + j->priv_in;
+    } else if (j->kind == MODEL_V5 && j->net_dims.n == 1) {
+        /* net.rs:41; the join reads both pooled beliefs and the seat */
+        j->in = V5_JOIN_IN;
+        j->hidden = V5_D;
+        j->pool = V5_POOL;
+        j->cfeat = V5_CFEAT;
     } else {
-        snprintf(g_err, sizeof g_err, "oracle supports the synthetic value-net tags only");
+        snprintf(g_err, sizeof g_err, "unsupported net_dims");
         return 0;
     }
     if (j->in < 2 * j->pool + 1) {
         snprintf(g_err, sizeof g_err, "net input narrower than the belief block");
         return 0;
     }
-    j->row_bytes = j->in - 2 * j->pool - 1;
+    j->row_bytes = j->kind == MODEL_V5 ? V5_ROW_BYTES : j->in - 2 * j->pool - 1;
     uint32_t N = j->nodes;
     if (!want(j->node_kind.n, N, "node_kind") || !want(j->node_player.n, N, "node_player") ||
         !want(j->legal_row_of.n, N, "legal_row_of") ||
@@ -301,7 +312,7 @@ static int parse_job(const uint8_t* b, size_t n, Job* j) {
         !want(j->cfg_off.n, 2 * (uint64_t)N + 1, "cfg_off") ||
         !want(j->cphi.n, (uint64_t)j->ncfg * j->cfeat, "cphi") || !want(j->cplayer.n, j->ncfg, "cplayer") ||
         !want(j->leaf_raw.n, (uint64_t)j->rows * j->row_bytes, "leaf_raw") ||
-        !want(j->card_feat.n, 0, "card_feat") ||
+        !want(j->card_feat.n, j->kind == MODEL_V5 ? (uint64_t)V5_NTYPE * V5_CARD_FEATS : 0, "card_feat") ||
         !want(j->leaf_coff.n, 2 * (uint64_t)j->rows + 1, "leaf_coff") ||
         !want(j->node_parent.n, N, "node_parent") || !want(j->rev_row_of.n, N, "rev_row_of") ||
         !want(j->rvd_row_of.n, N, "rvd_row_of") || !want(j->rev_cell.n, j->rev_src.n, "rev_cell") ||
@@ -407,7 +418,13 @@ typedef struct {
     const float* PB[16];
     const float* wread;
     float bread;
+    /* v5 (v5.c) */
+    V5* v5;
 } Net;
+
+/* GELU's tanh in the v5 restatement: its own (0) or the C library's (1). */
+static int g_v5_libm_tanh;
+void oracle_v5_set_libm_tanh(int on) { g_v5_libm_tanh = on; }
 
 static float q_op(const Net* n, float x) {
     if (n->mode == NET_F16 || n->mode == NET_F16A) return round_f16(x);
@@ -423,7 +440,7 @@ static float q_op(const Net* n, float x) {
 static int wide_sum(const Net* n) { return n->mode != NET_F32 && n->mode != NET_F16A; }
 
 static int net_init(Net* n, int mode, const uint32_t* dims, uint32_t ndims, const float* w, size_t nw,
-                    const float* b, size_t nb) {
+                    const float* b, size_t nb, const float* ln, size_t nln) {
     memset(n, 0, sizeof *n);
     n->mode = mode;
     if (mode == NET_EMPTY) return 1;
@@ -433,6 +450,17 @@ static int net_init(Net* n, int mode, const uint32_t* dims, uint32_t ndims, cons
     }
     n->kind = dims[0];
     size_t need_w = 0, need_b = 0;
+    if (n->kind == MODEL_V5 && ndims == 1) {
+        n->in = V5_JOIN_IN;
+        n->hidden = V5_D;
+        n->pool = V5_POOL;
+        n->v5 = v5_new(mode, w, nw, b, nb, ln, nln, g_v5_libm_tanh, g_err, sizeof g_err);
+        return n->v5 != NULL;
+    }
+    if (mode == NET_BF16A) {
+        snprintf(g_err, sizeof g_err, "the BF16A model is the v5 network's only");
+        return 0;
+    }
     if (n->kind == MODEL_MLP && ndims == 6) {
         n->in = dims[1];
         n->hidden = dims[2];
@@ -521,6 +549,8 @@ static int net_init(Net* n, int mode, const uint32_t* dims, uint32_t ndims, cons
 static void net_free(Net* n) {
     free(n->wq);
     n->wq = NULL;
+    v5_free(n->v5);
+    n->v5 = NULL;
 }
 
 /* One dense ReLU layer, y = relu(x W + b), with the row-major `gemm` loop of
@@ -623,8 +653,12 @@ typedef struct {
     float* wbuf;
     int last_traverser; /* -1 = none */
     int batch_ready;
-    /* two-tower: per interned config, the private tower output times the readout weight */
+    /* two-tower: per interned config, the private tower output times the readout weight;
+     * v5: f(c) */
     float* fcfg;
+    /* v5: the card tokens of both views, per row the board vector and its join
+     * projection, per config g(c) */
+    float *cards, *P, *Jp, *gcfg;
 } Solver;
 
 static inline uint32_t S_nc(const Solver* s, uint32_t i, int p) { return p ? s->nc1[i] : s->nc0[i]; }
@@ -725,7 +759,8 @@ static void belief_blocks(Solver* s, int only) {
             /* accumulate (engine/src/net.rs:161-170) */
             for (uint32_t k = 0; k < pool; k++) out[k] = 0.0f;
             for (uint32_t c = 0; c < n; c++) {
-                const float* row = j->cphi.v + (size_t)cidx[c] * j->cfeat + 1;
+                /* the config's pooling vector: g(c) for v5 (search.rs:1525-1545), else the job's embedding */
+                const float* row = s->gcfg ? s->gcfg + (size_t)cidx[c] * pool : j->cphi.v + (size_t)cidx[c] * j->cfeat + 1;
                 float w = s->wbuf[c];
                 for (uint32_t k = 0; k < pool; k++) out[k] += w * row[k];
             }
@@ -749,6 +784,13 @@ static void pbs_head(Solver* s, int traverser) {
     const Net* n = s->net;
     if (n->mode == NET_EMPTY) return;
     const Job* j = s->j;
+    if (n->v5) { /* Net::join per row (search.rs:1570-1578) */
+        for (uint32_t r = 0; r < j->rows; r++)
+            v5_join(n->v5, s->P + (size_t)r * V5_D, s->Jp + (size_t)r * V5_JW,
+                    s->xb + (size_t)(2 * r + (uint32_t)traverser) * V5_POOL,
+                    s->xb + (size_t)(2 * r + 1 - (uint32_t)traverser) * V5_POOL, traverser, s->h + (size_t)r * V5_D);
+        return;
+    }
     for (uint32_t r = 0; r < j->rows; r++) {
         query_input(s, r, traverser, s->xin);
         net_trunk(n, s->xin, n->W, n->B, n->in, n->layers, s->h + (size_t)r * n->hidden, s->scratch);
@@ -764,6 +806,7 @@ static float net_value(const Solver* s, uint32_t r, int p, uint32_t c) {
     const float* h = s->h + (size_t)r * n->hidden;
     const float* phi = j->cphi.v + (size_t)cidx[c] * j->cfeat;
     if (n->kind == MODEL_MLP) return head_value(n, h, (uint32_t)phi[0]);
+    if (n->v5) return v5_value(n->v5, s->fcfg + (size_t)cidx[c] * V5_D, h);
     /* two-tower: <f(c), h> + bias with f(c) = private tower output x readout weight */
     const float* f = s->fcfg + (size_t)cidx[c] * n->hidden;
     if (!wide_sum(n)) {
@@ -811,7 +854,23 @@ static void ensure_leaf_batch(Solver* s) {
     s->batch_ready = 1;
     const Net* n = s->net;
     const Job* j = s->j;
-    if (n->mode == NET_EMPTY || n->kind != MODEL_TWO_TOWER) return;
+    if (n->mode == NET_EMPTY) return;
+    if (n->v5) { /* search.rs:1463-1498: cards, board, join cache, configs, once per solve */
+        s->cards = (float*)malloc(sizeof(float) * 2 * V5_NTYPE * V5_TYPE);
+        s->P = (float*)malloc(sizeof(float) * ((size_t)j->rows * V5_D + 1));
+        s->Jp = (float*)malloc(sizeof(float) * ((size_t)j->rows * V5_JW + 1));
+        s->fcfg = (float*)malloc(sizeof(float) * ((size_t)j->ncfg * V5_D + 1));
+        s->gcfg = (float*)malloc(sizeof(float) * ((size_t)j->ncfg * V5_POOL + 1));
+        v5_cards(n->v5, j->card_feat.v, s->cards);
+        for (uint32_t r = 0; r < j->rows; r++)
+            v5_board(n->v5, j->leaf_raw.v + (size_t)r * V5_ROW_BYTES, s->cards, s->P + (size_t)r * V5_D,
+                     s->Jp + (size_t)r * V5_JW);
+        for (uint32_t c = 0; c < j->ncfg; c++)
+            v5_config(n->v5, j->cphi.v + (size_t)c * V5_CFEAT, j->cplayer.v[c], s->cards,
+                      s->fcfg + (size_t)c * V5_D, s->gcfg + (size_t)c * V5_POOL);
+        return;
+    }
+    if (n->kind != MODEL_TWO_TOWER) return;
     /* Private tower once per solve, then fold the readout weight in. */
     s->fcfg = (float*)malloc(((size_t)j->ncfg * n->hidden + 1) * sizeof(float));
     float* hbuf = (float*)malloc(n->hidden * sizeof(float));
@@ -1006,6 +1065,10 @@ static void solver_free(Solver* s) {
     free(s->scratch);
     free(s->wbuf);
     free(s->fcfg);
+    free(s->cards);
+    free(s->P);
+    free(s->Jp);
+    free(s->gcfg);
     memset(s, 0, sizeof *s);
 }
 
@@ -1246,8 +1309,8 @@ int oracle_job_shape(const uint8_t* b, size_t n, OracleShape* out) {
  * strategy: [ncells]; roots: [nroots * (n0 + n1)]; carries: [carry_slots * snapshot_configs];
  * conv: [2] = (nash_conv, zero_sum) of the final average (computed only if non-NULL). */
 int oracle_solve(const uint8_t* b, size_t n, int net_mode, const uint32_t* dims, uint32_t ndims,
-                 const float* w, size_t nw, const float* bias, size_t nb, float* strategy, float* roots,
-                 float* carries, float* conv) {
+                 const float* w, size_t nw, const float* bias, size_t nb, const float* ln, size_t nln,
+                 float* strategy, float* roots, float* carries, float* conv) {
     Job j;
     Net net;
     Solver s;
@@ -1255,7 +1318,7 @@ int oracle_solve(const uint8_t* b, size_t n, int net_mode, const uint32_t* dims,
     memset(&s, 0, sizeof s);
     memset(&net, 0, sizeof net);
     if (!parse_job(b, n, &j)) goto out;
-    if (!net_init(&net, net_mode, dims, ndims, w, nw, bias, nb)) goto out;
+    if (!net_init(&net, net_mode, dims, ndims, w, nw, bias, nb, ln, nln)) goto out;
     if (!solver_init(&s, &j, &net)) goto out;
     for (uint32_t t = 0; t < j.iters; t++) step(&s, (int)(t % 2));
     if (strategy) memcpy(strategy, s.snaps[s.nsnaps - 1], (size_t)j.ncells * sizeof(float));
@@ -1277,8 +1340,8 @@ out:
  * written when it exceeds cap), and every row's reach masses of both players
  * (mass: rows x 2, config-order sums). */
 int oracle_leaf_probe(const uint8_t* b, size_t n, int net_mode, const uint32_t* dims, uint32_t ndims,
-                      const float* w, size_t nw, const float* bias, size_t nb, int traverser, float* values,
-                      size_t cap, size_t* count, float* mass) {
+                      const float* w, size_t nw, const float* bias, size_t nb, const float* ln, size_t nln,
+                      int traverser, float* values, size_t cap, size_t* count, float* mass) {
     Job j;
     Net net;
     Solver s;
@@ -1286,7 +1349,7 @@ int oracle_leaf_probe(const uint8_t* b, size_t n, int net_mode, const uint32_t* 
     memset(&s, 0, sizeof s);
     memset(&net, 0, sizeof net);
     if (!parse_job(b, n, &j)) goto out;
-    if (!net_init(&net, net_mode, dims, ndims, w, nw, bias, nb)) goto out;
+    if (!net_init(&net, net_mode, dims, ndims, w, nw, bias, nb, ln, nln)) goto out;
     if (net_mode == NET_EMPTY || traverser < 0 || traverser > 1) {
         snprintf(g_err, sizeof g_err, "leaf probe needs a network and a traverser 0 or 1");
         goto out;
@@ -1326,7 +1389,7 @@ int oracle_mlp(uint32_t rows, const float* x, uint32_t nk, const uint32_t* keys,
                const uint32_t* dims, uint32_t ndims, const float* w, size_t nw, const float* bias, size_t nb,
                float* out, float* h_out) {
     Net net;
-    if (!net_init(&net, net_mode, dims, ndims, w, nw, bias, nb)) return -1;
+    if (!net_init(&net, net_mode, dims, ndims, w, nw, bias, nb, NULL, 0)) return -1;
     if (net.kind != MODEL_MLP) {
         snprintf(g_err, sizeof g_err, "oracle_mlp needs an MLP tag");
         net_free(&net);
@@ -1355,8 +1418,8 @@ typedef struct {
     int net_mode;
     const uint32_t* dims;
     uint32_t ndims;
-    const float *w, *b;
-    size_t nw, nb;
+    const float *w, *b, *ln;
+    size_t nw, nb, nln;
     volatile uint32_t next;
     volatile int failed;
     uint64_t node_iters;
@@ -1375,7 +1438,7 @@ static void* batch_worker(void* arg) {
         memset(&s, 0, sizeof s);
         memset(&net, 0, sizeof net);
         int ok = parse_job(bt->jobs[k], bt->lens[k], &j) &&
-                 net_init(&net, bt->net_mode, bt->dims, bt->ndims, bt->w, bt->nw, bt->b, bt->nb) &&
+                 net_init(&net, bt->net_mode, bt->dims, bt->ndims, bt->w, bt->nw, bt->b, bt->nb, bt->ln, bt->nln) &&
                  solver_init(&s, &j, &net);
         if (ok) {
             for (uint32_t t = 0; t < j.iters; t++) step(&s, (int)(t % 2));
@@ -1402,7 +1465,8 @@ static void* batch_worker(void* arg) {
  * Returns wall seconds, or a negative value on failure. */
 double oracle_solve_batch(uint32_t njobs, const uint8_t* const* jobs, const size_t* lens, uint32_t threads,
                           int net_mode, const uint32_t* dims, uint32_t ndims, const float* w, size_t nw,
-                          const float* bias, size_t nb, uint64_t* node_iters, uint64_t* leaf_queries) {
+                          const float* bias, size_t nb, const float* ln, size_t nln, uint64_t* node_iters,
+                          uint64_t* leaf_queries) {
     Batch bt;
     memset(&bt, 0, sizeof bt);
     bt.jobs = jobs;
@@ -1415,6 +1479,8 @@ double oracle_solve_batch(uint32_t njobs, const uint8_t* const* jobs, const size
     bt.b = bias;
     bt.nw = nw;
     bt.nb = nb;
+    bt.ln = ln;
+    bt.nln = nln;
     pthread_mutex_init(&bt.mu, NULL);
     if (threads < 1) threads = 1;
     pthread_t* th = (pthread_t*)malloc(threads * sizeof(pthread_t));
@@ -1467,7 +1533,7 @@ double oracle_mlp_batch(uint32_t rows, const float* x, uint32_t nk, const uint32
                         int net_mode, const uint32_t* dims, uint32_t ndims, const float* w, size_t nw,
                         const float* bias, size_t nb, float* out) {
     Net net;
-    if (!net_init(&net, net_mode, dims, ndims, w, nw, bias, nb)) return -1.0;
+    if (!net_init(&net, net_mode, dims, ndims, w, nw, bias, nb, NULL, 0)) return -1.0;
     MlpBatch m = {x, rows, nk, keys, &net, out, 0};
     if (threads < 1) threads = 1;
     pthread_t* th = (pthread_t*)malloc(threads * sizeof(pthread_t));

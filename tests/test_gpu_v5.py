@@ -1,0 +1,123 @@
+"""The v5 leaf network on the GPU (the reference's device path:
+engine/src/gpu/device.rs:836-1106 per wave, 1218-1305 per iteration), through
+the C ABI, against the oracle's restatement of engine/src/net.rs:
+
+- float32: the leaf values at the initial reach (wc_wave_leaf_probe: cards,
+  trunk, join cache, config encoder, pooled beliefs, join, readout) and whole
+  solves (strategies, root values, carries) bit-identical to the oracle;
+- the zero network: every leaf valued at value_bias;
+- 16-bit operands: the leaf values track the oracle's model of the same
+  operand rounding.
+"""
+import os
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+
+import oracle as O
+import warchest_wave as ww
+
+pytestmark = pytest.mark.gpu
+
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def pmap(fn, items):
+    with ThreadPoolExecutor(THREADS) as pool:
+        return list(pool.map(fn, items))
+
+
+def v5_jobs(trees=8, seed=31, **kw):
+    spec = dict(seed=seed, trees=trees, nodes_lo=30, nodes_hi=90, chance=1, terminal_p=0.1, notrans_p=0.05,
+                info_median=6.0, info_p99=40.0, info_cap=40, iters=16, nroots=2, dirichlet=1, depth=2, act_lo=3,
+                act_hi=8)
+    spec.update(kw)
+    return ww.synth_jobs(ww.V5_DIMS, **spec)
+
+
+_EX = {}
+
+
+def executor(precision):
+    if precision not in _EX:
+        _EX[precision] = ww.Executor(0, precision)
+    return _EX[precision]
+
+
+def device_probe(ex, jobs, net, p):
+    v = ex.publish(net)
+    wave = ww.Wave(jobs)
+    try:
+        return ex.leaf_probe(wave, v, p)
+    finally:
+        wave.close()
+
+
+def oracle_probe(jobs, net, mode, p):
+    out = pmap(lambda j: O.leaf_probe(j, net, mode, p), jobs)
+    return np.concatenate([v for v, _ in out]), np.concatenate([m for _, m in out])
+
+
+def test_v5_leaf_probe_float32_bit_exact():
+    jobs = v5_jobs()
+    net = ww.synth_weights(ww.V5_DIMS, 1)
+    ex = executor(ww.WC_PRECISE)
+    for p in (0, 1):
+        say(f"case v5 leaf probe float32: {len(jobs)} subgames, traverser {p}")
+        got, mass = device_probe(ex, jobs, net, p)
+        want, want_mass = oracle_probe(jobs, net, O.NET_F32, p)
+        np.testing.assert_array_equal(got, want)
+        np.testing.assert_array_equal(mass, want_mass)
+
+
+def test_v5_zero_network():
+    jobs = v5_jobs(trees=4, seed=33)
+    net = ww.synth_weights(ww.V5_DIMS, 1)
+    w = np.zeros_like(net.w)
+    b = np.zeros_like(net.b)
+    b[-1] = 0.375  # value_bias
+    zero = ww.Net(list(net.dims), w, b, net.ln)
+    for precision in (ww.WC_PRECISE, ww.WC_F16):
+        say(f"case v5 zero network: precision {precision}")
+        got, _ = device_probe(executor(precision), jobs, zero, 0)
+        assert got.size and np.all(got == np.float32(0.375))
+
+
+def test_v5_solve_float32_bit_exact():
+    jobs = v5_jobs(trees=6, seed=35)
+    net = ww.synth_weights(ww.V5_DIMS, 2)
+    say(f"case v5 solve float32: {len(jobs)} subgames, 16 iterations, 2 carried roots")
+    ex = executor(ww.WC_PRECISE)
+    v = ex.publish(net)
+    wave = ww.Wave(jobs)
+    got = ex.solve(wave, v)
+    wave.close()
+    refs = pmap(lambda j: O.solve(j, net, O.NET_F32), jobs)
+    for k, (g, o) in enumerate(zip(got, refs)):
+        np.testing.assert_array_equal(g.strategy, o["strategy"], err_msg=f"tree {k}: strategy")
+        np.testing.assert_array_equal(g.root_values, o["roots"], err_msg=f"tree {k}: root values")
+        np.testing.assert_array_equal(g.carries, o["carries"].astype(np.float16), err_msg=f"tree {k}: carries")
+
+
+@pytest.mark.parametrize("precision,mode,tol", [(ww.WC_F16, O.NET_F16A, 2e-3), (ww.WC_BF16, O.NET_BF16A, 1e-2)])
+def test_v5_leaf_probe_16bit_tracks_the_operand_model(precision, mode, tol):
+    jobs = v5_jobs(seed=37)
+    net = ww.synth_weights(ww.V5_DIMS, 1)
+    ex = executor(precision)
+    for p in (0, 1):
+        say(f"case v5 leaf probe precision {precision}: traverser {p}")
+        got, mass = device_probe(ex, jobs, net, p)
+        want, want_mass = oracle_probe(jobs, net, mode, p)
+        scale = float(np.abs(want).max())
+        err = np.abs(got.astype(np.float64) - want)
+        say(f"max error {err.max() / scale:.2e}, median {np.median(err) / scale:.2e} of the largest |value|")
+        assert err.max() <= tol * scale
+        assert np.median(err) <= 0.05 * tol * scale
+        np.testing.assert_allclose(mass, want_mass, rtol=2e-6, atol=1e-30)

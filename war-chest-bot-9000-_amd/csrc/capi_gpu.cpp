@@ -74,6 +74,11 @@ bool read_net(const wc_net_desc* net, NetCopy* out, std::string* err) {
     if (!out->ns.parse(out->dims, err)) return false;
     out->w.assign(net->w, net->w + net->nw);
     out->b.assign(net->b, net->b + net->nb);
+    if (net->nln && !net->ln) {
+        *err = "network description is incomplete";
+        return false;
+    }
+    out->ln.assign(net->ln, net->ln + net->nln);
     return true;
 }
 
@@ -110,7 +115,8 @@ uint64_t wc_executor_publish(wc_executor* ex, const wc_net_desc* net) {
         NetCopy n;
         std::string err;
         if (!read_net(net, &n, &err)) return fail(WC_ERR_INVALID, err);
-        v = ex->ex->publish(n.ns, n.dims, n.w.data(), n.w.size(), n.b.data(), n.b.size(), &err);
+        v = ex->ex->publish(n.ns, n.dims, n.w.data(), n.w.size(), n.b.data(), n.b.size(), &err, n.ln.data(),
+                            n.ln.size());
         return v ? WC_OK : fail(WC_ERR_INVALID, err);
     });
     return v;
@@ -202,6 +208,18 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
         s->leaf_input_bytes[p] = leaf_input_bytes(h, p, 2);
     }
     const NetShape& ns = h.net;
+    if (ns.kind == MODEL_V5) {
+        // Per pass: the join over every row (net.rs:801-841), plus one 256-long
+        // readout per (row, config) of the traverser (averaged over both).
+        const uint64_t join = 2ull * (uint64_t(v5::JOIN_IN) * v5::JW + uint64_t(v5::JBLOCKS) * v5::JW * v5::JW +
+                                      uint64_t(v5::JW) * v5::D);
+        s->mlp_flops_per_query = join + 2ull * v5::D;
+        const uint64_t slots = h.row_cfg.size();
+        const uint64_t tiles = h.tower_unit[0].size() + h.tower_unit[1].size();
+        s->mlp_flops_algorithmic = h.rows() * join + uint64_t(v5::D) * slots;
+        s->mlp_flops_executed = h.rows() * join + tiles * TOWER_TILE * TOWER_TILE * v5::D;
+        return WC_OK;
+    }
     if (ns.kind == MODEL_TWO_TOWER) {
         // Per pass: the public tower over every row, plus one width-long
         // readout per (row, config) of the traverser (averaged over both).

@@ -7,6 +7,7 @@
 #include "common.h"
 #include "job.h"
 #include "synth.h"
+#include "v5.h"
 
 namespace wc {
 thread_local std::string g_last_error;
@@ -38,7 +39,19 @@ int wc_net_sizes(const uint32_t* dims, uint32_t ndims, size_t* nw, size_t* nb) {
         *nb = size_t(ns.layers) * ns.hidden + size_t(ns.priv_layers) * ns.hidden + 1;
         return WC_OK;
     }
-    return fail(WC_ERR_UNSUPPORTED, "the v5 network bank is not built by this executor");
+    const v5::Layout L = v5::layout();  // net.rs:272-316
+    *nw = L.w_len;
+    *nb = L.b_len;
+    return WC_OK;
+}
+
+int wc_net_norms(const uint32_t* dims, uint32_t ndims, size_t* nln) {
+    if (!dims || !nln) return fail(WC_ERR_INVALID, "wc_net_norms: null argument");
+    NetShape ns;
+    std::string err;
+    if (!ns.parse(std::vector<uint32_t>(dims, dims + ndims), &err)) return fail(WC_ERR_INVALID, err);
+    *nln = ns.kind == MODEL_V5 ? v5::layout().ln_len : 0;
+    return WC_OK;
 }
 
 int wc_job_roundtrip(const uint8_t* job, size_t len, uint8_t* out, size_t cap, size_t* out_len) {
@@ -179,6 +192,21 @@ int wc_synth_weights(const uint32_t* dims, uint32_t ndims, uint64_t seed, float*
     }
     std::memcpy(w, vw.data(), nw * sizeof(float));
     std::memcpy(b, vb.data(), nb * sizeof(float));
+    return WC_OK;
+}
+
+int wc_synth_norms(const uint32_t* dims, uint32_t ndims, uint64_t seed, float* ln, size_t nln) {
+    size_t need = 0;
+    int rc = wc_net_norms(dims, ndims, &need);
+    if (rc) return rc;
+    if (nln != need || (need && !ln)) return fail(WC_ERR_INVALID, "wc_synth_norms: buffer size");
+    std::vector<float> v;
+    try {
+        synth_norms(std::vector<uint32_t>(dims, dims + ndims), seed, &v);
+    } catch (const std::exception& e) {
+        return fail(WC_ERR_INVALID, e.what());
+    }
+    if (need) std::memcpy(ln, v.data(), need * sizeof(float));
     return WC_OK;
 }
 

@@ -156,8 +156,64 @@ bool Executor::ensure_pinned(uint8_t** p, size_t* cap, size_t need, std::string*
     return true;
 }
 
+uint64_t Executor::publish_v5(const NetShape& ns, const float* w, size_t nw, const float* b, size_t nb,
+                              const float* ln, size_t nln, std::string* err) {
+    const v5::Layout L = v5::layout();
+    if (nw != L.w_len || nb != L.b_len || nln != L.ln_len || !w || !b || !ln) {
+        *err = "v5 weight bank sizes disagree with net.rs's layout (w " + std::to_string(L.w_len) + ", b " +
+               std::to_string(L.b_len) + ", ln " + std::to_string(L.ln_len) + ")";
+        return 0;
+    }
+    if (precision_ == WC_F16X) {
+        *err = "compensated f16 takes the MLP leaf network only";
+        return 0;
+    }
+    if (hipSetDevice(device_) != hipSuccess) {
+        *err = "hipSetDevice failed";
+        return 0;
+    }
+    // One allocation: the f32 blob (matrices, biases, norms) and the board tables.
+    const v5::Board bd = v5::board();
+    const size_t o_w = 0, o_b = align256(nw * 4), o_ln = o_b + align256(nb * 4), o_bd = o_ln + align256(nln * 4);
+    const size_t total = o_bd + align256(sizeof bd);
+    void* mem = nullptr;
+    if (hipMalloc(&mem, total) != hipSuccess) {
+        *err = "hipMalloc of the weight bank failed";
+        return 0;
+    }
+    char* base = (char*)mem;
+    bool okc = hipMemcpyAsync(base + o_w, w, nw * 4, hipMemcpyHostToDevice, stream_) == hipSuccess &&
+               hipMemcpyAsync(base + o_b, b, nb * 4, hipMemcpyHostToDevice, stream_) == hipSuccess &&
+               hipMemcpyAsync(base + o_ln, ln, nln * 4, hipMemcpyHostToDevice, stream_) == hipSuccess &&
+               hipMemcpyAsync(base + o_bd, &bd, sizeof bd, hipMemcpyHostToDevice, stream_) == hipSuccess &&
+               hipStreamSynchronize(stream_) == hipSuccess;
+    if (!okc) {
+        hipFree(mem);
+        *err = "weight upload failed";
+        return 0;
+    }
+    NetBank bank;
+    bank.ns = ns;
+    bank.precision = precision_;
+    bank.mem = mem;
+    bank.v5.w = (const float*)(base + o_w);
+    bank.v5.b = (const float*)(base + o_b);
+    bank.v5.ln = (const float*)(base + o_ln);
+    bank.v5.nb = (const uint8_t*)(base + o_bd) + offsetof(v5::Board, nb);
+    bank.v5.loc = (const uint8_t*)(base + o_bd) + offsetof(v5::Board, loc);
+    bank.v5.value_bias = b[L.value_bias];
+    bank.version = next_version_++;
+    banks_[bank.version] = bank;
+    return bank.version;
+}
+
 uint64_t Executor::publish(const NetShape& ns, const std::vector<uint32_t>& dims, const float* w, size_t nw,
-                           const float* b, size_t nb, std::string* err) {
+                           const float* b, size_t nb, std::string* err, const float* ln, size_t nln) {
+    if (ns.kind == MODEL_V5) return publish_v5(ns, w, nw, b, nb, ln, nln, err);
+    if (nln) {
+        *err = "the synthetic networks take no LayerNorm parameters";
+        return 0;
+    }
     const bool tower = ns.kind == MODEL_TWO_TOWER;
     if (ns.kind != MODEL_MLP && !tower) {
         *err = "this executor builds the MLP and two-tower leaf networks only";
@@ -316,7 +372,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
         size_t node_meta, nc, legal_value, draw_to, draw_p, reach_base, vals_base, rev_src, rev_cell, rvd_src, rvd_p,
             row_node, row_cfg_off, row_cfg, cfg_emb, pub_raw, term_node, term_util, roots, carried, exit_node,
             exit_coff, trees, units, bt[2], rt[2], dc[2], bl[2], rl[2], cv[2], lr[2], pg[2], twb[2], twu[2], cfg_priv,
-            unit_term, tb[2], tr[2], head_tile_n, cp[2];
+            unit_term, tb[2], tr[2], head_tile_n, cp[2], card_feat, row_job, cfg_job, cfg_owner;
     } o;
     o.node_meta = blob.put(w.node_meta);
     o.nc = blob.put(w.node_nc);
@@ -334,6 +390,10 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
     o.row_cfg = blob.put(w.row_cfg);
     o.cfg_emb = blob.put(w.cfg_emb);
     o.cfg_priv = blob.put(w.cfg_priv);
+    o.card_feat = blob.put(w.card_feat);
+    o.row_job = blob.put(w.row_job);
+    o.cfg_job = blob.put(w.cfg_job);
+    o.cfg_owner = blob.put(w.cfg_owner);
     o.pub_raw = blob.put(w.pub_raw);
     o.term_node = blob.put(w.term_node);
     o.term_util = blob.put(w.term_util);
@@ -402,14 +462,16 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
         return a;
     };
     const size_t prow = precision_ == WC_PRECISE ? rows : gemm_rows((uint32_t)rows);  // GEMM operands: padded rows
-    const bool tower = ns.kind == MODEL_TWO_TOWER;
+    const bool tower = ns.kind == MODEL_TWO_TOWER, v5net = ns.kind == MODEL_V5;
     const size_t ncfg = w.cfg_key.size(), pcfg = precision_ == WC_PRECISE ? ncfg : gemm_rows((uint32_t)ncfg);
-    size_t m_x = mtake(prow * ns.in * esz), m_x1 = mtake(prow * ns.in * esz), m_h0 = mtake(prow * ns.hidden * esz),
+    // Query-input width: the v5 join's 129 columns padded to whole k steps as a 16-bit operand.
+    const size_t xin = v5net && precision_ != WC_PRECISE ? v5::JOIN_IN_PAD : ns.in;
+    size_t m_x = mtake(prow * xin * esz), m_x1 = mtake(prow * xin * esz), m_h0 = mtake(prow * ns.hidden * esz),
            m_h1 = mtake(prow * ns.hidden * esz),
-           m_out = mtake(tower ? w.tower_len * 4 : rows * ns.heads * 4);
+           m_out = mtake(readout_net(ns.kind) ? w.tower_len * 4 : rows * ns.heads * 4);
     // The fused net's first-layer product over the fixed query columns, when
     // the pooled columns are whole 32-column k steps ahead of them.
-    const bool split = split_ && !tower && (precision_ == WC_F16 || precision_ == WC_BF16) &&
+    const bool split = split_ && ns.kind == MODEL_MLP && (precision_ == WC_F16 || precision_ == WC_BF16) &&
                        chain_fits(ns.in, ns.hidden, ns.layers) && ns.pool > 0 && ns.in > 2 * ns.pool &&
                        (2 * ns.pool) % 32 == 0;
     size_t m_s0 = split ? mtake(prow * ns.hidden * 4) : 0, m_s1 = split ? mtake(prow * ns.hidden * 4) : 0;
@@ -419,6 +481,18 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
         m_p0 = mtake(pcfg * ns.hidden * esz);
         m_p1 = mtake(pcfg * ns.hidden * esz);
         m_f = mtake(ncfg * ns.hidden * esz);
+    }
+    // v5: cards and bag rows per job, P and Jp per row, g and f per config, the join's input scratch.
+    const size_t njobs = w.trees.size();
+    size_t m_cards = 0, m_bag = 0, m_P = 0, m_Jp = 0, m_G = 0, m_F = 0, m_xf = 0;
+    if (v5net) {
+        m_cards = mtake(njobs * 2 * v5::NTYPE * v5::TYPE * 4);
+        m_bag = mtake(njobs * 2 * v5::NTYPE * 3 * v5::POOL * 4);
+        m_P = mtake(rows * v5::D * 4);
+        m_Jp = mtake(rows * v5::JW * 4);
+        m_G = mtake(ncfg * v5::POOL * 4);
+        m_F = mtake(ncfg * v5::D * esz);
+        m_xf = mtake(precision_ == WC_PRECISE ? 0 : rows * v5::JOIN_IN * 4);
     }
     if (!ensure(&mlp_, &mlp_cap_, mt, err)) return false;
 
@@ -491,10 +565,10 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
     d.ntrees = (uint32_t)w.trees.size();
     d.rows = w.rows();
     d.pool = ns.pool;
-    d.in = ns.in;
-    d.row_bytes = ns.row_bytes;
+    d.in = (uint32_t)xin;
+    d.row_bytes = v5net ? 0 : ns.row_bytes;  // v5: the public bytes feed the trunk, not the query input
     d.snapshot_configs = w.snapshot_configs;
-    d.xplane = uint64_t(prow) * ns.in;
+    d.xplane = uint64_t(prow) * xin;
     d.nexit = (uint32_t)w.exit_node.size();
     d.ncells = w.ncells;
     X_ = M + m_x;
@@ -512,6 +586,28 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
     F_ = tower ? M + m_f : nullptr;
     ncfg_ = tower ? (uint32_t)ncfg : 0;
     rows_ = w.rows();
+    v5_in_ = v5::WaveIn{};
+    v5_out_ = v5::WaveOut{};
+    v5_xf_ = nullptr;
+    if (v5net) {
+        v5_in_.jobs = (uint32_t)njobs;
+        v5_in_.rows = (uint32_t)rows;
+        v5_in_.ncfg = (uint32_t)ncfg;
+        v5_in_.card_feat = (const float*)(T + o.card_feat);
+        v5_in_.raw = (const uint8_t*)(T + o.pub_raw);
+        v5_in_.row_job = (const uint32_t*)(T + o.row_job);
+        v5_in_.phi = (const float*)(T + o.cfg_priv);
+        v5_in_.cfg_job = (const uint32_t*)(T + o.cfg_job);
+        v5_in_.cfg_owner = (const uint8_t*)(T + o.cfg_owner);
+        v5_out_.cards = (float*)(M + m_cards);
+        v5_out_.bag = (float*)(M + m_bag);
+        v5_out_.P = (float*)(M + m_P);
+        v5_out_.Jp = (float*)(M + m_Jp);
+        v5_out_.G = (float*)(M + m_G);
+        v5_out_.F = M + m_F;
+        v5_xf_ = precision_ == WC_PRECISE ? nullptr : (float*)(M + m_xf);
+        d.cfg_emb = v5_out_.G;  // the pooled beliefs pool g(c) (search.rs:1525-1545)
+    }
     launch_query_static(d, precision_, Xq_[0], Xq_[1], stream_);
     HIP_TRY(hipGetLastError());
     return true;
@@ -624,8 +720,17 @@ const NetBank* Executor::bank_of(uint64_t version, std::string* err) const {
     return &it->second;
 }
 
+void Executor::run_v5_build(const NetBank& bank) { v5::launch_build(precision_, bank.v5, v5_in_, v5_out_, stream_); }
+
+void Executor::run_v5(const NetBank& bank, int traverser) {
+    v5::launch_join(precision_, bank.v5, dev_.rows, Xq_[traverser], v5_out_.P, v5_out_.Jp, H_[0], v5_xf_, stream_);
+    launch_tower_head(dev_, traverser, precision_, H_[0], v5::D, v5_out_.F, bank.v5.value_bias, head_out_, stream_);
+}
+
 void Executor::leaf_net(const NetBank& bank, int q) {
-    if (bank.ns.kind == MODEL_TWO_TOWER)
+    if (bank.ns.kind == MODEL_V5)
+        run_v5(bank, q);
+    else if (bank.ns.kind == MODEL_TWO_TOWER)
         run_tower(bank, dev_.rows, q);
     else
         run_mlp(bank, dev_.rows, Xq_[q], nullptr, head_tile_n_, chain_plan_[q], chain_npass_[q], S_[q]);
@@ -700,6 +805,10 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     }
     const bool tower = bank.ns.kind == MODEL_TWO_TOWER;
     if (tower) run_tower_private(bank);  // F for this wave's configs under this bank
+    if (bank.ns.kind == MODEL_V5) {
+        run_v5_build(bank);  // cards, trunk, configs for this wave under this bank
+        mark(C_MLP);
+    }
     if (S_[0]) {
         static_products(bank);
         mark(C_MLP);
@@ -950,11 +1059,12 @@ bool Executor::leaf_probe(const WaveHost& w, uint64_t version, int traverser, st
     }
     if (!upload(w, *bank, 0, err)) return false;
     if (bank->ns.kind == MODEL_TWO_TOWER) run_tower_private(*bank);
+    if (bank->ns.kind == MODEL_V5) run_v5_build(*bank);
     static_products(*bank);
     init_state(w);
     leaf_net(*bank, traverser);
     HIP_TRY(hipGetLastError());
-    const size_t nout = bank->ns.kind == MODEL_TWO_TOWER ? w.tower_len : size_t(w.rows()) * bank->ns.heads;
+    const size_t nout = readout_net(bank->ns.kind) ? w.tower_len : size_t(w.rows()) * bank->ns.heads;
     std::vector<float> head(nout);
     mass->assign(size_t(w.rows()) * 2, 0.0f);
     if (nout) HIP_TRY(hipMemcpyAsync(head.data(), head_out_, nout * 4, hipMemcpyDeviceToHost, stream_));

@@ -12,6 +12,7 @@
 
 #include "job.h"
 #include "kernels.h"
+#include "v5.h"
 #include "wave.h"
 
 namespace wc {
@@ -31,6 +32,8 @@ struct NetBank {
     const float* PB[16] = {};
     const float* wread = nullptr;
     float bread = 0.0f;
+    // v5 network: the device view of its blob and board tables.
+    v5::Net v5;
 };
 
 struct Result {
@@ -89,7 +92,7 @@ class Executor {
 
     // Publish an immutable weight bank; returns its version (0 on failure).
     uint64_t publish(const NetShape& ns, const std::vector<uint32_t>& dims, const float* w, size_t nw,
-                     const float* b, size_t nb, std::string* err);
+                     const float* b, size_t nb, std::string* err, const float* ln = nullptr, size_t nln = 0);
     void retain_from(uint64_t oldest);
     bool has_version(uint64_t v) const { return banks_.count(v) != 0; }
 
@@ -151,6 +154,12 @@ class Executor {
     // Two-tower net: F for the uploaded wave's configs, then one traverser's public tower and readout.
     void run_tower_private(const NetBank& bank);
     void run_tower(const NetBank& bank, uint32_t rows, int traverser);
+    // v5 network: publish its bank; the per-wave build (cards, trunk, configs)
+    // for the uploaded wave under a bank, then per iteration the join and the readout.
+    uint64_t publish_v5(const NetShape& ns, const float* w, size_t nw, const float* b, size_t nb, const float* ln,
+                        size_t nln, std::string* err);
+    void run_v5_build(const NetBank& bank);
+    void run_v5(const NetBank& bank, int traverser);
     // The MLP over `rows` query rows: the fused kernel over `plan` (npass
     // passes, device copy) where it applies, else layer by layer (head width
     // per 128-row tile: head_tile_n).
@@ -214,6 +223,11 @@ class Executor {
     void* F_ = nullptr;
     uint32_t ncfg_ = 0;
     uint32_t rows_ = 0;
+    // v5 network: the uploaded wave's build inputs, its per-wave outputs and
+    // the join's float32 input scratch (16-bit path).
+    v5::WaveIn v5_in_{};
+    v5::WaveOut v5_out_{};
+    float* v5_xf_ = nullptr;
     void* scratch_ = nullptr;  // the allocation-free scratch on this device
     std::string scratch_err_;
     bool split_ = true;  // WC_CHAIN_SPLIT=0 turns the first layer's fixed-column product off

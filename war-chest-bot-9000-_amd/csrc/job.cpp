@@ -19,7 +19,12 @@ bool NetShape::parse(const std::vector<uint32_t>& dims, std::string* err) {
             if (err) *err = "v5 net_dims must be exactly [5]";
             return false;
         }
-        row_bytes = 0;  // checked by the v5 path, which this executor does not run
+        // The join reads both pooled beliefs and the seat; the trunk reads the
+        // row's public bytes (rebel.rs:966-986); the readout is 256 wide.
+        in = 2 * 64 + 1;
+        hidden = 256;
+        pool = 64;
+        row_bytes = V5_ROW_BYTES;
         cfeat = V5_CFEAT;
         card_feat = V5_CARD_FEAT;
         return true;
@@ -341,7 +346,7 @@ bool from_bytes(const uint8_t* b, size_t n, Job* out, std::string* err) {
         !check(t.cfg_off.size(), 2 * nodes + 1, "cfg_off", err) ||
         !check(t.cphi.size(), size_t(t.ncfg) * ns.cfeat, "cphi", err) ||
         !check(t.cplayer.size(), t.ncfg, "cplayer", err) ||
-        (ns.kind != MODEL_V5 && !check(t.leaf_raw.size(), size_t(t.rows) * ns.row_bytes, "leaf_raw", err)) ||
+        !check(t.leaf_raw.size(), size_t(t.rows) * ns.row_bytes, "leaf_raw", err) ||
         !check(t.card_feat.size(), ns.card_feat, "card_feat", err) ||
         !check(t.leaf_coff.size(), 2 * size_t(t.rows) + 1, "leaf_coff", err) ||
         !check(t.node_parent.size(), nodes, "node_parent", err) ||

@@ -30,6 +30,11 @@ enum ModelKind : uint32_t {
 // v5 payload widths (engine/src/rebel.rs:61-71,891,985-986; units.rs:46,71).
 constexpr uint32_t V5_CFEAT = 15;
 constexpr uint32_t V5_CARD_FEAT = 10 * (10 + 12 + 2 + 1);
+constexpr uint32_t V5_ROW_BYTES = 201;  // GPU_ROW_BYTES (rebel.rs:986)
+
+// The families whose leaf value is a readout <f(c), h(row)> + bias per
+// (row, config): the two-tower net and the v5 network (net.rs:844-853).
+inline bool readout_net(uint32_t kind) { return kind == MODEL_TWO_TOWER || kind == MODEL_V5; }
 
 struct Cfr {
     float alpha = 1.5f, beta = 0.0f, gamma = 2.0f, predict = 0.0f;

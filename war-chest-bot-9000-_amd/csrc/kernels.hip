@@ -544,7 +544,8 @@ __global__ void k_query_static(WaveDev w, void* x0, void* x1) {
         store_operand<PREC>(x0, at, -1.0f, w.xplane);
         store_operand<PREC>(x1, at, 1.0f, w.xplane);
     } else {
-        float v = (float)w.pub_raw[(size_t)row * w.row_bytes + (k - 1)] / 255.0f;
+        // public features; columns past them (a 16-bit operand's k padding) are zero
+        const float v = k - 1 < w.row_bytes ? (float)w.pub_raw[(size_t)row * w.row_bytes + (k - 1)] / 255.0f : 0.0f;
         store_operand<PREC>(x0, at, v, w.xplane);
         store_operand<PREC>(x1, at, v, w.xplane);
     }

@@ -97,12 +97,14 @@ uint64_t device_arena_bytes(const Job& j, int precision) {
     const uint64_t prow = precision == WC_PRECISE ? rows : (rows + GEMM_ROWS - 1) / GEMM_ROWS * GEMM_ROWS;
     const uint64_t ncfg = t.ncfg, pcfg = precision == WC_PRECISE ? ncfg : (ncfg + GEMM_ROWS - 1) / GEMM_ROWS * GEMM_ROWS;
     uint64_t mlp = 0;
-    take(&mlp, sat_mul(sat_mul(prow, ns.in), esz));
-    take(&mlp, sat_mul(sat_mul(prow, ns.in), esz));
+    const bool v5net = ns.kind == MODEL_V5;
+    const uint64_t xin = v5net && precision != WC_PRECISE ? v5::JOIN_IN_PAD : ns.in;
+    take(&mlp, sat_mul(sat_mul(prow, xin), esz));
+    take(&mlp, sat_mul(sat_mul(prow, xin), esz));
     take(&mlp, sat_mul(sat_mul(prow, ns.hidden), esz));
     take(&mlp, sat_mul(sat_mul(prow, ns.hidden), esz));
-    take(&mlp, tower ? sat_mul(sat_mul(rows, ncfg), 4) : sat_mul(sat_mul(rows, ns.heads), 4));
-    const bool split = !tower && (precision == WC_F16 || precision == WC_BF16) &&
+    take(&mlp, readout_net(ns.kind) ? sat_mul(sat_mul(rows, ncfg), 4) : sat_mul(sat_mul(rows, ns.heads), 4));
+    const bool split = ns.kind == MODEL_MLP && (precision == WC_F16 || precision == WC_BF16) &&
                        chain_fits(ns.in, ns.hidden, ns.layers) && ns.pool > 0 && ns.in > 2 * ns.pool &&
                        (2 * ns.pool) % 32 == 0;
     if (split) {
@@ -114,6 +116,15 @@ uint64_t device_arena_bytes(const Job& j, int precision) {
         take(&mlp, sat_mul(sat_mul(pcfg, ns.hidden), esz));
         take(&mlp, sat_mul(sat_mul(pcfg, ns.hidden), esz));
         take(&mlp, sat_mul(sat_mul(ncfg, ns.hidden), esz));
+    }
+    if (v5net) {  // cards and bag rows, P and Jp, g and f, the join's input scratch
+        take(&mlp, 2ull * v5::NTYPE * v5::TYPE * 4);
+        take(&mlp, 2ull * v5::NTYPE * 3 * v5::POOL * 4);
+        take(&mlp, sat_mul(rows, v5::D * 4));
+        take(&mlp, sat_mul(rows, v5::JW * 4));
+        take(&mlp, sat_mul(ncfg, v5::POOL * 4));
+        take(&mlp, sat_mul(ncfg, v5::D * esz));
+        take(&mlp, precision == WC_PRECISE ? 0 : sat_mul(rows, v5::JOIN_IN * 4));
     }
     return sat_add(next_pow2_or_self(arena), next_pow2_or_self(mlp));
 }
@@ -337,7 +348,8 @@ void Service::lane_main(uint32_t lane) {
             net = current_;
         }
         if (ok && net) {
-            uint64_t v = ex->publish(net->ns, net->dims, net->w.data(), net->w.size(), net->b.data(), net->b.size(), &err);
+            uint64_t v = ex->publish(net->ns, net->dims, net->w.data(), net->w.size(), net->b.data(), net->b.size(), &err,
+                                     net->ln.data(), net->ln.size());
             ok = v != 0;
             if (ok) bank_of[net->version] = v;
         }
@@ -434,7 +446,8 @@ void Service::lane_main(uint32_t lane) {
         uint64_t exv = 0;
         auto found = bank_of.find(net->version);
         if (found == bank_of.end()) {
-            exv = ex->publish(net->ns, net->dims, net->w.data(), net->w.size(), net->b.data(), net->b.size(), &err);
+            exv = ex->publish(net->ns, net->dims, net->w.data(), net->w.size(), net->b.data(), net->b.size(), &err,
+                                     net->ln.data(), net->ln.size());
             ok = exv != 0;
             if (ok) {
                 bank_of[net->version] = exv;

@@ -75,7 +75,7 @@ struct NetCopy {
     uint64_t version = 0;
     NetShape ns;
     std::vector<uint32_t> dims;
-    std::vector<float> w, b;
+    std::vector<float> w, b, ln;
 };
 
 class Service {

@@ -6,6 +6,8 @@
 // appearance, reverse gathers in the CPU accumulation order, BFS levels.
 #include "synth.h"
 
+#include "v5.h"
+
 #include <algorithm>
 #include <atomic>
 #include <cmath>
@@ -64,6 +66,35 @@ void feature_bytes(Rng& r, uint8_t* out, uint32_t width) {
         }
     }
     for (uint32_t k = full; k < width; k++) out[k] = q(r.unit());
+}
+
+// One synthetic public row of the v5 contract (rebel.rs:966-986): hex
+// occupants, stack heights and location markers, pile counts, the players'
+// marker, hand, face-down and bag sizes, initiative, the player to act and
+// the plies remaining.
+void v5_public_row(Rng& r, uint8_t* raw) {
+    for (uint32_t h = 0; h < 37; h++) {
+        const double u = r.unit();
+        const uint8_t owner = u < 0.2 ? 0 : u < 0.4 ? 1 : 255;
+        raw[h] = owner;
+        raw[37 + h] = owner == 255 ? 255 : (uint8_t)r.below(5);
+        raw[74 + h] = owner == 255 ? 0 : (uint8_t)(1 + r.below(5));
+        const double m = r.unit();
+        raw[111 + h] = m < 0.15 ? 0 : m < 0.3 ? 1 : 255;
+    }
+    for (uint32_t k = 0; k < 40; k++) raw[148 + k] = (uint8_t)r.below(6);
+    for (uint32_t p = 0; p < 2; p++) {
+        raw[188 + p] = (uint8_t)r.below(7);
+        raw[190 + p] = (uint8_t)r.below(4);
+        raw[192 + p] = (uint8_t)r.below(15);
+        raw[194 + p] = (uint8_t)r.below(19);
+    }
+    raw[196] = (uint8_t)r.below(2);
+    raw[197] = (uint8_t)r.below(2);
+    raw[198] = (uint8_t)r.below(2);
+    const uint32_t plies = r.below(257);
+    raw[199] = (uint8_t)(plies & 0xff);
+    raw[200] = (uint8_t)(plies >> 8);
 }
 
 uint32_t lognormal_count(Rng& r, float median, float p99, uint32_t cap) {
@@ -312,7 +343,22 @@ Job build_job(Rng& r, const SynthSpec& s, const NetShape& ns, bool whale) {
     // Per-tree infostate features: the pooled-belief embedding (and, for the
     // two-tower net, the private-tower input) of every config key.
     std::vector<float> emb[2], priv[2];
-    for (int p = 0; p < 2; p++) {
+    const bool v5 = ns.kind == MODEL_V5;
+    for (int p = 0; p < 2 && v5; p++) {
+        // v5: a config's hand, face-down and bag counts per coin slot, over the
+        // count normaliser (search.rs:1433-1458, CNORM = 5)
+        emb[p].resize(size_t(nroot[p]) * V5_CFEAT);
+        for (uint32_t k = 0; k < nroot[p]; k++) {
+            float* c = &emb[p][size_t(k) * V5_CFEAT];
+            uint32_t hand = r.below(4), fd = r.below(5);
+            for (uint32_t q = 0; q < V5_CFEAT; q++) c[q] = 0.0f;
+            for (uint32_t x = 0; x < hand; x++) c[r.below(5)] += 1.0f;
+            for (uint32_t x = 0; x < fd; x++) c[5 + r.below(5)] += 1.0f;
+            for (uint32_t q = 0; q < 5; q++) c[10 + q] = (float)r.below(4);
+            for (uint32_t q = 0; q < V5_CFEAT; q++) c[q] /= 5.0f;
+        }
+    }
+    for (int p = 0; p < 2 && !v5; p++) {
         emb[p].resize(size_t(nroot[p]) * ns.pool);
         for (uint32_t k = 0; k < nroot[p]; k++) feature_floats(r, &emb[p][size_t(k) * ns.pool], ns.pool);
         if (ns.priv_in) {
@@ -469,12 +515,17 @@ Job build_job(Rng& r, const SynthSpec& s, const NetShape& ns, bool whale) {
                     uint32_t idx = (uint32_t)t.cplayer.size();
                     it = intern.emplace(k, idx).first;
                     t.cplayer.push_back((uint8_t)p);
-                    t.cphi.push_back((float)key);
-                    const float* e = &emb[p][size_t(key) * ns.pool];
-                    t.cphi.insert(t.cphi.end(), e, e + ns.pool);
-                    if (ns.priv_in) {
-                        const float* q = &priv[p][size_t(key) * ns.priv_in];
-                        t.cphi.insert(t.cphi.end(), q, q + ns.priv_in);
+                    if (v5) {
+                        const float* e = &emb[p][size_t(key) * V5_CFEAT];
+                        t.cphi.insert(t.cphi.end(), e, e + V5_CFEAT);
+                    } else {
+                        t.cphi.push_back((float)key);
+                        const float* e = &emb[p][size_t(key) * ns.pool];
+                        t.cphi.insert(t.cphi.end(), e, e + ns.pool);
+                        if (ns.priv_in) {
+                            const float* q = &priv[p][size_t(key) * ns.priv_in];
+                            t.cphi.insert(t.cphi.end(), q, q + ns.priv_in);
+                        }
                     }
                 }
                 t.leaf_cidx.push_back(it->second);
@@ -485,8 +536,23 @@ Job build_job(Rng& r, const SynthSpec& s, const NetShape& ns, bool whale) {
     t.rows = (uint32_t)t.leaf_rows.size();
     t.ncfg = (uint32_t)t.cplayer.size();
     t.leaf_raw.resize(size_t(t.rows) * ns.row_bytes);
-    for (uint32_t row = 0; row < t.rows; row++)
-        feature_bytes(r, &t.leaf_raw[size_t(row) * ns.row_bytes], ns.row_bytes);
+    for (uint32_t row = 0; row < t.rows; row++) {
+        uint8_t* raw = &t.leaf_raw[size_t(row) * ns.row_bytes];
+        if (v5)
+            v5_public_row(r, raw);
+        else
+            feature_bytes(r, raw, ns.row_bytes);
+    }
+    if (v5) {  // the printed facts of the ten coin types in play (units.rs:71-110 widths)
+        t.card_feat.resize(V5_CARD_FEAT);
+        for (uint32_t ty = 0; ty < 10; ty++) {
+            float* f = &t.card_feat[size_t(ty) * 25];
+            for (uint32_t q = 0; q < 10; q++) f[q] = r.unit() < 0.3 ? 1.0f : 0.0f;
+            for (uint32_t q = 10; q < 22; q++) f[q] = (float)r.below(6) / 5.0f;
+            for (uint32_t q = 22; q < 24; q++) f[q] = r.unit() < 0.5 ? 1.0f : 0.0f;
+            f[24] = (float)r.unit();
+        }
+    }
     uint32_t snap_at = 0;
     auto exits = t.leaf_rows;
     exits.insert(exits.end(), t.term_leaves.begin(), t.term_leaves.end());
@@ -552,7 +618,6 @@ std::vector<Job> synth_jobs(const SynthSpec& spec) {
     NetShape ns;
     std::string err;
     if (!ns.parse(spec.net_dims, &err)) throw std::runtime_error(err);
-    if (ns.kind == MODEL_V5) throw std::runtime_error("synthetic jobs need a synthetic value-net tag");
     // Tree k's stream is the k-th draw of the master stream, so the trees are
     // independent and built on several host threads.
     Rng master(spec.seed);
@@ -614,8 +679,55 @@ void synth_weights(const std::vector<uint32_t>& dims, uint64_t seed, std::vector
         for (uint32_t l = 0; l < ns.priv_layers; l++) bias(ns.hidden);
         bias(1);
     } else {
-        throw std::runtime_error("synthetic weights need a synthetic value-net tag");
+        // v5 (net.rs:272-316): every matrix Kaiming-normal over its fan-in,
+        // the seat and position embeddings N(0, 0.25), biases U[-0.1, 0.1].
+        const v5::Layout L = v5::layout();
+        w->assign(L.w_len, 0.0f);
+        b->assign(L.b_len, 0.0f);
+        auto fill = [&](const v5::Span& sp) {
+            const double sd = std::sqrt(2.0 / (double)sp.i);
+            for (size_t k = 0; k < size_t(sp.i) * sp.o; k++) (*w)[sp.w + k] = (float)(sd * r.normal());
+            if (sp.bias)
+                for (uint32_t k = 0; k < sp.o; k++) (*b)[sp.b + k] = (float)(0.2 * r.unit() - 0.1);
+        };
+        auto embed = [&](uint32_t at, uint32_t n) {
+            for (uint32_t k = 0; k < n; k++) (*w)[at + k] = (float)(0.5 * r.normal());
+        };
+        fill(L.card[0]);
+        fill(L.card[1]);
+        fill(L.pile);
+        embed(L.seat, 2 * v5::TYPE);
+        fill(L.hex_stem);
+        fill(L.tok_stem);
+        embed(L.pos, v5::HEXES * v5::C);
+        fill(L.glob_stem);
+        for (uint32_t i = 0; i < v5::BLOCKS; i++) {
+            fill(L.mix[i]);
+            fill(L.pool[i]);
+            fill(L.out[i]);
+        }
+        for (const v5::Span* sp : {&L.board_out, &L.cfg1, &L.cfg_f, &L.cfg_g, &L.cfg_m, &L.join_p, &L.join_b})
+            fill(*sp);
+        for (uint32_t i = 0; i < v5::JBLOCKS; i++) fill(L.join_w[i]);
+        fill(L.join_out);
+        (*b)[L.value_bias] = (float)(0.2 * r.unit() - 0.1);
     }
+}
+
+void synth_norms(const std::vector<uint32_t>& dims, uint64_t seed, std::vector<float>* ln) {
+    NetShape ns;
+    std::string err;
+    if (!ns.parse(dims, &err)) throw std::runtime_error(err);
+    ln->clear();
+    if (ns.kind != MODEL_V5) return;
+    const v5::Layout L = v5::layout();
+    Rng r(seed ^ 0x4c4e4c4e4c4e4c4eull);
+    ln->assign(L.ln_len, 0.0f);
+    for (uint32_t i = 0; i < v5::NORMS; i++)
+        for (uint32_t k = 0; k < L.norm_width[i]; k++) {
+            (*ln)[L.norm_g[i] + k] = (float)(1.0 + 0.1 * r.normal());
+            (*ln)[L.norm_b[i] + k] = (float)(0.1 * r.normal());
+        }
 }
 
 void synth_features(uint32_t rows, uint32_t width, uint64_t seed, std::vector<float>* x) {

@@ -80,8 +80,13 @@ std::vector<Job> synth_jobs(const SynthSpec& spec);
 // Two-tower: w = public tower (in x width, width x width ...), private tower
 //      (priv_in x width, width x width ...), readout weight [width]; b = matching biases
 //      and one readout bias.
+// v5: w, b in the flat blob order of net.rs:272-316 (Kaiming-normal matrices,
+//      N(0, 0.25) embeddings, U[-0.1, 0.1] biases).
 void synth_weights(const std::vector<uint32_t>& dims, uint64_t seed, std::vector<float>* w,
                    std::vector<float>* b);
+// LayerNorm pairs of a family (v5: gains 1 + N(0, 0.01), shifts N(0, 0.01);
+// empty for the synthetic families).
+void synth_norms(const std::vector<uint32_t>& dims, uint64_t seed, std::vector<float>* ln);
 
 // Dense leaf-query features (U[0,1) with 30% of dims in one-hot blocks of width 8).
 void synth_features(uint32_t rows, uint32_t width, uint64_t seed, std::vector<float>* x);

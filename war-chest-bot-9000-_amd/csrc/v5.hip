@@ -1,0 +1,671 @@
+// The v5 leaf network on the device (engine/src/net.rs; the reference's
+// device path: engine/src/gpu/device.rs:836-1106 per wave, 1218-1305 per
+// iteration, wave_kernels.cu:301-579,778-830).
+//
+// Layout in HBM. Per wave: the card tokens of both seat views and their bag
+// rows per job, the board vector P (D floats) and its join projection Jp (JW
+// floats) per network row, f(c) (D) and g(c) (POOL) per interned config. The
+// trunk's activations (37 hexes x 96 channels per row) never leave LDS: one
+// workgroup carries a row from its raw bytes to P and Jp. Per iteration: the
+// join's activations stay in LDS too, one workgroup per tile of rows, from the
+// pooled query input to h.
+//
+// Arithmetic. WC_PRECISE follows the CPU net's loop order exactly (every
+// product of a Lin summed from the start value over ascending inputs,
+// skipping zero inputs, then the bias; LayerNorm and GELU in net.rs order;
+// tanh by the restatement's own formula below), so float32 results are
+// bit-identical to the CPU restatement. The 16-bit precisions round the
+// operands of the GEMMs the reference's fast mode runs on tensor cores.
+#include "v5.h"
+
+#include <algorithm>
+#include <cmath>
+
+#include "../../include/wc_wave.h"
+#include "kernels.h"
+
+namespace wc {
+namespace v5 {
+
+// ------------------------------------------------------------- host side
+
+namespace {
+struct Cursor {
+    uint32_t w = 0, b = 0, ln = 0;
+    Span lin(uint32_t i, uint32_t o, bool bias) {
+        Span s;
+        s.w = w;
+        s.b = bias ? b : 0;
+        s.i = i;
+        s.o = o;
+        s.bias = bias;
+        w += i * o;
+        if (bias) b += o;
+        return s;
+    }
+    uint32_t embed(uint32_t n) {
+        const uint32_t at = w;
+        w += n;
+        return at;
+    }
+};
+}  // namespace
+
+Layout layout() {
+    Layout L;
+    Cursor c;
+    L.card[0] = c.lin(CARD_FEATS, TYPE, true);
+    L.card[1] = c.lin(TYPE, TYPE, true);
+    L.pile = c.lin(PILE_COUNTS, TYPE, false);
+    L.seat = c.embed(2 * TYPE);
+    L.hex_stem = c.lin(HEX_FACTS, C, true);
+    L.tok_stem = c.lin(TYPE, C, false);
+    L.pos = c.embed(HEXES * C);
+    L.glob_stem = c.lin(LOOSE, C, false);
+    for (uint32_t i = 0; i < BLOCKS; i++) {
+        L.mix[i] = c.lin(2 * C, C, true);
+        L.pool[i] = c.lin(2 * C, C, true);
+        L.out[i] = c.lin(C, C, true);
+    }
+    L.board_out = c.lin(2 * C + LOOSE, D, true);
+    L.cfg1 = c.lin(3 + TYPE, CFGH, true);
+    L.cfg_f = c.lin(CFGH, D, true);
+    L.cfg_g = c.lin(CFGH, POOL, true);
+    L.cfg_m = c.lin(TYPE, 3 * POOL, false);
+    L.join_p = c.lin(D, JW, false);
+    L.join_b = c.lin(JOIN_IN, JW, true);
+    for (uint32_t i = 0; i < JBLOCKS; i++) L.join_w[i] = c.lin(JW, JW, true);
+    L.join_out = c.lin(JW, D, true);
+    L.value_bias = c.b;
+    c.b += 1;
+    uint32_t k = 0;
+    for (uint32_t i = 0; i < BLOCKS; i++) {
+        L.norm_width[k++] = C;
+        L.norm_width[k++] = C;
+    }
+    L.norm_width[k++] = C;     // trunk
+    L.norm_width[k++] = CFGH;  // config encoder
+    for (uint32_t i = 0; i < JBLOCKS; i++) L.norm_width[k++] = JW;
+    L.norm_width[k++] = JW;  // join output
+    L.norm_width[k++] = D;   // h
+    for (uint32_t i = 0; i < NORMS; i++) {
+        L.norm_g[i] = c.ln;
+        L.norm_b[i] = c.ln + L.norm_width[i];
+        c.ln += 2 * L.norm_width[i];
+    }
+    L.w_len = c.w;
+    L.b_len = c.b;
+    L.ln_len = c.ln;
+    return L;
+}
+
+Board board() {
+    // The radius-3 hexagon around (3, 3) in axial coordinates, hexes in
+    // row-major (y, then x) order (board.rs:1-6); directions as board.rs:14.
+    static const int dir[6][2] = {{1, 0}, {-1, 0}, {0, 1}, {0, -1}, {1, -1}, {-1, 1}};
+    static const int locs[10][2] = {{4, 0}, {6, 1}, {0, 5}, {2, 6}, {2, 1}, {3, 2}, {5, 3}, {1, 3}, {3, 4}, {4, 5}};
+    int hx[HEXES], hy[HEXES], n = 0;
+    auto valid = [](int x, int y) { return std::abs(x - 3) <= 3 && std::abs(y - 3) <= 3 && std::abs(x + y - 6) <= 3; };
+    for (int y = 0; y <= 6; y++)
+        for (int x = 0; x <= 6; x++)
+            if (valid(x, y)) {
+                hx[n] = x;
+                hy[n] = y;
+                n++;
+            }
+    auto at = [&](int x, int y) -> int {
+        for (int h = 0; h < (int)HEXES; h++)
+            if (hx[h] == x && hy[h] == y) return h;
+        return (int)HEXES;
+    };
+    Board b{};
+    for (uint32_t h = 0; h < HEXES; h++)
+        for (int d = 0; d < 6; d++) b.nb[h][d] = (uint8_t)at(hx[h] + dir[d][0], hy[h] + dir[d][1]);
+    for (const auto& l : locs) b.loc[at(l[0], l[1])] = 1;
+    return b;
+}
+
+Span mat_span(const Layout& L, uint32_t m) {
+    if (m == M_CARD0) return L.card[0];
+    if (m == M_CARD1) return L.card[1];
+    if (m == M_CFG_M) return L.cfg_m;
+    if (m >= M_MIX0 && m < M_MIX0 + BLOCKS) return L.mix[m - M_MIX0];
+    if (m >= M_POOL0 && m < M_POOL0 + BLOCKS) return L.pool[m - M_POOL0];
+    if (m >= M_OUT0 && m < M_OUT0 + BLOCKS) return L.out[m - M_OUT0];
+    if (m == M_BOARD) return L.board_out;
+    if (m == M_JOIN_P) return L.join_p;
+    if (m == M_CFG1) return L.cfg1;
+    if (m == M_CFG_F) return L.cfg_f;
+    if (m == M_CFG_G) return L.cfg_g;
+    if (m == M_JOIN_B) return L.join_b;
+    if (m >= M_JOIN_W0 && m < M_JOIN_W0 + JBLOCKS) return L.join_w[m - M_JOIN_W0];
+    return L.join_out;
+}
+
+// ----------------------------------------------------------- device side
+
+namespace {
+
+constexpr int NBLK = 192;  // trunk and config workgroups
+constexpr int JROWS = 8;   // rows per join workgroup (float32 path)
+
+// The blob layout, computed at compile time for the kernels (the same
+// cursor as layout(), which the host uses and a test compares).
+struct DevLayout {
+    Layout L;
+    constexpr DevLayout() : L() {
+        uint32_t w = 0, b = 0, ln = 0;
+        auto lin = [&](Span& s, uint32_t i, uint32_t o, bool bias) {
+            s.w = w;
+            s.b = bias ? b : 0;
+            s.i = i;
+            s.o = o;
+            s.bias = bias;
+            w += i * o;
+            if (bias) b += o;
+        };
+        lin(L.card[0], CARD_FEATS, TYPE, true);
+        lin(L.card[1], TYPE, TYPE, true);
+        lin(L.pile, PILE_COUNTS, TYPE, false);
+        L.seat = w;
+        w += 2 * TYPE;
+        lin(L.hex_stem, HEX_FACTS, C, true);
+        lin(L.tok_stem, TYPE, C, false);
+        L.pos = w;
+        w += HEXES * C;
+        lin(L.glob_stem, LOOSE, C, false);
+        for (uint32_t i = 0; i < BLOCKS; i++) {
+            lin(L.mix[i], 2 * C, C, true);
+            lin(L.pool[i], 2 * C, C, true);
+            lin(L.out[i], C, C, true);
+        }
+        lin(L.board_out, 2 * C + LOOSE, D, true);
+        lin(L.cfg1, 3 + TYPE, CFGH, true);
+        lin(L.cfg_f, CFGH, D, true);
+        lin(L.cfg_g, CFGH, POOL, true);
+        lin(L.cfg_m, TYPE, 3 * POOL, false);
+        lin(L.join_p, D, JW, false);
+        lin(L.join_b, JOIN_IN, JW, true);
+        for (uint32_t i = 0; i < JBLOCKS; i++) lin(L.join_w[i], JW, JW, true);
+        lin(L.join_out, JW, D, true);
+        L.value_bias = b;
+        b += 1;
+        uint32_t k = 0;
+        for (uint32_t i = 0; i < BLOCKS; i++) {
+            L.norm_width[k++] = C;
+            L.norm_width[k++] = C;
+        }
+        L.norm_width[k++] = C;
+        L.norm_width[k++] = CFGH;
+        for (uint32_t i = 0; i < JBLOCKS; i++) L.norm_width[k++] = JW;
+        L.norm_width[k++] = JW;
+        L.norm_width[k++] = D;
+        for (uint32_t i = 0; i < NORMS; i++) {
+            L.norm_g[i] = ln;
+            L.norm_b[i] = ln + L.norm_width[i];
+            ln += 2 * L.norm_width[i];
+        }
+        L.w_len = w;
+        L.b_len = b;
+        L.ln_len = ln;
+    }
+};
+constexpr DevLayout DL{};
+#define LY (DL.L)
+
+// tanh by the restatement's formula: e^x for x <= 0 by Cody-Waite reduction
+// (ln2 = 0.693145751953125 + 1.428606765330187e-6) and the degree-7 Taylor
+// polynomial on |r| <= ln2/2, then tanh|x| = (1 - e^{-2|x|}) / (1 + e^{-2|x|}).
+__device__ __forceinline__ float exp_neg(float x) {
+    const float n = rintf(x * 1.44269504f);
+    const float r = (x - n * 0.693145751953125f) - n * 1.428606765330187e-6f;
+    float p = 1.0f / 5040.0f;
+    p = 1.0f / 720.0f + r * p;
+    p = 1.0f / 120.0f + r * p;
+    p = 1.0f / 24.0f + r * p;
+    p = 1.0f / 6.0f + r * p;
+    p = 0.5f + r * p;
+    p = 1.0f + r * p;
+    p = 1.0f + r * p;
+    return ldexpf(p, (int)n);
+}
+__device__ __forceinline__ float tanh_r(float x) {
+    const float a = fabsf(x);
+    if (a > 20.0f) return x > 0.0f ? 1.0f : -1.0f;
+    const float t = exp_neg(-2.0f * a);
+    const float y = (1.0f - t) / (1.0f + t);
+    return x < 0.0f ? -y : y;
+}
+// net.rs:125-128
+__device__ __forceinline__ float gelu(float x) {
+    const float inner = 0.79788456f * (x + 0.044715f * x * x * x);
+    return 0.5f * x * (1.0f + tanh_r(inner));
+}
+
+__device__ __forceinline__ float bf16_round(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return __uint_as_float((u | 0x00400000u) & 0xffff0000u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return __uint_as_float(u & 0xffff0000u);
+}
+// An operand of a 16-bit GEMM, as the matrix cores see it.
+template <int PREC>
+__device__ __forceinline__ float qop(float x) {
+    if (PREC == WC_F16) return (float)(_Float16)x;
+    if (PREC == WC_BF16) return bf16_round(x);
+    return x;
+}
+template <int PREC>
+__device__ __forceinline__ uint16_t to16(float x) {
+    if (PREC == WC_F16) return __builtin_bit_cast(uint16_t, (_Float16)x);
+    return (uint16_t)(__float_as_uint(bf16_round(x)) >> 16);
+}
+
+// Output j of one Lin over an input vector x (LDS) of length k with matrix
+// W [k x o] row-major: `gemm` then Lin::bias. FAST marks a product the 16-bit
+// path runs with rounded operands (summed in float32 from zero, then the
+// start value, then the bias); otherwise the float32 CPU order (from the start
+// value, then the bias).
+template <int PREC, bool FAST>
+__device__ __forceinline__ float lin_out(const float* x, uint32_t k, const float* W, uint32_t o, uint32_t j,
+                                         float start, const float* bias) {
+    if (PREC == WC_PRECISE || !FAST) {
+        float acc = start;
+        for (uint32_t p = 0; p < k; p++) {
+            const float a = x[p];
+            if (a != 0.0f) acc += a * W[(size_t)p * o + j];
+        }
+        if (bias) acc += bias[j];
+        return acc;
+    }
+    float acc = 0.0f;
+    for (uint32_t p = 0; p < k; p++) {
+        const float a = qop<PREC>(x[p]);
+        if (a != 0.0f) acc += a * qop<PREC>(W[(size_t)p * o + j]);
+    }
+    float v = start + acc;
+    if (bias) v += bias[j];
+    return v;
+}
+
+// LayerNorm statistics of one row in the CPU order (net.rs:380-405): mean,
+// then 1 / sqrt(var + 1e-5).
+__device__ __forceinline__ void norm_stats(const float* x, uint32_t width, float* mean_out, float* inv_out) {
+    float sum = 0.0f;
+    for (uint32_t j = 0; j < width; j++) sum += x[j];
+    const float mean = sum / (float)width;
+    float sq = 0.0f;
+    for (uint32_t j = 0; j < width; j++) sq += (x[j] - mean) * (x[j] - mean);
+    const float var = sq / (float)width;
+    *mean_out = mean;
+    *inv_out = 1.0f / sqrtf(var + 1e-5f);
+}
+__device__ __forceinline__ float norm_apply(float x, float mean, float inv, const float* ln, uint32_t which, uint32_t j,
+                                            bool act) {
+    const float v = (x - mean) * inv * ln[LY.norm_g[which] + j] + ln[LY.norm_b[which] + j];
+    return act ? gelu(v) : v;
+}
+
+__device__ __forceinline__ int physical_type(int view, int t) {
+    return (view ? 1 - t / (int)NSLOT : t / (int)NSLOT) * (int)NSLOT + t % (int)NSLOT;
+}
+
+// --------------------------------------------------------------- cards
+
+// Net::cards (net.rs:459-471) for one (job, view, token), and the token's
+// count-weighted bag row cfg_m (net.rs:779-784). 192 threads.
+template <int PREC>
+__global__ __launch_bounds__(NBLK) void k_cards(Net net, WaveIn in, WaveOut out) {
+    __shared__ float facts[CARD_FEATS], hid[TYPE], card[TYPE];
+    const uint32_t id = blockIdx.x, t = id % NTYPE, view = (id / NTYPE) & 1, job = id / (2 * NTYPE);
+    const uint32_t j = threadIdx.x;
+    const float* cf = in.card_feat + (size_t)job * NTYPE * CARD_FEATS + (size_t)physical_type(view, t) * CARD_FEATS;
+    if (j < CARD_FEATS) facts[j] = cf[j];
+    __syncthreads();
+    if (j < TYPE)
+        hid[j] = gelu(lin_out<PREC, true>(facts, CARD_FEATS, net.w + LY.card[0].w, TYPE, j, 0.0f, net.b + LY.card[0].b));
+    __syncthreads();
+    if (j < TYPE) {
+        card[j] = lin_out<PREC, true>(hid, TYPE, net.w + LY.card[1].w, TYPE, j, 0.0f, net.b + LY.card[1].b);
+        out.cards[(size_t)id * TYPE + j] = card[j];
+    }
+    __syncthreads();
+    for (uint32_t m = j; m < 3 * POOL; m += NBLK)
+        out.bag[(size_t)id * 3 * POOL + m] = lin_out<PREC, true>(card, TYPE, net.w + LY.cfg_m.w, 3 * POOL, m, 0.0f, nullptr);
+}
+
+// -------------------------------------------------------------- configs
+
+// Net::configs (net.rs:735-797) for one config. 192 threads.
+template <int PREC>
+__global__ __launch_bounds__(NBLK) void k_configs(Net net, WaveIn in, WaveOut out) {
+    __shared__ float slot[NSLOT][3 + TYPE], hid[NSLOT][CFGH], u[CFGH], phi[CFEAT], stats[2];
+    const uint32_t c = blockIdx.x, j = threadIdx.x;
+    const uint32_t job = in.cfg_job[c], owner = in.cfg_owner[c];
+    if (j < CFEAT) phi[j] = in.phi[(size_t)c * CFEAT + j];
+    __syncthreads();
+    const float* cards = out.cards + ((size_t)job * 2 + owner) * NTYPE * TYPE;  // the owner's view: its slot k is token k
+    for (uint32_t x = j; x < NSLOT * (3 + TYPE); x += NBLK) {
+        const uint32_t k = x / (3 + TYPE), q = x % (3 + TYPE);
+        slot[k][q] = q < 3 ? phi[q * NSLOT + k] : cards[(size_t)k * TYPE + (q - 3)];
+    }
+    __syncthreads();
+    if (j < CFGH)
+        for (uint32_t k = 0; k < NSLOT; k++)
+            hid[k][j] = gelu(lin_out<PREC, true>(slot[k], 3 + TYPE, net.w + LY.cfg1.w, CFGH, j, 0.0f, net.b + LY.cfg1.b));
+    __syncthreads();
+    if (j < CFGH) {
+        float v = 0.0f;
+        for (uint32_t k = 0; k < NSLOT; k++) v += hid[k][j];
+        u[j] = v;
+    }
+    __syncthreads();
+    if (j == 0) norm_stats(u, CFGH, &stats[0], &stats[1]);
+    __syncthreads();
+    if (j < CFGH) u[j] = norm_apply(u[j], stats[0], stats[1], net.ln, LN_CFG, j, true);
+    __syncthreads();
+    for (uint32_t x = j; x < D; x += NBLK) {
+        const float f = lin_out<PREC, true>(u, CFGH, net.w + LY.cfg_f.w, D, x, 0.0f, net.b + LY.cfg_f.b);
+        if (PREC == WC_PRECISE)
+            ((float*)out.F)[(size_t)c * D + x] = f;
+        else
+            ((uint16_t*)out.F)[(size_t)c * D + x] = to16<PREC>(f);
+    }
+    if (j < POOL) {
+        float g = lin_out<PREC, true>(u, CFGH, net.w + LY.cfg_g.w, POOL, j, 0.0f, net.b + LY.cfg_g.b);
+        const float* bag = out.bag + ((size_t)job * 2 + owner) * NTYPE * 3 * POOL;
+        for (uint32_t k = 0; k < NSLOT; k++)
+            for (uint32_t zone = 0; zone < 3; zone++) {
+                const float count = phi[zone * NSLOT + k];
+                if (count == 0.0f) continue;
+                g += count * bag[(size_t)k * 3 * POOL + zone * POOL + j];
+            }
+        out.G[(size_t)c * POOL + j] = g;
+    }
+}
+
+// ---------------------------------------------------------------- trunk
+
+// Net::board + join_cache (net.rs:474-730) for one network row, every
+// activation in LDS. 192 threads: in the hex-wide products thread j % 96
+// owns channel j of every other hex.
+template <int PREC>
+__global__ __launch_bounds__(NBLK) void k_trunk(Net net, WaveIn in, WaveOut out) {
+    __shared__ float x[HEXES][C], a[HEXES][C], ns[HEXES][C], y[HEXES][C];
+    __shared__ float tok[NTYPE][TYPE], proj[NTYPE][C], tp[C], glob[C], loose[LOOSE], facts[HEXES][HEX_FACTS];
+    __shared__ float pooled[2 * C], gb[C], bin[2 * C + LOOSE], P[D], mean[HEXES], inv[HEXES];
+    __shared__ int occ[HEXES];
+    const uint32_t r = blockIdx.x, tid = threadIdx.x;
+    const uint32_t job = in.row_job[r];
+    const uint8_t* raw = in.raw + (size_t)r * ROW_BYTES;
+    const float* cards = out.cards + (size_t)job * 2 * NTYPE * TYPE;  // view 0
+    const float* W = net.w;
+    // tokens (net.rs:474-495)
+    for (uint32_t i = tid; i < NTYPE * TYPE; i += NBLK) {
+        const uint32_t t = i / TYPE, j = i % TYPE;
+        float piles[PILE_COUNTS];
+        for (uint32_t f = 0; f < PILE_COUNTS; f++) piles[f] = (float)raw[GR_PILES + t * PILE_COUNTS + f] / 5.0f;
+        const float v = lin_out<PREC, false>(piles, PILE_COUNTS, W + LY.pile.w, TYPE, j, 0.0f, nullptr);
+        tok[t][j] = v + (cards[(size_t)t * TYPE + j] + W[LY.seat + (t / NSLOT) * TYPE + j]);
+    }
+    // hex facts and loose scalars (wave_kernels.cu:254-296; rebel.rs:1174-1231)
+    if (tid < HEXES) {
+        const uint32_t h = tid;
+        const int owner = raw[GR_HEX_OWNER + h], marker = raw[GR_HEX_MARKER + h], sl = raw[GR_HEX_SLOT + h];
+        facts[h][0] = owner == 0 ? 1.0f : 0.0f;
+        facts[h][1] = owner == 1 ? 1.0f : 0.0f;
+        facts[h][2] = (float)raw[GR_HEX_HEIGHT + h] / 5.0f;
+        facts[h][3] = marker == 0 ? 1.0f : 0.0f;
+        facts[h][4] = marker == 1 ? 1.0f : 0.0f;
+        facts[h][5] = (float)net.loc[h];
+        occ[h] = owner < 2 && sl < (int)NSLOT ? owner * (int)NSLOT + sl : -1;
+    } else if (tid >= 64 && tid < 64 + LOOSE) {
+        const uint32_t q = tid - 64;
+        float v;
+        if (q < 12) {
+            const uint32_t p = q / 6, k = q % 6;
+            const int markers = raw[GR_MARKERS + p];
+            if (k == 0) v = (float)markers / 6.0f;
+            else if (k == 1) v = (float)(6 - markers) / 6.0f;
+            else if (k == 2) v = (float)raw[GR_HAND + p] / 3.0f;
+            else if (k == 3) v = (float)raw[GR_FD + p] / 21.0f;
+            else if (k == 4) v = (float)raw[GR_BAG + p] / 21.0f;
+            else v = raw[GR_INITIATIVE] == p ? 1.0f : 0.0f;
+        } else if (q == 12) {
+            v = (float)((int)raw[GR_PLIES] | (int)raw[GR_PLIES + 1] << 8) / 256.0f;
+        } else if (q == 13) {
+            v = raw[GR_INIT_MOVED] ? 1.0f : 0.0f;
+        } else {
+            v = raw[GR_TO_ACT] == 0 ? 1.0f : 0.0f;
+        }
+        loose[q] = v;
+    }
+    __syncthreads();
+    // stem (net.rs:499-543)
+    for (uint32_t i = tid; i < NTYPE * C; i += NBLK) {
+        const uint32_t t = i / C, j = i % C;
+        proj[t][j] = lin_out<PREC, false>(tok[t], TYPE, W + LY.tok_stem.w, C, j, 0.0f, nullptr);
+    }
+    __syncthreads();
+    if (tid < C) {
+        float v = 0.0f;
+        for (uint32_t t = 0; t < NTYPE; t++) v += gelu(proj[t][tid]) / (float)NTYPE;
+        tp[tid] = v;
+        glob[tid] = lin_out<PREC, false>(loose, LOOSE, W + LY.glob_stem.w, C, tid, 0.0f, nullptr);
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < HEXES * C; i += NBLK) {
+        const uint32_t h = i / C, j = i % C;
+        const float v = lin_out<PREC, false>(facts[h], HEX_FACTS, W + LY.hex_stem.w, C, j, 0.0f, net.b + LY.hex_stem.b);
+        const float o = occ[h] >= 0 ? proj[occ[h]][j] : 0.0f;
+        x[h][j] = v + (((o + W[LY.pos + h * C + j]) + glob[j]) + tp[j]);
+    }
+    __syncthreads();
+    const uint32_t j = tid % C, h0 = tid / C;  // hex-wide products: channel j of hexes h0, h0 + 2, ...
+    auto norm_rows = [&](float (*src)[C], float (*dst)[C], uint32_t which, bool act) {
+        if (tid < HEXES) norm_stats(src[tid], C, &mean[tid], &inv[tid]);
+        __syncthreads();
+        for (uint32_t i = tid; i < HEXES * C; i += NBLK) {
+            const uint32_t h = i / C, q = i % C;
+            dst[h][q] = norm_apply(src[h][q], mean[h], inv[h], net.ln, which, q, act);
+        }
+        __syncthreads();
+    };
+    for (uint32_t blk = 0; blk < BLOCKS; blk++) {
+        norm_rows(x, a, 2 * blk, true);
+        // neighbour sums (a zero start, directions in board order) and the
+        // mean / max pool (net.rs:553-585)
+        for (uint32_t i = tid; i < HEXES * C; i += NBLK) {
+            const uint32_t h = i / C, q = i % C;
+            float v = 0.0f;
+            for (int d = 0; d < 6; d++) {
+                const uint32_t n = net.nb[h * 6 + d];
+                if (n < HEXES) v += a[n][q];
+            }
+            ns[h][q] = v;
+        }
+        if (tid < C) {
+            float mn = 0.0f, top = -INFINITY;
+            for (uint32_t h = 0; h < HEXES; h++) {
+                mn += a[h][tid] / (float)HEXES;
+                top = fmaxf(top, a[h][tid]);
+            }
+            pooled[tid] = mn;
+            pooled[C + tid] = top;
+        }
+        __syncthreads();
+        if (tid < C)
+            gb[tid] = lin_out<PREC, true>(pooled, 2 * C, W + LY.pool[blk].w, C, tid, 0.0f, net.b + LY.pool[blk].b);
+        // mix: [a, ns] (192 inputs) -> C, then the pool bias broadcast
+        {
+            const float* Wm = W + LY.mix[blk].w;
+            float acc[(HEXES + 1) / 2];
+#pragma unroll
+            for (uint32_t m = 0; m < (HEXES + 1) / 2; m++) acc[m] = 0.0f;
+            for (uint32_t p = 0; p < 2 * C; p++) {
+                const float wv = PREC == WC_PRECISE ? Wm[(size_t)p * C + j] : qop<PREC>(Wm[(size_t)p * C + j]);
+#pragma unroll
+                for (uint32_t m = 0; m < (HEXES + 1) / 2; m++) {
+                    const uint32_t h = h0 + 2 * m;
+                    if (h < HEXES) {
+                        const float av = qop<PREC>(p < C ? a[h][p] : ns[h][p - C]);
+                        if (av != 0.0f) acc[m] += av * wv;
+                    }
+                }
+            }
+            __syncthreads();  // gb ready
+#pragma unroll
+            for (uint32_t m = 0; m < (HEXES + 1) / 2; m++) {
+                const uint32_t h = h0 + 2 * m;
+                if (h < HEXES) y[h][j] = (acc[m] + net.b[LY.mix[blk].b + j]) + gb[j];
+            }
+        }
+        __syncthreads();
+        norm_rows(y, y, 2 * blk + 1, true);
+        // out: C -> C, the residual add
+        {
+            const float* Wo = W + LY.out[blk].w;
+            float acc[(HEXES + 1) / 2];
+#pragma unroll
+            for (uint32_t m = 0; m < (HEXES + 1) / 2; m++) acc[m] = 0.0f;
+            for (uint32_t p = 0; p < C; p++) {
+                const float wv = PREC == WC_PRECISE ? Wo[(size_t)p * C + j] : qop<PREC>(Wo[(size_t)p * C + j]);
+#pragma unroll
+                for (uint32_t m = 0; m < (HEXES + 1) / 2; m++) {
+                    const uint32_t h = h0 + 2 * m;
+                    if (h < HEXES) {
+                        const float av = qop<PREC>(y[h][p]);
+                        if (av != 0.0f) acc[m] += av * wv;
+                    }
+                }
+            }
+#pragma unroll
+            for (uint32_t m = 0; m < (HEXES + 1) / 2; m++) {
+                const uint32_t h = h0 + 2 * m;
+                if (h < HEXES) x[h][j] += acc[m] + net.b[LY.out[blk].b + j];
+            }
+        }
+        __syncthreads();
+    }
+    norm_rows(x, a, LN_TRUNK, true);
+    // the board vector (net.rs:704-722) and its join projection
+    if (tid < C) {
+        float mn = 0.0f, top = -INFINITY;
+        for (uint32_t h = 0; h < HEXES; h++) {
+            mn += a[h][tid] / (float)HEXES;
+            top = fmaxf(top, a[h][tid]);
+        }
+        bin[tid] = mn;
+        bin[C + tid] = top;
+    } else if (tid < C + LOOSE) {
+        bin[2 * C + (tid - C)] = loose[tid - C];
+    }
+    __syncthreads();
+    for (uint32_t q = tid; q < D; q += NBLK) {
+        P[q] = lin_out<PREC, true>(bin, 2 * C + LOOSE, W + LY.board_out.w, D, q, 0.0f, net.b + LY.board_out.b);
+        out.P[(size_t)r * D + q] = P[q];
+    }
+    __syncthreads();
+    if (tid < JW) out.Jp[(size_t)r * JW + tid] = lin_out<PREC, true>(P, D, W + LY.join_p.w, JW, tid, 0.0f, nullptr);
+}
+
+// ----------------------------------------------------------------- join
+
+// Net::join (net.rs:801-841) for JROWS rows, float32 or rounded operands,
+// every activation in LDS. 128 threads: thread j owns column j (and j + 128
+// of the 256-wide output) of every row of the tile.
+template <int PREC>
+__global__ __launch_bounds__(JW) void k_join(Net net, uint32_t rows, const float* X, const float* P, const float* Jp,
+                                             float* H) {
+    __shared__ float xin[JROWS][JOIN_IN], z[JROWS][JW], t[JROWS][JW], h[JROWS][D], mean[JROWS], inv[JROWS];
+    const uint32_t r0 = blockIdx.x * JROWS, j = threadIdx.x;
+    const uint32_t nr = min((uint32_t)JROWS, rows - r0);
+    for (uint32_t i = j; i < nr * JOIN_IN; i += JW) xin[i / JOIN_IN][i % JOIN_IN] = X[(size_t)r0 * JOIN_IN + i];
+    __syncthreads();
+    for (uint32_t r = 0; r < nr; r++)
+        z[r][j] = lin_out<PREC, true>(xin[r], JOIN_IN, net.w + LY.join_b.w, JW, j, Jp[(size_t)(r0 + r) * JW + j],
+                                      net.b + LY.join_b.b);
+    __syncthreads();
+    auto norm_tile = [&](float (*src)[JW], float (*dst)[JW], uint32_t which) {
+        if (j < nr) norm_stats(src[j], JW, &mean[j], &inv[j]);
+        __syncthreads();
+        for (uint32_t r = 0; r < nr; r++) dst[r][j] = norm_apply(src[r][j], mean[r], inv[r], net.ln, which, j, true);
+        __syncthreads();
+    };
+    for (uint32_t blk = 0; blk < JBLOCKS; blk++) {
+        norm_tile(z, t, LN_JOIN + blk);
+        for (uint32_t r = 0; r < nr; r++)
+            z[r][j] += lin_out<PREC, true>(t[r], JW, net.w + LY.join_w[blk].w, JW, j, 0.0f, net.b + LY.join_w[blk].b);
+        __syncthreads();
+    }
+    norm_tile(z, z, LN_JOUT);
+    for (uint32_t r = 0; r < nr; r++)
+        for (uint32_t q = j; q < D; q += JW)
+            h[r][q] = lin_out<PREC, true>(z[r], JW, net.w + LY.join_out.w, D, q, P[(size_t)(r0 + r) * D + q],
+                                          net.b + LY.join_out.b);
+    __syncthreads();
+    if (j < nr) norm_stats(h[j], D, &mean[j], &inv[j]);
+    __syncthreads();
+    for (uint32_t r = 0; r < nr; r++)
+        for (uint32_t q = j; q < D; q += JW) {
+            const float v = norm_apply(h[r][q], mean[r], inv[r], net.ln, LN_H, q, false);
+            if (PREC == WC_PRECISE)
+                H[(size_t)(r0 + r) * D + q] = v;
+            else
+                ((uint16_t*)H)[frag_off(r0 + r, q, D)] = to16<PREC>(v);
+        }
+}
+
+// The 16-bit query input (fragment-major, K = JOIN_IN_PAD) back to float32
+// rows of JOIN_IN for the rounded-operand join.
+template <int PREC>
+__global__ void k_unpack_x(const uint16_t* X, uint32_t rows, float* out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)rows * JOIN_IN) return;
+    const uint32_t r = (uint32_t)(i / JOIN_IN), k = (uint32_t)(i % JOIN_IN);
+    const uint16_t v = X[frag_off(r, k, JOIN_IN_PAD)];
+    out[i] = PREC == WC_F16 ? (float)__builtin_bit_cast(_Float16, v) : __uint_as_float((uint32_t)v << 16);
+}
+
+}  // namespace
+
+static_assert(sizeof(Net) < 1024, "kernel argument");
+
+void launch_build(int precision, const Net& net, const WaveIn& in, const WaveOut& out, hipStream_t s) {
+    const uint32_t tokens = in.jobs * 2 * NTYPE;
+#define V5_BUILD(P)                                                                                   \
+    do {                                                                                              \
+        if (tokens) hipLaunchKernelGGL(k_cards<P>, dim3(tokens), dim3(NBLK), 0, s, net, in, out);     \
+        if (in.ncfg) hipLaunchKernelGGL(k_configs<P>, dim3(in.ncfg), dim3(NBLK), 0, s, net, in, out); \
+        if (in.rows) hipLaunchKernelGGL(k_trunk<P>, dim3(in.rows), dim3(NBLK), 0, s, net, in, out);   \
+    } while (0)
+    if (precision == WC_PRECISE)
+        V5_BUILD(WC_PRECISE);
+    else if (precision == WC_F16)
+        V5_BUILD(WC_F16);
+    else
+        V5_BUILD(WC_BF16);
+#undef V5_BUILD
+}
+
+void launch_join(int precision, const Net& net, uint32_t rows, const void* X, const float* P, const float* Jp,
+                 void* H, float* xf, hipStream_t s) {
+    if (!rows) return;
+    const dim3 g((rows + JROWS - 1) / JROWS);
+    if (precision == WC_PRECISE) {
+        hipLaunchKernelGGL(k_join<WC_PRECISE>, g, dim3(JW), 0, s, net, rows, (const float*)X, P, Jp, (float*)H);
+        return;
+    }
+    const size_t n = (size_t)rows * JOIN_IN;
+    const dim3 gx((unsigned)((n + 255) / 256));
+    if (precision == WC_F16) {
+        hipLaunchKernelGGL(k_unpack_x<WC_F16>, gx, dim3(256), 0, s, (const uint16_t*)X, rows, xf);
+        hipLaunchKernelGGL(k_join<WC_F16>, g, dim3(JW), 0, s, net, rows, xf, P, Jp, (float*)H);
+    } else {
+        hipLaunchKernelGGL(k_unpack_x<WC_BF16>, gx, dim3(256), 0, s, (const uint16_t*)X, rows, xf);
+        hipLaunchKernelGGL(k_join<WC_BF16>, g, dim3(JW), 0, s, net, rows, xf, P, Jp, (float*)H);
+    }
+}
+
+}  // namespace v5
+}  // namespace wc

@@ -147,7 +147,7 @@ void build_records(WaveHost* wp) {
         for (const Task& q : w.top_reach[p]) w.top_reach_rec[p].push_back(reach(q));
         // Network-leaf slots, unit by unit (the value sweep writes them first).
         const uint32_t heads = w.net.heads;
-        const bool tower = w.net.kind == MODEL_TWO_TOWER;
+        const bool tower = readout_net(w.net.kind);
         std::vector<uint32_t> row_blk;  // two-tower: each row's readout block for p
         if (tower) {
             row_blk.assign(w.rows(), NONE);
@@ -212,7 +212,7 @@ void build_records(WaveHost* wp) {
 
 }  // namespace
 
-constexpr size_t WAVE_HOST_BYTES = 2208;  // sizeof(WaveHost) on x86-64 (libstdc++)
+constexpr size_t WAVE_HOST_BYTES = 2304;  // sizeof(WaveHost) on x86-64 (libstdc++)
 static_assert(sizeof(WaveHost) == WAVE_HOST_BYTES, "a WaveHost member was added or changed: update reset()");
 void WaveHost::reset() {
     const WaveHost blank;
@@ -222,12 +222,14 @@ void WaveHost::reset() {
     for (auto* v : {&node_meta, &node_nc, &child_start, &child, &legal_row_of, &legal_off, &legal_value, &draw_off,
                     &draw_row_off, &draw_row_start, &draw_to, &reach_base, &vals_base, &parent, &rev_row_of,
                     &rev_start, &rev_src, &rev_cell, &rvd_row_of, &rvd_start, &rvd_src, &row_node, &row_cfg_off,
-                    &row_cfg, &cfg_key, &head_tile_n, &term_node, &exit_node, &exit_coff, &unit_row, &unit_term})
+                    &row_cfg, &cfg_key, &head_tile_n, &term_node, &exit_node, &exit_coff, &unit_row, &unit_term,
+                    &cfg_job, &row_job})
         keep(*v);
-    for (auto* v : {&draw_p, &rvd_p, &cfg_emb, &cfg_priv, &term_util, &roots, &carried}) keep(*v);
+    for (auto* v : {&draw_p, &rvd_p, &cfg_emb, &cfg_priv, &term_util, &roots, &carried, &card_feat}) keep(*v);
     keep(jobs);
     keep(trees);
     keep(pub_raw);
+    keep(cfg_owner);
     keep(units);
     keep(node_top);
     for (int p = 0; p < 2; p++) {
@@ -282,10 +284,6 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             return false;
         }
     if (!w.net.parse(w.meta.net_dims, err)) return false;
-    if (w.net.kind == MODEL_V5) {
-        *err = "the v5 leaf network is not built by this executor";
-        return false;
-    }
     if (!validated) {  // jobs validate independently; the first failure in job order is reported
         std::vector<std::string> errs(jobs.size());
         std::vector<uint8_t> bad(jobs.size(), 0);
@@ -478,7 +476,21 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
         for (uint32_t r : t.leaf_rows) w.row_node.push_back(node0 + r);
         append_shift<uint32_t>(w.row_cfg_off, t.leaf_coff, 1, member0, false);
         append_shift<uint32_t>(w.row_cfg, t.leaf_cidx, 0, cfg0, false);
-        for (uint32_t c = 0; c < t.ncfg; c++) {
+        const bool v5 = w.net.kind == MODEL_V5;
+        const uint32_t job_index = (uint32_t)w.trees.size();
+        if (v5) {
+            for (uint32_t r = 0; r < t.rows; r++) w.row_job.push_back(job_index);
+            w.card_feat.insert(w.card_feat.end(), t.card_feat.begin(), t.card_feat.end());
+        }
+        for (uint32_t c = 0; c < t.ncfg && v5; c++) {
+            // the config encoder reads the counts, the owner's card view and its job's table
+            w.cfg_key.push_back(0);
+            w.cfg_priv.insert(w.cfg_priv.end(), &t.cphi[size_t(c) * w.net.cfeat],
+                              &t.cphi[size_t(c) * w.net.cfeat] + w.net.cfeat);
+            w.cfg_job.push_back(job_index);
+            w.cfg_owner.push_back(t.cplayer[c]);
+        }
+        for (uint32_t c = 0; c < t.ncfg && !v5; c++) {
             const float* phi = &t.cphi[size_t(c) * w.net.cfeat];
             float key = phi[0];
             if (!(key >= 0.0f) || key != (float)(uint32_t)key || (w.net.heads && (uint32_t)key >= w.net.heads)) {
@@ -694,7 +706,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     }
     // Two-tower readout blocks: per tree and player, its rows times the
     // config range its rows name.
-    if (w.net.kind == MODEL_TWO_TOWER) {
+    if (readout_net(w.net.kind)) {
         job_rows.push_back(nrows);
         w.tower_len = 0;
         for (int p = 0; p < 2; p++) {
@@ -850,7 +862,9 @@ bool validate_deep(const WaveHost& w, std::string* err) {
     const uint64_t rows = w.rows();
     if (w.row_cfg_off.size() != 2 * rows + 1 || w.row_cfg_off.back() != w.row_cfg.size()) return fail("row_cfg_off");
     const uint64_t ncfg = w.cfg_key.size();
-    if (w.cfg_emb.size() != ncfg * w.net.pool || w.pub_raw.size() != rows * w.net.row_bytes) return fail("row payload");
+    if (w.cfg_emb.size() != (w.net.kind == MODEL_V5 ? 0 : ncfg * w.net.pool) ||
+        w.pub_raw.size() != rows * w.net.row_bytes)
+        return fail("row payload");
     for (uint64_t r = 0; r < rows; r++) {
         uint32_t node = w.row_node[r];
         if (node >= N || (w.node_meta[node] & 3u) != 2) return fail("row_node");
@@ -880,7 +894,20 @@ bool validate_deep(const WaveHost& w, std::string* err) {
     if (w.net.kind == MODEL_MLP)
         for (uint32_t k : w.cfg_key)
             if (k >= w.net.heads) return fail("cfg_key");
-    if (w.cfg_priv.size() != (w.net.kind == MODEL_TWO_TOWER ? ncfg * w.net.priv_in : 0)) return fail("cfg_priv");
+    if (w.cfg_priv.size() != (w.net.kind == MODEL_TWO_TOWER ? ncfg * w.net.priv_in
+                              : w.net.kind == MODEL_V5      ? ncfg * w.net.cfeat
+                                                            : 0))
+        return fail("cfg_priv");
+    if (w.net.kind == MODEL_V5) {  // the v5 build's per-config and per-row job indices
+        const uint64_t njobs = w.trees.size();
+        if (w.cfg_job.size() != ncfg || w.cfg_owner.size() != ncfg || w.row_job.size() != rows ||
+            w.card_feat.size() != njobs * w.net.card_feat || w.pub_raw.size() != uint64_t(rows) * w.net.row_bytes)
+            return fail("v5 tables");
+        for (uint64_t c = 0; c < ncfg; c++)
+            if (w.cfg_job[c] >= njobs || w.cfg_owner[c] > 1) return fail("v5 config owner");
+        for (uint32_t r : w.row_job)
+            if (r >= njobs) return fail("v5 row job");
+    }
     for (uint32_t t : w.term_node)
         if (t >= N || (w.node_meta[t] & 3u) != 2) return fail("term_node");
     const uint64_t nexit = w.exit_node.size();
@@ -988,12 +1015,12 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         for (const AccRec& r : w.acc_rec[p])
             if (r.ridx >= w.reach_len || uint64_t(r.lo) + r.n > w.ncells) return fail("accumulation record");
     }
-    const uint64_t heads_end = w.net.kind == MODEL_TWO_TOWER ? w.tower_len : uint64_t(rows) * w.net.heads;
+    const uint64_t heads_end = readout_net(w.net.kind) ? w.tower_len : uint64_t(rows) * w.net.heads;
     for (int p = 0; p < 2; p++)
         for (const LeafRec& r : w.leaf_rec[p])
             if (r.out >= w.vals_len || uint64_t(r.head) >= heads_end || r.mass >= 2 * rows)
                 return fail("leaf record");
-    if (w.net.kind == MODEL_TWO_TOWER)
+    if (readout_net(w.net.kind))
         for (int p = 0; p < 2; p++) {
             // Blocks lie inside the rows, configs and values; every row of a
             // block names only configs of the block; every unit tiles a block.

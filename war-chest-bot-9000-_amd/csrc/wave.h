@@ -174,8 +174,13 @@ struct WaveHost {
     std::vector<uint32_t> row_node, row_cfg_off, row_cfg;
     std::vector<uint32_t> cfg_key;  // head row of each interned config
     std::vector<float> cfg_emb;     // [ncfg, pool]
-    std::vector<float> cfg_priv;    // [ncfg, priv_in] private-tower features (two-tower net)
+    std::vector<float> cfg_priv;    // [ncfg, priv_in] private-tower features (two-tower); [ncfg, 15] counts (v5)
     std::vector<uint8_t> pub_raw;   // [rows, row_bytes]
+    // v5 network: each config's job and owning seat, each row's job, each
+    // job's card table ([jobs][NTYPE * CARD_FEATS], physical coin-type order).
+    std::vector<uint32_t> cfg_job, row_job;
+    std::vector<uint8_t> cfg_owner;
+    std::vector<float> card_feat;
     // Head columns each 128-row tile of the network rows needs: 1 + the largest
     // head key among the tile's configs (the head GEMM skips the rest).
     std::vector<uint32_t> head_tile_n;
@@ -214,7 +219,8 @@ struct WaveHost {
     std::vector<AccRec> acc_rec[2];
     std::vector<LeafRec> leaf_rec[2];  // unit-major network-leaf slots
     std::vector<PoolGroup> pool_grp[2];  // network rows grouped by config list, longest lists first
-    // Two-tower readout blocks and their tiles, per player; tower_len floats of values.
+    // Readout blocks of the two-tower and v5 nets (<f(c), h(row)> per row and
+    // config) and their tiles, per player; tower_len floats of values.
     std::vector<TowerBlock> tower_blk[2];
     std::vector<TowerUnit> tower_unit[2];
     uint64_t tower_len = 0;

@@ -22,7 +22,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libwcwave.so")
 
 WC_PRECISE, WC_F16, WC_BF16, WC_F16X = 0, 1, 2, 3
-MODEL_MLP, MODEL_TWO_TOWER = 101, 102
+MODEL_V5, MODEL_MLP, MODEL_TWO_TOWER = 5, 101, 102
 
 _lib = None
 
@@ -111,7 +111,7 @@ class WaveStats(C.Structure):
 
 # Symbols every build must export (checked by the CPU test suite).
 EXPORTS = [
-    "wc_last_error", "wc_net_sizes",
+    "wc_last_error", "wc_net_sizes", "wc_net_norms",
     "wc_service_create", "wc_service_destroy", "wc_set_weights", "wc_queued_work",
     "wc_submit", "wc_wait", "wc_poll", "wc_ticket_free", "wc_service_stats", "wc_job_work",
     "wc_result_tag", "wc_result_weight_version", "wc_result_strategy", "wc_result_root_values",
@@ -123,7 +123,7 @@ EXPORTS = [
     "wc_mlp_forward", "wc_mlp_forward_noalloc", "wc_time_mlp",
     "wc_job_roundtrip", "wc_job_validate",
     "wc_synth_spec_default", "wc_synth", "wc_jobset_count", "wc_jobset_job", "wc_jobset_free",
-    "wc_synth_weights", "wc_synth_features",
+    "wc_synth_weights", "wc_synth_norms", "wc_synth_features",
 ]
 
 _u8p = C.POINTER(C.c_uint8)
@@ -135,6 +135,7 @@ _u16p = C.POINTER(C.c_uint16)
 def _declare(L):
     L.wc_last_error.restype = C.c_char_p
     L.wc_net_sizes.argtypes = [_u32p, C.c_uint32, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+    L.wc_net_norms.argtypes = [_u32p, C.c_uint32, C.POINTER(C.c_size_t)]
     L.wc_service_create.argtypes = [C.c_int, C.POINTER(NetDesc), C.c_int, C.POINTER(ServiceOpts),
                                     C.POINTER(C.c_void_p)]
     L.wc_service_destroy.argtypes = [C.c_void_p]
@@ -201,6 +202,7 @@ def _declare(L):
     L.wc_jobset_free.argtypes = [C.c_void_p]
     L.wc_jobset_free.restype = None
     L.wc_synth_weights.argtypes = [_u32p, C.c_uint32, C.c_uint64, _f32p, C.c_size_t, _f32p, C.c_size_t]
+    L.wc_synth_norms.argtypes = [_u32p, C.c_uint32, C.c_uint64, _f32p, C.c_size_t]
     L.wc_synth_features.argtypes = [C.c_uint32, C.c_uint32, C.c_uint64, _f32p]
 
 
@@ -254,6 +256,10 @@ def two_tower_dims(inputs=512, width=512, pub_layers=2, priv_in=96, priv_layers=
     return [MODEL_TWO_TOWER, inputs, width, pub_layers, priv_in, priv_layers, pool]
 
 
+# The reference's production network (engine/src/net.rs:41 MODEL_TAG).
+V5_DIMS = [MODEL_V5]
+
+
 def net_sizes(dims):
     d, dp = _arr(dims, np.uint32)
     nw, nb = C.c_size_t(), C.c_size_t()
@@ -261,18 +267,29 @@ def net_sizes(dims):
     return nw.value, nb.value
 
 
+def net_norms(dims):
+    d, dp = _arr(dims, np.uint32)
+    n = C.c_size_t()
+    _check(lib().wc_net_norms(dp, len(d), C.byref(n)))
+    return n.value
+
+
 @dataclass
 class Net:
     dims: list
     w: np.ndarray
     b: np.ndarray
+    ln: np.ndarray = None  # v5: LayerNorm (gain, shift) pairs in application order
 
     def desc(self):
         """A NetDesc whose pointers stay valid while this object lives."""
         self._d, dp = _arr(self.dims, np.uint32)
         self._w, wp = _arr(self.w, np.float32)
         self._b, bp = _arr(self.b, np.float32)
-        return NetDesc(dp, len(self._d), wp, self._w.size, bp, self._b.size, None, 0)
+        if self.ln is None or len(self.ln) == 0:
+            return NetDesc(dp, len(self._d), wp, self._w.size, bp, self._b.size, None, 0)
+        self._ln, lp = _arr(self.ln, np.float32)
+        return NetDesc(dp, len(self._d), wp, self._w.size, bp, self._b.size, lp, self._ln.size)
 
 
 def synth_weights(dims, seed=1):
@@ -281,7 +298,12 @@ def synth_weights(dims, seed=1):
     b = np.zeros(nb, np.float32)
     d, dp = _arr(dims, np.uint32)
     _check(lib().wc_synth_weights(dp, len(d), seed, w.ctypes.data_as(_f32p), nw, b.ctypes.data_as(_f32p), nb))
-    return Net(list(dims), w, b)
+    nln = net_norms(dims)
+    if not nln:
+        return Net(list(dims), w, b)
+    ln = np.zeros(nln, np.float32)
+    _check(lib().wc_synth_norms(dp, len(d), seed, ln.ctypes.data_as(_f32p), nln))
+    return Net(list(dims), w, b, ln)
 
 
 def synth_features(rows, width, seed=7):

@@ -13,6 +13,9 @@ Each maps one benchmark/parity configuration onto the job contract:
       head row per infostate (567), 64 iterations.
   wave512w  512 depth-2 subgames, 10% whales (2,000 nodes, 567 infostates), 128
       iterations, two-tower bf16 net (512 -> 2x512 public, 96 -> 2x512 private).
+  wave256v5 the 256-subgame wave's trees with the reference's production v5 leaf
+      network (net_dims [5]): per-row public bytes (the GPU row format), per-job
+      card tables, per-config hand / face-down / bag counts.
 """
 from __future__ import annotations
 
@@ -42,6 +45,9 @@ SPECS = {
                collapse=0.6, chance=1, draw_lo=2, draw_hi=6, info_median=22.0, info_p99=567.0, info_cap=567,
                dirichlet=1, whale_frac=0.1, whale_nodes=2000, whale_info=567, iters=128, depth=2,
                snapshots=1, nroots=1, **DCFR),
+    "wave256v5": dict(net_dims=ww.V5_DIMS, seed=4, trees=256, nodes_lo=200, nodes_hi=800, act_lo=3, act_hi=12,
+               collapse=0.6, chance=1, draw_lo=2, draw_hi=6, info_median=22.0, info_p99=567.0, info_cap=567,
+               dirichlet=1, iters=64, depth=2, snapshots=1, nroots=1, **DCFR),
 }
 
 
