@@ -121,3 +121,33 @@ def test_v5_leaf_probe_16bit_tracks_the_operand_model(precision, mode, tol):
         assert err.max() <= tol * scale
         assert np.median(err) <= 0.05 * tol * scale
         np.testing.assert_allclose(mass, want_mass, rtol=2e-6, atol=1e-30)
+
+
+@pytest.mark.parametrize("precision,mode", [(ww.WC_F16, O.NET_F16A), (ww.WC_BF16, O.NET_BF16A)])
+def test_v5_matrix_core_join_tracks_the_scalar_path(precision, mode):
+    """The join on the matrix cores (the default 16-bit path) against the same
+    operands summed in ascending float32 order (WC_V5_SCALAR=1) and the
+    oracle's model: the MFMA's own summation order and the hardware-exponential
+    GELU only."""
+    jobs = v5_jobs(seed=39)
+    net = ww.synth_weights(ww.V5_DIMS, 1)
+    os.environ["WC_V5_SCALAR"] = "1"
+    try:
+        scalar = ww.Executor(0, precision)
+    finally:
+        del os.environ["WC_V5_SCALAR"]
+    try:
+        for p in (0, 1):
+            say(f"case v5 matrix-core join precision {precision}: traverser {p}")
+            got, _ = device_probe(executor(precision), jobs, net, p)
+            ref, _ = device_probe(scalar, jobs, net, p)
+            want, _ = oracle_probe(jobs, net, mode, p)
+            scale = float(np.abs(want).max())
+            for tag, other in (("scalar path", ref), ("oracle model", want)):
+                err = np.abs(got.astype(np.float64) - other)
+                say(f"against the {tag}: max {err.max() / scale:.2e}, median {np.median(err) / scale:.2e}")
+                tol = 2e-3 if precision == ww.WC_F16 else 1e-2
+                assert err.max() <= tol * scale
+                assert np.median(err) <= 0.1 * tol * scale
+    finally:
+        scalar.close()

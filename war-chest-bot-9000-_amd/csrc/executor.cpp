@@ -102,6 +102,7 @@ Executor::Executor(int device, int precision) : device_(device), precision_(prec
     if (!noalloc_scratch(device, &scratch_, &scratch_err_)) scratch_ = nullptr;
     if (const char* env = std::getenv("WC_CHAIN_SPLIT")) split_ = std::strcmp(env, "0") != 0;
     if (const char* env = std::getenv("WC_GRAPH")) graph_ = std::strcmp(env, "1") == 0;
+    if (const char* env = std::getenv("WC_V5_SCALAR")) v5_scalar_ = std::strcmp(env, "1") == 0;
     ok_ = true;
 }
 
@@ -172,10 +173,34 @@ uint64_t Executor::publish_v5(const NetShape& ns, const float* w, size_t nw, con
         *err = "hipSetDevice failed";
         return 0;
     }
-    // One allocation: the f32 blob (matrices, biases, norms) and the board tables.
+    // One allocation: the f32 blob (matrices, biases, norms), the board
+    // tables, and for the 16-bit path each matrix-core GEMM's B operand
+    // (fragment-major, one K-contiguous row per output, K padded to whole
+    // 32-column steps with zeros, rows padded to GEMM_ROWS) with the f32
+    // staging it is converted from.
     const v5::Board bd = v5::board();
     const size_t o_w = 0, o_b = align256(nw * 4), o_ln = o_b + align256(nb * 4), o_bd = o_ln + align256(nln * 4);
-    const size_t total = o_bd + align256(sizeof bd);
+    size_t total = o_bd + align256(sizeof bd);
+    const bool mfma = (precision_ == WC_F16 || precision_ == WC_BF16) && !v5_scalar_;
+    size_t o_m16[v5::M_COUNT] = {}, o_stage = 0, stage_floats = 0;
+    std::vector<float> stage;
+    if (mfma) {
+        for (uint32_t m = 0; m < v5::M_COUNT; m++) {
+            const v5::Span sp = v5::mat_span(L, m);
+            o_m16[m] = total;
+            total += align256(size_t(gemm_rows(sp.o)) * v5::kpad(sp.i) * 2);
+            stage_floats += size_t(v5::kpad(sp.i)) * sp.o;
+        }
+        o_stage = total;
+        total += align256(stage_floats * 4);
+        stage.assign(stage_floats, 0.0f);
+        size_t at = 0;
+        for (uint32_t m = 0; m < v5::M_COUNT; m++) {  // [kpad(i) x o], rows past i zero
+            const v5::Span sp = v5::mat_span(L, m);
+            std::copy(w + sp.w, w + sp.w + size_t(sp.i) * sp.o, stage.begin() + at);
+            at += size_t(v5::kpad(sp.i)) * sp.o;
+        }
+    }
     void* mem = nullptr;
     if (hipMalloc(&mem, total) != hipSuccess) {
         *err = "hipMalloc of the weight bank failed";
@@ -185,8 +210,20 @@ uint64_t Executor::publish_v5(const NetShape& ns, const float* w, size_t nw, con
     bool okc = hipMemcpyAsync(base + o_w, w, nw * 4, hipMemcpyHostToDevice, stream_) == hipSuccess &&
                hipMemcpyAsync(base + o_b, b, nb * 4, hipMemcpyHostToDevice, stream_) == hipSuccess &&
                hipMemcpyAsync(base + o_ln, ln, nln * 4, hipMemcpyHostToDevice, stream_) == hipSuccess &&
-               hipMemcpyAsync(base + o_bd, &bd, sizeof bd, hipMemcpyHostToDevice, stream_) == hipSuccess &&
-               hipStreamSynchronize(stream_) == hipSuccess;
+               hipMemcpyAsync(base + o_bd, &bd, sizeof bd, hipMemcpyHostToDevice, stream_) == hipSuccess;
+    if (mfma) {
+        okc = okc && hipMemsetAsync(base + o_m16[0], 0, o_stage - o_m16[0], stream_) == hipSuccess &&
+              hipMemcpyAsync(base + o_stage, stage.data(), stage_floats * 4, hipMemcpyHostToDevice, stream_) ==
+                  hipSuccess;
+        size_t at = 0;
+        for (uint32_t m = 0; m < v5::M_COUNT && okc; m++) {
+            const v5::Span sp = v5::mat_span(L, m);
+            launch_to16(precision_, (const float*)(base + o_stage) + at, base + o_m16[m], sp.o, v5::kpad(sp.i), true,
+                        stream_);
+            at += size_t(v5::kpad(sp.i)) * sp.o;
+        }
+    }
+    okc = okc && hipStreamSynchronize(stream_) == hipSuccess && hipGetLastError() == hipSuccess;
     if (!okc) {
         hipFree(mem);
         *err = "weight upload failed";
@@ -202,6 +239,8 @@ uint64_t Executor::publish_v5(const NetShape& ns, const float* w, size_t nw, con
     bank.v5.nb = (const uint8_t*)(base + o_bd) + offsetof(v5::Board, nb);
     bank.v5.loc = (const uint8_t*)(base + o_bd) + offsetof(v5::Board, loc);
     bank.v5.value_bias = b[L.value_bias];
+    if (mfma)
+        for (uint32_t m = 0; m < v5::M_COUNT; m++) bank.v5.m16[m] = (const uint16_t*)(base + o_m16[m]);
     bank.version = next_version_++;
     banks_[bank.version] = bank;
     return bank.version;

@@ -20,6 +20,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "../../include/wc_wave.h"
 #include "kernels.h"
@@ -616,6 +617,202 @@ __global__ __launch_bounds__(JW) void k_join(Net net, uint32_t rows, const float
         }
 }
 
+// ------------------------------------------------------- join on MFMA
+
+typedef _Float16 v5half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 v5bf8 __attribute__((ext_vector_type(8)));
+typedef float v5f4 __attribute__((ext_vector_type(4)));
+
+template <int PREC>
+__device__ __forceinline__ v5f4 mma(const uint4& a, const uint4& b, const v5f4& c) {
+    if (PREC == WC_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v5half8, a), __builtin_bit_cast(v5half8, b),
+                                                      c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v5bf8, a), __builtin_bit_cast(v5bf8, b), c, 0,
+                                                   0, 0);
+}
+
+// GELU of the 16-bit path: the same formula, tanh through the hardware
+// exponential (the operands it feeds are rounded to 16 bits anyway).
+__device__ __forceinline__ float gelu_fast(float x) {
+    const float u = 0.79788456f * (x + 0.044715f * x * x * x);
+    const float e = __expf(-2.0f * fabsf(u));
+    const float t = (1.0f - e) / (1.0f + e);
+    return 0.5f * x * (1.0f + (u < 0.0f ? -t : t));
+}
+
+constexpr int JT_ROWS = 64;          // rows per join workgroup
+constexpr int JT_WAVES = 4;          // each owns a quarter of the columns
+constexpr int JT_LD = JW + 8;        // LDS row stride of the 16-bit operand (halves)
+
+// Net::join for a 64-row tile on the matrix cores (16x16x32, 16-bit operands,
+// f32 accumulate). The residual stream z stays in the accumulator registers;
+// LayerNorm statistics are summed per row across the four wavefronts through
+// LDS; each GELU output becomes the next product's A operand in LDS. In the
+// accumulator layout lane l holds rows 4 (l / 16) + v, column l % 16 of each
+// 16 x 16 tile; an A fragment is 8 consecutive k of row l % 16.
+template <int PREC>
+__global__ __launch_bounds__(JT_WAVES * 64) void k_join_mfma(Net net, uint32_t rows, const uint16_t* __restrict__ X,
+                                                            const float* __restrict__ P, const float* __restrict__ Jp,
+                                                            uint16_t* __restrict__ H) {
+    __shared__ __attribute__((aligned(16))) uint16_t tA[JT_ROWS * JT_LD];
+    __shared__ float part[JT_WAVES][JT_ROWS], mean[JT_ROWS], inv[JT_ROWS];
+    const uint32_t wv = threadIdx.x >> 6, l = threadIdx.x & 63, q = l >> 4, i = l & 15;
+    const uint32_t r0 = blockIdx.x * JT_ROWS;
+    constexpr uint32_t RB = JT_ROWS / 16;
+    // Per-row statistics of a wave's accumulators (NC column blocks each),
+    // combined across the wavefronts: mean, then 1 / sqrt(var + 1e-5).
+    auto row_stats = [&](auto& z, auto ncb, float width) {
+        constexpr uint32_t NC = decltype(ncb)::value;
+        for (int pass = 0; pass < 2; pass++) {
+#pragma unroll
+            for (uint32_t rb = 0; rb < RB; rb++)
+#pragma unroll
+                for (uint32_t v = 0; v < 4; v++) {
+                    const uint32_t r = rb * 16 + 4 * q + v;
+                    float sacc = 0.0f;
+#pragma unroll
+                    for (uint32_t cb = 0; cb < NC; cb++) {
+                        const float d = pass == 0 ? z[rb][cb][v] : z[rb][cb][v] - mean[r];
+                        sacc += pass == 0 ? d : d * d;
+                    }
+                    sacc += __shfl_xor(sacc, 1);
+                    sacc += __shfl_xor(sacc, 2);
+                    sacc += __shfl_xor(sacc, 4);
+                    sacc += __shfl_xor(sacc, 8);
+                    if (i == 0) part[wv][r] = sacc;
+                }
+            __syncthreads();
+            if (threadIdx.x < JT_ROWS) {
+                float t = 0.0f;
+                for (uint32_t w2 = 0; w2 < JT_WAVES; w2++) t += part[w2][threadIdx.x];
+                if (pass == 0)
+                    mean[threadIdx.x] = t / width;
+                else
+                    inv[threadIdx.x] = 1.0f / sqrtf(t / width + 1e-5f);
+            }
+            __syncthreads();
+        }
+    };
+    // gelu(LN(z)) of a 128-wide stream into the A operand in LDS (16-bit).
+    auto to_operand = [&](float (&z)[RB][2][4], uint32_t which) {
+        row_stats(z, std::integral_constant<uint32_t, 2>{}, (float)JW);
+#pragma unroll
+        for (uint32_t rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (uint32_t cb = 0; cb < 2; cb++) {
+                const uint32_t col = (wv * 2 + cb) * 16 + i;
+                const float g = net.ln[LY.norm_g[which] + col], bt = net.ln[LY.norm_b[which] + col];
+#pragma unroll
+                for (uint32_t v = 0; v < 4; v++) {
+                    const uint32_t r = rb * 16 + 4 * q + v;
+                    const float y = gelu_fast((z[rb][cb][v] - mean[r]) * inv[r] * g + bt);
+                    tA[r * JT_LD + col] = to16<PREC>(y);
+                }
+            }
+        __syncthreads();
+    };
+    // acc[rb][cb] += A B^T over K / 32 steps: A from the LDS operand (or the
+    // fragment-major X), B fragment-major rows = output columns.
+    auto gemm = [&](auto& acc, auto ncb, const uint16_t* W, uint32_t K, uint32_t cb0, bool from_x) {
+        constexpr uint32_t NC = decltype(ncb)::value;
+        const uint32_t ks = K / 32;
+        for (uint32_t s = 0; s < ks; s++) {
+            uint4 af[RB], bf[NC];
+#pragma unroll
+            for (uint32_t rb = 0; rb < RB; rb++) {
+                if (from_x)
+                    af[rb] = *(const uint4*)(X + ((size_t)((r0 >> 4) + rb) * ks * 64 + (size_t)s * 64 + l) * 8);
+                else
+                    af[rb] = *(const uint4*)(tA + (rb * 16 + i) * JT_LD + s * 32 + 8 * q);
+            }
+#pragma unroll
+            for (uint32_t cb = 0; cb < NC; cb++)
+                bf[cb] = *(const uint4*)(W + ((size_t)(cb0 + cb) * ks * 64 + (size_t)s * 64 + l) * 8);
+#pragma unroll
+            for (uint32_t rb = 0; rb < RB; rb++)
+#pragma unroll
+                for (uint32_t cb = 0; cb < NC; cb++) acc[rb][cb] = mma<PREC>(af[rb], bf[cb], acc[rb][cb]);
+        }
+    };
+    // z = Jp + X join_b + b
+    float z[RB][2][4];
+    {
+        v5f4 acc[RB][2];
+#pragma unroll
+        for (uint32_t rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (uint32_t cb = 0; cb < 2; cb++) acc[rb][cb] = v5f4{0.0f, 0.0f, 0.0f, 0.0f};
+        gemm(acc, std::integral_constant<uint32_t, 2>{}, net.m16[M_JOIN_B], JOIN_IN_PAD, wv * 2, true);
+#pragma unroll
+        for (uint32_t rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (uint32_t cb = 0; cb < 2; cb++) {
+                const uint32_t col = (wv * 2 + cb) * 16 + i;
+                const float bias = net.b[LY.join_b.b + col];
+#pragma unroll
+                for (uint32_t v = 0; v < 4; v++) {
+                    const uint32_t row = r0 + rb * 16 + 4 * q + v;
+                    const float jp = row < rows ? Jp[(size_t)row * JW + col] : 0.0f;
+                    z[rb][cb][v] = (jp + acc[rb][cb][v]) + bias;
+                }
+            }
+    }
+    for (uint32_t blk = 0; blk < JBLOCKS; blk++) {
+        to_operand(z, LN_JOIN + blk);
+        v5f4 acc[RB][2];
+#pragma unroll
+        for (uint32_t rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (uint32_t cb = 0; cb < 2; cb++) acc[rb][cb] = v5f4{0.0f, 0.0f, 0.0f, 0.0f};
+        gemm(acc, std::integral_constant<uint32_t, 2>{}, net.m16[M_JOIN_W0 + blk], JW, wv * 2, false);
+        __syncthreads();  // every wave has read the operand before the next one is written
+#pragma unroll
+        for (uint32_t rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (uint32_t cb = 0; cb < 2; cb++) {
+                const float bias = net.b[LY.join_w[blk].b + (wv * 2 + cb) * 16 + i];
+#pragma unroll
+                for (uint32_t v = 0; v < 4; v++) z[rb][cb][v] += acc[rb][cb][v] + bias;
+            }
+    }
+    to_operand(z, LN_JOUT);
+    // h = LN_H(P + z join_out + b), 256 wide: four column blocks per wave
+    v5f4 acc[RB][4];
+#pragma unroll
+    for (uint32_t rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (uint32_t cb = 0; cb < 4; cb++) acc[rb][cb] = v5f4{0.0f, 0.0f, 0.0f, 0.0f};
+    gemm(acc, std::integral_constant<uint32_t, 4>{}, net.m16[M_JOIN_OUT], JW, wv * 4, false);
+    float h[RB][4][4];
+#pragma unroll
+    for (uint32_t rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (uint32_t cb = 0; cb < 4; cb++) {
+            const uint32_t col = (wv * 4 + cb) * 16 + i;
+            const float bias = net.b[LY.join_out.b + col];
+#pragma unroll
+            for (uint32_t v = 0; v < 4; v++) {
+                const uint32_t row = r0 + rb * 16 + 4 * q + v;
+                const float pv = row < rows ? P[(size_t)row * D + col] : 0.0f;
+                h[rb][cb][v] = (pv + acc[rb][cb][v]) + bias;
+            }
+        }
+    row_stats(h, std::integral_constant<uint32_t, 4>{}, (float)D);
+#pragma unroll
+    for (uint32_t rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (uint32_t cb = 0; cb < 4; cb++) {
+            const uint32_t col = (wv * 4 + cb) * 16 + i;
+            const float g = net.ln[LY.norm_g[LN_H] + col], bt = net.ln[LY.norm_b[LN_H] + col];
+#pragma unroll
+            for (uint32_t v = 0; v < 4; v++) {
+                const uint32_t r = rb * 16 + 4 * q + v, row = r0 + r;
+                if (row < rows) H[frag_off(row, col, D)] = to16<PREC>((h[rb][cb][v] - mean[r]) * inv[r] * g + bt);
+            }
+        }
+}
+
 // The 16-bit query input (fragment-major, K = JOIN_IN_PAD) back to float32
 // rows of JOIN_IN for the rounded-operand join.
 template <int PREC>
@@ -654,6 +851,16 @@ void launch_join(int precision, const Net& net, uint32_t rows, const void* X, co
     const dim3 g((rows + JROWS - 1) / JROWS);
     if (precision == WC_PRECISE) {
         hipLaunchKernelGGL(k_join<WC_PRECISE>, g, dim3(JW), 0, s, net, rows, (const float*)X, P, Jp, (float*)H);
+        return;
+    }
+    if (net.m16[M_JOIN_B]) {  // the matrix-core join
+        const dim3 gt((rows + JT_ROWS - 1) / JT_ROWS);
+        if (precision == WC_F16)
+            hipLaunchKernelGGL(k_join_mfma<WC_F16>, gt, dim3(JT_WAVES * 64), 0, s, net, rows, (const uint16_t*)X, P,
+                               Jp, (uint16_t*)H);
+        else
+            hipLaunchKernelGGL(k_join_mfma<WC_BF16>, gt, dim3(JT_WAVES * 64), 0, s, net, rows, (const uint16_t*)X, P,
+                               Jp, (uint16_t*)H);
         return;
     }
     const size_t n = (size_t)rows * JOIN_IN;
