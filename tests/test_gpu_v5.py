@@ -106,8 +106,15 @@ def test_v5_solve_float32_bit_exact():
         np.testing.assert_array_equal(g.carries, o["carries"].astype(np.float16), err_msg=f"tree {k}: carries")
 
 
-@pytest.mark.parametrize("precision,mode,tol", [(ww.WC_F16, O.NET_F16A, 2e-3), (ww.WC_BF16, O.NET_BF16A, 1e-2)])
+@pytest.mark.parametrize("precision,mode,tol", [(ww.WC_F16, O.NET_F16A, 3e-3), (ww.WC_BF16, O.NET_BF16A, 3e-2)])
 def test_v5_leaf_probe_16bit_tracks_the_operand_model(precision, mode, tol):
+    """16-bit leaf values against the oracle's model of the same operand
+    rounding (max within tol of the largest value, median within tol / 6),
+    and no further from the float32 values than the model is (their median
+    distance within 1.5x the model's): through eight residual blocks a
+    different summation order moves activations across 16-bit rounding
+    boundaries, so two faithful 16-bit evaluations differ by about as much as
+    each differs from float32."""
     jobs = v5_jobs(seed=37)
     net = ww.synth_weights(ww.V5_DIMS, 1)
     ex = executor(precision)
@@ -115,20 +122,26 @@ def test_v5_leaf_probe_16bit_tracks_the_operand_model(precision, mode, tol):
         say(f"case v5 leaf probe precision {precision}: traverser {p}")
         got, mass = device_probe(ex, jobs, net, p)
         want, want_mass = oracle_probe(jobs, net, mode, p)
-        scale = float(np.abs(want).max())
+        exact, _ = oracle_probe(jobs, net, O.NET_F32, p)
+        scale = float(np.abs(exact).max())
         err = np.abs(got.astype(np.float64) - want)
-        say(f"max error {err.max() / scale:.2e}, median {np.median(err) / scale:.2e} of the largest |value|")
+        dev32 = float(np.median(np.abs(got.astype(np.float64) - exact)))
+        emu32 = float(np.median(np.abs(want.astype(np.float64) - exact)))
+        say(f"against the model: max {err.max() / scale:.2e}, median {np.median(err) / scale:.2e}; median distance "
+            f"to float32: device {dev32 / scale:.2e}, model {emu32 / scale:.2e} of the largest |value|")
         assert err.max() <= tol * scale
-        assert np.median(err) <= 0.05 * tol * scale
+        assert np.median(err) <= tol / 6 * scale
+        assert dev32 <= 1.5 * emu32 + 1e-6 * scale
         np.testing.assert_allclose(mass, want_mass, rtol=2e-6, atol=1e-30)
 
 
 @pytest.mark.parametrize("precision,mode", [(ww.WC_F16, O.NET_F16A), (ww.WC_BF16, O.NET_BF16A)])
-def test_v5_matrix_core_join_tracks_the_scalar_path(precision, mode):
-    """The join on the matrix cores (the default 16-bit path) against the same
-    operands summed in ascending float32 order (WC_V5_SCALAR=1) and the
-    oracle's model: the MFMA's own summation order and the hardware-exponential
-    GELU only."""
+def test_v5_matrix_cores_track_the_scalar_path(precision, mode):
+    """The trunk and the join on the matrix cores (the default 16-bit path)
+    against the same operands summed in ascending float32 order
+    (WC_V5_SCALAR=1, the oracle model's order): the MFMA's own summation
+    order, the LayerNorm statistics' order and the hardware-exponential GELU
+    only, within the 16-bit bounds above."""
     jobs = v5_jobs(seed=39)
     net = ww.synth_weights(ww.V5_DIMS, 1)
     os.environ["WC_V5_SCALAR"] = "1"
@@ -136,18 +149,20 @@ def test_v5_matrix_core_join_tracks_the_scalar_path(precision, mode):
         scalar = ww.Executor(0, precision)
     finally:
         del os.environ["WC_V5_SCALAR"]
+    tol = 3e-3 if precision == ww.WC_F16 else 3e-2
     try:
         for p in (0, 1):
-            say(f"case v5 matrix-core join precision {precision}: traverser {p}")
+            say(f"case v5 matrix cores precision {precision}: traverser {p}")
             got, _ = device_probe(executor(precision), jobs, net, p)
             ref, _ = device_probe(scalar, jobs, net, p)
             want, _ = oracle_probe(jobs, net, mode, p)
             scale = float(np.abs(want).max())
-            for tag, other in (("scalar path", ref), ("oracle model", want)):
-                err = np.abs(got.astype(np.float64) - other)
-                say(f"against the {tag}: max {err.max() / scale:.2e}, median {np.median(err) / scale:.2e}")
-                tol = 2e-3 if precision == ww.WC_F16 else 1e-2
-                assert err.max() <= tol * scale
-                assert np.median(err) <= 0.1 * tol * scale
+            # the scalar path is the oracle's model, bit for bit up to the readout's MFMA
+            np.testing.assert_allclose(ref, want, rtol=0, atol=1e-3 * scale)
+            err = np.abs(got.astype(np.float64) - ref)
+            say(f"matrix cores against the scalar path: max {err.max() / scale:.2e}, median "
+                f"{np.median(err) / scale:.2e} of the largest |value|")
+            assert err.max() <= tol * scale
+            assert np.median(err) <= tol / 6 * scale
     finally:
         scalar.close()

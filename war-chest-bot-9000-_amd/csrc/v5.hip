@@ -813,6 +813,291 @@ __global__ __launch_bounds__(JT_WAVES * 64) void k_join_mfma(Net net, uint32_t r
         }
 }
 
+// ------------------------------------------------------ trunk on MFMA
+
+constexpr int TT_ROWS = 2;                        // network rows per workgroup
+constexpr int TT_CELLS = TT_ROWS * HEXES;         // 74 hex cells
+constexpr int TT_RB = (TT_CELLS + 15) / 16;       // 5 row blocks of 16 cells
+constexpr int TT_WAVES = C / 16;                  // one 16-channel column block per wavefront
+constexpr int TT_LD = 2 * C + 8;                  // LDS row stride of the 16-bit operand (halves)
+constexpr int TT_BIN = 2 * C + LOOSE;             // board input width
+
+// Net::board + join_cache (net.rs:474-730) for two network rows on the
+// matrix cores: the mix (192 -> 96) and out (96 -> 96) products of every
+// residual block run as 16x16x32 MFMA over the 74 hex cells (five 16-cell
+// blocks), wavefront w owning channels 16 w .. 16 w + 15 with the residual
+// stream x in its accumulator registers. The post-norm activations a stay in
+// LDS in float32 (the neighbour sums and the mean / max pool read them); the
+// GEMM A operand ([a, neighbours], then the mid-block activations) in LDS in
+// 16 bits. The stem, the pool bias, the board vector and the join cache are
+// one or two rows each and stay scalar, with rounded operands where the
+// reference's fast mode runs them on tensor cores.
+template <int PREC>
+__global__ __launch_bounds__(TT_WAVES * 64) void k_trunk_mfma(Net net, WaveIn in, WaveOut out) {
+    __shared__ float aF[TT_RB * 16][C];
+    __shared__ __attribute__((aligned(16))) uint16_t A16[TT_RB * 16 * TT_LD];
+    __shared__ float part[TT_WAVES][TT_RB * 16], mean[TT_RB * 16], inv[TT_RB * 16];
+    __shared__ float pooled[TT_ROWS][2 * C], gb[TT_ROWS][C], bin[TT_ROWS][TT_BIN], Pv[TT_ROWS][D];
+    __shared__ float loose[TT_ROWS][LOOSE], tp[TT_ROWS][C], glob[TT_ROWS][C];
+    __shared__ int occ[TT_CELLS];
+    // stem scratch in the operand's space: tokens, projected tokens, hex facts
+    float* tok = (float*)A16;                           // [TT_ROWS][NTYPE][TYPE]
+    float* proj = tok + TT_ROWS * NTYPE * TYPE;         // [TT_ROWS][NTYPE][C]
+    float* facts = proj + TT_ROWS * NTYPE * C;          // [TT_CELLS][HEX_FACTS]
+    static_assert(sizeof(float) * (TT_ROWS * NTYPE * (TYPE + C) + TT_CELLS * HEX_FACTS) <= sizeof(A16), "stem scratch");
+    const uint32_t tid = threadIdx.x, wv = tid >> 6, l = tid & 63, q = l >> 4, i = l & 15;
+    const uint32_t row0 = blockIdx.x * TT_ROWS, nrow = min((uint32_t)TT_ROWS, in.rows - row0);
+    const float* W = net.w;
+    // ---- stem (net.rs:474-543), float32 loops
+    for (uint32_t x = tid; x < TT_ROWS * NTYPE * TYPE; x += TT_WAVES * 64) {
+        const uint32_t rr = x / (NTYPE * TYPE), t = (x / TYPE) % NTYPE, j = x % TYPE;
+        if (rr >= nrow) {  // the last workgroup's missing row: zeros
+            tok[x] = 0.0f;
+            continue;
+        }
+        const uint8_t* raw = in.raw + (size_t)(row0 + rr) * ROW_BYTES;
+        const float* cards = out.cards + (size_t)in.row_job[row0 + rr] * 2 * NTYPE * TYPE;  // view 0
+        float piles[PILE_COUNTS];
+        for (uint32_t f = 0; f < PILE_COUNTS; f++) piles[f] = (float)raw[GR_PILES + t * PILE_COUNTS + f] / 5.0f;
+        const float v = lin_out<PREC, false>(piles, PILE_COUNTS, W + LY.pile.w, TYPE, j, 0.0f, nullptr);
+        tok[x] = v + (cards[(size_t)t * TYPE + j] + W[LY.seat + (t / NSLOT) * TYPE + j]);
+    }
+    for (uint32_t x = tid; x < TT_CELLS; x += TT_WAVES * 64) {
+        const uint32_t rr = x / HEXES, h = x % HEXES;
+        if (rr >= nrow) {
+            occ[x] = -1;
+            for (uint32_t f = 0; f < HEX_FACTS; f++) facts[x * HEX_FACTS + f] = 0.0f;
+            continue;
+        }
+        const uint8_t* raw = in.raw + (size_t)(row0 + rr) * ROW_BYTES;
+        const int owner = raw[GR_HEX_OWNER + h], marker = raw[GR_HEX_MARKER + h], sl = raw[GR_HEX_SLOT + h];
+        float* fx = facts + x * HEX_FACTS;
+        fx[0] = owner == 0 ? 1.0f : 0.0f;
+        fx[1] = owner == 1 ? 1.0f : 0.0f;
+        fx[2] = (float)raw[GR_HEX_HEIGHT + h] / 5.0f;
+        fx[3] = marker == 0 ? 1.0f : 0.0f;
+        fx[4] = marker == 1 ? 1.0f : 0.0f;
+        fx[5] = (float)net.loc[h];
+        occ[x] = owner < 2 && sl < (int)NSLOT ? owner * (int)NSLOT + sl : -1;
+    }
+    if (tid < TT_ROWS * LOOSE) {
+        const uint32_t rr = tid / LOOSE, qq = tid % LOOSE;
+        float v = 0.0f;
+        if (rr < nrow) {
+            const uint8_t* raw = in.raw + (size_t)(row0 + rr) * ROW_BYTES;
+            if (qq < 12) {
+                const uint32_t p = qq / 6, k = qq % 6;
+                const int markers = raw[GR_MARKERS + p];
+                if (k == 0) v = (float)markers / 6.0f;
+                else if (k == 1) v = (float)(6 - markers) / 6.0f;
+                else if (k == 2) v = (float)raw[GR_HAND + p] / 3.0f;
+                else if (k == 3) v = (float)raw[GR_FD + p] / 21.0f;
+                else if (k == 4) v = (float)raw[GR_BAG + p] / 21.0f;
+                else v = raw[GR_INITIATIVE] == p ? 1.0f : 0.0f;
+            } else if (qq == 12) {
+                v = (float)((int)raw[GR_PLIES] | (int)raw[GR_PLIES + 1] << 8) / 256.0f;
+            } else if (qq == 13) {
+                v = raw[GR_INIT_MOVED] ? 1.0f : 0.0f;
+            } else {
+                v = raw[GR_TO_ACT] == 0 ? 1.0f : 0.0f;
+            }
+        }
+        loose[rr][qq] = v;
+    }
+    __syncthreads();
+    for (uint32_t x = tid; x < TT_ROWS * NTYPE * C; x += TT_WAVES * 64) {
+        const uint32_t rr = x / (NTYPE * C), t = (x / C) % NTYPE, j = x % C;
+        proj[x] = lin_out<PREC, false>(tok + (rr * NTYPE + t) * TYPE, TYPE, W + LY.tok_stem.w, C, j, 0.0f, nullptr);
+    }
+    __syncthreads();
+    for (uint32_t x = tid; x < TT_ROWS * C; x += TT_WAVES * 64) {
+        const uint32_t rr = x / C, j = x % C;
+        float v = 0.0f;
+        for (uint32_t t = 0; t < NTYPE; t++) v += gelu(proj[(rr * NTYPE + t) * C + j]) / (float)NTYPE;
+        tp[rr][j] = v;
+        glob[rr][j] = lin_out<PREC, false>(loose[rr], LOOSE, W + LY.glob_stem.w, C, j, 0.0f, nullptr);
+    }
+    __syncthreads();
+    const uint32_t col = wv * 16 + i;
+    float x[TT_RB][4];
+#pragma unroll
+    for (uint32_t rb = 0; rb < TT_RB; rb++)
+#pragma unroll
+        for (uint32_t v = 0; v < 4; v++) {
+            const uint32_t cell = rb * 16 + 4 * q + v;
+            float val = 0.0f;
+            if (cell < TT_CELLS) {
+                const uint32_t rr = cell / HEXES, h = cell % HEXES;
+                const float st =
+                    lin_out<PREC, false>(facts + cell * HEX_FACTS, HEX_FACTS, W + LY.hex_stem.w, C, col, 0.0f,
+                                         net.b + LY.hex_stem.b);
+                const float o = occ[cell] >= 0 ? proj[(rr * NTYPE + occ[cell]) * C + col] : 0.0f;
+                val = st + (((o + W[LY.pos + h * C + col]) + glob[rr][col]) + tp[rr][col]);
+            }
+            x[rb][v] = val;
+        }
+    __syncthreads();  // the stem scratch is free: the operand space is reused below
+    // Per-cell LayerNorm statistics of a 96-wide stream held as [rb][v] per lane
+    // (channel `col`), combined over the six wavefronts.
+    auto cell_stats = [&](float (&z)[TT_RB][4]) {
+        for (int pass = 0; pass < 2; pass++) {
+#pragma unroll
+            for (uint32_t rb = 0; rb < TT_RB; rb++)
+#pragma unroll
+                for (uint32_t v = 0; v < 4; v++) {
+                    const uint32_t cell = rb * 16 + 4 * q + v;
+                    float d = pass == 0 ? z[rb][v] : z[rb][v] - mean[cell];
+                    float sacc = pass == 0 ? d : d * d;
+                    sacc += __shfl_xor(sacc, 1);
+                    sacc += __shfl_xor(sacc, 2);
+                    sacc += __shfl_xor(sacc, 4);
+                    sacc += __shfl_xor(sacc, 8);
+                    if (i == 0) part[wv][cell] = sacc;
+                }
+            __syncthreads();
+            if (tid < TT_RB * 16) {
+                float t = 0.0f;
+                for (uint32_t w2 = 0; w2 < TT_WAVES; w2++) t += part[w2][tid];
+                if (pass == 0)
+                    mean[tid] = t / (float)C;
+                else
+                    inv[tid] = 1.0f / sqrtf(t / (float)C + 1e-5f);
+            }
+            __syncthreads();
+        }
+    };
+    auto norm_val = [&](float z, uint32_t cell, uint32_t which) {
+        return gelu_fast((z - mean[cell]) * inv[cell] * net.ln[LY.norm_g[which] + col] + net.ln[LY.norm_b[which] + col]);
+    };
+    // acc[rb] += A16 (K columns) B^T for this wave's column block.
+    auto gemm = [&](float (&acc)[TT_RB][4], const uint16_t* Wt, uint32_t K) {
+        const uint32_t ks = K / 32;
+        v5f4 c[TT_RB];
+#pragma unroll
+        for (uint32_t rb = 0; rb < TT_RB; rb++) c[rb] = v5f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t st = 0; st < ks; st++) {
+            const uint4 bf = *(const uint4*)(Wt + ((size_t)wv * ks * 64 + (size_t)st * 64 + l) * 8);
+#pragma unroll
+            for (uint32_t rb = 0; rb < TT_RB; rb++) {
+                const uint4 af = *(const uint4*)(A16 + (rb * 16 + i) * TT_LD + st * 32 + 8 * q);
+                c[rb] = mma<PREC>(af, bf, c[rb]);
+            }
+        }
+#pragma unroll
+        for (uint32_t rb = 0; rb < TT_RB; rb++)
+#pragma unroll
+            for (uint32_t v = 0; v < 4; v++) acc[rb][v] = c[rb][v];
+    };
+    for (uint32_t blk = 0; blk < BLOCKS; blk++) {
+        cell_stats(x);
+#pragma unroll
+        for (uint32_t rb = 0; rb < TT_RB; rb++)
+#pragma unroll
+            for (uint32_t v = 0; v < 4; v++) {
+                const uint32_t cell = rb * 16 + 4 * q + v;
+                const float a = cell < TT_CELLS ? norm_val(x[rb][v], cell, 2 * blk) : 0.0f;
+                aF[cell][col] = a;
+                A16[cell * TT_LD + col] = to16<PREC>(a);
+            }
+        __syncthreads();
+        // neighbour sums (zero start, directions in board order) into the
+        // operand's upper half, and the mean / max pool of each row
+        for (uint32_t x2 = tid; x2 < TT_RB * 16 * C; x2 += TT_WAVES * 64) {
+            const uint32_t cell = x2 / C, j = x2 % C;
+            float v = 0.0f;
+            if (cell < TT_CELLS) {
+                const uint32_t base = cell / HEXES * HEXES, h = cell % HEXES;
+                for (int d = 0; d < 6; d++) {
+                    const uint32_t n = net.nb[h * 6 + d];
+                    if (n < HEXES) v += aF[base + n][j];
+                }
+            }
+            A16[cell * TT_LD + C + j] = to16<PREC>(v);
+        }
+        for (uint32_t x2 = tid; x2 < TT_ROWS * C; x2 += TT_WAVES * 64) {
+            const uint32_t rr = x2 / C, j = x2 % C;
+            float mn = 0.0f, top = -INFINITY;
+            for (uint32_t h = 0; h < HEXES; h++) {
+                const float v = aF[rr * HEXES + h][j];
+                mn += v / (float)HEXES;
+                top = fmaxf(top, v);
+            }
+            pooled[rr][j] = mn;
+            pooled[rr][C + j] = top;
+        }
+        __syncthreads();
+        for (uint32_t x2 = tid; x2 < TT_ROWS * C; x2 += TT_WAVES * 64) {
+            const uint32_t rr = x2 / C, j = x2 % C;
+            gb[rr][j] = lin_out<PREC, true>(pooled[rr], 2 * C, W + LY.pool[blk].w, C, j, 0.0f, net.b + LY.pool[blk].b);
+        }
+        float y[TT_RB][4];
+        gemm(y, net.m16[M_MIX0 + blk], 2 * C);
+        __syncthreads();  // gb written; every wave has read the operand
+        {
+            const float bm = net.b[LY.mix[blk].b + col];
+#pragma unroll
+            for (uint32_t rb = 0; rb < TT_RB; rb++)
+#pragma unroll
+                for (uint32_t v = 0; v < 4; v++) {
+                    const uint32_t cell = rb * 16 + 4 * q + v;
+                    y[rb][v] = (y[rb][v] + bm) + (cell < TT_CELLS ? gb[cell / HEXES][col] : 0.0f);
+                }
+        }
+        cell_stats(y);
+#pragma unroll
+        for (uint32_t rb = 0; rb < TT_RB; rb++)
+#pragma unroll
+            for (uint32_t v = 0; v < 4; v++) {
+                const uint32_t cell = rb * 16 + 4 * q + v;
+                A16[cell * TT_LD + col] = to16<PREC>(cell < TT_CELLS ? norm_val(y[rb][v], cell, 2 * blk + 1) : 0.0f);
+            }
+        __syncthreads();
+        float z[TT_RB][4];
+        gemm(z, net.m16[M_OUT0 + blk], C);
+        __syncthreads();  // every wave has read the operand before the next block writes it
+        const float bo = net.b[LY.out[blk].b + col];
+#pragma unroll
+        for (uint32_t rb = 0; rb < TT_RB; rb++)
+#pragma unroll
+            for (uint32_t v = 0; v < 4; v++) x[rb][v] += z[rb][v] + bo;
+    }
+    cell_stats(x);
+#pragma unroll
+    for (uint32_t rb = 0; rb < TT_RB; rb++)
+#pragma unroll
+        for (uint32_t v = 0; v < 4; v++) {
+            const uint32_t cell = rb * 16 + 4 * q + v;
+            aF[cell][col] = cell < TT_CELLS ? norm_val(x[rb][v], cell, LN_TRUNK) : 0.0f;
+        }
+    __syncthreads();
+    // the board vector (net.rs:704-722) and its join projection, per row
+    for (uint32_t x2 = tid; x2 < TT_ROWS * C; x2 += TT_WAVES * 64) {
+        const uint32_t rr = x2 / C, j = x2 % C;
+        float mn = 0.0f, top = -INFINITY;
+        for (uint32_t h = 0; h < HEXES; h++) {
+            const float v = aF[rr * HEXES + h][j];
+            mn += v / (float)HEXES;
+            top = fmaxf(top, v);
+        }
+        bin[rr][j] = mn;
+        bin[rr][C + j] = top;
+    }
+    if (tid < TT_ROWS * LOOSE) bin[tid / LOOSE][2 * C + tid % LOOSE] = loose[tid / LOOSE][tid % LOOSE];
+    __syncthreads();
+    for (uint32_t x2 = tid; x2 < TT_ROWS * D; x2 += TT_WAVES * 64) {
+        const uint32_t rr = x2 / D, j = x2 % D;
+        const float v = lin_out<PREC, true>(bin[rr], TT_BIN, W + LY.board_out.w, D, j, 0.0f, net.b + LY.board_out.b);
+        Pv[rr][j] = v;
+        if (rr < nrow) out.P[(size_t)(row0 + rr) * D + j] = v;
+    }
+    __syncthreads();
+    for (uint32_t x2 = tid; x2 < TT_ROWS * JW; x2 += TT_WAVES * 64) {
+        const uint32_t rr = x2 / JW, j = x2 % JW;
+        if (rr < nrow)
+            out.Jp[(size_t)(row0 + rr) * JW + j] = lin_out<PREC, true>(Pv[rr], D, W + LY.join_p.w, JW, j, 0.0f, nullptr);
+    }
+}
+
 // The 16-bit query input (fragment-major, K = JOIN_IN_PAD) back to float32
 // rows of JOIN_IN for the rounded-operand join.
 template <int PREC>
@@ -830,11 +1115,15 @@ static_assert(sizeof(Net) < 1024, "kernel argument");
 
 void launch_build(int precision, const Net& net, const WaveIn& in, const WaveOut& out, hipStream_t s) {
     const uint32_t tokens = in.jobs * 2 * NTYPE;
-#define V5_BUILD(P)                                                                                   \
-    do {                                                                                              \
-        if (tokens) hipLaunchKernelGGL(k_cards<P>, dim3(tokens), dim3(NBLK), 0, s, net, in, out);     \
-        if (in.ncfg) hipLaunchKernelGGL(k_configs<P>, dim3(in.ncfg), dim3(NBLK), 0, s, net, in, out); \
-        if (in.rows) hipLaunchKernelGGL(k_trunk<P>, dim3(in.rows), dim3(NBLK), 0, s, net, in, out);   \
+#define V5_BUILD(P)                                                                                          \
+    do {                                                                                                     \
+        if (tokens) hipLaunchKernelGGL(k_cards<P>, dim3(tokens), dim3(NBLK), 0, s, net, in, out);            \
+        if (in.ncfg) hipLaunchKernelGGL(k_configs<P>, dim3(in.ncfg), dim3(NBLK), 0, s, net, in, out);        \
+        if (in.rows && P != WC_PRECISE && net.m16[M_MIX0])                                                   \
+            hipLaunchKernelGGL(k_trunk_mfma<P>, dim3((in.rows + TT_ROWS - 1) / TT_ROWS), dim3(TT_WAVES * 64), \
+                               0, s, net, in, out);                                                          \
+        else if (in.rows)                                                                                    \
+            hipLaunchKernelGGL(k_trunk<P>, dim3(in.rows), dim3(NBLK), 0, s, net, in, out);                   \
     } while (0)
     if (precision == WC_PRECISE)
         V5_BUILD(WC_PRECISE);
