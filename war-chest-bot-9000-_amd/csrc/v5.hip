@@ -148,6 +148,7 @@ Span mat_span(const Layout& L, uint32_t m) {
 namespace {
 
 constexpr int NBLK = 192;  // trunk and config workgroups
+__host__ __device__ constexpr uint32_t kpad_dev(uint32_t k) { return (k + 31) / 32 * 32; }
 constexpr int JROWS = 8;   // rows per join workgroup (float32 path)
 
 // The blob layout, computed at compile time for the kernels (the same
@@ -270,19 +271,23 @@ __device__ __forceinline__ uint16_t to16(float x) {
 template <int PREC, bool FAST>
 __device__ __forceinline__ float lin_out(const float* x, uint32_t k, const float* W, uint32_t o, uint32_t j,
                                          float start, const float* bias) {
+    // Weight loads are unconditional (every index is in range) so that the
+    // unrolled loop keeps several in flight; a zero input skips the addition.
     if (PREC == WC_PRECISE || !FAST) {
         float acc = start;
+#pragma unroll 8
         for (uint32_t p = 0; p < k; p++) {
-            const float a = x[p];
-            if (a != 0.0f) acc += a * W[(size_t)p * o + j];
+            const float a = x[p], w = W[(size_t)p * o + j];
+            acc = a != 0.0f ? acc + a * w : acc;
         }
         if (bias) acc += bias[j];
         return acc;
     }
     float acc = 0.0f;
+#pragma unroll 8
     for (uint32_t p = 0; p < k; p++) {
-        const float a = qop<PREC>(x[p]);
-        if (a != 0.0f) acc += a * qop<PREC>(W[(size_t)p * o + j]);
+        const float a = qop<PREC>(x[p]), w = qop<PREC>(W[(size_t)p * o + j]);
+        acc = a != 0.0f ? acc + a * w : acc;
     }
     float v = start + acc;
     if (bias) v += bias[j];
@@ -821,6 +826,7 @@ constexpr int TT_RB = (TT_CELLS + 15) / 16;       // 5 row blocks of 16 cells
 constexpr int TT_WAVES = C / 16;                  // one 16-channel column block per wavefront
 constexpr int TT_LD = 2 * C + 8;                  // LDS row stride of the 16-bit operand (halves)
 constexpr int TT_BIN = 2 * C + LOOSE;             // board input width
+constexpr int TT_SLD = D + 8;                     // LDS row stride of the per-row operand (halves)
 
 // Net::board + join_cache (net.rs:474-730) for two network rows on the
 // matrix cores: the mix (192 -> 96) and out (96 -> 96) products of every
@@ -833,13 +839,18 @@ constexpr int TT_BIN = 2 * C + LOOSE;             // board input width
 // one or two rows each and stay scalar, with rounded operands where the
 // reference's fast mode runs them on tensor cores.
 template <int PREC>
-__global__ __launch_bounds__(TT_WAVES * 64) void k_trunk_mfma(Net net, WaveIn in, WaveOut out) {
+__global__ __launch_bounds__(TT_WAVES * 64) __attribute__((amdgpu_waves_per_eu(3, 3))) void k_trunk_mfma(
+    Net net, WaveIn in, WaveOut out) {  // three waves per SIMD: two workgroups per CU
     __shared__ float aF[TT_RB * 16][C];
     __shared__ __attribute__((aligned(16))) uint16_t A16[TT_RB * 16 * TT_LD];
     __shared__ float part[TT_WAVES][TT_RB * 16], mean[TT_RB * 16], inv[TT_RB * 16];
-    __shared__ float pooled[TT_ROWS][2 * C], gb[TT_ROWS][C], bin[TT_ROWS][TT_BIN], Pv[TT_ROWS][D];
+    __shared__ float gb[TT_ROWS][C];
     __shared__ float loose[TT_ROWS][LOOSE], tp[TT_ROWS][C], glob[TT_ROWS][C];
+    // The A operand of the per-row products (pool bias, board vector, join
+    // cache): one 16-row block whose rows past TT_ROWS stay zero.
+    __shared__ __attribute__((aligned(16))) uint16_t S16[16 * TT_SLD];
     __shared__ int occ[TT_CELLS];
+    __shared__ uint8_t nbc[TT_RB * 16][6];  // each cell's neighbour cells (the zero padding cell when off board)
     // stem scratch in the operand's space: tokens, projected tokens, hex facts
     float* tok = (float*)A16;                           // [TT_ROWS][NTYPE][TYPE]
     float* proj = tok + TT_ROWS * NTYPE * TYPE;         // [TT_ROWS][NTYPE][C]
@@ -848,6 +859,34 @@ __global__ __launch_bounds__(TT_WAVES * 64) void k_trunk_mfma(Net net, WaveIn in
     const uint32_t tid = threadIdx.x, wv = tid >> 6, l = tid & 63, q = l >> 4, i = l & 15;
     const uint32_t row0 = blockIdx.x * TT_ROWS, nrow = min((uint32_t)TT_ROWS, in.rows - row0);
     const float* W = net.w;
+    for (uint32_t x2 = tid; x2 < 16 * TT_SLD; x2 += TT_WAVES * 64) S16[x2] = 0;
+    static_assert(TT_RB * 16 > TT_CELLS, "a zero padding cell stands for a missing neighbour");
+    for (uint32_t x2 = tid; x2 < TT_RB * 16 * 6; x2 += TT_WAVES * 64) {
+        const uint32_t cell = x2 / 6, d = x2 % 6;
+        uint32_t n = TT_RB * 16 - 1;
+        if (cell < TT_CELLS) {
+            const uint32_t h = cell % HEXES, nh = net.nb[h * 6 + d];
+            if (nh < HEXES) n = cell - h + nh;
+        }
+        nbc[cell][d] = (uint8_t)n;
+    }
+    // out[r][n] (r < TT_ROWS) of the per-row operand S16 (K columns) times Wt
+    // (N outputs): this wave's 16-column blocks, one 16x16x32 MFMA per k step;
+    // emit(r, n, acc) receives each valid entry.
+    auto row_gemm = [&](const uint16_t* Wt, uint32_t K, uint32_t N, auto emit) {
+        const uint32_t ks = K / 32;
+        for (uint32_t cb = wv; cb < N / 16; cb += TT_WAVES) {
+            v5f4 c = v5f4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (uint32_t st = 0; st < ks; st++) {
+                const uint4 af = *(const uint4*)(S16 + i * TT_SLD + st * 32 + 8 * q);
+                const uint4 bf = *(const uint4*)(Wt + ((size_t)cb * ks * 64 + (size_t)st * 64 + l) * 8);
+                c = mma<PREC>(af, bf, c);
+            }
+            if (q == 0)
+#pragma unroll
+                for (uint32_t v = 0; v < TT_ROWS; v++) emit(v, cb * 16 + i, c[v]);
+        }
+    };
     // ---- stem (net.rs:474-543), float32 loops
     for (uint32_t x = tid; x < TT_ROWS * NTYPE * TYPE; x += TT_WAVES * 64) {
         const uint32_t rr = x / (NTYPE * TYPE), t = (x / TYPE) % NTYPE, j = x % TYPE;
@@ -905,9 +944,26 @@ __global__ __launch_bounds__(TT_WAVES * 64) void k_trunk_mfma(Net net, WaveIn in
         loose[rr][qq] = v;
     }
     __syncthreads();
-    for (uint32_t x = tid; x < TT_ROWS * NTYPE * C; x += TT_WAVES * 64) {
-        const uint32_t rr = x / (NTYPE * C), t = (x / C) % NTYPE, j = x % C;
-        proj[x] = lin_out<PREC, false>(tok + (rr * NTYPE + t) * TYPE, TYPE, W + LY.tok_stem.w, C, j, 0.0f, nullptr);
+    {
+        // tok_stem (float32, no bias): a thread's outputs tid + k * 384 share
+        // the channel, so each weight is loaded once for all of them
+        constexpr uint32_t NT = TT_WAVES * 64, NOUT = TT_ROWS * NTYPE * C / NT;
+        static_assert(TT_ROWS * NTYPE * C % NT == 0 && NT % C == 0, "projection mapping");
+        const uint32_t j = tid % C;
+        float acc[NOUT];
+#pragma unroll
+        for (uint32_t k = 0; k < NOUT; k++) acc[k] = 0.0f;
+#pragma unroll 8
+        for (uint32_t p = 0; p < TYPE; p++) {
+            const float wv2 = W[LY.tok_stem.w + p * C + j];
+#pragma unroll
+            for (uint32_t k = 0; k < NOUT; k++) {
+                const float a = tok[((tid + k * NT) / C) * TYPE + p];
+                acc[k] = a != 0.0f ? acc[k] + a * wv2 : acc[k];
+            }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < NOUT; k++) proj[tid + k * NT] = acc[k];
     }
     __syncthreads();
     for (uint32_t x = tid; x < TT_ROWS * C; x += TT_WAVES * 64) {
@@ -920,6 +976,10 @@ __global__ __launch_bounds__(TT_WAVES * 64) void k_trunk_mfma(Net net, WaveIn in
     __syncthreads();
     const uint32_t col = wv * 16 + i;
     float x[TT_RB][4];
+    float whex[HEX_FACTS];
+#pragma unroll
+    for (uint32_t f = 0; f < HEX_FACTS; f++) whex[f] = W[LY.hex_stem.w + f * C + col];
+    const float bhex = net.b[LY.hex_stem.b + col];
 #pragma unroll
     for (uint32_t rb = 0; rb < TT_RB; rb++)
 #pragma unroll
@@ -928,9 +988,13 @@ __global__ __launch_bounds__(TT_WAVES * 64) void k_trunk_mfma(Net net, WaveIn in
             float val = 0.0f;
             if (cell < TT_CELLS) {
                 const uint32_t rr = cell / HEXES, h = cell % HEXES;
-                const float st =
-                    lin_out<PREC, false>(facts + cell * HEX_FACTS, HEX_FACTS, W + LY.hex_stem.w, C, col, 0.0f,
-                                         net.b + LY.hex_stem.b);
+                float st = 0.0f;  // hex_stem: the float32 loop, then the bias
+#pragma unroll
+                for (uint32_t f = 0; f < HEX_FACTS; f++) {
+                    const float a = facts[cell * HEX_FACTS + f];
+                    st = a != 0.0f ? st + a * whex[f] : st;
+                }
+                st += bhex;
                 const float o = occ[cell] >= 0 ? proj[(rr * NTYPE + occ[cell]) * C + col] : 0.0f;
                 val = st + (((o + W[LY.pos + h * C + col]) + glob[rr][col]) + tp[rr][col]);
             }
@@ -969,26 +1033,35 @@ __global__ __launch_bounds__(TT_WAVES * 64) void k_trunk_mfma(Net net, WaveIn in
     auto norm_val = [&](float z, uint32_t cell, uint32_t which) {
         return gelu_fast((z - mean[cell]) * inv[cell] * net.ln[LY.norm_g[which] + col] + net.ln[LY.norm_b[which] + col]);
     };
-    // acc[rb] += A16 (K columns) B^T for this wave's column block.
-    auto gemm = [&](float (&acc)[TT_RB][4], const uint16_t* Wt, uint32_t K) {
-        const uint32_t ks = K / 32;
+    // This wave's B fragments (its 16-column block) of a K-column matrix,
+    // loaded ahead of the product that uses them.
+    auto load_b = [&](uint4* bf, const uint16_t* Wt, auto kk) {
+        constexpr uint32_t ks = decltype(kk)::value / 32;
+#pragma unroll
+        for (uint32_t st = 0; st < ks; st++) bf[st] = *(const uint4*)(Wt + ((size_t)wv * ks * 64 + (size_t)st * 64 + l) * 8);
+    };
+    // acc[rb] = A16 (K columns) B^T for this wave's column block.
+    auto gemm = [&](float (&acc)[TT_RB][4], const uint4* bf, auto kk) {
+        constexpr uint32_t ks = decltype(kk)::value / 32;
         v5f4 c[TT_RB];
 #pragma unroll
         for (uint32_t rb = 0; rb < TT_RB; rb++) c[rb] = v5f4{0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint32_t st = 0; st < ks; st++) {
-            const uint4 bf = *(const uint4*)(Wt + ((size_t)wv * ks * 64 + (size_t)st * 64 + l) * 8);
+#pragma unroll
+        for (uint32_t st = 0; st < ks; st++)
 #pragma unroll
             for (uint32_t rb = 0; rb < TT_RB; rb++) {
                 const uint4 af = *(const uint4*)(A16 + (rb * 16 + i) * TT_LD + st * 32 + 8 * q);
-                c[rb] = mma<PREC>(af, bf, c[rb]);
+                c[rb] = mma<PREC>(af, bf[st], c[rb]);
             }
-        }
 #pragma unroll
         for (uint32_t rb = 0; rb < TT_RB; rb++)
 #pragma unroll
             for (uint32_t v = 0; v < 4; v++) acc[rb][v] = c[rb][v];
     };
+    using K96 = std::integral_constant<uint32_t, C>;
+    using K192 = std::integral_constant<uint32_t, 2 * C>;
     for (uint32_t blk = 0; blk < BLOCKS; blk++) {
+        uint4 bmix[2 * C / 32], bpool[2 * C / 32];
         cell_stats(x);
 #pragma unroll
         for (uint32_t rb = 0; rb < TT_RB; rb++)
@@ -1000,19 +1073,22 @@ __global__ __launch_bounds__(TT_WAVES * 64) void k_trunk_mfma(Net net, WaveIn in
                 A16[cell * TT_LD + col] = to16<PREC>(a);
             }
         __syncthreads();
+        load_b(bpool, net.m16[M_POOL0 + blk], K192{});
+        load_b(bmix, net.m16[M_MIX0 + blk], K192{});
         // neighbour sums (zero start, directions in board order) into the
         // operand's upper half, and the mean / max pool of each row
-        for (uint32_t x2 = tid; x2 < TT_RB * 16 * C; x2 += TT_WAVES * 64) {
-            const uint32_t cell = x2 / C, j = x2 % C;
-            float v = 0.0f;
-            if (cell < TT_CELLS) {
-                const uint32_t base = cell / HEXES * HEXES, h = cell % HEXES;
-                for (int d = 0; d < 6; d++) {
-                    const uint32_t n = net.nb[h * 6 + d];
-                    if (n < HEXES) v += aF[base + n][j];
-                }
+        {
+            // a thread's elements share channel j: cells c0, c0 + 4, ... (384 = 4 x 96)
+            constexpr uint32_t NT = TT_WAVES * 64, STEP = NT / C;
+            static_assert(NT % C == 0 && (TT_RB * 16) % STEP == 0, "neighbour mapping");
+            const uint32_t j = tid % C, c0 = tid / C;
+#pragma unroll 1
+            for (uint32_t cell = c0; cell < TT_RB * 16; cell += STEP) {
+                float v = 0.0f;  // directions in board order; off board reads the zero cell
+#pragma unroll
+                for (int d = 0; d < 6; d++) v += aF[nbc[cell][d]][j];
+                A16[cell * TT_LD + C + j] = to16<PREC>(v);
             }
-            A16[cell * TT_LD + C + j] = to16<PREC>(v);
         }
         for (uint32_t x2 = tid; x2 < TT_ROWS * C; x2 += TT_WAVES * 64) {
             const uint32_t rr = x2 / C, j = x2 % C;
@@ -1022,16 +1098,23 @@ __global__ __launch_bounds__(TT_WAVES * 64) void k_trunk_mfma(Net net, WaveIn in
                 mn += v / (float)HEXES;
                 top = fmaxf(top, v);
             }
-            pooled[rr][j] = mn;
-            pooled[rr][C + j] = top;
+            S16[rr * TT_SLD + j] = to16<PREC>(mn);
+            S16[rr * TT_SLD + C + j] = to16<PREC>(top);
         }
         __syncthreads();
-        for (uint32_t x2 = tid; x2 < TT_ROWS * C; x2 += TT_WAVES * 64) {
-            const uint32_t rr = x2 / C, j = x2 % C;
-            gb[rr][j] = lin_out<PREC, true>(pooled[rr], 2 * C, W + LY.pool[blk].w, C, j, 0.0f, net.b + LY.pool[blk].b);
+        {  // the pool bias: one 16-column block per wave (C / 16 = TT_WAVES)
+            v5f4 c = v5f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t st = 0; st < 2 * C / 32; st++)
+                c = mma<PREC>(*(const uint4*)(S16 + i * TT_SLD + st * 32 + 8 * q), bpool[st], c);
+            if (q == 0)
+#pragma unroll
+                for (uint32_t v = 0; v < TT_ROWS; v++) gb[v][col] = c[v] + net.b[LY.pool[blk].b + col];
         }
         float y[TT_RB][4];
-        gemm(y, net.m16[M_MIX0 + blk], 2 * C);
+        gemm(y, bmix, K192{});
+        uint4 bout[C / 32];
+        load_b(bout, net.m16[M_OUT0 + blk], K96{});
         __syncthreads();  // gb written; every wave has read the operand
         {
             const float bm = net.b[LY.mix[blk].b + col];
@@ -1053,7 +1136,7 @@ __global__ __launch_bounds__(TT_WAVES * 64) void k_trunk_mfma(Net net, WaveIn in
             }
         __syncthreads();
         float z[TT_RB][4];
-        gemm(z, net.m16[M_OUT0 + blk], C);
+        gemm(z, bout, K96{});
         __syncthreads();  // every wave has read the operand before the next block writes it
         const float bo = net.b[LY.out[blk].b + col];
 #pragma unroll
@@ -1070,7 +1153,8 @@ __global__ __launch_bounds__(TT_WAVES * 64) void k_trunk_mfma(Net net, WaveIn in
             aF[cell][col] = cell < TT_CELLS ? norm_val(x[rb][v], cell, LN_TRUNK) : 0.0f;
         }
     __syncthreads();
-    // the board vector (net.rs:704-722) and its join projection, per row
+    // the board vector (net.rs:704-722) and its join projection, per row:
+    // [mean, max, loose] (zero-padded to whole k steps) as the operand
     for (uint32_t x2 = tid; x2 < TT_ROWS * C; x2 += TT_WAVES * 64) {
         const uint32_t rr = x2 / C, j = x2 % C;
         float mn = 0.0f, top = -INFINITY;
@@ -1079,23 +1163,26 @@ __global__ __launch_bounds__(TT_WAVES * 64) void k_trunk_mfma(Net net, WaveIn in
             mn += v / (float)HEXES;
             top = fmaxf(top, v);
         }
-        bin[rr][j] = mn;
-        bin[rr][C + j] = top;
+        S16[rr * TT_SLD + j] = to16<PREC>(mn);
+        S16[rr * TT_SLD + C + j] = to16<PREC>(top);
     }
-    if (tid < TT_ROWS * LOOSE) bin[tid / LOOSE][2 * C + tid % LOOSE] = loose[tid / LOOSE][tid % LOOSE];
-    __syncthreads();
-    for (uint32_t x2 = tid; x2 < TT_ROWS * D; x2 += TT_WAVES * 64) {
-        const uint32_t rr = x2 / D, j = x2 % D;
-        const float v = lin_out<PREC, true>(bin[rr], TT_BIN, W + LY.board_out.w, D, j, 0.0f, net.b + LY.board_out.b);
-        Pv[rr][j] = v;
-        if (rr < nrow) out.P[(size_t)(row0 + rr) * D + j] = v;
+    for (uint32_t x2 = tid; x2 < TT_ROWS * (kpad_dev(TT_BIN) - 2 * C); x2 += TT_WAVES * 64) {
+        const uint32_t rr = x2 / (kpad_dev(TT_BIN) - 2 * C), qq = x2 % (kpad_dev(TT_BIN) - 2 * C);
+        S16[rr * TT_SLD + 2 * C + qq] = to16<PREC>(qq < LOOSE ? loose[rr][qq] : 0.0f);
     }
     __syncthreads();
-    for (uint32_t x2 = tid; x2 < TT_ROWS * JW; x2 += TT_WAVES * 64) {
-        const uint32_t rr = x2 / JW, j = x2 % JW;
-        if (rr < nrow)
-            out.Jp[(size_t)(row0 + rr) * JW + j] = lin_out<PREC, true>(Pv[rr], D, W + LY.join_p.w, JW, j, 0.0f, nullptr);
-    }
+    float* Pf = aF[0];  // the two rows' board vectors, float32, in the activations' space
+    row_gemm(net.m16[M_BOARD], kpad_dev(TT_BIN), D, [&](uint32_t r, uint32_t n, float acc) {
+        const float v = acc + net.b[LY.board_out.b + n];
+        Pf[r * D + n] = v;
+        if (r < nrow) out.P[(size_t)(row0 + r) * D + n] = v;
+    });
+    __syncthreads();
+    for (uint32_t x2 = tid; x2 < TT_ROWS * D; x2 += TT_WAVES * 64) S16[(x2 / D) * TT_SLD + x2 % D] = to16<PREC>(Pf[x2]);
+    __syncthreads();
+    row_gemm(net.m16[M_JOIN_P], D, JW, [&](uint32_t r, uint32_t n, float acc) {
+        if (r < nrow) out.Jp[(size_t)(row0 + r) * JW + n] = acc;
+    });
 }
 
 // The 16-bit query input (fragment-major, K = JOIN_IN_PAD) back to float32
