@@ -647,15 +647,20 @@ __device__ __forceinline__ float gelu_fast(float x) {
 }
 
 constexpr int JT_ROWS = 64;          // rows per join workgroup
-constexpr int JT_WAVES = 4;          // each owns a quarter of the columns
+constexpr int JT_WAVES = 8;          // wavefront w owns columns 16 w .. 16 w + 15 of the 128-wide stream
 constexpr int JT_LD = JW + 8;        // LDS row stride of the 16-bit operand (halves)
+constexpr int JT_RB = JT_ROWS / 16;  // row blocks per tile
 
 // Net::join for a 64-row tile on the matrix cores (16x16x32, 16-bit operands,
-// f32 accumulate). The residual stream z stays in the accumulator registers;
-// LayerNorm statistics are summed per row across the four wavefronts through
-// LDS; each GELU output becomes the next product's A operand in LDS. In the
-// accumulator layout lane l holds rows 4 (l / 16) + v, column l % 16 of each
-// 16 x 16 tile; an A fragment is 8 consecutive k of row l % 16.
+// f32 accumulate). Eight wavefronts: wavefront w owns one 16-column block of
+// the 128-wide residual stream z (in its accumulator registers) and two of
+// the 256-wide output. LayerNorm statistics are summed per row across the
+// wavefronts through LDS; each GELU output becomes the next product's A
+// operand in LDS. Every product's B fragments (the wave's column block, all
+// k steps) are loaded before the norm that precedes the product, so their L2
+// latency overlaps it. In the accumulator layout lane l holds rows
+// 4 (l / 16) + v, column l % 16 of each 16 x 16 tile; an A fragment is 8
+// consecutive k of row l % 16.
 template <int PREC>
 __global__ __launch_bounds__(JT_WAVES * 64) void k_join_mfma(Net net, uint32_t rows, const uint16_t* __restrict__ X,
                                                             const float* __restrict__ P, const float* __restrict__ Jp,
@@ -664,14 +669,14 @@ __global__ __launch_bounds__(JT_WAVES * 64) void k_join_mfma(Net net, uint32_t r
     __shared__ float part[JT_WAVES][JT_ROWS], mean[JT_ROWS], inv[JT_ROWS];
     const uint32_t wv = threadIdx.x >> 6, l = threadIdx.x & 63, q = l >> 4, i = l & 15;
     const uint32_t r0 = blockIdx.x * JT_ROWS;
-    constexpr uint32_t RB = JT_ROWS / 16;
-    // Per-row statistics of a wave's accumulators (NC column blocks each),
+    const uint32_t col = wv * 16 + i;  // this lane's column of the 128-wide stream
+    // Per-row statistics of the wave's accumulators (NC column blocks each),
     // combined across the wavefronts: mean, then 1 / sqrt(var + 1e-5).
     auto row_stats = [&](auto& z, auto ncb, float width) {
         constexpr uint32_t NC = decltype(ncb)::value;
         for (int pass = 0; pass < 2; pass++) {
 #pragma unroll
-            for (uint32_t rb = 0; rb < RB; rb++)
+            for (uint32_t rb = 0; rb < JT_RB; rb++)
 #pragma unroll
                 for (uint32_t v = 0; v < 4; v++) {
                     const uint32_t r = rb * 16 + 4 * q + v;
@@ -690,6 +695,7 @@ __global__ __launch_bounds__(JT_WAVES * 64) void k_join_mfma(Net net, uint32_t r
             __syncthreads();
             if (threadIdx.x < JT_ROWS) {
                 float t = 0.0f;
+#pragma unroll
                 for (uint32_t w2 = 0; w2 < JT_WAVES; w2++) t += part[w2][threadIdx.x];
                 if (pass == 0)
                     mean[threadIdx.x] = t / width;
@@ -699,123 +705,113 @@ __global__ __launch_bounds__(JT_WAVES * 64) void k_join_mfma(Net net, uint32_t r
             __syncthreads();
         }
     };
-    // gelu(LN(z)) of a 128-wide stream into the A operand in LDS (16-bit).
-    auto to_operand = [&](float (&z)[RB][2][4], uint32_t which) {
-        row_stats(z, std::integral_constant<uint32_t, 2>{}, (float)JW);
+    // gelu(LN(z)) of the 128-wide stream into the A operand in LDS (16-bit).
+    auto to_operand = [&](float (&z)[JT_RB][1][4], uint32_t which) {
+        row_stats(z, std::integral_constant<uint32_t, 1>{}, (float)JW);
+        const float g = net.ln[LY.norm_g[which] + col], bt = net.ln[LY.norm_b[which] + col];
 #pragma unroll
-        for (uint32_t rb = 0; rb < RB; rb++)
+        for (uint32_t rb = 0; rb < JT_RB; rb++)
 #pragma unroll
-            for (uint32_t cb = 0; cb < 2; cb++) {
-                const uint32_t col = (wv * 2 + cb) * 16 + i;
-                const float g = net.ln[LY.norm_g[which] + col], bt = net.ln[LY.norm_b[which] + col];
-#pragma unroll
-                for (uint32_t v = 0; v < 4; v++) {
-                    const uint32_t r = rb * 16 + 4 * q + v;
-                    const float y = gelu_fast((z[rb][cb][v] - mean[r]) * inv[r] * g + bt);
-                    tA[r * JT_LD + col] = to16<PREC>(y);
-                }
+            for (uint32_t v = 0; v < 4; v++) {
+                const uint32_t r = rb * 16 + 4 * q + v;
+                tA[r * JT_LD + col] = to16<PREC>(gelu_fast((z[rb][0][v] - mean[r]) * inv[r] * g + bt));
             }
         __syncthreads();
     };
-    // acc[rb][cb] += A B^T over K / 32 steps: A from the LDS operand (or the
-    // fragment-major X), B fragment-major rows = output columns.
-    auto gemm = [&](auto& acc, auto ncb, const uint16_t* W, uint32_t K, uint32_t cb0, bool from_x) {
-        constexpr uint32_t NC = decltype(ncb)::value;
-        const uint32_t ks = K / 32;
-        for (uint32_t s = 0; s < ks; s++) {
-            uint4 af[RB], bf[NC];
+    // B fragments of column blocks cb0 .. cb0 + NC - 1 over KS k steps.
+    auto load_b = [&](auto& bf, const uint16_t* W, uint32_t cb0) {
+        constexpr uint32_t KS = sizeof(bf) / sizeof(bf[0]);
+        constexpr uint32_t NC = sizeof(bf[0]) / sizeof(uint4);
 #pragma unroll
-            for (uint32_t rb = 0; rb < RB; rb++) {
-                if (from_x)
-                    af[rb] = *(const uint4*)(X + ((size_t)((r0 >> 4) + rb) * ks * 64 + (size_t)s * 64 + l) * 8);
-                else
-                    af[rb] = *(const uint4*)(tA + (rb * 16 + i) * JT_LD + s * 32 + 8 * q);
-            }
+        for (uint32_t s = 0; s < KS; s++)
 #pragma unroll
             for (uint32_t cb = 0; cb < NC; cb++)
-                bf[cb] = *(const uint4*)(W + ((size_t)(cb0 + cb) * ks * 64 + (size_t)s * 64 + l) * 8);
+                bf[s][cb] = *(const uint4*)(W + ((size_t)(cb0 + cb) * KS * 64 + (size_t)s * 64 + l) * 8);
+    };
+    // acc[rb][cb] = A B^T: A from the LDS operand (or the fragment-major X).
+    auto gemm = [&](auto& acc, const auto& bf, bool from_x) {
+        constexpr uint32_t KS = sizeof(bf) / sizeof(bf[0]);
+        constexpr uint32_t NC = sizeof(bf[0]) / sizeof(uint4);
 #pragma unroll
-            for (uint32_t rb = 0; rb < RB; rb++)
+        for (uint32_t rb = 0; rb < JT_RB; rb++)
 #pragma unroll
-                for (uint32_t cb = 0; cb < NC; cb++) acc[rb][cb] = mma<PREC>(af[rb], bf[cb], acc[rb][cb]);
+            for (uint32_t cb = 0; cb < NC; cb++) acc[rb][cb] = v5f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t s = 0; s < KS; s++) {
+            uint4 af[JT_RB];
+#pragma unroll
+            for (uint32_t rb = 0; rb < JT_RB; rb++)
+                af[rb] = from_x ? *(const uint4*)(X + ((size_t)((r0 >> 4) + rb) * KS * 64 + (size_t)s * 64 + l) * 8)
+                                : *(const uint4*)(tA + (rb * 16 + i) * JT_LD + s * 32 + 8 * q);
+#pragma unroll
+            for (uint32_t rb = 0; rb < JT_RB; rb++)
+#pragma unroll
+                for (uint32_t cb = 0; cb < NC; cb++) acc[rb][cb] = mma<PREC>(af[rb], bf[s][cb], acc[rb][cb]);
         }
     };
     // z = Jp + X join_b + b
-    float z[RB][2][4];
+    float z[JT_RB][1][4];
+    uint4 bw[JW / 32][1];
     {
-        v5f4 acc[RB][2];
+        uint4 bb[JOIN_IN_PAD / 32][1];
+        load_b(bb, net.m16[M_JOIN_B], wv);
+        v5f4 acc[JT_RB][1];
+        gemm(acc, bb, true);
+        const float bias = net.b[LY.join_b.b + col];
 #pragma unroll
-        for (uint32_t rb = 0; rb < RB; rb++)
-#pragma unroll
-            for (uint32_t cb = 0; cb < 2; cb++) acc[rb][cb] = v5f4{0.0f, 0.0f, 0.0f, 0.0f};
-        gemm(acc, std::integral_constant<uint32_t, 2>{}, net.m16[M_JOIN_B], JOIN_IN_PAD, wv * 2, true);
-#pragma unroll
-        for (uint32_t rb = 0; rb < RB; rb++)
-#pragma unroll
-            for (uint32_t cb = 0; cb < 2; cb++) {
-                const uint32_t col = (wv * 2 + cb) * 16 + i;
-                const float bias = net.b[LY.join_b.b + col];
-#pragma unroll
-                for (uint32_t v = 0; v < 4; v++) {
-                    const uint32_t row = r0 + rb * 16 + 4 * q + v;
-                    const float jp = row < rows ? Jp[(size_t)row * JW + col] : 0.0f;
-                    z[rb][cb][v] = (jp + acc[rb][cb][v]) + bias;
-                }
-            }
-    }
-    for (uint32_t blk = 0; blk < JBLOCKS; blk++) {
-        to_operand(z, LN_JOIN + blk);
-        v5f4 acc[RB][2];
-#pragma unroll
-        for (uint32_t rb = 0; rb < RB; rb++)
-#pragma unroll
-            for (uint32_t cb = 0; cb < 2; cb++) acc[rb][cb] = v5f4{0.0f, 0.0f, 0.0f, 0.0f};
-        gemm(acc, std::integral_constant<uint32_t, 2>{}, net.m16[M_JOIN_W0 + blk], JW, wv * 2, false);
-        __syncthreads();  // every wave has read the operand before the next one is written
-#pragma unroll
-        for (uint32_t rb = 0; rb < RB; rb++)
-#pragma unroll
-            for (uint32_t cb = 0; cb < 2; cb++) {
-                const float bias = net.b[LY.join_w[blk].b + (wv * 2 + cb) * 16 + i];
-#pragma unroll
-                for (uint32_t v = 0; v < 4; v++) z[rb][cb][v] += acc[rb][cb][v] + bias;
-            }
-    }
-    to_operand(z, LN_JOUT);
-    // h = LN_H(P + z join_out + b), 256 wide: four column blocks per wave
-    v5f4 acc[RB][4];
-#pragma unroll
-    for (uint32_t rb = 0; rb < RB; rb++)
-#pragma unroll
-        for (uint32_t cb = 0; cb < 4; cb++) acc[rb][cb] = v5f4{0.0f, 0.0f, 0.0f, 0.0f};
-    gemm(acc, std::integral_constant<uint32_t, 4>{}, net.m16[M_JOIN_OUT], JW, wv * 4, false);
-    float h[RB][4][4];
-#pragma unroll
-    for (uint32_t rb = 0; rb < RB; rb++)
-#pragma unroll
-        for (uint32_t cb = 0; cb < 4; cb++) {
-            const uint32_t col = (wv * 4 + cb) * 16 + i;
-            const float bias = net.b[LY.join_out.b + col];
+        for (uint32_t rb = 0; rb < JT_RB; rb++)
 #pragma unroll
             for (uint32_t v = 0; v < 4; v++) {
                 const uint32_t row = r0 + rb * 16 + 4 * q + v;
-                const float pv = row < rows ? P[(size_t)row * D + col] : 0.0f;
+                const float jp = row < rows ? Jp[(size_t)row * JW + col] : 0.0f;
+                z[rb][0][v] = (jp + acc[rb][0][v]) + bias;
+            }
+    }
+    for (uint32_t blk = 0; blk < JBLOCKS; blk++) {
+        load_b(bw, net.m16[M_JOIN_W0 + blk], wv);
+        to_operand(z, LN_JOIN + blk);
+        v5f4 acc[JT_RB][1];
+        gemm(acc, bw, false);
+        __syncthreads();  // every wave has read the operand before the next one is written
+        const float bias = net.b[LY.join_w[blk].b + col];
+#pragma unroll
+        for (uint32_t rb = 0; rb < JT_RB; rb++)
+#pragma unroll
+            for (uint32_t v = 0; v < 4; v++) z[rb][0][v] += acc[rb][0][v] + bias;
+    }
+    // h = LN_H(P + z join_out + b), 256 wide: column blocks 2 w and 2 w + 1
+    uint4 bo[JW / 32][2];
+    load_b(bo, net.m16[M_JOIN_OUT], 2 * wv);
+    to_operand(z, LN_JOUT);
+    v5f4 acc[JT_RB][2];
+    gemm(acc, bo, false);
+    float h[JT_RB][2][4];
+#pragma unroll
+    for (uint32_t rb = 0; rb < JT_RB; rb++)
+#pragma unroll
+        for (uint32_t cb = 0; cb < 2; cb++) {
+            const uint32_t c2 = (2 * wv + cb) * 16 + i;
+            const float bias = net.b[LY.join_out.b + c2];
+#pragma unroll
+            for (uint32_t v = 0; v < 4; v++) {
+                const uint32_t row = r0 + rb * 16 + 4 * q + v;
+                const float pv = row < rows ? P[(size_t)row * D + c2] : 0.0f;
                 h[rb][cb][v] = (pv + acc[rb][cb][v]) + bias;
             }
         }
-    row_stats(h, std::integral_constant<uint32_t, 4>{}, (float)D);
+    row_stats(h, std::integral_constant<uint32_t, 2>{}, (float)D);
 #pragma unroll
-    for (uint32_t rb = 0; rb < RB; rb++)
+    for (uint32_t cb = 0; cb < 2; cb++) {
+        const uint32_t c2 = (2 * wv + cb) * 16 + i;
+        const float g = net.ln[LY.norm_g[LN_H] + c2], bt = net.ln[LY.norm_b[LN_H] + c2];
 #pragma unroll
-        for (uint32_t cb = 0; cb < 4; cb++) {
-            const uint32_t col = (wv * 4 + cb) * 16 + i;
-            const float g = net.ln[LY.norm_g[LN_H] + col], bt = net.ln[LY.norm_b[LN_H] + col];
+        for (uint32_t rb = 0; rb < JT_RB; rb++)
 #pragma unroll
             for (uint32_t v = 0; v < 4; v++) {
                 const uint32_t r = rb * 16 + 4 * q + v, row = r0 + r;
-                if (row < rows) H[frag_off(row, col, D)] = to16<PREC>((h[rb][cb][v] - mean[r]) * inv[r] * g + bt);
+                if (row < rows) H[frag_off(row, c2, D)] = to16<PREC>((h[rb][cb][v] - mean[r]) * inv[r] * g + bt);
             }
-        }
+    }
 }
 
 // ------------------------------------------------------ trunk on MFMA
