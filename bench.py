@@ -100,6 +100,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-mlp", action="store_true", help="skip the GEMM-chain-alone leg")
     ap.add_argument("--no-host", action="store_true", help="skip the host-path (PCIe-inclusive) leg")
+    ap.add_argument("--no-v5", action="store_true", help="skip the v5-network wave leg")
     ap.add_argument("--service", type=int, default=0, metavar="WAVES",
                     help="also stream WAVES copies of the wave's subgames through the service (wc_submit / wc_wait) "
                          "and report the end-to-end rate")
@@ -280,6 +281,35 @@ def main():
                             "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 5)}
         mex.close()
         log(f"[bench] GEMM chain alone: {chain_ms:.4f} ms, {tf:.1f} TFLOP/s")
+
+    if not args.no_v5:
+        # The reference's production leaf network (net_dims [5]) on the same
+        # 256 trees: per wave the card tokens, the board trunk of every
+        # network row and the config encoder; per iteration the pooled
+        # beliefs, the join and the readout (16-bit operands on the matrix cores).
+        vjobs = W.jobs("wave256v5")
+        vnet = W.net_for("wave256v5")
+        vex = ww.Executor(0, ww.WC_F16)
+        vv = vex.publish(vnet)
+        vwave = ww.Wave(vjobs)
+        vst = vwave.stats()
+        v_ms, v_parts = vex.time_wave(vwave, vv, reps=args.steps, warmup=args.warmup)
+        vwave.close()
+        vex.close()
+        v_ni = vst["nodes"] * vst["iters"]
+        vrows = vst["rows"]
+        # algorithmic FLOPs: the trunk per row (8 blocks of mix 192->96 and out 96->96 over
+        # 37 hexes, the pool bias 192->96, the board 207->256, the join cache 256->128) and the
+        # join per row and pass (129->128, 3 x 128->128, 128->256)
+        trunk = 8 * 37 * 2 * (192 * 96 + 96 * 96) + 8 * 2 * 192 * 96 + 2 * 207 * 256 + 2 * 256 * 128
+        join = 2 * (129 * 128 + 3 * 128 * 128 + 128 * 256)
+        out["v5_wave"] = {"workload": "wave256v5: the 256 depth-2 trees with the v5 leaf network, f16 operands",
+                          "ms_per_wave": round(v_ms, 3), "node_iters_per_s": round(v_ni / (v_ms * 1e-3), 1),
+                          "rows": vrows, "net_ms": round(v_parts[1], 3), "cfr_ms": round(v_parts[0], 3),
+                          "trunk_gflop_per_wave": round(vrows * trunk / 1e9, 2),
+                          "join_gflop_per_pass": round(vrows * join / 1e9, 3),
+                          "note": "net_ms = the per-wave build (cards, trunk, configs) + every join and readout"}
+        log(f"[bench] v5 wave: {v_ms:.2f} ms/wave ({v_parts[1]:.2f} ms in the network)")
 
     if not args.no_host:
         # The boundary takes host buffers: the same wave through wc_solve_wave

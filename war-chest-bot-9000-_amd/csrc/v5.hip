@@ -646,7 +646,7 @@ __device__ __forceinline__ float gelu_fast(float x) {
     return 0.5f * x * (1.0f + (u < 0.0f ? -t : t));
 }
 
-constexpr int JT_ROWS = 64;          // rows per join workgroup
+constexpr int JT_ROWS = 32;          // rows per join workgroup
 constexpr int JT_WAVES = 8;          // wavefront w owns columns 16 w .. 16 w + 15 of the 128-wide stream
 constexpr int JT_LD = JW + 8;        // LDS row stride of the 16-bit operand (halves)
 constexpr int JT_RB = JT_ROWS / 16;  // row blocks per tile

@@ -83,97 +83,145 @@ void append_shift(std::vector<T>& dst, const std::vector<T>& src, size_t skip, T
     }
 }
 
-// Row records from the task lists (see BackRec / ReachRec / AccRec).
+// Runs fn(lo, hi) over [0, n) in chunks on the host threads.
+template <class F>
+void chunked(size_t n, F fn, size_t chunk = 16384) {
+    parallel_for((n + chunk - 1) / chunk, [&](size_t c) { fn(c * chunk, std::min(n, (c + 1) * chunk)); });
+}
+
+// Row records from the task lists (see BackRec / ReachRec / AccRec). Every
+// record is a function of its task alone, once the opponent rows' child
+// value-base lists are laid out (first appearance among the value tasks, in
+// task order), so the records are built in parallel chunks.
 void build_records(WaveHost* wp) {
     WaveHost& w = *wp;
-    // The two players' records are independent (each thread writes only its
-    // player's lists and fields); the export bits of shared terminal entries
-    // are gathered per player and merged after.
-    std::vector<uint8_t> term_ex[2];
-    parallel_for(2, [&](size_t pi) {
+    std::vector<uint32_t> cvb_at[2];
+    parallel_for(2, [&](size_t pi) {  // the child value-base lists (serial per player: append order)
         const int p = (int)pi;
-        std::vector<uint32_t> cvb_at(w.nodes(), NONE);
-        auto back = [&](const Task& q) {
-            const uint32_t node = q.node, c = q.config;
+        cvb_at[p].assign(w.nodes(), NONE);
+        auto note = [&](const Task& q) {
+            const uint32_t node = q.node;
             const uint32_t kind = w.node_meta[node] & 3u, actor = w.node_meta[node] >> 2;
-            BackRec r{};
-            r.out = w.vals_base[2 * node + p] + c;
-            if (kind == 1) {
-                uint32_t child = w.child[w.child_start[node]];
-                uint32_t d0 = w.draw_off[node], rb = w.draw_row_off[node];
-                uint32_t lo = w.draw_row_start[rb + c], hi = w.draw_row_start[rb + c + 1];
-                r.arg = w.vals_base[2 * child + p];
-                r.start = d0 + lo;
-                r.kn = BACK_DRAW << 30 | (hi - lo);
-            } else if (actor != (uint32_t)p) {
-                if (cvb_at[node] == NONE) {
-                    cvb_at[node] = (uint32_t)w.child_vb[p].size();
-                    for (uint32_t x = w.child_start[node]; x < w.child_start[node + 1]; x++)
-                        w.child_vb[p].push_back(w.vals_base[2 * w.child[x] + p]);
-                }
-                r.arg = c;
-                r.start = cvb_at[node];
-                r.kn = BACK_OPP << 30 | (w.child_start[node + 1] - w.child_start[node]);
-            } else {
-                uint32_t row = w.legal_row_of[node] + c;
-                r.start = w.legal_off[row];
-                r.kn = BACK_OWN << 30 | (w.legal_off[row + 1] - w.legal_off[row]);
-            }
-            return r;
+            if (kind == 1 || actor == (uint32_t)p || cvb_at[p][node] != NONE) return;
+            cvb_at[p][node] = (uint32_t)w.child_vb[p].size();
+            for (uint32_t x = w.child_start[node]; x < w.child_start[node + 1]; x++)
+                w.child_vb[p].push_back(w.vals_base[2 * w.child[x] + p]);
         };
-        auto reach = [&](const Task& q) {
-            const uint32_t node = q.node, c = q.config;
-            ReachRec r{};
-            r.out = w.reach_base[2 * node + p] + c;
-            r.pbase = w.reach_base[2 * w.parent[node] + p];
-            if (w.rev_row_of[node] != NONE) {
-                uint32_t row = w.rev_row_of[node] + c;
-                r.start = w.rev_start[row];
-                r.kn = REACH_REV << 31 | (w.rev_start[row + 1] - w.rev_start[row]);
-            } else {
-                uint32_t row = w.rvd_row_of[node] + c;
-                r.start = w.rvd_start[row];
-                r.kn = REACH_RVD << 31 | (w.rvd_start[row + 1] - w.rvd_start[row]);
+        for (const Task& q : w.back_task[p]) note(q);
+        for (const Task& q : w.top_back[p]) note(q);
+    });
+    auto back = [&](int p, const Task& q) {
+        const uint32_t node = q.node, c = q.config;
+        const uint32_t kind = w.node_meta[node] & 3u, actor = w.node_meta[node] >> 2;
+        BackRec r{};
+        r.out = w.vals_base[2 * node + p] + c;
+        if (kind == 1) {
+            uint32_t child = w.child[w.child_start[node]];
+            uint32_t d0 = w.draw_off[node], rb = w.draw_row_off[node];
+            uint32_t lo = w.draw_row_start[rb + c], hi = w.draw_row_start[rb + c + 1];
+            r.arg = w.vals_base[2 * child + p];
+            r.start = d0 + lo;
+            r.kn = BACK_DRAW << 30 | (hi - lo);
+        } else if (actor != (uint32_t)p) {
+            r.arg = c;
+            r.start = cvb_at[p][node];
+            r.kn = BACK_OPP << 30 | (w.child_start[node + 1] - w.child_start[node]);
+        } else {
+            uint32_t row = w.legal_row_of[node] + c;
+            r.start = w.legal_off[row];
+            r.kn = BACK_OWN << 30 | (w.legal_off[row + 1] - w.legal_off[row]);
+        }
+        return r;
+    };
+    auto reach = [&](int p, const Task& q) {
+        const uint32_t node = q.node, c = q.config;
+        ReachRec r{};
+        r.out = w.reach_base[2 * node + p] + c;
+        r.pbase = w.reach_base[2 * w.parent[node] + p];
+        if (w.rev_row_of[node] != NONE) {
+            uint32_t row = w.rev_row_of[node] + c;
+            r.start = w.rev_start[row];
+            r.kn = REACH_REV << 31 | (w.rev_start[row + 1] - w.rev_start[row]);
+        } else {
+            uint32_t row = w.rvd_row_of[node] + c;
+            r.start = w.rvd_start[row];
+            r.kn = REACH_RVD << 31 | (w.rvd_start[row + 1] - w.rvd_start[row]);
+        }
+        return r;
+    };
+    for (int p = 0; p < 2; p++) {
+        w.back_rec[p].resize(w.back_task[p].size());
+        w.top_back_rec[p].resize(w.top_back[p].size());
+        w.reach_rec[p].resize(w.reach_task[p].size());
+        w.top_reach_rec[p].resize(w.top_reach[p].size());
+        w.acc_rec[p].resize(w.decision[p].size());
+    }
+    for (int p = 0; p < 2; p++) {
+        chunked(w.back_task[p].size(), [&](size_t lo, size_t hi) {
+            for (size_t k = lo; k < hi; k++) w.back_rec[p][k] = back(p, w.back_task[p][k]);
+        });
+        chunked(w.top_back[p].size(), [&](size_t lo, size_t hi) {
+            for (size_t k = lo; k < hi; k++) w.top_back_rec[p][k] = back(p, w.top_back[p][k]);
+        });
+        chunked(w.reach_task[p].size(), [&](size_t lo, size_t hi) {
+            for (size_t k = lo; k < hi; k++) w.reach_rec[p][k] = reach(p, w.reach_task[p][k]);
+        });
+        chunked(w.top_reach[p].size(), [&](size_t lo, size_t hi) {
+            for (size_t k = lo; k < hi; k++) w.top_reach_rec[p][k] = reach(p, w.top_reach[p][k]);
+        });
+        chunked(w.decision[p].size(), [&](size_t lo, size_t hi) {
+            for (size_t k = lo; k < hi; k++) {
+                const Task& q = w.decision[p][k];
+                const uint32_t row = w.legal_row_of[q.node] + q.config;
+                w.acc_rec[p][k] = {w.reach_base[2 * q.node + p] + q.config, w.legal_off[row],
+                                   w.legal_off[row + 1] - w.legal_off[row], 0};
             }
-            return r;
-        };
-        w.back_rec[p].reserve(w.back_task[p].size());
-        w.top_back_rec[p].reserve(w.top_back[p].size());
-        w.reach_rec[p].reserve(w.reach_task[p].size());
-        w.top_reach_rec[p].reserve(w.top_reach[p].size());
-        for (const Task& q : w.back_task[p]) w.back_rec[p].push_back(back(q));
-        for (const Task& q : w.top_back[p]) w.top_back_rec[p].push_back(back(q));
-        for (const Task& q : w.reach_task[p]) w.reach_rec[p].push_back(reach(q));
-        for (const Task& q : w.top_reach[p]) w.top_reach_rec[p].push_back(reach(q));
-        // Network-leaf slots, unit by unit (the value sweep writes them first).
-        const uint32_t heads = w.net.heads;
-        const bool tower = readout_net(w.net.kind);
-        std::vector<uint32_t> row_blk;  // two-tower: each row's readout block for p
+        });
+    }
+    // Network-leaf slots, unit by unit (the value sweep writes them first):
+    // each unit's first slot from a prefix sum, then the units in parallel.
+    const uint32_t heads = w.net.heads;
+    const bool tower = readout_net(w.net.kind);
+    for (int p = 0; p < 2; p++) {
+        std::vector<uint32_t> row_blk;  // readout nets: each row's readout block for p
         if (tower) {
             row_blk.assign(w.rows(), NONE);
             for (uint32_t bi = 0; bi < w.tower_blk[p].size(); bi++)
                 for (uint32_t r = w.tower_blk[p][bi].r0; r < w.tower_blk[p][bi].r1; r++) row_blk[r] = bi;
         }
-        auto tower_entry = [&](uint32_t r, uint32_t cfg) {
-            const TowerBlock& b = w.tower_blk[p][row_blk[r]];
-            return b.dbase + (r - b.r0) * (b.chi - b.clo) + (cfg - b.clo);
-        };
+        uint32_t at = 0;
         for (UnitDev& u : w.units) {
-            u.leaf0[p] = (uint32_t)w.leaf_rec[p].size();
+            u.leaf0[p] = at;
+            for (uint32_t k = u.row0; k < u.row1; k++) at += w.nc(w.row_node[w.unit_row[k]], p);
+            u.leaf1[p] = at;
+        }
+        w.leaf_rec[p].resize(at);
+        parallel_for(w.units.size(), [&](size_t ui) {
+            const UnitDev& u = w.units[ui];
+            uint32_t slot = u.leaf0[p];
             for (uint32_t k = u.row0; k < u.row1; k++) {
                 const uint32_t r = w.unit_row[k], node = w.row_node[r];
                 const uint32_t* cfgs = &w.row_cfg[w.row_cfg_off[2 * r + p]];
-                for (uint32_t c = 0; c < w.nc(node, p); c++)
-                    w.leaf_rec[p].push_back({w.vals_base[2 * node + p] + c,
-                                             tower ? tower_entry(r, cfgs[c]) : r * heads + w.cfg_key[cfgs[c]],
-                                             2 * r + (1 - p), 0});
+                for (uint32_t c = 0; c < w.nc(node, p); c++) {
+                    uint32_t head;
+                    if (tower) {
+                        const TowerBlock& b = w.tower_blk[p][row_blk[r]];
+                        head = b.dbase + (r - b.r0) * (b.chi - b.clo) + (cfgs[c] - b.clo);
+                    } else {
+                        head = r * heads + w.cfg_key[cfgs[c]];
+                    }
+                    w.leaf_rec[p][slot++] = {w.vals_base[2 * node + p] + c, head, 2 * r + (1 - p), 0};
+                }
             }
-            u.leaf1[p] = (uint32_t)w.leaf_rec[p].size();
-        }
-        // Exported slots: the values read outside their unit, by the top
-        // regions' rows or as a tree's root values. Only these leave an
-        // LDS-staged unit sweep for HBM.
-        std::vector<uint8_t> ex(w.vals_len, 0);
+        });
+    }
+    // Exported slots: the values read outside their unit, by the top
+    // regions' rows or as a tree's root values. Only these leave an
+    // LDS-staged unit sweep for HBM.
+    std::vector<uint8_t> ex[2], term_ex[2];
+    parallel_for(2, [&](size_t pi) {
+        const int p = (int)pi;
+        ex[p].assign(w.vals_len, 0);
         for (const BackRec& r : w.top_back_rec[p]) {
             const uint32_t n = r.kn & REC_N, kind = r.kn >> 30;
             for (uint32_t k = 0; k < n; k++) {
@@ -184,27 +232,27 @@ void build_records(WaveHost* wp) {
                     slot = r.arg + w.draw_to[r.start + k];
                 else
                     slot = w.child_vb[p][r.start + k] + r.arg;
-                if (slot < w.vals_len) ex[slot] = 1;
+                if (slot < w.vals_len) ex[p][slot] = 1;
             }
         }
         for (const TreeDev& t : w.trees)
-            for (uint32_t c = 0; c < w.nc(t.node0, p); c++) ex[w.vals_base[2 * t.node0 + p] + c] = 1;
-        for (BackRec& r : w.back_rec[p])
-            if (ex[r.out]) r.kn |= REC_EXPORT;
-        for (LeafRec& r : w.leaf_rec[p]) r.exported = ex[r.out];
+            for (uint32_t c = 0; c < w.nc(t.node0, p); c++) ex[p][w.vals_base[2 * t.node0 + p] + c] = 1;
         term_ex[p].assign(w.unit_term.size(), 0);
         for (size_t k = 0; k < w.unit_term.size(); k++) {
             const uint32_t node = w.term_node[w.unit_term[k] & TERM_INDEX];
             for (uint32_t c = 0; c < w.nc(node, p); c++)
-                if (ex[w.vals_base[2 * node + p] + c]) term_ex[p][k] = 1;
-        }
-        w.acc_rec[p].reserve(w.decision[p].size());
-        for (const Task& q : w.decision[p]) {
-            uint32_t row = w.legal_row_of[q.node] + q.config;
-            w.acc_rec[p].push_back({w.reach_base[2 * q.node + p] + q.config, w.legal_off[row],
-                                    w.legal_off[row + 1] - w.legal_off[row], 0});
+                if (ex[p][w.vals_base[2 * node + p] + c]) term_ex[p][k] = 1;
         }
     });
+    for (int p = 0; p < 2; p++) {
+        chunked(w.back_rec[p].size(), [&](size_t lo, size_t hi) {
+            for (size_t k = lo; k < hi; k++)
+                if (ex[p][w.back_rec[p][k].out]) w.back_rec[p][k].kn |= REC_EXPORT;
+        });
+        chunked(w.leaf_rec[p].size(), [&](size_t lo, size_t hi) {
+            for (size_t k = lo; k < hi; k++) w.leaf_rec[p][k].exported = ex[p][w.leaf_rec[p][k].out];
+        });
+    }
     for (size_t k = 0; k < w.unit_term.size(); k++)
         for (int p = 0; p < 2; p++)
             if (term_ex[p][k]) w.unit_term[k] |= term_export(p);
@@ -857,39 +905,59 @@ bool validate_deep(const WaveHost& w, std::string* err) {
             return nullptr;
     };
     if (const char* m = first_fail(N, node_check)) return fail(m);
-    for (uint32_t v : w.legal_value)
-        if (v != NONE && v >= w.vals_len) return fail("legal_value");
+    if (first_fail(w.legal_value.size(), [&](uint64_t k) -> const char* {
+            const uint32_t v = w.legal_value[k];
+            return v != NONE && v >= w.vals_len ? "legal_value" : nullptr;
+        }))
+        return fail("legal_value");
     const uint64_t rows = w.rows();
     if (w.row_cfg_off.size() != 2 * rows + 1 || w.row_cfg_off.back() != w.row_cfg.size()) return fail("row_cfg_off");
     const uint64_t ncfg = w.cfg_key.size();
     if (w.cfg_emb.size() != (w.net.kind == MODEL_V5 ? 0 : ncfg * w.net.pool) ||
         w.pub_raw.size() != rows * w.net.row_bytes)
         return fail("row payload");
-    for (uint64_t r = 0; r < rows; r++) {
-        uint32_t node = w.row_node[r];
-        if (node >= N || (w.node_meta[node] & 3u) != 2) return fail("row_node");
-        for (int p = 0; p < 2; p++)
-            if (w.row_cfg_off[2 * r + p + 1] - w.row_cfg_off[2 * r + p] != w.nc(node, p)) return fail("row configs");
-    }
-    for (uint32_t c : w.row_cfg)
-        if (c >= ncfg) return fail("row_cfg");
-    for (int p = 0; p < 2; p++) {  // every row in exactly one group, with the group's list
-        std::vector<uint8_t> seen(rows, 0);
-        for (const PoolGroup& g : w.pool_grp[p]) {
-            if (g.nrows == 0 || g.nrows > POOL_GROUP || (uint64_t)g.cfg + g.n > w.row_cfg.size())
-                return fail("pool group");
-            for (uint32_t i = 0; i < g.nrows; i++) {
-                const uint32_t r = g.row[i];
-                if (r >= rows || seen[r]) return fail("pool group row");
-                seen[r] = 1;
-                const uint32_t a = w.row_cfg_off[2 * r + p];
-                if (w.row_cfg_off[2 * r + p + 1] - a != g.n ||
-                    !std::equal(w.row_cfg.begin() + a, w.row_cfg.begin() + a + g.n, w.row_cfg.begin() + g.cfg))
-                    return fail("pool group list");
+    if (const char* m = first_fail(rows, [&](uint64_t r) -> const char* {
+            const uint32_t node = w.row_node[r];
+            if (node >= N || (w.node_meta[node] & 3u) != 2) return "row_node";
+            for (int p = 0; p < 2; p++)
+                if (w.row_cfg_off[2 * r + p + 1] - w.row_cfg_off[2 * r + p] != w.nc(node, p)) return "row configs";
+            return nullptr;
+        }))
+        return fail(m);
+    if (first_fail(w.row_cfg.size(), [&](uint64_t k) { return w.row_cfg[k] >= ncfg ? "row_cfg" : nullptr; }))
+        return fail("row_cfg");
+    {  // every row in exactly one group, with the group's list (the two players at once)
+        const char* gm[2] = {nullptr, nullptr};
+        parallel_for(2, [&](size_t p) {
+            std::vector<uint8_t> seen(rows, 0);
+            for (const PoolGroup& g : w.pool_grp[p]) {
+                if (g.nrows == 0 || g.nrows > POOL_GROUP || (uint64_t)g.cfg + g.n > w.row_cfg.size()) {
+                    gm[p] = "pool group";
+                    return;
+                }
+                for (uint32_t i = 0; i < g.nrows; i++) {
+                    const uint32_t r = g.row[i];
+                    if (r >= rows || seen[r]) {
+                        gm[p] = "pool group row";
+                        return;
+                    }
+                    seen[r] = 1;
+                    const uint32_t a = w.row_cfg_off[2 * r + p];
+                    if (w.row_cfg_off[2 * r + p + 1] - a != g.n ||
+                        !std::equal(w.row_cfg.begin() + a, w.row_cfg.begin() + a + g.n, w.row_cfg.begin() + g.cfg)) {
+                        gm[p] = "pool group list";
+                        return;
+                    }
+                }
             }
-        }
-        for (uint8_t v : seen)
-            if (!v) return fail("pool group cover");
+            for (uint8_t v : seen)
+                if (!v) {
+                    gm[p] = "pool group cover";
+                    return;
+                }
+        });
+        for (const char* m : gm)
+            if (m) return fail(m);
     }
     if (w.net.kind == MODEL_MLP)
         for (uint32_t k : w.cfg_key)
@@ -917,12 +985,21 @@ bool validate_deep(const WaveHost& w, std::string* err) {
             if (w.exit_node[e] >= N || w.exit_coff[2 * e + p + 1] - w.exit_coff[2 * e + p] != w.nc(w.exit_node[e], p))
                 return fail("exit configs");
     for (int p = 0; p < 2; p++) {
-        for (const Task& q : w.back_task[p])
-            if (q.node >= N || q.config >= w.nc(q.node, p)) return fail("back task");
-        for (const Task& q : w.reach_task[p])
-            if (q.node >= N || q.config >= w.nc(q.node, p) || w.parent[q.node] == NONE) return fail("reach task");
-        for (const Task& q : w.decision[p])
-            if (q.node >= N || q.config >= w.nc(q.node, p) || (w.node_meta[q.node] & 3u) != 0) return fail("decision task");
+        if (first_fail(w.back_task[p].size(), [&](uint64_t k) {
+                const Task& q = w.back_task[p][k];
+                return q.node >= N || q.config >= w.nc(q.node, p) ? "x" : nullptr;
+            }))
+            return fail("back task");
+        if (first_fail(w.reach_task[p].size(), [&](uint64_t k) {
+                const Task& q = w.reach_task[p][k];
+                return q.node >= N || q.config >= w.nc(q.node, p) || w.parent[q.node] == NONE ? "x" : nullptr;
+            }))
+            return fail("reach task");
+        if (first_fail(w.decision[p].size(), [&](uint64_t k) {
+                const Task& q = w.decision[p][k];
+                return q.node >= N || q.config >= w.nc(q.node, p) || (w.node_meta[q.node] & 3u) != 0 ? "x" : nullptr;
+            }))
+            return fail("decision task");
         if (w.back_lvl[p].size() != w.lvl_len || w.reach_lvl[p].size() != w.lvl_len) return fail("level arrays");
     }
     if (w.unit_row.size() != rows || w.unit_term.size() != w.term_node.size()) return fail("unit leaf lists");
@@ -1012,14 +1089,19 @@ bool validate_deep(const WaveHost& w, std::string* err) {
             return fail("reach record");
         for (const ReachRec& r : w.top_reach_rec[p])
             if (!reach_ok(r)) return fail("top reach record");
-        for (const AccRec& r : w.acc_rec[p])
-            if (r.ridx >= w.reach_len || uint64_t(r.lo) + r.n > w.ncells) return fail("accumulation record");
+        if (first_fail(w.acc_rec[p].size(), [&](uint64_t k) {
+                const AccRec& r = w.acc_rec[p][k];
+                return r.ridx >= w.reach_len || uint64_t(r.lo) + r.n > w.ncells ? "x" : nullptr;
+            }))
+            return fail("accumulation record");
     }
     const uint64_t heads_end = readout_net(w.net.kind) ? w.tower_len : uint64_t(rows) * w.net.heads;
     for (int p = 0; p < 2; p++)
-        for (const LeafRec& r : w.leaf_rec[p])
-            if (r.out >= w.vals_len || uint64_t(r.head) >= heads_end || r.mass >= 2 * rows)
-                return fail("leaf record");
+        if (first_fail(w.leaf_rec[p].size(), [&](uint64_t k) {
+                const LeafRec& r = w.leaf_rec[p][k];
+                return r.out >= w.vals_len || uint64_t(r.head) >= heads_end || r.mass >= 2 * rows ? "x" : nullptr;
+            }))
+            return fail("leaf record");
     if (readout_net(w.net.kind))
         for (int p = 0; p < 2; p++) {
             // Blocks lie inside the rows, configs and values; every row of a
