@@ -3,6 +3,10 @@
 - game value: textbook vanilla CFR over world states (tests/brute_cfr.py),
   for every CFR variant the reference names (engine/src/search.rs:141-179),
   as the reference checks its own solver (engine/tests/rebel_solver.rs:166-280);
+- the iterate itself: average strategy and Phase 2 root values after 1..6
+  iterations against a float64 world-state discounted-CFR restatement
+  (tests/tabular_dcfr.py), which fixes the discount schedule (which update
+  count feeds each factor, when the sums are seeded and discounted);
 - zero-sum root values and NashConv >= 0 and falling (rebel_solver.rs:239-263);
 - reverse gathers: reach replayed through the rev/rvd tables equals the
   forward scatter of search.rs:1273-1351 (pattern of serialize.rs:1411-1508),
@@ -495,3 +499,69 @@ def test_reduced_precision_models_match_numpy():
         got = O.mlp(x, keys, net, mode)
         ref = wide(q)
         assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max(), mode
+
+
+@pytest.mark.parametrize("variant", sorted(VARIANTS))
+def test_solver_trajectory_matches_tabular_dcfr(variant):
+    """The iterate itself, not only where it converges: after 1, 2, 3 and 6
+    alternating iterations the oracle's average strategy and its Phase 2 root
+    values equal a float64 world-state restatement of discounted CFR
+    (tests/tabular_dcfr.py) to float32 rounding. Trees with and without
+    no-successor cells, both players drawing."""
+    import tabular_dcfr as TD
+    checked = 0
+    for notrans in (0.0, 0.3):
+        for seed in range(200, 206):
+            job = tiny_terminal_tree(seed, variant, iters=6, notrans=notrans)
+            for iters in (1, 2, 3, 6):
+                j = with_iters(job, iters)
+                got = O.solve(j, None, O.NET_EMPTY)
+                strat, roots = TD.solve(wcj8.decode(j))
+                ds = float(np.abs(got["strategy"] - strat).max())
+                dr = float(np.abs(got["roots"] - roots).max() / max(np.abs(roots).max(), 1e-9))
+                assert ds < 5e-6 and dr < 5e-6, f"seed {seed} notrans {notrans} iters {iters}: {ds:.2e} {dr:.2e}"
+                checked += 1
+    assert checked == 48
+
+
+def test_trajectory_pin_sees_schedule_mistakes():
+    """The restatement with a mistake planted in its schedule departs from the
+    oracle by far more than the tolerance above: the discount factors of the
+    next update (m + 1 instead of m), no seeding of the average sums, and
+    average weights from the reach under the strategy before the update."""
+    import tabular_dcfr as TD
+
+    class LateFactors(TD.Solver):
+        def step(self, p):
+            self.steps[p] += 1
+            super().step(p)
+            self.steps[p] -= 1
+
+    class Unseeded(TD.Solver):
+        def _add_average(self, p):
+            if self.steps != [0, 0]:
+                super()._add_average(p)
+
+    class StaleReach(TD.Solver):
+        def step(self, p):
+            self.before = self.sigma.copy()
+            super().step(p)
+
+        def _add_average(self, p):
+            sigma = getattr(self, "before", self.sigma)
+            reach = TD.own_reach(self.t, sigma, self.prior[p], p)
+            for i, c, row in self.decision_rows(p):
+                for g, _, _ in row:
+                    self.sum[g] += reach[i][c] * self.sigma[g]
+
+    worst = {}
+    for seed in range(200, 206):
+        j = with_iters(tiny_terminal_tree(seed, "dcfr", iters=6), 3)
+        got = O.solve(j, None, O.NET_EMPTY)["strategy"]
+        d = wcj8.decode(j)
+        for cls in (LateFactors, Unseeded, StaleReach):
+            s = cls(d)
+            for it in range(3):
+                s.step(it % 2)
+            worst[cls.__name__] = max(worst.get(cls.__name__, 0.0), float(np.abs(s.average() - got).max()))
+    assert min(worst.values()) > 1e-2, worst
