@@ -196,21 +196,32 @@ __device__ __forceinline__ void reach_unit_one(const WaveDev& w, const UnitDev& 
                                                int p) {
     const ReachRec* rec = w.reach_rec[p];
     const uint32_t* lvl = w.reach_lvl[p] + u.lvl0;
-    const uint32_t L = u.nlevels;
+    const uint32_t L = u.nlevels, t = threadIdx.x;
     uint32_t b = L ? lvl[0] : 0, e = L ? lvl[1] : 0;
-    ReachRec nxt{};
-    if (L && b + threadIdx.x < e) nxt = rec[b + threadIdx.x];
+    ReachRec q{};
+    if (L && b + t < e) q = rec[b + t];
     for (uint32_t l = 0; l < L; l++) {
         const uint32_t lb = b, le = e;
-        const ReachRec first = nxt;
-        if (l + 1 < L) {
+        const bool more = l + 1 < L;
+        if (more) {
             b = le;
             e = lvl[l + 2];
-            if (b + threadIdx.x < e) nxt = rec[b + threadIdx.x];
         }
-        uint32_t k = lb + threadIdx.x;
-        if (k < le) reach_row(w, reach, strat, first);
-        for (k += blockDim.x; k < le; k += blockDim.x) reach_row(w, reach, strat, rec[k]);
+        // Each thread's rows form one stream across the levels: the record of
+        // its next row (in this level, else its first in the next level) is
+        // fetched while the current row runs.
+        if (lb + t >= le && more && b + t < e) q = rec[b + t];
+        for (uint32_t k = lb + t; k < le;) {
+            const uint32_t kn = k + blockDim.x;
+            ReachRec qn{};
+            if (kn < le)
+                qn = rec[kn];
+            else if (more && b + t < e)
+                qn = rec[b + t];
+            reach_row(w, reach, strat, q);
+            q = qn;
+            k = kn;
+        }
         __syncthreads();
     }
 }
@@ -786,26 +797,34 @@ __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, cons
         }
     }
     __syncthreads();
-    // Levels from the deepest up. The next level's bounds and each thread's
-    // first record of it are fetched while the current level runs.
+    // Levels from the deepest up. Each thread's rows form one stream across
+    // the levels: the record of its next row (in this level, else its first
+    // in the next level up) is fetched while the current row runs.
     const BackRec* back = w.back_rec[p];
     const uint32_t* blvl = w.back_lvl[p] + u.lvl0;
+    const uint32_t t = threadIdx.x;
     uint32_t l = u.nlevels;
     uint32_t e = l ? blvl[l] : 0, b = l ? blvl[l - 1] : 0;
-    BackRec nxt{};
-    if (l && b + threadIdx.x < e) nxt = back[b + threadIdx.x];
+    BackRec q{};
+    if (l && b + t < e) q = back[b + t];
     while (l-- > 0) {
         const uint32_t lb = b, le = e;
-        const BackRec first = nxt;
         if (l) {
             e = lb;
             b = blvl[l - 1];
-            if (b + threadIdx.x < e) nxt = back[b + threadIdx.x];
         }
-        uint32_t k = lb + threadIdx.x;
-        if (k < le) backprop_row<MODE, LDSV>(w, p, first, da, db, predict, w.snap, lds_vals, vw);
-        for (k += blockDim.x; k < le; k += blockDim.x)
-            backprop_row<MODE, LDSV>(w, p, back[k], da, db, predict, w.snap, lds_vals, vw);
+        if (lb + t >= le && l && b + t < e) q = back[b + t];
+        for (uint32_t k = lb + t; k < le;) {
+            const uint32_t kn = k + blockDim.x;
+            BackRec qn{};
+            if (kn < le)
+                qn = back[kn];
+            else if (l && b + t < e)
+                qn = back[b + t];
+            backprop_row<MODE, LDSV>(w, p, q, da, db, predict, w.snap, lds_vals, vw);
+            q = qn;
+            k = kn;
+        }
         __syncthreads();
     }
 }

@@ -637,13 +637,29 @@ __device__ __forceinline__ v5f4 mma(const uint4& a, const uint4& b, const v5f4& 
                                                    0, 0);
 }
 
-// GELU of the 16-bit path: the same formula, tanh through the hardware
-// exponential (the operands it feeds are rounded to 16 bits anyway).
+// GELU of the 16-bit path (the operands it feeds are rounded to 16 bits
+// anyway): 0.5 x (1 + tanh u) = x / (1 + e^(-2u)), through the hardware
+// base-2 exponential and reciprocal (about one ulp each). Large |u| reach the
+// limits: e^(-2u) = inf gives x * 0, e^(-2u) = 0 gives x.
 __device__ __forceinline__ float gelu_fast(float x) {
     const float u = 0.79788456f * (x + 0.044715f * x * x * x);
-    const float e = __expf(-2.0f * fabsf(u));
-    const float t = (1.0f - e) / (1.0f + e);
-    return 0.5f * x * (1.0f + (u < 0.0f ? -t : t));
+    const float e = __builtin_amdgcn_exp2f(-2.88539008f * u);  // -2 log2(e) u
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// The sum of x over each 16-lane row of the wavefront, in every lane of the
+// row: four DPP butterfly steps (lanes xor 1 and xor 2 by quad permutes, then
+// the half-row and row mirrors), no LDS traffic.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_mov<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+    x += dpp_mov<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+    x += dpp_mov<0x141>(x);  // row_half_mirror: lane i <-> 7 - i within 8
+    x += dpp_mov<0x140>(x);  // row_mirror: lane i <-> 15 - i
+    return x;
 }
 
 constexpr int JT_ROWS = 32;          // rows per join workgroup
@@ -686,10 +702,7 @@ __global__ __launch_bounds__(JT_WAVES * 64) void k_join_mfma(Net net, uint32_t r
                         const float d = pass == 0 ? z[rb][cb][v] : z[rb][cb][v] - mean[r];
                         sacc += pass == 0 ? d : d * d;
                     }
-                    sacc += __shfl_xor(sacc, 1);
-                    sacc += __shfl_xor(sacc, 2);
-                    sacc += __shfl_xor(sacc, 4);
-                    sacc += __shfl_xor(sacc, 8);
+                    sacc = row16_sum(sacc);
                     if (i == 0) part[wv][r] = sacc;
                 }
             __syncthreads();
@@ -1008,10 +1021,7 @@ __global__ __launch_bounds__(TT_WAVES * 64) __attribute__((amdgpu_waves_per_eu(3
                     const uint32_t cell = rb * 16 + 4 * q + v;
                     float d = pass == 0 ? z[rb][v] : z[rb][v] - mean[cell];
                     float sacc = pass == 0 ? d : d * d;
-                    sacc += __shfl_xor(sacc, 1);
-                    sacc += __shfl_xor(sacc, 2);
-                    sacc += __shfl_xor(sacc, 4);
-                    sacc += __shfl_xor(sacc, 8);
+                    sacc = row16_sum(sacc);
                     if (i == 0) part[wv][cell] = sacc;
                 }
             __syncthreads();
@@ -1091,7 +1101,7 @@ __global__ __launch_bounds__(TT_WAVES * 64) __attribute__((amdgpu_waves_per_eu(3
             float mn = 0.0f, top = -INFINITY;
             for (uint32_t h = 0; h < HEXES; h++) {
                 const float v = aF[rr * HEXES + h][j];
-                mn += v / (float)HEXES;
+                mn += v * (1.0f / (float)HEXES);
                 top = fmaxf(top, v);
             }
             S16[rr * TT_SLD + j] = to16<PREC>(mn);
@@ -1156,7 +1166,7 @@ __global__ __launch_bounds__(TT_WAVES * 64) __attribute__((amdgpu_waves_per_eu(3
         float mn = 0.0f, top = -INFINITY;
         for (uint32_t h = 0; h < HEXES; h++) {
             const float v = aF[rr * HEXES + h][j];
-            mn += v / (float)HEXES;
+            mn += v * (1.0f / (float)HEXES);
             top = fmaxf(top, v);
         }
         S16[rr * TT_SLD + j] = to16<PREC>(mn);
