@@ -166,3 +166,34 @@ def test_v5_matrix_cores_track_the_scalar_path(precision, mode):
             assert np.median(err) <= tol / 6 * scale
     finally:
         scalar.close()
+
+
+def test_v5_trunk_partial_workgroups():
+    """The matrix-core trunk takes four network rows per workgroup (two
+    groups of two): waves whose row count leaves the last workgroup one, two
+    or three rows (an empty or half-empty group) still match the scalar path
+    on every row."""
+    net = ww.synth_weights(ww.V5_DIMS, 1)
+    os.environ["WC_V5_SCALAR"] = "1"
+    try:
+        scalar = ww.Executor(0, ww.WC_F16)
+    finally:
+        del os.environ["WC_V5_SCALAR"]
+    seen = set()
+    try:
+        for trees in range(1, 9):
+            jobs = v5_jobs(trees=trees, seed=41 + trees)
+            wave = ww.Wave(jobs)
+            rows = wave.stats()["rows"]
+            wave.close()
+            if rows % 4 == 0 or rows % 4 in seen:
+                continue
+            seen.add(rows % 4)
+            say(f"case v5 partial workgroups: {trees} trees, {rows} rows")
+            got, _ = device_probe(executor(ww.WC_F16), jobs, net, 0)
+            ref, _ = device_probe(scalar, jobs, net, 0)
+            scale = float(np.abs(ref).max())
+            assert np.abs(got.astype(np.float64) - ref).max() <= 3e-3 * scale
+    finally:
+        scalar.close()
+    assert seen == {1, 2, 3}, seen

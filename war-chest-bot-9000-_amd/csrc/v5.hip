@@ -829,7 +829,8 @@ __global__ __launch_bounds__(JT_WAVES * 64) void k_join_mfma(Net net, uint32_t r
 
 // ------------------------------------------------------ trunk on MFMA
 
-constexpr int TT_ROWS = 2;                        // network rows per workgroup
+constexpr int TT_ROWS = 2;                        // network rows per group of wavefronts
+constexpr int TT_GROUPS = 2;                      // groups per workgroup
 constexpr int TT_CELLS = TT_ROWS * HEXES;         // 74 hex cells
 constexpr int TT_RB = (TT_CELLS + 15) / 16;       // 5 row blocks of 16 cells
 constexpr int TT_WAVES = C / 16;                  // one 16-channel column block per wavefront
@@ -848,29 +849,46 @@ constexpr int TT_SLD = D + 8;                     // LDS row stride of the per-r
 // one or two rows each and stay scalar, with rounded operands where the
 // reference's fast mode runs them on tensor cores.
 template <int PREC>
-__global__ __launch_bounds__(TT_WAVES * 64) __attribute__((amdgpu_waves_per_eu(3, 3))) void k_trunk_mfma(
-    Net net, WaveIn in, WaveOut out) {  // three waves per SIMD: two workgroups per CU
-    __shared__ float aF[TT_RB * 16][C];
-    __shared__ __attribute__((aligned(16))) uint16_t A16[TT_RB * 16 * TT_LD];
-    __shared__ float part[TT_WAVES][TT_RB * 16], mean[TT_RB * 16], inv[TT_RB * 16];
-    __shared__ float gb[TT_ROWS][C];
-    __shared__ float loose[TT_ROWS][LOOSE], tp[TT_ROWS][C], glob[TT_ROWS][C];
+__global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_waves_per_eu(3, 3))) void k_trunk_mfma(
+    Net net, WaveIn in, WaveOut out) {  // twelve waves: three per SIMD, one workgroup per CU
+    // Two groups of six wavefronts, each with its own pair of rows and its own
+    // LDS below; they share only the barriers and the neighbour table.
+    __shared__ float aF_g[TT_GROUPS][TT_RB * 16][C];
+    __shared__ __attribute__((aligned(16))) uint16_t A16_g[TT_GROUPS][TT_RB * 16 * TT_LD];
+    __shared__ float part_g[TT_GROUPS][TT_WAVES][TT_RB * 16], mean_g[TT_GROUPS][TT_RB * 16],
+        inv_g[TT_GROUPS][TT_RB * 16];
+    __shared__ float gb_g[TT_GROUPS][TT_ROWS][C];
+    __shared__ float loose_g[TT_GROUPS][TT_ROWS][LOOSE], tp_g[TT_GROUPS][TT_ROWS][C], glob_g[TT_GROUPS][TT_ROWS][C];
     // The A operand of the per-row products (pool bias, board vector, join
     // cache): one 16-row block whose rows past TT_ROWS stay zero.
-    __shared__ __attribute__((aligned(16))) uint16_t S16[16 * TT_SLD];
-    __shared__ int occ[TT_CELLS];
+    __shared__ __attribute__((aligned(16))) uint16_t S16_g[TT_GROUPS][16 * TT_SLD];
+    __shared__ int occ_g[TT_GROUPS][TT_CELLS];
     __shared__ uint8_t nbc[TT_RB * 16][6];  // each cell's neighbour cells (the zero padding cell when off board)
+    const uint32_t grp = threadIdx.x / (TT_WAVES * 64);
+    float(&aF)[TT_RB * 16][C] = aF_g[grp];
+    uint16_t* A16 = A16_g[grp];
+    float(&part)[TT_WAVES][TT_RB * 16] = part_g[grp];
+    float* mean = mean_g[grp];
+    float* inv = inv_g[grp];
+    float(&gb)[TT_ROWS][C] = gb_g[grp];
+    float(&loose)[TT_ROWS][LOOSE] = loose_g[grp];
+    float(&tp)[TT_ROWS][C] = tp_g[grp];
+    float(&glob)[TT_ROWS][C] = glob_g[grp];
+    uint16_t* S16 = S16_g[grp];
+    int* occ = occ_g[grp];
     // stem scratch in the operand's space: tokens, projected tokens, hex facts
     float* tok = (float*)A16;                           // [TT_ROWS][NTYPE][TYPE]
     float* proj = tok + TT_ROWS * NTYPE * TYPE;         // [TT_ROWS][NTYPE][C]
     float* facts = proj + TT_ROWS * NTYPE * C;          // [TT_CELLS][HEX_FACTS]
-    static_assert(sizeof(float) * (TT_ROWS * NTYPE * (TYPE + C) + TT_CELLS * HEX_FACTS) <= sizeof(A16), "stem scratch");
-    const uint32_t tid = threadIdx.x, wv = tid >> 6, l = tid & 63, q = l >> 4, i = l & 15;
-    const uint32_t row0 = blockIdx.x * TT_ROWS, nrow = min((uint32_t)TT_ROWS, in.rows - row0);
+    static_assert(sizeof(float) * (TT_ROWS * NTYPE * (TYPE + C) + TT_CELLS * HEX_FACTS) <= sizeof(A16_g[0]),
+                  "stem scratch");
+    const uint32_t tid = threadIdx.x % (TT_WAVES * 64), wv = tid >> 6, l = tid & 63, q = l >> 4, i = l & 15;
+    const uint32_t row0 = (blockIdx.x * TT_GROUPS + grp) * TT_ROWS;
+    const uint32_t nrow = row0 < in.rows ? min((uint32_t)TT_ROWS, in.rows - row0) : 0;  // 0: an empty group
     const float* W = net.w;
     for (uint32_t x2 = tid; x2 < 16 * TT_SLD; x2 += TT_WAVES * 64) S16[x2] = 0;
     static_assert(TT_RB * 16 > TT_CELLS, "a zero padding cell stands for a missing neighbour");
-    for (uint32_t x2 = tid; x2 < TT_RB * 16 * 6; x2 += TT_WAVES * 64) {
+    for (uint32_t x2 = threadIdx.x; x2 < TT_RB * 16 * 6; x2 += TT_GROUPS * TT_WAVES * 64) {
         const uint32_t cell = x2 / 6, d = x2 % 6;
         uint32_t n = TT_RB * 16 - 1;
         if (cell < TT_CELLS) {
@@ -1213,8 +1231,8 @@ void launch_build(int precision, const Net& net, const WaveIn& in, const WaveOut
         if (tokens) hipLaunchKernelGGL(k_cards<P>, dim3(tokens), dim3(NBLK), 0, s, net, in, out);            \
         if (in.ncfg) hipLaunchKernelGGL(k_configs<P>, dim3(in.ncfg), dim3(NBLK), 0, s, net, in, out);        \
         if (in.rows && P != WC_PRECISE && net.m16[M_MIX0])                                                   \
-            hipLaunchKernelGGL(k_trunk_mfma<P>, dim3((in.rows + TT_ROWS - 1) / TT_ROWS), dim3(TT_WAVES * 64), \
-                               0, s, net, in, out);                                                          \
+            hipLaunchKernelGGL(k_trunk_mfma<P>, dim3((in.rows + TT_GROUPS * TT_ROWS - 1) / (TT_GROUPS * TT_ROWS)), \
+                               dim3(TT_GROUPS * TT_WAVES * 64), 0, s, net, in, out);                         \
         else if (in.rows)                                                                                    \
             hipLaunchKernelGGL(k_trunk<P>, dim3(in.rows), dim3(NBLK), 0, s, net, in, out);                   \
     } while (0)
