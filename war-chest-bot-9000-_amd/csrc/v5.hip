@@ -682,41 +682,56 @@ __global__ __launch_bounds__(JT_WAVES * 64) void k_join_mfma(Net net, uint32_t r
                                                             const float* __restrict__ P, const float* __restrict__ Jp,
                                                             uint16_t* __restrict__ H) {
     __shared__ __attribute__((aligned(16))) uint16_t tA[JT_ROWS * JT_LD];
-    __shared__ float part[JT_WAVES][JT_ROWS], mean[JT_ROWS], inv[JT_ROWS];
+    __shared__ float part[JT_WAVES][JT_ROWS], part2[JT_WAVES][JT_ROWS], mean[JT_ROWS], inv[JT_ROWS];
     const uint32_t wv = threadIdx.x >> 6, l = threadIdx.x & 63, q = l >> 4, i = l & 15;
     const uint32_t r0 = blockIdx.x * JT_ROWS;
     const uint32_t col = wv * 16 + i;  // this lane's column of the 128-wide stream
     // Per-row statistics of the wave's accumulators (NC column blocks each),
     // combined across the wavefronts: mean, then 1 / sqrt(var + 1e-5).
+    // Each wavefront's sum and sum of squared deviations from its own mean
+    // (over its NC x 16 columns), combined across the wavefronts by the
+    // pairwise-variance formula (Chan, Golub and LeVeque) in one exchange.
     auto row_stats = [&](auto& z, auto ncb, float width) {
         constexpr uint32_t NC = decltype(ncb)::value;
-        for (int pass = 0; pass < 2; pass++) {
+        constexpr float NW = 16.0f * NC;  // columns per wavefront
 #pragma unroll
-            for (uint32_t rb = 0; rb < JT_RB; rb++)
+        for (uint32_t rb = 0; rb < JT_RB; rb++)
 #pragma unroll
-                for (uint32_t v = 0; v < 4; v++) {
-                    const uint32_t r = rb * 16 + 4 * q + v;
-                    float sacc = 0.0f;
+            for (uint32_t v = 0; v < 4; v++) {
+                const uint32_t r = rb * 16 + 4 * q + v;
+                float sacc = 0.0f;
 #pragma unroll
-                    for (uint32_t cb = 0; cb < NC; cb++) {
-                        const float d = pass == 0 ? z[rb][cb][v] : z[rb][cb][v] - mean[r];
-                        sacc += pass == 0 ? d : d * d;
-                    }
-                    sacc = row16_sum(sacc);
-                    if (i == 0) part[wv][r] = sacc;
+                for (uint32_t cb = 0; cb < NC; cb++) sacc += z[rb][cb][v];
+                sacc = row16_sum(sacc);
+                const float mw = sacc * (1.0f / NW);
+                float dacc = 0.0f;
+#pragma unroll
+                for (uint32_t cb = 0; cb < NC; cb++) {
+                    const float d = z[rb][cb][v] - mw;
+                    dacc += d * d;
                 }
-            __syncthreads();
-            if (threadIdx.x < JT_ROWS) {
-                float t = 0.0f;
-#pragma unroll
-                for (uint32_t w2 = 0; w2 < JT_WAVES; w2++) t += part[w2][threadIdx.x];
-                if (pass == 0)
-                    mean[threadIdx.x] = t / width;
-                else
-                    inv[threadIdx.x] = 1.0f / sqrtf(t / width + 1e-5f);
+                dacc = row16_sum(dacc);
+                if (i == 0) {
+                    part[wv][r] = sacc;
+                    part2[wv][r] = dacc;
+                }
             }
-            __syncthreads();
+        __syncthreads();
+        if (threadIdx.x < JT_ROWS) {
+            float t = 0.0f;
+#pragma unroll
+            for (uint32_t w2 = 0; w2 < JT_WAVES; w2++) t += part[w2][threadIdx.x];
+            const float m = t / width;
+            float m2 = 0.0f;
+#pragma unroll
+            for (uint32_t w2 = 0; w2 < JT_WAVES; w2++) {
+                const float dm = part[w2][threadIdx.x] * (1.0f / NW) - m;
+                m2 += part2[w2][threadIdx.x] + NW * dm * dm;
+            }
+            mean[threadIdx.x] = m;
+            inv[threadIdx.x] = 1.0f / sqrtf(m2 / width + 1e-5f);
         }
+        __syncthreads();
     };
     // gelu(LN(z)) of the 128-wide stream into the A operand in LDS (16-bit).
     auto to_operand = [&](float (&z)[JT_RB][1][4], uint32_t which) {
@@ -853,10 +868,10 @@ __global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_wa
     Net net, WaveIn in, WaveOut out) {  // twelve waves: three per SIMD, one workgroup per CU
     // Two groups of six wavefronts, each with its own pair of rows and its own
     // LDS below; they share only the barriers and the neighbour table.
-    __shared__ float aF_g[TT_GROUPS][TT_RB * 16][C];
+    __shared__ __attribute__((aligned(16))) float aF_g[TT_GROUPS][TT_RB * 16][C];
     __shared__ __attribute__((aligned(16))) uint16_t A16_g[TT_GROUPS][TT_RB * 16 * TT_LD];
-    __shared__ float part_g[TT_GROUPS][TT_WAVES][TT_RB * 16], mean_g[TT_GROUPS][TT_RB * 16],
-        inv_g[TT_GROUPS][TT_RB * 16];
+    __shared__ float part_g[TT_GROUPS][TT_WAVES][TT_RB * 16], part2_g[TT_GROUPS][TT_WAVES][TT_RB * 16],
+        mean_g[TT_GROUPS][TT_RB * 16], inv_g[TT_GROUPS][TT_RB * 16];
     __shared__ float gb_g[TT_GROUPS][TT_ROWS][C];
     __shared__ float loose_g[TT_GROUPS][TT_ROWS][LOOSE], tp_g[TT_GROUPS][TT_ROWS][C], glob_g[TT_GROUPS][TT_ROWS][C];
     // The A operand of the per-row products (pool bias, board vector, join
@@ -868,6 +883,7 @@ __global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_wa
     float(&aF)[TT_RB * 16][C] = aF_g[grp];
     uint16_t* A16 = A16_g[grp];
     float(&part)[TT_WAVES][TT_RB * 16] = part_g[grp];
+    float(&part2)[TT_WAVES][TT_RB * 16] = part2_g[grp];
     float* mean = mean_g[grp];
     float* inv = inv_g[grp];
     float(&gb)[TT_ROWS][C] = gb_g[grp];
@@ -1029,30 +1045,38 @@ __global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_wa
         }
     __syncthreads();  // the stem scratch is free: the operand space is reused below
     // Per-cell LayerNorm statistics of a 96-wide stream held as [rb][v] per lane
-    // (channel `col`), combined over the six wavefronts.
+    // (channel `col`): each wavefront's sum and sum of squared deviations from
+    // its own 16-channel mean, combined over the six wavefronts by the
+    // pairwise-variance formula (Chan, Golub and LeVeque): one exchange
+    // through LDS instead of one per pass.
     auto cell_stats = [&](float (&z)[TT_RB][4]) {
-        for (int pass = 0; pass < 2; pass++) {
 #pragma unroll
-            for (uint32_t rb = 0; rb < TT_RB; rb++)
+        for (uint32_t rb = 0; rb < TT_RB; rb++)
 #pragma unroll
-                for (uint32_t v = 0; v < 4; v++) {
-                    const uint32_t cell = rb * 16 + 4 * q + v;
-                    float d = pass == 0 ? z[rb][v] : z[rb][v] - mean[cell];
-                    float sacc = pass == 0 ? d : d * d;
-                    sacc = row16_sum(sacc);
-                    if (i == 0) part[wv][cell] = sacc;
+            for (uint32_t v = 0; v < 4; v++) {
+                const uint32_t cell = rb * 16 + 4 * q + v;
+                const float sw = row16_sum(z[rb][v]);
+                const float d = z[rb][v] - sw * (1.0f / 16.0f);
+                const float m2 = row16_sum(d * d);
+                if (i == 0) {
+                    part[wv][cell] = sw;
+                    part2[wv][cell] = m2;
                 }
-            __syncthreads();
-            if (tid < TT_RB * 16) {
-                float t = 0.0f;
-                for (uint32_t w2 = 0; w2 < TT_WAVES; w2++) t += part[w2][tid];
-                if (pass == 0)
-                    mean[tid] = t / (float)C;
-                else
-                    inv[tid] = 1.0f / sqrtf(t / (float)C + 1e-5f);
             }
-            __syncthreads();
+        __syncthreads();
+        if (tid < TT_RB * 16) {
+            float t = 0.0f;
+            for (uint32_t w2 = 0; w2 < TT_WAVES; w2++) t += part[w2][tid];
+            const float m = t * (1.0f / (float)C);
+            float m2 = 0.0f;
+            for (uint32_t w2 = 0; w2 < TT_WAVES; w2++) {
+                const float dm = part[w2][tid] * (1.0f / 16.0f) - m;
+                m2 += part2[w2][tid] + 16.0f * dm * dm;
+            }
+            mean[tid] = m;
+            inv[tid] = 1.0f / sqrtf(m2 * (1.0f / (float)C) + 1e-5f);
         }
+        __syncthreads();
     };
     auto norm_val = [&](float z, uint32_t cell, uint32_t which) {
         return gelu_fast((z - mean[cell]) * inv[cell] * net.ln[LY.norm_g[which] + col] + net.ln[LY.norm_b[which] + col]);
@@ -1102,16 +1126,39 @@ __global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_wa
         // neighbour sums (zero start, directions in board order) into the
         // operand's upper half, and the mean / max pool of each row
         {
-            // a thread's elements share channel j: cells c0, c0 + 4, ... (384 = 4 x 96)
-            constexpr uint32_t NT = TT_WAVES * 64, STEP = NT / C;
-            static_assert(NT % C == 0 && (TT_RB * 16) % STEP == 0, "neighbour mapping");
-            const uint32_t j = tid % C, c0 = tid / C;
-#pragma unroll 1
-            for (uint32_t cell = c0; cell < TT_RB * 16; cell += STEP) {
-                float v = 0.0f;  // directions in board order; off board reads the zero cell
+            // a thread per (cell, quarter of the channels): 24 channels as six
+            // float4 reads per neighbour, summed per channel from zero in
+            // board direction order (off board reads the zero cell)
+            constexpr uint32_t QW = C / 4;
+            static_assert(TT_RB * 16 * 4 <= TT_WAVES * 64 && QW % 8 == 0, "neighbour mapping");
+            if (tid < TT_RB * 16 * 4) {
+                const uint32_t cell = tid >> 2;
+                uint32_t nb[6];
 #pragma unroll
-                for (int d = 0; d < 6; d++) v += aF[nbc[cell][d]][j];
-                A16[cell * TT_LD + C + j] = to16<PREC>(v);
+                for (int d = 0; d < 6; d++) nb[d] = nbc[cell][d];
+                // 8 channels at a time: two float4 per neighbour, one 16-byte store
+#pragma unroll 1
+                for (uint32_t c0 = (tid & 3) * QW; c0 < (tid & 3) * QW + QW; c0 += 8) {
+                    float4 lo = make_float4(0.0f, 0.0f, 0.0f, 0.0f), hi = lo;
+#pragma unroll
+                    for (int d = 0; d < 6; d++) {
+                        const float4 a0 = *(const float4*)&aF[nb[d]][c0], a1 = *(const float4*)&aF[nb[d]][c0 + 4];
+                        lo.x += a0.x;
+                        lo.y += a0.y;
+                        lo.z += a0.z;
+                        lo.w += a0.w;
+                        hi.x += a1.x;
+                        hi.y += a1.y;
+                        hi.z += a1.z;
+                        hi.w += a1.w;
+                    }
+                    uint4 w4;
+                    w4.x = (uint32_t)to16<PREC>(lo.x) | (uint32_t)to16<PREC>(lo.y) << 16;
+                    w4.y = (uint32_t)to16<PREC>(lo.z) | (uint32_t)to16<PREC>(lo.w) << 16;
+                    w4.z = (uint32_t)to16<PREC>(hi.x) | (uint32_t)to16<PREC>(hi.y) << 16;
+                    w4.w = (uint32_t)to16<PREC>(hi.z) | (uint32_t)to16<PREC>(hi.w) << 16;
+                    *(uint4*)(A16 + cell * TT_LD + C + c0) = w4;
+                }
             }
         }
         for (uint32_t x2 = tid; x2 < TT_ROWS * C; x2 += TT_WAVES * 64) {
