@@ -986,10 +986,17 @@ __global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_wa
         }
         loose[rr][qq] = v;
     }
+    // tok_stem's matrix (64 x 96 float32) staged in the activations' space,
+    // which the stem does not use: one round of independent loads
+    float* wtok = &aF[0][0];
+    static_assert(TYPE * C <= sizeof(aF) / sizeof(float) && (TYPE * C) % (TT_WAVES * 64) == 0, "tok_stem staging");
+#pragma unroll
+    for (uint32_t k = 0; k < TYPE * C / (TT_WAVES * 64); k++)
+        wtok[tid + k * TT_WAVES * 64] = W[LY.tok_stem.w + tid + k * TT_WAVES * 64];
     __syncthreads();
     {
         // tok_stem (float32, no bias): a thread's outputs tid + k * 384 share
-        // the channel, so each weight is loaded once for all of them
+        // the channel, so each weight is read once for all of them
         constexpr uint32_t NT = TT_WAVES * 64, NOUT = TT_ROWS * NTYPE * C / NT;
         static_assert(TT_ROWS * NTYPE * C % NT == 0 && NT % C == 0, "projection mapping");
         const uint32_t j = tid % C;
@@ -998,7 +1005,7 @@ __global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_wa
         for (uint32_t k = 0; k < NOUT; k++) acc[k] = 0.0f;
 #pragma unroll 8
         for (uint32_t p = 0; p < TYPE; p++) {
-            const float wv2 = W[LY.tok_stem.w + p * C + j];
+            const float wv2 = wtok[p * C + j];
 #pragma unroll
             for (uint32_t k = 0; k < NOUT; k++) {
                 const float a = tok[((tid + k * NT) / C) * TYPE + p];
@@ -1012,7 +1019,7 @@ __global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_wa
     for (uint32_t x = tid; x < TT_ROWS * C; x += TT_WAVES * 64) {
         const uint32_t rr = x / C, j = x % C;
         float v = 0.0f;
-        for (uint32_t t = 0; t < NTYPE; t++) v += gelu(proj[(rr * NTYPE + t) * C + j]) / (float)NTYPE;
+        for (uint32_t t = 0; t < NTYPE; t++) v += gelu_fast(proj[(rr * NTYPE + t) * C + j]) * (1.0f / (float)NTYPE);
         tp[rr][j] = v;
         glob[rr][j] = lin_out<PREC, false>(loose[rr], LOOSE, W + LY.glob_stem.w, C, j, 0.0f, nullptr);
     }
