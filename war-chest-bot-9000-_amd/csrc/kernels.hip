@@ -437,7 +437,7 @@ __global__ __launch_bounds__(BLOCK) void k_pool_mfma(WaveDev w, int player, uint
     const PoolGroup* grp = w.pool_grp[p] + g;
     const uint32_t n = grp->n, G = grp->nrows;
     const uint32_t i = lane & 15, q = lane >> 4;  // A row / B column, and config within a 4-step
-    const float* ra = w.reach + w.reach_base[2 * w.row_node[grp->row[i < G ? i : 0]] + p];
+    const float* ra = w.reach + grp->rbase[i < POOL_GROUP ? i : 0];  // lane row 15 reads no reach
     const float aconst = i == 15 ? 1.0f : 0.0f;  // rows G..14 are zero, row 15 sums the embeddings
     const uint32_t* cfgs = w.row_cfg + grp->cfg;
     const uint32_t pool = w.pool, in = w.in;

@@ -748,6 +748,8 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
                 g.n = w.row_cfg_off[2 * rows_of[0] + p + 1] - g.cfg;
                 g.nrows = (uint32_t)std::min<size_t>(POOL_GROUP, rows_of.size() - k);
                 for (uint32_t i = 0; i < g.nrows; i++) g.row[i] = rows_of[k + i];
+                for (uint32_t i = 0; i < POOL_GROUP; i++)
+                    g.rbase[i] = w.reach_base[2 * w.row_node[g.row[i < g.nrows ? i : 0]] + p];
                 out.push_back(g);
             }
         std::stable_sort(out.begin(), out.end(), [](const PoolGroup& a, const PoolGroup& b) { return a.n > b.n; });
@@ -934,6 +936,13 @@ bool validate_deep(const WaveHost& w, std::string* err) {
                 if (g.nrows == 0 || g.nrows > POOL_GROUP || (uint64_t)g.cfg + g.n > w.row_cfg.size()) {
                     gm[p] = "pool group";
                     return;
+                }
+                for (uint32_t i = 0; i < POOL_GROUP; i++) {
+                    const uint32_t r = g.row[i < g.nrows ? i : 0];
+                    if (r >= rows || g.rbase[i] != w.reach_base[2 * w.row_node[r] + p]) {
+                        gm[p] = "pool group reach";
+                        return;
+                    }
                 }
                 for (uint32_t i = 0; i < g.nrows; i++) {
                     const uint32_t r = g.row[i];

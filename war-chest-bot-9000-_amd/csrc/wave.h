@@ -114,8 +114,13 @@ constexpr uint32_t POOL_GROUP = 15;
 struct PoolGroup {
     uint32_t cfg, n, nrows;  // the shared list row_cfg[cfg .. cfg + n), rows row[0 .. nrows)
     uint32_t row[POOL_GROUP];
+    // each row's reach slots of the group's player, reach_base[2 * node + p]
+    // (entries past nrows repeat row 0's): the pooling reads the reach with
+    // no lookup through the row's node
+    uint32_t rbase[POOL_GROUP];
+    uint32_t pad[3];
 };
-static_assert(sizeof(PoolGroup) == 18 * 4, "PoolGroup is 72 bytes");
+static_assert(sizeof(PoolGroup) == 36 * 4, "PoolGroup is 144 bytes");
 
 // One pass of the fused value net: up to CHAIN_PASS_BLOCKS 16-row blocks of the
 // network rows (any blocks, in any order; rb[0 .. n)) and the head columns
