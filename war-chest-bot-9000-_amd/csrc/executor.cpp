@@ -12,6 +12,7 @@
 #include <unordered_map>
 
 #include "../../include/wc_wave.h"
+#include "par.h"
 
 namespace wc {
 
@@ -58,8 +59,8 @@ struct Blob {
         for (const Piece& pc : pieces)
             for (size_t o = 0; o < pc.bytes; o += CHUNK)
                 parts.push_back({pc.src + o, std::min(CHUNK, pc.bytes - o), pc.at + o});
-        const size_t nt = std::min<size_t>(std::max(1u, std::min(8u, std::thread::hardware_concurrency())),
-                                           parts.size());
+        const size_t nt = std::min<size_t>(
+            std::max(1u, std::min({8u, std::thread::hardware_concurrency(), par_budget()})), parts.size());
         auto work = [&](size_t t) {
             for (size_t k = t; k < parts.size(); k += nt) std::memcpy(dst + parts[k].at, parts[k].src, parts[k].bytes);
         };

@@ -10,15 +10,34 @@
 
 namespace wc {
 
+// The calling thread's budget of host threads for parallel loops. Callers
+// that run side by side (a service's lanes packing at once) each take a share
+// of the cores, so that together they do not oversubscribe the host.
+inline unsigned& par_budget() {
+    static thread_local unsigned budget = 16;
+    return budget;
+}
+struct ParBudget {  // sets the calling thread's budget for its lifetime
+    unsigned old;
+    explicit ParBudget(unsigned n) : old(par_budget()) { par_budget() = std::max(1u, n); }
+    ~ParBudget() { par_budget() = old; }
+    ParBudget(const ParBudget&) = delete;
+    ParBudget& operator=(const ParBudget&) = delete;
+};
+
 // Runs fn(i) for every i in [0, n) on up to max_threads host threads (at most
-// the hardware's), taking indices from a shared counter. fn must not throw.
+// the hardware's and the caller's budget), taking indices from a shared
+// counter; loops nested inside fn share the caller's budget. fn must not throw.
 template <class F>
 void parallel_for(size_t n, F fn, unsigned max_threads = 16) {
     if (n == 0) return;
     const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
-    const size_t nt = std::min<size_t>(std::min(hw, std::max(1u, max_threads)), n);
+    const unsigned budget = par_budget();
+    const size_t nt = std::min<size_t>(std::min({hw, std::max(1u, max_threads), budget}), n);
+    const unsigned inner = std::max<unsigned>(1u, budget / (unsigned)nt);
     std::atomic<size_t> next{0};
     auto work = [&]() {
+        ParBudget share(inner);
         for (size_t i = next.fetch_add(1); i < n; i = next.fetch_add(1)) fn(i);
     };
     std::vector<std::thread> pool;

@@ -7,9 +7,11 @@
 #include <cstring>
 #include <iterator>
 #include <limits>
+#include <thread>
 
 #include "../../include/wc_wave.h"
 #include "kernels.h"
+#include "par.h"
 
 namespace wc {
 
@@ -336,6 +338,8 @@ void Service::answer(Flight& fl, bool ok, std::vector<Result>* results, std::str
 }
 
 void Service::lane_main(uint32_t lane) {
+    // this lane's share of the host's cores for packing and staging copies
+    ParBudget budget(std::max(1u, std::thread::hardware_concurrency()) / opts_.lanes);
     std::unique_ptr<Executor> ex(new Executor(device_, precision_));
     std::map<uint64_t, uint64_t> bank_of;  // service version -> executor version
     {

@@ -2,6 +2,7 @@
 #include "wave.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -730,14 +731,28 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     // infostates in the same order), at most POOL_GROUP per group, in row
     // order within a list; longest lists launch first.
     for (int p = 0; p < 2; p++) {
-        std::unordered_map<std::string, uint32_t> key_of;
+        // lists keyed by a 64-bit hash of their contents; equal hashes are
+        // confirmed element by element (a collision starts its own list)
+        std::unordered_multimap<uint64_t, uint32_t> key_of;
         std::vector<std::vector<uint32_t>> lists;
         for (uint32_t r = 0; r < nrows; r++) {
             const uint32_t a = w.row_cfg_off[2 * r + p], b = w.row_cfg_off[2 * r + p + 1];
-            std::string key((const char*)(w.row_cfg.data() + a), size_t(b - a) * sizeof(uint32_t));
-            auto it = key_of.emplace(std::move(key), (uint32_t)lists.size()).first;
-            if (it->second == lists.size()) lists.emplace_back();
-            lists[it->second].push_back(r);
+            uint64_t h = 0xcbf29ce484222325ull ^ (b - a);  // FNV-1a over the 32-bit entries
+            for (uint32_t x = a; x < b; x++) h = (h ^ w.row_cfg[x]) * 0x100000001b3ull;
+            uint32_t id = NONE;
+            auto range = key_of.equal_range(h);
+            for (auto it = range.first; it != range.second && id == NONE; ++it) {
+                const uint32_t r0 = lists[it->second][0];
+                const uint32_t a0 = w.row_cfg_off[2 * r0 + p], b0 = w.row_cfg_off[2 * r0 + p + 1];
+                if (b0 - a0 == b - a && std::equal(w.row_cfg.begin() + a, w.row_cfg.begin() + b, w.row_cfg.begin() + a0))
+                    id = it->second;
+            }
+            if (id == NONE) {
+                id = (uint32_t)lists.size();
+                key_of.emplace(h, id);
+                lists.emplace_back();
+            }
+            lists[id].push_back(r);
         }
         auto& out = w.pool_grp[p];
         out.clear();
@@ -819,7 +834,14 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     }
     build_records(&w);
     w.jobs = std::move(jobs);
-    if (!validate_deep(w, err)) return false;
+    // A wave packed from jobs that each passed validate() is this packer's own
+    // output and is not checked again (about 40% of the packing's host work);
+    // WC_DEEP_CHECK=1 checks it anyway. Every other wave is checked.
+    static const bool force_deep = [] {
+        const char* e = std::getenv("WC_DEEP_CHECK");
+        return e && *e && *e != '0';
+    }();
+    if ((!validated || force_deep) && !validate_deep(w, err)) return false;
     return true;
 }
 

@@ -246,7 +246,8 @@ struct WaveHost {
 // schedules, malformed tables or unsupported networks. `unit_slots` bounds the
 // value slots of one subtree unit.
 // `validated`: every job already passed validate() (the service checks each
-// job when it is submitted), so the per-job checks are not repeated.
+// job when it is submitted), so the per-job checks are not repeated, nor the
+// deep check of the packed wave (validate_deep) unless WC_DEEP_CHECK=1.
 bool pack_wave(std::vector<Job>&& jobs, WaveHost* w, std::string* err, uint32_t unit_slots = UNIT_SLOTS,
                bool validated = false);
 
