@@ -870,8 +870,8 @@ __global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_wa
     // LDS below; they share only the barriers and the neighbour table.
     __shared__ __attribute__((aligned(16))) float aF_g[TT_GROUPS][TT_RB * 16][C];
     __shared__ __attribute__((aligned(16))) uint16_t A16_g[TT_GROUPS][TT_RB * 16 * TT_LD];
-    __shared__ float part_g[TT_GROUPS][TT_WAVES][TT_RB * 16], part2_g[TT_GROUPS][TT_WAVES][TT_RB * 16],
-        mean_g[TT_GROUPS][TT_RB * 16], inv_g[TT_GROUPS][TT_RB * 16];
+    __shared__ float part_g[TT_GROUPS][TT_WAVES][TT_RB * 16], part2_g[TT_GROUPS][TT_WAVES][TT_RB * 16];
+    __shared__ __attribute__((aligned(16))) float mean_g[TT_GROUPS][TT_RB * 16], inv_g[TT_GROUPS][TT_RB * 16];
     __shared__ float gb_g[TT_GROUPS][TT_ROWS][C];
     __shared__ float loose_g[TT_GROUPS][TT_ROWS][LOOSE], tp_g[TT_GROUPS][TT_ROWS][C], glob_g[TT_GROUPS][TT_ROWS][C];
     // The A operand of the per-row products (pool bias, board vector, join
@@ -1085,8 +1085,13 @@ __global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_wa
         }
         __syncthreads();
     };
-    auto norm_val = [&](float z, uint32_t cell, uint32_t which) {
-        return gelu_fast((z - mean[cell]) * inv[cell] * net.ln[LY.norm_g[which] + col] + net.ln[LY.norm_b[which] + col]);
+    // gelu(LayerNorm(z)) of this lane's four cells 4 q .. 4 q + 3 of row block rb (their mean and
+    // 1 / std read as one 16-byte LDS load each), gain g and bias bt of channel `col`
+    auto norm4 = [&](const float (&z)[4], uint32_t rb, float g, float bt, float (&out)[4]) {
+        const float4 m4 = *(const float4*)&mean[rb * 16 + 4 * q], i4 = *(const float4*)&inv[rb * 16 + 4 * q];
+        const float m[4] = {m4.x, m4.y, m4.z, m4.w}, iv[4] = {i4.x, i4.y, i4.z, i4.w};
+#pragma unroll
+        for (uint32_t v = 0; v < 4; v++) out[v] = gelu_fast((z[v] - m[v]) * iv[v] * g + bt);
     };
     // This wave's B fragments (its 16-column block) of a K-column matrix,
     // loaded ahead of the product that uses them.
@@ -1118,15 +1123,21 @@ __global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_wa
     for (uint32_t blk = 0; blk < BLOCKS; blk++) {
         uint4 bmix[2 * C / 32], bpool[2 * C / 32];
         cell_stats(x);
+        {
+            const float g = net.ln[LY.norm_g[2 * blk] + col], bt = net.ln[LY.norm_b[2 * blk] + col];
 #pragma unroll
-        for (uint32_t rb = 0; rb < TT_RB; rb++)
+            for (uint32_t rb = 0; rb < TT_RB; rb++) {
+                float a4[4];
+                norm4(x[rb], rb, g, bt, a4);
 #pragma unroll
-            for (uint32_t v = 0; v < 4; v++) {
-                const uint32_t cell = rb * 16 + 4 * q + v;
-                const float a = cell < TT_CELLS ? norm_val(x[rb][v], cell, 2 * blk) : 0.0f;
-                aF[cell][col] = a;
-                A16[cell * TT_LD + col] = to16<PREC>(a);
+                for (uint32_t v = 0; v < 4; v++) {
+                    const uint32_t cell = rb * 16 + 4 * q + v;
+                    const float a = cell < TT_CELLS ? a4[v] : 0.0f;
+                    aF[cell][col] = a;
+                    A16[cell * TT_LD + col] = to16<PREC>(a);
+                }
             }
+        }
         __syncthreads();
         load_b(bpool, net.m16[M_POOL0 + blk], K192{});
         load_b(bmix, net.m16[M_MIX0 + blk], K192{});
@@ -1205,13 +1216,19 @@ __global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_wa
                 }
         }
         cell_stats(y);
+        {
+            const float g = net.ln[LY.norm_g[2 * blk + 1] + col], bt = net.ln[LY.norm_b[2 * blk + 1] + col];
 #pragma unroll
-        for (uint32_t rb = 0; rb < TT_RB; rb++)
+            for (uint32_t rb = 0; rb < TT_RB; rb++) {
+                float a4[4];
+                norm4(y[rb], rb, g, bt, a4);
 #pragma unroll
-            for (uint32_t v = 0; v < 4; v++) {
-                const uint32_t cell = rb * 16 + 4 * q + v;
-                A16[cell * TT_LD + col] = to16<PREC>(cell < TT_CELLS ? norm_val(y[rb][v], cell, 2 * blk + 1) : 0.0f);
+                for (uint32_t v = 0; v < 4; v++) {
+                    const uint32_t cell = rb * 16 + 4 * q + v;
+                    A16[cell * TT_LD + col] = to16<PREC>(cell < TT_CELLS ? a4[v] : 0.0f);
+                }
             }
+        }
         __syncthreads();
         float z[TT_RB][4];
         gemm(z, bout, K96{});
@@ -1223,13 +1240,19 @@ __global__ __launch_bounds__(TT_GROUPS * TT_WAVES * 64) __attribute__((amdgpu_wa
             for (uint32_t v = 0; v < 4; v++) x[rb][v] += z[rb][v] + bo;
     }
     cell_stats(x);
+    {
+        const float g = net.ln[LY.norm_g[LN_TRUNK] + col], bt = net.ln[LY.norm_b[LN_TRUNK] + col];
 #pragma unroll
-    for (uint32_t rb = 0; rb < TT_RB; rb++)
+        for (uint32_t rb = 0; rb < TT_RB; rb++) {
+            float a4[4];
+            norm4(x[rb], rb, g, bt, a4);
 #pragma unroll
-        for (uint32_t v = 0; v < 4; v++) {
-            const uint32_t cell = rb * 16 + 4 * q + v;
-            aF[cell][col] = cell < TT_CELLS ? norm_val(x[rb][v], cell, LN_TRUNK) : 0.0f;
+            for (uint32_t v = 0; v < 4; v++) {
+                const uint32_t cell = rb * 16 + 4 * q + v;
+                aF[cell][col] = cell < TT_CELLS ? a4[v] : 0.0f;
+            }
         }
+    }
     __syncthreads();
     // the board vector (net.rs:704-722) and its join projection, per row:
     // [mean, max, loose] (zero-padded to whole k steps) as the operand
