@@ -7,7 +7,8 @@ the C ABI, against the oracle's restatement of engine/src/net.rs:
   solves (strategies, root values, carries) bit-identical to the oracle;
 - the zero network: every leaf valued at value_bias;
 - 16-bit operands: the leaf values track the oracle's model of the same
-  operand rounding.
+  operand rounding;
+- jobs tagged [5] through the service boundary, bit-identical in float32.
 """
 import os
 import sys
@@ -101,6 +102,25 @@ def test_v5_solve_float32_bit_exact():
     wave.close()
     refs = pmap(lambda j: O.solve(j, net, O.NET_F32), jobs)
     for k, (g, o) in enumerate(zip(got, refs)):
+        np.testing.assert_array_equal(g.strategy, o["strategy"], err_msg=f"tree {k}: strategy")
+        np.testing.assert_array_equal(g.root_values, o["roots"], err_msg=f"tree {k}: root values")
+        np.testing.assert_array_equal(g.carries, o["carries"].astype(np.float16), err_msg=f"tree {k}: carries")
+
+
+def test_v5_jobs_through_the_service():
+    """Jobs tagged [5] submitted through the service (wc_submit / wc_wait:
+    two lanes, waves of at most three jobs, the v5 bank published at spawn)
+    come back bit-identical to the oracle's float32 solves, with their tags."""
+    jobs = v5_jobs(trees=7, seed=47)
+    net = ww.synth_weights(ww.V5_DIMS, 3)
+    say(f"case v5 service: {len(jobs)} subgames, 2 lanes, waves of at most 3")
+    with ww.spawn(0, net, ww.WC_PRECISE, lanes=2, wave_jobs=3, window_us=500) as client:
+        handles = [client.submit(j, tag=500 + k) for k, j in enumerate(jobs)]
+        got = [h.wait() for h in handles]
+        assert client.queued_work() == 0
+    refs = pmap(lambda j: O.solve(j, net, O.NET_F32), jobs)
+    for k, (g, o) in enumerate(zip(got, refs)):
+        assert g.tag == 500 + k
         np.testing.assert_array_equal(g.strategy, o["strategy"], err_msg=f"tree {k}: strategy")
         np.testing.assert_array_equal(g.root_values, o["roots"], err_msg=f"tree {k}: root values")
         np.testing.assert_array_equal(g.carries, o["carries"].astype(np.float16), err_msg=f"tree {k}: carries")
