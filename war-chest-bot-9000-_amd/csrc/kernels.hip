@@ -758,28 +758,37 @@ __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, cons
     // arrays with the run-time p would place the record in scratch memory.
     const uint32_t vw = p ? u.vwin[1] : u.vwin[0];
     const uint32_t leaf0 = p ? u.leaf0[1] : u.leaf0[0], leaf1 = p ? u.leaf1[1] : u.leaf1[0];
+    // The deepest level's bounds and each thread's first record of it are
+    // fetched before the leaf phase: they do not depend on its values.
+    const BackRec* back = w.back_rec[p];
+    const uint32_t* blvl = w.back_lvl[p] + u.lvl0;
+    const uint32_t t = threadIdx.x;
+    uint32_t l = u.nlevels;
+    uint32_t e = l ? blvl[l] : 0, b = l ? blvl[l - 1] : 0;
+    BackRec q{};
+    if (l && b + t < e) q = back[b + t];
     // Network leaves: one value slot per thread, LEAF_BATCH slots per thread
     // in flight (their records, then the values they name).
     for (uint32_t k0 = leaf0; k0 < leaf1; k0 += LEAF_BATCH * BLOCK) {
-        LeafRec q[LEAF_BATCH];
+        LeafRec lr[LEAF_BATCH];
         float h[LEAF_BATCH], m[LEAF_BATCH];
 #pragma unroll
         for (uint32_t j = 0; j < LEAF_BATCH; j++) {
             const uint32_t k = k0 + j * BLOCK + threadIdx.x;
-            if (k < leaf1) q[j] = w.leaf_rec[p][k];
+            if (k < leaf1) lr[j] = w.leaf_rec[p][k];
         }
 #pragma unroll
         for (uint32_t j = 0; j < LEAF_BATCH; j++)
             if (k0 + j * BLOCK + threadIdx.x < leaf1) {
-                h[j] = head_out[q[j].head];
-                m[j] = w.mass[q[j].mass];
+                h[j] = head_out[lr[j].head];
+                m[j] = w.mass[lr[j].mass];
             }
 #pragma unroll
         for (uint32_t j = 0; j < LEAF_BATCH; j++)
             if (k0 + j * BLOCK + threadIdx.x < leaf1) {
                 const float v = h[j] * m[j];
-                if (!LDSV || q[j].exported) w.vals[q[j].out] = v;
-                if (LDSV) lds_vals[q[j].out - vw] = v;
+                if (!LDSV || lr[j].exported) w.vals[lr[j].out] = v;
+                if (LDSV) lds_vals[lr[j].out - vw] = v;
             }
     }
     for (uint32_t x = u.term0 + threadIdx.x; x < u.term1; x += blockDim.x) {
@@ -800,13 +809,6 @@ __global__ __launch_bounds__(BLOCK) void k_sweep(WaveDev w, uint32_t unit0, cons
     // Levels from the deepest up. Each thread's rows form one stream across
     // the levels: the record of its next row (in this level, else its first
     // in the next level up) is fetched while the current row runs.
-    const BackRec* back = w.back_rec[p];
-    const uint32_t* blvl = w.back_lvl[p] + u.lvl0;
-    const uint32_t t = threadIdx.x;
-    uint32_t l = u.nlevels;
-    uint32_t e = l ? blvl[l] : 0, b = l ? blvl[l - 1] : 0;
-    BackRec q{};
-    if (l && b + t < e) q = back[b + t];
     while (l-- > 0) {
         const uint32_t lb = b, le = e;
         if (l) {
