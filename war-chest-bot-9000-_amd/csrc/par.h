@@ -5,6 +5,8 @@
 #include <algorithm>
 #include <atomic>
 #include <cstddef>
+#include <exception>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -27,7 +29,9 @@ struct ParBudget {  // sets the calling thread's budget for its lifetime
 
 // Runs fn(i) for every i in [0, n) on up to max_threads host threads (at most
 // the hardware's and the caller's budget), taking indices from a shared
-// counter; loops nested inside fn share the caller's budget. fn must not throw.
+// counter; loops nested inside fn share the caller's budget. The first
+// exception fn throws (std::bad_alloc on a huge wave) ends the loop and is
+// rethrown on the calling thread.
 template <class F>
 void parallel_for(size_t n, F fn, unsigned max_threads = 16) {
     if (n == 0) return;
@@ -36,14 +40,23 @@ void parallel_for(size_t n, F fn, unsigned max_threads = 16) {
     const size_t nt = std::min<size_t>(std::min({hw, std::max(1u, max_threads), budget}), n);
     const unsigned inner = std::max<unsigned>(1u, budget / (unsigned)nt);
     std::atomic<size_t> next{0};
+    std::exception_ptr failure;
+    std::mutex failure_lock;
     auto work = [&]() {
         ParBudget share(inner);
-        for (size_t i = next.fetch_add(1); i < n; i = next.fetch_add(1)) fn(i);
+        try {
+            for (size_t i = next.fetch_add(1); i < n; i = next.fetch_add(1)) fn(i);
+        } catch (...) {
+            std::lock_guard<std::mutex> hold(failure_lock);
+            if (!failure) failure = std::current_exception();
+            next.store(n);  // the other threads take no further index
+        }
     };
     std::vector<std::thread> pool;
     for (size_t t = 1; t < nt; t++) pool.emplace_back(work);
     work();
     for (auto& th : pool) th.join();
+    if (failure) std::rethrow_exception(failure);
 }
 
 }  // namespace wc

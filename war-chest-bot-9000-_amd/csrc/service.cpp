@@ -474,7 +474,14 @@ void Service::lane_main(uint32_t lane) {
             jobs.push_back(std::move(p.job));
         }
         F.version = net->version;
-        if (ok) ok = pack_wave(std::move(jobs), &wh, &err, UNIT_SLOTS, true);  // validated at submit
+        if (ok) {
+            try {  // validated at submit; a wave too large for host memory fails its tickets
+                ok = pack_wave(std::move(jobs), &wh, &err, UNIT_SLOTS, true);
+            } catch (const std::exception& e) {
+                ok = false;
+                err = std::string("packing the wave failed: ") + e.what();
+            }
+        }
         if (ok) ok = ex->launch(wh, exv, &F.f, &err);
         if (!ok) {
             std::vector<Result> none;

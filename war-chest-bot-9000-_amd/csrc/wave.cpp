@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <string>
 #include <unordered_map>
 
@@ -90,6 +91,130 @@ void chunked(size_t n, F fn, size_t chunk = 16384) {
     parallel_for((n + chunk - 1) / chunk, [&](size_t c) { fn(c * chunk, std::min(n, (c + 1) * chunk)); });
 }
 
+// One job's layout inside its own tree, independent of every other job of
+// the wave: preorder, value slots, reach length, depths, its subtree units
+// and its top region, and how many entries it adds to each unit list.
+struct JobLayout {
+    std::vector<uint32_t> pre, vb[2], depth, row_of, term_of;
+    uint32_t vlen = 0, reach_len = 0;
+    std::vector<uint32_t> unit_nodes;      // every unit's nodes (preorder), unit after unit
+    std::vector<uint32_t> unit_at{0};      // unit j: unit_nodes[unit_at[j] .. unit_at[j + 1])
+    std::vector<uint32_t> unit_d0;         // unit j's top depth
+    std::vector<uint32_t> top;             // the top region's nodes, preorder
+    uint32_t top_depths = 0;               // 1 + the deepest top node's depth (0: no top region)
+    uint32_t lvls = 0, max_levels = 0, nback[2] = {0, 0}, nreach[2] = {0, 0}, ndec[2] = {0, 0};
+    uint32_t nrow = 0, nterm = 0;
+    uint32_t max_vwin = 0;                 // filled with the unit records
+    std::vector<Task> top_back[2], top_reach[2], top_dec[2];
+    std::vector<uint32_t> top_back_d[2], top_reach_d[2];  // depth of each top task
+    std::string err;
+
+    uint32_t levels_of(uint32_t j) const {
+        uint32_t L = 0;
+        for (uint32_t x = unit_at[j]; x < unit_at[j + 1]; x++) L = std::max(L, depth[unit_nodes[x]] - unit_d0[j] + 1);
+        return L;
+    }
+
+    void build(const Tables& t, const NetShape& net, bool v5, uint32_t unit_slots) {
+        const uint32_t N = t.nodes;
+        pre = preorder(t);
+        if (pre.size() != N) {
+            err = "tree is not connected from its root";
+            return;
+        }
+        if (!value_layout(t, pre, vb, &vlen, &err)) return;
+        for (uint32_t c = 0; c < t.ncfg && !v5; c++) {
+            const float key = t.cphi[size_t(c) * net.cfeat];
+            if (!(key >= 0.0f) || key != (float)(uint32_t)key || (net.heads && (uint32_t)key >= net.heads)) {
+                err = "config head index out of range";
+                return;
+            }
+        }
+        for (uint32_t local : t.bfs_order)
+            for (int p = 0; p < 2; p++)
+                if (local == 0 || t.node_player[t.node_parent[local]] == p) reach_len += t.nc(local, p);
+        depth.assign(N, 0);
+        for (uint32_t l = 0; l < t.nlevels(); l++)
+            for (uint32_t k = t.level_start[l]; k < t.level_start[l + 1]; k++) depth[t.bfs_order[k]] = l;
+        std::vector<uint64_t> sub(N, 0);
+        for (size_t k = pre.size(); k-- > 0;) {
+            uint32_t i = pre[k];
+            sub[i] += std::max<uint32_t>(std::max(t.nc(i, 0), t.nc(i, 1)), 1);
+            if (t.node_parent[i] != NONE) sub[t.node_parent[i]] += sub[i];
+        }
+        std::vector<uint32_t> pos(N);
+        for (uint32_t k = 0; k < N; k++) pos[pre[k]] = k;
+        row_of.assign(N, NONE);
+        term_of.assign(N, NONE);
+        for (uint32_t r = 0; r < t.rows; r++) row_of[t.leaf_rows[r]] = r;
+        for (uint32_t k = 0; k < t.term_leaves.size(); k++) term_of[t.term_leaves[k]] = k;
+        auto close_unit = [&](uint32_t d0) {
+            unit_at.push_back((uint32_t)unit_nodes.size());
+            unit_d0.push_back(d0);
+        };
+        // The nodes of the subtree rooted at r, in preorder.
+        auto subtree = [&](uint32_t r) {
+            uint32_t k = pos[r];
+            uint32_t end = k + 1;
+            while (end < N && depth[pre[end]] > depth[r]) end++;
+            unit_nodes.insert(unit_nodes.end(), pre.begin() + k, pre.begin() + end);
+        };
+        if (sub[0] <= unit_slots) {
+            unit_nodes = pre;
+            close_unit(0);
+        } else {
+            for (uint32_t i : pre)
+                if (sub[i] > unit_slots) top.push_back(i);
+            // Runs of fitting sibling subtrees below each top node, in child order.
+            // A top child ends the run: its subtree's value slots lie between
+            // its siblings', and a unit's window must stay contiguous.
+            for (uint32_t i : top) {
+                uint64_t run_slots = 0;
+                bool open = false;
+                for (uint32_t k = t.node_child_start[i]; k < t.node_child_start[i + 1]; k++) {
+                    uint32_t c = t.node_child[k];
+                    const bool fits = sub[c] <= unit_slots;
+                    if (open && (!fits || run_slots + sub[c] > unit_slots)) {
+                        close_unit(depth[i] + 1);
+                        open = false;
+                        run_slots = 0;
+                    }
+                    if (!fits) continue;
+                    subtree(c);
+                    open = true;
+                    run_slots += sub[c];
+                }
+                if (open) close_unit(depth[i] + 1);
+            }
+            for (uint32_t i : top) top_depths = std::max(top_depths, depth[i] + 1);
+        }
+        // What the units add to the wave's unit lists.
+        for (uint32_t j = 0; j + 1 < unit_at.size(); j++) {
+            const uint32_t L = levels_of(j);
+            lvls += L + 1;
+            max_levels = std::max(max_levels, L);
+            for (uint32_t x = unit_at[j]; x < unit_at[j + 1]; x++) {
+                const uint32_t local = unit_nodes[x];
+                const uint8_t kind = t.node_kind[local];
+                for (int p = 0; p < 2; p++) {
+                    if (kind != 2 && !(kind == 1 && t.node_player[local] != p)) nback[p] += t.nc(local, p);
+                    if (local != 0 && t.node_player[t.node_parent[local]] == p) nreach[p] += t.nc(local, p);
+                    if (kind == 0 && t.node_player[local] == p) ndec[p] += t.nc(local, p);
+                }
+                nrow += row_of[local] != NONE;
+                nterm += term_of[local] != NONE;
+            }
+        }
+    }
+};
+
+// Where one job's entries start in each wave list.
+struct JobAt {
+    uint32_t node, child, lrow, cell, draw, drow, reach, vals, rrow, rev, vrow, rvd, row, coff, member, cfg, exit,
+        ecoff, ecfg, term, rootv, unit, lvl, urow, uterm, back[2], rch[2], dec[2];
+    size_t pub, card, priv, emb, roots, carried, rowjob;
+};
+
 // Row records from the task lists (see BackRec / ReachRec / AccRec). Every
 // record is a function of its task alone, once the opponent rows' child
 // value-base lists are laid out (first appearance among the value tasks, in
@@ -150,13 +275,16 @@ void build_records(WaveHost* wp) {
         }
         return r;
     };
-    for (int p = 0; p < 2; p++) {
-        w.back_rec[p].resize(w.back_task[p].size());
-        w.top_back_rec[p].resize(w.top_back[p].size());
-        w.reach_rec[p].resize(w.reach_task[p].size());
-        w.top_reach_rec[p].resize(w.top_reach[p].size());
-        w.acc_rec[p].resize(w.decision[p].size());
-    }
+    parallel_for(10, [&](size_t k) {  // the record lists side by side
+        const int p = (int)(k & 1);
+        switch (k >> 1) {
+            case 0: w.back_rec[p].resize(w.back_task[p].size()); break;
+            case 1: w.top_back_rec[p].resize(w.top_back[p].size()); break;
+            case 2: w.reach_rec[p].resize(w.reach_task[p].size()); break;
+            case 3: w.top_reach_rec[p].resize(w.top_reach[p].size()); break;
+            default: w.acc_rec[p].resize(w.decision[p].size()); break;
+        }
+    });
     for (int p = 0; p < 2; p++) {
         chunked(w.back_task[p].size(), [&](size_t lo, size_t hi) {
             for (size_t k = lo; k < hi; k++) w.back_rec[p][k] = back(p, w.back_task[p][k]);
@@ -183,6 +311,14 @@ void build_records(WaveHost* wp) {
     // each unit's first slot from a prefix sum, then the units in parallel.
     const uint32_t heads = w.net.heads;
     const bool tower = readout_net(w.net.kind);
+    uint32_t nleaf[2] = {0, 0};
+    for (UnitDev& u : w.units)
+        for (int p = 0; p < 2; p++) {
+            u.leaf0[p] = nleaf[p];
+            for (uint32_t k = u.row0; k < u.row1; k++) nleaf[p] += w.nc(w.row_node[w.unit_row[k]], p);
+            u.leaf1[p] = nleaf[p];
+        }
+    parallel_for(2, [&](size_t p) { w.leaf_rec[p].resize(nleaf[p]); });
     for (int p = 0; p < 2; p++) {
         std::vector<uint32_t> row_blk;  // readout nets: each row's readout block for p
         if (tower) {
@@ -190,13 +326,6 @@ void build_records(WaveHost* wp) {
             for (uint32_t bi = 0; bi < w.tower_blk[p].size(); bi++)
                 for (uint32_t r = w.tower_blk[p][bi].r0; r < w.tower_blk[p][bi].r1; r++) row_blk[r] = bi;
         }
-        uint32_t at = 0;
-        for (UnitDev& u : w.units) {
-            u.leaf0[p] = at;
-            for (uint32_t k = u.row0; k < u.row1; k++) at += w.nc(w.row_node[w.unit_row[k]], p);
-            u.leaf1[p] = at;
-        }
-        w.leaf_rec[p].resize(at);
         parallel_for(w.units.size(), [&](size_t ui) {
             const UnitDev& u = w.units[ui];
             uint32_t slot = u.leaf0[p];
@@ -349,12 +478,6 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             return false;
         }
 
-    w.legal_off.push_back(0);
-    w.child_start.clear();
-    w.rev_start.push_back(0);
-    w.rvd_start.push_back(0);
-    w.row_cfg_off.push_back(0);
-    w.exit_coff.push_back(0);
     if (unit_slots == 0) {
         *err = "unit budget must be positive";
         return false;
@@ -364,144 +487,188 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     for (const Job& job : jobs)
         for (uint32_t i = 0; i < job.t.nodes; i++)
             unit_slots = std::max(unit_slots, std::max(job.t.nc(i, 0), job.t.nc(i, 1)));
-    {  // every list's final size (or a bound on it) first: the loop below appends without regrowing
-        size_t nodes = 0, kids = 0, cells = 0, lrows = 0, draws = 0, drows = 0, revs = 0, rrows = 0, rvds = 0,
-               vrows = 0, rows = 0, members = 0, cfgs = 0, pub = 0, terms = 0, slots[2] = {0, 0};
-        for (const Job& j : jobs) {
-            const Tables& t = j.t;
-            nodes += t.nodes;
-            kids += t.node_child.size();
-            cells += t.ncells;
-            lrows += t.legal_off.size();
-            draws += t.draw_to.size();
-            drows += t.draw_row_start.size();
-            revs += t.rev_src.size();
-            rrows += t.rev_start.size();
-            rvds += t.rvd_src.size();
-            vrows += t.rvd_start.size();
-            rows += t.rows;
-            members += t.leaf_cidx.size();
-            cfgs += t.ncfg;
-            pub += t.leaf_raw.size();
-            terms += t.term_leaves.size();
-            for (uint32_t i = 0; i < t.nodes; i++)
-                for (int p = 0; p < 2; p++) slots[p] += t.nc(i, p);
+
+    // The jobs are packed in three steps: each job's own layout (in parallel),
+    // every job's offset into each wave list (a prefix over the jobs), then
+    // each job's entries written at its offsets (in parallel). The lists are
+    // exactly what appending the jobs one after another makes.
+    const size_t J = jobs.size();
+    const bool v5 = w.net.kind == MODEL_V5, tower = w.net.kind == MODEL_TWO_TOWER;
+    std::vector<JobLayout> lay(J);
+    parallel_for(J, [&](size_t k) { lay[k].build(jobs[k].t, w.net, v5, unit_slots); });
+    for (size_t k = 0; k < J; k++)  // the first failure in job order
+        if (!lay[k].err.empty()) {
+            *err = lay[k].err;
+            return false;
         }
-        for (auto* v : {&w.node_meta, &w.child_start, &w.legal_row_of, &w.draw_off, &w.draw_row_off, &w.parent,
-                        &w.rev_row_of, &w.rvd_row_of})
-            v->reserve(nodes + 1);
-        w.node_nc.reserve(2 * nodes);
-        w.reach_base.reserve(2 * nodes);
-        w.vals_base.reserve(2 * nodes);
-        w.child.reserve(kids);
-        w.legal_off.reserve(lrows + 1);
-        w.legal_value.reserve(cells);
-        w.draw_to.reserve(draws);
-        w.draw_p.reserve(draws);
-        w.draw_row_start.reserve(drows);
-        w.rev_src.reserve(revs);
-        w.rev_cell.reserve(revs);
-        w.rev_start.reserve(rrows + 1);
-        w.rvd_src.reserve(rvds);
-        w.rvd_p.reserve(rvds);
-        w.rvd_start.reserve(vrows + 1);
-        w.row_node.reserve(rows);
-        w.row_cfg_off.reserve(2 * rows + 1);
-        w.row_cfg.reserve(members);
-        w.cfg_key.reserve(cfgs);
-        w.cfg_emb.reserve(cfgs * w.net.pool);
-        w.pub_raw.reserve(pub);
-        w.term_node.reserve(terms);
-        w.term_util.reserve(terms);
-        w.exit_node.reserve(rows + terms);
-        w.exit_coff.reserve(2 * (rows + terms) + 1);
-        for (int p = 0; p < 2; p++) {  // every (node, config) of p is at most one task of each kind
-            w.back_task[p].reserve(slots[p]);
-            w.reach_task[p].reserve(slots[p]);
-            w.decision[p].reserve(slots[p]);
+    std::vector<JobAt> at(J);
+    JobAt n{};  // running totals: the next job's offsets
+    uint32_t top_levels = 0;
+    for (size_t k = 0; k < J; k++) {
+        const Tables& t = jobs[k].t;
+        const JobLayout& L = lay[k];
+        at[k] = n;
+        n.node += t.nodes;
+        n.child += (uint32_t)t.node_child.size();
+        n.lrow += (uint32_t)t.legal_off.size() - 1;
+        n.cell += t.ncells;
+        n.draw += (uint32_t)t.draw_to.size();
+        n.drow += (uint32_t)t.draw_row_start.size();
+        n.reach += L.reach_len;
+        n.vals += L.vlen;
+        n.rrow += (uint32_t)t.rev_start.size() - 1;
+        n.rev += (uint32_t)t.rev_src.size();
+        n.vrow += (uint32_t)t.rvd_start.size() - 1;
+        n.rvd += (uint32_t)t.rvd_src.size();
+        n.row += (uint32_t)t.leaf_rows.size();
+        n.coff += (uint32_t)t.leaf_coff.size() - 1;
+        n.member += (uint32_t)t.leaf_cidx.size();
+        n.cfg += t.ncfg;
+        n.exit += (uint32_t)(t.leaf_rows.size() + t.term_leaves.size());
+        n.ecoff += (uint32_t)t.snap_coff.size() - 1;
+        n.ecfg += t.snapshot_configs();
+        n.term += (uint32_t)t.term_leaves.size();
+        n.rootv += jobs[k].nroots() * (t.nc(0, 0) + t.nc(0, 1));
+        n.unit += (uint32_t)L.unit_d0.size();
+        n.lvl += L.lvls;
+        n.urow += L.nrow;
+        n.uterm += L.nterm;
+        for (int p = 0; p < 2; p++) {
+            n.back[p] += L.nback[p];
+            n.rch[p] += L.nreach[p];
+            n.dec[p] += L.ndec[p];
         }
+        n.pub += t.leaf_raw.size();
+        n.card += v5 ? t.card_feat.size() : 0;
+        n.priv += v5 ? size_t(t.ncfg) * w.net.cfeat : tower ? size_t(t.ncfg) * w.net.priv_in : 0;
+        n.emb += v5 ? 0 : size_t(t.ncfg) * w.net.pool;
+        n.roots += jobs[k].root[0].size() + jobs[k].root[1].size();
+        for (uint32_t r = 0; r < jobs[k].nroots(); r++) n.carried += jobs[k].carried[0][r].size() + jobs[k].carried[1][r].size();
+        n.rowjob += v5 ? t.rows : 0;
+        w.max_levels = std::max(w.max_levels, L.max_levels);
+        w.nroots_max = std::max(w.nroots_max, jobs[k].nroots());
+        top_levels = std::max(top_levels, L.top_depths);
     }
-    uint32_t cfg_total = 0;
-    std::vector<UnitDev> sub_units;
-    std::vector<std::vector<Task>> top_back[2], top_reach[2];
-    std::vector<Task> top_dec[2];
-    std::vector<uint32_t> job_rows;  // first network row of each job
+    // Every list at its final size, the larger ones side by side (a resize
+    // clears its new entries: the fill below overwrites them all).
+    std::vector<std::function<void()>> sizing = {
+        [&] {
+            for (auto* v : {&w.node_meta, &w.child_start, &w.legal_row_of, &w.draw_off, &w.draw_row_off, &w.parent,
+                            &w.rev_row_of, &w.rvd_row_of})
+                v->resize(n.node);
+            w.node_nc.resize(2 * size_t(n.node));
+            w.reach_base.resize(2 * size_t(n.node));
+            w.vals_base.resize(2 * size_t(n.node));
+            w.node_top.assign(n.node, 0);
+            w.child.resize(n.child);
+            w.legal_off.resize(1 + size_t(n.lrow));
+            w.legal_off[0] = 0;
+        },
+        [&] { w.legal_value.assign(n.cell, NONE); },
+        [&] { w.draw_to.resize(n.draw); },
+        [&] { w.draw_p.resize(n.draw); },
+        [&] { w.draw_row_start.resize(n.drow); },
+        [&] {
+            w.rev_start.resize(1 + size_t(n.rrow));
+            w.rev_start[0] = 0;
+            w.rvd_start.resize(1 + size_t(n.vrow));
+            w.rvd_start[0] = 0;
+        },
+        [&] { w.rev_src.resize(n.rev); },
+        [&] { w.rev_cell.resize(n.rev); },
+        [&] { w.rvd_src.resize(n.rvd); },
+        [&] { w.rvd_p.resize(n.rvd); },
+        [&] {
+            w.row_node.resize(n.row);
+            w.row_cfg_off.resize(1 + size_t(n.coff));
+            w.row_cfg_off[0] = 0;
+            w.row_cfg.resize(n.member);
+            w.cfg_key.resize(n.cfg);
+            w.cfg_job.resize(v5 ? n.cfg : 0);
+            w.cfg_owner.resize(v5 ? n.cfg : 0);
+            w.row_job.resize(n.rowjob);
+        },
+        [&] {
+            w.cfg_emb.resize(n.emb);
+            w.cfg_priv.resize(n.priv);
+            w.card_feat.resize(n.card);
+        },
+        [&] { w.pub_raw.resize(n.pub); },
+        [&] {
+            w.term_node.resize(n.term);
+            w.term_util.resize(n.term);
+            w.roots.resize(n.roots);
+            w.carried.resize(n.carried);
+            w.exit_node.resize(n.exit);
+            w.exit_coff.resize(1 + size_t(n.ecoff));
+            w.exit_coff[0] = 0;
+            w.trees.resize(J);
+            w.unit_row.resize(n.urow);
+            w.unit_term.resize(n.uterm);
+        },
+    };
+    for (int p = 0; p < 2; p++) {
+        sizing.push_back([&, p] {
+            w.back_lvl[p].resize(n.lvl);
+            w.reach_lvl[p].resize(n.lvl);
+            w.decision[p].resize(n.dec[p]);
+        });
+        sizing.push_back([&, p] { w.back_task[p].resize(n.back[p]); });
+        sizing.push_back([&, p] { w.reach_task[p].resize(n.rch[p]); });
+    }
+    parallel_for(sizing.size(), [&](size_t k) { sizing[k](); });
+    std::vector<UnitDev> sub_units(n.unit);
+    std::vector<uint32_t> job_rows(J);  // first network row of each job
+    w.ncells = n.cell;
+    w.reach_len = n.reach;
+    w.vals_len = n.vals;
+    w.snapshot_configs = n.ecfg;
+    w.root_values_len = n.rootv;
+    w.lvl_len = n.lvl;
 
-    for (const Job& job : jobs) {
+    parallel_for(J, [&](size_t k) {
+        const Job& job = jobs[k];
         const Tables& t = job.t;
-        const uint32_t N = t.nodes;
-        const uint32_t node0 = w.nodes();
-        const uint32_t child0 = (uint32_t)w.child.size();
-        const uint32_t legal_row0 = (uint32_t)w.legal_off.size() - 1;
-        const uint32_t cell0 = w.ncells;
-        const uint32_t draw0 = (uint32_t)w.draw_to.size();
-        const uint32_t draw_row0 = (uint32_t)w.draw_row_start.size();
-        const uint32_t reach0 = w.reach_len;
-        const uint32_t vals0 = w.vals_len;
-        const uint32_t rev_row0 = (uint32_t)w.rev_start.size() - 1;
-        const uint32_t rev0 = (uint32_t)w.rev_src.size();
-        const uint32_t rvd_row0 = (uint32_t)w.rvd_start.size() - 1;
-        const uint32_t rvd0 = (uint32_t)w.rvd_src.size();
-        const uint32_t row0 = w.rows();
-        const uint32_t member0 = (uint32_t)w.row_cfg.size();
-        const uint32_t cfg0 = cfg_total;
-        const uint32_t exit0 = (uint32_t)w.exit_node.size();
-        const uint32_t exit_cfg0 = w.snapshot_configs;
-
-        TreeDev td{};
-        td.node0 = node0;
-        td.nodes = N;
-        const uint32_t row_base = row0, term_base = (uint32_t)w.term_node.size();
+        const JobAt& a = at[k];
+        JobLayout& L = lay[k];
+        const uint32_t N = t.nodes, node0 = a.node;
         for (uint32_t i = 0; i < N; i++) {
-            w.node_meta.push_back(uint32_t(t.node_kind[i]) | uint32_t(t.node_player[i]) << 2);
-            w.node_nc.push_back(t.nc(i, 0));
-            w.node_nc.push_back(t.nc(i, 1));
-            w.child_start.push_back(child0 + t.node_child_start[i]);
-            w.legal_row_of.push_back(t.legal_row_of[i] == NONE ? NONE : legal_row0 + t.legal_row_of[i]);
-            w.draw_off.push_back(draw0 + t.draw_off[i]);
-            w.draw_row_off.push_back(draw_row0 + t.draw_row_off[i]);
-            w.parent.push_back(t.node_parent[i] == NONE ? NONE : node0 + t.node_parent[i]);
-            w.rev_row_of.push_back(t.rev_row_of[i] == NONE ? NONE : rev_row0 + t.rev_row_of[i]);
-            w.rvd_row_of.push_back(t.rvd_row_of[i] == NONE ? NONE : rvd_row0 + t.rvd_row_of[i]);
+            const uint32_t g = node0 + i;
+            w.node_meta[g] = uint32_t(t.node_kind[i]) | uint32_t(t.node_player[i]) << 2;
+            w.node_nc[2 * size_t(g)] = t.nc(i, 0);
+            w.node_nc[2 * size_t(g) + 1] = t.nc(i, 1);
+            w.child_start[g] = a.child + t.node_child_start[i];
+            w.legal_row_of[g] = t.legal_row_of[i] == NONE ? NONE : a.lrow + t.legal_row_of[i];
+            w.draw_off[g] = a.draw + t.draw_off[i];
+            w.draw_row_off[g] = a.drow + t.draw_row_off[i];
+            w.parent[g] = t.node_parent[i] == NONE ? NONE : node0 + t.node_parent[i];
+            w.rev_row_of[g] = t.rev_row_of[i] == NONE ? NONE : a.rrow + t.rev_row_of[i];
+            w.rvd_row_of[g] = t.rvd_row_of[i] == NONE ? NONE : a.vrow + t.rvd_row_of[i];
         }
-        for (uint32_t c : t.node_child) w.child.push_back(node0 + c);
-        append_shift<uint32_t>(w.legal_off, t.legal_off, 1, cell0, false);
-        w.draw_row_start.insert(w.draw_row_start.end(), t.draw_row_start.begin(), t.draw_row_start.end());
-        w.draw_to.insert(w.draw_to.end(), t.draw_to.begin(), t.draw_to.end());
-        w.draw_p.insert(w.draw_p.end(), t.draw_p.begin(), t.draw_p.end());
+        for (size_t x = 0; x < t.node_child.size(); x++) w.child[a.child + x] = node0 + t.node_child[x];
+        for (size_t x = 1; x < t.legal_off.size(); x++) w.legal_off[a.lrow + x] = t.legal_off[x] + a.cell;
+        std::copy(t.draw_row_start.begin(), t.draw_row_start.end(), w.draw_row_start.begin() + a.drow);
+        std::copy(t.draw_to.begin(), t.draw_to.end(), w.draw_to.begin() + a.draw);
+        std::copy(t.draw_p.begin(), t.draw_p.end(), w.draw_p.begin() + a.draw);
 
         // Reach slots in BFS order; a player who did not act at the parent
         // keeps the parent's vector (engine/src/gpu/wave.rs:358-374).
-        w.reach_base.resize(2 * size_t(node0 + N), 0);
-        uint32_t reach_at = reach0;
+        uint32_t reach_at = a.reach;
         for (uint32_t local : t.bfs_order) {
-            uint32_t node = node0 + local;
+            const uint32_t node = node0 + local;
             for (int p = 0; p < 2; p++) {
                 if (local == 0 || t.node_player[t.node_parent[local]] == p) {
-                    w.reach_base[2 * node + p] = reach_at;
+                    w.reach_base[2 * size_t(node) + p] = reach_at;
                     reach_at += t.nc(local, p);
                 } else {
-                    w.reach_base[2 * node + p] = w.reach_base[2 * (node0 + t.node_parent[local]) + p];
+                    w.reach_base[2 * size_t(node) + p] = w.reach_base[2 * size_t(node0 + t.node_parent[local]) + p];
                 }
             }
         }
-        w.reach_len = reach_at;
-
-        const std::vector<uint32_t> pre = preorder(t);
-        if (pre.size() != N) {
-            *err = "tree is not connected from its root";
-            return false;
-        }
-        std::vector<uint32_t> vb[2];
-        uint32_t vlen = 0;
-        if (!value_layout(t, pre, vb, &vlen, err)) return false;
-        w.vals_base.resize(2 * size_t(node0 + N), 0);
         for (uint32_t i = 0; i < N; i++)
-            for (int p = 0; p < 2; p++) w.vals_base[2 * (node0 + i) + p] = vals0 + vb[p][i];
-        w.vals_len = vals0 + vlen;
+            for (int p = 0; p < 2; p++) w.vals_base[2 * size_t(node0 + i) + p] = a.vals + L.vb[p][i];
 
         // Direct value index of each legal cell's successor (wave.rs:393-411).
-        w.legal_value.resize(cell0 + t.ncells, NONE);
         for (uint32_t i = 0; i < N; i++) {
             if (t.node_kind[i] != 0) continue;
             int p = t.node_player[i];
@@ -509,224 +676,192 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             for (uint32_t c = 0; c < t.nc(i, p); c++)
                 for (uint32_t g = t.legal_off[rowa + c]; g < t.legal_off[rowa + c + 1]; g++)
                     if (t.legal_trans[g] != NONE)
-                        w.legal_value[cell0 + g] = w.vals_base[2 * (node0 + t.legal_child[g]) + p] + t.legal_trans[g];
+                        w.legal_value[a.cell + g] = w.vals_base[2 * size_t(node0 + t.legal_child[g]) + p] + t.legal_trans[g];
         }
-        w.ncells += t.ncells;
 
-        append_shift<uint32_t>(w.rev_start, t.rev_start, 1, rev0, false);
-        w.rev_src.insert(w.rev_src.end(), t.rev_src.begin(), t.rev_src.end());
-        append_shift<uint32_t>(w.rev_cell, t.rev_cell, 0, cell0, false);
-        append_shift<uint32_t>(w.rvd_start, t.rvd_start, 1, rvd0, false);
-        w.rvd_src.insert(w.rvd_src.end(), t.rvd_src.begin(), t.rvd_src.end());
-        w.rvd_p.insert(w.rvd_p.end(), t.rvd_p.begin(), t.rvd_p.end());
+        for (size_t x = 1; x < t.rev_start.size(); x++) w.rev_start[a.rrow + x] = t.rev_start[x] + a.rev;
+        std::copy(t.rev_src.begin(), t.rev_src.end(), w.rev_src.begin() + a.rev);
+        for (size_t x = 0; x < t.rev_cell.size(); x++) w.rev_cell[a.rev + x] = t.rev_cell[x] + a.cell;
+        for (size_t x = 1; x < t.rvd_start.size(); x++) w.rvd_start[a.vrow + x] = t.rvd_start[x] + a.rvd;
+        std::copy(t.rvd_src.begin(), t.rvd_src.end(), w.rvd_src.begin() + a.rvd);
+        std::copy(t.rvd_p.begin(), t.rvd_p.end(), w.rvd_p.begin() + a.rvd);
 
         // Network rows and interned configs.
-        job_rows.push_back((uint32_t)w.row_node.size());
-        for (uint32_t r : t.leaf_rows) w.row_node.push_back(node0 + r);
-        append_shift<uint32_t>(w.row_cfg_off, t.leaf_coff, 1, member0, false);
-        append_shift<uint32_t>(w.row_cfg, t.leaf_cidx, 0, cfg0, false);
-        const bool v5 = w.net.kind == MODEL_V5;
-        const uint32_t job_index = (uint32_t)w.trees.size();
+        job_rows[k] = a.row;
+        for (size_t r = 0; r < t.leaf_rows.size(); r++) w.row_node[a.row + r] = node0 + t.leaf_rows[r];
+        for (size_t x = 1; x < t.leaf_coff.size(); x++) w.row_cfg_off[a.coff + x] = t.leaf_coff[x] + a.member;
+        for (size_t x = 0; x < t.leaf_cidx.size(); x++) w.row_cfg[a.member + x] = t.leaf_cidx[x] + a.cfg;
         if (v5) {
-            for (uint32_t r = 0; r < t.rows; r++) w.row_job.push_back(job_index);
-            w.card_feat.insert(w.card_feat.end(), t.card_feat.begin(), t.card_feat.end());
-        }
-        for (uint32_t c = 0; c < t.ncfg && v5; c++) {
+            std::fill(w.row_job.begin() + a.rowjob, w.row_job.begin() + a.rowjob + t.rows, (uint32_t)k);
+            std::copy(t.card_feat.begin(), t.card_feat.end(), w.card_feat.begin() + a.card);
             // the config encoder reads the counts, the owner's card view and its job's table
-            w.cfg_key.push_back(0);
-            w.cfg_priv.insert(w.cfg_priv.end(), &t.cphi[size_t(c) * w.net.cfeat],
-                              &t.cphi[size_t(c) * w.net.cfeat] + w.net.cfeat);
-            w.cfg_job.push_back(job_index);
-            w.cfg_owner.push_back(t.cplayer[c]);
-        }
-        for (uint32_t c = 0; c < t.ncfg && !v5; c++) {
-            const float* phi = &t.cphi[size_t(c) * w.net.cfeat];
-            float key = phi[0];
-            if (!(key >= 0.0f) || key != (float)(uint32_t)key || (w.net.heads && (uint32_t)key >= w.net.heads)) {
-                *err = "config head index out of range";
-                return false;
+            for (uint32_t c = 0; c < t.ncfg; c++) {
+                w.cfg_key[a.cfg + c] = 0;
+                std::copy(&t.cphi[size_t(c) * w.net.cfeat], &t.cphi[size_t(c) * w.net.cfeat] + w.net.cfeat,
+                          w.cfg_priv.begin() + a.priv + size_t(c) * w.net.cfeat);
+                w.cfg_job[a.cfg + c] = (uint32_t)k;
+                w.cfg_owner[a.cfg + c] = t.cplayer[c];
             }
-            w.cfg_key.push_back((uint32_t)key);
-            w.cfg_emb.insert(w.cfg_emb.end(), phi + 1, phi + 1 + w.net.pool);
-            if (w.net.kind == MODEL_TWO_TOWER)
-                w.cfg_priv.insert(w.cfg_priv.end(), phi + 1 + w.net.pool, phi + 1 + w.net.pool + w.net.priv_in);
+        } else {
+            for (uint32_t c = 0; c < t.ncfg; c++) {
+                const float* phi = &t.cphi[size_t(c) * w.net.cfeat];
+                w.cfg_key[a.cfg + c] = (uint32_t)phi[0];
+                std::copy(phi + 1, phi + 1 + w.net.pool, w.cfg_emb.begin() + a.emb + size_t(c) * w.net.pool);
+                if (tower)
+                    std::copy(phi + 1 + w.net.pool, phi + 1 + w.net.pool + w.net.priv_in,
+                              w.cfg_priv.begin() + a.priv + size_t(c) * w.net.priv_in);
+            }
         }
-        cfg_total += t.ncfg;
-        w.pub_raw.insert(w.pub_raw.end(), t.leaf_raw.begin(), t.leaf_raw.end());
-        for (size_t k = 0; k < t.term_leaves.size(); k++) {
-            w.term_node.push_back(node0 + t.term_leaves[k]);
-            w.term_util.push_back(t.terminal_utility[k]);
+        std::copy(t.leaf_raw.begin(), t.leaf_raw.end(), w.pub_raw.begin() + a.pub);
+        for (size_t x = 0; x < t.term_leaves.size(); x++) {
+            w.term_node[a.term + x] = node0 + t.term_leaves[x];
+            w.term_util[a.term + x] = t.terminal_utility[x];
         }
-        td.reach0 = reach0;
-        td.reach_len = reach_at - reach0;
-        td.root0 = (uint32_t)w.roots.size();
+
+        TreeDev td{};
+        td.node0 = node0;
+        td.nodes = N;
+        td.reach0 = a.reach;
+        td.reach_len = L.reach_len;
+        td.root0 = (uint32_t)a.roots;
         td.n0 = t.nc(0, 0);
         td.n1 = t.nc(0, 1);
-        w.roots.insert(w.roots.end(), job.root[0].begin(), job.root[0].end());
-        w.roots.insert(w.roots.end(), job.root[1].begin(), job.root[1].end());
-        td.carried0 = (uint32_t)w.carried.size();
+        std::copy(job.root[0].begin(), job.root[0].end(), w.roots.begin() + a.roots);
+        std::copy(job.root[1].begin(), job.root[1].end(), w.roots.begin() + a.roots + job.root[0].size());
+        td.carried0 = (uint32_t)a.carried;
         td.nroots = job.nroots();
-        for (uint32_t r = 0; r < job.nroots(); r++) {
-            w.carried.insert(w.carried.end(), job.carried[0][r].begin(), job.carried[0][r].end());
-            w.carried.insert(w.carried.end(), job.carried[1][r].begin(), job.carried[1][r].end());
-        }
-        td.root_value0 = w.root_values_len;
-        w.root_values_len += job.nroots() * (td.n0 + td.n1);
-        w.nroots_max = std::max(w.nroots_max, job.nroots());
-        td.exit0 = exit0;
+        size_t ca = a.carried;
+        for (uint32_t r = 0; r < job.nroots(); r++)
+            for (int p = 0; p < 2; p++) {
+                std::copy(job.carried[p][r].begin(), job.carried[p][r].end(), w.carried.begin() + ca);
+                ca += job.carried[p][r].size();
+            }
+        td.root_value0 = a.rootv;
+        td.exit0 = a.exit;
         td.nexit = (uint32_t)(t.leaf_rows.size() + t.term_leaves.size());
-        for (uint32_t r : t.leaf_rows) w.exit_node.push_back(node0 + r);
-        for (uint32_t r : t.term_leaves) w.exit_node.push_back(node0 + r);
-        append_shift<uint32_t>(w.exit_coff, t.snap_coff, 1, exit_cfg0, false);
-        w.snapshot_configs += t.snapshot_configs();
+        for (size_t r = 0; r < t.leaf_rows.size(); r++) w.exit_node[a.exit + r] = node0 + t.leaf_rows[r];
+        for (size_t r = 0; r < t.term_leaves.size(); r++)
+            w.exit_node[a.exit + t.leaf_rows.size() + r] = node0 + t.term_leaves[r];
+        for (size_t x = 1; x < t.snap_coff.size(); x++) w.exit_coff[a.ecoff + x] = t.snap_coff[x] + a.ecfg;
+        w.trees[k] = td;
 
-        // Sweep units of this tree.
-        w.node_top.resize(node0 + N, 0);
-        std::vector<uint32_t> depth(N, 0);
-        for (uint32_t l = 0; l < t.nlevels(); l++)
-            for (uint32_t k = t.level_start[l]; k < t.level_start[l + 1]; k++) depth[t.bfs_order[k]] = l;
-        std::vector<uint64_t> sub(N, 0);
-        for (size_t k = pre.size(); k-- > 0;) {
-            uint32_t i = pre[k];
-            sub[i] += std::max<uint32_t>(std::max(t.nc(i, 0), t.nc(i, 1)), 1);
-            if (t.node_parent[i] != NONE) sub[t.node_parent[i]] += sub[i];
-        }
-        std::vector<uint32_t> pos(N);
-        for (uint32_t k = 0; k < N; k++) pos[pre[k]] = k;
-        std::vector<uint32_t> row_of(N, NONE), term_of(N, NONE);
-        for (uint32_t r = 0; r < t.rows; r++) row_of[t.leaf_rows[r]] = r;
-        for (uint32_t k = 0; k < t.term_leaves.size(); k++) term_of[t.term_leaves[k]] = k;
-        const uint32_t tree_index = (uint32_t)w.trees.size();
-        // Emit one unit over `nodes` (in preorder) with unit-local levels depth - d0.
-        auto emit = [&](const std::vector<uint32_t>& nodes, uint32_t d0) {
+        // Sweep units of this tree: level l of unit u holds its nodes at depth
+        // d0 + l; each list is unit-major, then player, then level.
+        uint32_t lvl = a.lvl, urow = a.urow, uterm = a.uterm, back[2] = {a.back[0], a.back[1]},
+                 rch[2] = {a.rch[0], a.rch[1]}, dec[2] = {a.dec[0], a.dec[1]};
+        std::vector<std::vector<uint32_t>> by_level;
+        for (uint32_t j = 0; j + 1 < L.unit_at.size(); j++) {
+            const uint32_t b = L.unit_at[j], e = L.unit_at[j + 1], d0 = L.unit_d0[j];
             UnitDev u{};
-            u.tree = tree_index;
-            uint32_t L = 0;
-            for (uint32_t i : nodes) L = std::max(L, depth[i] - d0 + 1);
-            u.nlevels = L;
-            u.lvl0 = w.lvl_len;
-            w.lvl_len += L + 1;
-            w.max_levels = std::max(w.max_levels, L);
-            std::vector<std::vector<uint32_t>> by_level(L);
-            for (uint32_t i : nodes) by_level[depth[i] - d0].push_back(i);
+            u.tree = (uint32_t)k;
+            const uint32_t nl = L.levels_of(j);
+            u.nlevels = nl;
+            u.lvl0 = lvl;
+            lvl += nl + 1;
+            by_level.assign(nl, {});
+            for (uint32_t x = b; x < e; x++) by_level[L.depth[L.unit_nodes[x]] - d0].push_back(L.unit_nodes[x]);
             uint64_t slots = 0;
-            for (uint32_t i : nodes) slots += std::max(t.nc(i, 0), t.nc(i, 1));
+            for (uint32_t x = b; x < e; x++)
+                slots += std::max(t.nc(L.unit_nodes[x], 0), t.nc(L.unit_nodes[x], 1));
             u.slots = (uint32_t)std::min<uint64_t>(slots, 0xffffffffu);
             // Value window of each player: the unit owns a contiguous run of slots.
             for (int p = 0; p < 2; p++) {
                 uint32_t lo = NONE, hi = 0;
-                for (uint32_t i : nodes) {
+                for (uint32_t x = b; x < e; x++) {
+                    const uint32_t i = L.unit_nodes[x];
                     if (t.nc(i, p) == 0) continue;
-                    uint32_t b = w.vals_base[2 * (node0 + i) + p];
-                    lo = std::min(lo, b);
-                    hi = std::max(hi, b + t.nc(i, p));
+                    const uint32_t vb = a.vals + L.vb[p][i];
+                    lo = std::min(lo, vb);
+                    hi = std::max(hi, vb + t.nc(i, p));
                 }
                 u.vwin[p] = lo == NONE ? 0 : lo;
                 u.vwin_n[p] = lo == NONE ? 0 : hi - lo;
-                w.max_vwin = std::max(w.max_vwin, u.vwin_n[p]);
+                L.max_vwin = std::max(L.max_vwin, u.vwin_n[p]);
             }
             for (int p = 0; p < 2; p++) {
-                for (uint32_t l = 0; l < L; l++) {
-                    w.back_lvl[p].push_back((uint32_t)w.back_task[p].size());
-                    w.reach_lvl[p].push_back((uint32_t)w.reach_task[p].size());
+                for (uint32_t l = 0; l < nl; l++) {
+                    w.back_lvl[p][u.lvl0 + l] = back[p];
+                    w.reach_lvl[p][u.lvl0 + l] = rch[p];
                     for (uint32_t local : by_level[l]) {
-                        uint32_t node = node0 + local;
-                        uint8_t kind = t.node_kind[local];
+                        const uint32_t node = node0 + local;
+                        const uint8_t kind = t.node_kind[local];
                         if (kind != 2 && !(kind == 1 && t.node_player[local] != p))
-                            for (uint32_t c = 0; c < t.nc(local, p); c++) w.back_task[p].push_back({node, c});
+                            for (uint32_t c = 0; c < t.nc(local, p); c++) w.back_task[p][back[p]++] = {node, c};
                         if (local != 0 && t.node_player[t.node_parent[local]] == p)
-                            for (uint32_t c = 0; c < t.nc(local, p); c++) w.reach_task[p].push_back({node, c});
+                            for (uint32_t c = 0; c < t.nc(local, p); c++) w.reach_task[p][rch[p]++] = {node, c};
                     }
                 }
-                w.back_lvl[p].push_back((uint32_t)w.back_task[p].size());
-                w.reach_lvl[p].push_back((uint32_t)w.reach_task[p].size());
-                u.dec0[p] = (uint32_t)w.decision[p].size();
-                for (uint32_t local : nodes)
+                w.back_lvl[p][u.lvl0 + nl] = back[p];
+                w.reach_lvl[p][u.lvl0 + nl] = rch[p];
+                u.dec0[p] = dec[p];
+                for (uint32_t x = b; x < e; x++) {
+                    const uint32_t local = L.unit_nodes[x];
                     if (t.node_kind[local] == 0 && t.node_player[local] == p)
-                        for (uint32_t c = 0; c < t.nc(local, p); c++) w.decision[p].push_back({node0 + local, c});
-                u.dec1[p] = (uint32_t)w.decision[p].size();
-            }
-            u.row0 = (uint32_t)w.unit_row.size();
-            for (uint32_t local : nodes)
-                if (row_of[local] != NONE) w.unit_row.push_back(row_base + row_of[local]);
-            u.row1 = (uint32_t)w.unit_row.size();
-            u.term0 = (uint32_t)w.unit_term.size();
-            for (uint32_t local : nodes)
-                if (term_of[local] != NONE) w.unit_term.push_back(term_base + term_of[local]);
-            u.term1 = (uint32_t)w.unit_term.size();
-            sub_units.push_back(u);
-        };
-        // The nodes of the subtree rooted at r, in preorder.
-        auto subtree = [&](uint32_t r, std::vector<uint32_t>* out) {
-            uint32_t k = pos[r];
-            uint32_t end = k + 1;
-            while (end < N && depth[pre[end]] > depth[r]) end++;
-            out->insert(out->end(), pre.begin() + k, pre.begin() + end);
-        };
-        if (sub[0] <= unit_slots) {
-            emit(pre, 0);
-        } else {
-            std::vector<uint32_t> top;
-            for (uint32_t i : pre)
-                if (sub[i] > unit_slots) top.push_back(i);
-            // Runs of fitting sibling subtrees below each top node, in child order.
-            // A top child ends the run: its subtree's value slots lie between
-            // its siblings', and a unit's window must stay contiguous.
-            for (uint32_t i : top) {
-                std::vector<uint32_t> run;
-                uint64_t run_slots = 0;
-                for (uint32_t k = t.node_child_start[i]; k < t.node_child_start[i + 1]; k++) {
-                    uint32_t c = t.node_child[k];
-                    const bool fits = sub[c] <= unit_slots;
-                    if (!run.empty() && (!fits || run_slots + sub[c] > unit_slots)) {
-                        emit(run, depth[i] + 1);
-                        run.clear();
-                        run_slots = 0;
-                    }
-                    if (!fits) continue;
-                    subtree(c, &run);
-                    run_slots += sub[c];
+                        for (uint32_t c = 0; c < t.nc(local, p); c++) w.decision[p][dec[p]++] = {node0 + local, c};
                 }
-                if (!run.empty()) emit(run, depth[i] + 1);
+                u.dec1[p] = dec[p];
             }
-            // The top region joins every other tree's at its depth.
-            for (uint32_t local : top) {
-                uint32_t node = node0 + local, d = depth[local];
-                w.node_top[node] = 1;
-                for (int p = 0; p < 2; p++) {
-                    if (top_back[p].size() <= d) {
-                        top_back[p].resize(d + 1);
-                        top_reach[p].resize(d + 1);
+            u.row0 = urow;
+            for (uint32_t x = b; x < e; x++)
+                if (L.row_of[L.unit_nodes[x]] != NONE) w.unit_row[urow++] = a.row + L.row_of[L.unit_nodes[x]];
+            u.row1 = urow;
+            u.term0 = uterm;
+            for (uint32_t x = b; x < e; x++)
+                if (L.term_of[L.unit_nodes[x]] != NONE) w.unit_term[uterm++] = a.term + L.term_of[L.unit_nodes[x]];
+            u.term1 = uterm;
+            sub_units[a.unit + j] = u;
+        }
+        // This tree's top region, by depth (joined with the other trees' below).
+        for (uint32_t local : L.top) {
+            const uint32_t node = node0 + local, d = L.depth[local];
+            w.node_top[node] = 1;
+            for (int p = 0; p < 2; p++) {
+                const uint8_t kind = t.node_kind[local];
+                if (kind != 2 && !(kind == 1 && t.node_player[local] != p))
+                    for (uint32_t c = 0; c < t.nc(local, p); c++) {
+                        L.top_back[p].push_back({node, c});
+                        L.top_back_d[p].push_back(d);
                     }
-                    uint8_t kind = t.node_kind[local];
-                    if (kind != 2 && !(kind == 1 && t.node_player[local] != p))
-                        for (uint32_t c = 0; c < t.nc(local, p); c++) top_back[p][d].push_back({node, c});
-                    if (local != 0 && t.node_player[t.node_parent[local]] == p)
-                        for (uint32_t c = 0; c < t.nc(local, p); c++) top_reach[p][d].push_back({node, c});
-                    if (kind == 0 && t.node_player[local] == p)
-                        for (uint32_t c = 0; c < t.nc(local, p); c++) top_dec[p].push_back({node, c});
-                }
+                if (local != 0 && t.node_player[t.node_parent[local]] == p)
+                    for (uint32_t c = 0; c < t.nc(local, p); c++) {
+                        L.top_reach[p].push_back({node, c});
+                        L.top_reach_d[p].push_back(d);
+                    }
+                if (kind == 0 && t.node_player[local] == p)
+                    for (uint32_t c = 0; c < t.nc(local, p); c++) L.top_dec[p].push_back({node, c});
             }
         }
-        w.trees.push_back(td);
+    });
+    // Top regions: every tree's rows at one depth together, trees in job order.
+    std::vector<std::vector<Task>> top_back[2], top_reach[2];
+    std::vector<Task> top_dec[2];
+    for (int p = 0; p < 2; p++) {
+        top_back[p].resize(top_levels);
+        top_reach[p].resize(top_levels);
+        for (size_t k = 0; k < J; k++) {
+            const JobLayout& L = lay[k];
+            for (size_t x = 0; x < L.top_back[p].size(); x++) top_back[p][L.top_back_d[p][x]].push_back(L.top_back[p][x]);
+            for (size_t x = 0; x < L.top_reach[p].size(); x++)
+                top_reach[p][L.top_reach_d[p][x]].push_back(L.top_reach[p][x]);
+            top_dec[p].insert(top_dec[p].end(), L.top_dec[p].begin(), L.top_dec[p].end());
+        }
     }
+    for (size_t k = 0; k < J; k++) w.max_vwin = std::max(w.max_vwin, lay[k].max_vwin);
     w.child_start.push_back((uint32_t)w.child.size());
     // Head width per 128-row tile of the network rows.
     const uint32_t nrows = w.rows();
     w.head_tile_n.assign((nrows + 127) / 128, 0);
-    for (uint32_t r = 0; r < nrows; r++)
-        for (uint32_t x = w.row_cfg_off[2 * r]; x < w.row_cfg_off[2 * r + 2]; x++) {
-            uint32_t& n = w.head_tile_n[r / 128];
-            n = std::max(n, w.cfg_key[w.row_cfg[x]] + 1);
-        }
-    for (int p = 0; p < 2; p++) {
-        w.head_rb_n[p].assign((nrows + 15) / 16, 0);
-        for (uint32_t r = 0; r < nrows; r++)
-            for (uint32_t x = w.row_cfg_off[2 * r + p]; x < w.row_cfg_off[2 * r + p + 1]; x++) {
-                uint32_t& n = w.head_rb_n[p][r / 16];
-                n = std::max(n, w.cfg_key[w.row_cfg[x]] + 1);
-            }
-    }
+    for (int p = 0; p < 2; p++) w.head_rb_n[p].assign((nrows + 15) / 16, 0);
+    parallel_for(w.head_tile_n.size(), [&](size_t tile) {  // one 128-row tile (eight 16-row blocks) each
+        const uint32_t r1 = std::min<uint32_t>(nrows, (uint32_t)tile * 128 + 128);
+        for (uint32_t r = (uint32_t)tile * 128; r < r1; r++)
+            for (int p = 0; p < 2; p++)
+                for (uint32_t x = w.row_cfg_off[2 * r + p]; x < w.row_cfg_off[2 * r + p + 1]; x++) {
+                    const uint32_t key = w.cfg_key[w.row_cfg[x]] + 1;
+                    w.head_tile_n[tile] = std::max(w.head_tile_n[tile], key);
+                    w.head_rb_n[p][r / 16] = std::max(w.head_rb_n[p][r / 16], key);
+                }
+    });
     // Pool groups: rows with the same config list (same tree, same
     // infostates in the same order), at most POOL_GROUP per group, in row
     // order within a list; longest lists launch first.
