@@ -411,7 +411,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
     struct Off {
         size_t node_meta, nc, legal_value, draw_to, draw_p, reach_base, vals_base, rev_src, rev_cell, rvd_src, rvd_p,
             row_node, row_cfg_off, row_cfg, cfg_emb, pub_raw, term_node, term_util, roots, carried, exit_node,
-            exit_coff, trees, units, bt[2], rt[2], dc[2], bl[2], rl[2], cv[2], lr[2], pg[2], twb[2], twu[2], cfg_priv,
+            exit_coff, exit_reach, trees, units, bt[2], rt[2], dc[2], bl[2], rl[2], cv[2], lr[2], pg[2], twb[2], twu[2], cfg_priv,
             unit_term, tb[2], tr[2], head_tile_n, cp[2], card_feat, row_job, cfg_job, cfg_owner;
     } o;
     o.node_meta = blob.put(w.node_meta);
@@ -441,6 +441,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
     o.carried = blob.put(w.carried);
     o.exit_node = blob.put(w.exit_node);
     o.exit_coff = blob.put(w.exit_coff);
+    o.exit_reach = blob.put(w.exit_reach);
     o.trees = blob.put(w.trees);
     o.units = blob.put(w.units);
     for (int p = 0; p < 2; p++) {
@@ -563,6 +564,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
     d.carried = (const float*)(T + o.carried);
     d.exit_node = (const uint32_t*)(T + o.exit_node);
     d.exit_coff = (const uint32_t*)(T + o.exit_coff);
+    d.exit_reach = (const uint32_t*)(T + o.exit_reach);
     d.trees = (const TreeDev*)(T + o.trees);
     d.units = (const UnitDev*)(T + o.units);
     for (int p = 0; p < 2; p++) {

@@ -37,7 +37,7 @@ struct WaveDev {
     const uint32_t* term_node;
     const float* term_util;
     const float *roots, *carried;
-    const uint32_t *exit_node, *exit_coff;
+    const uint32_t *exit_node, *exit_coff, *exit_reach;
     const TreeDev* trees;
     const UnitDev* units;
     const BackRec* back_rec[2];

@@ -335,6 +335,22 @@ __device__ __forceinline__ uint32_t lane_value(uint32_t v, uint32_t j) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)j);
 }
 
+// tot + v's lanes 0 .. m - 1 (m <= 64), added one at a time in lane order.
+// Eight lanes are read per step (independent reads ahead of the dependent
+// adds); the caller sets lanes m .. 63 to +0.0, and adding +0.0 leaves a sum
+// that started at +0.0 unchanged (such a sum is never -0.0), so the result is
+// the plain sequential sum.
+__device__ __forceinline__ float lane_sum_in_order(float tot, float v, uint32_t m) {
+    for (uint32_t k0 = 0; k0 < m; k0 += 8) {
+        float y[8];
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++) y[i] = lane_value(v, k0 + i);
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++) tot += y[i];
+    }
+    return tot;
+}
+
 // Float32 net: one wavefront per (network row, player). The leaf's reach
 // mass, and the pooled belief sum_c beta(c) e(c) with beta the normalised
 // reach (normalize_weights, engine/src/rebel.rs:1054-1068; accumulate,
@@ -364,8 +380,7 @@ __global__ __launch_bounds__(BLOCK) void k_pool_exact(WaveDev w, int player, flo
     float tot = 0.0f;
     for (uint32_t c0 = 0; c0 < n; c0 += 64) {
         float v = c0 + lane < n ? r[c0 + lane] : 0.0f;
-        uint32_t m = n - c0 < 64 ? n - c0 : 64;
-        for (uint32_t j = 0; j < m; j++) tot += lane_value(v, j);
+        tot = lane_sum_in_order(tot, v, n - c0 < 64 ? n - c0 : 64);
     }
     float scale, flat;
     if (tot > SMOOTHF) {
@@ -897,39 +912,50 @@ void launch_normalize(const WaveDev& w, int touched0, int touched1, hipStream_t 
 }
 
 // Normalised beliefs at every exit, f16 (the carry store, engine/src/gpu/client.rs:20-111).
-// One wavefront per (exit, player): lanes load 64 configs at a time and the
-// mass is summed in config order from the lanes' values.
-__global__ __launch_bounds__(BLOCK) void k_gather_carry(WaveDev w, const float* reach, int slot) {
-    const uint32_t task = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t e = task >> 1, p = task & 1;
-    if (e >= w.nexit) return;  // wave-uniform
-    const uint32_t node = w.exit_node[e];
-    const uint32_t n = w.nc[2 * node + p];
-    const float* r = reach + w.reach_base[2 * node + p];
-    float tot = 0.0f;
-    for (uint32_t c0 = 0; c0 < n; c0 += 64) {
-        const float v = c0 + lane < n ? r[c0 + lane] : 0.0f;
-        const uint32_t m = n - c0 < 64 ? n - c0 : 64;
-        for (uint32_t j = 0; j < m; j++) tot += lane_value(v, j);
+// One wavefront per CARRY_TASKS (exit, player) tasks, task 2 e + p: their
+// reach slots and carry offsets (one scalar load each), then their first 64
+// configs, are fetched together; each task's mass is summed in config order
+// from the lanes' values.
+constexpr uint32_t CARRY_TASKS = 1;
+__global__ __launch_bounds__(64) void k_gather_carry(WaveDev w, const float* reach, int slot) {
+    const uint32_t lane = threadIdx.x, task0 = blockIdx.x * CARRY_TASKS, ntask = 2 * w.nexit;
+    uint32_t rb[CARRY_TASKS], cb[CARRY_TASKS], n[CARRY_TASKS];
+    float v[CARRY_TASKS];
+#pragma unroll
+    for (uint32_t j = 0; j < CARRY_TASKS; j++) {
+        const uint32_t t = task0 + j;  // wave-uniform
+        rb[j] = t < ntask ? w.exit_reach[t] : 0;
+        cb[j] = t < ntask ? w.exit_coff[t] : 0;
+        n[j] = t < ntask ? w.exit_coff[t + 1] - cb[j] : 0;
     }
-    float scale, flat;
-    if (tot > SMOOTHF) {
-        scale = 1.0f / tot;
-        flat = 0.0f;
-    } else {
-        scale = 0.0f;
-        flat = 1.0f / (float)(n > 0 ? n : 1);
+#pragma unroll
+    for (uint32_t j = 0; j < CARRY_TASKS; j++) v[j] = lane < n[j] ? reach[rb[j] + lane] : 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < CARRY_TASKS; j++) {
+        const float* r = reach + rb[j];
+        float tot = 0.0f;
+        for (uint32_t c0 = 0; c0 < n[j]; c0 += 64) {
+            const float x = c0 ? (c0 + lane < n[j] ? r[c0 + lane] : 0.0f) : v[j];
+            tot = lane_sum_in_order(tot, x, n[j] - c0 < 64 ? n[j] - c0 : 64);
+        }
+        float scale, flat;
+        if (tot > SMOOTHF) {
+            scale = 1.0f / tot;
+            flat = 0.0f;
+        } else {
+            scale = 0.0f;
+            flat = 1.0f / (float)(n[j] > 0 ? n[j] : 1);
+        }
+        uint16_t* dst = w.carry + (size_t)slot * w.snapshot_configs + cb[j];
+        for (uint32_t c = lane; c < n[j]; c += 64) dst[c] = f32_to_f16_rn((c < 64 ? v[j] : r[c]) * scale + flat);
     }
-    uint16_t* dst = w.carry + (size_t)slot * w.snapshot_configs + w.exit_coff[2 * e + p];
-    for (uint32_t c = lane; c < n; c += 64) dst[c] = f32_to_f16_rn(r[c] * scale + flat);
 }
 
 void launch_gather_carry(const WaveDev& w, const float* reach, int slot, hipStream_t s) {
-    size_t waves = (size_t)w.nexit * 2;
-    // one wavefront per (exit, player), one per workgroup: a wavefront that
-    // finishes frees its slot at once
-    if (waves) hipLaunchKernelGGL(k_gather_carry, dim3((uint32_t)waves), dim3(64), 0, s, w, reach, slot);
+    const size_t tasks = (size_t)w.nexit * 2;
+    if (tasks)
+        hipLaunchKernelGGL(k_gather_carry, dim3((uint32_t)((tasks + CARRY_TASKS - 1) / CARRY_TASKS)), dim3(64), 0, s, w,
+                           reach, slot);
 }
 
 __global__ void k_collect_root(WaveDev w, int root, int p) {

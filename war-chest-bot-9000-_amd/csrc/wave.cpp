@@ -307,6 +307,12 @@ void build_records(WaveHost* wp) {
             }
         });
     }
+    // Each exit's reach slots, so the carry gather reads them in one load.
+    w.exit_reach.resize(2 * w.exit_node.size());
+    chunked(w.exit_node.size(), [&](size_t lo, size_t hi) {
+        for (size_t e = lo; e < hi; e++)
+            for (int p = 0; p < 2; p++) w.exit_reach[2 * e + p] = w.reach_base[2 * size_t(w.exit_node[e]) + p];
+    });
     // Network-leaf slots, unit by unit (the value sweep writes them first):
     // each unit's first slot from a prefix sum, then the units in parallel.
     const uint32_t heads = w.net.heads;
@@ -390,7 +396,7 @@ void build_records(WaveHost* wp) {
 
 }  // namespace
 
-constexpr size_t WAVE_HOST_BYTES = 2304;  // sizeof(WaveHost) on x86-64 (libstdc++)
+constexpr size_t WAVE_HOST_BYTES = 2328;  // sizeof(WaveHost) on x86-64 (libstdc++)
 static_assert(sizeof(WaveHost) == WAVE_HOST_BYTES, "a WaveHost member was added or changed: update reset()");
 void WaveHost::reset() {
     const WaveHost blank;
@@ -400,7 +406,7 @@ void WaveHost::reset() {
     for (auto* v : {&node_meta, &node_nc, &child_start, &child, &legal_row_of, &legal_off, &legal_value, &draw_off,
                     &draw_row_off, &draw_row_start, &draw_to, &reach_base, &vals_base, &parent, &rev_row_of,
                     &rev_start, &rev_src, &rev_cell, &rvd_row_of, &rvd_start, &rvd_src, &row_node, &row_cfg_off,
-                    &row_cfg, &cfg_key, &head_tile_n, &term_node, &exit_node, &exit_coff, &unit_row, &unit_term,
+                    &row_cfg, &cfg_key, &head_tile_n, &term_node, &exit_node, &exit_coff, &exit_reach, &unit_row, &unit_term,
                     &cfg_job, &row_job})
         keep(*v);
     for (auto* v : {&draw_p, &rvd_p, &cfg_emb, &cfg_priv, &term_util, &roots, &carried, &card_feat}) keep(*v);
@@ -1146,9 +1152,11 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         if (t >= N || (w.node_meta[t] & 3u) != 2) return fail("term_node");
     const uint64_t nexit = w.exit_node.size();
     if (w.exit_coff.size() != 2 * nexit + 1 || w.exit_coff.back() != w.snapshot_configs) return fail("exit_coff");
+    if (w.exit_reach.size() != 2 * nexit) return fail("exit_reach");
     for (uint64_t e = 0; e < nexit; e++)
         for (int p = 0; p < 2; p++)
-            if (w.exit_node[e] >= N || w.exit_coff[2 * e + p + 1] - w.exit_coff[2 * e + p] != w.nc(w.exit_node[e], p))
+            if (w.exit_node[e] >= N || w.exit_coff[2 * e + p + 1] - w.exit_coff[2 * e + p] != w.nc(w.exit_node[e], p) ||
+                w.exit_reach[2 * e + p] != w.reach_base[2 * size_t(w.exit_node[e]) + p])
                 return fail("exit configs");
     for (int p = 0; p < 2; p++) {
         if (first_fail(w.back_task[p].size(), [&](uint64_t k) {

@@ -196,6 +196,7 @@ struct WaveHost {
     std::vector<float> roots, carried;
     uint32_t root_values_len = 0;
     std::vector<uint32_t> exit_node, exit_coff;
+    std::vector<uint32_t> exit_reach;  // reach slot of each (exit, player): reach_base[2 * exit_node[e] + p]
     uint32_t snapshot_configs = 0;
 
     // Subtree units in descending size; lists are unit-major and level l of
