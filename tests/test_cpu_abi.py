@@ -76,6 +76,51 @@ def test_wave_counts_add_up():
     assert st["cfr_bytes_per_iter"][0] == sum(p["cfr_bytes_per_iter"][0] for p in parts)
 
 
+@pytest.mark.parametrize("family", ["wave256", "wave256v5"])
+def test_wave_lists_are_the_jobs_lists_shifted(family):
+    # The packer lays the jobs out in parallel and writes each at its offset
+    # into every wave list; the result must be the jobs' own lists (each job
+    # packed alone) appended in job order, every index shifted by the lists
+    # before it: nodes, children, cells, legal rows, reach and value slots,
+    # snapshot configs.
+    jobs = W.jobs(family, trees=9, nodes_lo=60, nodes_hi=400)
+    NONE = 0xFFFFFFFF
+    names = ("child_start", "child", "legal_off", "legal_value", "reach_base", "vals_base", "row_node",
+             "exit_node", "exit_coff")
+    whole = ww.Wave(jobs)
+    F = {k: whole.array(k).astype(np.int64) for k in names}
+    node0 = child0 = cell0 = lrow0 = row0 = exit0 = reach_at = vals_at = cfg_at = 0
+    for j in jobs:
+        one = ww.Wave([j])
+        S = {k: one.array(k).astype(np.int64) for k in names}
+        st = one.stats()
+        one.close()
+        n, kids, cells = len(S["child_start"]) - 1, len(S["child"]), len(S["legal_value"])
+        lrows, rows, exits = len(S["legal_off"]) - 1, len(S["row_node"]), len(S["exit_node"])
+        np.testing.assert_array_equal(F["child_start"][node0:node0 + n + 1], S["child_start"] + child0)
+        np.testing.assert_array_equal(F["child"][child0:child0 + kids], S["child"] + node0)
+        np.testing.assert_array_equal(F["legal_off"][lrow0:lrow0 + lrows + 1], S["legal_off"] + cell0)
+        np.testing.assert_array_equal(F["row_node"][row0:row0 + rows], S["row_node"] + node0)
+        np.testing.assert_array_equal(F["exit_node"][exit0:exit0 + exits], S["exit_node"] + node0)
+        ecfg0 = F["exit_coff"][2 * exit0]
+        assert ecfg0 == cfg_at
+        np.testing.assert_array_equal(F["exit_coff"][2 * exit0:2 * (exit0 + exits) + 1], S["exit_coff"] + ecfg0)
+        reach0 = F["reach_base"][2 * node0] - S["reach_base"][0]
+        assert reach0 == reach_at
+        np.testing.assert_array_equal(F["reach_base"][2 * node0:2 * (node0 + n)], S["reach_base"] + reach0)
+        vals0 = F["vals_base"][2 * node0] - S["vals_base"][0]
+        assert vals0 == vals_at
+        np.testing.assert_array_equal(F["vals_base"][2 * node0:2 * (node0 + n)], S["vals_base"] + vals0)
+        lv = S["legal_value"]
+        np.testing.assert_array_equal(F["legal_value"][cell0:cell0 + cells], np.where(lv == NONE, NONE, lv + vals0))
+        node0, child0, cell0, lrow0, row0, exit0 = node0 + n, child0 + kids, cell0 + cells, lrow0 + lrows, \
+            row0 + rows, exit0 + exits
+        reach_at, vals_at, cfg_at = reach_at + st["reach_len"], vals_at + st["vals_len"], \
+            cfg_at + st["snapshot_configs"]
+    assert node0 == len(F["child_start"]) - 1 and cell0 == len(F["legal_value"]) and row0 == len(F["row_node"])
+    whole.close()
+
+
 @pytest.mark.parametrize("budget", [256, 1024, None])
 def test_unit_windows_fit_the_budget(budget, monkeypatch):
     # A unit is a run of sibling subtrees; its value slots form one window no

@@ -912,50 +912,37 @@ void launch_normalize(const WaveDev& w, int touched0, int touched1, hipStream_t 
 }
 
 // Normalised beliefs at every exit, f16 (the carry store, engine/src/gpu/client.rs:20-111).
-// One wavefront per CARRY_TASKS (exit, player) tasks, task 2 e + p: their
-// reach slots and carry offsets (one scalar load each), then their first 64
-// configs, are fetched together; each task's mass is summed in config order
-// from the lanes' values.
-constexpr uint32_t CARRY_TASKS = 1;
+// One wavefront per (exit, player), task 2 e + p: its reach slot and carry
+// offsets (scalar loads), then 64 configs at a time; the mass is summed in
+// config order from the lanes' values.
 __global__ __launch_bounds__(64) void k_gather_carry(WaveDev w, const float* reach, int slot) {
-    const uint32_t lane = threadIdx.x, task0 = blockIdx.x * CARRY_TASKS, ntask = 2 * w.nexit;
-    uint32_t rb[CARRY_TASKS], cb[CARRY_TASKS], n[CARRY_TASKS];
-    float v[CARRY_TASKS];
-#pragma unroll
-    for (uint32_t j = 0; j < CARRY_TASKS; j++) {
-        const uint32_t t = task0 + j;  // wave-uniform
-        rb[j] = t < ntask ? w.exit_reach[t] : 0;
-        cb[j] = t < ntask ? w.exit_coff[t] : 0;
-        n[j] = t < ntask ? w.exit_coff[t + 1] - cb[j] : 0;
+    const uint32_t lane = threadIdx.x, t = blockIdx.x;
+    if (t >= 2 * w.nexit) return;  // wave-uniform
+    const float* r = reach + w.exit_reach[t];
+    const uint32_t cb = w.exit_coff[t], n = w.exit_coff[t + 1] - cb;
+    const float v0 = lane < n ? r[lane] : 0.0f;
+    float tot = 0.0f;
+    for (uint32_t c0 = 0; c0 < n; c0 += 64) {
+        const float x = c0 ? (c0 + lane < n ? r[c0 + lane] : 0.0f) : v0;
+        tot = lane_sum_in_order(tot, x, n - c0 < 64 ? n - c0 : 64);
     }
-#pragma unroll
-    for (uint32_t j = 0; j < CARRY_TASKS; j++) v[j] = lane < n[j] ? reach[rb[j] + lane] : 0.0f;
-#pragma unroll
-    for (uint32_t j = 0; j < CARRY_TASKS; j++) {
-        const float* r = reach + rb[j];
-        float tot = 0.0f;
-        for (uint32_t c0 = 0; c0 < n[j]; c0 += 64) {
-            const float x = c0 ? (c0 + lane < n[j] ? r[c0 + lane] : 0.0f) : v[j];
-            tot = lane_sum_in_order(tot, x, n[j] - c0 < 64 ? n[j] - c0 : 64);
-        }
-        float scale, flat;
-        if (tot > SMOOTHF) {
-            scale = 1.0f / tot;
-            flat = 0.0f;
-        } else {
-            scale = 0.0f;
-            flat = 1.0f / (float)(n[j] > 0 ? n[j] : 1);
-        }
-        uint16_t* dst = w.carry + (size_t)slot * w.snapshot_configs + cb[j];
-        for (uint32_t c = lane; c < n[j]; c += 64) dst[c] = f32_to_f16_rn((c < 64 ? v[j] : r[c]) * scale + flat);
+    float scale, flat;
+    if (tot > SMOOTHF) {
+        scale = 1.0f / tot;
+        flat = 0.0f;
+    } else {
+        scale = 0.0f;
+        flat = 1.0f / (float)(n > 0 ? n : 1);
     }
+    uint16_t* dst = w.carry + (size_t)slot * w.snapshot_configs + cb;
+    for (uint32_t c = lane; c < n; c += 64) dst[c] = f32_to_f16_rn((c < 64 ? v0 : r[c]) * scale + flat);
 }
 
 void launch_gather_carry(const WaveDev& w, const float* reach, int slot, hipStream_t s) {
     const size_t tasks = (size_t)w.nexit * 2;
-    if (tasks)
-        hipLaunchKernelGGL(k_gather_carry, dim3((uint32_t)((tasks + CARRY_TASKS - 1) / CARRY_TASKS)), dim3(64), 0, s, w,
-                           reach, slot);
+    // one wavefront per task, one per workgroup: a wavefront that finishes
+    // frees its slot at once
+    if (tasks) hipLaunchKernelGGL(k_gather_carry, dim3((uint32_t)tasks), dim3(64), 0, s, w, reach, slot);
 }
 
 __global__ void k_collect_root(WaveDev w, int root, int p) {
