@@ -593,6 +593,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
     }
     d.nunits = (uint32_t)w.units.size();
     d.max_vwin = w.max_vwin;
+    d.max_rwin = w.max_rwin;
     d.nsub = w.nsub;
     d.regret = (float*)(A + a_regret);
     d.cur = (float*)(A + a_cur);

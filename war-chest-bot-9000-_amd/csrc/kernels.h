@@ -56,6 +56,7 @@ struct WaveDev {
     // sizes
     uint32_t ntrees, nunits, nsub, rows, pool, in, row_bytes, snapshot_configs, nexit, ncells;
     uint32_t max_vwin;  // widest unit value window (floats)
+    uint32_t max_rwin;  // widest unit reach window (floats)
     uint32_t ndec[2];
     uint32_t npool[2];  // pool groups of each player
     uint32_t nleaf[2];  // network-leaf slots of each player (leaf_rec entries)

@@ -27,6 +27,7 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 constexpr int BLOCK = 256;
 // The subtree sweep stages a unit's values in LDS when the widest window fits this.
 constexpr size_t SWEEP_LDS_MAX = 64 * 1024;
+constexpr size_t REACH_LDS_MAX = 32 * 1024;  // the reach pass keeps a unit's reach window in LDS up to this
 
 static inline unsigned grid_for(size_t n, int block = BLOCK) { return (unsigned)((n + block - 1) / block); }
 
@@ -98,9 +99,14 @@ constexpr uint32_t REACH_BATCH = 8;  // reach gathers and average accumulation
 constexpr uint32_t LEAF_BATCH = 4;
 
 // One child config's reach: the reverse gather in stored order (the CPU's
-// scatter order, engine/src/serialize.rs:714-723).
-__device__ __forceinline__ void reach_row(const WaveDev& w, float* reach, const float* strat, ReachRec q) {
+// scatter order, engine/src/serialize.rs:714-723). With LDSR the unit's reach
+// window [rw, rw + rn) is also kept in LDS at lr: parent reach inside it is
+// read from there, and the row's result goes to both.
+template <bool LDSR = false>
+__device__ __forceinline__ void reach_row(const WaveDev& w, float* reach, const float* strat, ReachRec q,
+                                          float* lr = nullptr, uint32_t rw = 0, uint32_t rn = 0) {
     const uint32_t lo = q.start, n = q.kn & REC_N, base = q.pbase;
+    auto parent = [&](uint32_t i) { return LDSR && i - rw < rn ? lr[i - rw] : reach[i]; };
     float v = 0.0f;
     if ((q.kn >> 31) == REACH_REV) {
         for (uint32_t c0 = 0; c0 < n; c0 += REACH_BATCH) {
@@ -116,7 +122,7 @@ __device__ __forceinline__ void reach_row(const WaveDev& w, float* reach, const 
 #pragma unroll
             for (uint32_t k = 0; k < REACH_BATCH; k++)
                 if (k < m) {
-                    a[k] = reach[base + src[k]];
+                    a[k] = parent(base + src[k]);
                     b[k] = strat[cell[k]];
                 }
 #pragma unroll
@@ -136,13 +142,14 @@ __device__ __forceinline__ void reach_row(const WaveDev& w, float* reach, const 
                 }
 #pragma unroll
             for (uint32_t k = 0; k < REACH_BATCH; k++)
-                if (k < m) a[k] = reach[base + src[k]];
+                if (k < m) a[k] = parent(base + src[k]);
 #pragma unroll
             for (uint32_t k = 0; k < REACH_BATCH; k++)
                 if (k < m) v += a[k] * pr[k];
         }
     }
     reach[q.out] = v;
+    if (LDSR) lr[q.out - rw] = v;
 }
 
 // sum = sum * ds + reach * cur over one decision row: the DCFR discount of the
@@ -191,9 +198,15 @@ __device__ __forceinline__ void reach_unit(const WaveDev& w, const UnitDev& u, f
 }
 
 // One player's top-down reach of one unit, the next level's bounds and each
-// thread's first record of it fetched while the current level runs.
+// thread's first record of it fetched while the current level runs; with
+// LDSR the unit's reach window lives in LDS as well (every slot of it is
+// written by a level above the rows that read it).
+template <bool LDSR>
 __device__ __forceinline__ void reach_unit_one(const WaveDev& w, const UnitDev& u, float* reach, const float* strat,
-                                               int p) {
+                                               int p, float* lr) {
+    // The player's fields by select: indexing them with the run-time p would
+    // place the record in scratch memory.
+    const uint32_t rw = p ? u.rwin[1] : u.rwin[0], rn = p ? u.rwin_n[1] : u.rwin_n[0];
     const ReachRec* rec = w.reach_rec[p];
     const uint32_t* lvl = w.reach_lvl[p] + u.lvl0;
     const uint32_t L = u.nlevels, t = threadIdx.x;
@@ -218,7 +231,7 @@ __device__ __forceinline__ void reach_unit_one(const WaveDev& w, const UnitDev& 
                 qn = rec[kn];
             else if (more && b + t < e)
                 qn = rec[b + t];
-            reach_row(w, reach, strat, q);
+            reach_row<LDSR>(w, reach, strat, q, lr, rw, rn);
             q = qn;
             k = kn;
         }
@@ -226,19 +239,27 @@ __device__ __forceinline__ void reach_unit_one(const WaveDev& w, const UnitDev& 
     }
 }
 
-// Subtree units' reach, one unit per workgroup.
+// Subtree units' reach, one unit per workgroup (one player's with its reach
+// window in LDS when LDSR).
+template <bool LDSR>
 __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, float* reach, const float* strat,
                                                int player) {
+    extern __shared__ float lds_reach[];  // the unit's reach window of the player (when LDSR)
     const UnitDev u = w.units[unit0 + blockIdx.x];
     if (player < 0)
         reach_unit(w, u, reach, strat, player);
     else
-        reach_unit_one(w, u, reach, strat, player);
+        reach_unit_one<LDSR>(w, u, reach, strat, player, lds_reach);
 }
 
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
                   hipStream_t s) {
-    if (n) hipLaunchKernelGGL(k_reach, dim3(n), dim3(BLOCK), 0, s, w, unit0, reach, strat, player);
+    if (!n) return;
+    const size_t lds = (size_t)w.max_rwin * sizeof(float);
+    if (player >= 0 && lds <= REACH_LDS_MAX)
+        hipLaunchKernelGGL(k_reach<true>, dim3(n), dim3(BLOCK), lds, s, w, unit0, reach, strat, player);
+    else
+        hipLaunchKernelGGL(k_reach<false>, dim3(n), dim3(BLOCK), 0, s, w, unit0, reach, strat, player);
 }
 
 // The average-strategy accumulation of player `acc` over all its decision rows

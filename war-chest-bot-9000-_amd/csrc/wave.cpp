@@ -104,7 +104,7 @@ struct JobLayout {
     uint32_t top_depths = 0;               // 1 + the deepest top node's depth (0: no top region)
     uint32_t lvls = 0, max_levels = 0, nback[2] = {0, 0}, nreach[2] = {0, 0}, ndec[2] = {0, 0};
     uint32_t nrow = 0, nterm = 0;
-    uint32_t max_vwin = 0;                 // filled with the unit records
+    uint32_t max_vwin = 0, max_rwin = 0;   // filled with the unit records
     std::vector<Task> top_back[2], top_reach[2], top_dec[2];
     std::vector<uint32_t> top_back_d[2], top_reach_d[2];  // depth of each top task
     std::string err;
@@ -396,7 +396,7 @@ void build_records(WaveHost* wp) {
 
 }  // namespace
 
-constexpr size_t WAVE_HOST_BYTES = 2328;  // sizeof(WaveHost) on x86-64 (libstdc++)
+constexpr size_t WAVE_HOST_BYTES = 2336;  // sizeof(WaveHost) on x86-64 (libstdc++)
 static_assert(sizeof(WaveHost) == WAVE_HOST_BYTES, "a WaveHost member was added or changed: update reset()");
 void WaveHost::reset() {
     const WaveHost blank;
@@ -451,6 +451,7 @@ void WaveHost::reset() {
     nroots_max = blank.nroots_max;
     carry_slots = blank.carry_slots;
     max_vwin = blank.max_vwin;
+    max_rwin = blank.max_rwin;
     tower_len = blank.tower_len;
 }
 
@@ -657,19 +658,28 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
         std::copy(t.draw_to.begin(), t.draw_to.end(), w.draw_to.begin() + a.draw);
         std::copy(t.draw_p.begin(), t.draw_p.end(), w.draw_p.begin() + a.draw);
 
-        // Reach slots in BFS order; a player who did not act at the parent
-        // keeps the parent's vector (engine/src/gpu/wave.rs:358-374).
+        // Reach slots: a player who did not act at the parent keeps the
+        // parent's vector, every other node gets its own (the slots of
+        // engine/src/gpu/wave.rs:358-374). They are handed out to the top
+        // region's nodes in BFS order, then unit by unit (below), each unit's
+        // nodes level by level, player 0's before player 1's: every unit owns
+        // one contiguous run of each player's slots, its reach window.
         uint32_t reach_at = a.reach;
-        for (uint32_t local : t.bfs_order) {
+        auto own_reach = [&](uint32_t local, int p) {
             const uint32_t node = node0 + local;
-            for (int p = 0; p < 2; p++) {
-                if (local == 0 || t.node_player[t.node_parent[local]] == p) {
-                    w.reach_base[2 * size_t(node) + p] = reach_at;
-                    reach_at += t.nc(local, p);
-                } else {
-                    w.reach_base[2 * size_t(node) + p] = w.reach_base[2 * size_t(node0 + t.node_parent[local]) + p];
-                }
+            if (local == 0 || t.node_player[t.node_parent[local]] == p) {
+                w.reach_base[2 * size_t(node) + p] = reach_at;
+                reach_at += t.nc(local, p);
+            } else {
+                w.reach_base[2 * size_t(node) + p] = w.reach_base[2 * size_t(node0 + t.node_parent[local]) + p];
             }
+        };
+        if (!L.top.empty()) {
+            std::vector<uint8_t> is_top(N, 0);
+            for (uint32_t i : L.top) is_top[i] = 1;
+            for (uint32_t local : t.bfs_order)
+                if (is_top[local])
+                    for (int p = 0; p < 2; p++) own_reach(local, p);
         }
         for (uint32_t i = 0; i < N; i++)
             for (int p = 0; p < 2; p++) w.vals_base[2 * size_t(node0 + i) + p] = a.vals + L.vb[p][i];
@@ -766,6 +776,16 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             lvl += nl + 1;
             by_level.assign(nl, {});
             for (uint32_t x = b; x < e; x++) by_level[L.depth[L.unit_nodes[x]] - d0].push_back(L.unit_nodes[x]);
+            for (int p = 0; p < 2; p++) {  // the unit's reach window of each player
+                // The tree's root (seeded, written by no row) stays outside it.
+                if (d0 == 0 && !by_level.empty() && by_level[0].size() == 1 && by_level[0][0] == 0) own_reach(0, p);
+                u.rwin[p] = reach_at;
+                for (uint32_t l = 0; l < nl; l++)
+                    for (uint32_t local : by_level[l])
+                        if (local != 0) own_reach(local, p);
+                u.rwin_n[p] = reach_at - u.rwin[p];
+                L.max_rwin = std::max(L.max_rwin, u.rwin_n[p]);
+            }
             uint64_t slots = 0;
             for (uint32_t x = b; x < e; x++)
                 slots += std::max(t.nc(L.unit_nodes[x], 0), t.nc(L.unit_nodes[x], 1));
@@ -817,6 +837,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             u.term1 = uterm;
             sub_units[a.unit + j] = u;
         }
+        if (reach_at != a.reach + L.reach_len) L.err = "reach slots: the units and top region do not cover the tree";
         // This tree's top region, by depth (joined with the other trees' below).
         for (uint32_t local : L.top) {
             const uint32_t node = node0 + local, d = L.depth[local];
@@ -838,6 +859,11 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             }
         }
     });
+    for (size_t k = 0; k < J; k++)
+        if (!lay[k].err.empty()) {
+            *err = lay[k].err;
+            return false;
+        }
     // Top regions: every tree's rows at one depth together, trees in job order.
     std::vector<std::vector<Task>> top_back[2], top_reach[2];
     std::vector<Task> top_dec[2];
@@ -852,7 +878,10 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
             top_dec[p].insert(top_dec[p].end(), L.top_dec[p].begin(), L.top_dec[p].end());
         }
     }
-    for (size_t k = 0; k < J; k++) w.max_vwin = std::max(w.max_vwin, lay[k].max_vwin);
+    for (size_t k = 0; k < J; k++) {
+        w.max_vwin = std::max(w.max_vwin, lay[k].max_vwin);
+        w.max_rwin = std::max(w.max_rwin, lay[k].max_rwin);
+    }
     w.child_start.push_back((uint32_t)w.child.size());
     // Head width per 128-row tile of the network rows.
     const uint32_t nrows = w.rows();
@@ -1301,6 +1330,28 @@ bool validate_deep(const WaveHost& w, std::string* err) {
     auto unit_check = [&](uint64_t ui) -> const char* {
         const UnitDev& u = w.units[ui];
         for (int p = 0; p < 2; p++) {
+            // The reach window: the unit's rows write inside it, and a row reads
+            // a slot inside it only once a shallower level has written it.
+            const uint64_t rlo = u.rwin[p], rn = u.rwin_n[p];
+            if (rlo + rn > w.reach_len) return "unit reach window";
+            std::vector<uint8_t> written(rn, 0);
+            for (uint32_t l = 0; l < u.nlevels; l++) {
+                const uint32_t b = w.reach_lvl[p][u.lvl0 + l], e = w.reach_lvl[p][u.lvl0 + l + 1];
+                for (uint32_t x = b; x < e; x++) {
+                    const ReachRec& r = w.reach_rec[p][x];
+                    const uint32_t n = r.kn & REC_N;
+                    for (uint32_t k = 0; k < n; k++) {
+                        const uint64_t i = uint64_t(r.pbase) +
+                                           ((r.kn >> 31) == REACH_REV ? w.rev_src[r.start + k] : w.rvd_src[r.start + k]);
+                        if (i - rlo < rn && !written[i - rlo]) return "unit reach row reads an unwritten window slot";
+                    }
+                }
+                for (uint32_t x = b; x < e; x++) {
+                    const uint64_t o = w.reach_rec[p][x].out;
+                    if (o - rlo >= rn) return "unit reach row writes outside its reach window";
+                    written[o - rlo] = 1;
+                }
+            }
             const uint64_t lo = u.vwin[p], hi = lo + u.vwin_n[p];
             auto in = [&](uint64_t i) { return i >= lo && i < hi; };
             if (u.leaf0[p] > u.leaf1[p] || u.leaf1[p] > w.leaf_rec[p].size()) return "unit leaf range";

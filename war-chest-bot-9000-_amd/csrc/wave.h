@@ -80,8 +80,9 @@ struct UnitDev {
     uint32_t tree;              // owning tree
     uint32_t vwin[2], vwin_n[2];  // the unit's value slots of each player: [vwin, vwin + vwin_n)
     uint32_t leaf0[2], leaf1[2];  // network-leaf value slots of each player: leaf_rec[p][leaf0 .. leaf1)
+    uint32_t rwin[2], rwin_n[2];  // the unit's own reach slots of each player: [rwin, rwin + rwin_n)
 };
-static_assert(sizeof(UnitDev) == 20 * 4, "UnitDev is 80 bytes");
+static_assert(sizeof(UnitDev) == 24 * 4, "UnitDev is 96 bytes");
 
 // One network-leaf value slot of the traverser: vals[out] = head_out[head] * mass[mass]
 // (the net's value of the slot's config times the opponent's reach mass);
@@ -218,6 +219,7 @@ struct WaveHost {
 
     uint32_t max_levels = 0, nroots_max = 0, carry_slots = 0;
     uint32_t max_vwin = 0;  // the widest unit value window (floats): the sweep's LDS size
+    uint32_t max_rwin = 0;  // the widest unit reach window (floats): the reach pass's LDS size
 
     // Device row records, index-aligned with the task lists above.
     std::vector<BackRec> back_rec[2], top_back_rec[2];
