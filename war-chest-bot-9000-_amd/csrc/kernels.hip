@@ -174,24 +174,21 @@ __device__ __forceinline__ void accumulate_row(const WaveDev& w, AccRec q, float
     }
 }
 
-// Top-down reach of one unit, level by level under block barriers: player p
-// alone, or both players (p < 0) whose task lists of a level are independent.
-__device__ __forceinline__ void reach_unit(const WaveDev& w, const UnitDev& u, float* reach, const float* strat,
-                                           int p) {
+// Both players' top-down reach of one unit, level by level under block
+// barriers (their rows of a level are independent); with LDSR each player's
+// reach window lives in LDS as well, player 0's at lr, player 1's at lr + stride.
+template <bool LDSR>
+__device__ __forceinline__ void reach_unit_both(const WaveDev& w, const UnitDev& u, float* reach, const float* strat,
+                                                float* lr, uint32_t stride) {
     for (uint32_t l = 0; l < u.nlevels; l++) {
-        if (p < 0) {
-            uint32_t b0 = w.reach_lvl[0][u.lvl0 + l], e0 = w.reach_lvl[0][u.lvl0 + l + 1];
-            uint32_t b1 = w.reach_lvl[1][u.lvl0 + l], e1 = w.reach_lvl[1][u.lvl0 + l + 1];
-            uint32_t n0 = e0 - b0, n = n0 + (e1 - b1);
-            for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
-                if (k < n0)
-                    reach_row(w, reach, strat, w.reach_rec[0][b0 + k]);
-                else
-                    reach_row(w, reach, strat, w.reach_rec[1][b1 + k - n0]);
-            }
-        } else {
-            uint32_t b = w.reach_lvl[p][u.lvl0 + l], e = w.reach_lvl[p][u.lvl0 + l + 1];
-            for (uint32_t k = b + threadIdx.x; k < e; k += blockDim.x) reach_row(w, reach, strat, w.reach_rec[p][k]);
+        uint32_t b0 = w.reach_lvl[0][u.lvl0 + l], e0 = w.reach_lvl[0][u.lvl0 + l + 1];
+        uint32_t b1 = w.reach_lvl[1][u.lvl0 + l], e1 = w.reach_lvl[1][u.lvl0 + l + 1];
+        uint32_t n0 = e0 - b0, n = n0 + (e1 - b1);
+        for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
+            if (k < n0)
+                reach_row<LDSR>(w, reach, strat, w.reach_rec[0][b0 + k], lr, u.rwin[0], u.rwin_n[0]);
+            else
+                reach_row<LDSR>(w, reach, strat, w.reach_rec[1][b1 + k - n0], lr + stride, u.rwin[1], u.rwin_n[1]);
         }
         __syncthreads();
     }
@@ -244,10 +241,10 @@ __device__ __forceinline__ void reach_unit_one(const WaveDev& w, const UnitDev& 
 template <bool LDSR>
 __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, float* reach, const float* strat,
                                                int player) {
-    extern __shared__ float lds_reach[];  // the unit's reach window of the player (when LDSR)
+    extern __shared__ float lds_reach[];  // the unit's reach window of each player handled (when LDSR)
     const UnitDev u = w.units[unit0 + blockIdx.x];
     if (player < 0)
-        reach_unit(w, u, reach, strat, player);
+        reach_unit_both<LDSR>(w, u, reach, strat, lds_reach, w.max_rwin);
     else
         reach_unit_one<LDSR>(w, u, reach, strat, player, lds_reach);
 }
@@ -255,8 +252,8 @@ __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, floa
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
                   hipStream_t s) {
     if (!n) return;
-    const size_t lds = (size_t)w.max_rwin * sizeof(float);
-    if (player >= 0 && lds <= REACH_LDS_MAX)
+    const size_t lds = (size_t)w.max_rwin * sizeof(float) * (player < 0 ? 2 : 1);
+    if (lds <= REACH_LDS_MAX)
         hipLaunchKernelGGL(k_reach<true>, dim3(n), dim3(BLOCK), lds, s, w, unit0, reach, strat, player);
     else
         hipLaunchKernelGGL(k_reach<false>, dim3(n), dim3(BLOCK), 0, s, w, unit0, reach, strat, player);
