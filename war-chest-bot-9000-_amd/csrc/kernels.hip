@@ -252,8 +252,10 @@ __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, floa
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
                   hipStream_t s) {
     if (!n) return;
-    const size_t lds = (size_t)w.max_rwin * sizeof(float) * (player < 0 ? 2 : 1);
-    if (lds <= REACH_LDS_MAX)
+    // Both players' windows (32 KB at the default unit budget) would leave room
+    // for five workgroups per CU instead of eight: that pass reads from L2.
+    const size_t lds = (size_t)w.max_rwin * sizeof(float);
+    if (player >= 0 && lds <= REACH_LDS_MAX)
         hipLaunchKernelGGL(k_reach<true>, dim3(n), dim3(BLOCK), lds, s, w, unit0, reach, strat, player);
     else
         hipLaunchKernelGGL(k_reach<false>, dim3(n), dim3(BLOCK), 0, s, w, unit0, reach, strat, player);
