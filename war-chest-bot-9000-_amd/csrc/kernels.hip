@@ -175,20 +175,20 @@ __device__ __forceinline__ void accumulate_row(const WaveDev& w, AccRec q, float
 }
 
 // Both players' top-down reach of one unit, level by level under block
-// barriers (their rows of a level are independent); with LDSR each player's
-// reach window lives in LDS as well, player 0's at lr, player 1's at lr + stride.
-template <bool LDSR>
-__device__ __forceinline__ void reach_unit_both(const WaveDev& w, const UnitDev& u, float* reach, const float* strat,
-                                                float* lr, uint32_t stride) {
+// barriers (their rows of a level are independent), parents read from L2:
+// both players' reach windows in LDS (32 KB at the default unit budget) would
+// leave room for five workgroups per CU instead of eight (88.6 against 76.4 µs
+// per launch).
+__device__ __forceinline__ void reach_unit_both(const WaveDev& w, const UnitDev& u, float* reach, const float* strat) {
     for (uint32_t l = 0; l < u.nlevels; l++) {
         uint32_t b0 = w.reach_lvl[0][u.lvl0 + l], e0 = w.reach_lvl[0][u.lvl0 + l + 1];
         uint32_t b1 = w.reach_lvl[1][u.lvl0 + l], e1 = w.reach_lvl[1][u.lvl0 + l + 1];
         uint32_t n0 = e0 - b0, n = n0 + (e1 - b1);
         for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
             if (k < n0)
-                reach_row<LDSR>(w, reach, strat, w.reach_rec[0][b0 + k], lr, u.rwin[0], u.rwin_n[0]);
+                reach_row(w, reach, strat, w.reach_rec[0][b0 + k]);
             else
-                reach_row<LDSR>(w, reach, strat, w.reach_rec[1][b1 + k - n0], lr + stride, u.rwin[1], u.rwin_n[1]);
+                reach_row(w, reach, strat, w.reach_rec[1][b1 + k - n0]);
         }
         __syncthreads();
     }
@@ -236,15 +236,15 @@ __device__ __forceinline__ void reach_unit_one(const WaveDev& w, const UnitDev& 
     }
 }
 
-// Subtree units' reach, one unit per workgroup (one player's with its reach
-// window in LDS when LDSR).
+// Subtree units' reach, one unit per workgroup: one player's with its reach
+// window in LDS when LDSR, or both players' (player < 0) from L2.
 template <bool LDSR>
 __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, float* reach, const float* strat,
                                                int player) {
-    extern __shared__ float lds_reach[];  // the unit's reach window of each player handled (when LDSR)
+    extern __shared__ float lds_reach[];  // the unit's reach window of the player (when LDSR)
     const UnitDev u = w.units[unit0 + blockIdx.x];
     if (player < 0)
-        reach_unit_both<LDSR>(w, u, reach, strat, lds_reach, w.max_rwin);
+        reach_unit_both(w, u, reach, strat);
     else
         reach_unit_one<LDSR>(w, u, reach, strat, player, lds_reach);
 }
@@ -252,8 +252,6 @@ __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, floa
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
                   hipStream_t s) {
     if (!n) return;
-    // Both players' windows (32 KB at the default unit budget) would leave room
-    // for five workgroups per CU instead of eight: that pass reads from L2.
     const size_t lds = (size_t)w.max_rwin * sizeof(float);
     if (player >= 0 && lds <= REACH_LDS_MAX)
         hipLaunchKernelGGL(k_reach<true>, dim3(n), dim3(BLOCK), lds, s, w, unit0, reach, strat, player);

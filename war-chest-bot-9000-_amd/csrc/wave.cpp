@@ -888,14 +888,21 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     w.head_tile_n.assign((nrows + 127) / 128, 0);
     for (int p = 0; p < 2; p++) w.head_rb_n[p].assign((nrows + 15) / 16, 0);
     parallel_for(w.head_tile_n.size(), [&](size_t tile) {  // one 128-row tile (eight 16-row blocks) each
-        const uint32_t r1 = std::min<uint32_t>(nrows, (uint32_t)tile * 128 + 128);
-        for (uint32_t r = (uint32_t)tile * 128; r < r1; r++)
-            for (int p = 0; p < 2; p++)
-                for (uint32_t x = w.row_cfg_off[2 * r + p]; x < w.row_cfg_off[2 * r + p + 1]; x++) {
-                    const uint32_t key = w.cfg_key[w.row_cfg[x]] + 1;
-                    w.head_tile_n[tile] = std::max(w.head_tile_n[tile], key);
-                    w.head_rb_n[p][r / 16] = std::max(w.head_rb_n[p][r / 16], key);
-                }
+        const uint32_t r0 = (uint32_t)tile * 128, r1 = std::min<uint32_t>(nrows, r0 + 128);
+        uint32_t rb[2][8] = {};  // the tile's blocks, kept local (neighbouring tiles share cache lines)
+        for (uint32_t r = r0; r < r1; r++)
+            for (int p = 0; p < 2; p++) {
+                uint32_t& m = rb[p][(r - r0) / 16];
+                for (uint32_t x = w.row_cfg_off[2 * r + p]; x < w.row_cfg_off[2 * r + p + 1]; x++)
+                    m = std::max(m, w.cfg_key[w.row_cfg[x]] + 1);
+            }
+        uint32_t t = 0;
+        for (uint32_t b = 0; r0 + 16 * b < r1; b++)
+            for (int p = 0; p < 2; p++) {
+                w.head_rb_n[p][r0 / 16 + b] = rb[p][b];
+                t = std::max(t, rb[p][b]);
+            }
+        w.head_tile_n[tile] = t;
     });
     // Pool groups: rows with the same config list (same tree, same
     // infostates in the same order), at most POOL_GROUP per group, in row
