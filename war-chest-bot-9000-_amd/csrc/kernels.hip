@@ -914,7 +914,30 @@ __global__ void k_normalize(WaveDev w, int touched0, int touched1) {
     int p;
     AccRec q = decision_row(w, i, &p);
     uint32_t lo = q.lo, hi = q.lo + q.n;
-    if (!(p ? touched1 : touched0)) {
+    const bool touched = p ? touched1 : touched0;
+    if (q.n <= ROW_BATCH) {  // the row's loads issued together, then the same sum and quotients
+        const float* src = touched ? w.sum : w.cur;
+        float x[ROW_BATCH];
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < q.n) x[k] = src[lo + k];
+        if (!touched) {
+#pragma unroll
+            for (uint32_t k = 0; k < ROW_BATCH; k++)
+                if (k < q.n) w.snap[lo + k] = x[k];
+            return;
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < q.n) s += x[k];
+        const float u = 1.0f / (float)(q.n ? q.n : 1);
+#pragma unroll
+        for (uint32_t k = 0; k < ROW_BATCH; k++)
+            if (k < q.n) w.snap[lo + k] = s > 0.0f ? x[k] / s : u;
+        return;
+    }
+    if (!touched) {
         for (uint32_t g = lo; g < hi; g++) w.snap[g] = w.cur[g];
         return;
     }
