@@ -661,6 +661,20 @@ __device__ __forceinline__ float row16_sum(float x) {
     x += dpp_mov<0x140>(x);  // row_mirror: lane i <-> 15 - i
     return x;
 }
+// row16_sum of N independent values, step by step across them: a DPP step
+// that reads the previous step's result needs two wait states, which the
+// other values' steps fill instead of s_nop. The same sums, bit for bit.
+template <int N>
+__device__ __forceinline__ void row16_sum_n(float (&x)[N]) {
+#pragma unroll
+    for (int k = 0; k < N; k++) x[k] += dpp_mov<0xB1>(x[k]);
+#pragma unroll
+    for (int k = 0; k < N; k++) x[k] += dpp_mov<0x4E>(x[k]);
+#pragma unroll
+    for (int k = 0; k < N; k++) x[k] += dpp_mov<0x141>(x[k]);
+#pragma unroll
+    for (int k = 0; k < N; k++) x[k] += dpp_mov<0x140>(x[k]);
+}
 
 constexpr int JT_ROWS = 32;          // rows per join workgroup
 constexpr int JT_WAVES = 8;          // wavefront w owns columns 16 w .. 16 w + 15 of the 128-wide stream
@@ -694,28 +708,39 @@ __global__ __launch_bounds__(JT_WAVES * 64) void k_join_mfma(Net net, uint32_t r
     auto row_stats = [&](auto& z, auto ncb, float width) {
         constexpr uint32_t NC = decltype(ncb)::value;
         constexpr float NW = 16.0f * NC;  // columns per wavefront
+        float sw[JT_RB * 4], dw[JT_RB * 4];  // the rows' sums, then squared deviations (rb, v)
 #pragma unroll
         for (uint32_t rb = 0; rb < JT_RB; rb++)
 #pragma unroll
             for (uint32_t v = 0; v < 4; v++) {
-                const uint32_t r = rb * 16 + 4 * q + v;
                 float sacc = 0.0f;
 #pragma unroll
                 for (uint32_t cb = 0; cb < NC; cb++) sacc += z[rb][cb][v];
-                sacc = row16_sum(sacc);
-                const float mw = sacc * (1.0f / NW);
+                sw[rb * 4 + v] = sacc;
+            }
+        row16_sum_n(sw);
+#pragma unroll
+        for (uint32_t rb = 0; rb < JT_RB; rb++)
+#pragma unroll
+            for (uint32_t v = 0; v < 4; v++) {
+                const float mw = sw[rb * 4 + v] * (1.0f / NW);
                 float dacc = 0.0f;
 #pragma unroll
                 for (uint32_t cb = 0; cb < NC; cb++) {
                     const float d = z[rb][cb][v] - mw;
                     dacc += d * d;
                 }
-                dacc = row16_sum(dacc);
-                if (i == 0) {
-                    part[wv][r] = sacc;
-                    part2[wv][r] = dacc;
-                }
+                dw[rb * 4 + v] = dacc;
             }
+        row16_sum_n(dw);
+#pragma unroll
+        for (uint32_t rb = 0; rb < JT_RB; rb++)
+#pragma unroll
+            for (uint32_t v = 0; v < 4; v++)
+                if (i == 0) {
+                    part[wv][rb * 16 + 4 * q + v] = sw[rb * 4 + v];
+                    part2[wv][rb * 16 + 4 * q + v] = dw[rb * 4 + v];
+                }
         __syncthreads();
         if (threadIdx.x < JT_ROWS) {
             float t = 0.0f;
