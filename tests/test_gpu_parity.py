@@ -126,6 +126,38 @@ def test_unit_budget_is_invisible():
             np.testing.assert_array_equal(x.carries, y.carries)
 
 
+def test_unit_windows_in_hbm_are_invisible():
+    """The sweep and reach passes keep a unit's value and reach windows in LDS when
+    they fit, else work on HBM alone (WC_UNIT_LDS=0 forces that path): the same
+    results bit for bit."""
+    import os
+    jobs = small_wave(trees=5, seed=23, nodes_lo=60, nodes_hi=120)
+    net = W.net_for("wave256")
+    say("case unit windows: the same wave with the windows in LDS and in HBM only")
+    lds = gpu_solve(jobs, net, ww.WC_PRECISE)
+    old = os.environ.get("WC_UNIT_LDS")
+    os.environ["WC_UNIT_LDS"] = "0"
+    try:
+        ex = ww.Executor(0, ww.WC_PRECISE)  # reads the switch at creation
+        try:
+            wave = ww.Wave(jobs)
+            hbm = ex.solve(wave, ex.publish(net))
+            wave.close()
+        finally:
+            ex.close()
+    finally:
+        if old is None:
+            del os.environ["WC_UNIT_LDS"]
+        else:
+            os.environ["WC_UNIT_LDS"] = old
+    for k, (x, y) in enumerate(zip(lds, hbm)):
+        np.testing.assert_array_equal(x.strategy, y.strategy, err_msg=f"tree {k}")
+        np.testing.assert_array_equal(x.root_values, y.root_values, err_msg=f"tree {k}")
+        np.testing.assert_array_equal(x.carries, y.carries, err_msg=f"tree {k}")
+    for k, (j, g) in enumerate(zip(jobs, hbm)):
+        assert_bit_exact(g, O.solve(j, net, O.NET_F32), f"tree {k} (HBM windows)")
+
+
 def test_wave_composition_is_invariant():
     jobs = small_wave(trees=6, seed=21)
     net = W.net_for("wave256")

@@ -103,6 +103,7 @@ Executor::Executor(int device, int precision) : device_(device), precision_(prec
     if (!noalloc_scratch(device, &scratch_, &scratch_err_)) scratch_ = nullptr;
     if (const char* env = std::getenv("WC_CHAIN_SPLIT")) split_ = std::strcmp(env, "0") != 0;
     if (const char* env = std::getenv("WC_GRAPH")) graph_ = std::strcmp(env, "1") == 0;
+    if (const char* env = std::getenv("WC_UNIT_LDS")) unit_lds_ = std::strcmp(env, "0") != 0;
     if (const char* env = std::getenv("WC_V5_SCALAR")) v5_scalar_ = std::strcmp(env, "1") == 0;
     ok_ = true;
 }
@@ -594,6 +595,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
     d.nunits = (uint32_t)w.units.size();
     d.max_vwin = w.max_vwin;
     d.max_rwin = w.max_rwin;
+    d.unit_lds = unit_lds_ ? 1u : 0u;
     d.nsub = w.nsub;
     d.regret = (float*)(A + a_regret);
     d.cur = (float*)(A + a_cur);

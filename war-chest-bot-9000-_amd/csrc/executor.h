@@ -232,6 +232,9 @@ class Executor {
     std::string scratch_err_;
     bool split_ = true;  // WC_CHAIN_SPLIT=0 turns the first layer's fixed-column product off
     bool graph_ = false; // WC_GRAPH=1: each wave's schedule runs as one captured HIP graph
+    // WC_UNIT_LDS=0: the sweep and reach passes read and write unit windows in
+    // HBM only (the paths taken when a window does not fit LDS)
+    bool unit_lds_ = true;
     // WC_V5_SCALAR=1: the v5 network's 16-bit path without the matrix cores
     // (rounded operands, float32 sums in ascending order)
     bool v5_scalar_ = false;

@@ -57,6 +57,7 @@ struct WaveDev {
     uint32_t ntrees, nunits, nsub, rows, pool, in, row_bytes, snapshot_configs, nexit, ncells;
     uint32_t max_vwin;  // widest unit value window (floats)
     uint32_t max_rwin;  // widest unit reach window (floats)
+    uint32_t unit_lds;  // 1: the sweep and reach passes keep unit windows in LDS when they fit
     uint32_t ndec[2];
     uint32_t npool[2];  // pool groups of each player
     uint32_t nleaf[2];  // network-leaf slots of each player (leaf_rec entries)

@@ -253,7 +253,7 @@ void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, co
                   hipStream_t s) {
     if (!n) return;
     const size_t lds = (size_t)w.max_rwin * sizeof(float);
-    if (player >= 0 && lds <= REACH_LDS_MAX)
+    if (player >= 0 && w.unit_lds && lds <= REACH_LDS_MAX)
         hipLaunchKernelGGL(k_reach<true>, dim3(n), dim3(BLOCK), lds, s, w, unit0, reach, strat, player);
     else
         hipLaunchKernelGGL(k_reach<false>, dim3(n), dim3(BLOCK), 0, s, w, unit0, reach, strat, player);
@@ -868,7 +868,7 @@ void launch_sweep(const WaveDev& w, uint32_t unit0, uint32_t n, const float* hea
                   int mode, float da, float db, float predict, hipStream_t s) {
     if (!n) return;
     const size_t lds = (size_t)w.max_vwin * sizeof(float);
-    const bool staged = lds <= SWEEP_LDS_MAX;
+    const bool staged = w.unit_lds && lds <= SWEEP_LDS_MAX;
 #define WC_SWEEP(M, L)                                                                                          \
     hipLaunchKernelGGL((k_sweep<M, L>), dim3(n), dim3(BLOCK), L ? lds : 0, s, w, unit0, head_out, heads, traverser, \
                        da, db, predict)
