@@ -236,12 +236,18 @@ __device__ __forceinline__ void reach_unit_one(const WaveDev& w, const UnitDev& 
     }
 }
 
-// Subtree units' reach, one unit per workgroup: one player's with its reach
-// window in LDS when LDSR, or both players' (player < 0) from L2.
+// Subtree units' reach: one player's, one unit per workgroup with its reach
+// window in LDS when LDSR; both players' (player < 0) either as one
+// workgroup per (unit, player), windows in LDS, or one per unit from L2.
 template <bool LDSR>
 __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, float* reach, const float* strat,
                                                int player) {
     extern __shared__ float lds_reach[];  // the unit's reach window of the player (when LDSR)
+    if (LDSR && player < 0) {  // the players' rows are independent: workgroup 2 u + p
+        const UnitDev u = w.units[unit0 + blockIdx.x / 2];
+        reach_unit_one<true>(w, u, reach, strat, (int)(blockIdx.x & 1), lds_reach);
+        return;
+    }
     const UnitDev u = w.units[unit0 + blockIdx.x];
     if (player < 0)
         reach_unit_both(w, u, reach, strat);
@@ -253,8 +259,9 @@ void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, co
                   hipStream_t s) {
     if (!n) return;
     const size_t lds = (size_t)w.max_rwin * sizeof(float);
-    if (player >= 0 && w.unit_lds && lds <= REACH_LDS_MAX)
-        hipLaunchKernelGGL(k_reach<true>, dim3(n), dim3(BLOCK), lds, s, w, unit0, reach, strat, player);
+    if (w.unit_lds && lds <= REACH_LDS_MAX)
+        hipLaunchKernelGGL(k_reach<true>, dim3(player < 0 ? 2 * n : n), dim3(BLOCK), lds, s, w, unit0, reach, strat,
+                           player);
     else
         hipLaunchKernelGGL(k_reach<false>, dim3(n), dim3(BLOCK), 0, s, w, unit0, reach, strat, player);
 }
