@@ -267,14 +267,24 @@ void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, co
 }
 
 // The average-strategy accumulation of player `acc` over all its decision rows
-// (units' and top regions'), one row per thread, in the workgroups of a launch
-// past its first `first` (the leaf-input kernels run it beside their own work:
-// both only read the final reach).
-__device__ __forceinline__ bool accumulate_blocks(const WaveDev& w, int acc, float ds, uint32_t first) {
-    if (acc < 0 || blockIdx.x < first) return false;
-    const uint32_t k = (blockIdx.x - first) * blockDim.x + threadIdx.x;
-    if (k < w.ndec[acc]) accumulate_row(w, w.acc_rec[acc][k], ds);
-    return true;
+// (units' and top regions'), one row per thread, in workgroups of a leaf-input
+// launch (both only read the final reach). The launch's pool_blocks pooling
+// workgroups come longest config lists first; the accumulation's workgroups
+// are dealt after the first quarter of them, so the streaming accumulation
+// runs beside the long lists rather than trailing the launch (3.94 -> 3.78 ms
+// per 256-subgame wave; right after the first eighth or half: 3.86 / 3.89).
+// Returns true for an accumulation workgroup, else sets *pool_block to the
+// workgroup's index among the pooling ones.
+__device__ __forceinline__ bool accumulate_blocks(const WaveDev& w, int acc, float ds, uint32_t pool_blocks,
+                                                  uint32_t* pool_block) {
+    const uint32_t nacc = acc >= 0 ? gridDim.x - pool_blocks : 0, q1 = pool_blocks / 4;
+    if (blockIdx.x >= q1 && blockIdx.x < q1 + nacc) {
+        const uint32_t k = (blockIdx.x - q1) * blockDim.x + threadIdx.x;
+        if (k < w.ndec[acc]) accumulate_row(w, w.acc_rec[acc][k], ds);
+        return true;
+    }
+    *pool_block = blockIdx.x < q1 ? blockIdx.x : blockIdx.x - nacc;
+    return false;
 }
 
 // Top-region reach at one depth, all trees together: one row per thread.
@@ -386,8 +396,9 @@ __device__ __forceinline__ float lane_sum_in_order(float tot, float v, uint32_t 
 // traverser q.
 __global__ __launch_bounds__(BLOCK) void k_pool_exact(WaveDev w, int player, float* x0, float* x1, int acc,
                                                     float ds, uint32_t pool_blocks) {
-    if (accumulate_blocks(w, acc, ds, pool_blocks)) return;
-    const uint32_t task = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    uint32_t pbk;
+    if (accumulate_blocks(w, acc, ds, pool_blocks, &pbk)) return;
+    const uint32_t task = __builtin_amdgcn_readfirstlane((pbk * blockDim.x + threadIdx.x) >> 6);
     const uint32_t lane = threadIdx.x & 63;
     uint32_t row, p;
     if (player < 0) {
@@ -465,8 +476,9 @@ __global__ __launch_bounds__(BLOCK) void k_pool_exact(WaveDev w, int player, flo
 template <int PREC>
 __global__ __launch_bounds__(BLOCK) void k_pool_mfma(WaveDev w, int player, uint16_t* x0, uint16_t* x1, int acc,
                                                    float ds, uint32_t pool_blocks) {
-    if (accumulate_blocks(w, acc, ds, pool_blocks)) return;
-    uint32_t g = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    uint32_t pbk;
+    if (accumulate_blocks(w, acc, ds, pool_blocks, &pbk)) return;
+    uint32_t g = __builtin_amdgcn_readfirstlane((pbk * blockDim.x + threadIdx.x) >> 6);
     const uint32_t lane = threadIdx.x & 63;
     uint32_t p = player < 0 ? 0u : (uint32_t)player;
     if (player < 0 && g >= w.npool[0]) {
