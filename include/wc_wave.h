@@ -218,6 +218,23 @@ int wc_collect(wc_executor* ex, wc_inflight* f, wc_result** results);
 int wc_wave_leaf_probe(wc_executor* ex, wc_wave* w, uint64_t version, int traverser, float* values, size_t cap,
                        size_t* count, float* mass);
 
+/* Tooling (no counterpart in the reference): the same values captured inside
+ * one whole schedule, right after the leaf net runs at each of `points`, so
+ * the leaf-input and value-net kernels are checked at the reach the solve
+ * itself produces. A point t >= 0 is iteration t (traverser t & 1); a point
+ * -(1 + 2 r + p) is Phase 2's evaluation for carried root r and player p.
+ * counts (4 entries) receives: [0] / [1] the values of one point of traverser
+ * 0 / 1 (each network row's configs of that player, wave order), [2] the
+ * network rows, [3] the reach floats of one point (each row's reach over its
+ * configs, player 0's then player 1's). Outputs are concatenated over the
+ * points in the order given: values (the sum of the points' value counts),
+ * mass (2 * rows per point: the rows' reach masses), reach (counts[3] per
+ * point; reach NULL: not captured). With values or mass NULL, or a buffer too
+ * small, only counts is written. */
+int wc_wave_leaf_trace(wc_executor* ex, wc_wave* w, uint64_t version, const int32_t* points, size_t npoints,
+                       float* values, size_t values_cap, float* mass, size_t mass_cap, float* reach, size_t reach_cap,
+                       size_t* counts);
+
 /* Benchmark helper: upload once, run the full schedule `warmup` times
  * untimed, then `reps` times timed (inputs resident in HBM), returning the
  * mean device time per wave in milliseconds, measured with HIP events on the

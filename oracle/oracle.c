@@ -659,6 +659,14 @@ typedef struct {
     /* v5: the card tokens of both views, per row the board vector and its join
      * projection, per config g(c) */
     float *cards, *P, *Jp, *gcfg;
+    /* replay (oracle_solve_replay): the network leaves' values and reach masses
+     * of every leaf-net evaluation in schedule order, consumed by readout */
+    const float *rp_vals, *rp_mass;
+    size_t rp_vn, rp_mn, rp_vpos, rp_mpos;
+    int rp_short; /* set when the replay ran out of values */
+    /* trace (oracle_solve_trace): the same, recorded from the solver's own net */
+    float *tr_vals, *tr_mass, *tr_reach; /* tr_reach optional: each row's reach of both players */
+    size_t tr_vpos, tr_mpos, tr_rpos;
 } Solver;
 
 static inline uint32_t S_nc(const Solver* s, uint32_t i, int p) { return p ? s->nc1[i] : s->nc0[i]; }
@@ -833,6 +841,24 @@ static void readout(Solver* s, int p) {
         float* v = s->vals + s->voff[i];
         for (uint32_t c = 0; c < S_nc(s, i, p); c++) v[c] = u * opp_reach;
     }
+    if (s->rp_vals) { /* replay: the given net values times the given opponent masses */
+        size_t need = 0;
+        for (uint32_t r = 0; r < j->rows; r++) need += S_nc(s, j->leaf_rows.v[r], p);
+        if (s->rp_vpos + need > s->rp_vn || s->rp_mpos + 2 * (size_t)j->rows > s->rp_mn) {
+            s->rp_short = 1;
+            return;
+        }
+        const float* rv = s->rp_vals + s->rp_vpos;
+        const float* rm = s->rp_mass + s->rp_mpos;
+        for (uint32_t r = 0; r < j->rows; r++) {
+            uint32_t i = j->leaf_rows.v[r], nn = S_nc(s, i, p);
+            float* v = s->vals + s->voff[i];
+            for (uint32_t c = 0; c < nn; c++) v[c] = *rv++ * rm[2 * r + (uint32_t)opp];
+        }
+        s->rp_vpos += need;
+        s->rp_mpos += 2 * (size_t)j->rows;
+        return;
+    }
     for (uint32_t r = 0; r < j->rows; r++) {
         uint32_t i = j->leaf_rows.v[r];
         float opp_reach = 0.0f;
@@ -845,8 +871,25 @@ static void readout(Solver* s, int p) {
             continue;
         }
         for (uint32_t c = 0; c < nn; c++) v[c] = net_value(s, r, p, c);
+        if (s->tr_vals) {
+            memcpy(s->tr_vals + s->tr_vpos, v, nn * sizeof(float));
+            s->tr_vpos += nn;
+            const float* rp = reach_of(s, i, p);
+            float own = 0.0f;
+            for (uint32_t c = 0; c < nn; c++) own += rp[c];
+            s->tr_mass[s->tr_mpos + 2 * r + (uint32_t)p] = own;
+            s->tr_mass[s->tr_mpos + 2 * r + (uint32_t)opp] = opp_reach;
+        }
         for (uint32_t c = 0; c < nn; c++) v[c] *= opp_reach;
     }
+    if (s->tr_vals) s->tr_mpos += 2 * (size_t)j->rows;
+    if (s->tr_reach)
+        for (uint32_t r = 0; r < j->rows; r++)
+            for (int q = 0; q < 2; q++) {
+                uint32_t i = j->leaf_rows.v[r], nq = S_nc(s, i, q);
+                memcpy(s->tr_reach + s->tr_rpos, reach_of(s, i, q), nq * sizeof(float));
+                s->tr_rpos += nq;
+            }
 }
 
 static void ensure_leaf_batch(Solver* s) {
@@ -1374,6 +1417,161 @@ int oracle_leaf_probe(const uint8_t* b, size_t n, int net_mode, const uint32_t* 
             for (uint32_t c = 0; c < S_nc(&s, i, p); c++) tot += ro[c];
             if (mass) mass[2 * r + (uint32_t)p] = tot;
         }
+    }
+    rc = 0;
+out:
+    solver_free(&s);
+    net_free(&net);
+    job_free(&j);
+    return rc;
+}
+
+/* Per network row, how many floats the leaf evaluations below take and give:
+ * out[0] / out[1] the values of traverser 0 / 1 (the sum over rows of nc_p),
+ * out[2] the rows, out[3] the rows' reach (the sum of nc_0 + nc_1). */
+int oracle_leaf_counts(const uint8_t* b, size_t n, size_t* out) {
+    Job j;
+    if (!parse_job(b, n, &j)) {
+        job_free(&j);
+        return -1;
+    }
+    out[0] = out[1] = out[3] = 0;
+    out[2] = j.rows;
+    for (uint32_t r = 0; r < j.rows; r++) {
+        uint32_t i = j.leaf_rows.v[r];
+        size_t a = j.cfg_off.v[2 * i + 1] - j.cfg_off.v[2 * i], c = j.cfg_off.v[2 * i + 2] - j.cfg_off.v[2 * i + 1];
+        out[0] += a;
+        out[1] += c;
+        out[3] += a + c;
+    }
+    job_free(&j);
+    return 0;
+}
+
+/* The leaf net's values for traverser p at a given reach: the leaf rows'
+ * reach is set from `reach` (per row in order, player 0's configs then player
+ * 1's) and the leaf input and net run as belief_blocks + pbs_head do. values
+ * (out[traverser] floats of oracle_leaf_counts) and mass (rows x 2, the
+ * config-order sums of the given reach) as oracle_leaf_probe gives them. */
+int oracle_leaf_eval(const uint8_t* b, size_t n, int net_mode, const uint32_t* dims, uint32_t ndims, const float* w,
+                     size_t nw, const float* bias, size_t nb, const float* ln, size_t nln, int traverser,
+                     const float* reach, float* values, float* mass) {
+    Job j;
+    Net net;
+    Solver s;
+    int rc = -1;
+    memset(&s, 0, sizeof s);
+    memset(&net, 0, sizeof net);
+    if (!parse_job(b, n, &j)) goto out;
+    if (!net_init(&net, net_mode, dims, ndims, w, nw, bias, nb, ln, nln)) goto out;
+    if (net_mode == NET_EMPTY || traverser < 0 || traverser > 1) {
+        snprintf(g_err, sizeof g_err, "leaf evaluation needs a network and a traverser 0 or 1");
+        goto out;
+    }
+    if (!solver_init(&s, &j, &net)) goto out;
+    {
+        const float* rr = reach;
+        for (uint32_t r = 0; r < j.rows; r++) {
+            uint32_t i = j.leaf_rows.v[r];
+            for (int p = 0; p < 2; p++) {
+                float* ro = reach_of(&s, i, p);
+                float tot = 0.0f;
+                for (uint32_t c = 0; c < S_nc(&s, i, p); c++) {
+                    ro[c] = *rr++;
+                    tot += ro[c];
+                }
+                if (mass) mass[2 * r + (uint32_t)p] = tot;
+            }
+        }
+    }
+    leaf_beliefs_both(&s);
+    pbs_head(&s, traverser);
+    {
+        size_t k = 0;
+        for (uint32_t r = 0; r < j.rows; r++)
+            for (uint32_t c = 0; c < S_nc(&s, j.leaf_rows.v[r], traverser); c++)
+                values[k++] = net_value(&s, r, traverser, c);
+    }
+    rc = 0;
+out:
+    solver_free(&s);
+    net_free(&net);
+    job_free(&j);
+    return rc;
+}
+
+/* oracle_solve recording every leaf-net evaluation in the layout
+ * oracle_solve_replay takes: vals and mass must hold the sum over the
+ * evaluations (iterations 0 .. iters-1, then per carried root players 0 and 1)
+ * of each one's values (the rows' configs of its player) and 2 * rows masses;
+ * reach (may be NULL) per evaluation each row's reach of both players, as
+ * oracle_leaf_eval takes it. */
+int oracle_solve_trace(const uint8_t* b, size_t n, int net_mode, const uint32_t* dims, uint32_t ndims,
+                       const float* w, size_t nw, const float* bias, size_t nb, const float* ln, size_t nln,
+                       float* vals, float* mass, float* reach, float* strategy, float* roots) {
+    Job j;
+    Net net;
+    Solver s;
+    int rc = -1;
+    memset(&s, 0, sizeof s);
+    memset(&net, 0, sizeof net);
+    if (!parse_job(b, n, &j)) goto out;
+    if (!net_init(&net, net_mode, dims, ndims, w, nw, bias, nb, ln, nln)) goto out;
+    if (net_mode == NET_EMPTY) {
+        snprintf(g_err, sizeof g_err, "a trace needs a network");
+        goto out;
+    }
+    if (!solver_init(&s, &j, &net)) goto out;
+    s.tr_vals = vals;
+    s.tr_mass = mass;
+    s.tr_reach = reach;
+    for (uint32_t t = 0; t < j.iters; t++) step(&s, (int)(t % 2));
+    if (strategy) memcpy(strategy, s.snaps[s.nsnaps - 1], (size_t)j.ncells * sizeof(float));
+    if (roots) value_under(&s, roots);
+    rc = 0;
+out:
+    solver_free(&s);
+    net_free(&net);
+    job_free(&j);
+    return rc;
+}
+
+/* oracle_solve with every network leaf's value given instead of computed:
+ * `vals` holds, for each leaf-net evaluation in schedule order (iterations
+ * 0 .. iters-1 with traverser t % 2, then per carried root players 0 and 1),
+ * each network row's values of that evaluation's player (row order, row config
+ * order), and `mass` the rows' reach masses of that evaluation (rows x 2); a
+ * network leaf's counterfactual value is its given value times the given mass
+ * of the opponent. Everything else (terminals, backprop, regret matching, the
+ * average, Phase 2, carries) is the solver's own. With the values and masses a
+ * device's leaf net produced inside its own solve, the outputs equal that
+ * device's bit for bit exactly when its CFR arithmetic is the solver's. */
+int oracle_solve_replay(const uint8_t* b, size_t n, const float* vals, size_t nvals, const float* mass, size_t nmass,
+                        float* strategy, float* roots, float* carries) {
+    Job j;
+    Net net;
+    Solver s;
+    int rc = -1;
+    memset(&s, 0, sizeof s);
+    memset(&net, 0, sizeof net);
+    if (!parse_job(b, n, &j)) goto out;
+    if (!net_init(&net, NET_EMPTY, NULL, 0, NULL, 0, NULL, 0, NULL, 0)) goto out;
+    if (!solver_init(&s, &j, &net)) goto out;
+    s.rp_vals = vals;
+    s.rp_mass = mass;
+    s.rp_vn = nvals;
+    s.rp_mn = nmass;
+    for (uint32_t t = 0; t < j.iters; t++) step(&s, (int)(t % 2));
+    if (strategy) memcpy(strategy, s.snaps[s.nsnaps - 1], (size_t)j.ncells * sizeof(float));
+    if (roots) value_under(&s, roots);
+    if (carries && j.snapshots) carried_beliefs(&s, carries);
+    if (s.rp_short) {
+        snprintf(g_err, sizeof g_err, "the replay holds fewer leaf values than the schedule evaluates");
+        goto out;
+    }
+    if (s.rp_vpos != nvals || s.rp_mpos != nmass) {
+        snprintf(g_err, sizeof g_err, "the replay holds more leaf values than the schedule evaluates");
+        goto out;
     }
     rc = 0;
 out:

@@ -58,6 +58,12 @@ def lib():
         L.oracle_leaf_probe.argtypes = [u8p, C.c_size_t, C.c_int, u32p, C.c_uint32, f32p, C.c_size_t, f32p,
                                         C.c_size_t, f32p, C.c_size_t, C.c_int, f32p, C.c_size_t,
                                         C.POINTER(C.c_size_t), f32p]
+        L.oracle_leaf_counts.argtypes = [u8p, C.c_size_t, C.POINTER(C.c_size_t)]
+        L.oracle_leaf_eval.argtypes = [u8p, C.c_size_t, C.c_int, u32p, C.c_uint32, f32p, C.c_size_t, f32p,
+                                       C.c_size_t, f32p, C.c_size_t, C.c_int, f32p, f32p, f32p]
+        L.oracle_solve_trace.argtypes = [u8p, C.c_size_t, C.c_int, u32p, C.c_uint32, f32p, C.c_size_t, f32p,
+                                         C.c_size_t, f32p, C.c_size_t, f32p, f32p, f32p, f32p, f32p]
+        L.oracle_solve_replay.argtypes = [u8p, C.c_size_t, f32p, C.c_size_t, f32p, C.c_size_t, f32p, f32p, f32p]
         net5 = [C.c_int, f32p, C.c_size_t, f32p, C.c_size_t, f32p, C.c_size_t, C.c_int]
         L.oracle_v5_sizes.argtypes = [C.POINTER(C.c_size_t)] * 3
         L.oracle_v5_cards.argtypes = net5 + [f32p, f32p]
@@ -309,3 +315,93 @@ class libm_tanh:
 
     def __exit__(self, *a):
         lib().oracle_v5_set_libm_tanh(0)
+
+
+def leaf_counts(job: bytes):
+    """(values of traverser 0, values of traverser 1, network rows, reach floats) that
+    one leaf evaluation of this job takes or gives (oracle_leaf_counts)."""
+    out = (C.c_size_t * 4)()
+    buf = (C.c_uint8 * len(job)).from_buffer_copy(job)
+    if lib().oracle_leaf_counts(buf, len(job), out) != 0:
+        raise ValueError(_err())
+    return int(out[0]), int(out[1]), int(out[2]), int(out[3])
+
+
+def leaf_eval(job: bytes, net, mode, traverser, reach):
+    """The leaf net's values for `traverser` at a given reach of the job's network rows
+    (per row, player 0's configs then player 1's), and the rows' masses [rows, 2]."""
+    n0, n1, rows, nreach = leaf_counts(job)
+    reach = np.ascontiguousarray(reach, np.float32)
+    if reach.size != nreach:
+        raise ValueError(f"reach holds {reach.size} floats, the job's rows take {nreach}")
+    vals = np.zeros(max(n1 if traverser else n0, 1), np.float32)
+    mass = np.zeros(max(2 * rows, 1), np.float32)
+    d, nd, w, nw, b, nb = _net_args(net, mode)
+    ln, nln = _ln_args(net, mode)
+    buf = (C.c_uint8 * len(job)).from_buffer_copy(job)
+    rc = lib().oracle_leaf_eval(buf, len(job), mode, _p(d, C.c_uint32), nd, _p(w, C.c_float), nw,
+                                _p(b, C.c_float), nb, _p(ln, C.c_float) if nln else None, nln, traverser,
+                                _p(reach if reach.size else np.zeros(1, np.float32), C.c_float),
+                                _p(vals, C.c_float), _p(mass, C.c_float))
+    if rc != 0:
+        raise ValueError(_err())
+    return vals[: n1 if traverser else n0], mass[: 2 * rows].reshape(rows, 2)
+
+
+def solve_replay(job: bytes, vals, mass):
+    """oracle_solve with every network leaf's value given (oracle_solve_replay): vals
+    and mass concatenated over the job's leaf-net evaluations in schedule order
+    (iterations, then per carried root players 0 and 1)."""
+    s = shape(job)
+    vals = np.ascontiguousarray(vals, np.float32)
+    mass = np.ascontiguousarray(mass, np.float32)
+    strategy = np.zeros(max(s.ncells, 1), np.float32)
+    roots = np.zeros(max(s.nroots * (s.root_n0 + s.root_n1), 1), np.float32)
+    carries = np.zeros(max(s.carry_slots * s.snapshot_configs, 1), np.float32)
+    buf = (C.c_uint8 * len(job)).from_buffer_copy(job)
+    one = np.zeros(1, np.float32)
+    rc = lib().oracle_solve_replay(buf, len(job), _p(vals if vals.size else one, C.c_float), vals.size,
+                                   _p(mass if mass.size else one, C.c_float), mass.size,
+                                   _p(strategy, C.c_float), _p(roots, C.c_float), _p(carries, C.c_float))
+    if rc != 0:
+        raise ValueError(_err())
+    return {
+        "strategy": strategy[: s.ncells],
+        "roots": roots[: s.nroots * (s.root_n0 + s.root_n1)].reshape(s.nroots, s.root_n0 + s.root_n1),
+        "carries": carries[: s.carry_slots * s.snapshot_configs].reshape(s.carry_slots, s.snapshot_configs),
+        "shape": s,
+    }
+
+
+def replay_sizes(job: bytes):
+    """(values, masses) a replay of this job takes: per leaf-net evaluation in
+    schedule order (iterations, then per carried root players 0 and 1)."""
+    s = shape(job)
+    n0, n1, rows, _ = leaf_counts(job)
+    trav = [t % 2 for t in range(s.iters)] + [p for _ in range(s.nroots) for p in (0, 1)]
+    return sum(n1 if p else n0 for p in trav), 2 * rows * len(trav)
+
+
+def solve_trace(job: bytes, net, mode=NET_F32):
+    """oracle_solve recording every leaf-net evaluation's values and masses in the
+    layout solve_replay takes, and the reach that fed each one (per evaluation, per
+    row, player 0's configs then player 1's): dict(vals, mass, reach, strategy, roots)."""
+    s = shape(job)
+    nv, nm = replay_sizes(job)
+    nreach = leaf_counts(job)[3] * (s.iters + 2 * s.nroots)
+    vals = np.zeros(max(nv, 1), np.float32)
+    mass = np.zeros(max(nm, 1), np.float32)
+    reach = np.zeros(max(nreach, 1), np.float32)
+    strategy = np.zeros(max(s.ncells, 1), np.float32)
+    roots = np.zeros(max(s.nroots * (s.root_n0 + s.root_n1), 1), np.float32)
+    d, nd, w, nw, b, nb = _net_args(net, mode)
+    ln, nln = _ln_args(net, mode)
+    buf = (C.c_uint8 * len(job)).from_buffer_copy(job)
+    rc = lib().oracle_solve_trace(buf, len(job), mode, _p(d, C.c_uint32), nd, _p(w, C.c_float), nw,
+                                  _p(b, C.c_float), nb, _p(ln, C.c_float) if nln else None, nln,
+                                  _p(vals, C.c_float), _p(mass, C.c_float), _p(reach, C.c_float),
+                                  _p(strategy, C.c_float), _p(roots, C.c_float))
+    if rc != 0:
+        raise ValueError(_err())
+    return {"vals": vals[:nv], "mass": mass[:nm], "reach": reach[:nreach], "strategy": strategy[: s.ncells],
+            "roots": roots[: s.nroots * (s.root_n0 + s.root_n1)].reshape(s.nroots, s.root_n0 + s.root_n1)}

@@ -10,6 +10,11 @@ for p in (PKG, ORACLE, os.path.join(ROOT, "tests")):
     if p not in sys.path:
         sys.path.insert(0, p)
 
+# Waves the service packs from jobs validated at submit skip the packed wave's
+# deep bounds check unless WC_DEEP_CHECK=1; the tests keep it on, so every
+# service-formed wave they run has passed it.
+os.environ.setdefault("WC_DEEP_CHECK", "1")
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs on the GPU box)")

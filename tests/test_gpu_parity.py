@@ -358,7 +358,11 @@ def test_wave64_compensated_f16_meets_the_2e3_bound():
     envelope checks of tests/envelope.py. Subgame 57, the most sensitive of
     the wave (5e-2 under plain f16), moves by 8e-3 here while the two
     compensated emulations move it by 1.1e-3 and 1.7e-3: even ~22-bit operands
-    leave it chaotic. Mean strategy error <= 1e-3."""
+    leave it chaotic (tests/test_gpu_trace.py replays the device's own leaf
+    values through the oracle's solver and gets the device's solve bit for bit).
+    Mean strategy error <= 1e-3. No subgame is unbounded: every root error is
+    within max(1e-2, 3x its compensated emulation's), a fifth of what plain f16
+    operands reach on this wave."""
     import envelope
     jobs = W.jobs("wave64")
     net = W.net_for("wave64")
@@ -368,7 +372,7 @@ def test_wave64_compensated_f16_meets_the_2e3_bound():
     refs = solve_refs(jobs, net, [O.NET_F32])[O.NET_F32]
     dev = np.array([np.abs(g.root_values - r["roots"]).max() / np.abs(r["roots"]).max() for g, r in zip(got, refs)])
     ms = [float(np.abs(g.strategy - r["strategy"]).mean()) for g, r in zip(got, refs)]
-    envelope.check(dev, env["F16X"], ms, 1e-3, say, "wave64 compensated f16", frac=0.95)
+    envelope.check(dev, env["F16X"], ms, 1e-3, say, "wave64 compensated f16", frac=0.95, cap=1e-2)
     assert (dev <= 2e-3).sum() >= 60
 
 

@@ -1,9 +1,12 @@
 """The service and the executor's launch/collect split on the GPU, through the C ABI.
 
+Every result is compared bit for bit with the float32 CPU solver (the oracle),
+not with another run of the device.
+
 - queued_work (engine/src/gpu/client.rs:274-291) is the sum of the queued
   jobs' job_cost while they wait, and drains to zero;
 - several lanes and several submitting threads return every job's result
-  bit-identical to a solve of that job alone (the reference's lanes,
+  bit-identical to the oracle's solve of that job (the reference's lanes,
   engine/src/gpu/service.rs:546-742);
 - wc_launch / wc_collect (engine/src/gpu/device.rs:596-831): two waves in
   flight on one executor, the packed wave freed while its wave runs;
@@ -11,12 +14,16 @@
   jobs run in one-job waves, guarded jobs after every lane has drained and
   trimmed, and the results carry their route flags (client.rs:119-121).
 """
+import os
 import sys
 import threading
+from concurrent.futures import ThreadPoolExecutor
+from types import SimpleNamespace
 
 import numpy as np
 import pytest
 
+import oracle as O
 import warchest_wave as ww
 import workloads as W
 
@@ -35,21 +42,16 @@ def small_jobs(trees, seed, **kw):
     return W.jobs("wave256", **spec)
 
 
-_EX = []
-
-
 def alone(jobs, net):
-    """Each job solved in a wave of its own (float32)."""
-    if not _EX:
-        _EX.append(ww.Executor(0, ww.WC_PRECISE))
-    ex = _EX[0]
-    v = ex.publish(net)
-    out = []
-    for j in jobs:
-        w = ww.Wave([j])
-        out.append(ex.solve(w, v)[0])
-        w.close()
-    return out
+    """Each job solved by the float32 CPU solver (the oracle), carries rounded to
+    f16 as the result store keeps them."""
+    def one(j):
+        o = O.solve(j, net, O.NET_F32)
+        return SimpleNamespace(strategy=o["strategy"], root_values=o["roots"],
+                               carries=o["carries"].astype(np.float16))
+
+    with ThreadPoolExecutor(min(16, os.cpu_count() or 1)) as pool:
+        return list(pool.map(one, jobs))
 
 
 def same(g, r, tag):

@@ -7,9 +7,9 @@
   oracle's model of its own operand rounding tightly, on every row of the
   waves, including the first layer's fixed-column split and the per-block
   head widths of the 256-subgame wave.
-- The 256-subgame wave's subgames at their full shape (200..800 nodes,
-  lognormal infostates up to 567, 64 iterations, the 567-head net): float32
-  bit-exact, f16 within the f16 envelope.
+- The 256-subgame wave at its full shape (200..800 nodes, lognormal
+  infostates up to 567, 64 iterations, the 567-head net): all 256 subgames
+  float32 bit-exact; 16 of them in f16 within the f16 envelope.
 - The heavy-tail wave's whales (2,000 nodes, 567 infostates per player,
   128 iterations, the two-tower net): float32 bit-exact; bf16 within the
   spread that bf16 rounding itself produces (tests/test_conditioning.py).
@@ -141,10 +141,14 @@ def full_wave256(trees=16):
     return W.jobs("wave256")[:trees]
 
 
-def test_wave256_full_shape_float32_bit_exact():
-    jobs = full_wave256()
+@pytest.mark.timeout(600)
+def test_wave256_whole_wave_float32_bit_exact():
+    """The benchmarked wave itself, every one of its 256 subgames (3,257 units,
+    13 top levels, 136,828 nodes): strategy, root values and carries bit for bit
+    against the float32 CPU solver (about 40 s of oracle time on 16 threads)."""
+    jobs = W.jobs("wave256")
     net = W.net_for("wave256")
-    say(f"case wave256 full shape float32: {len(jobs)} subgames of 200..800 nodes, 64 iterations, 567 heads")
+    say(f"case wave256 whole wave float32: all {len(jobs)} subgames of 200..800 nodes, 64 iterations, 567 heads")
     ex = executor(ww.WC_PRECISE)
     v = ex.publish(net)
     wave = ww.Wave(jobs)
@@ -217,11 +221,15 @@ def test_wave512w_whales_float32_bit_exact_and_bf16_near_float32():
         say(f"tree {k}: float32 bit-exact; bf16 mean strategy error {mean_s:.2e}, pointwise guard ratio "
             f"{ratio:.2f}, root error {rel:.2e} of the largest root value")
         # bf16 keeps 8 significant bits: over the 64-subgame wave its emulation's
-        # mean strategy error reaches 1.4e-2 and its root error 0.25 (median 6e-3);
-        # a near-tie between two actions can flip one strategy entry (the
-        # pointwise guard), which is reported, not bounded.
+        # mean strategy error reaches 1.4e-2 and its root error 0.25 (median 6e-3).
+        # A near-tie between two actions can flip one strategy entry: the
+        # reference's pointwise guard 0.4 + 0.1|x| (engine/src/gpu/tests.rs:436-443)
+        # measures 1.9-2.0 of its bound here, so it is held at 2.5 (the replay in
+        # tests/test_gpu_trace.py shows the flips are the solve's, given its leaf
+        # values).
         assert mean_s <= 1.5e-2, f"tree {k}"
         assert rel <= 5e-2, f"tree {k}"
+        assert ratio <= 2.5, f"tree {k}: pointwise guard ratio {ratio:.2f}"
 
 
 def test_wave512w_whale_leaf_probe_bf16():

@@ -4,7 +4,9 @@ wc_mlp_forward, through the C ABI, on device-resident buffers.
 Two calls in a row, the second with fewer rows (the shared scratch keeps the
 first call's contents), in f16 (the fused net), float32 (the exact net) and
 compensated f16 (layer by layer): outputs bit-identical to wc_mlp_forward's.
-Rows beyond the scratch are refused with an error naming it.
+Rows beyond the scratch are refused with an error naming it. The same two calls
+queued on a stream the caller created (the call returns at once; the caller
+synchronizes that stream) give the same outputs.
 """
 import ctypes as C
 import sys
@@ -32,8 +34,23 @@ class Hip:
         self.L.hipFree.argtypes = [C.c_void_p]
         self.L.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
         self.L.hipDeviceSynchronize.argtypes = []
-        for f in (self.L.hipMalloc, self.L.hipFree, self.L.hipMemcpy, self.L.hipDeviceSynchronize):
+        self.L.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.L.hipStreamSynchronize.argtypes = [C.c_void_p]
+        self.L.hipStreamDestroy.argtypes = [C.c_void_p]
+        for f in (self.L.hipMalloc, self.L.hipFree, self.L.hipMemcpy, self.L.hipDeviceSynchronize,
+                  self.L.hipStreamCreate, self.L.hipStreamSynchronize, self.L.hipStreamDestroy):
             f.restype = C.c_int
+
+    def stream(self):
+        s = C.c_void_p()
+        assert self.L.hipStreamCreate(C.byref(s)) == 0  # default flags and priority
+        return s.value
+
+    def sync(self, s):
+        assert self.L.hipStreamSynchronize(C.c_void_p(s)) == 0
+
+    def destroy(self, s):
+        assert self.L.hipStreamDestroy(C.c_void_p(s)) == 0
 
     def alloc(self, nbytes):
         p = C.c_void_p()
@@ -71,6 +88,39 @@ def test_noalloc_matches_mlp_forward_twice(precision):
             want = ex.mlp(v, x, heads=heads)
             np.testing.assert_array_equal(got, want)
     finally:
+        hip.free(xd)
+        hip.free(od)
+        ex.close()
+
+
+@pytest.mark.parametrize("precision", [ww.WC_F16, ww.WC_PRECISE])
+def test_noalloc_on_a_caller_stream(precision):
+    """Queued on the caller's own stream (the plan kernel and the net run there):
+    the call returns at once, and after the caller synchronizes that stream the
+    outputs equal wc_mlp_forward's, on two calls in a row, the second smaller."""
+    hip = Hip()
+    net = W.net_for("mlp65k")
+    heads = net.dims[4]
+    ex = ww.Executor(0, precision)
+    v = ex.publish(net)
+    sizes = (3000, 700) if precision != ww.WC_PRECISE else (1500, 500)
+    xd = hip.alloc(sizes[0] * 512 * 4)
+    od = hip.alloc(sizes[0] * heads * 4)
+    st = hip.stream()
+    try:
+        for call, rows in enumerate(sizes):
+            say(f"case no-alloc on a caller stream, precision {precision}: call {call + 1}, {rows} rows")
+            x = W.mlp65k_inputs(rows=rows, seed=60 + call)
+            hip.to_dev(xd, x)
+            ex.mlp_noalloc(v, rows, xd, od, stream=st)
+            hip.sync(st)
+            got = np.zeros((rows, heads), np.float32)
+            hip.to_host(got, od)
+            want = ex.mlp(v, x, heads=heads)
+            np.testing.assert_array_equal(got, want)
+    finally:
+        hip.sync(st)
+        hip.destroy(st)
         hip.free(xd)
         hip.free(od)
         ex.close()

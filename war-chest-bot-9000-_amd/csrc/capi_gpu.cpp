@@ -346,6 +346,36 @@ int wc_wave_leaf_probe(wc_executor* ex, wc_wave* w, uint64_t version, int traver
     });
 }
 
+int wc_wave_leaf_trace(wc_executor* ex, wc_wave* w, uint64_t version, const int32_t* points, size_t npoints,
+                       float* values, size_t values_cap, float* mass, size_t mass_cap, float* reach, size_t reach_cap,
+                       size_t* counts) {
+    if (!ex || !w || !counts || (npoints && !points)) return fail(WC_ERR_INVALID, "wc_wave_leaf_trace: null argument");
+    return shielded("wc_wave_leaf_trace", [&] {
+        const WaveHost& h = w->host;
+        size_t c[4] = {0, 0, h.rows(), 0};
+        for (uint32_t r = 0; r < h.rows(); r++) {
+            c[0] += h.nc(h.row_node[r], 0);
+            c[1] += h.nc(h.row_node[r], 1);
+        }
+        c[3] = c[0] + c[1];
+        std::copy(c, c + 4, counts);
+        size_t nv = 0;
+        for (size_t k = 0; k < npoints; k++) nv += c[points[k] >= 0 ? (points[k] & 1) : ((-points[k] - 1) & 1)];
+        if (!values || !mass || values_cap < nv || mass_cap < npoints * 2 * c[2] ||
+            (reach && reach_cap < npoints * c[3]))
+            return WC_OK;
+        LeafTrace t;
+        std::string err;
+        if (!ex->ex->leaf_trace(h, version, std::vector<int32_t>(points, points + npoints), reach != nullptr, &t,
+                                &err))
+            return fail(WC_ERR_DEVICE, err);
+        std::copy(t.values.begin(), t.values.end(), values);
+        std::copy(t.mass.begin(), t.mass.end(), mass);
+        if (reach) std::copy(t.reach.begin(), t.reach.end(), reach);
+        return WC_OK;
+    });
+}
+
 int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup, uint32_t reps, double* wave_ms,
                  double* kernel_ms) {
     if (!ex || !w || !wave_ms) return fail(WC_ERR_INVALID, "wc_time_wave: null argument");

@@ -828,7 +828,7 @@ void Executor::init_state(const WaveHost& w) {
     launch_pool(d, -1, precision_, Xq_[0], Xq_[1], s);
 }
 
-void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTimes* prof) {
+void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTimes* prof, const LeafHook* hook) {
     const WaveDev& d = dev_;
     hipStream_t s = stream_;
     const Meta& m = w.meta;
@@ -864,6 +864,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     for (uint32_t t = 0; t < m.iters; t++) {
         const int p = (int)(t & 1);
         leaf_net(bank, p);
+        if (hook) (*hook)((int32_t)t, p);
         mark(C_MLP);
         const float mm = (float)(t / 2 + 1);
         const float da = cfr_factor(mm, m.cfr.alpha), db = cfr_factor(mm, m.cfr.beta);
@@ -899,6 +900,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         mark(C_LEAF);
         for (int p = 0; p < 2; p++) {
             leaf_net(bank, p);
+            if (hook) (*hook)(phase2_point(root, p), p);
             launch_sweep(d, 0, nsub, head_out_, bank.ns.heads, p, MODE_VALUE, 0.0f, 0.0f, 0.0f, s);
             top_back(w, p, MODE_VALUE, 0.0f, 0.0f, 0.0f);
             launch_collect_root(d, (int)root, p, s);
@@ -1090,6 +1092,34 @@ bool Executor::solve(const WaveHost& w, uint64_t version, std::vector<Result>* o
     return collect(&f, out, err);
 }
 
+bool Executor::read_leaves(const WaveHost& w, const NetBank& bank, int p, std::vector<float>* values,
+                           std::vector<float>* mass, std::string* err) {
+    const size_t nout = readout_net(bank.ns.kind) ? w.tower_len : size_t(w.rows()) * bank.ns.heads;
+    std::vector<float> head(nout);
+    const size_t m0 = mass->size();
+    mass->resize(m0 + size_t(w.rows()) * 2, 0.0f);
+    if (nout) HIP_TRY(hipMemcpyAsync(head.data(), head_out_, nout * 4, hipMemcpyDeviceToHost, stream_));
+    if (w.rows()) HIP_TRY(hipMemcpyAsync(mass->data() + m0, dev_.mass, size_t(w.rows()) * 2 * 4, hipMemcpyDeviceToHost,
+                                         stream_));
+    HIP_TRY(hipStreamSynchronize(stream_));
+    // Each network-leaf value slot's net value, by the records the sweep reads.
+    std::unordered_map<uint32_t, uint32_t> head_of;
+    head_of.reserve(w.leaf_rec[p].size());
+    for (const LeafRec& q : w.leaf_rec[p]) head_of[q.out] = q.head;
+    for (uint32_t r = 0; r < w.rows(); r++) {
+        const uint32_t node = w.row_node[r], base = w.vals_base[2 * node + p];
+        for (uint32_t c = 0; c < w.nc(node, p); c++) {
+            auto it = head_of.find(base + c);
+            if (it == head_of.end() || it->second >= nout) {
+                *err = "network row " + std::to_string(r) + " has a value slot without a leaf record";
+                return false;
+            }
+            values->push_back(head[it->second]);
+        }
+    }
+    return true;
+}
+
 bool Executor::leaf_probe(const WaveHost& w, uint64_t version, int traverser, std::vector<float>* values,
                           std::vector<float>* mass, std::string* err) {
     const NetBank* bank = bank_of(version, err);
@@ -1109,29 +1139,89 @@ bool Executor::leaf_probe(const WaveHost& w, uint64_t version, int traverser, st
     init_state(w);
     leaf_net(*bank, traverser);
     HIP_TRY(hipGetLastError());
-    const size_t nout = readout_net(bank->ns.kind) ? w.tower_len : size_t(w.rows()) * bank->ns.heads;
-    std::vector<float> head(nout);
-    mass->assign(size_t(w.rows()) * 2, 0.0f);
-    if (nout) HIP_TRY(hipMemcpyAsync(head.data(), head_out_, nout * 4, hipMemcpyDeviceToHost, stream_));
-    if (w.rows()) HIP_TRY(hipMemcpyAsync(mass->data(), dev_.mass, mass->size() * 4, hipMemcpyDeviceToHost, stream_));
-    HIP_TRY(hipStreamSynchronize(stream_));
-    // Each network-leaf value slot's net value, by the records the sweep reads.
-    const int p = traverser;
-    std::unordered_map<uint32_t, uint32_t> head_of;
-    head_of.reserve(w.leaf_rec[p].size());
-    for (const LeafRec& q : w.leaf_rec[p]) head_of[q.out] = q.head;
     values->clear();
-    for (uint32_t r = 0; r < w.rows(); r++) {
-        const uint32_t node = w.row_node[r], base = w.vals_base[2 * node + p];
-        for (uint32_t c = 0; c < w.nc(node, p); c++) {
-            auto it = head_of.find(base + c);
-            if (it == head_of.end() || it->second >= nout) {
-                *err = "network row " + std::to_string(r) + " has a value slot without a leaf record";
-                return false;
-            }
-            values->push_back(head[it->second]);
-        }
+    mass->clear();
+    return read_leaves(w, *bank, traverser, values, mass, err);
+}
+
+bool Executor::leaf_trace(const WaveHost& w, uint64_t version, const std::vector<int32_t>& points, bool with_reach,
+                          LeafTrace* out, std::string* err) {
+    const NetBank* bank = bank_of(version, err);
+    if (!bank) return false;
+    if (in_flight_) {
+        *err = "collect the launched waves before tracing";
+        return false;
     }
+    const int32_t iters = (int32_t)w.meta.iters, roots = (int32_t)w.nroots_max;
+    // Output offsets of each requested point (values depend on its traverser).
+    size_t nval[2] = {0, 0}, nreach = 0;
+    for (uint32_t r = 0; r < w.rows(); r++) {
+        const uint32_t node = w.row_node[r];
+        nval[0] += w.nc(node, 0);
+        nval[1] += w.nc(node, 1);
+        nreach += size_t(w.nc(node, 0)) + w.nc(node, 1);
+    }
+    const size_t nmass = size_t(w.rows()) * 2;
+    std::vector<size_t> voff(points.size());
+    std::vector<int> seen(points.size(), 0);
+    size_t vtot = 0;
+    for (size_t k = 0; k < points.size(); k++) {
+        const int32_t pt = points[k];
+        if (pt >= iters || (pt < 0 && -pt > 2 * roots)) {
+            *err = "trace point " + std::to_string(pt) + " is outside the schedule (" + std::to_string(iters) +
+                   " iterations, " + std::to_string(roots) + " carried roots)";
+            return false;
+        }
+        voff[k] = vtot;
+        vtot += nval[pt >= 0 ? (pt & 1) : ((-pt - 1) & 1)];
+    }
+    out->values.assign(vtot, 0.0f);
+    out->mass.assign(points.size() * nmass, 0.0f);
+    out->reach.assign(with_reach ? points.size() * nreach : 0, 0.0f);
+    if (!upload(w, *bank, 0, err)) return false;
+    std::vector<float> reach(with_reach ? w.reach_len : 0), v, m;
+    std::string herr;
+    const LeafHook hook = [&](int32_t point, int p) {
+        for (size_t k = 0; k < points.size(); k++) {
+            if (points[k] != point || !herr.empty()) continue;
+            v.clear();
+            m.clear();
+            std::string e;
+            if (!read_leaves(w, *bank, p, &v, &m, &e)) {
+                herr = e;
+                return;
+            }
+            std::copy(v.begin(), v.end(), out->values.begin() + voff[k]);
+            std::copy(m.begin(), m.end(), out->mass.begin() + k * nmass);
+            seen[k] = 1;
+            if (!with_reach) continue;
+            if (w.reach_len &&
+                hipMemcpy(reach.data(), dev_.reach, size_t(w.reach_len) * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+                herr = "hipMemcpy of the reach failed";
+                return;
+            }
+            float* rr = out->reach.data() + k * nreach;
+            for (uint32_t r = 0; r < w.rows(); r++) {
+                const uint32_t node = w.row_node[r];
+                for (int q = 0; q < 2; q++) {
+                    const uint32_t b = w.reach_base[2 * node + q];
+                    for (uint32_t c = 0; c < w.nc(node, q); c++) *rr++ = reach[b + c];
+                }
+            }
+        }
+    };
+    run_schedule(w, *bank, nullptr, &hook);
+    HIP_TRY(hipStreamSynchronize(stream_));
+    HIP_TRY(hipGetLastError());
+    if (!herr.empty()) {
+        *err = herr;
+        return false;
+    }
+    for (size_t k = 0; k < points.size(); k++)
+        if (!seen[k]) {
+            *err = "trace point " + std::to_string(points[k]) + " was not reached by the schedule";
+            return false;
+        }
     return true;
 }
 

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <memory>
 #include <string>
@@ -74,6 +75,18 @@ struct InFlight {
     bool live = false;
 };
 
+// Leaf-net evaluations captured during a real schedule (Executor::leaf_trace),
+// concatenated over the requested points in request order: per point the
+// value of each network row's configs of that point's traverser (row order,
+// row config order), the rows' reach masses [rows x 2], and each row's reach
+// of both players over their configs (player 0's, then player 1's).
+struct LeafTrace {
+    std::vector<float> values, mass, reach;
+};
+// A schedule point: iteration t >= 0 (traverser t & 1), or Phase 2's
+// evaluation for carried root r and player p as -(1 + 2 r + p).
+constexpr int32_t phase2_point(uint32_t root, int p) { return -(1 + 2 * (int32_t)root + p); }
+
 // The fused kernel's view of a 16-bit MLP bank.
 ChainNet chain_net(const NetBank& bank);
 // The allocation-free entry point's scratch array on `device` (current): its
@@ -118,6 +131,13 @@ class Executor {
     // traverser (row config order), and the reach masses [rows x 2].
     bool leaf_probe(const WaveHost& w, uint64_t version, int traverser, std::vector<float>* values,
                     std::vector<float>* mass, std::string* err);
+    // The same values, masses and the reach that fed them, captured inside
+    // one whole schedule right after the leaf net runs at each of `points`
+    // (iterations and Phase 2 evaluations, phase2_point): the leaf-input and
+    // value-net kernels at the reach the solve itself reaches.
+    // with_reach false: the reach is not captured (out->reach stays empty).
+    bool leaf_trace(const WaveHost& w, uint64_t version, const std::vector<int32_t>& points, bool with_reach,
+                    LeafTrace* out, std::string* err);
     // Upload once, run `warmup` untimed schedules, then `reps` timed ones; mean
     // wave time, and per-class times of one extra profiled schedule.
     bool time_wave(const WaveHost& w, uint64_t version, uint32_t warmup, uint32_t reps, double* wave_ms,
@@ -136,7 +156,15 @@ class Executor {
     // Copies the wave's tables into the pinned staging of `slot` and queues
     // their upload; sets up the device views of the wave.
     bool upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std::string* err);
-    void run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTimes* prof);
+    // hook (optional): called after every leaf-net evaluation with its
+    // schedule point and traverser.
+    using LeafHook = std::function<void(int32_t point, int p)>;
+    void run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTimes* prof, const LeafHook* hook = nullptr);
+    // After a leaf-net evaluation for traverser p: copy the head outputs and
+    // masses to the host and read each network row's config values of p by
+    // the leaf records the sweep reads (appended to values and mass).
+    bool read_leaves(const WaveHost& w, const NetBank& bank, int p, std::vector<float>* values,
+                     std::vector<float>* mass, std::string* err);
     // Pieces of the schedule: the first layer's fixed-column products, the
     // initial CFR state (strategy, reach, sums, carries, leaf inputs), both
     // players' reach under a strategy, the top regions' value and reach

@@ -1030,9 +1030,10 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         return false;
     };
     // The first failure of check(i) over [0, n) in index order (nullptr: none),
-    // checked in chunks on several host threads.
+    // checked in chunks on several host threads (small chunks for short lists
+    // of heavy items such as units).
     auto first_fail = [&](uint64_t n, auto check) -> const char* {
-        const uint64_t chunk = 4096, nch = (n + chunk - 1) / chunk;
+        const uint64_t chunk = n < 65536 ? 16 : 4096, nch = (n + chunk - 1) / chunk;
         std::vector<const char*> e(nch, nullptr);
         parallel_for(nch, [&](size_t c) {
             for (uint64_t i = c * chunk; i < std::min<uint64_t>(n, (c + 1) * chunk); i++)
@@ -1293,12 +1294,13 @@ bool validate_deep(const WaveHost& w, std::string* err) {
             return fail("record counts");
         if (first_fail(w.back_rec[p].size(), [&](uint64_t k) { return back_ok(w.back_rec[p][k]) ? nullptr : "x"; }))
             return fail("back record");
-        for (const BackRec& r : w.top_back_rec[p])
-            if (!back_ok(r)) return fail("top back record");
+        if (first_fail(w.top_back_rec[p].size(), [&](uint64_t k) { return back_ok(w.top_back_rec[p][k]) ? nullptr : "x"; }))
+            return fail("top back record");
         if (first_fail(w.reach_rec[p].size(), [&](uint64_t k) { return reach_ok(w.reach_rec[p][k]) ? nullptr : "x"; }))
             return fail("reach record");
-        for (const ReachRec& r : w.top_reach_rec[p])
-            if (!reach_ok(r)) return fail("top reach record");
+        if (first_fail(w.top_reach_rec[p].size(),
+                       [&](uint64_t k) { return reach_ok(w.top_reach_rec[p][k]) ? nullptr : "x"; }))
+            return fail("top reach record");
         if (first_fail(w.acc_rec[p].size(), [&](uint64_t k) {
                 const AccRec& r = w.acc_rec[p][k];
                 return r.ridx >= w.reach_len || uint64_t(r.lo) + r.n > w.ncells ? "x" : nullptr;

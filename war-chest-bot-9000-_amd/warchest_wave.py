@@ -27,6 +27,12 @@ MODEL_V5, MODEL_MLP, MODEL_TWO_TOWER = 5, 101, 102
 _lib = None
 
 
+def phase2_point(root: int, p: int) -> int:
+    """The schedule point of Phase 2's leaf-net evaluation for carried root `root`
+    and player p (Executor.leaf_trace)."""
+    return -(1 + 2 * root + p)
+
+
 class WaveError(RuntimeError):
     pass
 
@@ -118,7 +124,7 @@ EXPORTS = [
     "wc_result_carries", "wc_result_routes", "wc_result_free",
     "wc_executor_create", "wc_executor_destroy", "wc_executor_publish",
     "wc_wave_pack", "wc_wave_free", "wc_wave_stats_get", "wc_wave_array", "wc_value_net_plan", "wc_solve_wave",
-    "wc_launch", "wc_inflight_ready", "wc_collect", "wc_wave_leaf_probe",
+    "wc_launch", "wc_inflight_ready", "wc_collect", "wc_wave_leaf_probe", "wc_wave_leaf_trace",
     "wc_time_wave",
     "wc_mlp_forward", "wc_mlp_forward_noalloc", "wc_time_mlp",
     "wc_job_roundtrip", "wc_job_validate",
@@ -158,6 +164,9 @@ def _declare(L):
     L.wc_collect.argtypes = [C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)]
     L.wc_wave_leaf_probe.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_int, _f32p, C.c_size_t,
                                      C.POINTER(C.c_size_t), _f32p]
+    L.wc_wave_leaf_trace.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(C.c_int32), C.c_size_t,
+                                     _f32p, C.c_size_t, _f32p, C.c_size_t, _f32p, C.c_size_t,
+                                     C.POINTER(C.c_size_t)]
     L.wc_result_tag.argtypes = [C.c_void_p]
     L.wc_result_tag.restype = C.c_uint64
     L.wc_result_weight_version.argtypes = [C.c_void_p]
@@ -489,6 +498,34 @@ class Executor:
         _check(lib().wc_wave_leaf_probe(self.h, wave.h, version, traverser, vals.ctypes.data_as(_f32p), vals.size,
                                         C.byref(n), mass.ctypes.data_as(_f32p)))
         return vals[: n.value], mass[:rows]
+
+    def leaf_trace(self, wave: Wave, version: int, points, reach=True):
+        """The leaf net's values captured inside one whole schedule right after the
+        net runs at each schedule point (wc_wave_leaf_trace): t >= 0 is iteration t
+        (traverser t & 1), phase2_point(root, p) Phase 2's evaluation. One dict per
+        point: traverser, values (row order, each row's configs of the traverser),
+        mass [rows, 2], reach (each row's reach over its configs, player 0's then
+        player 1's; None with reach=False)."""
+        pts = (C.c_int32 * max(len(points), 1))(*points)
+        counts = (C.c_size_t * 4)()
+        _check(lib().wc_wave_leaf_trace(self.h, wave.h, version, pts, len(points), None, 0, None, 0, None, 0,
+                                        counts))
+        nval, rows, nreach = (counts[0], counts[1]), counts[2], counts[3]
+        trav = [pt & 1 if pt >= 0 else (-pt - 1) & 1 for pt in points]
+        vals = np.zeros(max(sum(nval[p] for p in trav), 1), np.float32)
+        mass = np.zeros(max(len(points) * 2 * rows, 1), np.float32)
+        rbuf = np.zeros(max(len(points) * nreach, 1), np.float32) if reach else None
+        _check(lib().wc_wave_leaf_trace(self.h, wave.h, version, pts, len(points), vals.ctypes.data_as(_f32p),
+                                        vals.size, mass.ctypes.data_as(_f32p), mass.size,
+                                        rbuf.ctypes.data_as(_f32p) if reach else None,
+                                        rbuf.size if reach else 0, counts))
+        out, v0 = [], 0
+        for k, (pt, p) in enumerate(zip(points, trav)):
+            out.append({"point": pt, "traverser": p, "values": vals[v0:v0 + nval[p]].copy(),
+                        "mass": mass[k * 2 * rows:(k + 1) * 2 * rows].reshape(rows, 2).copy(),
+                        "reach": rbuf[k * nreach:(k + 1) * nreach].copy() if reach else None})
+            v0 += nval[p]
+        return out
 
     def time_wave(self, wave: Wave, version: int, reps: int, warmup: int = 1):
         """Mean device ms per wave over `reps` timed schedules after `warmup` untimed
