@@ -108,6 +108,10 @@ def main():
                     help="also time the schedule captured into one HIP graph and replayed")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="after the run, copy MIB MiB device to device 3 times (calibrates HBM counters)")
+    ap.add_argument("--no-peaks", action="store_true",
+                    help="skip measuring the device's HBM and MFMA peaks (the fractions then use the datasheet only)")
+    ap.add_argument("--no-accuracy", action="store_true",
+                    help="skip comparing the timed wave's first subgames with the float32 CPU solver")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the wave executor shards whole trees across devices with no exchange, "
@@ -127,6 +131,24 @@ def main():
     st = wave.stats()
     log(f"[bench] wave: {st['nodes']} nodes, {st['cells']} cells, {st['rows']} leaf rows, {st['levels']} levels")
 
+    pk = None
+    if not args.no_peaks:
+        # What this device sustains (HIP events), measured first, on an idle device:
+        # a 16-byte copy and read over 1 GiB buffers and the f16 MFMA on register
+        # operands. Every fraction is also given against these measured peaks.
+        pk = ww.peak_probe(0, 1 << 30)
+        hbm_meas = max(pk["hbm_copy_gbs"], pk["hbm_read_gbs"])
+        mfma_meas = pk["mfma_f16_tflops"]
+        peaks = {"hbm_copy_gbs": round(pk["hbm_copy_gbs"], 1), "hbm_read_gbs": round(pk["hbm_read_gbs"], 1),
+                 "mfma_f16_tflops": round(mfma_meas, 1),
+                 "mfma_f16_16x16x32_tflops": round(pk["mfma_f16_16x16x32_tflops"], 1),
+                 "datasheet_hbm_gbs": HBM_PEAK_GBS, "datasheet_mfma_f16_tflops": MFMA_F16_PEAK_TFLOPS,
+                 "note": "measured on this device with wc_peak_probe before the timed work (MFMA: the 32x32x16 "
+                         "instruction; the 16x16x32 one the value net issues beside it); `peak` fields are the "
+                         "datasheet's, `frac_measured` fields divide by the measured peak (HBM: the larger of "
+                         "copy and read)"}
+        log(f"[bench] peaks: HBM copy {pk['hbm_copy_gbs']:.0f} GB/s, read {pk['hbm_read_gbs']:.0f} GB/s, "
+            f"f16 MFMA {mfma_meas:.0f} TFLOP/s (16x16x32: {pk['mfma_f16_16x16x32_tflops']:.0f})")
     tower = args.workload == "wave512w"
     ex = ww.Executor(0, ww.WC_BF16 if tower else ww.WC_F16)
     ver = ex.publish(net)
@@ -137,7 +159,7 @@ def main():
     node_iters = st["nodes"] * iters
     queries = st["rows"] * (iters + 2 * st["nroots_max"])
     value = node_iters / (wave_ms * 1e-3)
-    cfr_ms, mlp_ms, leaf_ms, other_ms, iter_ms, back_ms, top_ms, reach_ms, _ = parts
+    cfr_ms, mlp_ms, leaf_ms, other_ms, iter_ms, back_ms, top_ms, reach_ms = parts[:8]
     # Algorithmic bytes of one launch of each CFR kernel, averaged over the two traversers.
     kernels = {"k_sweep<regret>": (0, back_ms), "top-region launches (k_back_rows, k_reach_rows)": (1, top_ms),
                "k_reach": (2, reach_ms)}
@@ -182,6 +204,19 @@ def main():
         roofline = {"bound": "mfma", "kernel": dominant, "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 5), "flops_per_launch": round(flops),
                     "launch_ms": round(launch_ms, 5)}
+        if not tower:
+            # Algorithmic bytes of one pass launch: the pooled input columns
+            # (16-bit), the first layer's fixed-column partial products (float32
+            # accumulator tiles, when split), every weight matrix once, and one
+            # float32 head output per (row, traverser config).
+            _, n_in, hidden, layers, heads_n, pool = dims
+            trunk_flops = 2 * (n_in * hidden + (layers - 1) * hidden * hidden)
+            head_cols = (st["mlp_flops_algorithmic"] - st["rows"] * trunk_flops) // (2 * hidden)
+            in_cols = 2 * pool if fixed else n_in
+            weights = 2 * (n_in * hidden + (layers - 1) * hidden * hidden + heads_n * hidden) + \
+                4 * (layers * hidden + heads_n)
+            roofline["algorithmic_bytes"] = int(st["rows"] * in_cols * 2 + (st["rows"] * hidden * 4 if fixed else 0)
+                                                + weights + head_cols * 4)
     else:
         d = by_kernel[dominant]
         trace_name = {"k_sweep<regret>": "wc::k_sweep<0, %s>" % ("true" if st["max_window"] * 4 <= 65536 else "false"),
@@ -298,19 +333,32 @@ def main():
         vex.close()
         v_ni = vst["nodes"] * vst["iters"]
         vrows = vst["rows"]
+        vpasses = vst["iters"] + 2 * vst["nroots_max"]
         # algorithmic FLOPs: the trunk per row (8 blocks of mix 192->96 and out 96->96 over
         # 37 hexes, the pool bias 192->96, the board 207->256, the join cache 256->128) and the
         # join per row and pass (129->128, 3 x 128->128, 128->256)
         trunk = 8 * 37 * 2 * (192 * 96 + 96 * 96) + 8 * 2 * 192 * 96 + 2 * 207 * 256 + 2 * 256 * 128
         join = 2 * (129 * 128 + 3 * 128 * 128 + 128 * 256)
+        build_ms, join_ms = v_parts[9], v_parts[10]
+        # the per-wave build is the cards, the trunk and the config encoder: its
+        # fraction counts the trunk's FLOPs only (a lower bound for the trunk kernel)
+        build_tf = vrows * trunk / (build_ms * 1e-3) / 1e12 if build_ms > 0 else 0.0
+        join_tf = vrows * join * vpasses / (join_ms * 1e-3) / 1e12 if join_ms > 0 else 0.0
         out["v5_wave"] = {"workload": "wave256v5: the 256 depth-2 trees with the v5 leaf network, f16 operands",
                           "ms_per_wave": round(v_ms, 3), "node_iters_per_s": round(v_ni / (v_ms * 1e-3), 1),
                           "rows": vrows, "net_ms": round(v_parts[1], 3), "cfr_ms": round(v_parts[0], 3),
                           "trunk_gflop_per_wave": round(vrows * trunk / 1e9, 2),
                           "join_gflop_per_pass": round(vrows * join / 1e9, 3),
+                          "build_ms": round(build_ms, 3), "join_ms_per_pass": round(join_ms / vpasses, 4),
+                          "trunk_mfma": {"achieved": round(build_tf, 2), "unit": "TFLOP/s",
+                                         "frac": round(build_tf / MFMA_F16_PEAK_TFLOPS, 5),
+                                         "note": "trunk FLOPs over the whole per-wave build (cards, trunk, configs)"},
+                          "join_mfma": {"achieved": round(join_tf, 2), "unit": "TFLOP/s",
+                                        "frac": round(join_tf / MFMA_F16_PEAK_TFLOPS, 5)},
                           "note": "net_ms = the per-wave build (cards, trunk, configs) + every join and readout"}
         log(f"[bench] v5 wave: {v_ms:.2f} ms/wave ({v_parts[1]:.2f} ms in the network)")
 
+    dev_results = None
     if not args.no_host:
         # The boundary takes host buffers: the same wave through wc_solve_wave
         # (pinned upload of the packed tables, the schedule, collection and the
@@ -322,7 +370,7 @@ def main():
         reps = 3
         t = time.time()
         for _ in range(reps):
-            ex.solve(wave, ver)
+            dev_results = ex.solve(wave, ver)
         solve_ms = (time.time() - t) / reps * 1e3
         out["host_path"] = {
             "solve_ms_per_wave": round(solve_ms, 3),
@@ -372,7 +420,44 @@ def main():
                                "cpu": host, "cpu_share": share}
         log(f"[bench] CPU oracle: {sec:.1f}s, {ni / sec:.0f} node-iters/s")
 
+        if not args.no_accuracy:
+            # The timed wave's results on the sampled subgames against the float32
+            # CPU solver: root errors relative to each subgame's largest root value,
+            # the reference's gate for its fast head (engine/src/gpu/tests.rs:413-444),
+            # and mean strategy errors. Outside the timed region.
+            from concurrent.futures import ThreadPoolExecutor
+
+            if dev_results is None:
+                dev_results = ex.solve(wave, ver)
+            with ThreadPoolExecutor(threads) as pool:
+                refs = list(pool.map(lambda j: O.solve(j, net, O.NET_F32), sample))
+            rel, gate, ms_err = [], [], []
+            for g, o in zip(dev_results, refs):
+                a, b = g.root_values.astype(np.float64), o["roots"].astype(np.float64)
+                rel.append(float(np.abs(a - b).max() / np.abs(b).max()))
+                gate.append(float((np.abs(a - b) / (1e-2 + 2e-3 * np.maximum(np.abs(a), np.abs(b)))).max()))
+                ms_err.append(float(np.abs(g.strategy - o["strategy"]).mean()))
+            rel = np.array(rel)
+            out["accuracy"] = {
+                "against": f"float32 CPU solver (the oracle), first {n} of the {len(jobs)} subgames",
+                "root_rel_err_median": float(np.median(rel)), "root_rel_err_max": float(rel.max()),
+                "subgames_within_2e-3": int((rel <= 2e-3).sum()), "subgames": n,
+                "root_gate_ratio_max": round(max(gate), 4), "mean_strategy_err_max": float(max(ms_err)),
+                "note": "root errors relative to each subgame's largest |root value|; root_gate_ratio = |d| / "
+                        "(1e-2 + 2e-3 |x|), the reference's bound for its fast head (<= 1 passes)"}
+            log(f"[bench] accuracy: root error median {np.median(rel):.2e}, max {rel.max():.2e}, "
+                f"{int((rel <= 2e-3).sum())} of {n} within 2e-3, gate ratio {max(gate):.2f}")
+
     ex.close()
+    if pk is not None:
+        out["peaks"] = peaks
+        for r in (out.get("roofline"), out.get("roofline_cfr_iteration"), out.get("roofline_mlp_in_wave"),
+                  out.get("roofline_leaf_input"), out.get("mlp_alone"), out.get("v5_wave", {}).get("trunk_mfma"),
+                  out.get("v5_wave", {}).get("join_mfma")):
+            if r:
+                r["frac_measured"] = round(r["achieved"] / (mfma_meas if r.get("unit") == "TFLOP/s" else hbm_meas), 5)
+        for d in out["roofline_cfr_iteration"]["kernels"].values():
+            d["frac_measured"] = round(d["achieved_gbs"] / hbm_meas, 5)
     if args.copy_probe:
         # A plain device-to-device copy through the HIP runtime's blit kernel:
         # the reference point that scales the HBM byte counters.

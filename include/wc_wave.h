@@ -238,17 +238,31 @@ int wc_wave_leaf_trace(wc_executor* ex, wc_wave* w, uint64_t version, const int3
 /* Benchmark helper: upload once, run the full schedule `warmup` times
  * untimed, then `reps` times timed (inputs resident in HBM), returning the
  * mean device time per wave in milliseconds, measured with HIP events on the
- * executor's stream. kernel_ms (optional, 9 doubles) receives one profiled
- * schedule's device time per launch class: [0] CFR sweeps, [1] leaf MLP,
+ * executor's stream. kernel_ms (optional, 11 doubles) receives one profiled
+ * schedule's device time per launch class: [0] CFR sweeps, [1] leaf net (all
+ * of it, [9] and [10] included),
  * [2] leaf input, [3] everything else; [4] the mean device time of one CFR
  * iteration (all its sweep kernels), and the mean device time per iteration of
  * [5] the subtree value sweep, [6] the top-region launches (values and reach,
  * one launch per depth each), [7] the subtree reach sweep; [8] the host time
  * to capture and instantiate the schedule as one HIP graph (0 when the
  * executor runs without graphs: the environment variable WC_GRAPH=1 at
- * executor creation turns them on). */
+ * executor creation turns them on); [9] the leaf net's per-wave work (the v5
+ * network's cards, trunk and config encoder; the two-tower net's private
+ * tower; the MLP's fixed-column products); [10] the v5 network's joins over
+ * the schedule (0 for the other nets). */
 int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup, uint32_t reps, double* wave_ms,
                  double* kernel_ms);
+
+/* Measurement helper (no counterpart in the reference): what this device
+ * sustains, timed with HIP events. copy_gbs: a 16-byte nontemporal load/store
+ * copy over two buffers of `bytes` (read + write traffic per second);
+ * read_gbs: the same loads alone; mfma_tflops: v_mfma_f32_32x32x16_f16 on
+ * register operands (f16 dense); mfma16_tflops: the same for
+ * v_mfma_f32_16x16x32_f16, the instruction the fused value net issues.
+ * Allocates 2 x bytes of device memory for the call. */
+int wc_peak_probe(int device, size_t bytes, double* copy_gbs, double* read_gbs, double* mfma_tflops,
+                  double* mfma16_tflops);
 
 /* Leaf-net inference alone (the value-net GEMM chain): x is rows x in f32 on
  * the host; out receives rows x heads f32 (head rows 0..heads-1). */

@@ -70,6 +70,7 @@ def lib():
         L.oracle_v5_board.argtypes = net5 + [u8p, C.c_uint32, f32p, f32p, f32p]
         L.oracle_v5_configs.argtypes = net5 + [f32p, u8p, C.c_uint32, f32p, f32p, f32p]
         L.oracle_v5_join.argtypes = net5 + [f32p, f32p, f32p, C.c_uint32, C.c_int, f32p]
+        L.oracle_v5_block.argtypes = net5 + [f32p, C.c_uint32, C.c_int]
         L.oracle_v5_gelu.argtypes = [C.c_float, C.c_int]
         L.oracle_v5_gelu.restype = C.c_float
         L.oracle_v5_set_libm_tanh.argtypes = [C.c_int]
@@ -294,6 +295,15 @@ def v5_join(net, P, Jp, pooled, player, mode=NET_F32, libm=False):
                             _p(h, C.c_float)) != 0:
         raise ValueError("v5 join")
     return h
+
+
+def v5_block(net, x, block, mode=NET_F32, libm=False):
+    """One residual block of the board trunk on x [rows, 37, 96]: the block's output."""
+    keep, a = _v5_net(net, mode, libm)
+    out = np.array(x, np.float32, copy=True, order="C")
+    if lib().oracle_v5_block(*a, _p(out, C.c_float), out.shape[0], int(block)) != 0:
+        raise ValueError("v5 block")
+    return out
 
 
 def v5_gelu(x, libm=False):

@@ -403,6 +403,42 @@ void v5_cards(const V5* n, const float* card_feat, float* cards) {
         }
 }
 
+/* Residual block i over one row's hexes, in place on x [HEXES][C]; a and y
+ * are [HEXES][C] scratch, z [C] (net.rs:548-595). */
+static void trunk_block(const V5* n, int i, float* x, float* a, float* y, float* z) {
+    const Layout* L = &n->L;
+    enum { H = V5_HEXES, C = V5_C };
+    float mixed[2 * V5_C], pooled[2 * V5_C], gb[V5_C];
+    memcpy(a, x, sizeof(float) * H * C);
+    for (int h = 0; h < H; h++) norm(n, ln_block(i, 0), a + (size_t)h * C, 1);
+    for (int j = 0; j < C; j++) {
+        float mean = 0.0f, top = -INFINITY;
+        for (int h = 0; h < H; h++) {
+            const float v = a[(size_t)h * C + j];
+            mean += v / (float)H;
+            top = fmaxf(top, v);
+        }
+        pooled[j] = mean;
+        pooled[C + j] = top;
+    }
+    apply_lin(n, L->poolm[i], 1, pooled, NULL, gb);
+    for (int h = 0; h < H; h++) {
+        memcpy(mixed, a + (size_t)h * C, sizeof(float) * C);
+        for (int j = 0; j < C; j++) mixed[C + j] = 0.0f;
+        for (int d = 0; d < 6; d++) {
+            const int nh = g_nb[h][d];
+            if (nh < 0) continue;
+            for (int j = 0; j < C; j++) mixed[C + j] += a[(size_t)nh * C + j];
+        }
+        float* yh = y + (size_t)h * C;
+        apply_lin(n, L->mix[i], 1, mixed, NULL, yh);
+        for (int j = 0; j < C; j++) yh[j] += gb[j];
+        norm(n, ln_block(i, 1), yh, 1);
+        apply_lin(n, L->out[i], 1, yh, NULL, z);
+        for (int j = 0; j < C; j++) x[(size_t)h * C + j] += z[j];
+    }
+}
+
 void v5_board(const V5* n, const uint8_t* raw, const float* cards, float* P, float* Jp) {
     const Layout* L = &n->L;
     enum { H = V5_HEXES, C = V5_C };
@@ -412,7 +448,7 @@ void v5_board(const V5* n, const uint8_t* raw, const float* cards, float* P, flo
     float* a = (float*)malloc(sizeof(float) * H * C);
     float* y = (float*)malloc(sizeof(float) * H * C);
     float* z = (float*)malloc(sizeof(float) * C);
-    float mixed[2 * V5_C], pooled[2 * V5_C], gb[V5_C], tp[V5_C], glob[V5_C], loose[V5_LOOSE], piles[V5_PILE_COUNTS];
+    float tp[V5_C], glob[V5_C], loose[V5_LOOSE], piles[V5_PILE_COUNTS];
     float facts[V5_HEX_FACTS];
     int occ[V5_HEXES];
     /* tokens (net.rs:474-495): pile counts through `pile`, then card + seat */
@@ -443,37 +479,7 @@ void v5_board(const V5* n, const uint8_t* raw, const float* cards, float* P, flo
             const float o = occ[h] >= 0 ? proj[(size_t)occ[h] * C + j] : 0.0f;
             x[(size_t)h * C + j] += o + pos[(size_t)h * C + j] + glob[j] + tp[j];
         }
-    /* residual blocks (net.rs:548-595) */
-    for (int i = 0; i < V5_BLOCKS; i++) {
-        memcpy(a, x, sizeof(float) * H * C);
-        for (int h = 0; h < H; h++) norm(n, ln_block(i, 0), a + (size_t)h * C, 1);
-        for (int j = 0; j < C; j++) {
-            float mean = 0.0f, top = -INFINITY;
-            for (int h = 0; h < H; h++) {
-                const float v = a[(size_t)h * C + j];
-                mean += v / (float)H;
-                top = fmaxf(top, v);
-            }
-            pooled[j] = mean;
-            pooled[C + j] = top;
-        }
-        apply_lin(n, L->poolm[i], 1, pooled, NULL, gb);
-        for (int h = 0; h < H; h++) {
-            memcpy(mixed, a + (size_t)h * C, sizeof(float) * C);
-            for (int j = 0; j < C; j++) mixed[C + j] = 0.0f;
-            for (int d = 0; d < 6; d++) {
-                const int nh = g_nb[h][d];
-                if (nh < 0) continue;
-                for (int j = 0; j < C; j++) mixed[C + j] += a[(size_t)nh * C + j];
-            }
-            float* yh = y + (size_t)h * C;
-            apply_lin(n, L->mix[i], 1, mixed, NULL, yh);
-            for (int j = 0; j < C; j++) yh[j] += gb[j];
-            norm(n, ln_block(i, 1), yh, 1);
-            apply_lin(n, L->out[i], 1, yh, NULL, z);
-            for (int j = 0; j < C; j++) x[(size_t)h * C + j] += z[j];
-        }
-    }
+    for (int i = 0; i < V5_BLOCKS; i++) trunk_block(n, i, x, a, y, z);
     for (int h = 0; h < H; h++) norm(n, LN_TRUNK, x + (size_t)h * C, 1);
     /* board vector (net.rs:700-723) and the join cache (net.rs:728-730) */
     float input[2 * V5_C + V5_LOOSE];
@@ -596,6 +602,23 @@ int oracle_v5_board(int mode, const float* w, size_t nw, const float* b, size_t 
     if (!n) return -1;
     for (uint32_t r = 0; r < rows; r++)
         v5_board(n, raw + (size_t)r * V5_ROW_BYTES, cards, P + (size_t)r * V5_D, Jp + (size_t)r * V5_JW);
+    v5_free(n);
+    return 0;
+}
+
+/* Residual block `block` of the trunk, in place on x [rows][HEXES][C]. */
+int oracle_v5_block(int mode, const float* w, size_t nw, const float* b, size_t nb, const float* ln, size_t nln,
+                    int libm, float* x, uint32_t rows, int block) {
+    if (block < 0 || block >= V5_BLOCKS) return -1;
+    V5* n = piece_net(mode, w, nw, b, nb, ln, nln, libm);
+    if (!n) return -1;
+    const size_t cells = (size_t)V5_HEXES * V5_C;
+    float* a = (float*)malloc(sizeof(float) * cells);
+    float* y = (float*)malloc(sizeof(float) * cells);
+    float z[V5_C];
+    for (uint32_t r = 0; r < rows; r++) trunk_block(n, block, x + (size_t)r * cells, a, y, z);
+    free(a);
+    free(y);
     v5_free(n);
     return 0;
 }

@@ -8,7 +8,17 @@ the C ABI, against the oracle's restatement of engine/src/net.rs:
 - the zero network: every leaf valued at value_bias;
 - 16-bit operands: the leaf values track the oracle's model of the same
   operand rounding;
-- jobs tagged [5] through the service boundary, bit-identical in float32.
+- jobs tagged [5] through the service boundary, bit-identical in float32;
+- whole f16 solves held to the reference's own gate for its fast tensor-core
+  head (engine/src/gpu/tests.rs:393-446) on its own test network and
+  schedule: root values within 1e-2 + 2e-3 |x| of the float32 solve, mean
+  strategy error <= 5e-3, strategy entries within 0.4 + 0.1 |x|; bf16 solves
+  near float32;
+- inside the benchmarked wave's full-shape solves (random-init network, 64
+  iterations), at iterations 0, 1, 2, 31, 63 and Phase 2, the leaf values
+  against the 16-bit operand model at the device's own reach, and the
+  oracle's replay of the device's own leaf values equal to the device's solve
+  bit for bit.
 """
 import os
 import sys
@@ -217,3 +227,129 @@ def test_v5_trunk_partial_workgroups():
     finally:
         scalar.close()
     assert seen == {1, 2, 3}, seen
+
+
+def reference_test_weights():
+    """The reference's GPU-test network (engine/src/gpu/tests.rs:34-46): every weight
+    (next_u64 / u64::MAX - 0.5) * 0.1 in float32 from its xorshift64* stream
+    (engine/src/rng.rs:8-21) seeded 0xD15EA5E, biases zero, LayerNorm gains one and
+    shifts zero."""
+    nw, nb = ww.net_sizes(ww.V5_DIMS)
+    nln = ww.net_norms(ww.V5_DIMS)
+    m = (1 << 64) - 1
+    x = 0xD15EA5E ^ 0x9E3779B97F4A7C15
+    raw = np.empty(nw, np.uint64)
+    for k in range(nw):
+        x ^= x >> 12
+        x ^= (x << 25) & m
+        x ^= x >> 27
+        raw[k] = (x * 0x2545F4914F6CDD1D) & m
+    w = (raw.astype(np.float32) / np.float32(m) - np.float32(0.5)) * np.float32(0.1)
+    ln = np.zeros(nln, np.float32)
+    at = 0
+    # per norm, its gains then its shifts (net.rs:272-316 order): 16 trunk-block
+    # norms of 96, the trunk's 96, the config encoder's 128, three join-block
+    # norms of 128, the join output's 128, the head's 256
+    for width in [96] * 16 + [96, 128] + [128] * 3 + [128, 256]:
+        ln[at:at + width] = 1.0
+        at += 2 * width
+    assert at == nln
+    return ww.Net(list(ww.V5_DIMS), w, np.zeros(nb, np.float32), ln)
+
+
+LINEAR = dict(alpha=1.0, beta=1.0, gamma=1.0, predict=0.0)  # Cfr::LINEAR, engine/src/search.rs:141-146
+
+
+def gate_ratios(g, o):
+    """engine/src/gpu/tests.rs:413-444: cmp(a, b, atol, rtol) is |a - b| <= atol + rtol
+    max(|a|, |b|) elementwise; roots at (1e-2, 2e-3), strategy entries at (0.4, 0.1)."""
+    def ratio(a, b, atol, rtol):
+        a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+        return np.abs(a - b) / (atol + rtol * np.maximum(np.abs(a), np.abs(b)))
+
+    pw = ratio(g.strategy, o["strategy"], 0.4, 0.1)
+    return (float(ratio(g.root_values, o["roots"], 1e-2, 2e-3).max()), float(np.abs(g.strategy - o["strategy"]).mean()),
+            float(pw.max()), float((pw > 1.0).mean()))
+
+
+def v5_full_shape(trees=8, **kw):
+    import workloads as W
+    return W.jobs("wave256v5", **kw)[:trees]
+
+
+@pytest.mark.parametrize("shape", ["small", "full"])
+def test_v5_f16_solves_meet_the_references_gate(shape):
+    """Whole f16 v5 solves against the float32 solver under the reference's gate for
+    its fast tensor-core head (engine/src/gpu/tests.rs:393-446), on the reference's
+    own test network and schedule (8 linear-CFR iterations, depth 2): root values
+    within 1e-2 + 2e-3 |x|, mean strategy error <= 5e-3, and every strategy entry
+    within 0.4 + 0.1 |x|. Eight small subgames and eight subgames of the benchmarked
+    v5 wave at full shape (200..800 nodes, infostates up to 567). On the full-shape
+    ones a near-tie flips single strategy entries under any f16 evaluation (the
+    oracle's f16 model itself exceeds the pointwise guard on one of them), so there
+    at most 1 in 1,000 entries may lie outside the guard; with the random-init
+    network of the v5 workloads and 64 iterations the gate is out of reach of any
+    16-bit evaluation (tests/test_gpu_trace.py and the replay below judge those)."""
+    net = reference_test_weights()
+    jobs = v5_jobs(trees=8, seed=43, iters=8, **LINEAR) if shape == "small" else \
+        v5_full_shape(iters=8, **LINEAR)
+    say(f"case v5 f16 reference gate: {len(jobs)} {shape} subgames, the reference's test network")
+    ex = executor(ww.WC_F16)
+    v = ex.publish(net)
+    wave = ww.Wave(jobs)
+    got = ex.solve(wave, v)
+    wave.close()
+    refs = pmap(lambda j: O.solve(j, net, O.NET_F32), jobs)
+    for k, (g, o) in enumerate(zip(got, refs)):
+        rr, ms, pw, out = gate_ratios(g, o)
+        say(f"v5 {shape} tree {k}: roots {rr:.2f} of the gate, mean strategy error {ms:.1e}, pointwise {pw:.2f} of "
+            f"the guard ({out:.1e} of the entries outside)")
+        assert rr <= 1.0 and ms <= 5e-3, f"tree {k}"
+        assert (pw <= 1.0) if shape == "small" else (out <= 1e-3), f"tree {k}"
+
+
+def test_v5_bf16_solves_track_float32():
+    """bf16 v5 solves (the reference gates only its f16 mode) on the same network and
+    schedule, judged by what bf16 operands do by themselves: per subgame the root
+    error within max(5e-2, 3x the oracle's bf16 model's), mean strategy error
+    <= 1.5e-2 (the bf16 whales' bounds); the median root error within 2x the
+    model's."""
+    net = reference_test_weights()
+    jobs = v5_jobs(trees=8, seed=43, iters=8, **LINEAR) + v5_full_shape(trees=4, iters=8, **LINEAR)
+    say(f"case v5 bf16: {len(jobs)} subgames, the reference's test network")
+    ex = executor(ww.WC_BF16)
+    v = ex.publish(net)
+    wave = ww.Wave(jobs)
+    got = ex.solve(wave, v)
+    wave.close()
+    refs = pmap(lambda j: O.solve(j, net, O.NET_F32), jobs)
+    emus = pmap(lambda j: O.solve(j, net, O.NET_BF16A), jobs)
+    devs, models = [], []
+    for k, (g, o, e) in enumerate(zip(got, refs, emus)):
+        scale = float(np.abs(o["roots"]).max())
+        rel = float(np.abs(g.root_values - o["roots"]).max()) / scale
+        emu = float(np.abs(e["roots"] - o["roots"]).max()) / scale
+        ms = float(np.abs(g.strategy - o["strategy"]).mean())
+        say(f"v5 bf16 tree {k}: root error {rel:.1e} of the largest root value (bf16 model {emu:.1e}), mean "
+            f"strategy error {ms:.1e}")
+        assert rel <= max(5e-2, 3 * emu) and ms <= 1.5e-2, f"tree {k}"
+        devs.append(rel)
+        models.append(emu)
+    assert np.median(devs) <= 2 * np.median(models) + 1e-4
+
+
+@pytest.mark.parametrize("precision,mode,tol", [(ww.WC_F16, O.NET_F16A, 3e-3), (ww.WC_BF16, O.NET_BF16A, 3e-2)])
+def test_v5_trace_tracks_the_operand_model_at_the_solves_reach(precision, mode, tol):
+    """The v5 leaf values inside the full-shape solves (the per-iteration pooling of
+    g(c), the join and the readout on the device's own reach) against the 16-bit
+    model, with the initial-reach probe's bounds (median within tol / 6)."""
+    from test_gpu_trace import check_trace_against_model
+    check_trace_against_model(precision, mode, tol, v5_full_shape(), ww.synth_weights(ww.V5_DIMS, 1),
+                              "wave256v5 full shape", median=1 / 6)
+
+
+@pytest.mark.parametrize("precision", [ww.WC_F16, ww.WC_BF16])
+def test_v5_replay_of_16bit_solves_bit_exact(precision):
+    from test_gpu_trace import replay_and_compare
+    say(f"case v5 replay precision {precision}: full-shape subgames, every leaf evaluation")
+    replay_and_compare(precision, v5_full_shape(), ww.synth_weights(ww.V5_DIMS, 1), f"wave256v5 {precision}")

@@ -217,19 +217,22 @@ def test_wave512w_whales_float32_bit_exact_and_bf16_near_float32():
         mean_s = float(np.abs(b.strategy - o["strategy"]).mean())
         tol = 0.4 + 0.1 * np.maximum(np.abs(b.strategy), np.abs(o["strategy"]))
         ratio = float((np.abs(b.strategy - o["strategy"]) / tol).max())
+        outside = float((np.abs(b.strategy - o["strategy"]) > tol).mean())
         rel = np.abs(b.root_values - o["roots"]).max() / np.abs(o["roots"]).max()
         say(f"tree {k}: float32 bit-exact; bf16 mean strategy error {mean_s:.2e}, pointwise guard ratio "
-            f"{ratio:.2f}, root error {rel:.2e} of the largest root value")
+            f"{ratio:.2f} ({outside:.1e} of the entries outside), root error {rel:.2e} of the largest root value")
         # bf16 keeps 8 significant bits: over the 64-subgame wave its emulation's
         # mean strategy error reaches 1.4e-2 and its root error 0.25 (median 6e-3).
-        # A near-tie between two actions can flip one strategy entry: the
+        # A near-tie between two actions can flip single strategy entries: the
         # reference's pointwise guard 0.4 + 0.1|x| (engine/src/gpu/tests.rs:436-443)
-        # measures 1.9-2.0 of its bound here, so it is held at 2.5 (the replay in
-        # tests/test_gpu_trace.py shows the flips are the solve's, given its leaf
-        # values).
+        # measures 1.9-2.0 of its bound here (a ratio bound of 2.5 would bind
+        # nothing: probabilities differ by at most 1 and the guard is at least
+        # 0.4), so at most 1 in 1,000 entries may lie outside it. The replay in
+        # tests/test_gpu_trace.py shows the flips are the solve's own, given its
+        # leaf values.
         assert mean_s <= 1.5e-2, f"tree {k}"
         assert rel <= 5e-2, f"tree {k}"
-        assert ratio <= 2.5, f"tree {k}: pointwise guard ratio {ratio:.2f}"
+        assert outside <= 1e-3, f"tree {k}: {outside:.1e} of the strategy entries outside the pointwise guard"
 
 
 def test_wave512w_whale_leaf_probe_bf16():

@@ -12,7 +12,11 @@ checks that do not share its code:
   tolerance);
 - special cases: a network with every matrix and bias zero values every leaf
   at value_bias; the config encoder does not depend on the order of a
-  config's coin slots (net.rs:751-757: a sum over slot tokens).
+  config's coin slots (net.rs:751-757: a sum over slot tokens);
+- the 16-bit models (NET_F16 / NET_F16A / NET_BF16 / NET_BF16A) against the
+  torch restatement with the operands of exactly the tensor-core products
+  rounded, piece by piece, and with any one of them left unrounded (a planted
+  mistake, which the comparison must see).
 """
 import math
 
@@ -191,3 +195,56 @@ def test_reduced_models_track_float32(net):
         err = float(np.abs(got - exact).max()) / scale
         print(f"mode {mode}: {err:.2e}")
         assert err < tol
+
+
+def _median_rel(got, want):
+    want = np.asarray(want, np.float64)
+    return float(np.median(np.abs(np.asarray(got, np.float64) - want)) / max(float(np.abs(want).max()), 1e-30))
+
+
+@pytest.mark.parametrize("kind,mode", [("f16", O.NET_F16), ("f16", O.NET_F16A), ("bf16", O.NET_BF16),
+                                       ("bf16", O.NET_BF16A)])
+def test_16bit_models_round_exactly_the_fast_products(net, kind, mode):
+    """The oracle's 16-bit v5 models (what the device's fast path is held to)
+    round the operands of exactly the products the reference runs on tensor
+    cores (T.FAST): piece by piece, each model agrees with the float64 torch
+    restatement that rounds those products' operands to a median of a few
+    float32 roundings (<= 2e-7 of the largest value), while the same
+    restatement with any one of those products left unrounded, the planted
+    mistake, moves the piece it feeds by a median >= 5e-6 (measured 1.7e-5 ..
+    7e-4). One trunk block is compared alone, on float32 inputs: through eight
+    blocks a single activation that rounds to the neighbouring 16-bit value
+    spreads to the level of the whole rounding effect."""
+    [job] = v5_jobs(trees=1, seed=11)
+    cf, raw, phi, owner = piece_inputs(job)
+    crd32 = O.v5_cards(net, cf)
+    P, Jp = O.v5_board(net, raw, crd32)
+    pooled = np.random.default_rng(5).random((P.shape[0], 2, 64)).astype(np.float32)
+    b32 = T.Blob(net)
+    x = T.stem(b32, raw, T.cards(b32, cf))[0]
+    for i in range(3):
+        x = T.block(b32, i, x)
+    x32 = x.numpy().astype(np.float32)
+    tx = torch.tensor(x32.astype(np.float64))
+
+    def pieces(blob):
+        tf, tg = T.configs(blob, phi, owner, torch.tensor(crd32.astype(np.float64)))
+        return {"cards": T.cards(blob, cf).numpy(), "f": tf.numpy(), "g": tg.numpy(),
+                "block": T.block(blob, 3, tx).numpy(), "h": T.join(blob, P, Jp, pooled, 1).numpy()}
+
+    f, g = O.v5_configs(net, phi, owner, crd32, mode)
+    got = {"cards": O.v5_cards(net, cf, mode), "f": f, "g": g, "block": O.v5_block(net, x32, 3, mode),
+           "h": O.v5_join(net, P, Jp, pooled, 1, mode)}
+    want = pieces(T.Blob(net).round(kind))
+    for k in got:
+        e = _median_rel(got[k], want[k])
+        print(f"{kind} model {mode}, {k}: median {e:.1e} of the largest value")
+        assert e <= 2e-7, k
+    feeds = {"card": ["cards"], "cfg1": ["f", "g"], "cfg_f": ["f"], "cfg_g": ["g"], "cfg_m": ["g"], "mix": ["block"],
+             "out": ["block"], "poolm": ["block"], "join_b": ["h"], "join_w": ["h"], "join_out": ["h"]}
+    for name, hit in feeds.items():
+        planted = pieces(T.Blob(net).round(kind, T.FAST - {name}))
+        for k in hit:
+            e = _median_rel(got[k], planted[k])
+            print(f"{kind} model {mode}, {name} left unrounded: {k} median {e:.1e}")
+            assert e >= 5e-6, (name, k)

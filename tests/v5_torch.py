@@ -8,12 +8,24 @@ It shares no code with oracle/v5.c: the blob layout is re-derived here from
 NetLayout::new's order (net.rs:272-316) and the public-row expansion from the
 GPU row layout (rebel.rs:966-986) and write_public_features_raw
 (rebel.rs:1144-1233).
+
+Rounded operands: with Blob.round(kind, names), the products named in `names`
+take both operands rounded to f16 or bf16 (each value first to float32, as the
+float32 activations it stands for, then to nearest-even), with the products and
+their sums in float64. FAST names the products the reference's fast mode runs
+on tensor cores (device.rs:836-1106, 1218-1305: the card describer, the
+config encoder, every trunk block's mix, out and pool-bias products, the board
+and join-cache projections, the join and the readout); the stem's small
+products (pile counts, hex facts, token projection, loose scalars) stay
+float32.
 """
 import numpy as np
 import torch
 import torch.nn.functional as F
 
 TYPE, C, BLOCKS, D, POOL, CFGH, JW, JBLOCKS = 64, 96, 8, 256, 64, 128, 128, 3
+FAST = frozenset({"card", "poolm", "mix", "out", "board_out", "join_p", "cfg1", "cfg_f", "cfg_g", "cfg_m", "join_b",
+                  "join_w", "join_out", "values"})
 JOIN_IN, HEXES, NSLOT, NTYPE, HEX_FACTS, PILES, CARD_FEATS, CFEAT, LOOSE = 129, 37, 5, 10, 6, 4, 25, 15, 15
 ROW = 201
 
@@ -40,6 +52,7 @@ class Blob:
         ln = torch.tensor(np.asarray(net.ln, np.float64))
         self.at_w = self.at_b = self.at_ln = 0
         self.w, self.b, self.lnv = w, b, ln
+        self.q, self.fast = None, frozenset()
 
         def lin(i, o, bias=True):
             W = self.w[self.at_w:self.at_w + i * o].reshape(i, o)
@@ -83,11 +96,20 @@ class Blob:
             self.norms.append((g, bt))
         assert (self.at_w, self.at_b, self.at_ln) == (len(w), len(b), len(ln))
 
+    def round(self, kind, names=FAST):
+        """Round both operands of the products in `names` to `kind` ("f16" or "bf16")."""
+        dt = {"f16": torch.float16, "bf16": torch.bfloat16}[kind]
+        self.q = lambda t: t.to(torch.float32).to(dt).to(torch.float64)
+        self.fast = frozenset(names)
+        return self
 
-def _lin(p, x):
-    W, B = p
-    y = x @ W
-    return y if B is None else y + B
+    def lin(self, name, p, x):
+        """x W (+ b), the operands rounded when `name` is a rounded product."""
+        W, B = p
+        if self.q is not None and name in self.fast:
+            x, W = self.q(x), self.q(W)
+        y = x @ W
+        return y if B is None else y + B
 
 
 def _ln(p, x, act=True):
@@ -105,7 +127,7 @@ def cards(blob, card_feat):
     cf = torch.tensor(np.asarray(card_feat, np.float64).reshape(NTYPE, CARD_FEATS))
     idx = torch.tensor([[_phys(v, t) for t in range(NTYPE)] for v in range(2)])
     x = cf[idx]
-    return _lin(blob.card[1], F.gelu(_lin(blob.card[0], x), approximate="tanh"))
+    return blob.lin("card", blob.card[1], F.gelu(blob.lin("card", blob.card[0], x), approximate="tanh"))
 
 
 def expand(raw):
@@ -129,29 +151,40 @@ def expand(raw):
             torch.tensor(np.stack(loose, axis=-1), dtype=torch.float64))
 
 
+def stem(blob, raw, crd):
+    """The trunk's input x [R, 37, C] and the loose scalars [R, 15] (net.rs:474-543)."""
+    facts, occ, piles, loose = expand(raw)
+    R = facts.shape[0]
+    tok = blob.lin("pile", blob.pile, piles) + crd[0][None] + blob.seat[torch.arange(NTYPE) // NSLOT][None]
+    proj = blob.lin("tok_stem", blob.tok_stem, tok)                 # [R, 10, C]
+    tp = F.gelu(proj, approximate="tanh").mean(dim=1)               # [R, C]
+    glob = blob.lin("glob_stem", blob.glob_stem, loose)
+    occp = torch.where((occ >= 0)[..., None], proj[torch.arange(R)[:, None], occ.clamp(min=0)], torch.zeros(()))
+    x = blob.lin("hex_stem", blob.hex_stem, facts) + occp + blob.pos[None] + glob[:, None] + tp[:, None]
+    return x, loose
+
+
+def block(blob, i, x):
+    """Residual block i on x [R, 37, C] (net.rs:548-595)."""
+    mix, pool, out = blob.blocks[i]
+    nb = torch.tensor(board()[0])
+    a = _ln(blob.norms[2 * i], x)
+    pad = torch.cat([a, torch.zeros(x.shape[0], 1, C, dtype=a.dtype)], dim=1)
+    neigh = pad[:, nb].sum(dim=2)                                    # [R, 37, C]
+    y = blob.lin("mix", mix, torch.cat([a, neigh], dim=-1))
+    gb = blob.lin("poolm", pool, torch.cat([a.mean(dim=1), a.amax(dim=1)], dim=-1))
+    y = _ln(blob.norms[2 * i + 1], y + gb[:, None])
+    return x + blob.lin("out", out, y)
+
+
 def board_vectors(blob, raw, crd):
     """Net::board and join_cache: P [R, D], Jp [R, JW]."""
-    facts, occ, piles, loose = expand(raw)
-    nb, _ = board()
-    nb = torch.tensor(nb)
-    R = facts.shape[0]
-    tok = piles @ blob.pile[0] + crd[0][None] + blob.seat[torch.arange(NTYPE) // NSLOT][None]
-    proj = tok @ blob.tok_stem[0]                                   # [R, 10, C]
-    tp = F.gelu(proj, approximate="tanh").mean(dim=1)               # [R, C]
-    glob = loose @ blob.glob_stem[0]
-    occp = torch.where((occ >= 0)[..., None], proj[torch.arange(R)[:, None], occ.clamp(min=0)], torch.zeros(()))
-    x = _lin(blob.hex_stem, facts) + occp + blob.pos[None] + glob[:, None] + tp[:, None]
-    for i, (mix, pool, out) in enumerate(blob.blocks):
-        a = _ln(blob.norms[2 * i], x)
-        pad = torch.cat([a, torch.zeros(R, 1, C, dtype=a.dtype)], dim=1)
-        neigh = pad[:, nb].sum(dim=2)                                # [R, 37, C]
-        y = _lin(mix, torch.cat([a, neigh], dim=-1))
-        gb = _lin(pool, torch.cat([a.mean(dim=1), a.amax(dim=1)], dim=-1))
-        y = _ln(blob.norms[2 * i + 1], y + gb[:, None])
-        x = x + _lin(out, y)
+    x, loose = stem(blob, raw, crd)
+    for i in range(BLOCKS):
+        x = block(blob, i, x)
     x = _ln(blob.norms[2 * BLOCKS], x)
-    P = _lin(blob.board_out, torch.cat([x.mean(dim=1), x.amax(dim=1), loose], dim=-1))
-    return P, P @ blob.join_p[0]
+    P = blob.lin("board_out", blob.board_out, torch.cat([x.mean(dim=1), x.amax(dim=1), loose], dim=-1))
+    return P, blob.lin("join_p", blob.join_p, P)
 
 
 def configs(blob, phi, owner, crd):
@@ -160,11 +193,11 @@ def configs(blob, phi, owner, crd):
     owner = torch.tensor(np.asarray(owner, np.int64))
     counts = phi.reshape(-1, 3, NSLOT).transpose(1, 2)                 # [n, slot, zone]
     slots = torch.cat([counts, crd[owner][:, :NSLOT]], dim=-1)         # [n, 5, 3 + TYPE]
-    u = F.gelu(_lin(blob.cfg1, slots), approximate="tanh").sum(dim=1)
+    u = F.gelu(blob.lin("cfg1", blob.cfg1, slots), approximate="tanh").sum(dim=1)
     u = _ln(blob.norms[2 * BLOCKS + 1], u)
-    f = _lin(blob.cfg_f, u)
-    g = _lin(blob.cfg_g, u)
-    bag = (crd @ blob.cfg_m[0]).reshape(2, NTYPE, 3, POOL)             # [view, token, zone, POOL]
+    f = blob.lin("cfg_f", blob.cfg_f, u)
+    g = blob.lin("cfg_g", blob.cfg_g, u)
+    bag = blob.lin("cfg_m", blob.cfg_m, crd).reshape(2, NTYPE, 3, POOL)             # [view, token, zone, POOL]
     g = g + torch.einsum("nkz,nkzj->nj", counts, bag[owner][:, :NSLOT])
     return f, g
 
@@ -173,13 +206,14 @@ def join(blob, P, Jp, pooled, player):
     """Net::join: h [R, D] from pooled [R, 2, POOL] (the player's block first)."""
     P, Jp, pooled = (torch.as_tensor(np.asarray(v, np.float64)) for v in (P, Jp, pooled))
     seat = torch.full((P.shape[0], 1), -1.0 if player == 0 else 1.0, dtype=torch.float64)
-    z = Jp + _lin(blob.join_b, torch.cat([pooled[:, 0], pooled[:, 1], seat], dim=-1))
+    z = Jp + blob.lin("join_b", blob.join_b, torch.cat([pooled[:, 0], pooled[:, 1], seat], dim=-1))
     for i in range(JBLOCKS):
-        z = z + _lin(blob.join_w[i], _ln(blob.norms[2 * BLOCKS + 2 + i], z))
+        z = z + blob.lin("join_w", blob.join_w[i], _ln(blob.norms[2 * BLOCKS + 2 + i], z))
     z = _ln(blob.norms[2 * BLOCKS + 2 + JBLOCKS], z)
-    return _ln(blob.norms[2 * BLOCKS + 3 + JBLOCKS], P + _lin(blob.join_out, z), act=False)
+    return _ln(blob.norms[2 * BLOCKS + 3 + JBLOCKS], P + blob.lin("join_out", blob.join_out, z), act=False)
 
 
 def values(blob, f, h):
     """Net::values for every (row of h, config of f): [R, n]."""
-    return torch.as_tensor(np.asarray(h, np.float64)) @ torch.as_tensor(np.asarray(f, np.float64)).T + blob.value_bias
+    h, f = torch.as_tensor(np.asarray(h, np.float64)), torch.as_tensor(np.asarray(f, np.float64))
+    return blob.lin("values", (f.T, None), h) + blob.value_bias

@@ -397,6 +397,8 @@ int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup,
         kernel_ms[6] = prof.top_mean;
         kernel_ms[7] = prof.reach_mean;
         kernel_ms[8] = prof.graph_build_ms;
+        kernel_ms[9] = prof.net_build;
+        kernel_ms[10] = prof.v5_join;
     }
     return WC_OK;
 }

@@ -767,9 +767,17 @@ const NetBank* Executor::bank_of(uint64_t version, std::string* err) const {
 
 void Executor::run_v5_build(const NetBank& bank) { v5::launch_build(precision_, bank.v5, v5_in_, v5_out_, stream_); }
 
-void Executor::run_v5(const NetBank& bank, int traverser) {
+void Executor::run_v5_join(const NetBank& bank, int traverser) {
     v5::launch_join(precision_, bank.v5, dev_.rows, Xq_[traverser], v5_out_.P, v5_out_.Jp, H_[0], v5_xf_, stream_);
+}
+
+void Executor::run_v5_readout(const NetBank& bank, int traverser) {
     launch_tower_head(dev_, traverser, precision_, H_[0], v5::D, v5_out_.F, bank.v5.value_bias, head_out_, stream_);
+}
+
+void Executor::run_v5(const NetBank& bank, int traverser) {
+    run_v5_join(bank, traverser);
+    run_v5_readout(bank, traverser);
 }
 
 void Executor::leaf_net(const NetBank& bank, int q) {
@@ -834,7 +842,9 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     const Meta& m = w.meta;
     const uint32_t nsub = w.nsub;
     // Per-class attribution: an event after every launch group, binned by class.
-    enum { C_BACK = 0, C_TOP = 1, C_REACH = 2, C_MLP = 3, C_LEAF = 4, C_OTHER = 5 };
+    // C_BUILD (the per-wave network work) and C_JOIN (the v5 join) count as
+    // leaf-net time and are also reported on their own.
+    enum { C_BACK = 0, C_TOP = 1, C_REACH = 2, C_MLP = 3, C_LEAF = 4, C_OTHER = 5, C_BUILD = 6, C_JOIN = 7 };
     std::vector<std::pair<hipEvent_t, int>> ev;
     hipEvent_t start = nullptr;
     auto mark = [&](int cls) {
@@ -849,21 +859,34 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         hipEventRecord(start, s);
     }
     const bool tower = bank.ns.kind == MODEL_TWO_TOWER;
-    if (tower) run_tower_private(bank);  // F for this wave's configs under this bank
+    if (tower) {
+        run_tower_private(bank);  // F for this wave's configs under this bank
+        mark(C_BUILD);
+    }
     if (bank.ns.kind == MODEL_V5) {
         run_v5_build(bank);  // cards, trunk, configs for this wave under this bank
-        mark(C_MLP);
+        mark(C_BUILD);
     }
     if (S_[0]) {
         static_products(bank);
-        mark(C_MLP);
+        mark(C_BUILD);
     }
+    // One traverser's leaf net; under profiling the v5 join is timed apart from its readout.
+    auto net_pass = [&](int p) {
+        if (prof && bank.ns.kind == MODEL_V5) {
+            run_v5_join(bank, p);
+            mark(C_JOIN);
+            run_v5_readout(bank, p);
+        } else {
+            leaf_net(bank, p);
+        }
+    };
     init_state(w);
     mark(C_OTHER);
     if (m.iters == 0) launch_normalize(d, 0, 0, s);
     for (uint32_t t = 0; t < m.iters; t++) {
         const int p = (int)(t & 1);
-        leaf_net(bank, p);
+        net_pass(p);
         if (hook) (*hook)((int32_t)t, p);
         mark(C_MLP);
         const float mm = (float)(t / 2 + 1);
@@ -899,7 +922,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         launch_pool(d, -1, precision_, Xq_[0], Xq_[1], s);
         mark(C_LEAF);
         for (int p = 0; p < 2; p++) {
-            leaf_net(bank, p);
+            net_pass(p);
             if (hook) (*hook)(phase2_point(root, p), p);
             launch_sweep(d, 0, nsub, head_out_, bank.ns.heads, p, MODE_VALUE, 0.0f, 0.0f, 0.0f, s);
             top_back(w, p, MODE_VALUE, 0.0f, 0.0f, 0.0f);
@@ -911,8 +934,8 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         hipStreamSynchronize(s);
         *prof = ScheduleTimes{};
         hipEvent_t prev = start;
-        double cls_ms[6] = {0, 0, 0, 0, 0, 0};
-        uint32_t cls_n[6] = {0, 0, 0, 0, 0, 0};
+        double cls_ms[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        uint32_t cls_n[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         for (auto& e : ev) {
             float ms = 0.0f;
             hipEventElapsedTime(&ms, prev, e.first);
@@ -924,7 +947,9 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         if (!ev.empty()) hipEventElapsedTime(&tot, start, ev.back().first);
         prof->total = tot;
         prof->cfr = cls_ms[C_BACK] + cls_ms[C_TOP] + cls_ms[C_REACH];
-        prof->mlp = cls_ms[C_MLP];
+        prof->mlp = cls_ms[C_MLP] + cls_ms[C_BUILD] + cls_ms[C_JOIN];
+        prof->net_build = cls_ms[C_BUILD];
+        prof->v5_join = cls_ms[C_JOIN];
         prof->leaf_input = cls_ms[C_LEAF];
         prof->other = cls_ms[C_OTHER];
         prof->back_mean = cls_n[C_BACK] ? cls_ms[C_BACK] / cls_n[C_BACK] : 0.0;

@@ -55,6 +55,8 @@ struct ScheduleTimes {
     double cfr_launch_mean = 0;  // mean device time of one CFR iteration (the three kernels)
     uint32_t cfr_launches = 0;
     double graph_build_ms = 0;   // host time to capture and instantiate the schedule's graph (0: not captured)
+    double net_build = 0;        // the per-wave network work (v5 build, private tower, fixed-column products)
+    double v5_join = 0;          // the v5 network's joins over the whole schedule (0 for other nets)
 };
 
 // Per-job facts the unpack of a collected wave needs, copied at launch so the
@@ -188,6 +190,8 @@ class Executor {
                         size_t nln, std::string* err);
     void run_v5_build(const NetBank& bank);
     void run_v5(const NetBank& bank, int traverser);
+    void run_v5_join(const NetBank& bank, int traverser);
+    void run_v5_readout(const NetBank& bank, int traverser);
     // The MLP over `rows` query rows: the fused kernel over `plan` (npass
     // passes, device copy) where it applies, else layer by layer (head width
     // per 128-row tile: head_tile_n).

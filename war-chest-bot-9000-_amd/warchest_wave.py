@@ -125,7 +125,7 @@ EXPORTS = [
     "wc_executor_create", "wc_executor_destroy", "wc_executor_publish",
     "wc_wave_pack", "wc_wave_free", "wc_wave_stats_get", "wc_wave_array", "wc_value_net_plan", "wc_solve_wave",
     "wc_launch", "wc_inflight_ready", "wc_collect", "wc_wave_leaf_probe", "wc_wave_leaf_trace",
-    "wc_time_wave",
+    "wc_time_wave", "wc_peak_probe",
     "wc_mlp_forward", "wc_mlp_forward_noalloc", "wc_time_mlp",
     "wc_job_roundtrip", "wc_job_validate",
     "wc_synth_spec_default", "wc_synth", "wc_jobset_count", "wc_jobset_job", "wc_jobset_free",
@@ -195,6 +195,7 @@ def _declare(L):
     L.wc_solve_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p)]
     L.wc_time_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32,
                                C.POINTER(C.c_double), C.POINTER(C.c_double)]
+    L.wc_peak_probe.argtypes = [C.c_int, C.c_size_t] + [C.POINTER(C.c_double)] * 4
     L.wc_mlp_forward.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, _f32p, _f32p]
     L.wc_mlp_forward_noalloc.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p]
     L.wc_time_mlp.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, _f32p, C.c_uint32,
@@ -255,6 +256,16 @@ def value_net_plan(cols, cus, heads=None):
     _check(lib().wc_value_net_plan(cp, nrb, heads, cus, out.ctypes.data_as(C.POINTER(C.c_uint32)), n.value,
                                    C.byref(n)))
     return [(int(r[1]), [int(b) for b in r[2:2 + r[0]]]) for r in out[:n.value]]
+
+
+def peak_probe(device=0, nbytes=1 << 30):
+    """What the device sustains (wc_peak_probe): HBM copy and read GB/s over buffers of
+    nbytes, and f16 MFMA TFLOP/s on register operands (32x32x16, and the 16x16x32
+    instruction the fused value net issues)."""
+    c, r, m, m16 = C.c_double(), C.c_double(), C.c_double(), C.c_double()
+    _check(lib().wc_peak_probe(device, nbytes, C.byref(c), C.byref(r), C.byref(m), C.byref(m16)))
+    return {"hbm_copy_gbs": c.value, "hbm_read_gbs": r.value, "mfma_f16_tflops": m.value,
+            "mfma_f16_16x16x32_tflops": m16.value}
 
 
 def mlp_dims(inputs=512, hidden=384, layers=3, heads=22, pool=64):
@@ -529,10 +540,11 @@ class Executor:
 
     def time_wave(self, wave: Wave, version: int, reps: int, warmup: int = 1):
         """Mean device ms per wave over `reps` timed schedules after `warmup` untimed
-        ones, and one profiled schedule's [cfr, mlp, leaf input, other, mean CFR iteration,
-        mean subtree sweep, mean top sweep, mean subtree reach, graph build (host)] ms."""
+        ones, and one profiled schedule's [cfr, leaf net, leaf input, other, mean CFR iteration,
+        mean subtree sweep, mean top sweep, mean subtree reach, graph build (host), the leaf
+        net's per-wave work, the v5 joins] ms."""
         ms = C.c_double()
-        parts = (C.c_double * 9)()
+        parts = (C.c_double * 11)()
         _check(lib().wc_time_wave(self.h, wave.h, version, warmup, reps, C.byref(ms), parts))
         return ms.value, list(parts)
 
