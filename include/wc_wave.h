@@ -100,6 +100,19 @@ uint64_t wc_set_weights(wc_service* svc, const wc_net_desc* net);
 uint64_t wc_queued_work(wc_service* svc);
 /* GpuClient::submit_tagged: copies the job bytes; the ticket is completed when the wave finishes. */
 int wc_submit(wc_service* svc, const uint8_t* job, size_t len, uint64_t tag, wc_ticket** out);
+/* PreparedJob::new (client.rs:165-181): parse, validate and cost one WCJ8 job
+ * once, for a service of `precision`. The handle is immutable and may be
+ * submitted any number of times, from any thread, to any service of that
+ * precision; each submission shares it (no copy, no re-parse). The job bytes
+ * may be freed when this returns. */
+typedef struct wc_prepared wc_prepared;
+int wc_prepare(const uint8_t* job, size_t len, int precision, wc_prepared** out);
+/* Its queued-work cost (client.rs:282-291). */
+uint64_t wc_prepared_cost(const wc_prepared* p);
+/* Drop the caller's handle; submissions still queued or running keep the job. */
+void wc_prepared_free(wc_prepared* p);
+/* GpuClient::submit_prepared / submit_tagged_prepared (client.rs:212-255). */
+int wc_submit_prepared(wc_service* svc, const wc_prepared* job, uint64_t tag, wc_ticket** out);
 /* SolveHandle::wait: blocks; *out owns the result (wc_result_free). Frees the ticket. */
 int wc_wait(wc_ticket* t, wc_result** out);
 /* 1 when wc_wait would not block, 0 otherwise. */

@@ -182,3 +182,29 @@ def test_dropped_handle_frees_its_ticket():
         got = [h.wait() for h in rest]
     for g, r in zip(got, alone(jobs[1:], net)):
         same(g, r, "after a dropped handle")
+
+
+def test_prepared_jobs_submitted_again_and_again():
+    """GpuClient::submit_prepared (engine/src/gpu/client.rs:212-255): jobs prepared once
+    and submitted three times each from several threads, interleaved with the same
+    jobs as WCJ8 bytes, all return the oracle's results; a job prepared for another
+    precision is refused; queued work drains to zero."""
+    jobs = small_jobs(6, 65)
+    net = W.net_for("wave256")
+    ref = alone(jobs, net)
+    say("case prepared jobs: 6 jobs x 3 prepared submissions + 6 byte submissions, 2 lanes")
+    prepared = [ww.PreparedJob(j, ww.WC_PRECISE) for j in jobs]
+    with ww.spawn(0, net, ww.WC_PRECISE, lanes=2, wave_jobs=4, window_us=500) as client:
+        with pytest.raises(ww.WaveError, match="precision"):
+            client.submit_prepared(ww.PreparedJob(jobs[0], ww.WC_F16))
+        items = [(k, r) for r in range(3) for k in range(len(jobs))]
+        with ThreadPoolExecutor(4) as pool:
+            handles = list(pool.map(lambda kr: (kr[0], client.submit_prepared(prepared[kr[0]], tag=10 * kr[0] + kr[1])),
+                                    items))
+        raw = [(k, client.submit(j, tag=900 + k)) for k, j in enumerate(jobs)]
+        for p in prepared:
+            p.close()  # queued submissions keep their job
+        got = [(k, h.wait()) for k, h in handles + raw]
+        assert client.queued_work() == 0
+    for k, g in got:
+        same(g, ref[k], f"job {k}")

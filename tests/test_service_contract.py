@@ -101,3 +101,21 @@ def test_route_predicates_follow_the_reservation():
         assert w["card_exclusive_route"] == int(reserved >= 6 * unit)
         assert w["arena_guard_route"] == int(mutable >= 4 * unit and not reserved >= 6 * unit)
         assert (w["cost_class"] == 31) == bool(w["exclusive_route"])
+
+
+def test_prepared_job_carries_the_jobs_cost():
+    """wc_prepare (PreparedJob::new, engine/src/gpu/client.rs:165-181) costs a job once:
+    its cost is job_cost of the work vector restated above, for each precision; bytes
+    that do not decode, or decode to an invalid job, are refused."""
+    jobs = W.jobs("wave64")[:3] + W.jobs("wave512w", trees=4)[:2]
+    for j in jobs:
+        d = wcj8.decode(j)
+        for prec in (ww.WC_PRECISE, ww.WC_F16, ww.WC_BF16):
+            p = ww.PreparedJob(j, prec)
+            assert p.cost == ww.job_work(j, prec)["cost"]
+            assert p.cost == restated_cost({**restated_work(d), "mutable_bytes": 0}, d["iters"])
+            p.close()
+    with pytest.raises(ww.WaveError):
+        ww.PreparedJob(jobs[0][:-9], ww.WC_F16)
+    with pytest.raises(ww.WaveError):
+        ww.PreparedJob(jobs[0], 17)

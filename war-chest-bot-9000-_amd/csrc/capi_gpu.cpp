@@ -33,6 +33,9 @@ struct wc_ticket {
 struct wc_inflight {
     InFlight f;
 };
+struct wc_prepared {
+    std::shared_ptr<const Prepared> p;
+};
 
 namespace {
 
@@ -499,6 +502,34 @@ int wc_submit(wc_service* svc, const uint8_t* job, size_t len, uint64_t tag, wc_
         std::shared_ptr<Ticket> t;
         std::string err;
         if (!svc->svc->submit(job, len, tag, &t, &err))
+            return fail(err == "GPU wave executor is gone" ? WC_ERR_GONE : WC_ERR_INVALID, err);
+        *out = new wc_ticket{t};
+        return WC_OK;
+    });
+}
+
+int wc_prepare(const uint8_t* job, size_t len, int precision, wc_prepared** out) {
+    if (!job || !out) return fail(WC_ERR_INVALID, "wc_prepare: null argument");
+    if (precision < WC_PRECISE || precision > WC_F16X) return fail(WC_ERR_INVALID, "wc_prepare: unknown precision");
+    return shielded("wc_prepare", [&] {
+        std::shared_ptr<const Prepared> p;
+        std::string err;
+        if (!prepare(job, len, precision, &p, &err)) return fail(WC_ERR_INVALID, err);
+        *out = new wc_prepared{std::move(p)};
+        return WC_OK;
+    });
+}
+
+uint64_t wc_prepared_cost(const wc_prepared* p) { return p && p->p ? p->p->cost : 0; }
+
+void wc_prepared_free(wc_prepared* p) { delete p; }
+
+int wc_submit_prepared(wc_service* svc, const wc_prepared* job, uint64_t tag, wc_ticket** out) {
+    if (!svc || !job || !out) return fail(WC_ERR_INVALID, "wc_submit_prepared: null argument");
+    return shielded("wc_submit_prepared", [&] {
+        std::shared_ptr<Ticket> t;
+        std::string err;
+        if (!svc->svc->submit_prepared(job->p, tag, &t, &err))
             return fail(err == "GPU wave executor is gone" ? WC_ERR_GONE : WC_ERR_INVALID, err);
         *out = new wc_ticket{t};
         return WC_OK;

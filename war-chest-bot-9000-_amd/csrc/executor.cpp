@@ -1032,12 +1032,12 @@ bool Executor::launch(const WaveHost& w, uint64_t version, InFlight* f, std::str
     for (size_t j = 0; j < w.jobs.size(); j++) {
         const TreeDev& t = w.trees[j];
         JobSlice& js = f->jobs[j];
-        js.ncells = w.jobs[j].t.ncells;
+        js.ncells = w.jobs[j]->t.ncells;
         js.nroots = t.nroots;
         js.n0 = t.n0;
         js.n1 = t.n1;
         js.root_value0 = t.root_value0;
-        js.snapshot_configs = w.jobs[j].t.snapshot_configs();
+        js.snapshot_configs = w.jobs[j]->t.snapshot_configs();
     }
     sl.busy = true;
     in_flight_++;

@@ -155,19 +155,19 @@ extern "C" int wc_peak_probe(int device, size_t bytes, double* copy_gbs, double*
         double t = timed([&] {
             hipLaunchKernelGGL(k_probe_copy, dim3(copy_grid), dim3(PROBE_BLOCK), 0, s, (const u32x4*)src, (u32x4*)dst,
                                n);
-        }, 2, reps);
+        }, 5, reps);
         *copy_gbs = 2.0 * double(n * sizeof(u32x4)) / t / 1e9;
         t = timed([&] {
             hipLaunchKernelGGL(k_probe_read, dim3(read_grid), dim3(PROBE_BLOCK), 0, s, (const u32x4*)src,
                                (uint32_t*)out, n);
-        }, 2, reps);
+        }, 5, reps);
         *read_gbs = double(n * sizeof(u32x4)) / t / 1e9;
         // 32x32x16: two wavefronts per SIMD (two 256-thread workgroups per CU);
         // 16x16x32: four (four workgroups per CU). Two accumulators each.
         const uint32_t iters = 8192;
         t = timed([&] {
             hipLaunchKernelGGL(k_probe_mfma32, dim3(cus * 2), dim3(PROBE_BLOCK), 0, s, (float*)out, iters);
-        }, 2, 3);
+        }, 100, 3);  // about 50 ms of warm-up launches: the clocks settle under a sustained MFMA load
         *mfma_tflops = double(cus) * 2 * (PROBE_BLOCK / 64) * iters * 2.0 * 32768.0 / t / 1e12;
         t = timed([&] {
             hipLaunchKernelGGL(k_probe_mfma16, dim3(cus * 4), dim3(PROBE_BLOCK), 0, s, (float*)out, iters);

@@ -229,19 +229,51 @@ uint64_t Service::set_weights(NetCopy net, std::string* err) {
     return copy->version;
 }
 
+bool prepare(const uint8_t* bytes, size_t len, int precision, std::shared_ptr<const Prepared>* out, std::string* err) {
+    auto job = std::make_shared<Job>();
+    if (!from_bytes(bytes, len, job.get(), err)) return false;
+    if (!validate(*job, err)) return false;
+    NetShape ns;
+    if (!ns.parse(job->meta.net_dims, err)) return false;
+    auto p = std::make_shared<Prepared>();
+    p->work = work_vector(*job, precision);
+    p->cost = job_cost(p->work, job->meta.iters);
+    p->precision = precision;
+    p->job = std::move(job);
+    *out = std::move(p);
+    return true;
+}
+
 bool Service::submit(const uint8_t* bytes, size_t len, uint64_t tag, std::shared_ptr<Ticket>* out,
                      std::string* err) {
+    std::shared_ptr<const Prepared> prep;
+    if (!prepare(bytes, len, precision_, &prep, err)) return false;
+    return submit_prepared(prep, tag, out, err);
+}
+
+bool Service::submit_prepared(const std::shared_ptr<const Prepared>& prep, uint64_t tag,
+                              std::shared_ptr<Ticket>* out, std::string* err) {
+    if (!prep || !prep->job) {
+        *err = "no prepared job";
+        return false;
+    }
+    if (prep->precision != precision_) {
+        *err = "the job was prepared for precision " + std::to_string(prep->precision) + ", the service runs " +
+               std::to_string(precision_);
+        return false;
+    }
     Pending p;
-    if (!from_bytes(bytes, len, &p.job, err)) return false;
-    if (!validate(p.job, err)) return false;
-    NetShape ns;
-    if (!ns.parse(p.job.meta.net_dims, err)) return false;
-    p.rows = p.job.t.rows;
-    p.work = work_vector(p.job, precision_);
+    p.job = prep->job;
+    p.rows = p.job->t.rows;
+    p.work = prep->work;
+    return enqueue(std::move(p), tag, prep->cost, out, err);
+}
+
+bool Service::enqueue(Pending&& p, uint64_t tag, uint64_t cost, std::shared_ptr<Ticket>* out, std::string* err) {
     p.cls = cost_class(p.work, opts_.class_shift, opts_.route_unit);
     p.ticket = std::make_shared<Ticket>();
     p.ticket->tag = tag;
-    p.ticket->cost = job_cost(p.work, p.job.meta.iters);
+    p.ticket->cost = cost;
     p.ticket->oversize = p.work.requires_exclusive_route(opts_.route_unit);
     p.ticket->card = p.work.requires_card_exclusive_route(opts_.route_unit);
     std::shared_ptr<Ticket> t = p.ticket;
@@ -276,12 +308,12 @@ void Service::fill_wave(std::unique_lock<std::mutex>& lk, uint32_t lane, long se
     queue_.erase(queue_.begin() + seed);
     const Pending& head = wave->front();
     if (head.cls == 31) return;
-    const Meta hm = head.job.meta;
+    const Meta hm = head.job->meta;
     const uint64_t hv = head.net->version;
     const uint8_t hc = head.cls;
     size_t rows = head.rows;
     auto compatible = [&](const Pending& q) {
-        const Meta& m = q.job.meta;
+        const Meta& m = q.job->meta;
         return q.net->version == hv && q.cls == hc && m.iters == hm.iters && m.snapshots == hm.snapshots &&
                m.snap_iters == hm.snap_iters && m.net_dims == hm.net_dims && m.depth == hm.depth &&
                std::memcmp(&m.cfr, &hm.cfr, sizeof(Cfr)) == 0;
@@ -468,7 +500,7 @@ void Service::lane_main(uint32_t lane) {
         const uint32_t k = last ^ 1;
         land(fl[k]);  // its slot is needed (normally landed already)
         Flight& F = fl[k];
-        std::vector<Job> jobs;
+        std::vector<std::shared_ptr<const Job>> jobs;
         for (auto& p : wave) {
             F.tickets.push_back(p.ticket);
             jobs.push_back(std::move(p.job));

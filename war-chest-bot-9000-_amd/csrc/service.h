@@ -52,6 +52,18 @@ uint64_t job_cost(const WorkVector& w, uint32_t iters);
 // 0..2) coarsens the ordinary classes.
 uint8_t cost_class(const WorkVector& w, uint32_t shift, uint64_t unit = WorkVector::ROUTE_UNIT);
 
+// PreparedJob (engine/src/gpu/client.rs:165-181): an immutable job with its
+// admission vector and cost computed once for an executor precision; cheap
+// to share between submissions.
+struct Prepared {
+    std::shared_ptr<const Job> job;
+    WorkVector work;
+    uint64_t cost = 0;
+    int precision = 0;
+};
+// Parse, validate and cost one WCJ8 job for `precision`.
+bool prepare(const uint8_t* bytes, size_t len, int precision, std::shared_ptr<const Prepared>* out, std::string* err);
+
 struct Ticket {
     std::mutex mu;
     std::condition_variable cv;
@@ -87,6 +99,11 @@ class Service {
     uint64_t set_weights(NetCopy net, std::string* err);
     uint64_t queued_work() const { return queued_.load(std::memory_order_relaxed); }
     bool submit(const uint8_t* bytes, size_t len, uint64_t tag, std::shared_ptr<Ticket>* out, std::string* err);
+    // GpuClient::submit_prepared (engine/src/gpu/client.rs:212-221): a job
+    // parsed, validated and costed once (Prepared), shared, not copied.
+    bool submit_prepared(const std::shared_ptr<const struct Prepared>& job, uint64_t tag, std::shared_ptr<Ticket>* out,
+                         std::string* err);
+    int precision() const { return precision_; }
     void shutdown();
     // Waves launched so far and guarded routes taken (for tests and tooling).
     uint64_t waves() const { return waves_.load(std::memory_order_relaxed); }
@@ -95,7 +112,7 @@ class Service {
   private:
     struct Pending {
         std::shared_ptr<Ticket> ticket;
-        Job job;
+        std::shared_ptr<const Job> job;
         WorkVector work;
         uint8_t cls = 0;
         size_t rows = 0;
@@ -107,6 +124,7 @@ class Service {
         std::vector<std::shared_ptr<Ticket>> tickets;
         uint64_t version = 0;
     };
+    bool enqueue(Pending&& p, uint64_t tag, uint64_t cost, std::shared_ptr<Ticket>* out, std::string* err);
     void lane_main(uint32_t lane);
     // Under mu_: the index of the first queued job this lane may seed a wave
     // with, or -1.

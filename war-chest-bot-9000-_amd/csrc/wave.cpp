@@ -455,16 +455,17 @@ void WaveHost::reset() {
     tower_len = blank.tower_len;
 }
 
-bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_t unit_slots, bool validated) {
+bool pack_wave(std::vector<std::shared_ptr<const Job>>&& jobs, WaveHost* out, std::string* err, uint32_t unit_slots,
+               bool validated) {
     if (jobs.empty()) {
         *err = "cannot pack an empty wave";
         return false;
     }
     WaveHost& w = *out;  // packed in place: a reused WaveHost keeps its buffers
     w.reset();
-    w.meta = jobs[0].meta;
+    w.meta = jobs[0]->meta;
     for (size_t k = 1; k < jobs.size(); k++)
-        if (!same_meta(jobs[0].meta, jobs[k].meta)) {
+        if (!same_meta(jobs[0]->meta, jobs[k]->meta)) {
             *err = "wave mixes different CFR schedules";
             return false;
         }
@@ -472,7 +473,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     if (!validated) {  // jobs validate independently; the first failure in job order is reported
         std::vector<std::string> errs(jobs.size());
         std::vector<uint8_t> bad(jobs.size(), 0);
-        parallel_for(jobs.size(), [&](size_t k) { bad[k] = !validate(jobs[k], &errs[k]); });
+        parallel_for(jobs.size(), [&](size_t k) { bad[k] = !validate(*jobs[k], &errs[k]); });
         for (size_t k = 0; k < jobs.size(); k++)
             if (bad[k]) {
                 *err = errs[k];
@@ -491,9 +492,9 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     }
     // Every leaf must fit a unit (tops carry no leaves): the budget is at least
     // the widest node of the wave.
-    for (const Job& job : jobs)
-        for (uint32_t i = 0; i < job.t.nodes; i++)
-            unit_slots = std::max(unit_slots, std::max(job.t.nc(i, 0), job.t.nc(i, 1)));
+    for (const auto& job : jobs)
+        for (uint32_t i = 0; i < job->t.nodes; i++)
+            unit_slots = std::max(unit_slots, std::max(job->t.nc(i, 0), job->t.nc(i, 1)));
 
     // The jobs are packed in three steps: each job's own layout (in parallel),
     // every job's offset into each wave list (a prefix over the jobs), then
@@ -502,7 +503,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     const size_t J = jobs.size();
     const bool v5 = w.net.kind == MODEL_V5, tower = w.net.kind == MODEL_TWO_TOWER;
     std::vector<JobLayout> lay(J);
-    parallel_for(J, [&](size_t k) { lay[k].build(jobs[k].t, w.net, v5, unit_slots); });
+    parallel_for(J, [&](size_t k) { lay[k].build(jobs[k]->t, w.net, v5, unit_slots); });
     for (size_t k = 0; k < J; k++)  // the first failure in job order
         if (!lay[k].err.empty()) {
             *err = lay[k].err;
@@ -512,7 +513,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     JobAt n{};  // running totals: the next job's offsets
     uint32_t top_levels = 0;
     for (size_t k = 0; k < J; k++) {
-        const Tables& t = jobs[k].t;
+        const Tables& t = jobs[k]->t;
         const JobLayout& L = lay[k];
         at[k] = n;
         n.node += t.nodes;
@@ -535,7 +536,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
         n.ecoff += (uint32_t)t.snap_coff.size() - 1;
         n.ecfg += t.snapshot_configs();
         n.term += (uint32_t)t.term_leaves.size();
-        n.rootv += jobs[k].nroots() * (t.nc(0, 0) + t.nc(0, 1));
+        n.rootv += jobs[k]->nroots() * (t.nc(0, 0) + t.nc(0, 1));
         n.unit += (uint32_t)L.unit_d0.size();
         n.lvl += L.lvls;
         n.urow += L.nrow;
@@ -549,11 +550,11 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
         n.card += v5 ? t.card_feat.size() : 0;
         n.priv += v5 ? size_t(t.ncfg) * w.net.cfeat : tower ? size_t(t.ncfg) * w.net.priv_in : 0;
         n.emb += v5 ? 0 : size_t(t.ncfg) * w.net.pool;
-        n.roots += jobs[k].root[0].size() + jobs[k].root[1].size();
-        for (uint32_t r = 0; r < jobs[k].nroots(); r++) n.carried += jobs[k].carried[0][r].size() + jobs[k].carried[1][r].size();
+        n.roots += jobs[k]->root[0].size() + jobs[k]->root[1].size();
+        for (uint32_t r = 0; r < jobs[k]->nroots(); r++) n.carried += jobs[k]->carried[0][r].size() + jobs[k]->carried[1][r].size();
         n.rowjob += v5 ? t.rows : 0;
         w.max_levels = std::max(w.max_levels, L.max_levels);
-        w.nroots_max = std::max(w.nroots_max, jobs[k].nroots());
+        w.nroots_max = std::max(w.nroots_max, jobs[k]->nroots());
         top_levels = std::max(top_levels, L.top_depths);
     }
     // Every list at its final size, the larger ones side by side (a resize
@@ -634,7 +635,7 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     w.lvl_len = n.lvl;
 
     parallel_for(J, [&](size_t k) {
-        const Job& job = jobs[k];
+        const Job& job = *jobs[k];
         const Tables& t = job.t;
         const JobAt& a = at[k];
         JobLayout& L = lay[k];
@@ -1024,6 +1025,13 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
 
 // Every index a kernel dereferences, checked against the buffer it indexes.
 // The device code relies on these bounds and performs no checks of its own.
+bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_t unit_slots, bool validated) {
+    std::vector<std::shared_ptr<const Job>> shared(jobs.size());
+    for (size_t k = 0; k < jobs.size(); k++) shared[k] = std::make_shared<const Job>(std::move(jobs[k]));
+    jobs.clear();
+    return pack_wave(std::move(shared), out, err, unit_slots, validated);
+}
+
 bool validate_deep(const WaveHost& w, std::string* err) {
     auto fail = [&](const char* m) {
         *err = std::string("wave bounds: ") + m;

@@ -16,6 +16,7 @@
 #pragma once
 
 #include <cstdint>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -158,7 +159,7 @@ constexpr uint32_t UNIT_SLOTS = 4096;
 struct WaveHost {
     Meta meta;
     NetShape net;
-    std::vector<Job> jobs;  // parsed, kept for result unpacking
+    std::vector<std::shared_ptr<const Job>> jobs;  // the wave's jobs (shared, immutable), kept for result unpacking
     std::vector<TreeDev> trees;
 
     // Tree and sparse-cell SoA, wave-global.
@@ -251,6 +252,9 @@ struct WaveHost {
 // `validated`: every job already passed validate() (the service checks each
 // job when it is submitted), so the per-job checks are not repeated, nor the
 // deep check of the packed wave (validate_deep) unless WC_DEEP_CHECK=1.
+bool pack_wave(std::vector<std::shared_ptr<const Job>>&& jobs, WaveHost* w, std::string* err,
+               uint32_t unit_slots = UNIT_SLOTS, bool validated = false);
+// The same for jobs owned by the caller (moved into the wave).
 bool pack_wave(std::vector<Job>&& jobs, WaveHost* w, std::string* err, uint32_t unit_slots = UNIT_SLOTS,
                bool validated = false);
 

@@ -120,6 +120,7 @@ EXPORTS = [
     "wc_last_error", "wc_net_sizes", "wc_net_norms",
     "wc_service_create", "wc_service_destroy", "wc_set_weights", "wc_queued_work",
     "wc_submit", "wc_wait", "wc_poll", "wc_ticket_free", "wc_service_stats", "wc_job_work",
+    "wc_prepare", "wc_prepared_cost", "wc_prepared_free", "wc_submit_prepared",
     "wc_result_tag", "wc_result_weight_version", "wc_result_strategy", "wc_result_root_values",
     "wc_result_carries", "wc_result_routes", "wc_result_free",
     "wc_executor_create", "wc_executor_destroy", "wc_executor_publish",
@@ -152,6 +153,12 @@ def _declare(L):
     L.wc_queued_work.restype = C.c_uint64
     L.wc_submit.argtypes = [C.c_void_p, _u8p, C.c_size_t, C.c_uint64, C.POINTER(C.c_void_p)]
     L.wc_wait.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+    L.wc_prepare.argtypes = [_u8p, C.c_size_t, C.c_int, C.POINTER(C.c_void_p)]
+    L.wc_prepared_cost.argtypes = [C.c_void_p]
+    L.wc_prepared_cost.restype = C.c_uint64
+    L.wc_prepared_free.argtypes = [C.c_void_p]
+    L.wc_prepared_free.restype = None
+    L.wc_submit_prepared.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p)]
     L.wc_poll.argtypes = [C.c_void_p]
     L.wc_ticket_free.argtypes = [C.c_void_p]
     L.wc_ticket_free.restype = None
@@ -626,6 +633,33 @@ class SolveHandle:
                 pass
 
 
+class PreparedJob:
+    """`PreparedJob` (engine/src/gpu/client.rs:165-181): a WCJ8 job parsed, validated
+    and costed once for a service precision (wc_prepare); submit it any number of
+    times with GpuClient.submit_prepared."""
+
+    def __init__(self, job: bytes, precision=WC_PRECISE):
+        buf, p = _bytes_ptr(job)
+        h = C.c_void_p()
+        _check(lib().wc_prepare(p, len(job), precision, C.byref(h)))
+        self.h = h
+
+    @property
+    def cost(self) -> int:
+        return int(lib().wc_prepared_cost(self.h))
+
+    def close(self):
+        if self.h:
+            lib().wc_prepared_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class GpuClient:
     """`GpuClient` (engine/src/gpu/client.rs:196-313) over the native service."""
 
@@ -636,6 +670,11 @@ class GpuClient:
         buf, p = _bytes_ptr(job)
         t = C.c_void_p()
         _check(lib().wc_submit(self.h, p, len(job), tag, C.byref(t)))
+        return SolveHandle(t)
+
+    def submit_prepared(self, job: PreparedJob, tag: int = 0) -> SolveHandle:
+        t = C.c_void_p()
+        _check(lib().wc_submit_prepared(self.h, job.h, tag, C.byref(t)))
         return SolveHandle(t)
 
     def set_weights(self, net: Net) -> int:
