@@ -147,6 +147,32 @@ def test_parity_waves_pack_and_validate(budget, family, monkeypatch):
         assert st["top_levels"] > 0
 
 
+def test_service_style_mixed_waves_pass_the_deep_check():
+    """The service buckets whatever compatible jobs its queue holds (one schedule,
+    any sizes, carried-root counts and tree shapes) and packs them from jobs
+    validated at submit, skipping the packed wave's deep bounds check
+    (validate_deep). The packer's output does not depend on that flag, so every
+    mix it can form must pass the check: 30 random mixes of 1..24 jobs from a
+    pool of differently shaped jobs with one schedule (small and full-size
+    trees, terminals, no-successor cells, 1..3 carried roots, a whale), packed
+    through wc_wave_pack, which runs the deep check."""
+    spec = dict(iters=8, info_median=6.0, info_p99=40.0, info_cap=40)
+    pool = (W.jobs("wave256", trees=6, nodes_lo=30, nodes_hi=90, chance=1, terminal_p=0.15, notrans_p=0.05,
+                   nroots=2, seed=71, **spec)
+            + W.jobs("wave256", trees=4, nodes_lo=200, nodes_hi=400, nroots=1, seed=72, **spec)
+            + W.jobs("wave256", trees=4, nodes_lo=40, nodes_hi=120, chance=1, terminal_p=0.3, nroots=3, seed=73,
+                     **spec)
+            + W.jobs("wave256", trees=2, nodes_lo=200, nodes_hi=300, whale_frac=1.0, whale_nodes=600,
+                     whale_info=120, nroots=1, seed=74, iters=8))
+    rng = np.random.default_rng(5)
+    for m in range(30):
+        pick = rng.choice(len(pool), size=int(rng.integers(1, 25)), replace=True)
+        wave = ww.Wave([pool[k] for k in pick])  # raises on any failed bound
+        st = wave.stats()
+        assert st["jobs"] == len(pick)
+        wave.close()
+
+
 def test_synthesis_is_seeded_and_prefix_stable():
     a = W.jobs("wave64", trees=4)
     b = W.jobs("wave64", trees=6)
