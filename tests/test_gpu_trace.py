@@ -131,6 +131,11 @@ def test_trace_float32_is_the_oracles_trace():
                                           err_msg=f"tree {k} point {pt}")
 
 
+# Subgames whose whole 16-bit solves land outside the emulations' envelope
+# (tests/envelope.py): reported one by one at every probed point.
+WATCH = {"wave64": (8, 15, 24, 37, 53, 57), "wave256": (6,)}
+
+
 def check_trace_against_model(precision, mode, tol, jobs, net, tag, median=0.05):
     s0 = O.shape(jobs[0])
     pts = probe_points(s0.iters, max(O.shape(j).nroots for j in jobs))
@@ -143,6 +148,11 @@ def check_trace_against_model(precision, mode, tol, jobs, net, tag, median=0.05)
         want = pmap(lambda k: O.leaf_eval(jobs[k], net, mode, p, per[i][k][2]), live)
         got = np.concatenate([per[i][k][0] for k in live])
         assert_tracks(got, np.concatenate([w for w, _ in want]), tol, f"{tag} point {pt}", median)
+        scale = float(max(np.abs(w).max() for w, _ in want if w.size))
+        for k in WATCH.get(tag, ()):
+            if k in live and per[i][k][0].size:
+                e = np.abs(per[i][k][0].astype(np.float64) - want[live.index(k)][0]) / scale
+                say(f"{tag} point {pt} subgame {k}: max error {e.max():.2e}, median {np.median(e):.2e}")
         # masses: the device's reach summed in another order. Any two orders of
         # a sum of n positive float32 terms agree within 2 (n - 1) 2^-24 of it;
         # lists hold up to 567 configs.
@@ -150,8 +160,12 @@ def check_trace_against_model(precision, mode, tol, jobs, net, tag, median=0.05)
                                    np.concatenate([m for _, m in want]), rtol=2 * 566 * 2.0 ** -24, atol=1e-30)
 
 
-@pytest.mark.parametrize("precision,mode,tol", [(ww.WC_F16, O.NET_F16, 2e-3), (ww.WC_BF16, O.NET_BF16, 1e-2)])
+@pytest.mark.parametrize("precision,mode,tol", [(ww.WC_F16, O.NET_F16, 2e-3), (ww.WC_BF16, O.NET_BF16, 1e-2),
+                                                (ww.WC_F16X, O.NET_F16X, 1e-5)])
 def test_trace_wave64_tracks_the_operand_model_at_the_solves_reach(precision, mode, tol):
+    """f16 and bf16 against their operand models; compensated f16 (hi + lo operand
+    pairs) against its own model, to a few float32 roundings (measured: max 6e-7,
+    median 8e-8 of the largest value at every probed point)."""
     check_trace_against_model(precision, mode, tol, W.jobs("wave64"), W.net_for("wave64"), "wave64")
 
 
