@@ -59,15 +59,8 @@ struct Blob {
         for (const Piece& pc : pieces)
             for (size_t o = 0; o < pc.bytes; o += CHUNK)
                 parts.push_back({pc.src + o, std::min(CHUNK, pc.bytes - o), pc.at + o});
-        const size_t nt = std::min<size_t>(
-            std::max(1u, std::min({8u, std::thread::hardware_concurrency(), par_budget()})), parts.size());
-        auto work = [&](size_t t) {
-            for (size_t k = t; k < parts.size(); k += nt) std::memcpy(dst + parts[k].at, parts[k].src, parts[k].bytes);
-        };
-        std::vector<std::thread> th;
-        for (size_t t = 1; t < nt; t++) th.emplace_back(work, t);
-        if (nt) work(0);
-        for (auto& x : th) x.join();
+        parallel_for(
+            parts.size(), [&](size_t k) { std::memcpy(dst + parts[k].at, parts[k].src, parts[k].bytes); }, 8);
     }
 };
 

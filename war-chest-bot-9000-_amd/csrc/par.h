@@ -1,20 +1,41 @@
 // A small host-side parallel loop for wave packing (independent per-job and
-// per-player work).
+// per-player work), over one pool of worker threads shared by every caller in
+// the process.
+//
+// A service's lanes pack waves side by side. With a fixed share of the cores
+// per lane, a lane packing a large wave kept its share while the other lanes'
+// threads sat idle waiting on the device; the shared pool lets every idle
+// worker join whichever loop still has indices left, so one large wave is
+// packed on all the cores the others are not using.
 #pragma once
+
+#include <sched.h>
 
 #include <algorithm>
 #include <atomic>
+#include <condition_variable>
 #include <cstddef>
 #include <exception>
+#include <functional>
 #include <mutex>
 #include <thread>
 #include <vector>
 
 namespace wc {
 
-// The calling thread's budget of host threads for parallel loops. Callers
-// that run side by side (a service's lanes packing at once) each take a share
-// of the cores, so that together they do not oversubscribe the host.
+// Host cores this process may run on (its affinity mask), at least 1.
+inline unsigned host_cores() {
+    cpu_set_t set;
+    CPU_ZERO(&set);
+    if (sched_getaffinity(0, sizeof(set), &set) == 0) {
+        const int n = CPU_COUNT(&set);
+        if (n > 0) return (unsigned)n;
+    }
+    return std::max(1u, std::thread::hardware_concurrency());
+}
+
+// The calling thread's cap on the threads one parallel loop may use (itself
+// included); loops nested inside a loop's body inherit it.
 inline unsigned& par_budget() {
     static thread_local unsigned budget = 16;
     return budget;
@@ -27,36 +48,110 @@ struct ParBudget {  // sets the calling thread's budget for its lifetime
     ParBudget& operator=(const ParBudget&) = delete;
 };
 
-// Runs fn(i) for every i in [0, n) on up to max_threads host threads (at most
-// the hardware's and the caller's budget), taking indices from a shared
-// counter; loops nested inside fn share the caller's budget. The first
-// exception fn throws (std::bad_alloc on a huge wave) ends the loop and is
-// rethrown on the calling thread.
+class HostPool {
+  public:
+    // The process's pool: host_cores() - 1 workers (callers work too). Never
+    // destroyed, so a thread still packing while the process exits does not
+    // meet a pool that is being torn down.
+    static HostPool& get() {
+        static HostPool* pool = new HostPool(host_cores() > 1 ? host_cores() - 1 : 0);
+        return *pool;
+    }
+
+    // Runs body(i) for every i in [0, n): the caller takes indices from a
+    // shared counter, and up to `helpers` idle workers join while indices
+    // remain. Returns when every index has run; the first exception a body
+    // throws ends the loop (no further index is taken) and is rethrown here.
+    void run(size_t n, unsigned helpers, unsigned budget, const std::function<void(size_t)>& body) {
+        Loop L;
+        L.n = n;
+        L.max_helpers = std::min<size_t>(helpers, n > 0 ? n - 1 : 0);
+        L.budget = budget;
+        L.body = &body;
+        if (L.max_helpers && !workers_.empty()) {
+            {
+                std::lock_guard<std::mutex> lk(mu_);
+                loops_.push_back(&L);
+            }
+            for (unsigned k = 0; k < L.max_helpers && k < workers_.size(); k++) work_cv_.notify_one();
+        }
+        drain(L);
+        {
+            std::unique_lock<std::mutex> lk(mu_);
+            auto it = std::find(loops_.begin(), loops_.end(), &L);
+            if (it != loops_.end()) loops_.erase(it);  // no helper joins from here on
+            done_cv_.wait(lk, [&] { return L.active == 0; });
+        }
+        if (L.failure) std::rethrow_exception(L.failure);
+    }
+
+  private:
+    struct Loop {
+        size_t n = 0;
+        std::atomic<size_t> next{0};
+        unsigned max_helpers = 0, budget = 1;
+        unsigned helpers = 0, active = 0;  // under mu_
+        const std::function<void(size_t)>* body = nullptr;
+        std::exception_ptr failure;
+        std::mutex failure_lock;
+    };
+
+    explicit HostPool(unsigned workers) {
+        for (unsigned w = 0; w < workers; w++) workers_.emplace_back([this] { worker(); });
+        for (auto& th : workers_) th.detach();
+    }
+
+    static void drain(Loop& L) {
+        ParBudget share(L.budget);
+        try {
+            for (size_t i = L.next.fetch_add(1); i < L.n; i = L.next.fetch_add(1)) (*L.body)(i);
+        } catch (...) {
+            std::lock_guard<std::mutex> hold(L.failure_lock);
+            if (!L.failure) L.failure = std::current_exception();
+            L.next.store(L.n);  // no thread takes a further index
+        }
+    }
+
+    void worker() {
+        std::unique_lock<std::mutex> lk(mu_);
+        for (;;) {
+            Loop* pick = nullptr;
+            work_cv_.wait(lk, [&] {
+                for (Loop* L : loops_)
+                    if (L->helpers < L->max_helpers && L->next.load(std::memory_order_relaxed) < L->n) {
+                        pick = L;
+                        return true;
+                    }
+                return false;
+            });
+            pick->helpers++;
+            pick->active++;
+            lk.unlock();
+            drain(*pick);
+            lk.lock();
+            if (--pick->active == 0) done_cv_.notify_all();
+        }
+    }
+
+    std::mutex mu_;
+    std::condition_variable work_cv_, done_cv_;
+    std::vector<Loop*> loops_;  // loops that helpers may still join
+    std::vector<std::thread> workers_;
+};
+
+// Runs fn(i) for every i in [0, n) on the calling thread and up to
+// min(max_threads, the caller's budget) - 1 pool workers; see HostPool::run.
 template <class F>
 void parallel_for(size_t n, F fn, unsigned max_threads = 16) {
     if (n == 0) return;
-    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
     const unsigned budget = par_budget();
-    const size_t nt = std::min<size_t>(std::min({hw, std::max(1u, max_threads), budget}), n);
-    const unsigned inner = std::max<unsigned>(1u, budget / (unsigned)nt);
-    std::atomic<size_t> next{0};
-    std::exception_ptr failure;
-    std::mutex failure_lock;
-    auto work = [&]() {
-        ParBudget share(inner);
-        try {
-            for (size_t i = next.fetch_add(1); i < n; i = next.fetch_add(1)) fn(i);
-        } catch (...) {
-            std::lock_guard<std::mutex> hold(failure_lock);
-            if (!failure) failure = std::current_exception();
-            next.store(n);  // the other threads take no further index
-        }
-    };
-    std::vector<std::thread> pool;
-    for (size_t t = 1; t < nt; t++) pool.emplace_back(work);
-    work();
-    for (auto& th : pool) th.join();
-    if (failure) std::rethrow_exception(failure);
+    const unsigned threads = std::max(1u, std::min(max_threads, budget));
+    if (threads == 1 || n == 1) {
+        for (size_t i = 0; i < n; i++) fn(i);
+        return;
+    }
+    const std::function<void(size_t)> body = [&fn](size_t i) { fn(i); };
+    HostPool::get().run(n, threads - 1, budget, body);
 }
 
 }  // namespace wc

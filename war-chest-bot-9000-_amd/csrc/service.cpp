@@ -4,6 +4,8 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <iterator>
 #include <limits>
@@ -195,6 +197,7 @@ Service::Service(int device, int precision, const ServiceOpts& opts)
     opts_.whale_lanes = std::min(std::max<uint32_t>(opts_.whale_lanes, 1), opts_.lanes);
     opts_.class_shift = std::min<uint32_t>(opts_.class_shift, 2);
     if (opts_.route_unit == 0) opts_.route_unit = WorkVector::ROUTE_UNIT;
+    if (const char* env = std::getenv("WC_SERVICE_PROFILE")) profile_ = std::strcmp(env, "0") != 0;
 }
 
 Service::~Service() { shutdown(); }
@@ -284,6 +287,8 @@ bool Service::enqueue(Pending&& p, uint64_t tag, uint64_t cost, std::shared_ptr<
             return false;
         }
         p.net = current_;
+        p.seq = ++next_seq_;
+        p.queued = std::chrono::steady_clock::now();
         queued_.fetch_add(t->cost, std::memory_order_relaxed);
         queue_.push_back(std::move(p));
     }
@@ -318,16 +323,31 @@ void Service::fill_wave(std::unique_lock<std::mutex>& lk, uint32_t lane, long se
                m.snap_iters == hm.snap_iters && m.net_dims == hm.net_dims && m.depth == hm.depth &&
                std::memcmp(&m.cfr, &hm.cfr, sizeof(Cfr)) == 0;
     };
+    // A job once passed over stays passed over (compatibility is fixed and the
+    // wave's rows only grow), so each sweep examines only jobs that arrived
+    // since the last one, and closes the gaps it leaves in one pass: a burst
+    // of thousands of queued jobs costs each filling lane linear work, not a
+    // rescan per wake-up and a deque shift per job taken.
+    uint64_t seen = 0;
     auto sweep = [&]() {
-        for (auto it = queue_.begin(); it != queue_.end() && wave->size() < opts_.wave_jobs;) {
-            if (compatible(*it) && rows + it->rows <= opts_.wave_rows) {
-                rows += it->rows;
-                wave->push_back(std::move(*it));
-                it = queue_.erase(it);
-            } else {
-                ++it;
+        const size_t from = (size_t)(std::partition_point(queue_.begin(), queue_.end(),
+                                                          [&](const Pending& q) { return q.seq <= seen; }) -
+                                     queue_.begin());
+        size_t keep = from;
+        for (size_t i = from; i < queue_.size(); i++) {
+            Pending& q = queue_[i];
+            if (wave->size() < opts_.wave_jobs) {
+                seen = q.seq;
+                if (compatible(q) && rows + q.rows <= opts_.wave_rows) {
+                    rows += q.rows;
+                    wave->push_back(std::move(q));
+                    continue;
+                }
             }
+            if (keep != i) queue_[keep] = std::move(q);
+            keep++;
         }
+        queue_.erase(queue_.begin() + (long)keep, queue_.end());
     };
     const auto deadline = std::chrono::steady_clock::now() + std::chrono::microseconds(opts_.window_us);
     for (;;) {
@@ -370,8 +390,8 @@ void Service::answer(Flight& fl, bool ok, std::vector<Result>* results, std::str
 }
 
 void Service::lane_main(uint32_t lane) {
-    // this lane's share of the host's cores for packing and staging copies
-    ParBudget budget(std::max(1u, std::thread::hardware_concurrency()) / opts_.lanes);
+    // packing and staging copies draw on the process's shared host pool: a
+    // lane packing a large wave gets the cores the other lanes leave idle
     std::unique_ptr<Executor> ex(new Executor(device_, precision_));
     std::map<uint64_t, uint64_t> bank_of;  // service version -> executor version
     {
@@ -411,6 +431,16 @@ void Service::lane_main(uint32_t lane) {
         std::vector<Result> res;
         std::string err;
         const bool ok = ex->collect(&F.f, &res, &err);
+        if (profile_) {
+            // the reference's per-wave line (engine/src/gpu/service.rs:795-806):
+            // flight_ms runs from the launch to the results on the host
+            const double flight_ms =
+                std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - F.launched).count();
+            std::fprintf(stderr,
+                         "wc_service device=%d lane=%u class=%u jobs=%zu rows=%zu oldest_ms=%.2f pack_ms=%.2f "
+                         "flight_ms=%.2f\n",
+                         device_, lane, (unsigned)F.cls, F.tickets.size(), F.rows, F.oldest_ms, F.pack_ms, flight_ms);
+        }
         answer(F, ok, &res, err);
     };
     auto land_all = [&]() {
@@ -501,8 +531,14 @@ void Service::lane_main(uint32_t lane) {
         land(fl[k]);  // its slot is needed (normally landed already)
         Flight& F = fl[k];
         std::vector<std::shared_ptr<const Job>> jobs;
+        const auto t_pack = std::chrono::steady_clock::now();
+        F.cls = wave.front().cls;
+        F.rows = 0;
+        F.oldest_ms = 0;
         for (auto& p : wave) {
             F.tickets.push_back(p.ticket);
+            F.rows += p.rows;
+            F.oldest_ms = std::max(F.oldest_ms, std::chrono::duration<double, std::milli>(t_pack - p.queued).count());
             jobs.push_back(std::move(p.job));
         }
         F.version = net->version;
@@ -514,6 +550,8 @@ void Service::lane_main(uint32_t lane) {
                 err = std::string("packing the wave failed: ") + e.what();
             }
         }
+        F.launched = std::chrono::steady_clock::now();
+        F.pack_ms = std::chrono::duration<double, std::milli>(F.launched - t_pack).count();
         if (ok) ok = ex->launch(wh, exv, &F.f, &err);
         if (!ok) {
             std::vector<Result> none;

@@ -6,6 +6,7 @@
 #pragma once
 
 #include <atomic>
+#include <chrono>
 #include <condition_variable>
 #include <cstdint>
 #include <deque>
@@ -117,12 +118,19 @@ class Service {
         uint8_t cls = 0;
         size_t rows = 0;
         std::shared_ptr<const NetCopy> net;  // the weights current when the job was submitted
+        uint64_t seq = 0;                    // arrival order: the queue is sorted by it
+        std::chrono::steady_clock::time_point queued;
     };
     // One launched wave of a lane: its tickets, weight version and executor record.
     struct Flight {
         InFlight f;
         std::vector<std::shared_ptr<Ticket>> tickets;
         uint64_t version = 0;
+        // for the per-wave profile line
+        uint8_t cls = 0;
+        size_t rows = 0;
+        double oldest_ms = 0, pack_ms = 0;
+        std::chrono::steady_clock::time_point launched;
     };
     bool enqueue(Pending&& p, uint64_t tag, uint64_t cost, std::shared_ptr<Ticket>* out, std::string* err);
     void lane_main(uint32_t lane);
@@ -135,10 +143,12 @@ class Service {
 
     int device_, precision_;
     ServiceOpts opts_;
+    bool profile_ = false;  // WC_SERVICE_PROFILE: one line per landed wave on stderr
     std::vector<std::thread> lanes_;
     std::mutex mu_;
     std::condition_variable cv_;
     std::deque<Pending> queue_;
+    uint64_t next_seq_ = 0;
     bool stop_ = false;
     // Guarded routes (engine/src/gpu/service.rs:452-532): one at a time; the
     // other lanes land their waves, trim their executors once per epoch and
