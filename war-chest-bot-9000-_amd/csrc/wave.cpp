@@ -5,6 +5,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <memory>
 #include <string>
 #include <unordered_map>
 
@@ -221,21 +222,58 @@ struct JobAt {
 // task order), so the records are built in parallel chunks.
 void build_records(WaveHost* wp) {
     WaveHost& w = *wp;
+    // The child value-base lists: each opponent decision node's children's
+    // value bases, nodes in the order of their first value task (the unit
+    // tasks, then the top tasks). Built in three parallel passes over the
+    // tasks: each node's first task (an atomic minimum), the list bytes each
+    // chunk of tasks adds (a prefix over the chunks), then the writes.
     std::vector<uint32_t> cvb_at[2];
-    parallel_for(2, [&](size_t pi) {  // the child value-base lists (serial per player: append order)
-        const int p = (int)pi;
-        cvb_at[p].assign(w.nodes(), NONE);
-        auto note = [&](const Task& q) {
-            const uint32_t node = q.node;
+    for (int p = 0; p < 2; p++) {
+        const std::vector<Task>& unit_tasks = w.back_task[p];
+        const std::vector<Task>& top_tasks = w.top_back[p];
+        const size_t nu = unit_tasks.size(), n = nu + top_tasks.size();
+        auto node_of = [&](size_t i) { return i < nu ? unit_tasks[i].node : top_tasks[i - nu].node; };
+        auto opp = [&](uint32_t node) {
             const uint32_t kind = w.node_meta[node] & 3u, actor = w.node_meta[node] >> 2;
-            if (kind == 1 || actor == (uint32_t)p || cvb_at[p][node] != NONE) return;
-            cvb_at[p][node] = (uint32_t)w.child_vb[p].size();
-            for (uint32_t x = w.child_start[node]; x < w.child_start[node + 1]; x++)
-                w.child_vb[p].push_back(w.vals_base[2 * w.child[x] + p]);
+            return kind != 1 && actor != (uint32_t)p;
         };
-        for (const Task& q : w.back_task[p]) note(q);
-        for (const Task& q : w.top_back[p]) note(q);
-    });
+        std::vector<uint32_t> first(w.nodes(), NONE);  // each opponent node's first task
+        chunked(n, [&](size_t lo, size_t hi) {
+            for (size_t i = lo; i < hi; i++) {
+                const uint32_t node = node_of(i);
+                if (!opp(node)) continue;
+                uint32_t cur = __atomic_load_n(&first[node], __ATOMIC_RELAXED);
+                while ((uint32_t)i < cur &&
+                       !__atomic_compare_exchange_n(&first[node], &cur, (uint32_t)i, true, __ATOMIC_RELAXED,
+                                                    __ATOMIC_RELAXED)) {
+                }
+            }
+        });
+        constexpr size_t CHUNK = 16384;
+        const size_t nch = (n + CHUNK - 1) / CHUNK;
+        std::vector<size_t> at(nch + 1, 0);
+        parallel_for(nch, [&](size_t c) {
+            size_t len = 0;
+            for (size_t i = c * CHUNK; i < std::min(n, (c + 1) * CHUNK); i++) {
+                const uint32_t node = node_of(i);
+                if (opp(node) && first[node] == (uint32_t)i) len += w.child_start[node + 1] - w.child_start[node];
+            }
+            at[c + 1] = len;
+        });
+        for (size_t c = 0; c < nch; c++) at[c + 1] += at[c];
+        w.child_vb[p].resize(at[nch]);
+        cvb_at[p].assign(w.nodes(), NONE);  // written by the chunk holding the node's first task only
+        parallel_for(nch, [&](size_t c) {
+            size_t o = at[c];
+            for (size_t i = c * CHUNK; i < std::min(n, (c + 1) * CHUNK); i++) {
+                const uint32_t node = node_of(i);
+                if (!opp(node) || first[node] != (uint32_t)i) continue;
+                cvb_at[p][node] = (uint32_t)o;
+                for (uint32_t x = w.child_start[node]; x < w.child_start[node + 1]; x++)
+                    w.child_vb[p][o++] = w.vals_base[2 * w.child[x] + p];
+            }
+        });
+    }
     auto back = [&](int p, const Task& q) {
         const uint32_t node = q.node, c = q.config;
         const uint32_t kind = w.node_meta[node] & 3u, actor = w.node_meta[node] >> 2;
@@ -317,12 +355,21 @@ void build_records(WaveHost* wp) {
     // each unit's first slot from a prefix sum, then the units in parallel.
     const uint32_t heads = w.net.heads;
     const bool tower = readout_net(w.net.kind);
-    uint32_t nleaf[2] = {0, 0};
-    for (UnitDev& u : w.units)
+    std::vector<uint32_t> unit_leaves(2 * w.units.size());
+    parallel_for(w.units.size(), [&](size_t ui) {
+        const UnitDev& u = w.units[ui];
         for (int p = 0; p < 2; p++) {
-            u.leaf0[p] = nleaf[p];
-            for (uint32_t k = u.row0; k < u.row1; k++) nleaf[p] += w.nc(w.row_node[w.unit_row[k]], p);
-            u.leaf1[p] = nleaf[p];
+            uint32_t c = 0;
+            for (uint32_t k = u.row0; k < u.row1; k++) c += w.nc(w.row_node[w.unit_row[k]], p);
+            unit_leaves[2 * ui + p] = c;
+        }
+    });
+    uint32_t nleaf[2] = {0, 0};
+    for (size_t ui = 0; ui < w.units.size(); ui++)
+        for (int p = 0; p < 2; p++) {
+            w.units[ui].leaf0[p] = nleaf[p];
+            nleaf[p] += unit_leaves[2 * ui + p];
+            w.units[ui].leaf1[p] = nleaf[p];
         }
     parallel_for(2, [&](size_t p) { w.leaf_rec[p].resize(nleaf[p]); });
     for (int p = 0; p < 2; p++) {
@@ -354,32 +401,52 @@ void build_records(WaveHost* wp) {
     // Exported slots: the values read outside their unit, by the top
     // regions' rows or as a tree's root values. Only these leave an
     // LDS-staged unit sweep for HBM.
-    std::vector<uint8_t> ex[2], term_ex[2];
-    parallel_for(2, [&](size_t pi) {
-        const int p = (int)pi;
-        ex[p].assign(w.vals_len, 0);
-        for (const BackRec& r : w.top_back_rec[p]) {
-            const uint32_t n = r.kn & REC_N, kind = r.kn >> 30;
-            for (uint32_t k = 0; k < n; k++) {
-                uint32_t slot;
-                if (kind == BACK_OWN)
-                    slot = w.legal_value[r.start + k];
-                else if (kind == BACK_DRAW)
-                    slot = r.arg + w.draw_to[r.start + k];
-                else
-                    slot = w.child_vb[p][r.start + k] + r.arg;
-                if (slot < w.vals_len) ex[p][slot] = 1;
-            }
-        }
-        for (const TreeDev& t : w.trees)
-            for (uint32_t c = 0; c < w.nc(t.node0, p); c++) ex[p][w.vals_base[2 * t.node0 + p] + c] = 1;
+    // (flags set from several threads at once: relaxed atomic byte stores of
+    // the same value)
+    std::unique_ptr<uint8_t[]> ex[2];
+    std::vector<uint8_t> term_ex[2];
+    for (int p = 0; p < 2; p++) {
+        ex[p].reset(new uint8_t[w.vals_len]);  // cleared in parallel below
+        uint8_t* flag = ex[p].get();
+        chunked(w.vals_len, [&](size_t lo, size_t hi) { std::fill(flag + lo, flag + hi, (uint8_t)0); });
+        chunked(
+            w.top_back_rec[p].size(),
+            [&](size_t lo, size_t hi) {
+                for (size_t i = lo; i < hi; i++) {
+                    const BackRec& r = w.top_back_rec[p][i];
+                    const uint32_t n = r.kn & REC_N, kind = r.kn >> 30;
+                    for (uint32_t k = 0; k < n; k++) {
+                        uint32_t slot;
+                        if (kind == BACK_OWN)
+                            slot = w.legal_value[r.start + k];
+                        else if (kind == BACK_DRAW)
+                            slot = r.arg + w.draw_to[r.start + k];
+                        else
+                            slot = w.child_vb[p][r.start + k] + r.arg;
+                        if (slot < w.vals_len) __atomic_store_n(flag + slot, (uint8_t)1, __ATOMIC_RELAXED);
+                    }
+                }
+            },
+            4096);
+        chunked(
+            w.trees.size(),
+            [&](size_t lo, size_t hi) {
+                for (size_t t = lo; t < hi; t++) {
+                    const uint32_t node0 = w.trees[t].node0;
+                    for (uint32_t c = 0; c < w.nc(node0, p); c++)
+                        __atomic_store_n(flag + w.vals_base[2 * node0 + p] + c, (uint8_t)1, __ATOMIC_RELAXED);
+                }
+            },
+            64);
         term_ex[p].assign(w.unit_term.size(), 0);
-        for (size_t k = 0; k < w.unit_term.size(); k++) {
-            const uint32_t node = w.term_node[w.unit_term[k] & TERM_INDEX];
-            for (uint32_t c = 0; c < w.nc(node, p); c++)
-                if (ex[p][w.vals_base[2 * node + p] + c]) term_ex[p][k] = 1;
-        }
-    });
+        chunked(w.unit_term.size(), [&](size_t lo, size_t hi) {
+            for (size_t k = lo; k < hi; k++) {
+                const uint32_t node = w.term_node[w.unit_term[k] & TERM_INDEX];
+                for (uint32_t c = 0; c < w.nc(node, p); c++)
+                    if (ex[p][w.vals_base[2 * node + p] + c]) term_ex[p][k] = 1;
+            }
+        });
+    }
     for (int p = 0; p < 2; p++) {
         chunked(w.back_rec[p].size(), [&](size_t lo, size_t hi) {
             for (size_t k = lo; k < hi; k++)
@@ -398,45 +465,29 @@ void build_records(WaveHost* wp) {
 
 constexpr size_t WAVE_HOST_BYTES = 2336;  // sizeof(WaveHost) on x86-64 (libstdc++)
 static_assert(sizeof(WaveHost) == WAVE_HOST_BYTES, "a WaveHost member was added or changed: update reset()");
+// Lists the packer sizes with resize() and then overwrites whole keep their
+// length (and contents) here: the next resize then clears only what the
+// wave adds over the last one's length, instead of every entry of a few
+// hundred MB again. Lists built by appending are emptied.
 void WaveHost::reset() {
     const WaveHost blank;
-    auto keep = [](auto& v) { v.clear(); };
+    auto empty = [](auto& v) { v.clear(); };
     meta = blank.meta;
     net = blank.net;
-    for (auto* v : {&node_meta, &node_nc, &child_start, &child, &legal_row_of, &legal_off, &legal_value, &draw_off,
-                    &draw_row_off, &draw_row_start, &draw_to, &reach_base, &vals_base, &parent, &rev_row_of,
-                    &rev_start, &rev_src, &rev_cell, &rvd_row_of, &rvd_start, &rvd_src, &row_node, &row_cfg_off,
-                    &row_cfg, &cfg_key, &head_tile_n, &term_node, &exit_node, &exit_coff, &exit_reach, &unit_row, &unit_term,
-                    &cfg_job, &row_job})
-        keep(*v);
-    for (auto* v : {&draw_p, &rvd_p, &cfg_emb, &cfg_priv, &term_util, &roots, &carried, &card_feat}) keep(*v);
-    keep(jobs);
-    keep(trees);
-    keep(pub_raw);
-    keep(cfg_owner);
-    keep(units);
-    keep(node_top);
+    empty(jobs);
+    empty(units);
+    empty(node_top);
+    empty(legal_value);
+    empty(head_tile_n);
     for (int p = 0; p < 2; p++) {
-        keep(head_rb_n[p]);
-        keep(back_task[p]);
-        keep(reach_task[p]);
-        keep(decision[p]);
-        keep(back_lvl[p]);
-        keep(reach_lvl[p]);
-        keep(top_back[p]);
-        keep(top_reach[p]);
-        keep(top_back_lvl[p]);
-        keep(top_reach_lvl[p]);
-        keep(back_rec[p]);
-        keep(top_back_rec[p]);
-        keep(reach_rec[p]);
-        keep(top_reach_rec[p]);
-        keep(acc_rec[p]);
-        keep(leaf_rec[p]);
-        keep(pool_grp[p]);
-        keep(tower_blk[p]);
-        keep(tower_unit[p]);
-        keep(child_vb[p]);
+        empty(head_rb_n[p]);
+        empty(top_back[p]);
+        empty(top_reach[p]);
+        empty(top_back_lvl[p]);
+        empty(top_reach_lvl[p]);
+        empty(pool_grp[p]);
+        empty(tower_blk[p]);
+        empty(tower_unit[p]);
         top_dec0[p] = blank.top_dec0[p];
     }
     reach_len = blank.reach_len;
@@ -907,14 +958,40 @@ bool pack_wave(std::vector<std::shared_ptr<const Job>>&& jobs, WaveHost* out, st
     });
     // Pool groups: rows with the same config list (same tree, same
     // infostates in the same order), at most POOL_GROUP per group, in row
-    // order within a list; longest lists launch first.
-    for (int p = 0; p < 2; p++) {
+    // order within a list; longest lists launch first. Config ids are
+    // wave-global, so a list never spans two trees: each tree's lists are
+    // found on their own, in parallel, and concatenated in tree order, which
+    // keeps the lists in the order of their first rows.
+    // (Rows with an empty list share one list across the wave: they are set
+    // aside per tree and grouped once, in row order, after the others.)
+    auto emit = [&](const std::vector<uint32_t>& rows_of, int p, std::vector<PoolGroup>* out) {
+        for (size_t k = 0; k < rows_of.size(); k += POOL_GROUP) {
+            PoolGroup g{};
+            g.cfg = w.row_cfg_off[2 * rows_of[0] + p];
+            g.n = w.row_cfg_off[2 * rows_of[0] + p + 1] - g.cfg;
+            g.nrows = (uint32_t)std::min<size_t>(POOL_GROUP, rows_of.size() - k);
+            for (uint32_t i = 0; i < g.nrows; i++) g.row[i] = rows_of[k + i];
+            for (uint32_t i = 0; i < POOL_GROUP; i++)
+                g.rbase[i] = w.reach_base[2 * w.row_node[g.row[i < g.nrows ? i : 0]] + p];
+            out->push_back(g);
+        }
+    };
+    std::vector<std::vector<PoolGroup>> tree_grp(2 * J);
+    std::vector<std::vector<uint32_t>> tree_empty(2 * J);
+    parallel_for(2 * J, [&](size_t i) {
+        const int p = (int)(i & 1);
+        const size_t k = i >> 1;
+        const uint32_t ra = job_rows[k], rb = k + 1 < J ? job_rows[k + 1] : nrows;
         // lists keyed by a 64-bit hash of their contents; equal hashes are
         // confirmed element by element (a collision starts its own list)
         std::unordered_multimap<uint64_t, uint32_t> key_of;
         std::vector<std::vector<uint32_t>> lists;
-        for (uint32_t r = 0; r < nrows; r++) {
+        for (uint32_t r = ra; r < rb; r++) {
             const uint32_t a = w.row_cfg_off[2 * r + p], b = w.row_cfg_off[2 * r + p + 1];
+            if (a == b) {
+                tree_empty[i].push_back(r);
+                continue;
+            }
             uint64_t h = 0xcbf29ce484222325ull ^ (b - a);  // FNV-1a over the 32-bit entries
             for (uint32_t x = a; x < b; x++) h = (h ^ w.row_cfg[x]) * 0x100000001b3ull;
             uint32_t id = NONE;
@@ -932,19 +1009,17 @@ bool pack_wave(std::vector<std::shared_ptr<const Job>>&& jobs, WaveHost* out, st
             }
             lists[id].push_back(r);
         }
+        for (const auto& rows_of : lists) emit(rows_of, p, &tree_grp[i]);
+    });
+    for (int p = 0; p < 2; p++) {
         auto& out = w.pool_grp[p];
         out.clear();
-        for (const auto& rows_of : lists)
-            for (size_t k = 0; k < rows_of.size(); k += POOL_GROUP) {
-                PoolGroup g{};
-                g.cfg = w.row_cfg_off[2 * rows_of[0] + p];
-                g.n = w.row_cfg_off[2 * rows_of[0] + p + 1] - g.cfg;
-                g.nrows = (uint32_t)std::min<size_t>(POOL_GROUP, rows_of.size() - k);
-                for (uint32_t i = 0; i < g.nrows; i++) g.row[i] = rows_of[k + i];
-                for (uint32_t i = 0; i < POOL_GROUP; i++)
-                    g.rbase[i] = w.reach_base[2 * w.row_node[g.row[i < g.nrows ? i : 0]] + p];
-                out.push_back(g);
-            }
+        std::vector<uint32_t> empty;
+        for (size_t k = 0; k < J; k++) {
+            out.insert(out.end(), tree_grp[2 * k + p].begin(), tree_grp[2 * k + p].end());
+            empty.insert(empty.end(), tree_empty[2 * k + p].begin(), tree_empty[2 * k + p].end());
+        }
+        emit(empty, p, &out);  // n = 0: sorted after every other group
         std::stable_sort(out.begin(), out.end(), [](const PoolGroup& a, const PoolGroup& b) { return a.n > b.n; });
     }
     // Two-tower readout blocks: per tree and player, its rows times the
