@@ -164,6 +164,18 @@ void wc_executor_destroy(wc_executor* ex);
 uint64_t wc_executor_publish(wc_executor* ex, const wc_net_desc* net);
 /* Wave::pack: concatenate compatible jobs into one wave-global index space. */
 int wc_wave_pack(const uint8_t* const* jobs, const size_t* lens, uint32_t njobs, wc_wave** out);
+/* Packs new jobs into an existing wave, reusing its host buffers (no
+ * counterpart in the reference, whose Wave::pack always builds a new wave:
+ * for callers of wc_launch that pack wave after wave, as the service's lanes
+ * do). A wave already launched may be repacked at once: wc_launch keeps what
+ * the collection needs. If the jobs do not parse, the wave keeps its jobs; if
+ * packing fails after that, the wave holds no jobs until it is repacked, and
+ * every entry point taking it fails with WC_ERR_INVALID. */
+int wc_wave_repack(wc_wave* w, const uint8_t* const* jobs, const size_t* lens, uint32_t njobs);
+/* A 64-bit digest of every list and count of a packed wave, for tests and
+ * tooling that compare two packings of the same jobs (no counterpart in the
+ * reference). */
+int wc_wave_digest(const wc_wave* w, uint64_t* out);
 void wc_wave_free(wc_wave* w);
 
 /* Counts of a packed wave, for admission, benchmarks and the roofline. */

@@ -173,6 +173,47 @@ def test_service_style_mixed_waves_pass_the_deep_check():
         wave.close()
 
 
+def test_repacking_a_wave_equals_packing_it_fresh():
+    """A reused wave (wc_wave_repack, the service lanes' path) keeps the
+    lengths and old contents of the lists the packer overwrites whole, so a
+    list entry the packer missed would keep the previous wave's value. Packing
+    mixes of differently shaped jobs one after another into one wave must give
+    every list and count exactly as a fresh pack does (wc_wave_digest), also
+    after a larger wave and after a smaller one."""
+    spec = dict(iters=8, info_median=6.0, info_p99=40.0, info_cap=40)
+    pool = (W.jobs("wave256", trees=6, nodes_lo=30, nodes_hi=90, chance=1, terminal_p=0.15, notrans_p=0.05,
+                   nroots=2, seed=81, **spec)
+            + W.jobs("wave256", trees=4, nodes_lo=200, nodes_hi=400, nroots=1, seed=82, **spec)
+            + W.jobs("wave256", trees=4, nodes_lo=40, nodes_hi=120, chance=1, terminal_p=0.3, nroots=3, seed=83,
+                     **spec))
+    rng = np.random.default_rng(8)
+    mixes = [[pool[k] for k in rng.choice(len(pool), size=int(rng.integers(1, 25)), replace=True)]
+             for _ in range(12)]
+    fresh = []
+    for mix in mixes:
+        w = ww.Wave(mix)
+        fresh.append(w.digest())
+        w.close()
+    reused = ww.Wave(pool)  # the largest wave first
+    for mix, want in zip(mixes, fresh):
+        reused.repack(mix)
+        assert reused.digest() == want
+        assert reused.stats()["jobs"] == len(mix)
+    # jobs that do not parse leave the wave as it was; a failed pack leaves it unusable
+    with pytest.raises(ww.WaveError):
+        reused.repack([b"not a job"])
+    assert reused.digest() == fresh[-1]
+    with pytest.raises(ww.WaveError):
+        reused.repack([W.jobs("wave64", trees=1)[0], W.jobs("wave256", trees=1)[0]])  # two schedules
+    with pytest.raises(ww.WaveError, match="no packed jobs"):
+        reused.digest()
+    with pytest.raises(ww.WaveError, match="no packed jobs"):
+        reused.stats()
+    reused.repack(mixes[0])
+    assert reused.digest() == fresh[0]
+    reused.close()
+
+
 def test_synthesis_is_seeded_and_prefix_stable():
     a = W.jobs("wave64", trees=4)
     b = W.jobs("wave64", trees=6)

@@ -20,6 +20,7 @@ struct wc_executor {
 };
 struct wc_wave {
     WaveHost host;
+    bool packed = false;  // false after a failed wc_wave_repack: the lists are partial
 };
 struct wc_result {
     Result r;
@@ -125,41 +126,86 @@ uint64_t wc_executor_publish(wc_executor* ex, const wc_net_desc* net) {
     return v;
 }
 
-int wc_wave_pack(const uint8_t* const* jobs, const size_t* lens, uint32_t njobs, wc_wave** out) {
-    if (!jobs || !lens || !out || njobs == 0) return fail(WC_ERR_INVALID, "wc_wave_pack: empty wave");
-    return shielded("wc_wave_pack", [&] {
-    std::vector<Job> parsed(njobs);
+namespace {
+
+// The jobs of a wave parsed (in parallel), and the subtree-unit budget
+// (WC_UNIT_SLOTS tunes it: value slots per unit).
+int parse_wave(const char* fn, const uint8_t* const* jobs, const size_t* lens, uint32_t njobs, std::vector<Job>* parsed,
+               uint32_t* slots) {
+    parsed->assign(njobs, Job{});
     std::vector<std::string> errs(njobs);
     std::vector<uint8_t> bad(njobs, 0);
     parallel_for(njobs, [&](size_t k) {  // jobs parse independently
         if (!jobs[k]) {
             errs[k] = "null job";
             bad[k] = 1;
-        } else if (!from_bytes(jobs[k], lens[k], &parsed[k], &errs[k])) {
+        } else if (!from_bytes(jobs[k], lens[k], &(*parsed)[k], &errs[k])) {
             bad[k] = 1;
         }
     });
     for (uint32_t k = 0; k < njobs; k++)
-        if (bad[k]) return fail(WC_ERR_INVALID, "job " + std::to_string(k) + ": " + errs[k]);
-    std::string err;
-    // WC_UNIT_SLOTS tunes the subtree-unit budget (value slots per unit).
-    uint32_t slots = UNIT_SLOTS;
+        if (bad[k]) return fail(WC_ERR_INVALID, std::string(fn) + ": job " + std::to_string(k) + ": " + errs[k]);
+    *slots = UNIT_SLOTS;
     if (const char* env = std::getenv("WC_UNIT_SLOTS")) {
         long v = std::strtol(env, nullptr, 10);
         if (v < 64 || v > (1L << 24)) return fail(WC_ERR_INVALID, "WC_UNIT_SLOTS out of range [64, 2^24]");
-        slots = (uint32_t)v;
+        *slots = (uint32_t)v;
     }
-    std::unique_ptr<wc_wave> w(new wc_wave);
-    if (!pack_wave(std::move(parsed), &w->host, &err, slots)) return fail(WC_ERR_INVALID, err);
-    *out = w.release();
     return WC_OK;
+}
+
+// A wave whose last repack failed holds partial lists: nothing may read them.
+bool unpacked(const wc_wave* w, const char* fn) {
+    if (w->packed) return false;
+    fail(WC_ERR_INVALID, std::string(fn) + ": the wave holds no packed jobs (its last repack failed)");
+    return true;
+}
+
+}  // namespace
+
+int wc_wave_pack(const uint8_t* const* jobs, const size_t* lens, uint32_t njobs, wc_wave** out) {
+    if (!jobs || !lens || !out || njobs == 0) return fail(WC_ERR_INVALID, "wc_wave_pack: empty wave");
+    return shielded("wc_wave_pack", [&] {
+        std::vector<Job> parsed;
+        uint32_t slots = 0;
+        const int rc = parse_wave("wc_wave_pack", jobs, lens, njobs, &parsed, &slots);
+        if (rc != WC_OK) return rc;
+        std::string err;
+        std::unique_ptr<wc_wave> w(new wc_wave);
+        if (!pack_wave(std::move(parsed), &w->host, &err, slots)) return fail(WC_ERR_INVALID, err);
+        w->packed = true;
+        *out = w.release();
+        return WC_OK;
     });
+}
+
+int wc_wave_repack(wc_wave* w, const uint8_t* const* jobs, const size_t* lens, uint32_t njobs) {
+    if (!w || !jobs || !lens || njobs == 0) return fail(WC_ERR_INVALID, "wc_wave_repack: null argument or empty wave");
+    return shielded("wc_wave_repack", [&] {
+        std::vector<Job> parsed;
+        uint32_t slots = 0;
+        const int rc = parse_wave("wc_wave_repack", jobs, lens, njobs, &parsed, &slots);
+        if (rc != WC_OK) return rc;  // the wave keeps its jobs
+        w->packed = false;
+        std::string err;
+        if (!pack_wave(std::move(parsed), &w->host, &err, slots)) return fail(WC_ERR_INVALID, err);
+        w->packed = true;
+        return WC_OK;
+    });
+}
+
+int wc_wave_digest(const wc_wave* w, uint64_t* out) {
+    if (!w || !out) return fail(WC_ERR_INVALID, "wc_wave_digest: null argument");
+    if (unpacked(w, "wc_wave_digest")) return WC_ERR_INVALID;
+    *out = digest(w->host);
+    return WC_OK;
 }
 
 void wc_wave_free(wc_wave* w) { delete w; }
 
 int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
     if (!w || !s) return fail(WC_ERR_INVALID, "wc_wave_stats_get: null argument");
+    if (unpacked(w, "wc_wave_stats_get")) return WC_ERR_INVALID;
     const WaveHost& h = w->host;
     std::memset(s, 0, sizeof *s);
     s->jobs = (uint32_t)h.jobs.size();
@@ -257,6 +303,7 @@ const uint32_t* wc_wave_array(const wc_wave* w, const char* name, size_t* n) {
         fail(WC_ERR_INVALID, "wc_wave_array: null argument");
         return nullptr;
     }
+    if (unpacked(w, "wc_wave_array")) return nullptr;
     const WaveHost& h = w->host;
     const std::vector<uint32_t>* v = nullptr;
     const std::string k = name;
@@ -301,6 +348,7 @@ int wc_value_net_plan(const uint32_t* cols, uint32_t nrb, uint32_t heads, uint32
 
 int wc_solve_wave(wc_executor* ex, wc_wave* w, uint64_t version, wc_result** results) {
     if (!ex || !w || !results) return fail(WC_ERR_INVALID, "wc_solve_wave: null argument");
+    if (unpacked(w, "wc_solve_wave")) return WC_ERR_INVALID;
     return shielded("wc_solve_wave", [&] {
         std::vector<Result> out;
         std::string err;
@@ -312,6 +360,7 @@ int wc_solve_wave(wc_executor* ex, wc_wave* w, uint64_t version, wc_result** res
 
 int wc_launch(wc_executor* ex, wc_wave* w, uint64_t version, wc_inflight** out) {
     if (!ex || !w || !out) return fail(WC_ERR_INVALID, "wc_launch: null argument");
+    if (unpacked(w, "wc_launch")) return WC_ERR_INVALID;
     return shielded("wc_launch", [&] {
         std::unique_ptr<wc_inflight> f(new wc_inflight);
         std::string err;
@@ -338,6 +387,7 @@ int wc_collect(wc_executor* ex, wc_inflight* f, wc_result** results) {
 int wc_wave_leaf_probe(wc_executor* ex, wc_wave* w, uint64_t version, int traverser, float* values, size_t cap,
                        size_t* count, float* mass) {
     if (!ex || !w || !count || (cap && !values)) return fail(WC_ERR_INVALID, "wc_wave_leaf_probe: null argument");
+    if (unpacked(w, "wc_wave_leaf_probe")) return WC_ERR_INVALID;
     return shielded("wc_wave_leaf_probe", [&] {
         std::vector<float> v, m;
         std::string err;
@@ -353,6 +403,7 @@ int wc_wave_leaf_trace(wc_executor* ex, wc_wave* w, uint64_t version, const int3
                        float* values, size_t values_cap, float* mass, size_t mass_cap, float* reach, size_t reach_cap,
                        size_t* counts) {
     if (!ex || !w || !counts || (npoints && !points)) return fail(WC_ERR_INVALID, "wc_wave_leaf_trace: null argument");
+    if (unpacked(w, "wc_wave_leaf_trace")) return WC_ERR_INVALID;
     return shielded("wc_wave_leaf_trace", [&] {
         const WaveHost& h = w->host;
         size_t c[4] = {0, 0, h.rows(), 0};
@@ -382,6 +433,7 @@ int wc_wave_leaf_trace(wc_executor* ex, wc_wave* w, uint64_t version, const int3
 int wc_time_wave(wc_executor* ex, wc_wave* w, uint64_t version, uint32_t warmup, uint32_t reps, double* wave_ms,
                  double* kernel_ms) {
     if (!ex || !w || !wave_ms) return fail(WC_ERR_INVALID, "wc_time_wave: null argument");
+    if (unpacked(w, "wc_time_wave")) return WC_ERR_INVALID;
     ScheduleTimes prof;
     std::string err;
     const int rc = shielded("wc_time_wave", [&] {

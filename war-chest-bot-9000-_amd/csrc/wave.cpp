@@ -464,7 +464,7 @@ void build_records(WaveHost* wp) {
 }  // namespace
 
 constexpr size_t WAVE_HOST_BYTES = 2336;  // sizeof(WaveHost) on x86-64 (libstdc++)
-static_assert(sizeof(WaveHost) == WAVE_HOST_BYTES, "a WaveHost member was added or changed: update reset()");
+static_assert(sizeof(WaveHost) == WAVE_HOST_BYTES, "a WaveHost member was added or changed: update reset() and digest()");
 // Lists the packer sizes with resize() and then overwrites whole keep their
 // length (and contents) here: the next resize then clears only what the
 // wave adds over the last one's length, instead of every entry of a few
@@ -1096,6 +1096,62 @@ bool pack_wave(std::vector<std::shared_ptr<const Job>>&& jobs, WaveHost* out, st
     }();
     if ((!validated || force_deep) && !validate_deep(w, err)) return false;
     return true;
+}
+
+uint64_t digest(const WaveHost& w) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    auto word = [&](uint64_t v) { h = (h ^ v) * 0x100000001b3ull; };
+    auto list = [&](const auto& v) {
+        const uint8_t* b = (const uint8_t*)v.data();
+        const size_t n = v.size() * sizeof(v[0]);
+        word(n);
+        size_t i = 0;
+        for (; i + 8 <= n; i += 8) {
+            uint64_t x;
+            std::memcpy(&x, b + i, 8);
+            word(x);
+        }
+        uint64_t tail = 0;
+        std::memcpy(&tail, b + i, n - i);
+        word(tail);
+    };
+    for (const auto* v : {&w.node_meta, &w.node_nc, &w.child_start, &w.child, &w.legal_row_of, &w.legal_off,
+                          &w.legal_value, &w.draw_off, &w.draw_row_off, &w.draw_row_start, &w.draw_to, &w.reach_base,
+                          &w.vals_base, &w.parent, &w.rev_row_of, &w.rev_start, &w.rev_src, &w.rev_cell, &w.rvd_row_of,
+                          &w.rvd_start, &w.rvd_src, &w.row_node, &w.row_cfg_off, &w.row_cfg, &w.cfg_key,
+                          &w.head_tile_n, &w.term_node, &w.exit_node, &w.exit_coff, &w.exit_reach, &w.unit_row,
+                          &w.unit_term, &w.cfg_job, &w.row_job})
+        list(*v);
+    for (const auto* v : {&w.draw_p, &w.rvd_p, &w.cfg_emb, &w.cfg_priv, &w.term_util, &w.roots, &w.carried, &w.card_feat})
+        list(*v);
+    list(w.pub_raw);
+    list(w.cfg_owner);
+    list(w.node_top);
+    list(w.trees);
+    list(w.units);
+    for (int p = 0; p < 2; p++) {
+        for (const auto* v : {&w.head_rb_n[p], &w.back_lvl[p], &w.reach_lvl[p], &w.top_back_lvl[p], &w.top_reach_lvl[p],
+                              &w.child_vb[p]})
+            list(*v);
+        for (const auto* v : {&w.back_task[p], &w.reach_task[p], &w.decision[p], &w.top_back[p], &w.top_reach[p]})
+            list(*v);
+        list(w.back_rec[p]);
+        list(w.top_back_rec[p]);
+        list(w.reach_rec[p]);
+        list(w.top_reach_rec[p]);
+        list(w.acc_rec[p]);
+        list(w.leaf_rec[p]);
+        list(w.pool_grp[p]);
+        list(w.tower_blk[p]);
+        list(w.tower_unit[p]);
+        word(w.top_dec0[p]);
+    }
+    for (uint64_t x : {(uint64_t)w.jobs.size(), (uint64_t)w.reach_len, (uint64_t)w.vals_len, (uint64_t)w.ncells,
+                       (uint64_t)w.root_values_len, (uint64_t)w.snapshot_configs, (uint64_t)w.nsub,
+                       (uint64_t)w.lvl_len, (uint64_t)w.top_levels, (uint64_t)w.max_levels, (uint64_t)w.nroots_max,
+                       (uint64_t)w.carry_slots, (uint64_t)w.max_vwin, (uint64_t)w.max_rwin, w.tower_len})
+        word(x);
+    return h;
 }
 
 // Every index a kernel dereferences, checked against the buffer it indexes.

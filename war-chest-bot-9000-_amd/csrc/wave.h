@@ -255,6 +255,10 @@ struct WaveHost {
 bool pack_wave(std::vector<std::shared_ptr<const Job>>&& jobs, WaveHost* w, std::string* err,
                uint32_t unit_slots = UNIT_SLOTS, bool validated = false);
 // The same for jobs owned by the caller (moved into the wave).
+// A 64-bit digest of every list and count of a packed wave (FNV-1a over
+// 8-byte words), for tests that compare two packings of the same jobs.
+uint64_t digest(const WaveHost& w);
+
 bool pack_wave(std::vector<Job>&& jobs, WaveHost* w, std::string* err, uint32_t unit_slots = UNIT_SLOTS,
                bool validated = false);
 

@@ -124,7 +124,7 @@ EXPORTS = [
     "wc_result_tag", "wc_result_weight_version", "wc_result_strategy", "wc_result_root_values",
     "wc_result_carries", "wc_result_routes", "wc_result_free",
     "wc_executor_create", "wc_executor_destroy", "wc_executor_publish",
-    "wc_wave_pack", "wc_wave_free", "wc_wave_stats_get", "wc_wave_array", "wc_value_net_plan", "wc_solve_wave",
+    "wc_wave_pack", "wc_wave_repack", "wc_wave_digest", "wc_wave_free", "wc_wave_stats_get", "wc_wave_array", "wc_value_net_plan", "wc_solve_wave",
     "wc_launch", "wc_inflight_ready", "wc_collect", "wc_wave_leaf_probe", "wc_wave_leaf_trace",
     "wc_time_wave", "wc_peak_probe",
     "wc_mlp_forward", "wc_mlp_forward_noalloc", "wc_time_mlp",
@@ -192,6 +192,8 @@ def _declare(L):
     L.wc_executor_publish.argtypes = [C.c_void_p, C.POINTER(NetDesc)]
     L.wc_executor_publish.restype = C.c_uint64
     L.wc_wave_pack.argtypes = [C.POINTER(_u8p), C.POINTER(C.c_size_t), C.c_uint32, C.POINTER(C.c_void_p)]
+    L.wc_wave_repack.argtypes = [C.c_void_p, C.POINTER(_u8p), C.POINTER(C.c_size_t), C.c_uint32]
+    L.wc_wave_digest.argtypes = [C.c_void_p, C.POINTER(C.c_uint64)]
     L.wc_wave_free.argtypes = [C.c_void_p]
     L.wc_wave_free.restype = None
     L.wc_wave_stats_get.argtypes = [C.c_void_p, C.POINTER(WaveStats)]
@@ -444,14 +446,30 @@ class Wave:
     """`Wave::pack` over WCJ8 jobs."""
 
     def __init__(self, jobs: Sequence[bytes]):
-        L = lib()
-        held = [_bytes_ptr(j) for j in jobs]  # the library parses the jobs during the call
-        ptrs = (_u8p * len(jobs))(*[p for _, p in held])
-        lens = (C.c_size_t * len(jobs))(*[len(j) for j in jobs])
+        held, ptrs, lens = Wave._marshal(jobs)  # the library parses the jobs during the call
         h = C.c_void_p()
-        _check(L.wc_wave_pack(ptrs, lens, len(jobs), C.byref(h)))
+        _check(lib().wc_wave_pack(ptrs, lens, len(jobs), C.byref(h)))
         self.h = h
         self.njobs = len(jobs)
+
+    @staticmethod
+    def _marshal(jobs):
+        held = [_bytes_ptr(j) for j in jobs]
+        ptrs = (_u8p * len(jobs))(*[p for _, p in held])
+        lens = (C.c_size_t * len(jobs))(*[len(j) for j in jobs])
+        return held, ptrs, lens
+
+    def repack(self, jobs: Sequence[bytes]):
+        """Pack other jobs into this wave's host buffers (wc_wave_repack)."""
+        held, ptrs, lens = Wave._marshal(jobs)
+        _check(lib().wc_wave_repack(self.h, ptrs, lens, len(jobs)))
+        self.njobs = len(jobs)
+
+    def digest(self) -> int:
+        """A digest of every packed list and count (wc_wave_digest)."""
+        d = C.c_uint64()
+        _check(lib().wc_wave_digest(self.h, C.byref(d)))
+        return int(d.value)
 
     def stats(self) -> dict:
         s = WaveStats()
