@@ -101,7 +101,7 @@ def main():
     ap.add_argument("--no-mlp", action="store_true", help="skip the GEMM-chain-alone leg")
     ap.add_argument("--no-host", action="store_true", help="skip the host-path (PCIe-inclusive) leg")
     ap.add_argument("--no-v5", action="store_true", help="skip the v5-network wave leg")
-    ap.add_argument("--service", type=int, default=24, metavar="WAVES",
+    ap.add_argument("--service", type=int, default=48, metavar="WAVES",
                     help="stream WAVES copies of the wave's subgames through the service and report the end-to-end "
                          "rate: prepared jobs (wc_prepare once, wc_submit_prepared per wave, as the reference's "
                          "throughput tape does) and, beside it, WCJ8 bytes per submission (wc_submit); 0 skips it")
@@ -391,7 +391,9 @@ def main():
 
         lanes, subs = args.service_lanes, 8
         prec = ww.WC_BF16 if tower else ww.WC_F16
-        cl = ww.spawn(0, net, prec, lanes=lanes, wave_jobs=len(jobs), wave_rows=1 << 30, window_us=100000)
+        # waves of up to 256 jobs and the reference's own row target and fill
+        # window (engine/src/gpu/service.rs:554-556: 48k rows, 800 us)
+        cl = ww.spawn(0, net, prec, lanes=lanes, wave_jobs=len(jobs), wave_rows=48 * 1024, window_us=800)
 
         launched = {}
 
@@ -435,7 +437,8 @@ def main():
                           "note": "end to end through the C ABI: jobs prepared once (parse, validate, cost) and "
                                   "submitted per wave, results waited on; lanes pack over one shared host thread pool, "
                                   "pinned transfers, lanes overlap on their own streams; the service forms its own "
-                                  "device waves (one cost class each: device_waves per WAVES). bytes_ms_per_wave: WCJ8 bytes per submission "
+                                  "device waves (one cost class each, at most 256 jobs and 48k network rows, an "
+                                  "800 us fill window from the oldest job: device_waves per WAVES). bytes_ms_per_wave: WCJ8 bytes per submission "
                                   "(parsed and validated every time). After full-size warm-up waves of both kinds, "
                                   "the two kinds are timed alternately, twice each (the means)"}
         log(f"[bench] service: {dt / args.service * 1e3:.1f} ms per wave end to end with prepared jobs, "

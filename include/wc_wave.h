@@ -78,7 +78,7 @@ typedef struct wc_service_opts {
     uint32_t lanes;        /* executor lanes (streams) per device; reference WARCHEST_WAVE_LANES, default 2 */
     uint32_t wave_jobs;    /* max jobs per wave; reference WARCHEST_WAVE_JOBS, default 64 */
     uint32_t wave_rows;    /* max network rows per wave; reference WARCHEST_WAVE_ROWS, default 49152 */
-    uint32_t window_us;    /* bucket-fill window; reference WARCHEST_WAVE_US, default 800 */
+    uint32_t window_us;    /* bucket-fill window, counted from the seed job's arrival; reference WARCHEST_WAVE_US, default 800 */
     uint32_t whale_lanes;  /* lanes that take exclusive-route jobs; reference WARCHEST_WAVE_WHALE_LANES,
                               default (0) 1, clamped to 1..lanes (service.rs:100) */
     uint32_t class_shift;  /* coarsens the cost classes; reference WARCHEST_WAVE_CLASS_SHIFT, 0..2 (service.rs:993) */

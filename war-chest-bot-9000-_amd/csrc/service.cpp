@@ -306,12 +306,13 @@ long Service::first_for(uint32_t lane) const {
 
 // Bucket a seed with compatible followers: the same weight version, cost
 // class and schedule metadata, at most wave_jobs jobs and wave_rows network
-// rows, filling for up to window_us; a class-31 seed runs alone
+// rows, filling until window_us after the seed was queued; a class-31 seed runs alone
 // (engine/src/gpu/service.rs:554-637).
 void Service::fill_wave(std::unique_lock<std::mutex>& lk, uint32_t lane, long seed, std::vector<Pending>* wave) {
     wave->push_back(std::move(queue_[(size_t)seed]));
     queue_.erase(queue_.begin() + seed);
     const Pending& head = wave->front();
+    const auto seed_queued = head.queued;
     if (head.cls == 31) return;
     const Meta hm = head.job->meta;
     const uint64_t hv = head.net->version;
@@ -349,7 +350,10 @@ void Service::fill_wave(std::unique_lock<std::mutex>& lk, uint32_t lane, long se
         }
         queue_.erase(queue_.begin() + (long)keep, queue_.end());
     };
-    const auto deadline = std::chrono::steady_clock::now() + std::chrono::microseconds(opts_.window_us);
+    // The fill window runs from the seed's arrival, not from now: a seed that
+    // has already waited that long in the queue (a burst of submissions)
+    // starts its wave with what is there (engine/src/gpu/service.rs:587-593).
+    const auto deadline = seed_queued + std::chrono::microseconds(opts_.window_us);
     for (;;) {
         sweep();
         if (wave->size() >= opts_.wave_jobs || stop_ || (guard_ && guard_lane_ != lane)) break;
@@ -430,16 +434,22 @@ void Service::lane_main(uint32_t lane) {
         if (!F.f.live) return;
         std::vector<Result> res;
         std::string err;
+        const auto t_collect = std::chrono::steady_clock::now();
         const bool ok = ex->collect(&F.f, &res, &err);
         if (profile_) {
             // the reference's per-wave line (engine/src/gpu/service.rs:795-806):
-            // flight_ms runs from the launch to the results on the host
-            const double flight_ms =
-                std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - F.launched).count();
+            // launch_ms is the launch call (staging copy, upload and schedule
+            // enqueued), flight_ms runs from the launch to the results on the
+            // host, collect_ms is the collection (waiting for the device, then
+            // the results unpacked)
+            const auto now = std::chrono::steady_clock::now();
+            const double flight_ms = std::chrono::duration<double, std::milli>(now - F.launched).count();
+            const double collect_ms = std::chrono::duration<double, std::milli>(now - t_collect).count();
             std::fprintf(stderr,
                          "wc_service device=%d lane=%u class=%u jobs=%zu rows=%zu oldest_ms=%.2f pack_ms=%.2f "
-                         "flight_ms=%.2f\n",
-                         device_, lane, (unsigned)F.cls, F.tickets.size(), F.rows, F.oldest_ms, F.pack_ms, flight_ms);
+                         "launch_ms=%.2f flight_ms=%.2f collect_ms=%.2f\n",
+                         device_, lane, (unsigned)F.cls, F.tickets.size(), F.rows, F.oldest_ms, F.pack_ms,
+                         F.launch_ms, flight_ms, collect_ms);
         }
         answer(F, ok, &res, err);
     };
@@ -553,6 +563,8 @@ void Service::lane_main(uint32_t lane) {
         F.launched = std::chrono::steady_clock::now();
         F.pack_ms = std::chrono::duration<double, std::milli>(F.launched - t_pack).count();
         if (ok) ok = ex->launch(wh, exv, &F.f, &err);
+        F.launch_ms =
+            std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - F.launched).count();
         if (!ok) {
             std::vector<Result> none;
             answer(F, false, &none, err);

@@ -129,7 +129,7 @@ class Service {
         // for the per-wave profile line
         uint8_t cls = 0;
         size_t rows = 0;
-        double oldest_ms = 0, pack_ms = 0;
+        double oldest_ms = 0, pack_ms = 0, launch_ms = 0;
         std::chrono::steady_clock::time_point launched;
     };
     bool enqueue(Pending&& p, uint64_t tag, uint64_t cost, std::shared_ptr<Ticket>* out, std::string* err);
