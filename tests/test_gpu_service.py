@@ -9,7 +9,8 @@ not with another run of the device.
   bit-identical to the oracle's solve of that job (the reference's lanes,
   engine/src/gpu/service.rs:546-742);
 - wc_launch / wc_collect (engine/src/gpu/device.rs:596-831): two waves in
-  flight on one executor, the packed wave freed while its wave runs;
+  flight on one executor, the packed wave freed while its wave runs, and a
+  wave repacked (wc_wave_repack) while its solve is in flight;
 - cost classes and guarded routes (service.rs:452-532,967-991): exclusive
   jobs run in one-job waves, guarded jobs after every lane has drained and
   trimmed, and the results carry their route flags (client.rs:119-121).
@@ -132,6 +133,37 @@ def test_launch_collect_two_waves_in_flight():
     for k, (g, r) in enumerate(zip(got, ref)):
         same(g, r, f"job {k}")
     same(got_c[0], ref[0], "relaunch")
+
+
+def test_repack_while_the_wave_is_in_flight():
+    """wc_wave_repack into a wave whose solve is still in flight (the service's
+    lanes repack their wave right after launching it): the wave in flight keeps
+    what it was launched with, and the repacked wave, launched next on the same
+    executor, solves its own jobs. Both bit-identical to the oracle, with waves
+    of different sizes so the reused lists shrink and grow."""
+    jobs = small_jobs(9, 59)
+    net = W.net_for("wave256")
+    ref = alone(jobs, net)
+    say("case repack in flight: waves of 6, 3 and 6 jobs through one reused wave on one executor")
+    ex = ww.Executor(0, ww.WC_PRECISE)
+    v = ex.publish(net)
+    w = ww.Wave(jobs[:6])
+    f1 = ex.launch(w, v)
+    w.repack(jobs[6:])  # smaller, while the first solve runs
+    f2 = ex.launch(w, v)
+    got1 = f1.collect()
+    w.repack(jobs[:6])  # larger again, while the second solve runs
+    got2 = f2.collect()
+    f3 = ex.launch(w, v)
+    got3 = f3.collect()
+    w.close()
+    ex.close()
+    for k, g in enumerate(got1):
+        same(g, ref[k], f"first wave, job {k}")
+    for k, g in enumerate(got2):
+        same(g, ref[6 + k], f"repacked wave, job {k}")
+    for k, g in enumerate(got3):
+        same(g, ref[k], f"repacked again, job {k}")
 
 
 def test_cost_classes_and_guarded_routes():
