@@ -90,6 +90,45 @@ def test_small_wave_float32_bit_exact():
         assert_bit_exact(g, o, f"tree {k}")
 
 
+CFR_VARIANTS = {  # the reference's schedules, engine/src/search.rs:141-179: alpha, beta, gamma, predict
+    "linear": (1.0, 1.0, 1.0, 0.0),
+    "plus": (float("inf"), float("-inf"), 2.0, 0.0),
+    "dcfr": (1.5, 0.0, 2.0, 0.0),
+    "pcfr": (float("inf"), float("-inf"), 2.0, 1.0),
+    "sapcfr": (float("inf"), float("-inf"), 2.0, float(np.float32(1.0 / 3.0))),
+}
+
+
+@pytest.mark.parametrize("variant", sorted(CFR_VARIANTS))
+def test_cfr_variants_float32_bit_exact(variant):
+    """Every discounting schedule the reference names (linear CFR, CFR+, DCFR,
+    predictive and SAPCFR: infinite alpha / beta, a fractional prediction), on a
+    small wave with chance nodes, terminals and carried roots, part of it in
+    top regions (a 300-slot unit budget): strategy, roots and carries
+    bit-identical to the oracle's."""
+    a, b, g, p = CFR_VARIANTS[variant]
+    jobs = small_wave(trees=6, seed=97, alpha=a, beta=b, gamma=g, predict=p)
+    net = W.net_for("wave256")
+    say(f"case cfr variant {variant}: {len(jobs)} trees, 8 iterations, 300-slot unit budget")
+    got = solve_with_budget(jobs, net, ww.WC_PRECISE, 300)
+    for k, (j, r) in enumerate(zip(jobs, got)):
+        assert_bit_exact(r, O.solve(j, net, O.NET_F32), f"{variant} tree {k}")
+
+
+@pytest.mark.parametrize("iters", [0, 1, 3, 5])
+def test_short_and_odd_schedules_float32_bit_exact(iters):
+    """Schedules of 0, 1, 3 and 5 iterations (no iteration at all: the uniform
+    start's average and root values; snapshots at every power of two and at the
+    end, a carry slot per snapshot but the last): bit-identical to the
+    oracle's."""
+    jobs = small_wave(trees=4, seed=91, iters=iters, nroots=2)
+    net = W.net_for("wave256")
+    say(f"case schedule of {iters} iterations: {len(jobs)} trees")
+    got = gpu_solve(jobs, net, ww.WC_PRECISE)
+    for k, (j, r) in enumerate(zip(jobs, got)):
+        assert_bit_exact(r, O.solve(j, net, O.NET_F32), f"{iters} iterations, tree {k}")
+
+
 def solve_with_budget(jobs, net, precision, slots):
     """Pack with a given subtree-unit budget (WC_UNIT_SLOTS), so that the top-region
     path (nodes whose subtree does not fit one unit) carries most of the tree."""
