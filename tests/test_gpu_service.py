@@ -135,6 +135,28 @@ def test_launch_collect_two_waves_in_flight():
     same(got_c[0], ref[0], "relaunch")
 
 
+def test_mixed_schedules_are_bucketed_apart():
+    """Jobs of different schedules submitted interleaved (DCFR and linear CFR,
+    8 and 5 iterations) share no wave: the service buckets only jobs with the
+    same schedule metadata (engine/src/gpu/service.rs:621-637). Every result
+    bit-identical to the oracle's solve of its own job."""
+    net = W.net_for("wave256")
+    groups = [small_jobs(4, 63), small_jobs(4, 65, alpha=1.0, beta=1.0, gamma=1.0),
+              small_jobs(4, 67, iters=5)]
+    jobs = [j for trio in zip(*groups) for j in trio]  # interleaved
+    ref = alone(jobs, net)
+    say("case mixed schedules: 12 jobs of three schedules interleaved, 2 lanes, waves of up to 64")
+    with ww.spawn(0, net, ww.WC_PRECISE, lanes=2, wave_jobs=64, window_us=200_000) as client:
+        handles = [client.submit(j, tag=k) for k, j in enumerate(jobs)]
+        got = [h.wait() for h in handles]
+        stats = client.stats()
+    say(f"{stats['waves']} waves")
+    assert stats["waves"] >= 3
+    for k, (g, r) in enumerate(zip(got, ref)):
+        assert g.tag == k
+        same(g, r, f"job {k}")
+
+
 def test_repack_while_the_wave_is_in_flight():
     """wc_wave_repack into a wave whose solve is still in flight (the service's
     lanes repack their wave right after launching it): the wave in flight keeps
