@@ -9,6 +9,7 @@
 // packed on all the cores the others are not using.
 #pragma once
 
+#include <pthread.h>
 #include <sched.h>
 
 #include <algorithm>
@@ -97,6 +98,16 @@ class HostPool {
     };
 
     explicit HostPool(unsigned workers) {
+        // A fork copies only the forking thread: the pool's lock is taken
+        // across the fork so that no worker holds it in the child, whose pool
+        // then has no workers (its loops run on their callers).
+        pthread_atfork([] { get().mu_.lock(); }, [] { get().mu_.unlock(); },
+                       [] {
+                           HostPool& p = get();
+                           p.workers_.clear();
+                           p.loops_.clear();
+                           p.mu_.unlock();
+                       });
         for (unsigned w = 0; w < workers; w++) workers_.emplace_back([this] { worker(); });
         for (auto& th : workers_) th.detach();
     }
