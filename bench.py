@@ -387,63 +387,57 @@ def main():
         # The drop-in's own throughput, as the reference measures it with its
         # throughput tape (engine/examples/wave_tape.rs:80-99): jobs prepared once
         # and submitted wave after wave by several threads, results waited on.
-        from concurrent.futures import ThreadPoolExecutor
+        # A native caller of the C ABI does it (wc_tape, built beside the
+        # library), in a child process: the figure is the library's, not the
+        # Python binding's.
+        import struct
+        import subprocess
+        import tempfile
 
         lanes, subs = args.service_lanes, 8
         prec = ww.WC_BF16 if tower else ww.WC_F16
-        # waves of up to 256 jobs and the reference's own row target and fill
-        # window (engine/src/gpu/service.rs:554-556: 48k rows, 800 us)
-        cl = ww.spawn(0, net, prec, lanes=lanes, wave_jobs=len(jobs), wave_rows=48 * 1024, window_us=800)
-
-        launched = {}
-
-        def stream(submit, items):
-            w0 = cl.stats()["waves"]
-            t0 = time.time()
-            with ThreadPoolExecutor(subs) as pool:
-                hs = list(pool.map(submit, items))
-            for h in hs:
-                h.wait()
-            dt = time.time() - t0
-            launched[submit] = launched.get(submit, 0) + cl.stats()["waves"] - w0
-            return dt
-
-        t = time.time()
-        prepared = [ww.PreparedJob(j, prec) for j in jobs]
-        prep_ms = (time.time() - t) * 1e3
-        waves = lambda n, xs: [(i, x) for _ in range(n) for i, x in enumerate(xs)]  # noqa: E731
-        by_prep = lambda ip: cl.submit_prepared(ip[1], tag=ip[0])  # noqa: E731
-        by_bytes = lambda ij: cl.submit(ij[1], tag=ij[0])  # noqa: E731
-        # warm-up: full-size waves of both kinds on every lane (each lane sizes its
-        # device buffers and pinned staging on its first waves)
-        stream(by_prep, waves(lanes, prepared))
-        stream(by_bytes, waves(lanes, jobs))
-        # timed: the two kinds alternately, twice each
-        dt = dt_raw = 0.0
-        launched.clear()
-        for _ in range(2):
-            dt += stream(by_prep, waves(args.service, prepared))
-            dt_raw += stream(by_bytes, waves(args.service, jobs))
-        dt, dt_raw = dt / 2, dt_raw / 2
-        cl.close()
+        tape_bin = os.path.join(ROOT, "war-chest-bot-9000-_amd", "wc_tape")
+        if not os.path.exists(tape_bin):
+            raise SystemExit(f"{tape_bin} is missing: build first (python __graft_entry__.py)")
+        with tempfile.NamedTemporaryFile(prefix="wc_", suffix=".tape", delete=False) as f:
+            f.write(b"WCTP" + struct.pack("<I", len(jobs)))
+            for j in jobs:
+                f.write(struct.pack("<Q", len(j)) + j)
+            dims = np.asarray(net.dims, np.uint32)
+            f.write(struct.pack("<I", dims.size) + dims.tobytes())
+            for arr in (net.w, net.b, net.ln if net.ln is not None else np.zeros(0, np.float32)):
+                a = np.ascontiguousarray(arr, np.float32)
+                f.write(struct.pack("<Q", a.size) + a.tobytes())
+            tape_file = f.name
+        try:
+            run = subprocess.run([tape_bin, tape_file, str(args.service), str(lanes), str(subs), str(prec)],
+                                 capture_output=True, text=True, timeout=900)
+        finally:
+            os.unlink(tape_file)
+        if run.returncode != 0:
+            raise SystemExit(f"wc_tape failed ({run.returncode}): {run.stderr[-2000:]}")
+        sv = json.loads(run.stdout.strip().splitlines()[-1])
+        dt = sv["ms_per_wave"] * args.service / 1e3
         out["service"] = {"waves": args.service, "lanes": lanes, "submit_threads": subs,
-                          "ms_per_wave": round(dt / args.service * 1e3, 2),
+                          "ms_per_wave": round(sv["ms_per_wave"], 2),
                           "node_iters_per_s": round(args.service * node_iters / dt, 1),
                           "solves_per_s": round(args.service * len(jobs) / dt, 1),
-                          "prepare_ms_once": round(prep_ms, 1),
-                          "bytes_ms_per_wave": round(dt_raw / args.service * 1e3, 2),
-                          "device_waves": round(launched[by_prep] / 2, 1),
-                          "bytes_device_waves": round(launched[by_bytes] / 2, 1),
+                          "prepare_ms_once": sv["prepare_ms_once"],
+                          "bytes_ms_per_wave": round(sv["bytes_ms_per_wave"], 2),
+                          "device_waves": sv["device_waves"],
+                          "bytes_device_waves": sv["bytes_device_waves"],
+                          "driver": "wc_tape (csrc/wave_tape.cpp), a native caller of the C ABI, in a child process",
                           "note": "end to end through the C ABI: jobs prepared once (parse, validate, cost) and "
-                                  "submitted per wave, results waited on; lanes pack over one shared host thread pool, "
-                                  "pinned transfers, lanes overlap on their own streams; the service forms its own "
-                                  "device waves (one cost class each, at most 256 jobs and 48k network rows, an "
-                                  "800 us fill window from the oldest job: device_waves per WAVES). bytes_ms_per_wave: WCJ8 bytes per submission "
-                                  "(parsed and validated every time). After full-size warm-up waves of both kinds, "
-                                  "the two kinds are timed alternately, twice each (the means)"}
-        log(f"[bench] service: {dt / args.service * 1e3:.1f} ms per wave end to end with prepared jobs, "
-            f"{dt_raw / args.service * 1e3:.1f} ms with bytes per submission "
-            f"({launched[by_prep] / 2:.1f} and {launched[by_bytes] / 2:.1f} device waves per {args.service})")
+                                  "submitted per wave from several threads, every result waited on and read; lanes "
+                                  "pack over one shared host thread pool, pinned transfers, lanes overlap on their "
+                                  "own streams; the service forms its own device waves (one cost class each, at "
+                                  "most 256 jobs and 48k network rows, an 800 us fill window from the oldest job: "
+                                  "device_waves per WAVES). bytes_ms_per_wave: WCJ8 bytes per submission (parsed and "
+                                  "validated every time). After full-size warm-up waves of both kinds, the two kinds "
+                                  "are timed alternately, twice each (the means)"}
+        log(f"[bench] service: {sv['ms_per_wave']:.1f} ms per wave end to end with prepared jobs, "
+            f"{sv['bytes_ms_per_wave']:.1f} ms with bytes per submission "
+            f"({sv['device_waves']:.1f} and {sv['bytes_device_waves']:.1f} device waves per {args.service}; native driver)")
 
     if not args.no_cpu:
         import oracle as O

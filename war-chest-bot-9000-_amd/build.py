@@ -59,8 +59,16 @@ def build(verbose=False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, OUT)
+    # the throughput tape: a native caller of the C ABI (no HIP code of its own)
+    tape = os.path.join(HERE, "wc_tape")
+    cmd = [hipcc(), "-x", "c++", *COMMON, os.path.join(SRC, "wave_tape.cpp"), "-o", tape + ".tmp", "-L" + HERE,
+           "-lwcwave", "-Wl,-rpath,$ORIGIN", "-lpthread"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"tape build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tape + ".tmp", tape)
     if verbose:
-        print(f"built {OUT}")
+        print(f"built {OUT} and {tape}")
     return OUT
 
 
