@@ -268,3 +268,21 @@ def test_value_net_plan_rejects_null_output():
     assert ww.lib().wc_value_net_plan(None, 4, 64, 256, None, 4, ww.C.byref(n)) == -1  # WC_ERR_INVALID
     assert n.value == 0
     assert ww.lib().wc_value_net_plan(None, 4, 64, 256, None, 0, None) == -1  # WC_ERR_INVALID
+
+
+def test_tape_refuses_bad_arguments_and_files(tmp_path):
+    """wc_tape (the service's throughput tape) is built beside the library; it
+    refuses a wrong argument count or zero waves (status 2) and a truncated
+    tape file (status 1, naming the file) before it touches a device."""
+    import struct
+    import subprocess
+
+    tape = os.path.join(ROOT, "war-chest-bot-9000-_amd", "wc_tape")
+    assert os.path.exists(tape), "build first: python __graft_entry__.py"
+    assert subprocess.run([tape], capture_output=True).returncode == 2
+    bad = tmp_path / "bad.tape"
+    bad.write_bytes(b"WCTP" + struct.pack("<I", 3) + struct.pack("<Q", 10) + b"short")
+    r = subprocess.run([tape, str(bad), "0", "1", "1", "1"], capture_output=True, text=True)
+    assert r.returncode == 2
+    r = subprocess.run([tape, str(bad), "1", "1", "1", "1"], capture_output=True, text=True)
+    assert r.returncode == 1 and "malformed tape file" in r.stderr
