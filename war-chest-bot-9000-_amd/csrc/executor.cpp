@@ -791,11 +791,23 @@ void Executor::top_back(const WaveHost& w, int p, int mode, float da, float db, 
 }
 
 // Top regions' reach, one depth per launch, top-down; p < 0: both players.
-void Executor::top_reach(const WaveHost& w, int p, float* reach, const float* strat) {
+// With reach2 (p >= 0), each launch also takes both players' rows of that
+// depth under strat2 into reach2 (an independent reach computation).
+void Executor::top_reach(const WaveHost& w, int p, float* reach, const float* strat, float* reach2,
+                         const float* strat2) {
     for (uint32_t l = 1; l < w.top_levels; l++) {
-        uint32_t b0 = w.top_reach_lvl[0][l], n0 = p == 1 ? 0 : w.top_reach_lvl[0][l + 1] - b0;
-        uint32_t b1 = w.top_reach_lvl[1][l], n1 = p == 0 ? 0 : w.top_reach_lvl[1][l + 1] - b1;
-        launch_reach_rows(dev_, top_reach_dev_[0] + b0, n0, top_reach_dev_[1] + b1, n1, reach, strat, stream_);
+        ReachSet set[3];
+        int k = 0;
+        for (int q = 0; q < 2; q++) {
+            const uint32_t b = w.top_reach_lvl[q][l], n = w.top_reach_lvl[q][l + 1] - b;
+            if (p < 0 || p == q) set[k++] = ReachSet{top_reach_dev_[q] + b, n, reach, strat};
+        }
+        if (reach2 && p >= 0)
+            for (int q = 0; q < 2; q++) {
+                const uint32_t b = w.top_reach_lvl[q][l], n = w.top_reach_lvl[q][l + 1] - b;
+                set[k++] = ReachSet{top_reach_dev_[q] + b, n, reach2, strat2};
+            }
+        launch_reach_rows(dev_, set[0], set[1], set[2], stream_);
     }
 }
 
@@ -876,6 +888,7 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
     };
     init_state(w);
     mark(C_OTHER);
+    int carry_pending = -1;  // a snapshot whose carries the next iteration's reach launches compute
     if (m.iters == 0) launch_normalize(d, 0, 0, s);
     for (uint32_t t = 0; t < m.iters; t++) {
         const int p = (int)(t & 1);
@@ -888,9 +901,16 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
         launch_sweep(d, 0, nsub, head_out_, bank.ns.heads, p, MODE_REGRET, da, db, m.cfr.predict, s);
         mark(C_BACK);
         top_back(w, p, MODE_REGRET, da, db, m.cfr.predict);
-        top_reach(w, p, d.reach, d.cur);
+        // A snapshot's carried beliefs (both players' reach under the average
+        // strategy, then the gather) ride in this iteration's reach launches:
+        // the average strategy does not change before the next snapshot,
+        // which is normalised after them.
+        float* snap_reach = carry_pending >= 0 ? d.snap_reach : nullptr;
+        top_reach(w, p, d.reach, d.cur, snap_reach, d.snap);
         mark(C_TOP);
-        launch_reach(d, 0, nsub, d.reach, d.cur, p, s);
+        launch_reach(d, 0, nsub, d.reach, d.cur, p, s, snap_reach, d.snap);
+        if (carry_pending >= 0) launch_gather_carry(d, d.snap_reach, carry_pending, s);
+        carry_pending = -1;
         mark(C_REACH);
         launch_pool(d, p, precision_, Xq_[0], Xq_[1], s, p, ds);  // with p's average accumulation
         mark(C_LEAF);
@@ -901,8 +921,12 @@ void Executor::run_schedule(const WaveHost& w, const NetBank& bank, ScheduleTime
             launch_normalize(d, 1, done >= 2 ? 1 : 0, s);
             if (m.snapshots && si + 1 < m.snap_iters.size()) {
                 launch_seed_reach(d, d.snap_reach, w.reach_len, -1, s);
-                reach_both(w, d.snap_reach, d.snap);
-                launch_gather_carry(d, d.snap_reach, (int)si, s);
+                if (done < m.iters) {
+                    carry_pending = (int)si;  // in the next iteration's reach launches
+                } else {
+                    reach_both(w, d.snap_reach, d.snap);
+                    launch_gather_carry(d, d.snap_reach, (int)si, s);
+                }
             }
             mark(C_OTHER);
         }

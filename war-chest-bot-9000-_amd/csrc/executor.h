@@ -175,7 +175,8 @@ class Executor {
     void init_state(const WaveHost& w);
     void reach_both(const WaveHost& w, float* reach, const float* strat);
     void top_back(const WaveHost& w, int p, int mode, float da, float db, float pr);
-    void top_reach(const WaveHost& w, int p, float* reach, const float* strat);
+    void top_reach(const WaveHost& w, int p, float* reach, const float* strat, float* reach2 = nullptr,
+                   const float* strat2 = nullptr);
     void leaf_net(const NetBank& bank, int q);
     const NetBank* bank_of(uint64_t version, std::string* err) const;
     // The schedule captured into one HIP graph (kernels only: the schedule

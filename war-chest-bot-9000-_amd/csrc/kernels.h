@@ -74,12 +74,22 @@ void launch_init_strategy(const WaveDev& w, hipStream_t s);
 // (root_index < 0) or its carried root `root_index`.
 void launch_seed_reach(const WaveDev& w, float* reach, size_t reach_len, int root_index, hipStream_t s);
 // Top-down reach of subtree units [unit0, unit0 + n) under `strat`, for one
-// player or both (player < 0).
+// player or both (player < 0). With reach2 (player >= 0), the same launch also
+// computes both players' reach under strat2 into reach2: a second, independent
+// reach computation over the same units (a snapshot's, under the average
+// strategy).
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
-                  hipStream_t s);
-// Top-region reach at one depth (rows of player 0 and of player 1).
-void launch_reach_rows(const WaveDev& w, const ReachRec* r0, uint32_t n0, const ReachRec* r1, uint32_t n1,
-                       float* reach, const float* strat, hipStream_t s);
+                  hipStream_t s, float* reach2 = nullptr, const float* strat2 = nullptr);
+// One set of top-region reach rows of one depth: their records, the reach they
+// write and the strategy they read.
+struct ReachSet {
+    const ReachRec* rows = nullptr;
+    uint32_t n = 0;
+    float* reach = nullptr;
+    const float* strat = nullptr;
+};
+// Top-region reach at one depth: up to three independent row sets in one launch.
+void launch_reach_rows(const WaveDev& w, const ReachSet& a, const ReachSet& b, const ReachSet& c, hipStream_t s);
 void launch_seed_sum(const WaveDev& w, hipStream_t s);
 // Leaf reach masses and pooled beliefs of one player (-1 = both), written into
 // the query inputs x0 (traverser 0) and x1 (traverser 1) in the operand precision.

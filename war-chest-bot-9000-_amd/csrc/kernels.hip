@@ -238,11 +238,23 @@ __device__ __forceinline__ void reach_unit_one(const WaveDev& w, const UnitDev& 
 
 // Subtree units' reach: one player's, one unit per workgroup with its reach
 // window in LDS when LDSR; both players' (player < 0) either as one
-// workgroup per (unit, player), windows in LDS, or one per unit from L2.
+// workgroup per (unit, player), windows in LDS, or one per unit from L2. With
+// reach2 (player >= 0), workgroup 3 u + k takes unit u's rows of player
+// `player` under strat into reach (k = 0) or of player k - 1 under strat2
+// into reach2: independent computations, one launch.
 template <bool LDSR>
 __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, float* reach, const float* strat,
-                                               int player) {
+                                               int player, float* reach2, const float* strat2) {
     extern __shared__ float lds_reach[];  // the unit's reach window of the player (when LDSR)
+    if (player >= 0 && reach2) {
+        const uint32_t k = blockIdx.x % 3;
+        const UnitDev u = w.units[unit0 + blockIdx.x / 3];
+        if (k == 0)
+            reach_unit_one<LDSR>(w, u, reach, strat, player, lds_reach);
+        else
+            reach_unit_one<LDSR>(w, u, reach2, strat2, (int)k - 1, lds_reach);
+        return;
+    }
     if (LDSR && player < 0) {  // the players' rows are independent: workgroup 2 u + p
         const UnitDev u = w.units[unit0 + blockIdx.x / 2];
         reach_unit_one<true>(w, u, reach, strat, (int)(blockIdx.x & 1), lds_reach);
@@ -256,14 +268,18 @@ __global__ __launch_bounds__(BLOCK) void k_reach(WaveDev w, uint32_t unit0, floa
 }
 
 void launch_reach(const WaveDev& w, uint32_t unit0, uint32_t n, float* reach, const float* strat, int player,
-                  hipStream_t s) {
+                  hipStream_t s, float* reach2, const float* strat2) {
     if (!n) return;
+    if (player < 0) reach2 = nullptr;  // both players already
     const size_t lds = (size_t)w.max_rwin * sizeof(float);
-    if (w.unit_lds && lds <= REACH_LDS_MAX)
-        hipLaunchKernelGGL(k_reach<true>, dim3(player < 0 ? 2 * n : n), dim3(BLOCK), lds, s, w, unit0, reach, strat,
-                           player);
+    const bool in_lds = w.unit_lds && lds <= REACH_LDS_MAX;
+    const uint32_t grid = reach2 ? 3 * n : player < 0 && in_lds ? 2 * n : n;
+    if (in_lds)
+        hipLaunchKernelGGL(k_reach<true>, dim3(grid), dim3(BLOCK), lds, s, w, unit0, reach, strat, player, reach2,
+                           strat2);
     else
-        hipLaunchKernelGGL(k_reach<false>, dim3(n), dim3(BLOCK), 0, s, w, unit0, reach, strat, player);
+        hipLaunchKernelGGL(k_reach<false>, dim3(grid), dim3(BLOCK), 0, s, w, unit0, reach, strat, player, reach2,
+                           strat2);
 }
 
 // The average-strategy accumulation of player `acc` over all its decision rows
@@ -287,15 +303,21 @@ __device__ __forceinline__ bool accumulate_blocks(const WaveDev& w, int acc, flo
     return false;
 }
 
-// Top-region reach at one depth, all trees together: one row per thread.
-__global__ __launch_bounds__(BLOCK) void k_reach_rows(WaveDev w, const ReachRec* r0, uint32_t n0,
-                                                    const ReachRec* r1, uint32_t n1, float* reach,
-                                                    const float* strat) {
+// Top-region reach at one depth, all trees together: one row per thread, the
+// rows of up to three independent sets (players, reach computations).
+__global__ __launch_bounds__(BLOCK) void k_reach_rows(WaveDev w, ReachSet a, ReachSet b, ReachSet c) {
     uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-    if (k < n0)
-        reach_row(w, reach, strat, r0[k]);
-    else if (k < n0 + n1)
-        reach_row(w, reach, strat, r1[k - n0]);
+    if (k < a.n) {
+        reach_row(w, a.reach, a.strat, a.rows[k]);
+        return;
+    }
+    k -= a.n;
+    if (k < b.n) {
+        reach_row(w, b.reach, b.strat, b.rows[k]);
+        return;
+    }
+    k -= b.n;
+    if (k < c.n) reach_row(w, c.reach, c.strat, c.rows[k]);
 }
 
 // A top depth holds 10k-50k rows, one per thread: one-wavefront workgroups
@@ -304,11 +326,9 @@ __global__ __launch_bounds__(BLOCK) void k_reach_rows(WaveDev w, const ReachRec*
 // of 256 subgames over 1,120 launches).
 constexpr int TOP_BLOCK = 64;
 
-void launch_reach_rows(const WaveDev& w, const ReachRec* r0, uint32_t n0, const ReachRec* r1, uint32_t n1,
-                       float* reach, const float* strat, hipStream_t s) {
-    if (n0 + n1)
-        hipLaunchKernelGGL(k_reach_rows, dim3(grid_for(n0 + n1, TOP_BLOCK)), dim3(TOP_BLOCK), 0, s, w, r0, n0, r1, n1,
-                           reach, strat);
+void launch_reach_rows(const WaveDev& w, const ReachSet& a, const ReachSet& b, const ReachSet& c, hipStream_t s) {
+    const size_t n = (size_t)a.n + b.n + c.n;
+    if (n) hipLaunchKernelGGL(k_reach_rows, dim3(grid_for(n, TOP_BLOCK)), dim3(TOP_BLOCK), 0, s, w, a, b, c);
 }
 
 // sum = reach * cur: one reach-weighted uniform strategy (engine/src/search.rs:854-870).
