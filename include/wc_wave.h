@@ -200,12 +200,33 @@ typedef struct wc_wave_stats {
 } wc_wave_stats;
 int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* out);
 
-/* Read-only view of one packed uint32 index array of a wave, by name, for tests
- * and tooling: "row_node", "reach_base", "vals_base", "exit_node", "exit_coff",
- * "legal_value", "child_start", "child", "legal_off". Returns NULL (and sets
- * wc_last_error) for an unknown name; *n receives the element count. The view
- * lives as long as the wave. */
+/* Read-only view of one packed table of a wave as uint32 words, by name, for
+ * tests and tooling: the index lists "row_node", "reach_base", "vals_base",
+ * "exit_node", "exit_coff", "legal_value", "child_start", "child",
+ * "legal_off", "node_meta", "node_nc", "row_cfg", "row_cfg_off", "draw_to",
+ * "rev_src", "rvd_src", "term_node", "unit_term"; the unit records "units"
+ * (24 words each); and per player p (0 or 1) "back_rec<p>", "top_back_rec<p>",
+ * "reach_rec<p>", "top_reach_rec<p>", "acc_rec<p>", "leaf_rec<p>" (4 words per
+ * record), "pool_grp<p>" (36 words per group), "child_vb<p>", "back_lvl<p>",
+ * "reach_lvl<p>". Returns NULL (and sets wc_last_error) for an unknown name;
+ * *n receives the word count. The view lives as long as the wave. */
 const uint32_t* wc_wave_array(const wc_wave* w, const char* name, size_t* n);
+
+/* Test support (no counterpart in the reference): overwrite word `index` of
+ * the packed table `name` (the names of wc_wave_array), for tests of the
+ * bounds checks against a wave the packer did not make. The wave then counts
+ * as unchecked: every later upload of it checks it on the device first. */
+int wc_wave_poke(wc_wave* w, const char* name, size_t index, uint32_t value);
+
+/* Checks every index of a packed wave that the device kernels follow (no
+ * counterpart in the reference, whose kernels bound-check as they go). With ex
+ * NULL, on the host: the check wc_wave_pack runs. With an executor, the check
+ * an upload runs for a wave packed without it (a service wave of jobs
+ * validated at submit): the structural checks on the host, then the element
+ * tables uploaded to ex's device and checked there, nothing else launched;
+ * `version` is a weight bank published on ex. WC_OK, or WC_ERR_INVALID with
+ * "wave bounds: <the first failing condition>" in wc_last_error. */
+int wc_wave_check(const wc_wave* w, wc_executor* ex, uint64_t version);
 
 /* The fused value net's pass plan, for tests and tooling (no counterpart in
  * the reference, whose head GEMMs take fixed tiles: device.rs:1218-1305): for

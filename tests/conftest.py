@@ -10,10 +10,9 @@ for p in (PKG, ORACLE, os.path.join(ROOT, "tests")):
     if p not in sys.path:
         sys.path.insert(0, p)
 
-# Waves the service packs from jobs validated at submit skip the packed wave's
-# deep bounds check unless WC_DEEP_CHECK=1; the tests keep it on, so every
-# service-formed wave they run has passed it.
-os.environ.setdefault("WC_DEEP_CHECK", "1")
+# Waves the service packs from jobs validated at submit are not checked on the
+# host (unless WC_DEEP_CHECK=1): their uploads check them on the device, which
+# is what the service tests run.
 
 
 def pytest_configure(config):

@@ -173,6 +173,32 @@ def test_service_style_mixed_waves_pass_the_deep_check():
         wave.close()
 
 
+def test_host_check_names_the_first_failing_condition(monkeypatch):
+    """wc_wave_check on the host (the check wc_wave_pack runs) against single-
+    fault edits of a packed wave (wc_wave_poke): each edit is refused with the
+    condition it breaks, and the wave passes again once the word is restored.
+    The device check (GPU tests) must name the same conditions."""
+    import bounds_cases as B
+
+    monkeypatch.setenv("WC_UNIT_SLOTS", B.UNIT_SLOTS)
+    wave = ww.Wave(B.jobs())
+    assert wave.stats()["top_levels"] > 0
+    wave.check()
+    cases = B.cases(wave)
+    assert len(cases) == 18
+    for name, index, value, msg in cases:
+        old = int(wave.array(name)[index])
+        wave.poke(name, index, value)
+        with pytest.raises(ww.WaveError, match="^wave bounds: " + re.escape(msg) + "$"):
+            wave.check()
+        wave.poke(name, index, old)
+        wave.check()
+    with pytest.raises(ww.WaveError, match="index beyond"):
+        wave.poke("row_node", wave.stats()["rows"], 0)
+    with pytest.raises(ww.WaveError, match="unknown array"):
+        wave.poke("no_such_table", 0, 0)
+
+
 def test_repacking_a_wave_equals_packing_it_fresh():
     """A reused wave (wc_wave_repack, the service lanes' path) keeps the
     lengths and old contents of the lists the packer overwrites whole, so a

@@ -19,7 +19,7 @@ BUILD = os.path.join(HERE, "_build")
 ARCH = os.environ.get("WC_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["job.cpp", "synth.cpp", "wave.cpp", "capi_host.cpp", "executor.cpp", "service.cpp", "capi_gpu.cpp",
-           "kernels.hip", "noalloc.hip", "v5.hip", "probe.hip"]
+           "kernels.hip", "noalloc.hip", "v5.hip", "probe.hip", "check.hip"]
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result", "-ffp-contract=off"]
 DEVICE = [f"--offload-arch={ARCH}", "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-gpu-flush-denormals-to-zero",

@@ -5,6 +5,7 @@
 #include <exception>
 #include <memory>
 #include <string>
+#include <type_traits>
 
 #include "../../include/wc_wave.h"
 #include "common.h"
@@ -297,6 +298,59 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* s) {
     return WC_OK;
 }
 
+extern "C++" {
+namespace {
+
+// One packed table of a wave as uint32 words, by name: index lists, and the
+// record and unit lists (structs of uint32 fields, field-major within each
+// entry). Null for an unknown name.
+template <class W>
+auto u32_table(W& h, const std::string& k, size_t* n) -> decltype(h.row_node.data()) {
+    using P = decltype(h.row_node.data());
+    auto list = [&](auto& v) -> P {
+        using E = typename std::remove_reference_t<decltype(v)>::value_type;
+        static_assert(sizeof(E) % 4 == 0, "a table of uint32 words");
+        *n = v.size() * (sizeof(E) / 4);
+        return (P)(void*)v.data();
+    };
+    if (k == "row_node") return list(h.row_node);
+    if (k == "reach_base") return list(h.reach_base);
+    if (k == "vals_base") return list(h.vals_base);
+    if (k == "exit_node") return list(h.exit_node);
+    if (k == "exit_coff") return list(h.exit_coff);
+    if (k == "legal_value") return list(h.legal_value);
+    if (k == "child_start") return list(h.child_start);
+    if (k == "child") return list(h.child);
+    if (k == "legal_off") return list(h.legal_off);
+    if (k == "node_meta") return list(h.node_meta);
+    if (k == "node_nc") return list(h.node_nc);
+    if (k == "row_cfg") return list(h.row_cfg);
+    if (k == "row_cfg_off") return list(h.row_cfg_off);
+    if (k == "draw_to") return list(h.draw_to);
+    if (k == "rev_src") return list(h.rev_src);
+    if (k == "rvd_src") return list(h.rvd_src);
+    if (k == "term_node") return list(h.term_node);
+    if (k == "unit_term") return list(h.unit_term);
+    if (k == "units") return list(h.units);
+    for (int p = 0; p < 2; p++) {
+        const std::string s = std::to_string(p);
+        if (k == "back_rec" + s) return list(h.back_rec[p]);
+        if (k == "top_back_rec" + s) return list(h.top_back_rec[p]);
+        if (k == "reach_rec" + s) return list(h.reach_rec[p]);
+        if (k == "top_reach_rec" + s) return list(h.top_reach_rec[p]);
+        if (k == "acc_rec" + s) return list(h.acc_rec[p]);
+        if (k == "leaf_rec" + s) return list(h.leaf_rec[p]);
+        if (k == "pool_grp" + s) return list(h.pool_grp[p]);
+        if (k == "child_vb" + s) return list(h.child_vb[p]);
+        if (k == "back_lvl" + s) return list(h.back_lvl[p]);
+        if (k == "reach_lvl" + s) return list(h.reach_lvl[p]);
+    }
+    return nullptr;
+}
+
+}  // namespace
+}  // extern "C++"
+
 const uint32_t* wc_wave_array(const wc_wave* w, const char* name, size_t* n) {
     if (n) *n = 0;
     if (!w || !name) {
@@ -304,24 +358,37 @@ const uint32_t* wc_wave_array(const wc_wave* w, const char* name, size_t* n) {
         return nullptr;
     }
     if (unpacked(w, "wc_wave_array")) return nullptr;
-    const WaveHost& h = w->host;
-    const std::vector<uint32_t>* v = nullptr;
-    const std::string k = name;
-    if (k == "row_node") v = &h.row_node;
-    else if (k == "reach_base") v = &h.reach_base;
-    else if (k == "vals_base") v = &h.vals_base;
-    else if (k == "exit_node") v = &h.exit_node;
-    else if (k == "exit_coff") v = &h.exit_coff;
-    else if (k == "legal_value") v = &h.legal_value;
-    else if (k == "child_start") v = &h.child_start;
-    else if (k == "child") v = &h.child;
-    else if (k == "legal_off") v = &h.legal_off;
+    size_t len = 0;
+    const uint32_t* v = u32_table(w->host, name, &len);
     if (!v) {
-        fail(WC_ERR_INVALID, "wc_wave_array: unknown array " + k);
+        fail(WC_ERR_INVALID, std::string("wc_wave_array: unknown array ") + name);
         return nullptr;
     }
-    if (n) *n = v->size();
-    return v->data();
+    if (n) *n = len;
+    return v;
+}
+
+int wc_wave_poke(wc_wave* w, const char* name, size_t index, uint32_t value) {
+    if (!w || !name) return fail(WC_ERR_INVALID, "wc_wave_poke: null argument");
+    if (unpacked(w, "wc_wave_poke")) return WC_ERR_INVALID;
+    size_t len = 0;
+    uint32_t* v = u32_table(w->host, name, &len);
+    if (!v) return fail(WC_ERR_INVALID, std::string("wc_wave_poke: unknown array ") + name);
+    if (index >= len) return fail(WC_ERR_INVALID, std::string("wc_wave_poke: index beyond ") + name);
+    v[index] = value;
+    w->host.checked = false;  // what the packer checked is no longer what the wave holds
+    return WC_OK;
+}
+
+int wc_wave_check(const wc_wave* w, wc_executor* ex, uint64_t version) {
+    if (!w) return fail(WC_ERR_INVALID, "wc_wave_check: null argument");
+    if (unpacked(w, "wc_wave_check")) return WC_ERR_INVALID;
+    return shielded("wc_wave_check", [&] {
+        std::string err;
+        if (!ex) return validate_deep(w->host, &err) ? WC_OK : fail(WC_ERR_INVALID, err);
+        if (ex->ex->check(w->host, version, &err)) return WC_OK;
+        return fail(err.rfind("wave bounds: ", 0) == 0 ? WC_ERR_INVALID : WC_ERR_DEVICE, err);
+    });
 }
 
 static_assert(CHAIN_PASS_BLOCKS == 8, "wc_value_net_plan rows are 2 + 8 words");

@@ -12,6 +12,7 @@
 #include <unordered_map>
 
 #include "../../include/wc_wave.h"
+#include "check.h"
 #include "par.h"
 
 namespace wc {
@@ -80,16 +81,24 @@ Executor::Executor(int device, int precision) : device_(device), precision_(prec
         err_ = "unknown precision";
         return;
     }
-    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking) != hipSuccess) {
-        err_ = "cannot create the executor stream";
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&copy_, hipStreamNonBlocking) != hipSuccess) {
+        err_ = "cannot create the executor streams";
         return;
     }
+    void* flag = nullptr;
+    if (hipHostMalloc(&flag, 256, hipHostMallocDefault) != hipSuccess) {
+        err_ = "cannot allocate the executor's pinned flag";
+        return;
+    }
+    check_host_ = (uint32_t*)flag;
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
         cus_ = (uint32_t)cus;
     for (Slot& sl : slots_)
         if (hipEventCreateWithFlags(&sl.uploaded, hipEventDisableTiming) != hipSuccess ||
-            hipEventCreateWithFlags(&sl.done, hipEventDisableTiming) != hipSuccess) {
+            hipEventCreateWithFlags(&sl.done, hipEventDisableTiming) != hipSuccess ||
+            hipEventRecord(sl.done, stream_) != hipSuccess) {  // (an upload waits on it: complete at once)
             err_ = "cannot create the executor's events";
             return;
         }
@@ -105,8 +114,9 @@ Executor::~Executor() {
     if (!stream_) return;
     hipSetDevice(device_);
     hipStreamSynchronize(stream_);
+    if (copy_) hipStreamSynchronize(copy_);
     for (auto& kv : banks_) hipFree(kv.second.mem);
-    hipFree(table_);
+    for (void* t : table_) hipFree(t);
     hipFree(arena_);
     hipFree(mlp_);
     for (Slot& sl : slots_) {
@@ -116,6 +126,8 @@ Executor::~Executor() {
         if (sl.done) hipEventDestroy(sl.done);
         if (sl.exec) hipGraphExecDestroy(sl.exec);
     }
+    if (check_host_) hipHostFree(check_host_);
+    if (copy_) hipStreamDestroy(copy_);
     hipStreamDestroy(stream_);
 }
 
@@ -123,6 +135,7 @@ bool Executor::ensure(void** p, size_t* cap, size_t need, std::string* err) {
     if (need <= *cap && *p) return true;
     if (*p) {
         HIP_TRY(hipStreamSynchronize(stream_));
+        HIP_TRY(hipStreamSynchronize(copy_));
         HIP_TRY(hipFree(*p));
         *p = nullptr;
     }
@@ -139,6 +152,7 @@ bool Executor::ensure_pinned(uint8_t** p, size_t* cap, size_t need, std::string*
     if (need <= *cap && *p) return true;
     if (*p) {
         HIP_TRY(hipStreamSynchronize(stream_));
+        HIP_TRY(hipStreamSynchronize(copy_));
         HIP_TRY(hipHostFree(*p));
         *p = nullptr;
         *cap = 0;
@@ -392,8 +406,11 @@ void Executor::retain_from(uint64_t oldest) {
     }
 }
 
-bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std::string* err) {
+bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std::string* err, bool device_check,
+                      std::function<void()>* meanwhile) {
     const NetShape& ns = bank.ns;
+    device_check = device_check || !w.checked;
+    if (device_check && !validate_shape(w, err)) return false;  // before the sizes below are trusted
     if (w.net.kind != ns.kind || w.net.in != ns.in || w.net.hidden != ns.hidden || w.net.pool != ns.pool ||
         w.net.heads != ns.heads || w.net.layers != ns.layers || w.net.priv_in != ns.priv_in ||
         w.net.priv_layers != ns.priv_layers) {
@@ -464,13 +481,17 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
         o.tb[p] = blob.put(w.top_back_rec[p]);
         o.tr[p] = blob.put(w.top_reach_rec[p]);
     }
-    if (!ensure(&table_, &table_cap_, blob.size, err)) return false;
+    // The device check's words follow the tables: it runs beside the wave
+    // before, which holds the solve state.
+    const size_t check_at = align256(blob.size), check_words = 1 + 2 * size_t(w.rows());
+    if (!ensure(&table_[slot], &table_cap_[slot], check_at + check_words * 4, err)) return false;
     Slot& sl = slots_[slot];
     if (sl.recorded) HIP_TRY(hipEventSynchronize(sl.uploaded));  // the slot's last upload has left its staging
     if (!ensure_pinned(&sl.pin, &sl.pin_cap, blob.size, err)) return false;
     blob.copy_to(sl.pin);
-    HIP_TRY(hipMemcpyAsync(table_, sl.pin, blob.size, hipMemcpyHostToDevice, stream_));
-    HIP_TRY(hipEventRecord(sl.uploaded, stream_));
+    HIP_TRY(hipStreamWaitEvent(copy_, sl.done, 0));  // the slot's last wave no longer reads its tables
+    HIP_TRY(hipMemcpyAsync(table_[slot], sl.pin, blob.size, hipMemcpyHostToDevice, copy_));
+    HIP_TRY(hipEventRecord(sl.uploaded, copy_));  // (recorded again below, after the check)
     sl.recorded = true;
 
     // Mutable arena.
@@ -531,7 +552,8 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
     }
     if (!ensure(&mlp_, &mlp_cap_, mt, err)) return false;
 
-    char* T = (char*)table_;
+    char* T = (char*)table_[slot];
+    check_ = (uint32_t*)(T + check_at);
     char* A = (char*)arena_;
     char* M = (char*)mlp_;
     WaveDev& d = dev_;
@@ -646,8 +668,48 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
         v5_xf_ = precision_ == WC_PRECISE ? nullptr : (float*)(M + m_xf);
         d.cfg_emb = v5_out_.G;  // the pooled beliefs pool g(c) (search.rs:1525-1545)
     }
+    if (device_check && !check_on_device(w, err, meanwhile)) return false;
+    HIP_TRY(hipEventRecord(sl.uploaded, copy_));
+    HIP_TRY(hipStreamWaitEvent(stream_, sl.uploaded, 0));  // the schedule reads the tables once they are in
     launch_query_static(d, precision_, Xq_[0], Xq_[1], stream_);
     HIP_TRY(hipGetLastError());
+    return true;
+}
+
+bool Executor::check_on_device(const WaveHost& w, std::string* err, std::function<void()>* meanwhile) {
+    if (w.max_rwin > CHECK_RWIN_MAX) return validate_deep(w, err);  // wider than the unit check's bitmap
+    // On the upload's stream, behind the tables' copy and beside the wave
+    // before; the host waits only for the copy and the check.
+    launch_zero((float*)check_, 1 + 2 * size_t(w.rows()), copy_);
+    launch_check(check_args(w, dev_, top_back_dev_, top_reach_dev_, check_, check_ + 1), copy_);
+    HIP_TRY(hipGetLastError());
+    *check_host_ = 0;
+    HIP_TRY(hipMemcpyAsync(check_host_, check_, sizeof(uint32_t), hipMemcpyDeviceToHost, copy_));
+    if (meanwhile && *meanwhile) {
+        const std::function<void()> f = std::move(*meanwhile);
+        *meanwhile = nullptr;
+        f();
+    }
+    HIP_TRY(hipStreamSynchronize(copy_));
+    const uint32_t flag = *(volatile uint32_t*)check_host_;
+    if (flag) {
+        const char* m = check_message(CHECK_BASE - flag);
+        *err = std::string("wave bounds: ") + (m ? m : "unknown condition");
+        return false;
+    }
+    return true;
+}
+
+bool Executor::check(const WaveHost& w, uint64_t version, std::string* err) {
+    const NetBank* bank = bank_of(version, err);
+    if (!bank) return false;
+    if (in_flight_) {
+        *err = "collect the launched waves before checking";
+        return false;
+    }
+    HIP_TRY(hipSetDevice(device_));
+    if (!upload(w, *bank, 0, err, true)) return false;
+    HIP_TRY(hipStreamSynchronize(stream_));
     return true;
 }
 
@@ -997,7 +1059,16 @@ bool Executor::capture(const WaveHost& w, const NetBank& bank, hipGraphExec_t* e
     return true;
 }
 
-bool Executor::launch(const WaveHost& w, uint64_t version, InFlight* f, std::string* err) {
+bool Executor::launch(const WaveHost& w, uint64_t version, InFlight* f, std::string* err,
+                      const std::function<void()>& meanwhile) {
+    std::function<void()> pending = meanwhile;  // called once: during the device check, else at the end
+    const bool ok = launch_wave(w, version, f, err, &pending);
+    if (pending) pending();
+    return ok;
+}
+
+bool Executor::launch_wave(const WaveHost& w, uint64_t version, InFlight* f, std::string* err,
+                           std::function<void()>* meanwhile) {
     const NetBank* bank = bank_of(version, err);
     if (!bank) return false;
     if (f->live) {
@@ -1017,7 +1088,17 @@ bool Executor::launch(const WaveHost& w, uint64_t version, InFlight* f, std::str
         return false;
     }
     Slot& sl = slots_[k];
-    if (!upload(w, *bank, k, err)) return false;
+    // Reserved from here (`meanwhile` may collect the other slot during the
+    // upload); released again on every failure below.
+    struct Reserve {
+        Slot& s;
+        bool keep = false;
+        ~Reserve() {
+            if (!keep) s.busy = false;
+        }
+    } reserve{sl};
+    sl.busy = true;
+    if (!upload(w, *bank, k, err, false, meanwhile)) return false;
     if (sl.exec) {
         HIP_TRY(hipGraphExecDestroy(sl.exec));
         sl.exec = nullptr;
@@ -1056,7 +1137,7 @@ bool Executor::launch(const WaveHost& w, uint64_t version, InFlight* f, std::str
         js.root_value0 = t.root_value0;
         js.snapshot_configs = w.jobs[j]->t.snapshot_configs();
     }
-    sl.busy = true;
+    reserve.keep = true;
     in_flight_++;
     f->live = true;
     return true;
@@ -1069,11 +1150,16 @@ bool Executor::trim(std::string* err) {
     }
     HIP_TRY(hipSetDevice(device_));
     HIP_TRY(hipStreamSynchronize(stream_));
-    HIP_TRY(hipFree(table_));
+    HIP_TRY(hipStreamSynchronize(copy_));
+    for (uint32_t k = 0; k < MAX_IN_FLIGHT; k++) {
+        HIP_TRY(hipFree(table_[k]));
+        table_[k] = nullptr;
+        table_cap_[k] = 0;
+    }
     HIP_TRY(hipFree(arena_));
     HIP_TRY(hipFree(mlp_));
-    table_ = arena_ = mlp_ = nullptr;
-    table_cap_ = arena_cap_ = mlp_cap_ = 0;
+    arena_ = mlp_ = nullptr;
+    arena_cap_ = mlp_cap_ = 0;
     for (Slot& sl : slots_) {
         if (sl.pin) HIP_TRY(hipHostFree(sl.pin));
         if (sl.res) HIP_TRY(hipHostFree(sl.res));

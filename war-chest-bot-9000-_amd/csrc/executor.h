@@ -113,12 +113,20 @@ class Executor {
 
     // Upload, run the whole schedule, collect one result per job.
     bool solve(const WaveHost& w, uint64_t version, std::vector<Result>* out, std::string* err);
+    // Upload the wave and check its indices on the device (what an upload
+    // runs for a wave that was not checked on the host), however it was packed.
+    bool check(const WaveHost& w, uint64_t version, std::string* err);
     // The same in two halves: launch queues the upload, the schedule and the
     // result copies and returns; collect waits and unpacks. At most
     // MAX_IN_FLIGHT waves may be launched and not yet collected; the packed
-    // wave may be reused as soon as launch returns.
+    // wave may be reused as soon as launch returns. A wave checked on the
+    // device makes launch wait for the check's result before it queues the
+    // schedule; `meanwhile` (optional) is called once, while that check runs
+    // (or once everything is queued), for a caller with other work such as
+    // collecting its previous wave (it may call collect on this executor).
     static constexpr uint32_t MAX_IN_FLIGHT = 2;
-    bool launch(const WaveHost& w, uint64_t version, InFlight* out, std::string* err);
+    bool launch(const WaveHost& w, uint64_t version, InFlight* out, std::string* err,
+                const std::function<void()>& meanwhile = {});
     bool collect(InFlight* f, std::vector<Result>* out, std::string* err);
     bool ready(const InFlight& f) const;
     uint32_t in_flight() const { return in_flight_; }
@@ -157,7 +165,16 @@ class Executor {
   private:
     // Copies the wave's tables into the pinned staging of `slot` and queues
     // their upload; sets up the device views of the wave.
-    bool upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std::string* err);
+    // A wave that did not pass validate_deep (`checked` false), or any wave
+    // with device_check, is checked before the schedule may read it:
+    // validate_shape on the host first, then the element tables on the device.
+    bool launch_wave(const WaveHost& w, uint64_t version, InFlight* out, std::string* err,
+                     std::function<void()>* meanwhile);
+    // `meanwhile` (if set) is called and cleared while a device check runs.
+    bool upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std::string* err, bool device_check = false,
+                std::function<void()>* meanwhile = nullptr);
+    // The device element checks of the uploaded wave; waits for their result.
+    bool check_on_device(const WaveHost& w, std::string* err, std::function<void()>* meanwhile);
     // hook (optional): called after every leaf-net evaluation with its
     // schedule point and traverser.
     using LeafHook = std::function<void(int32_t point, int p)>;
@@ -208,12 +225,15 @@ class Executor {
     bool ok_ = false;
     std::string err_;
     hipStream_t stream_ = nullptr;
+    hipStream_t copy_ = nullptr;  // table uploads and their device checks, beside the schedules
     std::map<uint64_t, NetBank> banks_;
     uint64_t next_version_ = 1;
 
-    // Device buffers of the current wave (grow-only).
-    void* table_ = nullptr;
-    size_t table_cap_ = 0;
+    // Device buffers (grow-only): the immutable tables of each launch slot (a
+    // wave's tables upload, and are checked, while the slot before it runs),
+    // then the solve state and the value net's buffers the waves use in turn.
+    void* table_[MAX_IN_FLIGHT] = {};
+    size_t table_cap_[MAX_IN_FLIGHT] = {};
     void* arena_ = nullptr;
     size_t arena_cap_ = 0;
     void* mlp_ = nullptr;  // query inputs, hidden activations, head outputs
@@ -236,6 +256,8 @@ class Executor {
     WaveDev dev_{};
     void* X_ = nullptr;
     void* Xq_[2] = {};  // the wave's query inputs, one per traverser
+    uint32_t* check_ = nullptr;       // the device check's flag word and pool-group row counters (after the tables)
+    uint32_t* check_host_ = nullptr;  // pinned landing of the flag word
     const BackRec* top_back_dev_[2] = {};    // top-region rows by depth (device copies)
     const ReachRec* top_reach_dev_[2] = {};
     const uint32_t* head_tile_n_ = nullptr;  // head width per 128-row tile (device copy)

@@ -562,7 +562,8 @@ void Service::lane_main(uint32_t lane) {
         }
         F.launched = std::chrono::steady_clock::now();
         F.pack_ms = std::chrono::duration<double, std::milli>(F.launched - t_pack).count();
-        if (ok) ok = ex->launch(wh, exv, &F.f, &err);
+        // the previous wave is answered while this one's upload is checked on the device
+        if (ok) ok = ex->launch(wh, exv, &F.f, &err, [&] { land(fl[k ^ 1]); });
         F.launch_ms =
             std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - F.launched).count();
         if (!ok) {
@@ -571,10 +572,7 @@ void Service::lane_main(uint32_t lane) {
         } else {
             waves_.fetch_add(1, std::memory_order_relaxed);
             last = k;
-            if (guarded)
-                land(F);  // the guarded wave runs alone
-            else
-                land(fl[k ^ 1]);  // answer the previous wave while this one runs
+            if (guarded) land(F);  // the guarded wave runs alone (no other flight is live)
         }
         if (guarded) {
             {

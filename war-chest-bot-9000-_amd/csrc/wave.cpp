@@ -503,6 +503,7 @@ void WaveHost::reset() {
     carry_slots = blank.carry_slots;
     max_vwin = blank.max_vwin;
     max_rwin = blank.max_rwin;
+    checked = blank.checked;
     tower_len = blank.tower_len;
 }
 
@@ -1094,10 +1095,13 @@ bool pack_wave(std::vector<std::shared_ptr<const Job>>&& jobs, WaveHost* out, st
         const char* e = std::getenv("WC_DEEP_CHECK");
         return e && *e && *e != '0';
     }();
+    w.checked = false;
     if ((!validated || force_deep) && !validate_deep(w, err)) return false;
+    w.checked = !validated || force_deep;
     return true;
 }
 
+// (`checked` records how the wave was checked, not what it holds: it stays out.)
 uint64_t digest(const WaveHost& w) {
     uint64_t h = 0xcbf29ce484222325ull;
     auto word = [&](uint64_t v) { h = (h ^ v) * 0x100000001b3ull; };
@@ -1163,7 +1167,127 @@ bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_
     return pack_wave(std::move(shared), out, err, unit_slots, validated);
 }
 
-bool validate_deep(const WaveHost& w, std::string* err) {
+bool validate_shape(const WaveHost& w, std::string* err) {
+    auto fail = [&](const char* m) {
+        *err = std::string("wave bounds: ") + m;
+        return false;
+    };
+    const uint64_t N = w.nodes();
+    if (w.node_nc.size() != 2 * N || w.child_start.size() != N + 1 || w.legal_row_of.size() != N ||
+        w.draw_off.size() != N || w.draw_row_off.size() != N || w.reach_base.size() != 2 * N ||
+        w.vals_base.size() != 2 * N || w.parent.size() != N || w.rev_row_of.size() != N || w.rvd_row_of.size() != N)
+        return fail("node arrays disagree");
+    if (w.legal_value.size() != w.ncells || w.legal_off.empty() || w.legal_off.back() != w.ncells)
+        return fail("cell arrays disagree");
+    const uint64_t rows = w.rows();
+    if (w.row_cfg_off.size() != 2 * rows + 1 || w.row_cfg_off.back() != w.row_cfg.size()) return fail("row_cfg_off");
+    const uint64_t ncfg = w.cfg_key.size();
+    if (w.cfg_emb.size() != (w.net.kind == MODEL_V5 ? 0 : ncfg * w.net.pool) ||
+        w.pub_raw.size() != rows * w.net.row_bytes)
+        return fail("row payload");
+    if (w.net.kind == MODEL_MLP)
+        for (uint32_t k : w.cfg_key)
+            if (k >= w.net.heads) return fail("cfg_key");
+    if (w.cfg_priv.size() != (w.net.kind == MODEL_TWO_TOWER ? ncfg * w.net.priv_in
+                              : w.net.kind == MODEL_V5      ? ncfg * w.net.cfeat
+                                                            : 0))
+        return fail("cfg_priv");
+    if (w.net.kind == MODEL_V5) {  // the v5 build's per-config and per-row job indices
+        const uint64_t njobs = w.trees.size();
+        if (w.cfg_job.size() != ncfg || w.cfg_owner.size() != ncfg || w.row_job.size() != rows ||
+            w.card_feat.size() != njobs * w.net.card_feat || w.pub_raw.size() != uint64_t(rows) * w.net.row_bytes)
+            return fail("v5 tables");
+        for (uint64_t c = 0; c < ncfg; c++)
+            if (w.cfg_job[c] >= njobs || w.cfg_owner[c] > 1) return fail("v5 config owner");
+        for (uint32_t r : w.row_job)
+            if (r >= njobs) return fail("v5 row job");
+    }
+    for (uint32_t t : w.term_node)
+        if (t >= N || (w.node_meta[t] & 3u) != 2) return fail("term_node");
+    const uint64_t nexit = w.exit_node.size();
+    if (w.exit_coff.size() != 2 * nexit + 1 || w.exit_coff.back() != w.snapshot_configs) return fail("exit_coff");
+    if (w.exit_reach.size() != 2 * nexit) return fail("exit_reach");
+    for (uint64_t e = 0; e < nexit; e++)
+        for (int p = 0; p < 2; p++)
+            if (w.exit_node[e] >= N || w.exit_coff[2 * e + p + 1] - w.exit_coff[2 * e + p] != w.nc(w.exit_node[e], p) ||
+                w.exit_reach[2 * e + p] != w.reach_base[2 * size_t(w.exit_node[e]) + p])
+                return fail("exit configs");
+    for (int p = 0; p < 2; p++) {
+        if (w.back_lvl[p].size() != w.lvl_len || w.reach_lvl[p].size() != w.lvl_len) return fail("level arrays");
+        if (w.back_rec[p].size() != w.back_task[p].size() || w.top_back_rec[p].size() != w.top_back[p].size() ||
+            w.reach_rec[p].size() != w.reach_task[p].size() || w.top_reach_rec[p].size() != w.top_reach[p].size() ||
+            w.acc_rec[p].size() != w.decision[p].size())
+            return fail("record counts");
+    }
+    if (w.unit_row.size() != rows || w.unit_term.size() != w.term_node.size()) return fail("unit leaf lists");
+    for (uint32_t r : w.unit_row)
+        if (r >= rows) return fail("unit_row");
+    for (uint32_t te : w.unit_term)
+        if ((te & TERM_INDEX) >= w.term_node.size()) return fail("unit_term");
+    if (w.nsub > w.units.size()) return fail("unit counts");
+    for (const UnitDev& u : w.units) {
+        if (uint64_t(u.lvl0) + u.nlevels + 1 > w.lvl_len || u.tree >= w.trees.size()) return fail("unit range");
+        for (int p = 0; p < 2; p++) {
+            const auto& bl = w.back_lvl[p];
+            const auto& rl = w.reach_lvl[p];
+            for (uint32_t l = 0; l < u.nlevels; l++) {
+                if (bl[u.lvl0 + l + 1] < bl[u.lvl0 + l] || bl[u.lvl0 + l + 1] > w.back_task[p].size())
+                    return fail("back levels");
+                if (rl[u.lvl0 + l + 1] < rl[u.lvl0 + l] || rl[u.lvl0 + l + 1] > w.reach_task[p].size())
+                    return fail("reach levels");
+            }
+            if (u.dec0[p] > u.dec1[p] || u.dec1[p] > w.decision[p].size()) return fail("decision range");
+            if (u.leaf0[p] > u.leaf1[p] || u.leaf1[p] > w.leaf_rec[p].size()) return fail("unit leaf range");
+        }
+        if (u.row0 > u.row1 || u.row1 > w.unit_row.size() || u.term0 > u.term1 || u.term1 > w.unit_term.size())
+            return fail("unit leaf range");
+    }
+    for (int p = 0; p < 2; p++) {
+        if (w.top_back_lvl[p].size() != w.top_levels + 1 || w.top_reach_lvl[p].size() != w.top_levels + 1)
+            return fail("top levels");
+        for (uint32_t l = 0; l < w.top_levels; l++)
+            if (w.top_back_lvl[p][l + 1] < w.top_back_lvl[p][l] || w.top_reach_lvl[p][l + 1] < w.top_reach_lvl[p][l])
+                return fail("top level order");
+        if (w.top_back_lvl[p][w.top_levels] != w.top_back[p].size() ||
+            w.top_reach_lvl[p][w.top_levels] != w.top_reach[p].size())
+            return fail("top level bounds");
+        if (w.top_dec0[p] > w.decision[p].size()) return fail("top decision rows");
+        for (const UnitDev& u : w.units)
+            if (u.dec1[p] > w.top_dec0[p]) return fail("unit decision rows overlap the top rows");
+    }
+    if (readout_net(w.net.kind))
+        for (int p = 0; p < 2; p++) {
+            for (const TowerBlock& b : w.tower_blk[p])
+                if (b.r0 >= b.r1 || b.r1 > rows || b.clo >= b.chi || b.chi > ncfg ||
+                    uint64_t(b.dbase) + uint64_t(b.r1 - b.r0) * (b.chi - b.clo) > w.tower_len)
+                    return fail("tower block");
+            for (const TowerUnit& u : w.tower_unit[p]) {
+                if (u.block >= w.tower_blk[p].size()) return fail("tower unit");
+                const TowerBlock& b = w.tower_blk[p][u.block];
+                if (u.row % 16 || u.row + 16 <= b.r0 || u.row >= b.r1 || u.cfg < b.clo || u.cfg >= b.chi)
+                    return fail("tower unit");
+            }
+        }
+    for (const TreeDev& t : w.trees) {
+        if (t.nodes == 0 || uint64_t(t.node0) + t.nodes > N) return fail("tree range");
+        if (uint64_t(t.reach0) + t.reach_len > w.reach_len) return fail("reach range");
+        if (t.n0 != w.nc(t.node0, 0) || t.n1 != w.nc(t.node0, 1)) return fail("root support");
+        const uint64_t nr = uint64_t(t.n0) + t.n1;
+        if (t.root0 + nr > w.roots.size() || t.carried0 + t.nroots * nr > w.carried.size() ||
+            t.root_value0 + t.nroots * nr > w.root_values_len)
+            return fail("root ranges");
+        if (uint64_t(t.exit0) + t.nexit > nexit) return fail("exit range");
+    }
+    return true;
+}
+
+namespace {
+
+// validate_deep's checks of the element tables, on host threads: the node
+// lists (including the host-only lists the row records were built from), the
+// tasks, the records and every element they name, the pool groups, the tower
+// blocks' rows and the units' windows. They assume validate_shape passed.
+bool validate_elements(const WaveHost& w, std::string* err) {
     auto fail = [&](const char* m) {
         *err = std::string("wave bounds: ") + m;
         return false;
@@ -1185,13 +1309,7 @@ bool validate_deep(const WaveHost& w, std::string* err) {
             if (m) return m;
         return nullptr;
     };
-    const uint64_t N = w.nodes();
-    if (w.node_nc.size() != 2 * N || w.child_start.size() != N + 1 || w.legal_row_of.size() != N ||
-        w.draw_off.size() != N || w.draw_row_off.size() != N || w.reach_base.size() != 2 * N ||
-        w.vals_base.size() != 2 * N || w.parent.size() != N || w.rev_row_of.size() != N || w.rvd_row_of.size() != N)
-        return fail("node arrays disagree");
-    if (w.legal_value.size() != w.ncells || w.legal_off.empty() || w.legal_off.back() != w.ncells)
-        return fail("cell arrays disagree");
+    const uint64_t N = w.nodes(), rows = w.rows(), ncfg = w.cfg_key.size();
     auto node_check = [&](uint64_t i) -> const char* {
         uint32_t kind = w.node_meta[i] & 3u, actor = w.node_meta[i] >> 2;
         if (kind > 2 || actor > 1) return "node_meta";
@@ -1251,12 +1369,6 @@ bool validate_deep(const WaveHost& w, std::string* err) {
             return v != NONE && v >= w.vals_len ? "legal_value" : nullptr;
         }))
         return fail("legal_value");
-    const uint64_t rows = w.rows();
-    if (w.row_cfg_off.size() != 2 * rows + 1 || w.row_cfg_off.back() != w.row_cfg.size()) return fail("row_cfg_off");
-    const uint64_t ncfg = w.cfg_key.size();
-    if (w.cfg_emb.size() != (w.net.kind == MODEL_V5 ? 0 : ncfg * w.net.pool) ||
-        w.pub_raw.size() != rows * w.net.row_bytes)
-        return fail("row payload");
     if (const char* m = first_fail(rows, [&](uint64_t r) -> const char* {
             const uint32_t node = w.row_node[r];
             if (node >= N || (w.node_meta[node] & 3u) != 2) return "row_node";
@@ -1307,33 +1419,6 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         for (const char* m : gm)
             if (m) return fail(m);
     }
-    if (w.net.kind == MODEL_MLP)
-        for (uint32_t k : w.cfg_key)
-            if (k >= w.net.heads) return fail("cfg_key");
-    if (w.cfg_priv.size() != (w.net.kind == MODEL_TWO_TOWER ? ncfg * w.net.priv_in
-                              : w.net.kind == MODEL_V5      ? ncfg * w.net.cfeat
-                                                            : 0))
-        return fail("cfg_priv");
-    if (w.net.kind == MODEL_V5) {  // the v5 build's per-config and per-row job indices
-        const uint64_t njobs = w.trees.size();
-        if (w.cfg_job.size() != ncfg || w.cfg_owner.size() != ncfg || w.row_job.size() != rows ||
-            w.card_feat.size() != njobs * w.net.card_feat || w.pub_raw.size() != uint64_t(rows) * w.net.row_bytes)
-            return fail("v5 tables");
-        for (uint64_t c = 0; c < ncfg; c++)
-            if (w.cfg_job[c] >= njobs || w.cfg_owner[c] > 1) return fail("v5 config owner");
-        for (uint32_t r : w.row_job)
-            if (r >= njobs) return fail("v5 row job");
-    }
-    for (uint32_t t : w.term_node)
-        if (t >= N || (w.node_meta[t] & 3u) != 2) return fail("term_node");
-    const uint64_t nexit = w.exit_node.size();
-    if (w.exit_coff.size() != 2 * nexit + 1 || w.exit_coff.back() != w.snapshot_configs) return fail("exit_coff");
-    if (w.exit_reach.size() != 2 * nexit) return fail("exit_reach");
-    for (uint64_t e = 0; e < nexit; e++)
-        for (int p = 0; p < 2; p++)
-            if (w.exit_node[e] >= N || w.exit_coff[2 * e + p + 1] - w.exit_coff[2 * e + p] != w.nc(w.exit_node[e], p) ||
-                w.exit_reach[2 * e + p] != w.reach_base[2 * size_t(w.exit_node[e]) + p])
-                return fail("exit configs");
     for (int p = 0; p < 2; p++) {
         if (first_fail(w.back_task[p].size(), [&](uint64_t k) {
                 const Task& q = w.back_task[p][k];
@@ -1350,46 +1435,12 @@ bool validate_deep(const WaveHost& w, std::string* err) {
                 return q.node >= N || q.config >= w.nc(q.node, p) || (w.node_meta[q.node] & 3u) != 0 ? "x" : nullptr;
             }))
             return fail("decision task");
-        if (w.back_lvl[p].size() != w.lvl_len || w.reach_lvl[p].size() != w.lvl_len) return fail("level arrays");
-    }
-    if (w.unit_row.size() != rows || w.unit_term.size() != w.term_node.size()) return fail("unit leaf lists");
-    for (uint32_t r : w.unit_row)
-        if (r >= rows) return fail("unit_row");
-    for (uint32_t te : w.unit_term)
-        if ((te & TERM_INDEX) >= w.term_node.size()) return fail("unit_term");
-    if (w.nsub > w.units.size()) return fail("unit counts");
-    for (const UnitDev& u : w.units) {
-        if (uint64_t(u.lvl0) + u.nlevels + 1 > w.lvl_len || u.tree >= w.trees.size()) return fail("unit range");
-        for (int p = 0; p < 2; p++) {
-            const auto& bl = w.back_lvl[p];
-            const auto& rl = w.reach_lvl[p];
-            for (uint32_t l = 0; l < u.nlevels; l++) {
-                if (bl[u.lvl0 + l + 1] < bl[u.lvl0 + l] || bl[u.lvl0 + l + 1] > w.back_task[p].size())
-                    return fail("back levels");
-                if (rl[u.lvl0 + l + 1] < rl[u.lvl0 + l] || rl[u.lvl0 + l + 1] > w.reach_task[p].size())
-                    return fail("reach levels");
-            }
-            if (u.dec0[p] > u.dec1[p] || u.dec1[p] > w.decision[p].size()) return fail("decision range");
-        }
-        if (u.row0 > u.row1 || u.row1 > w.unit_row.size() || u.term0 > u.term1 || u.term1 > w.unit_term.size())
-            return fail("unit leaf range");
     }
     for (int p = 0; p < 2; p++) {
-        if (w.top_back_lvl[p].size() != w.top_levels + 1 || w.top_reach_lvl[p].size() != w.top_levels + 1)
-            return fail("top levels");
-        for (uint32_t l = 0; l < w.top_levels; l++)
-            if (w.top_back_lvl[p][l + 1] < w.top_back_lvl[p][l] || w.top_reach_lvl[p][l + 1] < w.top_reach_lvl[p][l])
-                return fail("top level order");
-        if (w.top_back_lvl[p][w.top_levels] != w.top_back[p].size() ||
-            w.top_reach_lvl[p][w.top_levels] != w.top_reach[p].size())
-            return fail("top level bounds");
         for (const Task& q : w.top_back[p])
             if (q.node >= N || q.config >= w.nc(q.node, p)) return fail("top back task");
         for (const Task& q : w.top_reach[p])
             if (q.node >= N || q.config >= w.nc(q.node, p) || w.parent[q.node] == NONE) return fail("top reach task");
-        if (w.top_dec0[p] > w.decision[p].size()) return fail("top decision rows");
-        for (const UnitDev& u : w.units)
-            if (u.dec1[p] > w.top_dec0[p]) return fail("unit decision rows overlap the top rows");
     }
     // Row records: every slot and element they name.
     for (int p = 0; p < 2; p++) {
@@ -1427,10 +1478,6 @@ bool validate_deep(const WaveHost& w, std::string* err) {
             }
             return true;
         };
-        if (w.back_rec[p].size() != w.back_task[p].size() || w.top_back_rec[p].size() != w.top_back[p].size() ||
-            w.reach_rec[p].size() != w.reach_task[p].size() || w.top_reach_rec[p].size() != w.top_reach[p].size() ||
-            w.acc_rec[p].size() != w.decision[p].size())
-            return fail("record counts");
         if (first_fail(w.back_rec[p].size(), [&](uint64_t k) { return back_ok(w.back_rec[p][k]) ? nullptr : "x"; }))
             return fail("back record");
         if (first_fail(w.top_back_rec[p].size(), [&](uint64_t k) { return back_ok(w.top_back_rec[p][k]) ? nullptr : "x"; }))
@@ -1454,24 +1501,11 @@ bool validate_deep(const WaveHost& w, std::string* err) {
             }))
             return fail("leaf record");
     if (readout_net(w.net.kind))
-        for (int p = 0; p < 2; p++) {
-            // Blocks lie inside the rows, configs and values; every row of a
-            // block names only configs of the block; every unit tiles a block.
-            for (const TowerBlock& b : w.tower_blk[p]) {
-                if (b.r0 >= b.r1 || b.r1 > rows || b.clo >= b.chi || b.chi > ncfg ||
-                    uint64_t(b.dbase) + uint64_t(b.r1 - b.r0) * (b.chi - b.clo) > w.tower_len)
-                    return fail("tower block");
+        for (int p = 0; p < 2; p++)
+            for (const TowerBlock& b : w.tower_blk[p])
                 for (uint32_t r = b.r0; r < b.r1; r++)
                     for (uint32_t x = w.row_cfg_off[2 * r + p]; x < w.row_cfg_off[2 * r + p + 1]; x++)
                         if (w.row_cfg[x] < b.clo || w.row_cfg[x] >= b.chi) return fail("tower block configs");
-            }
-            for (const TowerUnit& u : w.tower_unit[p]) {
-                if (u.block >= w.tower_blk[p].size()) return fail("tower unit");
-                const TowerBlock& b = w.tower_blk[p][u.block];
-                if (u.row % 16 || u.row + 16 <= b.r0 || u.row >= b.r1 || u.cfg < b.clo || u.cfg >= b.chi)
-                    return fail("tower unit");
-            }
-        }
     // The subtree sweep keeps each unit's values in LDS: every slot a unit
     // writes (its leaves, its rows) and reads (its rows' children) must lie
     // inside the unit's window.
@@ -1502,7 +1536,6 @@ bool validate_deep(const WaveHost& w, std::string* err) {
             }
             const uint64_t lo = u.vwin[p], hi = lo + u.vwin_n[p];
             auto in = [&](uint64_t i) { return i >= lo && i < hi; };
-            if (u.leaf0[p] > u.leaf1[p] || u.leaf1[p] > w.leaf_rec[p].size()) return "unit leaf range";
             for (uint32_t k = u.leaf0[p]; k < u.leaf1[p]; k++)
                 if (!in(w.leaf_rec[p][k].out)) return "unit leaf outside its value window";
             for (uint32_t k = u.term0; k < u.term1; k++) {
@@ -1531,18 +1564,12 @@ bool validate_deep(const WaveHost& w, std::string* err) {
         return nullptr;
     };
     if (const char* m = first_fail(w.units.size(), unit_check)) return fail(m);
-    for (const TreeDev& t : w.trees) {
-        if (uint64_t(t.node0) + t.nodes > N) return fail("tree range");
-        if (uint64_t(t.reach0) + t.reach_len > w.reach_len) return fail("reach range");
-        if (t.n0 != w.nc(t.node0, 0) || t.n1 != w.nc(t.node0, 1)) return fail("root support");
-        const uint64_t nr = uint64_t(t.n0) + t.n1;
-        if (t.root0 + nr > w.roots.size() || t.carried0 + t.nroots * nr > w.carried.size() ||
-            t.root_value0 + t.nroots * nr > w.root_values_len)
-            return fail("root ranges");
-        if (uint64_t(t.exit0) + t.nexit > nexit) return fail("exit range");
-    }
     return true;
 }
+
+}  // namespace
+
+bool validate_deep(const WaveHost& w, std::string* err) { return validate_shape(w, err) && validate_elements(w, err); }
 
 bool check_chain_plan(const std::vector<ChainPass>& plan, const uint32_t* cols, uint32_t nrb, uint32_t heads,
                       std::string* err) {

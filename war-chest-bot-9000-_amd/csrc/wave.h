@@ -219,6 +219,10 @@ struct WaveHost {
     std::vector<uint8_t> node_top;  // 1 for a node of a top region
 
     uint32_t max_levels = 0, nroots_max = 0, carry_slots = 0;
+    // The packed lists passed validate_deep on the host. When not (a service
+    // wave of jobs validated at submit), an upload checks the element tables
+    // on the device before the schedule may read them.
+    bool checked = false;
     uint32_t max_vwin = 0;  // the widest unit value window (floats): the sweep's LDS size
     uint32_t max_rwin = 0;  // the widest unit reach window (floats): the reach pass's LDS size
 
@@ -251,7 +255,8 @@ struct WaveHost {
 // value slots of one subtree unit.
 // `validated`: every job already passed validate() (the service checks each
 // job when it is submitted), so the per-job checks are not repeated, nor the
-// deep check of the packed wave (validate_deep) unless WC_DEEP_CHECK=1.
+// deep check of the packed wave (validate_deep) unless WC_DEEP_CHECK=1: the
+// wave's `checked` stays false and its upload checks it on the device.
 bool pack_wave(std::vector<std::shared_ptr<const Job>>&& jobs, WaveHost* w, std::string* err,
                uint32_t unit_slots = UNIT_SLOTS, bool validated = false);
 // The same for jobs owned by the caller (moved into the wave).
@@ -262,8 +267,14 @@ uint64_t digest(const WaveHost& w);
 bool pack_wave(std::vector<Job>&& jobs, WaveHost* w, std::string* err, uint32_t unit_slots = UNIT_SLOTS,
                bool validated = false);
 
-// Bounds of every index the kernels dereference (run by pack_wave).
+// Bounds of every index the kernels dereference (run by pack_wave):
+// validate_shape, then the element tables on host threads.
 bool validate_deep(const WaveHost& w, std::string* err);
+// The checks of validate_deep that read no element table: each list's size
+// against the counts it must match, and the short per-config, per-unit,
+// per-tree and per-exit lists. An upload of a wave that did not pass
+// validate_deep runs these, then the element checks on the device (check.h).
+bool validate_shape(const WaveHost& w, std::string* err);
 
 // Algorithmic HBM bytes of one CFR iteration for traverser p (the counting
 // rule is written next to the implementation), split by the launch that moves

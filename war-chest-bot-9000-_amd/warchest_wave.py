@@ -124,7 +124,8 @@ EXPORTS = [
     "wc_result_tag", "wc_result_weight_version", "wc_result_strategy", "wc_result_root_values",
     "wc_result_carries", "wc_result_routes", "wc_result_free",
     "wc_executor_create", "wc_executor_destroy", "wc_executor_publish",
-    "wc_wave_pack", "wc_wave_repack", "wc_wave_digest", "wc_wave_free", "wc_wave_stats_get", "wc_wave_array", "wc_value_net_plan", "wc_solve_wave",
+    "wc_wave_pack", "wc_wave_repack", "wc_wave_digest", "wc_wave_free", "wc_wave_stats_get", "wc_wave_array",
+    "wc_wave_poke", "wc_wave_check", "wc_value_net_plan", "wc_solve_wave",
     "wc_launch", "wc_inflight_ready", "wc_collect", "wc_wave_leaf_probe", "wc_wave_leaf_trace",
     "wc_time_wave", "wc_peak_probe",
     "wc_mlp_forward", "wc_mlp_forward_noalloc", "wc_time_mlp",
@@ -199,6 +200,8 @@ def _declare(L):
     L.wc_wave_stats_get.argtypes = [C.c_void_p, C.POINTER(WaveStats)]
     L.wc_wave_array.argtypes = [C.c_void_p, C.c_char_p, C.POINTER(C.c_size_t)]
     L.wc_wave_array.restype = _u32p
+    L.wc_wave_poke.argtypes = [C.c_void_p, C.c_char_p, C.c_size_t, C.c_uint32]
+    L.wc_wave_check.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64]
     L.wc_value_net_plan.argtypes = [C.POINTER(C.c_uint32), C.c_uint32, C.c_uint32, C.c_uint32,
                                     C.POINTER(C.c_uint32), C.c_size_t, C.POINTER(C.c_size_t)]
     L.wc_solve_wave.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p)]
@@ -483,6 +486,16 @@ class Wave:
         if not p:
             _check(-1)
         return np.ctypeslib.as_array(p, (n.value,)).copy() if n.value else np.zeros(0, np.uint32)
+
+    def poke(self, name: str, index: int, value: int):
+        """Overwrite one word of a packed table (wc_wave_poke; test support): the
+        wave then counts as unchecked."""
+        _check(lib().wc_wave_poke(self.h, name.encode(), index, value & 0xFFFFFFFF))
+
+    def check(self, executor: "Executor" = None, version: int = 0):
+        """Check every index the kernels follow (wc_wave_check): on the host, or
+        with an executor on its device. Raises WaveError with "wave bounds: ..."."""
+        _check(lib().wc_wave_check(self.h, executor.h if executor is not None else None, version))
 
     def close(self):
         if self.h:
