@@ -205,10 +205,12 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* out);
  * "exit_node", "exit_coff", "legal_value", "child_start", "child",
  * "legal_off", "node_meta", "node_nc", "row_cfg", "row_cfg_off", "draw_to",
  * "rev_src", "rvd_src", "term_node", "unit_term"; the unit records "units"
- * (24 words each); and per player p (0 or 1) "back_rec<p>", "top_back_rec<p>",
- * "reach_rec<p>", "top_reach_rec<p>", "acc_rec<p>", "leaf_rec<p>" (4 words per
- * record), "pool_grp<p>" (36 words per group), "child_vb<p>", "back_lvl<p>",
- * "reach_lvl<p>". Returns NULL (and sets wc_last_error) for an unknown name;
+ * (24 words each) and "trees" (12 words each); and per player p (0 or 1)
+ * "back_rec<p>", "top_back_rec<p>", "reach_rec<p>", "top_reach_rec<p>",
+ * "acc_rec<p>", "leaf_rec<p>" (4 words per record), "pool_grp<p>" (36 words
+ * per group), "child_vb<p>", "back_lvl<p>", "reach_lvl<p>", the top regions'
+ * rows "top_back<p>", "top_reach<p>" (node, config: 2 words each) and their
+ * depth bounds "top_back_lvl<p>", "top_reach_lvl<p>". Returns NULL (and sets wc_last_error) for an unknown name;
  * *n receives the word count. The view lives as long as the wave. */
 const uint32_t* wc_wave_array(const wc_wave* w, const char* name, size_t* n);
 

@@ -332,6 +332,7 @@ auto u32_table(W& h, const std::string& k, size_t* n) -> decltype(h.row_node.dat
     if (k == "term_node") return list(h.term_node);
     if (k == "unit_term") return list(h.unit_term);
     if (k == "units") return list(h.units);
+    if (k == "trees") return list(h.trees);
     for (int p = 0; p < 2; p++) {
         const std::string s = std::to_string(p);
         if (k == "back_rec" + s) return list(h.back_rec[p]);
@@ -344,6 +345,10 @@ auto u32_table(W& h, const std::string& k, size_t* n) -> decltype(h.row_node.dat
         if (k == "child_vb" + s) return list(h.child_vb[p]);
         if (k == "back_lvl" + s) return list(h.back_lvl[p]);
         if (k == "reach_lvl" + s) return list(h.reach_lvl[p]);
+        if (k == "top_back" + s) return list(h.top_back[p]);
+        if (k == "top_reach" + s) return list(h.top_reach[p]);
+        if (k == "top_back_lvl" + s) return list(h.top_back_lvl[p]);
+        if (k == "top_reach_lvl" + s) return list(h.top_reach_lvl[p]);
     }
     return nullptr;
 }
