@@ -42,6 +42,8 @@ def cases(wave):
         ("legal_value", cell, vals_len + 7, "legal_value"),
         ("row_node", 0, n_nodes + 5, "row_node"),
         ("row_cfg", 0, 0xFFFFFFF0, "row_cfg"),
+        ("row_cfg_off", 0, 0xFFFFFFFD, "row_cfg_off"),  # a first offset near 2^32: row 0's list would wrap
+        ("exit_coff", 0, 0xFFFFFFFD, "exit_coff"),
         ("pool_grp0", G_NROWS, 0, "pool group"),
         ("pool_grp0", G_RBASE0, int(a("pool_grp0")[G_RBASE0]) + 1, "pool group reach"),
         ("back_rec0", 0, vals_len, "back record"),

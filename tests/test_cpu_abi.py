@@ -185,7 +185,7 @@ def test_host_check_names_the_first_failing_condition(monkeypatch):
     assert wave.stats()["top_levels"] > 0
     wave.check()
     cases = B.cases(wave)
-    assert len(cases) == 18
+    assert len(cases) == 20
     for name, index, value, msg in cases:
         old = int(wave.array(name)[index])
         wave.poke(name, index, value)

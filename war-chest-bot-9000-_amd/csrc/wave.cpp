@@ -1180,7 +1180,10 @@ bool validate_shape(const WaveHost& w, std::string* err) {
     if (w.legal_value.size() != w.ncells || w.legal_off.empty() || w.legal_off.back() != w.ncells)
         return fail("cell arrays disagree");
     const uint64_t rows = w.rows();
-    if (w.row_cfg_off.size() != 2 * rows + 1 || w.row_cfg_off.back() != w.row_cfg.size()) return fail("row_cfg_off");
+    // An offset list starts at 0 and ends at its list's length; with every
+    // difference equal to its count (checked per entry), no offset wraps.
+    if (w.row_cfg_off.size() != 2 * rows + 1 || w.row_cfg_off[0] != 0 || w.row_cfg_off.back() != w.row_cfg.size())
+        return fail("row_cfg_off");
     const uint64_t ncfg = w.cfg_key.size();
     if (w.cfg_emb.size() != (w.net.kind == MODEL_V5 ? 0 : ncfg * w.net.pool) ||
         w.pub_raw.size() != rows * w.net.row_bytes)
@@ -1205,7 +1208,8 @@ bool validate_shape(const WaveHost& w, std::string* err) {
     for (uint32_t t : w.term_node)
         if (t >= N || (w.node_meta[t] & 3u) != 2) return fail("term_node");
     const uint64_t nexit = w.exit_node.size();
-    if (w.exit_coff.size() != 2 * nexit + 1 || w.exit_coff.back() != w.snapshot_configs) return fail("exit_coff");
+    if (w.exit_coff.size() != 2 * nexit + 1 || w.exit_coff[0] != 0 || w.exit_coff.back() != w.snapshot_configs)
+        return fail("exit_coff");
     if (w.exit_reach.size() != 2 * nexit) return fail("exit_reach");
     for (uint64_t e = 0; e < nexit; e++)
         for (int p = 0; p < 2; p++)
