@@ -311,7 +311,7 @@ auto u32_table(W& h, const std::string& k, size_t* n) -> decltype(h.row_node.dat
         using E = typename std::remove_reference_t<decltype(v)>::value_type;
         static_assert(sizeof(E) % 4 == 0, "a table of uint32 words");
         *n = v.size() * (sizeof(E) / 4);
-        return (P)(void*)v.data();
+        return reinterpret_cast<P>(v.data());  // (the entries are structs of uint32 fields)
     };
     if (k == "row_node") return list(h.row_node);
     if (k == "reach_base") return list(h.reach_base);
