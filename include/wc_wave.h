@@ -153,7 +153,8 @@ void wc_result_free(wc_result* r);
 /* ------------------------------------------------------ executor (lane) API
  * Replaces Executor::{new, publish, launch, collect, solve}, Wave::pack and
  * Harvest::unpack (engine/src/gpu/device.rs:515-831, wave.rs:127-221): one
- * device, one stream, one wave at a time. */
+ * device; schedules in order on one stream, each wave's tables uploaded on a
+ * second stream while the wave before it runs. */
 
 typedef struct wc_executor wc_executor;
 typedef struct wc_wave wc_wave;

@@ -1,4 +1,5 @@
-// One device, one stream: weight banks, wave upload, the CFR schedule, results.
+// One device: weight banks, wave upload (on a copy stream, beside the schedule
+// before it), the CFR schedule (on the executor's stream), results.
 // Counterpart of the reference's `Executor` (engine/src/gpu/device.rs:515-831).
 #pragma once
 
