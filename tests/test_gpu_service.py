@@ -13,7 +13,9 @@ not with another run of the device.
   wave repacked (wc_wave_repack) while its solve is in flight;
 - cost classes and guarded routes (service.rs:452-532,967-991): exclusive
   jobs run in one-job waves, guarded jobs after every lane has drained and
-  trimmed, and the results carry their route flags (client.rs:119-121).
+  trimmed, and the results carry their route flags (client.rs:119-121);
+- the service's waves are bounds-checked at upload on the device by default,
+  and on the host with WC_DEEP_CHECK=1 (a child process).
 """
 import os
 import sys
@@ -262,3 +264,39 @@ def test_prepared_jobs_submitted_again_and_again():
         assert client.queued_work() == 0
     for k, g in got:
         same(g, ref[k], f"job {k}")
+
+
+_HOST_CHECKED_CHILD = r"""
+import sys
+import numpy as np
+sys.path[:0] = sys.argv[1:]
+import oracle as O
+import warchest_wave as ww
+import workloads as W
+jobs = W.jobs("wave256", trees=4, nodes_lo=30, nodes_hi=90, chance=1, terminal_p=0.15, nroots=2, iters=8, seed=57)
+net = W.net_for("wave256")
+with ww.spawn(0, net, ww.WC_PRECISE, lanes=2, wave_jobs=2, window_us=500) as client:
+    got = [h.wait() for h in [client.submit(j, tag=k) for k, j in enumerate(jobs)]]
+for k, (g, j) in enumerate(zip(got, jobs)):
+    o = O.solve(j, net, O.NET_F32)
+    np.testing.assert_array_equal(g.strategy, o["strategy"], err_msg=f"job {k}")
+    np.testing.assert_array_equal(g.root_values, o["roots"], err_msg=f"job {k}")
+print("host-checked service waves: 4 jobs bit-identical", flush=True)
+"""
+
+
+def test_service_with_host_checks():
+    """WC_DEEP_CHECK=1 makes the service check its waves on the host
+    (validate_deep) instead of at upload on the device; the setting is read
+    once per process, so a child process runs the service with it."""
+    import subprocess
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    paths = [os.path.join(root, "war-chest-bot-9000-_amd"), os.path.join(root, "oracle"), here]
+    env = dict(os.environ, WC_DEEP_CHECK="1")
+    say("case host-checked service: a child process, 4 jobs, 2 lanes")
+    run = subprocess.run([sys.executable, "-c", _HOST_CHECKED_CHILD, *paths], env=env, capture_output=True,
+                         text=True, timeout=240)
+    assert run.returncode == 0, run.stderr[-3000:]
+    say(run.stdout.strip())
