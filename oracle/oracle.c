@@ -5,8 +5,8 @@
  * (engine/src/search.rs) and CPU value net, operating on the WCJ8 job bytes
  * of the reference contract (docs/TREE.md, engine/src/serialize.rs). Only the
  * tests, the smoke check and the benchmark's CPU-baseline leg may load this
- * library, and only as the checker or the timed CPU baseline: the product
- * path never calls it.
+ * library, and only as what results are compared against or as the timed CPU
+ * baseline: the product path never calls it.
  *
  * Parity status per function (how each part is pinned is recorded in the
  * tests that exercise it):
