@@ -197,6 +197,11 @@ def test_host_check_names_the_first_failing_condition(monkeypatch):
         wave.poke("row_node", wave.stats()["rows"], 0)
     with pytest.raises(ww.WaveError, match="unknown array"):
         wave.poke("no_such_table", 0, 0)
+    # an empty table is a table of no words, not an unknown one
+    plain = ww.Wave(W.jobs("wave256", trees=2, nodes_lo=60, nodes_hi=90))
+    assert plain.stats()["terminals"] == 0 and len(plain.array("term_node")) == 0
+    with pytest.raises(ww.WaveError, match="unknown array"):
+        plain.array("no_such_table")
 
 
 def test_repacking_a_wave_equals_packing_it_fresh():

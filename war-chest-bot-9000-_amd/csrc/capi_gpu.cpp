@@ -303,15 +303,17 @@ namespace {
 
 // One packed table of a wave as uint32 words, by name: index lists, and the
 // record and unit lists (structs of uint32 fields, field-major within each
-// entry). Null for an unknown name.
+// entry). Null for an unknown name; an empty table is a valid pointer to no
+// words.
 template <class W>
 auto u32_table(W& h, const std::string& k, size_t* n) -> decltype(h.row_node.data()) {
     using P = decltype(h.row_node.data());
+    static uint32_t none[1] = {0};
     auto list = [&](auto& v) -> P {
         using E = typename std::remove_reference_t<decltype(v)>::value_type;
         static_assert(sizeof(E) % 4 == 0, "a table of uint32 words");
         *n = v.size() * (sizeof(E) / 4);
-        return reinterpret_cast<P>(v.data());  // (the entries are structs of uint32 fields)
+        return v.empty() ? none : reinterpret_cast<P>(v.data());  // (the entries are structs of uint32 fields)
     };
     if (k == "row_node") return list(h.row_node);
     if (k == "reach_base") return list(h.reach_base);
