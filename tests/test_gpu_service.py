@@ -266,6 +266,19 @@ def test_prepared_jobs_submitted_again_and_again():
         same(g, ref[k], f"job {k}")
 
 
+def test_two_tower_service_waves():
+    """Service waves of the two-tower net: their readout blocks are checked at
+    upload on the device too; every result bit-identical to the oracle."""
+    jobs = W.jobs("wave512w", trees=4, nodes_lo=40, nodes_hi=120, whale_frac=0.0, info_median=6.0, info_p99=40.0,
+                  info_cap=40, iters=8, nroots=2, seed=59)
+    net = W.net_for("wave512w")
+    say("case two-tower service: 4 jobs, 2 lanes, waves of at most 2")
+    with ww.spawn(0, net, ww.WC_PRECISE, lanes=2, wave_jobs=2, window_us=500) as client:
+        got = [h.wait() for h in [client.submit(j, tag=k) for k, j in enumerate(jobs)]]
+    for k, (g, r) in enumerate(zip(got, alone(jobs, net))):
+        same(g, r, f"job {k}")
+
+
 _HOST_CHECKED_CHILD = r"""
 import sys
 import numpy as np
