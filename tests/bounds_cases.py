@@ -52,7 +52,8 @@ def cases(wave):
         ("top_reach_rec1", 0, reach_len + 3, "top reach record"),
         ("acc_rec0", 1, ncells, "accumulation record"),
         ("leaf_rec0", 1, 0xFFFFFFF0, "leaf record"),
-        ("units", U_RWIN_N0, reach_len + 1, "unit reach window"),
+        ("units", U_RWIN_N0, reach_len + 1, "unit window size"),  # wider than the wave's widest window
+        ("units", U_RWIN0, reach_len + 1, "unit reach window"),  # a window past the reach table
     ]
     # Window conditions, on a unit with reach rows at its deepest level, value
     # rows and network leaves: a slot just outside the window, inside the table.

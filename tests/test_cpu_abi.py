@@ -185,7 +185,7 @@ def test_host_check_names_the_first_failing_condition(monkeypatch):
     assert wave.stats()["top_levels"] > 0
     wave.check()
     cases = B.cases(wave)
-    assert len(cases) == 20
+    assert len(cases) == 21
     for name, index, value, msg in cases:
         old = int(wave.array(name)[index])
         wave.poke(name, index, value)
@@ -202,6 +202,42 @@ def test_host_check_names_the_first_failing_condition(monkeypatch):
     assert plain.stats()["terminals"] == 0 and len(plain.array("term_node")) == 0
     with pytest.raises(ww.WaveError, match="unknown array"):
         plain.array("no_such_table")
+
+
+def test_host_check_survives_random_single_word_edits(monkeypatch):
+    """Random single-word edits of every table wc_wave_array names: the host
+    check accepts the wave or refuses it with "wave bounds: ...", and never
+    reads outside a table itself (a child node's check once read its parent's
+    actor before the parent's own check had bounded it)."""
+    import random
+
+    import bounds_cases as B
+
+    monkeypatch.setenv("WC_UNIT_SLOTS", B.UNIT_SLOTS)
+    wave = ww.Wave(B.jobs())
+    names = ["row_node", "reach_base", "vals_base", "exit_node", "exit_coff", "legal_value", "child_start", "child",
+             "legal_off", "node_meta", "node_nc", "row_cfg", "row_cfg_off", "draw_to", "rev_src", "rvd_src",
+             "term_node", "unit_term", "units", "trees"]
+    names += [f"{k}{p}" for k in ("back_rec", "top_back_rec", "reach_rec", "top_reach_rec", "acc_rec", "leaf_rec",
+                                  "pool_grp", "child_vb", "back_lvl", "reach_lvl", "top_back", "top_reach",
+                                  "top_back_lvl", "top_reach_lvl", "head_rb_n") for p in (0, 1)]
+    tables = {n: wave.array(n) for n in names}
+    rng = random.Random(5)
+    refused = 0
+    for _ in range(800):
+        name = rng.choice([n for n in names if len(tables[n])])
+        i = rng.randrange(len(tables[name]))
+        old = int(tables[name][i])
+        value = rng.choice([0, 1, old + 1, (old - 1) & 0xFFFFFFFF, 0xFFFFFFFF, 0x7FFFFFFF, rng.getrandbits(32)])
+        wave.poke(name, i, value)
+        try:
+            wave.check()
+        except ww.WaveError as e:
+            assert str(e).startswith("wave bounds: "), (name, i, value, str(e))
+            refused += 1
+        wave.poke(name, i, old)
+    wave.check()
+    assert refused > 200
 
 
 def test_repacking_a_wave_equals_packing_it_fresh():

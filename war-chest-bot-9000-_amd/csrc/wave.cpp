@@ -1242,6 +1242,9 @@ bool validate_shape(const WaveHost& w, std::string* err) {
             }
             if (u.dec0[p] > u.dec1[p] || u.dec1[p] > w.decision[p].size()) return fail("decision range");
             if (u.leaf0[p] > u.leaf1[p] || u.leaf1[p] > w.leaf_rec[p].size()) return fail("unit leaf range");
+            // The kernels size each unit's LDS windows by the wave's widest.
+            if (u.vwin_n[p] > w.max_vwin || u.rwin_n[p] > w.max_rwin || uint64_t(u.vwin[p]) + u.vwin_n[p] > w.vals_len)
+                return fail("unit window size");
         }
         if (u.row0 > u.row1 || u.row1 > w.unit_row.size() || u.term0 > u.term1 || u.term1 > w.unit_term.size())
             return fail("unit leaf range");
@@ -1346,6 +1349,7 @@ bool validate_elements(const WaveHost& w, std::string* err) {
         uint32_t par = w.parent[i];
         if (par != NONE) {
             if (par >= N) return "parent";
+            if ((w.node_meta[par] & 3u) > 2 || (w.node_meta[par] >> 2) > 1) return "node_meta";  // read before its own check
             int p = (int)(w.node_meta[par] >> 2);
             uint64_t nc = w.nc((uint32_t)i, p);
             if (w.rev_row_of[i] != NONE) {
