@@ -48,6 +48,48 @@ def test_truncated_and_corrupt_jobs_are_rejected():
         ww.job_validate(j + b"\0")
 
 
+@pytest.mark.parametrize("family", ["wave256", "wave512w", "wave256v5"])
+def test_edited_jobs_are_refused_or_pack_into_checked_waves(family):
+    """Random byte edits of WCJ8 jobs (bit flips, bytes, whole words, truncation):
+    parsing and validation accept or refuse them, and an accepted job packs into a
+    wave that passes the deep bounds check (wc_wave_pack runs it), as the service
+    relies on for jobs validated at submit. Edits like these found, in validation:
+    row ranges running backwards (rev_start, rvd_start), offsets checked one step
+    at a time while being read (draw_off, node_child_start), a draw bound that
+    overflowed 32 bits, carry layouts (snap_coff) and snapshot iterations that
+    only the packer noticed, a leaf listed twice among the network and terminal
+    leaves, child lists naming a node twice, and head rows converted before
+    their range was checked."""
+    import random
+
+    jobs = W.jobs(family, trees=3, nodes_lo=60, nodes_hi=150, seed=91,
+                  **({"whale_frac": 0.0} if family == "wave512w" else {}))
+    rng = random.Random(7)
+    accepted = 0
+    for _ in range(1500):
+        b = bytearray(rng.choice(jobs))
+        for _ in range(rng.randint(1, 4)):
+            at = rng.randrange(len(b))
+            kind = rng.randrange(4)
+            if kind == 0:
+                b[at] ^= 1 << rng.randrange(8)
+            elif kind == 1:
+                b[at] = rng.randrange(256)
+            elif kind == 2:
+                w = at & ~3
+                if w + 4 <= len(b):
+                    b[w:w + 4] = (0xFFFFFFFF if rng.randrange(4) == 0 else rng.randrange(1024)).to_bytes(4, "little")
+            else:
+                del b[at + 1:]
+        try:
+            ww.job_validate(bytes(b))
+        except ww.WaveError:
+            continue
+        accepted += 1
+        ww.Wave([bytes(b)]).close()  # raises if the packed wave fails its bounds check
+    assert accepted > 100
+
+
 def test_wave_pack_names_the_first_bad_job():
     # Jobs parse on several threads; the error still names the first bad one.
     jobs = W.jobs("wave64", trees=5)

@@ -392,12 +392,24 @@ bool validate(const Job& job, std::string* err) {
     };
     const uint32_t N = t.nodes;
     if (N == 0) return fail("no nodes");
+    for (uint32_t x : job.meta.snap_iters)
+        if (x > job.meta.iters) return fail("snap_iters beyond iters");
+    NetShape ns;
+    std::string nerr;
+    if (!ns.parse(job.meta.net_dims, &nerr)) return fail(nerr);
+    if (ns.kind != MODEL_V5)
+        for (uint32_t c = 0; c < t.ncfg; c++) {
+            uint32_t row;
+            if (!head_row(t.cphi[size_t(c) * ns.cfeat], ns.heads, &row)) return fail("config head index out of range");
+        }
     if (t.cfg_off[0] != 0) return fail("cfg_off[0] != 0");
     for (size_t i = 0; i + 1 < t.cfg_off.size(); i++)
         if (t.cfg_off[i + 1] < t.cfg_off[i]) return fail("cfg_off not monotone");
     if (t.node_child_start[0] != 0 || t.node_child_start[N] != t.node_child.size())
         return fail("node_child_start bounds");
     if (t.soff[0] != 0 || t.soff[N] != t.ncells) return fail("soff bounds");
+    if (t.draw_off[0] != 0 || t.draw_off[N] != t.draw_to.size() || t.draw_p.size() != t.draw_to.size())
+        return fail("draw_off bounds");
     if (t.reach_off[0] != 0) return fail("reach_off[0] != 0");
     if (t.node_parent[0] != NONE) return fail("root has a parent");
     if (job.root[0].size() != t.nc(0, 0) || job.root[1].size() != t.nc(0, 1))
@@ -405,11 +417,24 @@ bool validate(const Job& job, std::string* err) {
     for (uint32_t r = 0; r < job.nroots(); r++)
         if (job.carried[0][r].size() != t.nc(0, 0) || job.carried[1][r].size() != t.nc(0, 1))
             return fail("carried root length != root support");
+    // Every node but the root is exactly one node's child.
+    if (t.node_child.size() != size_t(N) - 1) return fail("child lists do not name every node once");
+    {
+        std::vector<uint8_t> seen(N, 0);
+        for (uint32_t ch : t.node_child)
+            if (ch == 0 || ch >= N || seen[ch]++) return fail("child lists do not name every node once");
+    }
+    // The per-node offset lists, whole, before the loop below reads through
+    // them: with both ends bounded and every step non-negative, every entry
+    // lies inside its list.
+    for (uint32_t i = 0; i < N; i++) {
+        if (t.node_child_start[i + 1] < t.node_child_start[i]) return fail("child CSR");
+        if (t.soff[i + 1] < t.soff[i]) return fail("soff not monotone");
+        if (t.draw_off[i + 1] < t.draw_off[i]) return fail("draw_off not monotone");
+    }
     for (uint32_t i = 0; i < N; i++) {
         if (t.node_kind[i] > 2) return fail("node_kind");
         if (t.node_player[i] > 1) return fail("node_player");
-        if (t.node_child_start[i + 1] < t.node_child_start[i]) return fail("child CSR");
-        if (t.soff[i + 1] < t.soff[i]) return fail("soff not monotone");
         if (t.reach_off[i + 1] - t.reach_off[i] != t.nc(i, 0) + t.nc(i, 1)) return fail("reach_off");
         const uint32_t c0 = t.node_child_start[i], c1 = t.node_child_start[i + 1];
         for (uint32_t k = c0; k < c1; k++) {
@@ -431,7 +456,7 @@ bool validate(const Job& job, std::string* err) {
             uint32_t d0 = t.draw_off[i], d1 = t.draw_off[i + 1];
             for (uint32_t c = 0; c < t.nc(i, me); c++) {
                 uint32_t lo = t.draw_row_start[rb + c], hi = t.draw_row_start[rb + c + 1];
-                if (hi < lo || d0 + hi > d1) return fail("draw row bounds");
+                if (hi < lo || uint64_t(d0) + hi > d1) return fail("draw row bounds");
                 for (uint32_t x = lo; x < hi; x++)
                     if (t.draw_to[d0 + x] >= t.nc(ch, me)) return fail("draw_to out of child support");
             }
@@ -446,7 +471,7 @@ bool validate(const Job& job, std::string* err) {
                 return fail("legal rows disagree with soff");
             for (uint32_t c = 0; c < t.nc(i, me); c++) {
                 uint32_t lo = t.legal_off[row0 + c], hi = t.legal_off[row0 + c + 1];
-                if (hi < lo) return fail("legal_off not monotone");
+                if (hi < lo || hi > t.soff[i + 1]) return fail("legal_off not monotone");
                 for (uint32_t x = lo; x < hi; x++) {
                     if (t.cell_row[x] != c) return fail("cell_row disagrees with legal_off");
                     uint32_t ch = t.legal_child[x];
@@ -471,15 +496,21 @@ bool validate(const Job& job, std::string* err) {
         if (t.rev_row_of[i] != NONE) {
             uint32_t row0 = t.rev_row_of[i];
             if (size_t(row0) + t.nc(i, me) >= t.rev_start.size()) return fail("rev rows out of range");
-            for (uint32_t c = 0; c < t.nc(i, me); c++)
-                for (uint32_t x = t.rev_start[row0 + c]; x < t.rev_start[row0 + c + 1]; x++)
-                    if (x >= t.rev_src.size() || t.rev_src[x] >= t.nc(par, me)) return fail("rev_src");
+            for (uint32_t c = 0; c < t.nc(i, me); c++) {
+                const uint32_t lo = t.rev_start[row0 + c], hi = t.rev_start[row0 + c + 1];
+                if (hi < lo || hi > t.rev_src.size()) return fail("rev_start");  // the packer takes hi - lo
+                for (uint32_t x = lo; x < hi; x++)
+                    if (t.rev_src[x] >= t.nc(par, me)) return fail("rev_src");
+            }
         } else if (t.rvd_row_of[i] != NONE) {
             uint32_t row0 = t.rvd_row_of[i];
             if (size_t(row0) + t.nc(i, me) >= t.rvd_start.size()) return fail("rvd rows out of range");
-            for (uint32_t c = 0; c < t.nc(i, me); c++)
-                for (uint32_t x = t.rvd_start[row0 + c]; x < t.rvd_start[row0 + c + 1]; x++)
-                    if (x >= t.rvd_src.size() || t.rvd_src[x] >= t.nc(par, me)) return fail("rvd_src");
+            for (uint32_t c = 0; c < t.nc(i, me); c++) {
+                const uint32_t lo = t.rvd_start[row0 + c], hi = t.rvd_start[row0 + c + 1];
+                if (hi < lo || hi > t.rvd_src.size()) return fail("rvd_start");
+                for (uint32_t x = lo; x < hi; x++)
+                    if (t.rvd_src[x] >= t.nc(par, me)) return fail("rvd_src");
+            }
         } else {
             return fail("non-root node without gather rows");
         }
@@ -488,6 +519,24 @@ bool validate(const Job& job, std::string* err) {
         if (t.leaf_rows[r] >= N || t.node_kind[t.leaf_rows[r]] != 2) return fail("leaf_rows");
     for (size_t r = 0; r < t.term_leaves.size(); r++)
         if (t.term_leaves[r] >= N || t.node_kind[t.term_leaves[r]] != 2) return fail("term_leaves");
+    {  // every leaf is valued once: a network row or a terminal, not both, not twice
+        std::vector<uint8_t> seen(N, 0);
+        for (uint32_t x : t.leaf_rows)
+            if (seen[x]++) return fail("leaf listed twice");
+        for (uint32_t x : t.term_leaves)
+            if (seen[x]++) return fail("leaf listed twice");
+        for (uint32_t i = 0; i < N; i++)
+            if (t.node_kind[i] == 2 && !seen[i]) return fail("leaf neither a network row nor a terminal");
+    }
+    // The carry store's layout: the exits (network leaves, then terminal
+    // leaves), each one's configs of player 0 then player 1.
+    if (t.snap_coff[0] != 0) return fail("snap_coff[0] != 0");
+    for (size_t e = 0; e < t.leaf_rows.size() + t.term_leaves.size(); e++) {
+        const uint32_t node = e < t.leaf_rows.size() ? t.leaf_rows[e] : t.term_leaves[e - t.leaf_rows.size()];
+        for (int p = 0; p < 2; p++)
+            if (t.snap_coff[2 * e + p + 1] - t.snap_coff[2 * e + p] != t.nc(node, p))
+                return fail("snap_coff span != support");
+    }
     for (uint32_t r = 0; r < t.rows; r++)
         for (int p = 0; p < 2; p++) {
             uint32_t lo = t.leaf_coff[2 * r + p], hi = t.leaf_coff[2 * r + p + 1];

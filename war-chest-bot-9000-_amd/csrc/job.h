@@ -108,7 +108,19 @@ std::vector<uint8_t> to_bytes(const Job& job);
 bool from_bytes(const uint8_t* b, size_t n, Job* out, std::string* err);
 
 // Structural checks beyond the reader's count checks: every index in range,
-// every CSR monotone, parents before children. Returns false with a message.
+// every CSR monotone, parents before children, and (for the MLP nets) each
+// config's head row below the net's heads. Returns false with a message.
 bool validate(const Job& job, std::string* err);
+
+// A config's head row: cphi[c][0] of the MLP nets holds it as a float. True
+// (with the row in *row) when it is a whole number below `heads` (any whole
+// number when heads is 0); the range is checked before the conversion.
+inline bool head_row(float key, uint32_t heads, uint32_t* row) {
+    if (!(key >= 0.0f && key < 4294967296.0f)) return false;
+    const uint32_t r = (uint32_t)key;
+    if ((float)r != key || (heads && r >= heads)) return false;
+    *row = r;
+    return true;
+}
 
 }  // namespace wc

@@ -125,8 +125,8 @@ struct JobLayout {
         }
         if (!value_layout(t, pre, vb, &vlen, &err)) return;
         for (uint32_t c = 0; c < t.ncfg && !v5; c++) {
-            const float key = t.cphi[size_t(c) * net.cfeat];
-            if (!(key >= 0.0f) || key != (float)(uint32_t)key || (net.heads && (uint32_t)key >= net.heads)) {
+            uint32_t row;
+            if (!head_row(t.cphi[size_t(c) * net.cfeat], net.heads, &row)) {
                 err = "config head index out of range";
                 return;
             }
