@@ -211,7 +211,11 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* out);
  * "acc_rec<p>", "leaf_rec<p>" (4 words per record), "pool_grp<p>" (36 words
  * per group), "child_vb<p>", "back_lvl<p>", "reach_lvl<p>", the top regions'
  * rows "top_back<p>", "top_reach<p>" (node, config: 2 words each) and their
- * depth bounds "top_back_lvl<p>", "top_reach_lvl<p>", and "head_rb_n<p>" (the
+ * depth bounds "top_back_lvl<p>", "top_reach_lvl<p>", the top regions' value
+ * launches "top_back_run<p>" (4 words each: depth, the second depth of a fused
+ * pair or 0xFFFFFFFF, its first chunk bound, its chunk count) and their chunk
+ * bounds "top_back_chunk<p>" (per fused pair, chunks + 1 row bounds in the
+ * deeper depth, then chunks + 1 in the shallower), and "head_rb_n<p>" (the
  * head columns each 16-row block of network rows needs for traverser p). Returns NULL (and sets wc_last_error) for an unknown name;
  * *n receives the word count. The view lives as long as the wave. */
 const uint32_t* wc_wave_array(const wc_wave* w, const char* name, size_t* n);

@@ -54,6 +54,9 @@ def cases(wave):
         ("leaf_rec0", 1, 0xFFFFFFF0, "leaf record"),
         ("units", U_RWIN_N0, reach_len + 1, "unit window size"),  # wider than the wave's widest window
         ("units", U_RWIN0, reach_len + 1, "unit reach window"),  # a window past the reach table
+        ("top_back_run0", 0, st["top_levels"] + 3, "top back runs"),  # a depth the wave does not have
+        ("top_back_chunk0", 1, 0, "top back chunks"),  # a chunk bound before the depth's first row
+        ("top_back_chunk0", 0, int(a("top_back_chunk0")[0]) + 1, "top back chunks"),  # skips the first row
     ]
     # Window conditions, on a unit with reach rows at its deepest level, value
     # rows and network leaves: a slot just outside the window, inside the table.

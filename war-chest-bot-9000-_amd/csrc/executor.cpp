@@ -423,7 +423,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
         size_t node_meta, nc, legal_value, draw_to, draw_p, reach_base, vals_base, rev_src, rev_cell, rvd_src, rvd_p,
             row_node, row_cfg_off, row_cfg, cfg_emb, pub_raw, term_node, term_util, roots, carried, exit_node,
             exit_coff, exit_reach, trees, units, bt[2], rt[2], dc[2], bl[2], rl[2], cv[2], lr[2], pg[2], twb[2], twu[2], cfg_priv,
-            unit_term, tb[2], tr[2], head_tile_n, cp[2], card_feat, row_job, cfg_job, cfg_owner;
+            unit_term, tb[2], tr[2], tc[2], head_tile_n, cp[2], card_feat, row_job, cfg_job, cfg_owner;
     } o;
     o.node_meta = blob.put(w.node_meta);
     o.nc = blob.put(w.node_nc);
@@ -480,6 +480,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
     for (int p = 0; p < 2; p++) {
         o.tb[p] = blob.put(w.top_back_rec[p]);
         o.tr[p] = blob.put(w.top_reach_rec[p]);
+        o.tc[p] = blob.put(w.top_back_chunk[p]);
     }
     // The device check's words follow the tables: it runs beside the wave
     // before, which holds the solve state.
@@ -606,6 +607,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
     for (int p = 0; p < 2; p++) {
         top_back_dev_[p] = (const BackRec*)(T + o.tb[p]);
         top_reach_dev_[p] = (const ReachRec*)(T + o.tr[p]);
+        top_chunk_dev_[p] = (const uint32_t*)(T + o.tc[p]);
     }
     d.nunits = (uint32_t)w.units.size();
     d.max_vwin = w.max_vwin;
@@ -844,11 +846,19 @@ void Executor::leaf_net(const NetBank& bank, int q) {
         run_mlp(bank, dev_.rows, Xq_[q], nullptr, head_tile_n_, chain_plan_[q], chain_npass_[q], S_[q]);
 }
 
-// Top regions, one depth per launch: values bottom-up.
+// Top regions' values bottom-up, one launch per run of the wave's plan: one
+// depth, or two whose dependent rows the packer grouped into chunks.
 void Executor::top_back(const WaveHost& w, int p, int mode, float da, float db, float pr) {
-    for (uint32_t l = w.top_levels; l-- > 0;) {
-        uint32_t b = w.top_back_lvl[p][l], e = w.top_back_lvl[p][l + 1];
-        launch_back_rows(dev_, top_back_dev_[p] + b, e - b, p, mode, da, db, pr, stream_);
+    const std::vector<uint32_t>& run = w.top_back_run[p];
+    for (size_t i = 0; i < run.size(); i += TOP_RUN) {
+        const uint32_t l = run[i];
+        if (run[i + 1] == NONE) {
+            const uint32_t b = w.top_back_lvl[p][l], e = w.top_back_lvl[p][l + 1];
+            launch_back_rows(dev_, top_back_dev_[p] + b, e - b, p, mode, da, db, pr, stream_);
+        } else {
+            launch_back_pair(dev_, top_back_dev_[p], top_chunk_dev_[p] + run[i + 2], run[i + 3], p, mode, da, db, pr,
+                             stream_);
+        }
     }
 }
 

@@ -261,6 +261,7 @@ class Executor {
     uint32_t* check_host_ = nullptr;  // pinned landing of the flag word
     const BackRec* top_back_dev_[2] = {};    // top-region rows by depth (device copies)
     const ReachRec* top_reach_dev_[2] = {};
+    const uint32_t* top_chunk_dev_[2] = {};  // chunk bounds of the fused value launches
     const uint32_t* head_tile_n_ = nullptr;  // head width per 128-row tile (device copy)
     const ChainPass* chain_plan_[2] = {};    // fused value net passes per traverser (device copies)
     uint32_t chain_npass_[2] = {0, 0};

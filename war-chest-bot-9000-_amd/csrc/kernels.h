@@ -108,6 +108,12 @@ void launch_sweep(const WaveDev& w, uint32_t unit0, uint32_t n, const float* hea
 // Top-region values at one depth for the traverser.
 void launch_back_rows(const WaveDev& w, const BackRec* rows, uint32_t n, int traverser, int mode, float da,
                       float db, float predict, hipStream_t s);
+// Top-region values at two depths in one launch of `chunks` workgroups:
+// workgroup k runs rows[off[k] .. off[k + 1]) of the deeper depth, then
+// rows[off[chunks + 1 + k] .. off[chunks + 2 + k]) of the shallower one,
+// which read no deeper row of another chunk (WaveHost::top_back_run).
+void launch_back_pair(const WaveDev& w, const BackRec* rows, const uint32_t* off, uint32_t chunks, int traverser,
+                      int mode, float da, float db, float predict, hipStream_t s);
 void launch_normalize(const WaveDev& w, int touched0, int touched1, hipStream_t s);
 void launch_gather_carry(const WaveDev& w, const float* reach, int slot, hipStream_t s);
 void launch_collect_root(const WaveDev& w, int root, int player, hipStream_t s);

@@ -944,6 +944,34 @@ void launch_back_rows(const WaveDev& w, const BackRec* rows, uint32_t n, int tra
                            traverser, da, db, predict);
 }
 
+// Two top depths in one launch: each workgroup takes one chunk's rows of the
+// deeper depth, then (after a block barrier: the values it wrote are read by
+// the same workgroup) that chunk's rows of the shallower depth. Sparing the
+// launch boundary saves its fixed cost, about as long as a depth's own rows
+// take.
+template <int MODE>
+__global__ __launch_bounds__(BLOCK) void k_back_pair(WaveDev w, const BackRec* rows, const uint32_t* off,
+                                                   uint32_t chunks, int p, float da, float db, float predict) {
+    const uint32_t k = blockIdx.x;
+    for (uint32_t i = off[k] + threadIdx.x; i < off[k + 1]; i += blockDim.x)
+        backprop_row<MODE, false>(w, p, rows[i], da, db, predict, w.snap, nullptr, 0);
+    __syncthreads();
+    const uint32_t* o = off + chunks + 1;
+    for (uint32_t i = o[k] + threadIdx.x; i < o[k + 1]; i += blockDim.x)
+        backprop_row<MODE, false>(w, p, rows[i], da, db, predict, w.snap, nullptr, 0);
+}
+
+void launch_back_pair(const WaveDev& w, const BackRec* rows, const uint32_t* off, uint32_t chunks, int traverser,
+                      int mode, float da, float db, float predict, hipStream_t s) {
+    if (!chunks) return;
+    if (mode == MODE_VALUE)
+        hipLaunchKernelGGL(k_back_pair<MODE_VALUE>, dim3(chunks), dim3(TOP_BLOCK), 0, s, w, rows, off, chunks,
+                           traverser, da, db, predict);
+    else
+        hipLaunchKernelGGL(k_back_pair<MODE_REGRET>, dim3(chunks), dim3(TOP_BLOCK), 0, s, w, rows, off, chunks,
+                           traverser, da, db, predict);
+}
+
 // Average strategy: sum / row sum, uniform when the sum is not positive, the
 // literal current strategy for a player whose sum was never updated
 // (engine/src/search.rs:899-938).

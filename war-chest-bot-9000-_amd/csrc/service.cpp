@@ -553,8 +553,12 @@ void Service::lane_main(uint32_t lane) {
         }
         F.version = net->version;
         if (ok) {
-            try {  // validated at submit; a wave too large for host memory fails its tickets
-                ok = pack_wave(std::move(jobs), &wh, &err, UNIT_SLOTS, true);
+            // Validated at submit; a wave too large for host memory fails its
+            // tickets. The lanes pack without fused top-depth launches: the
+            // service is bound by the host, and their planning costs the lane
+            // more host time than the launches save on the device.
+            try {
+                ok = pack_wave(std::move(jobs), &wh, &err, UNIT_SLOTS, true, false);
             } catch (const std::exception& e) {
                 ok = false;
                 err = std::string("packing the wave failed: ") + e.what();

@@ -461,9 +461,230 @@ void build_records(WaveHost* wp) {
             if (term_ex[p][k]) w.unit_term[k] |= term_export(p);
 }
 
+// The top regions' value launches (WaveHost::top_back_run). The non-empty
+// depths are taken deepest first; each depth and the next one above fuse
+// into one launch when every group of their dependent rows stays small (a
+// group: a shallower row with the deeper rows whose values it reads, closed
+// under sharing them; at most TOP_FUSE_MAX rows), else the depth runs alone
+// and the next is tried with the one above it. A fused pair's rows are
+// reordered within each depth so that each chunk (whole groups, at most
+// TOP_CHUNK_ROWS rows of each depth unless one group holds more) is
+// contiguous in both. The rows of two trees share no slot, so each tree's
+// rows of a depth (a contiguous range: trees are in job order at every
+// depth) are grouped on their own, in parallel. Without `fuse` every depth is
+// its own launch.
+void plan_top_back(WaveHost* wp, bool fuse) {
+    WaveHost& w = *wp;
+    const size_t J = w.trees.size();
+    parallel_for(2, [&](size_t pi) {  // the players' rows are apart
+        const int p = (int)pi;
+        std::vector<uint32_t>& run = w.top_back_run[p];
+        std::vector<uint32_t>& chunk = w.top_back_chunk[p];
+        run.clear();
+        chunk.clear();
+        const std::vector<uint32_t>& lvl = w.top_back_lvl[p];
+        std::vector<Task>& task = w.top_back[p];
+        std::vector<BackRec>& rec = w.top_back_rec[p];
+        std::vector<uint32_t> depths;  // the non-empty ones, deepest first
+        for (uint32_t l = w.top_levels; l-- > 0;)
+            if (lvl[l + 1] > lvl[l]) depths.push_back(l);
+        // Tree k's rows at depth d: [cut(d, k), cut(d, k + 1)).
+        auto cut = [&](uint32_t d, size_t k) -> uint32_t {
+            if (k >= J) return lvl[d + 1];
+            return (uint32_t)(std::lower_bound(task.begin() + lvl[d], task.begin() + lvl[d + 1], w.trees[k].node0,
+                                               [](const Task& t, uint32_t n) { return t.node < n; }) -
+                              task.begin());
+        };
+        // The slots a record reads (none for a record whose elements fall
+        // outside their lists: validation refuses such a wave later).
+        auto reads = [&](const BackRec& r, auto&& fn) {
+            const uint32_t n = r.kn & REC_N, kind = r.kn >> 30;
+            const size_t len = kind == BACK_OWN    ? w.legal_value.size()
+                               : kind == BACK_DRAW ? w.draw_to.size()
+                                                   : w.child_vb[p].size();
+            if (uint64_t(r.start) + n > len) return;
+            for (uint32_t k = 0; k < n; k++) {
+                if (kind == BACK_OWN) {
+                    if (w.legal_value[r.start + k] != NONE) fn(w.legal_value[r.start + k]);
+                } else if (kind == BACK_DRAW) {
+                    fn(r.arg + w.draw_to[r.start + k]);
+                } else {
+                    fn(w.child_vb[p][r.start + k] + r.arg);
+                }
+            }
+        };
+        // One tree's groups for the pair (deeper depth a, shallower b): a
+        // group per row (a's rows, then b's), numbered in order of first
+        // appearance over b's rows, then a's. False when a group outgrows
+        // TOP_FUSE_MAX (or another tree's did: `stop`).
+        struct Grouping {
+            uint32_t a0 = 0, na = 0, b0 = 0, nb = 0;
+            std::vector<uint32_t> label, size_a, size_b;
+        };
+        auto group = [&](uint32_t a, uint32_t b, size_t k, Grouping* g, const bool* stop) {
+            g->a0 = cut(a, k);
+            g->na = cut(a, k + 1) - g->a0;
+            g->b0 = cut(b, k);
+            g->nb = cut(b, k + 1) - g->b0;
+            const uint32_t a0 = g->a0, na = g->na, b0 = g->b0, nb = g->nb;
+            // a's rows by output slot: each node's rows are consecutive, its
+            // configs in order from its value base, so a slot is found among
+            // the nodes' slot ranges (few, sorted by base). Rows laid out
+            // otherwise, or ranges that overlap, leave the pair apart.
+            struct Range {
+                uint32_t base, n, row;
+            };
+            std::vector<Range> ranges;
+            for (uint32_t i = 0; i < na;) {
+                const uint32_t base = rec[a0 + i].out;
+                uint32_t j = i;
+                for (; j < na && task[a0 + j].node == task[a0 + i].node; j++)
+                    if (task[a0 + j].config != j - i || rec[a0 + j].out != base + (j - i)) return false;
+                ranges.push_back({base, j - i, i});
+                i = j;
+            }
+            std::sort(ranges.begin(), ranges.end(), [](const Range& x, const Range& y) { return x.base < y.base; });
+            for (size_t r = 1; r < ranges.size(); r++)
+                if (uint64_t(ranges[r - 1].base) + ranges[r - 1].n > ranges[r].base) return false;
+            // The rows of one node of b read the same few children: the
+            // ranges found for the current node are tried first.
+            constexpr uint32_t RECENT = 16;
+            const Range* recent[RECENT];
+            uint32_t nrecent = 0;
+            auto row_of = [&](uint32_t s) -> uint32_t {  // NONE: no row of a writes s
+                for (uint32_t q = 0; q < nrecent; q++)
+                    if (s - recent[q]->base < recent[q]->n) return recent[q]->row + (s - recent[q]->base);
+                auto it = std::upper_bound(ranges.begin(), ranges.end(), s,
+                                           [](uint32_t v, const Range& r) { return v < r.base; });
+                if (it == ranges.begin()) return NONE;
+                --it;
+                if (s - it->base >= it->n) return NONE;
+                if (nrecent < RECENT) recent[nrecent++] = &*it;
+                return it->row + (s - it->base);
+            };
+            std::vector<uint32_t> up(na + nb), size(na + nb, 1);
+            for (uint32_t i = 0; i < na + nb; i++) up[i] = i;
+            auto find = [&](uint32_t x) {
+                while (up[x] != x) x = up[x] = up[up[x]];
+                return x;
+            };
+            bool fits = true;
+            for (uint32_t j = 0; j < nb && fits; j++) {
+                if ((j & 255) == 0 && __atomic_load_n(stop, __ATOMIC_RELAXED)) return false;
+                if (j == 0 || task[b0 + j].node != task[b0 + j - 1].node) nrecent = 0;
+                reads(rec[b0 + j], [&](uint32_t s) {
+                    const uint32_t i = row_of(s);
+                    if (i == NONE) return;
+                    uint32_t x = find(i), y = find(na + j);
+                    if (x == y) return;
+                    if (size[x] > size[y]) std::swap(x, y);
+                    up[x] = y;
+                    size[y] += size[x];
+                    if (size[y] > TOP_FUSE_MAX) fits = false;
+                });
+            }
+            if (!fits) return false;
+            std::vector<uint32_t>& id = size;  // reused: each root's group number
+            std::fill(id.begin(), id.end(), NONE);
+            g->label.assign(na + nb, 0);
+            g->size_a.clear();
+            g->size_b.clear();
+            for (uint32_t v = 0; v < na + nb; v++) {
+                const uint32_t x = v < nb ? na + v : v - nb;  // b's rows first
+                const uint32_t r = find(x);
+                if (id[r] == NONE) {
+                    id[r] = (uint32_t)g->size_a.size();
+                    g->size_a.push_back(0);
+                    g->size_b.push_back(0);
+                }
+                g->label[x] = id[r];
+                (x < na ? g->size_a : g->size_b)[id[r]]++;
+            }
+            return true;
+        };
+        // A fused pair: each tree's groups dealt into chunks in order, and
+        // its rows of each depth reordered by (chunk, group).
+        auto fuse_pair = [&](std::vector<Grouping>& gs, std::vector<std::vector<uint32_t>>& ca,
+                             std::vector<std::vector<uint32_t>>& cb) {
+            parallel_for(J, [&](size_t k) {
+                Grouping& g = gs[k];
+                const size_t ng = g.size_a.size();
+                std::vector<uint32_t> gchunk(ng);
+                for (size_t c = 0; c < ng; c++) {
+                    const bool open = !ca[k].empty(), empty = open && ca[k].back() == 0 && cb[k].back() == 0;
+                    if (!open || (!empty && (ca[k].back() + g.size_a[c] > TOP_CHUNK_ROWS ||
+                                             cb[k].back() + g.size_b[c] > TOP_CHUNK_ROWS))) {
+                        ca[k].push_back(0);
+                        cb[k].push_back(0);
+                    }
+                    gchunk[c] = (uint32_t)ca[k].size() - 1;
+                    ca[k].back() += g.size_a[c];
+                    cb[k].back() += g.size_b[c];
+                }
+                auto reorder = [&](uint32_t base, uint32_t n, bool side_b, const std::vector<uint32_t>& per_chunk) {
+                    const uint32_t lab0 = side_b ? g.na : 0;
+                    std::vector<uint32_t> fill(per_chunk.size(), 0), gat(ng);
+                    for (size_t c = 1; c < per_chunk.size(); c++) fill[c] = fill[c - 1] + per_chunk[c - 1];
+                    for (size_t c = 0; c < ng; c++) {  // groups inside a chunk keep their order
+                        gat[c] = fill[gchunk[c]];
+                        fill[gchunk[c]] += side_b ? g.size_b[c] : g.size_a[c];
+                    }
+                    std::vector<Task> t(n);
+                    std::vector<BackRec> r(n);
+                    for (uint32_t i = 0; i < n; i++) {
+                        const uint32_t to = gat[g.label[lab0 + i]]++;
+                        t[to] = task[base + i];
+                        r[to] = rec[base + i];
+                    }
+                    std::copy(t.begin(), t.end(), task.begin() + base);
+                    std::copy(r.begin(), r.end(), rec.begin() + base);
+                };
+                reorder(g.a0, g.na, false, ca[k]);
+                reorder(g.b0, g.nb, true, cb[k]);
+            });
+        };
+        for (size_t i = 0; i < depths.size();) {
+            const uint32_t a = depths[i];
+            // A draw of the traverser sums outcomes that several of its
+            // configs share: rows of b that draw join large groups, so such a
+            // pair is not grouped at all.
+            auto draws = [&](uint32_t d) {
+                for (uint32_t r = lvl[d]; r < lvl[d + 1]; r++)
+                    if ((rec[r].kn >> 30) == BACK_DRAW) return true;
+                return false;
+            };
+            if (fuse && i + 1 < depths.size() && !draws(depths[i + 1])) {
+                const uint32_t b = depths[i + 1];
+                std::vector<Grouping> gs(J);
+                bool stop = false;
+                parallel_for(J, [&](size_t k) {
+                    if (!group(a, b, k, &gs[k], &stop)) __atomic_store_n(&stop, true, __ATOMIC_RELAXED);
+                });
+                if (!stop) {
+                    std::vector<std::vector<uint32_t>> ca(J), cb(J);  // rows of a and of b per chunk, per tree
+                    fuse_pair(gs, ca, cb);
+                    size_t nchunks = 0;
+                    for (size_t k = 0; k < J; k++) nchunks += ca[k].size();
+                    run.insert(run.end(), {a, b, (uint32_t)chunk.size(), (uint32_t)nchunks});
+                    for (int side = 0; side < 2; side++) {
+                        uint32_t at = lvl[side ? b : a];
+                        chunk.push_back(at);
+                        for (size_t k = 0; k < J; k++)
+                            for (uint32_t n : side ? cb[k] : ca[k]) chunk.push_back(at += n);
+                    }
+                    i += 2;
+                    continue;
+                }
+            }
+            run.insert(run.end(), {a, NONE, (uint32_t)chunk.size(), 0u});
+            i += 1;
+        }
+    });
+}
+
 }  // namespace
 
-constexpr size_t WAVE_HOST_BYTES = 2336;  // sizeof(WaveHost) on x86-64 (libstdc++)
+constexpr size_t WAVE_HOST_BYTES = 2432;  // sizeof(WaveHost) on x86-64 (libstdc++)
 static_assert(sizeof(WaveHost) == WAVE_HOST_BYTES, "a WaveHost member was added or changed: update reset() and digest()");
 // Lists the packer sizes with resize() and then overwrites whole keep their
 // length (and contents) here: the next resize then clears only what the
@@ -485,6 +706,8 @@ void WaveHost::reset() {
         empty(top_reach[p]);
         empty(top_back_lvl[p]);
         empty(top_reach_lvl[p]);
+        empty(top_back_run[p]);
+        empty(top_back_chunk[p]);
         empty(pool_grp[p]);
         empty(tower_blk[p]);
         empty(tower_unit[p]);
@@ -508,7 +731,7 @@ void WaveHost::reset() {
 }
 
 bool pack_wave(std::vector<std::shared_ptr<const Job>>&& jobs, WaveHost* out, std::string* err, uint32_t unit_slots,
-               bool validated) {
+               bool validated, bool fuse_top) {
     if (jobs.empty()) {
         *err = "cannot pack an empty wave";
         return false;
@@ -1087,6 +1310,12 @@ bool pack_wave(std::vector<std::shared_ptr<const Job>>&& jobs, WaveHost* out, st
         return false;
     }
     build_records(&w);
+    // WC_TOP_FUSE=0 or 1 overrides the caller's choice.
+    static const int top_fuse_env = [] {
+        const char* e = std::getenv("WC_TOP_FUSE");
+        return e && *e ? (*e == '0' ? 0 : 1) : -1;
+    }();
+    plan_top_back(&w, top_fuse_env < 0 ? fuse_top : top_fuse_env == 1);
     w.jobs = std::move(jobs);
     // A wave packed from jobs that each passed validate() is this packer's own
     // output and is not checked again (about 40% of the packing's host work);
@@ -1135,7 +1364,7 @@ uint64_t digest(const WaveHost& w) {
     list(w.units);
     for (int p = 0; p < 2; p++) {
         for (const auto* v : {&w.head_rb_n[p], &w.back_lvl[p], &w.reach_lvl[p], &w.top_back_lvl[p], &w.top_reach_lvl[p],
-                              &w.child_vb[p]})
+                              &w.top_back_run[p], &w.top_back_chunk[p], &w.child_vb[p]})
             list(*v);
         for (const auto* v : {&w.back_task[p], &w.reach_task[p], &w.decision[p], &w.top_back[p], &w.top_reach[p]})
             list(*v);
@@ -1160,11 +1389,12 @@ uint64_t digest(const WaveHost& w) {
 
 // Every index a kernel dereferences, checked against the buffer it indexes.
 // The device code relies on these bounds and performs no checks of its own.
-bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_t unit_slots, bool validated) {
+bool pack_wave(std::vector<Job>&& jobs, WaveHost* out, std::string* err, uint32_t unit_slots, bool validated,
+               bool fuse_top) {
     std::vector<std::shared_ptr<const Job>> shared(jobs.size());
     for (size_t k = 0; k < jobs.size(); k++) shared[k] = std::make_shared<const Job>(std::move(jobs[k]));
     jobs.clear();
-    return pack_wave(std::move(shared), out, err, unit_slots, validated);
+    return pack_wave(std::move(shared), out, err, unit_slots, validated, fuse_top);
 }
 
 bool validate_shape(const WaveHost& w, std::string* err) {
@@ -1258,6 +1488,35 @@ bool validate_shape(const WaveHost& w, std::string* err) {
         if (w.top_back_lvl[p][w.top_levels] != w.top_back[p].size() ||
             w.top_reach_lvl[p][w.top_levels] != w.top_reach[p].size())
             return fail("top level bounds");
+        // The value launches: every non-empty depth once, deepest first; a
+        // fused pair's chunk bounds run through each depth's rows in order.
+        const std::vector<uint32_t>& run = w.top_back_run[p];
+        const std::vector<uint32_t>& off = w.top_back_chunk[p];
+        if (run.size() % TOP_RUN) return fail("top back runs");
+        uint32_t next = w.top_levels;  // depths below this one are still to come
+        auto take = [&](uint32_t d) {
+            if (d >= next) return false;
+            for (uint32_t l = d + 1; l < next; l++)
+                if (w.top_back_lvl[p][l + 1] > w.top_back_lvl[p][l]) return false;  // a depth left out
+            next = d;
+            return w.top_back_lvl[p][d + 1] > w.top_back_lvl[p][d];
+        };
+        for (size_t i = 0; i < run.size(); i += TOP_RUN) {
+            const uint32_t a = run[i], b = run[i + 1], at = run[i + 2], nch = run[i + 3];
+            if (!take(a)) return fail("top back runs");
+            if (b == NONE) continue;
+            if (!take(b) || nch == 0 || uint64_t(at) + 2 * (uint64_t(nch) + 1) > off.size())
+                return fail("top back runs");
+            for (int side = 0; side < 2; side++) {
+                const uint32_t d = side ? b : a;
+                const uint32_t* o = off.data() + at + side * (nch + 1);
+                if (o[0] != w.top_back_lvl[p][d] || o[nch] != w.top_back_lvl[p][d + 1]) return fail("top back chunks");
+                for (uint32_t k = 0; k < nch; k++)
+                    if (o[k + 1] < o[k]) return fail("top back chunks");
+            }
+        }
+        for (uint32_t l = 0; l < next; l++)
+            if (w.top_back_lvl[p][l + 1] > w.top_back_lvl[p][l]) return fail("top back runs");
         if (w.top_dec0[p] > w.decision[p].size()) return fail("top decision rows");
         for (const UnitDev& u : w.units)
             if (u.dec1[p] > w.top_dec0[p]) return fail("unit decision rows overlap the top rows");

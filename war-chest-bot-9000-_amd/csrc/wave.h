@@ -155,6 +155,11 @@ bool check_chain_plan(const std::vector<ChainPass>& plan, const uint32_t* cols, 
 
 // Default unit budget in value slots (floats of one player's value vector).
 constexpr uint32_t UNIT_SLOTS = 4096;
+// Top-region value launches: words per run (WaveHost::top_back_run), the rows
+// a fused chunk takes per depth before it closes (one per thread of a
+// one-wavefront workgroup), and the largest group of dependent rows of two
+// depths that still fuses them into one launch.
+constexpr uint32_t TOP_RUN = 4, TOP_CHUNK_ROWS = 64, TOP_FUSE_MAX = 128;
 
 struct WaveHost {
     Meta meta;
@@ -216,6 +221,16 @@ struct WaveHost {
     uint32_t top_dec0[2] = {0, 0};
     std::vector<uint32_t> top_back_lvl[2], top_reach_lvl[2];
     uint32_t top_levels = 0;
+    // The value pass's launches over the top depths, deepest first, TOP_RUN
+    // words each: {depth, second depth or NONE, first chunk offset, chunks}.
+    // A run of two depths (the next non-empty one above) is one launch of
+    // `chunks` workgroups: workgroup k runs the deeper depth's rows
+    // [off[k], off[k + 1]), then, after a barrier, the shallower depth's rows
+    // [off[chunks + 1 + k], off[chunks + 2 + k]), off = top_back_chunk[p] +
+    // first chunk offset. The deeper rows whose values a shallower row reads
+    // sit in its chunk, so no other workgroup's results are needed. A run of
+    // one depth is one launch over its rows.
+    std::vector<uint32_t> top_back_run[2], top_back_chunk[2];
     std::vector<uint8_t> node_top;  // 1 for a node of a top region
 
     uint32_t max_levels = 0, nroots_max = 0, carry_slots = 0;
@@ -257,15 +272,18 @@ struct WaveHost {
 // job when it is submitted), so the per-job checks are not repeated, nor the
 // deep check of the packed wave (validate_deep) unless WC_DEEP_CHECK=1: the
 // wave's `checked` stays false and its upload checks it on the device.
+// `fuse_top`: plan fused launches over pairs of top depths (one launch fewer
+// per pair, for some host work: WaveHost::top_back_run); WC_TOP_FUSE=0 or 1
+// overrides it.
 bool pack_wave(std::vector<std::shared_ptr<const Job>>&& jobs, WaveHost* w, std::string* err,
-               uint32_t unit_slots = UNIT_SLOTS, bool validated = false);
+               uint32_t unit_slots = UNIT_SLOTS, bool validated = false, bool fuse_top = true);
 // The same for jobs owned by the caller (moved into the wave).
 // A 64-bit digest of every list and count of a packed wave (FNV-1a over
 // 8-byte words), for tests that compare two packings of the same jobs.
 uint64_t digest(const WaveHost& w);
 
 bool pack_wave(std::vector<Job>&& jobs, WaveHost* w, std::string* err, uint32_t unit_slots = UNIT_SLOTS,
-               bool validated = false);
+               bool validated = false, bool fuse_top = true);
 
 // Bounds of every index the kernels dereference (run by pack_wave):
 // validate_shape, then the element tables on host threads.
