@@ -57,6 +57,9 @@ def cases(wave):
         ("top_back_run0", 0, st["top_levels"] + 3, "top back runs"),  # a depth the wave does not have
         ("top_back_chunk0", 1, 0, "top back chunks"),  # a chunk bound before the depth's first row
         ("top_back_chunk0", 0, int(a("top_back_chunk0")[0]) + 1, "top back chunks"),  # skips the first row
+        ("top_reach_run1", 0, 0, "top reach runs"),  # the root depth, which has no reach rows
+        ("top_reach_chunk1", 0, int(a("top_reach_chunk1")[0]) + 1, "top reach chunks"),
+        ("top_reach_par1", 0, 0xFFFFFFF0, "top reach parents"),  # a parent row past the top rows
     ]
     # Window conditions, on a unit with reach rows at its deepest level, value
     # rows and network leaves: a slot just outside the window, inside the table.

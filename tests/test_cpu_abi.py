@@ -227,7 +227,7 @@ def test_host_check_names_the_first_failing_condition(monkeypatch):
     assert wave.stats()["top_levels"] > 0
     wave.check()
     cases = B.cases(wave)
-    assert len(cases) == 24
+    assert len(cases) == 27
     for name, index, value, msg in cases:
         old = int(wave.array(name)[index])
         wave.poke(name, index, value)
@@ -262,7 +262,8 @@ def test_host_check_survives_random_single_word_edits(monkeypatch):
              "term_node", "unit_term", "units", "trees"]
     names += [f"{k}{p}" for k in ("back_rec", "top_back_rec", "reach_rec", "top_reach_rec", "acc_rec", "leaf_rec",
                                   "pool_grp", "child_vb", "back_lvl", "reach_lvl", "top_back", "top_reach",
-                                  "top_back_lvl", "top_reach_lvl", "top_back_run", "top_back_chunk", "head_rb_n")
+                                  "top_back_lvl", "top_reach_lvl", "top_back_run", "top_back_chunk", "top_reach_run",
+                                  "top_reach_chunk", "top_reach_par", "head_rb_n")
               for p in (0, 1)]
     tables = {n: wave.array(n) for n in names}
     rng = random.Random(5)

@@ -185,3 +185,88 @@ def test_a_row_moved_out_of_its_chunk_is_caught(monkeypatch):
             wave.poke(name, words * r2 + k, int(x[k]))
     with pytest.raises(AssertionError, match="not equal"):  # the chunk comparison, not an earlier check
         check_plan(wave)
+
+
+def reach_reads(tables, rec):
+    """The reach slots a list of top reach records reads (wave.h ReachRec:
+    the parent's slots pbase + rev_src or rvd_src entries), as (reader
+    index, slot) arrays."""
+    pbase, start, kn = rec[:, 1].astype(np.int64), rec[:, 2].astype(np.int64), rec[:, 3].astype(np.int64)
+    rev, n = (kn >> 31) == 0, kn & 0x1FFFFFFF
+    reader = np.repeat(np.arange(len(rec)), n)
+    idx = np.repeat(start, n) + (np.arange(int(n.sum())) - np.repeat(np.cumsum(n) - n, n))
+    use_rev = np.repeat(rev, n)
+    src = np.where(use_rev, tables["rev_src"][np.where(use_rev, idx, 0)], tables["rvd_src"][np.where(use_rev, 0, idx)])
+    return reader, np.repeat(pbase, n) + src
+
+
+def check_reach_plan(wave):
+    """The reach pass's runs (WaveHost::top_reach_run): every non-empty depth
+    once, top-down; in a fused pair every shallower row is computed by some
+    chunk, and each chunk computes every shallower row its deeper rows read."""
+    a = wave.array
+    tables = {n: a(n).astype(np.int64) for n in ("rev_src", "rvd_src")}
+    top_levels = wave.stats()["top_levels"]
+    fused = 0
+    for p in (0, 1):
+        lvl = a(f"top_reach_lvl{p}")
+        rec = a(f"top_reach_rec{p}").reshape(-1, 4)
+        runs = a(f"top_reach_run{p}").reshape(-1, 4)
+        off = a(f"top_reach_chunk{p}").astype(np.int64)
+        par = a(f"top_reach_par{p}").astype(np.int64)
+        depths = [d for d in range(top_levels) if lvl[d + 1] > lvl[d]]
+        launched = []
+        for d, e, at, nch in (tuple(int(x) for x in r) for r in runs):
+            launched.append(d)
+            if e == NONE:
+                continue
+            launched.append(e)
+            fused += 1
+            assert depths.index(e) == depths.index(d) + 1
+            ob, oq = off[at:at + nch + 1], off[at + nch + 1:at + 2 * nch + 2]
+            assert ob[0] == lvl[e] and ob[-1] == lvl[e + 1] and np.all(np.diff(ob) >= 0) and np.all(np.diff(oq) >= 0)
+            names = par[oq[0]:oq[-1]]
+            assert np.all((names >= lvl[d]) & (names < lvl[d + 1]))
+            assert set(names.tolist()) == set(range(lvl[d], lvl[d + 1])), "every shallower row is computed"
+            # (chunk, shallower row) pairs the plan computes, and those the deeper rows read
+            chunk_of_name = np.searchsorted(oq, np.arange(oq[0], oq[-1]), side="right") - 1
+            have = set((chunk_of_name * (1 << 32) + names).tolist())
+            shallow = rec[lvl[d]:lvl[d + 1]]
+            order = np.argsort(shallow[:, 0])
+            outs = shallow[order, 0].astype(np.int64)
+            reader, slot = reach_reads(tables, rec[lvl[e]:lvl[e + 1]])
+            at_slot = np.searchsorted(outs, slot)
+            hit = (at_slot < len(outs)) & (outs[np.minimum(at_slot, len(outs) - 1)] == slot)
+            assert hit.any()
+            row = lvl[d] + order[at_slot[hit]]
+            chunk = np.searchsorted(ob, lvl[e] + reader[hit], side="right") - 1
+            need = set((chunk * (1 << 32) + row).tolist())
+            assert need <= have, "a deeper row reads a shallower row its chunk does not compute"
+        assert launched == depths
+    return fused
+
+
+@pytest.mark.parametrize("family,spec", FAMILIES, ids=[f for f, _ in FAMILIES])
+def test_fused_reach_chunks_compute_what_they_read(family, spec, monkeypatch):
+    monkeypatch.setenv("WC_UNIT_SLOTS", "256")
+    wave = ww.Wave(W.jobs(family, **spec))
+    assert check_reach_plan(wave) >= 2
+    wave.check()
+
+
+def test_the_benchmarked_wave_fuses_its_reach_pairs():
+    assert check_reach_plan(ww.Wave(W.jobs("wave256"))) == 6  # three pairs of each player's depths
+
+
+def test_a_parent_left_out_of_its_chunk_is_caught(monkeypatch):
+    monkeypatch.setenv("WC_UNIT_SLOTS", "256")
+    wave = ww.Wave(W.jobs("wave256", trees=6, nodes_lo=150, nodes_hi=300, seed=81))
+    check_reach_plan(wave)
+    a = wave.array
+    d, e, at, nch = (int(x) for x in next(r for r in a("top_reach_run0").reshape(-1, 4) if r[1] != NONE))
+    off = a("top_reach_chunk0")
+    first = int(off[at + nch + 1])  # chunk 0's first named shallower row, which its deeper rows read
+    assert off[at + 1] > off[at]  # chunk 0 has deeper rows
+    wave.poke("top_reach_par0", first, int(a("top_reach_par0")[first]) ^ 1)
+    with pytest.raises(AssertionError):
+        check_reach_plan(wave)

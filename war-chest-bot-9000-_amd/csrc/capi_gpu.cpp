@@ -353,6 +353,9 @@ auto u32_table(W& h, const std::string& k, size_t* n) -> decltype(h.row_node.dat
         if (k == "top_reach_lvl" + s) return list(h.top_reach_lvl[p]);
         if (k == "top_back_run" + s) return list(h.top_back_run[p]);
         if (k == "top_back_chunk" + s) return list(h.top_back_chunk[p]);
+        if (k == "top_reach_run" + s) return list(h.top_reach_run[p]);
+        if (k == "top_reach_chunk" + s) return list(h.top_reach_chunk[p]);
+        if (k == "top_reach_par" + s) return list(h.top_reach_par[p]);
         if (k == "head_rb_n" + s) return list(h.head_rb_n[p]);
     }
     return nullptr;

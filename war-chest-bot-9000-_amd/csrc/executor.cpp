@@ -423,7 +423,7 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
         size_t node_meta, nc, legal_value, draw_to, draw_p, reach_base, vals_base, rev_src, rev_cell, rvd_src, rvd_p,
             row_node, row_cfg_off, row_cfg, cfg_emb, pub_raw, term_node, term_util, roots, carried, exit_node,
             exit_coff, exit_reach, trees, units, bt[2], rt[2], dc[2], bl[2], rl[2], cv[2], lr[2], pg[2], twb[2], twu[2], cfg_priv,
-            unit_term, tb[2], tr[2], tc[2], head_tile_n, cp[2], card_feat, row_job, cfg_job, cfg_owner;
+            unit_term, tb[2], tr[2], tc[2], rc[2], rp[2], head_tile_n, cp[2], card_feat, row_job, cfg_job, cfg_owner;
     } o;
     o.node_meta = blob.put(w.node_meta);
     o.nc = blob.put(w.node_nc);
@@ -481,6 +481,8 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
         o.tb[p] = blob.put(w.top_back_rec[p]);
         o.tr[p] = blob.put(w.top_reach_rec[p]);
         o.tc[p] = blob.put(w.top_back_chunk[p]);
+        o.rc[p] = blob.put(w.top_reach_chunk[p]);
+        o.rp[p] = blob.put(w.top_reach_par[p]);
     }
     // The device check's words follow the tables: it runs beside the wave
     // before, which holds the solve state.
@@ -608,6 +610,8 @@ bool Executor::upload(const WaveHost& w, const NetBank& bank, uint32_t slot, std
         top_back_dev_[p] = (const BackRec*)(T + o.tb[p]);
         top_reach_dev_[p] = (const ReachRec*)(T + o.tr[p]);
         top_chunk_dev_[p] = (const uint32_t*)(T + o.tc[p]);
+        top_reach_chunk_dev_[p] = (const uint32_t*)(T + o.rc[p]);
+        top_reach_par_dev_[p] = (const uint32_t*)(T + o.rp[p]);
     }
     d.nunits = (uint32_t)w.units.size();
     d.max_vwin = w.max_vwin;
@@ -862,24 +866,43 @@ void Executor::top_back(const WaveHost& w, int p, int mode, float da, float db, 
     }
 }
 
-// Top regions' reach, one depth per launch, top-down; p < 0: both players.
-// With reach2 (p >= 0), each launch also takes both players' rows of that
-// depth under strat2 into reach2 (an independent reach computation).
+// Top regions' reach, top-down, one launch per depth at which a run of the
+// wave's plan starts (one depth, or two chunk by chunk); p < 0: both players.
+// With reach2 (p >= 0), the launches also take both players' rows under
+// strat2 into reach2 (an independent reach computation). The sets are
+// independent, so each follows its own runs.
 void Executor::top_reach(const WaveHost& w, int p, float* reach, const float* strat, float* reach2,
                          const float* strat2) {
-    for (uint32_t l = 1; l < w.top_levels; l++) {
-        ReachSet set[3];
-        int k = 0;
-        for (int q = 0; q < 2; q++) {
-            const uint32_t b = w.top_reach_lvl[q][l], n = w.top_reach_lvl[q][l + 1] - b;
-            if (p < 0 || p == q) set[k++] = ReachSet{top_reach_dev_[q] + b, n, reach, strat};
-        }
-        if (reach2 && p >= 0)
-            for (int q = 0; q < 2; q++) {
-                const uint32_t b = w.top_reach_lvl[q][l], n = w.top_reach_lvl[q][l + 1] - b;
-                set[k++] = ReachSet{top_reach_dev_[q] + b, n, reach2, strat2};
+    struct Set {
+        int q;
+        float* reach;
+        const float* strat;
+        size_t next;  // the set's next run
+    } sets[3];
+    int ns = 0;
+    for (int q = 0; q < 2; q++)
+        if (p < 0 || p == q) sets[ns++] = Set{q, reach, strat, 0};
+    if (reach2 && p >= 0)
+        for (int q = 0; q < 2; q++) sets[ns++] = Set{q, reach2, strat2, 0};
+    for (uint32_t l = 0; l < w.top_levels; l++) {
+        ReachSet one[3];
+        ReachPair two[3] = {};
+        int n1 = 0, n2 = 0;
+        for (int i = 0; i < ns; i++) {
+            Set& s = sets[i];
+            const std::vector<uint32_t>& run = w.top_reach_run[s.q];
+            if (s.next >= run.size() || run[s.next] != l) continue;
+            if (run[s.next + 1] == NONE) {
+                const uint32_t b = w.top_reach_lvl[s.q][l], n = w.top_reach_lvl[s.q][l + 1] - b;
+                one[n1++] = ReachSet{top_reach_dev_[s.q] + b, n, s.reach, s.strat};
+            } else {
+                two[n2++] = ReachPair{top_reach_dev_[s.q], top_reach_chunk_dev_[s.q] + run[s.next + 2],
+                                      top_reach_par_dev_[s.q], run[s.next + 3], s.reach, s.strat};
             }
-        launch_reach_rows(dev_, set[0], set[1], set[2], stream_);
+            s.next += TOP_RUN;
+        }
+        if (n1) launch_reach_rows(dev_, one[0], one[1], one[2], stream_);
+        if (n2) launch_reach_pair(dev_, two[0], two[1], two[2], stream_);
     }
 }
 

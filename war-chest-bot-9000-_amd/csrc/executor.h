@@ -262,6 +262,8 @@ class Executor {
     const BackRec* top_back_dev_[2] = {};    // top-region rows by depth (device copies)
     const ReachRec* top_reach_dev_[2] = {};
     const uint32_t* top_chunk_dev_[2] = {};  // chunk bounds of the fused value launches
+    const uint32_t* top_reach_chunk_dev_[2] = {};  // chunk bounds of the fused reach launches
+    const uint32_t* top_reach_par_dev_[2] = {};    // and the shallower rows each chunk computes
     const uint32_t* head_tile_n_ = nullptr;  // head width per 128-row tile (device copy)
     const ChainPass* chain_plan_[2] = {};    // fused value net passes per traverser (device copies)
     uint32_t chain_npass_[2] = {0, 0};

@@ -90,6 +90,20 @@ struct ReachSet {
 };
 // Top-region reach at one depth: up to three independent row sets in one launch.
 void launch_reach_rows(const WaveDev& w, const ReachSet& a, const ReachSet& b, const ReachSet& c, hipStream_t s);
+// One reach computation's rows of two top depths, chunk by chunk
+// (WaveHost::top_reach_run): workgroup k of the set computes the shallower
+// rows rows[par[off[chunks + 1 + k] .. off[chunks + 2 + k])], then the deeper
+// rows rows[off[k] .. off[k + 1]), which read no shallower row of another
+// chunk.
+struct ReachPair {
+    const ReachRec* rows;
+    const uint32_t* off;
+    const uint32_t* par;
+    uint32_t chunks;
+    float* reach;
+    const float* strat;
+};
+void launch_reach_pair(const WaveDev& w, const ReachPair& a, const ReachPair& b, const ReachPair& c, hipStream_t s);
 void launch_seed_sum(const WaveDev& w, hipStream_t s);
 // Leaf reach masses and pooled beliefs of one player (-1 = both), written into
 // the query inputs x0 (traverser 0) and x1 (traverser 1) in the operand precision.

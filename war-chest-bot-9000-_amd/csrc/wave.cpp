@@ -682,9 +682,150 @@ void plan_top_back(WaveHost* wp, bool fuse) {
     });
 }
 
+// The reach pass's launches over the top depths (WaveHost::top_reach_run).
+// The non-empty depths are taken top-down; each depth and the next one below
+// fuse into one launch when chunks of the deeper depth's rows (TOP_CHUNK_ROWS
+// consecutive rows of one tree) each read at most TOP_FUSE_MAX rows of the
+// shallower depth (a reach row reads parent reach slots through its gather).
+// Each chunk names those rows and computes them itself, so a shallower row
+// read by two chunks is computed twice; the shallower rows no chunk reads
+// fill chunks of their own. Reach rows keep no state, so computing one twice
+// writes the same value twice. The rows keep their order. Without `fuse`
+// every depth is its own launch.
+void plan_top_reach(WaveHost* wp, bool fuse) {
+    WaveHost& w = *wp;
+    const size_t J = w.trees.size();
+    parallel_for(2, [&](size_t pi) {
+        const int p = (int)pi;
+        std::vector<uint32_t>& run = w.top_reach_run[p];
+        std::vector<uint32_t>& chunk = w.top_reach_chunk[p];
+        std::vector<uint32_t>& par = w.top_reach_par[p];
+        run.clear();
+        chunk.clear();
+        par.clear();
+        const std::vector<uint32_t>& lvl = w.top_reach_lvl[p];
+        const std::vector<Task>& task = w.top_reach[p];
+        const std::vector<ReachRec>& rec = w.top_reach_rec[p];
+        std::vector<uint32_t> depths;  // the non-empty ones, top-down
+        for (uint32_t l = 0; l < w.top_levels; l++)
+            if (lvl[l + 1] > lvl[l]) depths.push_back(l);
+        auto cut = [&](uint32_t d, size_t k) -> uint32_t {
+            if (k >= J) return lvl[d + 1];
+            return (uint32_t)(std::lower_bound(task.begin() + lvl[d], task.begin() + lvl[d + 1], w.trees[k].node0,
+                                               [](const Task& t, uint32_t n) { return t.node < n; }) -
+                              task.begin());
+        };
+        // One tree's chunks for the pair (shallower d, deeper e): the deeper
+        // rows per chunk and the shallower rows each chunk names (wave-global
+        // row indices), then the chunks of unread shallower rows. False when
+        // a chunk would name more than TOP_FUSE_MAX rows (or another tree's
+        // did: `stop`), or the shallower rows are not laid out node by node.
+        struct Chunks {
+            std::vector<uint32_t> deep, npar, par;
+        };
+        auto plan = [&](uint32_t d, uint32_t e, size_t k, Chunks* c, const bool* stop) {
+            const uint32_t a0 = cut(d, k), na = cut(d, k + 1) - a0, b0 = cut(e, k), nb = cut(e, k + 1) - b0;
+            struct Range {
+                uint32_t base, n, row;
+            };
+            std::vector<Range> ranges;
+            for (uint32_t i = 0; i < na;) {
+                const uint32_t base = rec[a0 + i].out;
+                uint32_t j = i;
+                for (; j < na && task[a0 + j].node == task[a0 + i].node; j++)
+                    if (task[a0 + j].config != j - i || rec[a0 + j].out != base + (j - i)) return false;
+                ranges.push_back({base, j - i, i});
+                i = j;
+            }
+            std::sort(ranges.begin(), ranges.end(), [](const Range& x, const Range& y) { return x.base < y.base; });
+            for (size_t r = 1; r < ranges.size(); r++)
+                if (uint64_t(ranges[r - 1].base) + ranges[r - 1].n > ranges[r].base) return false;
+            const Range* last = nullptr;  // a row's gather reads one parent's slots
+            auto row_of = [&](uint32_t s) -> uint32_t {
+                if (last && s - last->base < last->n) return last->row + (s - last->base);
+                auto it = std::upper_bound(ranges.begin(), ranges.end(), s,
+                                           [](uint32_t v, const Range& r) { return v < r.base; });
+                if (it == ranges.begin()) return NONE;
+                --it;
+                if (s - it->base >= it->n) return NONE;
+                last = &*it;
+                return it->row + (s - it->base);
+            };
+            std::vector<uint8_t> read(na, 0);
+            std::vector<uint32_t> mine;
+            for (uint32_t c0 = 0; c0 < nb; c0 += TOP_CHUNK_ROWS) {
+                if (__atomic_load_n(stop, __ATOMIC_RELAXED)) return false;
+                const uint32_t c1 = std::min(nb, c0 + TOP_CHUNK_ROWS);
+                mine.clear();
+                for (uint32_t j = c0; j < c1; j++) {
+                    const ReachRec& q = rec[b0 + j];
+                    const uint32_t n = q.kn & REC_N;
+                    const std::vector<uint32_t>& src = (q.kn >> 31) == REACH_REV ? w.rev_src : w.rvd_src;
+                    if (uint64_t(q.start) + n > src.size()) continue;  // refused by validation later
+                    for (uint32_t x = 0; x < n; x++) {
+                        const uint32_t i = row_of(q.pbase + src[q.start + x]);
+                        if (i != NONE) mine.push_back(i);
+                    }
+                }
+                std::sort(mine.begin(), mine.end());
+                mine.erase(std::unique(mine.begin(), mine.end()), mine.end());
+                if (mine.size() > TOP_FUSE_MAX) return false;
+                c->deep.push_back(c1 - c0);
+                c->npar.push_back((uint32_t)mine.size());
+                for (uint32_t i : mine) {
+                    c->par.push_back(a0 + i);
+                    read[i] = 1;
+                }
+            }
+            uint32_t fill = 0;  // unread shallower rows, TOP_CHUNK_ROWS per chunk
+            for (uint32_t i = 0; i < na; i++) {
+                if (read[i]) continue;
+                if (fill == 0) {
+                    c->deep.push_back(0);
+                    c->npar.push_back(0);
+                }
+                c->par.push_back(a0 + i);
+                c->npar.back()++;
+                fill = fill + 1 == TOP_CHUNK_ROWS ? 0 : fill + 1;
+            }
+            return true;
+        };
+        for (size_t i = 0; i < depths.size();) {
+            const uint32_t d = depths[i];
+            if (fuse && i + 1 < depths.size()) {
+                const uint32_t e = depths[i + 1];
+                std::vector<Chunks> cs(J);
+                bool stop = false;
+                parallel_for(J, [&](size_t k) {
+                    if (!plan(d, e, k, &cs[k], &stop)) __atomic_store_n(&stop, true, __ATOMIC_RELAXED);
+                });
+                if (!stop) {
+                    size_t nchunks = 0;
+                    for (size_t k = 0; k < J; k++) nchunks += cs[k].deep.size();
+                    run.insert(run.end(), {d, e, (uint32_t)chunk.size(), (uint32_t)nchunks});
+                    uint32_t at = lvl[e];
+                    chunk.push_back(at);
+                    for (size_t k = 0; k < J; k++)
+                        for (uint32_t n : cs[k].deep) chunk.push_back(at += n);
+                    uint32_t pat = (uint32_t)par.size();
+                    chunk.push_back(pat);
+                    for (size_t k = 0; k < J; k++) {
+                        for (uint32_t n : cs[k].npar) chunk.push_back(pat += n);
+                        par.insert(par.end(), cs[k].par.begin(), cs[k].par.end());
+                    }
+                    i += 2;
+                    continue;
+                }
+            }
+            run.insert(run.end(), {d, NONE, (uint32_t)chunk.size(), 0u});
+            i += 1;
+        }
+    });
+}
+
 }  // namespace
 
-constexpr size_t WAVE_HOST_BYTES = 2432;  // sizeof(WaveHost) on x86-64 (libstdc++)
+constexpr size_t WAVE_HOST_BYTES = 2576;  // sizeof(WaveHost) on x86-64 (libstdc++)
 static_assert(sizeof(WaveHost) == WAVE_HOST_BYTES, "a WaveHost member was added or changed: update reset() and digest()");
 // Lists the packer sizes with resize() and then overwrites whole keep their
 // length (and contents) here: the next resize then clears only what the
@@ -708,6 +849,9 @@ void WaveHost::reset() {
         empty(top_reach_lvl[p]);
         empty(top_back_run[p]);
         empty(top_back_chunk[p]);
+        empty(top_reach_run[p]);
+        empty(top_reach_chunk[p]);
+        empty(top_reach_par[p]);
         empty(pool_grp[p]);
         empty(tower_blk[p]);
         empty(tower_unit[p]);
@@ -1316,6 +1460,7 @@ bool pack_wave(std::vector<std::shared_ptr<const Job>>&& jobs, WaveHost* out, st
         return e && *e ? (*e == '0' ? 0 : 1) : -1;
     }();
     plan_top_back(&w, top_fuse_env < 0 ? fuse_top : top_fuse_env == 1);
+    plan_top_reach(&w, top_fuse_env < 0 ? fuse_top : top_fuse_env == 1);
     w.jobs = std::move(jobs);
     // A wave packed from jobs that each passed validate() is this packer's own
     // output and is not checked again (about 40% of the packing's host work);
@@ -1364,7 +1509,8 @@ uint64_t digest(const WaveHost& w) {
     list(w.units);
     for (int p = 0; p < 2; p++) {
         for (const auto* v : {&w.head_rb_n[p], &w.back_lvl[p], &w.reach_lvl[p], &w.top_back_lvl[p], &w.top_reach_lvl[p],
-                              &w.top_back_run[p], &w.top_back_chunk[p], &w.child_vb[p]})
+                              &w.top_back_run[p], &w.top_back_chunk[p], &w.top_reach_run[p],
+                              &w.top_reach_chunk[p], &w.top_reach_par[p], &w.child_vb[p]})
             list(*v);
         for (const auto* v : {&w.back_task[p], &w.reach_task[p], &w.decision[p], &w.top_back[p], &w.top_reach[p]})
             list(*v);
@@ -1517,6 +1663,41 @@ bool validate_shape(const WaveHost& w, std::string* err) {
         }
         for (uint32_t l = 0; l < next; l++)
             if (w.top_back_lvl[p][l + 1] > w.top_back_lvl[p][l]) return fail("top back runs");
+        // The reach launches: every non-empty depth once, top-down; a fused
+        // pair's deeper bounds run through its rows, its parent lists through
+        // top_reach_par, each entry a row of the shallower depth.
+        const std::vector<uint32_t>& rrun = w.top_reach_run[p];
+        const std::vector<uint32_t>& roff = w.top_reach_chunk[p];
+        const std::vector<uint32_t>& rpar = w.top_reach_par[p];
+        const std::vector<uint32_t>& rl = w.top_reach_lvl[p];
+        if (rrun.size() % TOP_RUN) return fail("top reach runs");
+        uint32_t from = 0;  // depths from this one on are still to come
+        auto reach_take = [&](uint32_t d) {
+            if (d < from || d >= w.top_levels) return false;
+            for (uint32_t l = from; l < d; l++)
+                if (rl[l + 1] > rl[l]) return false;  // a depth left out
+            from = d + 1;
+            return rl[d + 1] > rl[d];
+        };
+        for (size_t i = 0; i < rrun.size(); i += TOP_RUN) {
+            const uint32_t d = rrun[i], e = rrun[i + 1], at = rrun[i + 2], nch = rrun[i + 3];
+            if (!reach_take(d)) return fail("top reach runs");
+            if (e == NONE) continue;
+            if (!reach_take(e) || nch == 0 || uint64_t(at) + 2 * (uint64_t(nch) + 1) > roff.size())
+                return fail("top reach runs");
+            const uint32_t* o = roff.data() + at;
+            if (o[0] != rl[e] || o[nch] != rl[e + 1]) return fail("top reach chunks");
+            for (uint32_t k = 0; k < nch; k++)
+                if (o[k + 1] < o[k]) return fail("top reach chunks");
+            const uint32_t* q = o + nch + 1;
+            if (q[nch] > rpar.size()) return fail("top reach chunks");
+            for (uint32_t k = 0; k < nch; k++)
+                if (q[k + 1] < q[k]) return fail("top reach chunks");
+            for (uint32_t x = q[0]; x < q[nch]; x++)
+                if (rpar[x] < rl[d] || rpar[x] >= rl[d + 1]) return fail("top reach parents");
+        }
+        for (uint32_t l = from; l < w.top_levels; l++)
+            if (rl[l + 1] > rl[l]) return fail("top reach runs");
         if (w.top_dec0[p] > w.decision[p].size()) return fail("top decision rows");
         for (const UnitDev& u : w.units)
             if (u.dec1[p] > w.top_dec0[p]) return fail("unit decision rows overlap the top rows");

@@ -231,6 +231,17 @@ struct WaveHost {
     // sit in its chunk, so no other workgroup's results are needed. A run of
     // one depth is one launch over its rows.
     std::vector<uint32_t> top_back_run[2], top_back_chunk[2];
+    // The reach pass's launches over the top depths, top-down, TOP_RUN words
+    // each: {depth, second depth or NONE, first chunk offset, chunks}. A run
+    // of two depths (the next non-empty one below) is one launch of `chunks`
+    // workgroups: workgroup k computes the shallower depth's rows named by
+    // top_reach_par[p][off[chunks + 1 + k] .. off[chunks + 2 + k]), then,
+    // after a barrier, the deeper depth's rows [off[k], off[k + 1]), off =
+    // top_reach_chunk[p] + first chunk offset. Each chunk names every
+    // shallower row its deeper rows read (a shallower row read by several
+    // chunks is computed by each: the same value, written again); shallower
+    // rows that no deeper row reads fill chunks with no deeper rows.
+    std::vector<uint32_t> top_reach_run[2], top_reach_chunk[2], top_reach_par[2];
     std::vector<uint8_t> node_top;  // 1 for a node of a top region
 
     uint32_t max_levels = 0, nroots_max = 0, carry_slots = 0;
