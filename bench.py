@@ -163,7 +163,7 @@ def main():
     value = node_iters / (wave_ms * 1e-3)
     cfr_ms, mlp_ms, leaf_ms, other_ms, iter_ms, back_ms, top_ms, reach_ms = parts[:8]
     # Algorithmic bytes of one launch of each CFR kernel, averaged over the two traversers.
-    kernels = {"k_sweep<regret>": (0, back_ms), "top-region launches (k_back_rows, k_back_pair, k_reach_rows)": (1, top_ms),
+    kernels = {"k_sweep<regret>": (0, back_ms), "top-region launches (k_back_rows, k_back_pair, k_reach_rows, k_reach_pair)": (1, top_ms),
                "k_reach": (2, reach_ms)}
     by_kernel = {}
     for name, (k, ms) in kernels.items():

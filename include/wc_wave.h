@@ -215,7 +215,12 @@ int wc_wave_stats_get(const wc_wave* w, wc_wave_stats* out);
  * launches "top_back_run<p>" (4 words each: depth, the second depth of a fused
  * pair or 0xFFFFFFFF, its first chunk bound, its chunk count) and their chunk
  * bounds "top_back_chunk<p>" (per fused pair, chunks + 1 row bounds in the
- * deeper depth, then chunks + 1 in the shallower), and "head_rb_n<p>" (the
+ * deeper depth, then chunks + 1 in the shallower), the reach pass's launches
+ * "top_reach_run<p>" (4 words each, top-down: depth, the deeper depth of a
+ * fused pair or 0xFFFFFFFF, its first chunk bound, its chunk count), their
+ * chunk bounds "top_reach_chunk<p>" (per fused pair, chunks + 1 row bounds in
+ * the deeper depth, then chunks + 1 bounds into "top_reach_par<p>", the
+ * shallower rows each chunk computes), and "head_rb_n<p>" (the
  * head columns each 16-row block of network rows needs for traverser p). Returns NULL (and sets wc_last_error) for an unknown name;
  * *n receives the word count. The view lives as long as the wave. */
 const uint32_t* wc_wave_array(const wc_wave* w, const char* name, size_t* n);
