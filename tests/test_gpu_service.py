@@ -313,3 +313,52 @@ def test_service_with_host_checks():
                          text=True, timeout=240)
     assert run.returncode == 0, run.stderr[-3000:]
     say(run.stdout.strip())
+
+
+_FUSED_CHILD = r"""
+import sys
+import numpy as np
+sys.path[:0] = sys.argv[1:]
+import oracle as O
+import warchest_wave as ww
+import workloads as W
+NONE = 0xFFFFFFFF
+def fused(w, name):
+    return any(r[1] != NONE for p in (0, 1) for r in w.array(name + str(p)).reshape(-1, 4))
+jobs = []
+for j in W.jobs("wave256")[:96]:  # trees whose own top regions fuse value and reach pairs
+    w = ww.Wave([j])
+    if fused(w, "top_back_run") and fused(w, "top_reach_run"):
+        jobs.append(j)
+    w.close()
+    if len(jobs) == 3:
+        break
+assert len(jobs) == 3, len(jobs)
+net = W.net_for("wave256")
+with ww.spawn(0, net, ww.WC_PRECISE, lanes=2, wave_jobs=3, window_us=20000) as client:
+    got = [h.wait() for h in [client.submit(j, tag=k) for k, j in enumerate(jobs)]]
+for k, (g, j) in enumerate(zip(got, jobs)):
+    o = O.solve(j, net, O.NET_F32)
+    np.testing.assert_array_equal(g.strategy, o["strategy"], err_msg=f"job {k}")
+    np.testing.assert_array_equal(g.root_values, o["roots"], err_msg=f"job {k}")
+print("service waves with fused top launches: 3 jobs bit-identical", flush=True)
+"""
+
+
+def test_service_with_fused_top_launches():
+    """WC_TOP_FUSE=1 makes the service's lanes plan fused top-depth launches
+    (value pairs and reach pairs), whose run, chunk and parent tables the
+    upload's structural checks bound; by default the lanes pack one depth per
+    launch. The setting is read once per process, so a child process runs the
+    service with it, on full-size subgames whose top regions fuse both."""
+    import subprocess
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    paths = [os.path.join(root, "war-chest-bot-9000-_amd"), os.path.join(root, "oracle"), here]
+    env = dict(os.environ, WC_TOP_FUSE="1")
+    say("case fused-top service: a child process, 3 full-size jobs, 2 lanes")
+    run = subprocess.run([sys.executable, "-c", _FUSED_CHILD, *paths], env=env, capture_output=True, text=True,
+                         timeout=240)
+    assert run.returncode == 0, run.stderr[-3000:]
+    say(run.stdout.strip())
